@@ -1,0 +1,332 @@
+"""Pins the CPU oracle against the reference's golden vectors, the reference-held
+activation arrays, closed forms and brute force.  CPU only."""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import quant as Q
+from oracle.attention import (decode_attention, exact_softmax_correction,
+                              query_aware_kscore_slot, softmax_rows,
+                              vectorized_joint_correction)
+from oracle.cache import OCache, OCfg
+from oracle.store import decode_append, process_page, write_pages_for_kv_head
+
+F16, F32 = np.float16, np.float32
+
+
+# ------------------------------------------------------------ packing (closed form)
+@pytest.mark.parametrize("bits", [2, 3, 4])
+def test_pack_roundtrip_and_bytes(bits):
+    rng = np.random.default_rng(bits)
+    lo, hi = -(2 ** (bits - 1)), 2 ** (bits - 1) - 1
+    codes = rng.integers(lo, hi + 1, size=(37, 128)).astype(np.int8)
+    p = Q.pack_codes_2d(codes, bits)
+    assert p.shape == (37, Q.packed_row_bytes(128, bits))
+    assert np.array_equal(Q.unpack_codes_2d(p, bits, 128), codes)
+    flat = codes.ravel()[:101]
+    p1 = {2: Q.pack_int2, 3: Q.pack_int3, 4: Q.pack_int4}[bits](flat)
+    assert np.array_equal({2: Q.unpack_int2, 3: Q.unpack_int3, 4: Q.unpack_int4}[bits](p1, 101), flat)
+
+
+def test_pack_bit_positions():
+    # INT3: 8 codes -> 24-bit LE word sum((c_i & 7) << 3i)  (quantizer.py:304-324)
+    c = np.array([[1, 2, 3, -1, -4, 0, -2, 3]], np.int8)
+    word = sum((int(v) & 7) << (3 * i) for i, v in enumerate(c[0]))
+    assert Q.pack_int3_2d(c).view(np.uint8).tolist() == [[word & 255, (word >> 8) & 255, word >> 16]]
+    # INT4: low nibble = even index;  INT2: LSB first
+    assert Q.pack_int4_2d(np.array([[3, -2]], np.int8)).view(np.uint8).tolist() == [[0x03 | (0x0E << 4)]]
+    assert Q.pack_int2_2d(np.array([[1, -2, 0, -1]], np.int8)).view(np.uint8).tolist() == [[1 | (2 << 2) | (0 << 4) | (3 << 6)]]
+
+
+def test_pack_4bit_roundtrip():
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((16, 32)).astype(F32)
+    p, s = Q.pack_4bit(x)
+    r = Q.unpack_4bit(p, s, x.size).reshape(x.shape)
+    assert p.shape == (256,)
+    assert np.linalg.norm(r - x) / np.linalg.norm(x) < 0.3     # test_care_kv.py:69-74
+
+
+# ------------------------------------------------------------ quantizer KAT
+@pytest.mark.parametrize("layer", ["00", "21"])
+def test_quantizer_fp32_against_reference_activations(golden, layer):
+    """|dequant(quant(|x|))| vs the reference-held K_hat/V_hat (INT3, g=32, fp32).
+    Cells where x/scale is an exact k+1/2 tie are exempt (the reference ran a
+    different division)."""
+    g = golden("activations_3d_slices.npz")
+    for kv in ("k", "v"):
+        x = g[f"l{layer}_{kv}_fp"]
+        ref = g[f"l{layer}_{kv}_hat"]
+        codes, scale = Q.quantize(x, 3, 32)
+        xh = np.abs(Q.dequantize(codes, scale, 32))
+        q = (x.reshape(x.shape[0], -1, 32) / scale[..., None]).reshape(x.shape)
+        tie = np.abs(np.abs(q - np.floor(q)) - 0.5) < 1e-6
+        diff = np.abs(xh - ref)
+        assert diff[~tie].max() <= 1e-6
+        assert tie.mean() < 1e-3
+
+
+def test_quantizer_fp16_chain_matches_torch():
+    """The fp16 rounding convention (fp32 op, round to fp16) equals torch's CPU
+    half arithmetic; torch is the library the reference calls."""
+    import torch
+    x = (torch.randn(4096, 64) * 3).half()
+    for bits in (2, 3, 4):
+        qm = 2 ** (bits - 1) - 1
+        m = x.reshape(-1, 2, 32).abs().amax(-1, keepdim=True).clamp(min=1e-8)
+        sc = m / qm
+        tq = (x.reshape(-1, 2, 32) / sc).round().clamp(-qm - 1, qm).to(torch.int8).reshape(x.shape)
+        codes, scale = Q.quantize(x.numpy(), bits, 32)
+        assert np.array_equal(codes, tq.numpy())
+        assert np.array_equal(scale, sc[..., 0].numpy())
+
+
+# ------------------------------------------------------------ store / cache goldens
+def _cfg_from_store(tag, **kw):
+    base = dict(num_layers=1, num_heads=2, num_kv_heads=2, head_dim=128, page_size=16, max_pages=8,
+                base_bits=3, group_size=32, k_channel_group=32, v_token_block=4, sketch_dim=32)
+    if tag == "abs":
+        base.update(store_budget_mode="absolute", store_abs_k=2, store_abs_v=4)
+    else:
+        base.update(store_budget_mode="ratio", store_budget_ratio=0.03)
+    base.update(kw)
+    return OCfg(**base)
+
+
+def _compare_cache(c: OCache, g, prefix="", err_ulp=1):
+    L = 0
+    H, P = c.valid_tokens.shape[1:]
+    for nm, arr in (("K_codes", c.base_K_codes), ("V_codes", c.base_V_codes),
+                    ("K_scale", c.base_K_scale), ("V_scale", c.base_V_scale),
+                    ("K_master", c.base_K_scale_master), ("V_master", c.base_V_scale_master),
+                    ("valid", c.valid_tokens)):
+        ref = g[prefix + nm]
+        mine = arr[L][:, :ref.shape[1]]
+        valid = c.valid_tokens[L][:, :ref.shape[1]]
+        if nm.endswith("codes") or nm.endswith("scale"):
+            # padded rows of a partial page are never read; compare valid rows
+            for h in range(ref.shape[0]):
+                for p in range(ref.shape[1]):
+                    n = int(valid[h, p])
+                    assert np.array_equal(mine[h, p, :n], ref[h, p, :n]), (nm, h, p)
+        else:
+            assert np.array_equal(mine, ref), nm
+    nk = g[prefix + "k_res"].shape[0]
+    nv = g[prefix + "v_res"].shape[0]
+    assert c.next_k_slot == nk and c.next_v_slot == nv
+    assert np.array_equal(c.k_residual_buf[:nk], g[prefix + "k_res"])
+    assert np.array_equal(c.k_residual_scale[:nk], g[prefix + "k_res_scale"])
+    assert np.array_equal(c.v_residual_buf[:nv], g[prefix + "v_res"])
+    assert np.array_equal(c.v_residual_scale[:nv], g[prefix + "v_res_scale"])
+    for h in range(H):
+        for p in range(g[prefix + "k_slots"].shape[1]):
+            m = c.meta_table[L][h][p]
+            if g[prefix + "k_slots"][h, p, 0] == -2:
+                assert m is None
+                continue
+            assert m.k_residual_slots == g[prefix + "k_slots"][h, p].tolist()
+            assert m.v_residual_slots == g[prefix + "v_slots"][h, p].tolist()
+            for nm, ref in (("k_err", m.k_error_norm), ("v_err", m.v_error_norm), ("k_sketch", m.k_sketch)):
+                a = ref.astype(F16).view(np.int16).astype(np.int32)
+                b = g[prefix + nm][h, p].view(np.int16).astype(np.int32)
+                assert np.abs(a - b).max() <= err_ulp, (nm, h, p)
+
+
+@pytest.mark.parametrize("tag", ["abs", "ratio"])
+def test_store_pages_golden(golden, tag):
+    g = golden("store_d128.npz")
+    c = OCache(_cfg_from_store(tag))
+    for h in range(2):
+        write_pages_for_kv_head(c, 0, h, g["K"][h], g["V"][h], token_start_abs=0, sink_tokens=4)
+    _compare_cache(c, g, prefix=tag + "_")
+
+
+def test_sketch_projection_fixture(golden):
+    from oracle.store import sketch_proj
+    import os
+    ref = np.load(os.path.join(os.path.dirname(__file__), "golden", "sketch_proj_32x32.npy"))
+    assert np.array_equal(sketch_proj(32, 32), ref)
+
+
+def test_append_golden(golden):
+    g = golden("append_d64.npz")
+    cfg = OCfg(num_layers=1, num_heads=1, num_kv_heads=1, head_dim=64, page_size=16, max_pages=4,
+               base_bits=3, group_size=32, store_budget_mode="absolute")
+    c = OCache(cfg)
+    X = g["X"]
+    page = np.concatenate([X[:, :10], np.zeros((2, 6, 64), F16)], 1)
+    Kc, Ks = Q.quantize(page[0], 3, 32)
+    Vc, Vs = Q.quantize(page[1], 3, 32)
+    p0 = c.alloc_page(0, 0)
+    c.write_base(0, 0, p0, Kc, Ks, Vc, Vs, 10)
+    for i in range(10, 16):
+        kc, ks = Q.quantize(X[0, i:i + 1], 3, 32)
+        vc, vs = Q.quantize(X[1, i:i + 1], 3, 32)
+        c.append_to_page(0, 0, p0, kc[0], ks[0], vc[0], vs[0])
+    p1 = c.alloc_page(0, 0)
+    for i in range(16, 21):
+        kc, ks = Q.quantize(X[0, i:i + 1], 3, 32)
+        vc, vs = Q.quantize(X[1, i:i + 1], 3, 32)
+        c.append_to_page(0, 0, p1, kc[0], ks[0], vc[0], vs[0])
+    Kc2, Ks2, Vc2, Vs2, lens = c.read_base_concat(0, 0, [p0, p1])
+    assert lens == g["read_lens"].tolist()
+    for a, b in ((Kc2, "read_Kc"), (Ks2, "read_Ks"), (Vc2, "read_Vc"), (Vs2, "read_Vs")):
+        assert np.array_equal(a, g[b]), b
+    # decode-opened page: master 0 -> every scale reads back as 0 (reference behaviour)
+    assert float(c.base_K_scale_master[0, 0, p1]) == 0.0 and np.all(Ks2[16:] == 0)
+
+
+# ------------------------------------------------------------ decode goldens
+DECODE_CASES = {
+    "c1": dict(Hq=32, Hkv=4, D=64, store=dict(store_budget_mode="ratio", store_budget_ratio=0.03), k_mode="exact"),
+    "c1_tight": dict(Hq=32, Hkv=4, D=64, store=dict(store_budget_mode="ratio", store_budget_ratio=0.03), k_mode="exact"),
+    "gqa4_d128": dict(Hq=8, Hkv=2, D=128, store=dict(store_budget_mode="absolute", store_abs_k=2, store_abs_v=4), k_mode="exact"),
+    "mha_d128_linear": dict(Hq=2, Hkv=2, D=128, store=dict(store_budget_mode="ratio", store_budget_ratio=0.03), k_mode="linear"),
+}
+
+
+def build_decode_case(g, name):
+    """Rebuild the golden case's cache with the oracle (prefill pages + decode appends)."""
+    spec = DECODE_CASES[name]
+    T, n_app = int(g["T"]), int(g["n_append"])
+    cfg = OCfg(num_layers=1, num_heads=spec["Hq"], num_kv_heads=spec["Hkv"], head_dim=spec["D"], page_size=16,
+               max_pages=max(T // 16 + 4, 400), base_bits=3, group_size=32, k_channel_group=32,
+               v_token_block=4, sketch_dim=32, read_budget_mode="absolute", read_abs_k=int(g["read_k"]),
+               read_abs_v=int(g["read_v"]), route_policy="joint", **spec["store"])
+    c = OCache(cfg)
+    for h in range(spec["Hkv"]):
+        write_pages_for_kv_head(c, 0, h, g["K"][h, :T], g["V"][h, :T], token_start_abs=0, sink_tokens=4)
+    for t in range(T, T + n_app):
+        decode_append(c, 0, g["K"][:, t], g["V"][:, t])
+    return c, spec
+
+
+def selection_matches(sel_a, sel_b, scores_r, budget, eps=1e-4):
+    """Selections equal, except swaps between candidates whose normalised
+    scores are within eps (relative) of the k-th largest score."""
+    if np.array_equal(sel_a, sel_b):
+        return True
+    for q in range(sel_a.shape[0]):
+        if np.array_equal(sel_a[q], sel_b[q]):
+            continue
+        s = scores_r[q]
+        kth = np.sort(s)[::-1][budget - 1]
+        diff = np.nonzero(sel_a[q] != sel_b[q])[0]
+        if not np.all(np.abs(s[diff] - kth) <= eps * max(abs(kth), 1e-30)):
+            return False
+    return True
+
+
+@pytest.mark.parametrize("name", list(DECODE_CASES))
+def test_decode_golden(golden, name):
+    g = golden(f"decode_{name}.npz")
+    c, spec = build_decode_case(g, name)
+    _compare_cache(c, g)
+    diag = {}
+    out = decode_attention(c, 0, g["Q"], k_mode=spec["k_mode"], kind="both", k_corr_scale=0.1,
+                           score_normalize=True, kscore_live=True, diag=diag)
+    ref = g["O"].astype(F32)
+    assert np.abs(out.astype(F32) - ref).max() <= 2e-3
+    for h, d in diag.items():
+        assert np.abs(d["O_base"] - g[f"h{h}_O_base"]).max() <= 1e-5
+        if f"h{h}_sel_k" in g:
+            sK, sV = d["score_K_r"], d["score_V_r"]
+            merged = np.concatenate([sK, sV], 1)
+            sel_ref = np.concatenate([g[f"h{h}_sel_k"], g[f"h{h}_sel_v"]], 1)
+            sel_me = np.concatenate([d["sel_k"], d["sel_v"]], 1)
+            mb = int(sel_ref[0].sum())
+            assert selection_matches(sel_me, sel_ref, merged, mb)
+            np.testing.assert_allclose(d["score_K"], g[f"h{h}_score_K"], rtol=2e-5, atol=1e-12)
+            np.testing.assert_allclose(d["score_V"], g[f"h{h}_score_V"], rtol=2e-5, atol=1e-12)
+    if "decode_step_out" in g:
+        # the reference decode_step itself (correction gated off by read_budget_ratio=0)
+        base = decode_attention(c, 0, g["Q"], correction=False)
+        assert np.abs(base.astype(F32) - g["decode_step_out"].astype(F32)).max() <= 2e-3
+
+
+# ------------------------------------------------------------ reference test fixture grid
+def test_reference_fixture_grid(golden):
+    g = golden("ref_fixture_d32.npz")
+    base = dict(num_layers=1, num_heads=3, num_kv_heads=1, head_dim=32, page_size=8, max_pages=4, base_bits=3,
+                group_size=8, k_channel_group=16, v_token_block=4, store_budget_mode="absolute",
+                read_budget_mode="absolute", store_abs_k=2, store_abs_v=2, read_abs_k=2, read_abs_v=2,
+                sketch_dim=4, packed_base=False, scale_quant="none")
+    from oracle.store import sketch_proj
+    P = sketch_proj(16, 4)
+    for pol in ("joint", "separate"):
+        c = OCache(OCfg(route_policy=pol, **base))
+        for p in range(4):
+            Kc, Ks = Q.quantize(g["K"][p], 3, 8)
+            Vc, Vs = Q.quantize(g["V"][p], 3, 8)
+            pid = c.alloc_page(0, 0)
+            c.write_base(0, 0, pid, Kc, Ks, Vc, Vs, 8)
+            process_page(c, 0, 0, pid, g["K"][p], g["V"][p], Kc, Ks, Vc, Vs, token_start=p * 8, num_valid=8, P=P)
+        if pol == "joint":
+            assert np.array_equal(c.base_K_codes[0], g["cache_K_codes"])
+            assert np.array_equal(c.k_residual_buf[:c.next_k_slot], g["cache_k_res"])
+        pids = list(range(4))
+        Kc, Ks, Vc, Vs, _ = c.read_base_concat(0, 0, pids)
+        Kb = Q.dequantize(Kc, Ks, 8).astype(F32)
+        Vb = Q.dequantize(Vc, Vs, 8).astype(F32)
+        S = (g["Q"] @ Kb.T) / F32(math.sqrt(32))
+        A = softmax_rows(S)
+        O = A @ Vb
+        for live in (0, 1):
+            for mode in ("linear", "exact"):
+                for kind in ("both", "k", "v"):
+                    for norm in (False, True):
+                        tag = f"{pol}_live{live}_{mode}_{kind}_n{int(norm)}"
+                        d = {}
+                        dl = vectorized_joint_correction(c, 0, 0, pids, g["Q"], S, A, Vb, O, kind=kind,
+                                                         k_corr_scale=0.1, score_normalize=norm,
+                                                         kscore_live=bool(live), k_mode=mode, sketch_P=P, diag=d)
+                        np.testing.assert_allclose(dl, g[f"{tag}_delta"], atol=1e-5, err_msg=tag)
+                        for key in ("sel_k", "sel_v"):
+                            if f"{tag}_{key}" in g:
+                                assert np.array_equal(d[key], g[f"{tag}_{key}"]), (tag, key)
+
+
+# ------------------------------------------------------------ math pins
+def test_exact_renorm_vs_fp64_bruteforce():
+    """attention.py:96-118 against a direct fp64 softmax of (s + ds) (cf. the
+    reference's tests/test_exact_k_correction.py:71-111)."""
+    rng = np.random.default_rng(7)
+    Qn, N, D = 3, 40, 16
+    S = rng.standard_normal((Qn, N))
+    A = softmax_rows(S.astype(F32))
+    ds = np.zeros((Qn, N)); ds[:, 5:13] = rng.standard_normal((Qn, 8)) * 0.7
+    V = rng.standard_normal((N, D)).astype(F32)
+    RV = np.zeros((N, D), F32); RV[20:24] = rng.standard_normal((4, D)) * 0.1
+    sel = np.zeros((Qn, N), bool); sel[:, 20:24] = True
+    O = A @ V
+    got = exact_softmax_correction(A, ds, V, O, RV, sel)
+    a64 = np.exp(S + ds - (S + ds).max(1, keepdims=True)); a64 /= a64.sum(1, keepdims=True)
+    ref = a64 @ V.astype(np.float64) + (a64 * sel) @ RV.astype(np.float64) - O
+    assert np.abs(got - ref).max() < 1e-5
+    # boundedness: ||O_new|| <= max ||V_t + RV_t||  (test_exact_k_correction.py:134-147)
+    assert np.linalg.norm(O + got, axis=1).max() <= np.linalg.norm(V + RV, axis=1).max() + 1e-5
+
+
+def test_kscore_closed_form():
+    rng = np.random.default_rng(3)
+    Qs, dK, A, Vs = (rng.standard_normal((2, 32)), rng.standard_normal((16, 32)),
+                     rng.random((2, 16)) * 0.1, rng.standard_normal((16, 64)))
+    got = query_aware_kscore_slot(Qs, dK, A, Vs, 128)
+    ds = Qs @ dK.T / math.sqrt(128)
+    ref = np.sqrt(((ds * A * (1 - A)) ** 2).sum(1)) * np.linalg.norm(Vs)
+    np.testing.assert_allclose(got, ref, rtol=1e-5)
+
+
+def test_read_zero_and_kind_v_invariants(golden):
+    g = golden("decode_gqa4_d128.npz")
+    c, spec = build_decode_case(g, "gqa4_d128")
+    c.cfg.read_abs_k = c.cfg.read_abs_v = 0
+    d0 = {}
+    out0 = decode_attention(c, 0, g["Q"], correction=True, k_mode="exact", diag=d0)
+    outb = decode_attention(c, 0, g["Q"], correction=False)
+    assert np.array_equal(out0, outb)                       # READ=0 == base, bit-exact
+    c.cfg.read_abs_k = c.cfg.read_abs_v = 8
+    o_lin = decode_attention(c, 0, g["Q"], kind="v", k_mode="linear")
+    o_ex = decode_attention(c, 0, g["Q"], kind="v", k_mode="exact")
+    assert np.array_equal(o_lin, o_ex)                      # kind=v: exact == linear
