@@ -1,0 +1,254 @@
+#!/usr/bin/env python3
+"""CARE-KV fused decode attention benchmark on one MI355X.
+
+Default workload is BASELINE config 3 (Mistral-7B GQA decode): batch 64,
+32 query / 8 kv heads, head_dim 128, 32768-token context in 16-token pages,
+uniform INT3 g=32 base with int8 page scales, 3% store budget (1 K + 1 V slot
+per page), top-256 joint read (128 K + 128 V budget), query-aware K score,
+exact softmax renormalisation.  One step = one decode token through one
+layer's attention for the whole batch (projections excluded).  Inputs are
+resident in HBM before timing; the timed region is K launches of the fused
+kernel bracketed by HIP events on the launch stream.
+
+Prints one JSON line on stdout; progress goes to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG_DIR = os.path.join(ROOT, "care-kv-sparse-residual-correction-for-low-bit-kv-cache-quantization_amd")
+for _p in (ROOT, PKG_DIR):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PAPER_ENV = dict(CAREKV_STORE_POLICY="residual_kind_aware", CAREKV_PREFILL_RESIDUAL_KIND="both",
+                 CAREKV_KSCORE_LIVE="1", CAREKV_SCORE_NORMALIZE="1", CAREKV_K_CORRECTION_MODE="exact",
+                 CAREKV_K_CORRECTION_SCALE="0.1")
+
+CONFIGS = {
+    # name: B, Hq, Hkv, D, N, read_k, read_v, distribution, seed
+    "c1": dict(B=1, Hq=32, Hkv=4, D=64, N=512, rk=32, rv=32, dist="outlier8", seed=1,
+               workload="config1 TinyLlama decode B=1 32q/4kv D=64 N=512"),
+    "c2": dict(B=16, Hq=32, Hkv=32, D=128, N=4096, rk=64, rv=64, dist="student_t", seed=2,
+               workload="config2 Llama-2-7B decode B=16 32q/32kv D=128 N=4096"),
+    "c3": dict(B=64, Hq=32, Hkv=8, D=128, N=32768, rk=128, rv=128, dist="outlier10", seed=3,
+               workload="config3 Mistral-7B GQA decode B=64 32q/8kv D=128 N=32768"),
+}
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def gen_kv(torch, spec, b, device):
+    """Synthetic post-RoPE K/V (Hkv, N, D) fp16 for sequence b (generated on device)."""
+    g = torch.Generator(device=device).manual_seed(spec["seed"] * 100003 + b)
+    H, N, D = spec["Hkv"], spec["N"], spec["D"]
+    K = torch.randn(H, N, D, generator=g, device=device)
+    V = torch.randn(H, N, D, generator=g, device=device)
+    if spec["dist"].startswith("outlier"):
+        mult = float(spec["dist"][len("outlier"):])
+        for h in range(H):
+            ch = torch.randperm(D, generator=g, device=device)[:4]
+            K[h][:, ch] *= mult
+    elif spec["dist"] == "student_t":
+        n_ch = max(1, round(0.02 * D))
+        for X in (K, V):
+            for h in range(H):
+                ch = torch.randperm(D, generator=g, device=device)[:n_ch]
+                z = torch.randn(N, n_ch, generator=g, device=device)
+                chi = (torch.randn(3, N, n_ch, generator=g, device=device) ** 2).sum(0)
+                X[h][:, ch] = 6.0 * z / torch.sqrt(chi / 3.0)
+    return K.half(), V.half()
+
+
+def algorithmic_bytes(spec, cfg, cache, diag_np):
+    """Bytes one decode step must move (per the roofline model):
+    packed K+V codes, int8 group scales, fp16 masters, every stored K slot
+    (read by the query-aware K score), fp16 V errors, int32 slot tables, the
+    selected V slots (union over the GQA group) and q/out."""
+    import numpy as np
+    B, Hq, Hkv, D, N = spec["B"], spec["Hq"], spec["Hkv"], spec["D"], spec["N"]
+    bits, G, P = cfg.base_bits, D // 32, math.ceil(N / 16)
+    grp = Hq // Hkv
+    k_slots = (cache.k_slot[0, :, :B, :P] >= 0).sum().item()          # stored K slots (all b, kvh)
+    per_bkv_fixed = (2 * N * D * bits / 8 + 2 * N * G + 2 * P * 2 + P * 4 * 2 + P * (D // 32 + 4) * 4
+                     + 2 * grp * D * 2)
+    total = B * Hkv * per_bkv_fixed + k_slots * (16 * 32 // 2 + 2)
+    v_union = 0
+    for b in range(B):
+        for h in range(Hkv):
+            s = set()
+            for j in range(grp):
+                for x in diag_np[b, h * grp + j]:
+                    if x < 0:
+                        break
+                    if (int(x) >> 30) == 1:
+                        s.add(int(x) & ((1 << 30) - 1))
+            v_union += len(s)
+    total += v_union * (4 * D // 2 + 2)
+    return float(total), int(k_slots), int(v_union)
+
+
+def oracle_slice_from_device(cache, seq, kvh, spec):
+    """Copy one (sequence, kv head) of the device cache into the CPU oracle."""
+    import numpy as np
+    from oracle.cache import OCache, OCfg, OMeta
+    cfg = cache.cfg
+    P = cache.num_pages(0, kvh, seq)
+    ocfg = OCfg(num_layers=1, num_heads=spec["Hq"] // spec["Hkv"], num_kv_heads=1, head_dim=cfg.head_dim,
+                page_size=16, max_pages=P, base_bits=cfg.base_bits, group_size=32, k_channel_group=32,
+                v_token_block=4, sketch_dim=cfg.sketch_dim, read_budget_mode="absolute", read_abs_k=spec["rk"],
+                read_abs_v=spec["rv"], route_policy="joint", store_budget_mode="ratio", store_budget_ratio=0.03)
+    oc = OCache(ocfg, max_slots=cache.n_slots)
+    g = lambda t: t[0, kvh, seq, :P].cpu().numpy()  # noqa: E731
+    oc.base_K_codes[0, 0] = g(cache.kcodes)
+    oc.base_V_codes[0, 0] = g(cache.vcodes)
+    oc.base_K_scale[0, 0] = g(cache.kscale)
+    oc.base_V_scale[0, 0] = g(cache.vscale)
+    oc.base_K_scale_master[0, 0] = g(cache.kmaster)
+    oc.base_V_scale_master[0, 0] = g(cache.vmaster)
+    oc.valid_tokens[0, 0] = g(cache.valid)
+    oc.k_residual_buf[:] = cache.k_res[seq].cpu().numpy()
+    oc.v_residual_buf[:] = cache.v_res[seq].cpu().numpy()
+    oc.k_residual_scale[:, 0] = cache.k_res_scale[seq].cpu().numpy()
+    oc.v_residual_scale[:, 0] = cache.v_res_scale[seq].cpu().numpy()
+    hm, ks, vs, ke, ve, sk = (g(cache.has_meta), g(cache.k_slot), g(cache.v_slot), g(cache.k_err),
+                              g(cache.v_err), g(cache.k_sketch))
+    for p in range(P):
+        if hm[p]:
+            oc.meta_table[0][0][p] = OMeta(page_id=p, layer_id=0, kv_head=0, token_start=p * 16,
+                                           num_tokens=int(oc.valid_tokens[0, 0, p]),
+                                           k_residual_slots=ks[p].tolist(), v_residual_slots=vs[p].tolist(),
+                                           k_error_norm=ke[p], v_error_norm=ve[p], k_sketch=sk[p])
+    oc.next_page[0][0] = P
+    return oc
+
+
+def cpu_baseline(cache, spec, q_np, slices):
+    """Time the oracle (numpy restatement of the reference decode path:
+    read_base_concat + dequantize + base attention + vectorized joint
+    correction) on `slices` (sequence, kv head) slices; extrapolate to the
+    whole batch."""
+    import numpy as np
+    from oracle import quant as Q
+    from oracle.attention import base_attention, vectorized_joint_correction
+    grp = spec["Hq"] // spec["Hkv"]
+    total = 0.0
+    for i in range(slices):
+        seq, kvh = i % spec["B"], (i // spec["B"]) % spec["Hkv"]
+        oc = oracle_slice_from_device(cache, seq, kvh, spec)
+        Qg = q_np[seq, kvh * grp:(kvh + 1) * grp]
+        t0 = time.perf_counter()
+        pids = oc.all_page_ids(0, 0)
+        Kc, Ks, Vc, Vs, _ = oc.read_base_concat(0, 0, pids)
+        Kh = Q.dequantize(Kc, Ks, 32).astype(np.float32)
+        Vh = Q.dequantize(Vc, Vs, 32).astype(np.float32)
+        S, A, O = base_attention(Kh, Vh, Qg.astype(np.float32))
+        d = vectorized_joint_correction(oc, 0, 0, pids, Qg, S, A, Vh, O, kind="both", k_corr_scale=0.1,
+                                        score_normalize=True, kscore_live=True, k_mode="exact")
+        _ = (O + d).astype(np.float16)
+        total += time.perf_counter() - t0
+    per_slice = total / slices
+    return per_slice * spec["B"] * spec["Hkv"] * 1e6, per_slice
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
+    ap.add_argument("--cpu-slices", type=int, default=2)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--split-pages", type=int, default=None)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): the decode path is embarrassingly "
+              "parallel over (sequence, kv head) and is not built for several GPUs in this tree.", file=sys.stderr)
+        sys.exit(2)
+    os.environ.update(PAPER_ENV)
+    import numpy as np
+    import torch
+    import care_kv
+    spec = CONFIGS[args.config]
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    B, Hq, Hkv, D, N = spec["B"], spec["Hq"], spec["Hkv"], spec["D"], spec["N"]
+    P = math.ceil(N / 16)
+    cfg = care_kv.CacheConfig(num_layers=1, num_heads=Hq, num_kv_heads=Hkv, head_dim=D, page_size=16,
+                              max_pages=P + 4, base_bits=3, group_size=32, k_channel_group=32, v_token_block=4,
+                              sketch_dim=32, packed_base=True, scale_quant="int8", store_budget_mode="ratio",
+                              store_budget_ratio=0.03, read_budget_ratio=0.0, read_budget_mode="absolute",
+                              read_abs_k=spec["rk"], read_abs_v=spec["rv"], route_policy="joint")
+    t0 = time.time()
+    cache = care_kv.CAREKVCache(cfg, device=dev, n_seq=B)
+    for b in range(B):
+        K, V = gen_kv(torch, spec, b, dev)
+        cache.write_prefill(0, K, V, seqs=[b])
+        del K, V
+    torch.cuda.synchronize()
+    log(f"[bench] {args.config}: cache built in {time.time() - t0:.1f}s "
+        f"({torch.cuda.memory_allocated() / 2**30:.2f} GiB allocated)")
+    gq = torch.Generator(device=dev).manual_seed(spec["seed"] + 7)
+    q = torch.randn(B, Hq, D, generator=gq, device=dev).half()
+    out, diag = care_kv.decode_attention(cache, 0, q, diag_cap=512, split_pages=args.split_pages)
+    torch.cuda.synchronize()
+    diag_np = diag.cpu().numpy()
+    nbytes, k_slots, v_union = algorithmic_bytes(spec, cfg, cache, diag_np)
+    for _ in range(args.warmup):
+        care_kv.decode_attention(cache, 0, q, out=out, split_pages=args.split_pages)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for _ in range(args.steps):
+        care_kv.decode_attention(cache, 0, q, out=out, split_pages=args.split_pages)
+    ev1.record(stream)
+    ev1.synchronize()
+    ms_total = ev0.elapsed_time(ev1)
+    ms_step = ms_total / args.steps
+    us_step = ms_step * 1e3
+    gbps = nbytes / (ms_step * 1e-3) / 1e9
+    log(f"[bench] {us_step:.1f} us/step, {nbytes / 1e9:.3f} GB algorithmic/step, {gbps:.0f} GB/s, "
+        f"K slots {k_slots}, V union {v_union}")
+    cpu = None
+    if not args.no_cpu_baseline:
+        q_np = q.cpu().numpy()
+        cpu_us, per_slice = cpu_baseline(cache, spec, q_np, args.cpu_slices)
+        try:
+            import threadpoolctl
+            info = threadpoolctl.threadpool_info()
+            cores = max([i.get("num_threads", 1) for i in info] + [1])
+        except Exception:
+            cores = int(os.environ.get("OMP_NUM_THREADS", "1"))
+        cpu = {"value": round(cpu_us, 1), "unit": "us/step", "cores": cores, "kind": "port",
+               "sample": f"{args.cpu_slices} of {B * Hkv} (sequence, kv-head) slices of the same cache "
+                         f"({per_slice:.3f} s each, numpy oracle), extrapolated x{B * Hkv}"}
+        log(f"[bench] cpu oracle {per_slice:.3f} s/slice -> {cpu_us / 1e3:.1f} ms/step extrapolated")
+    line = {
+        "metric": "CARE-KV decode-attn us/step + HBM GB/s (% roofline), Mistral-7B shape 32K ctx",
+        "value": round(us_step, 2), "unit": "us/step", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int3-packed KV, fp16 q/out, fp32 softmax", "data": "synthetic",
+        "config": {"workload": spec["workload"], "global_batch": B, "seq_len": N, "parallelism": "single-gpu",
+                   "base": "uniform INT3 g=32, int8 page scales", "store": "ratio 0.03 (1K+1V slot/page)",
+                   "read": f"joint top-{spec['rk'] + spec['rv']} (K {spec['rk']} + V {spec['rv']}), "
+                           "KSCORE_LIVE, normalize, exact"},
+        "hbm_gbps": round(gbps, 1),
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": 8000.0, "unit": "GB/s",
+                     "frac": round(gbps / 8000.0, 4), "traffic": None,
+                     "algorithmic_bytes_per_launch": int(nbytes)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

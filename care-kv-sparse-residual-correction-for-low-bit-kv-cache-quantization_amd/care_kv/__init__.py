@@ -1,0 +1,19 @@
+"""CARE-KV quantized decode attention for MI355X (gfx950 HIP kernels).
+
+Public surface follows the reference package's names (``CacheConfig``,
+``CAREKVCache``, ``PageMeta``, ``apply_carekv_env_overrides``,
+``layer_budget_multiplier``, ``CAREKVMultiHeadAttention``, ...); the compute
+runs in ``libcarekv_hip.so`` through a C ABI (include/carekv.h).
+"""
+from .config import (CacheConfig, apply_carekv_env_overrides, layer_budget_multiplier,
+                     resolve_read_knobs, resolve_store_knobs)
+from .cache import CAREKVCache, PageMeta, get_sketch_proj, packed_row_bytes
+from .attention import CAREKVMultiHeadAttention, decode_attention
+from ._lib import CarekvError
+
+__version__ = "0.1.0"
+__all__ = [
+    "CacheConfig", "apply_carekv_env_overrides", "layer_budget_multiplier", "resolve_read_knobs",
+    "resolve_store_knobs", "CAREKVCache", "PageMeta", "get_sketch_proj", "packed_row_bytes",
+    "CAREKVMultiHeadAttention", "decode_attention", "CarekvError",
+]

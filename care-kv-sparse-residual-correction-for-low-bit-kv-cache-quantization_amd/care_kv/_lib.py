@@ -1,0 +1,106 @@
+"""ctypes binding of libcarekv_hip.so (C ABI declared in include/carekv.h).
+
+The library is required: every entry point raises if it is missing or if
+the tensors handed to it are not on a HIP device.  There is no fallback.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import threading
+
+import torch
+
+_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libcarekv_hip.so")
+_lib = None
+_lock = threading.Lock()
+
+
+class CarekvError(RuntimeError):
+    pass
+
+
+class Arena(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in (
+        "kcodes", "vcodes", "kscale", "vscale", "kmaster", "vmaster", "valid", "has_meta", "k_slot", "v_slot",
+        "k_err", "v_err", "k_sketch", "v_sq", "k_res", "k_res_scale", "v_res", "v_res_scale", "next_slot")] + \
+        [(n, C.c_int32) for n in (
+            "n_seq", "n_kv_heads", "max_pages", "head_dim", "base_bits", "page_size", "group_size",
+            "k_channel_group", "v_token_block", "sketch_dim", "scale_mode", "residual_bits", "n_slots")]
+
+
+class StoreParams(C.Structure):
+    _fields_ = [("k_budget", C.c_int32), ("v_budget", C.c_int32), ("joint_budget", C.c_int32),
+                ("joint", C.c_int32), ("store_none", C.c_int32), ("sensitivity", C.c_double),
+                ("sink_tokens", C.c_int32), ("sketch_proj", C.c_void_p)]
+
+
+class DecodeParams(C.Structure):
+    _fields_ = [("batch", C.c_int32), ("n_heads", C.c_int32), ("seq_slot", C.c_void_p), ("n_pages", C.c_void_p),
+                ("max_pages_used", C.c_int32), ("sm_scale", C.c_float), ("sensitivity", C.c_float),
+                ("correction", C.c_int32), ("kind", C.c_int32), ("joint", C.c_int32), ("normalize", C.c_int32),
+                ("k_exact", C.c_int32), ("k_corr_scale", C.c_float), ("lambda_k", C.c_float),
+                ("lambda_v", C.c_float), ("budget_ratio", C.c_int32), ("abs_k", C.c_int32), ("abs_v", C.c_int32),
+                ("ratio_k", C.c_double), ("ratio_v", C.c_double), ("k_cap", C.c_int32), ("v_cap", C.c_int32),
+                ("split_pages", C.c_int32)]
+
+
+# page job: int32 x 6 (seq, kv_head, page, num_valid, token_start, is_recent)
+PAGE_JOB_INTS = 6
+
+EXPORTS = ["carekv_store_pages", "carekv_store_workspace_bytes", "carekv_append_rows", "carekv_decode_attn",
+           "carekv_decode_workspace_bytes", "carekv_read_pages", "carekv_quantize_rows", "carekv_last_error"]
+
+
+def lib_path() -> str:
+    return _LIB_PATH
+
+
+def load(path: str | None = None):
+    """Load the HIP library (raises if it has not been built)."""
+    global _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        p = path or _LIB_PATH
+        if not os.path.exists(p):
+            raise CarekvError(f"{p} not found: build it with `python -m care_kv.build` "
+                              "(or __graft_entry__.build()); there is no non-HIP fallback")
+        lib = C.CDLL(p)
+        vp, i32, i64 = C.c_void_p, C.c_int32, C.c_int64
+        lib.carekv_last_error.restype = C.c_char_p
+        lib.carekv_store_workspace_bytes.restype = i64
+        lib.carekv_store_workspace_bytes.argtypes = [i32]
+        lib.carekv_store_pages.restype = C.c_int
+        lib.carekv_store_pages.argtypes = [C.POINTER(Arena), C.POINTER(StoreParams), vp, vp, vp, i32, vp, i32, vp, vp]
+        lib.carekv_append_rows.restype = C.c_int
+        lib.carekv_append_rows.argtypes = [C.POINTER(Arena), vp, vp, vp, i32, vp]
+        lib.carekv_decode_workspace_bytes.restype = i64
+        lib.carekv_decode_workspace_bytes.argtypes = [C.POINTER(Arena), C.POINTER(DecodeParams)]
+        lib.carekv_decode_attn.restype = C.c_int
+        lib.carekv_decode_attn.argtypes = [C.POINTER(Arena), C.POINTER(DecodeParams), vp, vp, vp, i64, vp, i32, vp]
+        lib.carekv_read_pages.restype = C.c_int
+        lib.carekv_read_pages.argtypes = [C.POINTER(Arena), i32, i32, i32, vp, vp, vp, vp, vp, vp]
+        lib.carekv_quantize_rows.restype = C.c_int
+        lib.carekv_quantize_rows.argtypes = [vp, i32, i32, i32, i32, i32, vp, vp, vp]
+        _lib = lib
+        return lib
+
+
+def check(rc: int, what: str):
+    if rc != 0:
+        msg = load().carekv_last_error()
+        raise CarekvError(f"{what} failed (code {rc}): {msg.decode() if msg else ''}")
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    if t is None:
+        return None
+    if not t.is_cuda:
+        raise CarekvError("CARE-KV HIP kernels need device tensors (got a CPU tensor); "
+                          "there is no CPU implementation in the product path")
+    return t.data_ptr()
+
+
+def stream_ptr(device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream

@@ -1,0 +1,365 @@
+"""Paged CARE-KV cache on the device.
+
+``CAREKVCache`` keeps the reference's interface (cache.py:416-904): per
+(layer, kv head) page counters, ``alloc_page`` / ``get_open_page`` /
+``all_page_ids`` / ``read_base_concat`` / ``meta_table`` / slot arenas.  Its
+storage is one device arena per model sized for ``n_seq`` sequence slots, so
+a batch of sequences is decoded by one kernel launch per layer; with
+``n_seq=1`` it is a drop-in for the reference's one-cache-per-sequence object
+and its buffer attributes have the reference shapes.
+
+Memory layout (all device tensors):
+  base codes   int8 [L, Hkv, n_seq, P, T, row_bytes]  (always bit-packed)
+  base scales  int8 [L, Hkv, n_seq, P, T, G] + fp16 master [L, Hkv, n_seq, P]
+               (scale_quant=int8) or fp16 [L, Hkv, n_seq, P, T, G]
+  page meta    valid/has_meta/k_slot/v_slot/k_err/v_err/k_sketch/v_sq per page
+  slot arenas  int8 [n_seq, S, slot_bytes] + fp16 scales, shared by layers
+Page counters and valid counts are mirrored on the host (they evolve
+deterministically), so appends and decode never read device memory back.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from typing import Dict, List, Optional, Sequence, Tuple
+
+import numpy as np
+import torch
+
+from . import _lib
+from .config import CacheConfig, resolve_store_knobs, store_caps
+
+F16 = torch.float16
+
+
+@dataclass
+class PageMeta:
+    """Per-page metadata (same fields as the reference PageMeta)."""
+    page_id: int
+    layer_id: int
+    kv_head: int
+    token_start: int
+    num_tokens: int
+    k_residual_slots: List[int] = field(default_factory=list)
+    v_residual_slots: List[int] = field(default_factory=list)
+    k_error_norm: Optional[torch.Tensor] = None
+    v_error_norm: Optional[torch.Tensor] = None
+    k_sketch: Optional[torch.Tensor] = None
+    prior_score: float = 0.0
+
+
+def packed_row_bytes(D: int, bits: int) -> int:
+    if bits == 2 and D % 4 == 0:
+        return D // 4
+    if bits == 3 and D % 8 == 0:
+        return D * 3 // 8
+    if bits == 4 and D % 2 == 0:
+        return D // 2
+    raise ValueError(f"Unsupported base_bits={bits} for head_dim={D}")
+
+
+_SKETCH_CACHE: Dict[Tuple[int, int, str], torch.Tensor] = {}
+
+
+def get_sketch_proj(head_dim: int, k_channel_group: int, sketch_dim: int, device) -> torch.Tensor:
+    """Fixed random projection (kcg, sketch_dim): randn from a CPU generator
+    seeded 42, divided by sqrt(sketch_dim) (residual_store.py:206-214)."""
+    key = (k_channel_group, sketch_dim, str(device))
+    if key not in _SKETCH_CACHE:
+        gen = torch.Generator(device="cpu").manual_seed(42)
+        P = torch.randn(k_channel_group, sketch_dim, generator=gen) / math.sqrt(sketch_dim)
+        _SKETCH_CACHE[key] = P.to(device)
+    return _SKETCH_CACHE[key]
+
+
+def check_kernel_config(cfg: CacheConfig):
+    """Configurations the HIP kernels implement; anything else is rejected."""
+    bad = []
+    if cfg.base_quantizer != "uniform":
+        bad.append(f"base_quantizer={cfg.base_quantizer} (only 'uniform' is built)")
+    if cfg.page_size != 16:
+        bad.append(f"page_size={cfg.page_size} (16)")
+    if cfg.group_size != 32:
+        bad.append(f"group_size={cfg.group_size} (32)")
+    if cfg.k_channel_group != 32:
+        bad.append(f"k_channel_group={cfg.k_channel_group} (32)")
+    if cfg.v_token_block != 4:
+        bad.append(f"v_token_block={cfg.v_token_block} (4)")
+    if cfg.head_dim not in (64, 128):
+        bad.append(f"head_dim={cfg.head_dim} (64 or 128)")
+    if cfg.base_bits not in (2, 3, 4):
+        bad.append(f"base_bits={cfg.base_bits} (2, 3 or 4)")
+    if cfg.residual_bits != 4:
+        bad.append(f"residual_bits={cfg.residual_bits} (4)")
+    if cfg.scale_quant == "none" and cfg.scale_dtype != "fp16":
+        bad.append(f"scale_dtype={cfg.scale_dtype} with scale_quant=none (fp16)")
+    if cfg.sketch_dim > 64:
+        bad.append(f"sketch_dim={cfg.sketch_dim} (<= 64)")
+    if bad:
+        raise NotImplementedError("CARE-KV HIP kernels do not support: " + "; ".join(bad))
+
+
+class CAREKVCache:
+    """Device-resident paged cache for ``n_seq`` sequences of one model."""
+
+    def __init__(self, cfg: CacheConfig, device=None, n_seq: int = 1, n_slots: Optional[int] = None):
+        check_kernel_config(cfg)
+        if device is None:
+            device = torch.device("cuda", torch.cuda.current_device())
+        self.cfg = cfg
+        self.device = torch.device(device)
+        if self.device.type != "cuda":
+            raise _lib.CarekvError("CAREKVCache lives on a HIP device (got %s)" % self.device)
+        self.n_seq = n_seq
+        L, H, P, T, D = cfg.num_layers, cfg.num_kv_heads, cfg.max_pages, cfg.page_size, cfg.head_dim
+        G = D // cfg.group_size
+        self.ncg = D // cfg.k_channel_group
+        self.nvb = math.ceil(T / cfg.v_token_block)
+        self._packed_row_bytes = packed_row_bytes(D, cfg.base_bits)
+        dev = self.device
+        shp = (L, H, n_seq, P)
+        self.kcodes = torch.zeros(*shp, T, self._packed_row_bytes, dtype=torch.int8, device=dev)
+        self.vcodes = torch.zeros_like(self.kcodes)
+        self.scale_mode = 1 if cfg.scale_quant == "int8" else 0
+        sdt = torch.int8 if self.scale_mode else F16
+        self.kscale = torch.zeros(*shp, T, G, dtype=sdt, device=dev)
+        self.vscale = torch.zeros_like(self.kscale)
+        self.kmaster = torch.zeros(*shp, dtype=F16, device=dev)
+        self.vmaster = torch.zeros_like(self.kmaster)
+        self.valid = torch.zeros(*shp, dtype=torch.int32, device=dev)
+        self.has_meta = torch.zeros(*shp, dtype=torch.int8, device=dev)
+        self.k_slot = torch.full((*shp, self.ncg), -1, dtype=torch.int32, device=dev)
+        self.v_slot = torch.full((*shp, self.nvb), -1, dtype=torch.int32, device=dev)
+        self.k_err = torch.zeros(*shp, self.ncg, dtype=F16, device=dev)
+        self.v_err = torch.zeros(*shp, self.nvb, dtype=F16, device=dev)
+        self.k_sketch = torch.zeros(*shp, self.ncg, cfg.sketch_dim, dtype=F16, device=dev)
+        self.v_sq = torch.zeros(*shp, dtype=torch.float32, device=dev)
+        self.k_cap, self.v_cap = store_caps(cfg)
+        if n_slots is None:
+            n_slots = max(64, P * H * L * self.k_cap, P * H * L * self.v_cap)
+        self.n_slots = n_slots
+        self.k_slot_bytes = T * cfg.k_channel_group * cfg.residual_bits // 8
+        self.v_slot_bytes = cfg.v_token_block * D * cfg.residual_bits // 8
+        self.k_res = torch.zeros(n_seq, n_slots, self.k_slot_bytes, dtype=torch.int8, device=dev)
+        self.v_res = torch.zeros(n_seq, n_slots, self.v_slot_bytes, dtype=torch.int8, device=dev)
+        self.k_res_scale = torch.zeros(n_seq, n_slots, dtype=F16, device=dev)
+        self.v_res_scale = torch.zeros(n_seq, n_slots, dtype=F16, device=dev)
+        self.next_slot = torch.zeros(n_seq, 2, dtype=torch.int32, device=dev)
+        self.sketch_proj = get_sketch_proj(D, cfg.k_channel_group, cfg.sketch_dim, dev).contiguous()
+        # host mirrors
+        self.next_page = np.zeros((L, H, n_seq), dtype=np.int64)
+        self.valid_host = np.zeros((L, H, n_seq, P), dtype=np.int32)
+        self._token_start = np.zeros((L, H, n_seq, P), dtype=np.int64)
+        self._arenas: Dict[int, _lib.Arena] = {}
+        self._ws: Dict[str, torch.Tensor] = {}
+        self._row_tables: Dict[tuple, torch.Tensor] = {}
+        _lib.load()
+
+    # ------------------------------------------------------------ C structs
+    def arena(self, layer: int) -> _lib.Arena:
+        a = self._arenas.get(layer)
+        if a is None:
+            cfg = self.cfg
+            g = lambda t: t[layer].data_ptr()  # noqa: E731
+            a = _lib.Arena(
+                kcodes=g(self.kcodes), vcodes=g(self.vcodes), kscale=g(self.kscale), vscale=g(self.vscale),
+                kmaster=g(self.kmaster), vmaster=g(self.vmaster), valid=g(self.valid), has_meta=g(self.has_meta),
+                k_slot=g(self.k_slot), v_slot=g(self.v_slot), k_err=g(self.k_err), v_err=g(self.v_err),
+                k_sketch=g(self.k_sketch), v_sq=g(self.v_sq), k_res=self.k_res.data_ptr(),
+                k_res_scale=self.k_res_scale.data_ptr(), v_res=self.v_res.data_ptr(),
+                v_res_scale=self.v_res_scale.data_ptr(), next_slot=self.next_slot.data_ptr(),
+                n_seq=self.n_seq, n_kv_heads=cfg.num_kv_heads, max_pages=cfg.max_pages, head_dim=cfg.head_dim,
+                base_bits=cfg.base_bits, page_size=cfg.page_size, group_size=cfg.group_size,
+                k_channel_group=cfg.k_channel_group, v_token_block=cfg.v_token_block, sketch_dim=cfg.sketch_dim,
+                scale_mode=self.scale_mode, residual_bits=cfg.residual_bits, n_slots=self.n_slots)
+            self._arenas[layer] = a
+        return a
+
+    def workspace(self, name: str, nbytes: int) -> torch.Tensor:
+        """Zero-initialised scratch owned by the cache (grown on demand)."""
+        t = self._ws.get(name)
+        if t is None or t.numel() < nbytes:
+            t = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device=self.device)
+            self._ws[name] = t
+        return t
+
+    # ------------------------------------------------------------ allocation
+    def alloc_page(self, layer: int, kv_head: int, seq: int = 0) -> int:
+        pid = int(self.next_page[layer, kv_head, seq])
+        assert pid < self.cfg.max_pages, "KV cache is full"
+        self.next_page[layer, kv_head, seq] += 1
+        return pid
+
+    def get_open_page(self, layer: int, kv_head: int, seq: int = 0) -> Optional[int]:
+        n = int(self.next_page[layer, kv_head, seq])
+        if n == 0:
+            return None
+        last = n - 1
+        return last if self.valid_host[layer, kv_head, seq, last] < self.cfg.page_size else None
+
+    def page_valid(self, layer: int, kv_head: int, page_id: int, seq: int = 0) -> int:
+        return int(self.valid_host[layer, kv_head, seq, page_id])
+
+    def num_pages(self, layer: int, kv_head: int, seq: int = 0) -> int:
+        return int(self.next_page[layer, kv_head, seq])
+
+    def all_page_ids(self, layer: int, kv_head: int, seq: int = 0) -> List[int]:
+        return list(range(self.num_pages(layer, kv_head, seq)))
+
+    def total_valid_tokens(self, layer: int, kv_head: int, seq: int = 0) -> int:
+        n = self.num_pages(layer, kv_head, seq)
+        return int(self.valid_host[layer, kv_head, seq, :n].sum())
+
+    def reset_sequence(self, seq: int):
+        """Forget a sequence slot (pages, metadata, residual slots)."""
+        self.valid[:, :, seq].zero_()
+        self.has_meta[:, :, seq].zero_()
+        self.k_slot[:, :, seq].fill_(-1)
+        self.v_slot[:, :, seq].fill_(-1)
+        self.next_slot[seq].zero_()
+        self.next_page[:, :, seq] = 0
+        self.valid_host[:, :, seq] = 0
+        self._token_start[:, :, seq] = 0
+
+    # ------------------------------------------------------------ page writes
+    def write_prefill(self, layer: int, K: torch.Tensor, V: torch.Tensor, token_start_abs: int = 0,
+                      sink_tokens: int = 4, seqs: Optional[Sequence[int]] = None):
+        """Quantize + pack + store pages for a prompt chunk of every listed
+        sequence (layer.py:204-334, uniform base quantizer).
+
+        K, V: fp16 post-RoPE keys / values, (Hkv, T, D) for one sequence or
+        (B, Hkv, T, D) with ``seqs`` naming the B sequence slots."""
+        cfg = self.cfg
+        if K.dim() == 3:
+            K, V = K.unsqueeze(0), V.unsqueeze(0)
+        B, H, T, D = K.shape
+        assert H == cfg.num_kv_heads and D == cfg.head_dim and V.shape == K.shape
+        seqs = list(range(B)) if seqs is None else list(seqs)
+        assert len(seqs) == B and len(set(seqs)) == B
+        if T == 0:
+            return
+        ps = cfg.page_size
+        n_new = math.ceil(T / ps)
+        pad = n_new * ps - T
+        Kp, Vp = K.to(F16), V.to(F16)
+        if pad:
+            Kp = torch.nn.functional.pad(Kp, (0, 0, 0, pad))
+            Vp = torch.nn.functional.pad(Vp, (0, 0, 0, pad))
+        Kp = Kp.contiguous().view(B * H * n_new * ps, D)
+        Vp = Vp.contiguous().view(B * H * n_new * ps, D)
+        jobs = np.zeros((B * H * n_new, _lib.PAGE_JOB_INTS), dtype=np.int32)
+        group_ptr = np.zeros(B + 1, dtype=np.int32)
+        j = 0
+        for bi, s in enumerate(seqs):
+            for h in range(H):
+                for p in range(n_new):
+                    pid = self.alloc_page(layer, h, s)
+                    nv = min(ps, T - p * ps)
+                    jobs[j] = (s, h, pid, nv, token_start_abs + p * ps, int(p >= n_new - 4))
+                    self.valid_host[layer, h, s, pid] = nv
+                    self._token_start[layer, h, s, pid] = token_start_abs + p * ps
+                    j += 1
+            group_ptr[bi + 1] = j
+        jobs_d = torch.from_numpy(jobs).to(self.device, non_blocking=False)
+        gp_d = torch.from_numpy(group_ptr).to(self.device)
+        knobs = resolve_store_knobs(cfg, layer)
+        sp = _lib.StoreParams(k_budget=knobs.k_budget, v_budget=knobs.v_budget, joint_budget=knobs.joint_budget,
+                              joint=int(knobs.joint), store_none=int(knobs.store_none),
+                              sensitivity=knobs.sensitivity, sink_tokens=int(sink_tokens),
+                              sketch_proj=self.sketch_proj.data_ptr())
+        lib = _lib.load()
+        ws = self.workspace("store", int(lib.carekv_store_workspace_bytes(len(jobs))))
+        a = self.arena(layer)
+        _lib.check(lib.carekv_store_pages(a, sp, Kp.data_ptr(), Vp.data_ptr(), jobs_d.data_ptr(), len(jobs),
+                                          gp_d.data_ptr(), B, ws.data_ptr(), _lib.stream_ptr(self.device)),
+                   "carekv_store_pages")
+
+    def append(self, layer: int, k: torch.Tensor, v: torch.Tensor, seqs: Optional[Sequence[int]] = None):
+        """Append one decode token per listed sequence and kv head
+        (layer.py:1028-1146).  k, v: (Hkv, D) or (B, Hkv, D) fp16."""
+        cfg = self.cfg
+        if k.dim() == 2:
+            k, v = k.unsqueeze(0), v.unsqueeze(0)
+        B, H, D = k.shape
+        seqs = list(range(B)) if seqs is None else list(seqs)
+        dest = np.zeros((B * H, 4), dtype=np.int32)
+        r = 0
+        for s in seqs:
+            for h in range(H):
+                pid = self.get_open_page(layer, h, s)
+                fresh = 0
+                if pid is None:
+                    pid = self.alloc_page(layer, h, s)
+                    fresh = 1
+                    self._token_start[layer, h, s, pid] = self.total_valid_tokens(layer, h, s)
+                dest[r] = (s, h, pid, fresh)
+                self.valid_host[layer, h, s, pid] += 1
+                r += 1
+        dest_d = torch.from_numpy(dest).to(self.device)
+        kk = k.to(F16).contiguous().view(B * H, D)
+        vv = v.to(F16).contiguous().view(B * H, D)
+        lib = _lib.load()
+        _lib.check(lib.carekv_append_rows(self.arena(layer), kk.data_ptr(), vv.data_ptr(), dest_d.data_ptr(), B * H,
+                                          _lib.stream_ptr(self.device)), "carekv_append_rows")
+
+    # ------------------------------------------------------------ reads
+    def read_base_concat(self, layer: int, kv_head: int, page_ids: Optional[List[int]] = None, seq: int = 0):
+        """(K_codes int8 (N, D), K_scale fp16 (N, G), V_codes, V_scale, valid_lens)
+        for the valid rows of pages 0..n-1 (cache.py:720-772)."""
+        n = self.num_pages(layer, kv_head, seq)
+        if page_ids is not None and list(page_ids) != list(range(len(page_ids))):
+            raise NotImplementedError("read_base_concat reads a prefix of pages (0..n-1)")
+        if page_ids is not None:
+            n = len(page_ids)
+        lens = [int(x) for x in self.valid_host[layer, kv_head, seq, :n]]
+        N = sum(lens)
+        D, G = self.cfg.head_dim, self.cfg.head_dim // self.cfg.group_size
+        kc = torch.zeros(N, D, dtype=torch.int8, device=self.device)
+        vc = torch.zeros_like(kc)
+        ks = torch.zeros(N, G, dtype=F16, device=self.device)
+        vs = torch.zeros_like(ks)
+        if N:
+            rs = torch.from_numpy(np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int32)).to(self.device)
+            lib = _lib.load()
+            _lib.check(lib.carekv_read_pages(self.arena(layer), seq, kv_head, n, rs.data_ptr(), kc.data_ptr(),
+                                             ks.data_ptr(), vc.data_ptr(), vs.data_ptr(),
+                                             _lib.stream_ptr(self.device)), "carekv_read_pages")
+            torch.cuda.current_stream(self.device).synchronize()
+        return kc, ks, vc, vs, lens
+
+    def page_meta(self, layer: int, kv_head: int, page_id: int, seq: int = 0) -> Optional[PageMeta]:
+        idx = (layer, kv_head, seq, page_id)
+        if not int(self.has_meta[idx].item()):
+            return None
+        return PageMeta(page_id=page_id, layer_id=layer, kv_head=kv_head,
+                        token_start=int(self._token_start[idx]), num_tokens=int(self.valid_host[idx]),
+                        k_residual_slots=self.k_slot[idx].tolist(), v_residual_slots=self.v_slot[idx].tolist(),
+                        k_error_norm=self.k_err[idx].clone(), v_error_norm=self.v_err[idx].clone(),
+                        k_sketch=self.k_sketch[idx].clone())
+
+    @property
+    def meta_table(self):
+        """[layer][kv_head][page] -> PageMeta | None for sequence 0 (reads the device)."""
+        cfg = self.cfg
+        return [[[self.page_meta(l, h, p) for p in range(cfg.max_pages)] for h in range(cfg.num_kv_heads)]
+                for l in range(cfg.num_layers)]
+
+    def num_stored_residual_slots(self, seq: int = 0) -> Tuple[int, int]:
+        ns = self.next_slot[seq].tolist()
+        return int(ns[0]), int(ns[1])
+
+    # reference-shaped views for a single-sequence cache
+    def _view(self, t):
+        return t[:, :, 0] if self.n_seq == 1 else t
+
+    base_K_codes = property(lambda self: self._view(self.kcodes))
+    base_V_codes = property(lambda self: self._view(self.vcodes))
+    base_K_scale = property(lambda self: self._view(self.kscale))
+    base_V_scale = property(lambda self: self._view(self.vscale))
+    base_K_scale_master = property(lambda self: self._view(self.kmaster) if self.scale_mode else None)
+    base_V_scale_master = property(lambda self: self._view(self.vmaster) if self.scale_mode else None)
+    valid_tokens = property(lambda self: self._view(self.valid))
+    k_residual_buf = property(lambda self: self.k_res[0] if self.n_seq == 1 else self.k_res)
+    v_residual_buf = property(lambda self: self.v_res[0] if self.n_seq == 1 else self.v_res)
+    k_residual_scale = property(lambda self: (self.k_res_scale[0] if self.n_seq == 1 else self.k_res_scale).unsqueeze(-1))
+    v_residual_scale = property(lambda self: (self.v_res_scale[0] if self.n_seq == 1 else self.v_res_scale).unsqueeze(-1))

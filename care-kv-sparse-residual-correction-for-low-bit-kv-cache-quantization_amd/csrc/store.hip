@@ -1,0 +1,573 @@
+// Page writes (quantize + pack + int8 page scales), store-time residual
+// candidates / selection / slot packing, and single-token decode appends.
+//
+// Reference semantics (paths relative to the reference root):
+//   quantize (fp16 arithmetic)        quantizer.py:31-64
+//   INT2/3/4 packing                  quantizer.py:257-372
+//   int8 scale codes + fp16 master    cache.py:592-654, 689-695
+//   process_page                      residual_store.py:239-464
+//   4-bit residual slot packing       residual_store.py:121-136
+//   decode append + store on fill     layer.py:1028-1146
+#include "common.h"
+
+namespace carekv {
+
+struct StoreWs {  // per job: [0]=K count, [1]=V count, [2]=K base, [3]=V base
+  int32_t* v;
+};
+
+// One wave quantizes one row group: 32 fp16 values -> codes, fp16 scale.
+// fp16 chain of quantizer.py:51-59: max|x| (exact), scale=half(max/qmax),
+// code=clamp(rint(half(x/scale))), NaN (0/0 on an all-zero group) -> 0.
+template <int BITS>
+__device__ __forceinline__ _Float16 quant_group(const float* x, int* code) {
+  constexpr int qmax = (1 << (BITS - 1)) - 1;
+  float m = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) m = fmaxf(m, fabsf(x[i]));
+  const _Float16 scale = (_Float16)(m / (float)qmax);
+  const float sf = (float)scale;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    const float qh = (float)(_Float16)(x[i] / sf);
+    float r = rintf(qh);
+    r = fminf(fmaxf(r, (float)(-qmax - 1)), (float)qmax);
+    code[i] = (qh != qh) ? 0 : (int)r;
+  }
+  return scale;
+}
+
+template <int BITS>
+__device__ __forceinline__ void pack_group(const int* code, uint32_t* w) {
+#pragma unroll
+  for (int i = 0; i < BITS; ++i) w[i] = 0;
+#pragma unroll
+  for (int k = 0; k < 32; ++k) {
+    const uint32_t u = (uint32_t)code[k] & ((1u << BITS) - 1u);
+    const int bit = BITS * k;
+    w[bit >> 5] |= u << (bit & 31);
+    if ((bit & 31) + BITS > 32) w[(bit >> 5) + 1] |= u >> (32 - (bit & 31));
+  }
+}
+
+// int8 scale code of `s` against master `m` (cache.py:601-602, 692-693).
+__device__ __forceinline__ int8_t scale_code(float s, float m) {
+  const float q = s / m;
+  if (q != q) return 0;
+  return (int8_t)fminf(fmaxf(rintf(q), -128.f), 127.f);
+}
+
+// Store decision for one page: candidate order by prior (double, stable,
+// descending), prior > 0 only, per-kind budgets or joint budget
+// (residual_store.py:372-422).  sel_k/sel_v receive candidate indices in
+// slot-allocation order; returns counts.
+template <int NCG>
+__device__ __forceinline__ void select_candidates(const float* kerr, const float* verr,
+                                                  const carekv_store_params& sp, double struct_prior,
+                                                  int* sel_k, int& nk, int* sel_v, int& nv, int* order_kind,
+                                                  int* order_idx, int& n_order) {
+  double pk[NCG], pv[kVtb];
+  int ik[NCG], iv[kVtb];
+#pragma unroll
+  for (int i = 0; i < NCG; ++i) { pk[i] = (double)kerr[i] * sp.sensitivity * struct_prior; ik[i] = i; }
+#pragma unroll
+  for (int i = 0; i < kVtb; ++i) { pv[i] = (double)verr[i] * sp.sensitivity * struct_prior; iv[i] = i; }
+  // stable insertion sort, descending
+  for (int i = 1; i < NCG; ++i)
+    for (int j = i; j > 0 && pk[j] > pk[j - 1]; --j) {
+      double t = pk[j]; pk[j] = pk[j - 1]; pk[j - 1] = t;
+      int u = ik[j]; ik[j] = ik[j - 1]; ik[j - 1] = u;
+    }
+  for (int i = 1; i < kVtb; ++i)
+    for (int j = i; j > 0 && pv[j] > pv[j - 1]; --j) {
+      double t = pv[j]; pv[j] = pv[j - 1]; pv[j - 1] = t;
+      int u = iv[j]; iv[j] = iv[j - 1]; iv[j - 1] = u;
+    }
+  int pos_k = 0, pos_v = 0;
+  for (int i = 0; i < NCG; ++i) pos_k += pk[i] > 0.0;
+  for (int i = 0; i < kVtb; ++i) pos_v += pv[i] > 0.0;
+  nk = nv = n_order = 0;
+  if (sp.store_none) return;
+  if (sp.joint) {
+    // merge the two sorted positive lists, K before V on equal priors
+    int a = 0, b = 0;
+    while (n_order < sp.joint_budget && (a < pos_k || b < pos_v)) {
+      const bool take_k = (b >= pos_v) || (a < pos_k && pk[a] >= pv[b]);
+      if (take_k) { order_kind[n_order] = 0; order_idx[n_order++] = ik[a]; sel_k[nk++] = ik[a++]; }
+      else        { order_kind[n_order] = 1; order_idx[n_order++] = iv[b]; sel_v[nv++] = iv[b++]; }
+    }
+  } else {
+    const int kb = min(sp.k_budget, pos_k), vb = min(sp.v_budget, pos_v);
+    for (int i = 0; i < kb; ++i) { order_kind[n_order] = 0; order_idx[n_order++] = ik[i]; sel_k[nk++] = ik[i]; }
+    for (int i = 0; i < vb; ++i) { order_kind[n_order] = 1; order_idx[n_order++] = iv[i]; sel_v[nv++] = iv[i]; }
+  }
+}
+
+// One wave per page job.  Lane l handles token t = l / NG, quant group g = l % NG.
+// MODE 0: write base + metadata + counts.  MODE 1: write residual slots.
+template <int D, int BITS, int MODE>
+__global__ __launch_bounds__(256) void store_pages_kernel(carekv_arena A, carekv_store_params sp,
+                                                          const uint16_t* __restrict__ Kx,
+                                                          const uint16_t* __restrict__ Vx,
+                                                          const carekv_page_job* __restrict__ jobs,
+                                                          int n_jobs, StoreWs ws) {
+  constexpr int NG = D / 32;       // quant groups == K channel groups
+  constexpr int RB = row_bytes(D, BITS);
+  constexpr int CB = 4 * BITS;     // packed bytes per 32 codes
+  const int lane = threadIdx.x & 63;
+  const int job_id = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (job_id >= n_jobs) return;
+  const carekv_page_job job = jobs[job_id];
+  const int t = lane / NG, g = lane % NG;
+  const bool active = t < kPage;
+  const int nvld = job.num_valid;
+  const long pg = ((long)job.kv_head * A.n_seq + job.seq) * A.max_pages + job.page;
+
+  // ---- quantize own (t, g) group of K and V, fp16 chain
+  float xk[32], xv[32], rk[32], rv[32];
+  int ck[32], cv[32];
+  _Float16 sk = 0, sv = 0;
+  if (active) {
+    const uint16_t* kp = Kx + ((long)job_id * kPage + t) * D + g * 32;
+    const uint16_t* vp = Vx + ((long)job_id * kPage + t) * D + g * 32;
+#pragma unroll
+    for (int i = 0; i < 32; i += 8) {
+      uint4 a = *reinterpret_cast<const uint4*>(kp + i);
+      uint4 b = *reinterpret_cast<const uint4*>(vp + i);
+      const uint32_t wa[4] = {a.x, a.y, a.z, a.w}, wb[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        xk[i + 2 * j] = h2f((uint16_t)wa[j]); xk[i + 2 * j + 1] = h2f((uint16_t)(wa[j] >> 16));
+        xv[i + 2 * j] = h2f((uint16_t)wb[j]); xv[i + 2 * j + 1] = h2f((uint16_t)(wb[j] >> 16));
+      }
+    }
+    sk = quant_group<BITS>(xk, ck);
+    sv = quant_group<BITS>(xv, cv);
+    // residual against the fp16 scale (residual_store.py:276-285)
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      rk[i] = (t < nvld) ? (float)(_Float16)(xk[i] - (float)dq(ck[i], sk)) : 0.f;
+      rv[i] = (t < nvld) ? (float)(_Float16)(xv[i] - (float)dq(cv[i], sv)) : 0.f;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) { rk[i] = rv[i] = 0.f; ck[i] = cv[i] = 0; }
+  }
+
+  // ---- candidate errors (fp32): K per channel group, V per 4-token block
+  float sq_k = 0.f, sq_v = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) { sq_k += rk[i] * rk[i]; sq_v += rv[i] * rv[i]; }
+  float nrm_k = active ? sqrtf(sq_k) : 0.f;      // ||R_K[t, cg]||
+  float kerr[NG], verr[kVtb];
+  {
+    float s = nrm_k;  // sum over tokens (lanes with equal g)
+#pragma unroll
+    for (int o = NG; o < NG * kPage; o <<= 1) s += __shfl_xor(s, o, 64);
+#pragma unroll
+    for (int c = 0; c < NG; ++c) {
+      const float sc = __shfl(s, c, 64);
+      kerr[c] = nvld > 0 ? sc / (float)nvld : 0.f;
+    }
+    float tv = sq_v;  // ||R_V[t]||^2 over the row: sum over the NG lanes of token t
+#pragma unroll
+    for (int o = 1; o < NG; o <<= 1) tv += __shfl_xor(tv, o, 64);
+    const float tn = (active && t < nvld) ? sqrtf(tv) : 0.f;
+#pragma unroll
+    for (int b = 0; b < kVtb; ++b) {
+      float acc = 0.f;
+      for (int i = 0; i < kVtb; ++i) acc += __shfl(tn, (b * kVtb + i) * NG, 64);
+      const int t0 = b * kVtb, t1 = min(t0 + kVtb, nvld);
+      verr[b] = t1 > t0 ? acc / (float)(t1 - t0) : 0.f;
+    }
+  }
+  double struct_prior = 1.0;
+  if (job.is_recent) struct_prior *= 1.5;
+  if (job.token_start < sp.sink_tokens) struct_prior *= 2.0;
+  int sel_k[NG], sel_v[kVtb], okind[NG + kVtb], oidx[NG + kVtb], nk, nv, nord;
+  select_candidates<NG>(kerr, verr, sp, struct_prior, sel_k, nk, sel_v, nv, okind, oidx, nord);
+
+  if (MODE == 0) {
+    // ---- packed base codes
+    if (active) {
+      uint32_t w[BITS];
+      pack_group<BITS>(ck, w);
+      store_bytes<CB>(A.kcodes + (pg * kPage + t) * RB + g * CB, w);
+      pack_group<BITS>(cv, w);
+      store_bytes<CB>(A.vcodes + (pg * kPage + t) * RB + g * CB, w);
+    }
+    // ---- scales
+    if (A.scale_mode == 1) {
+      const float mk = wave_max(active ? (float)sk : 0.f);
+      const float mv = wave_max(active ? (float)sv : 0.f);
+      const _Float16 mkh = (_Float16)(mk / 127.f), mvh = (_Float16)(mv / 127.f);
+      const int8_t qk = scale_code((float)sk, (float)mkh), qv = scale_code((float)sv, (float)mvh);
+      if (active) {
+        ((int8_t*)A.kscale)[(pg * kPage + t) * NG + g] = qk;
+        ((int8_t*)A.vscale)[(pg * kPage + t) * NG + g] = qv;
+      }
+      // V_hat as read back from the cache: half(code * half(scode * master))
+      const _Float16 svr = (_Float16)((float)qv * (float)mvh);
+      float vs = 0.f;
+      if (active && t < nvld) {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) { const float vh = (float)dq(cv[i], svr); vs += vh * vh; }
+      }
+      vs = wave_sum(vs);
+      if (lane == 0) {
+        A.kmaster[pg] = half2bits(mkh);
+        A.vmaster[pg] = half2bits(mvh);
+        A.v_sq[pg] = vs;
+      }
+    } else {
+      if (active) {
+        ((uint16_t*)A.kscale)[(pg * kPage + t) * NG + g] = half2bits(sk);
+        ((uint16_t*)A.vscale)[(pg * kPage + t) * NG + g] = half2bits(sv);
+      }
+      float vs = 0.f;
+      if (active && t < nvld) {
+#pragma unroll
+        for (int i = 0; i < 32; ++i) { const float vh = (float)dq(cv[i], sv); vs += vh * vh; }
+      }
+      vs = wave_sum(vs);
+      if (lane == 0) A.v_sq[pg] = vs;
+    }
+    // ---- K sketch: half(mean_t R_K[t, cg] @ P)  (residual_store.py:305,311-312)
+    {
+      float mean[32];
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        float s = rk[i];
+#pragma unroll
+        for (int o = NG; o < NG * kPage; o <<= 1) s += __shfl_xor(s, o, 64);
+        mean[i] = nvld > 0 ? s / (float)nvld : 0.f;
+      }
+      const int SD = A.sketch_dim;
+      for (int k = t; k < SD; k += kPage) {
+        if (!active) break;
+        float acc = 0.f;
+#pragma unroll
+        for (int c = 0; c < 32; ++c) acc += mean[c] * sp.sketch_proj[c * SD + k];
+        A.k_sketch[(pg * NG + g) * SD + k] = f2h(acc);
+      }
+    }
+    if (lane < NG) A.k_err[pg * NG + lane] = f2h(kerr[lane]);
+    if (lane < kVtb) A.v_err[pg * kVtb + lane] = f2h(verr[lane]);
+    if (lane == 0) {
+      A.valid[pg] = nvld;
+      A.has_meta[pg] = 1;
+      ws.v[job_id * 4 + 0] = nk;
+      ws.v[job_id * 4 + 1] = nv;
+    }
+  } else {
+    // ---- residual slots at the scanned bases (residual_store.py:424-438)
+    const int base_k = ws.v[job_id * 4 + 2], base_v = ws.v[job_id * 4 + 3];
+    const long seq_off = (long)job.seq * A.n_slots;
+    constexpr int KSB = kPage * 32 / 2;     // 16 tokens x 32 channels, 4-bit
+    const int VSB = kVtb * D / 2;
+    int kslot_of[NG], vslot_of[kVtb];
+#pragma unroll
+    for (int c = 0; c < NG; ++c) kslot_of[c] = -1;
+#pragma unroll
+    for (int b = 0; b < kVtb; ++b) vslot_of[b] = -1;
+    // slot ids past the arena are dropped (never written) and flagged
+    for (int i = 0; i < nk; ++i) {
+      if (base_k + i < A.n_slots) kslot_of[sel_k[i]] = base_k + i;
+      else if (lane == 0) ws.v[n_jobs * 4] = 1;
+    }
+    for (int i = 0; i < nv; ++i) {
+      if (base_v + i < A.n_slots) vslot_of[sel_v[i]] = base_v + i;
+      else if (lane == 0) ws.v[n_jobs * 4] = 1;
+    }
+    // K payload of channel group g: pack_4bit(R_K[:, cg]) over all 16 rows
+    {
+      float m = 0.f;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) m = fmaxf(m, fabsf(rk[i]));
+#pragma unroll
+      for (int o = NG; o < NG * kPage; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+      const float s = fmaxf(m, 1e-8f) / 7.0f;
+      const int slot = kslot_of[g];
+      if (active && slot >= 0) {
+        uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+          const int c = (int)fminf(fmaxf(rintf(rk[i] / s), -8.f), 7.f);
+          w[i >> 3] |= ((uint32_t)c & 15u) << (4 * (i & 7));
+        }
+        int8_t* dst = A.k_res + (seq_off + slot) * KSB + t * 16;
+        *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+        if (t == 0) A.k_res_scale[seq_off + slot] = f2h(s);
+      }
+    }
+    // V payload of block t/4: pack_4bit(R_V[4b..4b+3, :])
+    {
+      float m = 0.f;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) m = fmaxf(m, fabsf(rv[i]));
+#pragma unroll
+      for (int o = 1; o < NG * kVtb; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+      const float s = fmaxf(m, 1e-8f) / 7.0f;
+      const int b = t / kVtb;
+      const int slot = active ? vslot_of[b] : -1;
+      if (slot >= 0) {
+        uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int i = 0; i < 32; ++i) {
+          const int c = (int)fminf(fmaxf(rintf(rv[i] / s), -8.f), 7.f);
+          w[i >> 3] |= ((uint32_t)c & 15u) << (4 * (i & 7));
+        }
+        int8_t* dst = A.v_res + (seq_off + slot) * VSB + (t - b * kVtb) * (D / 2) + g * 16;
+        *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
+        if (t == b * kVtb && g == 0) A.v_res_scale[seq_off + slot] = f2h(s);
+      }
+    }
+    if (lane < NG) A.k_slot[pg * NG + lane] = kslot_of[lane];
+    if (lane < kVtb) A.v_slot[pg * kVtb + lane] = vslot_of[lane];
+  }
+}
+
+// Exclusive scan of per-job slot counts inside each sequence group (jobs of
+// one group are contiguous and ordered like the reference's process_page
+// calls); bases start at next_slot[seq], which is advanced.
+__global__ __launch_bounds__(256) void store_scan_kernel(carekv_arena A, const carekv_page_job* __restrict__ jobs,
+                                                         const int32_t* __restrict__ group_ptr, StoreWs ws) {
+  __shared__ int sk[256], sv[256];
+  __shared__ int carry_k, carry_v;
+  const int g = blockIdx.x;
+  const int j0 = group_ptr[g], j1 = group_ptr[g + 1];
+  if (j1 <= j0) return;
+  const int seq = jobs[j0].seq;
+  if (threadIdx.x == 0) { carry_k = A.next_slot[2 * seq]; carry_v = A.next_slot[2 * seq + 1]; }
+  __syncthreads();
+  for (int base = j0; base < j1; base += 256) {
+    const int j = base + threadIdx.x;
+    const int ck = j < j1 ? ws.v[j * 4] : 0, cv = j < j1 ? ws.v[j * 4 + 1] : 0;
+    sk[threadIdx.x] = ck; sv[threadIdx.x] = cv;
+    __syncthreads();
+    for (int o = 1; o < 256; o <<= 1) {   // Hillis-Steele inclusive scan
+      const int ak = threadIdx.x >= o ? sk[threadIdx.x - o] : 0;
+      const int av = threadIdx.x >= o ? sv[threadIdx.x - o] : 0;
+      __syncthreads();
+      sk[threadIdx.x] += ak; sv[threadIdx.x] += av;
+      __syncthreads();
+    }
+    if (j < j1) {
+      ws.v[j * 4 + 2] = carry_k + sk[threadIdx.x] - ck;
+      ws.v[j * 4 + 3] = carry_v + sv[threadIdx.x] - cv;
+    }
+    __syncthreads();
+    if (threadIdx.x == 255) { carry_k += sk[255]; carry_v += sv[255]; }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) { A.next_slot[2 * seq] = carry_k; A.next_slot[2 * seq + 1] = carry_v; }
+}
+
+// Decode append: one wave per (row); lane g < D/32 quantizes group g.
+template <int D, int BITS>
+__global__ __launch_bounds__(256) void append_rows_kernel(carekv_arena A, const uint16_t* __restrict__ Kx,
+                                                          const uint16_t* __restrict__ Vx,
+                                                          const int32_t* __restrict__ dest, int n_rows) {
+  constexpr int NG = D / 32;
+  constexpr int RB = row_bytes(D, BITS);
+  constexpr int CB = 4 * BITS;
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= n_rows) return;
+  const int seq = dest[row * 4], kvh = dest[row * 4 + 1], page = dest[row * 4 + 2], fresh = dest[row * 4 + 3];
+  const long pg = ((long)kvh * A.n_seq + seq) * A.max_pages + page;
+  const int off = fresh ? 0 : A.valid[pg];
+  if (off >= kPage) return;  // caller contract violated; never write past the page
+  if (lane < NG) {
+    const int g = lane;
+    float xk[32], xv[32];
+    int ck[32], cv[32];
+    for (int i = 0; i < 32; ++i) {
+      xk[i] = h2f(Kx[(long)row * D + g * 32 + i]);
+      xv[i] = h2f(Vx[(long)row * D + g * 32 + i]);
+    }
+    const _Float16 sk = quant_group<BITS>(xk, ck), sv = quant_group<BITS>(xv, cv);
+    uint32_t w[BITS];
+    pack_group<BITS>(ck, w);
+    store_bytes<CB>(A.kcodes + (pg * kPage + off) * RB + g * CB, w);
+    pack_group<BITS>(cv, w);
+    store_bytes<CB>(A.vcodes + (pg * kPage + off) * RB + g * CB, w);
+    if (A.scale_mode == 1) {
+      const float mk = fmaxf(fresh ? 0.f : h2f(A.kmaster[pg]), 1e-8f);
+      const float mv = fmaxf(fresh ? 0.f : h2f(A.vmaster[pg]), 1e-8f);
+      ((int8_t*)A.kscale)[(pg * kPage + off) * NG + g] = scale_code((float)sk, mk);
+      ((int8_t*)A.vscale)[(pg * kPage + off) * NG + g] = scale_code((float)sv, mv);
+    } else {
+      ((uint16_t*)A.kscale)[(pg * kPage + off) * NG + g] = half2bits(sk);
+      ((uint16_t*)A.vscale)[(pg * kPage + off) * NG + g] = half2bits(sv);
+    }
+  }
+  const bool full = off + 1 == kPage;
+  if (lane == 0) {
+    A.valid[pg] = off + 1;
+    if (fresh) {
+      if (A.scale_mode == 1) { A.kmaster[pg] = 0; A.vmaster[pg] = 0; }
+      A.has_meta[pg] = full ? 1 : 0;
+    }
+    if (full) { A.has_meta[pg] = 1; A.v_sq[pg] = 0.f; }
+  }
+  if (full) {
+    // store on page fill with K_orig = K_hat: zero residual -> no slots,
+    // zero errors, zero sketch (layer.py:1088-1146)
+    if (lane < NG) { A.k_slot[pg * NG + lane] = -1; A.k_err[pg * NG + lane] = 0; }
+    if (lane < kVtb) { A.v_slot[pg * kVtb + lane] = -1; A.v_err[pg * kVtb + lane] = 0; }
+    for (int i = lane; i < NG * A.sketch_dim; i += 64) A.k_sketch[pg * NG * A.sketch_dim + i] = 0;
+  }
+}
+
+// read_base_concat for one (seq, kv head): unpacked codes + fp16 scales.
+template <int D, int BITS>
+__global__ __launch_bounds__(256) void read_pages_kernel(carekv_arena A, int seq, int kvh, int n_pages,
+                                                         const int32_t* __restrict__ row_start, int8_t* kc,
+                                                         uint16_t* ks, int8_t* vc, uint16_t* vs) {
+  constexpr int NG = D / 32;
+  constexpr int RB = row_bytes(D, BITS);
+  constexpr int CB = 4 * BITS;
+  const int p = blockIdx.x;
+  if (p >= n_pages) return;
+  const long pg = ((long)kvh * A.n_seq + seq) * A.max_pages + p;
+  const int n = A.valid[pg];
+  const int r0 = row_start[p];
+  for (int idx = threadIdx.x; idx < n * NG; idx += blockDim.x) {
+    const int t = idx / NG, g = idx % NG;
+    const long out_row = r0 + t;
+#pragma unroll
+    for (int which = 0; which < 2; ++which) {
+      const int8_t* src = (which ? A.vcodes : A.kcodes) + (pg * kPage + t) * RB + g * CB;
+      uint32_t w[BITS];
+      load_bytes<CB>(w, src);
+      int8_t* dst = (which ? vc : kc) + out_row * D + g * 32;
+      for (int i = 0; i < 32; ++i) dst[i] = (int8_t)get_code<BITS>(w, i);
+      uint16_t s;
+      if (A.scale_mode == 1) {
+        const int8_t q = ((const int8_t*)(which ? A.vscale : A.kscale))[(pg * kPage + t) * NG + g];
+        const uint16_t m = which ? A.vmaster[pg] : A.kmaster[pg];
+        s = f2h((float)q * h2f(m));
+      } else {
+        s = ((const uint16_t*)(which ? A.vscale : A.kscale))[(pg * kPage + t) * NG + g];
+      }
+      (which ? vs : ks)[out_row * NG + g] = s;
+    }
+  }
+}
+
+// Row quantizer API (quantizer.py:31-64 + pack_codes_2d).
+template <int BITS>
+__global__ void quantize_rows_kernel(const uint16_t* __restrict__ x, int rows, int D, int pack, int8_t* codes,
+                                     uint16_t* scale) {
+  const int G = D / 32;
+  const int id = blockIdx.x * blockDim.x + threadIdx.x;
+  if (id >= rows * G) return;
+  const int r = id / G, g = id % G;
+  float v[32];
+  int c[32];
+  for (int i = 0; i < 32; ++i) v[i] = h2f(x[(long)r * D + g * 32 + i]);
+  const _Float16 s = quant_group<BITS>(v, c);
+  scale[id] = half2bits(s);
+  if (pack) {
+    uint32_t w[BITS];
+    pack_group<BITS>(c, w);
+    int8_t* dst = codes + (long)r * row_bytes(D, BITS) + g * 4 * BITS;
+    for (int i = 0; i < 4 * BITS; ++i) dst[i] = (int8_t)(w[i >> 2] >> (8 * (i & 3)));
+  } else {
+    for (int i = 0; i < 32; ++i) codes[(long)r * D + g * 32 + i] = (int8_t)c[i];
+  }
+}
+
+}  // namespace carekv
+
+// ------------------------------------------------------------------ host side
+#include "host_util.h"
+
+using namespace carekv;
+
+extern "C" int64_t carekv_store_workspace_bytes(int32_t n_jobs) { return (int64_t)n_jobs * 16 + 16; }
+
+template <int D, int BITS>
+static int launch_store(const carekv_arena& A, const carekv_store_params& sp, const uint16_t* K, const uint16_t* V,
+                        const carekv_page_job* jobs, int n_jobs, const int32_t* group_ptr, int n_groups,
+                        StoreWs ws, hipStream_t s) {
+  const int blocks = (n_jobs + 3) / 4;
+  hipLaunchKernelGGL((store_pages_kernel<D, BITS, 0>), dim3(blocks), dim3(256), 0, s, A, sp, K, V, jobs, n_jobs, ws);
+  CAREKV_CHECK_LAUNCH("store_pages(count)");
+  hipLaunchKernelGGL(store_scan_kernel, dim3(n_groups), dim3(256), 0, s, A, jobs, group_ptr, ws);
+  CAREKV_CHECK_LAUNCH("store_scan");
+  hipLaunchKernelGGL((store_pages_kernel<D, BITS, 1>), dim3(blocks), dim3(256), 0, s, A, sp, K, V, jobs, n_jobs, ws);
+  CAREKV_CHECK_LAUNCH("store_pages(write)");
+  return CAREKV_OK;
+}
+
+extern "C" int carekv_store_pages(const carekv_arena* arena, const carekv_store_params* sp, const uint16_t* K,
+                                  const uint16_t* V, const carekv_page_job* jobs_dev, int32_t n_jobs,
+                                  const int32_t* group_ptr_dev, int32_t n_groups, void* workspace,
+                                  void* stream) {
+  CAREKV_REQUIRE(arena && sp && K && V && jobs_dev && group_ptr_dev && workspace, "null argument");
+  CAREKV_REQUIRE(n_jobs >= 0 && n_groups >= 0, "negative sizes");
+  if (n_jobs == 0) return CAREKV_OK;
+  const carekv_arena& A = *arena;
+  CAREKV_REQUIRE(check_arena(A), last_error_buf());
+  CAREKV_REQUIRE(A.residual_bits == 4, "kernels support residual_bits=4");
+  CAREKV_REQUIRE(sp->sketch_proj != nullptr, "sketch_proj is required");
+  StoreWs ws{(int32_t*)workspace};
+  hipStream_t s = (hipStream_t)stream;
+  return dispatch_db(A.head_dim, A.base_bits, [&](auto d, auto b) {
+    return launch_store<decltype(d)::value, decltype(b)::value>(A, *sp, K, V, jobs_dev, n_jobs, group_ptr_dev,
+                                                                n_groups, ws, s);
+  });
+}
+
+extern "C" int carekv_append_rows(const carekv_arena* arena, const uint16_t* k_rows, const uint16_t* v_rows,
+                                  const int32_t* dest_dev, int32_t n_rows, void* stream) {
+  CAREKV_REQUIRE(arena && k_rows && v_rows && dest_dev, "null argument");
+  if (n_rows <= 0) return CAREKV_OK;
+  const carekv_arena& A = *arena;
+  CAREKV_REQUIRE(check_arena(A), last_error_buf());
+  hipStream_t s = (hipStream_t)stream;
+  return dispatch_db(A.head_dim, A.base_bits, [&](auto d, auto b) {
+    hipLaunchKernelGGL((append_rows_kernel<decltype(d)::value, decltype(b)::value>), dim3((n_rows + 3) / 4),
+                       dim3(256), 0, s, A, k_rows, v_rows, dest_dev, n_rows);
+    CAREKV_CHECK_LAUNCH("append_rows");
+    return CAREKV_OK;
+  });
+}
+
+extern "C" int carekv_read_pages(const carekv_arena* arena, int32_t seq, int32_t kv_head, int32_t n_pages,
+                                 const int32_t* row_start_dev, int8_t* kc, uint16_t* ks, int8_t* vc, uint16_t* vs,
+                                 void* stream) {
+  CAREKV_REQUIRE(arena && row_start_dev && kc && ks && vc && vs, "null argument");
+  const carekv_arena& A = *arena;
+  CAREKV_REQUIRE(check_arena(A), last_error_buf());
+  CAREKV_REQUIRE(seq >= 0 && seq < A.n_seq && kv_head >= 0 && kv_head < A.n_kv_heads, "seq/kv_head out of range");
+  CAREKV_REQUIRE(n_pages >= 0 && n_pages <= A.max_pages, "n_pages out of range");
+  if (n_pages == 0) return CAREKV_OK;
+  hipStream_t s = (hipStream_t)stream;
+  return dispatch_db(A.head_dim, A.base_bits, [&](auto d, auto b) {
+    hipLaunchKernelGGL((read_pages_kernel<decltype(d)::value, decltype(b)::value>), dim3(n_pages), dim3(64), 0, s,
+                       A, seq, kv_head, n_pages, row_start_dev, kc, ks, vc, vs);
+    CAREKV_CHECK_LAUNCH("read_pages");
+    return CAREKV_OK;
+  });
+}
+
+extern "C" int carekv_quantize_rows(const uint16_t* x, int32_t rows, int32_t D, int32_t bits, int32_t group,
+                                    int32_t pack, int8_t* codes, uint16_t* scale, void* stream) {
+  CAREKV_REQUIRE(x && codes && scale, "null argument");
+  CAREKV_REQUIRE(group == 32 && D % 32 == 0 && D > 0, "kernels support group_size=32 and D % 32 == 0");
+  CAREKV_REQUIRE(bits >= 2 && bits <= 4, "bits must be 2, 3 or 4");
+  if (rows <= 0) return CAREKV_OK;
+  hipStream_t s = (hipStream_t)stream;
+  const int n = rows * (D / 32);
+  const int blocks = (n + 255) / 256;
+  switch (bits) {
+    case 2: hipLaunchKernelGGL(quantize_rows_kernel<2>, dim3(blocks), dim3(256), 0, s, x, rows, D, pack, codes, scale); break;
+    case 3: hipLaunchKernelGGL(quantize_rows_kernel<3>, dim3(blocks), dim3(256), 0, s, x, rows, D, pack, codes, scale); break;
+    default: hipLaunchKernelGGL(quantize_rows_kernel<4>, dim3(blocks), dim3(256), 0, s, x, rows, D, pack, codes, scale); break;
+  }
+  CAREKV_CHECK_LAUNCH("quantize_rows");
+  return CAREKV_OK;
+}

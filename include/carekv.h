@@ -1,0 +1,174 @@
+/*
+ * carekv.h -- C ABI of the MI355X-native CARE-KV quantized decode-attention
+ * path (libcarekv_hip.so, HIP kernels built for gfx950).
+ *
+ * The reference (soeunida/CARE-KV-..., a PyTorch prototype) has no FFI; each
+ * entry point below replaces the Python functions named in its comment
+ * (paths relative to the reference root).  All functions return 0 on
+ * success or a negative code; carekv_last_error() returns the message of the
+ * last failure on the calling thread.  Every pointer is a device pointer
+ * unless stated otherwise; work is enqueued on `stream` (a hipStream_t) and
+ * nothing synchronises with the host.
+ */
+#ifndef CAREKV_H_
+#define CAREKV_H_
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define CAREKV_OK 0
+#define CAREKV_EINVAL -1   /* bad shape / unsupported configuration      */
+#define CAREKV_ELAUNCH -2  /* HIP launch or runtime error                */
+#define CAREKV_ESPACE -3   /* workspace or slot arena too small          */
+
+/* Paged cache of one layer, shared by all sequence slots.  Layout mirrors
+ * CAREKVCache._init_buffers (cache.py:430-536) with the sequence slot as an
+ * extra dimension next to the kv head:
+ *   page index pg = (kv_head * n_seq + seq) * max_pages + page
+ *   kcodes/vcodes  int8   [pg][page_size][row_bytes]   packed base codes
+ *   kscale/vscale  int8   [pg][page_size][G]  (scale_mode 1: int8 codes)
+ *                  fp16   [pg][page_size][G]  (scale_mode 0: raw fp16)
+ *   kmaster/vmaster fp16  [pg]                 per-page master scale
+ *   valid          int32  [pg]                 valid tokens per page
+ *   has_meta       int8   [pg]                 PageMeta present (cache.py:530)
+ *   k_slot         int32  [pg][D/kcg]          K residual slot id or -1
+ *   v_slot         int32  [pg][page/vtb]       V residual slot id or -1
+ *   k_err/v_err    fp16   [pg][..]             PageMeta.k/v_error_norm
+ *   k_sketch       fp16   [pg][D/kcg][sketch]  PageMeta.k_sketch
+ *   v_sq           fp32   [pg]                 sum of V_hat^2 over valid rows
+ *   k_res/v_res    int8   [n_seq][n_slots][slot_bytes] residual slot arena
+ *   k_res_scale/v_res_scale fp16 [n_seq][n_slots]
+ *   next_slot      int32  [n_seq][2]           next free K / V slot id
+ * Slot arenas are per sequence and shared by all layers of that sequence,
+ * like the reference's per-sequence k_residual_buf (cache.py:522-527). */
+typedef struct carekv_arena {
+  int8_t* kcodes;
+  int8_t* vcodes;
+  void* kscale;
+  void* vscale;
+  uint16_t* kmaster;
+  uint16_t* vmaster;
+  int32_t* valid;
+  int8_t* has_meta;
+  int32_t* k_slot;
+  int32_t* v_slot;
+  uint16_t* k_err;
+  uint16_t* v_err;
+  uint16_t* k_sketch;
+  float* v_sq;
+  int8_t* k_res;
+  uint16_t* k_res_scale;
+  int8_t* v_res;
+  uint16_t* v_res_scale;
+  int32_t* next_slot;
+  int32_t n_seq, n_kv_heads, max_pages, head_dim, base_bits, page_size, group_size;
+  int32_t k_channel_group, v_token_block, sketch_dim, scale_mode, residual_bits, n_slots;
+} carekv_arena;
+
+/* Store-time knobs, resolved on the host from CacheConfig and the
+ * CAREKV_STORE_* environment (residual_store.py:104-114,379-422). */
+typedef struct carekv_store_params {
+  int32_t k_budget;        /* per-page K slots to keep (after mode/ratio/floor) */
+  int32_t v_budget;        /* per-page V slots to keep                          */
+  int32_t joint_budget;    /* joint store policy budget                         */
+  int32_t joint;           /* 1: CAREKV_STORE_POLICY=joint                      */
+  int32_t store_none;      /* 1: ratio budgets all <= 0 -> store nothing        */
+  double sensitivity;      /* cfg.layer_sensitivity[layer]                      */
+  int32_t sink_tokens;     /* prefill: is_sink = token_start < sink_tokens      */
+  const float* sketch_proj;/* [k_channel_group][sketch_dim] fp32 (get_sketch_proj) */
+} carekv_store_params;
+
+/* One page write (prefill).  X rows for page j are X[j*page_size .. +page_size),
+ * zero padded past num_valid (layer.py:254-271). */
+typedef struct carekv_page_job {
+  int32_t seq, kv_head, page, num_valid;
+  int32_t token_start;     /* absolute position of the first row              */
+  int32_t is_recent;       /* layer.py:275: p >= num_pages - 4                 */
+} carekv_page_job;
+
+/* Replaces CAREKVLayer._write_pages_for_kv_head's uniform branch
+ * (layer.py:254-332): quantize + pack + int8 scales (quantizer.py:31-64,
+ * 304-372; cache.py:592-654), then ResidualStoreManager.process_page
+ * (residual_store.py:239-464) with deterministic slot ids (ascending in
+ * job order, like the reference free-list pop(0), cache.py:548-560).
+ * K, V: fp16 [n_jobs*page_size][head_dim].  Jobs are grouped by sequence:
+ * group g is jobs [group_ptr[g], group_ptr[g+1]) (device int32 array), all of
+ * one sequence and in the reference's call order (kv head major, page
+ * minor).  workspace must hold carekv_store_workspace_bytes(n_jobs) bytes. */
+int carekv_store_pages(const carekv_arena* arena, const carekv_store_params* sp,
+                       const uint16_t* K, const uint16_t* V, const carekv_page_job* jobs_dev,
+                       int32_t n_jobs, const int32_t* group_ptr_dev, int32_t n_groups,
+                       void* workspace, void* stream);
+int64_t carekv_store_workspace_bytes(int32_t n_jobs);
+
+/* One decode-token append per row (layer.py:1028-1146, cache.py:656-701):
+ * quantize the row, pack it at (seq, kv_head, page, valid[pg]), encode its
+ * scales against the page's fixed master (clamped at 1e-8), bump valid, and
+ * when the page becomes full write its PageMeta with the store run on
+ * K_orig = K_hat (zero residual: no slots, zero errors and sketches).
+ * dest_dev: int32 [n_rows][4] = (seq, kv_head, page, fresh); fresh=1 marks
+ * a page just allocated by the caller (layer.py:1029-1035): it starts empty
+ * with a zero master and no metadata, like the reference's zeroed buffers. */
+int carekv_append_rows(const carekv_arena* arena, const uint16_t* k_rows, const uint16_t* v_rows,
+                       const int32_t* dest_dev, int32_t n_rows, void* stream);
+
+/* Decode attention + comb+ex residual correction.  Replaces, per sequence
+ * and kv head, CAREKVCache.read_base_concat (cache.py:720-772) + dequantize
+ * (quantizer.py:67-82) + base attention (attention.py:1009-1022) +
+ * vectorized_joint_correction (attention.py:576-957, KSCORE_LIVE=1) over the
+ * kv head's query heads, output half(O_base + dO) (attention.py:1036-1039). */
+typedef struct carekv_decode_params {
+  int32_t batch;           /* rows of q / out                                  */
+  int32_t n_heads;         /* query heads; kv head = h / (n_heads/n_kv_heads)   */
+  const int32_t* seq_slot; /* device [batch]: arena sequence slot of each row   */
+  const int32_t* n_pages;  /* device [batch]: pages in use (page ids 0..n-1)    */
+  int32_t max_pages_used;  /* host upper bound of n_pages[]                     */
+  float sm_scale;          /* fp32(1/sqrt(head_dim))                            */
+  float sensitivity;       /* cfg.layer_sensitivity[layer]                      */
+  int32_t correction;      /* 0: base attention only                            */
+  int32_t kind;            /* 0 both, 1 k, 2 v   (CAREKV_PREFILL_RESIDUAL_KIND) */
+  int32_t joint;           /* 1 joint, 0 separate (route_policy)                */
+  int32_t normalize;       /* CAREKV_SCORE_NORMALIZE                            */
+  int32_t k_exact;         /* CAREKV_K_CORRECTION_MODE: 1 exact, 0 linear       */
+  float k_corr_scale;      /* CAREKV_K_CORRECTION_SCALE (linear mode)           */
+  float lambda_k, lambda_v;/* CAREKV_KSCORE_LAMBDA_K/V                          */
+  int32_t budget_ratio;    /* 0 absolute (abs_k/abs_v), 1 ratio (ratio_k/v)     */
+  int32_t abs_k, abs_v;    /* _resolve_read_budgets, multiplier applied         */
+  double ratio_k, ratio_v;
+  int32_t k_cap, v_cap;    /* max stored K / V slots per page                   */
+  int32_t split_pages;     /* pages per work-group in the streaming pass        */
+} carekv_decode_params;
+
+/* q, out: fp16 [batch][n_heads][head_dim].  diag (optional, NULL to skip):
+ * int32 [batch][n_heads][diag_cap] selected candidates, each encoded
+ * kind<<30 | page<<3 | sub (kind 0 = K with sub = channel group,
+ * 1 = V with sub = token block), sorted ascending, -1 padded. */
+int carekv_decode_attn(const carekv_arena* arena, const carekv_decode_params* dp, const uint16_t* q,
+                       uint16_t* out, void* workspace, int64_t workspace_bytes, int32_t* diag,
+                       int32_t diag_cap, void* stream);
+int64_t carekv_decode_workspace_bytes(const carekv_arena* arena, const carekv_decode_params* dp);
+
+/* read_base_concat (cache.py:720-772) for one (seq, kv_head): unpacked int8
+ * codes [N][D] and fp16 scales [N][G] of the valid rows of pages 0..n_pages-1
+ * (int8 scales expanded as half(code * master)).  row_start_dev: int32
+ * [n_pages] exclusive prefix of valid[] (host computed). */
+int carekv_read_pages(const carekv_arena* arena, int32_t seq, int32_t kv_head, int32_t n_pages,
+                      const int32_t* row_start_dev, int8_t* kc, uint16_t* ks, int8_t* vc,
+                      uint16_t* vs, void* stream);
+
+/* Symmetric per-group quantizer on fp16 rows (quantizer.py:31-64, fp16
+ * arithmetic) with optional bit packing (quantizer.py:364-372).
+ * x fp16 [rows][D]; codes int8 [rows][D] (or packed [rows][row_bytes] when
+ * pack != 0); scale fp16 [rows][D/group]. */
+int carekv_quantize_rows(const uint16_t* x, int32_t rows, int32_t D, int32_t bits, int32_t group,
+                         int32_t pack, int8_t* codes, uint16_t* scale, void* stream);
+
+const char* carekv_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* CAREKV_H_ */

@@ -1,0 +1,112 @@
+"""Shared helpers for the parity tests (not collected by pytest)."""
+from __future__ import annotations
+
+import math
+import os
+
+import numpy as np
+
+from oracle import quant as Q
+from oracle.attention import decode_attention as oracle_decode
+from oracle.cache import OCache, OCfg
+from oracle.store import decode_append, write_pages_for_kv_head
+
+F16, F32 = np.float16, np.float32
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+# decode golden cases written by tests/golden/make_golden.py
+DECODE_CASES = {
+    "c1": dict(Hq=32, Hkv=4, D=64, store=dict(store_budget_mode="ratio", store_budget_ratio=0.03), k_mode="exact"),
+    "c1_tight": dict(Hq=32, Hkv=4, D=64, store=dict(store_budget_mode="ratio", store_budget_ratio=0.03), k_mode="exact"),
+    "gqa4_d128": dict(Hq=8, Hkv=2, D=128, store=dict(store_budget_mode="absolute", store_abs_k=2, store_abs_v=4),
+                      k_mode="exact"),
+    "mha_d128_linear": dict(Hq=2, Hkv=2, D=128, store=dict(store_budget_mode="ratio", store_budget_ratio=0.03),
+                            k_mode="linear"),
+}
+
+PAPER_ENV = dict(CAREKV_STORE_POLICY="residual_kind_aware", CAREKV_PREFILL_RESIDUAL_KIND="both",
+                 CAREKV_KSCORE_LIVE="1", CAREKV_SCORE_NORMALIZE="1", CAREKV_K_CORRECTION_SCALE="0.1")
+
+
+def load_golden(name):
+    return dict(np.load(os.path.join(GOLDEN, name), allow_pickle=False))
+
+
+def case_cfg_kwargs(g, spec):
+    T = int(g["T"])
+    return dict(num_layers=1, num_heads=spec["Hq"], num_kv_heads=spec["Hkv"], head_dim=spec["D"], page_size=16,
+                max_pages=max(T // 16 + 4, 400), base_bits=3, group_size=32, k_channel_group=32, v_token_block=4,
+                sketch_dim=32, read_budget_mode="absolute", read_abs_k=int(g["read_k"]), read_abs_v=int(g["read_v"]),
+                route_policy="joint", **spec["store"])
+
+
+def build_oracle_case(g, name):
+    spec = DECODE_CASES[name]
+    c = OCache(OCfg(**case_cfg_kwargs(g, spec)))
+    T, n_app = int(g["T"]), int(g["n_append"])
+    for h in range(spec["Hkv"]):
+        write_pages_for_kv_head(c, 0, h, g["K"][h, :T], g["V"][h, :T], token_start_abs=0, sink_tokens=4)
+    for t in range(T, T + n_app):
+        decode_append(c, 0, g["K"][:, t], g["V"][:, t])
+    return c, spec
+
+
+def oracle_candidates(oc, layer, h, n_pages):
+    """Candidate ids (kind, page, sub) in the reference's index order."""
+    cfg = oc.cfg
+    K, V = [], []
+    for p in range(n_pages):
+        m = oc.meta_table[layer][h][p]
+        nv = int(oc.valid_tokens[layer, h, p])
+        if nv == 0 or m is None:
+            continue
+        for cg, s in enumerate(m.k_residual_slots):
+            if s >= 0:
+                K.append((0, p, cg))
+        for vb, s in enumerate(m.v_residual_slots):
+            if s >= 0 and vb * cfg.v_token_block < nv:
+                V.append((1, p, vb))
+    return K, V
+
+
+def decode_diag(code_row):
+    out = []
+    for x in code_row:
+        x = int(x)
+        if x < 0:
+            break
+        out.append((x >> 30, (x >> 3) & ((1 << 27) - 1), x & 7))
+    return out
+
+
+def oracle_selection(diag_h, Kc, Vc):
+    """Per query row: set of selected candidate ids from the oracle diag."""
+    rows = []
+    sk, sv = diag_h["sel_k"], diag_h["sel_v"]
+    for j in range(sk.shape[0] if sk is not None else sv.shape[0]):
+        s = set()
+        if sk is not None:
+            s |= {Kc[i] for i in np.nonzero(sk[j])[0]}
+        if sv is not None:
+            s |= {Vc[i] for i in np.nonzero(sv[j])[0]}
+        rows.append(s)
+    return rows
+
+
+def ties_explain(mine: set, ref: set, diag_h, Kc, Vc, j, eps=1e-4):
+    """True if every disagreement is between candidates whose normalised
+    scores sit within eps (relative) of the selection boundary."""
+    if mine == ref:
+        return True
+    sK, sV = diag_h["score_K_r"], diag_h["score_V_r"]
+    vals = {}
+    if sK is not None:
+        vals.update({c: float(sK[j, i]) for i, c in enumerate(Kc)})
+    if sV is not None:
+        vals.update({c: float(sV[j, i]) for i, c in enumerate(Vc)})
+    ref_vals = sorted((vals[c] for c in ref), reverse=True)
+    kth = ref_vals[-1] if ref_vals else 0.0
+    for c in mine ^ ref:
+        if c not in vals or abs(vals[c] - kth) > eps * max(abs(kth), 1e-30):
+            return False
+    return True

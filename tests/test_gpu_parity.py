@@ -1,0 +1,294 @@
+"""HIP kernels vs the reference goldens and the CPU oracle (needs a GPU).
+
+Bars: packed codes, int8 scale codes, masters, valid counts, slot ids and
+residual slot bytes bit-exact; fp16 error norms / sketches within one fp16
+ulp; selected candidates equal except swaps across an epsilon-tie of the
+normalised scores (relative 1e-4 of the selection boundary); decode output
+within max-abs 2e-3 and relative-L2 1e-2 of the reference fp32 path.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import (DECODE_CASES, PAPER_ENV, build_oracle_case, case_cfg_kwargs, decode_diag, load_golden,
+                     oracle_candidates, oracle_selection, ties_explain)
+from oracle import quant as Q
+from oracle.attention import decode_attention as oracle_decode
+from oracle.cache import OCache, OCfg
+from oracle.store import decode_append, write_pages_for_kv_head
+
+pytestmark = pytest.mark.gpu
+
+F16, F32 = np.float16, np.float32
+
+
+@pytest.fixture(autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a HIP device")
+
+
+@pytest.fixture
+def paper_env(monkeypatch):
+    for k, v in PAPER_ENV.items():
+        monkeypatch.setenv(k, v)
+    return monkeypatch
+
+
+def _ulp_diff(a, b):
+    a = np.ascontiguousarray(a).astype(F16).view(np.int16).astype(np.int32)
+    b = np.ascontiguousarray(b).astype(F16).view(np.int16).astype(np.int32)
+    return int(np.abs(a - b).max()) if a.size else 0
+
+
+def compare_cache_to_golden(cache, g, prefix=""):
+    """Device cache (layer 0, sequence 0) vs golden reference arrays."""
+    valid = cache.valid[0, :, 0].cpu().numpy()
+    assert np.array_equal(valid, g[prefix + "valid"]), "valid_tokens"
+    H, P = valid.shape
+    for nm, t in (("K_codes", cache.kcodes), ("V_codes", cache.vcodes), ("K_scale", cache.kscale),
+                  ("V_scale", cache.vscale)):
+        mine = t[0, :, 0].cpu().numpy()
+        ref = g[prefix + nm]
+        for h in range(H):
+            for p in range(P):
+                n = int(valid[h, p])
+                assert np.array_equal(mine[h, p, :n], ref[h, p, :n]), (nm, h, p)
+    for nm, t in (("K_master", cache.kmaster), ("V_master", cache.vmaster)):
+        mine = t[0, :, 0].cpu().numpy()
+        used = valid > 0
+        assert np.array_equal(mine[used], g[prefix + nm][used]), nm
+    nk, nv = g[prefix + "k_res"].shape[0], g[prefix + "v_res"].shape[0]
+    assert cache.next_slot[0].tolist() == [nk, nv], "slot counters"
+    assert np.array_equal(cache.k_res[0, :nk].cpu().numpy(), g[prefix + "k_res"])
+    assert np.array_equal(cache.k_res_scale[0, :nk].cpu().numpy(), g[prefix + "k_res_scale"][:, 0])
+    assert np.array_equal(cache.v_res[0, :nv].cpu().numpy(), g[prefix + "v_res"])
+    assert np.array_equal(cache.v_res_scale[0, :nv].cpu().numpy(), g[prefix + "v_res_scale"][:, 0])
+    has_meta = cache.has_meta[0, :, 0].cpu().numpy()
+    ks = cache.k_slot[0, :, 0].cpu().numpy()
+    vs = cache.v_slot[0, :, 0].cpu().numpy()
+    ke = cache.k_err[0, :, 0].cpu().numpy()
+    ve = cache.v_err[0, :, 0].cpu().numpy()
+    sk = cache.k_sketch[0, :, 0].cpu().numpy()
+    for h in range(H):
+        for p in range(P):
+            if g[prefix + "k_slots"][h, p, 0] == -2:
+                assert has_meta[h, p] == 0, ("meta present", h, p)
+                continue
+            assert has_meta[h, p] == 1, ("meta missing", h, p)
+            assert ks[h, p].tolist() == g[prefix + "k_slots"][h, p].tolist(), ("k_slots", h, p)
+            assert vs[h, p].tolist() == g[prefix + "v_slots"][h, p].tolist(), ("v_slots", h, p)
+            assert _ulp_diff(ke[h, p], g[prefix + "k_err"][h, p]) <= 1, ("k_err", h, p)
+            assert _ulp_diff(ve[h, p], g[prefix + "v_err"][h, p]) <= 1, ("v_err", h, p)
+            assert _ulp_diff(sk[h, p], g[prefix + "k_sketch"][h, p]) <= 1, ("k_sketch", h, p)
+
+
+# ------------------------------------------------------------------ store
+@pytest.mark.parametrize("tag", ["abs", "ratio"])
+def test_store_pages_match_reference(paper_env, tag):
+    import care_kv
+    g = load_golden("store_d128.npz")
+    kw = dict(num_layers=1, num_heads=2, num_kv_heads=2, head_dim=128, page_size=16, max_pages=8, base_bits=3,
+              group_size=32, k_channel_group=32, v_token_block=4, sketch_dim=32, packed_base=True,
+              scale_quant="int8")
+    kw.update(dict(store_budget_mode="absolute", store_abs_k=2, store_abs_v=4) if tag == "abs"
+              else dict(store_budget_mode="ratio", store_budget_ratio=0.03))
+    cache = care_kv.CAREKVCache(care_kv.CacheConfig(**kw), device="cuda")
+    cache.write_prefill(0, torch.from_numpy(g["K"]).cuda(), torch.from_numpy(g["V"]).cuda())
+    torch.cuda.synchronize()
+    compare_cache_to_golden(cache, g, tag + "_")
+
+
+def test_append_matches_reference(paper_env):
+    """int8-scale appends into a partial prefill page and a decode-opened page
+    (zero master -> zero scales, the reference's behaviour)."""
+    import care_kv
+    g = load_golden("append_d64.npz")
+    cfg = care_kv.CacheConfig(num_layers=1, num_heads=1, num_kv_heads=1, head_dim=64, page_size=16, max_pages=4,
+                              base_bits=3, group_size=32, packed_base=True, scale_quant="int8",
+                              store_budget_mode="absolute")
+    cache = care_kv.CAREKVCache(cfg, device="cuda")
+    X = torch.from_numpy(g["X"]).cuda()                  # (2, 21, 64): K rows, V rows
+    cache.write_prefill(0, X[0:1, :10], X[1:2, :10])
+    for i in range(10, 21):
+        cache.append(0, X[0:1, i], X[1:2, i])
+    kc, ks, vc, vs, lens = cache.read_base_concat(0, 0)
+    assert lens == g["read_lens"].tolist()
+    assert np.array_equal(kc.cpu().numpy(), g["read_Kc"])
+    assert np.array_equal(vc.cpu().numpy(), g["read_Vc"])
+    assert np.array_equal(ks.cpu().numpy(), g["read_Ks"])
+    assert np.array_equal(vs.cpu().numpy(), g["read_Vs"])
+
+
+# ------------------------------------------------------------------ decode
+def build_gpu_case(g, name):
+    import care_kv
+    spec = DECODE_CASES[name]
+    cfg = care_kv.CacheConfig(packed_base=True, scale_quant="int8", read_budget_ratio=0.0,
+                              **case_cfg_kwargs(g, spec))
+    cache = care_kv.CAREKVCache(cfg, device="cuda")
+    T, n_app = int(g["T"]), int(g["n_append"])
+    K = torch.from_numpy(g["K"]).cuda()
+    V = torch.from_numpy(g["V"]).cuda()
+    cache.write_prefill(0, K[:, :T], V[:, :T])
+    for t in range(T, T + n_app):
+        cache.append(0, K[:, t], V[:, t])
+    torch.cuda.synchronize()
+    return cache, spec
+
+
+def check_decode(cache, oc, spec, Qh, ref_out, paper_env, k_mode):
+    """GPU decode vs oracle selection (epsilon-tie exempt) and reference output."""
+    import care_kv
+    paper_env.setenv("CAREKV_K_CORRECTION_MODE", k_mode)
+    q = torch.from_numpy(Qh).cuda()
+    out, diag = care_kv.decode_attention(cache, 0, q.unsqueeze(0), diag_cap=1024)
+    torch.cuda.synchronize()
+    out = out[0].cpu().numpy().astype(F32)
+    diag = diag[0].cpu().numpy()
+    odiag = {}
+    o_out = oracle_decode(oc, 0, Qh, k_mode=k_mode, kind="both", k_corr_scale=0.1, score_normalize=True,
+                          kscore_live=True, diag=odiag)
+    Hq, Hkv = spec["Hq"], spec["Hkv"]
+    grp = Hq // Hkv
+    n_mismatch = 0
+    for h in range(Hkv):
+        d = odiag[h]
+        if d.get("sel_k") is None and d.get("sel_v") is None:
+            continue
+        Kc, Vc = oracle_candidates(oc, 0, h, oc.next_page[0][h])
+        ref_rows = oracle_selection(d, Kc, Vc)
+        for j in range(grp):
+            mine = set(decode_diag(diag[h * grp + j]))
+            if mine != ref_rows[j]:
+                n_mismatch += 1
+                assert ties_explain(mine, ref_rows[j], d, Kc, Vc, j), (h, j, sorted(mine ^ ref_rows[j]))
+    err = np.abs(out - ref_out.astype(F32))
+    assert err.max() <= 2e-3, err.max()
+    rel = np.linalg.norm(out - ref_out.astype(F32)) / max(np.linalg.norm(ref_out.astype(F32)), 1e-30)
+    assert rel <= 1e-2, rel
+    return n_mismatch, o_out
+
+
+@pytest.mark.parametrize("name", list(DECODE_CASES))
+def test_decode_matches_reference(paper_env, name):
+    g = load_golden(f"decode_{name}.npz")
+    cache, spec = build_gpu_case(g, name)
+    compare_cache_to_golden(cache, g)
+    oc, _ = build_oracle_case(g, name)
+    check_decode(cache, oc, spec, g["Q"], g["O"], paper_env, spec["k_mode"])
+
+
+def test_decode_base_only_matches_reference_decode_step(paper_env):
+    """Compat gate: the reference decode_step applies no correction when
+    read_budget_ratio == 0 (attention.py:1025); its output is the base path."""
+    import care_kv
+    g = load_golden("decode_gqa4_d128.npz")
+    cache, spec = build_gpu_case(g, "gqa4_d128")
+    mha = care_kv.CAREKVMultiHeadAttention(cache.cfg, 0)
+    out = mha.forward(cache, torch.from_numpy(g["Q"]).cuda()).cpu().numpy().astype(F32)
+    ref = g["decode_step_out"].astype(F32)
+    assert np.abs(out - ref).max() <= 2e-3
+
+
+def test_read_zero_is_base_bit_exact(paper_env):
+    import care_kv
+    g = load_golden("decode_gqa4_d128.npz")
+    cache, spec = build_gpu_case(g, "gqa4_d128")
+    q = torch.from_numpy(g["Q"]).cuda().unsqueeze(0)
+    base = care_kv.decode_attention(cache, 0, q, correction=False)
+    cache.cfg.read_abs_k = cache.cfg.read_abs_v = 0
+    corr0 = care_kv.decode_attention(cache, 0, q, correction=True)
+    assert torch.equal(base, corr0)
+
+
+# ------------------------------------------------------------------ random shapes vs oracle
+RANDOM_CASES = [
+    # D, bits, Hq, Hkv, T, n_append, policy, k_mode, store (abs k, abs v) or ratio, read (k, v)
+    (128, 3, 8, 2, 700, 5, "joint", "exact", (1, 1), (6, 6)),
+    (128, 2, 4, 4, 333, 0, "separate", "exact", (2, 4), (2, 3)),
+    (128, 4, 16, 1, 512, 17, "joint", "linear", (2, 2), (8, 4)),
+    (64, 3, 32, 4, 256, 3, "joint", "exact", (1, 1), (5, 7)),
+    (64, 2, 8, 8, 150, 20, "separate", "linear", (1, 2), (3, 3)),
+    (64, 4, 4, 1, 1024, 0, "joint", "exact", (2, 4), (16, 16)),
+]
+
+
+@pytest.mark.parametrize("case", RANDOM_CASES, ids=[f"D{c[0]}b{c[1]}g{c[2]//c[3]}{c[6]}{c[7]}" for c in RANDOM_CASES])
+def test_decode_random_vs_oracle(paper_env, case):
+    import care_kv
+    D, bits, Hq, Hkv, T, n_app, pol, kmode, (sk, sv), (rk, rv) = case
+    rng = np.random.default_rng(D * 7 + bits * 3 + Hq + T)
+    K = (rng.standard_normal((Hkv, T + n_app, D)) * 1.0).astype(F16)
+    V = rng.standard_normal((Hkv, T + n_app, D)).astype(F16)
+    K[:, :, rng.permutation(D)[:3]] *= F16(6.0)
+    Qh = rng.standard_normal((Hq, D)).astype(F16)
+    common = dict(num_layers=1, num_heads=Hq, num_kv_heads=Hkv, head_dim=D, page_size=16,
+                  max_pages=(T + n_app) // 16 + 4, base_bits=bits, group_size=32, k_channel_group=32,
+                  v_token_block=4, sketch_dim=32, read_budget_mode="absolute", read_abs_k=rk, read_abs_v=rv,
+                  route_policy=pol, store_budget_mode="absolute", store_abs_k=sk, store_abs_v=sv)
+    oc = OCache(OCfg(**common))
+    for h in range(Hkv):
+        write_pages_for_kv_head(oc, 0, h, K[h, :T], V[h, :T])
+    for t in range(T, T + n_app):
+        decode_append(oc, 0, K[:, t], V[:, t])
+    cfg = care_kv.CacheConfig(packed_base=True, scale_quant="int8", read_budget_ratio=0.0, **common)
+    cache = care_kv.CAREKVCache(cfg, device="cuda")
+    Kd, Vd = torch.from_numpy(K).cuda(), torch.from_numpy(V).cuda()
+    cache.write_prefill(0, Kd[:, :T], Vd[:, :T])
+    for t in range(T, T + n_app):
+        cache.append(0, Kd[:, t], Vd[:, t])
+    torch.cuda.synchronize()
+    # cache bytes equal the oracle's
+    assert np.array_equal(cache.valid[0, :, 0].cpu().numpy(), oc.valid_tokens[0])
+    assert np.array_equal(cache.k_slot[0, :, 0].cpu().numpy()[cache.has_meta[0, :, 0].cpu().numpy() == 1],
+                          np.array([m.k_residual_slots for row in oc.meta_table[0] for m in row if m is not None]))
+    paper_env.setenv("CAREKV_K_CORRECTION_MODE", kmode)
+    odiag = {}
+    o_out = oracle_decode(oc, 0, Qh, k_mode=kmode, kind="both", k_corr_scale=0.1, score_normalize=True,
+                          kscore_live=True, diag=odiag)
+    out, diag = care_kv.decode_attention(cache, 0, torch.from_numpy(Qh).cuda().unsqueeze(0), diag_cap=1024)
+    out = out[0].cpu().numpy().astype(F32)
+    err = np.abs(out - o_out.astype(F32))
+    assert err.max() <= 2e-3, err.max()
+    grp = Hq // Hkv
+    diag = diag[0].cpu().numpy()
+    for h in range(Hkv):
+        d = odiag[h]
+        Kc, Vc = oracle_candidates(oc, 0, h, oc.next_page[0][h])
+        ref_rows = oracle_selection(d, Kc, Vc)
+        for j in range(grp):
+            mine = set(decode_diag(diag[h * grp + j]))
+            if pol == "joint":
+                assert ties_explain(mine, ref_rows[j], d, Kc, Vc, j), (h, j)
+            else:
+                for kind in (0, 1):
+                    a = {c for c in mine if c[0] == kind}
+                    b = {c for c in ref_rows[j] if c[0] == kind}
+                    assert ties_explain(a, b, d, Kc, Vc, j), (h, j, kind)
+
+
+def test_batched_sequences_match_single(paper_env):
+    """B sequences in one launch == each sequence decoded alone."""
+    import care_kv
+    rng = np.random.default_rng(11)
+    D, Hq, Hkv, B = 128, 8, 2, 3
+    cfg = care_kv.CacheConfig(num_layers=1, num_heads=Hq, num_kv_heads=Hkv, head_dim=D, page_size=16, max_pages=40,
+                              base_bits=3, group_size=32, packed_base=True, scale_quant="int8",
+                              store_budget_mode="absolute", store_abs_k=1, store_abs_v=1,
+                              read_budget_mode="absolute", read_abs_k=8, read_abs_v=8, route_policy="joint",
+                              read_budget_ratio=0.0)
+    paper_env.setenv("CAREKV_K_CORRECTION_MODE", "exact")
+    cache = care_kv.CAREKVCache(cfg, device="cuda", n_seq=B)
+    lens = [300, 517, 64]
+    for s, T in enumerate(lens):
+        K = torch.from_numpy(rng.standard_normal((Hkv, T, D)).astype(F16)).cuda()
+        V = torch.from_numpy(rng.standard_normal((Hkv, T, D)).astype(F16)).cuda()
+        cache.write_prefill(0, K, V, seqs=[s])
+    q = torch.from_numpy(rng.standard_normal((B, Hq, D)).astype(F16)).cuda()
+    both = care_kv.decode_attention(cache, 0, q)
+    for s in range(B):
+        one = care_kv.decode_attention(cache, 0, q[s:s + 1], seqs=[s])
+        assert torch.equal(both[s], one[0])

@@ -1,0 +1,135 @@
+"""CPU tests: the C-ABI library loads and exports every declared symbol, and the
+host-side knob resolution matches the reference's budget arithmetic."""
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _ensure_built():
+    from care_kv import _lib
+    if not os.path.exists(_lib.lib_path()):
+        from care_kv.build import build
+        build()
+    return _lib
+
+
+def test_library_exports_header_symbols():
+    _lib = _ensure_built()
+    lib = _lib.load()
+    hdr = open(os.path.join(ROOT, "include", "carekv.h")).read()
+    declared = set(re.findall(r"\b(carekv_[a-z_]+)\s*\(", hdr))
+    assert declared, "no declarations parsed"
+    for name in sorted(declared):
+        assert hasattr(lib, name), name
+    assert set(_lib.EXPORTS) <= declared
+
+
+def _struct_fields(hdr, name):
+    body = hdr[hdr.index(f"typedef struct {name}"):hdr.index(f"}} {name};")]
+    body = re.sub(r"/\*.*?\*/", " ", body, flags=re.S)
+    body = body[body.index("{") + 1:]
+    names = []
+    for stmt in body.split(";"):
+        stmt = stmt.strip()
+        if not stmt:
+            continue
+        decl = re.sub(r"^(const\s+)?\w+\s*", "", stmt)          # drop the type
+        names += [re.sub(r"[\s*]", "", d) for d in decl.split(",")]
+    return names
+
+
+def test_c_structs_match_header_layout():
+    """ctypes mirrors of the C structs have the header's field order."""
+    _lib = _ensure_built()
+    hdr = open(os.path.join(ROOT, "include", "carekv.h")).read()
+    for cname, py in (("carekv_arena", _lib.Arena), ("carekv_store_params", _lib.StoreParams),
+                      ("carekv_decode_params", _lib.DecodeParams)):
+        assert [f[0] for f in py._fields_] == _struct_fields(hdr, cname), cname
+
+
+def test_cpu_tensor_is_rejected():
+    _lib = _ensure_built()
+    import torch
+    with pytest.raises(_lib.CarekvError):
+        _lib.ptr(torch.zeros(3))
+
+
+def test_unsupported_config_rejected():
+    import care_kv
+    from care_kv.cache import check_kernel_config
+    with pytest.raises(NotImplementedError):
+        check_kernel_config(care_kv.CacheConfig(page_size=8, group_size=32, base_bits=3))
+    with pytest.raises(NotImplementedError):
+        check_kernel_config(care_kv.CacheConfig(base_quantizer="kivi_style", group_size=32))
+    check_kernel_config(care_kv.CacheConfig(group_size=32, base_bits=3, head_dim=128))
+
+
+def test_config_validation_matches_reference():
+    import care_kv
+    with pytest.raises(ValueError):
+        care_kv.CacheConfig(scale_quant="int4")
+    with pytest.raises(ValueError):
+        care_kv.CacheConfig(route_policy="greedy")
+    c = care_kv.CacheConfig(num_heads=8, packed_storage=True)
+    assert c.num_kv_heads == 8 and c.packed_base and c.layer_sensitivity == [1.0] * 32
+
+
+def test_store_knobs(monkeypatch):
+    """Ratio 3% at D=128 resolves to 1 K + 1 V slot per page
+    (residual_store.py:403-408); absolute mode passes the counts through."""
+    import care_kv
+    monkeypatch.delenv("CAREKV_STORE_POLICY", raising=False)
+    monkeypatch.delenv("CAREKV_PREFILL_RESIDUAL_KIND", raising=False)
+    c = care_kv.CacheConfig(num_layers=1, head_dim=128, group_size=32, store_budget_mode="ratio",
+                            store_budget_ratio=0.03)
+    s = care_kv.resolve_store_knobs(c, 0)
+    assert (s.k_budget, s.v_budget, s.joint, s.store_none) == (1, 1, False, False)
+    c = care_kv.CacheConfig(num_layers=1, group_size=32, store_budget_mode="absolute", store_abs_k=2,
+                            store_abs_v=4, store_budget_ratio=0.0)
+    s = care_kv.resolve_store_knobs(c, 0)
+    assert (s.k_budget, s.v_budget, s.store_none) == (2, 4, False)
+    monkeypatch.setenv("CAREKV_PREFILL_RESIDUAL_KIND", "v")
+    s = care_kv.resolve_store_knobs(c, 0)
+    assert (s.k_budget, s.v_budget) == (0, 4)
+    c = care_kv.CacheConfig(num_layers=1, group_size=32, store_budget_ratio=0.0)
+    assert care_kv.resolve_store_knobs(c, 0).store_none
+
+
+def test_layer_budget_multiplier_mean_one():
+    import care_kv
+    c = care_kv.CacheConfig(num_layers=22, group_size=32, budget_policy="u_shaped")
+    m = [care_kv.layer_budget_multiplier(c, l) for l in range(22)]
+    assert abs(sum(m) / 22 - 1.0) < 1e-12 and m[0] > 1.5 and m[11] < 0.6
+
+
+def test_env_overrides(monkeypatch):
+    import care_kv
+    monkeypatch.setenv("CAREKV_BASE_BITS", "3")
+    monkeypatch.setenv("CAREKV_SCALE_QUANT", "int8")
+    monkeypatch.setenv("CAREKV_PACKED_BASE", "1")
+    monkeypatch.setenv("CAREKV_LAYER_SENSITIVITY", "1.5,1.0")
+    kw = care_kv.apply_carekv_env_overrides({})
+    assert kw == dict(base_bits=3, scale_quant="int8", packed_base=True, layer_sensitivity=[1.5, 1.0])
+
+
+def test_read_knobs(monkeypatch):
+    import care_kv
+    monkeypatch.setenv("CAREKV_K_CORRECTION_MODE", "exact")
+    monkeypatch.setenv("CAREKV_KSCORE_LIVE", "1")
+    monkeypatch.setenv("CAREKV_SCORE_NORMALIZE", "1")
+    c = care_kv.CacheConfig(num_layers=1, group_size=32, read_budget_mode="absolute", read_abs_k=128,
+                            read_abs_v=128, route_policy="joint")
+    r = care_kv.resolve_read_knobs(c, 0)
+    assert (r.k_exact, r.kscore_live, r.normalize, r.joint, r.abs_k, r.abs_v, r.budget_ratio) == \
+        (True, True, True, True, 128, 128, False)
+
+
+def test_bench_rejects_multi_gpu():
+    import subprocess
+    import sys
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode != 0 and "one GPU" in r.stderr
