@@ -168,6 +168,8 @@ def main():
     ap.add_argument("--cpu-slices", type=int, default=2)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--split-pages", type=int, default=None)
+    ap.add_argument("--no-correction", action="store_true",
+                    help="time the base attention path only (streaming pass + split combine)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): the decode path is embarrassingly "
@@ -202,14 +204,15 @@ def main():
     torch.cuda.synchronize()
     diag_np = diag.cpu().numpy()
     nbytes, k_slots, v_union = algorithmic_bytes(spec, cfg, cache, diag_np)
+    corr = not args.no_correction
     for _ in range(args.warmup):
-        care_kv.decode_attention(cache, 0, q, out=out, split_pages=args.split_pages)
+        care_kv.decode_attention(cache, 0, q, out=out, split_pages=args.split_pages, correction=corr)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     ev0.record(stream)
     for _ in range(args.steps):
-        care_kv.decode_attention(cache, 0, q, out=out, split_pages=args.split_pages)
+        care_kv.decode_attention(cache, 0, q, out=out, split_pages=args.split_pages, correction=corr)
     ev1.record(stream)
     ev1.synchronize()
     ms_total = ev0.elapsed_time(ev1)

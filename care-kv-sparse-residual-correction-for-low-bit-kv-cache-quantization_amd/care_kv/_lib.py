@@ -62,7 +62,7 @@ def load(path: str | None = None):
     with _lock:
         if _lib is not None:
             return _lib
-        p = path or _LIB_PATH
+        p = path or os.environ.get("CAREKV_LIB") or _LIB_PATH
         if not os.path.exists(p):
             raise CarekvError(f"{p} not found: build it with `python -m care_kv.build` "
                               "(or __graft_entry__.build()); there is no non-HIP fallback")

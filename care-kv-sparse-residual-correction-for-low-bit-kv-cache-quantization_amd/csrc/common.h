@@ -119,4 +119,8 @@ __device__ __forceinline__ void store_bytes(int8_t* p, const uint32_t* w) {
 
 __host__ __device__ constexpr int row_bytes(int D, int bits) { return D * bits / 8; }
 
+// Wait for this wave's outstanding LDS operations; also a compiler barrier
+// for memory so LDS writes by other lanes are read after they landed.
+__device__ __forceinline__ void lds_sync_wave() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
 }  // namespace carekv
