@@ -21,7 +21,7 @@ REPO = os.path.dirname(ROOT)
 INCLUDE = os.path.join(REPO, "include")
 LIB_NAME = "libcarekv_hip.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = ["capi.cpp", "store.hip", "decode.hip", "decode_stream.hip", "decode_finalize.hip"]
+SOURCES = ["capi.cpp", "store.hip", "decode.hip", "decode_stream.hip", "decode_select.hip", "decode_apply.hip"]
 ARCH = os.environ.get("CAREKV_OFFLOAD_ARCH", "gfx950")
 
 
@@ -36,6 +36,9 @@ def common_flags():
     return ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-I", INCLUDE, "-I", CSRC,
             "-fhip-fp32-correctly-rounded-divide-sqrt", "-fno-fast-math", "-ffp-contract=off",
             "-mcode-object-version=5",
+            # MFMA accumulators in VGPRs: avoids AGPR<->VGPR copies of the
+            # loop-carried output tiles
+            "-mllvm", "-amdgpu-mfma-vgpr-form=1",
             # packed FP32 ops disabled on purpose
             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
             "-Wno-unused-command-line-argument"]

@@ -1,5 +1,5 @@
 // C ABI of the decode path: workspace layout, argument checks, launches of
-// the streaming and finalize kernels on the caller's stream.
+// the streaming, select, apply and combine kernels on the caller's stream.
 #include "decode_common.h"
 #include "host_util.h"
 
@@ -7,7 +7,7 @@ using namespace carekv;
 
 namespace {
 struct WsLayout {
-  long pml, po, rec, scores, sel, err, total;
+  long err, pml, po, rec, scores, mask, ob, ml, num, den, total;
   int nsplit, F, ncand;
 };
 
@@ -25,9 +25,13 @@ WsLayout ws_layout(const carekv_arena& A, const carekv_decode_params& dp) {
   L.err = off; off += 256;
   L.pml = off; off += al(BH * L.nsplit * 16 * 2 * 4);
   L.po = off; off += al(BH * L.nsplit * 16 * (long)D * 4);
-  L.rec = off; off += al(BH * (long)Pm * GQ * L.F * 4);
-  L.scores = off; off += al(BH * (long)GQ * L.ncand * 4);
-  L.sel = off; off += al(BH * (long)GQ * L.ncand * 4);
+  L.rec = off; off += al(BH * GQ * (long)Pm * L.F * 4);
+  L.scores = off; off += al(BH * GQ * (long)L.ncand * 4);
+  L.mask = off; off += al(BH * GQ * (long)Pm);
+  L.ob = off; off += al(BH * GQ * (long)D * 4);
+  L.ml = off; off += al(BH * GQ * 2 * 4);
+  L.num = off; off += al(BH * L.nsplit * GQ * (long)D * 4);
+  L.den = off; off += al(BH * L.nsplit * GQ * 4);
   L.total = off;
   return L;
 }
@@ -51,7 +55,8 @@ extern "C" int carekv_decode_attn(const carekv_arena* arena, const carekv_decode
   CAREKV_REQUIRE(GQ >= 1 && GQ <= 16, "query heads per kv head must be in 1..16");
   CAREKV_REQUIRE(dp->seq_slot && dp->n_pages, "seq_slot and n_pages are required");
   CAREKV_REQUIRE(dp->max_pages_used >= 0 && dp->max_pages_used <= A.max_pages, "max_pages_used out of range");
-  CAREKV_REQUIRE(dp->split_pages > 0 && dp->split_pages % 4 == 0, "split_pages must be a positive multiple of 4");
+  CAREKV_REQUIRE(dp->split_pages > 0 && dp->split_pages % 4 == 0 && dp->split_pages <= 1024,
+                 "split_pages must be a multiple of 4 in 4..1024");
   CAREKV_REQUIRE(dp->k_cap >= 0 && dp->k_cap <= A.head_dim / 32, "k_cap out of range");
   CAREKV_REQUIRE(dp->v_cap >= 0 && dp->v_cap <= 4, "v_cap out of range");
   CAREKV_REQUIRE(dp->lambda_k > 0.f && dp->lambda_v > 0.f, "KSCORE lambdas must be positive");
@@ -70,19 +75,26 @@ extern "C" int carekv_decode_attn(const carekv_arena* arena, const carekv_decode
   a.po = (float*)(ws + L.po);
   a.rec = (float*)(ws + L.rec);
   a.scores = (float*)(ws + L.scores);
-  a.sel = (int32_t*)(ws + L.sel);
+  a.mask = (uint8_t*)(ws + L.mask);
+  a.ob = (float*)(ws + L.ob);
+  a.ml = (float*)(ws + L.ml);
+  a.num = (float*)(ws + L.num);
+  a.den = (float*)(ws + L.den);
   a.diag = diag; a.diag_cap = diag_cap;
   a.B = dp->batch; a.Hq = dp->n_heads; a.GQ = GQ; a.nsplit = L.nsplit; a.SP = dp->split_pages;
   a.Pmax = dp->max_pages_used > 0 ? dp->max_pages_used : 1;
   a.k_cap = dp->k_cap; a.v_cap = dp->v_cap; a.F = L.F; a.ncand = L.ncand;
   a.sm_scale = dp->sm_scale; a.sens = dp->sensitivity; a.sens_d = (double)dp->sensitivity;
   a.k_corr_scale = dp->k_corr_scale; a.lam_k = dp->lambda_k; a.lam_v = dp->lambda_v;
-  a.sqrt_d = (float)sqrt((double)A.head_dim);
+  a.sm_log2 = (float)((double)dp->sm_scale * 1.4426950408889634074);  // log2(e)
+  a.inv_sqrt_d = (float)(1.0 / sqrt((double)A.head_dim));
   a.correction = dp->correction; a.kind = dp->kind; a.joint = dp->joint; a.normalize = dp->normalize;
   a.k_exact = dp->k_exact; a.budget_ratio = dp->budget_ratio; a.abs_k = dp->abs_k; a.abs_v = dp->abs_v;
   a.ratio_k = dp->ratio_k; a.ratio_v = dp->ratio_v;
   hipStream_t s = (hipStream_t)stream;
   int rc = launch_decode_stream(A, a, s);
-  if (rc != CAREKV_OK) return rc;
-  return launch_decode_finalize(A, a, s);
+  if (rc == CAREKV_OK) rc = launch_decode_select(A, a, s);
+  if (rc == CAREKV_OK && a.correction) rc = launch_decode_apply(A, a, s);
+  if (rc == CAREKV_OK && a.correction) rc = launch_decode_combine(A, a, s);
+  return rc;
 }

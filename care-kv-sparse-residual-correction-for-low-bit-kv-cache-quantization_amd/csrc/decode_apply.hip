@@ -1,0 +1,261 @@
+// Apply pass of the CARE-KV decode: one work-group per (page chunk, kv
+// head, sequence), after the select kernel.  Every page of the chunk that
+// any query of the GQA group selected a slot of is processed once for all
+// the group's queries, a wave per page, with the per-query masks:
+//
+//   a_t   = 2^(x_t - M)                    (unnormalised attention weight)
+//   dS_t  = sum over selected K slots of q_cg . R_K[t] (raw, residual scale)
+//   exact mode (attention.py:96-118 in closed form; with sum_t A_t = 1):
+//     num += sum_t a_t (e^{dS_t/sqrt(D)} - 1) V_hat_t
+//          + sum_{t in selected V blocks} a_t e^{dS_t/sqrt(D)} R_V[t]
+//     den += sum_t a_t (e^{dS_t/sqrt(D)} - 1)
+//     out  = (O_base + num / L) / (1 + den / L)
+//   linear mode (attention.py:938-943):
+//     num += k_corr_scale * sum_t a_t dS_t V_hat_t + sum_{sel V} a_t R_V[t]
+//     den += k_corr_scale * sum_t a_t dS_t
+//     out  = O_base + (num - den * O_base) / L
+// Both products run on MFMA like the streaming pass (weights as fp16 P,
+// V_hat / R_V transposed through LDS).  The combine kernel sums the chunk
+// partials in chunk order and writes half(out).
+#include "block_util.h"
+#include "decode_page.h"
+#include "host_util.h"
+
+namespace carekv {
+
+template <int D, int BITS>
+constexpr bool same_slot_order() {
+  using G = PageGeom<D, BITS>;
+  for (int i = 0; i < G::CH; ++i)
+    if (G::PB::T.slot_code[i] != G::PR::T.slot_code[i]) return false;
+  return true;
+}
+
+template <int D, int BITS, int SM>
+__global__ __launch_bounds__(256) void decode_apply_kernel(carekv_arena A, DecodeArgs a) {
+  using G = PageGeom<D, BITS>;
+  static_assert(same_slot_order<D, BITS>(), "V residual tile must use the V_hat slot order");
+  constexpr int NT = G::NT, NCG = G::NCG, CH = G::CH;
+  constexpr int VT_WORDS = kPage * G::VROW;
+  constexpr int MERGE_BYTES = 4 * 16 * D * 4;
+  constexpr int TILE_BYTES = 4 * VT_WORDS * 4;
+  constexpr int LDS_BYTES = MERGE_BYTES > TILE_BYTES ? MERGE_BYTES : TILE_BYTES;
+  constexpr int kMaxSP = 1024;
+  __shared__ __align__(16) char smem[LDS_BYTES];
+  __shared__ __align__(16) _Float16 sq[16 * D];
+  __shared__ int s_items[kMaxSP];
+  __shared__ float s_den[4][16];
+  __shared__ BlockScratch bs;
+
+  const int chunk = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int GQ = a.GQ;
+  const int bk = b * A.n_kv_heads + kvh;
+  const int seq_raw = a.seq_slot[b], np_raw = a.n_pages[b];
+  const bool row_ok = seq_raw >= 0 && seq_raw < A.n_seq && np_raw >= 0 && np_raw <= a.Pmax;
+  const int seq = row_ok ? seq_raw : 0, np = row_ok ? np_raw : 0;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ln = lane & 15, lj = lane >> 4;
+  const long pg_base = ((long)kvh * A.n_seq + seq) * A.max_pages;
+  const RowRes rr = row_resources<D, BITS, SM>(A, pg_base);
+  const uint8_t* maskb = a.mask + (long)bk * GQ * a.Pmax;
+  const bool exact = a.k_exact != 0;
+
+  // ---- pages of the chunk with any selected slot
+  const int p_begin = chunk * a.SP, p_end = min(p_begin + a.SP, np);
+  int n_items = 0;
+  for (int p0 = p_begin; p0 < p_end; p0 += kBlock) {
+    const int p = p0 + threadIdx.x;
+    unsigned any = 0;
+    if (p < p_end)
+      for (int n = 0; n < GQ; ++n) any |= maskb[(long)n * a.Pmax + p];
+    int tot;
+    const int pos = block_excl_scan(any ? 1 : 0, bs, &tot);
+    if (any) s_items[n_items + pos] = p;
+    n_items += tot;
+  }
+  stage_q<D>(sq, a.q + ((long)b * a.Hq + kvh * GQ) * D, GQ);
+  __syncthreads();
+
+  half8_t qB[G::NS];
+  load_q_operand<D, BITS>(qB, sq, ln, lj);
+  const bool qv = ln < GQ;
+  const float Mq = qv ? a.ml[((long)bk * GQ + ln) * 2] : 0.f;
+  uint32_t* vt = reinterpret_cast<uint32_t*>(smem) + w * VT_WORDS;
+  float4_t nacc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) nacc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+  float den = 0.f;
+
+  for (int it = w; it < n_items; it += 4) {
+    const int p = __builtin_amdgcn_readfirstlane(s_items[it]);
+    const long pg = pg_base + p;
+    const unsigned mk = qv ? maskb[(long)ln * a.Pmax + p] : 0u;
+    const unsigned kbits = mk & 15u, vbits = mk >> 4;
+    PageRegs<D, BITS> cur;
+    PageMeta<NCG> cm;
+    load_page_regs<D, BITS, SM>(cur, rr, p, ln, lj);
+    load_page_meta<NCG>(cm, A, pg);
+    float ckm = 0.f, cvm = 0.f;
+    if constexpr (SM == 1) { ckm = h2f(A.kmaster[pg]); cvm = h2f(A.vmaster[pg]); }
+    const int nv = cm.nv;
+    // ---- attention weights of the page
+    const _Float16 ks = lane_scale<SM>(cur.ksc, ckm), vs = lane_scale<SM>(cur.vsc, cvm);
+    const float4_t sacc = page_scores<D, BITS>(cur.kw, ks, qB);
+    float at[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      at[i] = (4 * lj + i < nv) ? __builtin_amdgcn_exp2f(sacc[i] * a.sm_log2 - Mq) : 0.f;
+    // ---- dS over the K slots this lane's query selected
+    float wk[4] = {0.f, 0.f, 0.f, 0.f};
+    int rk = 0;
+#pragma unroll
+    for (int cg = 0; cg < NCG; ++cg) {
+      const int slot = cm.ksl[cg];
+      if (slot < 0) continue;
+      if (rk >= a.k_cap) break;
+      if (__any((kbits >> rk) & 1u)) {
+        const long so = (long)seq * A.n_slots + slot;
+        const float4_t racc = kslot_dot(A.k_res + so * G::KSB, sq, D, cg, ln, lj);
+        const float rs = h2f(A.k_res_scale[so]);
+        if ((kbits >> rk) & 1u) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) wk[i] += racc[i] * rs;
+        }
+      }
+      ++rk;
+    }
+    // ---- V block of this lane's tokens (4j .. 4j+3): stored slot rank
+    int vrank = -1, vslot = -1, rv = 0;
+#pragma unroll
+    for (int vb = 0; vb < kVtb; ++vb) {
+      if (cm.vsl[vb] < 0) continue;
+      if (vb == lj) { vrank = rv; vslot = cm.vsl[vb]; }
+      ++rv;
+    }
+    const bool vsel = vrank >= 0 && vrank < a.v_cap && ((vbits >> vrank) & 1u);
+    float ck[4], cv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (exact) {
+        const float ds = wk[i] * a.inv_sqrt_d;
+        ck[i] = kbits ? at[i] * expm1f(ds) : 0.f;
+        cv[i] = vsel ? at[i] * expf(ds) : 0.f;
+      } else {
+        ck[i] = kbits ? a.k_corr_scale * at[i] * wk[i] : 0.f;
+        cv[i] = vsel ? at[i] : 0.f;
+      }
+    }
+    den += (ck[0] + ck[1]) + (ck[2] + ck[3]);
+    // ---- num += ck V_hat
+    if (__any(kbits != 0u)) {
+      half2_t vp[CH / 2];
+      dequant_pairs<BITS, CH, BITS>(cur.vw, vs, vp);
+      vtile_write<D, BITS>(vt, vp, ln, lj);
+      half4_t ap;
+      ap[0] = (_Float16)ck[0]; ap[1] = (_Float16)ck[1]; ap[2] = (_Float16)ck[2]; ap[3] = (_Float16)ck[3];
+      lds_sync_wave();
+      pv_accumulate<D, BITS>(vt, ap, nacc, ln, lj);
+      lds_sync_wave();
+    }
+    // ---- num += cv R_V  (rows of unselected blocks are zero)
+    if (__any(vsel)) {
+      // row m = token of this lane's load: block m / 4, token m % 4 of the slot
+      const int vb_row = ln >> 2;
+      int rrank = -1, rslot = -1, r2 = 0;
+#pragma unroll
+      for (int vb = 0; vb < kVtb; ++vb) {
+        if (cm.vsl[vb] < 0) continue;
+        if (vb == vb_row) { rrank = r2; rslot = cm.vsl[vb]; }
+        ++r2;
+      }
+      // any query selected this row's block?
+      bool row_sel = false;
+      for (int n = 0; n < GQ; ++n)
+        row_sel |= rrank >= 0 && rrank < a.v_cap && ((maskb[(long)n * a.Pmax + p] >> (4 + rrank)) & 1u);
+      half2_t rp[CH / 2];
+      if (row_sel && 4 * vb_row < nv) {
+        const long so = (long)seq * A.n_slots + rslot;
+        const __amdgpu_buffer_rsrc_t r = make_rsrc(A.v_res + so * G::VSB, G::VSB);
+        uint32_t rw[CH / 8];
+        buf_load<CH / 2>(rw, r, (ln & 3) * (D / 2) + lj * (CH / 2));
+        dequant_pairs<4, CH, BITS>(rw, bits2half(A.v_res_scale[so]), rp);
+      } else {
+#pragma unroll
+        for (int i = 0; i < CH / 2; ++i) rp[i] = half2_t{(_Float16)0.f, (_Float16)0.f};
+      }
+      vtile_write<D, BITS>(vt, rp, ln, lj);
+      half4_t ap;
+      ap[0] = (_Float16)cv[0]; ap[1] = (_Float16)cv[1]; ap[2] = (_Float16)cv[2]; ap[3] = (_Float16)cv[3];
+      lds_sync_wave();
+      pv_accumulate<D, BITS>(vt, ap, nacc, ln, lj);
+      lds_sync_wave();
+    }
+    (void)vslot;
+  }
+
+  // ---- merge the waves and write the chunk partial
+  den = col_sum(den);
+  float* so = reinterpret_cast<float*>(smem);  // [4][16][D]
+  __syncthreads();
+  if (lj == 0) s_den[w][ln] = den;
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int slot = ln * NT + t;
+    const int dim = (slot / CH) * CH + G::PB::T.slot_code[slot % CH];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) so[(w * 16 + 4 * lj + i) * D + dim] = nacc[t][i];
+  }
+  __syncthreads();
+  const long cbase = ((long)bk * a.nsplit + chunk) * GQ;
+  for (int idx = threadIdx.x; idx < GQ * D; idx += 256) {
+    const int qq = idx / D, d = idx % D;
+    a.num[(cbase + qq) * D + d] = ((so[qq * D + d] + so[(16 + qq) * D + d]) + so[(32 + qq) * D + d]) +
+                                  so[(48 + qq) * D + d];
+    if (d == 0) a.den[cbase + qq] = ((s_den[0][qq] + s_den[1][qq]) + s_den[2][qq]) + s_den[3][qq];
+  }
+}
+
+// out = half(O_base + correction) from the chunk partials (fixed order).
+__global__ __launch_bounds__(256) void decode_combine_kernel(int Hkv, int D, DecodeArgs a) {
+  const int kvh = blockIdx.x, b = blockIdx.y;
+  const int GQ = a.GQ;
+  const int bk = b * Hkv + kvh;
+  for (int idx = threadIdx.x; idx < GQ * D; idx += 256) {
+    const int qq = idx / D, d = idx % D;
+    const long bq = (long)bk * GQ + qq;
+    const float ob = a.ob[bq * D + d];
+    const float L = a.ml[bq * 2 + 1];
+    float nm = 0.f, dn = 0.f;
+    for (int c = 0; c < a.nsplit; ++c) {
+      const long cb = ((long)bk * a.nsplit + c) * GQ + qq;
+      nm += a.num[cb * D + d];
+      dn += a.den[cb];
+    }
+    float o = ob;
+    if (L > 0.f) o = a.k_exact ? (ob + nm / L) / (1.f + dn / L) : ob + (nm - dn * ob) / L;
+    a.out[((long)b * a.Hq + kvh * GQ + qq) * D + d] = f2h(o);
+  }
+}
+
+int launch_decode_apply(const carekv_arena& A, const DecodeArgs& a, hipStream_t s) {
+  if (a.SP > 1024) {
+    set_error("split_pages must be at most 1024");
+    return CAREKV_EINVAL;
+  }
+  const dim3 grid(a.nsplit, A.n_kv_heads, a.B);
+  return dispatch_dbs(A.head_dim, A.base_bits, A.scale_mode, [&](auto d, auto bb, auto sm) {
+    hipLaunchKernelGGL((decode_apply_kernel<decltype(d)::value, decltype(bb)::value, decltype(sm)::value>), grid,
+                       dim3(256), 0, s, A, a);
+    CAREKV_CHECK_LAUNCH("decode_apply");
+    return CAREKV_OK;
+  });
+}
+
+int launch_decode_combine(const carekv_arena& A, const DecodeArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL(decode_combine_kernel, dim3(A.n_kv_heads, a.B), dim3(256), 0, s, A.n_kv_heads, A.head_dim, a);
+  CAREKV_CHECK_LAUNCH("decode_combine");
+  return CAREKV_OK;
+}
+
+}  // namespace carekv

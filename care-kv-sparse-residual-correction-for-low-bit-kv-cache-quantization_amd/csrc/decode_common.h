@@ -1,4 +1,6 @@
-// Shared definitions of the two decode kernels (streaming pass, finalize).
+// Shared definitions of the decode kernels: streaming pass, select, apply,
+// combine (launched in that order on one stream; each kernel boundary
+// orders the workspace writes of the previous kernel).
 #pragma once
 
 #include "common.h"
@@ -10,27 +12,38 @@ struct DecodeArgs {
   uint16_t* out;
   const int32_t* seq_slot;
   const int32_t* n_pages;
-  float* pml;          // [B*Hkv][nsplit][16][2]  split max / sum
+  float* pml;          // [B*Hkv][nsplit][16][2]  split max (base-2 logits) / sum
   float* po;           // [B*Hkv][nsplit][16][D]  split unnormalised O
-  float* rec;          // [B*Hkv][Pmax][GQ][F]    per-page records
-  float* scores;       // [B*Hkv][GQ][ncand]
-  int32_t* sel;        // [B*Hkv][GQ][ncand]
+  float* rec;          // [B*Hkv][GQ][Pmax][F]    per-page records
+  float* scores;       // [B*Hkv][GQ][ncand]      candidate scores
+  uint8_t* mask;       // [B*Hkv][GQ][Pmax]       selected slots per page
+  float* ob;           // [B*Hkv][GQ][D]          O_base
+  float* ml;           // [B*Hkv][GQ][2]          global max (base 2) / sum
+  float* num;          // [B*Hkv][nsplit][GQ][D]  apply partial numerators
+  float* den;          // [B*Hkv][nsplit][GQ]     apply partial denominators
   int32_t* diag;
   int32_t* err_flag;
   int diag_cap;
   int B, Hq, GQ, nsplit, SP, Pmax, k_cap, v_cap, F, ncand;
-  float sm_scale, sens, k_corr_scale, lam_k, lam_v, sqrt_d;
+  float sm_scale, sm_log2, sens, k_corr_scale, lam_k, lam_v, inv_sqrt_d;
   int correction, kind, joint, normalize, k_exact, budget_ratio, abs_k, abs_v;
   double ratio_k, ratio_v, sens_d;
 };
 
-// Page record layout per (sequence, kv head, page, query):
-//   [0]                      m_ref: logit reference (running max) of the page
+// Page record per (sequence, kv head, query, page), F floats:
+//   [0]                      m_ref: running max of the base-2 logits
+//                            x = s * log2(e) at the page
 //   [1 + 3r .. 3 + 3r]       M2, M3, M4 of the r-th stored K slot (cg order)
-//   [1 + 3*k_cap + r]        sum_t exp(s_t - m_ref) over the r-th stored V block
-// with Mk = sum_t dS_t^2 exp(s_t - m_ref)^k over the page's valid tokens.
+//   [1 + 3*k_cap + r]        sum_t e_t over the r-th stored V block
+// with e_t = 2^(x_t - m_ref) and Mk = sum_t dS_t^2 e_t^k over the page's
+// valid tokens.  Written only for pages with metadata.
+//
+// Selection mask per (sequence, kv head, query, page): bit r = the r-th
+// stored K slot of the page is selected, bit 4 + r = the r-th stored V block.
 
 int launch_decode_stream(const carekv_arena& A, const DecodeArgs& a, hipStream_t s);
-int launch_decode_finalize(const carekv_arena& A, const DecodeArgs& a, hipStream_t s);
+int launch_decode_select(const carekv_arena& A, const DecodeArgs& a, hipStream_t s);
+int launch_decode_apply(const carekv_arena& A, const DecodeArgs& a, hipStream_t s);
+int launch_decode_combine(const carekv_arena& A, const DecodeArgs& a, hipStream_t s);
 
 }  // namespace carekv

@@ -1,0 +1,394 @@
+// Per-page building blocks shared by the streaming and apply kernels of the
+// decode (gfx950, wave64).  A wave works on one 16-token page at a time;
+// lane l = 16*j + m holds token m, dims [j*D/4, (j+1)*D/4) of the page when
+// it loads codes, and query column m, tokens 4j..4j+3 in MFMA results.
+#pragma once
+
+#include "decode_common.h"
+
+namespace carekv {
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef const __attribute__((address_space(4))) int32_t cint32_t;  // read-only, scalar loads when uniform
+
+constexpr uint32_t kBufFlags = 0x00020000u;  // raw buffer resource word 3 (gfx9 family)
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, (int)kBufFlags);
+}
+
+__device__ __forceinline__ float4_t mfma16x32(half8_t a, half8_t b, float4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// x[l] op x[l ^ 16] and x[l] op x[l ^ 32] through the gfx950 lane-swap
+// instructions: both results hold the pair {x[l], x[l^16]} (resp. ^32) in
+// some order, and the ops used are commutative, so the lanes of a pair end
+// with identical bits.
+__device__ __forceinline__ float pair16_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float pair32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float pair16_max(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// Sum over the four lanes m, m+16, m+32, m+48 (the token groups of a query).
+__device__ __forceinline__ float col_sum(float v) { return pair32_sum(pair16_sum(v)); }
+__device__ __forceinline__ float col_max(float v) { return pair32_max(pair16_max(v)); }
+
+// ---------------------------------------------------------------- code pairs
+// A chunk of NC codes (FB-bit two's complement fields of a little-endian
+// bit string) is decoded two codes at a time into fp16 pairs.  The pairs are
+// (blk + k, blk + k + PD) inside blocks of BLK codes (geometry of schedule
+// SB); the pair order fixes the order of the reduction dimension of the
+// MFMAs that consume them.  A pair is masked out of 32-bit windows of the
+// bit string into the mantissas of two fp16 values 1024 + u * 2^o
+// (u = offset-binary code, o = field offset), after which one packed FMA
+// gives the two signed codes exactly.
+template <int SB> struct PairGeom;
+template <> struct PairGeom<2> { static constexpr int BLK = 16, PD = 8; };
+template <> struct PairGeom<3> { static constexpr int BLK = 8, PD = 4; };
+template <> struct PairGeom<4> { static constexpr int BLK = 8, PD = 4; };
+
+template <int FB, int NC, int SB>
+struct Pairs {
+  static constexpr int NP = NC / 2;
+  static constexpr int NW = (NC * FB + 31) / 32;
+  static constexpr int MAXO = 10 - FB;  // field must stay inside the 10-bit mantissa
+  struct Tab {
+    int a[NP], b[NP];      // code indices of the pair
+    int Wa[NP], Wb[NP];    // window start bits of the low / high field
+    int ha[NP], hb[NP];    // highest bit any user of that window needs
+    int ao[NP], bo[NP];    // field offsets inside the low / high halves
+    int slot_code[NC];     // fp16 slot 2i (+1) -> code a_i (b_i)
+  };
+  static constexpr Tab make() {
+    Tab t{};
+    constexpr int BLK = PairGeom<SB>::BLK, PD = PairGeom<SB>::PD;
+    constexpr int NONE = -100000;
+    int n = 0, W = NONE, WA = NONE, WB = NONE;
+    for (int blk = 0; blk < NC; blk += BLK)
+      for (int k = 0; k < BLK / 2; ++k) {
+        const int ia = blk + k, ib = ia + PD;
+        const int ba = FB * ia, bb = FB * ib;
+        t.a[n] = ia; t.b[n] = ib;
+        t.slot_code[2 * n] = ia; t.slot_code[2 * n + 1] = ib;
+        const int lo_a = ba - MAXO, hi_a = ba;            // Wa range: ao in [0, MAXO]
+        const int lo_b = bb - 16 - MAXO, hi_b = bb - 16;  // Wb range: bo in [0, MAXO]
+        const int lo = lo_a > lo_b ? lo_a : lo_b, hi = hi_a < hi_b ? hi_a : hi_b;
+        if (lo <= hi) {  // one window serves both fields
+          if (!(W >= lo && W <= hi)) W = hi;
+          t.Wa[n] = t.Wb[n] = W;
+        } else {  // two windows
+          W = NONE;
+          if (!(WA >= lo_a && WA <= hi_a)) WA = hi_a;
+          if (!(WB >= lo_b && WB <= hi_b)) WB = hi_b;
+          t.Wa[n] = WA; t.Wb[n] = WB;
+        }
+        t.ao[n] = ba - t.Wa[n];
+        t.bo[n] = bb - 16 - t.Wb[n];
+        ++n;
+      }
+    // highest needed bit per distinct window value
+    for (int i = 0; i < NP; ++i) {
+      int h_a = 0, h_b = 0;
+      for (int j = 0; j < NP; ++j) {
+        const int na = FB * t.a[j] + FB - 1, nb = FB * t.b[j] + FB - 1;
+        if (t.Wa[j] == t.Wa[i] && na > h_a) h_a = na;
+        if (t.Wb[j] == t.Wa[i] && nb > h_a) h_a = nb;
+        if (t.Wa[j] == t.Wb[i] && na > h_b) h_b = na;
+        if (t.Wb[j] == t.Wb[i] && nb > h_b) h_b = nb;
+      }
+      t.ha[i] = h_a; t.hb[i] = h_b;
+    }
+    return t;
+  }
+  static constexpr Tab T = make();
+};
+
+// 32-bit window of the bit string in w starting at bit W (may be negative);
+// bits above `hi` are not needed.
+template <int NW>
+__device__ __forceinline__ uint32_t window(const uint32_t* w, int W, int hi) {
+  if (W < 0) return w[0] << (-W);
+  const int d = W >> 5, s = W & 31;
+  if (s == 0) return w[d];
+  if (hi < 32 * (d + 1) || d + 1 >= NW) return w[d] >> s;
+  return __builtin_amdgcn_alignbit(w[d + 1], w[d], s);
+}
+
+// Pair i of the chunk as two exact signed codes in fp16.
+template <int FB, int NC, int SB>
+__device__ __forceinline__ half2_t code_pair(const uint32_t* w, int i) {
+  using P = Pairs<FB, NC, SB>;
+  constexpr uint32_t fm = (1u << FB) - 1u, top = 1u << (FB - 1);
+  const int ao = P::T.ao[i], bo = P::T.bo[i];
+  const uint32_t ma = fm << ao, mb = fm << (16 + bo);
+  const uint32_t fa = top << ao, fb = top << (16 + bo);  // two's complement -> offset binary
+  uint32_t x;
+  if (P::T.Wa[i] == P::T.Wb[i]) {
+    const uint32_t v = window<P::NW>(w, P::T.Wa[i], P::T.ha[i]);
+    x = ((v ^ (fa | fb)) & (ma | mb)) | 0x64006400u;
+  } else {
+    const uint32_t va = window<P::NW>(w, P::T.Wa[i], P::T.ha[i]);
+    const uint32_t vb = window<P::NW>(w, P::T.Wb[i], P::T.hb[i]);
+    x = ((va ^ fa) & ma) | ((vb ^ fb) & mb) | 0x64006400u;
+  }
+  half2_t v;
+  __builtin_memcpy(&v, &x, 4);
+  const half2_t sc = {(_Float16)(1.0f / (float)(1 << ao)), (_Float16)(1.0f / (float)(1 << bo))};
+  const half2_t of = {(_Float16)(-(1024.0f / (float)(1 << ao) + (float)top)),
+                      (_Float16)(-(1024.0f / (float)(1 << bo) + (float)top))};
+  return __builtin_elementwise_fma(v, sc, of);
+}
+
+// Exact half(code * s) for all pairs of the chunk (quantizer.py:67-82: the
+// product code*s is exact in fp32 and rounded once to fp16; the packed fp16
+// multiply of the exact code rounds the same exact product once).
+template <int FB, int NC, int SB>
+__device__ __forceinline__ void dequant_pairs(const uint32_t* w, _Float16 s, half2_t* out) {
+  const half2_t ss = {s, s};
+#pragma unroll
+  for (int i = 0; i < NC / 2; ++i) out[i] = code_pair<FB, NC, SB>(w, i) * ss;
+}
+
+__device__ __forceinline__ uint32_t h2bits(half2_t v) {
+  uint32_t u;
+  __builtin_memcpy(&u, &v, 4);
+  return u;
+}
+
+// Buffer load of N bytes (N = 4, 6, 8, 12, 16) at byte offset off.
+template <int N>
+__device__ __forceinline__ void buf_load(uint32_t* w, __amdgpu_buffer_rsrc_t r, uint32_t off) {
+  if constexpr (N == 16) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    w[0] = v[0]; w[1] = v[1]; w[2] = v[2]; w[3] = v[3];
+  } else if constexpr (N == 12) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b96(r, off, 0, 0);
+    w[0] = v[0]; w[1] = v[1]; w[2] = v[2];
+  } else if constexpr (N == 8) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    w[0] = v[0]; w[1] = v[1];
+  } else if constexpr (N == 4) {
+    w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+  } else {
+    static_assert(N == 6, "chunk size");
+    const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+    const uint32_t mid = __builtin_amdgcn_raw_buffer_load_b16(r, off + 2, 0, 0);
+    const uint32_t hi = __builtin_amdgcn_raw_buffer_load_b16(r, off + 4, 0, 0);
+    w[0] = lo | (mid << 16);
+    w[1] = hi;
+  }
+}
+
+// ---------------------------------------------------------------- geometry
+template <int D, int BITS>
+struct PageGeom {
+  static constexpr int CH = D / 4;              // codes per lane (quarter row)
+  static constexpr int CHB = CH * BITS / 8;     // packed bytes per lane
+  static constexpr int NWC = (CHB + 3) / 4;     // 32-bit words per lane chunk
+  static constexpr int RB = row_bytes(D, BITS); // packed bytes per row
+  static constexpr int NCG = D / 32;            // K channel groups / scale groups
+  static constexpr int NS = CH / 8;             // 16x16x32 MFMA steps for S
+  static constexpr int NT = D / 16;             // PV output tiles
+  static constexpr int VROW = D / 2 + 4;        // V tile row stride in words (padded)
+  static constexpr int KSB = kPage * 32 / 2;    // K residual slot bytes
+  static constexpr int VSB = kVtb * D / 2;      // V residual slot bytes
+  using PB = Pairs<BITS, CH, BITS>;             // base codes
+  using PR = Pairs<4, CH, BITS>;                // V residual codes, base pair order
+  using PK = Pairs<4, 8, 4>;                    // K residual codes (8 per lane)
+};
+
+// Row resources of one (kv head, sequence): codes and scales of its pages.
+struct RowRes {
+  __amdgpu_buffer_rsrc_t kc, vc, ks, vs;
+};
+
+template <int D, int BITS, int SM>
+__device__ __forceinline__ RowRes row_resources(const carekv_arena& A, long pg_base) {
+  using G = PageGeom<D, BITS>;
+  const uint32_t rows = (uint32_t)A.max_pages * kPage;
+  constexpr int ssz = SM == 1 ? 1 : 2;
+  RowRes r;
+  r.kc = make_rsrc(A.kcodes + pg_base * kPage * G::RB, rows * G::RB);
+  r.vc = make_rsrc(A.vcodes + pg_base * kPage * G::RB, rows * G::RB);
+  r.ks = make_rsrc((const char*)A.kscale + pg_base * kPage * G::NCG * ssz, rows * G::NCG * ssz);
+  r.vs = make_rsrc((const char*)A.vscale + pg_base * kPage * G::NCG * ssz, rows * G::NCG * ssz);
+  return r;
+}
+
+// Lane's share of one page: packed codes and raw scale codes of its token
+// and quarter row.
+template <int D, int BITS>
+struct PageRegs {
+  uint32_t kw[PageGeom<D, BITS>::NWC], vw[PageGeom<D, BITS>::NWC];
+  int ksc, vsc;
+};
+
+template <int D, int BITS, int SM>
+__device__ __forceinline__ void load_page_regs(PageRegs<D, BITS>& r, const RowRes& rr, int p, int ln, int lj) {
+  using G = PageGeom<D, BITS>;
+  const uint32_t row = (uint32_t)(p * kPage + ln);
+  buf_load<G::CHB>(r.kw, rr.kc, row * G::RB + lj * G::CHB);
+  buf_load<G::CHB>(r.vw, rr.vc, row * G::RB + lj * G::CHB);
+  const int gi = (lj * G::CH) / 32;
+  if constexpr (SM == 1) {
+    r.ksc = (int)(int8_t)__builtin_amdgcn_raw_buffer_load_b8(rr.ks, row * G::NCG + gi, 0, 0);
+    r.vsc = (int)(int8_t)__builtin_amdgcn_raw_buffer_load_b8(rr.vs, row * G::NCG + gi, 0, 0);
+  } else {
+    r.ksc = __builtin_amdgcn_raw_buffer_load_b16(rr.ks, (row * G::NCG + gi) * 2, 0, 0);
+    r.vsc = __builtin_amdgcn_raw_buffer_load_b16(rr.vs, (row * G::NCG + gi) * 2, 0, 0);
+  }
+}
+
+// Scale of the lane's (token, group): int8 code read back as
+// half(code * master) (cache.py:713-718, SM = 1) or the raw fp16 scale.
+template <int SM>
+__device__ __forceinline__ _Float16 lane_scale(int code, float master) {
+  if constexpr (SM == 1) return (_Float16)((float)code * master);
+  else return bits2half((uint16_t)code);
+}
+
+// Uniform per-page metadata (scalar registers).
+template <int NCG>
+struct PageMeta {
+  int nv, meta;
+  int ksl[NCG], vsl[kVtb];
+};
+
+// Slot ids outside the arena read as "no slot".
+template <int NCG>
+__device__ __forceinline__ void load_page_meta(PageMeta<NCG>& m, const carekv_arena& A, long pg) {
+  m.nv = ((cint32_t*)A.valid)[pg];
+  m.meta = __builtin_amdgcn_readfirstlane((int)A.has_meta[pg]);
+#pragma unroll
+  for (int c = 0; c < NCG; ++c) {
+    const int s = ((cint32_t*)A.k_slot)[pg * NCG + c];
+    m.ksl[c] = s < A.n_slots ? s : -1;
+  }
+#pragma unroll
+  for (int v = 0; v < kVtb; ++v) {
+    const int s = ((cint32_t*)A.v_slot)[pg * kVtb + v];
+    m.vsl[v] = s < A.n_slots ? s : -1;
+  }
+}
+
+// S[token 4j+i][query m] += K_hat . q for the page (NS MFMA 16x16x32 steps).
+template <int D, int BITS>
+__device__ __forceinline__ float4_t page_scores(const uint32_t* kw, _Float16 ks, const half8_t* qB) {
+  using G = PageGeom<D, BITS>;
+  half2_t kp[G::CH / 2];
+  dequant_pairs<BITS, G::CH, BITS>(kw, ks, kp);
+  float4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < G::NS; ++s) {
+    const half8_t ak = {kp[4 * s][0], kp[4 * s][1], kp[4 * s + 1][0], kp[4 * s + 1][1],
+                        kp[4 * s + 2][0], kp[4 * s + 2][1], kp[4 * s + 3][0], kp[4 * s + 3][1]};
+    acc = mfma16x32(ak, qB[s], acc);
+  }
+  return acc;
+}
+
+// q in the order of the page_scores reduction: lane (m = query, j) holds
+// q_m at the dims of step s of its chunk.
+template <int D, int BITS>
+__device__ __forceinline__ void load_q_operand(half8_t* qB, const _Float16* sq, int ln, int lj) {
+  using G = PageGeom<D, BITS>;
+  using P = typename G::PB;
+  const _Float16* qp = sq + ln * D + lj * G::CH;
+#pragma unroll
+  for (int s = 0; s < G::NS; ++s)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) qB[s][e] = qp[P::T.slot_code[8 * s + e]];
+}
+
+// V tile rows in LDS: row m = token, CH/2 fp16 pairs per lane chunk, in
+// the slot order of the base pair schedule.
+template <int D, int BITS>
+__device__ __forceinline__ void vtile_write(uint32_t* vt, const half2_t* vp, int ln, int lj) {
+  using G = PageGeom<D, BITS>;
+  uint32_t* dst = vt + ln * G::VROW + lj * (G::CH / 2);
+#pragma unroll
+  for (int i = 0; i < G::CH / 2; i += 4)
+    *reinterpret_cast<uint4*>(dst + i) = make_uint4(h2bits(vp[i]), h2bits(vp[i + 1]), h2bits(vp[i + 2]),
+                                                    h2bits(vp[i + 3]));
+}
+
+// acc[t] += P V_tile: tile t, column n stands for slot n*NT + t (16x16x16
+// MFMA, k = the page's 16 tokens; P in the A layout: lane (m, j) holds
+// P[query m][token 4j+i]).
+template <int D, int BITS>
+__device__ __forceinline__ void pv_accumulate(const uint32_t* vt, half4_t ap, float4_t* acc, int ln, int lj) {
+  using G = PageGeom<D, BITS>;
+  constexpr int NT = G::NT;
+  uint32_t vr[4][NT / 2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t* src = vt + (4 * lj + i) * G::VROW + ln * (NT / 2);
+    if constexpr (NT / 2 == 4) {
+      const uint4 x = *reinterpret_cast<const uint4*>(src);
+      vr[i][0] = x.x; vr[i][1] = x.y; vr[i][2] = x.z; vr[i][3] = x.w;
+    } else {
+      const uint2 x = *reinterpret_cast<const uint2*>(src);
+      vr[i][0] = x.x; vr[i][1] = x.y;
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const int wi = t >> 1;
+    const uint32_t sel = (t & 1) ? 0x07060302u : 0x05040100u;  // high / low halves of two words
+    const uint32_t p01 = __builtin_amdgcn_perm(vr[1][wi], vr[0][wi], sel);
+    const uint32_t p23 = __builtin_amdgcn_perm(vr[3][wi], vr[2][wi], sel);
+    half4_t bv;
+    __builtin_memcpy(&bv, &p01, 4);
+    __builtin_memcpy(reinterpret_cast<char*>(&bv) + 4, &p23, 4);
+    acc[t] = mfma16(ap, bv, acc[t]);
+  }
+}
+
+// dS numerator of one K residual slot: racc[i] = sum_d code[token 4j+i][d] *
+// q_m[cg*32 + d] (exact codes, fp32 accumulation); the caller applies the
+// slot scale.  The slot holds 16 rows of 32 4-bit codes (16 bytes a row).
+__device__ __forceinline__ float4_t kslot_dot(const int8_t* slot_base, const _Float16* sq, int D, int cg, int ln,
+                                              int lj) {
+  using P = Pairs<4, 8, 4>;
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(slot_base, kPage * 16);
+  uint32_t w[1];
+  w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, ln * 16 + lj * 4, 0, 0);
+  half8_t ar;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const half2_t c = code_pair<4, 8, 4>(w, i);
+    ar[2 * i] = c[0];
+    ar[2 * i + 1] = c[1];
+  }
+  half8_t bq;
+  const _Float16* qp = sq + ln * D + cg * 32 + 8 * lj;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) bq[e] = qp[P::T.slot_code[e]];
+  const float4_t z = {0.f, 0.f, 0.f, 0.f};
+  return mfma16x32(ar, bq, z);
+}
+
+// Stage the GQ query rows of (b, kv head) in LDS as fp16 [16][D] (rows >= GQ
+// zero).  Call with all threads of the block, followed by a barrier.
+template <int D>
+__device__ __forceinline__ void stage_q(_Float16* sq, const uint16_t* q, int GQ) {
+  for (int i = threadIdx.x; i < 16 * D; i += blockDim.x) {
+    const int n = i / D;
+    sq[i] = n < GQ ? bits2half(q[i]) : (_Float16)0.f;
+  }
+}
+
+}  // namespace carekv

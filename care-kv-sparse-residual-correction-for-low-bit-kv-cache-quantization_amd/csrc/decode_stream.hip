@@ -4,163 +4,57 @@
 // Per page (lane l: m = l % 16, j = l / 16):
 //   * K and V codes of token m, dims [j*D/4, (j+1)*D/4) are dequantised
 //     exactly, half(code * scale) (quantizer.py:67-82; int8 scale codes read
-//     back as half(code * master), cache.py:713-718), two codes at a time:
-//     a packed field pair is masked into the mantissas of two fp16 values
-//     1024 + u*2^p (u = offset-binary code), one packed FMA recovers the two
-//     signed codes exactly, one packed multiply applies the scale with a
-//     single round-to-nearest-even.  The pairing fixes the order of the
-//     reduction dimension; q is loaded in the same order.
-//   * S = K_hat q for all query heads of the GQA group on MFMA 16x16x16 f16
-//     (rows: tokens, columns: query heads), online softmax in fp32.
-//   * O += P V_hat on MFMA, V_hat transposed through LDS.
-//   * For every stored K slot: dS = q_cg R_K / sqrt(D) on MFMA and the
-//     moments sum dS^2 e^k (k = 2, 3, 4) of e = exp(s - m_ref); for every
-//     stored V slot the block mass sum e.  These give the query-aware K score
-//     (attention.py:167-184) and V score (attention.py:788-790) once the
-//     global softmax statistics are known (finalize kernel).
-// The next page's codes, scales and slot tables are loaded while the
-// current page is processed.
-#include "decode_common.h"
+//     back as half(code * master), cache.py:713-718), two codes at a time.
+//   * S = K_hat q for all query heads of the GQA group on MFMA 16x16x32 f16
+//     (rows: tokens, columns: query heads); online softmax in fp32 on the
+//     base-2 logits s * log2(e) / sqrt(D).
+//   * O += P V_hat on MFMA 16x16x16 f16, V_hat transposed through LDS.
+//   * With correction on, the page record: the running max m_ref, for every
+//     stored K slot the moments sum dS^2 e^k (k = 2, 3, 4) of
+//     e = 2^(x - m_ref), dS = q_cg . R_K / sqrt(D), and for every stored V
+//     block the mass sum e.  Those give the query-aware K score
+//     (attention.py:167-184) and the V score (attention.py:788-790) once the
+//     global softmax statistics are known (select kernel).
+// The next page's codes, scales and metadata are loaded while the current
+// page is processed.
+#include "decode_page.h"
 #include "host_util.h"
 
 namespace carekv {
 
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
-
-// ---------------------------------------------------------------- unpack schedule
-// Codes are pair-wise (k, k + PD) inside blocks of BLK codes.
-template <int BITS> struct PairGeom;
-template <> struct PairGeom<2> { static constexpr int BLK = 16, PD = 8; };
-template <> struct PairGeom<3> { static constexpr int BLK = 8, PD = 4; };
-template <> struct PairGeom<4> { static constexpr int BLK = 8, PD = 4; };
-
-template <int BITS, int NC>
-struct Unpack {
-  static constexpr int NP = NC / 2;
-  static constexpr int NW = (NC * BITS + 31) / 32;
-  struct Tab {
-    int a[NP], b[NP], W[NP], ao[NP], bo[NP];
-    uint32_t xr[NW];
-    int slot_code[NC];  // slot e (2i + half) -> code index within the chunk
-  };
-  static constexpr Tab make() {
-    Tab t{};
-    constexpr int BLK = PairGeom<BITS>::BLK, PD = PairGeom<BITS>::PD, MAXO = 10 - BITS;
-    int n = 0;
-    for (int blk = 0; blk < NC; blk += BLK)
-      for (int k = 0; k < BLK / 2; ++k) {
-        const int ia = blk + k, ib = ia + PD;
-        const int ba = BITS * ia, bb = BITS * ib;
-        int lo = ba - MAXO, hi = ba;
-        if (bb - 16 - MAXO > lo) lo = bb - 16 - MAXO;
-        if (bb - 16 < hi) hi = bb - 16;
-        int W = hi;
-        for (int c = hi; c >= lo; --c)
-          if (c >= 0 && c % 32 == 0) { W = c; break; }
-        t.a[n] = ia; t.b[n] = ib; t.W[n] = W; t.ao[n] = ba - W; t.bo[n] = bb - W - 16;
-        t.slot_code[2 * n] = ia; t.slot_code[2 * n + 1] = ib;
-        ++n;
-      }
-    for (int k = 0; k < NC; ++k) {  // two's complement -> offset binary: flip each field's top bit
-      const int bit = BITS * k + BITS - 1;
-      t.xr[bit / 32] |= 1u << (bit % 32);
-    }
-    return t;
-  }
-  static constexpr Tab T = make();
-};
-
-// 32-bit window of the code bit string starting at bit W (W may be negative).
-template <int BITS, int NC>
-__device__ __forceinline__ uint32_t window(const uint32_t* w, int W, int hi_bit) {
-  if (W < 0) return w[0] << (-W);
-  const int d = W / 32, s = W % 32;
-  if (s == 0) return w[d];
-  if (hi_bit < 32 * (d + 1)) return w[d] >> s;
-  return __builtin_amdgcn_alignbit(w[d + 1], w[d], s);
-}
-
-// Exact half(code*s) for NC codes (two's complement, LE bit string in w,
-// w is modified) as NC/2 fp16 pairs (codes a_i, b_i of the schedule).
-template <int BITS, int NC>
-__device__ __forceinline__ void unpack_pairs(uint32_t* w, _Float16 s, half2_t* out) {
-  using U = Unpack<BITS, NC>;
-#pragma unroll
-  for (int i = 0; i < U::NW; ++i) w[i] ^= U::T.xr[i];
-  const half2_t ss = {s, s};
-  constexpr uint32_t fmask = (1u << BITS) - 1u;
-#pragma unroll
-  for (int i = 0; i < U::NP; ++i) {
-    const int W = U::T.W[i], ao = U::T.ao[i], bo = U::T.bo[i];
-    uint32_t x = window<BITS, NC>(w, W, BITS * U::T.b[i] + BITS - 1);
-    x = (x & ((fmask << ao) | (fmask << (16 + bo)))) | 0x64006400u;
-    half2_t v;
-    __builtin_memcpy(&v, &x, 4);
-    const half2_t sc = {(_Float16)(1.0f / (float)(1 << ao)), (_Float16)(1.0f / (float)(1 << bo))};
-    const half2_t of = {(_Float16)(-(1024.0f / (float)(1 << ao) + (float)(1 << (BITS - 1)))),
-                        (_Float16)(-(1024.0f / (float)(1 << bo) + (float)(1 << (BITS - 1))))};
-    const half2_t c = __builtin_elementwise_fma(v, sc, of);  // exact signed codes
-    out[i] = c * ss;                                          // one RNE rounding each
-  }
-}
-
-__device__ __forceinline__ uint32_t h2bits(half2_t v) {
-  uint32_t u;
-  __builtin_memcpy(&u, &v, 4);
-  return u;
-}
-
-template <int D, int BITS>
+template <int D, int BITS, int SM>
 __global__ __launch_bounds__(256) void decode_stream_kernel(carekv_arena A, DecodeArgs a) {
-  constexpr int NT = D / 16;           // MFMA k-steps for S; PV output tiles
-  constexpr int CH = D / 4;            // codes per lane (one quarter of a row)
-  constexpr int CHB = CH * BITS / 8;   // packed bytes per lane
-  constexpr int NWC = (CHB + 3) / 4;   // 32-bit words per lane chunk
-  constexpr int RB = row_bytes(D, BITS);
-  constexpr int NCG = D / 32;
-  constexpr int KSB = kPage * 32 / 2;
-  using U = Unpack<BITS, CH>;
-
-  constexpr int LDS_BYTES = 4 * 16 * D * 4;  // merge buffer; the V tiles use the first half
+  using G = PageGeom<D, BITS>;
+  constexpr int NT = G::NT, NCG = G::NCG, CH = G::CH;
+  constexpr int VT_WORDS = kPage * G::VROW;          // one wave's V tile
+  constexpr int MERGE_BYTES = 4 * 16 * D * 4;        // [4 waves][16 queries][D] fp32
+  constexpr int TILE_BYTES = 4 * VT_WORDS * 4;
+  constexpr int LDS_BYTES = MERGE_BYTES > TILE_BYTES ? MERGE_BYTES : TILE_BYTES;
   __shared__ __align__(16) char smem[LDS_BYTES];
+  __shared__ __align__(16) _Float16 sq[16 * D];
   __shared__ float s_m[4][16], s_l[4][16];
 
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-  const int Hkv = A.n_kv_heads, GQ = a.GQ;
-  const int bk = b * Hkv + kvh;
+  const int GQ = a.GQ;
+  const int bk = b * A.n_kv_heads + kvh;
   const int seq_raw = a.seq_slot[b], np_raw = a.n_pages[b];
   const bool row_ok = seq_raw >= 0 && seq_raw < A.n_seq && np_raw >= 0 && np_raw <= a.Pmax;
   const int seq = row_ok ? seq_raw : 0, np = row_ok ? np_raw : 0;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int ln = lane & 15, lj = lane >> 4;
   const long pg_base = ((long)kvh * A.n_seq + seq) * A.max_pages;
-  const int F = a.F;
-  const int gi = (lj * CH) / 32;  // quant group of this lane's chunk
+  const RowRes rr = row_resources<D, BITS, SM>(A, pg_base);
+  const bool corr = a.correction != 0;
+  const float sm_log2 = a.sm_log2;
+  const long rq = (long)a.Pmax * a.F;  // record stride between query heads
 
-  // ---- B operands.  S step s uses codes (a_2s, b_2s, a_2s+1, b_2s+1) of the
-  // lane's chunk; lane (n = query, j) holds q_n at those dims.  qR[cg][s]:
-  // q_n[cg*32 + 8j + 4s + i] for the dS product with the 4-bit K slot rows.
-  half4_t qB[NT], qR[NCG][2];
-  {
-    const bool qv = ln < GQ;
-    const uint16_t* qp = a.q + ((long)b * a.Hq + kvh * GQ + (qv ? ln : 0)) * D;
-#pragma unroll
-    for (int s = 0; s < NT; ++s) {
-      const int c0 = lj * CH;
-      qB[s][0] = qv ? bits2half(qp[c0 + U::T.a[2 * s]]) : (_Float16)0.f;
-      qB[s][1] = qv ? bits2half(qp[c0 + U::T.b[2 * s]]) : (_Float16)0.f;
-      qB[s][2] = qv ? bits2half(qp[c0 + U::T.a[2 * s + 1]]) : (_Float16)0.f;
-      qB[s][3] = qv ? bits2half(qp[c0 + U::T.b[2 * s + 1]]) : (_Float16)0.f;
-    }
-#pragma unroll
-    for (int cg = 0; cg < NCG; ++cg)
-#pragma unroll
-      for (int s = 0; s < 2; ++s)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) qR[cg][s][i] = qv ? bits2half(qp[cg * 32 + 8 * lj + 4 * s + i]) : (_Float16)0.f;
-  }
+  stage_q<D>(sq, a.q + ((long)b * a.Hq + kvh * GQ) * D, GQ);
+  __syncthreads();
+  half8_t qB[G::NS];
+  load_q_operand<D, BITS>(qB, sq, ln, lj);
 
-  uint32_t* vt = reinterpret_cast<uint32_t*>(smem) + w * kPage * (D / 2);  // this wave's V tile, pairs
+  uint32_t* vt = reinterpret_cast<uint32_t*>(smem) + w * VT_WORDS;
   float m_run = -INFINITY, l_run = 0.f;
   float4_t oacc[NT];
 #pragma unroll
@@ -168,119 +62,54 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(carekv_arena A, Deco
 
   const int p_begin = split * a.SP, p_end = min(p_begin + a.SP, np);
 
-  // ---- prefetched page state
-  uint32_t kw[NWC + 1], vw[NWC + 1];
-  int ksc = 0, vsc = 0, nvld = 0, meta = 0;
-  float kmast = 0.f, vmast = 0.f;
-  int ksl[NCG], vsl[kVtb];
-  auto load_page = [&](int p, uint32_t* kwo, uint32_t* vwo, int& kso, int& vso, float& kmo, float& vmo, int& nvo,
-                       int& meo, int* kslo, int* vslo) {
-    const long pg = pg_base + p;
-    kwo[NWC] = 0; vwo[NWC] = 0;
-    load_bytes<CHB>(kwo, A.kcodes + (pg * kPage + ln) * RB + lj * CHB);
-    load_bytes<CHB>(vwo, A.vcodes + (pg * kPage + ln) * RB + lj * CHB);
-    if (A.scale_mode == 1) {
-      kso = ((const int8_t*)A.kscale)[(pg * kPage + ln) * NCG + gi];
-      vso = ((const int8_t*)A.vscale)[(pg * kPage + ln) * NCG + gi];
-      kmo = h2f(A.kmaster[pg]);
-      vmo = h2f(A.vmaster[pg]);
-    } else {
-      kso = ((const uint16_t*)A.kscale)[(pg * kPage + ln) * NCG + gi];
-      vso = ((const uint16_t*)A.vscale)[(pg * kPage + ln) * NCG + gi];
-    }
-    nvo = A.valid[pg];
-    meo = A.has_meta[pg];
-#pragma unroll
-    for (int c = 0; c < NCG; ++c) kslo[c] = A.k_slot[pg * NCG + c];
-#pragma unroll
-    for (int v = 0; v < kVtb; ++v) vslo[v] = A.v_slot[pg * kVtb + v];
-  };
+  PageRegs<D, BITS> nx;
+  PageMeta<NCG> nm;
+  float nkm = 0.f, nvm = 0.f;
   int p = p_begin + w;
-  if (p < p_end) load_page(p, kw, vw, ksc, vsc, kmast, vmast, nvld, meta, ksl, vsl);
-
+  if (p < p_end) {
+    load_page_regs<D, BITS, SM>(nx, rr, p, ln, lj);
+    load_page_meta<NCG>(nm, A, pg_base + p);
+    if constexpr (SM == 1) { nkm = h2f(A.kmaster[pg_base + p]); nvm = h2f(A.vmaster[pg_base + p]); }
+  }
   for (; p < p_end; p += 4) {
-    // current page state
-    uint32_t ckw[NWC + 1], cvw[NWC + 1];
-#pragma unroll
-    for (int i = 0; i <= NWC; ++i) { ckw[i] = kw[i]; cvw[i] = vw[i]; }
-    const int cks = ksc, cvs = vsc, nv = nvld, cmeta = meta;
-    const float ckm = kmast, cvm = vmast;
-    int cksl[NCG], cvsl[kVtb];
-#pragma unroll
-    for (int c = 0; c < NCG; ++c) cksl[c] = ksl[c];
-#pragma unroll
-    for (int v = 0; v < kVtb; ++v) cvsl[v] = vsl[v];
-    if (p + 4 < p_end) load_page(p + 4, kw, vw, ksc, vsc, kmast, vmast, nvld, meta, ksl, vsl);
-    const long pg = pg_base + p;
-    float* rec = a.rec + ((long)bk * a.Pmax + p) * GQ * F;
-    if (nv <= 0) {
-      if (lj == 0 && ln < GQ) rec[ln * F] = -INFINITY;
-      continue;
+    const PageRegs<D, BITS> cur = nx;
+    const PageMeta<NCG> cm = nm;
+    const float ckm = nkm, cvm = nvm;
+    if (p + 4 < p_end) {
+      load_page_regs<D, BITS, SM>(nx, rr, p + 4, ln, lj);
+      load_page_meta<NCG>(nm, A, pg_base + p + 4);
+      if constexpr (SM == 1) { nkm = h2f(A.kmaster[pg_base + p + 4]); nvm = h2f(A.vmaster[pg_base + p + 4]); }
     }
-    // K slot rows of this page (issued early, used after the attention math)
-    uint32_t rw[NCG];
-    float rsc[NCG];
-#pragma unroll
-    for (int cg = 0; cg < NCG; ++cg) {
-      rw[cg] = 0; rsc[cg] = 0.f;
-      if (cmeta && cksl[cg] >= 0) {
-        const long so = (long)seq * A.n_slots + cksl[cg];
-        rw[cg] = *reinterpret_cast<const uint32_t*>(A.k_res + so * KSB + ln * 16 + lj * 4);
-        rsc[cg] = h2f(A.k_res_scale[so]);
-      }
-    }
-    _Float16 ks, vs;
-    if (A.scale_mode == 1) {
-      ks = (_Float16)((float)cks * ckm);
-      vs = (_Float16)((float)cvs * cvm);
-    } else {
-      ks = bits2half((uint16_t)cks);
-      vs = bits2half((uint16_t)cvs);
-    }
+    const int nv = cm.nv;
+    if (nv <= 0) continue;
     // ---- S = K_hat q
-    half2_t kp[CH / 2];
-    unpack_pairs<BITS, CH>(ckw, ks, kp);
-    float4_t sacc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < NT; ++s) {
-      const half4_t ak = {kp[2 * s][0], kp[2 * s][1], kp[2 * s + 1][0], kp[2 * s + 1][1]};
-      sacc = mfma16(ak, qB[s], sacc);
-    }
-    // V_hat pairs to LDS while the softmax runs
+    const _Float16 ks = lane_scale<SM>(cur.ksc, ckm), vs = lane_scale<SM>(cur.vsc, cvm);
+    const float4_t sacc = page_scores<D, BITS>(cur.kw, ks, qB);
+    // ---- V_hat pairs to LDS while the softmax runs
     {
       half2_t vp[CH / 2];
-      unpack_pairs<BITS, CH>(cvw, vs, vp);
-      uint32_t* dst = vt + ln * (D / 2) + lj * (CH / 2);
-#pragma unroll
-      for (int i = 0; i < CH / 2; i += 4) {
-        *reinterpret_cast<uint4*>(dst + i) = make_uint4(h2bits(vp[i]), h2bits(vp[i + 1]), h2bits(vp[i + 2]),
-                                                        h2bits(vp[i + 3]));
-      }
+      dequant_pairs<BITS, CH, BITS>(cur.vw, vs, vp);
+      vtile_write<D, BITS>(vt, vp, ln, lj);
     }
     // lane (n = query, j): sacc[i] = S[token 4j+i][query n]
-    float sv[4], e[4];
-    float mx = -INFINITY;
+    float x[4];
+    if (nv >= kPage) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      sv[i] = (4 * lj + i < nv) ? sacc[i] * a.sm_scale : -INFINITY;
-      mx = fmaxf(mx, sv[i]);
+      for (int i = 0; i < 4; ++i) x[i] = sacc[i] * sm_log2;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[i] = (4 * lj + i < nv) ? sacc[i] * sm_log2 : -INFINITY;
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx);
-    float f_old = 1.f;
-    if (m_new > m_run) f_old = (m_run == -INFINITY) ? 0.f : expf(m_run - m_new);
+    const float mx = col_max(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));
+    const float m_new = fmaxf(m_run, mx);  // finite: token 0 of a page is always valid
+    const float f_old = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first page
     m_run = m_new;
-    float esum = 0.f;
+    float e[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      e[i] = (4 * lj + i < nv) ? expf(sv[i] - m_run) : 0.f;
-      esum += e[i];
-    }
-    esum += __shfl_xor(esum, 16, 64);
-    esum += __shfl_xor(esum, 32, 64);
-    l_run = l_run * f_old + esum;
-    if (__builtin_amdgcn_read_exec() && __any(f_old != 1.f)) {
+    for (int i = 0; i < 4; ++i) e[i] = __builtin_amdgcn_exp2f(x[i] - m_new);
+    l_run = l_run * f_old + col_sum((e[0] + e[1]) + (e[2] + e[3]));
+    if (__builtin_expect(__any(f_old != 1.f), 0)) {
+      // rows of oacc are queries 4j+i: their factors live in lanes 4j+i
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float fi = __shfl(f_old, 4 * lj + i, 64);
@@ -288,82 +117,54 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(carekv_arena A, Deco
         for (int t = 0; t < NT; ++t) oacc[t][i] *= fi;
       }
     }
-    const half4_t ap = {(_Float16)e[0], (_Float16)e[1], (_Float16)e[2], (_Float16)e[3]};
-    // ---- O += P V_hat.  Tile t, column n stands for V slot n*NT + t.
+    half4_t ap;
+    ap[0] = (_Float16)e[0]; ap[1] = (_Float16)e[1]; ap[2] = (_Float16)e[2]; ap[3] = (_Float16)e[3];
+    // ---- O += P V_hat
     lds_sync_wave();
-    uint32_t vr[4][NT / 2];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t* src = vt + (4 * lj + i) * (D / 2) + ln * (NT / 2);
-      if constexpr (NT / 2 == 4) {
-        const uint4 x = *reinterpret_cast<const uint4*>(src);
-        vr[i][0] = x.x; vr[i][1] = x.y; vr[i][2] = x.z; vr[i][3] = x.w;
-      } else {
-        const uint2 x = *reinterpret_cast<const uint2*>(src);
-        vr[i][0] = x.x; vr[i][1] = x.y;
-      }
-    }
-#pragma unroll
-    for (int t = 0; t < NT; ++t) {
-      const int wi = t >> 1;
-      const uint32_t sel = (t & 1) ? 0x07060302u : 0x05040100u;  // high / low halves of two words
-      const uint32_t p01 = __builtin_amdgcn_perm(vr[1][wi], vr[0][wi], sel);
-      const uint32_t p23 = __builtin_amdgcn_perm(vr[3][wi], vr[2][wi], sel);
-      half4_t bv;
-      __builtin_memcpy(&bv, &p01, 4);
-      __builtin_memcpy(reinterpret_cast<char*>(&bv) + 4, &p23, 4);
-      oacc[t] = mfma16(ap, bv, oacc[t]);
-    }
-    lds_sync_wave();
+    pv_accumulate<D, BITS>(vt, ap, oacc, ln, lj);
 
-    // ---- record: m_ref, K-slot moments, V-block masses
-    if (lj == 0 && ln < GQ) rec[ln * F] = m_run;
-    if (cmeta) {
+    if (corr && cm.meta) {
+      // ---- page record (layout in decode_common.h)
+      float* rec = a.rec + ((long)bk * GQ * a.Pmax + p) * a.F + ln * rq;
+      if (lj == 0 && ln < GQ) rec[0] = m_new;
       int rk = 0;
 #pragma unroll
       for (int cg = 0; cg < NCG; ++cg) {
-        if (cksl[cg] < 0) continue;
+        const int slot = cm.ksl[cg];
+        if (slot < 0) continue;
         if (rk >= a.k_cap) { if (lane == 0) *a.err_flag = 1; break; }
-        half4_t r0, r1;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          r0[i] = (_Float16)(float)get_code<4>(&rw[cg], i);
-          r1[i] = (_Float16)(float)get_code<4>(&rw[cg], 4 + i);
-        }
-        float4_t racc = {0.f, 0.f, 0.f, 0.f};
-        racc = mfma16(r0, qR[cg][0], racc);
-        racc = mfma16(r1, qR[cg][1], racc);
+        const long so = (long)seq * A.n_slots + slot;
+        const float4_t racc = kslot_dot(A.k_res + so * G::KSB, sq, D, cg, ln, lj);
+        const float f = h2f(A.k_res_scale[so]) * a.inv_sqrt_d;
         float M2 = 0.f, M3 = 0.f, M4 = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float ds = (racc[i] * rsc[cg]) / a.sqrt_d;
-          const float y = ds * e[i];
-          const float x = y * y;
-          const float xe = x * e[i];
-          M2 += x;
+          const float y = (racc[i] * f) * e[i];
+          const float xx = y * y;
+          const float xe = xx * e[i];
+          M2 += xx;
           M3 += xe;
-          M4 += xe * e[i];
+          M4 = fmaf(xe, e[i], M4);
         }
-        M2 += __shfl_xor(M2, 16, 64); M2 += __shfl_xor(M2, 32, 64);
-        M3 += __shfl_xor(M3, 16, 64); M3 += __shfl_xor(M3, 32, 64);
-        M4 += __shfl_xor(M4, 16, 64); M4 += __shfl_xor(M4, 32, 64);
+        M2 = col_sum(M2); M3 = col_sum(M3); M4 = col_sum(M4);
         if (lj == 0 && ln < GQ) {
-          float* r = rec + ln * F + 1 + 3 * rk;
-          r[0] = M2; r[1] = M3; r[2] = M4;
+          rec[1 + 3 * rk] = M2; rec[2 + 3 * rk] = M3; rec[3 + 3 * rk] = M4;
         }
         ++rk;
       }
-      int rv = 0, my_slot = -1, my_rank = 0;
+      int rv = 0, my_rank = -1;
 #pragma unroll
       for (int vb = 0; vb < kVtb; ++vb) {
-        if (vb == lj) { my_slot = cvsl[vb]; my_rank = rv; }
-        rv += cvsl[vb] >= 0;
+        if (cm.vsl[vb] < 0) continue;
+        if (vb == lj) my_rank = rv;
+        ++rv;
       }
-      if (my_slot >= 0 && ln < GQ) {
-        if (my_rank < a.v_cap) rec[ln * F + 1 + 3 * a.k_cap + my_rank] = e[0] + e[1] + e[2] + e[3];
+      if (my_rank >= 0 && ln < GQ) {
+        if (my_rank < a.v_cap) rec[1 + 3 * a.k_cap + my_rank] = (e[0] + e[1]) + (e[2] + e[3]);
         else *a.err_flag = 1;
       }
     }
+    lds_sync_wave();
   }
 
   // ---- merge the 4 waves' (m, l, O) and write the split partial; V slot
@@ -374,7 +175,7 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(carekv_arena A, Deco
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     const int slot = ln * NT + t;
-    const int dim = (slot / CH) * CH + U::T.slot_code[slot % CH];
+    const int dim = (slot / CH) * CH + G::PB::T.slot_code[slot % CH];
 #pragma unroll
     for (int i = 0; i < 4; ++i) so[(w * 16 + 4 * lj + i) * D + dim] = oacc[t][i];
   }
@@ -389,7 +190,7 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(carekv_arena A, Deco
     if (M != -INFINITY) {
 #pragma unroll
       for (int ww = 0; ww < 4; ++ww) {
-        const float f = s_m[ww][qq] == -INFINITY ? 0.f : expf(s_m[ww][qq] - M);
+        const float f = __builtin_amdgcn_exp2f(s_m[ww][qq] - M);
         L += s_l[ww][qq] * f;
         O += so[(ww * 16 + qq) * D + d] * f;
       }
@@ -401,8 +202,9 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(carekv_arena A, Deco
 
 int launch_decode_stream(const carekv_arena& A, const DecodeArgs& a, hipStream_t s) {
   dim3 grid(a.nsplit, A.n_kv_heads, a.B);
-  return dispatch_db(A.head_dim, A.base_bits, [&](auto d, auto bb) {
-    hipLaunchKernelGGL((decode_stream_kernel<decltype(d)::value, decltype(bb)::value>), grid, dim3(256), 0, s, A, a);
+  return dispatch_dbs(A.head_dim, A.base_bits, A.scale_mode, [&](auto d, auto bb, auto sm) {
+    hipLaunchKernelGGL((decode_stream_kernel<decltype(d)::value, decltype(bb)::value, decltype(sm)::value>), grid,
+                       dim3(256), 0, s, A, a);
     CAREKV_CHECK_LAUNCH("decode_stream");
     return CAREKV_OK;
   });

@@ -55,4 +55,15 @@ int dispatch_db(int D, int bits, F&& f) {
   return CAREKV_EINVAL;
 }
 
+// dispatch_db plus the scale encoding (0: fp16 scales, 1: int8 codes).
+template <typename F>
+int dispatch_dbs(int D, int bits, int scale_mode, F&& f) {
+  using S0 = std::integral_constant<int, 0>;
+  using S1 = std::integral_constant<int, 1>;
+  return dispatch_db(D, bits, [&](auto d, auto bb) {
+    if (scale_mode == 1) return f(d, bb, S1{});
+    return f(d, bb, S0{});
+  });
+}
+
 }  // namespace carekv
