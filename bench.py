@@ -69,18 +69,25 @@ def gen_kv(torch, spec, b, device):
 
 
 def algorithmic_bytes(spec, cfg, cache, diag_np):
-    """Bytes one decode step must move (per the roofline model):
-    packed K+V codes, int8 group scales, fp16 masters, every stored K slot
-    (read by the query-aware K score), fp16 V errors, int32 slot tables, the
-    selected V slots (union over the GQA group) and q/out."""
-    import numpy as np
+    """Bytes one decode step must move (the roofline model), split into the
+    streaming kernel's share and the rest.
+
+    Streaming kernel (reads every page once): packed K+V codes, int8 group
+    scales, fp16 page masters, valid/has_meta/slot tables, every stored K
+    residual slot (the query-aware K score needs dS on all of them) with its
+    scale, q.  Rest of the step: the page tables again for scoring (v_sq,
+    v_err), the selected V residual slots (union over the GQA group) and
+    the fp16 output.  Workspace traffic between the kernels is not counted."""
     B, Hq, Hkv, D, N = spec["B"], spec["Hq"], spec["Hkv"], spec["D"], spec["N"]
     bits, G, P = cfg.base_bits, D // 32, math.ceil(N / 16)
     grp = Hq // Hkv
     k_slots = (cache.k_slot[0, :, :B, :P] >= 0).sum().item()          # stored K slots (all b, kvh)
-    per_bkv_fixed = (2 * N * D * bits / 8 + 2 * N * G + 2 * P * 2 + P * 4 * 2 + P * (D // 32 + 4) * 4
-                     + 2 * grp * D * 2)
-    total = B * Hkv * per_bkv_fixed + k_slots * (16 * 32 // 2 + 2)
+    per_bkv_stream = (2 * N * D * bits / 8            # K + V codes
+                      + 2 * N * G                     # int8 scales
+                      + 2 * P * 2                     # fp16 masters
+                      + P * (4 + 1 + (G + 4) * 4)     # valid, has_meta, k_slot, v_slot
+                      + grp * D * 2)                  # q
+    stream = B * Hkv * per_bkv_stream + k_slots * (16 * 32 // 2 + 2)
     v_union = 0
     for b in range(B):
         for h in range(Hkv):
@@ -92,8 +99,43 @@ def algorithmic_bytes(spec, cfg, cache, diag_np):
                     if (int(x) >> 30) == 1:
                         s.add(int(x) & ((1 << 30) - 1))
             v_union += len(s)
-    total += v_union * (4 * D // 2 + 2)
-    return float(total), int(k_slots), int(v_union)
+    rest = B * Hkv * P * (4 + 4 * 2) + v_union * (4 * D // 2 + 2) + B * Hq * D * 2
+    return float(stream), float(stream + rest), int(k_slots), int(v_union)
+
+
+def copy_calibration(mib, steps):
+    """Plain device-to-device copy of `mib` MiB (torch copy kernel): the
+    reference kernel for scaling FETCH_SIZE / WRITE_SIZE counters and an
+    achievable-bandwidth yardstick."""
+    import torch
+    dev = torch.device("cuda", 0)
+    n = mib * 2**20 // 4
+    src = torch.empty(n, dtype=torch.float32, device=dev).fill_(1.0)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        dst.copy_(src)
+    e1.record()
+    e1.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    gbs = 2 * n * 4 / (ms * 1e-3) / 1e9
+    print(json.dumps({"metric": "device copy GB/s (read+write)", "value": round(gbs, 1), "unit": "GB/s",
+                      "bytes_read_per_launch": n * 4, "bytes_written_per_launch": n * 4, "steps": steps,
+                      "ms_per_launch": round(ms, 4)}), flush=True)
+
+
+def load_traffic(kernel, workload):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC
+    summary (profiles/<kernel>_<workload>_traffic.json), or None."""
+    p = os.path.join(ROOT, "profiles", f"{kernel}_{workload}_traffic.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        return json.load(f)
 
 
 def oracle_slice_from_device(cache, seq, kvh, spec):
@@ -170,11 +212,16 @@ def main():
     ap.add_argument("--split-pages", type=int, default=None)
     ap.add_argument("--no-correction", action="store_true",
                     help="time the base attention path only (streaming pass + split combine)")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="instead of the decode, time a plain device copy of this many MiB (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): the decode path is embarrassingly "
               "parallel over (sequence, kv head) and is not built for several GPUs in this tree.", file=sys.stderr)
         sys.exit(2)
+    if args.copy_mib > 0:
+        copy_calibration(args.copy_mib, args.steps)
+        return
     os.environ.update(PAPER_ENV)
     import numpy as np
     import torch
@@ -203,24 +250,37 @@ def main():
     out, diag = care_kv.decode_attention(cache, 0, q, diag_cap=512, split_pages=args.split_pages)
     torch.cuda.synchronize()
     diag_np = diag.cpu().numpy()
-    nbytes, k_slots, v_union = algorithmic_bytes(spec, cfg, cache, diag_np)
+    stream_bytes, nbytes, k_slots, v_union = algorithmic_bytes(spec, cfg, cache, diag_np)
     corr = not args.no_correction
     for _ in range(args.warmup):
         care_kv.decode_attention(cache, 0, q, out=out, split_pages=args.split_pages, correction=corr)
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
+    # per-step phase events (recorded once so that the handles exist), re-recorded by the library on the
+    # launch stream around its kernels
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(args.steps)]
+    for row in evs:
+        for e in row:
+            e.record(stream)
+    torch.cuda.synchronize()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     ev0.record(stream)
-    for _ in range(args.steps):
-        care_kv.decode_attention(cache, 0, q, out=out, split_pages=args.split_pages, correction=corr)
+    for k in range(args.steps):
+        care_kv.decode_attention(cache, 0, q, out=out, split_pages=args.split_pages, correction=corr,
+                                 phase_events=evs[k])
     ev1.record(stream)
     ev1.synchronize()
     ms_total = ev0.elapsed_time(ev1)
     ms_step = ms_total / args.steps
     us_step = ms_step * 1e3
+    phase = [sum(row[i].elapsed_time(row[i + 1]) for row in evs) / args.steps * 1e3 for i in range(4)]
+    names = ["stream", "select", "apply", "combine"]
     gbps = nbytes / (ms_step * 1e-3) / 1e9
+    stream_gbps = stream_bytes / (phase[0] * 1e-6) / 1e9
     log(f"[bench] {us_step:.1f} us/step, {nbytes / 1e9:.3f} GB algorithmic/step, {gbps:.0f} GB/s, "
         f"K slots {k_slots}, V union {v_union}")
+    log("[bench] phases (us): " + ", ".join(f"{n} {t:.1f}" for n, t in zip(names, phase)) +
+        f"; streaming kernel {stream_bytes / 1e9:.3f} GB -> {stream_gbps:.0f} GB/s")
     cpu = None
     if not args.no_cpu_baseline:
         q_np = q.cpu().numpy()
@@ -235,6 +295,8 @@ def main():
                "sample": f"{args.cpu_slices} of {B * Hkv} (sequence, kv-head) slices of the same cache "
                          f"({per_slice:.3f} s each, numpy oracle), extrapolated x{B * Hkv}"}
         log(f"[bench] cpu oracle {per_slice:.3f} s/slice -> {cpu_us / 1e3:.1f} ms/step extrapolated")
+    tr = load_traffic("decode_stream", args.config + ("_base" if args.no_correction else ""))
+    traffic = None if tr is None else tr.get("hbm_bytes_per_launch")
     line = {
         "metric": "CARE-KV decode-attn us/step + HBM GB/s (% roofline), Mistral-7B shape 32K ctx",
         "value": round(us_step, 2), "unit": "us/step", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -245,9 +307,12 @@ def main():
                    "read": f"joint top-{spec['rk'] + spec['rv']} (K {spec['rk']} + V {spec['rv']}), "
                            "KSCORE_LIVE, normalize, exact"},
         "hbm_gbps": round(gbps, 1),
-        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": 8000.0, "unit": "GB/s",
-                     "frac": round(gbps / 8000.0, 4), "traffic": None,
-                     "algorithmic_bytes_per_launch": int(nbytes)},
+        "phases_us": {n: round(t, 2) for n, t in zip(names, phase)},
+        "roofline": {"bound": "hbm", "kernel": f"decode_stream_kernel<{D},{cfg.base_bits},1>",
+                     "achieved": round(stream_gbps, 1), "peak": 8000.0, "unit": "GB/s",
+                     "frac": round(stream_gbps / 8000.0, 4), "traffic": traffic,
+                     "algorithmic_bytes_per_launch": int(stream_bytes), "launch_us": round(phase[0], 2),
+                     "step_frac": round(gbps / 8000.0, 4), "step_algorithmic_bytes": int(nbytes)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

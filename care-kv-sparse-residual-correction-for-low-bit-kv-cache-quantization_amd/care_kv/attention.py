@@ -12,6 +12,7 @@ points (attention.py:964-1077) on top of it.
 """
 from __future__ import annotations
 
+import ctypes
 import math
 import os
 from typing import Optional, Sequence
@@ -37,12 +38,14 @@ def default_split_pages(max_pages: int, rows: int) -> int:
 
 def decode_attention(cache: CAREKVCache, layer: int, q: torch.Tensor, seqs: Optional[Sequence[int]] = None, *,
                      correction: bool = True, knobs: Optional[ReadKnobs] = None, split_pages: Optional[int] = None,
-                     diag_cap: int = 0, out: Optional[torch.Tensor] = None):
+                     diag_cap: int = 0, out: Optional[torch.Tensor] = None, phase_events=None):
     """q: (B, Hq, D) fp16 post-RoPE queries of B sequences -> (B, Hq, D) fp16.
 
     With ``diag_cap > 0`` also returns the selected candidates per query
     head as an int32 (B, Hq, diag_cap) tensor (kind<<30 | page<<3 | sub, -1
-    padded), for parity checks."""
+    padded), for parity checks.  ``phase_events``: optional sequence of 5
+    recorded torch.cuda.Event (timing enabled), re-recorded on the launch
+    stream around the streaming, select, apply and combine kernels."""
     cfg: CacheConfig = cache.cfg
     if q.dim() == 2:
         q = q.unsqueeze(0)
@@ -75,6 +78,12 @@ def decode_attention(cache: CAREKVCache, layer: int, q: torch.Tensor, seqs: Opti
         lambda_k=knobs.lambda_k, lambda_v=knobs.lambda_v, budget_ratio=int(knobs.budget_ratio),
         abs_k=knobs.abs_k, abs_v=knobs.abs_v, ratio_k=knobs.ratio_k, ratio_v=knobs.ratio_v,
         k_cap=cache.k_cap, v_cap=cache.v_cap, split_pages=int(split_pages))
+    ev_arr = None
+    if phase_events is not None:
+        if len(phase_events) != 5:
+            raise ValueError("phase_events needs 5 events")
+        ev_arr = (ctypes.c_void_p * 5)(*[int(e.cuda_event) for e in phase_events])
+        dp.phase_events = ctypes.cast(ev_arr, ctypes.c_void_p)
     lib = _lib.load()
     a = cache.arena(layer)
     nbytes = int(lib.carekv_decode_workspace_bytes(a, dp))

@@ -7,7 +7,7 @@ using namespace carekv;
 
 namespace {
 struct WsLayout {
-  long err, pml, po, rec, scores, mask, ob, ml, num, den, total;
+  long err, pml, po, rec, scores, mask, ml, num, den, total;
   int nsplit, F, ncand;
 };
 
@@ -28,7 +28,6 @@ WsLayout ws_layout(const carekv_arena& A, const carekv_decode_params& dp) {
   L.rec = off; off += al(BH * GQ * (long)Pm * L.F * 4);
   L.scores = off; off += al(BH * GQ * (long)L.ncand * 4);
   L.mask = off; off += al(BH * GQ * (long)Pm);
-  L.ob = off; off += al(BH * GQ * (long)D * 4);
   L.ml = off; off += al(BH * GQ * 2 * 4);
   L.num = off; off += al(BH * L.nsplit * GQ * (long)D * 4);
   L.den = off; off += al(BH * L.nsplit * GQ * 4);
@@ -76,7 +75,6 @@ extern "C" int carekv_decode_attn(const carekv_arena* arena, const carekv_decode
   a.rec = (float*)(ws + L.rec);
   a.scores = (float*)(ws + L.scores);
   a.mask = (uint8_t*)(ws + L.mask);
-  a.ob = (float*)(ws + L.ob);
   a.ml = (float*)(ws + L.ml);
   a.num = (float*)(ws + L.num);
   a.den = (float*)(ws + L.den);
@@ -92,9 +90,22 @@ extern "C" int carekv_decode_attn(const carekv_arena* arena, const carekv_decode
   a.k_exact = dp->k_exact; a.budget_ratio = dp->budget_ratio; a.abs_k = dp->abs_k; a.abs_v = dp->abs_v;
   a.ratio_k = dp->ratio_k; a.ratio_v = dp->ratio_v;
   hipStream_t s = (hipStream_t)stream;
-  int rc = launch_decode_stream(A, a, s);
+  hipEvent_t* ev = (hipEvent_t*)dp->phase_events;
+  auto mark = [&](int i) -> int {
+    if (ev && hipEventRecord(ev[i], s) != hipSuccess) {
+      set_error("carekv_decode_attn: hipEventRecord failed on phase event %d", i);
+      return CAREKV_ELAUNCH;
+    }
+    return CAREKV_OK;
+  };
+  int rc = mark(0);
+  if (rc == CAREKV_OK) rc = launch_decode_stream(A, a, s);
+  if (rc == CAREKV_OK) rc = mark(1);
   if (rc == CAREKV_OK) rc = launch_decode_select(A, a, s);
+  if (rc == CAREKV_OK) rc = mark(2);
   if (rc == CAREKV_OK && a.correction) rc = launch_decode_apply(A, a, s);
+  if (rc == CAREKV_OK) rc = mark(3);
   if (rc == CAREKV_OK && a.correction) rc = launch_decode_combine(A, a, s);
+  if (rc == CAREKV_OK) rc = mark(4);
   return rc;
 }

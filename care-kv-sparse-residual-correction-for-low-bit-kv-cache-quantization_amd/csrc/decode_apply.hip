@@ -32,17 +32,20 @@ constexpr bool same_slot_order() {
 }
 
 template <int D, int BITS, int SM>
-__global__ __launch_bounds__(256) void decode_apply_kernel(carekv_arena A, DecodeArgs a) {
+// 4 waves per SIMD: the register budget is capped at 128 VGPRs.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8)))
+void decode_apply_kernel(carekv_arena A, DecodeArgs a) {
   using G = PageGeom<D, BITS>;
   static_assert(same_slot_order<D, BITS>(), "V residual tile must use the V_hat slot order");
   constexpr int NT = G::NT, NCG = G::NCG, CH = G::CH;
   constexpr int VT_WORDS = kPage * G::VROW;
-  constexpr int MERGE_BYTES = 4 * 16 * D * 4;
+  constexpr int MERGE_BYTES = 4 * 16 * (D / 2) * 4;
   constexpr int TILE_BYTES = 4 * VT_WORDS * 4;
   constexpr int LDS_BYTES = MERGE_BYTES > TILE_BYTES ? MERGE_BYTES : TILE_BYTES;
   constexpr int kMaxSP = 1024;
   __shared__ __align__(16) char smem[LDS_BYTES];
   __shared__ __align__(16) _Float16 sq[16 * D];
+  __shared__ __align__(16) _Float16 sqr[16 * D];
   __shared__ int s_items[kMaxSP];
   __shared__ float s_den[4][16];
   __shared__ BlockScratch bs;
@@ -74,7 +77,7 @@ __global__ __launch_bounds__(256) void decode_apply_kernel(carekv_arena A, Decod
     if (any) s_items[n_items + pos] = p;
     n_items += tot;
   }
-  stage_q<D>(sq, a.q + ((long)b * a.Hq + kvh * GQ) * D, GQ);
+  stage_q<D>(sq, sqr, a.q + ((long)b * a.Hq + kvh * GQ) * D, GQ);
   __syncthreads();
 
   half8_t qB[G::NS];
@@ -87,17 +90,36 @@ __global__ __launch_bounds__(256) void decode_apply_kernel(carekv_arena A, Decod
   for (int t = 0; t < NT; ++t) nacc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
   float den = 0.f;
 
+  // e^x - 1 and e^x from the hardware base-2 exponential; a short series
+  // keeps e^x - 1 accurate for the small |x| of residual logit shifts.
+  auto em1 = [](float x) {
+    if (fabsf(x) < 0.03125f) return x * (1.f + x * (0.5f + x * (0.16666667f + x * 0.041666668f)));
+    return __builtin_amdgcn_exp2f(x * 1.44269504f) - 1.f;
+  };
+  // The tile rows a page leaves unwritten keep finite data from earlier
+  // pages and meet zero weights; start from zeros.
+  for (int i = lane; i < VT_WORDS; i += 64) vt[i] = 0u;
+  lds_sync_wave();
+
+  // one item ahead: codes, metadata (one field per lane) and mask bytes
+  PageRegs<D, BITS> nx;
+  int nmv = 0, p_next = 0;
+  unsigned nmk = 0;
+  auto fetch = [&](int it) {
+    p_next = __builtin_amdgcn_readfirstlane(s_items[it]);
+    load_page_regs<D, BITS, SM>(nx, rr, p_next, ln, lj);
+    nmv = meta_lanes_load<NCG>(A, pg_base + p_next, lane);
+    nmk = qv ? maskb[(long)ln * a.Pmax + p_next] : 0u;
+  };
+  if (w < n_items) fetch(w);
   for (int it = w; it < n_items; it += 4) {
-    const int p = __builtin_amdgcn_readfirstlane(s_items[it]);
-    const long pg = pg_base + p;
-    const unsigned mk = qv ? maskb[(long)ln * a.Pmax + p] : 0u;
+    const int p = p_next;
+    const PageRegs<D, BITS> cur = nx;
+    const PageMeta<NCG> cm = meta_from_lanes<NCG>(nmv, A);
+    const unsigned mk = nmk;
+    if (it + 4 < n_items) fetch(it + 4);
+    const float ckm = h2f((uint16_t)cm.kmaster), cvm = h2f((uint16_t)cm.vmaster);
     const unsigned kbits = mk & 15u, vbits = mk >> 4;
-    PageRegs<D, BITS> cur;
-    PageMeta<NCG> cm;
-    load_page_regs<D, BITS, SM>(cur, rr, p, ln, lj);
-    load_page_meta<NCG>(cm, A, pg);
-    float ckm = 0.f, cvm = 0.f;
-    if constexpr (SM == 1) { ckm = h2f(A.kmaster[pg]); cvm = h2f(A.vmaster[pg]); }
     const int nv = cm.nv;
     // ---- attention weights of the page
     const _Float16 ks = lane_scale<SM>(cur.ksc, ckm), vs = lane_scale<SM>(cur.vsc, cvm);
@@ -108,29 +130,29 @@ __global__ __launch_bounds__(256) void decode_apply_kernel(carekv_arena A, Decod
       at[i] = (4 * lj + i < nv) ? __builtin_amdgcn_exp2f(sacc[i] * a.sm_log2 - Mq) : 0.f;
     // ---- dS over the K slots this lane's query selected
     float wk[4] = {0.f, 0.f, 0.f, 0.f};
-    int rk = 0;
+    if (__any(kbits != 0u)) {
+      int rk = 0;
 #pragma unroll
-    for (int cg = 0; cg < NCG; ++cg) {
-      const int slot = cm.ksl[cg];
-      if (slot < 0) continue;
-      if (rk >= a.k_cap) break;
-      if (__any((kbits >> rk) & 1u)) {
-        const long so = (long)seq * A.n_slots + slot;
-        const float4_t racc = kslot_dot(A.k_res + so * G::KSB, sq, D, cg, ln, lj);
-        const float rs = h2f(A.k_res_scale[so]);
-        if ((kbits >> rk) & 1u) {
+      for (int cg = 0; cg < NCG; ++cg) {
+        const int slot = cm.ksl[cg];
+        if (slot < 0) continue;
+        if (rk >= a.k_cap) break;
+        if (__any((kbits >> rk) & 1u)) {
+          const long so = (long)seq * A.n_slots + slot;
+          const float4_t racc = kslot_dot(A.k_res + so * G::KSB, sqr, D, cg, ln, lj);
+          const float rs = ((kbits >> rk) & 1u) ? h2f(A.k_res_scale[so]) : 0.f;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) wk[i] += racc[i] * rs;
+          for (int i = 0; i < 4; ++i) wk[i] = fmaf(racc[i], rs, wk[i]);
         }
+        ++rk;
       }
-      ++rk;
     }
     // ---- V block of this lane's tokens (4j .. 4j+3): stored slot rank
-    int vrank = -1, vslot = -1, rv = 0;
+    int vrank = -1, rv = 0;
 #pragma unroll
     for (int vb = 0; vb < kVtb; ++vb) {
       if (cm.vsl[vb] < 0) continue;
-      if (vb == lj) { vrank = rv; vslot = cm.vsl[vb]; }
+      if (vb == lj) vrank = rv;
       ++rv;
     }
     const bool vsel = vrank >= 0 && vrank < a.v_cap && ((vbits >> vrank) & 1u);
@@ -138,9 +160,9 @@ __global__ __launch_bounds__(256) void decode_apply_kernel(carekv_arena A, Decod
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       if (exact) {
-        const float ds = wk[i] * a.inv_sqrt_d;
-        ck[i] = kbits ? at[i] * expm1f(ds) : 0.f;
-        cv[i] = vsel ? at[i] * expf(ds) : 0.f;
+        const float m1 = em1(wk[i] * a.inv_sqrt_d);
+        ck[i] = kbits ? at[i] * m1 : 0.f;
+        cv[i] = vsel ? at[i] * (1.f + m1) : 0.f;
       } else {
         ck[i] = kbits ? a.k_corr_scale * at[i] * wk[i] : 0.f;
         cv[i] = vsel ? at[i] : 0.f;
@@ -158,9 +180,11 @@ __global__ __launch_bounds__(256) void decode_apply_kernel(carekv_arena A, Decod
       pv_accumulate<D, BITS>(vt, ap, nacc, ln, lj);
       lds_sync_wave();
     }
-    // ---- num += cv R_V  (rows of unselected blocks are zero)
-    if (__any(vsel)) {
-      // row m = token of this lane's load: block m / 4, token m % 4 of the slot
+    // ---- num += cv R_V over the V blocks some query selected; the other
+    // rows keep finite data and meet zero weights
+    const unsigned vsel_any = __ballot(vsel) ? 1u : 0u;
+    if (vsel_any) {
+      // this lane loads row m = ln: block m / 4, token m % 4 of that block's slot
       const int vb_row = ln >> 2;
       int rrank = -1, rslot = -1, r2 = 0;
 #pragma unroll
@@ -169,54 +193,42 @@ __global__ __launch_bounds__(256) void decode_apply_kernel(carekv_arena A, Decod
         if (vb == vb_row) { rrank = r2; rslot = cm.vsl[vb]; }
         ++r2;
       }
-      // any query selected this row's block?
-      bool row_sel = false;
-      for (int n = 0; n < GQ; ++n)
-        row_sel |= rrank >= 0 && rrank < a.v_cap && ((maskb[(long)n * a.Pmax + p] >> (4 + rrank)) & 1u);
-      half2_t rp[CH / 2];
-      if (row_sel && 4 * vb_row < nv) {
+      // blocks selected by any query: OR of the lanes' V masks
+      unsigned vany = 0;
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        if (__any((vbits >> r) & 1u)) vany |= 1u << r;
+      if (rrank >= 0 && rrank < a.v_cap && ((vany >> rrank) & 1u)) {
         const long so = (long)seq * A.n_slots + rslot;
         const __amdgpu_buffer_rsrc_t r = make_rsrc(A.v_res + so * G::VSB, G::VSB);
         uint32_t rw[CH / 8];
         buf_load<CH / 2>(rw, r, (ln & 3) * (D / 2) + lj * (CH / 2));
+        half2_t rp[CH / 2];
         dequant_pairs<4, CH, BITS>(rw, bits2half(A.v_res_scale[so]), rp);
-      } else {
-#pragma unroll
-        for (int i = 0; i < CH / 2; ++i) rp[i] = half2_t{(_Float16)0.f, (_Float16)0.f};
+        vtile_write<D, BITS>(vt, rp, ln, lj);
       }
-      vtile_write<D, BITS>(vt, rp, ln, lj);
       half4_t ap;
       ap[0] = (_Float16)cv[0]; ap[1] = (_Float16)cv[1]; ap[2] = (_Float16)cv[2]; ap[3] = (_Float16)cv[3];
       lds_sync_wave();
       pv_accumulate<D, BITS>(vt, ap, nacc, ln, lj);
       lds_sync_wave();
     }
-    (void)vslot;
   }
 
   // ---- merge the waves and write the chunk partial
   den = col_sum(den);
-  float* so = reinterpret_cast<float*>(smem);  // [4][16][D]
-  __syncthreads();
   if (lj == 0) s_den[w][ln] = den;
-#pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    const int slot = ln * NT + t;
-    const int dim = (slot / CH) * CH + G::PB::T.slot_code[slot % CH];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) so[(w * 16 + 4 * lj + i) * D + dim] = nacc[t][i];
-  }
-  __syncthreads();
   const long cbase = ((long)bk * a.nsplit + chunk) * GQ;
-  for (int idx = threadIdx.x; idx < GQ * D; idx += 256) {
-    const int qq = idx / D, d = idx % D;
-    a.num[(cbase + qq) * D + d] = ((so[qq * D + d] + so[(16 + qq) * D + d]) + so[(32 + qq) * D + d]) +
-                                  so[(48 + qq) * D + d];
-    if (d == 0) a.den[cbase + qq] = ((s_den[0][qq] + s_den[1][qq]) + s_den[2][qq]) + s_den[3][qq];
+  sum_waves<D, BITS>(reinterpret_cast<float*>(smem), nacc, w, ln, lj, GQ, a.num + cbase * D);
+  if ((int)threadIdx.x < GQ) {
+    const int qq = threadIdx.x;
+    a.den[cbase + qq] = ((s_den[0][qq] + s_den[1][qq]) + s_den[2][qq]) + s_den[3][qq];
   }
 }
 
-// out = half(O_base + correction) from the chunk partials (fixed order).
+// out = half(O_base + correction): O_base from the split partials of the
+// streaming pass, the correction from the chunk partials of the apply pass
+// (both summed in a fixed order).
 __global__ __launch_bounds__(256) void decode_combine_kernel(int Hkv, int D, DecodeArgs a) {
   const int kvh = blockIdx.x, b = blockIdx.y;
   const int GQ = a.GQ;
@@ -224,14 +236,21 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(int Hkv, int D, Dec
   for (int idx = threadIdx.x; idx < GQ * D; idx += 256) {
     const int qq = idx / D, d = idx % D;
     const long bq = (long)bk * GQ + qq;
-    const float ob = a.ob[bq * D + d];
-    const float L = a.ml[bq * 2 + 1];
-    float nm = 0.f, dn = 0.f;
-    for (int c = 0; c < a.nsplit; ++c) {
-      const long cb = ((long)bk * a.nsplit + c) * GQ + qq;
-      nm += a.num[cb * D + d];
-      dn += a.den[cb];
+    const float M = a.ml[bq * 2], L = a.ml[bq * 2 + 1];
+    float O = 0.f, nm = 0.f, dn = 0.f;
+    if (L > 0.f) {
+      for (int s = 0; s < a.nsplit; ++s) {
+        const long base = ((long)bk * a.nsplit + s) * 16 + qq;
+        const float ms = a.pml[base * 2];
+        if (ms != -INFINITY) O += a.po[base * D + d] * __builtin_amdgcn_exp2f(ms - M);
+      }
+      for (int c = 0; c < a.nsplit; ++c) {
+        const long cb = ((long)bk * a.nsplit + c) * GQ + qq;
+        nm += a.num[cb * D + d];
+        dn += a.den[cb];
+      }
     }
+    const float ob = L > 0.f ? O / L : 0.f;
     float o = ob;
     if (L > 0.f) o = a.k_exact ? (ob + nm / L) / (1.f + dn / L) : ob + (nm - dn * ob) / L;
     a.out[((long)b * a.Hq + kvh * GQ + qq) * D + d] = f2h(o);

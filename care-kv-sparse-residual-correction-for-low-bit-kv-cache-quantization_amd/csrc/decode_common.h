@@ -17,7 +17,6 @@ struct DecodeArgs {
   float* rec;          // [B*Hkv][GQ][Pmax][F]    per-page records
   float* scores;       // [B*Hkv][GQ][ncand]      candidate scores
   uint8_t* mask;       // [B*Hkv][GQ][Pmax]       selected slots per page
-  float* ob;           // [B*Hkv][GQ][D]          O_base
   float* ml;           // [B*Hkv][GQ][2]          global max (base 2) / sum
   float* num;          // [B*Hkv][nsplit][GQ][D]  apply partial numerators
   float* den;          // [B*Hkv][nsplit][GQ]     apply partial denominators

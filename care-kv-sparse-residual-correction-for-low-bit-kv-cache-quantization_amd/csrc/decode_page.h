@@ -42,6 +42,19 @@ __device__ __forceinline__ float pair32_max(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
+// Reduce three per-lane values over the 4 lane groups j = l / 16 with three
+// lane swaps: afterwards group 0 holds sum(a), group 1 sum(b), groups 2
+// and 3 sum(c).  permlane16_swap(X, Y) exchanges the odd 16-lane rows of X
+// with the even rows of Y; permlane32_swap(X, Y) the upper half of X with
+// the lower half of Y.
+__device__ __forceinline__ float moments_reduce(float a, float b, float c) {
+  const auto ab = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  const float x = __uint_as_float(ab[0]) + __uint_as_float(ab[1]);  // even rows: a pair sum, odd rows: b
+  const float cc = pair16_sum(c);
+  const auto xc = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(cc), false, false);
+  return __uint_as_float(xc[0]) + __uint_as_float(xc[1]);  // lower half: x total, upper half: c total
+}
+
 // Sum over the four lanes m, m+16, m+32, m+48 (the token groups of a query).
 __device__ __forceinline__ float col_sum(float v) { return pair32_sum(pair16_sum(v)); }
 __device__ __forceinline__ float col_max(float v) { return pair32_max(pair16_max(v)); }
@@ -265,23 +278,44 @@ template <int NCG>
 struct PageMeta {
   int nv, meta;
   int ksl[NCG], vsl[kVtb];
+  uint32_t kmaster, vmaster;  // fp16 bits (int8 scale mode)
 };
+
+// The metadata of a page spread over the lanes of one VGPR (lane 0 valid,
+// 1 has_meta, 2.. k_slot, 6..9 v_slot, 10/11 the fp16 masters): vector
+// loads, so a prefetch of the next page stays in flight while the wave
+// waits for its own LDS traffic (scalar loads share the LDS wait counter).
+template <int NCG>
+__device__ __forceinline__ int meta_lanes_load(const carekv_arena& A, long pg, int lane) {
+  int v = 0;
+  if (lane == 0) v = A.valid[pg];
+  else if (lane == 1) v = A.has_meta[pg];
+  else if (lane < 2 + NCG) v = A.k_slot[pg * NCG + lane - 2];
+  else if (lane >= 6 && lane < 10) v = A.v_slot[pg * kVtb + lane - 6];
+  else if (lane == 10 && A.scale_mode == 1) v = A.kmaster[pg];
+  else if (lane == 11 && A.scale_mode == 1) v = A.vmaster[pg];
+  return v;
+}
 
 // Slot ids outside the arena read as "no slot".
 template <int NCG>
-__device__ __forceinline__ void load_page_meta(PageMeta<NCG>& m, const carekv_arena& A, long pg) {
-  m.nv = ((cint32_t*)A.valid)[pg];
-  m.meta = __builtin_amdgcn_readfirstlane((int)A.has_meta[pg]);
+__device__ __forceinline__ PageMeta<NCG> meta_from_lanes(int v, const carekv_arena& A) {
+  PageMeta<NCG> m;
+  m.nv = __builtin_amdgcn_readlane(v, 0);
+  m.meta = __builtin_amdgcn_readlane(v, 1);
 #pragma unroll
   for (int c = 0; c < NCG; ++c) {
-    const int s = ((cint32_t*)A.k_slot)[pg * NCG + c];
+    const int s = __builtin_amdgcn_readlane(v, 2 + c);
     m.ksl[c] = s < A.n_slots ? s : -1;
   }
 #pragma unroll
-  for (int v = 0; v < kVtb; ++v) {
-    const int s = ((cint32_t*)A.v_slot)[pg * kVtb + v];
-    m.vsl[v] = s < A.n_slots ? s : -1;
+  for (int b = 0; b < kVtb; ++b) {
+    const int s = __builtin_amdgcn_readlane(v, 6 + b);
+    m.vsl[b] = s < A.n_slots ? s : -1;
   }
+  m.kmaster = (uint32_t)__builtin_amdgcn_readlane(v, 10) & 0xffffu;
+  m.vmaster = (uint32_t)__builtin_amdgcn_readlane(v, 11) & 0xffffu;
+  return m;
 }
 
 // S[token 4j+i][query m] += K_hat . q for the page (NS MFMA 16x16x32 steps).
@@ -359,13 +393,11 @@ __device__ __forceinline__ void pv_accumulate(const uint32_t* vt, half4_t ap, fl
 
 // dS numerator of one K residual slot: racc[i] = sum_d code[token 4j+i][d] *
 // q_m[cg*32 + d] (exact codes, fp32 accumulation); the caller applies the
-// slot scale.  The slot holds 16 rows of 32 4-bit codes (16 bytes a row).
-__device__ __forceinline__ float4_t kslot_dot(const int8_t* slot_base, const _Float16* sq, int D, int cg, int ln,
-                                              int lj) {
-  using P = Pairs<4, 8, 4>;
-  const __amdgpu_buffer_rsrc_t r = make_rsrc(slot_base, kPage * 16);
-  uint32_t w[1];
-  w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, ln * 16 + lj * 4, 0, 0);
+// slot scale.  The slot holds 16 rows of 32 4-bit codes (16 bytes a row);
+// word = bytes 4j..4j+3 of row m (codes 8j..8j+7).  sqr holds q in the
+// residual pair order (stage_q).
+__device__ __forceinline__ float4_t kslot_dot_w(uint32_t word, const _Float16* sqr, int D, int cg, int ln, int lj) {
+  const uint32_t w[1] = {word};
   half8_t ar;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -373,21 +405,105 @@ __device__ __forceinline__ float4_t kslot_dot(const int8_t* slot_base, const _Fl
     ar[2 * i] = c[0];
     ar[2 * i + 1] = c[1];
   }
-  half8_t bq;
-  const _Float16* qp = sq + ln * D + cg * 32 + 8 * lj;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) bq[e] = qp[P::T.slot_code[e]];
+  const half8_t bq = *reinterpret_cast<const half8_t*>(sqr + ln * D + cg * 32 + 8 * lj);
   const float4_t z = {0.f, 0.f, 0.f, 0.f};
   return mfma16x32(ar, bq, z);
 }
 
+__device__ __forceinline__ float4_t kslot_dot(const int8_t* slot_base, const _Float16* sqr, int D, int cg, int ln,
+                                              int lj) {
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(slot_base, kPage * 16);
+  return kslot_dot_w(__builtin_amdgcn_raw_buffer_load_b32(r, ln * 16 + lj * 4, 0, 0), sqr, D, cg, ln, lj);
+}
+
 // Stage the GQ query rows of (b, kv head) in LDS as fp16 [16][D] (rows >= GQ
-// zero).  Call with all threads of the block, followed by a barrier.
+// zero), in natural order (sq) and in the pair order of the K residual
+// codes inside every 8-dim block (sqr).  Call with all threads of the
+// block, followed by a barrier.
 template <int D>
-__device__ __forceinline__ void stage_q(_Float16* sq, const uint16_t* q, int GQ) {
+__device__ __forceinline__ void stage_q(_Float16* sq, _Float16* sqr, const uint16_t* q, int GQ) {
+  using P = Pairs<4, 8, 4>;
   for (int i = threadIdx.x; i < 16 * D; i += blockDim.x) {
     const int n = i / D;
-    sq[i] = n < GQ ? bits2half(q[i]) : (_Float16)0.f;
+    const _Float16 v = n < GQ ? bits2half(q[i]) : (_Float16)0.f;
+    sq[i] = v;
+    const int blk = i & ~7, e = i & 7;
+    _Float16 vr = (_Float16)0.f;
+    if (n < GQ) vr = bits2half(q[blk + P::T.slot_code[e]]);
+    sqr[i] = vr;
+  }
+}
+
+// Merge the 4 waves' online-softmax partials (m, l, O rows = queries) into
+// one split partial: po[q][d] = sum_w O_w[q][d] 2^(m_w - M), pml[q] = (M, L).
+// O comes in the PV accumulator layout (tile t, lane (n, j): rows 4j+i,
+// column n = slot n*NT + t).  Two rounds of D/2 dims through so[4][16][D/2].
+// Call with all threads of the block.
+template <int D, int BITS>
+__device__ __forceinline__ void merge_waves(float* so, float (*s_m)[16], float (*s_l)[16], float m_run,
+                                            float l_run, const float4_t* oacc, int w, int ln, int lj, int GQ,
+                                            float* po, float* pml) {
+  using G = PageGeom<D, BITS>;
+  constexpr int NT = G::NT, CH = G::CH, DH = D / 2;
+  __syncthreads();
+  if (lj == 0) { s_m[w][ln] = m_run; s_l[w][ln] = l_run; }
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int slot = ln * NT + t;
+      const int dim = (slot / CH) * CH + G::PB::T.slot_code[slot % CH];
+      if ((dim >= DH) != (half == 1)) continue;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) so[(w * 16 + 4 * lj + i) * DH + dim - half * DH] = oacc[t][i];
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < GQ * DH; idx += blockDim.x) {
+      const int qq = idx / DH, d = idx % DH;
+      float M = -INFINITY;
+#pragma unroll
+      for (int ww = 0; ww < 4; ++ww) M = fmaxf(M, s_m[ww][qq]);
+      float L = 0.f, O = 0.f;
+      if (M != -INFINITY) {
+#pragma unroll
+        for (int ww = 0; ww < 4; ++ww) {
+          const float f = __builtin_amdgcn_exp2f(s_m[ww][qq] - M);
+          L += s_l[ww][qq] * f;
+          O += so[(ww * 16 + qq) * DH + d] * f;
+        }
+      }
+      po[qq * D + half * DH + d] = O;
+      if (half == 0 && d == 0) { pml[qq * 2] = M; pml[qq * 2 + 1] = L; }
+    }
+    __syncthreads();
+  }
+}
+
+// Sum the 4 waves' PV accumulators (rows = queries) into out[q][d] (fixed
+// wave order), two rounds of D/2 dims through so[4][16][D/2].  Call with all
+// threads of the block.
+template <int D, int BITS>
+__device__ __forceinline__ void sum_waves(float* so, const float4_t* acc, int w, int ln, int lj, int GQ, float* out) {
+  using G = PageGeom<D, BITS>;
+  constexpr int NT = G::NT, CH = G::CH, DH = D / 2;
+  __syncthreads();
+#pragma unroll
+  for (int half = 0; half < 2; ++half) {
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+      const int slot = ln * NT + t;
+      const int dim = (slot / CH) * CH + G::PB::T.slot_code[slot % CH];
+      if ((dim >= DH) != (half == 1)) continue;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) so[(w * 16 + 4 * lj + i) * DH + dim - half * DH] = acc[t][i];
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < GQ * DH; idx += blockDim.x) {
+      const int qq = idx / DH, d = idx % DH;
+      out[qq * D + half * DH + d] = ((so[qq * DH + d] + so[(16 + qq) * DH + d]) + so[(32 + qq) * DH + d]) +
+                                    so[(48 + qq) * DH + d];
+    }
+    __syncthreads();
   }
 }
 

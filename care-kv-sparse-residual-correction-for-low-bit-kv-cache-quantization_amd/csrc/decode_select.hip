@@ -1,7 +1,8 @@
 // Select pass of the CARE-KV decode: one work-group per (query head of the
 // GQA group, kv head, sequence), after the streaming kernel.
-//   * combines the split partials into the softmax statistics (M, L) and
-//     O_base of the query (attention.py:1015-1022);
+//   * combines the split partials into the softmax statistics (M, L) of the
+//     query (with correction off, also O_base, which is then the output:
+//     attention.py:1015-1022);
 //   * scores every stored slot from the page records: the query-aware K
 //     score ||dS * A(1-A)|| * ||V_page|| * sens (attention.py:167-184, 704-760)
 //     and the V score mass * v_err * sens (attention.py:780-790, with
@@ -9,9 +10,9 @@
 //   * normalises each kind by its mean score (attention.py:830-844),
 //     resolves the read budgets (residual_router.py:37-76) and selects the
 //     joint or per-kind top-k with ties toward the lowest candidate index
-//     (attention.py:856-875), by a 4-pass radix select on the float bits;
-//   * writes the per-page selection masks for the apply kernel, the
-//     optional diag list, and with correction off the output itself.
+//     (attention.py:856-875), by a radix select on the float bits;
+//   * writes the per-page selection masks for the apply kernel and the
+//     optional diag list.
 // Candidate index: K slot r of page p -> p*k_cap + r; V block r of page p
 // -> np*k_cap + p*v_cap + r (the reference's [score_K | score_V] order).
 #include <limits.h>
@@ -24,55 +25,59 @@ namespace carekv {
 
 constexpr float kEps = 1e-6f;  // residual_router.py:34
 
+template <int N>
+__device__ __forceinline__ void load_slots(int* out, const int32_t* p) {
+  if constexpr (N == 4) {
+    const int4 v = *reinterpret_cast<const int4*>(p);
+    out[0] = v.x; out[1] = v.y; out[2] = v.z; out[3] = v.w;
+  } else {
+    static_assert(N == 2, "slot row");
+    const int2 v = *reinterpret_cast<const int2*>(p);
+    out[0] = v.x; out[1] = v.y;
+  }
+}
+
 // Slot ids outside the arena read as "no slot" (as in the streaming kernel).
 __device__ __forceinline__ bool slot_ok(const carekv_arena& A, int s) { return s >= 0 && s < A.n_slots; }
 
-struct CandView {
-  const float* sc;
-  int nK, nV;
-  int norm;
-  float divK, divV, lamK, lamV;
-};
-
-// Non-negative float bits of candidate i, or -1 for an empty position.
-__device__ __forceinline__ int cand_bits(const CandView& cv, int i) {
-  float x = cv.sc[i];
-  if (!(x >= 0.f)) return -1;
-  if (cv.norm) x = i < cv.nK ? (x / cv.divK) * cv.lamK : (x / cv.divV) * cv.lamV;
-  return (int)(__float_as_uint(x) & 0x7fffffffu);
-}
-
 struct Sel {
-  uint32_t tau;  // threshold bits
+  uint32_t tau;  // threshold key
   int take;      // candidates equal to tau to take (lowest index first)
   int eq;        // candidates equal to tau
   bool on;
 };
 
-// k-th largest of the candidates [lo, hi).
-__device__ Sel radix_select(const CandView& cv, int lo, int hi, int k, int* hist, BlockScratch& bs) {
+// k-th largest key of the candidates [lo, hi) (key -1: empty position),
+// by 8-bit radix passes from the top; per-wave histograms keep the LDS
+// atomics of a wave on its own copy.
+__device__ Sel radix_select(const int* key, int lo, int hi, int k, int (*hist)[256], BlockScratch& bs) {
   Sel r{0u, INT_MAX, 0, true};
   int cnt = 0;
-  for (int i = lo + threadIdx.x; i < hi; i += kBlock) cnt += cand_bits(cv, i) >= 0;
-  const int nvalid = block_isum(cnt, bs);
+  for (int i = lo + threadIdx.x; i < hi; i += kBlock) cnt += key[i] >= 0;
+  const int nvalid = block_isum_fast(cnt, bs);
   if (nvalid <= k) return r;  // every valid candidate is taken
   uint32_t prefix = 0, mask = 0;
   int krem = k;
-  const int lane = threadIdx.x & 63;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   for (int pass = 0; pass < 4; ++pass) {
     const int shift = 24 - 8 * pass;
-    hist[threadIdx.x] = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) hist[c][threadIdx.x] = 0;
     __syncthreads();
     for (int i = lo + threadIdx.x; i < hi; i += kBlock) {
-      const int u = cand_bits(cv, i);
-      if (u >= 0 && ((uint32_t)u & mask) == prefix) atomicAdd(&hist[((uint32_t)u >> shift) & 255u], 1);
+      const int u = key[i];
+      if (u >= 0 && ((uint32_t)u & mask) == prefix) atomicAdd(&hist[w][((uint32_t)u >> shift) & 255u], 1);
     }
     __syncthreads();
     if (threadIdx.x < 64) {
       // lane l covers digits 255-4l .. 252-4l (descending)
       int c[4], loc = 0;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) { c[i] = hist[255 - 4 * lane - i]; loc += c[i]; }
+      for (int i = 0; i < 4; ++i) {
+        const int d = 255 - 4 * lane - i;
+        c[i] = ((hist[0][d] + hist[1][d]) + hist[2][d]) + hist[3][d];
+        loc += c[i];
+      }
       int incl = loc;
 #pragma unroll
       for (int o = 1; o < 64; o <<= 1) {
@@ -98,21 +103,39 @@ __device__ Sel radix_select(const CandView& cv, int lo, int hi, int k, int* hist
     prefix |= (uint32_t)bs.bc[0] << shift;
     krem = bs.bc[1];
     mask |= 255u << shift;
-    r.eq = bs.bc[2];
+    const int in_bin = bs.bc[2];
     __syncthreads();
+    if (krem == in_bin) {  // the whole bin is taken: every key >= prefix is selected
+      r.tau = prefix; r.take = INT_MAX; r.eq = 0;
+      return r;
+    }
+    r.eq = in_bin;
   }
   r.tau = prefix;
   r.take = krem;
   return r;
 }
 
+constexpr int kLdsCand = 8192;  // candidates kept in LDS (32 KB); more go to the workspace
+
+// Work-groups are dealt to the 8 XCDs round-robin by linear id; the GQ
+// query work-groups of one (sequence, kv head) share its page tables, so
+// they are mapped to one XCD (one L2): within a window of 8*GQ ids, XCD x
+// gets pair window*8 + x for queries 0..GQ-1.
+constexpr int kXcd = 8;
+
 template <int D>
 __global__ __launch_bounds__(256) void decode_select_kernel(carekv_arena A, DecodeArgs a) {
   constexpr int NCG = D / 32;
+  constexpr int FMAX = 1 + 3 * NCG + kVtb;
   __shared__ BlockScratch bs;
-  __shared__ int hist[256];
-  const int qq = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  __shared__ int hist[4][256];
+  extern __shared__ float s_cand[];  // ncand floats when they fit (size set at launch)
   const int GQ = a.GQ;
+  const int win = blockIdx.x / (kXcd * GQ), rem = blockIdx.x % (kXcd * GQ);
+  const int pair = win * kXcd + rem % kXcd, qq = rem / kXcd;
+  if (pair >= a.B * A.n_kv_heads) return;
+  const int kvh = pair % A.n_kv_heads, b = pair / A.n_kv_heads;
   const int bk = b * A.n_kv_heads + kvh;
   const int seq_raw = a.seq_slot[b], np_raw = a.n_pages[b];
   const bool row_ok = seq_raw >= 0 && seq_raw < A.n_seq && np_raw >= 0 && np_raw <= a.Pmax;
@@ -121,13 +144,12 @@ __global__ __launch_bounds__(256) void decode_select_kernel(carekv_arena A, Deco
   const long pg_base = ((long)kvh * A.n_seq + seq) * A.max_pages;
   const int tid = threadIdx.x;
   const long bq = (long)bk * GQ + qq;
-  uint16_t* outp = a.out + ((long)b * a.Hq + kvh * GQ + qq) * D;
   int32_t* diagp = a.diag ? a.diag + ((long)b * a.Hq + kvh * GQ + qq) * a.diag_cap : nullptr;
 
-  // ---- softmax statistics and O_base from the split partials
+  // ---- softmax statistics from the split partials
   float mloc = -INFINITY;
   for (int s = tid; s < a.nsplit; s += kBlock) mloc = fmaxf(mloc, a.pml[(((long)bk * a.nsplit + s) * 16 + qq) * 2]);
-  const float M = block_max(mloc, bs);
+  const float M = block_max_fast(mloc, bs);
   float lloc = 0.f;
   if (M != -INFINITY)
     for (int s = tid; s < a.nsplit; s += kBlock) {
@@ -135,49 +157,65 @@ __global__ __launch_bounds__(256) void decode_select_kernel(carekv_arena A, Deco
       const float ms = a.pml[base * 2];
       if (ms != -INFINITY) lloc += a.pml[base * 2 + 1] * __builtin_amdgcn_exp2f(ms - M);
     }
-  const float L = block_sum(lloc, bs);
-  for (int d = tid; d < D; d += kBlock) {
-    float O = 0.f;
-    if (M != -INFINITY)
-      for (int s = 0; s < a.nsplit; ++s) {
-        const long base = ((long)bk * a.nsplit + s) * 16 + qq;
-        const float ms = a.pml[base * 2];
-        if (ms != -INFINITY) O += a.po[base * D + d] * __builtin_amdgcn_exp2f(ms - M);
-      }
-    const float ob = L > 0.f ? O / L : 0.f;
-    if (a.correction) a.ob[bq * D + d] = ob;
-    else outp[d] = f2h(ob);
-  }
+  const float L = block_sum_fast(lloc, bs);
   if (tid == 0) { a.ml[bq * 2] = M; a.ml[bq * 2 + 1] = L; }
   if (!a.correction) {
+    // base attention only: O_base is the output
+    uint16_t* outp = a.out + ((long)b * a.Hq + kvh * GQ + qq) * D;
+    for (int d = tid; d < D; d += kBlock) {
+      float O = 0.f;
+      if (M != -INFINITY)
+#pragma unroll 8
+        for (int s = 0; s < a.nsplit; ++s) {
+          const long base = ((long)bk * a.nsplit + s) * 16 + qq;
+          const float ms = a.pml[base * 2];
+          if (ms != -INFINITY) O += a.po[base * D + d] * __builtin_amdgcn_exp2f(ms - M);
+        }
+      outp[d] = f2h(L > 0.f ? O / L : 0.f);
+    }
     if (diagp)
       for (int i = tid; i < a.diag_cap; i += kBlock) diagp[i] = -1;
     return;
   }
 
-  // ---- score every stored slot
-  const int k_cap = a.k_cap, v_cap = a.v_cap;
+  // ---- score every stored slot (all loads of a page issued up front)
+  const int k_cap = a.k_cap, v_cap = a.v_cap, F = a.F;
   const int nK = np * k_cap, nV = np * v_cap;
-  const float* recq = a.rec + bq * a.Pmax * a.F;
-  float* sc = a.scores + bq * a.ncand;
+  const float* recq = a.rec + bq * a.Pmax * F;
+  float* sc = a.ncand <= kLdsCand ? s_cand : a.scores + bq * a.ncand;
+  int* key = reinterpret_cast<int*>(sc);
   uint8_t* maskq = a.mask + bq * a.Pmax;
+  const float invL = L > 0.f ? 1.f / L : 0.f;
   float sumK = 0.f, sumV = 0.f;
   int cntK = 0, cntV = 0;
-  const bool have_stats = L > 0.f;
+#pragma unroll 2
   for (int p = tid; p < np; p += kBlock) {
     const long pg = pg_base + p;
     const int nv = A.valid[pg];
-    const bool ok = have_stats && nv > 0 && A.has_meta[pg];
-    const float* r = recq + (long)p * a.F;
-    const float c = ok ? __builtin_amdgcn_exp2f(r[0] - M) / L : 0.f;
-    const float vnorm = ok ? sqrtf(A.v_sq[pg]) : 0.f;
+    const int hm = A.has_meta[pg];
+    const float vsq = A.v_sq[pg];
+    int ksl[NCG], vsl[kVtb];
+    load_slots<NCG>(ksl, A.k_slot + pg * NCG);
+    load_slots<kVtb>(vsl, A.v_slot + pg * kVtb);
+    const uint2 e2 = *reinterpret_cast<const uint2*>(A.v_err + pg * kVtb);
+    const uint16_t verr[kVtb] = {(uint16_t)e2.x, (uint16_t)(e2.x >> 16), (uint16_t)e2.y, (uint16_t)(e2.y >> 16)};
+    float r[FMAX];
+    const float* rp = recq + (long)p * F;
+#pragma unroll
+    for (int f = 0; f < FMAX; ++f) r[f] = f < F ? rp[f] : 0.f;
+    const bool ok = L > 0.f && nv > 0 && hm;
+    const float c = ok ? __builtin_amdgcn_exp2f(r[0] - M) * invL : 0.f;
+    const float vnorm = __builtin_amdgcn_sqrtf(vsq);
     int rk = 0;
 #pragma unroll
     for (int cg = 0; cg < NCG; ++cg) {
-      if (!ok || !slot_ok(A, A.k_slot[pg * NCG + cg]) || rk >= k_cap) continue;
-      const float M2 = r[1 + 3 * rk], M3 = r[2 + 3 * rk], M4 = r[3 + 3 * rk];
+      if (!ok || !slot_ok(A, ksl[cg]) || rk >= k_cap) continue;
+      float M2 = 0.f, M3 = 0.f, M4 = 0.f;
+#pragma unroll
+      for (int j = 0; j < NCG; ++j)
+        if (j == rk) { M2 = r[1 + 3 * j]; M3 = r[2 + 3 * j]; M4 = r[3 + 3 * j]; }
       const float q2 = c * c * (M2 - c * (2.f * M3 - c * M4));
-      float ks = sqrtf(fmaxf(q2, 0.f)) * vnorm;
+      float ks = __builtin_amdgcn_sqrtf(fmaxf(q2, 0.f)) * vnorm;
       if (!isfinite(ks)) ks = 0.f;
       ks = ks * a.sens;
       sc[p * k_cap + rk] = ks;
@@ -189,11 +227,16 @@ __global__ __launch_bounds__(256) void decode_select_kernel(carekv_arena A, Deco
     int rv = 0;
 #pragma unroll
     for (int vb = 0; vb < kVtb; ++vb) {
-      if (!ok || !slot_ok(A, A.v_slot[pg * kVtb + vb]) || rv >= v_cap) continue;
+      if (!ok || !slot_ok(A, vsl[vb]) || rv >= v_cap) continue;
       float vsc = -1.f;
       if (vb * kVtb < nv) {
-        const float verr_s = (float)((double)h2f(A.v_err[pg * kVtb + vb]) * a.sens_d);
-        vsc = (c * r[1 + 3 * k_cap + rv]) * verr_s;
+        float E = 0.f;
+        const int fe = 1 + 3 * k_cap + rv;
+#pragma unroll
+        for (int f = 1; f < FMAX; ++f)
+          if (f == fe) E = r[f];
+        const float verr_s = (float)((double)h2f(verr[vb]) * a.sens_d);
+        vsc = (c * E) * verr_s;
         vsc = vsc * a.sens;
         sumV += vsc;
         ++cntV;
@@ -203,8 +246,9 @@ __global__ __launch_bounds__(256) void decode_select_kernel(carekv_arena A, Deco
     }
     for (; rv < v_cap; ++rv) sc[nK + p * v_cap + rv] = -1.f;
   }
-  const float tK = block_sum(sumK, bs), tV = block_sum(sumV, bs);
-  const int n_k = block_isum(cntK, bs), n_v = block_isum(cntV, bs);
+  float tK = sumK, tV = sumV;
+  int n_k = cntK, n_v = cntV;
+  block_sum4(tK, tV, n_k, n_v, bs);  // also orders the score stores before their reads
 
   // ---- read budgets (residual_router.py:37-76 via attention.py:662-670)
   const bool want_k = (a.kind == 0 || a.kind == 1) && n_k > 0;
@@ -224,89 +268,119 @@ __global__ __launch_bounds__(256) void decode_select_kernel(carekv_arena A, Deco
   const bool haveK = want_k && bud_k > 0, haveV = want_v && bud_v > 0;
   const bool do_norm = a.normalize && a.kind == 0 && haveK && haveV;
   const bool joint = a.joint && a.kind == 0 && haveK && haveV;
-  const CandView cv{sc, nK, nV, do_norm ? 1 : 0,
-                    n_k > 0 ? fmaxf(tK / (float)n_k, kEps) : kEps,
-                    n_v > 0 ? fmaxf(tV / (float)n_v, kEps) : kEps, a.lam_k, a.lam_v};
+
+  // ---- keys: non-negative float bits of the (normalised) scores, -1 empty
+  {
+    const float divK = n_k > 0 ? fmaxf(tK / (float)n_k, kEps) : kEps;
+    const float divV = n_v > 0 ? fmaxf(tV / (float)n_v, kEps) : kEps;
+    for (int i = tid; i < nK + nV; i += kBlock) {
+      float x = sc[i];
+      int u = -1;
+      if (x >= 0.f) {
+        if (do_norm) x = i < nK ? (x / divK) * a.lam_k : (x / divV) * a.lam_v;
+        u = (int)(__float_as_uint(x) & 0x7fffffffu);
+      }
+      key[i] = u;
+    }
+    __syncthreads();
+  }
 
   // ---- thresholds
   Sel sk{0u, 0, 0, false}, sv{0u, 0, 0, false};
   if (joint) {
     const int mb = min(bud_k + bud_v, n_k + n_v);
-    sk = radix_select(cv, 0, nK + nV, mb, hist, bs);
+    sk = radix_select(key, 0, nK + nV, mb, hist, bs);
     sv = sk;
   } else {
-    if (haveK) sk = radix_select(cv, 0, nK, min(bud_k, n_k), hist, bs);
-    if (haveV) sv = radix_select(cv, nK, nK + nV, min(bud_v, n_v), hist, bs);
+    if (haveK) sk = radix_select(key, 0, nK, min(bud_k, n_k), hist, bs);
+    if (haveV) sv = radix_select(key, nK, nK + nV, min(bud_v, n_v), hist, bs);
   }
 
-  // ---- masks and diag: a sweep over the K candidates, then the V ones
-  int sel_run = 0, eqK_seen = 0;
+  // ---- masks: one sweep over the pages; ties at a threshold are taken in
+  // candidate order (all K candidates precede the V ones)
+  const bool rankK = sk.on && sk.take < sk.eq, rankV = sv.on && sv.take < sv.eq;
+  int eqK_total = 0;
+  if (joint && rankK) {  // V ties of a joint selection rank after every K tie
+    int c = 0;
+    for (int i = tid; i < nK; i += kBlock) c += key[i] >= 0 && (uint32_t)key[i] == sk.tau;
+    eqK_total = block_isum_fast(c, bs);
+  }
+  int eq_runK = 0, eq_runV = joint ? eqK_total : 0;
+  for (int p0 = 0; p0 < np; p0 += kBlock) {
+    const int p = p0 + tid;
+    const bool pv = p < np;
+    int uk[4] = {-1, -1, -1, -1}, uv[4] = {-1, -1, -1, -1};
+    int eqk = 0, eqv = 0;
+    if (pv) {
+      if (sk.on)
+        for (int r = 0; r < k_cap; ++r) {
+          uk[r] = key[p * k_cap + r];
+          eqk += uk[r] >= 0 && (uint32_t)uk[r] == sk.tau;
+        }
+      if (sv.on)
+        for (int r = 0; r < v_cap; ++r) {
+          uv[r] = key[nK + p * v_cap + r];
+          eqv += uv[r] >= 0 && (uint32_t)uv[r] == sv.tau;
+        }
+    }
+    int ek = 0, ev = 0;
+    if (rankK) { int tot; ek = block_excl_scan(eqk, bs, &tot) + eq_runK; eq_runK += tot; }
+    if (rankV) { int tot; ev = block_excl_scan(eqv, bs, &tot) + eq_runV; eq_runV += tot; }
+    unsigned bits = 0;
+    for (int r = 0; r < k_cap; ++r) {
+      if (uk[r] < 0) continue;
+      const uint32_t x = (uint32_t)uk[r];
+      bool take = x > sk.tau;
+      if (x == sk.tau) { take = ek < sk.take; ++ek; }
+      if (take) bits |= 1u << r;
+    }
+    for (int r = 0; r < v_cap; ++r) {
+      if (uv[r] < 0) continue;
+      const uint32_t x = (uint32_t)uv[r];
+      bool take = x > sv.tau;
+      if (x == sv.tau) { take = ev < sv.take; ++ev; }
+      if (take) bits |= 1u << (4 + r);
+    }
+    if (pv) maskq[p] = (uint8_t)bits;
+  }
+  if (!diagp) return;
+  // ---- diag: selected candidates in ascending candidate order (each
+  // thread reads back the mask bytes it wrote)
+  int sel_run = 0;
   for (int kind = 0; kind < 2; ++kind) {
-    const Sel& s = kind == 0 ? sk : sv;
-    const int cap = kind == 0 ? k_cap : v_cap;
-    const int seg0 = kind == 0 ? 0 : nK;
-    const bool need_rank = s.on && s.take < s.eq;
-    int eq_run = (kind == 1 && joint) ? eqK_seen : 0;
     for (int p0 = 0; p0 < np; p0 += kBlock) {
       const int p = p0 + tid;
-      const bool pv = p < np;
-      int u[4] = {-1, -1, -1, -1};
-      int eqc = 0;
-      if (pv && s.on)
-        for (int r = 0; r < cap; ++r) {
-          u[r] = cand_bits(cv, seg0 + p * cap + r);
-          eqc += u[r] >= 0 && (uint32_t)u[r] == s.tau;
+      const unsigned bits = p < np ? (kind == 0 ? (maskq[p] & 15u) : (maskq[p] >> 4)) : 0u;
+      int tot;
+      int pos = block_excl_scan(__popc(bits), bs, &tot) + sel_run;
+      sel_run += tot;
+      if (!bits) continue;
+      const long pg = pg_base + p;
+      const int cap = kind == 0 ? k_cap : v_cap;
+      const int nsub = kind == 0 ? NCG : kVtb;
+      int rr = 0;
+      for (int sub = 0; sub < nsub && rr < cap; ++sub) {
+        const int slot = kind == 0 ? A.k_slot[pg * NCG + sub] : A.v_slot[pg * kVtb + sub];
+        if (!slot_ok(A, slot)) continue;
+        if ((bits >> rr) & 1u) {
+          if (pos < a.diag_cap) diagp[pos] = (kind << 30) | (p << 3) | sub;
+          ++pos;
         }
-      int eq_before = 0;
-      if (need_rank) {
-        int tot;
-        eq_before = block_excl_scan(eqc, bs, &tot) + eq_run;
-        eq_run += tot;
-      }
-      unsigned bits = 0;
-      for (int r = 0; r < cap; ++r) {
-        if (u[r] < 0) continue;
-        const uint32_t x = (uint32_t)u[r];
-        bool take = x > s.tau;
-        if (x == s.tau) { take = eq_before < s.take; ++eq_before; }
-        if (take) bits |= 1u << r;
-      }
-      if (pv) {
-        if (kind == 0) maskq[p] = (uint8_t)bits;
-        else maskq[p] = (uint8_t)(maskq[p] | (bits << 4));
-      }
-      if (diagp) {
-        int tot;
-        int pos = block_excl_scan(__popc(bits), bs, &tot) + sel_run;
-        sel_run += tot;
-        if (bits) {
-          const long pg = pg_base + p;
-          int rr = 0;
-          const int nsub = kind == 0 ? NCG : kVtb;
-          for (int sub = 0; sub < nsub && rr < cap; ++sub) {
-            const int slot = kind == 0 ? A.k_slot[pg * NCG + sub] : A.v_slot[pg * kVtb + sub];
-            if (!slot_ok(A, slot)) continue;
-            if ((bits >> rr) & 1u) {
-              if (pos < a.diag_cap) diagp[pos] = (kind << 30) | (p << 3) | sub;
-              ++pos;
-            }
-            ++rr;
-          }
-        }
+        ++rr;
       }
     }
-    if (kind == 0) eqK_seen = eq_run;  // K ties rank before the V ones of a joint selection
   }
-  if (diagp)
-    for (int i = sel_run + tid; i < a.diag_cap; i += kBlock) diagp[i] = -1;
+  for (int i = sel_run + tid; i < a.diag_cap; i += kBlock) diagp[i] = -1;
 }
 
 int launch_decode_select(const carekv_arena& A, const DecodeArgs& a, hipStream_t s) {
-  const dim3 grid(a.GQ, A.n_kv_heads, a.B);
+  const int pairs = a.B * A.n_kv_heads;
+  const dim3 grid(((pairs + kXcd - 1) / kXcd) * kXcd * a.GQ);
+  const size_t lds = (a.correction && a.ncand <= kLdsCand) ? (size_t)a.ncand * sizeof(float) : 0;
   if (A.head_dim == 64) {
-    hipLaunchKernelGGL(decode_select_kernel<64>, grid, dim3(kBlock), 0, s, A, a);
+    hipLaunchKernelGGL(decode_select_kernel<64>, grid, dim3(kBlock), lds, s, A, a);
   } else if (A.head_dim == 128) {
-    hipLaunchKernelGGL(decode_select_kernel<128>, grid, dim3(kBlock), 0, s, A, a);
+    hipLaunchKernelGGL(decode_select_kernel<128>, grid, dim3(kBlock), lds, s, A, a);
   } else {
     set_error("unsupported head_dim %d", A.head_dim);
     return CAREKV_EINVAL;

@@ -23,15 +23,18 @@
 namespace carekv {
 
 template <int D, int BITS, int SM>
-__global__ __launch_bounds__(256) void decode_stream_kernel(carekv_arena A, DecodeArgs a) {
+// 4 waves per SIMD: the register budget is capped at 128 VGPRs.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8)))
+void decode_stream_kernel(carekv_arena A, DecodeArgs a) {
   using G = PageGeom<D, BITS>;
   constexpr int NT = G::NT, NCG = G::NCG, CH = G::CH;
   constexpr int VT_WORDS = kPage * G::VROW;          // one wave's V tile
-  constexpr int MERGE_BYTES = 4 * 16 * D * 4;        // [4 waves][16 queries][D] fp32
+  constexpr int MERGE_BYTES = 4 * 16 * (D / 2) * 4;  // [4 waves][16 queries][D/2] fp32, two rounds
   constexpr int TILE_BYTES = 4 * VT_WORDS * 4;
   constexpr int LDS_BYTES = MERGE_BYTES > TILE_BYTES ? MERGE_BYTES : TILE_BYTES;
   __shared__ __align__(16) char smem[LDS_BYTES];
   __shared__ __align__(16) _Float16 sq[16 * D];
+  __shared__ __align__(16) _Float16 sqr[16 * D];
   __shared__ float s_m[4][16], s_l[4][16];
 
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
@@ -49,7 +52,7 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(carekv_arena A, Deco
   const float sm_log2 = a.sm_log2;
   const long rq = (long)a.Pmax * a.F;  // record stride between query heads
 
-  stage_q<D>(sq, a.q + ((long)b * a.Hq + kvh * GQ) * D, GQ);
+  stage_q<D>(sq, sqr, a.q + ((long)b * a.Hq + kvh * GQ) * D, GQ);
   __syncthreads();
   half8_t qB[G::NS];
   load_q_operand<D, BITS>(qB, sq, ln, lj);
@@ -63,25 +66,35 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(carekv_arena A, Deco
   const int p_begin = split * a.SP, p_end = min(p_begin + a.SP, np);
 
   PageRegs<D, BITS> nx;
-  PageMeta<NCG> nm;
-  float nkm = 0.f, nvm = 0.f;
+  int nmv = 0;  // next page's metadata, one field per lane
   int p = p_begin + w;
   if (p < p_end) {
     load_page_regs<D, BITS, SM>(nx, rr, p, ln, lj);
-    load_page_meta<NCG>(nm, A, pg_base + p);
-    if constexpr (SM == 1) { nkm = h2f(A.kmaster[pg_base + p]); nvm = h2f(A.vmaster[pg_base + p]); }
+    nmv = meta_lanes_load<NCG>(A, pg_base + p, lane);
   }
   for (; p < p_end; p += 4) {
     const PageRegs<D, BITS> cur = nx;
-    const PageMeta<NCG> cm = nm;
-    const float ckm = nkm, cvm = nvm;
+    const PageMeta<NCG> cm = meta_from_lanes<NCG>(nmv, A);
     if (p + 4 < p_end) {
       load_page_regs<D, BITS, SM>(nx, rr, p + 4, ln, lj);
-      load_page_meta<NCG>(nm, A, pg_base + p + 4);
-      if constexpr (SM == 1) { nkm = h2f(A.kmaster[pg_base + p + 4]); nvm = h2f(A.vmaster[pg_base + p + 4]); }
+      nmv = meta_lanes_load<NCG>(A, pg_base + p + 4, lane);
     }
+    const float ckm = h2f((uint16_t)cm.kmaster), cvm = h2f((uint16_t)cm.vmaster);
     const int nv = cm.nv;
     if (nv <= 0) continue;
+    // K residual rows of the stored slots, issued before the page math
+    uint32_t krow[NCG];
+    if (corr && cm.meta) {
+#pragma unroll
+      for (int cg = 0; cg < NCG; ++cg) {
+        krow[cg] = 0u;
+        if (cm.ksl[cg] >= 0) {
+          const long so = (long)seq * A.n_slots + cm.ksl[cg];
+          const __amdgpu_buffer_rsrc_t r = make_rsrc(A.k_res + so * G::KSB, G::KSB);
+          krow[cg] = __builtin_amdgcn_raw_buffer_load_b32(r, ln * 16 + lj * 4, 0, 0);
+        }
+      }
+    }
     // ---- S = K_hat q
     const _Float16 ks = lane_scale<SM>(cur.ksc, ckm), vs = lane_scale<SM>(cur.vsc, cvm);
     const float4_t sacc = page_scores<D, BITS>(cur.kw, ks, qB);
@@ -134,21 +147,24 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(carekv_arena A, Deco
         if (slot < 0) continue;
         if (rk >= a.k_cap) { if (lane == 0) *a.err_flag = 1; break; }
         const long so = (long)seq * A.n_slots + slot;
-        const float4_t racc = kslot_dot(A.k_res + so * G::KSB, sq, D, cg, ln, lj);
-        const float f = h2f(A.k_res_scale[so]) * a.inv_sqrt_d;
+        const float4_t racc = kslot_dot_w(krow[cg], sqr, D, cg, ln, lj);
+        // moments of u = racc * e (dS = racc * f scales them by f^2):
+        // M2 = sum u^2, M3 = sum u^2 e, M4 = sum (u e)^2
         float M2 = 0.f, M3 = 0.f, M4 = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float y = (racc[i] * f) * e[i];
-          const float xx = y * y;
-          const float xe = xx * e[i];
-          M2 += xx;
-          M3 += xe;
-          M4 = fmaf(xe, e[i], M4);
+          const float u = racc[i] * e[i];
+          const float ue = u * e[i];
+          M2 = fmaf(u, u, M2);
+          M3 = fmaf(ue, u, M3);
+          M4 = fmaf(ue, ue, M4);
         }
-        M2 = col_sum(M2); M3 = col_sum(M3); M4 = col_sum(M4);
-        if (lj == 0 && ln < GQ) {
-          rec[1 + 3 * rk] = M2; rec[2 + 3 * rk] = M3; rec[3 + 3 * rk] = M4;
+        // reduce over the 4 token groups j: group 0 ends with M2, 1 with
+        // M3, 2 and 3 with M4
+        const float mj = moments_reduce(M2, M3, M4);
+        if (lj < 3 && ln < GQ) {
+          const float f = h2f(A.k_res_scale[so]) * a.inv_sqrt_d;
+          rec[1 + 3 * rk + lj] = mj * (f * f);
         }
         ++rk;
       }
@@ -167,37 +183,12 @@ __global__ __launch_bounds__(256) void decode_stream_kernel(carekv_arena A, Deco
     lds_sync_wave();
   }
 
-  // ---- merge the 4 waves' (m, l, O) and write the split partial; V slot
-  // n*NT + t maps back to dim chunk*CH + slot_code[slot % CH].
-  float* so = reinterpret_cast<float*>(smem);  // [4][16][D]
-  __syncthreads();
-  if (lj == 0) { s_m[w][ln] = m_run; s_l[w][ln] = l_run; }
-#pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    const int slot = ln * NT + t;
-    const int dim = (slot / CH) * CH + G::PB::T.slot_code[slot % CH];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) so[(w * 16 + 4 * lj + i) * D + dim] = oacc[t][i];
-  }
-  __syncthreads();
-  const long pbase = ((long)bk * a.nsplit + split) * 16;
-  for (int idx = threadIdx.x; idx < GQ * D; idx += 256) {
-    const int qq = idx / D, d = idx % D;
-    float M = -INFINITY;
-#pragma unroll
-    for (int ww = 0; ww < 4; ++ww) M = fmaxf(M, s_m[ww][qq]);
-    float L = 0.f, O = 0.f;
-    if (M != -INFINITY) {
-#pragma unroll
-      for (int ww = 0; ww < 4; ++ww) {
-        const float f = __builtin_amdgcn_exp2f(s_m[ww][qq] - M);
-        L += s_l[ww][qq] * f;
-        O += so[(ww * 16 + qq) * D + d] * f;
-      }
-    }
-    a.po[(pbase + qq) * D + d] = O;
-    if (d == 0) { a.pml[(pbase + qq) * 2] = M; a.pml[(pbase + qq) * 2 + 1] = L; }
-  }
+  // ---- merge the 4 waves' (m, l, O) and write the split partial, half
+  // of the dims per round; V slot n*NT + t maps back to dim
+  // chunk*CH + slot_code[slot % CH].
+  merge_waves<D, BITS>(reinterpret_cast<float*>(smem), s_m, s_l, m_run, l_run, oacc, w, ln, lj, GQ,
+                       a.po + ((long)bk * a.nsplit + split) * 16 * D,
+                       a.pml + ((long)bk * a.nsplit + split) * 16 * 2);
 }
 
 int launch_decode_stream(const carekv_arena& A, const DecodeArgs& a, hipStream_t s) {

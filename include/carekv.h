@@ -140,6 +140,12 @@ typedef struct carekv_decode_params {
   double ratio_k, ratio_v;
   int32_t k_cap, v_cap;    /* max stored K / V slots per page                   */
   int32_t split_pages;     /* pages per work-group in the streaming pass        */
+  void* phase_events;      /* optional timing hook: NULL, or a host array of 5
+                            * hipEvent_t made by the caller, recorded on
+                            * `stream` before the streaming kernel and after the
+                            * streaming, select, apply and combine kernels (no
+                            * reference counterpart; with correction off the
+                            * last two are recorded right after select)       */
 } carekv_decode_params;
 
 /* q, out: fp16 [batch][n_heads][head_dim].  diag (optional, NULL to skip):
