@@ -24,6 +24,4 @@ reference root):
                    batched joint correction (comb+ex selector).  Pinned by
                    goldens, an fp64 brute force of the exact
                    renormalisation, and the READ=0 / kind=v invariants.
-* ``prefill``   -- ``layer.py:935-972`` causal attention over dequantised
-                   tiles.  Pinned by an fp64 textbook softmax attention.
 """
