@@ -29,11 +29,11 @@ KIND_CODE = {"both": 0, "k": 1, "v": 2}
 
 def default_split_pages(max_pages: int, rows: int) -> int:
     """Pages per work-group: enough work-groups to fill 256 CUs several times
-    over, and a multiple of the 4 waves of a work-group."""
+    over, and a multiple of 16 (4 waves x 4-page windows)."""
     target = int(os.environ.get("CAREKV_DECODE_TARGET_WGS", "4096"))
     sp = math.ceil(max(1, max_pages) * max(1, rows) / target)
-    sp = max(4, min(256, sp))
-    return (sp + 3) // 4 * 4
+    sp = max(16, min(256, sp))
+    return (sp + 15) // 16 * 16
 
 
 def decode_attention(cache: CAREKVCache, layer: int, q: torch.Tensor, seqs: Optional[Sequence[int]] = None, *,

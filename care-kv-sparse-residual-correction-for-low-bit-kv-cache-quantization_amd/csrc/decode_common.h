@@ -41,6 +41,7 @@ struct DecodeArgs {
 // stored K slot of the page is selected, bit 4 + r = the r-th stored V block.
 
 int launch_decode_stream(const carekv_arena& A, const DecodeArgs& a, hipStream_t s);
+int launch_decode_stream4(const carekv_arena& A, const DecodeArgs& a, hipStream_t s);  // GQ <= 4, SP % 16 == 0
 int launch_decode_select(const carekv_arena& A, const DecodeArgs& a, hipStream_t s);
 int launch_decode_apply(const carekv_arena& A, const DecodeArgs& a, hipStream_t s);
 int launch_decode_combine(const carekv_arena& A, const DecodeArgs& a, hipStream_t s);

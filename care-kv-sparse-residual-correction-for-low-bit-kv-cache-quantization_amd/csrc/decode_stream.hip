@@ -192,6 +192,7 @@ void decode_stream_kernel(carekv_arena A, DecodeArgs a) {
 }
 
 int launch_decode_stream(const carekv_arena& A, const DecodeArgs& a, hipStream_t s) {
+  if (a.GQ <= 4 && a.SP % 16 == 0) return launch_decode_stream4(A, a, s);  // 4-page windows, 4x4x4 MFMA
   dim3 grid(a.nsplit, A.n_kv_heads, a.B);
   return dispatch_dbs(A.head_dim, A.base_bits, A.scale_mode, [&](auto d, auto bb, auto sm) {
     hipLaunchKernelGGL((decode_stream_kernel<decltype(d)::value, decltype(bb)::value, decltype(sm)::value>), grid,

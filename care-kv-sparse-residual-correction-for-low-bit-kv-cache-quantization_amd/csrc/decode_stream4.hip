@@ -1,0 +1,377 @@
+// Streaming pass of the CARE-KV decode for GQA groups of at most 4 query
+// heads (same inputs and outputs as decode_stream.hip): one work-group per
+// (split of pages, kv head, sequence), 4 waves, a window of 4 consecutive
+// pages (64 tokens) per wave iteration.
+//
+// K side, one token row per lane (lane l = token l % 16 of page l / 16):
+//   * the lane dequantises its whole K row exactly, half(code * scale)
+//     (quantizer.py:67-82, cache.py:713-718), two codes at a time;
+//   * S = K_hat q on v_mfma_f32_4x4x4_16b_f16, 16 blocks: block b = tokens
+//     4b..4b+3 (rows), column c = query head c; lane 4b + c receives
+//     S[4b..4b+3][c], so every lane holds logits of a real (token, query)
+//     pair and the softmax and K-slot moments run without padding columns;
+//   * online softmax over the window on base-2 logits in fp32;
+//   * for every stored K slot of the window's pages, dS = q_cg . R_K on the
+//     same MFMA layout and the moments sum dS^2 e^k (k = 2, 3, 4).
+// V side, per page (lane l: token l % 16, dims [(l/16) D/4, ...)):
+//   V_hat through the padded LDS tile, O += P V_hat on MFMA 16x16x16 with P
+//   moved from the S layout by ds_bpermute.
+// The page records and split partials are those of decode_stream.hip, with
+// m_ref the running max at the window.
+#include "decode_page.h"
+#include "host_util.h"
+
+namespace carekv {
+
+__device__ __forceinline__ float4_t mfma4x4(half4_t a, half4_t b, float4_t c) {
+  return __builtin_amdgcn_mfma_f32_4x4x4f16(a, b, c, 0, 0, 0);
+}
+
+// v from lane (i + N) % 16 of the same 16-lane row (DPP row rotate)
+template <int N>
+__device__ __forceinline__ float row_ror(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 + N, 0xf, 0xf, false));
+}
+// Sum / max over the lanes {i, i+4, i+8, i+12} of each 16-lane row.
+__device__ __forceinline__ float row4_sum(float v) {
+  v += row_ror<4>(v);
+  return v + row_ror<8>(v);
+}
+__device__ __forceinline__ float row4_max(float v) {
+  v = fmaxf(v, row_ror<4>(v));
+  return fmaxf(v, row_ror<8>(v));
+}
+
+__device__ __forceinline__ uint32_t pack_h2(float x, float y) {
+  const half2_t h = {(_Float16)x, (_Float16)y};
+  return h2bits(h);
+}
+
+// Buffer load of a packed row of N bytes (N a multiple of 8) at byte offset off.
+template <int N>
+__device__ __forceinline__ void buf_load_row(uint32_t* w, __amdgpu_buffer_rsrc_t r, uint32_t off) {
+  if constexpr (N % 16 == 0) {
+#pragma unroll
+    for (int i = 0; i < N / 16; ++i) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off + 16 * i, 0, 0);
+      w[4 * i] = v[0]; w[4 * i + 1] = v[1]; w[4 * i + 2] = v[2]; w[4 * i + 3] = v[3];
+    }
+  } else {
+    static_assert(N % 8 == 0, "row bytes");
+#pragma unroll
+    for (int i = 0; i < N / 8; ++i) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, off + 8 * i, 0, 0);
+      w[2 * i] = v[0]; w[2 * i + 1] = v[1];
+    }
+  }
+}
+
+// Metadata of page pg in lane field f (see meta_lanes_load); 0 for pages
+// outside the split.
+template <int NCG>
+__device__ __forceinline__ int meta_field_load(const carekv_arena& A, long pg, bool page_ok, int f) {
+  int v = 0;
+  if (!page_ok) return 0;
+  if (f == 0) v = A.valid[pg];
+  else if (f == 1) v = A.has_meta[pg];
+  else if (f < 2 + NCG) v = A.k_slot[pg * NCG + f - 2];
+  else if (f >= 6 && f < 10) v = A.v_slot[pg * kVtb + f - 6];
+  else if (f == 10 && A.scale_mode == 1) v = A.kmaster[pg];
+  else if (f == 11 && A.scale_mode == 1) v = A.vmaster[pg];
+  return v;
+}
+
+// One window's share of a lane: the K side (prefetched a window ahead)
+// and the V side (loaded at the top of the window's iteration; the S and
+// softmax work covers its latency).
+template <int D, int BITS, int SM>
+struct WinK {
+  static constexpr int RB = row_bytes(D, BITS), NWR = RB / 4, NCG = D / 32;
+  static constexpr int KSW = SM == 1 ? (NCG + 3) / 4 : (2 * NCG + 3) / 4;  // K scale words of a row
+  uint32_t kw[NWR];
+  uint32_t ksc[KSW];
+  int meta;  // field (lane % 16) of page (lane / 16)
+};
+template <int D, int BITS, int SM>
+struct WinV {
+  static constexpr int NWC = PageGeom<D, BITS>::NWC;
+  static constexpr int VSW = SM == 1 ? 1 : 2;  // V scale words (4 pages)
+  uint32_t vw[4][NWC];
+  uint32_t vsc[VSW];
+};
+
+template <int D, int BITS, int SM>
+__global__ __launch_bounds__(256) void decode_stream4_kernel(carekv_arena A, DecodeArgs a) {
+  using G = PageGeom<D, BITS>;
+  using WK = WinK<D, BITS, SM>;
+  using WV = WinV<D, BITS, SM>;
+  using PF = Pairs<BITS, D, BITS>;  // pair schedule of a whole row
+  using PR = Pairs<4, 32, 4>;       // pair schedule of a K residual row
+  constexpr int NCG = G::NCG, CH = G::CH, RB = G::RB, CHB = G::CHB;
+  constexpr int NS4 = D / 4;        // 4x4x4 steps over the head dim
+  constexpr int VT_WORDS = kPage * G::VROW;
+  constexpr int MERGE_BYTES = 4 * 16 * (D / 2) * 4;
+  constexpr int TILE_BYTES = 4 * VT_WORDS * 4;
+  constexpr int LDS_BYTES = MERGE_BYTES > TILE_BYTES ? MERGE_BYTES : TILE_BYTES;
+  __shared__ __align__(16) char smem[LDS_BYTES];
+  __shared__ __align__(16) _Float16 sq4[NS4 * 16];       // [step][query][4]: q in the row pair order
+  __shared__ __align__(16) _Float16 sqr4[NCG * 8 * 16];  // [cg][step][query][4]: q in the residual order
+  __shared__ float s_m[4][16], s_l[4][16];
+
+  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int GQ = a.GQ;
+  const int bk = b * A.n_kv_heads + kvh;
+  const int seq_raw = a.seq_slot[b], np_raw = a.n_pages[b];
+  const bool row_ok = seq_raw >= 0 && seq_raw < A.n_seq && np_raw >= 0 && np_raw <= a.Pmax;
+  const int seq = row_ok ? seq_raw : 0, np = row_ok ? np_raw : 0;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ln = lane & 15, lj = lane >> 4;  // V side: token ln, chunk lj; K side: token ln of page lj
+  const int sc = lane & 3, sbk = ln >> 2;    // S layout: query sc, tokens 4*sbk.. of page lj
+  const long pg_base = ((long)kvh * A.n_seq + seq) * A.max_pages;
+  const RowRes rr = row_resources<D, BITS, SM>(A, pg_base);
+  const bool corr = a.correction != 0;
+  const float sm_log2 = a.sm_log2;
+  const long rq = (long)a.Pmax * a.F;  // record stride between query heads
+  float* rec_q = a.rec + ((long)bk * GQ + sc) * rq;  // this lane's query (valid when sc < GQ)
+
+  {  // q in the MFMA orders
+    const uint16_t* qg = a.q + ((long)b * a.Hq + kvh * GQ) * D;
+    for (int i = threadIdx.x; i < NS4 * 16; i += 256) {
+      const int s = i >> 4, c = (i >> 2) & 3, e = i & 3;
+      sq4[i] = c < GQ ? bits2half(qg[c * D + PF::T.slot_code[4 * s + e]]) : (_Float16)0.f;
+    }
+    for (int i = threadIdx.x; i < NCG * 128; i += 256) {
+      const int cg = i >> 7, s = (i >> 4) & 7, c = (i >> 2) & 3, e = i & 3;
+      sqr4[i] = c < GQ ? bits2half(qg[c * D + cg * 32 + PR::T.slot_code[4 * s + e]]) : (_Float16)0.f;
+    }
+  }
+  __syncthreads();
+
+  uint32_t* vt = reinterpret_cast<uint32_t*>(smem) + w * VT_WORDS;
+  float m_run = -INFINITY, l_run = 0.f;
+  float4_t oacc[G::NT];
+#pragma unroll
+  for (int t = 0; t < G::NT; ++t) oacc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int p_begin = split * a.SP, p_end = min(p_begin + a.SP, np);
+  WK nx;
+  auto load_wink = [&](int q0) {
+    const int pk = q0 + lj;  // this lane's page on the K side
+    const uint32_t krow = (uint32_t)(pk * kPage + ln);
+    buf_load_row<RB>(nx.kw, rr.kc, krow * RB);
+    if constexpr (SM == 1) {
+      if constexpr (NCG == 4) nx.ksc[0] = __builtin_amdgcn_raw_buffer_load_b32(rr.ks, krow * NCG, 0, 0);
+      else nx.ksc[0] = __builtin_amdgcn_raw_buffer_load_b16(rr.ks, krow * NCG, 0, 0);
+    } else {
+      if constexpr (NCG == 4) {
+        const auto v = __builtin_amdgcn_raw_buffer_load_b64(rr.ks, krow * NCG * 2, 0, 0);
+        nx.ksc[0] = v[0]; nx.ksc[1] = v[1];
+      } else {
+        nx.ksc[0] = __builtin_amdgcn_raw_buffer_load_b32(rr.ks, krow * NCG * 2, 0, 0);
+      }
+    }
+    nx.meta = meta_field_load<NCG>(A, pg_base + pk, pk < p_end, ln);
+  };
+  auto load_winv = [&](WV& v, int q0) {
+    const int gi = (lj * CH) / 32;
+#pragma unroll
+    for (int pi = 0; pi < 4; ++pi) {
+      const uint32_t vrow = (uint32_t)((q0 + pi) * kPage + ln);
+      buf_load<CHB>(v.vw[pi], rr.vc, vrow * RB + lj * CHB);
+    }
+    if constexpr (SM == 1) {
+      uint32_t sv = 0;
+#pragma unroll
+      for (int pi = 0; pi < 4; ++pi)
+        sv |= (__builtin_amdgcn_raw_buffer_load_b8(rr.vs, (uint32_t)((q0 + pi) * kPage + ln) * NCG + gi, 0, 0) &
+               0xffu) << (8 * pi);
+      v.vsc[0] = sv;
+    } else {
+      uint32_t s0 = 0, s1 = 0;
+#pragma unroll
+      for (int pi = 0; pi < 4; ++pi) {
+        const uint32_t h =
+            __builtin_amdgcn_raw_buffer_load_b16(rr.vs, ((uint32_t)((q0 + pi) * kPage + ln) * NCG + gi) * 2, 0, 0) &
+            0xffffu;
+        if (pi < 2) s0 |= h << (16 * pi);
+        else s1 |= h << (16 * (pi - 2));
+      }
+      v.vsc[0] = s0; v.vsc[1] = s1;
+    }
+  };
+
+  int p0 = p_begin + 4 * w;
+  if (p0 < p_end) load_wink(p0);
+  for (; p0 < p_end; p0 += 16) {
+    const WK cur = nx;
+    WV cv;
+    load_winv(cv, p0);
+    if (p0 + 16 < p_end) load_wink(p0 + 16);
+    int nvp[4];
+#pragma unroll
+    for (int pi = 0; pi < 4; ++pi) nvp[pi] = __builtin_amdgcn_readlane(cur.meta, 16 * pi);
+    if (nvp[0] <= 0 && nvp[1] <= 0 && nvp[2] <= 0 && nvp[3] <= 0) continue;
+    const int my_nv = __shfl(cur.meta, lane & 48, 64);        // valid tokens of this lane's page
+    const int my_meta = __shfl(cur.meta, (lane & 48) + 1, 64);
+
+    // ---- S = K_hat q on 4x4x4 blocks
+    _Float16 ksg[NCG];
+    {
+      const float km = SM == 1 ? h2f((uint16_t)__shfl(cur.meta, (lane & 48) + 10, 64)) : 0.f;
+#pragma unroll
+      for (int g = 0; g < NCG; ++g) {
+        if constexpr (SM == 1) ksg[g] = (_Float16)((float)(int8_t)(cur.ksc[0] >> (8 * g)) * km);
+        else ksg[g] = bits2half((uint16_t)(cur.ksc[g >> 1] >> (16 * (g & 1))));
+      }
+    }
+    float4_t sa0 = {0.f, 0.f, 0.f, 0.f}, sa1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < NS4; ++s) {
+      const int g = PF::T.a[2 * s] / 32;
+      const half2_t ss = {ksg[g], ksg[g]};
+      const half2_t c0 = code_pair<BITS, D, BITS>(cur.kw, 2 * s) * ss;
+      const half2_t c1 = code_pair<BITS, D, BITS>(cur.kw, 2 * s + 1) * ss;
+      const half4_t ak = {c0[0], c0[1], c1[0], c1[1]};
+      const half4_t bq = *reinterpret_cast<const half4_t*>(sq4 + (s * 4 + sc) * 4);
+      if (s & 1) sa1 = mfma4x4(ak, bq, sa1);
+      else sa0 = mfma4x4(ak, bq, sa0);
+    }
+    // ---- online softmax over the window (lane: tokens 4*sbk+i of page lj, query sc)
+    float x[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = (4 * sbk + i < my_nv) ? (sa0[i] + sa1[i]) * sm_log2 : -INFINITY;
+    const float mx = pair32_max(pair16_max(row4_max(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])))));
+    const float m_new = fmaxf(m_run, mx);  // finite: some page of the window has a valid token
+    const float f_old = __builtin_amdgcn_exp2f(m_run - m_new);
+    m_run = m_new;
+    float e[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) e[i] = __builtin_amdgcn_exp2f(x[i] - m_new);
+    l_run = l_run * f_old + pair32_sum(pair16_sum(row4_sum((e[0] + e[1]) + (e[2] + e[3]))));
+    if (__builtin_expect(__any(f_old != 1.f), 0)) {
+      // rows of oacc are queries 4j+i; query i's factor lives in lane i
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float fi = __shfl(f_old, i, 64);
+#pragma unroll
+        for (int t = 0; t < G::NT; ++t) oacc[t][i] *= fi;
+      }
+    }
+    const uint32_t e01 = pack_h2(e[0], e[1]), e23 = pack_h2(e[2], e[3]);
+
+    // ---- O += P V_hat, page by page
+#pragma unroll
+    for (int pi = 0; pi < 4; ++pi) {
+      if (nvp[pi] <= 0) continue;
+      float vm = 0.f;
+      if constexpr (SM == 1) vm = h2f((uint16_t)__builtin_amdgcn_readlane(cur.meta, 16 * pi + 11));
+      _Float16 vs;
+      if constexpr (SM == 1) vs = (_Float16)((float)(int8_t)(cv.vsc[0] >> (8 * pi)) * vm);
+      else vs = bits2half((uint16_t)(cv.vsc[pi >> 1] >> (16 * (pi & 1))));
+      half2_t vp[CH / 2];
+      dequant_pairs<BITS, CH, BITS>(cv.vw[pi], vs, vp);
+      vtile_write<D, BITS>(vt, vp, ln, lj);
+      // P in the A layout: lane (n, j) <- S lane 16*pi + 4*j + n (queries n < 4)
+      const int src = (16 * pi + 4 * lj + (ln & 3)) * 4;
+      uint32_t p01 = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)e01);
+      uint32_t p23 = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)e23);
+      if (ln >= 4) { p01 = 0u; p23 = 0u; }
+      half4_t ap;
+      __builtin_memcpy(&ap, &p01, 4);
+      __builtin_memcpy(reinterpret_cast<char*>(&ap) + 4, &p23, 4);
+      lds_sync_wave();
+      pv_accumulate<D, BITS>(vt, ap, oacc, ln, lj);
+      lds_sync_wave();
+    }
+
+    if (!corr) continue;
+    // ---- page records: m_ref, K-slot moments, V-block masses (this lane:
+    // page lj, query sc; the lanes with sbk == 0 write)
+    const int my_page = p0 + lj;
+    const bool rec_lane = sc < GQ && my_meta != 0 && my_nv > 0;
+    float* rec = rec_q + (long)my_page * a.F;
+    if (rec_lane && sbk == 0) rec[0] = m_new;
+    int kslot[NCG];
+#pragma unroll
+    for (int cg = 0; cg < NCG; ++cg) {
+      const int s = __shfl(cur.meta, (lane & 48) + 2 + cg, 64);
+      kslot[cg] = (my_meta != 0 && s >= 0 && s < A.n_slots) ? s : -1;
+    }
+    int nks = 0;
+#pragma unroll
+    for (int cg = 0; cg < NCG; ++cg) nks += kslot[cg] >= 0;
+    if (nks > a.k_cap && sbk == 0 && sc == 0) *a.err_flag = 1;
+    for (int r = 0; r < a.k_cap; ++r) {
+      int cgr = -1, slotr = -1, cnt = 0;
+#pragma unroll
+      for (int cg = 0; cg < NCG; ++cg) {
+        if (kslot[cg] < 0) continue;
+        if (cnt == r) { cgr = cg; slotr = kslot[cg]; }
+        ++cnt;
+      }
+      const bool has = cgr >= 0;
+      if (!__any(has)) break;
+      uint32_t rw[4] = {0u, 0u, 0u, 0u};
+      if (has) {
+        const uint4 v = *reinterpret_cast<const uint4*>(A.k_res + ((long)seq * A.n_slots + slotr) * G::KSB + ln * 16);
+        rw[0] = v.x; rw[1] = v.y; rw[2] = v.z; rw[3] = v.w;
+      }
+      const int cgq = has ? cgr : 0;
+      float4_t racc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const half2_t c0 = code_pair<4, 32, 4>(rw, 2 * s);
+        const half2_t c1 = code_pair<4, 32, 4>(rw, 2 * s + 1);
+        const half4_t ar = {c0[0], c0[1], c1[0], c1[1]};
+        const half4_t bq = *reinterpret_cast<const half4_t*>(sqr4 + ((cgq * 8 + s) * 4 + sc) * 4);
+        racc = mfma4x4(ar, bq, racc);
+      }
+      // moments of u = racc * e (dS = racc * f scales them by f^2)
+      float M2 = 0.f, M3 = 0.f, M4 = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float u = racc[i] * e[i];
+        const float ue = u * e[i];
+        M2 = fmaf(u, u, M2);
+        M3 = fmaf(ue, u, M3);
+        M4 = fmaf(ue, ue, M4);
+      }
+      M2 = row4_sum(M2); M3 = row4_sum(M3); M4 = row4_sum(M4);
+      if (has && rec_lane && sbk == 0) {
+        const float f = h2f(A.k_res_scale[(long)seq * A.n_slots + slotr]) * a.inv_sqrt_d;
+        const float f2 = f * f;
+        rec[1 + 3 * r] = M2 * f2; rec[2 + 3 * r] = M3 * f2; rec[3 + 3 * r] = M4 * f2;
+      }
+    }
+    // V block sbk of page lj: its stored-slot rank and mass
+    int vrank = -1, rv = 0;
+#pragma unroll
+    for (int vb = 0; vb < kVtb; ++vb) {
+      const int s = __shfl(cur.meta, (lane & 48) + 6 + vb, 64);
+      if (s < 0 || s >= A.n_slots) continue;
+      if (vb == sbk) vrank = rv;
+      ++rv;
+    }
+    if (rec_lane && vrank >= 0) {
+      if (vrank < a.v_cap) rec[1 + 3 * a.k_cap + vrank] = (e[0] + e[1]) + (e[2] + e[3]);
+      else *a.err_flag = 1;
+    }
+  }
+
+  merge_waves<D, BITS>(reinterpret_cast<float*>(smem), s_m, s_l, m_run, l_run, oacc, w, ln, lj, GQ,
+                       a.po + ((long)bk * a.nsplit + split) * 16 * D,
+                       a.pml + ((long)bk * a.nsplit + split) * 16 * 2);
+}
+
+int launch_decode_stream4(const carekv_arena& A, const DecodeArgs& a, hipStream_t s) {
+  dim3 grid(a.nsplit, A.n_kv_heads, a.B);
+  return dispatch_dbs(A.head_dim, A.base_bits, A.scale_mode, [&](auto d, auto bb, auto sm) {
+    hipLaunchKernelGGL((decode_stream4_kernel<decltype(d)::value, decltype(bb)::value, decltype(sm)::value>), grid,
+                       dim3(256), 0, s, A, a);
+    CAREKV_CHECK_LAUNCH("decode_stream4");
+    return CAREKV_OK;
+  });
+}
+
+}  // namespace carekv
