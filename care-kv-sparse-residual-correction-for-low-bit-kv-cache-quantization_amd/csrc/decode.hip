@@ -7,7 +7,7 @@ using namespace carekv;
 
 namespace {
 struct WsLayout {
-  long err, pml, po, rec, scores, mask, ml, num, den, total;
+  long err, pml, po, rec, ebuf, scores, mask, ml, num, den, total;
   int nsplit, F, ncand;
 };
 
@@ -26,6 +26,7 @@ WsLayout ws_layout(const carekv_arena& A, const carekv_decode_params& dp) {
   L.pml = off; off += al(BH * L.nsplit * 16 * 2 * 4);
   L.po = off; off += al(BH * L.nsplit * 16 * (long)D * 4);
   L.rec = off; off += al(BH * GQ * (long)Pm * L.F * 4);
+  L.ebuf = off; off += al(BH * GQ * (long)Pm * 16 * 2);
   L.scores = off; off += al(BH * GQ * (long)L.ncand * 4);
   L.mask = off; off += al(BH * GQ * (long)Pm);
   L.ml = off; off += al(BH * GQ * 2 * 4);
@@ -73,6 +74,7 @@ extern "C" int carekv_decode_attn(const carekv_arena* arena, const carekv_decode
   a.pml = (float*)(ws + L.pml);
   a.po = (float*)(ws + L.po);
   a.rec = (float*)(ws + L.rec);
+  a.ebuf = (uint16_t*)(ws + L.ebuf);
   a.scores = (float*)(ws + L.scores);
   a.mask = (uint8_t*)(ws + L.mask);
   a.ml = (float*)(ws + L.ml);

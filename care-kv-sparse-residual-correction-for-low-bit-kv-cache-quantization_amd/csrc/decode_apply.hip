@@ -3,7 +3,8 @@
 // any query of the GQA group selected a slot of is processed once for all
 // the group's queries, a wave per page, with the per-query masks:
 //
-//   a_t   = 2^(x_t - M)                    (unnormalised attention weight)
+//   a_t   = e_t 2^(m_ref - M)              (unnormalised attention weight, e_t
+//                                            stored by the streaming pass)
 //   dS_t  = sum over selected K slots of q_cg . R_K[t] (raw, residual scale)
 //   exact mode (attention.py:96-118 in closed form; with sum_t A_t = 1):
 //     num += sum_t a_t (e^{dS_t/sqrt(D)} - 1) V_hat_t
@@ -31,13 +32,33 @@ constexpr bool same_slot_order() {
   return true;
 }
 
-template <int D, int BITS, int SM>
+// One page of the apply pass as loaded ahead of its use.
+template <int D, int BITS>
+struct ApplyItem {
+  static constexpr int NWC = PageGeom<D, BITS>::NWC, NCG = D / 32, CH = D / 4;
+  int p;               // page (wave-uniform)
+  int meta;            // page metadata, one field per lane
+  unsigned mk;         // selection mask byte of this lane's query (ln)
+  unsigned kany, vany; // slots selected by any query of the group (wave-uniform)
+  uint32_t e01, e23;   // e of tokens 4j..4j+3 for query ln, fp16 pairs
+  float mref;          // m_ref of query ln at the page
+  uint32_t vw[NWC];    // V codes of token ln, chunk lj (when a K slot is selected)
+  uint32_t vsc;        // its scale code
+  uint32_t kr[NCG];    // K residual word of each stored slot (cg order) that is selected
+  float krs[NCG];      // and its scale
+  uint32_t rv[CH / 8]; // V residual chunk of tile row ln (when its block is selected)
+  float rvs;           // and its scale
+  bool rsel;           // tile row ln holds a selected V block
+};
+
 // 4 waves per SIMD: the register budget is capped at 128 VGPRs.
+template <int D, int BITS, int SM>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8)))
 void decode_apply_kernel(carekv_arena A, DecodeArgs a) {
   using G = PageGeom<D, BITS>;
+  using Item = ApplyItem<D, BITS>;
   static_assert(same_slot_order<D, BITS>(), "V residual tile must use the V_hat slot order");
-  constexpr int NT = G::NT, NCG = G::NCG, CH = G::CH;
+  constexpr int NT = G::NT, NCG = G::NCG, CH = G::CH, CHB = G::CHB, RB = G::RB;
   constexpr int VT_WORDS = kPage * G::VROW;
   constexpr int MERGE_BYTES = 4 * 16 * (D / 2) * 4;
   constexpr int TILE_BYTES = 4 * VT_WORDS * 4;
@@ -63,6 +84,8 @@ void decode_apply_kernel(carekv_arena A, DecodeArgs a) {
   const RowRes rr = row_resources<D, BITS, SM>(A, pg_base);
   const uint8_t* maskb = a.mask + (long)bk * GQ * a.Pmax;
   const bool exact = a.k_exact != 0;
+  const bool qv = ln < GQ;
+  const long qrow = (long)bk * GQ + (qv ? ln : 0);  // this lane's query row of the workspace
 
   // ---- pages of the chunk with any selected slot
   const int p_begin = chunk * a.SP, p_end = min(p_begin + a.SP, np);
@@ -80,10 +103,7 @@ void decode_apply_kernel(carekv_arena A, DecodeArgs a) {
   stage_q<D>(sq, sqr, a.q + ((long)b * a.Hq + kvh * GQ) * D, GQ);
   __syncthreads();
 
-  half8_t qB[G::NS];
-  load_q_operand<D, BITS>(qB, sq, ln, lj);
-  const bool qv = ln < GQ;
-  const float Mq = qv ? a.ml[((long)bk * GQ + ln) * 2] : 0.f;
+  const float Mq = qv ? a.ml[qrow * 2] : 0.f;
   uint32_t* vt = reinterpret_cast<uint32_t*>(smem) + w * VT_WORDS;
   float4_t nacc[NT];
 #pragma unroll
@@ -101,46 +121,109 @@ void decode_apply_kernel(carekv_arena A, DecodeArgs a) {
   for (int i = lane; i < VT_WORDS; i += 64) vt[i] = 0u;
   lds_sync_wave();
 
-  // one item ahead: codes, metadata (one field per lane) and mask bytes
-  PageRegs<D, BITS> nx;
-  int nmv = 0, p_next = 0;
-  unsigned nmk = 0;
-  auto fetch = [&](int it) {
-    p_next = __builtin_amdgcn_readfirstlane(s_items[it]);
-    load_page_regs<D, BITS, SM>(nx, rr, p_next, ln, lj);
-    nmv = meta_lanes_load<NCG>(A, pg_base + p_next, lane);
-    nmk = qv ? maskb[(long)ln * a.Pmax + p_next] : 0u;
+  // Two-stage prefetch: the metadata and masks of item it + 8, and the data
+  // of item it + 4 (issued with that item's metadata already at hand).
+  struct MStage { int p, meta; unsigned mk; };
+  auto load_m = [&](int it) {
+    MStage m;
+    m.p = __builtin_amdgcn_readfirstlane(s_items[it]);
+    m.meta = meta_lanes_load<NCG>(A, pg_base + m.p, lane);
+    m.mk = qv ? maskb[(long)ln * a.Pmax + m.p] : 0u;
+    return m;
   };
-  if (w < n_items) fetch(w);
-  for (int it = w; it < n_items; it += 4) {
-    const int p = p_next;
-    const PageRegs<D, BITS> cur = nx;
-    const PageMeta<NCG> cm = meta_from_lanes<NCG>(nmv, A);
-    const unsigned mk = nmk;
-    if (it + 4 < n_items) fetch(it + 4);
-    const float ckm = h2f((uint16_t)cm.kmaster), cvm = h2f((uint16_t)cm.vmaster);
-    const unsigned kbits = mk & 15u, vbits = mk >> 4;
-    const int nv = cm.nv;
-    // ---- attention weights of the page
-    const _Float16 ks = lane_scale<SM>(cur.ksc, ckm), vs = lane_scale<SM>(cur.vsc, cvm);
-    const float4_t sacc = page_scores<D, BITS>(cur.kw, ks, qB);
-    float at[4];
+  auto load_d = [&](const MStage& m, Item& d) {
+    d.p = m.p; d.meta = m.meta; d.mk = m.mk;
+    const PageMeta<NCG> pm = meta_from_lanes<NCG>(m.meta, A);
+    const unsigned kb = m.mk & 15u, vb = m.mk >> 4;
+    d.kany = 0; d.vany = 0;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      at[i] = (4 * lj + i < nv) ? __builtin_amdgcn_exp2f(sacc[i] * a.sm_log2 - Mq) : 0.f;
-    // ---- dS over the K slots this lane's query selected
-    float wk[4] = {0.f, 0.f, 0.f, 0.f};
-    if (__any(kbits != 0u)) {
+    for (int r = 0; r < 4; ++r) {
+      if (__any((kb >> r) & 1u)) d.kany |= 1u << r;
+      if (__any((vb >> r) & 1u)) d.vany |= 1u << r;
+    }
+    d.e01 = 0u; d.e23 = 0u; d.mref = 0.f;
+    if (qv) {
+      const uint2 e = *reinterpret_cast<const uint2*>(a.ebuf + (qrow * a.Pmax + m.p) * 16 + 4 * lj);
+      d.e01 = e.x; d.e23 = e.y;
+      d.mref = a.rec[(qrow * a.Pmax + m.p) * a.F];
+    }
+    if (d.kany) {
+      const uint32_t vrow = (uint32_t)(m.p * kPage + ln);
+      buf_load<CHB>(d.vw, rr.vc, vrow * RB + lj * CHB);
+      const int gi = (lj * CH) / 32;
+      if constexpr (SM == 1) d.vsc = __builtin_amdgcn_raw_buffer_load_b8(rr.vs, vrow * NCG + gi, 0, 0);
+      else d.vsc = __builtin_amdgcn_raw_buffer_load_b16(rr.vs, (vrow * NCG + gi) * 2, 0, 0);
       int rk = 0;
 #pragma unroll
       for (int cg = 0; cg < NCG; ++cg) {
-        const int slot = cm.ksl[cg];
-        if (slot < 0) continue;
+        d.kr[cg] = 0u; d.krs[cg] = 0.f;
+        if (pm.ksl[cg] < 0) continue;
+        if (rk < a.k_cap && ((d.kany >> rk) & 1u)) {
+          const long so = (long)seq * A.n_slots + pm.ksl[cg];
+          const __amdgpu_buffer_rsrc_t r = make_rsrc(A.k_res + so * G::KSB, G::KSB);
+          d.kr[cg] = __builtin_amdgcn_raw_buffer_load_b32(r, ln * 16 + lj * 4, 0, 0);
+          d.krs[cg] = h2f(A.k_res_scale[so]);
+        }
+        ++rk;
+      }
+    }
+    d.rsel = false;
+    if (d.vany) {
+      // tile row ln: block ln / 4, token ln % 4 of that block's slot
+      const int vb_row = ln >> 2;
+      int rrank = -1, rslot = -1, r2 = 0;
+#pragma unroll
+      for (int v = 0; v < kVtb; ++v) {
+        if (pm.vsl[v] < 0) continue;
+        if (v == vb_row) { rrank = r2; rslot = pm.vsl[v]; }
+        ++r2;
+      }
+      d.rsel = rrank >= 0 && rrank < a.v_cap && ((d.vany >> rrank) & 1u) && 4 * vb_row < pm.nv;
+      if (d.rsel) {
+        const long so = (long)seq * A.n_slots + rslot;
+        const __amdgpu_buffer_rsrc_t r = make_rsrc(A.v_res + so * G::VSB, G::VSB);
+        buf_load<CH / 2>(d.rv, r, (ln & 3) * (D / 2) + lj * (CH / 2));
+        d.rvs = h2f(A.v_res_scale[so]);
+      }
+    }
+  };
+
+  MStage mB{}, mC{};
+  Item cur, nxt;
+  if (w < n_items) {
+    const MStage m0 = load_m(w);
+    if (w + 4 < n_items) mB = load_m(w + 4);
+    load_d(m0, nxt);
+  }
+  for (int it = w; it < n_items; it += 4) {
+    cur = nxt;
+    if (it + 8 < n_items) mC = load_m(it + 8);
+    if (it + 4 < n_items) load_d(mB, nxt);
+    mB = mC;
+
+    const PageMeta<NCG> cm = meta_from_lanes<NCG>(cur.meta, A);
+    const unsigned kbits = cur.mk & 15u, vbits = cur.mk >> 4;
+    // ---- attention weights of the page: a_t = e_t 2^(m_ref - M)
+    float at[4];
+    {
+      const float f = qv ? __builtin_amdgcn_exp2f(cur.mref - Mq) : 0.f;
+      half2_t e01, e23;
+      __builtin_memcpy(&e01, &cur.e01, 4);
+      __builtin_memcpy(&e23, &cur.e23, 4);
+      at[0] = (float)e01[0] * f; at[1] = (float)e01[1] * f;
+      at[2] = (float)e23[0] * f; at[3] = (float)e23[1] * f;
+    }
+    // ---- dS over the K slots this lane's query selected
+    float wk[4] = {0.f, 0.f, 0.f, 0.f};
+    if (cur.kany) {
+      int rk = 0;
+#pragma unroll
+      for (int cg = 0; cg < NCG; ++cg) {
+        if (cm.ksl[cg] < 0) continue;
         if (rk >= a.k_cap) break;
-        if (__any((kbits >> rk) & 1u)) {
-          const long so = (long)seq * A.n_slots + slot;
-          const float4_t racc = kslot_dot(A.k_res + so * G::KSB, sqr, D, cg, ln, lj);
-          const float rs = ((kbits >> rk) & 1u) ? h2f(A.k_res_scale[so]) : 0.f;
+        if ((cur.kany >> rk) & 1u) {
+          const float4_t racc = kslot_dot_w(cur.kr[cg], sqr, D, cg, ln, lj);
+          const float rs = ((kbits >> rk) & 1u) ? cur.krs[cg] : 0.f;
 #pragma unroll
           for (int i = 0; i < 4; ++i) wk[i] = fmaf(racc[i], rs, wk[i]);
         }
@@ -170,7 +253,10 @@ void decode_apply_kernel(carekv_arena A, DecodeArgs a) {
     }
     den += (ck[0] + ck[1]) + (ck[2] + ck[3]);
     // ---- num += ck V_hat
-    if (__any(kbits != 0u)) {
+    if (cur.kany) {
+      float vm = 0.f;
+      if constexpr (SM == 1) vm = h2f((uint16_t)cm.vmaster);
+      const _Float16 vs = lane_scale<SM>(SM == 1 ? (int)(int8_t)cur.vsc : (int)cur.vsc, vm);
       half2_t vp[CH / 2];
       dequant_pairs<BITS, CH, BITS>(cur.vw, vs, vp);
       vtile_write<D, BITS>(vt, vp, ln, lj);
@@ -182,29 +268,10 @@ void decode_apply_kernel(carekv_arena A, DecodeArgs a) {
     }
     // ---- num += cv R_V over the V blocks some query selected; the other
     // rows keep finite data and meet zero weights
-    const unsigned vsel_any = __ballot(vsel) ? 1u : 0u;
-    if (vsel_any) {
-      // this lane loads row m = ln: block m / 4, token m % 4 of that block's slot
-      const int vb_row = ln >> 2;
-      int rrank = -1, rslot = -1, r2 = 0;
-#pragma unroll
-      for (int vb = 0; vb < kVtb; ++vb) {
-        if (cm.vsl[vb] < 0) continue;
-        if (vb == vb_row) { rrank = r2; rslot = cm.vsl[vb]; }
-        ++r2;
-      }
-      // blocks selected by any query: OR of the lanes' V masks
-      unsigned vany = 0;
-#pragma unroll
-      for (int r = 0; r < 4; ++r)
-        if (__any((vbits >> r) & 1u)) vany |= 1u << r;
-      if (rrank >= 0 && rrank < a.v_cap && ((vany >> rrank) & 1u)) {
-        const long so = (long)seq * A.n_slots + rslot;
-        const __amdgpu_buffer_rsrc_t r = make_rsrc(A.v_res + so * G::VSB, G::VSB);
-        uint32_t rw[CH / 8];
-        buf_load<CH / 2>(rw, r, (ln & 3) * (D / 2) + lj * (CH / 2));
+    if (cur.vany) {
+      if (cur.rsel) {
         half2_t rp[CH / 2];
-        dequant_pairs<4, CH, BITS>(rw, bits2half(A.v_res_scale[so]), rp);
+        dequant_pairs<4, CH, BITS>(cur.rv, (_Float16)cur.rvs, rp);
         vtile_write<D, BITS>(vt, rp, ln, lj);
       }
       half4_t ap;
@@ -262,6 +329,7 @@ int launch_decode_apply(const carekv_arena& A, const DecodeArgs& a, hipStream_t 
     set_error("split_pages must be at most 1024");
     return CAREKV_EINVAL;
   }
+  if (a.GQ <= 4) return launch_decode_apply4(A, a, s);  // windows of 4 pages, 4x4x4 layout
   const dim3 grid(a.nsplit, A.n_kv_heads, a.B);
   return dispatch_dbs(A.head_dim, A.base_bits, A.scale_mode, [&](auto d, auto bb, auto sm) {
     hipLaunchKernelGGL((decode_apply_kernel<decltype(d)::value, decltype(bb)::value, decltype(sm)::value>), grid,

@@ -1,0 +1,345 @@
+// Apply pass for GQA groups of at most 4 query heads (same inputs and
+// outputs as decode_apply.hip): one work-group per (page chunk, kv head,
+// sequence); each wave takes windows of 4 selected pages.
+//
+// Per window, in the layout of the 4x4x4 streaming pass (lane l: page
+// l / 16 of the window, tokens 4*((l%16)/4) .. +3, query head l % 4):
+//   * a_t = e_t 2^(m_ref - M) from the weights the streaming pass stored;
+//   * dS_t = sum over the K slots the lane's query selected of
+//     q_cg . R_K[t] * scale, on v_mfma_f32_4x4x4_16b_f16 (one residual row
+//     per lane);
+//   * the exact (attention.py:96-118) or linear (attention.py:938-943)
+//     weights of V_hat and of the selected V residual rows.
+// Then O-sized partials on MFMA 16x16x16 through the LDS tile:
+//   * num += ck V_hat for each page of the window with a selected K slot;
+//   * num += cv R_V for the selected V blocks of the window, 4 blocks per
+//     tile, dequantised by all 64 lanes.
+// den accumulates the K weights; decode_combine_kernel finishes.
+#include "block_util.h"
+#include "decode_page.h"
+#include "host_util.h"
+
+namespace carekv {
+
+template <int D, int BITS, int SM>
+__global__ __launch_bounds__(256) void decode_apply4_kernel(carekv_arena A, DecodeArgs a) {
+  using G = PageGeom<D, BITS>;
+  using PR = Pairs<4, 32, 4>;  // pair schedule of a K residual row
+  constexpr int NT = G::NT, NCG = G::NCG, CH = G::CH, CHB = G::CHB, RB = G::RB;
+  constexpr int VT_WORDS = kPage * G::VROW;
+  constexpr int MERGE_BYTES = 4 * 16 * (D / 2) * 4;
+  constexpr int TILE_BYTES = 4 * VT_WORDS * 4;
+  constexpr int LDS_BYTES = MERGE_BYTES > TILE_BYTES ? MERGE_BYTES : TILE_BYTES;
+  constexpr int kMaxSP = 1024;
+  __shared__ __align__(16) char smem[LDS_BYTES];
+  __shared__ __align__(16) _Float16 sqr4[NCG * 8 * 16];  // [cg][step][query][4]: q in the residual order
+  __shared__ int s_items[kMaxSP];
+  __shared__ float s_den[4][4];
+  __shared__ BlockScratch bs;
+
+  const int chunk = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  const int GQ = a.GQ;
+  const int bk = b * A.n_kv_heads + kvh;
+  const int seq_raw = a.seq_slot[b], np_raw = a.n_pages[b];
+  const bool row_ok = seq_raw >= 0 && seq_raw < A.n_seq && np_raw >= 0 && np_raw <= a.Pmax;
+  const int seq = row_ok ? seq_raw : 0, np = row_ok ? np_raw : 0;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ln = lane & 15, lj = lane >> 4;  // V side: token/row ln, chunk lj; S side: page lj of the window
+  const int sc = lane & 3, sbk = ln >> 2;    // S side: query sc, tokens 4*sbk.. (V block sbk)
+  const long pg_base = ((long)kvh * A.n_seq + seq) * A.max_pages;
+  const RowRes rr = row_resources<D, BITS, SM>(A, pg_base);
+  const uint8_t* maskb = a.mask + (long)bk * GQ * a.Pmax;
+  const bool exact = a.k_exact != 0;
+  const bool qv = sc < GQ;
+  const long qrow = (long)bk * GQ + (qv ? sc : 0);  // this lane's query row of the workspace
+
+  // ---- pages of the chunk with any selected slot
+  const int p_begin = chunk * a.SP, p_end = min(p_begin + a.SP, np);
+  int n_items = 0;
+  for (int p0 = p_begin; p0 < p_end; p0 += kBlock) {
+    const int p = p0 + threadIdx.x;
+    unsigned any = 0;
+    if (p < p_end)
+      for (int n = 0; n < GQ; ++n) any |= maskb[(long)n * a.Pmax + p];
+    int tot;
+    const int pos = block_excl_scan(any ? 1 : 0, bs, &tot);
+    if (any) s_items[n_items + pos] = p;
+    n_items += tot;
+  }
+  {  // q in the residual MFMA order
+    const uint16_t* qg = a.q + ((long)b * a.Hq + kvh * GQ) * D;
+    for (int i = threadIdx.x; i < NCG * 128; i += 256) {
+      const int cg = i >> 7, s = (i >> 4) & 7, c = (i >> 2) & 3, e = i & 3;
+      sqr4[i] = c < GQ ? bits2half(qg[c * D + cg * 32 + PR::T.slot_code[4 * s + e]]) : (_Float16)0.f;
+    }
+  }
+  __syncthreads();
+
+  const float Mq = qv ? a.ml[qrow * 2] : 0.f;
+  uint32_t* vt = reinterpret_cast<uint32_t*>(smem) + w * VT_WORDS;
+  float4_t nacc[NT];
+#pragma unroll
+  for (int t = 0; t < NT; ++t) nacc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+  float den = 0.f;
+  // Tile rows a pass leaves unwritten keep finite data and meet zero weights.
+  for (int i = lane; i < VT_WORDS; i += 64) vt[i] = 0u;
+  lds_sync_wave();
+
+  auto em1 = [](float x) {  // e^x - 1, a short series for the small |x| of residual logit shifts
+    if (fabsf(x) < 0.03125f) return x * (1.f + x * (0.5f + x * (0.16666667f + x * 0.041666668f)));
+    return __builtin_amdgcn_exp2f(x * 1.44269504f) - 1.f;
+  };
+
+  // one window ahead: page metadata (lane 16*pi + field), the lane's mask
+  // byte, stored weights and m_ref
+  struct WinPre { int meta; unsigned mk; uint32_t e01, e23; float mref; int page; };
+  auto load_pre = [&](int base) {
+    WinPre x;
+    const int it = base + lj;
+    x.page = it < n_items ? s_items[it] : -1;  // this lane's page (S side)
+    const bool ok = x.page >= 0;
+    x.meta = meta_field_load<NCG>(A, pg_base + (ok ? x.page : 0), ok, ln);
+    x.mk = (ok && qv) ? maskb[(long)sc * a.Pmax + x.page] : 0u;
+    x.e01 = 0u; x.e23 = 0u; x.mref = 0.f;
+    if (ok && qv) {
+      const uint2 e = *reinterpret_cast<const uint2*>(a.ebuf + (qrow * a.Pmax + x.page) * 16 + 4 * sbk);
+      x.e01 = e.x; x.e23 = e.y;
+      x.mref = a.rec[(qrow * a.Pmax + x.page) * a.F];
+    }
+    return x;
+  };
+
+  WinPre nx{};
+  int base = 4 * w;
+  if (base < n_items) nx = load_pre(base);
+  for (; base < n_items; base += 16) {
+    const WinPre cur = nx;
+    if (base + 16 < n_items) nx = load_pre(base + 16);
+    int pgi[4];
+#pragma unroll
+    for (int pi = 0; pi < 4; ++pi) pgi[pi] = __builtin_amdgcn_readlane(cur.page, 16 * pi);
+    // slots selected by any query, per page (bit r of kany[pi] / vany[pi])
+    const unsigned kbits = cur.mk & 15u, vbits = cur.mk >> 4;
+    unsigned kany[4] = {0u, 0u, 0u, 0u}, vany[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const unsigned long long kb = __ballot((kbits >> r) & 1u), vb = __ballot((vbits >> r) & 1u);
+#pragma unroll
+      for (int pi = 0; pi < 4; ++pi) {
+        if ((kb >> (16 * pi)) & 0xffffull) kany[pi] |= 1u << r;
+        if ((vb >> (16 * pi)) & 0xffffull) vany[pi] |= 1u << r;
+      }
+    }
+    // this lane's page fields (S side and K-residual side share page lj)
+    const int my_nv = __shfl(cur.meta, lane & 48, 64);
+    int kslot[NCG], vslot[kVtb];
+#pragma unroll
+    for (int cg = 0; cg < NCG; ++cg) {
+      const int s = __shfl(cur.meta, (lane & 48) + 2 + cg, 64);
+      kslot[cg] = (s >= 0 && s < A.n_slots) ? s : -1;
+    }
+#pragma unroll
+    for (int v = 0; v < kVtb; ++v) {
+      const int s = __shfl(cur.meta, (lane & 48) + 6 + v, 64);
+      vslot[v] = (s >= 0 && s < A.n_slots) ? s : -1;
+    }
+    const unsigned kany_all = kany[0] | kany[1] | kany[2] | kany[3];
+
+    // ---- V codes and scales of the pages with a selected K slot (V side:
+    // token ln, chunk lj)
+    uint32_t vw[4][G::NWC];
+    uint32_t vsc[4];
+    const int gi = (lj * CH) / 32;
+#pragma unroll
+    for (int pi = 0; pi < 4; ++pi) {
+      if (!kany[pi]) continue;
+      const uint32_t vrow = (uint32_t)(pgi[pi] * kPage + ln);
+      buf_load<CHB>(vw[pi], rr.vc, vrow * RB + lj * CHB);
+      if constexpr (SM == 1) vsc[pi] = __builtin_amdgcn_raw_buffer_load_b8(rr.vs, vrow * NCG + gi, 0, 0);
+      else vsc[pi] = __builtin_amdgcn_raw_buffer_load_b16(rr.vs, (vrow * NCG + gi) * 2, 0, 0);
+    }
+
+    // ---- attention weights a_t = e_t 2^(m_ref - M)
+    float at[4];
+    {
+      const float f = qv ? __builtin_amdgcn_exp2f(cur.mref - Mq) : 0.f;
+      half2_t e01, e23;
+      __builtin_memcpy(&e01, &cur.e01, 4);
+      __builtin_memcpy(&e23, &cur.e23, 4);
+      at[0] = (float)e01[0] * f; at[1] = (float)e01[1] * f;
+      at[2] = (float)e23[0] * f; at[3] = (float)e23[1] * f;
+    }
+    // ---- dS over the selected K slots (rank r: r-th stored slot of the page)
+    float wk[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int r = 0; r < a.k_cap && r < NCG; ++r) {
+      if (!((kany_all >> r) & 1u)) continue;
+      int cgr = -1, slotr = -1, cnt = 0;
+#pragma unroll
+      for (int cg = 0; cg < NCG; ++cg) {
+        if (kslot[cg] < 0) continue;
+        if (cnt == r) { cgr = cg; slotr = kslot[cg]; }
+        ++cnt;
+      }
+      // rows are needed for pages where some query selected rank r
+      const unsigned pk = (kany[0] >> r & 1u) | ((kany[1] >> r & 1u) << 1) | ((kany[2] >> r & 1u) << 2) |
+                          ((kany[3] >> r & 1u) << 3);
+      const bool need = cgr >= 0 && ((pk >> lj) & 1u);
+      uint32_t rw[4] = {0u, 0u, 0u, 0u};
+      float rs = 0.f;
+      if (need) {
+        const long so = (long)seq * A.n_slots + slotr;
+        const uint4 v = *reinterpret_cast<const uint4*>(A.k_res + so * G::KSB + ln * 16);
+        rw[0] = v.x; rw[1] = v.y; rw[2] = v.z; rw[3] = v.w;
+        rs = h2f(A.k_res_scale[so]);
+      }
+      const int cgq = cgr >= 0 ? cgr : 0;
+      float4_t racc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 8; ++s) {
+        const half2_t c0 = code_pair<4, 32, 4>(rw, 2 * s);
+        const half2_t c1 = code_pair<4, 32, 4>(rw, 2 * s + 1);
+        const half4_t ar = {c0[0], c0[1], c1[0], c1[1]};
+        const half4_t bq = *reinterpret_cast<const half4_t*>(sqr4 + ((cgq * 8 + s) * 4 + sc) * 4);
+        racc = mfma4x4(ar, bq, racc);
+      }
+      // the S-side lane (page lj, query sc) takes rank r if its query selected it
+      const float use = (need && ((kbits >> r) & 1u)) ? rs : 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) wk[i] = fmaf(racc[i], use, wk[i]);
+    }
+    // ---- weights of V_hat (ck) and of the V residual rows (cv)
+    int vrank = -1, rvn = 0;
+#pragma unroll
+    for (int v = 0; v < kVtb; ++v) {
+      if (vslot[v] < 0) continue;
+      if (v == sbk) vrank = rvn;
+      ++rvn;
+    }
+    const bool vsel = vrank >= 0 && vrank < a.v_cap && ((vbits >> vrank) & 1u) && 4 * sbk < my_nv;
+    float ck[4], cv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (exact) {
+        const float m1 = kbits ? em1(wk[i] * a.inv_sqrt_d) : 0.f;
+        ck[i] = kbits ? at[i] * m1 : 0.f;
+        cv[i] = vsel ? at[i] * (1.f + m1) : 0.f;
+      } else {
+        ck[i] = kbits ? a.k_corr_scale * at[i] * wk[i] : 0.f;
+        cv[i] = vsel ? at[i] : 0.f;
+      }
+    }
+    den += (ck[0] + ck[1]) + (ck[2] + ck[3]);
+    const half2_t ck01 = {(_Float16)ck[0], (_Float16)ck[1]}, ck23 = {(_Float16)ck[2], (_Float16)ck[3]};
+    const half2_t cv01 = {(_Float16)cv[0], (_Float16)cv[1]}, cv23 = {(_Float16)cv[2], (_Float16)cv[3]};
+    const uint32_t k01 = h2bits(ck01), k23 = h2bits(ck23), v01 = h2bits(cv01), v23 = h2bits(cv23);
+
+    // ---- num += ck V_hat, page by page
+#pragma unroll
+    for (int pi = 0; pi < 4; ++pi) {
+      if (!kany[pi]) continue;
+      _Float16 vs;
+      if constexpr (SM == 1) {
+        const float vm = h2f((uint16_t)__builtin_amdgcn_readlane(cur.meta, 16 * pi + 11));
+        vs = (_Float16)((float)(int8_t)vsc[pi] * vm);
+      } else {
+        vs = bits2half((uint16_t)vsc[pi]);
+      }
+      half2_t vp[CH / 2];
+      dequant_pairs<BITS, CH, BITS>(vw[pi], vs, vp);
+      vtile_write<D, BITS>(vt, vp, ln, lj);
+      const int src = (16 * pi + 4 * lj + (ln & 3)) * 4;
+      uint32_t p01 = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)k01);
+      uint32_t p23 = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)k23);
+      if (ln >= 4) { p01 = 0u; p23 = 0u; }
+      half4_t ap;
+      __builtin_memcpy(&ap, &p01, 4);
+      __builtin_memcpy(reinterpret_cast<char*>(&ap) + 4, &p23, 4);
+      lds_sync_wave();
+      pv_accumulate<D, BITS>(vt, ap, nacc, ln, lj);
+      lds_sync_wave();
+    }
+
+    // ---- num += cv R_V: the window's selected V blocks, 4 per tile
+    // (block u of a round fills tile rows 4u..4u+3)
+    // selected blocks in (page, block) order; the k-th is found by a scan
+    // (block u of a round fills tile rows 4u..4u+3)
+    auto find_block = [&](int k, int& pi_o, int& vb_o, int& slot_o) {
+      int cnt = 0;
+      bool found = false;
+#pragma unroll
+      for (int pi = 0; pi < 4; ++pi) {
+        int rank = 0;
+#pragma unroll
+        for (int v = 0; v < kVtb; ++v) {
+          const int s = __builtin_amdgcn_readlane(cur.meta, 16 * pi + 6 + v);
+          if (s < 0 || s >= A.n_slots) continue;
+          if (rank < a.v_cap && ((vany[pi] >> rank) & 1u)) {
+            if (cnt == k) { pi_o = pi; vb_o = v; slot_o = s; found = true; }
+            ++cnt;
+          }
+          ++rank;
+        }
+      }
+      return found ? cnt : -cnt - 1;  // count of blocks (negative when k is past the end)
+    };
+    int nblk;
+    {
+      int d0, d1, d2;
+      const int r = find_block(-1, d0, d1, d2);
+      nblk = -r - 1;
+    }
+    for (int r0 = 0; r0 < nblk; r0 += 4) {
+      int bpi = 0, bvb = 0, bslot = -1;
+      const bool bok = find_block(r0 + lj, bpi, bvb, bslot) >= 0;
+      // load + dequantise: lane l -> block r0 + l / 16, row m = (l % 16) / 4, chunk l % 4
+      if (bok) {
+        const int m = ln >> 2, c = ln & 3;
+        const long so = (long)seq * A.n_slots + bslot;
+        uint32_t rw[CH / 8];
+        const __amdgpu_buffer_rsrc_t r = make_rsrc(A.v_res + so * G::VSB, G::VSB);
+        buf_load<CH / 2>(rw, r, m * (D / 2) + c * (CH / 2));
+        half2_t rp[CH / 2];
+        dequant_pairs<4, CH, BITS>(rw, bits2half(A.v_res_scale[so]), rp);
+        vtile_write<D, BITS>(vt, rp, 4 * lj + m, c);
+      }
+      // P rows: lane (n, j) <- S lane of block r0 + j (page pi, V block vb): 16*pi + 4*vb + n
+      const int src = (16 * bpi + 4 * bvb + (ln & 3)) * 4;
+      uint32_t p01 = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)v01);
+      uint32_t p23 = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)v23);
+      if (ln >= 4 || !bok) { p01 = 0u; p23 = 0u; }
+      half4_t ap;
+      __builtin_memcpy(&ap, &p01, 4);
+      __builtin_memcpy(reinterpret_cast<char*>(&ap) + 4, &p23, 4);
+      lds_sync_wave();
+      pv_accumulate<D, BITS>(vt, ap, nacc, ln, lj);
+      lds_sync_wave();
+    }
+  }
+
+  // ---- merge the waves and write the chunk partial
+  {
+    float d = den + row_ror<4>(den);
+    d = d + row_ror<8>(d);
+    den = pair32_sum(pair16_sum(d));  // lanes with query sc hold its total
+  }
+  if (lane < 4) s_den[w][lane] = den;
+  const long cbase = ((long)bk * a.nsplit + chunk) * GQ;
+  sum_waves<D, BITS>(reinterpret_cast<float*>(smem), nacc, w, ln, lj, GQ, a.num + cbase * D);
+  if ((int)threadIdx.x < GQ) {
+    const int qq = threadIdx.x;
+    a.den[cbase + qq] = ((s_den[0][qq] + s_den[1][qq]) + s_den[2][qq]) + s_den[3][qq];
+  }
+}
+
+int launch_decode_apply4(const carekv_arena& A, const DecodeArgs& a, hipStream_t s) {
+  const dim3 grid(a.nsplit, A.n_kv_heads, a.B);
+  return dispatch_dbs(A.head_dim, A.base_bits, A.scale_mode, [&](auto d, auto bb, auto sm) {
+    hipLaunchKernelGGL((decode_apply4_kernel<decltype(d)::value, decltype(bb)::value, decltype(sm)::value>), grid,
+                       dim3(256), 0, s, A, a);
+    CAREKV_CHECK_LAUNCH("decode_apply4");
+    return CAREKV_OK;
+  });
+}
+
+}  // namespace carekv

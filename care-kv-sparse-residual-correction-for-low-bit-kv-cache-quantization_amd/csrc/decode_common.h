@@ -15,6 +15,7 @@ struct DecodeArgs {
   float* pml;          // [B*Hkv][nsplit][16][2]  split max (base-2 logits) / sum
   float* po;           // [B*Hkv][nsplit][16][D]  split unnormalised O
   float* rec;          // [B*Hkv][GQ][Pmax][F]    per-page records
+  uint16_t* ebuf;      // [B*Hkv][GQ][Pmax][16]   fp16 e = 2^(x - m_ref) per token (correction on)
   float* scores;       // [B*Hkv][GQ][ncand]      candidate scores
   uint8_t* mask;       // [B*Hkv][GQ][Pmax]       selected slots per page
   float* ml;           // [B*Hkv][GQ][2]          global max (base 2) / sum
@@ -37,6 +38,8 @@ struct DecodeArgs {
 // with e_t = 2^(x_t - m_ref) and Mk = sum_t dS_t^2 e_t^k over the page's
 // valid tokens.  Written only for pages with metadata.
 //
+// ebuf holds the page's e_t (0 past the valid tokens) for the apply pass.
+//
 // Selection mask per (sequence, kv head, query, page): bit r = the r-th
 // stored K slot of the page is selected, bit 4 + r = the r-th stored V block.
 
@@ -44,6 +47,7 @@ int launch_decode_stream(const carekv_arena& A, const DecodeArgs& a, hipStream_t
 int launch_decode_stream4(const carekv_arena& A, const DecodeArgs& a, hipStream_t s);  // GQ <= 4, SP % 16 == 0
 int launch_decode_select(const carekv_arena& A, const DecodeArgs& a, hipStream_t s);
 int launch_decode_apply(const carekv_arena& A, const DecodeArgs& a, hipStream_t s);
+int launch_decode_apply4(const carekv_arena& A, const DecodeArgs& a, hipStream_t s);  // GQ <= 4
 int launch_decode_combine(const carekv_arena& A, const DecodeArgs& a, hipStream_t s);
 
 }  // namespace carekv

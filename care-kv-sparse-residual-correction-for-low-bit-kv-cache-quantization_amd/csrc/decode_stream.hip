@@ -140,6 +140,9 @@ void decode_stream_kernel(carekv_arena A, DecodeArgs a) {
       // ---- page record (layout in decode_common.h)
       float* rec = a.rec + ((long)bk * GQ * a.Pmax + p) * a.F + ln * rq;
       if (lj == 0 && ln < GQ) rec[0] = m_new;
+      if (ln < GQ)
+        *reinterpret_cast<uint2*>(a.ebuf + (((long)bk * GQ + ln) * a.Pmax + p) * 16 + 4 * lj) =
+            make_uint2(h2bits(half2_t{ap[0], ap[1]}), h2bits(half2_t{ap[2], ap[3]}));
       int rk = 0;
 #pragma unroll
       for (int cg = 0; cg < NCG; ++cg) {

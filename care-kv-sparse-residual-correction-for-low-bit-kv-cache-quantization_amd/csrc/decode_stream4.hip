@@ -23,64 +23,6 @@
 
 namespace carekv {
 
-__device__ __forceinline__ float4_t mfma4x4(half4_t a, half4_t b, float4_t c) {
-  return __builtin_amdgcn_mfma_f32_4x4x4f16(a, b, c, 0, 0, 0);
-}
-
-// v from lane (i + N) % 16 of the same 16-lane row (DPP row rotate)
-template <int N>
-__device__ __forceinline__ float row_ror(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x120 + N, 0xf, 0xf, false));
-}
-// Sum / max over the lanes {i, i+4, i+8, i+12} of each 16-lane row.
-__device__ __forceinline__ float row4_sum(float v) {
-  v += row_ror<4>(v);
-  return v + row_ror<8>(v);
-}
-__device__ __forceinline__ float row4_max(float v) {
-  v = fmaxf(v, row_ror<4>(v));
-  return fmaxf(v, row_ror<8>(v));
-}
-
-__device__ __forceinline__ uint32_t pack_h2(float x, float y) {
-  const half2_t h = {(_Float16)x, (_Float16)y};
-  return h2bits(h);
-}
-
-// Buffer load of a packed row of N bytes (N a multiple of 8) at byte offset off.
-template <int N>
-__device__ __forceinline__ void buf_load_row(uint32_t* w, __amdgpu_buffer_rsrc_t r, uint32_t off) {
-  if constexpr (N % 16 == 0) {
-#pragma unroll
-    for (int i = 0; i < N / 16; ++i) {
-      const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off + 16 * i, 0, 0);
-      w[4 * i] = v[0]; w[4 * i + 1] = v[1]; w[4 * i + 2] = v[2]; w[4 * i + 3] = v[3];
-    }
-  } else {
-    static_assert(N % 8 == 0, "row bytes");
-#pragma unroll
-    for (int i = 0; i < N / 8; ++i) {
-      const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, off + 8 * i, 0, 0);
-      w[2 * i] = v[0]; w[2 * i + 1] = v[1];
-    }
-  }
-}
-
-// Metadata of page pg in lane field f (see meta_lanes_load); 0 for pages
-// outside the split.
-template <int NCG>
-__device__ __forceinline__ int meta_field_load(const carekv_arena& A, long pg, bool page_ok, int f) {
-  int v = 0;
-  if (!page_ok) return 0;
-  if (f == 0) v = A.valid[pg];
-  else if (f == 1) v = A.has_meta[pg];
-  else if (f < 2 + NCG) v = A.k_slot[pg * NCG + f - 2];
-  else if (f >= 6 && f < 10) v = A.v_slot[pg * kVtb + f - 6];
-  else if (f == 10 && A.scale_mode == 1) v = A.kmaster[pg];
-  else if (f == 11 && A.scale_mode == 1) v = A.vmaster[pg];
-  return v;
-}
-
 // One window's share of a lane: the K side (prefetched a window ahead)
 // and the V side (loaded at the top of the window's iteration; the S and
 // softmax work covers its latency).
@@ -292,6 +234,8 @@ __global__ __launch_bounds__(256) void decode_stream4_kernel(carekv_arena A, Dec
     const bool rec_lane = sc < GQ && my_meta != 0 && my_nv > 0;
     float* rec = rec_q + (long)my_page * a.F;
     if (rec_lane && sbk == 0) rec[0] = m_new;
+    if (rec_lane)
+      *reinterpret_cast<uint2*>(a.ebuf + (((long)bk * GQ + sc) * a.Pmax + my_page) * 16 + 4 * sbk) = make_uint2(e01, e23);
     int kslot[NCG];
 #pragma unroll
     for (int cg = 0; cg < NCG; ++cg) {
