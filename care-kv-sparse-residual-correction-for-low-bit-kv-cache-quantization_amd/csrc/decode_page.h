@@ -359,34 +359,26 @@ __device__ __forceinline__ void vtile_write(uint32_t* vt, const half2_t* vp, int
                                                     h2bits(vp[i + 3]));
 }
 
-// acc[t] += P V_tile: tile t, column n stands for slot n*NT + t (16x16x16
-// MFMA, k = the page's 16 tokens; P in the A layout: lane (m, j) holds
-// P[query m][token 4j+i]).
+// acc[t] += P V_tile on MFMA 16x16x16: tile t, column n stands for slot
+// 16t + n; k = the page's 16 tokens, P in the A layout (lane (m, j) holds
+// P[query m][token 4j+i]).  The B operand (tokens 4j..4j+3 of one slot
+// column per lane) comes straight from the token-major tile through the
+// gfx950 transpose load: in each 16-lane group, output lane i receives
+// element i % 4 of the 4-half rows read by lanes i/4, i/4+4, i/4+8,
+// i/4+12, so lane r of group j reads row 4j + r/4, slots 4(r%4) .. +3 of
+// the tile's 16.
 template <int D, int BITS>
 __device__ __forceinline__ void pv_accumulate(const uint32_t* vt, half4_t ap, float4_t* acc, int ln, int lj) {
   using G = PageGeom<D, BITS>;
-  constexpr int NT = G::NT;
-  uint32_t vr[4][NT / 2];
+  typedef short short4_t __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) short4_t lds_short4;
+  const __attribute__((address_space(3))) char* base =
+      (const __attribute__((address_space(3))) char*)vt + ((4 * lj + (ln >> 2)) * G::VROW) * 4 + (ln & 3) * 8;
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t* src = vt + (4 * lj + i) * G::VROW + ln * (NT / 2);
-    if constexpr (NT / 2 == 4) {
-      const uint4 x = *reinterpret_cast<const uint4*>(src);
-      vr[i][0] = x.x; vr[i][1] = x.y; vr[i][2] = x.z; vr[i][3] = x.w;
-    } else {
-      const uint2 x = *reinterpret_cast<const uint2*>(src);
-      vr[i][0] = x.x; vr[i][1] = x.y;
-    }
-  }
-#pragma unroll
-  for (int t = 0; t < NT; ++t) {
-    const int wi = t >> 1;
-    const uint32_t sel = (t & 1) ? 0x07060302u : 0x05040100u;  // high / low halves of two words
-    const uint32_t p01 = __builtin_amdgcn_perm(vr[1][wi], vr[0][wi], sel);
-    const uint32_t p23 = __builtin_amdgcn_perm(vr[3][wi], vr[2][wi], sel);
+  for (int t = 0; t < G::NT; ++t) {
+    const short4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(base + 32 * t));
     half4_t bv;
-    __builtin_memcpy(&bv, &p01, 4);
-    __builtin_memcpy(reinterpret_cast<char*>(&bv) + 4, &p23, 4);
+    __builtin_memcpy(&bv, &v, 8);
     acc[t] = mfma16(ap, bv, acc[t]);
   }
 }
@@ -437,7 +429,7 @@ __device__ __forceinline__ void stage_q(_Float16* sq, _Float16* sqr, const uint1
 // Merge the 4 waves' online-softmax partials (m, l, O rows = queries) into
 // one split partial: po[q][d] = sum_w O_w[q][d] 2^(m_w - M), pml[q] = (M, L).
 // O comes in the PV accumulator layout (tile t, lane (n, j): rows 4j+i,
-// column n = slot n*NT + t).  Two rounds of D/2 dims through so[4][16][D/2].
+// column n = slot 16t + n).  Two rounds of D/2 dims through so[4][16][D/2].
 // Call with all threads of the block.
 template <int D, int BITS>
 __device__ __forceinline__ void merge_waves(float* so, float (*s_m)[16], float (*s_l)[16], float m_run,
@@ -451,7 +443,7 @@ __device__ __forceinline__ void merge_waves(float* so, float (*s_m)[16], float (
   for (int half = 0; half < 2; ++half) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const int slot = ln * NT + t;
+      const int slot = 16 * t + ln;
       const int dim = (slot / CH) * CH + G::PB::T.slot_code[slot % CH];
       if ((dim >= DH) != (half == 1)) continue;
 #pragma unroll
@@ -491,7 +483,7 @@ __device__ __forceinline__ void sum_waves(float* so, const float4_t* acc, int w,
   for (int half = 0; half < 2; ++half) {
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-      const int slot = ln * NT + t;
+      const int slot = 16 * t + ln;
       const int dim = (slot / CH) * CH + G::PB::T.slot_code[slot % CH];
       if ((dim >= DH) != (half == 1)) continue;
 #pragma unroll

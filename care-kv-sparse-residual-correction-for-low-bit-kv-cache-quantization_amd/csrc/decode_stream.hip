@@ -187,7 +187,7 @@ void decode_stream_kernel(carekv_arena A, DecodeArgs a) {
   }
 
   // ---- merge the 4 waves' (m, l, O) and write the split partial, half
-  // of the dims per round; V slot n*NT + t maps back to dim
+  // of the dims per round; V slot 16t + n (tile t, column n) maps back to dim
   // chunk*CH + slot_code[slot % CH].
   merge_waves<D, BITS>(reinterpret_cast<float*>(smem), s_m, s_l, m_run, l_run, oacc, w, ln, lj, GQ,
                        a.po + ((long)bk * a.nsplit + split) * 16 * D,
