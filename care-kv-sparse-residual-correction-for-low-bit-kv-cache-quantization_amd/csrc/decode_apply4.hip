@@ -10,7 +10,9 @@
 //     per lane);
 //   * the exact (attention.py:96-118) or linear (attention.py:938-943)
 //     weights of V_hat and of the selected V residual rows.
-// Then O-sized partials on MFMA 16x16x16 through the LDS tile:
+// Then O-sized partials through the LDS tile, num^T += V^T c^T on 4x4x4
+// blocks (A from the tile by the transpose load), which keeps only the 4
+// query heads in the accumulator:
 //   * num += ck V_hat for each page of the window with a selected K slot;
 //   * num += cv R_V for the selected V blocks of the window, 4 blocks per
 //     tile, dequantised by all 64 lanes.
@@ -25,9 +27,9 @@ template <int D, int BITS, int SM>
 __global__ __launch_bounds__(256) void decode_apply4_kernel(carekv_arena A, DecodeArgs a) {
   using G = PageGeom<D, BITS>;
   using PR = Pairs<4, 32, 4>;  // pair schedule of a K residual row
-  constexpr int NT = G::NT, NCG = G::NCG, CH = G::CH, CHB = G::CHB, RB = G::RB;
+  constexpr int NCG = G::NCG, CH = G::CH, CHB = G::CHB, RB = G::RB;
   constexpr int VT_WORDS = kPage * G::VROW;
-  constexpr int MERGE_BYTES = 4 * 16 * (D / 2) * 4;
+  constexpr int MERGE_BYTES = 4 * 4 * D * 4;  // [wave][query][D] fp32
   constexpr int TILE_BYTES = 4 * VT_WORDS * 4;
   constexpr int LDS_BYTES = MERGE_BYTES > TILE_BYTES ? MERGE_BYTES : TILE_BYTES;
   constexpr int kMaxSP = 1024;
@@ -35,6 +37,7 @@ __global__ __launch_bounds__(256) void decode_apply4_kernel(carekv_arena A, Deco
   __shared__ __align__(16) _Float16 sqr4[NCG * 8 * 16];  // [cg][step][query][4]: q in the residual order
   __shared__ int s_items[kMaxSP];
   __shared__ float s_den[4][4];
+  __shared__ __align__(16) uint2 s_pk[4][64], s_pv[4][64];  // per wave: [page][query][token group] ck, cv
   __shared__ BlockScratch bs;
 
   const int chunk = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
@@ -78,9 +81,9 @@ __global__ __launch_bounds__(256) void decode_apply4_kernel(carekv_arena A, Deco
 
   const float Mq = qv ? a.ml[qrow * 2] : 0.f;
   uint32_t* vt = reinterpret_cast<uint32_t*>(smem) + w * VT_WORDS;
-  float4_t nacc[NT];
+  float4_t nacc[D / 64];  // num[query sc][slots 64h + 4(lane/4) .. +3]
 #pragma unroll
-  for (int t = 0; t < NT; ++t) nacc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+  for (int h = 0; h < D / 64; ++h) nacc[h] = float4_t{0.f, 0.f, 0.f, 0.f};
   float den = 0.f;
   // Tile rows a pass leaves unwritten keep finite data and meet zero weights.
   for (int i = lane; i < VT_WORDS; i += 64) vt[i] = 0u;
@@ -232,7 +235,8 @@ __global__ __launch_bounds__(256) void decode_apply4_kernel(carekv_arena A, Deco
     den += (ck[0] + ck[1]) + (ck[2] + ck[3]);
     const half2_t ck01 = {(_Float16)ck[0], (_Float16)ck[1]}, ck23 = {(_Float16)ck[2], (_Float16)ck[3]};
     const half2_t cv01 = {(_Float16)cv[0], (_Float16)cv[1]}, cv23 = {(_Float16)cv[2], (_Float16)cv[3]};
-    const uint32_t k01 = h2bits(ck01), k23 = h2bits(ck23), v01 = h2bits(cv01), v23 = h2bits(cv23);
+    pw_store(s_pk[w], h2bits(ck01), h2bits(ck23), lane);
+    pw_store(s_pv[w], h2bits(cv01), h2bits(cv23), lane);
 
     // ---- num += ck V_hat, page by page
 #pragma unroll
@@ -248,22 +252,17 @@ __global__ __launch_bounds__(256) void decode_apply4_kernel(carekv_arena A, Deco
       half2_t vp[CH / 2];
       dequant_pairs<BITS, CH, BITS>(vw[pi], vs, vp);
       vtile_write<D, BITS>(vt, vp, ln, lj);
-      const int src = (16 * pi + 4 * lj + (ln & 3)) * 4;
-      uint32_t p01 = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)k01);
-      uint32_t p23 = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)k23);
-      if (ln >= 4) { p01 = 0u; p23 = 0u; }
-      half4_t ap;
-      __builtin_memcpy(&ap, &p01, 4);
-      __builtin_memcpy(reinterpret_cast<char*>(&ap) + 4, &p23, 4);
       lds_sync_wave();
-      pv_accumulate<D, BITS>(vt, ap, nacc, ln, lj);
+      uint2 pg[4];  // ck[query sc][tokens 4g..4g+3] of page pi
+      pw_load(s_pk[w], pi, sc, pg);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) pv4_group<D, BITS>(vt, 4 * g, pg[g].x, pg[g].y, nacc, lane);
       lds_sync_wave();
     }
 
     // ---- num += cv R_V: the window's selected V blocks, 4 per tile
-    // (block u of a round fills tile rows 4u..4u+3)
-    // selected blocks in (page, block) order; the k-th is found by a scan
-    // (block u of a round fills tile rows 4u..4u+3)
+    // (block u of a round fills tile rows 4u..4u+3); the selected blocks are
+    // taken in (page, block) order and the k-th is found by a scan
     auto find_block = [&](int k, int& pi_o, int& vb_o, int& slot_o) {
       int cnt = 0;
       bool found = false;
@@ -303,16 +302,16 @@ __global__ __launch_bounds__(256) void decode_apply4_kernel(carekv_arena A, Deco
         dequant_pairs<4, CH, BITS>(rw, bits2half(A.v_res_scale[so]), rp);
         vtile_write<D, BITS>(vt, rp, 4 * lj + m, c);
       }
-      // P rows: lane (n, j) <- S lane of block r0 + j (page pi, V block vb): 16*pi + 4*vb + n
-      const int src = (16 * bpi + 4 * bvb + (ln & 3)) * 4;
-      uint32_t p01 = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)v01);
-      uint32_t p23 = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)v23);
-      if (ln >= 4 || !bok) { p01 = 0u; p23 = 0u; }
-      half4_t ap;
-      __builtin_memcpy(&ap, &p01, 4);
-      __builtin_memcpy(reinterpret_cast<char*>(&ap) + 4, &p23, 4);
       lds_sync_wave();
-      pv_accumulate<D, BITS>(vt, ap, nacc, ln, lj);
+      // block r0 + u (page pi_u, V block vb_u, held by lanes 16u..): cv[query
+      // sc][its 4 tokens] from S lane 16*pi_u + 4*vb_u + sc
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (r0 + u >= nblk) break;
+        const int upi = __builtin_amdgcn_readlane(bpi, 16 * u), uvb = __builtin_amdgcn_readlane(bvb, 16 * u);
+        const uint2 pu = s_pv[w][(upi * 4 + sc) * 4 + uvb];
+        pv4_group<D, BITS>(vt, 4 * u, pu.x, pu.y, nacc, lane);
+      }
       lds_sync_wave();
     }
   }
@@ -325,7 +324,7 @@ __global__ __launch_bounds__(256) void decode_apply4_kernel(carekv_arena A, Deco
   }
   if (lane < 4) s_den[w][lane] = den;
   const long cbase = ((long)bk * a.nsplit + chunk) * GQ;
-  sum_waves<D, BITS>(reinterpret_cast<float*>(smem), nacc, w, ln, lj, GQ, a.num + cbase * D);
+  sum4_waves<D, BITS>(reinterpret_cast<float*>(smem), nacc, w, lane, GQ, a.num + cbase * D);
   if ((int)threadIdx.x < GQ) {
     const int qq = threadIdx.x;
     a.den[cbase + qq] = ((s_den[0][qq] + s_den[1][qq]) + s_den[2][qq]) + s_den[3][qq];

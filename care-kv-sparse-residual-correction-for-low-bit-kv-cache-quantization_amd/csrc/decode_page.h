@@ -558,4 +558,106 @@ __device__ __forceinline__ int meta_field_load(const carekv_arena& A, long pg, b
   return v;
 }
 
+// ---------------------------------------------------------------- 4x4x4 PV
+// O[q][slot] += sum_t P[q][t] V_tile[t][slot] for the 4 tokens of tile rows
+// row0 .. row0+3, on v_mfma_f32_4x4x4_16b_f16 with A = V^T (block b = slots
+// 4b..4b+3 of a 64-slot half) and B = P (4 query heads):
+//   * the A operand comes from the token-major tile through the transpose
+//     load: source lane s of 16-lane group G reads row row0 + s/4, slots
+//     16G + 4(s%4) .. +3, and lane r of the group receives slots 16G + r of
+//     rows row0 .. row0+3;
+//   * p01/p23 hold P[query lane % 4][the 4 tokens] as fp16 pairs.
+// Lane l accumulates O[query l % 4][slots 64h + 4(l/4) .. +3] in acc[h].
+template <int D, int BITS>
+__device__ __forceinline__ void pv4_group(const uint32_t* vt, int row0, uint32_t p01, uint32_t p23, float4_t* acc,
+                                          int lane) {
+  using G = PageGeom<D, BITS>;
+  typedef short short4_t __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) short4_t lds_short4;
+  half4_t bq;
+  __builtin_memcpy(&bq, &p01, 4);
+  __builtin_memcpy(reinterpret_cast<char*>(&bq) + 4, &p23, 4);
+  const int s = lane & 15, g16 = lane >> 4;
+  const __attribute__((address_space(3))) char* base = (const __attribute__((address_space(3))) char*)vt +
+                                                       ((row0 + (s >> 2)) * G::VROW) * 4 + (16 * g16 + 4 * (s & 3)) * 2;
+#pragma unroll
+  for (int h = 0; h < D / 64; ++h) {
+    const short4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(base + 128 * h));
+    half4_t av;
+    __builtin_memcpy(&av, &v, 8);
+    acc[h] = mfma4x4(av, bq, acc[h]);
+  }
+}
+
+// Weights of a 4-page window for the 4x4x4 PV, staged per wave in LDS: the
+// S-layout lane 16*pi + 4*g + q (page pi, tokens 4g..4g+3, query q) stores
+// its 4 fp16 weights at pw[pi][q][g], so a lane reads the 4 token groups of
+// a page for its own query with two 16-byte loads.
+__device__ __forceinline__ void pw_store(uint2* pw, uint32_t w01, uint32_t w23, int lane) {
+  pw[((lane >> 4) * 4 + (lane & 3)) * 4 + ((lane >> 2) & 3)] = make_uint2(w01, w23);
+}
+__device__ __forceinline__ void pw_load(const uint2* pw, int pi, int q, uint2 (&p)[4]) {
+  const uint4* s = reinterpret_cast<const uint4*>(pw + (pi * 4 + q) * 4);
+  const uint4 a = s[0], b = s[1];
+  p[0] = make_uint2(a.x, a.y);
+  p[1] = make_uint2(a.z, a.w);
+  p[2] = make_uint2(b.x, b.y);
+  p[3] = make_uint2(b.z, b.w);
+}
+
+// Dim of slot s (slot order of the base pair schedule, chunks of CH).
+template <int D, int BITS>
+__device__ __forceinline__ int slot_dim(int slot) {
+  using G = PageGeom<D, BITS>;
+  return (slot / G::CH) * G::CH + G::PB::T.slot_code[slot % G::CH];
+}
+
+// merge_waves for the 4x4x4 PV layout (lane l: query l % 4, slots
+// 64h + 4(l/4) + i): so holds [4 waves][4 queries][D] fp32.
+template <int D, int BITS>
+__device__ __forceinline__ void merge4_waves(float* so, float (*s_m)[4], float (*s_l)[4], float m_run, float l_run,
+                                             const float4_t* acc, int w, int lane, int GQ, float* po, float* pml) {
+  __syncthreads();
+  if (lane < 4) { s_m[w][lane] = m_run; s_l[w][lane] = l_run; }
+  const int q = lane & 3, b = lane >> 2;
+#pragma unroll
+  for (int h = 0; h < D / 64; ++h)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) so[(w * 4 + q) * D + slot_dim<D, BITS>(64 * h + 4 * b + i)] = acc[h][i];
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < GQ * D; idx += blockDim.x) {
+    const int qq = idx / D, d = idx % D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) M = fmaxf(M, s_m[ww][qq]);
+    float L = 0.f, O = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int ww = 0; ww < 4; ++ww) {
+        const float f = __builtin_amdgcn_exp2f(s_m[ww][qq] - M);
+        L += s_l[ww][qq] * f;
+        O += so[(ww * 4 + qq) * D + d] * f;
+      }
+    }
+    po[qq * D + d] = O;
+    if (d == 0) { pml[qq * 2] = M; pml[qq * 2 + 1] = L; }
+  }
+}
+
+// sum_waves for the 4x4x4 PV layout: out[q][d] = sum over the 4 waves.
+template <int D, int BITS>
+__device__ __forceinline__ void sum4_waves(float* so, const float4_t* acc, int w, int lane, int GQ, float* out) {
+  __syncthreads();
+  const int q = lane & 3, b = lane >> 2;
+#pragma unroll
+  for (int h = 0; h < D / 64; ++h)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) so[(w * 4 + q) * D + slot_dim<D, BITS>(64 * h + 4 * b + i)] = acc[h][i];
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < GQ * D; idx += blockDim.x) {
+    const int qq = idx / D, d = idx % D;
+    out[qq * D + d] = ((so[qq * D + d] + so[(4 + qq) * D + d]) + so[(8 + qq) * D + d]) + so[(12 + qq) * D + d];
+  }
+}
+
 }  // namespace carekv

@@ -14,8 +14,9 @@
 //   * for every stored K slot of the window's pages, dS = q_cg . R_K on the
 //     same MFMA layout and the moments sum dS^2 e^k (k = 2, 3, 4).
 // V side, per page (lane l: token l % 16, dims [(l/16) D/4, ...)):
-//   V_hat through the padded LDS tile, O += P V_hat on MFMA 16x16x16 with P
-//   moved from the S layout by ds_bpermute.
+//   V_hat through the padded LDS tile, O^T += V_hat^T P^T on 4x4x4 blocks
+//   (A from the tile by the transpose load, P moved from the S layout by
+//   ds_bpermute), so the accumulator holds only the 4 query heads.
 // The page records and split partials are those of decode_stream.hip, with
 // m_ref the running max at the window.
 #include "decode_page.h"
@@ -52,13 +53,14 @@ __global__ __launch_bounds__(256) void decode_stream4_kernel(carekv_arena A, Dec
   constexpr int NCG = G::NCG, CH = G::CH, RB = G::RB, CHB = G::CHB;
   constexpr int NS4 = D / 4;        // 4x4x4 steps over the head dim
   constexpr int VT_WORDS = kPage * G::VROW;
-  constexpr int MERGE_BYTES = 4 * 16 * (D / 2) * 4;
+  constexpr int MERGE_BYTES = 4 * 4 * D * 4;  // [wave][query][D] fp32
   constexpr int TILE_BYTES = 4 * VT_WORDS * 4;
   constexpr int LDS_BYTES = MERGE_BYTES > TILE_BYTES ? MERGE_BYTES : TILE_BYTES;
   __shared__ __align__(16) char smem[LDS_BYTES];
   __shared__ __align__(16) _Float16 sq4[NS4 * 16];       // [step][query][4]: q in the row pair order
   __shared__ __align__(16) _Float16 sqr4[NCG * 8 * 16];  // [cg][step][query][4]: q in the residual order
-  __shared__ float s_m[4][16], s_l[4][16];
+  __shared__ float s_m[4][4], s_l[4][4];
+  __shared__ __align__(16) uint2 s_pw[4][64];            // per wave: [page][query][token group] weights
 
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int GQ = a.GQ;
@@ -92,9 +94,9 @@ __global__ __launch_bounds__(256) void decode_stream4_kernel(carekv_arena A, Dec
 
   uint32_t* vt = reinterpret_cast<uint32_t*>(smem) + w * VT_WORDS;
   float m_run = -INFINITY, l_run = 0.f;
-  float4_t oacc[G::NT];
+  float4_t oacc[D / 64];  // O[query sc][slots 64h + 4(lane/4) .. +3]
 #pragma unroll
-  for (int t = 0; t < G::NT; ++t) oacc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
+  for (int h = 0; h < D / 64; ++h) oacc[h] = float4_t{0.f, 0.f, 0.f, 0.f};
 
   const int p_begin = split * a.SP, p_end = min(p_begin + a.SP, np);
   WK nx;
@@ -192,15 +194,11 @@ __global__ __launch_bounds__(256) void decode_stream4_kernel(carekv_arena A, Dec
     for (int i = 0; i < 4; ++i) e[i] = __builtin_amdgcn_exp2f(x[i] - m_new);
     l_run = l_run * f_old + pair32_sum(pair16_sum(row4_sum((e[0] + e[1]) + (e[2] + e[3]))));
     if (__builtin_expect(__any(f_old != 1.f), 0)) {
-      // rows of oacc are queries 4j+i; query i's factor lives in lane i
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float fi = __shfl(f_old, i, 64);
-#pragma unroll
-        for (int t = 0; t < G::NT; ++t) oacc[t][i] *= fi;
-      }
+      for (int h = 0; h < D / 64; ++h) oacc[h] *= f_old;  // the lane's own query
     }
     const uint32_t e01 = pack_h2(e[0], e[1]), e23 = pack_h2(e[2], e[3]);
+    pw_store(s_pw[w], e01, e23, lane);
 
     // ---- O += P V_hat, page by page
 #pragma unroll
@@ -214,16 +212,11 @@ __global__ __launch_bounds__(256) void decode_stream4_kernel(carekv_arena A, Dec
       half2_t vp[CH / 2];
       dequant_pairs<BITS, CH, BITS>(cv.vw[pi], vs, vp);
       vtile_write<D, BITS>(vt, vp, ln, lj);
-      // P in the A layout: lane (n, j) <- S lane 16*pi + 4*j + n (queries n < 4)
-      const int src = (16 * pi + 4 * lj + (ln & 3)) * 4;
-      uint32_t p01 = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)e01);
-      uint32_t p23 = (uint32_t)__builtin_amdgcn_ds_bpermute(src, (int)e23);
-      if (ln >= 4) { p01 = 0u; p23 = 0u; }
-      half4_t ap;
-      __builtin_memcpy(&ap, &p01, 4);
-      __builtin_memcpy(reinterpret_cast<char*>(&ap) + 4, &p23, 4);
       lds_sync_wave();
-      pv_accumulate<D, BITS>(vt, ap, oacc, ln, lj);
+      uint2 pg[4];  // P[query sc][tokens 4g..4g+3] of page pi
+      pw_load(s_pw[w], pi, sc, pg);
+#pragma unroll
+      for (int g = 0; g < 4; ++g) pv4_group<D, BITS>(vt, 4 * g, pg[g].x, pg[g].y, oacc, lane);
       lds_sync_wave();
     }
 
@@ -303,7 +296,7 @@ __global__ __launch_bounds__(256) void decode_stream4_kernel(carekv_arena A, Dec
     }
   }
 
-  merge_waves<D, BITS>(reinterpret_cast<float*>(smem), s_m, s_l, m_run, l_run, oacc, w, ln, lj, GQ,
+  merge4_waves<D, BITS>(reinterpret_cast<float*>(smem), s_m, s_l, m_run, l_run, oacc, w, lane, GQ,
                        a.po + ((long)bk * a.nsplit + split) * 16 * D,
                        a.pml + ((long)bk * a.nsplit + split) * 16 * 2);
 }
