@@ -3,6 +3,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include "common.h"
 #include "host_util.h"
 
 namespace carekv {
@@ -52,6 +53,14 @@ bool check_arena(const carekv_arena& A) {
   }
   if (A.n_seq <= 0 || A.n_kv_heads <= 0 || A.max_pages <= 0 || A.n_slots <= 0) {
     set_error("arena dimensions must be positive");
+    return false;
+  }
+  // the kernels address one (kv head, sequence) row of pages and one
+  // sequence's slot arena with 32-bit buffer offsets below 2^31
+  const long row_span = (long)A.max_pages * kPage * row_bytes(A.head_dim, A.base_bits);
+  const long slot_span = (long)A.n_slots * (kPage * 32 / 2 > kVtb * A.head_dim / 2 ? kPage * 32 / 2 : kVtb * A.head_dim / 2);
+  if (row_span >= (1L << 31) || slot_span >= (1L << 31)) {
+    set_error("a row of pages or a sequence's slot arena exceeds 2 GiB");
     return false;
   }
   return true;

@@ -17,6 +17,15 @@
 //   * num += cv R_V for the selected V blocks of the window, 4 blocks per
 //     tile, dequantised by all 64 lanes.
 // den accumulates the K weights; decode_combine_kernel finishes.
+//
+// The loop is a software pipeline: the pages, metadata and mask bytes of a
+// window are read two windows ahead, and each load that depends on them
+// (stored weights, K residual rows, V codes, the first 4 V residual blocks)
+// is issued for the next window as soon as the current window is done with
+// the registers it lands in.  Every prefetch is issued by every lane (a lane
+// with nothing to fetch reads out of range of a buffer resource, which
+// returns 0 without a memory access, or a mapped stand-in it then drops), so
+// the in-order load counter never waits across a branch.
 #include "block_util.h"
 #include "decode_page.h"
 #include "host_util.h"
@@ -24,20 +33,22 @@
 namespace carekv {
 
 template <int D, int BITS, int SM>
-__global__ __launch_bounds__(256) void decode_apply4_kernel(carekv_arena A, DecodeArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void decode_apply4_kernel(carekv_arena A, DecodeArgs a) {
   using G = PageGeom<D, BITS>;
   using PR = Pairs<4, 32, 4>;  // pair schedule of a K residual row
-  constexpr int NCG = G::NCG, CH = G::CH, CHB = G::CHB, RB = G::RB;
+  constexpr int NCG = G::NCG, CH = G::CH, CHB = G::CHB, RB = G::RB, NWC = G::NWC;
   constexpr int VT_WORDS = kPage * G::VROW;
   constexpr int MERGE_BYTES = 4 * 4 * D * 4;  // [wave][query][D] fp32
   constexpr int TILE_BYTES = 4 * VT_WORDS * 4;
   constexpr int LDS_BYTES = MERGE_BYTES > TILE_BYTES ? MERGE_BYTES : TILE_BYTES;
   constexpr int kMaxSP = 1024;
+  constexpr uint32_t kOut = 0x80000000u;  // an out-of-range buffer offset
   __shared__ __align__(16) char smem[LDS_BYTES];
   __shared__ __align__(16) _Float16 sqr4[NCG * 8 * 16];  // [cg][step][query][4]: q in the residual order
   __shared__ int s_items[kMaxSP];
   __shared__ float s_den[4][4];
   __shared__ __align__(16) uint2 s_pk[4][64], s_pv[4][64];  // per wave: [page][query][token group] ck, cv
+  __shared__ int s_blk[4][2][16];  // per wave and window parity: selected V blocks, (4 pi + vb) | slot << 4
   __shared__ BlockScratch bs;
 
   const int chunk = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
@@ -52,6 +63,10 @@ __global__ __launch_bounds__(256) void decode_apply4_kernel(carekv_arena A, Deco
   const int sc = lane & 3, sbk = ln >> 2;    // S side: query sc, tokens 4*sbk.. (V block sbk)
   const long pg_base = ((long)kvh * A.n_seq + seq) * A.max_pages;
   const RowRes rr = row_resources<D, BITS, SM>(A, pg_base);
+  const __amdgpu_buffer_rsrc_t kres = make_rsrc(A.k_res + (long)seq * A.n_slots * G::KSB, (uint32_t)A.n_slots * G::KSB);
+  const __amdgpu_buffer_rsrc_t vres = make_rsrc(A.v_res + (long)seq * A.n_slots * G::VSB, (uint32_t)A.n_slots * G::VSB);
+  const uint16_t* kres_s = A.k_res_scale + (long)seq * A.n_slots;
+  const uint16_t* vres_s = A.v_res_scale + (long)seq * A.n_slots;
   const uint8_t* maskb = a.mask + (long)bk * GQ * a.Pmax;
   const bool exact = a.k_exact != 0;
   const bool qv = sc < GQ;
@@ -94,128 +109,205 @@ __global__ __launch_bounds__(256) void decode_apply4_kernel(carekv_arena A, Deco
     return __builtin_amdgcn_exp2f(x * 1.44269504f) - 1.f;
   };
 
-  // one window ahead: page metadata (lane 16*pi + field), the lane's mask
-  // byte, stored weights and m_ref
-  struct WinPre { int meta; unsigned mk; uint32_t e01, e23; float mref; int page; };
+  // ---- pipeline stages
+  // page (S side: page lj), its metadata field ln, the lane's mask byte
+  struct WinPre { int page, meta; unsigned mk; };
   auto load_pre = [&](int base) {
     WinPre x;
     const int it = base + lj;
-    x.page = it < n_items ? s_items[it] : -1;  // this lane's page (S side)
+    x.page = it < n_items ? s_items[min(it, kMaxSP - 1)] : -1;
     const bool ok = x.page >= 0;
-    x.meta = meta_field_load<NCG>(A, pg_base + (ok ? x.page : 0), ok, ln);
-    x.mk = (ok && qv) ? maskb[(long)sc * a.Pmax + x.page] : 0u;
-    x.e01 = 0u; x.e23 = 0u; x.mref = 0.f;
-    if (ok && qv) {
-      const uint2 e = *reinterpret_cast<const uint2*>(a.ebuf + (qrow * a.Pmax + x.page) * 16 + 4 * sbk);
-      x.e01 = e.x; x.e23 = e.y;
-      x.mref = a.rec[(qrow * a.Pmax + x.page) * a.F];
-    }
+    const int pc = ok ? x.page : 0;
+    x.meta = meta_field_any<NCG, SM>(A, pg_base, pc, ok, ln);
+    const unsigned m = maskb[(long)(qv ? sc : 0) * a.Pmax + pc];
+    x.mk = (ok && qv) ? m : 0u;
     return x;
   };
-
-  WinPre nx{};
-  int base = 4 * w;
-  if (base < n_items) nx = load_pre(base);
-  for (; base < n_items; base += 16) {
-    const WinPre cur = nx;
-    if (base + 16 < n_items) nx = load_pre(base + 16);
-    int pgi[4];
+  // uniform digest of a window: pages, which slot ranks any query selected
+  struct Plan { int pg[4]; unsigned kany[4], vany[4]; int nblk; };
+  auto make_plan = [&](const WinPre& x, int par) {
+    Plan p;
 #pragma unroll
-    for (int pi = 0; pi < 4; ++pi) pgi[pi] = __builtin_amdgcn_readlane(cur.page, 16 * pi);
-    // slots selected by any query, per page (bit r of kany[pi] / vany[pi])
-    const unsigned kbits = cur.mk & 15u, vbits = cur.mk >> 4;
-    unsigned kany[4] = {0u, 0u, 0u, 0u}, vany[4] = {0u, 0u, 0u, 0u};
+    for (int pi = 0; pi < 4; ++pi) {
+      p.pg[pi] = __builtin_amdgcn_readlane(x.page, 16 * pi);
+      p.kany[pi] = 0u;
+      p.vany[pi] = 0u;
+    }
+    const unsigned kbits = x.mk & 15u, vbits = x.mk >> 4;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const unsigned long long kb = __ballot((kbits >> r) & 1u), vb = __ballot((vbits >> r) & 1u);
 #pragma unroll
       for (int pi = 0; pi < 4; ++pi) {
-        if ((kb >> (16 * pi)) & 0xffffull) kany[pi] |= 1u << r;
-        if ((vb >> (16 * pi)) & 0xffffull) vany[pi] |= 1u << r;
+        if ((kb >> (16 * pi)) & 0xffffull) p.kany[pi] |= 1u << r;
+        if ((vb >> (16 * pi)) & 0xffffull) p.vany[pi] |= 1u << r;
       }
     }
-    // this lane's page fields (S side and K-residual side share page lj)
-    const int my_nv = __shfl(cur.meta, lane & 48, 64);
-    int kslot[NCG], vslot[kVtb];
+    // selected V blocks in (page, block) order: lane l stands for block
+    // bb = l % 16 (page bb / 4, V block bb % 4); its rank among the page's
+    // stored blocks decides whether a query selected it
+    const int bb = lane & 15, bpi = bb >> 2;
+    const int s = __shfl(x.meta, 16 * bpi + 6 + (bb & 3), 64);
+    const bool stored = s >= 0 && s < A.n_slots;
+    const unsigned sm = (unsigned)(__ballot(stored) & 0xffffull);
+    const int rank = __builtin_popcount(sm & (0xfu << (4 * bpi)) & ((1u << bb) - 1u));
+    const unsigned va = bpi == 0 ? p.vany[0] : bpi == 1 ? p.vany[1] : bpi == 2 ? p.vany[2] : p.vany[3];
+    const bool sel = stored && rank < a.v_cap && ((va >> rank) & 1u);
+    const unsigned selm = (unsigned)(__ballot(sel) & 0xffffull);
+    p.nblk = __builtin_popcount(selm);
+    if (lane < 16 && sel) s_blk[w][par][__builtin_popcount(selm & ((1u << bb) - 1u))] = bb | (s << 4);
+    return p;
+  };
+  // stored weights and m_ref of the lane's (page, query)
+  struct WinE { uint32_t e01, e23; float mref; };
+  auto load_e = [&](const WinPre& x) {
+    WinE e;
+    const long r = qrow * a.Pmax + (x.page >= 0 ? x.page : 0);
+    const uint2 v = *reinterpret_cast<const uint2*>(a.ebuf + r * 16 + 4 * sbk);
+    e.e01 = v.x; e.e23 = v.y;
+    e.mref = a.rec[r * a.F];
+    return e;
+  };
+  // K residual row ln of the lowest selected rank of the lane's page lj
+  struct KRow { uint32_t w[4]; float scale; int rank; };
+  auto load_krow = [&](const WinPre& x, const Plan& p) {
+    KRow k;
+    const unsigned ka = lj == 0 ? p.kany[0] : lj == 1 ? p.kany[1] : lj == 2 ? p.kany[2] : p.kany[3];
+    const int r0 = ka ? __builtin_ctz(ka) : -1;
+    int slot = -1, cnt = 0;
 #pragma unroll
     for (int cg = 0; cg < NCG; ++cg) {
-      const int s = __shfl(cur.meta, (lane & 48) + 2 + cg, 64);
-      kslot[cg] = (s >= 0 && s < A.n_slots) ? s : -1;
+      const int s = __shfl(x.meta, (lane & 48) + 2 + cg, 64);
+      if (s < 0 || s >= A.n_slots) continue;
+      if (cnt == r0) slot = s;
+      ++cnt;
     }
-#pragma unroll
-    for (int v = 0; v < kVtb; ++v) {
-      const int s = __shfl(cur.meta, (lane & 48) + 6 + v, 64);
-      vslot[v] = (s >= 0 && s < A.n_slots) ? s : -1;
-    }
-    const unsigned kany_all = kany[0] | kany[1] | kany[2] | kany[3];
-
-    // ---- V codes and scales of the pages with a selected K slot (V side:
-    // token ln, chunk lj)
-    uint32_t vw[4][G::NWC];
-    uint32_t vsc[4];
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(kres, slot >= 0 ? (uint32_t)slot * G::KSB + ln * 16 : kOut, 0, 0);
+    k.w[0] = v[0]; k.w[1] = v[1]; k.w[2] = v[2]; k.w[3] = v[3];
+    k.scale = h2f(kres_s[slot >= 0 ? slot : 0]);
+    k.rank = slot >= 0 ? r0 : -1;
+    return k;
+  };
+  // V codes and scales (V side: token ln, chunk lj) of the pages with a
+  // selected K slot
+  struct VCodes { uint32_t vw[4][NWC]; uint32_t vsc[4]; };
+  auto load_vcodes = [&](const Plan& p) {
+    VCodes v;
     const int gi = (lj * CH) / 32;
 #pragma unroll
     for (int pi = 0; pi < 4; ++pi) {
-      if (!kany[pi]) continue;
-      const uint32_t vrow = (uint32_t)(pgi[pi] * kPage + ln);
-      buf_load<CHB>(vw[pi], rr.vc, vrow * RB + lj * CHB);
-      if constexpr (SM == 1) vsc[pi] = __builtin_amdgcn_raw_buffer_load_b8(rr.vs, vrow * NCG + gi, 0, 0);
-      else vsc[pi] = __builtin_amdgcn_raw_buffer_load_b16(rr.vs, (vrow * NCG + gi) * 2, 0, 0);
+      const bool on = p.kany[pi] != 0u;
+      const uint32_t vrow = (uint32_t)(max(p.pg[pi], 0) * kPage + ln);
+      buf_load<CHB>(v.vw[pi], rr.vc, on ? vrow * RB + lj * CHB : kOut);
+      if constexpr (SM == 1) v.vsc[pi] = __builtin_amdgcn_raw_buffer_load_b8(rr.vs, on ? vrow * NCG + gi : kOut, 0, 0);
+      else v.vsc[pi] = __builtin_amdgcn_raw_buffer_load_b16(rr.vs, on ? (vrow * NCG + gi) * 2 : kOut, 0, 0);
     }
+    return v;
+  };
+  // V residual rows of blocks r0 .. r0+3 of the list (lane l: block
+  // r0 + l / 16, row (l % 16) / 4, chunk l % 4)
+  struct VRes { uint32_t w[CH / 8]; float scale; };
+  auto load_vres = [&](int par, int r0, int nblk) {
+    VRes v;
+    const int k = r0 + lj;
+    const int e = s_blk[w][par][min(k, 15)];
+    const bool on = k < nblk;
+    const int slot = on ? (e >> 4) : 0;
+    const int m = ln >> 2, c = ln & 3;
+    buf_load<CH / 2>(v.w, vres, on ? (uint32_t)slot * G::VSB + m * (D / 2) + c * (CH / 2) : kOut);
+    v.scale = h2f(vres_s[slot]);
+    return v;
+  };
+
+  // ---- prologue: window 0 resolved, window 1's page records in flight
+  int base = 4 * w, par = 0;
+  WinPre pre0 = load_pre(base), pre1 = load_pre(base + 16);
+  Plan plan0 = make_plan(pre0, 0);
+  WinE e0 = load_e(pre0);
+  KRow kr0 = load_krow(pre0, plan0);
+  VCodes vc0 = load_vcodes(plan0);
+  VRes vr0 = load_vres(0, 0, plan0.nblk);
+
+  for (; base < n_items; base += 16, par ^= 1) {
+    const WinPre cur = pre0;
+    const Plan cp = plan0;
+    const WinE ce = e0;
+    pre0 = pre1;
+    pre1 = load_pre(base + 32);
+    plan0 = make_plan(pre0, par ^ 1);
+    e0 = load_e(pre0);
+
+    const unsigned kbits = cur.mk & 15u, vbits = cur.mk >> 4;
+    const int my_nv = __shfl(cur.meta, lane & 48, 64);
+    const unsigned kany_all = cp.kany[0] | cp.kany[1] | cp.kany[2] | cp.kany[3];
 
     // ---- attention weights a_t = e_t 2^(m_ref - M)
     float at[4];
     {
-      const float f = qv ? __builtin_amdgcn_exp2f(cur.mref - Mq) : 0.f;
+      const float f = qv ? __builtin_amdgcn_exp2f(ce.mref - Mq) : 0.f;
       half2_t e01, e23;
-      __builtin_memcpy(&e01, &cur.e01, 4);
-      __builtin_memcpy(&e23, &cur.e23, 4);
+      __builtin_memcpy(&e01, &ce.e01, 4);
+      __builtin_memcpy(&e23, &ce.e23, 4);
       at[0] = (float)e01[0] * f; at[1] = (float)e01[1] * f;
       at[2] = (float)e23[0] * f; at[3] = (float)e23[1] * f;
     }
+
     // ---- dS over the selected K slots (rank r: r-th stored slot of the page)
     float wk[4] = {0.f, 0.f, 0.f, 0.f};
-    for (int r = 0; r < a.k_cap && r < NCG; ++r) {
-      if (!((kany_all >> r) & 1u)) continue;
-      int cgr = -1, slotr = -1, cnt = 0;
+    {
+      int kslot[NCG];
 #pragma unroll
       for (int cg = 0; cg < NCG; ++cg) {
-        if (kslot[cg] < 0) continue;
-        if (cnt == r) { cgr = cg; slotr = kslot[cg]; }
-        ++cnt;
+        const int s = __shfl(cur.meta, (lane & 48) + 2 + cg, 64);
+        kslot[cg] = (s >= 0 && s < A.n_slots) ? s : -1;
       }
-      // rows are needed for pages where some query selected rank r
-      const unsigned pk = (kany[0] >> r & 1u) | ((kany[1] >> r & 1u) << 1) | ((kany[2] >> r & 1u) << 2) |
-                          ((kany[3] >> r & 1u) << 3);
-      const bool need = cgr >= 0 && ((pk >> lj) & 1u);
-      uint32_t rw[4] = {0u, 0u, 0u, 0u};
-      float rs = 0.f;
-      if (need) {
-        const long so = (long)seq * A.n_slots + slotr;
-        const uint4 v = *reinterpret_cast<const uint4*>(A.k_res + so * G::KSB + ln * 16);
-        rw[0] = v.x; rw[1] = v.y; rw[2] = v.z; rw[3] = v.w;
-        rs = h2f(A.k_res_scale[so]);
-      }
-      const int cgq = cgr >= 0 ? cgr : 0;
-      float4_t racc = {0.f, 0.f, 0.f, 0.f};
+      const unsigned ka = lj == 0 ? cp.kany[0] : lj == 1 ? cp.kany[1] : lj == 2 ? cp.kany[2] : cp.kany[3];
+      for (int r = 0; r < a.k_cap && r < NCG; ++r) {
+        if (!((kany_all >> r) & 1u)) continue;
+        int cgr = -1, slotr = -1, cnt = 0;
 #pragma unroll
-      for (int s = 0; s < 8; ++s) {
-        const half2_t c0 = code_pair<4, 32, 4>(rw, 2 * s);
-        const half2_t c1 = code_pair<4, 32, 4>(rw, 2 * s + 1);
-        const half4_t ar = {c0[0], c0[1], c1[0], c1[1]};
-        const half4_t bq = *reinterpret_cast<const half4_t*>(sqr4 + ((cgq * 8 + s) * 4 + sc) * 4);
-        racc = mfma4x4(ar, bq, racc);
-      }
-      // the S-side lane (page lj, query sc) takes rank r if its query selected it
-      const float use = (need && ((kbits >> r) & 1u)) ? rs : 0.f;
+        for (int cg = 0; cg < NCG; ++cg) {
+          if (kslot[cg] < 0) continue;
+          if (cnt == r) { cgr = cg; slotr = kslot[cg]; }
+          ++cnt;
+        }
+        // rows are needed for pages where some query selected rank r
+        const bool need = cgr >= 0 && ((ka >> r) & 1u);
+        uint32_t rw[4] = {kr0.w[0], kr0.w[1], kr0.w[2], kr0.w[3]};
+        float rs = kr0.scale;
+        const bool fetch = need && r != kr0.rank;
+        if (__any(fetch)) {  // a rank past the prefetched one (rare)
+          const auto v = __builtin_amdgcn_raw_buffer_load_b128(kres, fetch ? (uint32_t)slotr * G::KSB + ln * 16 : kOut, 0, 0);
+          const float fs = h2f(kres_s[fetch ? slotr : 0]);
+          if (fetch) {
+            rw[0] = v[0]; rw[1] = v[1]; rw[2] = v[2]; rw[3] = v[3];
+            rs = fs;
+          }
+        }
+        const int cgq = cgr >= 0 ? cgr : 0;
+        float4_t racc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) wk[i] = fmaf(racc[i], use, wk[i]);
+        for (int s = 0; s < 8; ++s) {
+          const half2_t c0 = code_pair<4, 32, 4>(rw, 2 * s);
+          const half2_t c1 = code_pair<4, 32, 4>(rw, 2 * s + 1);
+          const half4_t ar = {c0[0], c0[1], c1[0], c1[1]};
+          const half4_t bq = *reinterpret_cast<const half4_t*>(sqr4 + ((cgq * 8 + s) * 4 + sc) * 4);
+          racc = mfma4x4(ar, bq, racc);
+        }
+        // the S-side lane (page lj, query sc) takes rank r if its query selected it
+        const float use = (need && ((kbits >> r) & 1u)) ? rs : 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) wk[i] = fmaf(racc[i], use, wk[i]);
+      }
     }
+    kr0 = load_krow(pre0, plan0);
+
     // ---- weights of V_hat (ck) and of the V residual rows (cv)
     int vrank = -1, rvn = 0;
 #pragma unroll
     for (int v = 0; v < kVtb; ++v) {
-      if (vslot[v] < 0) continue;
+      const int s = __shfl(cur.meta, (lane & 48) + 6 + v, 64);
+      if (s < 0 || s >= A.n_slots) continue;
       if (v == sbk) vrank = rvn;
       ++rvn;
     }
@@ -241,16 +333,16 @@ __global__ __launch_bounds__(256) void decode_apply4_kernel(carekv_arena A, Deco
     // ---- num += ck V_hat, page by page
 #pragma unroll
     for (int pi = 0; pi < 4; ++pi) {
-      if (!kany[pi]) continue;
+      if (!cp.kany[pi]) continue;
       _Float16 vs;
       if constexpr (SM == 1) {
         const float vm = h2f((uint16_t)__builtin_amdgcn_readlane(cur.meta, 16 * pi + 11));
-        vs = (_Float16)((float)(int8_t)vsc[pi] * vm);
+        vs = (_Float16)((float)(int8_t)vc0.vsc[pi] * vm);
       } else {
-        vs = bits2half((uint16_t)vsc[pi]);
+        vs = bits2half((uint16_t)vc0.vsc[pi]);
       }
       half2_t vp[CH / 2];
-      dequant_pairs<BITS, CH, BITS>(vw[pi], vs, vp);
+      dequant_pairs<BITS, CH, BITS>(vc0.vw[pi], vs, vp);
       vtile_write<D, BITS>(vt, vp, ln, lj);
       lds_sync_wave();
       uint2 pg[4];  // ck[query sc][tokens 4g..4g+3] of page pi
@@ -260,60 +352,30 @@ __global__ __launch_bounds__(256) void decode_apply4_kernel(carekv_arena A, Deco
       lds_sync_wave();
     }
 
-    // ---- num += cv R_V: the window's selected V blocks, 4 per tile
-    // (block u of a round fills tile rows 4u..4u+3); the selected blocks are
-    // taken in (page, block) order and the k-th is found by a scan
-    auto find_block = [&](int k, int& pi_o, int& vb_o, int& slot_o) {
-      int cnt = 0;
-      bool found = false;
-#pragma unroll
-      for (int pi = 0; pi < 4; ++pi) {
-        int rank = 0;
-#pragma unroll
-        for (int v = 0; v < kVtb; ++v) {
-          const int s = __builtin_amdgcn_readlane(cur.meta, 16 * pi + 6 + v);
-          if (s < 0 || s >= A.n_slots) continue;
-          if (rank < a.v_cap && ((vany[pi] >> rank) & 1u)) {
-            if (cnt == k) { pi_o = pi; vb_o = v; slot_o = s; found = true; }
-            ++cnt;
-          }
-          ++rank;
-        }
-      }
-      return found ? cnt : -cnt - 1;  // count of blocks (negative when k is past the end)
-    };
-    int nblk;
-    {
-      int d0, d1, d2;
-      const int r = find_block(-1, d0, d1, d2);
-      nblk = -r - 1;
-    }
-    for (int r0 = 0; r0 < nblk; r0 += 4) {
-      int bpi = 0, bvb = 0, bslot = -1;
-      const bool bok = find_block(r0 + lj, bpi, bvb, bslot) >= 0;
-      // load + dequantise: lane l -> block r0 + l / 16, row m = (l % 16) / 4, chunk l % 4
-      if (bok) {
+    vc0 = load_vcodes(plan0);
+
+    // ---- num += cv R_V: the window's selected V blocks, 4 per tile (block
+    // u of a round fills tile rows 4u..4u+3); round 0 was prefetched
+    for (int r0 = 0; r0 < cp.nblk; r0 += 4) {
+      const VRes rv = r0 == 0 ? vr0 : load_vres(par, r0, cp.nblk);
+      if (r0 + lj < cp.nblk) {
         const int m = ln >> 2, c = ln & 3;
-        const long so = (long)seq * A.n_slots + bslot;
-        uint32_t rw[CH / 8];
-        const __amdgpu_buffer_rsrc_t r = make_rsrc(A.v_res + so * G::VSB, G::VSB);
-        buf_load<CH / 2>(rw, r, m * (D / 2) + c * (CH / 2));
         half2_t rp[CH / 2];
-        dequant_pairs<4, CH, BITS>(rw, bits2half(A.v_res_scale[so]), rp);
+        dequant_pairs<4, CH, BITS>(rv.w, (_Float16)rv.scale, rp);
         vtile_write<D, BITS>(vt, rp, 4 * lj + m, c);
       }
       lds_sync_wave();
-      // block r0 + u (page pi_u, V block vb_u, held by lanes 16u..): cv[query
-      // sc][its 4 tokens] from S lane 16*pi_u + 4*vb_u + sc
+      // block r0 + u: cv[query sc][its 4 tokens] from S lane 16*pi_u + 4*vb_u + sc
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        if (r0 + u >= nblk) break;
-        const int upi = __builtin_amdgcn_readlane(bpi, 16 * u), uvb = __builtin_amdgcn_readlane(bvb, 16 * u);
-        const uint2 pu = s_pv[w][(upi * 4 + sc) * 4 + uvb];
+        if (r0 + u >= cp.nblk) break;
+        const int bu = s_blk[w][par][r0 + u] & 15;
+        const uint2 pu = s_pv[w][((bu >> 2) * 4 + sc) * 4 + (bu & 3)];
         pv4_group<D, BITS>(vt, 4 * u, pu.x, pu.y, nacc, lane);
       }
       lds_sync_wave();
     }
+    vr0 = load_vres(par ^ 1, 0, plan0.nblk);
   }
 
   // ---- merge the waves and write the chunk partial

@@ -228,10 +228,12 @@ struct RowRes {
   __amdgpu_buffer_rsrc_t kc, vc, ks, vs;
 };
 
+// pg_end clamps the resources at that page of the row: a load past it
+// returns 0 without a memory access.
 template <int D, int BITS, int SM>
-__device__ __forceinline__ RowRes row_resources(const carekv_arena& A, long pg_base) {
+__device__ __forceinline__ RowRes row_resources(const carekv_arena& A, long pg_base, int pg_end = -1) {
   using G = PageGeom<D, BITS>;
-  const uint32_t rows = (uint32_t)A.max_pages * kPage;
+  const uint32_t rows = (uint32_t)(pg_end >= 0 ? pg_end : A.max_pages) * kPage;
   constexpr int ssz = SM == 1 ? 1 : 2;
   RowRes r;
   r.kc = make_rsrc(A.kcodes + pg_base * kPage * G::RB, rows * G::RB);
@@ -556,6 +558,27 @@ __device__ __forceinline__ int meta_field_load(const carekv_arena& A, long pg, b
   else if (f == 10 && A.scale_mode == 1) v = A.kmaster[pg];
   else if (f == 11 && A.scale_mode == 1) v = A.vmaster[pg];
   return v;
+}
+
+// Field f of page p of a row (layout of meta_field_load) with no branch:
+// three loads (the int32, fp16 and int8 arrays) that every lane issues.  A
+// lane whose field is in another array, or whose page is not ok, reads page
+// 0 of the row (always mapped) and drops the value; a page that is not ok
+// gives 0.
+template <int NCG, int SM>
+__device__ __forceinline__ int meta_field_any(const carekv_arena& A, long pg_base, int p, bool ok, int f) {
+  const long pg = pg_base + (ok ? p : 0);
+  const bool in_ks = f >= 2 && f < 2 + NCG, in_vs = f >= 6 && f < 6 + kVtb;
+  const int32_t* p32 = in_ks ? A.k_slot + pg * NCG + (f - 2) : in_vs ? A.v_slot + pg * kVtb + (f - 6) : A.valid + pg;
+  const int v32 = *p32;
+  int v16 = 0;
+  if constexpr (SM == 1) v16 = (int)(f == 11 ? A.vmaster : A.kmaster)[pg];
+  const int v8 = (int)A.has_meta[pg];
+  int v = 0;
+  if (f == 0 || in_ks || in_vs) v = v32;
+  if (f == 1) v = v8;
+  if (f == 10 || f == 11) v = v16;
+  return ok ? v : 0;
 }
 
 // ---------------------------------------------------------------- 4x4x4 PV
