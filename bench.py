@@ -295,7 +295,11 @@ def main():
                "sample": f"{args.cpu_slices} of {B * Hkv} (sequence, kv-head) slices of the same cache "
                          f"({per_slice:.3f} s each, numpy oracle), extrapolated x{B * Hkv}"}
         log(f"[bench] cpu oracle {per_slice:.3f} s/slice -> {cpu_us / 1e3:.1f} ms/step extrapolated")
-    tr = load_traffic("decode_stream", args.config + ("_base" if args.no_correction else ""))
+    # the library runs the 4-query-head streaming kernel when a kv head has at
+    # most 4 query heads and the split is a multiple of 16 pages
+    sp = args.split_pages or care_kv.attention.default_split_pages(P, B * Hkv)
+    stream_kernel = "decode_stream4_kernel" if Hq // Hkv <= 4 and sp % 16 == 0 else "decode_stream_kernel"
+    tr = load_traffic(stream_kernel, args.config + ("_base" if args.no_correction else ""))
     traffic = None if tr is None else tr.get("hbm_bytes_per_launch")
     line = {
         "metric": "CARE-KV decode-attn us/step + HBM GB/s (% roofline), Mistral-7B shape 32K ctx",
@@ -308,7 +312,7 @@ def main():
                            "KSCORE_LIVE, normalize, exact"},
         "hbm_gbps": round(gbps, 1),
         "phases_us": {n: round(t, 2) for n, t in zip(names, phase)},
-        "roofline": {"bound": "hbm", "kernel": f"decode_stream_kernel<{D},{cfg.base_bits},1>",
+        "roofline": {"bound": "hbm", "kernel": f"{stream_kernel}<{D},{cfg.base_bits},1>",
                      "achieved": round(stream_gbps, 1), "peak": 8000.0, "unit": "GB/s",
                      "frac": round(stream_gbps / 8000.0, 4), "traffic": traffic,
                      "algorithmic_bytes_per_launch": int(stream_bytes), "launch_us": round(phase[0], 2),
