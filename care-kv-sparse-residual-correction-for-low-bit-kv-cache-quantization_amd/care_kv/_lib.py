@@ -45,11 +45,17 @@ class DecodeParams(C.Structure):
                 ("split_pages", C.c_int32), ("phase_events", C.c_void_p)]
 
 
+class PrefillParams(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("batch", "n_heads", "n_kv_heads", "seq_len", "head_dim", "causal")] + \
+        [("sm_scale", C.c_float)]
+
+
 # page job: int32 x 6 (seq, kv_head, page, num_valid, token_start, is_recent)
 PAGE_JOB_INTS = 6
 
 EXPORTS = ["carekv_store_pages", "carekv_store_workspace_bytes", "carekv_append_rows", "carekv_decode_attn",
-           "carekv_decode_workspace_bytes", "carekv_read_pages", "carekv_quantize_rows", "carekv_last_error"]
+           "carekv_decode_workspace_bytes", "carekv_read_pages", "carekv_quantize_rows", "carekv_prefill_attn",
+           "carekv_dequantize_rows", "carekv_last_error"]
 
 
 def lib_path() -> str:
@@ -83,6 +89,10 @@ def load(path: str | None = None):
         lib.carekv_read_pages.argtypes = [C.POINTER(Arena), i32, i32, i32, vp, vp, vp, vp, vp, vp]
         lib.carekv_quantize_rows.restype = C.c_int
         lib.carekv_quantize_rows.argtypes = [vp, i32, i32, i32, i32, i32, vp, vp, vp]
+        lib.carekv_prefill_attn.restype = C.c_int
+        lib.carekv_prefill_attn.argtypes = [C.POINTER(PrefillParams), vp, vp, vp, vp, vp, vp]
+        lib.carekv_dequantize_rows.restype = C.c_int
+        lib.carekv_dequantize_rows.argtypes = [vp, vp, i32, i32, i32, vp, vp]
         _lib = lib
         return lib
 

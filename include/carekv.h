@@ -172,6 +172,30 @@ int carekv_read_pages(const carekv_arena* arena, int32_t seq, int32_t kv_head, i
 int carekv_quantize_rows(const uint16_t* x, int32_t rows, int32_t D, int32_t bits, int32_t group,
                          int32_t pack, int8_t* codes, uint16_t* scale, void* stream);
 
+/* Prefill attention over dequantised K/V: CAREKVLayer._causal_attention_pure
+ * (layer.py:935-972) for a batch of sequences, with GQA heads read in place
+ * instead of repeat_interleave'd (layer.py:774-775).  q fp16
+ * [batch][n_heads][seq_len][head_dim], k/v fp16 [batch][n_kv_heads][seq_len]
+ * [head_dim] (post-RoPE K_hat, V_hat), out fp16 like q.  Scores are the fp32
+ * product times sm_scale; causal != 0 masks tokens after the query (the
+ * attention_mask=None branch, layer.py:958-962).  The (T, T) weights are not
+ * materialised: lse (optional, fp32 [batch][n_heads][seq_len]) receives the
+ * natural log-sum-exp of each query's scaled scores, so that any weight is
+ * exp(score * sm_scale - lse).  head_dim 64 or 128. */
+typedef struct carekv_prefill_params {
+  int32_t batch, n_heads, n_kv_heads, seq_len, head_dim, causal;
+  float sm_scale;
+} carekv_prefill_params;
+
+int carekv_prefill_attn(const carekv_prefill_params* params, const uint16_t* q, const uint16_t* k,
+                        const uint16_t* v, uint16_t* out, float* lse, void* stream);
+
+/* dequantize (quantizer.py:67-82): out fp16 [rows][D] = half(code * scale)
+ * from unpacked int8 codes [rows][D] and fp16 group scales [rows][D/group]
+ * as carekv_quantize_rows (pack = 0) writes them; group must be 32. */
+int carekv_dequantize_rows(const int8_t* codes, const uint16_t* scale, int32_t rows, int32_t D, int32_t group,
+                           uint16_t* out, void* stream);
+
 const char* carekv_last_error(void);
 
 #ifdef __cplusplus

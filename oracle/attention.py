@@ -14,6 +14,9 @@ Follows ``attention.py`` of the reference:
   * ``decode_attention``           -- attention.py:979-1077 with the
     correction call swapped for the batched joint correction over the GQA
     group's queries (per-query-row semantics, attention.py:830-875).
+  * ``causal_attention_pure``      -- layer.py:935-972 (the prefill
+    attention over dequantised K/V, attention_mask=None branch), with the
+    GQA heads of layer.py:774-775 read in place.
 """
 from __future__ import annotations
 
@@ -333,3 +336,37 @@ def decode_attention(cache: OCache, layer_id, Qh, page_ids_by_kvh=None, correcti
             d.update(S=S, A=A, O_base=O_base, V_hat=Vh, K_hat=Kh)
         out[heads] = O.astype(F16)
     return out
+
+
+def causal_attention_pure(Qh, K, V, causal=True, rows=None):
+    """layer.py:935-972: scores = fp32(Q) . fp32(K) / sqrt(D); causal mask with
+    finfo(fp32).min above the diagonal; softmax in fp32; weights cast to
+    fp16; O = weights @ V with fp32 accumulation, returned in fp16.
+
+    Qh (Hq, T, D) fp16, K/V (Hkv, T, D) fp16; query head h reads kv head
+    h // (Hq / Hkv) (repeat_interleave, layer.py:774-775).  ``rows``
+    restricts the computation to those query rows (for long sequences).
+    Returns (O (Hq, n_rows, D) fp16, lse (Hq, n_rows) fp32)."""
+    Qh = np.asarray(Qh, dtype=F16)
+    K = np.asarray(K, dtype=F16)
+    V = np.asarray(V, dtype=F16)
+    Hq, T, D = Qh.shape
+    grp = Hq // K.shape[0]
+    rows = np.arange(T) if rows is None else np.asarray(rows)
+    out = np.zeros((Hq, len(rows), D), dtype=F16)
+    lse = np.zeros((Hq, len(rows)), dtype=F32)
+    inv = F32(math.sqrt(D))
+    mn = np.finfo(F32).min
+    for h in range(Hq):
+        Kf = K[h // grp].astype(F32)
+        Vf = V[h // grp].astype(F32)
+        S = (Qh[h, rows].astype(F32) @ Kf.T) / inv  # (n_rows, T)
+        if causal:
+            S = S + np.where(np.arange(T)[None, :] > rows[:, None], mn, F32(0)).astype(F32)
+        m = S.max(axis=-1, keepdims=True)
+        e = np.exp(S - m, dtype=F32)
+        z = e.sum(axis=-1, keepdims=True, dtype=F32)
+        A = (e / z).astype(F16)
+        out[h] = (A.astype(F32) @ Vf).astype(F16)
+        lse[h] = (m[:, 0] + np.log(z[:, 0])).astype(F32)
+    return out, lse

@@ -46,7 +46,7 @@ def test_c_structs_match_header_layout():
     _lib = _ensure_built()
     hdr = open(os.path.join(ROOT, "include", "carekv.h")).read()
     for cname, py in (("carekv_arena", _lib.Arena), ("carekv_store_params", _lib.StoreParams),
-                      ("carekv_decode_params", _lib.DecodeParams)):
+                      ("carekv_decode_params", _lib.DecodeParams), ("carekv_prefill_params", _lib.PrefillParams)):
         assert [f[0] for f in py._fields_] == _struct_fields(hdr, cname), cname
 
 

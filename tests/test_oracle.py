@@ -330,3 +330,60 @@ def test_read_zero_and_kind_v_invariants(golden):
     o_lin = decode_attention(c, 0, g["Q"], kind="v", k_mode="linear")
     o_ex = decode_attention(c, 0, g["Q"], kind="v", k_mode="exact")
     assert np.array_equal(o_lin, o_ex)                      # kind=v: exact == linear
+
+
+# ---- prefill attention (layer.py:935-972)
+
+def _prefill_inputs(Hq, Hkv, T, D, seed):
+    rng = np.random.default_rng(seed)
+    Qh = rng.standard_normal((Hq, T, D)).astype(np.float16)
+    K = rng.standard_normal((Hkv, T, D)).astype(np.float16)
+    V = rng.standard_normal((Hkv, T, D)).astype(np.float16)
+    return Qh, K, V
+
+
+def test_prefill_attention_vs_fp64_bruteforce():
+    """Row-by-row float64 softmax attention (the textbook definition) on a
+    tiny GQA input: the oracle differs only by its fp32 arithmetic and the
+    fp16 cast of the weights and of O."""
+    from oracle.attention import causal_attention_pure
+    Hq, Hkv, T, D = 4, 2, 23, 32
+    Qh, K, V = _prefill_inputs(Hq, Hkv, T, D, 5)
+    O, lse = causal_attention_pure(Qh, K, V)
+    for h in range(Hq):
+        kv = h // (Hq // Hkv)
+        for t in range(T):
+            s = np.array([float(np.dot(Qh[h, t].astype(np.float64), K[kv, j].astype(np.float64))) / math.sqrt(D)
+                          for j in range(t + 1)])
+            w = np.exp(s - s.max())
+            z = w.sum()
+            o = (w / z) @ V[kv, :t + 1].astype(np.float64)
+            np.testing.assert_allclose(O[h, t].astype(np.float64), o, atol=2e-3, rtol=2e-3)
+            assert abs(lse[h, t] - (s.max() + math.log(z))) < 1e-4
+
+
+def test_prefill_attention_causal_and_gqa_properties():
+    from oracle.attention import causal_attention_pure
+    Hq, Hkv, T, D = 4, 2, 40, 64
+    Qh, K, V = _prefill_inputs(Hq, Hkv, T, D, 6)
+    O, _ = causal_attention_pure(Qh, K, V)
+    # the first query sees only token 0
+    for h in range(Hq):
+        assert np.array_equal(O[h, 0], V[h // 2, 0])
+    # tokens after t do not change row t
+    K2, V2 = K.copy(), V.copy()
+    K2[:, 30:] = 7.0
+    V2[:, 30:] = -3.0
+    O2, _ = causal_attention_pure(Qh, K2, V2)
+    assert np.array_equal(O[:, :30], O2[:, :30])
+    # GQA: reading kv head h // 2 in place == repeat_interleave'd K/V
+    Or, _ = causal_attention_pure(Qh, np.repeat(K, 2, axis=0), np.repeat(V, 2, axis=0))
+    assert np.array_equal(O, Or)
+    # row subsets agree with the full computation
+    rows = [0, 17, 39]
+    Os, _ = causal_attention_pure(Qh, K, V, rows=rows)
+    assert np.array_equal(Os, O[:, rows])
+    # without the mask the last row is unchanged and the first sees everything
+    On, _ = causal_attention_pure(Qh, K, V, causal=False)
+    assert np.array_equal(On[:, -1], O[:, -1])
+    assert not np.array_equal(On[:, 0], O[:, 0])
