@@ -42,6 +42,11 @@ CONFIGS = {
 }
 
 
+# BASELINE config 4 (prefill / append path at Llama-2-13B shape); `--config c4`
+PREFILL_CONFIG = dict(B=4, H=40, D=128, T=8192, bits=3, seed=4,
+                      workload="config4 Llama-2-13B prefill B=4 40q/40kv D=128 T=8192")
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -201,12 +206,87 @@ def cpu_baseline(cache, spec, q_np, slices):
     return per_slice * spec["B"] * spec["Hkv"] * 1e6, per_slice
 
 
+def prefill_bench(args):
+    """Config 4: causal prefill attention over dequantised K/V (layer.py:935-972)
+    at B=4, 40 heads, D=128, T=8192, plus the quantize + pack + residual store
+    of the same K/V into pages (timed separately).  One step = one layer's
+    prefill attention for the batch."""
+    os.environ.update(PAPER_ENV)
+    import torch
+    import care_kv
+    c = PREFILL_CONFIG
+    B, H, D, T = c["B"], c["H"], c["D"], c["T"]
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    g = torch.Generator(device=dev).manual_seed(c["seed"])
+    q = torch.randn(B, H, T, D, generator=g, device=dev).half()
+    # K, V ~ N(0,1) with per-channel log-normal scales (sigma 1)
+    kx = (torch.randn(B, H, T, D, generator=g, device=dev) *
+          torch.exp(torch.randn(B, H, 1, D, generator=g, device=dev))).half()
+    vx = (torch.randn(B, H, T, D, generator=g, device=dev) *
+          torch.exp(torch.randn(B, H, 1, D, generator=g, device=dev))).half()
+    # store path: quantize + pack + residual candidates/slots into the paged cache
+    P = math.ceil(T / 16)
+    cfg = care_kv.CacheConfig(num_layers=1, num_heads=H, num_kv_heads=H, head_dim=D, page_size=16,
+                              max_pages=P + 4, base_bits=c["bits"], group_size=32, k_channel_group=32,
+                              v_token_block=4, sketch_dim=32, packed_base=True, scale_quant="int8",
+                              store_budget_mode="ratio", store_budget_ratio=0.03, read_budget_ratio=0.0)
+    cache = care_kv.CAREKVCache(cfg, device=dev, n_seq=B)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    cache.write_prefill(0, kx[0], vx[0], seqs=[0])  # warm-up (allocations, library load)
+    torch.cuda.synchronize()
+    cache = care_kv.CAREKVCache(cfg, device=dev, n_seq=B)
+    torch.cuda.synchronize()
+    e0.record()
+    for b in range(B):
+        cache.write_prefill(0, kx[b], vx[b], seqs=[b])
+    e1.record()
+    e1.synchronize()
+    store_ms = e0.elapsed_time(e1)
+    # K_hat, V_hat of the prefill path (fp16 group scales)
+    kh = care_kv.quant_dequant(kx, c["bits"])
+    vh = care_kv.quant_dequant(vx, c["bits"])
+    del kx, vx
+    out = torch.empty_like(q)
+    for _ in range(args.warmup):
+        care_kv.prefill_attention(q, kh, vh, out=out)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev0.record(stream)
+    for _ in range(args.steps):
+        care_kv.prefill_attention(q, kh, vh, out=out)
+    ev1.record(stream)
+    ev1.synchronize()
+    ms = ev0.elapsed_time(ev1) / args.steps
+    flops = 4.0 * B * H * D * (T * (T + 1) / 2)  # QK^T and PV over the causal triangle
+    tflops = flops / (ms * 1e-3) / 1e12
+    store_bytes = 2 * B * H * T * D * 2  # fp16 K and V read once by the store path
+    log(f"[bench] c4 prefill attention {ms * 1e3:.1f} us/step, {flops / 1e12:.3f} TFLOP -> {tflops:.1f} TFLOP/s "
+        f"({tflops / 2500 * 100:.1f}% of 2.5 PF fp16 dense); store path {store_ms:.1f} ms for {B} sequences")
+    line = {
+        "metric": "CARE-KV prefill attention over dequantised K/V, TFLOP/s (Llama-2-13B shape, 8K prompt)",
+        "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp16 MFMA (fp32 accumulate, fp32 softmax)", "data": "synthetic",
+        "config": {"workload": c["workload"], "global_batch": B, "seq_len": T, "parallelism": "single-gpu",
+                   "base": f"uniform INT{c['bits']} g=32 (K_hat/V_hat with fp16 group scales)", "causal": True},
+        "roofline": {"bound": "mfma", "kernel": f"prefill_attn_kernel<{D}>", "achieved": round(tflops, 2),
+                     "peak": 2500.0, "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4), "traffic": None,
+                     "algorithmic_flops_per_launch": flops, "launch_us": round(ms * 1e3, 2)},
+        "store_path": {"ms": round(store_ms, 3), "fp16_bytes_in": store_bytes,
+                       "gbps_in": round(store_bytes / (store_ms * 1e-3) / 1e9, 1)},
+        "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS))
+    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS) + ["c4"])
     ap.add_argument("--cpu-slices", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--split-pages", type=int, default=None)
@@ -221,6 +301,9 @@ def main():
         sys.exit(2)
     if args.copy_mib > 0:
         copy_calibration(args.copy_mib, args.steps)
+        return
+    if args.config == "c4":
+        prefill_bench(args)
         return
     os.environ.update(PAPER_ENV)
     import numpy as np
