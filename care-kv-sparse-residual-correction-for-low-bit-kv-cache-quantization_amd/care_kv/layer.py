@@ -1,0 +1,174 @@
+"""``CAREKVLayer``: the per-layer prefill / decode driver (layer.py:147-1163 of
+the reference), batched over sequences, with every CARE-KV computation in
+the HIP library:
+
+* projections and RoPE stay torch matmuls / elementwise ops on the caller's
+  device (the reference does the same, layer.py:665-690, 996-1014);
+* the page store (quantize, pack, residual candidates, slots) is
+  ``CAREKVCache.write_prefill`` (``carekv_store_pages``);
+* the decode append with store-on-fill is ``CAREKVCache.append``
+  (``carekv_append_rows``);
+* prefill attention is ``prefill_attention`` over (K_post, V) in the ``fp``
+  mode or over the fp16-scale K_hat / V_hat in the quantised modes
+  (``carekv_prefill_attn``, layer.py:759-781);
+* decode attention with the comb+ex correction is ``decode_attention``
+  (``carekv_decode_attn``, layer.py:1148-1160).
+"""
+from __future__ import annotations
+
+import os
+import warnings
+from typing import Any, Dict, Optional, Sequence, Tuple
+
+import torch
+from torch import Tensor, nn
+
+from .attention import decode_attention
+from .cache import CAREKVCache
+from .config import CacheConfig
+from .prefill import prefill_attention, quant_dequant
+
+try:  # the reference takes RoPE from transformers as well (layer.py:65-69)
+    from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
+except Exception:  # pragma: no cover - transformers missing
+    apply_rotary_pos_emb = None
+
+F16 = torch.float16
+PREFILL_MODES = ("fp", "base_quant", "carekv_eval", "carekv_stored")
+_warned = set()
+
+
+def resolve_prefill_mode() -> str:
+    """``_resolve_prefill_mode`` (layer.py:129-140)."""
+    raw = os.environ.get("CAREKV_PREFILL_MODE", "fp").lower()
+    if raw == "carekv":
+        return "carekv_eval"
+    if raw in {"quant", "int"}:
+        return "base_quant"
+    if raw not in PREFILL_MODES:
+        raise ValueError(f"CAREKV_PREFILL_MODE={raw!r} is not one of {PREFILL_MODES}")
+    return raw
+
+
+def _rope(q: Tensor, k: Tensor, cos: Tensor, sin: Tensor) -> Tuple[Tensor, Tensor]:
+    """q (B, Hq, T, D), k (B, Hkv, T, D); cos/sin (B or 1, T, rot)."""
+    if apply_rotary_pos_emb is not None:
+        return apply_rotary_pos_emb(q, k, cos, sin)
+    c, s = cos.unsqueeze(1), sin.unsqueeze(1)
+
+    def rot(x):
+        h = x.shape[-1] // 2
+        return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
+    return q * c + rot(q) * s, k * c + rot(k) * s
+
+
+class CAREKVLayer(nn.Module):
+    """Drop-in attention layer over the CARE-KV cache (layer.py:147-183)."""
+
+    def __init__(self, cfg: CacheConfig, layer_id: int, W_Q: Tensor, W_K: Tensor, W_V: Tensor, W_O: Tensor,
+                 device: Optional[torch.device] = None):
+        super().__init__()
+        self.cfg = cfg
+        self.layer_id = layer_id
+        self.device = torch.device(device) if device is not None else W_Q.device
+        self.W_Q = nn.Parameter(W_Q, requires_grad=False)
+        self.W_K = nn.Parameter(W_K, requires_grad=False)
+        self.W_V = nn.Parameter(W_V, requires_grad=False)
+        self.W_O = nn.Parameter(W_O, requires_grad=False)
+
+    # ------------------------------------------------------------ helpers
+    def _project(self, hidden: Tensor):
+        """hidden (B, T, model_dim) -> Q (B, Hq, T, D), K/V (B, Hkv, T, D)."""
+        cfg = self.cfg
+        B, T, _ = hidden.shape
+        Hq, Hkv, D = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim
+        Q = (hidden @ self.W_Q.T).reshape(B, T, Hq, D).transpose(1, 2)
+        K = (hidden @ self.W_K.T).reshape(B, T, Hkv, D).transpose(1, 2)
+        V = (hidden @ self.W_V.T).reshape(B, T, Hkv, D).transpose(1, 2)
+        return Q, K, V
+
+    def _out(self, O: Tensor, dtype) -> Tensor:
+        """O (B, Hq, T, D) -> (B, T, model_dim) through W_O."""
+        B, Hq, T, D = O.shape
+        return O.transpose(1, 2).reshape(B, T, Hq * D).to(self.W_O.dtype) @ self.W_O.T
+
+    @staticmethod
+    def _check_mask(attention_mask: Optional[Tensor], T: int):
+        """The kernel applies the causal mask itself (the attention_mask=None
+        branch of layer.py:951-962).  An additive mask that masks more than
+        the causal triangle (padding) is refused rather than ignored."""
+        if attention_mask is None or not torch.is_tensor(attention_mask) or attention_mask.dtype == torch.bool:
+            if torch.is_tensor(attention_mask) and attention_mask.dtype == torch.bool:
+                last = attention_mask.reshape(-1, attention_mask.shape[-1])[-1]
+                if not bool(last.all()):
+                    raise NotImplementedError("padded attention masks are not supported by the prefill kernel")
+            return
+        last = attention_mask.reshape(-1, attention_mask.shape[-2], attention_mask.shape[-1])[:, -1, -T:]
+        if bool((last < 0).any()):
+            raise NotImplementedError("padded attention masks are not supported by the prefill kernel")
+
+    # ------------------------------------------------------------ prefill
+    def prefill(self, cache: CAREKVCache, hidden: Tensor, sink_tokens: int = 4,
+                attention_mask: Optional[Tensor] = None,
+                position_embeddings: Optional[Tuple[Tensor, Tensor]] = None, token_start_abs: int = 0,
+                debug_stats: Optional[Dict[str, Any]] = None, seqs: Optional[Sequence[int]] = None) -> Tensor:
+        """layer.py:643-935 for a batch: hidden (T, model_dim) or (B, T,
+        model_dim) -> the attention output through W_O, same leading shape.
+
+        Every mode writes the pages (post-RoPE K, layer.py:719-737).  The
+        output is attention over (K_post, V) in ``fp`` mode and over the
+        dequantised K_hat / V_hat otherwise.  The prefill-time sparse
+        correction of ``carekv_eval`` / ``carekv_stored`` is not built: those
+        modes return the base attention and warn once."""
+        squeeze = hidden.dim() == 2
+        if squeeze:
+            hidden = hidden.unsqueeze(0)
+        cfg = self.cfg
+        B, T, _ = hidden.shape
+        mode = resolve_prefill_mode()
+        self._check_mask(attention_mask, T)
+        Q, K, V = self._project(hidden)
+        if position_embeddings is not None:
+            cos, sin = position_embeddings
+            Q, K = _rope(Q, K, cos.to(Q.dtype), sin.to(Q.dtype))
+        Qh, Kh, Vh = Q.to(F16).contiguous(), K.to(F16).contiguous(), V.to(F16).contiguous()
+        seqs = list(range(B)) if seqs is None else list(seqs)
+        cache.write_prefill(self.layer_id, Kh, Vh, token_start_abs=token_start_abs, sink_tokens=sink_tokens,
+                            seqs=seqs)
+        if mode == "fp":
+            O = prefill_attention(Qh, Kh, Vh)
+        else:
+            if mode in ("carekv_eval", "carekv_stored") and mode not in _warned:
+                _warned.add(mode)
+                warnings.warn(f"CAREKV_PREFILL_MODE={mode}: the prefill-time sparse correction is not built; "
+                              "the prefill output is the base attention over K_hat / V_hat (decode-time "
+                              "correction is unaffected)", RuntimeWarning, stacklevel=2)
+            O = prefill_attention(Qh, quant_dequant(Kh, cfg.base_bits, cfg.group_size),
+                                  quant_dequant(Vh, cfg.base_bits, cfg.group_size))
+        out = self._out(O, hidden.dtype).to(hidden.dtype)
+        return out[0] if squeeze else out
+
+    # ------------------------------------------------------------ decode
+    def decode_step(self, cache: CAREKVCache, hidden: Tensor,
+                    position_embeddings: Optional[Tuple[Tensor, Tensor]] = None,
+                    debug_stats: Optional[Dict[str, Any]] = None, seqs: Optional[Sequence[int]] = None) -> Tensor:
+        """layer.py:978-1163 for a batch: hidden (1, model_dim) of one
+        sequence or (B, 1, model_dim) -> same shape.  Appends the token's
+        K / V (store on page fill with K_orig = K_hat, layer.py:1088-1146),
+        then runs the decode attention, with the comb+ex correction when a
+        read budget ratio is set."""
+        squeeze = hidden.dim() == 2
+        if squeeze:
+            hidden = hidden.unsqueeze(0)
+        B = hidden.shape[0]
+        Q, K, V = self._project(hidden[:, -1:])
+        if position_embeddings is not None:
+            cos, sin = position_embeddings
+            Q, K = _rope(Q, K, cos.to(Q.dtype), sin.to(Q.dtype))
+        seqs = list(range(B)) if seqs is None else list(seqs)
+        cache.append(self.layer_id, K[:, :, 0].to(F16), V[:, :, 0].to(F16), seqs=seqs)
+        # the reference corrects only when read_budget_ratio > 0 (attention.py:1025)
+        O = decode_attention(cache, self.layer_id, Q[:, :, 0].to(F16), seqs=seqs,
+                             correction=self.cfg.read_budget_ratio > 0)  # (B, Hq, D)
+        out = self._out(O.unsqueeze(2), hidden.dtype).to(hidden.dtype)  # (B, 1, model_dim)
+        return out[0] if squeeze else out

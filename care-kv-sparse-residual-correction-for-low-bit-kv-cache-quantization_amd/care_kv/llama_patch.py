@@ -1,0 +1,174 @@
+"""HuggingFace LLaMA monkey-patch (llama_patch.py of the reference).
+
+``patch_llama_model(model, care_cfg)`` swaps every attention module that has
+a ``q_proj`` for a ``CAREKVLlamaAttention`` running ``CAREKVLayer`` prefill
+and decode over one shared ``CAREKVCache`` (all layers, one slot per batch
+row).  Differences from the reference, all at the boundary:
+
+* a batch of B > 1 rows runs as one batched kernel call per layer instead of
+  a Python loop over per-sequence caches (llama_patch.py:229-258), and a new
+  prefill resets the batch's pages for every B (the reference never resets
+  for B > 1, its quirk (vi));
+* the forward accepts both the transformers 4.x keyword ``past_key_value``
+  and the 5.x ``past_key_values``, and returns ``(attn_output, None)`` on
+  5.x (``LlamaDecoderLayer`` unpacks two values) and the reference's
+  3-tuple on 4.x.
+"""
+from __future__ import annotations
+
+import os
+from typing import Dict, Optional
+
+import torch
+from torch import nn
+
+from .cache import CAREKVCache
+from .config import CacheConfig
+from .layer import CAREKVLayer
+
+try:
+    import transformers
+    _HF_MAJOR = int(transformers.__version__.split(".")[0])
+except Exception:  # pragma: no cover
+    _HF_MAJOR = 5
+
+
+class _SharedState:
+    """One cache for all patched layers of a model and the per-row prefill
+    flags of each layer (llama_patch.py:84-101, 321-348)."""
+
+    def __init__(self):
+        self.cache: Optional[CAREKVCache] = None
+        self.prefilled: Dict[int, set] = {}
+
+
+class CAREKVLlamaAttention(nn.Module):
+    """Wraps a HF ``LlamaAttention`` (llama_patch.py:41-288)."""
+
+    def __init__(self, original_attn: nn.Module, cfg: CacheConfig, layer_id: int, device: torch.device,
+                 shared: Optional[_SharedState] = None):
+        super().__init__()
+        self.cfg = cfg
+        self.layer_id = layer_id
+        self.device = torch.device(device)
+        self.original_attn = original_attn
+        self.care_layer = CAREKVLayer(cfg, layer_id, original_attn.q_proj.weight.data,
+                                      original_attn.k_proj.weight.data, original_attn.v_proj.weight.data,
+                                      original_attn.o_proj.weight.data, device=self.device)
+        self._shared = shared if shared is not None else _SharedState()
+
+    # ------------------------------------------------------------ cache
+    def _cache_for(self, batch: int, device) -> CAREKVCache:
+        st = self._shared
+        if st.cache is None or st.cache.n_seq < batch or st.cache.device != torch.device(device):
+            st.cache = CAREKVCache(self.cfg, device=device, n_seq=batch)
+            st.prefilled.clear()
+        return st.cache
+
+    def reset_cache(self, seq_id: Optional[int] = None):
+        """llama_patch.py:103-110: forget every row (or one)."""
+        st = self._shared
+        if st.cache is None:
+            return
+        if seq_id is None:
+            for s in range(st.cache.n_seq):
+                st.cache.reset_sequence(s)
+            st.prefilled.clear()
+        else:
+            st.cache.reset_sequence(seq_id)
+            for flags in st.prefilled.values():
+                flags.discard(seq_id)
+
+    def _flags(self) -> set:
+        return self._shared.prefilled.setdefault(self.layer_id, set())
+
+    # ------------------------------------------------------------ forward
+    def forward(self, hidden_states, attention_mask=None, position_ids=None, past_key_value=None,
+                output_attentions=False, use_cache=False, cache_position=None, past_key_values=None, **kwargs):
+        """llama_patch.py:112-288."""
+        pkv = past_key_values if past_key_values is not None else past_key_value
+        return_mode = os.environ.get("CAREKV_RETURN", "care").lower()
+        position_embeddings = kwargs.get("position_embeddings", None)
+        if return_mode in {"original", "passthrough", "hf"} or position_embeddings is None:
+            # the reference falls back to HF attention without RoPE inputs
+            call = dict(attention_mask=attention_mask, position_ids=position_ids, **kwargs)
+            if _HF_MAJOR >= 5:
+                call["past_key_values"] = pkv
+            else:
+                call.update(past_key_value=pkv, output_attentions=output_attentions, use_cache=use_cache)
+            if cache_position is not None:
+                call["cache_position"] = cache_position
+            return self.original_attn(hidden_states, **call)
+
+        B, T, _ = hidden_states.shape
+        seqs = list(range(B))
+        hf_len = 0
+        if use_cache and pkv is not None:
+            try:
+                hf_len = pkv.get_seq_length(self.layer_id)
+            except Exception:
+                try:
+                    hf_len = pkv.get_seq_length()
+                except Exception:
+                    hf_len = 0
+        cache = self._cache_for(B, hidden_states.device)
+        flags = self._flags()
+        # a new prompt: several tokens, or one token HF has no cache for
+        # (llama_patch.py:177-199); layer 0 clears the rows for every layer
+        new_prompt = T > 1 or (use_cache and hf_len == 0 and not all(s in flags for s in seqs))
+        if new_prompt:
+            if self.layer_id == 0:
+                self.reset_cache()
+                flags = self._flags()
+            flags.difference_update(seqs)
+        if not all(s in flags for s in seqs):
+            out = self.care_layer.prefill(cache, hidden_states, attention_mask=attention_mask,
+                                          position_embeddings=position_embeddings, seqs=seqs)
+            flags.update(seqs)
+        else:
+            out = self.care_layer.decode_step(cache, hidden_states, position_embeddings=position_embeddings,
+                                              seqs=seqs)
+
+        # keep HF's own cache length in step so that it sends one token per
+        # decode call (llama_patch.py:262-285)
+        if use_cache and pkv is not None and hasattr(pkv, "update"):
+            try:
+                z = hidden_states.new_zeros((B, self.cfg.num_kv_heads, T, self.cfg.head_dim))
+                pkv.update(z, z, self.layer_id)
+            except Exception:
+                pass
+        if _HF_MAJOR >= 5:
+            return out, None
+        return out, None, pkv
+
+
+def patch_llama_model(model: nn.Module, care_cfg: CacheConfig, device: Optional[torch.device] = None) -> nn.Module:
+    """llama_patch.py:292-352: replace every ``*Attention`` module with a
+    ``q_proj`` by ``CAREKVLlamaAttention`` (layer id = first integer in the
+    module path); all of them share one cache."""
+    if device is None:
+        try:
+            device = next(model.parameters()).device
+        except StopIteration:
+            device = torch.device("cuda", torch.cuda.current_device())
+    shared = _SharedState()
+    targets = []
+    for name, module in model.named_modules():
+        if "Attention" in type(module).__name__ and hasattr(module, "q_proj"):
+            targets.append((name, module))
+    for name, module in targets:
+        parts = name.split(".")
+        parent = model
+        for part in parts[:-1]:
+            parent = getattr(parent, part)
+        layer_id = next((int(p) for p in parts if p.isdigit()), 0)
+        setattr(parent, parts[-1], CAREKVLlamaAttention(module, care_cfg, layer_id, device, shared=shared))
+    print(f"[CARE-KV] Replaced {len(targets)} attention layers with CARE-KV.")
+    return model
+
+
+def reset_all_caches(model: nn.Module):
+    """llama_patch.py:355-359."""
+    for module in model.modules():
+        if isinstance(module, CAREKVLlamaAttention):
+            module.reset_cache()

@@ -1,0 +1,166 @@
+"""The reference's Python boundary over the HIP library (needs a GPU):
+``CAREKVLayer`` prefill / decode_step (layer.py:643-1163),
+``patch_llama_model`` on a transformers LlamaForCausalLM
+(llama_patch.py:112-359) and ``CAREKVAdapter`` (baselines/carekv_adapter.py).
+
+Bars: the layer's prefill output matches the oracle's
+``causal_attention_pure`` over the oracle's K_hat / V_hat followed by W_O
+(fp32 on the CPU) within 2e-2 relative to the output scale (the projections
+run in fp16 on the device); the cache the layer writes is byte-identical to
+``write_prefill`` of the same K / V; the patched model's fp-mode logits
+match the unpatched HF model's within 2e-2 of their scale.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import quant as Q
+from oracle.attention import causal_attention_pure
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True)
+def _need_gpu():
+    if not torch.cuda.is_available():
+        pytest.skip("needs a HIP device")
+
+
+def _cfg(L=1, Hq=8, Hkv=2, D=64, P=32, **kw):
+    import care_kv
+    base = dict(num_layers=L, num_heads=Hq, num_kv_heads=Hkv, head_dim=D, page_size=16, max_pages=P, base_bits=3,
+                group_size=32, k_channel_group=32, v_token_block=4, sketch_dim=32, packed_base=True,
+                scale_quant="int8", store_budget_mode="ratio", store_budget_ratio=0.03, read_budget_ratio=0.0)
+    base.update(kw)
+    return care_kv.CacheConfig(**base)
+
+
+def _layer(cfg, model_dim, seed):
+    import care_kv
+    g = torch.Generator().manual_seed(seed)
+    Hq, Hkv, D = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim
+    mk = lambda o, i: (torch.randn(o, i, generator=g) / math.sqrt(i)).half().cuda()  # noqa: E731
+    return care_kv.CAREKVLayer(cfg, 0, mk(Hq * D, model_dim), mk(Hkv * D, model_dim), mk(Hkv * D, model_dim),
+                               mk(model_dim, Hq * D))
+
+
+@pytest.mark.parametrize("mode", ["fp", "base_quant"])
+def test_layer_prefill_matches_oracle(monkeypatch, mode):
+    import care_kv
+    monkeypatch.setenv("CAREKV_PREFILL_MODE", mode)
+    print(f"layer prefill mode={mode}", flush=True)
+    cfg = _cfg()
+    T, model_dim = 70, 256
+    lay = _layer(cfg, model_dim, 3)
+    hidden = (torch.randn(T, model_dim, generator=torch.Generator().manual_seed(4))).half().cuda()
+    cache = care_kv.CAREKVCache(cfg, n_seq=1)
+    out = lay.prefill(cache, hidden).float().cpu().numpy()
+    # the oracle side: the same projections (same shapes as the layer's),
+    # then layer.py:759-781 on the CPU
+    Qt, Kt, Vt = lay._project(hidden.unsqueeze(0))
+    Qd, Kd, Vd = Qt[0].cpu().numpy(), Kt[0].cpu().numpy(), Vt[0].cpu().numpy()
+    Kraw, Vraw = Kt.contiguous(), Vt.contiguous()
+    if mode == "base_quant":
+        Kd = Q.dequantize(*Q.quantize(Kd, 3, 32), 32)
+        Vd = Q.dequantize(*Q.quantize(Vd, 3, 32), 32)
+    O, _ = causal_attention_pure(Qd, Kd, Vd)
+    ref = O.transpose(1, 0, 2).reshape(T, -1).astype(np.float32) @ lay.W_O.float().cpu().numpy().T
+    scale = float(np.abs(ref).max())
+    assert np.abs(out - ref).max() <= 2e-2 * scale
+    # the pages are those of write_prefill on the same post-RoPE K / V
+    ref_cache = care_kv.CAREKVCache(cfg, n_seq=1)
+    ref_cache.write_prefill(0, Kraw, Vraw, seqs=[0])
+    for nm in ("kcodes", "vcodes", "kscale", "vscale", "kmaster", "vmaster", "valid", "k_slot", "v_slot"):
+        assert torch.equal(getattr(cache, nm), getattr(ref_cache, nm)), nm
+
+
+def test_layer_decode_steps_match_direct_calls(monkeypatch):
+    """decode_step = append + decode_attention + W_O on the same cache."""
+    import care_kv
+    monkeypatch.setenv("CAREKV_PREFILL_MODE", "base_quant")
+    print("layer decode steps", flush=True)
+    cfg = _cfg()
+    T, model_dim = 45, 256
+    lay = _layer(cfg, model_dim, 5)
+    g = torch.Generator().manual_seed(6)
+    hidden = torch.randn(T + 3, model_dim, generator=g).half().cuda()
+    cache = care_kv.CAREKVCache(cfg, n_seq=1)
+    twin = care_kv.CAREKVCache(cfg, n_seq=1)
+    lay.prefill(cache, hidden[:T])
+    lay.prefill(twin, hidden[:T])
+    for t in range(T, T + 3):
+        out = lay.decode_step(cache, hidden[t:t + 1])
+        Qt, Kt, Vt = lay._project(hidden[t:t + 1].unsqueeze(0))
+        twin.append(0, Kt[:, :, 0], Vt[:, :, 0])
+        o = care_kv.decode_attention(twin, 0, Qt[:, :, 0], correction=False)
+        ref = lay._out(o.unsqueeze(2), o.dtype)[0]
+        torch.testing.assert_close(out, ref, rtol=2e-3, atol=2e-3)
+    assert cache.total_valid_tokens(0, 0) == T + 3
+
+
+def _tiny_llama(seed=0):
+    from transformers import LlamaConfig, LlamaForCausalLM
+    torch.manual_seed(seed)
+    c = LlamaConfig(hidden_size=256, intermediate_size=512, num_hidden_layers=2, num_attention_heads=4,
+                    num_key_value_heads=2, vocab_size=1000, max_position_embeddings=1024)
+    c._attn_implementation = "eager"
+    return LlamaForCausalLM(c).half().cuda().eval()
+
+
+def test_patched_llama_prefill_matches_hf(monkeypatch):
+    import care_kv
+    monkeypatch.setenv("CAREKV_PREFILL_MODE", "fp")
+    print("patched llama prefill", flush=True)
+    ids = torch.randint(0, 1000, (1, 48), generator=torch.Generator().manual_seed(1)).cuda()
+    m = _tiny_llama()
+    with torch.no_grad():
+        ref = m(ids, use_cache=False).logits.float()
+    cfg = _cfg(L=2, Hq=4, Hkv=2, D=64, P=16)
+    care_kv.patch_llama_model(m, cfg)
+    with torch.no_grad():
+        got = m(ids, use_cache=False).logits.float()
+    assert torch.isfinite(got).all()
+    scale = float(ref.abs().max())
+    assert float((got - ref).abs().max()) <= 2e-2 * scale
+
+
+def test_patched_llama_generates_with_cache(monkeypatch):
+    """greedy generate with use_cache=True: one prefill, then one decode
+    step per new token through the CARE-KV cache (HF's cache length kept in
+    step with zeros)."""
+    import care_kv
+    monkeypatch.setenv("CAREKV_PREFILL_MODE", "base_quant")
+    print("patched llama generate", flush=True)
+    ids = torch.randint(0, 1000, (1, 37), generator=torch.Generator().manual_seed(2)).cuda()
+    m = _tiny_llama(1)
+    cfg = _cfg(L=2, Hq=4, Hkv=2, D=64, P=16)
+    care_kv.patch_llama_model(m, cfg)
+    with torch.no_grad():
+        out = m.generate(ids, max_new_tokens=5, do_sample=False, use_cache=True)
+    assert out.shape == (1, 42)
+    attn = [mod for mod in m.modules() if isinstance(mod, care_kv.CAREKVLlamaAttention)]
+    cache = attn[0]._shared.cache
+    for layer in range(2):
+        assert cache.total_valid_tokens(layer, 0) == 41  # prompt + 4 decode appends
+    care_kv.reset_all_caches(m)
+    assert cache.total_valid_tokens(0, 0) == 0
+
+
+def test_adapter_patches_a_given_model(monkeypatch):
+    import care_kv
+    import care_kv.layer
+    print("adapter", flush=True)
+    a = care_kv.CAREKVAdapter(sk=1, sv=1, rk=2, rv=2)
+    for k, v in a.env().items():  # restored after the test
+        monkeypatch.setenv(k, v)
+    care_kv.layer._warned.clear()
+    m = a.setup_model(_tiny_llama(2))
+    ids = torch.randint(0, 1000, (1, 20), generator=torch.Generator().manual_seed(3)).cuda()
+    with pytest.warns(RuntimeWarning):
+        with torch.no_grad():
+            logits = m(ids).logits
+    assert torch.isfinite(logits.float()).all()
+    st = a.collect_debug_stats()
+    assert st["stored_k_slots"] > 0 and st["stored_v_slots"] > 0

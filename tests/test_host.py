@@ -133,3 +133,33 @@ def test_bench_rejects_multi_gpu():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
                        text=True, timeout=120)
     assert r.returncode != 0 and "one GPU" in r.stderr
+
+
+def test_adapter_interface_and_limits():
+    """CAREKVAdapter keeps the reference constructor and reporting surface
+    (baselines/carekv_adapter.py:23-263); unbuilt options raise."""
+    from care_kv import CAREKVAdapter
+    a = CAREKVAdapter(sk=2, sv=4, rk=2, rv=2, bits=3)
+    assert a.name == "CAREKV_fixed_SK2SV4_RK2RV2"
+    env = a.env()
+    assert env["CAREKV_PREFILL_MODE"] == "carekv_stored" and env["CAREKV_STORE_ABS_V"] == "4"
+    m = a.estimate_memory(2048, num_layers=22, hkv=4, head_dim=64)
+    fp16 = 22 * 2 * 2048 * 4 * 64 * 2 / 2**20
+    assert abs(m["base_memory_MB"] - round(fp16 * 3 / 16, 4)) < 1e-3
+    assert a.effective_budgets()["effective_read_budget"] == "fixed RK=2 RV=2"
+    with pytest.raises(NotImplementedError):
+        CAREKVAdapter(base_quantizer="kivi_style")
+    with pytest.raises(NotImplementedError):
+        CAREKVAdapter(mode="adaptive")
+
+
+def test_prefill_mode_resolution(monkeypatch):
+    """_resolve_prefill_mode (layer.py:129-140)."""
+    from care_kv.layer import resolve_prefill_mode
+    for raw, want in (("fp", "fp"), ("quant", "base_quant"), ("int", "base_quant"), ("carekv", "carekv_eval"),
+                      ("carekv_stored", "carekv_stored")):
+        monkeypatch.setenv("CAREKV_PREFILL_MODE", raw)
+        assert resolve_prefill_mode() == want
+    monkeypatch.setenv("CAREKV_PREFILL_MODE", "bogus")
+    with pytest.raises(ValueError):
+        resolve_prefill_mode()
