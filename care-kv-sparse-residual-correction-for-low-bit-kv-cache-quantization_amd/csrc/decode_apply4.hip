@@ -327,7 +327,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     den += (ck[0] + ck[1]) + (ck[2] + ck[3]);
     const half2_t ck01 = {(_Float16)ck[0], (_Float16)ck[1]}, ck23 = {(_Float16)ck[2], (_Float16)ck[3]};
     const half2_t cv01 = {(_Float16)cv[0], (_Float16)cv[1]}, cv23 = {(_Float16)cv[2], (_Float16)cv[3]};
-    pw_store(s_pk[w], h2bits(ck01), h2bits(ck23), lane);
+    pw_store_strided(s_pk[w], h2bits(ck01), h2bits(ck23), lane);
     pw_store(s_pv[w], h2bits(cv01), h2bits(cv23), lane);
 
     // ---- num += ck V_hat, page by page
@@ -345,24 +345,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
       dequant_pairs<BITS, CH, BITS>(vc0.vw[pi], vs, vp);
       vtile_write<D, BITS>(vt, vp, ln, lj);
       lds_sync_wave();
-      uint2 pg[4];  // ck[query sc][tokens 4g..4g+3] of page pi
+      uint2 pg[4];  // ck[query sc][tokens g, g+4, g+8, g+12] of page pi
       pw_load(s_pk[w], pi, sc, pg);
 #pragma unroll
-      for (int g = 0; g < 4; ++g) pv4_group<D, BITS>(vt, 4 * g, pg[g].x, pg[g].y, nacc, lane);
+      for (int g = 0; g < 4; ++g) pv4_group<D, BITS>(vt, g, pg[g].x, pg[g].y, nacc, lane);
       lds_sync_wave();
     }
 
     vc0 = load_vcodes(plan0);
 
     // ---- num += cv R_V: the window's selected V blocks, 4 per tile (block
-    // u of a round fills tile rows 4u..4u+3); round 0 was prefetched
+    // u of a round fills tile rows u, u+4, u+8, u+12); round 0 was prefetched
     for (int r0 = 0; r0 < cp.nblk; r0 += 4) {
       const VRes rv = r0 == 0 ? vr0 : load_vres(par, r0, cp.nblk);
       if (r0 + lj < cp.nblk) {
         const int m = ln >> 2, c = ln & 3;
         half2_t rp[CH / 2];
         dequant_pairs<4, CH, BITS>(rv.w, (_Float16)rv.scale, rp);
-        vtile_write<D, BITS>(vt, rp, 4 * lj + m, c);
+        vtile_write<D, BITS>(vt, rp, lj + 4 * m, c);
       }
       lds_sync_wave();
       // block r0 + u: cv[query sc][its 4 tokens] from S lane 16*pi_u + 4*vb_u + sc
@@ -371,7 +371,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         if (r0 + u >= cp.nblk) break;
         const int bu = s_blk[w][par][r0 + u] & 15;
         const uint2 pu = s_pv[w][((bu >> 2) * 4 + sc) * 4 + (bu & 3)];
-        pv4_group<D, BITS>(vt, 4 * u, pu.x, pu.y, nacc, lane);
+        pv4_group<D, BITS>(vt, u, pu.x, pu.y, nacc, lane);
       }
       lds_sync_wave();
     }

@@ -582,17 +582,20 @@ __device__ __forceinline__ int meta_field_any(const carekv_arena& A, long pg_bas
 }
 
 // ---------------------------------------------------------------- 4x4x4 PV
-// O[q][slot] += sum_t P[q][t] V_tile[t][slot] for the 4 tokens of tile rows
-// row0 .. row0+3, on v_mfma_f32_4x4x4_16b_f16 with A = V^T (block b = slots
-// 4b..4b+3 of a 64-slot half) and B = P (4 query heads):
+// O[q][slot] += sum_m P[q][g + 4m] V_tile[g + 4m][slot], m = 0..3 (token
+// group g of a 16-row tile: rows g, g+4, g+8, g+12), on
+// v_mfma_f32_4x4x4_16b_f16 with A = V^T (block b = slots 4b..4b+3 of a
+// 64-slot half) and B = P (4 query heads):
 //   * the A operand comes from the token-major tile through the transpose
-//     load: source lane s of 16-lane group G reads row row0 + s/4, slots
+//     load: source lane s of 16-lane group G reads row g + 4(s/4), slots
 //     16G + 4(s%4) .. +3, and lane r of the group receives slots 16G + r of
-//     rows row0 .. row0+3;
-//   * p01/p23 hold P[query lane % 4][the 4 tokens] as fp16 pairs.
+//     rows g, g+4, g+8, g+12.  With the row stride of D/2 + 4 words, the 4
+//     rows 4 apart sit 16 banks apart, so each half-wave's 32 reads hit 64
+//     distinct banks (rows 1 apart would overlap);
+//   * p01/p23 hold P[query lane % 4][tokens g, g+4, g+8, g+12] as fp16 pairs.
 // Lane l accumulates O[query l % 4][slots 64h + 4(l/4) .. +3] in acc[h].
 template <int D, int BITS>
-__device__ __forceinline__ void pv4_group(const uint32_t* vt, int row0, uint32_t p01, uint32_t p23, float4_t* acc,
+__device__ __forceinline__ void pv4_group(const uint32_t* vt, int g, uint32_t p01, uint32_t p23, float4_t* acc,
                                           int lane) {
   using G = PageGeom<D, BITS>;
   typedef short short4_t __attribute__((ext_vector_type(4)));
@@ -602,7 +605,7 @@ __device__ __forceinline__ void pv4_group(const uint32_t* vt, int row0, uint32_t
   __builtin_memcpy(reinterpret_cast<char*>(&bq) + 4, &p23, 4);
   const int s = lane & 15, g16 = lane >> 4;
   const __attribute__((address_space(3))) char* base = (const __attribute__((address_space(3))) char*)vt +
-                                                       ((row0 + (s >> 2)) * G::VROW) * 4 + (16 * g16 + 4 * (s & 3)) * 2;
+                                                       ((g + 4 * (s >> 2)) * G::VROW) * 4 + (16 * g16 + 4 * (s & 3)) * 2;
 #pragma unroll
   for (int h = 0; h < D / 64; ++h) {
     const short4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(base + 128 * h));
@@ -612,12 +615,24 @@ __device__ __forceinline__ void pv4_group(const uint32_t* vt, int row0, uint32_t
   }
 }
 
-// Weights of a 4-page window for the 4x4x4 PV, staged per wave in LDS: the
-// S-layout lane 16*pi + 4*g + q (page pi, tokens 4g..4g+3, query q) stores
-// its 4 fp16 weights at pw[pi][q][g], so a lane reads the 4 token groups of
-// a page for its own query with two 16-byte loads.
+// Weights of a 4-page window for the 4x4x4 PV, staged per wave in LDS.  The
+// S-layout lane 16*pi + 4*j + q (page pi, tokens 4j..4j+3, query q):
+//   * pw_store puts its 4 fp16 weights at pw[pi][q][j] (token groups of 4
+//     consecutive tokens);
+//   * pw_store_strided puts weight i at pw[pi][q][i][j], so that entry
+//     [pi][q][g] holds tokens g, g+4, g+8, g+12 (the token groups of
+//     pv4_group).
+// A lane then reads the 4 groups of a page for its own query with two
+// 16-byte loads (pw_load).
 __device__ __forceinline__ void pw_store(uint2* pw, uint32_t w01, uint32_t w23, int lane) {
   pw[((lane >> 4) * 4 + (lane & 3)) * 4 + ((lane >> 2) & 3)] = make_uint2(w01, w23);
+}
+__device__ __forceinline__ void pw_store_strided(uint2* pw, uint32_t w01, uint32_t w23, int lane) {
+  uint16_t* h = reinterpret_cast<uint16_t*>(pw) + ((lane >> 4) * 4 + (lane & 3)) * 16 + ((lane >> 2) & 3);
+  h[0] = (uint16_t)w01;
+  h[4] = (uint16_t)(w01 >> 16);
+  h[8] = (uint16_t)w23;
+  h[12] = (uint16_t)(w23 >> 16);
 }
 __device__ __forceinline__ void pw_load(const uint2* pw, int pi, int q, uint2 (&p)[4]) {
   const uint4* s = reinterpret_cast<const uint4*>(pw + (pi * 4 + q) * 4);

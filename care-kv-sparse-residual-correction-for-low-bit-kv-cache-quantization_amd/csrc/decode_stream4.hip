@@ -198,7 +198,7 @@ __global__ __launch_bounds__(256) void decode_stream4_kernel(carekv_arena A, Dec
       for (int h = 0; h < D / 64; ++h) oacc[h] *= f_old;  // the lane's own query
     }
     const uint32_t e01 = pack_h2(e[0], e[1]), e23 = pack_h2(e[2], e[3]);
-    pw_store(s_pw[w], e01, e23, lane);
+    pw_store_strided(s_pw[w], e01, e23, lane);
 
     // ---- O += P V_hat, page by page
 #pragma unroll
@@ -213,10 +213,10 @@ __global__ __launch_bounds__(256) void decode_stream4_kernel(carekv_arena A, Dec
       dequant_pairs<BITS, CH, BITS>(cv.vw[pi], vs, vp);
       vtile_write<D, BITS>(vt, vp, ln, lj);
       lds_sync_wave();
-      uint2 pg[4];  // P[query sc][tokens 4g..4g+3] of page pi
+      uint2 pg[4];  // P[query sc][tokens g, g+4, g+8, g+12] of page pi
       pw_load(s_pw[w], pi, sc, pg);
 #pragma unroll
-      for (int g = 0; g < 4; ++g) pv4_group<D, BITS>(vt, 4 * g, pg[g].x, pg[g].y, oacc, lane);
+      for (int g = 0; g < 4; ++g) pv4_group<D, BITS>(vt, g, pg[g].x, pg[g].y, oacc, lane);
       lds_sync_wave();
     }
 
