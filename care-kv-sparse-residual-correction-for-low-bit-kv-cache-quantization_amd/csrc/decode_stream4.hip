@@ -24,9 +24,10 @@
 
 namespace carekv {
 
-// One window's share of a lane: the K side (prefetched a window ahead)
-// and the V side (loaded at the top of the window's iteration; the S and
-// softmax work covers its latency).
+// One window's share of a lane: the K side (K rows and scales; reloaded for
+// the next window once the window's PV is done, so the records and the next
+// window's top cover the latency) and the V side (fetched a whole window
+// ahead).  The register cap of 4 waves per SIMD holds with both in flight.
 template <int D, int BITS, int SM>
 struct WinK {
   static constexpr int RB = row_bytes(D, BITS), NWR = RB / 4, NCG = D / 32;
@@ -44,7 +45,7 @@ struct WinV {
 };
 
 template <int D, int BITS, int SM>
-__global__ __launch_bounds__(256) void decode_stream4_kernel(carekv_arena A, DecodeArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void decode_stream4_kernel(carekv_arena A, DecodeArgs a) {
   using G = PageGeom<D, BITS>;
   using WK = WinK<D, BITS, SM>;
   using WV = WinV<D, BITS, SM>;
@@ -73,7 +74,11 @@ __global__ __launch_bounds__(256) void decode_stream4_kernel(carekv_arena A, Dec
   const int ln = lane & 15, lj = lane >> 4;  // V side: token ln, chunk lj; K side: token ln of page lj
   const int sc = lane & 3, sbk = ln >> 2;    // S layout: query sc, tokens 4*sbk.. of page lj
   const long pg_base = ((long)kvh * A.n_seq + seq) * A.max_pages;
-  const RowRes rr = row_resources<D, BITS, SM>(A, pg_base);
+  const int p_begin = split * a.SP, p_end = min(p_begin + a.SP, np);
+  // code and scale loads past page p_end read out of range of the resources
+  // (0, no memory access), so every prefetch is issued unconditionally and
+  // the in-order load counter never waits across a branch
+  const RowRes rr = row_resources<D, BITS, SM>(A, pg_base, p_end);
   const bool corr = a.correction != 0;
   const float sm_log2 = a.sm_log2;
   const long rq = (long)a.Pmax * a.F;  // record stride between query heads
@@ -98,26 +103,29 @@ __global__ __launch_bounds__(256) void decode_stream4_kernel(carekv_arena A, Dec
 #pragma unroll
   for (int h = 0; h < D / 64; ++h) oacc[h] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-  const int p_begin = split * a.SP, p_end = min(p_begin + a.SP, np);
-  WK nx;
-  auto load_wink = [&](int q0) {
-    const int pk = q0 + lj;  // this lane's page on the K side
-    const uint32_t krow = (uint32_t)(pk * kPage + ln);
-    buf_load_row<RB>(nx.kw, rr.kc, krow * RB);
+  // K rows and scales of the window, page metadata (one field per lane),
+  // V codes and scales one window ahead
+  WK kx;
+  auto load_k = [&](int q0) {
+    const uint32_t krow = (uint32_t)((q0 + lj) * kPage + ln);
+    buf_load_row<RB>(kx.kw, rr.kc, krow * RB);
     if constexpr (SM == 1) {
-      if constexpr (NCG == 4) nx.ksc[0] = __builtin_amdgcn_raw_buffer_load_b32(rr.ks, krow * NCG, 0, 0);
-      else nx.ksc[0] = __builtin_amdgcn_raw_buffer_load_b16(rr.ks, krow * NCG, 0, 0);
+      if constexpr (NCG == 4) kx.ksc[0] = __builtin_amdgcn_raw_buffer_load_b32(rr.ks, krow * NCG, 0, 0);
+      else kx.ksc[0] = __builtin_amdgcn_raw_buffer_load_b16(rr.ks, krow * NCG, 0, 0);
     } else {
       if constexpr (NCG == 4) {
         const auto v = __builtin_amdgcn_raw_buffer_load_b64(rr.ks, krow * NCG * 2, 0, 0);
-        nx.ksc[0] = v[0]; nx.ksc[1] = v[1];
+        kx.ksc[0] = v[0]; kx.ksc[1] = v[1];
       } else {
-        nx.ksc[0] = __builtin_amdgcn_raw_buffer_load_b32(rr.ks, krow * NCG * 2, 0, 0);
+        kx.ksc[0] = __builtin_amdgcn_raw_buffer_load_b32(rr.ks, krow * NCG * 2, 0, 0);
       }
     }
-    nx.meta = meta_field_load<NCG>(A, pg_base + pk, pk < p_end, ln);
   };
-  auto load_winv = [&](WV& v, int q0) {
+  auto load_meta = [&](int q0) {
+    const int pk = q0 + lj;
+    return meta_field_any<NCG, SM>(A, pg_base, pk, pk < p_end, ln);
+  };
+  auto load_v = [&](WV& v, int q0) {
     const int gi = (lj * CH) / 32;
 #pragma unroll
     for (int pi = 0; pi < 4; ++pi) {
@@ -146,27 +154,31 @@ __global__ __launch_bounds__(256) void decode_stream4_kernel(carekv_arena A, Dec
   };
 
   int p0 = p_begin + 4 * w;
-  if (p0 < p_end) load_wink(p0);
+  int meta_nx = 0;
+  WV vn;
+  if (p0 < p_end) {
+    load_k(p0);
+    meta_nx = load_meta(p0);
+    load_v(vn, p0);
+  }
   for (; p0 < p_end; p0 += 16) {
-    const WK cur = nx;
-    WV cv;
-    load_winv(cv, p0);
-    if (p0 + 16 < p_end) load_wink(p0 + 16);
+    const int cmeta = meta_nx;  // page metadata of this window
+    const WV cv = vn;           // V of this window
+    load_v(vn, p0 + 16);
     int nvp[4];
 #pragma unroll
-    for (int pi = 0; pi < 4; ++pi) nvp[pi] = __builtin_amdgcn_readlane(cur.meta, 16 * pi);
-    if (nvp[0] <= 0 && nvp[1] <= 0 && nvp[2] <= 0 && nvp[3] <= 0) continue;
-    const int my_nv = __shfl(cur.meta, lane & 48, 64);        // valid tokens of this lane's page
-    const int my_meta = __shfl(cur.meta, (lane & 48) + 1, 64);
+    for (int pi = 0; pi < 4; ++pi) nvp[pi] = __builtin_amdgcn_readlane(cmeta, 16 * pi);
+    const int my_nv = __shfl(cmeta, lane & 48, 64);        // valid tokens of this lane's page
+    const int my_meta = __shfl(cmeta, (lane & 48) + 1, 64);
 
     // ---- S = K_hat q on 4x4x4 blocks
     _Float16 ksg[NCG];
     {
-      const float km = SM == 1 ? h2f((uint16_t)__shfl(cur.meta, (lane & 48) + 10, 64)) : 0.f;
+      const float km = SM == 1 ? h2f((uint16_t)__shfl(cmeta, (lane & 48) + 10, 64)) : 0.f;
 #pragma unroll
       for (int g = 0; g < NCG; ++g) {
-        if constexpr (SM == 1) ksg[g] = (_Float16)((float)(int8_t)(cur.ksc[0] >> (8 * g)) * km);
-        else ksg[g] = bits2half((uint16_t)(cur.ksc[g >> 1] >> (16 * (g & 1))));
+        if constexpr (SM == 1) ksg[g] = (_Float16)((float)(int8_t)(kx.ksc[0] >> (8 * g)) * km);
+        else ksg[g] = bits2half((uint16_t)(kx.ksc[g >> 1] >> (16 * (g & 1))));
       }
     }
     float4_t sa0 = {0.f, 0.f, 0.f, 0.f}, sa1 = {0.f, 0.f, 0.f, 0.f};
@@ -174,24 +186,26 @@ __global__ __launch_bounds__(256) void decode_stream4_kernel(carekv_arena A, Dec
     for (int s = 0; s < NS4; ++s) {
       const int g = PF::T.a[2 * s] / 32;
       const half2_t ss = {ksg[g], ksg[g]};
-      const half2_t c0 = code_pair<BITS, D, BITS>(cur.kw, 2 * s) * ss;
-      const half2_t c1 = code_pair<BITS, D, BITS>(cur.kw, 2 * s + 1) * ss;
+      const half2_t c0 = code_pair<BITS, D, BITS>(kx.kw, 2 * s) * ss;
+      const half2_t c1 = code_pair<BITS, D, BITS>(kx.kw, 2 * s + 1) * ss;
       const half4_t ak = {c0[0], c0[1], c1[0], c1[1]};
       const half4_t bq = *reinterpret_cast<const half4_t*>(sq4 + (s * 4 + sc) * 4);
       if (s & 1) sa1 = mfma4x4(ak, bq, sa1);
       else sa0 = mfma4x4(ak, bq, sa0);
     }
+
     // ---- online softmax over the window (lane: tokens 4*sbk+i of page lj, query sc)
     float x[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) x[i] = (4 * sbk + i < my_nv) ? (sa0[i] + sa1[i]) * sm_log2 : -INFINITY;
     const float mx = pair32_max(pair16_max(row4_max(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])))));
-    const float m_new = fmaxf(m_run, mx);  // finite: some page of the window has a valid token
-    const float f_old = __builtin_amdgcn_exp2f(m_run - m_new);
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;  // a window with no valid token so far
+    const float f_old = __builtin_amdgcn_exp2f(m_run - m_use);
     m_run = m_new;
     float e[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) e[i] = __builtin_amdgcn_exp2f(x[i] - m_new);
+    for (int i = 0; i < 4; ++i) e[i] = __builtin_amdgcn_exp2f(x[i] - m_use);
     l_run = l_run * f_old + pair32_sum(pair16_sum(row4_sum((e[0] + e[1]) + (e[2] + e[3]))));
     if (__builtin_expect(__any(f_old != 1.f), 0)) {
 #pragma unroll
@@ -205,7 +219,7 @@ __global__ __launch_bounds__(256) void decode_stream4_kernel(carekv_arena A, Dec
     for (int pi = 0; pi < 4; ++pi) {
       if (nvp[pi] <= 0) continue;
       float vm = 0.f;
-      if constexpr (SM == 1) vm = h2f((uint16_t)__builtin_amdgcn_readlane(cur.meta, 16 * pi + 11));
+      if constexpr (SM == 1) vm = h2f((uint16_t)__builtin_amdgcn_readlane(cmeta, 16 * pi + 11));
       _Float16 vs;
       if constexpr (SM == 1) vs = (_Float16)((float)(int8_t)(cv.vsc[0] >> (8 * pi)) * vm);
       else vs = bits2half((uint16_t)(cv.vsc[pi >> 1] >> (16 * (pi & 1))));
@@ -220,6 +234,8 @@ __global__ __launch_bounds__(256) void decode_stream4_kernel(carekv_arena A, Dec
       lds_sync_wave();
     }
 
+    load_k(p0 + 16);  // the next window's K rows and metadata
+    meta_nx = load_meta(p0 + 16);
     if (!corr) continue;
     // ---- page records: m_ref, K-slot moments, V-block masses (this lane:
     // page lj, query sc; the lanes with sbk == 0 write)
@@ -232,7 +248,7 @@ __global__ __launch_bounds__(256) void decode_stream4_kernel(carekv_arena A, Dec
     int kslot[NCG];
 #pragma unroll
     for (int cg = 0; cg < NCG; ++cg) {
-      const int s = __shfl(cur.meta, (lane & 48) + 2 + cg, 64);
+      const int s = __shfl(cmeta, (lane & 48) + 2 + cg, 64);
       kslot[cg] = (my_meta != 0 && s >= 0 && s < A.n_slots) ? s : -1;
     }
     int nks = 0;
@@ -285,7 +301,7 @@ __global__ __launch_bounds__(256) void decode_stream4_kernel(carekv_arena A, Dec
     int vrank = -1, rv = 0;
 #pragma unroll
     for (int vb = 0; vb < kVtb; ++vb) {
-      const int s = __shfl(cur.meta, (lane & 48) + 6 + vb, 64);
+      const int s = __shfl(cmeta, (lane & 48) + 6 + vb, 64);
       if (s < 0 || s >= A.n_slots) continue;
       if (vb == sbk) vrank = rv;
       ++rv;
