@@ -8,48 +8,14 @@ namespace carekv {
 
 constexpr int kBlock = 256;
 
+// Work-group scratch of the reductions below: wave totals and broadcast
+// slots (small, so that it costs little of a work-group's LDS).
 struct BlockScratch {
-  float f[kBlock];
-  int i[kBlock];
+  float f[16];
+  int i[16];
   int wsum[4];
   int bc[8];
 };
-
-__device__ __forceinline__ float block_sum(float v, BlockScratch& s) {
-  s.f[threadIdx.x] = v;
-  __syncthreads();
-  for (int o = kBlock / 2; o > 0; o >>= 1) {
-    if ((int)threadIdx.x < o) s.f[threadIdx.x] += s.f[threadIdx.x + o];
-    __syncthreads();
-  }
-  const float r = s.f[0];
-  __syncthreads();
-  return r;
-}
-
-__device__ __forceinline__ float block_max(float v, BlockScratch& s) {
-  s.f[threadIdx.x] = v;
-  __syncthreads();
-  for (int o = kBlock / 2; o > 0; o >>= 1) {
-    if ((int)threadIdx.x < o) s.f[threadIdx.x] = fmaxf(s.f[threadIdx.x], s.f[threadIdx.x + o]);
-    __syncthreads();
-  }
-  const float r = s.f[0];
-  __syncthreads();
-  return r;
-}
-
-__device__ __forceinline__ int block_isum(int v, BlockScratch& s) {
-  s.i[threadIdx.x] = v;
-  __syncthreads();
-  for (int o = kBlock / 2; o > 0; o >>= 1) {
-    if ((int)threadIdx.x < o) s.i[threadIdx.x] += s.i[threadIdx.x + o];
-    __syncthreads();
-  }
-  const int r = s.i[0];
-  __syncthreads();
-  return r;
-}
 
 // Butterfly wave reductions (fixed pattern: every lane ends with the same
 // bits).

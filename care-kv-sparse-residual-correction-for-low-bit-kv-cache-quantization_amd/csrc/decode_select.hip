@@ -48,8 +48,8 @@ struct Sel {
 };
 
 // k-th largest key of the candidates [lo, hi) (key -1: empty position),
-// by 8-bit radix passes from the top; per-wave histograms keep the LDS
-// atomics of a wave on its own copy.
+// by 8-bit radix passes from the top; two histograms (one per wave pair)
+// spread the LDS atomics.
 __device__ Sel radix_select(const int* key, int lo, int hi, int k, int (*hist)[256], BlockScratch& bs) {
   Sel r{0u, INT_MAX, 0, true};
   int cnt = 0;
@@ -62,11 +62,11 @@ __device__ Sel radix_select(const int* key, int lo, int hi, int k, int (*hist)[2
   for (int pass = 0; pass < 4; ++pass) {
     const int shift = 24 - 8 * pass;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) hist[c][threadIdx.x] = 0;
+    for (int c = 0; c < 2; ++c) hist[c][threadIdx.x] = 0;
     __syncthreads();
     for (int i = lo + threadIdx.x; i < hi; i += kBlock) {
       const int u = key[i];
-      if (u >= 0 && ((uint32_t)u & mask) == prefix) atomicAdd(&hist[w][((uint32_t)u >> shift) & 255u], 1);
+      if (u >= 0 && ((uint32_t)u & mask) == prefix) atomicAdd(&hist[w >> 1][((uint32_t)u >> shift) & 255u], 1);
     }
     __syncthreads();
     if (threadIdx.x < 64) {
@@ -75,7 +75,7 @@ __device__ Sel radix_select(const int* key, int lo, int hi, int k, int (*hist)[2
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int d = 255 - 4 * lane - i;
-        c[i] = ((hist[0][d] + hist[1][d]) + hist[2][d]) + hist[3][d];
+        c[i] = hist[0][d] + hist[1][d];
         loc += c[i];
       }
       int incl = loc;
@@ -125,11 +125,11 @@ constexpr int kLdsCand = 8192;  // candidates kept in LDS (32 KB); more go to th
 constexpr int kXcd = 8;
 
 template <int D>
-__global__ __launch_bounds__(256) void decode_select_kernel(carekv_arena A, DecodeArgs a) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) void decode_select_kernel(carekv_arena A, DecodeArgs a) {
   constexpr int NCG = D / 32;
   constexpr int FMAX = 1 + 3 * NCG + kVtb;
   __shared__ BlockScratch bs;
-  __shared__ int hist[4][256];
+  __shared__ int hist[2][256];  // one histogram per wave pair
   extern __shared__ float s_cand[];  // ncand floats when they fit (size set at launch)
   const int GQ = a.GQ;
   const int win = blockIdx.x / (kXcd * GQ), rem = blockIdx.x % (kXcd * GQ);
@@ -188,7 +188,7 @@ __global__ __launch_bounds__(256) void decode_select_kernel(carekv_arena A, Deco
   const float invL = L > 0.f ? 1.f / L : 0.f;
   float sumK = 0.f, sumV = 0.f;
   int cntK = 0, cntV = 0;
-#pragma unroll 2
+#pragma unroll 1
   for (int p = tid; p < np; p += kBlock) {
     const long pg = pg_base + p;
     const int nv = A.valid[pg];
