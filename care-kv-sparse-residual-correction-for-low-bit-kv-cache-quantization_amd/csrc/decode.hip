@@ -91,6 +91,15 @@ extern "C" int carekv_decode_attn(const carekv_arena* arena, const carekv_decode
   a.correction = dp->correction; a.kind = dp->kind; a.joint = dp->joint; a.normalize = dp->normalize;
   a.k_exact = dp->k_exact; a.budget_ratio = dp->budget_ratio; a.abs_k = dp->abs_k; a.abs_v = dp->abs_v;
   a.ratio_k = dp->ratio_k; a.ratio_v = dp->ratio_v;
+  {  // apply chunks: the largest power-of-two multiple of the split (at most
+     // 1024 pages) that still gives >= 1024 work-groups, which every CU holds
+     // at once; fewer, longer chunks amortise the per-work-group item scan
+    const long pairs = (long)a.B * A.n_kv_heads;
+    int m = 1;
+    while (a.SP * 2 * m <= 1024 && pairs * ((a.nsplit + 2 * m - 1) / (2 * m)) >= 1024) m *= 2;
+    a.SPA = a.SP * m;
+    a.napply = (a.nsplit + m - 1) / m;
+  }
   hipStream_t s = (hipStream_t)stream;
   hipEvent_t* ev = (hipEvent_t*)dp->phase_events;
   auto mark = [&](int i) -> int {

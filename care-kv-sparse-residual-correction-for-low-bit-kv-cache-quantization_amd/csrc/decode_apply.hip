@@ -88,7 +88,7 @@ void decode_apply_kernel(carekv_arena A, DecodeArgs a) {
   const long qrow = (long)bk * GQ + (qv ? ln : 0);  // this lane's query row of the workspace
 
   // ---- pages of the chunk with any selected slot
-  const int p_begin = chunk * a.SP, p_end = min(p_begin + a.SP, np);
+  const int p_begin = chunk * a.SPA, p_end = min(p_begin + a.SPA, np);
   int n_items = 0;
   for (int p0 = p_begin; p0 < p_end; p0 += kBlock) {
     const int p = p0 + threadIdx.x;
@@ -311,7 +311,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(int Hkv, int D, Dec
         const float ms = a.pml[base * 2];
         if (ms != -INFINITY) O += a.po[base * D + d] * __builtin_amdgcn_exp2f(ms - M);
       }
-      for (int c = 0; c < a.nsplit; ++c) {
+      for (int c = 0; c < a.napply; ++c) {
         const long cb = ((long)bk * a.nsplit + c) * GQ + qq;
         nm += a.num[cb * D + d];
         dn += a.den[cb];
@@ -325,12 +325,12 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(int Hkv, int D, Dec
 }
 
 int launch_decode_apply(const carekv_arena& A, const DecodeArgs& a, hipStream_t s) {
-  if (a.SP > 1024) {
-    set_error("split_pages must be at most 1024");
+  if (a.SPA > 1024) {
+    set_error("apply chunks must be at most 1024 pages");
     return CAREKV_EINVAL;
   }
   if (a.GQ <= 4) return launch_decode_apply4(A, a, s);  // windows of 4 pages, 4x4x4 layout
-  const dim3 grid(a.nsplit, A.n_kv_heads, a.B);
+  const dim3 grid(a.napply, A.n_kv_heads, a.B);
   return dispatch_dbs(A.head_dim, A.base_bits, A.scale_mode, [&](auto d, auto bb, auto sm) {
     hipLaunchKernelGGL((decode_apply_kernel<decltype(d)::value, decltype(bb)::value, decltype(sm)::value>), grid,
                        dim3(256), 0, s, A, a);

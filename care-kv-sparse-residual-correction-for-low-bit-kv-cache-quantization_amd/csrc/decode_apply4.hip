@@ -73,7 +73,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
   const long qrow = (long)bk * GQ + (qv ? sc : 0);  // this lane's query row of the workspace
 
   // ---- pages of the chunk with any selected slot
-  const int p_begin = chunk * a.SP, p_end = min(p_begin + a.SP, np);
+  const int p_begin = chunk * a.SPA, p_end = min(p_begin + a.SPA, np);
   int n_items = 0;
   for (int p0 = p_begin; p0 < p_end; p0 += kBlock) {
     const int p = p0 + threadIdx.x;
@@ -394,7 +394,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
 }
 
 int launch_decode_apply4(const carekv_arena& A, const DecodeArgs& a, hipStream_t s) {
-  const dim3 grid(a.nsplit, A.n_kv_heads, a.B);
+  const dim3 grid(a.napply, A.n_kv_heads, a.B);
   return dispatch_dbs(A.head_dim, A.base_bits, A.scale_mode, [&](auto d, auto bb, auto sm) {
     hipLaunchKernelGGL((decode_apply4_kernel<decltype(d)::value, decltype(bb)::value, decltype(sm)::value>), grid,
                        dim3(256), 0, s, A, a);

@@ -27,6 +27,7 @@ struct DecodeArgs {
   int B, Hq, GQ, nsplit, SP, Pmax, k_cap, v_cap, F, ncand;
   float sm_scale, sm_log2, sens, k_corr_scale, lam_k, lam_v, inv_sqrt_d;
   int correction, kind, joint, normalize, k_exact, budget_ratio, abs_k, abs_v;
+  int SPA, napply;  // apply pass: pages per chunk (a multiple of SP) and chunk count (<= nsplit)
   double ratio_k, ratio_v, sens_d;
 };
 
