@@ -42,7 +42,8 @@ class DecodeParams(C.Structure):
                 ("k_exact", C.c_int32), ("k_corr_scale", C.c_float), ("lambda_k", C.c_float),
                 ("lambda_v", C.c_float), ("budget_ratio", C.c_int32), ("abs_k", C.c_int32), ("abs_v", C.c_int32),
                 ("ratio_k", C.c_double), ("ratio_v", C.c_double), ("k_cap", C.c_int32), ("v_cap", C.c_int32),
-                ("split_pages", C.c_int32), ("phase_events", C.c_void_p)]
+                ("split_pages", C.c_int32), ("phase_events", C.c_void_p), ("k_proxy", C.c_int32),
+                ("sketch_proj", C.c_void_p)]
 
 
 class PrefillParams(C.Structure):

@@ -5,7 +5,8 @@ sequences of one layer.  It computes, per (sequence, kv head), what the
 reference computes with ``read_base_concat`` + ``dequantize`` + base
 attention (attention.py:996-1022) followed by ``vectorized_joint_correction``
 over the kv head's query heads (attention.py:576-957): the comb+ex selector
-(CAREKV_KSCORE_LIVE=1) with per-query score normalisation, joint or separate
+(CAREKV_KSCORE_LIVE=1) or the sketch-proxy K score (CAREKV_KSCORE_LIVE=0,
+attention.py:718-725), per-query score normalisation, joint or separate
 top-k, and the exact (or linear) K correction.  ``CAREKVAttention`` and
 ``CAREKVMultiHeadAttention`` keep the reference's per-head / multi-head entry
 points (attention.py:964-1077) on top of it.
@@ -21,7 +22,7 @@ import numpy as np
 import torch
 
 from . import _lib
-from .cache import CAREKVCache
+from .cache import CAREKVCache, get_sketch_proj
 from .config import CacheConfig, ReadKnobs, resolve_read_knobs
 
 KIND_CODE = {"both": 0, "k": 1, "v": 2}
@@ -54,9 +55,6 @@ def decode_attention(cache: CAREKVCache, layer: int, q: torch.Tensor, seqs: Opti
     seqs = list(range(B)) if seqs is None else list(seqs)
     if knobs is None:
         knobs = resolve_read_knobs(cfg, layer)
-    if correction and not knobs.kscore_live:
-        raise NotImplementedError("the decode kernel implements the query-aware (KSCORE_LIVE=1) K selector; "
-                                  "set CAREKV_KSCORE_LIVE=1 (the reference's vectorized paper config)")
     q = q.to(torch.float16).contiguous()
     npages = np.array([cache.num_pages(layer, 0, s) for s in seqs], dtype=np.int32)
     max_np = int(npages.max()) if B else 0
@@ -78,6 +76,10 @@ def decode_attention(cache: CAREKVCache, layer: int, q: torch.Tensor, seqs: Opti
         lambda_k=knobs.lambda_k, lambda_v=knobs.lambda_v, budget_ratio=int(knobs.budget_ratio),
         abs_k=knobs.abs_k, abs_v=knobs.abs_v, ratio_k=knobs.ratio_k, ratio_v=knobs.ratio_v,
         k_cap=cache.k_cap, v_cap=cache.v_cap, split_pages=int(split_pages))
+    if correction and not knobs.kscore_live:
+        P = get_sketch_proj(cfg.head_dim, cfg.k_channel_group, cfg.sketch_dim, dev)
+        dp.k_proxy = 1
+        dp.sketch_proj = P.data_ptr()
     ev_arr = None
     if phase_events is not None:
         if len(phase_events) != 5:

@@ -7,7 +7,7 @@ using namespace carekv;
 
 namespace {
 struct WsLayout {
-  long err, pml, po, rec, ebuf, scores, mask, ml, num, den, total;
+  long err, pml, po, rec, ebuf, scores, mask, ml, num, den, xbuf, prox, total;
   int nsplit, F, ncand;
 };
 
@@ -32,6 +32,9 @@ WsLayout ws_layout(const carekv_arena& A, const carekv_decode_params& dp) {
   L.ml = off; off += al(BH * GQ * 2 * 4);
   L.num = off; off += al(BH * L.nsplit * GQ * (long)D * 4);
   L.den = off; off += al(BH * L.nsplit * GQ * 4);
+  const bool proxy = dp.k_proxy != 0 && dp.correction != 0;
+  L.xbuf = off; off += proxy ? al(BH * GQ * (long)Pm * 16 * 4) : 0;
+  L.prox = off; off += proxy ? al(BH * GQ * (long)Pm * 4 * 4) : 0;
   L.total = off;
   return L;
 }
@@ -61,6 +64,10 @@ extern "C" int carekv_decode_attn(const carekv_arena* arena, const carekv_decode
   CAREKV_REQUIRE(dp->v_cap >= 0 && dp->v_cap <= 4, "v_cap out of range");
   CAREKV_REQUIRE(dp->lambda_k > 0.f && dp->lambda_v > 0.f, "KSCORE lambdas must be positive");
   CAREKV_REQUIRE(!diag || diag_cap > 0, "diag_cap must be positive");
+  const bool proxy = dp->k_proxy != 0 && dp->correction != 0;
+  CAREKV_REQUIRE(!proxy || dp->sketch_proj, "the sketch proxy needs sketch_proj");
+  CAREKV_REQUIRE(!proxy || (A.k_sketch && A.k_channel_group == 32 && A.sketch_dim >= 1 && A.sketch_dim <= 64),
+                 "the sketch proxy needs k_sketch, k_channel_group 32 and sketch_dim in 1..64");
   const WsLayout L = ws_layout(A, *dp);
   if (workspace_bytes < L.total) {
     set_error("carekv_decode_attn: workspace too small (%lld < %lld)", (long long)workspace_bytes,
@@ -80,12 +87,19 @@ extern "C" int carekv_decode_attn(const carekv_arena* arena, const carekv_decode
   a.ml = (float*)(ws + L.ml);
   a.num = (float*)(ws + L.num);
   a.den = (float*)(ws + L.den);
+  a.proxy = proxy ? 1 : 0;
+  a.xbuf = proxy ? (float*)(ws + L.xbuf) : nullptr;
+  a.prox = proxy ? (float*)(ws + L.prox) : nullptr;
+  a.sketch_proj = dp->sketch_proj;
   a.diag = diag; a.diag_cap = diag_cap;
   a.B = dp->batch; a.Hq = dp->n_heads; a.GQ = GQ; a.nsplit = L.nsplit; a.SP = dp->split_pages;
   a.Pmax = dp->max_pages_used > 0 ? dp->max_pages_used : 1;
   a.k_cap = dp->k_cap; a.v_cap = dp->v_cap; a.F = L.F; a.ncand = L.ncand;
   a.sm_scale = dp->sm_scale; a.sens = dp->sensitivity; a.sens_d = (double)dp->sensitivity;
-  a.k_corr_scale = dp->k_corr_scale; a.lam_k = dp->lambda_k; a.lam_v = dp->lambda_v;
+  a.k_corr_scale = dp->k_corr_scale;
+  // the KSCORE lambdas weigh the normalised scores of the live selector only
+  // (attention.py:838-844)
+  a.lam_k = proxy ? 1.f : dp->lambda_k; a.lam_v = proxy ? 1.f : dp->lambda_v;
   a.sm_log2 = (float)((double)dp->sm_scale * 1.4426950408889634074);  // log2(e)
   a.inv_sqrt_d = (float)(1.0 / sqrt((double)A.head_dim));
   a.correction = dp->correction; a.kind = dp->kind; a.joint = dp->joint; a.normalize = dp->normalize;
@@ -112,6 +126,7 @@ extern "C" int carekv_decode_attn(const carekv_arena* arena, const carekv_decode
   int rc = mark(0);
   if (rc == CAREKV_OK) rc = launch_decode_stream(A, a, s);
   if (rc == CAREKV_OK) rc = mark(1);
+  if (rc == CAREKV_OK && proxy) rc = launch_decode_proxy(A, a, s);
   if (rc == CAREKV_OK) rc = launch_decode_select(A, a, s);
   if (rc == CAREKV_OK) rc = mark(2);
   if (rc == CAREKV_OK && a.correction) rc = launch_decode_apply(A, a, s);

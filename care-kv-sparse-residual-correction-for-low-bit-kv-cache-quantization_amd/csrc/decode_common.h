@@ -21,6 +21,9 @@ struct DecodeArgs {
   float* ml;           // [B*Hkv][GQ][2]          global max (base 2) / sum
   float* num;          // [B*Hkv][nsplit][GQ][D]  apply partial numerators
   float* den;          // [B*Hkv][nsplit][GQ]     apply partial denominators
+  float* xbuf;         // [B*Hkv][GQ][Pmax][16]   fp32 base-2 logits x (sketch proxy only)
+  float* prox;         // [B*Hkv][GQ][Pmax][4]    mass, boundary, vdiff (sketch proxy only)
+  const float* sketch_proj;  // [32][sketch_dim] fp32 (sketch proxy only)
   int32_t* diag;
   int32_t* err_flag;
   int diag_cap;
@@ -28,6 +31,7 @@ struct DecodeArgs {
   float sm_scale, sm_log2, sens, k_corr_scale, lam_k, lam_v, inv_sqrt_d;
   int correction, kind, joint, normalize, k_exact, budget_ratio, abs_k, abs_v;
   int SPA, napply;  // apply pass: pages per chunk (a multiple of SP) and chunk count (<= nsplit)
+  int proxy;        // 1: K scores from the sketch proxy (prox records), 0: from the moments
   double ratio_k, ratio_v, sens_d;
 };
 
@@ -40,12 +44,16 @@ struct DecodeArgs {
 // valid tokens.  Written only for pages with metadata.
 //
 // ebuf holds the page's e_t (0 past the valid tokens) for the apply pass.
+// With the sketch proxy the K moments are not written; xbuf holds the
+// page's x_t (-inf past the valid tokens) and decode_proxy_kernel turns
+// them into the prox records.
 //
 // Selection mask per (sequence, kv head, query, page): bit r = the r-th
 // stored K slot of the page is selected, bit 4 + r = the r-th stored V block.
 
 int launch_decode_stream(const carekv_arena& A, const DecodeArgs& a, hipStream_t s);
 int launch_decode_stream4(const carekv_arena& A, const DecodeArgs& a, hipStream_t s);  // GQ <= 4, SP % 16 == 0
+int launch_decode_proxy(const carekv_arena& A, const DecodeArgs& a, hipStream_t s);
 int launch_decode_select(const carekv_arena& A, const DecodeArgs& a, hipStream_t s);
 int launch_decode_apply(const carekv_arena& A, const DecodeArgs& a, hipStream_t s);
 int launch_decode_apply4(const carekv_arena& A, const DecodeArgs& a, hipStream_t s);  // GQ <= 4

@@ -5,8 +5,10 @@
 //     attention.py:1015-1022);
 //   * scores every stored slot from the page records: the query-aware K
 //     score ||dS * A(1-A)|| * ||V_page|| * sens (attention.py:167-184, 704-760)
-//     and the V score mass * v_err * sens (attention.py:780-790, with
-//     v_err already scaled by sens in build_v_slot_index);
+//     or, with the sketch proxy, mass * |q_cg P . k_sketch| * boundary *
+//     vdiff * sens (attention.py:718-725) from the decode_proxy_kernel
+//     records, and the V score mass * v_err * sens (attention.py:780-790,
+//     with v_err already scaled by sens in build_v_slot_index);
 //   * normalises each kind by its mean score (attention.py:830-844),
 //     resolves the read budgets (residual_router.py:37-76) and selects the
 //     joint or per-kind top-k with ties toward the lowest candidate index
@@ -124,12 +126,14 @@ constexpr int kLdsCand = 8192;  // candidates kept in LDS (32 KB); more go to th
 // gets pair window*8 + x for queries 0..GQ-1.
 constexpr int kXcd = 8;
 
-template <int D>
+// PX: K scores from the sketch proxy records instead of the moments.
+template <int D, bool PX>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) void decode_select_kernel(carekv_arena A, DecodeArgs a) {
   constexpr int NCG = D / 32;
   constexpr int FMAX = 1 + 3 * NCG + kVtb;
   __shared__ BlockScratch bs;
   __shared__ int hist[2][256];  // one histogram per wave pair
+  __shared__ float s_qs[NCG * 64];  // q_cg P per channel group (sketch proxy)
   extern __shared__ float s_cand[];  // ncand floats when they fit (size set at launch)
   const int GQ = a.GQ;
   const int win = blockIdx.x / (kXcd * GQ), rem = blockIdx.x % (kXcd * GQ);
@@ -178,6 +182,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
     return;
   }
 
+  // ---- q sketches q_cg P (fp32, attention.py:722) for the proxy
+  const int skd = A.sketch_dim;
+  if constexpr (PX) {
+    const uint16_t* qg = a.q + ((long)b * a.Hq + kvh * GQ + qq) * D;
+    for (int i = tid; i < NCG * skd; i += kBlock) {
+      const int cg = i / skd, j = i % skd;
+      float acc = 0.f;
+      for (int c = 0; c < 32; ++c) acc = fmaf(h2f(qg[cg * 32 + c]), a.sketch_proj[c * skd + j], acc);
+      s_qs[cg * 64 + j] = acc;
+    }
+    __syncthreads();
+  }
+
   // ---- score every stored slot (all loads of a page issued up front)
   const int k_cap = a.k_cap, v_cap = a.v_cap, F = a.F;
   const int nK = np * k_cap, nV = np * v_cap;
@@ -188,6 +205,29 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
   const float invL = L > 0.f ? 1.f / L : 0.f;
   float sumK = 0.f, sumV = 0.f;
   int cntK = 0, cntV = 0;
+  if constexpr (PX) {  // K scores of the sketch proxy, one page per thread
+#pragma unroll 1
+    for (int p = tid; p < np; p += kBlock) {
+      const long pg = pg_base + p;
+      const bool ok = L > 0.f && A.valid[pg] > 0 && A.has_meta[pg];
+      float4 px = make_float4(0.f, 0.f, 0.f, 0.f);  // mass, boundary, vdiff
+      if (ok) px = *reinterpret_cast<const float4*>(a.prox + (bq * a.Pmax + p) * 4);
+      int rk = 0;
+#pragma unroll 1
+      for (int cg = 0; cg < NCG; ++cg) {
+        if (!ok || !slot_ok(A, A.k_slot[pg * NCG + cg]) || rk >= k_cap) continue;
+        const uint16_t* ks = A.k_sketch + (pg * NCG + cg) * skd;
+        float dot = 0.f;
+        for (int j = 0; j < skd; ++j) dot = fmaf(s_qs[cg * 64 + j], h2f(ks[j]), dot);
+        const float kp = (((px.x * fabsf(dot)) * px.y) * px.z) * a.sens;
+        sc[p * k_cap + rk] = kp;
+        sumK += kp;
+        ++cntK;
+        ++rk;
+      }
+      for (; rk < k_cap; ++rk) sc[p * k_cap + rk] = -1.f;
+    }
+  }
 #pragma unroll 1
   for (int p = tid; p < np; p += kBlock) {
     const long pg = pg_base + p;
@@ -206,24 +246,26 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
     const bool ok = L > 0.f && nv > 0 && hm;
     const float c = ok ? __builtin_amdgcn_exp2f(r[0] - M) * invL : 0.f;
     const float vnorm = __builtin_amdgcn_sqrtf(vsq);
-    int rk = 0;
+    if constexpr (!PX) {
+      int rk = 0;
 #pragma unroll
-    for (int cg = 0; cg < NCG; ++cg) {
-      if (!ok || !slot_ok(A, ksl[cg]) || rk >= k_cap) continue;
-      float M2 = 0.f, M3 = 0.f, M4 = 0.f;
+      for (int cg = 0; cg < NCG; ++cg) {
+        if (!ok || !slot_ok(A, ksl[cg]) || rk >= k_cap) continue;
+        float M2 = 0.f, M3 = 0.f, M4 = 0.f;
 #pragma unroll
-      for (int j = 0; j < NCG; ++j)
-        if (j == rk) { M2 = r[1 + 3 * j]; M3 = r[2 + 3 * j]; M4 = r[3 + 3 * j]; }
-      const float q2 = c * c * (M2 - c * (2.f * M3 - c * M4));
-      float ks = __builtin_amdgcn_sqrtf(fmaxf(q2, 0.f)) * vnorm;
-      if (!isfinite(ks)) ks = 0.f;
-      ks = ks * a.sens;
-      sc[p * k_cap + rk] = ks;
-      sumK += ks;
-      ++cntK;
-      ++rk;
+        for (int j = 0; j < NCG; ++j)
+          if (j == rk) { M2 = r[1 + 3 * j]; M3 = r[2 + 3 * j]; M4 = r[3 + 3 * j]; }
+        const float q2 = c * c * (M2 - c * (2.f * M3 - c * M4));
+        float ks = __builtin_amdgcn_sqrtf(fmaxf(q2, 0.f)) * vnorm;
+        if (!isfinite(ks)) ks = 0.f;
+        ks = ks * a.sens;
+        sc[p * k_cap + rk] = ks;
+        sumK += ks;
+        ++cntK;
+        ++rk;
+      }
+      for (; rk < k_cap; ++rk) sc[p * k_cap + rk] = -1.f;
     }
-    for (; rk < k_cap; ++rk) sc[p * k_cap + rk] = -1.f;
     int rv = 0;
 #pragma unroll
     for (int vb = 0; vb < kVtb; ++vb) {
@@ -377,10 +419,13 @@ int launch_decode_select(const carekv_arena& A, const DecodeArgs& a, hipStream_t
   const int pairs = a.B * A.n_kv_heads;
   const dim3 grid(((pairs + kXcd - 1) / kXcd) * kXcd * a.GQ);
   const size_t lds = (a.correction && a.ncand <= kLdsCand) ? (size_t)a.ncand * sizeof(float) : 0;
+  const bool px = a.correction && a.proxy;
   if (A.head_dim == 64) {
-    hipLaunchKernelGGL(decode_select_kernel<64>, grid, dim3(kBlock), lds, s, A, a);
+    if (px) hipLaunchKernelGGL((decode_select_kernel<64, true>), grid, dim3(kBlock), lds, s, A, a);
+    else hipLaunchKernelGGL((decode_select_kernel<64, false>), grid, dim3(kBlock), lds, s, A, a);
   } else if (A.head_dim == 128) {
-    hipLaunchKernelGGL(decode_select_kernel<128>, grid, dim3(kBlock), lds, s, A, a);
+    if (px) hipLaunchKernelGGL((decode_select_kernel<128, true>), grid, dim3(kBlock), lds, s, A, a);
+    else hipLaunchKernelGGL((decode_select_kernel<128, false>), grid, dim3(kBlock), lds, s, A, a);
   } else {
     set_error("unsupported head_dim %d", A.head_dim);
     return CAREKV_EINVAL;

@@ -84,7 +84,7 @@ void decode_stream_kernel(carekv_arena A, DecodeArgs a) {
     if (nv <= 0) continue;
     // K residual rows of the stored slots, issued before the page math
     uint32_t krow[NCG];
-    if (corr && cm.meta) {
+    if (corr && cm.meta && !a.proxy) {
 #pragma unroll
       for (int cg = 0; cg < NCG; ++cg) {
         krow[cg] = 0u;
@@ -113,6 +113,9 @@ void decode_stream_kernel(carekv_arena A, DecodeArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) x[i] = (4 * lj + i < nv) ? sacc[i] * sm_log2 : -INFINITY;
     }
+    if (a.proxy && corr && cm.meta && ln < GQ)  // logits for the proxy's margins
+      *reinterpret_cast<float4*>(a.xbuf + (((long)bk * GQ + ln) * a.Pmax + p) * 16 + 4 * lj) =
+          make_float4(x[0], x[1], x[2], x[3]);
     const float mx = col_max(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));
     const float m_new = fmaxf(m_run, mx);  // finite: token 0 of a page is always valid
     const float f_old = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first page
@@ -149,6 +152,7 @@ void decode_stream_kernel(carekv_arena A, DecodeArgs a) {
         const int slot = cm.ksl[cg];
         if (slot < 0) continue;
         if (rk >= a.k_cap) { if (lane == 0) *a.err_flag = 1; break; }
+        if (a.proxy) { ++rk; continue; }  // the sketch proxy scores K slots without the moments
         const long so = (long)seq * A.n_slots + slot;
         const float4_t racc = kslot_dot_w(krow[cg], sqr, D, cg, ln, lj);
         // moments of u = racc * e (dS = racc * f scales them by f^2):

@@ -198,6 +198,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     float x[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) x[i] = (4 * sbk + i < my_nv) ? (sa0[i] + sa1[i]) * sm_log2 : -INFINITY;
+    if (a.proxy && corr && sc < GQ && my_meta != 0 && my_nv > 0)  // logits for the proxy's margins
+      *reinterpret_cast<float4*>(a.xbuf + (((long)bk * GQ + sc) * a.Pmax + p0 + lj) * 16 + 4 * sbk) =
+          make_float4(x[0], x[1], x[2], x[3]);
     const float mx = pair32_max(pair16_max(row4_max(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])))));
     const float m_new = fmaxf(m_run, mx);
     const float m_use = m_new == -INFINITY ? 0.f : m_new;  // a window with no valid token so far
@@ -255,7 +258,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
 #pragma unroll
     for (int cg = 0; cg < NCG; ++cg) nks += kslot[cg] >= 0;
     if (nks > a.k_cap && sbk == 0 && sc == 0) *a.err_flag = 1;
-    for (int r = 0; r < a.k_cap; ++r) {
+    const int n_mom = a.proxy ? 0 : a.k_cap;  // the sketch proxy scores K slots without the moments
+    for (int r = 0; r < n_mom; ++r) {
       int cgr = -1, slotr = -1, cnt = 0;
 #pragma unroll
       for (int cg = 0; cg < NCG; ++cg) {

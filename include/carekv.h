@@ -118,8 +118,9 @@ int carekv_append_rows(const carekv_arena* arena, const uint16_t* k_rows, const 
 /* Decode attention + comb+ex residual correction.  Replaces, per sequence
  * and kv head, CAREKVCache.read_base_concat (cache.py:720-772) + dequantize
  * (quantizer.py:67-82) + base attention (attention.py:1009-1022) +
- * vectorized_joint_correction (attention.py:576-957, KSCORE_LIVE=1) over the
- * kv head's query heads, output half(O_base + dO) (attention.py:1036-1039). */
+ * vectorized_joint_correction (attention.py:576-957, KSCORE_LIVE=1 or the
+ * KSCORE_LIVE=0 sketch proxy) over the kv head's query heads, output
+ * half(O_base + dO) (attention.py:1036-1039). */
 typedef struct carekv_decode_params {
   int32_t batch;           /* rows of q / out                                  */
   int32_t n_heads;         /* query heads; kv head = h / (n_heads/n_kv_heads)   */
@@ -146,6 +147,15 @@ typedef struct carekv_decode_params {
                             * streaming, select, apply and combine kernels (no
                             * reference counterpart; with correction off the
                             * last two are recorded right after select)       */
+  int32_t k_proxy;         /* 0: the query-aware K score (CAREKV_KSCORE_LIVE=1,
+                            * attention.py:704-717); 1: the sketch proxy
+                            * mass * |q_sketch . k_sketch| * boundary * vdiff
+                            * * sens (KSCORE_LIVE=0, attention.py:718-725, the
+                            * score of ResidualRouter.route,
+                            * residual_router.py:160-198)                     */
+  const float* sketch_proj;/* device [k_channel_group][sketch_dim] fp32, the
+                            * get_sketch_proj matrix (residual_store.py:206-214);
+                            * required when k_proxy = 1                       */
 } carekv_decode_params;
 
 /* q, out: fp16 [batch][n_heads][head_dim].  diag (optional, NULL to skip):

@@ -246,6 +246,17 @@ def golden_decode(ck):
                  store=ratio3, read_k=8, read_v=8, k_mode="linear")
 
 
+def golden_decode_proxy(ck):
+    """The sketch-proxy K score (CAREKV_KSCORE_LIVE=0, attention.py:718-725)
+    under the same comb+ex knobs otherwise."""
+    ratio3 = dict(store_budget_mode="ratio", store_budget_ratio=0.03)
+    _decode_case(ck, "c1_proxy", Hq=32, Hkv=4, D=64, T=512, seed=1, outlier_mult=8.0,
+                 store=ratio3, read_k=4, read_v=4, kscore_live=False)
+    _decode_case(ck, "gqa4_d128_proxy", Hq=8, Hkv=2, D=128, T=1000, seed=3, outlier_mult=10.0,
+                 store=dict(store_budget_mode="absolute", store_abs_k=2, store_abs_v=4),
+                 read_k=16, read_v=16, n_append=27, kscore_live=False)
+
+
 def golden_reference_fixture(ck):
     """The reference's own test fixture (tests/test_vectorized_carekv.py:30-58):
     D=32, page 8, g 8, kcg 16, vtb 4, sketch 4, SK=SV=2, fp32 inputs."""
@@ -329,14 +340,21 @@ def golden_activation_slices():
     np.savez_compressed(os.path.join(HERE, "activations_3d_slices.npz"), **out)
 
 
+PARTS = ("activations", "sketch", "store", "append", "decode", "decode_proxy", "fixture")
+
 if __name__ == "__main__":
+    # CAREKV_GOLDEN_PARTS=decode_proxy,... writes only those fixtures
+    parts = [p for p in os.environ.get("CAREKV_GOLDEN_PARTS", ",".join(PARTS)).split(",") if p]
+    if os.environ.get("CAREKV_GOLDEN_ONLY_ACTIVATIONS", "0") == "1":
+        parts = ["activations"]
     torch.set_num_threads(1)
-    golden_activation_slices()
-    if os.environ.get("CAREKV_GOLDEN_ONLY_ACTIVATIONS", "0") != "1":
+    if "activations" in parts:
+        golden_activation_slices()
+    if any(p != "activations" for p in parts):
         ck = _import_reference()
-        golden_sketch(ck)
-        golden_store(ck)
-        golden_append(ck)
-        golden_decode(ck)
-        golden_reference_fixture(ck)
+        fns = dict(sketch=golden_sketch, store=golden_store, append=golden_append, decode=golden_decode,
+                   decode_proxy=golden_decode_proxy, fixture=golden_reference_fixture)
+        for p in parts:
+            if p in fns:
+                fns[p](ck)
     print("golden fixtures written to", HERE)

@@ -22,6 +22,12 @@ DECODE_CASES = {
                       k_mode="exact"),
     "mha_d128_linear": dict(Hq=2, Hkv=2, D=128, store=dict(store_budget_mode="ratio", store_budget_ratio=0.03),
                             k_mode="linear"),
+    # the sketch-proxy K score (CAREKV_KSCORE_LIVE=0)
+    "c1_proxy": dict(Hq=32, Hkv=4, D=64, store=dict(store_budget_mode="ratio", store_budget_ratio=0.03),
+                     k_mode="exact", live=False, score_rtol=1e-3, tie_eps=2e-3),
+    "gqa4_d128_proxy": dict(Hq=8, Hkv=2, D=128, store=dict(store_budget_mode="absolute", store_abs_k=2,
+                                                           store_abs_v=4), k_mode="exact", live=False,
+                           score_rtol=1e-3, tie_eps=2e-3),
 }
 
 PAPER_ENV = dict(CAREKV_STORE_POLICY="residual_kind_aware", CAREKV_PREFILL_RESIDUAL_KIND="both",

@@ -178,12 +178,7 @@ def test_append_golden(golden):
 
 
 # ------------------------------------------------------------ decode goldens
-DECODE_CASES = {
-    "c1": dict(Hq=32, Hkv=4, D=64, store=dict(store_budget_mode="ratio", store_budget_ratio=0.03), k_mode="exact"),
-    "c1_tight": dict(Hq=32, Hkv=4, D=64, store=dict(store_budget_mode="ratio", store_budget_ratio=0.03), k_mode="exact"),
-    "gqa4_d128": dict(Hq=8, Hkv=2, D=128, store=dict(store_budget_mode="absolute", store_abs_k=2, store_abs_v=4), k_mode="exact"),
-    "mha_d128_linear": dict(Hq=2, Hkv=2, D=128, store=dict(store_budget_mode="ratio", store_budget_ratio=0.03), k_mode="linear"),
-}
+from helpers import DECODE_CASES  # noqa: E402  (shared with the GPU parity tests)
 
 
 def build_decode_case(g, name):
@@ -225,7 +220,7 @@ def test_decode_golden(golden, name):
     _compare_cache(c, g)
     diag = {}
     out = decode_attention(c, 0, g["Q"], k_mode=spec["k_mode"], kind="both", k_corr_scale=0.1,
-                           score_normalize=True, kscore_live=True, diag=diag)
+                           score_normalize=True, kscore_live=spec.get("live", True), diag=diag)
     ref = g["O"].astype(F32)
     assert np.abs(out.astype(F32) - ref).max() <= 2e-3
     for h, d in diag.items():
@@ -237,7 +232,10 @@ def test_decode_golden(golden, name):
             sel_me = np.concatenate([d["sel_k"], d["sel_v"]], 1)
             mb = int(sel_ref[0].sum())
             assert selection_matches(sel_me, sel_ref, merged, mb)
-            np.testing.assert_allclose(d["score_K"], g[f"h{h}_score_K"], rtol=2e-5, atol=1e-12)
+            # the proxy's boundary term sums a_t / (s_top - s_t): near-top tokens
+            # amplify the fp32 rounding of the logits (numpy vs torch order)
+            np.testing.assert_allclose(d["score_K"], g[f"h{h}_score_K"], rtol=spec.get("score_rtol", 2e-5),
+                                       atol=1e-12)
             np.testing.assert_allclose(d["score_V"], g[f"h{h}_score_V"], rtol=2e-5, atol=1e-12)
     if "decode_step_out" in g:
         # the reference decode_step itself (correction gated off by read_budget_ratio=0)
