@@ -43,7 +43,8 @@ class DecodeParams(C.Structure):
                 ("lambda_v", C.c_float), ("budget_ratio", C.c_int32), ("abs_k", C.c_int32), ("abs_v", C.c_int32),
                 ("ratio_k", C.c_double), ("ratio_v", C.c_double), ("k_cap", C.c_int32), ("v_cap", C.c_int32),
                 ("split_pages", C.c_int32), ("phase_events", C.c_void_p), ("k_proxy", C.c_int32),
-                ("sketch_proj", C.c_void_p)]
+                ("sketch_proj", C.c_void_p), ("route_policy", C.c_int32), ("adaptive_score", C.c_int32),
+                ("rel_threshold", C.c_double), ("abs_threshold", C.c_double), ("min_keep", C.c_int32)]
 
 
 class PrefillParams(C.Structure):

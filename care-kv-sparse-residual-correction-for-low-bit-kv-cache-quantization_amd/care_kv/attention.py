@@ -75,7 +75,10 @@ def decode_attention(cache: CAREKVCache, layer: int, q: torch.Tensor, seqs: Opti
         normalize=int(knobs.normalize), k_exact=int(knobs.k_exact), k_corr_scale=knobs.k_corr_scale,
         lambda_k=knobs.lambda_k, lambda_v=knobs.lambda_v, budget_ratio=int(knobs.budget_ratio),
         abs_k=knobs.abs_k, abs_v=knobs.abs_v, ratio_k=knobs.ratio_k, ratio_v=knobs.ratio_v,
-        k_cap=cache.k_cap, v_cap=cache.v_cap, split_pages=int(split_pages))
+        k_cap=cache.k_cap, v_cap=cache.v_cap, split_pages=int(split_pages),
+        route_policy=int(knobs.route_policy), adaptive_score=int(bool(knobs.adaptive_score)),
+        rel_threshold=float(knobs.rel_threshold), abs_threshold=float(knobs.abs_threshold),
+        min_keep=int(knobs.min_keep))
     if correction and not knobs.kscore_live:
         P = get_sketch_proj(cfg.head_dim, cfg.k_channel_group, cfg.sketch_dim, dev)
         dp.k_proxy = 1

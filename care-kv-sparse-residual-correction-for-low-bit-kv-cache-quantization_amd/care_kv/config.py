@@ -226,6 +226,11 @@ class ReadKnobs:
     ratio_k: float
     ratio_v: float
     kscore_live: bool
+    route_policy: int = 0        # 0 joint/separate by `joint`, 2 k_first, 3 adaptive (route only)
+    adaptive_score: bool = False  # read_budget_mode adaptive_score thresholds (route only)
+    rel_threshold: float = 0.0
+    abs_threshold: float = 0.0
+    min_keep: int = 0
 
 
 def resolve_read_knobs(cfg: CacheConfig, layer_id: int) -> ReadKnobs:
@@ -253,6 +258,11 @@ def resolve_read_knobs(cfg: CacheConfig, layer_id: int) -> ReadKnobs:
         ratio_k=res(cfg.read_budget_ratio_k, cfg.read_budget_ratio) * lm,
         ratio_v=res(cfg.read_budget_ratio_v, cfg.read_budget_ratio) * lm,
         kscore_live=os.environ.get("CAREKV_KSCORE_LIVE", "0") == "1",
+        route_policy={"k_first": 2, "adaptive": 3}.get(cfg.route_policy, 0),
+        adaptive_score=cfg.read_budget_mode == "adaptive_score",
+        rel_threshold=float(cfg.read_relative_threshold or 0.0),
+        abs_threshold=float(cfg.read_absolute_threshold or 0.0),
+        min_keep=int(cfg.read_min_keep or 0),
     )
 
 

@@ -33,7 +33,8 @@ WsLayout ws_layout(const carekv_arena& A, const carekv_decode_params& dp) {
   L.num = off; off += al(BH * L.nsplit * GQ * (long)D * 4);
   L.den = off; off += al(BH * L.nsplit * GQ * 4);
   const bool proxy = dp.k_proxy != 0 && dp.correction != 0;
-  L.xbuf = off; off += proxy ? al(BH * GQ * (long)Pm * 16 * 4) : 0;
+  const bool need_x = dp.correction != 0 && (dp.k_proxy != 0 || dp.route_policy == 3);
+  L.xbuf = off; off += need_x ? al(BH * GQ * (long)Pm * 16 * 4) : 0;
   L.prox = off; off += proxy ? al(BH * GQ * (long)Pm * 4 * 4) : 0;
   L.total = off;
   return L;
@@ -66,6 +67,10 @@ extern "C" int carekv_decode_attn(const carekv_arena* arena, const carekv_decode
   CAREKV_REQUIRE(!diag || diag_cap > 0, "diag_cap must be positive");
   const bool proxy = dp->k_proxy != 0 && dp->correction != 0;
   CAREKV_REQUIRE(!proxy || dp->sketch_proj, "the sketch proxy needs sketch_proj");
+  CAREKV_REQUIRE(dp->route_policy == 0 || dp->route_policy == 2 || dp->route_policy == 3,
+                 "route_policy must be 0 (joint flag), 2 (k_first) or 3 (adaptive)");
+  CAREKV_REQUIRE(dp->min_keep >= 0, "min_keep must be non-negative");
+  const bool need_x = dp->correction != 0 && (proxy || dp->route_policy == 3);
   CAREKV_REQUIRE(!proxy || (A.k_sketch && A.k_channel_group == 32 && A.sketch_dim >= 1 && A.sketch_dim <= 64),
                  "the sketch proxy needs k_sketch, k_channel_group 32 and sketch_dim in 1..64");
   const WsLayout L = ws_layout(A, *dp);
@@ -88,7 +93,10 @@ extern "C" int carekv_decode_attn(const carekv_arena* arena, const carekv_decode
   a.num = (float*)(ws + L.num);
   a.den = (float*)(ws + L.den);
   a.proxy = proxy ? 1 : 0;
-  a.xbuf = proxy ? (float*)(ws + L.xbuf) : nullptr;
+  a.xbuf = need_x ? (float*)(ws + L.xbuf) : nullptr;
+  a.policy = dp->route_policy == 0 ? (dp->joint ? 1 : 0) : dp->route_policy;
+  a.adaptive_score = dp->adaptive_score != 0;
+  a.rel_thr = dp->rel_threshold; a.abs_thr = dp->abs_threshold; a.min_keep = dp->min_keep;
   a.prox = proxy ? (float*)(ws + L.prox) : nullptr;
   a.sketch_proj = dp->sketch_proj;
   a.diag = diag; a.diag_cap = diag_cap;
@@ -97,9 +105,11 @@ extern "C" int carekv_decode_attn(const carekv_arena* arena, const carekv_decode
   a.k_cap = dp->k_cap; a.v_cap = dp->v_cap; a.F = L.F; a.ncand = L.ncand;
   a.sm_scale = dp->sm_scale; a.sens = dp->sensitivity; a.sens_d = (double)dp->sensitivity;
   a.k_corr_scale = dp->k_corr_scale;
-  // the KSCORE lambdas weigh the normalised scores of the live selector only
-  // (attention.py:838-844)
-  a.lam_k = proxy ? 1.f : dp->lambda_k; a.lam_v = proxy ? 1.f : dp->lambda_v;
+  // the KSCORE lambdas weigh the normalised scores of the live selector of
+  // vectorized_joint_correction only (attention.py:838-844); the router's
+  // policies and thresholds have none
+  const bool no_lam = proxy || dp->route_policy >= 2 || dp->adaptive_score;
+  a.lam_k = no_lam ? 1.f : dp->lambda_k; a.lam_v = no_lam ? 1.f : dp->lambda_v;
   a.sm_log2 = (float)((double)dp->sm_scale * 1.4426950408889634074);  // log2(e)
   a.inv_sqrt_d = (float)(1.0 / sqrt((double)A.head_dim));
   a.correction = dp->correction; a.kind = dp->kind; a.joint = dp->joint; a.normalize = dp->normalize;

@@ -21,7 +21,7 @@ struct DecodeArgs {
   float* ml;           // [B*Hkv][GQ][2]          global max (base 2) / sum
   float* num;          // [B*Hkv][nsplit][GQ][D]  apply partial numerators
   float* den;          // [B*Hkv][nsplit][GQ]     apply partial denominators
-  float* xbuf;         // [B*Hkv][GQ][Pmax][16]   fp32 base-2 logits x (sketch proxy only)
+  float* xbuf;         // [B*Hkv][GQ][Pmax][16]   fp32 base-2 logits x (sketch proxy, adaptive policy)
   float* prox;         // [B*Hkv][GQ][Pmax][4]    mass, boundary, vdiff (sketch proxy only)
   const float* sketch_proj;  // [32][sketch_dim] fp32 (sketch proxy only)
   int32_t* diag;
@@ -32,7 +32,9 @@ struct DecodeArgs {
   int correction, kind, joint, normalize, k_exact, budget_ratio, abs_k, abs_v;
   int SPA, napply;  // apply pass: pages per chunk (a multiple of SP) and chunk count (<= nsplit)
   int proxy;        // 1: K scores from the sketch proxy (prox records), 0: from the moments
-  double ratio_k, ratio_v, sens_d;
+  int policy;       // 0 separate, 1 joint, 2 k_first, 3 adaptive (ResidualRouter.route)
+  int adaptive_score, min_keep;  // read_budget_mode adaptive_score and its floor
+  double ratio_k, ratio_v, sens_d, rel_thr, abs_thr;
 };
 
 // Page record per (sequence, kv head, query, page), F floats:

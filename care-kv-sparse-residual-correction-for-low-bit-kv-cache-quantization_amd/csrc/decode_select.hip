@@ -118,6 +118,64 @@ __device__ Sel radix_select(const int* key, int lo, int hi, int k, int (*hist)[2
   return r;
 }
 
+// Selection masks of one query from the thresholds: keys above tau are
+// taken, ties at tau in candidate order (V ties of a joint selection after
+// every K tie).  which: bit 0 rewrites the K bits of the mask bytes, bit 1
+// the V bits; the other kind's bits are kept.  Each thread owns pages
+// tid, tid + kBlock, ...
+__device__ void write_masks(const int* key, uint8_t* maskq, int np, int k_cap, int v_cap, int nK, const Sel& sk,
+                            const Sel& sv, bool joint, int which, BlockScratch& bs) {
+  const int tid = threadIdx.x;
+  const bool rankK = sk.on && sk.take < sk.eq, rankV = sv.on && sv.take < sv.eq;
+  int eqK_total = 0;
+  if (joint && rankK) {  // V ties of a joint selection rank after every K tie
+    int c = 0;
+    for (int i = tid; i < nK; i += kBlock) c += key[i] >= 0 && (uint32_t)key[i] == sk.tau;
+    eqK_total = block_isum_fast(c, bs);
+  }
+  int eq_runK = 0, eq_runV = joint ? eqK_total : 0;
+  for (int p0 = 0; p0 < np; p0 += kBlock) {
+    const int p = p0 + tid;
+    const bool pv = p < np;
+    int uk[4] = {-1, -1, -1, -1}, uv[4] = {-1, -1, -1, -1};
+    int eqk = 0, eqv = 0;
+    if (pv) {
+      if (sk.on)
+        for (int r = 0; r < k_cap; ++r) {
+          uk[r] = key[p * k_cap + r];
+          eqk += uk[r] >= 0 && (uint32_t)uk[r] == sk.tau;
+        }
+      if (sv.on)
+        for (int r = 0; r < v_cap; ++r) {
+          uv[r] = key[nK + p * v_cap + r];
+          eqv += uv[r] >= 0 && (uint32_t)uv[r] == sv.tau;
+        }
+    }
+    int ek = 0, ev = 0;
+    if (rankK) { int tot; ek = block_excl_scan(eqk, bs, &tot) + eq_runK; eq_runK += tot; }
+    if (rankV) { int tot; ev = block_excl_scan(eqv, bs, &tot) + eq_runV; eq_runV += tot; }
+    unsigned bits = 0;
+    for (int r = 0; r < k_cap; ++r) {
+      if (uk[r] < 0) continue;
+      const uint32_t x = (uint32_t)uk[r];
+      bool take = x > sk.tau;
+      if (x == sk.tau) { take = ek < sk.take; ++ek; }
+      if (take) bits |= 1u << r;
+    }
+    for (int r = 0; r < v_cap; ++r) {
+      if (uv[r] < 0) continue;
+      const uint32_t x = (uint32_t)uv[r];
+      bool take = x > sv.tau;
+      if (x == sv.tau) { take = ev < sv.take; ++ev; }
+      if (take) bits |= 1u << (4 + r);
+    }
+    if (pv) {
+      const unsigned keep = (which & 1 ? 0u : 15u) | (which & 2 ? 0u : 0xf0u);
+      maskq[p] = (uint8_t)((maskq[p] & keep) | bits);
+    }
+  }
+}
+
 constexpr int kLdsCand = 8192;  // candidates kept in LDS (32 KB); more go to the workspace
 
 // Work-groups are dealt to the 8 XCDs round-robin by linear id; the GQ
@@ -308,8 +366,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
   bud_k = min(bud_k, totk);
   bud_v = min(bud_v, totv);
   const bool haveK = want_k && bud_k > 0, haveV = want_v && bud_v > 0;
-  const bool do_norm = a.normalize && a.kind == 0 && haveK && haveV;
-  const bool joint = a.joint && a.kind == 0 && haveK && haveV;
+  // policies 2/3 and the score thresholds exist only in ResidualRouter.route,
+  // which normalises each kind whenever kind is "both" (residual_router.py:292-303)
+  const int pol = a.policy;
+  const bool route = pol >= 2 || a.adaptive_score;
+  const bool do_norm = a.normalize && a.kind == 0 && (route || (haveK && haveV));
+  const bool joint = pol == 1 && a.kind == 0 && haveK && haveV;
 
   // ---- keys: non-negative float bits of the (normalised) scores, -1 empty
   {
@@ -327,63 +389,116 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
     __syncthreads();
   }
 
-  // ---- thresholds
+  // ---- how many of each kind (residual_router.py:305-365)
+  int takeK = haveK ? min(bud_k, n_k) : 0, takeV = haveV ? min(bud_v, n_v) : 0;
+  if (pol == 2) {
+    // k_first: the K budget first; the rest of the joint allowance (the V
+    // budget, the budgets being capped at the candidate counts) on the V
+    // candidates scoring at least their mean
+    takeV = 0;
+    if (haveV) {
+      float sv_loc = 0.f;
+      for (int i = nK + tid; i < nK + nV; i += kBlock)
+        if (key[i] >= 0) sv_loc += __int_as_float(key[i]);
+      const float vmean = block_sum_fast(sv_loc, bs) / (float)n_v;
+      int ge = 0;
+      for (int i = nK + tid; i < nK + nV; i += kBlock) ge += key[i] >= 0 && __int_as_float(key[i]) >= vmean;
+      takeV = min(bud_v, block_isum_fast(ge, bs));
+    }
+  } else if (pol == 3) {
+    // adaptive: the joint allowance split by the attention entropy,
+    // v_frac = H(max(a, 1e-6)) / log(max(N, 2))
+    const int total = bud_k + bud_v;
+    takeK = takeV = 0;
+    if (total > 0) {
+      const float* xq = a.xbuf + bq * a.Pmax * 16;
+      float h = 0.f;
+      int nt = 0;
+      for (int i = tid; i < np * 16; i += kBlock) {
+        const int nvp = A.valid[pg_base + (i >> 4)];
+        if ((i & 15) >= nvp) continue;
+        ++nt;
+        const float at = L > 0.f ? __builtin_amdgcn_exp2f(xq[i] - M) / L : 0.f;
+        const float ac = fmaxf(at, kEps);
+        h += ac * logf(ac);
+      }
+      const float ent = -block_sum_fast(h, bs);
+      const int N = block_isum_fast(nt, bs);
+      const double vfrac = fmin(1.0, fmax(0.0, (double)ent / log((double)max(N, 2))));
+      const int v_alloc = max(0, (int)rint((double)total * vfrac));  // Python round: half to even
+      const int k_alloc = max(0, total - v_alloc);
+      takeK = want_k ? min(k_alloc, n_k) : 0;
+      takeV = want_v ? min(v_alloc, n_v) : 0;
+    }
+  }
+
+  // ---- thresholds and masks
   Sel sk{0u, 0, 0, false}, sv{0u, 0, 0, false};
   if (joint) {
     const int mb = min(bud_k + bud_v, n_k + n_v);
     sk = radix_select(key, 0, nK + nV, mb, hist, bs);
     sv = sk;
   } else {
-    if (haveK) sk = radix_select(key, 0, nK, min(bud_k, n_k), hist, bs);
-    if (haveV) sv = radix_select(key, nK, nK + nV, min(bud_v, n_v), hist, bs);
+    if (takeK > 0) sk = radix_select(key, 0, nK, takeK, hist, bs);
+    if (takeV > 0) sv = radix_select(key, nK, nK + nV, takeV, hist, bs);
   }
+  write_masks(key, maskq, np, k_cap, v_cap, nK, sk, sv, joint, 3, bs);
 
-  // ---- masks: one sweep over the pages; ties at a threshold are taken in
-  // candidate order (all K candidates precede the V ones)
-  const bool rankK = sk.on && sk.take < sk.eq, rankV = sv.on && sv.take < sv.eq;
-  int eqK_total = 0;
-  if (joint && rankK) {  // V ties of a joint selection rank after every K tie
-    int c = 0;
-    for (int i = tid; i < nK; i += kBlock) c += key[i] >= 0 && (uint32_t)key[i] == sk.tau;
-    eqK_total = block_isum_fast(c, bs);
-  }
-  int eq_runK = 0, eq_runV = joint ? eqK_total : 0;
-  for (int p0 = 0; p0 < np; p0 += kBlock) {
-    const int p = p0 + tid;
-    const bool pv = p < np;
-    int uk[4] = {-1, -1, -1, -1}, uv[4] = {-1, -1, -1, -1};
-    int eqk = 0, eqv = 0;
-    if (pv) {
-      if (sk.on)
-        for (int r = 0; r < k_cap; ++r) {
-          uk[r] = key[p * k_cap + r];
-          eqk += uk[r] >= 0 && (uint32_t)uk[r] == sk.tau;
+  // ---- read_budget_mode adaptive_score: per kind, keep the selected slots
+  // whose score passes max(rel * top, abs) (top = the kind's best selected
+  // score), or the best min_keep of them when fewer pass
+  // (residual_router.py:366-410)
+  if (a.adaptive_score) {
+    for (int kind = 0; kind < 2; ++kind) {
+      const int lo = kind == 0 ? 0 : nK, cap = kind == 0 ? k_cap : v_cap;
+      float top = 0.f;
+      int nsel = 0;
+      for (int p = tid; p < np; p += kBlock) {
+        const unsigned bits = kind == 0 ? (maskq[p] & 15u) : (maskq[p] >> 4);
+        for (int r = 0; r < cap; ++r)
+          if ((bits >> r) & 1u) {
+            top = fmaxf(top, __int_as_float(key[lo + p * cap + r]));
+            ++nsel;
+          }
+      }
+      top = block_max_fast(top, bs);
+      nsel = block_isum_fast(nsel, bs);
+      if (nsel == 0) continue;
+      auto passes = [&](float x) {
+        return (a.rel_thr <= 0.0 || (double)x >= a.rel_thr * (double)top) &&
+               (a.abs_thr <= 0.0 || (double)x >= a.abs_thr);
+      };
+      int kept = 0;
+      for (int p = tid; p < np; p += kBlock) {
+        const unsigned bits = kind == 0 ? (maskq[p] & 15u) : (maskq[p] >> 4);
+        for (int r = 0; r < cap; ++r)
+          if (((bits >> r) & 1u) && passes(__int_as_float(key[lo + p * cap + r]))) ++kept;
+      }
+      kept = block_isum_fast(kept, bs);
+      if (a.min_keep > 0 && kept < a.min_keep) {
+        // the best min_keep selected ones, ties in candidate order
+        for (int p = tid; p < np; p += kBlock) {
+          const unsigned bits = kind == 0 ? (maskq[p] & 15u) : (maskq[p] >> 4);
+          for (int r = 0; r < cap; ++r)
+            if (!((bits >> r) & 1u)) key[lo + p * cap + r] = -1;
         }
-      if (sv.on)
-        for (int r = 0; r < v_cap; ++r) {
-          uv[r] = key[nK + p * v_cap + r];
-          eqv += uv[r] >= 0 && (uint32_t)uv[r] == sv.tau;
+        __syncthreads();
+        const Sel s2 = radix_select(key, lo, lo + np * cap, min(a.min_keep, nsel), hist, bs);
+        const Sel off{0u, 0, 0, false};
+        write_masks(key, maskq, np, k_cap, v_cap, nK, kind == 0 ? s2 : off, kind == 0 ? off : s2, false,
+                    kind == 0 ? 1 : 2, bs);
+      } else {
+        for (int p = tid; p < np; p += kBlock) {
+          unsigned m = maskq[p];
+          for (int r = 0; r < cap; ++r) {
+            const unsigned bit = 1u << (kind == 0 ? r : 4 + r);
+            if ((m & bit) && !passes(__int_as_float(key[lo + p * cap + r]))) m &= ~bit;
+          }
+          maskq[p] = (uint8_t)m;
         }
+      }
+      __syncthreads();
     }
-    int ek = 0, ev = 0;
-    if (rankK) { int tot; ek = block_excl_scan(eqk, bs, &tot) + eq_runK; eq_runK += tot; }
-    if (rankV) { int tot; ev = block_excl_scan(eqv, bs, &tot) + eq_runV; eq_runV += tot; }
-    unsigned bits = 0;
-    for (int r = 0; r < k_cap; ++r) {
-      if (uk[r] < 0) continue;
-      const uint32_t x = (uint32_t)uk[r];
-      bool take = x > sk.tau;
-      if (x == sk.tau) { take = ek < sk.take; ++ek; }
-      if (take) bits |= 1u << r;
-    }
-    for (int r = 0; r < v_cap; ++r) {
-      if (uv[r] < 0) continue;
-      const uint32_t x = (uint32_t)uv[r];
-      bool take = x > sv.tau;
-      if (x == sv.tau) { take = ev < sv.take; ++ev; }
-      if (take) bits |= 1u << (4 + r);
-    }
-    if (pv) maskq[p] = (uint8_t)bits;
   }
   if (!diagp) return;
   // ---- diag: selected candidates in ascending candidate order (each

@@ -113,7 +113,7 @@ void decode_stream_kernel(carekv_arena A, DecodeArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) x[i] = (4 * lj + i < nv) ? sacc[i] * sm_log2 : -INFINITY;
     }
-    if (a.proxy && corr && cm.meta && ln < GQ)  // logits for the proxy's margins
+    if (a.xbuf && corr && ln < GQ)  // logits for the proxy's margins / the entropy
       *reinterpret_cast<float4*>(a.xbuf + (((long)bk * GQ + ln) * a.Pmax + p) * 16 + 4 * lj) =
           make_float4(x[0], x[1], x[2], x[3]);
     const float mx = col_max(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));

@@ -198,7 +198,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     float x[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) x[i] = (4 * sbk + i < my_nv) ? (sa0[i] + sa1[i]) * sm_log2 : -INFINITY;
-    if (a.proxy && corr && sc < GQ && my_meta != 0 && my_nv > 0)  // logits for the proxy's margins
+    if (a.xbuf && corr && sc < GQ && my_nv > 0)  // logits for the proxy's margins / the entropy
       *reinterpret_cast<float4*>(a.xbuf + (((long)bk * GQ + sc) * a.Pmax + p0 + lj) * 16 + 4 * sbk) =
           make_float4(x[0], x[1], x[2], x[3]);
     const float mx = pair32_max(pair16_max(row4_max(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])))));

@@ -156,6 +156,13 @@ typedef struct carekv_decode_params {
   const float* sketch_proj;/* device [k_channel_group][sketch_dim] fp32, the
                             * get_sketch_proj matrix (residual_store.py:206-214);
                             * required when k_proxy = 1                       */
+  int32_t route_policy;    /* 0: `joint` decides (joint / separate); 2 k_first,
+                            * 3 adaptive: the policies of ResidualRouter.route
+                            * (residual_router.py:322-365)                     */
+  int32_t adaptive_score;  /* read_budget_mode adaptive_score: per-kind score
+                            * thresholds after the policy (:366-410)          */
+  double rel_threshold, abs_threshold; /* CAREKV_READ_RELATIVE/ABSOLUTE_THRESHOLD */
+  int32_t min_keep;        /* CAREKV_READ_MIN_KEEP                             */
 } carekv_decode_params;
 
 /* q, out: fp16 [batch][n_heads][head_dim].  diag (optional, NULL to skip):

@@ -11,6 +11,10 @@ Follows ``attention.py`` of the reference:
     no prefilter, no chunking, no selector/position variants, raw_error V
     score, no K clamp/guard)
   * ``_resolve_read_budgets``      -- residual_router.py:37-76
+  * ``route_selection``            -- the selection of ResidualRouter.route
+    (residual_router.py:275-410): per-kind normalisation, the joint /
+    separate / k_first / adaptive policies and the adaptive_score
+    thresholds, on given per-query score rows
   * ``decode_attention``           -- attention.py:979-1077 with the
     correction call swapped for the batched joint correction over the GQA
     group's queries (per-query-row semantics, attention.py:830-875).
@@ -144,6 +148,72 @@ def build_k_slot_index(cache: OCache, layer_id, kv_head, page_ids):
     return out
 
 
+def route_selection(sK, sV, bk, bv, policy, kind, normalize, A_row=None, adaptive_score=False, rel_thr=0.0,
+                    abs_thr=0.0, min_keep=0):
+    """residual_router.py:275-410 for one query: sK / sV are the raw K / V
+    candidate scores (None when that kind has no candidates), bk / bv the
+    resolved budgets.  Python-float arithmetic and stable sorts as in the
+    reference.  Returns boolean selection rows (None for an absent kind)."""
+    kc = [] if sK is None else [(float(s), i) for i, s in enumerate(sK)]
+    vc = [] if sV is None else [(float(s), i) for i, s in enumerate(sV)]
+    selk = None if sK is None else np.zeros(len(kc), bool)
+    selv = None if sV is None else np.zeros(len(vc), bool)
+    if len(kc) + len(vc) == 0 or (bk == 0 and bv == 0):
+        return selk, selv
+
+    def _norm(c):
+        if not c:
+            return c
+        mean = sum(abs(x[0]) for x in c) / len(c)
+        sc = mean if mean > EPS else EPS
+        return [(x[0] / sc, x[1]) for x in c]
+    if normalize and kind == "both":
+        kc, vc = _norm(kc), _norm(vc)
+    desc = lambda c: sorted(c, key=lambda x: x[0], reverse=True)  # noqa: E731  stable
+    if policy == "joint":
+        mb = bk + bv if (bk > 0 and bv > 0) else max(bk, bv)
+        allc = [("K",) + x for x in kc] + [("V",) + x for x in vc]
+        sel = sorted(allc, key=lambda x: x[1], reverse=True)[:mb]
+    elif policy == "k_first":
+        kp = desc(kc)[:bk]
+        rem = max(0, bk + bv - len(kp))
+        vs = desc(vc)
+        vp = []
+        if vs and rem > 0:
+            vmean = sum(x[0] for x in vs) / len(vs)
+            vp = [x for x in vs if x[0] >= vmean][:rem]
+        sel = [("K",) + x for x in kp] + [("V",) + x for x in vp]
+    elif policy == "adaptive":
+        total = bk + bv
+        sel = []
+        if total > 0:
+            a = np.maximum(np.asarray(A_row, F32), F32(EPS))
+            ent = float(-(a * np.log(a)).sum(dtype=F32))
+            max_ent = math.log(max(a.size, 2))
+            v_frac = max(0.0, min(1.0, ent / max_ent))
+            v_alloc = max(0, int(round(total * v_frac)))
+            k_alloc = max(0, total - v_alloc)
+            sel = [("K",) + x for x in desc(kc)[:k_alloc]] + [("V",) + x for x in desc(vc)[:v_alloc]]
+    else:
+        sel = [("K",) + x for x in desc(kc)[:bk]] + [("V",) + x for x in desc(vc)[:bv]]
+    if adaptive_score:
+        def _filter(lst):
+            if not lst:
+                return lst
+            top = float(abs(lst[0][1]))
+            kept = [c for c in lst if (rel_thr <= 0 or abs(c[1]) >= rel_thr * top)
+                    and (abs_thr <= 0 or abs(c[1]) >= abs_thr)]
+            if min_keep > 0 and len(kept) < min_keep:
+                kept = lst[:min(min_keep, len(lst))]
+            return kept
+        sk_ = sorted([c for c in sel if c[0] == "K"], key=lambda c: c[1], reverse=True)
+        sv_ = sorted([c for c in sel if c[0] == "V"], key=lambda c: c[1], reverse=True)
+        sel = _filter(sk_) + _filter(sv_)
+    for c in sel:
+        (selk if c[0] == "K" else selv)[c[2]] = True
+    return selk, selv
+
+
 def topk_lowest_index(scores, k):
     """Per-row top-k with ties resolved toward the lowest index."""
     order = np.argsort(-scores, axis=1, kind="stable")
@@ -188,8 +258,10 @@ def vectorized_joint_correction(cache: OCache, layer_id, kv_head, page_ids, Q_q,
         return delta
 
     kcg = cfg.k_channel_group
+    # policies and thresholds only ResidualRouter.route has
+    route_mode = policy in ("k_first", "adaptive") or cfg.read_budget_mode == "adaptive_score"
     score_K = None
-    if want_k and bk > 0:
+    if want_k and (bk > 0 or route_mode):
         score_K = np.zeros((Qn, n_k), F32)
         need_proxy = not kscore_live
         if need_proxy:
@@ -222,14 +294,22 @@ def vectorized_joint_correction(cache: OCache, layer_id, kv_head, page_ids, Q_q,
             qdr = np.abs((qs * kx["sketch"][si][None]).sum(1, dtype=F32))
             score_K[:, si] = mass * qdr * boundary * pvd * F32(sens)
     score_V = None
-    if want_v and bv > 0:
+    if want_v and (bv > 0 or route_mode):
         V_resid, v_starts, v_lens, v_err, _ = v_idx
         ar = np.arange(N)[None]
         v_mask = ((ar >= v_starts[:, None]) & (ar < (v_starts + v_lens)[:, None])).astype(F32)
         score_V = (A @ v_mask.T) * v_err[None]
         score_V = (score_V * F32(sens)).astype(F32)
 
-    if score_normalize and kind == "both" and score_K is not None and score_V is not None:
+    if route_mode:
+        sK, sV = score_K, score_V  # route_selection normalises per kind itself
+        if score_normalize and kind == "both":  # normalised copies for the diag
+            if sK is not None:
+                sK = sK / np.maximum(np.abs(sK).mean(1, keepdims=True, dtype=F32), F32(EPS))
+            if sV is not None:
+                sV = sV / np.maximum(np.abs(sV).mean(1, keepdims=True, dtype=F32), F32(EPS))
+        score_K_raw, score_V_raw = score_K, score_V
+    elif score_normalize and kind == "both" and score_K is not None and score_V is not None:
         nk = np.maximum(np.abs(score_K).mean(1, keepdims=True, dtype=F32), F32(EPS))
         nv_ = np.maximum(np.abs(score_V).mean(1, keepdims=True, dtype=F32), F32(EPS))
         sK, sV = score_K / nk, score_V / nv_
@@ -247,6 +327,18 @@ def vectorized_joint_correction(cache: OCache, layer_id, kv_head, page_ids, Q_q,
             sel_k[:] = fk
         if sel_v is not None:
             sel_v[:] = fv
+    elif route_mode:
+        for j in range(Qn):
+            rk, rv = route_selection(None if score_K_raw is None else score_K_raw[j],
+                                     None if score_V_raw is None else score_V_raw[j], bk, bv, policy,
+                                     kind, score_normalize, A_row=A[j],
+                                     adaptive_score=cfg.read_budget_mode == "adaptive_score",
+                                     rel_thr=cfg.read_relative_threshold, abs_thr=cfg.read_absolute_threshold,
+                                     min_keep=cfg.read_min_keep)
+            if rk is not None:
+                sel_k[j] = rk
+            if rv is not None:
+                sel_v[j] = rv
     elif policy == "joint" and kind == "both" and sK is not None and sV is not None:
         mb = (bk + bv) if (bk > 0 and bv > 0) else max(bk, bv)
         merged = np.concatenate([sK, sV], axis=1)

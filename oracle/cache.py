@@ -46,6 +46,9 @@ class OCfg:
     read_abs_v: int = 0
     route_policy: str = "joint"
     budget_policy: str = "uniform"
+    read_relative_threshold: float = 0.0
+    read_absolute_threshold: float = 0.0
+    read_min_keep: int = 0
 
     def __post_init__(self):
         if self.layer_sensitivity is None:

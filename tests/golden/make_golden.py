@@ -257,6 +257,80 @@ def golden_decode_proxy(ck):
                  read_k=16, read_v=16, n_append=27, kscore_live=False)
 
 
+ROUTE_VARIANTS = [  # (route_policy, adaptive_score (rel, abs, min_keep) or None)
+    ("joint", None), ("separate", None), ("k_first", None), ("adaptive", None),
+    ("joint", (0.5, 0.0, 0)), ("separate", (0.0, 1.5, 3)), ("k_first", (0.8, 0.0, 2)), ("adaptive", (0.3, 0.9, 0)),
+]
+
+
+def golden_route(ck):
+    """ResidualRouter.route (residual_router.py:88-452) selections per query
+    under every route_policy and the adaptive_score thresholds, with the raw
+    candidate scores of vectorized_joint_correction (KSCORE_LIVE=0, the same
+    score formulas at sensitivity 1) and the attention rows they came from."""
+    from CARE_KV.care_kv.attention import vectorized_joint_correction, set_chunk_recorder
+    _set_env(CAREKV_STORE_POLICY="residual_kind_aware", CAREKV_PREFILL_RESIDUAL_KIND="both",
+             CAREKV_K_CORRECTION_MODE="exact", CAREKV_KSCORE_LIVE="0", CAREKV_SCORE_NORMALIZE="1",
+             CAREKV_DEBUG_STATS="0")
+    Hq, Hkv, D, T = 8, 2, 64, 300
+    cfg = ck.CacheConfig(num_layers=1, num_heads=Hq, num_kv_heads=Hkv, head_dim=D, page_size=16, max_pages=64,
+                         base_bits=3, group_size=32, k_channel_group=32, v_token_block=4, sketch_dim=32,
+                         packed_base=True, scale_quant="int8", read_budget_ratio=0.0, read_budget_mode="absolute",
+                         read_abs_k=6, read_abs_v=6, route_policy="joint", store_budget_mode="absolute",
+                         store_abs_k=2, store_abs_v=2)
+    cache = ck.CAREKVCache(cfg, torch.device("cpu"))
+    layer = _selector_layer(ck, cfg)
+    K, V = _gen_kv(7, Hkv, T, D, outlier_mult=8.0)
+    Qh = torch.randn(Hq, D, generator=torch.Generator().manual_seed(8)).half()
+    for h in range(Hkv):
+        layer._write_pages_for_kv_head(cache, h, K[h], V[h], token_start_abs=0, sink_tokens=4)
+    out = {}
+    grp = Hq // Hkv
+    sf = 1.0 / math.sqrt(D)
+    for h in range(Hkv):
+        pids = cache.all_page_ids(0, h)
+        Kc, Ks, Vc, Vs, _ = cache.read_base_concat(0, h, pids)
+        N = Kc.shape[0]
+        Kb = ck.dequantize(Kc, Ks, (N, D), layer.base_qcfg).float()
+        Vb = ck.dequantize(Vc, Vs, (N, D), layer.base_qcfg).float()
+        heads = list(range(h * grp, (h + 1) * grp))
+        S = torch.stack([(Kb @ Qh[i].float()) * sf for i in heads])
+        A = torch.softmax(S, dim=1)
+        O = torch.stack([(A[j].unsqueeze(-1) * Vb).sum(0) for j in range(grp)])
+        rec = []
+        set_chunk_recorder(rec)
+        vectorized_joint_correction(cache, cfg, layer.router, 0, h, pids, Q_q=Qh[heads].float(), S=S, A=A,
+                                    V_base=Vb, O_base=O, kind="both", k_corr_scale=0.1, score_normalize=True)
+        set_chunk_recorder(None)
+        out[f"h{h}_score_K"] = rec[0]["score_K"].numpy()
+        out[f"h{h}_score_V"] = rec[0]["score_V"].numpy()
+        out[f"h{h}_A"] = A.numpy()
+        kc, vc = [], []
+        for pid in pids:
+            m = cache.meta_table[0][h][pid]
+            nv = int(cache.valid_tokens[0, h, pid].item())
+            if nv == 0 or m is None:
+                continue
+            kc += [(pid, cg) for cg, sl in enumerate(m.k_residual_slots) if sl >= 0]
+            vc += [(pid, vb) for vb, sl in enumerate(m.v_residual_slots) if sl >= 0 and vb * 4 < nv]
+        out[f"h{h}_kcand"] = np.array(kc, np.int32).reshape(-1, 2)
+        out[f"h{h}_vcand"] = np.array(vc, np.int32).reshape(-1, 2)
+        for vi, (pol, asc) in enumerate(ROUTE_VARIANTS):
+            cfg.route_policy = pol
+            cfg.read_budget_mode = "adaptive_score" if asc else "absolute"
+            if asc:
+                cfg.read_relative_threshold, cfg.read_absolute_threshold, cfg.read_min_keep = asc
+            for j, qh in enumerate(heads):
+                ks, vs = layer.router.route(cache=cache, kv_head=h, page_ids=pids, q=Qh[qh].float(), s_base=S[j],
+                                            a_base=A[j], O_base=O[j], V_base_full=Vb, kind="both",
+                                            score_normalize=True)
+                out[f"h{h}_v{vi}_q{j}_k"] = np.array([(p, c) for p, c, _ in ks], np.int32).reshape(-1, 2)
+                out[f"h{h}_v{vi}_q{j}_v"] = np.array([(p, b) for p, b, _ in vs], np.int32).reshape(-1, 2)
+        cfg.route_policy, cfg.read_budget_mode = "joint", "absolute"
+    out["budgets"] = np.array([6, 6], np.int32)
+    np.savez_compressed(os.path.join(HERE, "route_d64.npz"), **out)
+
+
 def golden_reference_fixture(ck):
     """The reference's own test fixture (tests/test_vectorized_carekv.py:30-58):
     D=32, page 8, g 8, kcg 16, vtb 4, sketch 4, SK=SV=2, fp32 inputs."""
@@ -340,7 +414,7 @@ def golden_activation_slices():
     np.savez_compressed(os.path.join(HERE, "activations_3d_slices.npz"), **out)
 
 
-PARTS = ("activations", "sketch", "store", "append", "decode", "decode_proxy", "fixture")
+PARTS = ("activations", "sketch", "store", "append", "decode", "decode_proxy", "route", "fixture")
 
 if __name__ == "__main__":
     # CAREKV_GOLDEN_PARTS=decode_proxy,... writes only those fixtures
@@ -353,7 +427,7 @@ if __name__ == "__main__":
     if any(p != "activations" for p in parts):
         ck = _import_reference()
         fns = dict(sketch=golden_sketch, store=golden_store, append=golden_append, decode=golden_decode,
-                   decode_proxy=golden_decode_proxy, fixture=golden_reference_fixture)
+                   decode_proxy=golden_decode_proxy, route=golden_route, fixture=golden_reference_fixture)
         for p in parts:
             if p in fns:
                 fns[p](ck)

@@ -302,3 +302,72 @@ def test_batched_sequences_match_single(paper_env):
     for s in range(B):
         one = care_kv.decode_attention(cache, 0, q[s:s + 1], seqs=[s])
         assert torch.equal(both[s], one[0])
+
+
+# ------------------------------------------------------------------ router policies vs oracle
+POLICY_CASES = [
+    # policy, adaptive_score (rel, abs, min_keep) or None, live
+    ("k_first", None, True),
+    ("adaptive", None, True),
+    ("k_first", None, False),
+    ("adaptive", None, False),
+    ("joint", (0.5, 0.0, 0), True),
+    ("separate", (0.0, 1.5, 3), False),
+    ("k_first", (0.8, 0.0, 2), True),
+    ("adaptive", (0.3, 0.9, 0), False),
+]
+
+
+@pytest.mark.parametrize("D,Hq,Hkv,T", [(128, 8, 2, 700), (64, 16, 2, 400)], ids=["D128g4", "D64g8"])
+@pytest.mark.parametrize("case", POLICY_CASES,
+                         ids=[f"{c[0]}-{'as' if c[1] else 'fixed'}-{'live' if c[2] else 'proxy'}" for c in POLICY_CASES])
+def test_decode_route_policies_vs_oracle(paper_env, case, D, Hq, Hkv, T):
+    """The route-only policies (k_first, adaptive entropy split) and the
+    adaptive_score thresholds (residual_router.py:305-410) on the GPU vs the
+    oracle's route_selection, selections up to epsilon ties and outputs."""
+    import care_kv
+    pol, asc, live = case
+    print(f"route policy case {case} D={D} Hq={Hq} Hkv={Hkv} T={T}", flush=True)
+    paper_env.setenv("CAREKV_KSCORE_LIVE", "1" if live else "0")
+    paper_env.setenv("CAREKV_K_CORRECTION_MODE", "exact")
+    eps = 1e-4 if live else 2e-3
+    rng = np.random.default_rng(D + Hq + T + len(pol))
+    K = rng.standard_normal((Hkv, T, D)).astype(F16)
+    V = rng.standard_normal((Hkv, T, D)).astype(F16)
+    K[:, :, rng.permutation(D)[:3]] *= F16(6.0)
+    Qh = rng.standard_normal((Hq, D)).astype(F16)
+    rel, ab, keep = asc if asc else (0.0, 0.0, 0)
+    common = dict(num_layers=1, num_heads=Hq, num_kv_heads=Hkv, head_dim=D, page_size=16, max_pages=T // 16 + 4,
+                  base_bits=3, group_size=32, k_channel_group=32, v_token_block=4, sketch_dim=32,
+                  read_budget_mode="adaptive_score" if asc else "absolute", read_abs_k=6, read_abs_v=6,
+                  route_policy=pol, store_budget_mode="absolute", store_abs_k=2, store_abs_v=2,
+                  read_relative_threshold=rel, read_absolute_threshold=ab, read_min_keep=keep)
+    oc = OCache(OCfg(**common))
+    for h in range(Hkv):
+        write_pages_for_kv_head(oc, 0, h, K[h], V[h])
+    cfg = care_kv.CacheConfig(packed_base=True, scale_quant="int8", read_budget_ratio=0.0, **common)
+    cache = care_kv.CAREKVCache(cfg, device="cuda")
+    cache.write_prefill(0, torch.from_numpy(K).cuda(), torch.from_numpy(V).cuda())
+    torch.cuda.synchronize()
+    odiag = {}
+    o_out = oracle_decode(oc, 0, Qh, k_mode="exact", kind="both", k_corr_scale=0.1, score_normalize=True,
+                          kscore_live=live, diag=odiag)
+    out, diag = care_kv.decode_attention(cache, 0, torch.from_numpy(Qh).cuda().unsqueeze(0), diag_cap=1024)
+    out = out[0].cpu().numpy().astype(F32)
+    diag = diag[0].cpu().numpy()
+    grp = Hq // Hkv
+    n_sel = 0
+    for h in range(Hkv):
+        d = odiag[h]
+        Kc, Vc = oracle_candidates(oc, 0, h, oc.next_page[0][h])
+        ref_rows = oracle_selection(d, Kc, Vc)
+        for j in range(grp):
+            mine = set(decode_diag(diag[h * grp + j]))
+            n_sel += len(ref_rows[j])
+            for kind in (0, 1):  # the route policies and thresholds act per kind
+                a_ = {c for c in mine if c[0] == kind}
+                b_ = {c for c in ref_rows[j] if c[0] == kind}
+                assert ties_explain(a_, b_, d, Kc, Vc, j, eps=eps), (h, j, kind, sorted(a_ ^ b_))
+    assert n_sel > 0
+    err = np.abs(out - o_out.astype(F32))
+    assert err.max() <= 2e-3, err.max()

@@ -385,3 +385,41 @@ def test_prefill_attention_causal_and_gqa_properties():
     On, _ = causal_attention_pure(Qh, K, V, causal=False)
     assert np.array_equal(On[:, -1], O[:, -1])
     assert not np.array_equal(On[:, 0], O[:, 0])
+
+
+# ------------------------------------------------------------ router policies
+def test_route_selection_matches_reference(golden):
+    """route_selection on the reference's raw candidate scores reproduces
+    ResidualRouter.route's selections under every route_policy and the
+    adaptive_score thresholds (fixture written by make_golden.py from
+    residual_router.py:88-452), up to swaps inside a 1e-5 relative tie."""
+    from oracle.attention import route_selection
+    g = golden("route_d64.npz")
+    variants = [("joint", None), ("separate", None), ("k_first", None), ("adaptive", None),
+                ("joint", (0.5, 0.0, 0)), ("separate", (0.0, 1.5, 3)), ("k_first", (0.8, 0.0, 2)),
+                ("adaptive", (0.3, 0.9, 0))]
+    bk, bv = (int(x) for x in g["budgets"])
+    n_checked = 0
+    for h in range(2):
+        sK, sV, A = g[f"h{h}_score_K"], g[f"h{h}_score_V"], g[f"h{h}_A"]
+        kc = [tuple(x) for x in g[f"h{h}_kcand"].tolist()]
+        vc = [tuple(x) for x in g[f"h{h}_vcand"].tolist()]
+        for vi, (pol, asc) in enumerate(variants):
+            for j in range(sK.shape[0]):
+                rel, ab, keep = asc if asc else (0.0, 0.0, 0)
+                selk, selv = route_selection(sK[j], sV[j], bk, bv, pol, "both", True, A_row=A[j],
+                                             adaptive_score=asc is not None, rel_thr=rel, abs_thr=ab,
+                                             min_keep=keep)
+                mine_k = {kc[i] for i in np.nonzero(selk)[0]}
+                mine_v = {vc[i] for i in np.nonzero(selv)[0]}
+                ref_k = {tuple(x) for x in g[f"h{h}_v{vi}_q{j}_k"].tolist()}
+                ref_v = {tuple(x) for x in g[f"h{h}_v{vi}_q{j}_v"].tolist()}
+                for mine, ref, cand, s in ((mine_k, ref_k, kc, sK[j]), (mine_v, ref_v, vc, sV[j])):
+                    if mine == ref:
+                        continue
+                    val = {c: float(s[i]) for i, c in enumerate(cand)}
+                    kth = min(val[c] for c in ref) if ref else 0.0
+                    assert all(abs(val[c] - kth) <= 1e-5 * max(abs(kth), 1e-30) for c in mine ^ ref), \
+                        (h, pol, asc, j, sorted(mine ^ ref))
+                n_checked += 1
+    assert n_checked == 2 * len(variants) * 4
