@@ -2,10 +2,11 @@
 the evaluation-harness entry point that configures CARE-KV through the
 ``CAREKV_*`` environment and patches a LLaMA model.
 
-Same constructor, ``setup_model`` environment and reporting methods.  Only the
-uniform base quantizer and the fixed read budget are built; the side-buffer
-base quantizers (KIVI / RotateKV / KVQuant) and the adaptive read budget
-raise ``NotImplementedError``.  ``setup_model`` also accepts an already built
+Same constructor, ``setup_model`` environment and reporting methods, with
+the fixed (RK/RV) and the adaptive (adaptive_score with rel_threshold under
+the max_rk/max_rv caps) read budgets.  Only the uniform base quantizer is
+built; the side-buffer base quantizers (KIVI / RotateKV / KVQuant) raise
+``NotImplementedError``.  ``setup_model`` also accepts an already built
 ``nn.Module`` (a random-init model when no checkpoint is at hand)."""
 from __future__ import annotations
 
@@ -39,8 +40,6 @@ class CAREKVAdapter:
             raise NotImplementedError(f"base_quantizer={base_quantizer!r}: only the uniform packed base is built")
         if mode not in ("fixed", "adaptive"):
             raise ValueError(f"mode must be 'fixed' or 'adaptive' (got {mode!r})")
-        if mode == "adaptive":
-            raise NotImplementedError("the adaptive_score read budget is not built")
         self.mode, self.rel_threshold = mode, rel_threshold
         self.sk, self.sv, self.rk, self.rv = sk, sv, rk, rv
         self.max_rk, self.max_rv = max_rk, max_rv
@@ -52,7 +51,8 @@ class CAREKVAdapter:
         self.bits_k = bits_k if bits_k > 0 else bits
         self.bits_v = bits_v if bits_v > 0 else bits
         self.max_pages = max_pages if max_pages > 0 else 512
-        self.name = f"CAREKV_fixed_SK{sk}SV{sv}_RK{rk}RV{rv}"
+        self.name = (f"CAREKV_adaptive_rel{rel_threshold:.2f}" if mode == "adaptive"
+                     else f"CAREKV_fixed_SK{sk}SV{sv}_RK{rk}RV{rv}")
         self.bit_width = f"INT{bits}"
         self.k_quant_scheme = "per-channel-group=32 + selected residual slots"
         self.v_quant_scheme = "per-channel-group=32 + selected residual slots"
@@ -60,7 +60,12 @@ class CAREKVAdapter:
 
     def env(self) -> dict:
         """The CAREKV_* settings of setup_model (carekv_adapter.py:103-145)."""
-        return dict(
+        read = (dict(CAREKV_READ_BUDGET_MODE="adaptive_score", CAREKV_READ_ABS_K=str(self.max_rk),
+                     CAREKV_READ_ABS_V=str(self.max_rv), CAREKV_READ_RELATIVE_THRESHOLD=str(self.rel_threshold))
+                if self.mode == "adaptive" else
+                dict(CAREKV_READ_BUDGET_MODE="absolute", CAREKV_READ_ABS_K=str(self.rk),
+                     CAREKV_READ_ABS_V=str(self.rv), CAREKV_READ_RELATIVE_THRESHOLD="0.0"))
+        return dict(**read,
             CAREKV_PREFILL_MODE="carekv_stored", CAREKV_PREFILL_RESIDUAL_KIND="both", CAREKV_ROUTE_POLICY="joint",
             CAREKV_SCORE_NORMALIZE="1", CAREKV_CORRECTION_IMPL=self.correction_impl, CAREKV_BUDGET_POLICY="uniform",
             CAREKV_PACKED_BASE="1", CAREKV_SCALE_QUANT="int8", CAREKV_BASE_BITS=str(self.bits),
@@ -68,8 +73,7 @@ class CAREKVAdapter:
             CAREKV_STORE_ABS_V=str(self.sv), CAREKV_DEBUG_STATS="1", CAREKV_BASE_QUANTIZER=self.base_quantizer,
             CAREKV_K_BITS=str(self.bits_k), CAREKV_V_BITS=str(self.bits_v), CAREKV_K_STORE_MODE=self.k_store_mode,
             CAREKV_K_CHANNEL_GROUP=str(self.k_channel_group), CAREKV_V_TOKEN_BLOCK=str(self.v_token_block),
-            CAREKV_READ_BUDGET_MODE="absolute", CAREKV_READ_ABS_K=str(self.rk), CAREKV_READ_ABS_V=str(self.rv),
-            CAREKV_READ_RELATIVE_THRESHOLD="0.0", CAREKV_READ_ABSOLUTE_THRESHOLD="0.0", CAREKV_READ_MIN_KEEP="0")
+            CAREKV_READ_ABSOLUTE_THRESHOLD="0.0", CAREKV_READ_MIN_KEEP="0")
 
     def setup_model(self, model_id: Union[str, nn.Module]):
         """carekv_adapter.py:101-172: set the environment, load (a local
@@ -123,8 +127,9 @@ class CAREKVAdapter:
                     residual_memory_MB=round(residual_mb, 4), base_quantizer=self.base_quantizer)
 
     def effective_budgets(self):
-        return dict(effective_store_budget=f"SK={self.sk} SV={self.sv}",
-                    effective_read_budget=f"fixed RK={self.rk} RV={self.rv}")
+        read = (f"adaptive rel={self.rel_threshold} max RK={self.max_rk} RV={self.max_rv}"
+                if self.mode == "adaptive" else f"fixed RK={self.rk} RV={self.rv}")
+        return dict(effective_store_budget=f"SK={self.sk} SV={self.sv}", effective_read_budget=read)
 
     def notes(self) -> str:
         return ("CARE-KV paper-best (carekv_stored, joint+normalize, cached, "

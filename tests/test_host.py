@@ -149,8 +149,11 @@ def test_adapter_interface_and_limits():
     assert a.effective_budgets()["effective_read_budget"] == "fixed RK=2 RV=2"
     with pytest.raises(NotImplementedError):
         CAREKVAdapter(base_quantizer="kivi_style")
-    with pytest.raises(NotImplementedError):
-        CAREKVAdapter(mode="adaptive")
+    ad = CAREKVAdapter(mode="adaptive", rel_threshold=0.25, max_rk=4, max_rv=6)
+    assert ad.name == "CAREKV_adaptive_rel0.25"
+    e = ad.env()
+    assert (e["CAREKV_READ_BUDGET_MODE"], e["CAREKV_READ_ABS_K"], e["CAREKV_READ_ABS_V"],
+            e["CAREKV_READ_RELATIVE_THRESHOLD"]) == ("adaptive_score", "4", "6", "0.25")
 
 
 def test_prefill_mode_resolution(monkeypatch):
