@@ -79,6 +79,8 @@ extern "C" int carekv_decode_attn(const carekv_arena* arena, const carekv_decode
               (long long)L.total);
     return CAREKV_ESPACE;
   }
+  CAREKV_REQUIRE(L.prox - L.rec < (1L << 32) - 256,
+                 "workspace from the records to the logits exceeds 4 GiB: lower batch or max_pages_used");
   char* ws = (char*)workspace;
   DecodeArgs a{};
   a.q = q; a.out = out; a.seq_slot = dp->seq_slot; a.n_pages = dp->n_pages;
@@ -98,6 +100,9 @@ extern "C" int carekv_decode_attn(const carekv_arena* arena, const carekv_decode
   a.adaptive_score = dp->adaptive_score != 0;
   a.rel_thr = dp->rel_threshold; a.abs_thr = dp->abs_threshold; a.min_keep = dp->min_keep;
   a.prox = proxy ? (float*)(ws + L.prox) : nullptr;
+  a.ws_span = (uint32_t)(L.prox - L.rec);
+  a.ws_e_off = (uint32_t)(L.ebuf - L.rec);
+  a.ws_x_off = (uint32_t)(L.xbuf - L.rec);
   a.sketch_proj = dp->sketch_proj;
   a.diag = diag; a.diag_cap = diag_cap;
   a.B = dp->batch; a.Hq = dp->n_heads; a.GQ = GQ; a.nsplit = L.nsplit; a.SP = dp->split_pages;

@@ -35,6 +35,9 @@ struct DecodeArgs {
   int policy;       // 0 separate, 1 joint, 2 k_first, 3 adaptive (ResidualRouter.route)
   int adaptive_score, min_keep;  // read_budget_mode adaptive_score and its floor
   double ratio_k, ratio_v, sens_d, rel_thr, abs_thr;
+  // byte span of the workspace from rec to the end of xbuf (< 4 GiB), and
+  // the offsets of ebuf and xbuf from rec: one buffer resource covers them
+  uint32_t ws_span, ws_e_off, ws_x_off;
 };
 
 // Page record per (sequence, kv head, query, page), F floats:

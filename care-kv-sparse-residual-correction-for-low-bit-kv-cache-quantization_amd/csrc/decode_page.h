@@ -165,6 +165,28 @@ __device__ __forceinline__ half2_t code_pair(const uint32_t* w, int i) {
   return __builtin_elementwise_fma(v, sc, of);
 }
 
+// Pair i of the chunk as two offset-binary codes u = code + 2^(FB-1) held as
+// fp16 subnormals u * 2^(o - 24), o = the field's offset inside its half
+// (the masked field without exponent bits): one bitop3 per window.  MFMA
+// products of these with fp16 weights are exact in fp32; the consumer
+// scales slot s by 2^(24 - o(s)) (slot_off) and subtracts 2^(FB-1) times
+// the sum of the weights it applied.
+template <int FB, int NC, int SB>
+__device__ __forceinline__ uint32_t code_pair_sub(const uint32_t* w, int i) {
+  using P = Pairs<FB, NC, SB>;
+  constexpr uint32_t fm = (1u << FB) - 1u, top = 1u << (FB - 1);
+  const int ao = P::T.ao[i], bo = P::T.bo[i];
+  const uint32_t ma = fm << ao, mb = fm << (16 + bo);
+  const uint32_t fa = top << ao, fb = top << (16 + bo);
+  if (P::T.Wa[i] == P::T.Wb[i]) {
+    const uint32_t v = window<P::NW>(w, P::T.Wa[i], P::T.ha[i]);
+    return (v ^ (fa | fb)) & (ma | mb);
+  }
+  const uint32_t va = window<P::NW>(w, P::T.Wa[i], P::T.ha[i]);
+  const uint32_t vb = window<P::NW>(w, P::T.Wb[i], P::T.hb[i]);
+  return ((va ^ fa) & ma) | ((vb ^ fb) & mb);
+}
+
 // Exact half(code * s) for all pairs of the chunk (quantizer.py:67-82: the
 // product code*s is exact in fp32 and rounded once to fp16; the packed fp16
 // multiply of the exact code rounds the same exact product once).
@@ -359,6 +381,14 @@ __device__ __forceinline__ void vtile_write(uint32_t* vt, const half2_t* vp, int
   for (int i = 0; i < G::CH / 2; i += 4)
     *reinterpret_cast<uint4*>(dst + i) = make_uint4(h2bits(vp[i]), h2bits(vp[i + 1]), h2bits(vp[i + 2]),
                                                     h2bits(vp[i + 3]));
+}
+
+template <int D, int BITS>
+__device__ __forceinline__ void vtile_write_raw(uint32_t* vt, const uint32_t* vp, int ln, int lj) {
+  using G = PageGeom<D, BITS>;
+  uint32_t* dst = vt + ln * G::VROW + lj * (G::CH / 2);
+#pragma unroll
+  for (int i = 0; i < G::CH / 2; i += 4) *reinterpret_cast<uint4*>(dst + i) = make_uint4(vp[i], vp[i + 1], vp[i + 2], vp[i + 3]);
 }
 
 // acc[t] += P V_tile on MFMA 16x16x16: tile t, column n stands for slot
@@ -565,6 +595,29 @@ __device__ __forceinline__ int meta_field_load(const carekv_arena& A, long pg, b
 // lane whose field is in another array, or whose page is not ok, reads page
 // 0 of the row (always mapped) and drops the value; a page that is not ok
 // gives 0.
+// meta_field_any with every load on a row base (uniform) plus a 32-bit lane
+// index: five loads per lane (valid, k_slot, v_slot, master, has_meta) and
+// a select of values, so no per-lane 64-bit address stays live.
+template <int NCG, int SM>
+__device__ __forceinline__ int meta_field_row(const carekv_arena& A, long pg_base, int p, bool ok, int f) {
+  const uint32_t pp = ok ? (uint32_t)p : 0u;
+  const bool in_ks = f >= 2 && f < 2 + NCG, in_vs = f >= 6 && f < 6 + kVtb;
+  const uint32_t fk = in_ks ? (uint32_t)(f - 2) : 0u, fv = in_vs ? (uint32_t)(f - 6) : 0u;
+  const int vk = (A.k_slot + pg_base * NCG)[pp * NCG + fk];
+  const int vv = (A.v_slot + pg_base * kVtb)[pp * kVtb + fv];
+  const int vn = (A.valid + pg_base)[pp];
+  int v16 = 0;
+  if constexpr (SM == 1) v16 = (int)(f == 11 ? A.vmaster + pg_base : A.kmaster + pg_base)[pp];
+  const int v8 = (int)(A.has_meta + pg_base)[pp];
+  int v = 0;
+  if (f == 0) v = vn;
+  if (in_ks) v = vk;
+  if (in_vs) v = vv;
+  if (f == 1) v = v8;
+  if (f == 10 || f == 11) v = v16;
+  return ok ? v : 0;
+}
+
 template <int NCG, int SM>
 __device__ __forceinline__ int meta_field_any(const carekv_arena& A, long pg_base, int p, bool ok, int f) {
   const long pg = pg_base + (ok ? p : 0);
@@ -648,6 +701,104 @@ template <int D, int BITS>
 __device__ __forceinline__ int slot_dim(int slot) {
   using G = PageGeom<D, BITS>;
   return (slot / G::CH) * G::CH + G::PB::T.slot_code[slot % G::CH];
+}
+
+// Field offset o of slot s in code_pair_sub form (its value is u * 2^(o-24)).
+template <int D, int BITS>
+__device__ __forceinline__ int slot_off(int slot) {
+  using G = PageGeom<D, BITS>;
+  const int r = slot % G::CH, i = r >> 1;
+  return (r & 1) ? G::PB::T.bo[i] : G::PB::T.ao[i];
+}
+
+// ---------------------------------------------------------------- 4x4x4 PV on raw V codes
+// The V scales (one per token and 32-dim group) move from the codes into
+// the weights: P'[q][t][G] = half(P[q][t] * s_V[t][G]), so the V tile holds
+// the codes in code_pair_sub form and needs one bitop3 per pair.  In a PV
+// step over the 64-slot half h, lanes 0-31 cover group 2h and lanes 32-63
+// group 2h + 1 (slots 64h .. 64h+31 and 64h+32 .. 64h+63 are the chunks of
+// one group each at D = 128, and of half a group each at D = 64).
+//
+// Weights per wave in LDS, fp16 [page][G][query][16]: entry i*4 + m holds
+// token 4m + i, so that the 4 halves of [g*4 .. g*4+3] are the tokens g,
+// g+4, g+8, g+12 of pv4_group.  The S-layout lane 16*pi + 4*j + q (tokens
+// 4j..4j+3 of page pi, query q) writes its 4 weights of group G.
+template <int NCG>
+__device__ __forceinline__ void pwg_store(uint16_t* pw, int G, uint32_t w01, uint32_t w23, int lane) {
+  uint16_t* h = pw + (((lane >> 4) * NCG + G) * 4 + (lane & 3)) * 16 + ((lane >> 2) & 3);
+  h[0] = (uint16_t)w01;
+  h[4] = (uint16_t)(w01 >> 16);
+  h[8] = (uint16_t)w23;
+  h[12] = (uint16_t)(w23 >> 16);
+}
+template <int NCG>
+__device__ __forceinline__ void pwg_load(const uint16_t* pw, int pi, int G, int q, uint2 (&p)[4]) {
+  const uint4* s = reinterpret_cast<const uint4*>(pw + ((pi * NCG + G) * 4 + q) * 16);
+  const uint4 a = s[0], b = s[1];
+  p[0] = make_uint2(a.x, a.y);
+  p[1] = make_uint2(a.z, a.w);
+  p[2] = make_uint2(b.x, b.y);
+  p[3] = make_uint2(b.z, b.w);
+}
+
+// One PV step of token group g over the 64-slot half h (the layout of
+// pv4_group) with the weights p01/p23 of the lane's group.
+template <int D, int BITS>
+__device__ __forceinline__ void pv4_step(const uint32_t* vt, int g, int h, uint32_t p01, uint32_t p23, float4_t& acc,
+                                         int lane) {
+  using G = PageGeom<D, BITS>;
+  typedef short short4_t __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) short4_t lds_short4;
+  half4_t bq;
+  __builtin_memcpy(&bq, &p01, 4);
+  __builtin_memcpy(reinterpret_cast<char*>(&bq) + 4, &p23, 4);
+  const int s = lane & 15, g16 = lane >> 4;
+  const __attribute__((address_space(3))) char* base = (const __attribute__((address_space(3))) char*)vt +
+                                                       ((g + 4 * (s >> 2)) * G::VROW) * 4 + (16 * g16 + 4 * (s & 3)) * 2 +
+                                                       128 * h;
+  const short4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)base);
+  half4_t av;
+  __builtin_memcpy(&av, &v, 8);
+  acc = mfma4x4(av, bq, acc);
+}
+
+// merge4_waves for accumulators over raw codes: slot s of the lane's query
+// is acc * 2^(24 - o(s)) - 2^(BITS-1) * wsum, wsum = the lane's group's
+// weight sum over the split (bias[h] for the half h).
+template <int D, int BITS>
+__device__ __forceinline__ void merge4_waves_raw(float* so, float (*s_m)[4], float (*s_l)[4], float m_run, float l_run,
+                                                 const float4_t* acc, const float* bias, int w, int lane, int GQ,
+                                                 float* po, float* pml) {
+  constexpr float top = (float)(1 << (BITS - 1));
+  __syncthreads();
+  if (lane < 4) { s_m[w][lane] = m_run; s_l[w][lane] = l_run; }
+  const int q = lane & 3, b = lane >> 2;
+#pragma unroll
+  for (int h = 0; h < D / 64; ++h)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int slot = 64 * h + 4 * b + i;
+      so[(w * 4 + q) * D + slot_dim<D, BITS>(slot)] =
+          fmaf(acc[h][i], __builtin_ldexpf(1.0f, 24 - slot_off<D, BITS>(slot)), -top * bias[h]);
+    }
+  __syncthreads();
+  for (int idx = threadIdx.x; idx < GQ * D; idx += blockDim.x) {
+    const int qq = idx / D, d = idx % D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) M = fmaxf(M, s_m[ww][qq]);
+    float L = 0.f, O = 0.f;
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int ww = 0; ww < 4; ++ww) {
+        const float f = __builtin_amdgcn_exp2f(s_m[ww][qq] - M);
+        L += s_l[ww][qq] * f;
+        O += so[(ww * 4 + qq) * D + d] * f;
+      }
+    }
+    po[qq * D + d] = O;
+    if (d == 0) { pml[qq * 2] = M; pml[qq * 2 + 1] = L; }
+  }
 }
 
 // merge_waves for the 4x4x4 PV layout (lane l: query l % 4, slots

@@ -14,9 +14,14 @@
 //   * for every stored K slot of the window's pages, dS = q_cg . R_K on the
 //     same MFMA layout and the moments sum dS^2 e^k (k = 2, 3, 4).
 // V side, per page (lane l: token l % 16, dims [(l/16) D/4, ...)):
-//   V_hat through the padded LDS tile, O^T += V_hat^T P^T on 4x4x4 blocks
-//   (A from the tile by the transpose load, P moved from the S layout by
-//   ds_bpermute), so the accumulator holds only the 4 query heads.
+//   the raw codes (code_pair_sub form, one bitop3 per pair) through the
+//   padded LDS tile, O^T += V^T P'^T on 4x4x4 blocks (A from the tile by the
+//   transpose load), so the accumulator holds only the 4 query heads.  The
+//   V scales ride on the weights, P'[t][G] = half(half(e_t) * s_V[t][G]);
+//   the merge undoes the code offset and the subnormal scaling.  The output
+//   differs from sum_t a_t half(code * s) by the fp16 rounding of P' and of
+//   half(code * s), within the output tolerance; V_hat enters nothing
+//   else of this pass.
 // The page records and split partials are those of decode_stream.hip, with
 // m_ref the running max at the window.
 #include "decode_page.h"
@@ -61,7 +66,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
   __shared__ __align__(16) _Float16 sq4[NS4 * 16];       // [step][query][4]: q in the row pair order
   __shared__ __align__(16) _Float16 sqr4[NCG * 8 * 16];  // [cg][step][query][4]: q in the residual order
   __shared__ float s_m[4][4], s_l[4][4];
-  __shared__ __align__(16) uint2 s_pw[4][64];            // per wave: [page][query][token group] weights
+  __shared__ __align__(16) uint16_t s_pw[4][4 * NCG * 64];  // per wave: [page][G][query][16] weights P'
+  __shared__ __align__(16) uint16_t s_vs[4][4 * NCG * 16];  // per wave: [page][G][token] V scales
 
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int GQ = a.GQ;
@@ -81,8 +87,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
   const RowRes rr = row_resources<D, BITS, SM>(A, pg_base, p_end);
   const bool corr = a.correction != 0;
   const float sm_log2 = a.sm_log2;
-  const long rq = (long)a.Pmax * a.F;  // record stride between query heads
-  float* rec_q = a.rec + ((long)bk * GQ + sc) * rq;  // this lane's query (valid when sc < GQ)
+  const int rq = a.Pmax * a.F;  // record stride between query heads
+  // records, stored weights and the K residual slots of (sequence, kv head)
+  // through buffer resources: SGPR bases, 32-bit lane offsets
+  typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
+  // one resource over the workspace from the records to the logits (a
+  // span the host keeps below 4 GiB) with per-array SGPR offsets
+  const __amdgpu_buffer_rsrc_t rs_ws = make_rsrc(a.rec, a.ws_span);
+  const uint32_t so_rec = (uint32_t)(bk * GQ * rq) * 4u;
+  const uint32_t so_e = a.ws_e_off + (uint32_t)(bk * GQ * a.Pmax) * 32u;
+  const uint32_t so_x = a.ws_x_off + (uint32_t)(bk * GQ * a.Pmax) * 64u;
+  // lane parts of the record, weight and logit offsets (page lj, tokens
+  // 4*sbk.., query sc); the window start p0 goes into the SGPR offset
+  const uint32_t vo_rec = (uint32_t)(sc * rq + lj * a.F) * 4u;
+  const uint32_t vo_e = (uint32_t)((sc * a.Pmax + lj) * 16 + 4 * sbk) * 2u;
+  const uint32_t vo_x = (uint32_t)((sc * a.Pmax + lj) * 16 + 4 * sbk) * 4u;
+  const int8_t* kres_row = A.k_res + (long)seq * A.n_slots * G::KSB;  // K residual slots of the sequence
+  const uint16_t* kres_sc = A.k_res_scale + (long)seq * A.n_slots;
 
   {  // q in the MFMA orders
     const uint16_t* qg = a.q + ((long)b * a.Hq + kvh * GQ) * D;
@@ -99,9 +120,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
 
   uint32_t* vt = reinterpret_cast<uint32_t*>(smem) + w * VT_WORDS;
   float m_run = -INFINITY, l_run = 0.f;
-  float4_t oacc[D / 64];  // O[query sc][slots 64h + 4(lane/4) .. +3]
+  float4_t oacc[D / 64];  // O[query sc][slots 64h + 4(lane/4) .. +3] over raw codes
 #pragma unroll
   for (int h = 0; h < D / 64; ++h) oacc[h] = float4_t{0.f, 0.f, 0.f, 0.f};
+  float wsum[NCG];  // sum of the lane's weights P'[t][G] (its query, its tokens)
+#pragma unroll
+  for (int g = 0; g < NCG; ++g) wsum[g] = 0.f;
+  const half2_t one2 = {(_Float16)1.f, (_Float16)1.f};
 
   // K rows and scales of the window, page metadata (one field per lane),
   // V codes and scales one window ahead
@@ -123,15 +148,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
   };
   auto load_meta = [&](int q0) {
     const int pk = q0 + lj;
-    return meta_field_any<NCG, SM>(A, pg_base, pk, pk < p_end, ln);
+    return meta_field_row<NCG, SM>(A, pg_base, pk, pk < p_end, ln);
   };
-  auto load_v = [&](WV& v, int q0) {
+  auto load_vpage = [&](WV& v, int q0, int pi) {
+    const uint32_t vrow = (uint32_t)((q0 + pi) * kPage + ln);
+    buf_load<CHB>(v.vw[pi], rr.vc, vrow * RB + lj * CHB);
+  };
+  auto load_vscale = [&](WV& v, int q0) {
     const int gi = (lj * CH) / 32;
-#pragma unroll
-    for (int pi = 0; pi < 4; ++pi) {
-      const uint32_t vrow = (uint32_t)((q0 + pi) * kPage + ln);
-      buf_load<CHB>(v.vw[pi], rr.vc, vrow * RB + lj * CHB);
-    }
     if constexpr (SM == 1) {
       uint32_t sv = 0;
 #pragma unroll
@@ -153,24 +177,70 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     }
   };
 
+  // Load schedule of a window (one register set per buffer): this
+  // window's first K residual rows at the top; the next window's K rows and
+  // metadata once the S step has consumed the K registers; the next
+  // window's V codes page by page as the PV step consumes them, its V
+  // scales once they are in LDS.  The loads complete in issue order, so
+  // the records wait for nothing issued after the top, the next window's S
+  // step for nothing issued during the PV step, and every load has most of
+  // a window to land.
   int p0 = p_begin + 4 * w;
   int meta_nx = 0;
-  WV vn;
+  WV cv;
   if (p0 < p_end) {
     load_k(p0);
     meta_nx = load_meta(p0);
-    load_v(vn, p0);
+#pragma unroll
+    for (int pi = 0; pi < 4; ++pi) load_vpage(cv, p0, pi);
+    load_vscale(cv, p0);
   }
+  const bool mom = corr && !a.proxy && a.k_cap > 0;  // the sketch proxy scores K slots without the moments
   for (; p0 < p_end; p0 += 16) {
     const int cmeta = meta_nx;  // page metadata of this window
-    const WV cv = vn;           // V of this window
-    load_v(vn, p0 + 16);
+    const int my_meta = __shfl(cmeta, (lane & 48) + 1, 64);
+    // stored K slots of the lane's page (the metadata lanes' ballots: bit
+    // 16*pi + f = field f of page pi names a slot inside the arena) and the
+    // first one's residual row
+    const int fld = lane & 15;
+    const bool in_arena = cmeta >= 0 && cmeta < A.n_slots;
+    const uint64_t kbal = __ballot(fld >= 2 && fld < 2 + NCG && in_arena);
+    const uint64_t vbal = __ballot(fld >= 6 && fld < 6 + kVtb && in_arena);
+    const uint32_t kmask0 = my_meta != 0 ? (uint32_t)(kbal >> (16 * lj + 2)) & ((1u << NCG) - 1u) : 0u;
+    uint32_t rw0[4] = {0u, 0u, 0u, 0u};
+    uint32_t ksc0 = 0u;
+    if (mom) {
+      const int cg0 = kmask0 ? (int)__builtin_ctz(kmask0) : 0;
+      const int slot0 = __shfl(cmeta, (lane & 48) + 2 + cg0, 64);
+      const uint32_t soff0 = kmask0 ? (uint32_t)slot0 : 0u;  // lanes without a slot read slot 0 and drop it
+      const uint4 v = *reinterpret_cast<const uint4*>(kres_row + (soff0 * G::KSB + ln * 16));
+      rw0[0] = v.x; rw0[1] = v.y; rw0[2] = v.z; rw0[3] = v.w;
+      ksc0 = kres_sc[soff0];
+    }
     int nvp[4];
 #pragma unroll
     for (int pi = 0; pi < 4; ++pi) nvp[pi] = __builtin_amdgcn_readlane(cmeta, 16 * pi);
     const int my_nv = __shfl(cmeta, lane & 48, 64);        // valid tokens of this lane's page
-    const int my_meta = __shfl(cmeta, (lane & 48) + 1, 64);
 
+    // ---- V scales of the window to LDS ([page][G][token]); the V-layout
+    // lane (token ln, chunk lj) holds those of its token and group
+    {
+      const int gi = (lj * CH) / 32;
+#pragma unroll
+      for (int pi = 0; pi < 4; ++pi) {
+        _Float16 vs;
+        if constexpr (SM == 1) {
+          const float vm = h2f((uint16_t)__builtin_amdgcn_readlane(cmeta, 16 * pi + 11));
+          vs = (_Float16)((float)(int8_t)(cv.vsc[0] >> (8 * pi)) * vm);
+        } else {
+          vs = bits2half((uint16_t)(cv.vsc[pi >> 1] >> (16 * (pi & 1))));
+        }
+        s_vs[w][(pi * NCG + gi) * 16 + ln] = half2bits(vs);
+      }
+      load_vscale(cv, p0 + 16);
+    }
+
+    __builtin_amdgcn_sched_barrier(0);  // phases stay apart: bounds the live registers
     // ---- S = K_hat q on 4x4x4 blocks
     _Float16 ksg[NCG];
     {
@@ -194,13 +264,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
       else sa0 = mfma4x4(ak, bq, sa0);
     }
 
+    __builtin_amdgcn_sched_barrier(0);
+
     // ---- online softmax over the window (lane: tokens 4*sbk+i of page lj, query sc)
     float x[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) x[i] = (4 * sbk + i < my_nv) ? (sa0[i] + sa1[i]) * sm_log2 : -INFINITY;
-    if (a.xbuf && corr && sc < GQ && my_nv > 0)  // logits for the proxy's margins / the entropy
-      *reinterpret_cast<float4*>(a.xbuf + (((long)bk * GQ + sc) * a.Pmax + p0 + lj) * 16 + 4 * sbk) =
-          make_float4(x[0], x[1], x[2], x[3]);
+    if (a.xbuf && corr && sc < GQ && my_nv > 0) {  // logits for the proxy's margins / the entropy
+      typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
+      __builtin_amdgcn_raw_buffer_store_b128(
+          u4_t{__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]), __float_as_uint(x[3])}, rs_ws,
+          vo_x, so_x + (uint32_t)p0 * 64u, 0);
+    }
     const float mx = pair32_max(pair16_max(row4_max(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])))));
     const float m_new = fmaxf(m_run, mx);
     const float m_use = m_new == -INFINITY ? 0.f : m_new;  // a window with no valid token so far
@@ -213,75 +288,90 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     if (__builtin_expect(__any(f_old != 1.f), 0)) {
 #pragma unroll
       for (int h = 0; h < D / 64; ++h) oacc[h] *= f_old;  // the lane's own query
+#pragma unroll
+      for (int g = 0; g < NCG; ++g) wsum[g] *= f_old;
     }
     const uint32_t e01 = pack_h2(e[0], e[1]), e23 = pack_h2(e[2], e[3]);
-    pw_store_strided(s_pw[w], e01, e23, lane);
+    lds_sync_wave();  // the V scales of the window
+    {
+      half2_t eh01, eh23;
+      __builtin_memcpy(&eh01, &e01, 4);
+      __builtin_memcpy(&eh23, &e23, 4);
+#pragma unroll
+      for (int g = 0; g < NCG; ++g) {
+        const uint2 sv = *reinterpret_cast<const uint2*>(&s_vs[w][(lj * NCG + g) * 16 + 4 * sbk]);
+        half2_t s01, s23;
+        __builtin_memcpy(&s01, &sv.x, 4);
+        __builtin_memcpy(&s23, &sv.y, 4);
+        const half2_t p01 = eh01 * s01, p23 = eh23 * s23;
+        wsum[g] = __builtin_amdgcn_fdot2(p01, one2, wsum[g], false);
+        wsum[g] = __builtin_amdgcn_fdot2(p23, one2, wsum[g], false);
+        pwg_store<NCG>(s_pw[w], g, h2bits(p01), h2bits(p23), lane);
+      }
+    }
 
+    __builtin_amdgcn_sched_barrier(0);
     // ---- O += P V_hat, page by page
 #pragma unroll
     for (int pi = 0; pi < 4; ++pi) {
-      if (nvp[pi] <= 0) continue;
-      float vm = 0.f;
-      if constexpr (SM == 1) vm = h2f((uint16_t)__builtin_amdgcn_readlane(cmeta, 16 * pi + 11));
-      _Float16 vs;
-      if constexpr (SM == 1) vs = (_Float16)((float)(int8_t)(cv.vsc[0] >> (8 * pi)) * vm);
-      else vs = bits2half((uint16_t)(cv.vsc[pi >> 1] >> (16 * (pi & 1))));
-      half2_t vp[CH / 2];
-      dequant_pairs<BITS, CH, BITS>(cv.vw[pi], vs, vp);
-      vtile_write<D, BITS>(vt, vp, ln, lj);
-      lds_sync_wave();
-      uint2 pg[4];  // P[query sc][tokens g, g+4, g+8, g+12] of page pi
-      pw_load(s_pw[w], pi, sc, pg);
+      const bool live = nvp[pi] > 0;
+      if (live) {
+        uint32_t vp[CH / 2];
 #pragma unroll
-      for (int g = 0; g < 4; ++g) pv4_group<D, BITS>(vt, g, pg[g].x, pg[g].y, oacc, lane);
+        for (int i = 0; i < CH / 2; ++i) vp[i] = code_pair_sub<BITS, CH, BITS>(cv.vw[pi], i);
+        vtile_write_raw<D, BITS>(vt, vp, ln, lj);
+      }
+      load_vpage(cv, p0 + 16, pi);  // the next window's page pi into the registers just consumed
+      if (!live) continue;
+      lds_sync_wave();
+#pragma unroll
+      for (int h = 0; h < D / 64; ++h) {
+        uint2 pg[4];  // P'[query sc][tokens g, g+4, g+8, g+12] of page pi, the lane's group
+        pwg_load<NCG>(s_pw[w], pi, 2 * h + (lane >> 5), sc, pg);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) pv4_step<D, BITS>(vt, g, h, pg[g].x, pg[g].y, oacc[h], lane);
+      }
       lds_sync_wave();
     }
-
     load_k(p0 + 16);  // the next window's K rows and metadata
     meta_nx = load_meta(p0 + 16);
+    __builtin_amdgcn_sched_barrier(0);
     if (!corr) continue;
     // ---- page records: m_ref, K-slot moments, V-block masses (this lane:
     // page lj, query sc; the lanes with sbk == 0 write)
     const int my_page = p0 + lj;
     const bool rec_lane = sc < GQ && my_meta != 0 && my_nv > 0;
-    float* rec = rec_q + (long)my_page * a.F;
-    if (rec_lane && sbk == 0) rec[0] = m_new;
+    const uint32_t so_rp = so_rec + (uint32_t)(p0 * a.F) * 4u;  // the window's part of the offsets is uniform
+    if (rec_lane && sbk == 0) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(m_new), rs_ws, vo_rec, so_rp, 0);
     if (rec_lane)
-      *reinterpret_cast<uint2*>(a.ebuf + (((long)bk * GQ + sc) * a.Pmax + my_page) * 16 + 4 * sbk) = make_uint2(e01, e23);
-    int kslot[NCG];
-#pragma unroll
-    for (int cg = 0; cg < NCG; ++cg) {
-      const int s = __shfl(cmeta, (lane & 48) + 2 + cg, 64);
-      kslot[cg] = (my_meta != 0 && s >= 0 && s < A.n_slots) ? s : -1;
-    }
-    int nks = 0;
-#pragma unroll
-    for (int cg = 0; cg < NCG; ++cg) nks += kslot[cg] >= 0;
-    if (nks > a.k_cap && sbk == 0 && sc == 0) *a.err_flag = 1;
-    const int n_mom = a.proxy ? 0 : a.k_cap;  // the sketch proxy scores K slots without the moments
-    for (int r = 0; r < n_mom; ++r) {
-      int cgr = -1, slotr = -1, cnt = 0;
-#pragma unroll
-      for (int cg = 0; cg < NCG; ++cg) {
-        if (kslot[cg] < 0) continue;
-        if (cnt == r) { cgr = cg; slotr = kslot[cg]; }
-        ++cnt;
-      }
-      const bool has = cgr >= 0;
+      __builtin_amdgcn_raw_buffer_store_b64(u2_t{e01, e23}, rs_ws,
+                                            vo_e, so_e + (uint32_t)p0 * 32u, 0);
+    const uint32_t vmask = (uint32_t)(vbal >> (16 * lj + 6)) & 0xfu;
+    uint32_t kmask = kmask0;
+    if ((int)__builtin_popcount(kmask) > a.k_cap && sbk == 0 && sc == 0) *a.err_flag = 1;
+    for (int r = 0; mom && r < a.k_cap; ++r) {
+      const bool has = kmask != 0u;
       if (!__any(has)) break;
-      uint32_t rw[4] = {0u, 0u, 0u, 0u};
-      if (has) {
-        const uint4 v = *reinterpret_cast<const uint4*>(A.k_res + ((long)seq * A.n_slots + slotr) * G::KSB + ln * 16);
+      const int cgr = has ? (int)__builtin_ctz(kmask) : 0;  // the r-th stored channel group
+      kmask &= kmask - 1u;
+      uint32_t rw[4], kscr;
+      if (r == 0) {
+        rw[0] = rw0[0]; rw[1] = rw0[1]; rw[2] = rw0[2]; rw[3] = rw0[3];
+        kscr = ksc0;
+      } else {
+        const int slotr = __shfl(cmeta, (lane & 48) + 2 + cgr, 64);
+        const uint32_t soff = has ? (uint32_t)slotr : 0u;  // lanes without a slot read slot 0 and drop it
+        const uint4 v = *reinterpret_cast<const uint4*>(kres_row + (soff * G::KSB + ln * 16));
         rw[0] = v.x; rw[1] = v.y; rw[2] = v.z; rw[3] = v.w;
+        kscr = kres_sc[soff];
       }
-      const int cgq = has ? cgr : 0;
       float4_t racc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < 8; ++s) {
         const half2_t c0 = code_pair<4, 32, 4>(rw, 2 * s);
         const half2_t c1 = code_pair<4, 32, 4>(rw, 2 * s + 1);
         const half4_t ar = {c0[0], c0[1], c1[0], c1[1]};
-        const half4_t bq = *reinterpret_cast<const half4_t*>(sqr4 + ((cgq * 8 + s) * 4 + sc) * 4);
+        const half4_t bq = *reinterpret_cast<const half4_t*>(sqr4 + ((cgr * 8 + s) * 4 + sc) * 4);
         racc = mfma4x4(ar, bq, racc);
       }
       // moments of u = racc * e (dS = racc * f scales them by f^2)
@@ -296,29 +386,39 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
       }
       M2 = row4_sum(M2); M3 = row4_sum(M3); M4 = row4_sum(M4);
       if (has && rec_lane && sbk == 0) {
-        const float f = h2f(A.k_res_scale[(long)seq * A.n_slots + slotr]) * a.inv_sqrt_d;
+        const float f = h2f((uint16_t)kscr) * a.inv_sqrt_d;
         const float f2 = f * f;
-        rec[1 + 3 * r] = M2 * f2; rec[2 + 3 * r] = M3 * f2; rec[3 + 3 * r] = M4 * f2;
+        const uint32_t o = so_rp + (uint32_t)(1 + 3 * r) * 4u;
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(M2 * f2), rs_ws, vo_rec, o, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(M3 * f2), rs_ws, vo_rec, o + 4u, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(M4 * f2), rs_ws, vo_rec, o + 8u, 0);
       }
     }
     // V block sbk of page lj: its stored-slot rank and mass
-    int vrank = -1, rv = 0;
-#pragma unroll
-    for (int vb = 0; vb < kVtb; ++vb) {
-      const int s = __shfl(cmeta, (lane & 48) + 6 + vb, 64);
-      if (s < 0 || s >= A.n_slots) continue;
-      if (vb == sbk) vrank = rv;
-      ++rv;
-    }
-    if (rec_lane && vrank >= 0) {
-      if (vrank < a.v_cap) rec[1 + 3 * a.k_cap + vrank] = (e[0] + e[1]) + (e[2] + e[3]);
+    if (rec_lane && ((vmask >> sbk) & 1u)) {
+      const int vrank = (int)__builtin_popcount(__builtin_amdgcn_ubfe(vmask, 0u, (uint32_t)sbk));  // blocks before sbk
+      if (vrank < a.v_cap)
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint((e[0] + e[1]) + (e[2] + e[3])), rs_ws,
+                                              vo_rec + (uint32_t)vrank * 4u, so_rp + (uint32_t)(1 + 3 * a.k_cap) * 4u, 0);
       else *a.err_flag = 1;
     }
   }
 
-  merge4_waves<D, BITS>(reinterpret_cast<float*>(smem), s_m, s_l, m_run, l_run, oacc, w, lane, GQ,
-                       a.po + ((long)bk * a.nsplit + split) * 16 * D,
-                       a.pml + ((long)bk * a.nsplit + split) * 16 * 2);
+  // weight sums per (query, group) over the wave: lanes l with l % 4 = q
+  float bias[D / 64];
+  {
+#pragma unroll
+    for (int g = 0; g < NCG; ++g) wsum[g] = col_sum(row4_sum(wsum[g]));
+#pragma unroll
+    for (int h = 0; h < D / 64; ++h) {
+      float lo = wsum[2 * h], hi = wsum[2 * h + 1];
+      asm volatile("" : "+v"(lo), "+v"(hi));  // a select of values, not of array slots
+      bias[h] = (lane >> 5) ? hi : lo;
+    }
+  }
+  merge4_waves_raw<D, BITS>(reinterpret_cast<float*>(smem), s_m, s_l, m_run, l_run, oacc, bias, w, lane, GQ,
+                           a.po + ((long)bk * a.nsplit + split) * 16 * D,
+                           a.pml + ((long)bk * a.nsplit + split) * 16 * 2);
 }
 
 int launch_decode_stream4(const carekv_arena& A, const DecodeArgs& a, hipStream_t s) {
