@@ -595,6 +595,12 @@ __device__ __forceinline__ int meta_field_load(const carekv_arena& A, long pg, b
 // lane whose field is in another array, or whose page is not ok, reads page
 // 0 of the row (always mapped) and drops the value; a page that is not ok
 // gives 0.
+// *(T*)(base + off) with a 32-bit byte offset (base uniform).
+template <typename T>
+__device__ __forceinline__ T ld_off(const void* base, uint32_t off) {
+  return *reinterpret_cast<const T*>(reinterpret_cast<const char*>(base) + off);
+}
+
 // meta_field_any with every load on a row base (uniform) plus a 32-bit lane
 // index: five loads per lane (valid, k_slot, v_slot, master, has_meta) and
 // a select of values, so no per-lane 64-bit address stays live.
@@ -603,12 +609,17 @@ __device__ __forceinline__ int meta_field_row(const carekv_arena& A, long pg_bas
   const uint32_t pp = ok ? (uint32_t)p : 0u;
   const bool in_ks = f >= 2 && f < 2 + NCG, in_vs = f >= 6 && f < 6 + kVtb;
   const uint32_t fk = in_ks ? (uint32_t)(f - 2) : 0u, fv = in_vs ? (uint32_t)(f - 6) : 0u;
-  const int vk = (A.k_slot + pg_base * NCG)[pp * NCG + fk];
-  const int vv = (A.v_slot + pg_base * kVtb)[pp * kVtb + fv];
-  const int vn = (A.valid + pg_base)[pp];
+  // 32-bit byte offsets from uniform bases: SGPR-base + VGPR-offset loads
+  const int vk = ld_off<int>(A.k_slot + pg_base * NCG, (pp * NCG + fk) * 4u);
+  const int vv = ld_off<int>(A.v_slot + pg_base * kVtb, (pp * kVtb + fv) * 4u);
+  const int vn = ld_off<int>(A.valid + pg_base, pp * 4u);
   int v16 = 0;
-  if constexpr (SM == 1) v16 = (int)(f == 11 ? A.vmaster + pg_base : A.kmaster + pg_base)[pp];
-  const int v8 = (int)(A.has_meta + pg_base)[pp];
+  if constexpr (SM == 1) {
+    const int mk = (int)ld_off<uint16_t>(A.kmaster + pg_base, pp * 2u);
+    const int mv = (int)ld_off<uint16_t>(A.vmaster + pg_base, pp * 2u);
+    v16 = f == 11 ? mv : mk;
+  }
+  const int v8 = (int)ld_off<int8_t>(A.has_meta + pg_base, pp);
   int v = 0;
   if (f == 0) v = vn;
   if (in_ks) v = vk;

@@ -185,7 +185,10 @@ constexpr int kLdsCand = 8192;  // candidates kept in LDS (32 KB); more go to th
 constexpr int kXcd = 8;
 
 // PX: K scores from the sketch proxy records instead of the moments.
-template <int D, bool PX>
+// K1: k_cap = v_cap = 1 (records [m_ref, M2, M3, M4, mass]), the common
+// store budget of one K and one V slot per page, scored without the
+// generic rank loops.
+template <int D, bool PX, bool K1>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) void decode_select_kernel(carekv_arena A, DecodeArgs a) {
   constexpr int NCG = D / 32;
   constexpr int FMAX = 1 + 3 * NCG + kVtb;
@@ -286,8 +289,57 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
       for (; rk < k_cap; ++rk) sc[p * k_cap + rk] = -1.f;
     }
   }
+  if constexpr (K1 && !PX) {
+    // one K and one V candidate per page: the first stored channel group
+    // and the first stored V block (attention.py:540-573, 386-441 with one
+    // slot per kind), scored as in the generic loop below
+    const bool sens1 = a.sens_d == 1.0;
+#pragma unroll 2
+    for (int p = tid; p < np; p += kBlock) {
+      const long pg = pg_base + p;
+      const int nv = A.valid[pg];
+      const int hm = A.has_meta[pg];
+      const float vsq = A.v_sq[pg];
+      int ksl[NCG], vsl[kVtb];
+      load_slots<NCG>(ksl, A.k_slot + pg * NCG);
+      load_slots<kVtb>(vsl, A.v_slot + pg * kVtb);
+      const uint2 e2 = *reinterpret_cast<const uint2*>(A.v_err + pg * kVtb);
+      const float* rp = recq + (long)p * 5;
+      const float r0 = rp[0], M2 = rp[1], M3 = rp[2], M4 = rp[3], E = rp[4];
+      const bool ok = L > 0.f && nv > 0 && hm;
+      const float c = ok ? __builtin_amdgcn_exp2f(r0 - M) * invL : 0.f;
+      bool kh = false;
+#pragma unroll
+      for (int cg = 0; cg < NCG; ++cg) kh |= slot_ok(A, ksl[cg]);
+      float ks = -1.f;
+      if (ok && kh) {
+        const float q2 = c * c * (M2 - c * (2.f * M3 - c * M4));
+        ks = __builtin_amdgcn_sqrtf(fmaxf(q2, 0.f)) * __builtin_amdgcn_sqrtf(vsq);
+        if (!isfinite(ks)) ks = 0.f;
+        ks = ks * a.sens;
+        sumK += ks;
+        ++cntK;
+      }
+      sc[p] = ks;
+      int vb1 = -1;
+#pragma unroll
+      for (int vb = kVtb - 1; vb >= 0; --vb)
+        if (slot_ok(A, vsl[vb])) vb1 = vb;
+      float vsc = -1.f;
+      if (ok && vb1 >= 0 && vb1 * kVtb < nv) {
+        const uint32_t ew = vb1 < 2 ? e2.x : e2.y;
+        const float ve = h2f((uint16_t)(ew >> (16 * (vb1 & 1))));
+        const float verr_s = sens1 ? ve : (float)((double)ve * a.sens_d);
+        vsc = (c * E) * verr_s;
+        vsc = vsc * a.sens;
+        sumV += vsc;
+        ++cntV;
+      }
+      sc[nK + p] = vsc;
+    }
+  }
 #pragma unroll 1
-  for (int p = tid; p < np; p += kBlock) {
+  for (int p = tid; p < (K1 && !PX ? 0 : np); p += kBlock) {
     const long pg = pg_base + p;
     const int nv = A.valid[pg];
     const int hm = A.has_meta[pg];
@@ -535,12 +587,15 @@ int launch_decode_select(const carekv_arena& A, const DecodeArgs& a, hipStream_t
   const dim3 grid(((pairs + kXcd - 1) / kXcd) * kXcd * a.GQ);
   const size_t lds = (a.correction && a.ncand <= kLdsCand) ? (size_t)a.ncand * sizeof(float) : 0;
   const bool px = a.correction && a.proxy;
+  const bool k1 = a.k_cap == 1 && a.v_cap == 1;
   if (A.head_dim == 64) {
-    if (px) hipLaunchKernelGGL((decode_select_kernel<64, true>), grid, dim3(kBlock), lds, s, A, a);
-    else hipLaunchKernelGGL((decode_select_kernel<64, false>), grid, dim3(kBlock), lds, s, A, a);
+    if (px) hipLaunchKernelGGL((decode_select_kernel<64, true, false>), grid, dim3(kBlock), lds, s, A, a);
+    else if (k1) hipLaunchKernelGGL((decode_select_kernel<64, false, true>), grid, dim3(kBlock), lds, s, A, a);
+    else hipLaunchKernelGGL((decode_select_kernel<64, false, false>), grid, dim3(kBlock), lds, s, A, a);
   } else if (A.head_dim == 128) {
-    if (px) hipLaunchKernelGGL((decode_select_kernel<128, true>), grid, dim3(kBlock), lds, s, A, a);
-    else hipLaunchKernelGGL((decode_select_kernel<128, false>), grid, dim3(kBlock), lds, s, A, a);
+    if (px) hipLaunchKernelGGL((decode_select_kernel<128, true, false>), grid, dim3(kBlock), lds, s, A, a);
+    else if (k1) hipLaunchKernelGGL((decode_select_kernel<128, false, true>), grid, dim3(kBlock), lds, s, A, a);
+    else hipLaunchKernelGGL((decode_select_kernel<128, false, false>), grid, dim3(kBlock), lds, s, A, a);
   } else {
     set_error("unsupported head_dim %d", A.head_dim);
     return CAREKV_EINVAL;

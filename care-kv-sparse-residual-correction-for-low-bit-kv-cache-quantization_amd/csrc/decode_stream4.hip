@@ -213,9 +213,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
       const int cg0 = kmask0 ? (int)__builtin_ctz(kmask0) : 0;
       const int slot0 = __shfl(cmeta, (lane & 48) + 2 + cg0, 64);
       const uint32_t soff0 = kmask0 ? (uint32_t)slot0 : 0u;  // lanes without a slot read slot 0 and drop it
-      const uint4 v = *reinterpret_cast<const uint4*>(kres_row + (soff0 * G::KSB + ln * 16));
+      const uint4 v = ld_off<uint4>(kres_row, soff0 * G::KSB + ln * 16);
       rw0[0] = v.x; rw0[1] = v.y; rw0[2] = v.z; rw0[3] = v.w;
-      ksc0 = kres_sc[soff0];
+      ksc0 = ld_off<uint16_t>(kres_sc, soff0 * 2u);
     }
     int nvp[4];
 #pragma unroll
@@ -361,9 +361,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
       } else {
         const int slotr = __shfl(cmeta, (lane & 48) + 2 + cgr, 64);
         const uint32_t soff = has ? (uint32_t)slotr : 0u;  // lanes without a slot read slot 0 and drop it
-        const uint4 v = *reinterpret_cast<const uint4*>(kres_row + (soff * G::KSB + ln * 16));
+        const uint4 v = ld_off<uint4>(kres_row, soff * G::KSB + ln * 16);
         rw[0] = v.x; rw[1] = v.y; rw[2] = v.z; rw[3] = v.w;
-        kscr = kres_sc[soff];
+        kscr = ld_off<uint16_t>(kres_sc, soff * 2u);
       }
       float4_t racc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
