@@ -412,11 +412,17 @@ def decode_attention(cache: OCache, layer_id, Qh, page_ids_by_kvh=None, correcti
     for h in range(Hkv):
         pids = cache.all_page_ids(layer_id, h) if page_ids_by_kvh is None else page_ids_by_kvh[h]
         heads = list(range(h * grp, (h + 1) * grp))
-        Kc, Ks, Vc, Vs, _ = cache.read_base_concat(layer_id, h, pids)
-        if Kc.shape[0] == 0:
-            continue
-        Kh = Q.dequantize(Kc, Ks, cfg.group_size).astype(F32)
-        Vh = Q.dequantize(Vc, Vs, cfg.group_size).astype(F32)
+        if cfg.side_buffer:  # attention.py:997-1008: fp16 K_hat / V_hat, no dequantisation
+            Kh, Vh, _ = cache.read_base_hat_concat(layer_id, h, pids)
+            if Kh.shape[0] == 0:
+                continue
+            Kh, Vh = Kh.astype(F32), Vh.astype(F32)
+        else:
+            Kc, Ks, Vc, Vs, _ = cache.read_base_concat(layer_id, h, pids)
+            if Kc.shape[0] == 0:
+                continue
+            Kh = Q.dequantize(Kc, Ks, cfg.group_size).astype(F32)
+            Vh = Q.dequantize(Vc, Vs, cfg.group_size).astype(F32)
         Qg = np.asarray(Qh)[heads].astype(F32)
         S, A, O_base = base_attention(Kh, Vh, Qg)
         d = None if diag is None else diag.setdefault(h, {})

@@ -49,6 +49,21 @@ class OCfg:
     read_relative_threshold: float = 0.0
     read_absolute_threshold: float = 0.0
     read_min_keep: int = 0
+    base_quantizer: str = "uniform"
+    k_bits_override: int = -1
+    v_bits_override: int = -1
+
+    @property
+    def side_buffer(self) -> bool:
+        """fp16 K_hat / V_hat side buffer (cache.py:487-499; the decode read
+        checks these three names, attention.py:997)."""
+        return self.base_quantizer in ("kivi_style", "rotatekv_style", "kvquant_style")
+
+    def kivi_bits(self):
+        """``layer.py:197-202``."""
+        kb = self.k_bits_override if self.k_bits_override > 0 else self.base_bits
+        vb = self.v_bits_override if self.v_bits_override > 0 else self.base_bits
+        return int(kb), int(vb)
 
     def __post_init__(self):
         if self.layer_sensitivity is None:
@@ -109,6 +124,11 @@ class OCache:
             self.base_V_scale = np.zeros((L, H, P, T, G), F16)
             self.base_K_scale_master = self.base_V_scale_master = None
         self.valid_tokens = np.zeros((L, H, P), np.int32)
+        if cfg.side_buffer:                                     # cache.py:487-499
+            self.base_K_hat_fp16 = np.zeros((L, H, P, T, D), F16)
+            self.base_V_hat_fp16 = np.zeros((L, H, P, T, D), F16)
+        else:
+            self.base_K_hat_fp16 = self.base_V_hat_fp16 = None
         if max_slots is None:                                   # cache.py:507-509
             ratio_est = int(P * H * L * cfg.store_budget_ratio * 4)
             abs_est = int(P * H * L * (cfg.store_abs_k + cfg.store_abs_v) * 2)
@@ -201,6 +221,35 @@ class OCache:
             self.base_V_scale[idx] = np.asarray(V_scale_row).astype(F16)
         self.valid_tokens[layer, kv_head, page_id] = off + 1
         return off
+
+    # -- fp16 side buffer (cache.py:800-865)
+    def write_base_kivi(self, layer, kv_head, page_id, K_hat, V_hat, num_valid):
+        assert self.base_K_hat_fp16 is not None and 0 <= num_valid <= self.cfg.page_size
+        self.base_K_hat_fp16[layer, kv_head, page_id] = np.asarray(K_hat).astype(F16)
+        self.base_V_hat_fp16[layer, kv_head, page_id] = np.asarray(V_hat).astype(F16)
+        self.valid_tokens[layer, kv_head, page_id] = num_valid
+
+    def append_to_page_kivi(self, layer, kv_head, page_id, K_hat_row, V_hat_row):
+        off = int(self.valid_tokens[layer, kv_head, page_id])
+        assert off < self.cfg.page_size, "page already full"
+        self.base_K_hat_fp16[layer, kv_head, page_id, off] = np.asarray(K_hat_row).astype(F16)
+        self.base_V_hat_fp16[layer, kv_head, page_id, off] = np.asarray(V_hat_row).astype(F16)
+        self.valid_tokens[layer, kv_head, page_id] = off + 1
+        return off
+
+    def read_base_hat_concat(self, layer, kv_head, page_ids):
+        Kh, Vh, lens = [], [], []
+        for pid in page_ids:
+            n = int(self.valid_tokens[layer, kv_head, pid])
+            lens.append(n)
+            if n == 0:
+                continue
+            Kh.append(self.base_K_hat_fp16[layer, kv_head, pid, :n])
+            Vh.append(self.base_V_hat_fp16[layer, kv_head, pid, :n])
+        if not Kh:
+            e = np.zeros((0, self.cfg.head_dim), F16)
+            return e, e, lens
+        return np.concatenate(Kh), np.concatenate(Vh), lens
 
     # -- base read (cache.py:707-772)
     def unpack_rows(self, rows):

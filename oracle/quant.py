@@ -66,6 +66,28 @@ def dequantize(codes, scale, group_size: int):
     return (xg * s).reshape(codes.shape).astype(scale.dtype)
 
 
+def kivi_qdq(x, bits: int, per_channel: bool):
+    """``kivi_helpers.py:35-59``: symmetric quant-dequant of a (..., T, D)
+    array with one scale per channel over T (``quant_dequant_kivi_k``,
+    per_channel) or per token over D (``quant_dequant_kivi_v``), in x's
+    dtype.  The 1e-8 floor is 0 in float16, so an all-zero channel (or a
+    zero component of a single-row K) gives 0/0 = NaN and stays NaN through
+    round and clamp (torch propagates it) -- unlike ``quantize``, whose int8
+    cast turns it into 0."""
+    x = np.asarray(x)
+    dt = x.dtype
+    qm = float(qmax_of(bits))
+    axis = -2 if per_channel else -1
+    m = np.abs(x).max(axis=axis, keepdims=True)                            # exact
+    scale = _rt(m.astype(F32) / F32(qm), dt)
+    scale = np.maximum(scale, np.asarray(1e-8).astype(dt))                 # .clamp(min=1e-8) in dt
+    with np.errstate(invalid="ignore", divide="ignore"):
+        q = _rt(x.astype(F32) / scale.astype(F32), dt)
+    q = np.rint(q.astype(F32))
+    q = np.where(np.isnan(q), q, np.clip(q, -qm - 1, qm))
+    return _rt(q * scale.astype(F32), dt)
+
+
 def quantize_and_residual(x, bits, group_size):
     """``quantizer.py:85-99``."""
     codes, scale = quantize(x, bits, group_size)

@@ -156,6 +156,26 @@ def write_pages_for_kv_head(cache: OCache, layer_id: int, kv_h: int, K_kv, V_kv,
     T, D = K_kv.shape
     ps = cfg.page_size
     num_pages = math.ceil(T / ps)
+    if cfg.side_buffer:
+        # layer.py:226-299: K_hat / V_hat over the whole prompt, pages of the
+        # fp16 side buffer, residuals against them (kivi_style / kvquant_style
+        # post-RoPE: per-channel K, per-token V)
+        assert cfg.base_quantizer in ("kivi_style", "kvquant_style"), cfg.base_quantizer
+        kb, vb = cfg.kivi_bits()
+        Kh_seq = Q.kivi_qdq(K_kv, kb, per_channel=True).astype(K_kv.dtype)
+        Vh_seq = Q.kivi_qdq(V_kv, vb, per_channel=False).astype(V_kv.dtype)
+        for p in range(num_pages):
+            t0, t1 = p * ps, min((p + 1) * ps, T)
+            nv = t1 - t0
+            pad = lambda a: np.concatenate([a, np.zeros((ps - nv, D), a.dtype)]) if nv < ps else a
+            Kp, Vp, Khp, Vhp = pad(K_kv[t0:t1]), pad(V_kv[t0:t1]), pad(Kh_seq[t0:t1]), pad(Vh_seq[t0:t1])
+            pid = cache.alloc_page(layer_id, kv_h)
+            cache.write_base_kivi(layer_id, kv_h, pid, Khp, Vhp, num_valid=nv)
+            process_page(cache, layer_id, kv_h, pid, Kp, Vp, None, None, None, None,
+                         token_start=token_start_abs + t0, num_valid=nv, is_recent=p >= num_pages - 4,
+                         is_sink=(token_start_abs + t0) < sink_tokens, K_hat_override=Khp, V_hat_override=Vhp,
+                         P=P, **store_kw)
+        return
     for p in range(num_pages):
         t0, t1 = p * ps, min((p + 1) * ps, T)
         nv = t1 - t0
@@ -190,6 +210,21 @@ def decode_append(cache: OCache, layer_id: int, k_rows, v_rows, **store_kw):
         if pid is None:
             pid = cache.alloc_page(layer_id, h)
             cache.valid_tokens[layer_id, h, pid] = 0
+        if cfg.side_buffer:
+            # layer.py:1037-1075 (post-RoPE): the row quantised alone, K per
+            # channel over T = 1, V per token; on fill K_orig = K_hat (:1089-1101)
+            kb, vb = cfg.kivi_bits()
+            kh = Q.kivi_qdq(k_rows[h:h + 1], kb, per_channel=True)[0]
+            vh = Q.kivi_qdq(v_rows[h:h + 1], vb, per_channel=False)[0]
+            cache.append_to_page_kivi(layer_id, h, pid, kh, vh)
+            if int(cache.valid_tokens[layer_id, h, pid]) == ps:
+                Kh = cache.base_K_hat_fp16[layer_id, h, pid].astype(k_rows.dtype)
+                Vh = cache.base_V_hat_fp16[layer_id, h, pid].astype(v_rows.dtype)
+                ts = pos_abs + 1 - ps
+                process_page(cache, layer_id, h, pid, Kh, Vh, None, None, None, None, token_start=ts,
+                             num_valid=ps, is_recent=True, is_sink=ts < 4, K_hat_override=Kh,
+                             V_hat_override=Vh, **store_kw)
+            continue
         kc, ks = Q.quantize(k_rows[h:h + 1], cfg.base_bits, cfg.group_size)
         vc, vs = Q.quantize(v_rows[h:h + 1], cfg.base_bits, cfg.group_size)
         cache.append_to_page(layer_id, h, pid, kc[0], ks[0], vc[0], vs[0])

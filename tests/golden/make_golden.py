@@ -62,6 +62,9 @@ def _cache_arrays(cache, L=0):
         K_scale=cache.base_K_scale[L].numpy(), V_scale=cache.base_V_scale[L].numpy(),
         valid=cache.valid_tokens[L].numpy(),
     )
+    if getattr(cache, "base_K_hat_fp16", None) is not None:  # side-buffer base (KIVI)
+        d["K_hat"] = cache.base_K_hat_fp16[L].numpy()
+        d["V_hat"] = cache.base_V_hat_fp16[L].numpy()
     if cache.base_K_scale_master is not None:
         d["K_master"] = cache.base_K_scale_master[L].numpy()
         d["V_master"] = cache.base_V_scale_master[L].numpy()
@@ -167,16 +170,16 @@ def _selector_layer(ck, cfg):
 
 
 def _decode_case(ck, name, *, Hq, Hkv, D, T, seed, outlier_mult, store, read_k, read_v,
-                 n_append=0, k_mode="exact", kscore_live=True):
+                 n_append=0, k_mode="exact", kscore_live=True, base_quantizer="uniform", base_bits=3):
     from CARE_KV.care_kv.attention import vectorized_joint_correction, set_chunk_recorder
     _set_env(CAREKV_STORE_POLICY="residual_kind_aware", CAREKV_PREFILL_RESIDUAL_KIND="both",
              CAREKV_K_CORRECTION_MODE=k_mode, CAREKV_KSCORE_LIVE="1" if kscore_live else "0",
              CAREKV_SCORE_NORMALIZE="1", CAREKV_DEBUG_STATS="0")
     cfg = ck.CacheConfig(num_layers=1, num_heads=Hq, num_kv_heads=Hkv, head_dim=D, page_size=16,
-                         max_pages=max(T // 16 + 4, 400), base_bits=3, group_size=32, k_channel_group=32,
+                         max_pages=max(T // 16 + 4, 400), base_bits=base_bits, group_size=32, k_channel_group=32,
                          v_token_block=4, sketch_dim=32, packed_base=True, scale_quant="int8",
                          read_budget_ratio=0.0, read_budget_mode="absolute", read_abs_k=read_k,
-                         read_abs_v=read_v, route_policy="joint", **store)
+                         read_abs_v=read_v, route_policy="joint", base_quantizer=base_quantizer, **store)
     cache = ck.CAREKVCache(cfg, torch.device("cpu"))
     layer = _selector_layer(ck, cfg)
     K, V = _gen_kv(seed, Hkv, T + n_append, D, outlier_mult=outlier_mult)
@@ -199,10 +202,14 @@ def _decode_case(ck, name, *, Hq, Hkv, D, T, seed, outlier_mult, store, read_k, 
     sf = 1.0 / math.sqrt(D)
     for h in range(Hkv):
         pids = cache.all_page_ids(0, h)
-        Kc, Ks, Vc, Vs, _ = cache.read_base_concat(0, h, pids)
-        N = Kc.shape[0]
-        Kb = ck.dequantize(Kc, Ks, (N, D), layer.base_qcfg).float()
-        Vb = ck.dequantize(Vc, Vs, (N, D), layer.base_qcfg).float()
+        if base_quantizer == "uniform":
+            Kc, Ks, Vc, Vs, _ = cache.read_base_concat(0, h, pids)
+            N = Kc.shape[0]
+            Kb = ck.dequantize(Kc, Ks, (N, D), layer.base_qcfg).float()
+            Vb = ck.dequantize(Vc, Vs, (N, D), layer.base_qcfg).float()
+        else:  # the fp16 side buffer (attention.py:997-1008)
+            Kh, Vh, _ = cache.read_base_hat_concat(0, h, pids)
+            Kb, Vb = Kh.float(), Vh.float()
         heads = list(range(h * grp, (h + 1) * grp))
         S = torch.stack([(Kb @ Qh[i].float()) * sf for i in heads])
         A = torch.softmax(S, dim=1)
@@ -244,6 +251,18 @@ def golden_decode(ck):
     # MHA slice (c2 shape per head), linear K mode for coverage
     _decode_case(ck, "mha_d128_linear", Hq=2, Hkv=2, D=128, T=512, seed=2, outlier_mult=6.0,
                  store=ratio3, read_k=8, read_v=8, k_mode="linear")
+
+
+def golden_decode_kivi(ck):
+    """KIVI-style base (per-channel K over the whole prompt, per-token V,
+    fp16 side buffer; kivi_helpers.py:35-59, cache.py:797-865) under the
+    same comb+ex correction, INT2 as in config 3."""
+    ratio3 = dict(store_budget_mode="ratio", store_budget_ratio=0.03)
+    _decode_case(ck, "c1_kivi", Hq=32, Hkv=4, D=64, T=512, seed=1, outlier_mult=8.0,
+                 store=ratio3, read_k=32, read_v=32, base_quantizer="kivi_style", base_bits=2)
+    _decode_case(ck, "gqa4_d128_kivi", Hq=8, Hkv=2, D=128, T=1000, seed=3, outlier_mult=10.0,
+                 store=dict(store_budget_mode="absolute", store_abs_k=2, store_abs_v=4),
+                 read_k=16, read_v=16, n_append=27, base_quantizer="kivi_style", base_bits=2)
 
 
 def golden_decode_proxy(ck):
@@ -289,10 +308,14 @@ def golden_route(ck):
     sf = 1.0 / math.sqrt(D)
     for h in range(Hkv):
         pids = cache.all_page_ids(0, h)
-        Kc, Ks, Vc, Vs, _ = cache.read_base_concat(0, h, pids)
-        N = Kc.shape[0]
-        Kb = ck.dequantize(Kc, Ks, (N, D), layer.base_qcfg).float()
-        Vb = ck.dequantize(Vc, Vs, (N, D), layer.base_qcfg).float()
+        if base_quantizer == "uniform":
+            Kc, Ks, Vc, Vs, _ = cache.read_base_concat(0, h, pids)
+            N = Kc.shape[0]
+            Kb = ck.dequantize(Kc, Ks, (N, D), layer.base_qcfg).float()
+            Vb = ck.dequantize(Vc, Vs, (N, D), layer.base_qcfg).float()
+        else:  # the fp16 side buffer (attention.py:997-1008)
+            Kh, Vh, _ = cache.read_base_hat_concat(0, h, pids)
+            Kb, Vb = Kh.float(), Vh.float()
         heads = list(range(h * grp, (h + 1) * grp))
         S = torch.stack([(Kb @ Qh[i].float()) * sf for i in heads])
         A = torch.softmax(S, dim=1)
@@ -414,7 +437,7 @@ def golden_activation_slices():
     np.savez_compressed(os.path.join(HERE, "activations_3d_slices.npz"), **out)
 
 
-PARTS = ("activations", "sketch", "store", "append", "decode", "decode_proxy", "route", "fixture")
+PARTS = ("activations", "sketch", "store", "append", "decode", "decode_proxy", "decode_kivi", "route", "fixture")
 
 if __name__ == "__main__":
     # CAREKV_GOLDEN_PARTS=decode_proxy,... writes only those fixtures
@@ -427,7 +450,8 @@ if __name__ == "__main__":
     if any(p != "activations" for p in parts):
         ck = _import_reference()
         fns = dict(sketch=golden_sketch, store=golden_store, append=golden_append, decode=golden_decode,
-                   decode_proxy=golden_decode_proxy, route=golden_route, fixture=golden_reference_fixture)
+                   decode_proxy=golden_decode_proxy, decode_kivi=golden_decode_kivi, route=golden_route,
+                   fixture=golden_reference_fixture)
         for p in parts:
             if p in fns:
                 fns[p](ck)

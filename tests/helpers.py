@@ -28,6 +28,14 @@ DECODE_CASES = {
     "gqa4_d128_proxy": dict(Hq=8, Hkv=2, D=128, store=dict(store_budget_mode="absolute", store_abs_k=2,
                                                            store_abs_v=4), k_mode="exact", live=False,
                            score_rtol=1e-3, tie_eps=2e-3),
+    # KIVI-style INT2 base in the fp16 side buffer (base_quantizer=kivi_style)
+    # (the K score sums ||dS * A(1-A)|| over wider-spread logits than the
+    # uniform INT3 cases: fp32 order differences reach 3e-5 relative)
+    "c1_kivi": dict(Hq=32, Hkv=4, D=64, store=dict(store_budget_mode="ratio", store_budget_ratio=0.03),
+                    k_mode="exact", base_quantizer="kivi_style", base_bits=2, score_rtol=1e-4),
+    "gqa4_d128_kivi": dict(Hq=8, Hkv=2, D=128, store=dict(store_budget_mode="absolute", store_abs_k=2,
+                                                          store_abs_v=4), k_mode="exact",
+                           base_quantizer="kivi_style", base_bits=2, score_rtol=1e-4),
 }
 
 PAPER_ENV = dict(CAREKV_STORE_POLICY="residual_kind_aware", CAREKV_PREFILL_RESIDUAL_KIND="both",
@@ -41,9 +49,10 @@ def load_golden(name):
 def case_cfg_kwargs(g, spec):
     T = int(g["T"])
     return dict(num_layers=1, num_heads=spec["Hq"], num_kv_heads=spec["Hkv"], head_dim=spec["D"], page_size=16,
-                max_pages=max(T // 16 + 4, 400), base_bits=3, group_size=32, k_channel_group=32, v_token_block=4,
-                sketch_dim=32, read_budget_mode="absolute", read_abs_k=int(g["read_k"]), read_abs_v=int(g["read_v"]),
-                route_policy="joint", **spec["store"])
+                max_pages=max(T // 16 + 4, 400), base_bits=spec.get("base_bits", 3), group_size=32,
+                k_channel_group=32, v_token_block=4, sketch_dim=32, read_budget_mode="absolute",
+                read_abs_k=int(g["read_k"]), read_abs_v=int(g["read_v"]), route_policy="joint",
+                base_quantizer=spec.get("base_quantizer", "uniform"), **spec["store"])
 
 
 def build_oracle_case(g, name):

@@ -112,6 +112,10 @@ def _compare_cache(c: OCache, g, prefix="", err_ulp=1):
                     assert np.array_equal(mine[h, p, :n], ref[h, p, :n]), (nm, h, p)
         else:
             assert np.array_equal(mine, ref), nm
+    if prefix + "K_hat" in g:  # fp16 side buffer: every row, padded ones included (zeros)
+        for nm, arr in (("K_hat", c.base_K_hat_fp16), ("V_hat", c.base_V_hat_fp16)):
+            ref = g[prefix + nm]
+            assert np.array_equal(arr[L][:, :ref.shape[1]].view(np.uint16), ref.view(np.uint16)), nm
     nk = g[prefix + "k_res"].shape[0]
     nv = g[prefix + "v_res"].shape[0]
     assert c.next_k_slot == nk and c.next_v_slot == nv
@@ -186,9 +190,10 @@ def build_decode_case(g, name):
     spec = DECODE_CASES[name]
     T, n_app = int(g["T"]), int(g["n_append"])
     cfg = OCfg(num_layers=1, num_heads=spec["Hq"], num_kv_heads=spec["Hkv"], head_dim=spec["D"], page_size=16,
-               max_pages=max(T // 16 + 4, 400), base_bits=3, group_size=32, k_channel_group=32,
-               v_token_block=4, sketch_dim=32, read_budget_mode="absolute", read_abs_k=int(g["read_k"]),
-               read_abs_v=int(g["read_v"]), route_policy="joint", **spec["store"])
+               max_pages=max(T // 16 + 4, 400), base_bits=spec.get("base_bits", 3), group_size=32,
+               k_channel_group=32, v_token_block=4, sketch_dim=32, read_budget_mode="absolute",
+               read_abs_k=int(g["read_k"]), read_abs_v=int(g["read_v"]), route_policy="joint",
+               base_quantizer=spec.get("base_quantizer", "uniform"), **spec["store"])
     c = OCache(cfg)
     for h in range(spec["Hkv"]):
         write_pages_for_kv_head(c, 0, h, g["K"][h, :T], g["V"][h, :T], token_start_abs=0, sink_tokens=4)
