@@ -26,13 +26,15 @@ class Arena(C.Structure):
         "k_err", "v_err", "k_sketch", "v_sq", "k_res", "k_res_scale", "v_res", "v_res_scale", "next_slot")] + \
         [(n, C.c_int32) for n in (
             "n_seq", "n_kv_heads", "max_pages", "head_dim", "base_bits", "page_size", "group_size",
-            "k_channel_group", "v_token_block", "sketch_dim", "scale_mode", "residual_bits", "n_slots")]
+            "k_channel_group", "v_token_block", "sketch_dim", "scale_mode", "residual_bits", "n_slots",
+            "hat_bits_k", "hat_bits_v")]
 
 
 class StoreParams(C.Structure):
     _fields_ = [("k_budget", C.c_int32), ("v_budget", C.c_int32), ("joint_budget", C.c_int32),
                 ("joint", C.c_int32), ("store_none", C.c_int32), ("sensitivity", C.c_double),
-                ("sink_tokens", C.c_int32), ("sketch_proj", C.c_void_p)]
+                ("sink_tokens", C.c_int32), ("sketch_proj", C.c_void_p), ("k_hat", C.c_void_p),
+                ("v_hat", C.c_void_p)]
 
 
 class DecodeParams(C.Structure):
@@ -57,7 +59,7 @@ PAGE_JOB_INTS = 6
 
 EXPORTS = ["carekv_store_pages", "carekv_store_workspace_bytes", "carekv_append_rows", "carekv_decode_attn",
            "carekv_decode_workspace_bytes", "carekv_read_pages", "carekv_quantize_rows", "carekv_prefill_attn",
-           "carekv_dequantize_rows", "carekv_last_error"]
+           "carekv_dequantize_rows", "carekv_kivi_qdq", "carekv_last_error"]
 
 
 def lib_path() -> str:
@@ -95,6 +97,8 @@ def load(path: str | None = None):
         lib.carekv_prefill_attn.argtypes = [C.POINTER(PrefillParams), vp, vp, vp, vp, vp, vp]
         lib.carekv_dequantize_rows.restype = C.c_int
         lib.carekv_dequantize_rows.argtypes = [vp, vp, i32, i32, i32, vp, vp]
+        lib.carekv_kivi_qdq.restype = C.c_int
+        lib.carekv_kivi_qdq.argtypes = [vp, i32, i32, i32, i32, i32, vp, vp]
         _lib = lib
         return lib
 

@@ -4,8 +4,9 @@ the evaluation-harness entry point that configures CARE-KV through the
 
 Same constructor, ``setup_model`` environment and reporting methods, with
 the fixed (RK/RV) and the adaptive (adaptive_score with rel_threshold under
-the max_rk/max_rv caps) read budgets.  Only the uniform base quantizer is
-built; the side-buffer base quantizers (KIVI / RotateKV / KVQuant) raise
+the max_rk/max_rv caps) read budgets.  The uniform packed base and the
+side-buffer bases kivi_style / kvquant_style (post-RoPE) are built; the
+rotation bases (RotateKV, random rotation) and pre-RoPE KVQuant raise
 ``NotImplementedError``.  ``setup_model`` also accepts an already built
 ``nn.Module`` (a random-init model when no checkpoint is at hand)."""
 from __future__ import annotations
@@ -36,8 +37,11 @@ class CAREKVAdapter:
                  rv: int = 2, max_rk: int = 4, max_rv: int = 4, bits: int = 3, base_quantizer: str = "uniform",
                  bits_k: int = -1, bits_v: int = -1, max_pages: int = 0, k_store_mode: str = "post_rope",
                  correction_impl: str = "cached", k_channel_group: int = 32, v_token_block: int = 4):
-        if base_quantizer != "uniform":
-            raise NotImplementedError(f"base_quantizer={base_quantizer!r}: only the uniform packed base is built")
+        if base_quantizer not in ("uniform", "kivi_style", "kvquant_style"):
+            raise NotImplementedError(f"base_quantizer={base_quantizer!r}: the uniform, kivi_style and "
+                                      "kvquant_style (post-RoPE) bases are built")
+        if base_quantizer == "kvquant_style" and k_store_mode != "post_rope":
+            raise NotImplementedError("kvquant_style with k_store_mode=pre_rope is not built")
         if mode not in ("fixed", "adaptive"):
             raise ValueError(f"mode must be 'fixed' or 'adaptive' (got {mode!r})")
         self.mode, self.rel_threshold = mode, rel_threshold

@@ -72,11 +72,26 @@ def get_sketch_proj(head_dim: int, k_channel_group: int, sketch_dim: int, device
     return _SKETCH_CACHE[key]
 
 
+# Base quantizers whose pages hold fp16 K_hat / V_hat (the side buffer of
+# cache.py:487-499) and that the kernels implement: per-channel K / per-token
+# V (kivi_helpers.py:35-59; kvquant_style post-RoPE is the same quantizer).
+HAT_QUANTIZERS = ("kivi_style", "kvquant_style")
+
+
+def hat_bits(cfg: CacheConfig) -> Tuple[int, int]:
+    """``CAREKVLayer._kivi_bits`` (layer.py:197-202)."""
+    kb = cfg.k_bits_override if cfg.k_bits_override > 0 else cfg.base_bits
+    vb = cfg.v_bits_override if cfg.v_bits_override > 0 else cfg.base_bits
+    return int(kb), int(vb)
+
+
 def check_kernel_config(cfg: CacheConfig):
     """Configurations the HIP kernels implement; anything else is rejected."""
     bad = []
-    if cfg.base_quantizer != "uniform":
-        bad.append(f"base_quantizer={cfg.base_quantizer} (only 'uniform' is built)")
+    if cfg.base_quantizer not in ("uniform",) + HAT_QUANTIZERS:
+        bad.append(f"base_quantizer={cfg.base_quantizer} (uniform, kivi_style or kvquant_style post-RoPE)")
+    if cfg.base_quantizer == "kvquant_style" and getattr(cfg, "k_store_mode", "post_rope") != "post_rope":
+        bad.append("kvquant_style with k_store_mode=pre_rope (post_rope only)")
     if cfg.page_size != 16:
         bad.append(f"page_size={cfg.page_size} (16)")
     if cfg.group_size != 32:
@@ -99,6 +114,21 @@ def check_kernel_config(cfg: CacheConfig):
         raise NotImplementedError("CARE-KV HIP kernels do not support: " + "; ".join(bad))
 
 
+def kivi_qdq(x: torch.Tensor, bits: int, per_channel: bool) -> torch.Tensor:
+    """``quant_dequant_kivi_k`` (per_channel: one scale per channel over the
+    rows) / ``quant_dequant_kivi_v`` (one scale per row) of kivi_helpers.py:35-59
+    on an fp16 device tensor (..., T, D), through carekv_kivi_qdq."""
+    _lib.ptr(x)  # a device tensor, or CarekvError
+    x = x.to(F16).contiguous()
+    T, D = x.shape[-2], x.shape[-1]
+    n_mat = x.numel() // max(T * D, 1)
+    out = torch.empty_like(x)
+    lib = _lib.load()
+    _lib.check(lib.carekv_kivi_qdq(x.data_ptr(), n_mat, T, D, int(bits), int(per_channel), out.data_ptr(),
+                                   _lib.stream_ptr(x.device)), "carekv_kivi_qdq")
+    return out
+
+
 class CAREKVCache:
     """Device-resident paged cache for ``n_seq`` sequences of one model."""
 
@@ -115,7 +145,9 @@ class CAREKVCache:
         G = D // cfg.group_size
         self.ncg = D // cfg.k_channel_group
         self.nvb = math.ceil(T / cfg.v_token_block)
-        self._packed_row_bytes = packed_row_bytes(D, cfg.base_bits)
+        self.hat = cfg.base_quantizer in HAT_QUANTIZERS  # fp16 K_hat / V_hat pages
+        self._arena_bits = 16 if self.hat else cfg.base_bits
+        self._packed_row_bytes = 2 * D if self.hat else packed_row_bytes(D, cfg.base_bits)
         dev = self.device
         shp = (L, H, n_seq, P)
         self.kcodes = torch.zeros(*shp, T, self._packed_row_bytes, dtype=torch.int8, device=dev)
@@ -169,9 +201,10 @@ class CAREKVCache:
                 k_res_scale=self.k_res_scale.data_ptr(), v_res=self.v_res.data_ptr(),
                 v_res_scale=self.v_res_scale.data_ptr(), next_slot=self.next_slot.data_ptr(),
                 n_seq=self.n_seq, n_kv_heads=cfg.num_kv_heads, max_pages=cfg.max_pages, head_dim=cfg.head_dim,
-                base_bits=cfg.base_bits, page_size=cfg.page_size, group_size=cfg.group_size,
+                base_bits=self._arena_bits, page_size=cfg.page_size, group_size=cfg.group_size,
                 k_channel_group=cfg.k_channel_group, v_token_block=cfg.v_token_block, sketch_dim=cfg.sketch_dim,
-                scale_mode=self.scale_mode, residual_bits=cfg.residual_bits, n_slots=self.n_slots)
+                scale_mode=self.scale_mode, residual_bits=cfg.residual_bits, n_slots=self.n_slots,
+                hat_bits_k=hat_bits(cfg)[0], hat_bits_v=hat_bits(cfg)[1])
             self._arenas[layer] = a
         return a
 
@@ -225,10 +258,14 @@ class CAREKVCache:
     def write_prefill(self, layer: int, K: torch.Tensor, V: torch.Tensor, token_start_abs: int = 0,
                       sink_tokens: int = 4, seqs: Optional[Sequence[int]] = None):
         """Quantize + pack + store pages for a prompt chunk of every listed
-        sequence (layer.py:204-334, uniform base quantizer).
+        sequence (layer.py:204-334).  With a side-buffer base quantizer
+        (kivi_style / kvquant_style) K_hat / V_hat are computed over the whole
+        chunk first -- K per channel over T, V per token (layer.py:226-245) --
+        and written as fp16 pages, the residuals taken against them.
 
         K, V: fp16 post-RoPE keys / values, (Hkv, T, D) for one sequence or
-        (B, Hkv, T, D) with ``seqs`` naming the B sequence slots."""
+        (B, Hkv, T, D) with ``seqs`` naming the B sequence slots.  Returns
+        (K_hat, V_hat) of the chunk for the side-buffer base, else None."""
         cfg = self.cfg
         if K.dim() == 3:
             K, V = K.unsqueeze(0), V.unsqueeze(0)
@@ -241,12 +278,19 @@ class CAREKVCache:
         ps = cfg.page_size
         n_new = math.ceil(T / ps)
         pad = n_new * ps - T
-        Kp, Vp = K.to(F16), V.to(F16)
-        if pad:
-            Kp = torch.nn.functional.pad(Kp, (0, 0, 0, pad))
-            Vp = torch.nn.functional.pad(Vp, (0, 0, 0, pad))
-        Kp = Kp.contiguous().view(B * H * n_new * ps, D)
-        Vp = Vp.contiguous().view(B * H * n_new * ps, D)
+        Kp, Vp = K.to(F16).contiguous(), V.to(F16).contiguous()
+        hats = None
+        if self.hat:
+            kb, vb = hat_bits(cfg)
+            Kh, Vh = kivi_qdq(Kp, kb, per_channel=True), kivi_qdq(Vp, vb, per_channel=False)
+            hats = (Kh, Vh)
+        pads = lambda x: torch.nn.functional.pad(x, (0, 0, 0, pad)) if pad else x  # noqa: E731
+        Kp = pads(Kp).contiguous().view(B * H * n_new * ps, D)
+        Vp = pads(Vp).contiguous().view(B * H * n_new * ps, D)
+        Khp = Vhp = None
+        if hats is not None:
+            Khp = pads(hats[0]).contiguous().view(B * H * n_new * ps, D)
+            Vhp = pads(hats[1]).contiguous().view(B * H * n_new * ps, D)
         jobs = np.zeros((B * H * n_new, _lib.PAGE_JOB_INTS), dtype=np.int32)
         group_ptr = np.zeros(B + 1, dtype=np.int32)
         j = 0
@@ -266,13 +310,18 @@ class CAREKVCache:
         sp = _lib.StoreParams(k_budget=knobs.k_budget, v_budget=knobs.v_budget, joint_budget=knobs.joint_budget,
                               joint=int(knobs.joint), store_none=int(knobs.store_none),
                               sensitivity=knobs.sensitivity, sink_tokens=int(sink_tokens),
-                              sketch_proj=self.sketch_proj.data_ptr())
+                              sketch_proj=self.sketch_proj.data_ptr(),
+                              k_hat=Khp.data_ptr() if Khp is not None else None,
+                              v_hat=Vhp.data_ptr() if Vhp is not None else None)
         lib = _lib.load()
         ws = self.workspace("store", int(lib.carekv_store_workspace_bytes(len(jobs))))
         a = self.arena(layer)
         _lib.check(lib.carekv_store_pages(a, sp, Kp.data_ptr(), Vp.data_ptr(), jobs_d.data_ptr(), len(jobs),
                                           gp_d.data_ptr(), B, ws.data_ptr(), _lib.stream_ptr(self.device)),
                    "carekv_store_pages")
+        if hats is not None:
+            return hats[0] if B > 1 else hats[0][0], hats[1] if B > 1 else hats[1][0]
+        return None
 
     def append(self, layer: int, k: torch.Tensor, v: torch.Tensor, seqs: Optional[Sequence[int]] = None):
         """Append one decode token per listed sequence and kv head
@@ -303,6 +352,24 @@ class CAREKVCache:
                                           _lib.stream_ptr(self.device)), "carekv_append_rows")
 
     # ------------------------------------------------------------ reads
+    def read_base_hat_concat(self, layer: int, kv_head: int, page_ids: Optional[List[int]] = None, seq: int = 0):
+        """(K_hat fp16 (N, D), V_hat fp16 (N, D), valid_lens) of the fp16
+        side buffer (cache.py:841-865)."""
+        if not self.hat:
+            raise _lib.CarekvError("read_base_hat_concat needs a side-buffer base quantizer")
+        n = self.num_pages(layer, kv_head, seq)
+        pids = list(range(n)) if page_ids is None else list(page_ids)
+        lens = [int(self.valid_host[layer, kv_head, seq, p]) for p in pids]
+        D = self.cfg.head_dim
+        kh = self.kcodes[layer, kv_head, seq].view(F16).view(self.cfg.max_pages, self.cfg.page_size, D)
+        vh = self.vcodes[layer, kv_head, seq].view(F16).view(self.cfg.max_pages, self.cfg.page_size, D)
+        ks = [kh[p, :n_] for p, n_ in zip(pids, lens) if n_]
+        vs = [vh[p, :n_] for p, n_ in zip(pids, lens) if n_]
+        if not ks:
+            e = torch.zeros(0, D, dtype=F16, device=self.device)
+            return e, e, lens
+        return torch.cat(ks), torch.cat(vs), lens
+
     def read_base_concat(self, layer: int, kv_head: int, page_ids: Optional[List[int]] = None, seq: int = 0):
         """(K_codes int8 (N, D), K_scale fp16 (N, G), V_codes, V_scale, valid_lens)
         for the valid rows of pages 0..n-1 (cache.py:720-772)."""
@@ -352,6 +419,8 @@ class CAREKVCache:
     def _view(self, t):
         return t[:, :, 0] if self.n_seq == 1 else t
 
+    base_K_hat_fp16 = property(lambda self: self._view(self.kcodes).view(F16) if self.hat else None)
+    base_V_hat_fp16 = property(lambda self: self._view(self.vcodes).view(F16) if self.hat else None)
     base_K_codes = property(lambda self: self._view(self.kcodes))
     base_V_codes = property(lambda self: self._view(self.vcodes))
     base_K_scale = property(lambda self: self._view(self.kscale))

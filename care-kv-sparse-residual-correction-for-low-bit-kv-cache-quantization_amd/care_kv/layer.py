@@ -133,8 +133,8 @@ class CAREKVLayer(nn.Module):
             Q, K = _rope(Q, K, cos.to(Q.dtype), sin.to(Q.dtype))
         Qh, Kh, Vh = Q.to(F16).contiguous(), K.to(F16).contiguous(), V.to(F16).contiguous()
         seqs = list(range(B)) if seqs is None else list(seqs)
-        cache.write_prefill(self.layer_id, Kh, Vh, token_start_abs=token_start_abs, sink_tokens=sink_tokens,
-                            seqs=seqs)
+        hats = cache.write_prefill(self.layer_id, Kh, Vh, token_start_abs=token_start_abs,
+                                   sink_tokens=sink_tokens, seqs=seqs)
         if mode == "fp":
             O = prefill_attention(Qh, Kh, Vh)
         else:
@@ -143,8 +143,12 @@ class CAREKVLayer(nn.Module):
                 warnings.warn(f"CAREKV_PREFILL_MODE={mode}: the prefill-time sparse correction is not built; "
                               "the prefill output is the base attention over K_hat / V_hat (decode-time "
                               "correction is unaffected)", RuntimeWarning, stacklevel=2)
-            O = prefill_attention(Qh, quant_dequant(Kh, cfg.base_bits, cfg.group_size),
-                                  quant_dequant(Vh, cfg.base_bits, cfg.group_size))
+            if hats is not None:  # side-buffer base: the K_hat / V_hat the pages hold (layer.py:328-332)
+                Khat, Vhat = (hats[0].unsqueeze(0), hats[1].unsqueeze(0)) if hats[0].dim() == 3 else hats
+                O = prefill_attention(Qh, Khat, Vhat)
+            else:
+                O = prefill_attention(Qh, quant_dequant(Kh, cfg.base_bits, cfg.group_size),
+                                      quant_dequant(Vh, cfg.base_bits, cfg.group_size))
         out = self._out(O, hidden.dtype).to(hidden.dtype)
         return out[0] if squeeze else out
 

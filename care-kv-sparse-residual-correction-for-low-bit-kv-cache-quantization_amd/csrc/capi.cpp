@@ -20,13 +20,15 @@ void set_error(const char* fmt, ...) {
 }
 
 bool check_arena(const carekv_arena& A) {
-  if (!A.kcodes || !A.vcodes || !A.kscale || !A.vscale || !A.valid || !A.has_meta || !A.k_slot || !A.v_slot ||
+  const bool hat = A.base_bits == 16;
+  if (!A.kcodes || !A.vcodes || (!hat && (!A.kscale || !A.vscale)) || !A.valid || !A.has_meta || !A.k_slot ||
+      !A.v_slot ||
       !A.k_err || !A.v_err || !A.k_sketch || !A.v_sq || !A.k_res || !A.k_res_scale || !A.v_res ||
       !A.v_res_scale || !A.next_slot) {
     set_error("arena has a null buffer");
     return false;
   }
-  if (A.scale_mode == 1 && (!A.kmaster || !A.vmaster)) {
+  if (!hat && A.scale_mode == 1 && (!A.kmaster || !A.vmaster)) {
     set_error("scale_mode=int8 needs master buffers");
     return false;
   }
@@ -39,8 +41,12 @@ bool check_arena(const carekv_arena& A) {
     set_error("kernels support head_dim 64 or 128 (got %d)", A.head_dim);
     return false;
   }
-  if (A.base_bits < 2 || A.base_bits > 4) {
-    set_error("base_bits must be 2, 3 or 4 (got %d)", A.base_bits);
+  if ((A.base_bits < 2 || A.base_bits > 4) && !hat) {
+    set_error("base_bits must be 2, 3, 4 or 16 (fp16 side buffer) (got %d)", A.base_bits);
+    return false;
+  }
+  if (hat && (A.hat_bits_k < 2 || A.hat_bits_k > 4 || A.hat_bits_v < 2 || A.hat_bits_v > 4)) {
+    set_error("base_bits=16 needs hat_bits_k/v in 2..4 (got %d/%d)", A.hat_bits_k, A.hat_bits_v);
     return false;
   }
   if (A.scale_mode != 0 && A.scale_mode != 1) {

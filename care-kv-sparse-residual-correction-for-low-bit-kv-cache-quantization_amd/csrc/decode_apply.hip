@@ -15,9 +15,11 @@
 //     num += k_corr_scale * sum_t a_t dS_t V_hat_t + sum_{sel V} a_t R_V[t]
 //     den += k_corr_scale * sum_t a_t dS_t
 //     out  = O_base + (num - den * O_base) / L
-// Both products run on MFMA like the streaming pass (weights as fp16 P,
-// V_hat / R_V transposed through LDS).  The combine kernel sums the chunk
-// partials in chunk order and writes half(out).
+// Both products run on MFMA like the streaming pass (V_hat / R_V transposed
+// through LDS), with each weight split into fp16 hi + lo halves: the
+// correction terms can be large against O_base (wide V rows, large dS) and
+// partly cancel, so fp16 weights alone cost several output ulps.  The
+// combine kernel sums the chunk partials in chunk order and writes half(out).
 #include "block_util.h"
 #include "decode_page.h"
 #include "host_util.h"
@@ -51,9 +53,10 @@ struct ApplyItem {
   bool rsel;           // tile row ln holds a selected V block
 };
 
-// 4 waves per SIMD: the register budget is capped at 128 VGPRs.
+// 4 waves per SIMD (2 for the fp16 base, whose rows take twice the
+// registers): the register budget is capped at 128 (256) VGPRs.
 template <int D, int BITS, int SM>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BITS == 16 ? 2 : 4, 8)))
 void decode_apply_kernel(carekv_arena A, DecodeArgs a) {
   using G = PageGeom<D, BITS>;
   using Item = ApplyItem<D, BITS>;
@@ -260,10 +263,10 @@ void decode_apply_kernel(carekv_arena A, DecodeArgs a) {
       half2_t vp[CH / 2];
       dequant_pairs<BITS, CH, BITS>(cur.vw, vs, vp);
       vtile_write<D, BITS>(vt, vp, ln, lj);
-      half4_t ap;
-      ap[0] = (_Float16)ck[0]; ap[1] = (_Float16)ck[1]; ap[2] = (_Float16)ck[2]; ap[3] = (_Float16)ck[3];
+      half4_t ah, al;
+      split_weights(ck, ah, al);
       lds_sync_wave();
-      pv_accumulate<D, BITS>(vt, ap, nacc, ln, lj);
+      pv_accumulate2<D, BITS>(vt, ah, al, nacc, ln, lj);
       lds_sync_wave();
     }
     // ---- num += cv R_V over the V blocks some query selected; the other
@@ -274,10 +277,10 @@ void decode_apply_kernel(carekv_arena A, DecodeArgs a) {
         dequant_pairs<4, CH, BITS>(cur.rv, (_Float16)cur.rvs, rp);
         vtile_write<D, BITS>(vt, rp, ln, lj);
       }
-      half4_t ap;
-      ap[0] = (_Float16)cv[0]; ap[1] = (_Float16)cv[1]; ap[2] = (_Float16)cv[2]; ap[3] = (_Float16)cv[3];
+      half4_t ah, al;
+      split_weights(cv, ah, al);
       lds_sync_wave();
-      pv_accumulate<D, BITS>(vt, ap, nacc, ln, lj);
+      pv_accumulate2<D, BITS>(vt, ah, al, nacc, ln, lj);
       lds_sync_wave();
     }
   }
@@ -329,9 +332,9 @@ int launch_decode_apply(const carekv_arena& A, const DecodeArgs& a, hipStream_t 
     set_error("apply chunks must be at most 1024 pages");
     return CAREKV_EINVAL;
   }
-  if (a.GQ <= 4) return launch_decode_apply4(A, a, s);  // windows of 4 pages, 4x4x4 layout
+  if (A.base_bits != 16 && a.GQ <= 4) return launch_decode_apply4(A, a, s);  // windows of 4 pages, 4x4x4 layout
   const dim3 grid(a.napply, A.n_kv_heads, a.B);
-  return dispatch_dbs(A.head_dim, A.base_bits, A.scale_mode, [&](auto d, auto bb, auto sm) {
+  return dispatch_dbs16(A.head_dim, A.base_bits, A.scale_mode, [&](auto d, auto bb, auto sm) {
     hipLaunchKernelGGL((decode_apply_kernel<decltype(d)::value, decltype(bb)::value, decltype(sm)::value>), grid,
                        dim3(256), 0, s, A, a);
     CAREKV_CHECK_LAUNCH("decode_apply");

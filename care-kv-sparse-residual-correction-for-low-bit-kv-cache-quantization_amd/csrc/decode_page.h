@@ -72,6 +72,7 @@ template <int SB> struct PairGeom;
 template <> struct PairGeom<2> { static constexpr int BLK = 16, PD = 8; };
 template <> struct PairGeom<3> { static constexpr int BLK = 8, PD = 4; };
 template <> struct PairGeom<4> { static constexpr int BLK = 8, PD = 4; };
+template <> struct PairGeom<16> { static constexpr int BLK = 2, PD = 1; };  // natural order (fp16 base)
 
 template <int FB, int NC, int SB>
 struct Pairs {
@@ -124,6 +125,24 @@ struct Pairs {
       }
       t.ha[i] = h_a; t.hb[i] = h_b;
     }
+    return t;
+  }
+  static constexpr Tab T = make();
+};
+
+// The fp16 side-buffer base (BITS = 16, base_quantizer kivi_style): the
+// "codes" are the K_hat / V_hat values themselves, pair i = 32-bit word i.
+template <int NC>
+struct Pairs<16, NC, 16> {
+  static constexpr int NP = NC / 2;
+  struct Tab {
+    int a[NP], b[NP];  // code indices of pair i: 2i, 2i + 1
+    int slot_code[NC];
+  };
+  static constexpr Tab make() {
+    Tab t{};
+    for (int i = 0; i < NP; ++i) { t.a[i] = 2 * i; t.b[i] = 2 * i + 1; }
+    for (int i = 0; i < NC; ++i) t.slot_code[i] = i;
     return t;
   }
   static constexpr Tab T = make();
@@ -192,9 +211,14 @@ __device__ __forceinline__ uint32_t code_pair_sub(const uint32_t* w, int i) {
 // multiply of the exact code rounds the same exact product once).
 template <int FB, int NC, int SB>
 __device__ __forceinline__ void dequant_pairs(const uint32_t* w, _Float16 s, half2_t* out) {
-  const half2_t ss = {s, s};
+  if constexpr (FB == 16) {  // fp16 base: the values themselves, no scale
 #pragma unroll
-  for (int i = 0; i < NC / 2; ++i) out[i] = code_pair<FB, NC, SB>(w, i) * ss;
+    for (int i = 0; i < NC / 2; ++i) __builtin_memcpy(&out[i], &w[i], 4);
+  } else {
+    const half2_t ss = {s, s};
+#pragma unroll
+    for (int i = 0; i < NC / 2; ++i) out[i] = code_pair<FB, NC, SB>(w, i) * ss;
+  }
 }
 
 __device__ __forceinline__ uint32_t h2bits(half2_t v) {
@@ -203,10 +227,16 @@ __device__ __forceinline__ uint32_t h2bits(half2_t v) {
   return u;
 }
 
-// Buffer load of N bytes (N = 4, 6, 8, 12, 16) at byte offset off.
+// Buffer load of N bytes (N = 4, 6, 8, 12, 16 or a multiple of 16) at byte offset off.
 template <int N>
 __device__ __forceinline__ void buf_load(uint32_t* w, __amdgpu_buffer_rsrc_t r, uint32_t off) {
-  if constexpr (N == 16) {
+  if constexpr (N > 16 && N % 16 == 0) {
+#pragma unroll
+    for (int i = 0; i < N / 16; ++i) {
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off + 16 * i, 0, 0);
+      w[4 * i] = v[0]; w[4 * i + 1] = v[1]; w[4 * i + 2] = v[2]; w[4 * i + 3] = v[3];
+    }
+  } else if constexpr (N == 16) {
     const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
     w[0] = v[0]; w[1] = v[1]; w[2] = v[2]; w[3] = v[3];
   } else if constexpr (N == 12) {
@@ -260,8 +290,13 @@ __device__ __forceinline__ RowRes row_resources(const carekv_arena& A, long pg_b
   RowRes r;
   r.kc = make_rsrc(A.kcodes + pg_base * kPage * G::RB, rows * G::RB);
   r.vc = make_rsrc(A.vcodes + pg_base * kPage * G::RB, rows * G::RB);
-  r.ks = make_rsrc((const char*)A.kscale + pg_base * kPage * G::NCG * ssz, rows * G::NCG * ssz);
-  r.vs = make_rsrc((const char*)A.vscale + pg_base * kPage * G::NCG * ssz, rows * G::NCG * ssz);
+  if constexpr (BITS == 16) {  // no scales: empty resources, loads return 0
+    r.ks = make_rsrc(nullptr, 0u);
+    r.vs = make_rsrc(nullptr, 0u);
+  } else {
+    r.ks = make_rsrc((const char*)A.kscale + pg_base * kPage * G::NCG * ssz, rows * G::NCG * ssz);
+    r.vs = make_rsrc((const char*)A.vscale + pg_base * kPage * G::NCG * ssz, rows * G::NCG * ssz);
+  }
   return r;
 }
 
@@ -412,6 +447,37 @@ __device__ __forceinline__ void pv_accumulate(const uint32_t* vt, half4_t ap, fl
     half4_t bv;
     __builtin_memcpy(&bv, &v, 8);
     acc[t] = mfma16(ap, bv, acc[t]);
+  }
+}
+
+// pv_accumulate with weights carried as hi + lo fp16 pairs (w = hi + lo to
+// about 22 bits): the tile is read once and met by both halves.  Used where
+// fp16 weights lose too much, e.g. correction weights a_t (e^dS - 1) that
+// multiply wide V rows and partly cancel against O_base.
+template <int D, int BITS>
+__device__ __forceinline__ void pv_accumulate2(const uint32_t* vt, half4_t ah, half4_t al, float4_t* acc, int ln,
+                                               int lj) {
+  using G = PageGeom<D, BITS>;
+  typedef short short4_t __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) short4_t lds_short4;
+  const __attribute__((address_space(3))) char* base =
+      (const __attribute__((address_space(3))) char*)vt + ((4 * lj + (ln >> 2)) * G::VROW) * 4 + (ln & 3) * 8;
+#pragma unroll
+  for (int t = 0; t < G::NT; ++t) {
+    const short4_t v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_short4*)(base + 32 * t));
+    half4_t bv;
+    __builtin_memcpy(&bv, &v, 8);
+    acc[t] = mfma16(al, bv, acc[t]);
+    acc[t] = mfma16(ah, bv, acc[t]);
+  }
+}
+
+// Split fp32 weights into fp16 hi + lo (lo = the rounding error of hi).
+__device__ __forceinline__ void split_weights(const float (&c)[4], half4_t& hi, half4_t& lo) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    hi[i] = (_Float16)c[i];
+    lo[i] = (_Float16)(c[i] - (float)hi[i]);
   }
 }
 

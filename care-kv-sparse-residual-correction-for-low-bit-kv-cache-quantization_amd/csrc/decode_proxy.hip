@@ -143,7 +143,7 @@ __global__ __launch_bounds__(256) void decode_proxy_kernel(carekv_arena A, Decod
 
 int launch_decode_proxy(const carekv_arena& A, const DecodeArgs& a, hipStream_t s) {
   const dim3 grid(a.nsplit, A.n_kv_heads, a.B);
-  return dispatch_dbs(A.head_dim, A.base_bits, A.scale_mode, [&](auto d, auto bb, auto sm) {
+  return dispatch_dbs16(A.head_dim, A.base_bits, A.scale_mode, [&](auto d, auto bb, auto sm) {
     hipLaunchKernelGGL((decode_proxy_kernel<decltype(d)::value, decltype(bb)::value, decltype(sm)::value>), grid,
                        dim3(256), 0, s, A, a);
     CAREKV_CHECK_LAUNCH("decode_proxy");

@@ -23,8 +23,9 @@
 namespace carekv {
 
 template <int D, int BITS, int SM>
-// 4 waves per SIMD: the register budget is capped at 128 VGPRs.
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8)))
+// 4 waves per SIMD (2 for the fp16 base, whose rows take twice the
+// registers): the register budget is capped at 128 (256) VGPRs.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BITS == 16 ? 2 : 4, 8)))
 void decode_stream_kernel(carekv_arena A, DecodeArgs a) {
   using G = PageGeom<D, BITS>;
   constexpr int NT = G::NT, NCG = G::NCG, CH = G::CH;
@@ -199,9 +200,10 @@ void decode_stream_kernel(carekv_arena A, DecodeArgs a) {
 }
 
 int launch_decode_stream(const carekv_arena& A, const DecodeArgs& a, hipStream_t s) {
-  if (a.GQ <= 4 && a.SP % 16 == 0) return launch_decode_stream4(A, a, s);  // 4-page windows, 4x4x4 MFMA
+  if (A.base_bits != 16 && a.GQ <= 4 && a.SP % 16 == 0)
+    return launch_decode_stream4(A, a, s);  // 4-page windows, 4x4x4 MFMA
   dim3 grid(a.nsplit, A.n_kv_heads, a.B);
-  return dispatch_dbs(A.head_dim, A.base_bits, A.scale_mode, [&](auto d, auto bb, auto sm) {
+  return dispatch_dbs16(A.head_dim, A.base_bits, A.scale_mode, [&](auto d, auto bb, auto sm) {
     hipLaunchKernelGGL((decode_stream_kernel<decltype(d)::value, decltype(bb)::value, decltype(sm)::value>), grid,
                        dim3(256), 0, s, A, a);
     CAREKV_CHECK_LAUNCH("decode_stream");

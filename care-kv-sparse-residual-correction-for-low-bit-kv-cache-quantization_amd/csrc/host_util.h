@@ -66,4 +66,19 @@ int dispatch_dbs(int D, int bits, int scale_mode, F&& f) {
   });
 }
 
+// dispatch_dbs plus base_bits = 16 (the fp16 side buffer; scale mode 0):
+// for the kernels that implement that base.
+template <typename F>
+int dispatch_dbs16(int D, int bits, int scale_mode, F&& f) {
+  using B16 = std::integral_constant<int, 16>;
+  using S0 = std::integral_constant<int, 0>;
+  if (bits == 16) {
+    if (D == 64) return f(std::integral_constant<int, 64>{}, B16{}, S0{});
+    if (D == 128) return f(std::integral_constant<int, 128>{}, B16{}, S0{});
+    set_error("unsupported head_dim=%d for the fp16 base (64|128)", D);
+    return CAREKV_EINVAL;
+  }
+  return dispatch_dbs(D, bits, scale_mode, f);
+}
+
 }  // namespace carekv

@@ -123,11 +123,29 @@ __global__ __launch_bounds__(256) void store_pages_kernel(carekv_arena A, carekv
   const int nvld = job.num_valid;
   const long pg = ((long)job.kv_head * A.n_seq + job.seq) * A.max_pages + job.page;
 
-  // ---- quantize own (t, g) group of K and V, fp16 chain
+  // ---- quantize own (t, g) group of K and V, fp16 chain (or, for the fp16
+  // side-buffer base, take the given K_hat / V_hat)
   float xk[32], xv[32], rk[32], rv[32];
   int ck[32], cv[32];
   _Float16 sk = 0, sv = 0;
-  if (active) {
+  float hk[32], hv[32];  // K_hat / V_hat of the fp16 base
+  if constexpr (BITS == 16) {
+    if (active) {
+      const long o = ((long)job_id * kPage + t) * D + g * 32;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        xk[i] = h2f(Kx[o + i]); xv[i] = h2f(Vx[o + i]);
+        hk[i] = h2f(sp.k_hat[o + i]); hv[i] = h2f(sp.v_hat[o + i]);
+        // residual against the given K_hat (residual_store.py:272-285)
+        rk[i] = (t < nvld) ? (float)(_Float16)(xk[i] - hk[i]) : 0.f;
+        rv[i] = (t < nvld) ? (float)(_Float16)(xv[i] - hv[i]) : 0.f;
+        ck[i] = cv[i] = 0;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 32; ++i) { rk[i] = rv[i] = hk[i] = hv[i] = 0.f; ck[i] = cv[i] = 0; }
+    }
+  } else if (active) {
     const uint16_t* kp = Kx + ((long)job_id * kPage + t) * D + g * 32;
     const uint16_t* vp = Vx + ((long)job_id * kPage + t) * D + g * 32;
 #pragma unroll
@@ -187,7 +205,27 @@ __global__ __launch_bounds__(256) void store_pages_kernel(carekv_arena A, carekv
   int sel_k[NG], sel_v[kVtb], okind[NG + kVtb], oidx[NG + kVtb], nk, nv, nord;
   select_candidates<NG>(kerr, verr, sp, struct_prior, sel_k, nk, sel_v, nv, okind, oidx, nord);
 
-  if (MODE == 0) {
+  if constexpr (MODE == 0 && BITS == 16) {
+    // ---- fp16 side-buffer rows (cache.py:800-818) and sum of V_hat^2
+    if (active) {
+      uint32_t wk[16], wv[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        wk[i] = (uint32_t)f2h(hk[2 * i]) | ((uint32_t)f2h(hk[2 * i + 1]) << 16);
+        wv[i] = (uint32_t)f2h(hv[2 * i]) | ((uint32_t)f2h(hv[2 * i + 1]) << 16);
+      }
+      store_bytes<64>(A.kcodes + (pg * kPage + t) * RB + g * 64, wk);
+      store_bytes<64>(A.vcodes + (pg * kPage + t) * RB + g * 64, wv);
+    }
+    float vs = 0.f;
+    if (active && t < nvld) {
+#pragma unroll
+      for (int i = 0; i < 32; ++i) vs += hv[i] * hv[i];
+    }
+    vs = wave_sum(vs);
+    if (lane == 0) A.v_sq[pg] = vs;
+  }
+  if constexpr (MODE == 0 && BITS != 16) {
     // ---- packed base codes
     if (active) {
       uint32_t w[BITS];
@@ -232,6 +270,8 @@ __global__ __launch_bounds__(256) void store_pages_kernel(carekv_arena A, carekv
       vs = wave_sum(vs);
       if (lane == 0) A.v_sq[pg] = vs;
     }
+  }
+  if (MODE == 0) {
     // ---- K sketch: half(mean_t R_K[t, cg] @ P)  (residual_store.py:305,311-312)
     {
       float mean[32];
@@ -361,6 +401,100 @@ __global__ __launch_bounds__(256) void store_scan_kernel(carekv_arena A, const c
     __syncthreads();
   }
   if (threadIdx.x == 0) { A.next_slot[2 * seq] = carry_k; A.next_slot[2 * seq + 1] = carry_v; }
+}
+
+// KIVI-style value (kivi_helpers.py:35-59): half(clamp(rint(half(x / s))) * s)
+// in fp16 arithmetic; a NaN quotient (0/0) stays NaN through rint and
+// clamp, as torch's clamp propagates it.
+__device__ __forceinline__ float kivi_value(float x, float scale, int bits) {
+  const float qmax = (float)((1 << (bits - 1)) - 1);
+  const float q = rintf((float)(_Float16)(x / scale));
+  const float c = (q != q) ? q : fminf(fmaxf(q, -qmax - 1.f), qmax);
+  // the product's sign is the code's (scale >= 0): a code of -0 (the rint of
+  // a small negative quotient) gives -0 as in the reference, which a fused
+  // multiply-add with a +0 addend would turn into +0
+  const float r = (float)(_Float16)(c * scale);
+  return (c != c) ? r : copysignf(r, c);
+}
+// scale = half(max|x| / qmax); the 1e-8 floor is 0 in fp16 (a no-op)
+__device__ __forceinline__ float kivi_scale(float amax, int bits) {
+  return (float)(_Float16)(amax / (float)((1 << (bits - 1)) - 1));
+}
+
+// quant_dequant_kivi_k: one work-group per (matrix, 64 columns); 4 row
+// groups reduce max|x| per column through LDS.
+__global__ __launch_bounds__(256) void kivi_channel_kernel(const uint16_t* __restrict__ x, int rows, int D, int bits,
+                                                           uint16_t* __restrict__ out) {
+  __shared__ float s_max[4][64];
+  const int m = blockIdx.x, c0 = blockIdx.y * 64;
+  const int lane = threadIdx.x & 63, rg = threadIdx.x >> 6;
+  const int d = c0 + lane;
+  const long base = (long)m * rows * D;
+  float a = 0.f;
+  if (d < D)
+    for (int r = rg; r < rows; r += 4) a = fmaxf(a, fabsf(h2f(x[base + (long)r * D + d])));
+  s_max[rg][lane] = a;
+  __syncthreads();
+  const float amax = fmaxf(fmaxf(s_max[0][lane], s_max[1][lane]), fmaxf(s_max[2][lane], s_max[3][lane]));
+  const float sc = kivi_scale(amax, bits);
+  if (d < D)
+    for (int r = rg; r < rows; r += 4) {
+      const long i = base + (long)r * D + d;
+      out[i] = f2h(kivi_value(h2f(x[i]), sc, bits));
+    }
+}
+
+// quant_dequant_kivi_v: one wave per row.
+__global__ __launch_bounds__(256) void kivi_token_kernel(const uint16_t* __restrict__ x, long n_rows, int D, int bits,
+                                                         uint16_t* __restrict__ out) {
+  const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= n_rows) return;
+  const uint16_t* xr = x + row * D;
+  float a = 0.f;
+  for (int d = lane; d < D; d += 64) a = fmaxf(a, fabsf(h2f(xr[d])));
+  const float sc = kivi_scale(wave_max(a), bits);
+  for (int d = lane; d < D; d += 64) out[row * D + d] = f2h(kivi_value(h2f(xr[d]), sc, bits));
+}
+
+// Decode append for the fp16 side-buffer base: one wave per row; K per
+// channel over the one row (scale |k_d| / qmax), V per token
+// (layer.py:1037-1075, cache.py:820-838).
+template <int D>
+__global__ __launch_bounds__(256) void append_hat_rows_kernel(carekv_arena A, const uint16_t* __restrict__ Kx,
+                                                              const uint16_t* __restrict__ Vx,
+                                                              const int32_t* __restrict__ dest, int n_rows) {
+  constexpr int NG = D / 32;
+  const int lane = threadIdx.x & 63;
+  const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= n_rows) return;
+  const int seq = dest[row * 4], kvh = dest[row * 4 + 1], page = dest[row * 4 + 2], fresh = dest[row * 4 + 3];
+  const long pg = ((long)kvh * A.n_seq + seq) * A.max_pages + page;
+  const int off = fresh ? 0 : A.valid[pg];
+  if (off >= kPage) return;  // caller contract violated; never write past the page
+  uint16_t* krow = reinterpret_cast<uint16_t*>(A.kcodes) + (pg * kPage + off) * D;
+  uint16_t* vrow = reinterpret_cast<uint16_t*>(A.vcodes) + (pg * kPage + off) * D;
+  float av = 0.f;
+  for (int d = lane; d < D; d += 64) av = fmaxf(av, fabsf(h2f(Vx[(long)row * D + d])));
+  const float sv = kivi_scale(wave_max(av), A.hat_bits_v);
+  for (int d = lane; d < D; d += 64) {
+    const float k = h2f(Kx[(long)row * D + d]);
+    krow[d] = f2h(kivi_value(k, kivi_scale(fabsf(k), A.hat_bits_k), A.hat_bits_k));
+    vrow[d] = f2h(kivi_value(h2f(Vx[(long)row * D + d]), sv, A.hat_bits_v));
+  }
+  const bool full = off + 1 == kPage;
+  if (lane == 0) {
+    A.valid[pg] = off + 1;
+    if (fresh) A.has_meta[pg] = full ? 1 : 0;
+    if (full) { A.has_meta[pg] = 1; A.v_sq[pg] = 0.f; }
+  }
+  if (full) {
+    // store on page fill with K_orig = K_hat: zero residual -> no slots,
+    // zero errors, zero sketch (layer.py:1088-1101)
+    if (lane < NG) { A.k_slot[pg * NG + lane] = -1; A.k_err[pg * NG + lane] = 0; }
+    if (lane < kVtb) { A.v_slot[pg * kVtb + lane] = -1; A.v_err[pg * kVtb + lane] = 0; }
+    for (int i = lane; i < NG * A.sketch_dim; i += 64) A.k_sketch[pg * NG * A.sketch_dim + i] = 0;
+  }
 }
 
 // Decode append: one wave per (row); lane g < D/32 quantizes group g.
@@ -515,6 +649,11 @@ extern "C" int carekv_store_pages(const carekv_arena* arena, const carekv_store_
   CAREKV_REQUIRE(sp->sketch_proj != nullptr, "sketch_proj is required");
   StoreWs ws{(int32_t*)workspace};
   hipStream_t s = (hipStream_t)stream;
+  if (A.base_bits == 16) {
+    CAREKV_REQUIRE(sp->k_hat && sp->v_hat, "the fp16 base (base_bits=16) needs k_hat and v_hat");
+    if (A.head_dim == 64) return launch_store<64, 16>(A, *sp, K, V, jobs_dev, n_jobs, group_ptr_dev, n_groups, ws, s);
+    return launch_store<128, 16>(A, *sp, K, V, jobs_dev, n_jobs, group_ptr_dev, n_groups, ws, s);
+  }
   return dispatch_db(A.head_dim, A.base_bits, [&](auto d, auto b) {
     return launch_store<decltype(d)::value, decltype(b)::value>(A, *sp, K, V, jobs_dev, n_jobs, group_ptr_dev,
                                                                 n_groups, ws, s);
@@ -528,6 +667,16 @@ extern "C" int carekv_append_rows(const carekv_arena* arena, const uint16_t* k_r
   const carekv_arena& A = *arena;
   CAREKV_REQUIRE(check_arena(A), last_error_buf());
   hipStream_t s = (hipStream_t)stream;
+  if (A.base_bits == 16) {
+    if (A.head_dim == 64)
+      hipLaunchKernelGGL(append_hat_rows_kernel<64>, dim3((n_rows + 3) / 4), dim3(256), 0, s, A, k_rows, v_rows,
+                         dest_dev, n_rows);
+    else
+      hipLaunchKernelGGL(append_hat_rows_kernel<128>, dim3((n_rows + 3) / 4), dim3(256), 0, s, A, k_rows, v_rows,
+                         dest_dev, n_rows);
+    CAREKV_CHECK_LAUNCH("append_hat_rows");
+    return CAREKV_OK;
+  }
   return dispatch_db(A.head_dim, A.base_bits, [&](auto d, auto b) {
     hipLaunchKernelGGL((append_rows_kernel<decltype(d)::value, decltype(b)::value>), dim3((n_rows + 3) / 4),
                        dim3(256), 0, s, A, k_rows, v_rows, dest_dev, n_rows);
@@ -544,6 +693,7 @@ extern "C" int carekv_read_pages(const carekv_arena* arena, int32_t seq, int32_t
   CAREKV_REQUIRE(check_arena(A), last_error_buf());
   CAREKV_REQUIRE(seq >= 0 && seq < A.n_seq && kv_head >= 0 && kv_head < A.n_kv_heads, "seq/kv_head out of range");
   CAREKV_REQUIRE(n_pages >= 0 && n_pages <= A.max_pages, "n_pages out of range");
+  CAREKV_REQUIRE(A.base_bits != 16, "the fp16 base has no codes to read: read its pages directly");
   if (n_pages == 0) return CAREKV_OK;
   hipStream_t s = (hipStream_t)stream;
   return dispatch_db(A.head_dim, A.base_bits, [&](auto d, auto b) {
@@ -569,5 +719,24 @@ extern "C" int carekv_quantize_rows(const uint16_t* x, int32_t rows, int32_t D, 
     default: hipLaunchKernelGGL(quantize_rows_kernel<4>, dim3(blocks), dim3(256), 0, s, x, rows, D, pack, codes, scale); break;
   }
   CAREKV_CHECK_LAUNCH("quantize_rows");
+  return CAREKV_OK;
+}
+
+extern "C" int carekv_kivi_qdq(const uint16_t* x, int32_t n_mat, int32_t rows, int32_t D, int32_t bits,
+                               int32_t per_channel, uint16_t* out, void* stream) {
+  CAREKV_REQUIRE(x && out, "null argument");
+  CAREKV_REQUIRE(bits >= 2 && bits <= 4, "bits must be 2, 3 or 4");
+  CAREKV_REQUIRE(D > 0 && D <= 1024 && n_mat >= 0 && rows >= 0, "bad shape");
+  if (n_mat == 0 || rows == 0) return CAREKV_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (per_channel) {
+    CAREKV_REQUIRE(n_mat <= 65535 * 1024, "too many matrices");
+    hipLaunchKernelGGL(kivi_channel_kernel, dim3(n_mat, (D + 63) / 64), dim3(256), 0, s, x, rows, D, bits, out);
+  } else {
+    const long n_rows = (long)n_mat * rows;
+    CAREKV_REQUIRE((n_rows + 3) / 4 <= 0x7fffffffL, "too many rows");
+    hipLaunchKernelGGL(kivi_token_kernel, dim3((unsigned)((n_rows + 3) / 4)), dim3(256), 0, s, x, n_rows, D, bits, out);
+  }
+  CAREKV_CHECK_LAUNCH("kivi_qdq");
   return CAREKV_OK;
 }

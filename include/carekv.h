@@ -28,7 +28,11 @@ extern "C" {
  * CAREKVCache._init_buffers (cache.py:430-536) with the sequence slot as an
  * extra dimension next to the kv head:
  *   page index pg = (kv_head * n_seq + seq) * max_pages + page
- *   kcodes/vcodes  int8   [pg][page_size][row_bytes]   packed base codes
+ *   kcodes/vcodes  int8   [pg][page_size][row_bytes]   packed base codes,
+ *                  or, with base_bits = 16, fp16 [pg][page_size][head_dim]:
+ *                  the K_hat / V_hat side buffer of the KIVI-style base
+ *                  (cache.py:487-499, base_K_hat_fp16); the scale and
+ *                  master buffers are then unused and may be NULL
  *   kscale/vscale  int8   [pg][page_size][G]  (scale_mode 1: int8 codes)
  *                  fp16   [pg][page_size][G]  (scale_mode 0: raw fp16)
  *   kmaster/vmaster fp16  [pg]                 per-page master scale
@@ -66,6 +70,8 @@ typedef struct carekv_arena {
   int32_t* next_slot;
   int32_t n_seq, n_kv_heads, max_pages, head_dim, base_bits, page_size, group_size;
   int32_t k_channel_group, v_token_block, sketch_dim, scale_mode, residual_bits, n_slots;
+  int32_t hat_bits_k, hat_bits_v; /* base_bits = 16: the KIVI bits of a decode
+                                   * append's K and V row (layer.py:197-202)  */
 } carekv_arena;
 
 /* Store-time knobs, resolved on the host from CacheConfig and the
@@ -79,6 +85,10 @@ typedef struct carekv_store_params {
   double sensitivity;      /* cfg.layer_sensitivity[layer]                      */
   int32_t sink_tokens;     /* prefill: is_sink = token_start < sink_tokens      */
   const float* sketch_proj;/* [k_channel_group][sketch_dim] fp32 (get_sketch_proj) */
+  const uint16_t* k_hat;   /* base_bits = 16: fp16 K_hat / V_hat rows laid out  */
+  const uint16_t* v_hat;   /* like K / V, written as the pages and the residual
+                            * base (process_page with K_hat_override,
+                            * residual_store.py:272-275); NULL otherwise       */
 } carekv_store_params;
 
 /* One page write (prefill).  X rows for page j are X[j*page_size .. +page_size),
@@ -106,7 +116,10 @@ int64_t carekv_store_workspace_bytes(int32_t n_jobs);
 
 /* One decode-token append per row (layer.py:1028-1146, cache.py:656-701):
  * quantize the row, pack it at (seq, kv_head, page, valid[pg]), encode its
- * scales against the page's fixed master (clamped at 1e-8), bump valid, and
+ * scales against the page's fixed master (clamped at 1e-8) -- with
+ * base_bits = 16, quant-dequant it alone in KIVI style (K per channel over
+ * the one row, V per token, hat_bits_k/v; layer.py:1037-1075,
+ * cache.py:820-838) and write the fp16 row --, bump valid, and
  * when the page becomes full write its PageMeta with the store run on
  * K_orig = K_hat (zero residual: no slots, zero errors and sketches).
  * dest_dev: int32 [n_rows][4] = (seq, kv_head, page, fresh); fresh=1 marks
@@ -188,6 +201,16 @@ int carekv_read_pages(const carekv_arena* arena, int32_t seq, int32_t kv_head, i
  * pack != 0); scale fp16 [rows][D/group]. */
 int carekv_quantize_rows(const uint16_t* x, int32_t rows, int32_t D, int32_t bits, int32_t group,
                          int32_t pack, int8_t* codes, uint16_t* scale, void* stream);
+
+/* KIVI-style quant-dequant (kivi_helpers.py:35-59), in fp16 arithmetic:
+ * x, out fp16 [n_mat][rows][D].  per_channel != 0: quant_dequant_kivi_k,
+ * one scale per (matrix, column) over the rows (K over the sequence);
+ * per_channel == 0: quant_dequant_kivi_v, one scale per row (V per token).
+ * scale = half(max|x| / qmax), code = clamp(rint(half(x / scale))),
+ * out = half(code * scale); an all-zero channel (or a zero component of a
+ * single-row K) gives NaN, as in the reference.  bits 2, 3 or 4; D <= 1024. */
+int carekv_kivi_qdq(const uint16_t* x, int32_t n_mat, int32_t rows, int32_t D, int32_t bits, int32_t per_channel,
+                    uint16_t* out, void* stream);
 
 /* Prefill attention over dequantised K/V: CAREKVLayer._causal_attention_pure
  * (layer.py:935-972) for a batch of sequences, with GQA heads read in place

@@ -4,7 +4,8 @@ Bars: packed codes, int8 scale codes, masters, valid counts, slot ids and
 residual slot bytes bit-exact; fp16 error norms / sketches within one fp16
 ulp; selected candidates equal except swaps across an epsilon-tie of the
 normalised scores (relative 1e-4 of the selection boundary); decode output
-within max-abs 2e-3 and relative-L2 1e-2 of the reference fp32 path.
+within max-abs 2e-3 (or one fp16 ulp of the reference output, where that is
+larger) and relative-L2 1e-2 of the reference fp32 path.
 """
 import math
 
@@ -48,18 +49,28 @@ def compare_cache_to_golden(cache, g, prefix=""):
     valid = cache.valid[0, :, 0].cpu().numpy()
     assert np.array_equal(valid, g[prefix + "valid"]), "valid_tokens"
     H, P = valid.shape
-    for nm, t in (("K_codes", cache.kcodes), ("V_codes", cache.vcodes), ("K_scale", cache.kscale),
-                  ("V_scale", cache.vscale)):
-        mine = t[0, :, 0].cpu().numpy()
-        ref = g[prefix + nm]
-        for h in range(H):
-            for p in range(P):
-                n = int(valid[h, p])
-                assert np.array_equal(mine[h, p, :n], ref[h, p, :n]), (nm, h, p)
-    for nm, t in (("K_master", cache.kmaster), ("V_master", cache.vmaster)):
-        mine = t[0, :, 0].cpu().numpy()
-        used = valid > 0
-        assert np.array_equal(mine[used], g[prefix + nm][used]), nm
+    if prefix + "K_hat" in g:
+        # fp16 side buffer: K_hat / V_hat rows bit for bit (NaN patterns included)
+        for nm, t in (("K_hat", cache.kcodes), ("V_hat", cache.vcodes)):
+            mine = t[0, :, 0].cpu().numpy().view(np.uint16)
+            ref = g[prefix + nm].view(np.uint16)
+            for h in range(H):
+                for p in range(P):
+                    n = int(valid[h, p])
+                    assert np.array_equal(mine[h, p, :n], ref[h, p, :n]), (nm, h, p)
+    else:
+        for nm, t in (("K_codes", cache.kcodes), ("V_codes", cache.vcodes), ("K_scale", cache.kscale),
+                      ("V_scale", cache.vscale)):
+            mine = t[0, :, 0].cpu().numpy()
+            ref = g[prefix + nm]
+            for h in range(H):
+                for p in range(P):
+                    n = int(valid[h, p])
+                    assert np.array_equal(mine[h, p, :n], ref[h, p, :n]), (nm, h, p)
+        for nm, t in (("K_master", cache.kmaster), ("V_master", cache.vmaster)):
+            mine = t[0, :, 0].cpu().numpy()
+            used = valid > 0
+            assert np.array_equal(mine[used], g[prefix + nm][used]), nm
     nk, nv = g[prefix + "k_res"].shape[0], g[prefix + "v_res"].shape[0]
     assert cache.next_slot[0].tolist() == [nk, nv], "slot counters"
     assert np.array_equal(cache.k_res[0, :nk].cpu().numpy(), g[prefix + "k_res"])
@@ -122,6 +133,32 @@ def test_append_matches_reference(paper_env):
     assert np.array_equal(vs.cpu().numpy(), g["read_Vs"])
 
 
+@pytest.mark.parametrize("bits", [2, 3, 4])
+def test_kivi_qdq_matches_oracle(bits):
+    """carekv_kivi_qdq vs the oracle's quant_dequant_kivi_k / _v, bit for bit
+    (NaN included: an all-zero K channel and a zero component of a one-row K
+    divide 0 by a zero scale, as in the reference)."""
+    import care_kv
+    rng = np.random.default_rng(bits)
+    X = (rng.standard_normal((3, 70, 128)) * np.exp(rng.standard_normal((1, 1, 128)))).astype(F16)
+    X[1, :, 5] = 0
+    X[2, 4, 7] = 0
+    xd = torch.from_numpy(X).cuda()
+
+    def same(got, ref):  # bit for bit (signed zeros included); NaN where the reference has NaN
+        nan = np.isnan(ref.astype(F32))
+        return np.array_equal(np.isnan(got.astype(F32)), nan) and \
+            np.array_equal(got.view(np.uint16)[~nan], ref.view(np.uint16)[~nan])
+    for per_channel in (True, False):
+        got = care_kv.kivi_qdq(xd, bits, per_channel).cpu().numpy()
+        ref = Q.kivi_qdq(X, bits, per_channel)
+        assert same(got, ref), per_channel
+    row = xd[2, 4:5]
+    got = care_kv.kivi_qdq(row, bits, True).cpu().numpy()
+    ref = Q.kivi_qdq(X[2, 4:5], bits, True)
+    assert np.isnan(ref[0, 7]) and same(got, ref)
+
+
 # ------------------------------------------------------------------ decode
 def build_gpu_case(g, name):
     import care_kv
@@ -168,8 +205,13 @@ def check_decode(cache, oc, spec, Qh, ref_out, paper_env, k_mode):
                 n_mismatch += 1
                 assert ties_explain(mine, ref_rows[j], d, Kc, Vc, j, eps=spec.get("tie_eps", 1e-4)), \
                     (h, j, sorted(mine ^ ref_rows[j]))
-    err = np.abs(out - ref_out.astype(F32))
-    assert err.max() <= 2e-3, err.max()
+    # max-abs 2e-3, or one fp16 ulp of the reference where that is larger
+    # (both sides round an fp32 result to fp16: outputs of magnitude >= 2,
+    # as with the INT2 KIVI base's wide per-token V scales, can flip an ulp)
+    ref32 = ref_out.astype(F32)
+    err = np.abs(out - ref32)
+    ulp = np.spacing(np.abs(ref_out).astype(F16)).astype(F32)
+    assert np.all(err <= np.maximum(2e-3, ulp)), (err.max(), float(np.abs(ref32).max()))
     rel = np.linalg.norm(out - ref_out.astype(F32)) / max(np.linalg.norm(ref_out.astype(F32)), 1e-30)
     assert rel <= 1e-2, rel
     return n_mismatch, o_out

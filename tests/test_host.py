@@ -62,9 +62,13 @@ def test_unsupported_config_rejected():
     from care_kv.cache import check_kernel_config
     with pytest.raises(NotImplementedError):
         check_kernel_config(care_kv.CacheConfig(page_size=8, group_size=32, base_bits=3))
-    with pytest.raises(NotImplementedError):
-        check_kernel_config(care_kv.CacheConfig(base_quantizer="kivi_style", group_size=32))
+    with pytest.raises(NotImplementedError):  # rotation bases are not built
+        check_kernel_config(care_kv.CacheConfig(base_quantizer="rotatekv_style", group_size=32))
+    with pytest.raises(NotImplementedError):  # pre-RoPE KVQuant is not built
+        check_kernel_config(care_kv.CacheConfig(base_quantizer="kvquant_style", k_store_mode="pre_rope",
+                                                group_size=32))
     check_kernel_config(care_kv.CacheConfig(group_size=32, base_bits=3, head_dim=128))
+    check_kernel_config(care_kv.CacheConfig(base_quantizer="kivi_style", group_size=32, base_bits=2))
 
 
 def test_config_validation_matches_reference():
@@ -148,7 +152,8 @@ def test_adapter_interface_and_limits():
     assert abs(m["base_memory_MB"] - round(fp16 * 3 / 16, 4)) < 1e-3
     assert a.effective_budgets()["effective_read_budget"] == "fixed RK=2 RV=2"
     with pytest.raises(NotImplementedError):
-        CAREKVAdapter(base_quantizer="kivi_style")
+        CAREKVAdapter(base_quantizer="rotatekv_style")
+    assert CAREKVAdapter(base_quantizer="kivi_style", bits=2).env()["CAREKV_BASE_QUANTIZER"] == "kivi_style"
     ad = CAREKVAdapter(mode="adaptive", rel_threshold=0.25, max_rk=4, max_rv=6)
     assert ad.name == "CAREKV_adaptive_rel0.25"
     e = ad.env()
