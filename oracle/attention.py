@@ -436,6 +436,54 @@ def decode_attention(cache: OCache, layer_id, Qh, page_ids_by_kvh=None, correcti
     return out
 
 
+def prefill_stored(cache: OCache, layer_id, Qh, K_hat, V_hat, correction=True, diag=None, **corr_kw):
+    """Prefill attention of ``CAREKVLayer.prefill`` in carekv_stored mode
+    (layer.py:780-838) with the vectorized correction (layer.py:538-557).
+
+    Qh (Hq, T, D) fp16 post-RoPE queries; K_hat / V_hat (Hkv, T, D) fp16 the
+    page writer's dequantised prompt (write_pages_for_kv_head).  Per kv head:
+    the causal base attention of _causal_attention_pure (fp32 scores with
+    finfo(fp32).min above the diagonal, softmax weights cast to fp16,
+    O_base = half(A @ V_hat)), then vectorized_joint_correction over the
+    kv_group x T queries (head-major) against every page of the kv head,
+    out = half(O_base + delta).  ``correction=False`` or no read budget gives
+    the base (the any_read_budget short-circuit, layer.py:810-823).
+    Returns (T, Hq, D) fp16."""
+    cfg = cache.cfg
+    Qh = np.asarray(Qh, F16)
+    Hq, T, D = Qh.shape
+    Hkv = cfg.num_kv_heads
+    grp = Hq // Hkv
+    mn = np.finfo(F32).min
+    causal = np.where(np.arange(T)[None, :] > np.arange(T)[:, None], mn, F32(0)).astype(F32)
+    any_budget = ((cfg.read_budget_mode in ("absolute", "adaptive_score") and (cfg.read_abs_k > 0 or cfg.read_abs_v > 0))
+                  or cfg.read_budget_ratio > 0 or (cfg.read_budget_ratio_k or 0) > 0
+                  or (cfg.read_budget_ratio_v or 0) > 0)
+    out = np.zeros((Hq, T, D), F16)
+    for h in range(Hkv):
+        heads = list(range(h * grp, (h + 1) * grp))
+        Kf = np.asarray(K_hat[h], F16).astype(F32)
+        Vf = np.asarray(V_hat[h], F16).astype(F32)
+        Qg = Qh[heads].astype(F32)
+        S = (Qg @ Kf.T) / F32(math.sqrt(D)) + causal[None]
+        m = S.max(axis=-1, keepdims=True)
+        e = np.exp(S - m, dtype=F32)
+        A = (e / e.sum(axis=-1, keepdims=True, dtype=F32)).astype(F16)
+        O_base = (A.astype(F32) @ Vf).astype(F16)
+        if not (correction and any_budget):
+            out[heads] = O_base
+            continue
+        pids = cache.all_page_ids(layer_id, h)
+        d = None if diag is None else diag.setdefault(h, {})
+        delta = vectorized_joint_correction(cache, layer_id, h, pids, Qg.reshape(-1, D), S.reshape(-1, T),
+                                            A.astype(F32).reshape(-1, T), Vf, O_base.astype(F32).reshape(-1, D),
+                                            diag=d, **corr_kw)
+        out[heads] = (O_base.astype(F32) + delta.reshape(grp, T, D)).astype(F16)
+        if d is not None:
+            d.update(S=S.reshape(-1, T), A=A.astype(F32).reshape(-1, T), V_hat=Vf, K_hat=Kf)
+    return out.transpose(1, 0, 2)
+
+
 def causal_attention_pure(Qh, K, V, causal=True, rows=None):
     """layer.py:935-972: scores = fp32(Q) . fp32(K) / sqrt(D); causal mask with
     finfo(fp32).min above the diagonal; softmax in fp32; weights cast to

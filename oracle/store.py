@@ -149,7 +149,11 @@ def process_page(cache: OCache, layer_id: int, kv_head: int, page_id: int,
 
 def write_pages_for_kv_head(cache: OCache, layer_id: int, kv_h: int, K_kv, V_kv,
                             token_start_abs: int = 0, sink_tokens: int = 4, P=None, **store_kw):
-    """``layer.py:204-334`` (uniform base quantizer): pad, quantize, write, store."""
+    """``layer.py:204-334``: pad, quantize, write, store.  Returns the prompt's
+    (K_hat, V_hat) over its valid rows as the reference's page writer does
+    (layer.py:331-334): half(code * fp16 group scale) for the uniform base
+    (the pages keep the int8-requantised scales), the KIVI quant-dequant for
+    the side-buffer bases."""
     cfg = cache.cfg
     K_kv = np.asarray(K_kv)
     V_kv = np.asarray(V_kv)
@@ -175,7 +179,8 @@ def write_pages_for_kv_head(cache: OCache, layer_id: int, kv_h: int, K_kv, V_kv,
                          token_start=token_start_abs + t0, num_valid=nv, is_recent=p >= num_pages - 4,
                          is_sink=(token_start_abs + t0) < sink_tokens, K_hat_override=Khp, V_hat_override=Vhp,
                          P=P, **store_kw)
-        return
+        return Kh_seq, Vh_seq
+    k_hat, v_hat = [], []
     for p in range(num_pages):
         t0, t1 = p * ps, min((p + 1) * ps, T)
         nv = t1 - t0
@@ -192,6 +197,9 @@ def write_pages_for_kv_head(cache: OCache, layer_id: int, kv_h: int, K_kv, V_kv,
         process_page(cache, layer_id, kv_h, pid, Kp, Vp, Kc, Ks, Vc, Vs,
                      token_start=token_start_abs + t0, num_valid=nv,
                      is_recent=is_recent, is_sink=is_sink, P=P, **store_kw)
+        k_hat.append(Q.dequantize(Kc, Ks, cfg.group_size).astype(K_kv.dtype)[:nv])
+        v_hat.append(Q.dequantize(Vc, Vs, cfg.group_size).astype(V_kv.dtype)[:nv])
+    return np.concatenate(k_hat), np.concatenate(v_hat)
 
 
 def decode_append(cache: OCache, layer_id: int, k_rows, v_rows, **store_kw):

@@ -276,6 +276,69 @@ def golden_decode_proxy(ck):
                  read_k=16, read_v=16, n_append=27, kscore_live=False)
 
 
+def _prefill_case(ck, name, *, Hq, Hkv, D, T, seed, outlier_mult, store, read_k, read_v, k_mode="exact",
+                  policy="joint", base_bits=3):
+    """CAREKVLayer.prefill in carekv_stored mode (layer.py:643-840) with the
+    vectorized correction over all kv_group x T queries of a kv head
+    (layer.py:538-557): the causal base attention over the prefill's own
+    K_hat / V_hat, then vectorized_joint_correction with the fp16 attention
+    weights.  Also the base_quant output of the same prompt (fresh cache)."""
+    from CARE_KV.care_kv.attention import set_chunk_recorder
+    env = dict(CAREKV_STORE_POLICY="residual_kind_aware", CAREKV_PREFILL_RESIDUAL_KIND="both",
+               CAREKV_K_CORRECTION_MODE=k_mode, CAREKV_KSCORE_LIVE="1", CAREKV_SCORE_NORMALIZE="1",
+               CAREKV_DEBUG_STATS="0", CAREKV_CORRECTION_IMPL="vectorized")
+    _set_env(**env)
+    K, V = _gen_kv(seed, Hkv, T, D, outlier_mult=outlier_mult)
+    qg = torch.Generator().manual_seed(seed + 200)
+    Q = torch.randn(T, Hq, D, generator=qg).half()
+    hidden = torch.cat([Q.reshape(T, -1), K.permute(1, 0, 2).reshape(T, -1), V.permute(1, 0, 2).reshape(T, -1)], 1)
+    out = {}
+    for mode in ("base_quant", "carekv_stored"):
+        _set_env(CAREKV_PREFILL_MODE=mode)
+        cfg = ck.CacheConfig(num_layers=1, num_heads=Hq, num_kv_heads=Hkv, head_dim=D, page_size=16,
+                             max_pages=T // 16 + 4, base_bits=base_bits, group_size=32, k_channel_group=32,
+                             v_token_block=4, sketch_dim=32, packed_base=True, scale_quant="int8",
+                             read_budget_ratio=0.0, read_budget_mode="absolute", read_abs_k=read_k,
+                             read_abs_v=read_v, route_policy=policy, correction_impl="vectorized", **store)
+        cache = ck.CAREKVCache(cfg, torch.device("cpu"))
+        layer = _selector_layer(ck, cfg)
+        rec = []
+        set_chunk_recorder(rec)
+        o = layer.prefill(cache, hidden)
+        set_chunk_recorder(None)
+        out[mode] = o[:, :Hq * D].reshape(T, Hq, D).numpy()
+        if mode == "carekv_stored":
+            # per kv head, the query chunks' records in query order (the
+            # assembled record of a chunked call carries no scores)
+            for h in range(Hkv):
+                parts = sorted((r for r in rec if r["kv_head"] == h and r.get("q_offset", 0) != -1),
+                               key=lambda r: r.get("q_offset", 0))
+                for key in ("score_K", "score_V", "sel_k", "sel_v"):
+                    vs = [r.get(key) for r in parts]
+                    if vs and all(v is not None for v in vs):
+                        out[f"h{h}_{key}"] = torch.cat(vs, 0).numpy()
+    d = _cache_arrays(cache)
+    d.update({k: v for k, v in out.items() if k.startswith("h")})
+    d.update(K=K.numpy(), V=V.numpy(), Q=Q.numpy(), O=out["carekv_stored"], O_base=out["base_quant"],
+             T=np.array(T), n_append=np.array(0), read_k=np.array(read_k), read_v=np.array(read_v))
+    _set_env(CAREKV_PREFILL_MODE="fp", CAREKV_CORRECTION_IMPL="cached")
+    np.savez_compressed(os.path.join(HERE, f"prefill_{name}.npz"), **d)
+
+
+def golden_prefill(ck):
+    ratio3 = dict(store_budget_mode="ratio", store_budget_ratio=0.03)
+    # TinyLlama head shape (GQA 8, D=64), a partial last page, tight joint read
+    _prefill_case(ck, "gqa8_d64", Hq=16, Hkv=2, D=64, T=200, seed=21, outlier_mult=8.0, store=ratio3,
+                  read_k=4, read_v=4)
+    # GQA 4, D=128, paper store budget SK=2 SV=4, separate policy
+    _prefill_case(ck, "gqa4_d128", Hq=8, Hkv=2, D=128, T=150, seed=22, outlier_mult=10.0,
+                  store=dict(store_budget_mode="absolute", store_abs_k=2, store_abs_v=4), read_k=6, read_v=6,
+                  policy="separate")
+    # MHA, linear K mode
+    _prefill_case(ck, "mha_d128_linear", Hq=2, Hkv=2, D=128, T=120, seed=23, outlier_mult=6.0, store=ratio3,
+                  read_k=3, read_v=3, k_mode="linear")
+
+
 ROUTE_VARIANTS = [  # (route_policy, adaptive_score (rel, abs, min_keep) or None)
     ("joint", None), ("separate", None), ("k_first", None), ("adaptive", None),
     ("joint", (0.5, 0.0, 0)), ("separate", (0.0, 1.5, 3)), ("k_first", (0.8, 0.0, 2)), ("adaptive", (0.3, 0.9, 0)),
@@ -437,7 +500,8 @@ def golden_activation_slices():
     np.savez_compressed(os.path.join(HERE, "activations_3d_slices.npz"), **out)
 
 
-PARTS = ("activations", "sketch", "store", "append", "decode", "decode_proxy", "decode_kivi", "route", "fixture")
+PARTS = ("activations", "sketch", "store", "append", "decode", "decode_proxy", "decode_kivi", "prefill", "route",
+         "fixture")
 
 if __name__ == "__main__":
     # CAREKV_GOLDEN_PARTS=decode_proxy,... writes only those fixtures
@@ -450,7 +514,8 @@ if __name__ == "__main__":
     if any(p != "activations" for p in parts):
         ck = _import_reference()
         fns = dict(sketch=golden_sketch, store=golden_store, append=golden_append, decode=golden_decode,
-                   decode_proxy=golden_decode_proxy, decode_kivi=golden_decode_kivi, route=golden_route,
+                   decode_proxy=golden_decode_proxy, decode_kivi=golden_decode_kivi, prefill=golden_prefill,
+                   route=golden_route,
                    fixture=golden_reference_fixture)
         for p in parts:
             if p in fns:

@@ -38,6 +38,38 @@ DECODE_CASES = {
                            base_quantizer="kivi_style", base_bits=2, score_rtol=1e-4),
 }
 
+# prefill (carekv_stored, vectorized correction) golden cases
+PREFILL_CASES = {
+    "gqa8_d64": dict(Hq=16, Hkv=2, D=64, store=dict(store_budget_mode="ratio", store_budget_ratio=0.03),
+                     k_mode="exact", policy="joint"),
+    "gqa4_d128": dict(Hq=8, Hkv=2, D=128, store=dict(store_budget_mode="absolute", store_abs_k=2, store_abs_v=4),
+                      k_mode="exact", policy="separate"),
+    "mha_d128_linear": dict(Hq=2, Hkv=2, D=128, store=dict(store_budget_mode="ratio", store_budget_ratio=0.03),
+                            k_mode="linear", policy="joint"),
+}
+
+
+def prefill_cfg_kwargs(g, spec):
+    T = int(g["T"])
+    return dict(num_layers=1, num_heads=spec["Hq"], num_kv_heads=spec["Hkv"], head_dim=spec["D"], page_size=16,
+                max_pages=T // 16 + 4, base_bits=3, group_size=32, k_channel_group=32, v_token_block=4,
+                sketch_dim=32, read_budget_mode="absolute", read_abs_k=int(g["read_k"]),
+                read_abs_v=int(g["read_v"]), route_policy=spec["policy"], **spec["store"])
+
+
+def build_oracle_prefill(g, name):
+    """Oracle cache of a prefill golden case and the page writer's K_hat / V_hat."""
+    spec = PREFILL_CASES[name]
+    c = OCache(OCfg(**prefill_cfg_kwargs(g, spec)))
+    T = int(g["T"])
+    kh, vh = [], []
+    for h in range(spec["Hkv"]):
+        a, b = write_pages_for_kv_head(c, 0, h, g["K"][h, :T], g["V"][h, :T], token_start_abs=0, sink_tokens=4)
+        kh.append(a)
+        vh.append(b)
+    return c, spec, np.stack(kh), np.stack(vh)
+
+
 PAPER_ENV = dict(CAREKV_STORE_POLICY="residual_kind_aware", CAREKV_PREFILL_RESIDUAL_KIND="both",
                  CAREKV_KSCORE_LIVE="1", CAREKV_SCORE_NORMALIZE="1", CAREKV_K_CORRECTION_SCALE="0.1")
 

@@ -6,7 +6,7 @@ import numpy as np
 import pytest
 
 from oracle import quant as Q
-from oracle.attention import (decode_attention, exact_softmax_correction,
+from oracle.attention import (decode_attention, exact_softmax_correction, prefill_stored,
                               query_aware_kscore_slot, softmax_rows,
                               vectorized_joint_correction)
 from oracle.cache import OCache, OCfg
@@ -182,7 +182,7 @@ def test_append_golden(golden):
 
 
 # ------------------------------------------------------------ decode goldens
-from helpers import DECODE_CASES  # noqa: E402  (shared with the GPU parity tests)
+from helpers import DECODE_CASES, PREFILL_CASES, build_oracle_prefill  # noqa: E402  (shared with the GPU tests)
 
 
 def build_decode_case(g, name):
@@ -246,6 +246,56 @@ def test_decode_golden(golden, name):
         # the reference decode_step itself (correction gated off by read_budget_ratio=0)
         base = decode_attention(c, 0, g["Q"], correction=False)
         assert np.abs(base.astype(F32) - g["decode_step_out"].astype(F32)).max() <= 2e-3
+
+
+# ------------------------------------------------------------ prefill carekv_stored
+@pytest.mark.parametrize("name", list(PREFILL_CASES))
+def test_prefill_stored_golden(golden, name):
+    """CAREKVLayer.prefill in carekv_stored mode with the vectorized
+    correction (layer.py:538-557, 780-838): cache bytes, the base_quant
+    output, the corrected output and the per-query selections."""
+    g = golden(f"prefill_{name}.npz")
+    c, spec, Kh, Vh = build_oracle_prefill(g, name)
+    _compare_cache(c, g)
+    Qh = g["Q"].transpose(1, 0, 2)
+    base = prefill_stored(c, 0, Qh, Kh, Vh, correction=False)
+    # torch's fp16 einsum and numpy's fp32 matmul sum in different orders:
+    # up to 0.2% of the outputs land one fp16 rounding apart (where the sum
+    # cancels, up to 1.2e-4 absolute on small outputs)
+    ref = g["O_base"]
+    err = np.abs(base.astype(F32) - ref.astype(F32))
+    ulp = np.spacing(np.maximum(np.abs(ref), np.abs(base))).astype(F32)
+    assert np.all(err <= np.maximum(ulp, 2.5e-4)) and np.mean(err > 0) < 5e-3, (err.max(), np.mean(err > 0))
+    diag = {}
+    out = prefill_stored(c, 0, Qh, Kh, Vh, k_mode=spec["k_mode"], kind="both", k_corr_scale=0.1,
+                         score_normalize=True, kscore_live=True, diag=diag)
+    err = np.abs(out.astype(F32) - g["O"].astype(F32))
+    assert err.max() <= 1e-3, err.max()
+    for h, d in diag.items():
+        if f"h{h}_sel_k" in g:
+            sK, sV = d["score_K_r"], d["score_V_r"]
+            merged = np.concatenate([sK, sV], 1)
+            # candidates of pages after a query's row score 0 (A = 0 there);
+            # top-k picks among such ties arbitrarily and they change nothing
+            pos = merged > 0
+            sel_ref = np.concatenate([g[f"h{h}_sel_k"], g[f"h{h}_sel_v"]], 1) & pos
+            sel_me = np.concatenate([d["sel_k"], d["sel_v"]], 1) & pos
+            if spec["policy"] == "joint":
+                mb = int(np.concatenate([g[f"h{h}_sel_k"], g[f"h{h}_sel_v"]], 1)[0].sum())
+                assert selection_matches(sel_me, sel_ref, merged, mb)
+            else:
+                nk = sK.shape[1]
+                for lo, hi, cap in ((0, nk, int(g["read_k"])), (nk, merged.shape[1], int(g["read_v"]))):
+                    assert selection_matches(sel_me[:, lo:hi], sel_ref[:, lo:hi], merged[:, lo:hi],
+                                             min(cap, hi - lo))
+            # the weights are fp16 roundings of softmax values: where numpy's
+            # and torch's fp32 softmax straddle a rounding point a weight
+            # moves one fp16 ulp (2^-11 relative), and so does its score term
+            for key in ("score_K", "score_V"):
+                a, b = d[key], g[f"h{h}_{key}"]
+                rel = np.abs(a - b) / np.maximum(np.abs(b), 1e-30)
+                rel[(np.abs(a - b) <= 1e-12)] = 0.0
+                assert rel.max() <= 1e-3 and np.mean(rel > 2e-5) < 1e-3, (key, rel.max(), np.mean(rel > 2e-5))
 
 
 # ------------------------------------------------------------ reference test fixture grid
