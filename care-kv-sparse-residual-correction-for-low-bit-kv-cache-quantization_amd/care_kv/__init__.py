@@ -8,7 +8,7 @@ runs in ``libcarekv_hip.so`` through a C ABI (include/carekv.h).
 from .config import (CacheConfig, apply_carekv_env_overrides, layer_budget_multiplier,
                      resolve_read_knobs, resolve_store_knobs)
 from .cache import CAREKVCache, PageMeta, get_sketch_proj, kivi_qdq, packed_row_bytes
-from .attention import CAREKVMultiHeadAttention, decode_attention
+from .attention import CAREKVMultiHeadAttention, decode_attention, prefill_correction
 from .prefill import dequantize_rows, prefill_attention, quant_dequant, quantize_rows
 from .layer import CAREKVLayer
 from .llama_patch import CAREKVLlamaAttention, patch_llama_model, reset_all_caches
@@ -19,7 +19,7 @@ __version__ = "0.1.0"
 __all__ = [
     "CacheConfig", "apply_carekv_env_overrides", "layer_budget_multiplier", "resolve_read_knobs",
     "resolve_store_knobs", "CAREKVCache", "PageMeta", "get_sketch_proj", "kivi_qdq", "packed_row_bytes",
-    "CAREKVMultiHeadAttention", "decode_attention", "prefill_attention", "quantize_rows", "dequantize_rows",
+    "CAREKVMultiHeadAttention", "decode_attention", "prefill_correction", "prefill_attention", "quantize_rows", "dequantize_rows",
     "quant_dequant", "CAREKVLayer", "CAREKVLlamaAttention", "patch_llama_model", "reset_all_caches",
     "CAREKVAdapter", "CarekvError",
 ]

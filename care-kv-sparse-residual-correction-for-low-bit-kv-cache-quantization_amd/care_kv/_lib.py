@@ -54,12 +54,18 @@ class PrefillParams(C.Structure):
         [("sm_scale", C.c_float)]
 
 
+class PrefillCorrParams(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("seq", "n_tokens", "row_begin", "n_rows")] + \
+        [(n, C.c_void_p) for n in ("k_hat", "v_hat", "lse")]
+
+
 # page job: int32 x 6 (seq, kv_head, page, num_valid, token_start, is_recent)
 PAGE_JOB_INTS = 6
 
 EXPORTS = ["carekv_store_pages", "carekv_store_workspace_bytes", "carekv_append_rows", "carekv_decode_attn",
            "carekv_decode_workspace_bytes", "carekv_read_pages", "carekv_quantize_rows", "carekv_prefill_attn",
-           "carekv_dequantize_rows", "carekv_kivi_qdq", "carekv_last_error"]
+           "carekv_dequantize_rows", "carekv_kivi_qdq", "carekv_prefill_correct",
+           "carekv_prefill_correct_workspace_bytes", "carekv_last_error"]
 
 
 def lib_path() -> str:
@@ -97,6 +103,12 @@ def load(path: str | None = None):
         lib.carekv_prefill_attn.argtypes = [C.POINTER(PrefillParams), vp, vp, vp, vp, vp, vp]
         lib.carekv_dequantize_rows.restype = C.c_int
         lib.carekv_dequantize_rows.argtypes = [vp, vp, i32, i32, i32, vp, vp]
+        lib.carekv_prefill_correct_workspace_bytes.restype = i64
+        lib.carekv_prefill_correct_workspace_bytes.argtypes = [C.POINTER(Arena), C.POINTER(DecodeParams),
+                                                               C.POINTER(PrefillCorrParams)]
+        lib.carekv_prefill_correct.restype = C.c_int
+        lib.carekv_prefill_correct.argtypes = [C.POINTER(Arena), C.POINTER(DecodeParams),
+                                               C.POINTER(PrefillCorrParams), vp, vp, vp, i64, vp, i32, vp]
         lib.carekv_kivi_qdq.restype = C.c_int
         lib.carekv_kivi_qdq.argtypes = [vp, i32, i32, i32, i32, i32, vp, vp]
         _lib = lib

@@ -37,6 +37,83 @@ def default_split_pages(max_pages: int, rows: int) -> int:
     return (sp + 15) // 16 * 16
 
 
+def _read_params(cache: CAREKVCache, layer: int, knobs: ReadKnobs, *, batch: int, n_heads: int, correction: bool,
+                 split_pages: int, max_pages: int, seq_ptr: int = 0, np_ptr: int = 0):
+    """carekv_decode_params of the resolved read knobs (the sketch proxy's
+    projection is set by the caller)."""
+    cfg = cache.cfg
+    return _lib.DecodeParams(
+        batch=batch, n_heads=n_heads, seq_slot=seq_ptr, n_pages=np_ptr, max_pages_used=max_pages,
+        sm_scale=float(np.float32(1.0 / math.sqrt(cfg.head_dim))), sensitivity=float(cfg.layer_sensitivity[layer]),
+        correction=int(bool(correction)), kind=KIND_CODE[knobs.kind], joint=int(knobs.joint),
+        normalize=int(knobs.normalize), k_exact=int(knobs.k_exact), k_corr_scale=knobs.k_corr_scale,
+        lambda_k=knobs.lambda_k, lambda_v=knobs.lambda_v, budget_ratio=int(knobs.budget_ratio),
+        abs_k=knobs.abs_k, abs_v=knobs.abs_v, ratio_k=knobs.ratio_k, ratio_v=knobs.ratio_v,
+        k_cap=cache.k_cap, v_cap=cache.v_cap, split_pages=int(split_pages),
+        route_policy=int(knobs.route_policy), adaptive_score=int(bool(knobs.adaptive_score)),
+        rel_threshold=float(knobs.rel_threshold), abs_threshold=float(knobs.abs_threshold),
+        min_keep=int(knobs.min_keep))
+
+
+def prefill_correction(cache: CAREKVCache, layer: int, q: torch.Tensor, k_hat: torch.Tensor, v_hat: torch.Tensor,
+                       lse: torch.Tensor, seq: int = 0, *, knobs: Optional[ReadKnobs] = None,
+                       split_pages: Optional[int] = None, diag_cap: int = 0, rows_per_call: Optional[int] = None):
+    """The prefill-time correction of ``carekv_stored`` mode (layer.py:780-838)
+    with the vectorized correction over all kv_group x T queries
+    (layer.py:538-557), for the prompt that sequence ``seq`` of the cache
+    holds (written by ``write_prefill`` from token 0).
+
+    q (T, Hq, D) fp16 post-RoPE queries; k_hat / v_hat (Hkv, T, D) fp16 the
+    page writer's dequantised prompt (``quant_dequant`` for the uniform
+    base, the KIVI quant-dequant for the side-buffer bases); lse (Hq, T)
+    fp32 from ``prefill_attention(..., return_lse=True)`` over the same
+    K_hat / V_hat.  Returns the corrected attention output (T, Hq, D) fp16,
+    and with ``diag_cap > 0`` the selected candidates per (row, head)."""
+    cfg: CacheConfig = cache.cfg
+    if knobs is None:
+        knobs = resolve_read_knobs(cfg, layer)
+    if not knobs.kscore_live:
+        raise NotImplementedError("the prefill correction is built for the query-aware K score "
+                                  "(CAREKV_KSCORE_LIVE=1) only")
+    T, Hq, D = q.shape
+    Hkv = cfg.num_kv_heads
+    if (Hq, D) != (cfg.num_heads, cfg.head_dim) or k_hat.shape != (Hkv, T, D) or v_hat.shape != (Hkv, T, D) \
+            or lse.shape != (Hq, T):
+        raise ValueError("prefill_correction: q (T, Hq, D), k_hat / v_hat (Hkv, T, D), lse (Hq, T) expected")
+    dev = cache.device
+    q = q.to(torch.float16).contiguous()
+    k_hat = k_hat.to(torch.float16).contiguous()
+    v_hat = v_hat.to(torch.float16).contiguous()
+    lse = lse.to(torch.float32).contiguous()
+    pages = -(-T // cfg.page_size)
+    if cache.num_pages(layer, 0, seq) != pages:
+        raise ValueError(f"sequence {seq} holds {cache.num_pages(layer, 0, seq)} pages, the prompt needs {pages}: "
+                         "the cache must hold exactly the prompt")
+    if rows_per_call is None:  # bound the workspace: rows x pages x query heads
+        rows_per_call = max(1, min(T, (1 << 22) // max(1, pages * Hq)))
+    if split_pages is None:
+        split_pages = default_split_pages(pages, rows_per_call * Hkv)
+    lib = _lib.load()
+    a = cache.arena(layer)
+    out = torch.empty(T, Hq, D, dtype=torch.float16, device=dev)
+    diag = torch.empty(T, Hq, diag_cap, dtype=torch.int32, device=dev) if diag_cap > 0 else None
+    dp = _read_params(cache, layer, knobs, batch=0, n_heads=Hq, correction=True, split_pages=split_pages,
+                      max_pages=pages)
+    for r0 in range(0, T, rows_per_call):
+        n = min(rows_per_call, T - r0)
+        pp = _lib.PrefillCorrParams(seq=seq, n_tokens=T, row_begin=r0, n_rows=n, k_hat=k_hat.data_ptr(),
+                                    v_hat=v_hat.data_ptr(), lse=lse.data_ptr())
+        nbytes = int(lib.carekv_prefill_correct_workspace_bytes(a, dp, pp))
+        if nbytes < 0:
+            raise _lib.CarekvError(f"carekv_prefill_correct_workspace_bytes rejected the parameters: "
+                                   f"{lib.carekv_last_error().decode()}")
+        ws = cache.workspace("prefill_correct", nbytes)
+        _lib.check(lib.carekv_prefill_correct(a, dp, pp, q[r0].data_ptr(), out[r0].data_ptr(), ws.data_ptr(),
+                                              ws.numel(), None if diag is None else diag[r0].data_ptr(),
+                                              int(diag_cap), _lib.stream_ptr(dev)), "carekv_prefill_correct")
+    return (out, diag) if diag_cap > 0 else out
+
+
 def decode_attention(cache: CAREKVCache, layer: int, q: torch.Tensor, seqs: Optional[Sequence[int]] = None, *,
                      correction: bool = True, knobs: Optional[ReadKnobs] = None, split_pages: Optional[int] = None,
                      diag_cap: int = 0, out: Optional[torch.Tensor] = None, phase_events=None):
@@ -68,17 +145,8 @@ def decode_attention(cache: CAREKVCache, layer: int, q: torch.Tensor, seqs: Opti
         cache._row_tables[key] = meta
     if split_pages is None:
         split_pages = default_split_pages(max_np, B * cfg.num_kv_heads)
-    dp = _lib.DecodeParams(
-        batch=B, n_heads=Hq, seq_slot=meta[0].data_ptr(), n_pages=meta[1].data_ptr(), max_pages_used=max_np,
-        sm_scale=float(np.float32(1.0 / math.sqrt(D))), sensitivity=float(cfg.layer_sensitivity[layer]),
-        correction=int(bool(correction)), kind=KIND_CODE[knobs.kind], joint=int(knobs.joint),
-        normalize=int(knobs.normalize), k_exact=int(knobs.k_exact), k_corr_scale=knobs.k_corr_scale,
-        lambda_k=knobs.lambda_k, lambda_v=knobs.lambda_v, budget_ratio=int(knobs.budget_ratio),
-        abs_k=knobs.abs_k, abs_v=knobs.abs_v, ratio_k=knobs.ratio_k, ratio_v=knobs.ratio_v,
-        k_cap=cache.k_cap, v_cap=cache.v_cap, split_pages=int(split_pages),
-        route_policy=int(knobs.route_policy), adaptive_score=int(bool(knobs.adaptive_score)),
-        rel_threshold=float(knobs.rel_threshold), abs_threshold=float(knobs.abs_threshold),
-        min_keep=int(knobs.min_keep))
+    dp = _read_params(cache, layer, knobs, batch=B, n_heads=Hq, correction=correction, split_pages=split_pages,
+                      max_pages=max_np, seq_ptr=meta[0].data_ptr(), np_ptr=meta[1].data_ptr())
     if correction and not knobs.kscore_live:
         P = get_sketch_proj(cfg.head_dim, cfg.k_channel_group, cfg.sketch_dim, dev)
         dp.k_proxy = 1

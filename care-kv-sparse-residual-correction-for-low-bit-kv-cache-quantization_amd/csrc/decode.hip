@@ -1,5 +1,6 @@
 // C ABI of the decode path: workspace layout, argument checks, launches of
 // the streaming, select, apply and combine kernels on the caller's stream.
+#include "block_util.h"
 #include "decode_common.h"
 #include "host_util.h"
 
@@ -46,9 +47,33 @@ extern "C" int64_t carekv_decode_workspace_bytes(const carekv_arena* arena, cons
   return ws_layout(*arena, *dp).total;
 }
 
-extern "C" int carekv_decode_attn(const carekv_arena* arena, const carekv_decode_params* dp, const uint16_t* q,
-                                  uint16_t* out, void* workspace, int64_t workspace_bytes, int32_t* diag,
-                                  int32_t diag_cap, void* stream) {
+namespace {
+// Prefill rows of carekv_prefill_correct (null for a decode step).
+struct PfRows {
+  const carekv_prefill_corr_params* p;
+  int pages;
+};
+
+__global__ __launch_bounds__(256) void prompt_vsq_kernel(const uint16_t* __restrict__ v, int T, int D, int pages,
+                                                         float* __restrict__ vsq) {
+  // one wave per (page, kv head): sum of V_hat^2 over the page's prompt rows
+  const int p = blockIdx.x * 4 + (threadIdx.x >> 6), kvh = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  if (p >= pages) return;
+  const int r1 = min(T, (p + 1) * kPage);
+  float acc = 0.f;
+  for (int r = p * kPage; r < r1; ++r)
+    for (int d = lane; d < D; d += 64) {
+      const float x = h2f(v[((long)kvh * T + r) * D + d]);
+      acc = fmaf(x, x, acc);
+    }
+  acc = wave_sum_f(acc);
+  if (lane == 0) vsq[(long)kvh * pages + p] = acc;
+}
+
+int run_decode(const carekv_arena* arena, const carekv_decode_params* dp, const PfRows* pf, const uint16_t* q,
+               uint16_t* out, void* workspace, int64_t workspace_bytes, int32_t* diag, int32_t diag_cap,
+               void* stream) {
   CAREKV_REQUIRE(arena && dp && q && out && workspace, "null argument");
   const carekv_arena& A = *arena;
   CAREKV_REQUIRE(check_arena(A), last_error_buf());
@@ -57,7 +82,7 @@ extern "C" int carekv_decode_attn(const carekv_arena* arena, const carekv_decode
   CAREKV_REQUIRE(dp->n_heads % A.n_kv_heads == 0, "n_heads must be a multiple of n_kv_heads");
   const int GQ = dp->n_heads / A.n_kv_heads;
   CAREKV_REQUIRE(GQ >= 1 && GQ <= 16, "query heads per kv head must be in 1..16");
-  CAREKV_REQUIRE(dp->seq_slot && dp->n_pages, "seq_slot and n_pages are required");
+  CAREKV_REQUIRE(pf || (dp->seq_slot && dp->n_pages), "seq_slot and n_pages are required");
   CAREKV_REQUIRE(dp->max_pages_used >= 0 && dp->max_pages_used <= A.max_pages, "max_pages_used out of range");
   CAREKV_REQUIRE(dp->split_pages > 0 && dp->split_pages % 4 == 0 && dp->split_pages <= 1024,
                  "split_pages must be a multiple of 4 in 4..1024");
@@ -74,9 +99,10 @@ extern "C" int carekv_decode_attn(const carekv_arena* arena, const carekv_decode
   CAREKV_REQUIRE(!proxy || (A.k_sketch && A.k_channel_group == 32 && A.sketch_dim >= 1 && A.sketch_dim <= 64),
                  "the sketch proxy needs k_sketch, k_channel_group 32 and sketch_dim in 1..64");
   const WsLayout L = ws_layout(A, *dp);
-  if (workspace_bytes < L.total) {
-    set_error("carekv_decode_attn: workspace too small (%lld < %lld)", (long long)workspace_bytes,
-              (long long)L.total);
+  const long vsq_off = L.total, need = L.total + (pf ? (long)A.n_kv_heads * pf->pages * 4 : 0);
+  if (workspace_bytes < need) {
+    set_error("%s: workspace too small (%lld < %lld)", pf ? "carekv_prefill_correct" : "carekv_decode_attn",
+              (long long)workspace_bytes, (long long)need);
     return CAREKV_ESPACE;
   }
   CAREKV_REQUIRE(L.prox - L.rec < (1L << 32) - 256,
@@ -130,6 +156,16 @@ extern "C" int carekv_decode_attn(const carekv_arena* arena, const carekv_decode
     a.napply = (a.nsplit + m - 1) / m;
   }
   hipStream_t s = (hipStream_t)stream;
+  if (pf) {
+    const carekv_prefill_corr_params& P = *pf->p;
+    a.pf = 1;
+    a.pf_seq = P.seq; a.pf_row0 = P.row_begin; a.pf_pages = pf->pages; a.pf_T = P.n_tokens;
+    a.pf_k = P.k_hat; a.pf_v = P.v_hat; a.pf_lse = P.lse;
+    a.pf_vsq = (float*)(ws + vsq_off);
+    hipLaunchKernelGGL(prompt_vsq_kernel, dim3((unsigned)((pf->pages + 3) / 4), A.n_kv_heads), dim3(256), 0, s,
+                       P.v_hat, P.n_tokens, A.head_dim, pf->pages, a.pf_vsq);
+    CAREKV_CHECK_LAUNCH("prompt_vsq");
+  }
   hipEvent_t* ev = (hipEvent_t*)dp->phase_events;
   auto mark = [&](int i) -> int {
     if (ev && hipEventRecord(ev[i], s) != hipSuccess) {
@@ -149,4 +185,59 @@ extern "C" int carekv_decode_attn(const carekv_arena* arena, const carekv_decode
   if (rc == CAREKV_OK && a.correction) rc = launch_decode_combine(A, a, s);
   if (rc == CAREKV_OK) rc = mark(4);
   return rc;
+}
+}  // namespace
+
+extern "C" int carekv_decode_attn(const carekv_arena* arena, const carekv_decode_params* dp, const uint16_t* q,
+                                  uint16_t* out, void* workspace, int64_t workspace_bytes, int32_t* diag,
+                                  int32_t diag_cap, void* stream) {
+  return run_decode(arena, dp, nullptr, q, out, workspace, workspace_bytes, diag, diag_cap, stream);
+}
+
+namespace {
+// The decode parameters of a prefill-rows call and its page count, or an
+// error message.
+int prefill_setup(const carekv_arena* arena, const carekv_decode_params* read,
+                  const carekv_prefill_corr_params* pp, carekv_decode_params& dp, PfRows& pf) {
+  CAREKV_REQUIRE(arena && read && pp, "null argument");
+  const carekv_arena& A = *arena;
+  CAREKV_REQUIRE(pp->seq >= 0 && pp->seq < A.n_seq, "seq out of range");
+  CAREKV_REQUIRE(pp->n_tokens >= 1, "n_tokens must be positive");
+  const int pages = (pp->n_tokens + kPage - 1) / kPage;
+  CAREKV_REQUIRE(pages <= A.max_pages, "the prompt needs more pages than the arena holds");
+  CAREKV_REQUIRE(pp->row_begin >= 0 && pp->n_rows >= 1 && pp->row_begin + pp->n_rows <= pp->n_tokens,
+                 "rows must lie in [0, n_tokens)");
+  CAREKV_REQUIRE(pp->k_hat && pp->v_hat && pp->lse, "k_hat, v_hat and lse are required");
+  CAREKV_REQUIRE((long)pp->n_tokens * A.head_dim * 2 < (1L << 32), "prompt rows exceed 4 GiB per kv head");
+  CAREKV_REQUIRE(read->correction != 0, "prefill rows run the correction (correction must be 1)");
+  CAREKV_REQUIRE(read->k_proxy == 0, "prefill rows support the query-aware K score only (k_proxy must be 0)");
+  dp = *read;
+  dp.batch = pp->n_rows;
+  dp.max_pages_used = pages;
+  dp.seq_slot = nullptr;
+  dp.n_pages = nullptr;
+  pf.p = pp;
+  pf.pages = pages;
+  return CAREKV_OK;
+}
+}  // namespace
+
+extern "C" int64_t carekv_prefill_correct_workspace_bytes(const carekv_arena* arena,
+                                                          const carekv_decode_params* read,
+                                                          const carekv_prefill_corr_params* pp) {
+  carekv_decode_params dp{};
+  PfRows pf{};
+  if (prefill_setup(arena, read, pp, dp, pf) != CAREKV_OK || dp.split_pages <= 0) return -1;
+  return ws_layout(*arena, dp).total + (int64_t)arena->n_kv_heads * pf.pages * 4;
+}
+
+extern "C" int carekv_prefill_correct(const carekv_arena* arena, const carekv_decode_params* read,
+                                      const carekv_prefill_corr_params* pp, const uint16_t* q, uint16_t* out,
+                                      void* workspace, int64_t workspace_bytes, int32_t* diag, int32_t diag_cap,
+                                      void* stream) {
+  carekv_decode_params dp{};
+  PfRows pf{};
+  const int rc = prefill_setup(arena, read, pp, dp, pf);
+  if (rc != CAREKV_OK) return rc;
+  return run_decode(arena, &dp, &pf, q, out, workspace, workspace_bytes, diag, diag_cap, stream);
 }

@@ -77,14 +77,23 @@ void decode_apply_kernel(carekv_arena A, DecodeArgs a) {
   const int chunk = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int GQ = a.GQ;
   const int bk = b * A.n_kv_heads + kvh;
-  const int seq_raw = a.seq_slot[b], np_raw = a.n_pages[b];
-  const bool row_ok = seq_raw >= 0 && seq_raw < A.n_seq && np_raw >= 0 && np_raw <= a.Pmax;
-  const int seq = row_ok ? seq_raw : 0, np = row_ok ? np_raw : 0;
+  const EntryRow er = entry_row(A, a, b);
+  const int seq = er.seq, np = er.np;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int ln = lane & 15, lj = lane >> 4;
   const long pg_base = ((long)kvh * A.n_seq + seq) * A.max_pages;
-  const RowRes rr = row_resources<D, BITS, SM>(A, pg_base);
+  RowRes rr;
+  if (BITS == 16 && a.pf) {  // prefill rows: the prompt's dense fp16 K_hat / V_hat
+    const long off = (long)kvh * a.pf_T * D;  // rows past the prompt read as 0
+    const uint32_t bytes = (uint32_t)a.pf_T * D * 2;
+    rr.kc = make_rsrc(a.pf_k + off, bytes);
+    rr.vc = make_rsrc(a.pf_v + off, bytes);
+    rr.ks = make_rsrc(nullptr, 0u);
+    rr.vs = make_rsrc(nullptr, 0u);
+  } else {
+    rr = row_resources<D, BITS, SM>(A, pg_base);
+  }
   const uint8_t* maskb = a.mask + (long)bk * GQ * a.Pmax;
   const bool exact = a.k_exact != 0;
   const bool qv = ln < GQ;
@@ -322,7 +331,17 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(int Hkv, int D, Dec
     }
     const float ob = L > 0.f ? O / L : 0.f;
     float o = ob;
-    if (L > 0.f) o = a.k_exact ? (ob + nm / L) / (1.f + dn / L) : ob + (nm - dn * ob) / L;
+    if (L > 0.f) {
+      if (a.k_exact) {
+        o = (ob + nm / L) / (1.f + dn / L);
+      } else if (a.pf) {
+        // prefill rows: the reference adds the linear terms to its
+        // unnormalised fp16-weight O_base (layer.py:553-557)
+        o = O + (nm - dn * O);
+      } else {
+        o = ob + (nm - dn * ob) / L;
+      }
+    }
     a.out[((long)b * a.Hq + kvh * GQ + qq) * D + d] = f2h(o);
   }
 }
@@ -332,9 +351,12 @@ int launch_decode_apply(const carekv_arena& A, const DecodeArgs& a, hipStream_t 
     set_error("apply chunks must be at most 1024 pages");
     return CAREKV_EINVAL;
   }
-  if (A.base_bits != 16 && a.GQ <= 4) return launch_decode_apply4(A, a, s);  // windows of 4 pages, 4x4x4 layout
+  if (!a.pf && A.base_bits != 16 && a.GQ <= 4)
+    return launch_decode_apply4(A, a, s);  // windows of 4 pages, 4x4x4 layout
   const dim3 grid(a.napply, A.n_kv_heads, a.B);
-  return dispatch_dbs16(A.head_dim, A.base_bits, A.scale_mode, [&](auto d, auto bb, auto sm) {
+  // prefill rows read the prompt's fp16 K_hat / V_hat whatever the cache base
+  const int bits = a.pf ? 16 : A.base_bits, smode = a.pf ? 0 : A.scale_mode;
+  return dispatch_dbs16(A.head_dim, bits, smode, [&](auto d, auto bb, auto sm) {
     hipLaunchKernelGGL((decode_apply_kernel<decltype(d)::value, decltype(bb)::value, decltype(sm)::value>), grid,
                        dim3(256), 0, s, A, a);
     CAREKV_CHECK_LAUNCH("decode_apply");

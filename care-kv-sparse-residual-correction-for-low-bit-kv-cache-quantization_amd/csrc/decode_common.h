@@ -38,7 +38,42 @@ struct DecodeArgs {
   // byte span of the workspace from rec to the end of xbuf (< 4 GiB), and
   // the offsets of ebuf and xbuf from rec: one buffer resource covers them
   uint32_t ws_span, ws_e_off, ws_x_off;
+  // Prefill rows (carekv_prefill_correct): batch entry b is row pf_row0 + b
+  // of the prompt held by sequence pf_seq; it sees the prompt's first
+  // pf_row0 + b + 1 tokens.  The streaming and apply passes read the
+  // prompt's dense fp16 K_hat / V_hat (pf_k / pf_v, [Hkv][pf_T][D])
+  // instead of the cache codes; the weights are half(2^(x - lse2)) with the
+  // row's base-2 log-sum-exp (pf_lse, natural log, [Hq][pf_T]) as the
+  // reference's fp16 attention weights; every candidate of the prompt's
+  // pf_pages pages counts towards the normalisation and the budgets.
+  int pf;
+  int pf_seq, pf_row0, pf_pages, pf_T;
+  const uint16_t* pf_k;
+  const uint16_t* pf_v;
+  const float* pf_lse;
+  float* pf_vsq;  // [Hkv][pf_pages] sum of V_hat^2 over each page's prompt rows
 };
+
+// The cache row and visible extent of batch entry b.
+struct EntryRow {
+  int seq, np, ntok;
+};
+__device__ __forceinline__ EntryRow entry_row(const carekv_arena& A, const DecodeArgs& a, int b) {
+  EntryRow e;
+  if (a.pf) {
+    const int row = a.pf_row0 + b;
+    e.seq = a.pf_seq;
+    e.ntok = row + 1;
+    e.np = row / kPage + 1;
+  } else {
+    const int s = a.seq_slot[b], n = a.n_pages[b];
+    const bool ok = s >= 0 && s < A.n_seq && n >= 0 && n <= a.Pmax;
+    e.seq = ok ? s : 0;
+    e.np = ok ? n : 0;
+    e.ntok = 0x7fffffff;
+  }
+  return e;
+}
 
 // Page record per (sequence, kv head, query, page), F floats:
 //   [0]                      m_ref: running max of the base-2 logits

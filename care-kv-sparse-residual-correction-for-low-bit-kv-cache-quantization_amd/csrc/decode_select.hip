@@ -202,10 +202,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
   if (pair >= a.B * A.n_kv_heads) return;
   const int kvh = pair % A.n_kv_heads, b = pair / A.n_kv_heads;
   const int bk = b * A.n_kv_heads + kvh;
-  const int seq_raw = a.seq_slot[b], np_raw = a.n_pages[b];
-  const bool row_ok = seq_raw >= 0 && seq_raw < A.n_seq && np_raw >= 0 && np_raw <= a.Pmax;
-  const int np = row_ok ? np_raw : 0;
-  const int seq = row_ok ? seq_raw : 0;
+  const EntryRow er = entry_row(A, a, b);
+  const int np = er.np, seq = er.seq;
   const long pg_base = ((long)kvh * A.n_seq + seq) * A.max_pages;
   const int tid = threadIdx.x;
   const long bq = (long)bk * GQ + qq;
@@ -263,7 +261,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
   float* sc = a.ncand <= kLdsCand ? s_cand : a.scores + bq * a.ncand;
   int* key = reinterpret_cast<int*>(sc);
   uint8_t* maskq = a.mask + bq * a.Pmax;
-  const float invL = L > 0.f ? 1.f / L : 0.f;
+  // prefill rows: e_t are already the reference's attention weights
+  const float invL = L > 0.f ? (a.pf ? 1.f : 1.f / L) : 0.f;
+  const float* vsq_row = a.pf ? a.pf_vsq + (long)kvh * a.pf_pages : nullptr;
   float sumK = 0.f, sumV = 0.f;
   int cntK = 0, cntV = 0;
   if constexpr (PX) {  // K scores of the sketch proxy, one page per thread
@@ -299,7 +299,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
       const long pg = pg_base + p;
       const int nv = A.valid[pg];
       const int hm = A.has_meta[pg];
-      const float vsq = A.v_sq[pg];
+      const float vsq = vsq_row ? vsq_row[p] : A.v_sq[pg];
       int ksl[NCG], vsl[kVtb];
       load_slots<NCG>(ksl, A.k_slot + pg * NCG);
       load_slots<kVtb>(vsl, A.v_slot + pg * kVtb);
@@ -343,7 +343,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
     const long pg = pg_base + p;
     const int nv = A.valid[pg];
     const int hm = A.has_meta[pg];
-    const float vsq = A.v_sq[pg];
+    const float vsq = vsq_row ? vsq_row[p] : A.v_sq[pg];
     int ksl[NCG], vsl[kVtb];
     load_slots<NCG>(ksl, A.k_slot + pg * NCG);
     load_slots<kVtb>(vsl, A.v_slot + pg * kVtb);
@@ -397,6 +397,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
       ++rv;
     }
     for (; rv < v_cap; ++rv) sc[nK + p * v_cap + rv] = -1.f;
+  }
+  if (a.pf) {
+    // prefill rows: the candidates of the prompt's later pages score 0
+    // (A = 0 past the row) but count, as in the reference's candidate set
+    // over all pages of the kv head (layer.py:514-517)
+    for (int p = np + tid; p < a.pf_pages; p += kBlock) {
+      const long pg = pg_base + p;
+      const int nv = A.valid[pg];
+      if (nv <= 0 || !A.has_meta[pg]) continue;
+      int rk = 0, rv = 0;  // the stored slots by rank, as the scoring loops count them
+      for (int cg = 0; cg < NCG; ++cg) rk += slot_ok(A, A.k_slot[pg * NCG + cg]) ? 1 : 0;
+      cntK += min(rk, k_cap);
+      for (int vb = 0; vb < kVtb; ++vb) {
+        if (!slot_ok(A, A.v_slot[pg * kVtb + vb])) continue;
+        if (rv >= v_cap) break;
+        if (vb * kVtb < nv) ++cntV;
+        ++rv;
+      }
+    }
   }
   float tK = sumK, tV = sumV;
   int n_k = cntK, n_v = cntV;
@@ -470,7 +489,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
         const int nvp = A.valid[pg_base + (i >> 4)];
         if ((i & 15) >= nvp) continue;
         ++nt;
-        const float at = L > 0.f ? __builtin_amdgcn_exp2f(xq[i] - M) / L : 0.f;
+        float at = L > 0.f ? __builtin_amdgcn_exp2f(xq[i] - M) : 0.f;
+        at = a.pf ? (float)(_Float16)at : at / L;
         const float ac = fmaxf(at, kEps);
         h += ac * logf(ac);
       }

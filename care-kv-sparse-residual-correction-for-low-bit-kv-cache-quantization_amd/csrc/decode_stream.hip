@@ -17,12 +17,18 @@
 //     global softmax statistics are known (select kernel).
 // The next page's codes, scales and metadata are loaded while the current
 // page is processed.
+//
+// PF (prefill rows, BITS = 16): the entry's rows come from the prompt's
+// dense fp16 K_hat / V_hat; tokens past the entry's row are masked; the
+// reference max is the row's log-sum-exp, fixed for every page, so that
+// e_t = half(2^(x_t - lse2)) is the reference's fp16 attention weight
+// (layer.py:964) and the moments and masses are taken over it.
 #include "decode_page.h"
 #include "host_util.h"
 
 namespace carekv {
 
-template <int D, int BITS, int SM>
+template <int D, int BITS, int SM, bool PF = false>
 // 4 waves per SIMD (2 for the fp16 base, whose rows take twice the
 // registers): the register budget is capped at 128 (256) VGPRs.
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(BITS == 16 ? 2 : 4, 8)))
@@ -41,14 +47,24 @@ void decode_stream_kernel(carekv_arena A, DecodeArgs a) {
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int GQ = a.GQ;
   const int bk = b * A.n_kv_heads + kvh;
-  const int seq_raw = a.seq_slot[b], np_raw = a.n_pages[b];
-  const bool row_ok = seq_raw >= 0 && seq_raw < A.n_seq && np_raw >= 0 && np_raw <= a.Pmax;
-  const int seq = row_ok ? seq_raw : 0, np = row_ok ? np_raw : 0;
+  const EntryRow er = entry_row(A, a, b);
+  const int seq = er.seq, np = er.np;
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int ln = lane & 15, lj = lane >> 4;
   const long pg_base = ((long)kvh * A.n_seq + seq) * A.max_pages;
-  const RowRes rr = row_resources<D, BITS, SM>(A, pg_base);
+  RowRes rr;
+  if constexpr (PF) {
+    static_assert(BITS == 16, "prefill rows are fp16");
+    const long off = (long)kvh * a.pf_T * D;  // rows past the prompt read as 0
+    const uint32_t bytes = (uint32_t)a.pf_T * D * 2;
+    rr.kc = make_rsrc(a.pf_k + off, bytes);
+    rr.vc = make_rsrc(a.pf_v + off, bytes);
+    rr.ks = make_rsrc(nullptr, 0u);
+    rr.vs = make_rsrc(nullptr, 0u);
+  } else {
+    rr = row_resources<D, BITS, SM>(A, pg_base);
+  }
   const bool corr = a.correction != 0;
   const float sm_log2 = a.sm_log2;
   const long rq = (long)a.Pmax * a.F;  // record stride between query heads
@@ -60,6 +76,8 @@ void decode_stream_kernel(carekv_arena A, DecodeArgs a) {
 
   uint32_t* vt = reinterpret_cast<uint32_t*>(smem) + w * VT_WORDS;
   float m_run = -INFINITY, l_run = 0.f;
+  if constexpr (PF)  // lane column ln is query ln (columns >= GQ hold zero queries)
+    m_run = ln < GQ ? a.pf_lse[(long)(kvh * GQ + ln) * a.pf_T + a.pf_row0 + b] * 1.4426950408889634f : 0.f;
   float4_t oacc[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) oacc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -81,7 +99,7 @@ void decode_stream_kernel(carekv_arena A, DecodeArgs a) {
       nmv = meta_lanes_load<NCG>(A, pg_base + p + 4, lane);
     }
     const float ckm = h2f((uint16_t)cm.kmaster), cvm = h2f((uint16_t)cm.vmaster);
-    const int nv = cm.nv;
+    const int nv = PF ? min(cm.nv, er.ntok - p * kPage) : cm.nv;
     if (nv <= 0) continue;
     // K residual rows of the stored slots, issued before the page math
     uint32_t krow[NCG];
@@ -117,13 +135,22 @@ void decode_stream_kernel(carekv_arena A, DecodeArgs a) {
     if (a.xbuf && corr && ln < GQ)  // logits for the proxy's margins / the entropy
       *reinterpret_cast<float4*>(a.xbuf + (((long)bk * GQ + ln) * a.Pmax + p) * 16 + 4 * lj) =
           make_float4(x[0], x[1], x[2], x[3]);
-    const float mx = col_max(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));
-    const float m_new = fmaxf(m_run, mx);  // finite: token 0 of a page is always valid
-    const float f_old = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first page
-    m_run = m_new;
+    float m_new, f_old;
+    if constexpr (PF) {
+      m_new = m_run;
+      f_old = 1.f;
+    } else {
+      const float mx = col_max(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));
+      m_new = fmaxf(m_run, mx);  // finite: token 0 of a page is always valid
+      f_old = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first page
+      m_run = m_new;
+    }
     float e[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) e[i] = __builtin_amdgcn_exp2f(x[i] - m_new);
+    for (int i = 0; i < 4; ++i) {
+      e[i] = __builtin_amdgcn_exp2f(x[i] - m_new);
+      if constexpr (PF) e[i] = (float)(_Float16)e[i];
+    }
     l_run = l_run * f_old + col_sum((e[0] + e[1]) + (e[2] + e[3]));
     if (__builtin_expect(__any(f_old != 1.f), 0)) {
       // rows of oacc are queries 4j+i: their factors live in lanes 4j+i
@@ -200,9 +227,17 @@ void decode_stream_kernel(carekv_arena A, DecodeArgs a) {
 }
 
 int launch_decode_stream(const carekv_arena& A, const DecodeArgs& a, hipStream_t s) {
+  dim3 grid(a.nsplit, A.n_kv_heads, a.B);
+  if (a.pf) {
+    auto go = [&](auto kern) {
+      hipLaunchKernelGGL(kern, grid, dim3(256), 0, s, A, a);
+      CAREKV_CHECK_LAUNCH("decode_stream (prefill rows)");
+      return CAREKV_OK;
+    };
+    return A.head_dim == 64 ? go(decode_stream_kernel<64, 16, 0, true>) : go(decode_stream_kernel<128, 16, 0, true>);
+  }
   if (A.base_bits != 16 && a.GQ <= 4 && a.SP % 16 == 0)
     return launch_decode_stream4(A, a, s);  // 4-page windows, 4x4x4 MFMA
-  dim3 grid(a.nsplit, A.n_kv_heads, a.B);
   return dispatch_dbs16(A.head_dim, A.base_bits, A.scale_mode, [&](auto d, auto bb, auto sm) {
     hipLaunchKernelGGL((decode_stream_kernel<decltype(d)::value, decltype(bb)::value, decltype(sm)::value>), grid,
                        dim3(256), 0, s, A, a);

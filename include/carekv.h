@@ -230,6 +230,44 @@ typedef struct carekv_prefill_params {
 int carekv_prefill_attn(const carekv_prefill_params* params, const uint16_t* q, const uint16_t* k,
                         const uint16_t* v, uint16_t* out, float* lse, void* stream);
 
+/* Prefill-time sparse correction of CAREKVLayer.prefill in carekv_stored
+ * mode (layer.py:780-838) with the vectorized correction over all
+ * kv_group x T queries of each kv head (layer.py:538-557): for every prompt
+ * row t in [row_begin, row_begin + n_rows) and query head h,
+ *   out[t - row_begin][h] = half(O_base + vectorized_joint_correction(...))
+ * with the base attention of _causal_attention_pure (fp32 scores, softmax
+ * weights cast to fp16, layer.py:952-965) over the prompt's first t + 1
+ * tokens, scored against the stored slots of every page of the prompt (the
+ * candidates of pages after row t score 0 but count towards the
+ * normalisation and the budgets, as in the reference).
+ * The arena's sequence `seq` must hold exactly the prompt's pages
+ * (carekv_store_pages over tokens 0..n_tokens-1).  k_hat / v_hat are the
+ * page writer's dequantised prompt (layer.py:331-334: half(code * fp16 group
+ * scale), before the int8 requantisation of the page scales; the KIVI
+ * quant-dequant for the side-buffer bases), fp16 [n_kv_heads][n_tokens]
+ * [head_dim]; lse is carekv_prefill_attn's natural log-sum-exp of the same
+ * rows, fp32 [n_heads][n_tokens]. */
+typedef struct carekv_prefill_corr_params {
+  int32_t seq;        /* arena sequence slot holding the prompt              */
+  int32_t n_tokens;   /* prompt length T                                     */
+  int32_t row_begin;  /* first prompt row to correct                         */
+  int32_t n_rows;     /* rows to correct                                     */
+  const uint16_t* k_hat;
+  const uint16_t* v_hat;
+  const float* lse;
+} carekv_prefill_corr_params;
+
+/* read: the read knobs, as for a decode step; its batch, seq_slot, n_pages
+ * and max_pages_used are ignored, correction must be 1 and k_proxy 0.
+ * q, out: fp16 [n_rows][n_heads][head_dim] (the prompt rows' post-RoPE
+ * queries, row-major over the rows).  diag as carekv_decode_attn, per row. */
+int carekv_prefill_correct(const carekv_arena* arena, const carekv_decode_params* read,
+                           const carekv_prefill_corr_params* rows, const uint16_t* q, uint16_t* out,
+                           void* workspace, int64_t workspace_bytes, int32_t* diag, int32_t diag_cap,
+                           void* stream);
+int64_t carekv_prefill_correct_workspace_bytes(const carekv_arena* arena, const carekv_decode_params* read,
+                                               const carekv_prefill_corr_params* rows);
+
 /* dequantize (quantizer.py:67-82): out fp16 [rows][D] = half(code * scale)
  * from unpacked int8 codes [rows][D] and fp16 group scales [rows][D/group]
  * as carekv_quantize_rows (pack = 0) writes them; group must be 32. */

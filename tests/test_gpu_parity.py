@@ -13,10 +13,12 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import (DECODE_CASES, PAPER_ENV, build_oracle_case, case_cfg_kwargs, decode_diag, load_golden,
-                     oracle_candidates, oracle_selection, ties_explain)
+from helpers import (DECODE_CASES, PAPER_ENV, PREFILL_CASES, build_oracle_case, build_oracle_prefill,
+                     case_cfg_kwargs, decode_diag, load_golden, oracle_candidates, oracle_selection,
+                     prefill_cfg_kwargs, ties_explain)
 from oracle import quant as Q
 from oracle.attention import decode_attention as oracle_decode
+from oracle.attention import prefill_stored
 from oracle.cache import OCache, OCfg
 from oracle.store import decode_append, write_pages_for_kv_head
 
@@ -247,6 +249,74 @@ def test_read_zero_is_base_bit_exact(paper_env):
     cache.cfg.read_abs_k = cache.cfg.read_abs_v = 0
     corr0 = care_kv.decode_attention(cache, 0, q, correction=True)
     assert torch.equal(base, corr0)
+
+
+# ------------------------------------------------------------------ prefill carekv_stored
+@pytest.mark.parametrize("name", list(PREFILL_CASES))
+def test_prefill_correction_matches_reference(paper_env, name):
+    """carekv_prefill_correct vs the reference's CAREKVLayer.prefill in
+    carekv_stored mode (vectorized correction): the corrected output within
+    the decode bar, and each (row, head)'s selection equal to the oracle's
+    over the positive-score candidates up to epsilon ties (1e-3 relative:
+    the fp16 attention weights are roundings of softmax values, and a weight
+    whose fp32 value straddles a rounding point moves one fp16 ulp)."""
+    import care_kv
+    g = load_golden(f"prefill_{name}.npz")
+    spec = PREFILL_CASES[name]
+    paper_env.setenv("CAREKV_K_CORRECTION_MODE", spec["k_mode"])
+    print(f"prefill correction case {name}", flush=True)
+    cfg = care_kv.CacheConfig(packed_base=True, scale_quant="int8", read_budget_ratio=0.0,
+                              **prefill_cfg_kwargs(g, spec))
+    cache = care_kv.CAREKVCache(cfg, device="cuda")
+    T, Hq, Hkv = int(g["T"]), spec["Hq"], spec["Hkv"]
+    grp = Hq // Hkv
+    K = torch.from_numpy(g["K"]).cuda()
+    V = torch.from_numpy(g["V"]).cuda()
+    cache.write_prefill(0, K, V)
+    torch.cuda.synchronize()
+    compare_cache_to_golden(cache, g)
+    Kh, Vh = care_kv.quant_dequant(K, 3, 32), care_kv.quant_dequant(V, 3, 32)
+    Q = torch.from_numpy(g["Q"]).cuda()  # (T, Hq, D)
+    Ob, lse = care_kv.prefill_attention(Q.transpose(0, 1), Kh, Vh, return_lse=True)
+    base = Ob.transpose(0, 1).cpu().numpy().astype(F32)
+    assert np.abs(base - g["O_base"].astype(F32)).max() <= 2e-3
+    out, diag = care_kv.prefill_correction(cache, 0, Q, Kh, Vh, lse, diag_cap=256, rows_per_call=64)
+    torch.cuda.synchronize()
+    out = out.cpu().numpy().astype(F32)
+    ref = g["O"].astype(F32)
+    err = np.abs(out - ref)
+    ulp = np.spacing(np.abs(g["O"])).astype(F32)
+    assert np.all(err <= np.maximum(2e-3, ulp)), (err.max(), np.unravel_index(err.argmax(), err.shape))
+    # selections against the oracle (the candidates of later pages score 0
+    # and are left out on both sides)
+    oc, _, okh, ovh = build_oracle_prefill(g, name)
+    odiag = {}
+    prefill_stored(oc, 0, g["Q"].transpose(1, 0, 2), okh, ovh, k_mode=spec["k_mode"], kind="both",
+                   k_corr_scale=0.1, score_normalize=True, kscore_live=True, diag=odiag)
+    diag = diag.cpu().numpy()
+    n_tie = 0
+    for h in range(Hkv):
+        d = odiag[h]
+        Kc, Vc = oracle_candidates(oc, 0, h, oc.next_page[0][h])
+        ref_rows = oracle_selection(d, Kc, Vc)
+        sK, sV = d["score_K_r"], d["score_V_r"]
+        for gi in range(grp):
+            for t in range(T):
+                j = gi * T + t
+                vals = {c: float(sK[j, i]) for i, c in enumerate(Kc)}
+                vals.update({c: float(sV[j, i]) for i, c in enumerate(Vc)})
+                mine = {c for c in decode_diag(diag[t, h * grp + gi]) if vals.get(c, 0.0) > 0}
+                refs = {c for c in ref_rows[j] if vals[c] > 0}
+                if mine != refs:
+                    n_tie += 1
+                    if spec["policy"] == "joint":
+                        assert ties_explain(mine, refs, d, Kc, Vc, j, eps=1e-3), (h, gi, t, sorted(mine ^ refs))
+                    else:
+                        for kind in (0, 1):
+                            a = {c for c in mine if c[0] == kind}
+                            b = {c for c in refs if c[0] == kind}
+                            assert ties_explain(a, b, d, Kc, Vc, j, eps=1e-3), (h, gi, t, kind)
+    assert n_tie <= max(2, T * Hq // 100), n_tie
 
 
 # ------------------------------------------------------------------ random shapes vs oracle
