@@ -10,7 +10,9 @@ the HIP library:
   (``carekv_append_rows``);
 * prefill attention is ``prefill_attention`` over (K_post, V) in the ``fp``
   mode or over the fp16-scale K_hat / V_hat in the quantised modes
-  (``carekv_prefill_attn``, layer.py:759-781);
+  (``carekv_prefill_attn``, layer.py:759-781), plus the stored-slot sparse
+  correction in ``carekv_stored`` mode (``prefill_correction``,
+  ``carekv_prefill_correct``, layer.py:808-838);
 * decode attention with the comb+ex correction is ``decode_attention``
   (``carekv_decode_attn``, layer.py:1148-1160).
 """
@@ -23,9 +25,9 @@ from typing import Any, Dict, Optional, Sequence, Tuple
 import torch
 from torch import Tensor, nn
 
-from .attention import decode_attention
+from .attention import decode_attention, prefill_correction
 from .cache import CAREKVCache
-from .config import CacheConfig
+from .config import CacheConfig, any_read_budget
 from .prefill import prefill_attention, quant_dequant
 
 try:  # the reference takes RoPE from transformers as well (layer.py:65-69)
@@ -117,9 +119,10 @@ class CAREKVLayer(nn.Module):
 
         Every mode writes the pages (post-RoPE K, layer.py:719-737).  The
         output is attention over (K_post, V) in ``fp`` mode and over the
-        dequantised K_hat / V_hat otherwise.  The prefill-time sparse
-        correction of ``carekv_eval`` / ``carekv_stored`` is not built: those
-        modes return the base attention and warn once."""
+        dequantised K_hat / V_hat otherwise; ``carekv_stored`` adds the
+        sparse correction from the stored slots (``prefill_correction``,
+        layer.py:808-838).  The in-memory correction of ``carekv_eval`` is
+        not built: that mode returns the base attention and warns once."""
         squeeze = hidden.dim() == 2
         if squeeze:
             hidden = hidden.unsqueeze(0)
@@ -138,17 +141,25 @@ class CAREKVLayer(nn.Module):
         if mode == "fp":
             O = prefill_attention(Qh, Kh, Vh)
         else:
-            if mode in ("carekv_eval", "carekv_stored") and mode not in _warned:
+            if mode == "carekv_eval" and mode not in _warned:
                 _warned.add(mode)
-                warnings.warn(f"CAREKV_PREFILL_MODE={mode}: the prefill-time sparse correction is not built; "
-                              "the prefill output is the base attention over K_hat / V_hat (decode-time "
-                              "correction is unaffected)", RuntimeWarning, stacklevel=2)
+                warnings.warn("CAREKV_PREFILL_MODE=carekv_eval: the in-memory prefill correction is not built; "
+                              "the prefill output is the base attention over K_hat / V_hat (carekv_stored and "
+                              "the decode-time correction are built)", RuntimeWarning, stacklevel=2)
             if hats is not None:  # side-buffer base: the K_hat / V_hat the pages hold (layer.py:328-332)
                 Khat, Vhat = (hats[0].unsqueeze(0), hats[1].unsqueeze(0)) if hats[0].dim() == 3 else hats
-                O = prefill_attention(Qh, Khat, Vhat)
             else:
-                O = prefill_attention(Qh, quant_dequant(Kh, cfg.base_bits, cfg.group_size),
-                                      quant_dequant(Vh, cfg.base_bits, cfg.group_size))
+                Khat = quant_dequant(Kh, cfg.base_bits, cfg.group_size)
+                Vhat = quant_dequant(Vh, cfg.base_bits, cfg.group_size)
+            stored = mode == "carekv_stored" and any_read_budget(cfg)
+            if stored and token_start_abs != 0:
+                raise NotImplementedError("carekv_stored prefill correction of a prompt continuation "
+                                          "(token_start_abs > 0): the reference scores one prompt at a time")
+            O, lse = prefill_attention(Qh, Khat, Vhat, return_lse=True)
+            if stored:  # layer.py:808-838: the sparse correction from the stored slots
+                for b, sq in enumerate(seqs):
+                    O[b] = prefill_correction(cache, self.layer_id, Qh[b].transpose(0, 1), Khat[b], Vhat[b],
+                                              lse[b], seq=sq).transpose(0, 1)
         out = self._out(O, hidden.dtype).to(hidden.dtype)
         return out[0] if squeeze else out
 

@@ -76,6 +76,37 @@ def test_layer_prefill_matches_oracle(monkeypatch, mode):
         assert torch.equal(getattr(cache, nm), getattr(ref_cache, nm)), nm
 
 
+def test_layer_prefill_carekv_stored_matches_reference(monkeypatch):
+    """CAREKVLayer.prefill in carekv_stored mode (layer.py:780-838) on the
+    reference prefill golden: identity projections pick q / k / v out of
+    hidden = [q; k; v] and W_O returns the attention output (both exact in
+    fp16), so the layer output is the corrected attention itself."""
+    import care_kv
+    from helpers import PAPER_ENV, PREFILL_CASES, load_golden, prefill_cfg_kwargs
+    for k, v in PAPER_ENV.items():
+        monkeypatch.setenv(k, v)
+    monkeypatch.setenv("CAREKV_PREFILL_MODE", "carekv_stored")
+    monkeypatch.setenv("CAREKV_K_CORRECTION_MODE", "exact")
+    print("layer prefill carekv_stored golden gqa8_d64", flush=True)
+    g = load_golden("prefill_gqa8_d64.npz")
+    spec = PREFILL_CASES["gqa8_d64"]
+    cfg = care_kv.CacheConfig(packed_base=True, scale_quant="int8", read_budget_ratio=0.0,
+                              **prefill_cfg_kwargs(g, spec))
+    T, Hq, Hkv, D = int(g["T"]), spec["Hq"], spec["Hkv"], spec["D"]
+    nq, nk = Hq * D, Hkv * D
+    eye = torch.eye(nq + 2 * nk, dtype=torch.float16, device="cuda")
+    lay = care_kv.CAREKVLayer(cfg, 0, eye[:nq].contiguous(), eye[nq:nq + nk].contiguous(),
+                              eye[nq + nk:].contiguous(), eye[:nq, :nq].contiguous())
+    Q, K, V = (torch.from_numpy(g[n]) for n in ("Q", "K", "V"))
+    hidden = torch.cat([Q.reshape(T, -1), K.permute(1, 0, 2).reshape(T, -1), V.permute(1, 0, 2).reshape(T, -1)],
+                       1).cuda()
+    cache = care_kv.CAREKVCache(cfg, n_seq=1)
+    out = lay.prefill(cache, hidden).float().cpu().numpy().reshape(T, Hq, D)
+    ref = g["O"].astype(np.float32)
+    err = np.abs(out - ref)
+    assert np.all(err <= np.maximum(2e-3, np.spacing(np.abs(g["O"])).astype(np.float32))), err.max()
+
+
 def test_layer_decode_steps_match_direct_calls(monkeypatch):
     """decode_step = append + decode_attention + W_O on the same cache."""
     import care_kv
