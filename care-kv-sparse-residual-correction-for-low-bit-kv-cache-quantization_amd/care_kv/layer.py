@@ -152,6 +152,14 @@ class CAREKVLayer(nn.Module):
                 Khat = quant_dequant(Kh, cfg.base_bits, cfg.group_size)
                 Vhat = quant_dequant(Vh, cfg.base_bits, cfg.group_size)
             stored = mode == "carekv_stored" and any_read_budget(cfg)
+            if stored and os.environ.get("CAREKV_KSCORE_LIVE", "0") != "1":
+                stored = False
+                if "carekv_stored_proxy" not in _warned:
+                    _warned.add("carekv_stored_proxy")
+                    warnings.warn("CAREKV_PREFILL_MODE=carekv_stored with the sketch-proxy K score "
+                                  "(CAREKV_KSCORE_LIVE=0): the prefill correction is built for the query-aware "
+                                  "score only; the prefill output is the base attention over K_hat / V_hat",
+                                  RuntimeWarning, stacklevel=2)
             if stored and token_start_abs != 0:
                 raise NotImplementedError("carekv_stored prefill correction of a prompt continuation "
                                           "(token_start_abs > 0): the reference scores one prompt at a time")
