@@ -12,10 +12,11 @@ struct WsLayout {
   int nsplit, F, ncand;
 };
 
-WsLayout ws_layout(const carekv_arena& A, const carekv_decode_params& dp) {
+// gq: query columns per (entry, kv head); 0 = n_heads / n_kv_heads
+WsLayout ws_layout(const carekv_arena& A, const carekv_decode_params& dp, int gq = 0) {
   WsLayout L{};
   const long BH = (long)dp.batch * A.n_kv_heads;
-  const int GQ = dp.n_heads / A.n_kv_heads;
+  const int GQ = gq > 0 ? gq : dp.n_heads / A.n_kv_heads;
   const int D = A.head_dim;
   const int Pm = dp.max_pages_used > 0 ? dp.max_pages_used : 1;
   L.nsplit = (Pm + dp.split_pages - 1) / dp.split_pages;
@@ -52,6 +53,7 @@ namespace {
 struct PfRows {
   const carekv_prefill_corr_params* p;
   int pages;
+  int R, G0;  // rows per entry, query heads per kv head
 };
 
 __global__ __launch_bounds__(256) void prompt_vsq_kernel(const uint16_t* __restrict__ v, int T, int D, int pages,
@@ -80,7 +82,7 @@ int run_decode(const carekv_arena* arena, const carekv_decode_params* dp, const 
   CAREKV_REQUIRE(A.residual_bits == 4, "kernels support residual_bits=4");
   CAREKV_REQUIRE(dp->batch > 0 && dp->n_heads > 0, "batch and n_heads must be positive");
   CAREKV_REQUIRE(dp->n_heads % A.n_kv_heads == 0, "n_heads must be a multiple of n_kv_heads");
-  const int GQ = dp->n_heads / A.n_kv_heads;
+  const int GQ = pf ? pf->G0 * pf->R : dp->n_heads / A.n_kv_heads;
   CAREKV_REQUIRE(GQ >= 1 && GQ <= 16, "query heads per kv head must be in 1..16");
   CAREKV_REQUIRE(pf || (dp->seq_slot && dp->n_pages), "seq_slot and n_pages are required");
   CAREKV_REQUIRE(dp->max_pages_used >= 0 && dp->max_pages_used <= A.max_pages, "max_pages_used out of range");
@@ -98,7 +100,7 @@ int run_decode(const carekv_arena* arena, const carekv_decode_params* dp, const 
   const bool need_x = dp->correction != 0 && (proxy || dp->route_policy == 3);
   CAREKV_REQUIRE(!proxy || (A.k_sketch && A.k_channel_group == 32 && A.sketch_dim >= 1 && A.sketch_dim <= 64),
                  "the sketch proxy needs k_sketch, k_channel_group 32 and sketch_dim in 1..64");
-  const WsLayout L = ws_layout(A, *dp);
+  const WsLayout L = ws_layout(A, *dp, GQ);
   const long vsq_off = L.total, need = L.total + (pf ? (long)A.n_kv_heads * pf->pages * 4 : 0);
   if (workspace_bytes < need) {
     set_error("%s: workspace too small (%lld < %lld)", pf ? "carekv_prefill_correct" : "carekv_decode_attn",
@@ -159,7 +161,8 @@ int run_decode(const carekv_arena* arena, const carekv_decode_params* dp, const 
   if (pf) {
     const carekv_prefill_corr_params& P = *pf->p;
     a.pf = 1;
-    a.pf_seq = P.seq; a.pf_row0 = P.row_begin; a.pf_pages = pf->pages; a.pf_T = P.n_tokens;
+    a.pf_seq = P.seq; a.pf_row0 = P.row_begin; a.pf_row_end = P.row_begin + P.n_rows;
+    a.pf_R = pf->R; a.pf_G0 = pf->G0; a.pf_pages = pf->pages; a.pf_T = P.n_tokens;
     a.pf_k = P.k_hat; a.pf_v = P.v_hat; a.pf_lse = P.lse;
     a.pf_vsq = (float*)(ws + vsq_off);
     hipLaunchKernelGGL(prompt_vsq_kernel, dim3((unsigned)((pf->pages + 3) / 4), A.n_kv_heads), dim3(256), 0, s,
@@ -211,13 +214,18 @@ int prefill_setup(const carekv_arena* arena, const carekv_decode_params* read,
   CAREKV_REQUIRE((long)pp->n_tokens * A.head_dim * 2 < (1L << 32), "prompt rows exceed 4 GiB per kv head");
   CAREKV_REQUIRE(read->correction != 0, "prefill rows run the correction (correction must be 1)");
   CAREKV_REQUIRE(read->k_proxy == 0, "prefill rows support the query-aware K score only (k_proxy must be 0)");
+  CAREKV_REQUIRE(read->n_heads > 0 && read->n_heads % A.n_kv_heads == 0 && read->n_heads / A.n_kv_heads <= 16,
+                 "n_heads must be a multiple of n_kv_heads with at most 16 query heads per kv head");
   dp = *read;
-  dp.batch = pp->n_rows;
+  pf.p = pp;
+  pf.pages = pages;
+  // pack consecutive rows into the 16 query columns of an entry
+  pf.G0 = read->n_heads / A.n_kv_heads;
+  pf.R = 16 / pf.G0;
+  dp.batch = (pp->n_rows + pf.R - 1) / pf.R;
   dp.max_pages_used = pages;
   dp.seq_slot = nullptr;
   dp.n_pages = nullptr;
-  pf.p = pp;
-  pf.pages = pages;
   return CAREKV_OK;
 }
 }  // namespace
@@ -228,7 +236,7 @@ extern "C" int64_t carekv_prefill_correct_workspace_bytes(const carekv_arena* ar
   carekv_decode_params dp{};
   PfRows pf{};
   if (prefill_setup(arena, read, pp, dp, pf) != CAREKV_OK || dp.split_pages <= 0) return -1;
-  return ws_layout(*arena, dp).total + (int64_t)arena->n_kv_heads * pf.pages * 4;
+  return ws_layout(*arena, dp, pf.G0 * pf.R).total + (int64_t)arena->n_kv_heads * pf.pages * 4;
 }
 
 extern "C" int carekv_prefill_correct(const carekv_arena* arena, const carekv_decode_params* read,

@@ -112,7 +112,14 @@ void decode_apply_kernel(carekv_arena A, DecodeArgs a) {
     if (any) s_items[n_items + pos] = p;
     n_items += tot;
   }
-  stage_q<D>(sq, sqr, a.q + ((long)b * a.Hq + kvh * GQ) * D, GQ);
+  if (a.pf) {
+    stage_q_by<D>(sq, sqr, [&](int n) {
+      const PfCol x = pf_col(a, b, kvh, n);
+      return x.ok ? a.q + pf_row_off(a, x) * D : (const uint16_t*)nullptr;
+    });
+  } else {
+    stage_q<D>(sq, sqr, a.q + ((long)b * a.Hq + kvh * GQ) * D, GQ);
+  }
   __syncthreads();
 
   const float Mq = qv ? a.ml[qrow * 2] : 0.f;
@@ -314,6 +321,12 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(int Hkv, int D, Dec
   const int bk = b * Hkv + kvh;
   for (int idx = threadIdx.x; idx < GQ * D; idx += 256) {
     const int qq = idx / D, d = idx % D;
+    long orow = (long)b * a.Hq + kvh * GQ + qq;
+    if (a.pf) {  // prefill rows: the column's (row, head); padding columns write nothing
+      const PfCol x = pf_col(a, b, kvh, qq);
+      if (!x.ok) continue;
+      orow = pf_row_off(a, x);
+    }
     const long bq = (long)bk * GQ + qq;
     const float M = a.ml[bq * 2], L = a.ml[bq * 2 + 1];
     float O = 0.f, nm = 0.f, dn = 0.f;
@@ -342,7 +355,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(int Hkv, int D, Dec
         o = ob + (nm - dn * ob) / L;
       }
     }
-    a.out[((long)b * a.Hq + kvh * GQ + qq) * D + d] = f2h(o);
+    a.out[orow * D + d] = f2h(o);
   }
 }
 

@@ -46,22 +46,26 @@ struct DecodeArgs {
   // row's base-2 log-sum-exp (pf_lse, natural log, [Hq][pf_T]) as the
   // reference's fp16 attention weights; every candidate of the prompt's
   // pf_pages pages counts towards the normalisation and the budgets.
+  // Entry b packs pf_R consecutive rows: its GQ = pf_G0 * pf_R query
+  // columns are (row pf_row0 + b * pf_R + c / pf_G0, head c % pf_G0 of the
+  // kv head's group); rows from pf_row_end on are padding.
   int pf;
-  int pf_seq, pf_row0, pf_pages, pf_T;
+  int pf_seq, pf_row0, pf_row_end, pf_R, pf_G0, pf_pages, pf_T;
   const uint16_t* pf_k;
   const uint16_t* pf_v;
   const float* pf_lse;
   float* pf_vsq;  // [Hkv][pf_pages] sum of V_hat^2 over each page's prompt rows
 };
 
-// The cache row and visible extent of batch entry b.
+// The cache row and visible extent of batch entry b (for prefill rows, of
+// its last row).
 struct EntryRow {
   int seq, np, ntok;
 };
 __device__ __forceinline__ EntryRow entry_row(const carekv_arena& A, const DecodeArgs& a, int b) {
   EntryRow e;
   if (a.pf) {
-    const int row = a.pf_row0 + b;
+    const int row = min(a.pf_row0 + (b + 1) * a.pf_R, a.pf_row_end) - 1;
     e.seq = a.pf_seq;
     e.ntok = row + 1;
     e.np = row / kPage + 1;
@@ -73,6 +77,24 @@ __device__ __forceinline__ EntryRow entry_row(const carekv_arena& A, const Decod
     e.ntok = 0x7fffffff;
   }
   return e;
+}
+
+// Query column c of prefill entry b of kv head kvh: its prompt row, its
+// query head, and whether the row exists.
+struct PfCol {
+  int row, head;
+  bool ok;
+};
+__device__ __forceinline__ PfCol pf_col(const DecodeArgs& a, int b, int kvh, int c) {
+  PfCol x;
+  x.row = a.pf_row0 + b * a.pf_R + c / a.pf_G0;
+  x.head = kvh * a.pf_G0 + c % a.pf_G0;
+  x.ok = c < a.GQ && x.row < a.pf_row_end;
+  return x;
+}
+// Element offset of a column's row in q / out / diag rows ([n_rows][Hq][.]).
+__device__ __forceinline__ long pf_row_off(const DecodeArgs& a, const PfCol& x) {
+  return (long)(x.row - a.pf_row0) * a.Hq + x.head;
 }
 
 // Page record per (sequence, kv head, query, page), F floats:

@@ -510,18 +510,20 @@ __device__ __forceinline__ float4_t kslot_dot(const int8_t* slot_base, const _Fl
 // zero), in natural order (sq) and in the pair order of the K residual
 // codes inside every 8-dim block (sqr).  Call with all threads of the
 // block, followed by a barrier.
-template <int D>
-__device__ __forceinline__ void stage_q(_Float16* sq, _Float16* sqr, const uint16_t* q, int GQ) {
+// rowp(n) gives query row n (nullptr: a zero row).
+template <int D, class RowPtr>
+__device__ __forceinline__ void stage_q_by(_Float16* sq, _Float16* sqr, RowPtr rowp) {
   using P = Pairs<4, 8, 4>;
   for (int i = threadIdx.x; i < 16 * D; i += blockDim.x) {
-    const int n = i / D;
-    const _Float16 v = n < GQ ? bits2half(q[i]) : (_Float16)0.f;
-    sq[i] = v;
-    const int blk = i & ~7, e = i & 7;
-    _Float16 vr = (_Float16)0.f;
-    if (n < GQ) vr = bits2half(q[blk + P::T.slot_code[e]]);
-    sqr[i] = vr;
+    const int n = i / D, d = i % D;
+    const uint16_t* r = rowp(n);
+    sq[i] = r ? bits2half(r[d]) : (_Float16)0.f;
+    sqr[i] = r ? bits2half(r[(d & ~7) + P::T.slot_code[d & 7]]) : (_Float16)0.f;
   }
+}
+template <int D>
+__device__ __forceinline__ void stage_q(_Float16* sq, _Float16* sqr, const uint16_t* q, int GQ) {
+  stage_q_by<D>(sq, sqr, [&](int n) { return n < GQ ? q + n * D : (const uint16_t*)nullptr; });
 }
 
 // Merge the 4 waves' online-softmax partials (m, l, O rows = queries) into

@@ -207,7 +207,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
   const long pg_base = ((long)kvh * A.n_seq + seq) * A.max_pages;
   const int tid = threadIdx.x;
   const long bq = (long)bk * GQ + qq;
-  int32_t* diagp = a.diag ? a.diag + ((long)b * a.Hq + kvh * GQ + qq) * a.diag_cap : nullptr;
+  int32_t* diagp = nullptr;
+  if (a.diag) {
+    if (a.pf) {  // prefill rows: the column's (row, head); padding columns write nothing
+      const PfCol x = pf_col(a, b, kvh, qq);
+      diagp = x.ok ? a.diag + pf_row_off(a, x) * a.diag_cap : nullptr;
+    } else {
+      diagp = a.diag + ((long)b * a.Hq + kvh * GQ + qq) * a.diag_cap;
+    }
+  }
 
   // ---- softmax statistics from the split partials
   float mloc = -INFINITY;

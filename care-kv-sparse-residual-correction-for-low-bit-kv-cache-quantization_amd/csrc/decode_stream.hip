@@ -69,15 +69,26 @@ void decode_stream_kernel(carekv_arena A, DecodeArgs a) {
   const float sm_log2 = a.sm_log2;
   const long rq = (long)a.Pmax * a.F;  // record stride between query heads
 
-  stage_q<D>(sq, sqr, a.q + ((long)b * a.Hq + kvh * GQ) * D, GQ);
+  if constexpr (PF) {
+    stage_q_by<D>(sq, sqr, [&](int n) {
+      const PfCol x = pf_col(a, b, kvh, n);
+      return x.ok ? a.q + pf_row_off(a, x) * D : (const uint16_t*)nullptr;
+    });
+  } else {
+    stage_q<D>(sq, sqr, a.q + ((long)b * a.Hq + kvh * GQ) * D, GQ);
+  }
   __syncthreads();
   half8_t qB[G::NS];
   load_q_operand<D, BITS>(qB, sq, ln, lj);
 
   uint32_t* vt = reinterpret_cast<uint32_t*>(smem) + w * VT_WORDS;
   float m_run = -INFINITY, l_run = 0.f;
-  if constexpr (PF)  // lane column ln is query ln (columns >= GQ hold zero queries)
-    m_run = ln < GQ ? a.pf_lse[(long)(kvh * GQ + ln) * a.pf_T + a.pf_row0 + b] * 1.4426950408889634f : 0.f;
+  int ntok_l = 0;  // prefill rows: tokens the lane's query column sees
+  if constexpr (PF) {  // lane column ln (padding columns hold zero queries)
+    const PfCol x = pf_col(a, b, kvh, ln);
+    m_run = x.ok ? a.pf_lse[(long)x.head * a.pf_T + x.row] * 1.4426950408889634f : 0.f;
+    ntok_l = x.ok ? x.row + 1 : 0;
+  }
   float4_t oacc[NT];
 #pragma unroll
   for (int t = 0; t < NT; ++t) oacc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -125,7 +136,11 @@ void decode_stream_kernel(carekv_arena A, DecodeArgs a) {
     }
     // lane (n = query, j): sacc[i] = S[token 4j+i][query n]
     float x[4];
-    if (nv >= kPage) {
+    if constexpr (PF) {  // the causal limit of the lane's column
+      const int nvl = min(nv, ntok_l - p * kPage);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[i] = (4 * lj + i < nvl) ? sacc[i] * sm_log2 : -INFINITY;
+    } else if (nv >= kPage) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) x[i] = sacc[i] * sm_log2;
     } else {
