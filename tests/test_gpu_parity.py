@@ -319,6 +319,57 @@ def test_prefill_correction_matches_reference(paper_env, name):
     assert n_tie <= max(2, T * Hq // 100), n_tie
 
 
+PREFILL_RANDOM = [
+    # D, Hq, Hkv, T, policy, k_mode, store (abs k, abs v), read (k, v)
+    (128, 16, 1, 97, "joint", "exact", (1, 1), (5, 5)),       # GQ 16: one row per entry
+    (64, 12, 4, 130, "joint", "exact", (2, 4), (4, 6)),       # GQ 3: five rows per entry, 15 columns
+    (128, 4, 4, 75, "separate", "exact", (1, 2), (3, 3)),     # MHA: sixteen rows per entry
+    (64, 8, 2, 260, "joint", "linear", (1, 1), (16, 16)),     # budget above the visible candidates
+]
+
+
+@pytest.mark.parametrize("case", PREFILL_RANDOM, ids=[f"D{c[0]}g{c[1] // c[2]}T{c[3]}{c[4]}{c[5]}"
+                                                      for c in PREFILL_RANDOM])
+def test_prefill_correction_random_vs_oracle(paper_env, case):
+    """carekv_prefill_correct vs the oracle's prefill_stored on random
+    prompts: GQA widths that pack 1, 5 and 16 rows per entry, a partial last
+    page, separate / linear variants and read budgets above the candidates
+    a row can see."""
+    import care_kv
+    D, Hq, Hkv, T, pol, kmode, (sk, sv), (rk, rv) = case
+    paper_env.setenv("CAREKV_K_CORRECTION_MODE", kmode)
+    print(f"prefill random case {case}", flush=True)
+    rng = np.random.default_rng(D + Hq * 7 + T)
+    K = rng.standard_normal((Hkv, T, D)).astype(F16)
+    V = rng.standard_normal((Hkv, T, D)).astype(F16)
+    K[:, :, rng.permutation(D)[:3]] *= F16(6.0)
+    Qt = rng.standard_normal((T, Hq, D)).astype(F16)
+    common = dict(num_layers=1, num_heads=Hq, num_kv_heads=Hkv, head_dim=D, page_size=16, max_pages=T // 16 + 4,
+                  base_bits=3, group_size=32, k_channel_group=32, v_token_block=4, sketch_dim=32,
+                  read_budget_mode="absolute", read_abs_k=rk, read_abs_v=rv, route_policy=pol,
+                  store_budget_mode="absolute", store_abs_k=sk, store_abs_v=sv)
+    oc = OCache(OCfg(**common))
+    hats = [write_pages_for_kv_head(oc, 0, h, K[h], V[h]) for h in range(Hkv)]
+    okh, ovh = np.stack([a for a, _ in hats]), np.stack([b for _, b in hats])
+    ref = prefill_stored(oc, 0, Qt.transpose(1, 0, 2), okh, ovh, k_mode=kmode, kind="both", k_corr_scale=0.1,
+                         score_normalize=True, kscore_live=True).astype(F32)
+    cfg = care_kv.CacheConfig(packed_base=True, scale_quant="int8", read_budget_ratio=0.0, **common)
+    cache = care_kv.CAREKVCache(cfg, device="cuda")
+    Kd, Vd = torch.from_numpy(K).cuda(), torch.from_numpy(V).cuda()
+    cache.write_prefill(0, Kd, Vd)
+    Kh, Vh = care_kv.quant_dequant(Kd, 3, 32), care_kv.quant_dequant(Vd, 3, 32)
+    assert np.array_equal(Kh.cpu().numpy().view(np.uint16), okh.view(np.uint16))
+    Q = torch.from_numpy(Qt).cuda()
+    _, lse = care_kv.prefill_attention(Q.transpose(0, 1), Kh, Vh, return_lse=True)
+    out = care_kv.prefill_correction(cache, 0, Q, Kh, Vh, lse, rows_per_call=50)
+    out = out.cpu().numpy().astype(F32)
+    err = np.abs(out - ref)
+    ulp = np.spacing(np.abs(ref).astype(F16)).astype(F32)
+    # rows whose selection crosses an epsilon tie may differ more: allow a few
+    bad = np.any(err > np.maximum(2e-3, ulp), axis=-1)
+    assert bad.mean() <= 0.01, (bad.mean(), err.max())
+
+
 # ------------------------------------------------------------------ random shapes vs oracle
 RANDOM_CASES = [
     # D, bits, Hq, Hkv, T, n_append, policy, k_mode, store (abs k, abs v) or ratio, read (k, v)
