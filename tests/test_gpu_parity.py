@@ -325,6 +325,8 @@ PREFILL_RANDOM = [
     (64, 12, 4, 130, "joint", "exact", (2, 4), (4, 6)),       # GQ 3: five rows per entry, 15 columns
     (128, 4, 4, 75, "separate", "exact", (1, 2), (3, 3)),     # MHA: sixteen rows per entry
     (64, 8, 2, 260, "joint", "linear", (1, 1), (16, 16)),     # budget above the visible candidates
+    (64, 8, 2, 5, "joint", "exact", (1, 1), (2, 2)),          # one partial page
+    (128, 8, 2, 16, "separate", "exact", (2, 4), (3, 3)),     # exactly one page
 ]
 
 
@@ -447,16 +449,19 @@ def test_batched_sequences_match_single(paper_env):
     """B sequences in one launch == each sequence decoded alone."""
     import care_kv
     rng = np.random.default_rng(11)
-    D, Hq, Hkv, B = 128, 8, 2, 3
+    D, Hq, Hkv = 128, 8, 2
     cfg = care_kv.CacheConfig(num_layers=1, num_heads=Hq, num_kv_heads=Hkv, head_dim=D, page_size=16, max_pages=40,
                               base_bits=3, group_size=32, packed_base=True, scale_quant="int8",
                               store_budget_mode="absolute", store_abs_k=1, store_abs_v=1,
                               read_budget_mode="absolute", read_abs_k=8, read_abs_v=8, route_policy="joint",
                               read_budget_ratio=0.0)
     paper_env.setenv("CAREKV_K_CORRECTION_MODE", "exact")
+    lens = [300, 517, 64, 1, 0]  # ragged, a one-token sequence and an empty one
+    B = len(lens)
     cache = care_kv.CAREKVCache(cfg, device="cuda", n_seq=B)
-    lens = [300, 517, 64]
     for s, T in enumerate(lens):
+        if T == 0:
+            continue
         K = torch.from_numpy(rng.standard_normal((Hkv, T, D)).astype(F16)).cuda()
         V = torch.from_numpy(rng.standard_normal((Hkv, T, D)).astype(F16)).cuda()
         cache.write_prefill(0, K, V, seqs=[s])
@@ -465,6 +470,8 @@ def test_batched_sequences_match_single(paper_env):
     for s in range(B):
         one = care_kv.decode_attention(cache, 0, q[s:s + 1], seqs=[s])
         assert torch.equal(both[s], one[0])
+    assert torch.isfinite(both[3]).all()
+    assert torch.count_nonzero(both[4]) == 0  # nothing to attend to: zeros, as an empty softmax sum gives
 
 
 # ------------------------------------------------------------------ router policies vs oracle
