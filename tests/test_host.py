@@ -171,3 +171,31 @@ def test_prefill_mode_resolution(monkeypatch):
     monkeypatch.setenv("CAREKV_PREFILL_MODE", "bogus")
     with pytest.raises(ValueError):
         resolve_prefill_mode()
+
+
+def test_prefill_correct_rejects_bad_rows():
+    """carekv_prefill_correct_workspace_bytes validates the prompt rows and
+    the read knobs on the host (no device call): rows outside the prompt, a
+    prompt longer than the arena, the sketch proxy and correction off are
+    refused with -1; a valid request sizes the workspace."""
+    import ctypes as C
+    _lib = _ensure_built()
+    lib = _lib.load()
+    a = _lib.Arena(n_seq=2, n_kv_heads=2, max_pages=8, head_dim=64, base_bits=3, page_size=16, group_size=32,
+                   k_channel_group=32, v_token_block=4, sketch_dim=32, scale_mode=1, residual_bits=4, n_slots=64)
+    dp = _lib.DecodeParams(n_heads=8, correction=1, k_cap=2, v_cap=4, split_pages=16, lambda_k=1.0, lambda_v=1.0)
+
+    def ws(**kw):
+        p = dict(seq=0, n_tokens=100, row_begin=0, n_rows=100, k_hat=1, v_hat=1, lse=1)
+        p.update(kw)
+        return lib.carekv_prefill_correct_workspace_bytes(C.byref(a), C.byref(dp), C.byref(_lib.PrefillCorrParams(**p)))
+
+    assert ws() > 0
+    assert ws(row_begin=60, n_rows=41) == -1      # past the prompt
+    assert ws(n_tokens=16 * 8 + 1, n_rows=1) == -1  # more pages than the arena row
+    assert ws(seq=2) == -1                         # no such sequence slot
+    assert ws(k_hat=0) == -1                       # missing K_hat
+    dp.k_proxy = 1
+    assert ws() == -1                              # the sketch proxy is not built for prompt rows
+    dp.k_proxy, dp.correction = 0, 0
+    assert ws() == -1                              # the pass is the correction
