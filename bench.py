@@ -39,6 +39,10 @@ CONFIGS = {
                workload="config2 Llama-2-7B decode B=16 32q/32kv D=128 N=4096"),
     "c3": dict(B=64, Hq=32, Hkv=8, D=128, N=32768, rk=128, rv=128, dist="outlier10", seed=3,
                workload="config3 Mistral-7B GQA decode B=64 32q/8kv D=128 N=32768"),
+    # config 3 with the base its text names: KIVI-style INT2 (per-channel K,
+    # per-token V), kept as the reference keeps it, fp16 K_hat / V_hat pages
+    "c3kivi": dict(B=64, Hq=32, Hkv=8, D=128, N=32768, rk=128, rv=128, dist="outlier10", seed=3, kivi=2,
+                   workload="config3 Mistral-7B GQA decode B=64 32q/8kv D=128 N=32768, KIVI-style INT2 base"),
 }
 
 
@@ -87,9 +91,11 @@ def algorithmic_bytes(spec, cfg, cache, diag_np):
     bits, G, P = cfg.base_bits, D // 32, math.ceil(N / 16)
     grp = Hq // Hkv
     k_slots = (cache.k_slot[0, :, :B, :P] >= 0).sum().item()          # stored K slots (all b, kvh)
-    per_bkv_stream = (2 * N * D * bits / 8            # K + V codes
-                      + 2 * N * G                     # int8 scales
-                      + 2 * P * 2                     # fp16 masters
+    if spec.get("kivi"):  # fp16 K_hat / V_hat rows, no scales
+        base = 2 * N * D * 2
+    else:                 # K + V codes, int8 scales, fp16 masters
+        base = 2 * N * D * bits / 8 + 2 * N * G + 2 * P * 2
+    per_bkv_stream = (base
                       + P * (4 + 1 + (G + 4) * 4)     # valid, has_meta, k_slot, v_slot
                       + grp * D * 2)                  # q
     stream = B * Hkv * per_bkv_stream + k_slots * (16 * 32 // 2 + 2)
@@ -149,18 +155,24 @@ def oracle_slice_from_device(cache, seq, kvh, spec):
     from oracle.cache import OCache, OCfg, OMeta
     cfg = cache.cfg
     P = cache.num_pages(0, kvh, seq)
+    kivi = bool(spec.get("kivi"))
     ocfg = OCfg(num_layers=1, num_heads=spec["Hq"] // spec["Hkv"], num_kv_heads=1, head_dim=cfg.head_dim,
                 page_size=16, max_pages=P, base_bits=cfg.base_bits, group_size=32, k_channel_group=32,
                 v_token_block=4, sketch_dim=cfg.sketch_dim, read_budget_mode="absolute", read_abs_k=spec["rk"],
-                read_abs_v=spec["rv"], route_policy="joint", store_budget_mode="ratio", store_budget_ratio=0.03)
+                read_abs_v=spec["rv"], route_policy="joint", store_budget_mode="ratio", store_budget_ratio=0.03,
+                base_quantizer="kivi_style" if kivi else "uniform")
     oc = OCache(ocfg, max_slots=cache.n_slots)
     g = lambda t: t[0, kvh, seq, :P].cpu().numpy()  # noqa: E731
-    oc.base_K_codes[0, 0] = g(cache.kcodes)
-    oc.base_V_codes[0, 0] = g(cache.vcodes)
-    oc.base_K_scale[0, 0] = g(cache.kscale)
-    oc.base_V_scale[0, 0] = g(cache.vscale)
-    oc.base_K_scale_master[0, 0] = g(cache.kmaster)
-    oc.base_V_scale_master[0, 0] = g(cache.vmaster)
+    if kivi:  # fp16 rows of the side buffer
+        oc.base_K_hat_fp16[0, 0] = g(cache.kcodes).view(np.float16)
+        oc.base_V_hat_fp16[0, 0] = g(cache.vcodes).view(np.float16)
+    else:
+        oc.base_K_codes[0, 0] = g(cache.kcodes)
+        oc.base_V_codes[0, 0] = g(cache.vcodes)
+        oc.base_K_scale[0, 0] = g(cache.kscale)
+        oc.base_V_scale[0, 0] = g(cache.vscale)
+        oc.base_K_scale_master[0, 0] = g(cache.kmaster)
+        oc.base_V_scale_master[0, 0] = g(cache.vmaster)
     oc.valid_tokens[0, 0] = g(cache.valid)
     oc.k_residual_buf[:] = cache.k_res[seq].cpu().numpy()
     oc.v_residual_buf[:] = cache.v_res[seq].cpu().numpy()
@@ -194,9 +206,13 @@ def cpu_baseline(cache, spec, q_np, slices):
         Qg = q_np[seq, kvh * grp:(kvh + 1) * grp]
         t0 = time.perf_counter()
         pids = oc.all_page_ids(0, 0)
-        Kc, Ks, Vc, Vs, _ = oc.read_base_concat(0, 0, pids)
-        Kh = Q.dequantize(Kc, Ks, 32).astype(np.float32)
-        Vh = Q.dequantize(Vc, Vs, 32).astype(np.float32)
+        if spec.get("kivi"):  # attention.py:997-1008: the fp16 side buffer, no dequantisation
+            Kh, Vh, _ = oc.read_base_hat_concat(0, 0, pids)
+            Kh, Vh = Kh.astype(np.float32), Vh.astype(np.float32)
+        else:
+            Kc, Ks, Vc, Vs, _ = oc.read_base_concat(0, 0, pids)
+            Kh = Q.dequantize(Kc, Ks, 32).astype(np.float32)
+            Vh = Q.dequantize(Vc, Vs, 32).astype(np.float32)
         S, A, O = base_attention(Kh, Vh, Qg.astype(np.float32))
         d = vectorized_joint_correction(oc, 0, 0, pids, Qg, S, A, Vh, O, kind="both", k_corr_scale=0.1,
                                         score_normalize=True, kscore_live=True, k_mode="exact")
@@ -419,11 +435,13 @@ def main():
     torch.cuda.set_device(dev)
     B, Hq, Hkv, D, N = spec["B"], spec["Hq"], spec["Hkv"], spec["D"], spec["N"]
     P = math.ceil(N / 16)
+    kivi = spec.get("kivi")
+    base_kw = dict(base_bits=kivi, base_quantizer="kivi_style") if kivi else dict(base_bits=3)
     cfg = care_kv.CacheConfig(num_layers=1, num_heads=Hq, num_kv_heads=Hkv, head_dim=D, page_size=16,
-                              max_pages=P + 4, base_bits=3, group_size=32, k_channel_group=32, v_token_block=4,
+                              max_pages=P + 4, group_size=32, k_channel_group=32, v_token_block=4,
                               sketch_dim=32, packed_base=True, scale_quant="int8", store_budget_mode="ratio",
                               store_budget_ratio=0.03, read_budget_ratio=0.0, read_budget_mode="absolute",
-                              read_abs_k=spec["rk"], read_abs_v=spec["rv"], route_policy="joint")
+                              read_abs_k=spec["rk"], read_abs_v=spec["rv"], route_policy="joint", **base_kw)
     t0 = time.time()
     cache = care_kv.CAREKVCache(cfg, device=dev, n_seq=B)
     for b in range(B):
@@ -492,21 +510,26 @@ def main():
     # the library runs the 4-query-head streaming kernel when a kv head has at
     # most 4 query heads and the split is a multiple of 16 pages
     sp = args.split_pages or care_kv.attention.default_split_pages(P, B * Hkv)
-    stream_kernel = "decode_stream4_kernel" if Hq // Hkv <= 4 and sp % 16 == 0 else "decode_stream_kernel"
+    stream_kernel = ("decode_stream4_kernel" if Hq // Hkv <= 4 and sp % 16 == 0 and not kivi
+                     else "decode_stream_kernel")
+    kbits, ksm = (16, 0) if kivi else (cfg.base_bits, 1)
     tr = load_traffic(stream_kernel, args.config + ("_base" if args.no_correction else ""))
     traffic = None if tr is None else tr.get("hbm_bytes_per_launch")
     line = {
         "metric": "CARE-KV decode-attn us/step + HBM GB/s (% roofline), Mistral-7B shape 32K ctx",
         "value": round(us_step, 2), "unit": "us/step", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
-        "dtype": "int3-packed KV, fp16 q/out, fp32 softmax", "data": "synthetic",
+        "dtype": ("fp16 K_hat/V_hat side buffer (KIVI INT2 values)" if kivi else "int3-packed KV") +
+                 ", fp16 q/out, fp32 softmax", "data": "synthetic",
         "config": {"workload": spec["workload"], "global_batch": B, "seq_len": N, "parallelism": "single-gpu",
-                   "base": "uniform INT3 g=32, int8 page scales", "store": "ratio 0.03 (1K+1V slot/page)",
+                   "base": (f"KIVI-style INT{kivi} (per-channel K, per-token V), fp16 side buffer" if kivi
+                            else "uniform INT3 g=32, int8 page scales"),
+                   "store": "ratio 0.03 (1K+1V slot/page)",
                    "read": f"joint top-{spec['rk'] + spec['rv']} (K {spec['rk']} + V {spec['rv']}), "
                            "KSCORE_LIVE, normalize, exact"},
         "hbm_gbps": round(gbps, 1),
         "phases_us": {n: round(t, 2) for n, t in zip(names, phase)},
-        "roofline": {"bound": "hbm", "kernel": f"{stream_kernel}<{D},{cfg.base_bits},1>",
+        "roofline": {"bound": "hbm", "kernel": f"{stream_kernel}<{D},{kbits},{ksm}>",
                      "achieved": round(stream_gbps, 1), "peak": 8000.0, "unit": "GB/s",
                      "frac": round(stream_gbps / 8000.0, 4), "traffic": traffic,
                      "algorithmic_bytes_per_launch": int(stream_bytes), "launch_us": round(phase[0], 2),
