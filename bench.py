@@ -399,12 +399,95 @@ def prefill_correction_bench(args):
     print(json.dumps(line), flush=True)
 
 
+# end-to-end random-init TinyLlama-1.1B through
+# patch_llama_model, paper-best configuration; `--config c5`
+E2E_CONFIG = dict(B=32, T=2048, new=256, seed=5,
+                  workload="config5 TinyLlama-1.1B random init, 22 layers, B=32, prompt 2048, 256 greedy tokens")
+
+
+def e2e_bench(args):
+    """Greedy generation through the patched HF model: carekv_stored prefill
+    (store + prefill attention + stored-slot correction) and one CARE-KV
+    decode step per layer and token, paper-best knobs (README.md:151-165).
+    value = generated tokens / s over the whole generate call.  Quality:
+    teacher-forced top-1 agreement of the unpatched fp16 model with the
+    generated tokens (the reference model cannot run on the GPU box)."""
+    os.environ.update(PAPER_ENV)
+    os.environ.update(CAREKV_PREFILL_MODE="carekv_stored", CAREKV_CORRECTION_IMPL="vectorized")
+    import torch
+    from transformers import LlamaConfig, LlamaForCausalLM
+    import care_kv
+    c = E2E_CONFIG
+    B, T, new = c["B"], c["T"], c["new"]
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    mc = LlamaConfig(hidden_size=2048, intermediate_size=5632, num_hidden_layers=22, num_attention_heads=32,
+                     num_key_value_heads=4, vocab_size=32000, max_position_embeddings=4096, rms_norm_eps=1e-5,
+                     initializer_range=0.02)
+    mc._attn_implementation = "eager"
+    torch.manual_seed(c["seed"])
+    t0 = time.time()
+    with dev:  # initialise on the device
+        model = LlamaForCausalLM(mc).half().eval()
+        ref = LlamaForCausalLM(mc).half().eval()
+    ref.load_state_dict(model.state_dict())
+    log(f"[bench] c5: models built in {time.time() - t0:.1f}s")
+    P = (T + new) // 16 + 4
+    cc = care_kv.CacheConfig(num_layers=22, num_heads=32, num_kv_heads=4, head_dim=64, page_size=16, max_pages=P,
+                             base_bits=3, group_size=32, k_channel_group=32, v_token_block=4, sketch_dim=32,
+                             packed_base=True, scale_quant="int8", store_budget_mode="absolute", store_abs_k=2,
+                             store_abs_v=4, read_budget_mode="absolute", read_abs_k=2, read_abs_v=2,
+                             route_policy="joint", read_budget_ratio=0.0, correction_impl="vectorized")
+    care_kv.patch_llama_model(model, cc)
+    g = torch.Generator().manual_seed(c["seed"] + 1)
+    ids = torch.randint(0, 32000, (B, T), generator=g).to(dev)
+    with torch.no_grad():
+        model.generate(ids[:, :64], max_new_tokens=4, do_sample=False, use_cache=True)  # warm-up
+        care_kv.reset_all_caches(model)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        out = model.generate(ids, max_new_tokens=new, do_sample=False, use_cache=True)
+        torch.cuda.synchronize()
+        sec = time.perf_counter() - t0
+        care_kv.reset_all_caches(model)
+        # time the prefill alone (one forward over the prompt, the cache written)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        model(ids, use_cache=False)
+        torch.cuda.synchronize()
+        pre = time.perf_counter() - t1
+        care_kv.reset_all_caches(model)
+        # teacher-forced agreement: fp16 eager attention on the generated sequence
+        agree = 0
+        for b0 in range(0, B, 4):
+            lg = ref(out[b0:b0 + 4, :-1], use_cache=False).logits[:, T - 1:]
+            agree += int((lg.argmax(-1) == out[b0:b0 + 4, T:]).sum())
+            del lg
+    agreement = agree / (B * new)
+    tps = B * new / sec
+    log(f"[bench] c5: generate {sec:.2f} s for {B}x{new} tokens ({tps:.0f} tokens/s), prefill alone {pre * 1e3:.0f} ms; "
+        f"teacher-forced top-1 agreement with fp16 attention {agreement:.4f}")
+    line = {
+        "metric": "CARE-KV end-to-end greedy generation tokens/s (TinyLlama-1.1B shape, random init, INT3 comb+ex)",
+        "value": round(tps, 1), "unit": "tokens/s", "n_gpus": 1, "steps": 1, "warmup": 1,
+        "ms_per_step": round(sec * 1e3, 1), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp16 model, int3-packed KV", "data": "synthetic (random-init weights, random token ids)",
+        "config": {"workload": c["workload"], "global_batch": B, "seq_len": T, "new_tokens": new,
+                   "parallelism": "single-gpu",
+                   "carekv": "carekv_stored prefill, store abs 2K/4V, read abs 2K/2V joint, KSCORE_LIVE, exact"},
+        "prefill_ms": round(pre * 1e3, 1),
+        "top1_agreement_vs_fp16_attention": round(agreement, 4),
+        "roofline": None, "cpu_baseline": None,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS) + ["c4", "pfc"])
+    ap.add_argument("--config", default="c3", choices=sorted(CONFIGS) + ["c4", "c5", "pfc"])
     ap.add_argument("--cpu-slices", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--split-pages", type=int, default=None)
@@ -425,6 +508,9 @@ def main():
         return
     if args.config == "pfc":
         prefill_correction_bench(args)
+        return
+    if args.config == "c5":
+        e2e_bench(args)
         return
     os.environ.update(PAPER_ENV)
     import numpy as np
