@@ -327,18 +327,20 @@ PREFILL_RANDOM = [
     (64, 8, 2, 260, "joint", "linear", (1, 1), (16, 16)),     # budget above the visible candidates
     (64, 8, 2, 5, "joint", "exact", (1, 1), (2, 2)),          # one partial page
     (128, 8, 2, 16, "separate", "exact", (2, 4), (3, 3)),     # exactly one page
+    (128, 8, 2, 150, "joint", "exact", (2, 4), (6, 6), "kivi_style"),  # the KIVI-style fp16 side buffer
 ]
 
 
 @pytest.mark.parametrize("case", PREFILL_RANDOM, ids=[f"D{c[0]}g{c[1] // c[2]}T{c[3]}{c[4]}{c[5]}"
-                                                      for c in PREFILL_RANDOM])
+                                                      + (c[8] if len(c) > 8 else "") for c in PREFILL_RANDOM])
 def test_prefill_correction_random_vs_oracle(paper_env, case):
     """carekv_prefill_correct vs the oracle's prefill_stored on random
     prompts: GQA widths that pack 1, 5 and 16 rows per entry, a partial last
     page, separate / linear variants and read budgets above the candidates
     a row can see."""
     import care_kv
-    D, Hq, Hkv, T, pol, kmode, (sk, sv), (rk, rv) = case
+    D, Hq, Hkv, T, pol, kmode, (sk, sv), (rk, rv) = case[:8]
+    base = dict(base_bits=2, base_quantizer=case[8]) if len(case) > 8 else dict(base_bits=3)
     paper_env.setenv("CAREKV_K_CORRECTION_MODE", kmode)
     print(f"prefill random case {case}", flush=True)
     rng = np.random.default_rng(D + Hq * 7 + T)
@@ -347,9 +349,9 @@ def test_prefill_correction_random_vs_oracle(paper_env, case):
     K[:, :, rng.permutation(D)[:3]] *= F16(6.0)
     Qt = rng.standard_normal((T, Hq, D)).astype(F16)
     common = dict(num_layers=1, num_heads=Hq, num_kv_heads=Hkv, head_dim=D, page_size=16, max_pages=T // 16 + 4,
-                  base_bits=3, group_size=32, k_channel_group=32, v_token_block=4, sketch_dim=32,
+                  group_size=32, k_channel_group=32, v_token_block=4, sketch_dim=32,
                   read_budget_mode="absolute", read_abs_k=rk, read_abs_v=rv, route_policy=pol,
-                  store_budget_mode="absolute", store_abs_k=sk, store_abs_v=sv)
+                  store_budget_mode="absolute", store_abs_k=sk, store_abs_v=sv, **base)
     oc = OCache(OCfg(**common))
     hats = [write_pages_for_kv_head(oc, 0, h, K[h], V[h]) for h in range(Hkv)]
     okh, ovh = np.stack([a for a, _ in hats]), np.stack([b for _, b in hats])
@@ -358,8 +360,11 @@ def test_prefill_correction_random_vs_oracle(paper_env, case):
     cfg = care_kv.CacheConfig(packed_base=True, scale_quant="int8", read_budget_ratio=0.0, **common)
     cache = care_kv.CAREKVCache(cfg, device="cuda")
     Kd, Vd = torch.from_numpy(K).cuda(), torch.from_numpy(V).cuda()
-    cache.write_prefill(0, Kd, Vd)
-    Kh, Vh = care_kv.quant_dequant(Kd, 3, 32), care_kv.quant_dequant(Vd, 3, 32)
+    hats = cache.write_prefill(0, Kd, Vd)
+    if hats is not None:  # side-buffer base: the K_hat / V_hat the pages hold
+        Kh, Vh = hats
+    else:
+        Kh, Vh = care_kv.quant_dequant(Kd, 3, 32), care_kv.quant_dequant(Vd, 3, 32)
     assert np.array_equal(Kh.cpu().numpy().view(np.uint16), okh.view(np.uint16))
     Q = torch.from_numpy(Qt).cuda()
     _, lse = care_kv.prefill_attention(Q.transpose(0, 1), Kh, Vh, return_lse=True)
