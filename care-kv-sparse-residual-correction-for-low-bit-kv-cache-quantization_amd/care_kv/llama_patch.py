@@ -130,10 +130,14 @@ class CAREKVLlamaAttention(nn.Module):
                                               seqs=seqs)
 
         # keep HF's own cache length in step so that it sends one token per
-        # decode call (llama_patch.py:262-285)
+        # decode call (llama_patch.py:262-285).  The reference appends fp16
+        # zeros of the full K/V shape (a second KV cache's worth of memory);
+        # here the placeholders have head_dim 1: the length HF reads
+        # (shape[-2], of a non-empty tensor) advances at 1/head_dim of the
+        # memory.
         if use_cache and pkv is not None and hasattr(pkv, "update"):
             try:
-                z = hidden_states.new_zeros((B, self.cfg.num_kv_heads, T, self.cfg.head_dim))
+                z = hidden_states.new_zeros((B, self.cfg.num_kv_heads, T, 1))
                 pkv.update(z, z, self.layer_id)
             except Exception:
                 pass

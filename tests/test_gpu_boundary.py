@@ -177,6 +177,13 @@ def test_patched_llama_generates_with_cache(monkeypatch):
         assert cache.total_valid_tokens(layer, 0) == 41  # prompt + 4 decode appends
     care_kv.reset_all_caches(m)
     assert cache.total_valid_tokens(0, 0) == 0
+    # HF's cache tracks the length only: one-wide placeholders, not a second KV cache
+    from transformers import DynamicCache
+    hf = DynamicCache()
+    with torch.no_grad():
+        m(ids, past_key_values=hf, use_cache=True)
+    assert hf.get_seq_length() == 37
+    assert all(lay.keys.shape[-1] == 1 for lay in getattr(hf, "layers", []))
 
 
 def test_adapter_patches_a_given_model(monkeypatch):
