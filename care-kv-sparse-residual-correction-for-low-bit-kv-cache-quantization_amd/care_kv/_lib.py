@@ -34,7 +34,7 @@ class StoreParams(C.Structure):
     _fields_ = [("k_budget", C.c_int32), ("v_budget", C.c_int32), ("joint_budget", C.c_int32),
                 ("joint", C.c_int32), ("store_none", C.c_int32), ("sensitivity", C.c_double),
                 ("sink_tokens", C.c_int32), ("sketch_proj", C.c_void_p), ("k_hat", C.c_void_p),
-                ("v_hat", C.c_void_p)]
+                ("v_hat", C.c_void_p), ("keep_base", C.c_int32)]
 
 
 class DecodeParams(C.Structure):

@@ -132,7 +132,13 @@ def kivi_qdq(x: torch.Tensor, bits: int, per_channel: bool) -> torch.Tensor:
 class CAREKVCache:
     """Device-resident paged cache for ``n_seq`` sequences of one model."""
 
-    def __init__(self, cfg: CacheConfig, device=None, n_seq: int = 1, n_slots: Optional[int] = None):
+    def __init__(self, cfg: CacheConfig, device=None, n_seq: int = 1, n_slots: Optional[int] = None,
+                 streaming_store: bool = False):
+        """``streaming_store`` (no reference counterpart, packed bases): keep
+        each open page's true fp16 rows and, when decode appends fill the
+        page, store its residuals against the page's own base instead of
+        the reference's zero-residual fill store (layer.py:1128-1146), so
+        that decode-filled pages get slots."""
         check_kernel_config(cfg)
         if device is None:
             device = torch.device("cuda", torch.cuda.current_device())
@@ -166,6 +172,13 @@ class CAREKVCache:
         self.v_err = torch.zeros(*shp, self.nvb, dtype=F16, device=dev)
         self.k_sketch = torch.zeros(*shp, self.ncg, cfg.sketch_dim, dtype=F16, device=dev)
         self.v_sq = torch.zeros(*shp, dtype=torch.float32, device=dev)
+        self.streaming_store = bool(streaming_store)
+        if self.streaming_store:
+            if self.hat:
+                raise NotImplementedError("the streaming store is built for the packed bases")
+            # true rows of every (layer, seq, kv head)'s open page
+            self.open_k = torch.zeros(L, n_seq, H, T, D, dtype=F16, device=dev)
+            self.open_v = torch.zeros_like(self.open_k)
         self.k_cap, self.v_cap = store_caps(cfg)
         if n_slots is None:
             n_slots = max(64, P * H * L * self.k_cap, P * H * L * self.v_cap)
@@ -319,6 +332,14 @@ class CAREKVCache:
         _lib.check(lib.carekv_store_pages(a, sp, Kp.data_ptr(), Vp.data_ptr(), jobs_d.data_ptr(), len(jobs),
                                           gp_d.data_ptr(), B, ws.data_ptr(), _lib.stream_ptr(self.device)),
                    "carekv_store_pages")
+        if self.streaming_store:  # the last page stays open: keep its true rows
+            last = T - (n_new - 1) * ps
+            sl = torch.tensor(seqs, device=self.device)
+            self.open_k[layer, sl] = 0
+            self.open_v[layer, sl] = 0
+            if last < ps:
+                self.open_k[layer, sl, :, :last] = K[:, :, (n_new - 1) * ps:].to(F16)
+                self.open_v[layer, sl, :, :last] = V[:, :, (n_new - 1) * ps:].to(F16)
         if hats is not None:
             return hats[0] if B > 1 else hats[0][0], hats[1] if B > 1 else hats[1][0]
         return None
@@ -332,6 +353,8 @@ class CAREKVCache:
         B, H, D = k.shape
         seqs = list(range(B)) if seqs is None else list(seqs)
         dest = np.zeros((B * H, 4), dtype=np.int32)
+        offs = np.zeros(B * H, dtype=np.int64)
+        filled = []  # (seq, kv head, page) the appends fill
         r = 0
         for s in seqs:
             for h in range(H):
@@ -342,7 +365,10 @@ class CAREKVCache:
                     fresh = 1
                     self._token_start[layer, h, s, pid] = self.total_valid_tokens(layer, h, s)
                 dest[r] = (s, h, pid, fresh)
+                offs[r] = self.valid_host[layer, h, s, pid]
                 self.valid_host[layer, h, s, pid] += 1
+                if self.valid_host[layer, h, s, pid] == cfg.page_size:
+                    filled.append((s, h, pid))
                 r += 1
         dest_d = torch.from_numpy(dest).to(self.device)
         kk = k.to(F16).contiguous().view(B * H, D)
@@ -350,6 +376,46 @@ class CAREKVCache:
         lib = _lib.load()
         _lib.check(lib.carekv_append_rows(self.arena(layer), kk.data_ptr(), vv.data_ptr(), dest_d.data_ptr(), B * H,
                                           _lib.stream_ptr(self.device)), "carekv_append_rows")
+        if self.streaming_store:
+            si = torch.from_numpy(dest[:, 0].astype(np.int64)).to(self.device)
+            hi = torch.from_numpy(dest[:, 1].astype(np.int64)).to(self.device)
+            oi = torch.from_numpy(offs).to(self.device)
+            self.open_k[layer, si, hi, oi] = kk
+            self.open_v[layer, si, hi, oi] = vv
+            if filled:
+                self._streaming_fill_store(layer, filled)
+
+    def _streaming_fill_store(self, layer: int, filled):
+        """Store the filled pages' residuals from their true rows against the
+        pages' own base (carekv_store_pages with keep_base), as the fill store
+        of layer.py:1128-1146 with K_orig = the true rows."""
+        cfg = self.cfg
+        ps = cfg.page_size
+        filled = sorted(filled)  # grouped by sequence, kv heads in order
+        jobs = np.zeros((len(filled), _lib.PAGE_JOB_INTS), dtype=np.int32)
+        seqs = sorted({f[0] for f in filled})
+        group_ptr = np.zeros(len(seqs) + 1, dtype=np.int32)
+        for j, (s, h, pid) in enumerate(filled):
+            jobs[j] = (s, h, pid, ps, int(self._token_start[layer, h, s, pid]), 1)
+            group_ptr[seqs.index(s) + 1] = j + 1
+        si = torch.tensor([f[0] for f in filled], device=self.device)
+        hi = torch.tensor([f[1] for f in filled], device=self.device)
+        Kp = self.open_k[layer, si, hi].contiguous().view(-1, cfg.head_dim)
+        Vp = self.open_v[layer, si, hi].contiguous().view(-1, cfg.head_dim)
+        knobs = resolve_store_knobs(cfg, layer)
+        sp = _lib.StoreParams(k_budget=knobs.k_budget, v_budget=knobs.v_budget, joint_budget=knobs.joint_budget,
+                              joint=int(knobs.joint), store_none=int(knobs.store_none),
+                              sensitivity=knobs.sensitivity, sink_tokens=4,
+                              sketch_proj=self.sketch_proj.data_ptr(), keep_base=1)
+        lib = _lib.load()
+        ws = self.workspace("store", int(lib.carekv_store_workspace_bytes(len(jobs))))
+        jobs_d = torch.from_numpy(jobs).to(self.device)
+        gp_d = torch.from_numpy(group_ptr).to(self.device)
+        _lib.check(lib.carekv_store_pages(self.arena(layer), sp, Kp.data_ptr(), Vp.data_ptr(), jobs_d.data_ptr(),
+                                          len(jobs), gp_d.data_ptr(), len(seqs), ws.data_ptr(),
+                                          _lib.stream_ptr(self.device)), "carekv_store_pages (streaming)")
+        self.open_k[layer, si, hi] = 0
+        self.open_v[layer, si, hi] = 0
 
     # ------------------------------------------------------------ reads
     def read_base_hat_concat(self, layer: int, kv_head: int, page_ids: Optional[List[int]] = None, seq: int = 0):

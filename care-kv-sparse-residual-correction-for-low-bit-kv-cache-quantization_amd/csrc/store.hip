@@ -159,8 +159,29 @@ __global__ __launch_bounds__(256) void store_pages_kernel(carekv_arena A, carekv
         xv[i + 2 * j] = h2f((uint16_t)wb[j]); xv[i + 2 * j + 1] = h2f((uint16_t)(wb[j] >> 16));
       }
     }
-    sk = quant_group<BITS>(xk, ck);
-    sv = quant_group<BITS>(xv, cv);
+    if (sp.keep_base) {
+      // streaming store of a page the decode appends filled: the page keeps
+      // its base, the residual is taken against it as the decode reads it,
+      // half(code * half(scale code * master)) (layer.py:1104-1133)
+      const long row = pg * kPage + t;
+      uint32_t w[BITS];
+      load_bytes<CB>(w, A.kcodes + row * RB + g * CB);
+#pragma unroll
+      for (int i = 0; i < 32; ++i) ck[i] = get_code<BITS>(w, i);
+      load_bytes<CB>(w, A.vcodes + row * RB + g * CB);
+#pragma unroll
+      for (int i = 0; i < 32; ++i) cv[i] = get_code<BITS>(w, i);
+      if (A.scale_mode == 1) {
+        sk = (_Float16)((float)((const int8_t*)A.kscale)[row * NG + g] * h2f(A.kmaster[pg]));
+        sv = (_Float16)((float)((const int8_t*)A.vscale)[row * NG + g] * h2f(A.vmaster[pg]));
+      } else {
+        sk = bits2half(((const uint16_t*)A.kscale)[row * NG + g]);
+        sv = bits2half(((const uint16_t*)A.vscale)[row * NG + g]);
+      }
+    } else {
+      sk = quant_group<BITS>(xk, ck);
+      sv = quant_group<BITS>(xv, cv);
+    }
     // residual against the fp16 scale (residual_store.py:276-285)
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
@@ -225,7 +246,16 @@ __global__ __launch_bounds__(256) void store_pages_kernel(carekv_arena A, carekv
     vs = wave_sum(vs);
     if (lane == 0) A.v_sq[pg] = vs;
   }
-  if constexpr (MODE == 0 && BITS != 16) {
+  if (MODE == 0 && BITS != 16 && sp.keep_base) {
+    // ---- the page keeps its base; only the sum of V_hat^2 is refreshed
+    float vs = 0.f;
+    if (active && t < nvld) {
+#pragma unroll
+      for (int i = 0; i < 32; ++i) { const float vh = (float)dq(cv[i], sv); vs += vh * vh; }
+    }
+    vs = wave_sum(vs);
+    if (lane == 0) A.v_sq[pg] = vs;
+  } else if constexpr (MODE == 0 && BITS != 16) {
     // ---- packed base codes
     if (active) {
       uint32_t w[BITS];
@@ -651,6 +681,7 @@ extern "C" int carekv_store_pages(const carekv_arena* arena, const carekv_store_
   hipStream_t s = (hipStream_t)stream;
   if (A.base_bits == 16) {
     CAREKV_REQUIRE(sp->k_hat && sp->v_hat, "the fp16 base (base_bits=16) needs k_hat and v_hat");
+    CAREKV_REQUIRE(!sp->keep_base, "keep_base (streaming store) is built for the packed bases");
     if (A.head_dim == 64) return launch_store<64, 16>(A, *sp, K, V, jobs_dev, n_jobs, group_ptr_dev, n_groups, ws, s);
     return launch_store<128, 16>(A, *sp, K, V, jobs_dev, n_jobs, group_ptr_dev, n_groups, ws, s);
   }

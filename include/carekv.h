@@ -89,6 +89,14 @@ typedef struct carekv_store_params {
   const uint16_t* v_hat;   /* like K / V, written as the pages and the residual
                             * base (process_page with K_hat_override,
                             * residual_store.py:272-275); NULL otherwise       */
+  int32_t keep_base;       /* 1: streaming store of pages the decode appends
+                            * filled (packed bases): K / V are the pages' true
+                            * rows, the pages keep their codes and scales and
+                            * the residuals are taken against them as the decode
+                            * reads them.  No reference counterpart: the
+                            * reference stores such pages with K_orig = K_hat
+                            * (layer.py:1128-1146), which leaves them no slots.
+                            * 0: store as the prefill does                    */
 } carekv_store_params;
 
 /* One page write (prefill).  X rows for page j are X[j*page_size .. +page_size),

@@ -197,17 +197,25 @@ def write_pages_for_kv_head(cache: OCache, layer_id: int, kv_h: int, K_kv, V_kv,
         process_page(cache, layer_id, kv_h, pid, Kp, Vp, Kc, Ks, Vc, Vs,
                      token_start=token_start_abs + t0, num_valid=nv,
                      is_recent=is_recent, is_sink=is_sink, P=P, **store_kw)
+        if nv < ps:  # the open page's true rows, for a streaming fill store
+            cache.open_rows[(layer_id, kv_h, pid)] = (Kp.copy(), Vp.copy())
         k_hat.append(Q.dequantize(Kc, Ks, cfg.group_size).astype(K_kv.dtype)[:nv])
         v_hat.append(Q.dequantize(Vc, Vs, cfg.group_size).astype(V_kv.dtype)[:nv])
     return np.concatenate(k_hat), np.concatenate(v_hat)
 
 
-def decode_append(cache: OCache, layer_id: int, k_rows, v_rows, **store_kw):
+def decode_append(cache: OCache, layer_id: int, k_rows, v_rows, streaming: bool = False, **store_kw):
     """Cache side of ``CAREKVLayer.decode_step`` (``layer.py:1001-1146``,
     uniform base quantizer): append one token per kv head into the open page
     (allocating one when full) and, when the append fills the page, run the
     store with K_orig = K_hat (zero residual, so the page gets metadata with no
-    slots and a refilled partial prefill page loses its slots)."""
+    slots and a refilled partial prefill page loses its slots).
+
+    ``streaming=True`` (no reference counterpart; packed bases): the open
+    page's true rows are kept (``cache.open_rows``, the prompt's partial last
+    page included) and the fill store runs process_page on them against the
+    page's own codes and read-back scales, so decode-filled pages get
+    residual slots."""
     cfg = cache.cfg
     k_rows = np.asarray(k_rows)
     v_rows = np.asarray(v_rows)
@@ -218,6 +226,11 @@ def decode_append(cache: OCache, layer_id: int, k_rows, v_rows, **store_kw):
         if pid is None:
             pid = cache.alloc_page(layer_id, h)
             cache.valid_tokens[layer_id, h, pid] = 0
+        if streaming:
+            kt, vt = cache.open_rows.setdefault(
+                (layer_id, h, pid), (np.zeros((ps, cfg.head_dim), k_rows.dtype), np.zeros((ps, cfg.head_dim), v_rows.dtype)))
+            off = int(cache.valid_tokens[layer_id, h, pid])
+            kt[off], vt[off] = k_rows[h], v_rows[h]
         if cfg.side_buffer:
             # layer.py:1037-1075 (post-RoPE): the row quantised alone, K per
             # channel over T = 1, V per token; on fill K_orig = K_hat (:1089-1101)
@@ -244,5 +257,7 @@ def decode_append(cache: OCache, layer_id: int, k_rows, v_rows, **store_kw):
             Kh = Q.dequantize(Kc, Ks, cfg.group_size).astype(k_rows.dtype)
             Vh = Q.dequantize(Vc, Vs, cfg.group_size).astype(v_rows.dtype)
             ts = pos_abs + 1 - ps
+            if streaming:  # the true rows instead of K_hat
+                Kh, Vh = cache.open_rows.pop((layer_id, h, pid))
             process_page(cache, layer_id, h, pid, Kh, Vh, Kc, Ks, Vc, Vs, token_start=ts,
                          num_valid=ps, is_recent=True, is_sink=ts < 4, **store_kw)

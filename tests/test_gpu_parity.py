@@ -479,6 +479,60 @@ def test_batched_sequences_match_single(paper_env):
     assert torch.count_nonzero(both[4]) == 0  # nothing to attend to: zeros, as an empty softmax sum gives
 
 
+@pytest.mark.parametrize("D,bits", [(64, 3), (128, 2)])
+def test_streaming_store_matches_oracle(paper_env, D, bits):
+    """streaming_store (no reference counterpart): decode appends fill the
+    prompt's partial page and three decode-opened pages, each fill stored
+    from the true rows against the page's own base -- slot ids, residual
+    bytes and scales equal the oracle's process_page on the same inputs, and
+    the decode over the cache matches the oracle's."""
+    import care_kv
+    paper_env.setenv("CAREKV_K_CORRECTION_MODE", "exact")
+    Hq, Hkv, T, n_app = 8, 2, 100, 60
+    print(f"streaming store D={D} bits={bits}", flush=True)
+    rng = np.random.default_rng(D + bits)
+    K = rng.standard_normal((Hkv, T + n_app, D)).astype(F16)
+    V = rng.standard_normal((Hkv, T + n_app, D)).astype(F16)
+    K[:, :, rng.permutation(D)[:3]] *= F16(6.0)
+    Qh = rng.standard_normal((Hq, D)).astype(F16)
+    common = dict(num_layers=1, num_heads=Hq, num_kv_heads=Hkv, head_dim=D, page_size=16,
+                  max_pages=(T + n_app) // 16 + 4, base_bits=bits, group_size=32, k_channel_group=32,
+                  v_token_block=4, sketch_dim=32, read_budget_mode="absolute", read_abs_k=6, read_abs_v=6,
+                  route_policy="joint", store_budget_mode="absolute", store_abs_k=2, store_abs_v=4)
+    oc = OCache(OCfg(**common))
+    for h in range(Hkv):
+        write_pages_for_kv_head(oc, 0, h, K[h, :T], V[h, :T])
+    for t in range(T, T + n_app):
+        decode_append(oc, 0, K[:, t], V[:, t], streaming=True)
+    cfg = care_kv.CacheConfig(packed_base=True, scale_quant="int8", read_budget_ratio=0.0, **common)
+    cache = care_kv.CAREKVCache(cfg, device="cuda", streaming_store=True)
+    Kd, Vd = torch.from_numpy(K).cuda(), torch.from_numpy(V).cuda()
+    cache.write_prefill(0, Kd[:, :T], Vd[:, :T])
+    for t in range(T, T + n_app):
+        cache.append(0, Kd[:, t], Vd[:, t])
+    torch.cuda.synchronize()
+    nk, nv = oc.next_k_slot, oc.next_v_slot
+    assert cache.next_slot[0].tolist() == [nk, nv]
+    assert np.array_equal(cache.k_res[0, :nk].cpu().numpy(), oc.k_residual_buf[:nk])
+    assert np.array_equal(cache.v_res[0, :nv].cpu().numpy(), oc.v_residual_buf[:nv])
+    assert np.array_equal(cache.k_res_scale[0, :nk].cpu().numpy(), oc.k_residual_scale[:nk, 0])
+    assert np.array_equal(cache.v_res_scale[0, :nv].cpu().numpy(), oc.v_residual_scale[:nv, 0])
+    P = oc.next_page[0][0]
+    for h in range(Hkv):
+        for p in range(P):
+            m = oc.meta_table[0][h][p]
+            assert m is not None, (h, p)
+            assert cache.k_slot[0, h, 0, p].tolist() == list(m.k_residual_slots), (h, p)
+            assert cache.v_slot[0, h, 0, p].tolist() == list(m.v_residual_slots), (h, p)
+    # decode-filled pages hold slots now (the reference's fill store leaves none)
+    assert any(s >= 0 for s in oc.meta_table[0][0][P - 2].k_residual_slots)
+    out = care_kv.decode_attention(cache, 0, torch.from_numpy(Qh).cuda().unsqueeze(0))[0].cpu().numpy()
+    ref = oracle_decode(oc, 0, Qh, k_mode="exact", kind="both", k_corr_scale=0.1, score_normalize=True,
+                        kscore_live=True)
+    err = np.abs(out.astype(F32) - ref.astype(F32))
+    assert err.max() <= 2e-3, err.max()
+
+
 # ------------------------------------------------------------------ router policies vs oracle
 POLICY_CASES = [
     # policy, adaptive_score (rel, abs, min_keep) or None, live

@@ -478,3 +478,26 @@ def test_route_selection_matches_reference(golden):
                         (h, pol, asc, j, sorted(mine ^ ref))
                 n_checked += 1
     assert n_checked == 2 * len(variants) * 4
+
+
+def test_streaming_fill_store_gives_decode_pages_slots():
+    """decode_append(streaming=True) (no reference counterpart): a page the
+    appends fill is stored from its true rows against its own codes, so it
+    gets residual slots, and those residuals are true minus read-back base;
+    the reference's fill store (streaming=False) gives the same page none."""
+    rng = np.random.default_rng(3)
+    D, H, T, n = 64, 1, 20, 30
+    K = rng.standard_normal((H, T + n, D)).astype(F16)
+    V = rng.standard_normal((H, T + n, D)).astype(F16)
+    kw = dict(num_layers=1, num_heads=2, num_kv_heads=H, head_dim=D, page_size=16, max_pages=8, base_bits=3,
+              group_size=32, k_channel_group=32, v_token_block=4, sketch_dim=32, store_budget_mode="absolute",
+              store_abs_k=2, store_abs_v=4)
+    slots = {}
+    for streaming in (False, True):
+        c = OCache(OCfg(**kw))
+        write_pages_for_kv_head(c, 0, 0, K[0, :T], V[0, :T])
+        for t in range(T, T + n):
+            decode_append(c, 0, K[:, t], V[:, t], streaming=streaming)
+        slots[streaming] = [c.meta_table[0][0][p].k_residual_slots for p in (1, 2)]
+    assert all(s < 0 for row in slots[False] for s in row)
+    assert all(sum(s >= 0 for s in row) == 2 for row in slots[True])
