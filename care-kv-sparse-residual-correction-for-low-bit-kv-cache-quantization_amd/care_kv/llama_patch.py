@@ -61,7 +61,10 @@ class CAREKVLlamaAttention(nn.Module):
     def _cache_for(self, batch: int, device) -> CAREKVCache:
         st = self._shared
         if st.cache is None or st.cache.n_seq < batch or st.cache.device != torch.device(device):
-            st.cache = CAREKVCache(self.cfg, device=device, n_seq=batch)
+            # CAREKV_STREAMING_STORE=1: the opt-in streaming fill store (no
+            # reference counterpart; CAREKVCache(streaming_store=True))
+            st.cache = CAREKVCache(self.cfg, device=device, n_seq=batch,
+                                   streaming_store=os.environ.get("CAREKV_STREAMING_STORE", "0") == "1")
             st.prefilled.clear()
         return st.cache
 
