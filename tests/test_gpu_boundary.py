@@ -186,6 +186,30 @@ def test_patched_llama_generates_with_cache(monkeypatch):
     assert all(lay.keys.shape[-1] == 1 for lay in getattr(hf, "layers", []))
 
 
+def test_patched_llama_streaming_store(monkeypatch):
+    """CAREKV_STREAMING_STORE=1: pages filled during generate get residual
+    slots (the reference's fill store leaves them none)."""
+    import care_kv
+    monkeypatch.setenv("CAREKV_PREFILL_MODE", "base_quant")
+    monkeypatch.setenv("CAREKV_STREAMING_STORE", "1")
+    monkeypatch.setenv("CAREKV_STORE_POLICY", "residual_kind_aware")
+    print("patched llama generate, streaming store", flush=True)
+    ids = torch.randint(0, 1000, (2, 37), generator=torch.Generator().manual_seed(4)).cuda()
+    m = _tiny_llama(2)
+    cfg = _cfg(L=2, Hq=4, Hkv=2, D=64, P=16, store_budget_mode="absolute", store_abs_k=2, store_abs_v=4)
+    care_kv.patch_llama_model(m, cfg)
+    with torch.no_grad():
+        out = m.generate(ids, max_new_tokens=30, do_sample=False, use_cache=True)
+    assert out.shape == (2, 67)
+    attn = [mod for mod in m.modules() if isinstance(mod, care_kv.CAREKVLlamaAttention)]
+    cache = attn[0]._shared.cache
+    assert cache.streaming_store
+    # tokens 37..63 filled pages 2 and 3 during decode: both hold K slots now
+    ks = cache.k_slot[0, 0, 0].cpu().numpy()
+    assert (ks[2] >= 0).sum() == 2 and (ks[3] >= 0).sum() == 2
+    care_kv.reset_all_caches(m)
+
+
 def test_adapter_patches_a_given_model(monkeypatch):
     import care_kv
     import care_kv.layer
