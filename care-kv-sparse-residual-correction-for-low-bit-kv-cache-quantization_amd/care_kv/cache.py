@@ -134,7 +134,7 @@ class CAREKVCache:
 
     def __init__(self, cfg: CacheConfig, device=None, n_seq: int = 1, n_slots: Optional[int] = None,
                  streaming_store: bool = False):
-        """``streaming_store`` (no reference counterpart, packed bases): keep
+        """``streaming_store`` (no reference counterpart): keep
         each open page's true fp16 rows and, when decode appends fill the
         page, store its residuals against the page's own base instead of
         the reference's zero-residual fill store (layer.py:1128-1146), so
@@ -174,8 +174,6 @@ class CAREKVCache:
         self.v_sq = torch.zeros(*shp, dtype=torch.float32, device=dev)
         self.streaming_store = bool(streaming_store)
         if self.streaming_store:
-            if self.hat:
-                raise NotImplementedError("the streaming store is built for the packed bases")
             # true rows of every (layer, seq, kv head)'s open page
             self.open_k = torch.zeros(L, n_seq, H, T, D, dtype=F16, device=dev)
             self.open_v = torch.zeros_like(self.open_k)
@@ -406,7 +404,12 @@ class CAREKVCache:
         sp = _lib.StoreParams(k_budget=knobs.k_budget, v_budget=knobs.v_budget, joint_budget=knobs.joint_budget,
                               joint=int(knobs.joint), store_none=int(knobs.store_none),
                               sensitivity=knobs.sensitivity, sink_tokens=4,
-                              sketch_proj=self.sketch_proj.data_ptr(), keep_base=1)
+                              sketch_proj=self.sketch_proj.data_ptr(), keep_base=0 if self.hat else 1)
+        if self.hat:  # the fp16 base: the pages' own K_hat / V_hat rows as the residual base
+            pi = torch.tensor([f[2] for f in filled], device=self.device)
+            Khat = self.kcodes[layer, hi, si, pi].view(F16).contiguous().view(-1, cfg.head_dim)
+            Vhat = self.vcodes[layer, hi, si, pi].view(F16).contiguous().view(-1, cfg.head_dim)
+            sp.k_hat, sp.v_hat = Khat.data_ptr(), Vhat.data_ptr()
         lib = _lib.load()
         ws = self.workspace("store", int(lib.carekv_store_workspace_bytes(len(jobs))))
         jobs_d = torch.from_numpy(jobs).to(self.device)

@@ -179,6 +179,8 @@ def write_pages_for_kv_head(cache: OCache, layer_id: int, kv_h: int, K_kv, V_kv,
                          token_start=token_start_abs + t0, num_valid=nv, is_recent=p >= num_pages - 4,
                          is_sink=(token_start_abs + t0) < sink_tokens, K_hat_override=Khp, V_hat_override=Vhp,
                          P=P, **store_kw)
+            if nv < ps:  # the open page's true rows, for a streaming fill store
+                cache.open_rows[(layer_id, kv_h, pid)] = (Kp.copy(), Vp.copy())
         return Kh_seq, Vh_seq
     k_hat, v_hat = [], []
     for p in range(num_pages):
@@ -211,11 +213,11 @@ def decode_append(cache: OCache, layer_id: int, k_rows, v_rows, streaming: bool 
     store with K_orig = K_hat (zero residual, so the page gets metadata with no
     slots and a refilled partial prefill page loses its slots).
 
-    ``streaming=True`` (no reference counterpart; packed bases): the open
+    ``streaming=True`` (no reference counterpart): the open
     page's true rows are kept (``cache.open_rows``, the prompt's partial last
     page included) and the fill store runs process_page on them against the
-    page's own codes and read-back scales, so decode-filled pages get
-    residual slots."""
+    page's own codes and read-back scales (the page's K_hat / V_hat rows for
+    the side-buffer base), so decode-filled pages get residual slots."""
     cfg = cache.cfg
     k_rows = np.asarray(k_rows)
     v_rows = np.asarray(v_rows)
@@ -242,7 +244,8 @@ def decode_append(cache: OCache, layer_id: int, k_rows, v_rows, streaming: bool 
                 Kh = cache.base_K_hat_fp16[layer_id, h, pid].astype(k_rows.dtype)
                 Vh = cache.base_V_hat_fp16[layer_id, h, pid].astype(v_rows.dtype)
                 ts = pos_abs + 1 - ps
-                process_page(cache, layer_id, h, pid, Kh, Vh, None, None, None, None, token_start=ts,
+                Ko, Vo = cache.open_rows.pop((layer_id, h, pid)) if streaming else (Kh, Vh)
+                process_page(cache, layer_id, h, pid, Ko, Vo, None, None, None, None, token_start=ts,
                              num_valid=ps, is_recent=True, is_sink=ts < 4, K_hat_override=Kh,
                              V_hat_override=Vh, **store_kw)
             continue

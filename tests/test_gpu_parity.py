@@ -479,8 +479,8 @@ def test_batched_sequences_match_single(paper_env):
     assert torch.count_nonzero(both[4]) == 0  # nothing to attend to: zeros, as an empty softmax sum gives
 
 
-@pytest.mark.parametrize("D,bits", [(64, 3), (128, 2)])
-def test_streaming_store_matches_oracle(paper_env, D, bits):
+@pytest.mark.parametrize("D,bits,base", [(64, 3, "uniform"), (128, 2, "uniform"), (64, 2, "kivi_style")])
+def test_streaming_store_matches_oracle(paper_env, D, bits, base):
     """streaming_store (no reference counterpart): decode appends fill the
     prompt's partial page and three decode-opened pages, each fill stored
     from the true rows against the page's own base -- slot ids, residual
@@ -489,7 +489,7 @@ def test_streaming_store_matches_oracle(paper_env, D, bits):
     import care_kv
     paper_env.setenv("CAREKV_K_CORRECTION_MODE", "exact")
     Hq, Hkv, T, n_app = 8, 2, 100, 60
-    print(f"streaming store D={D} bits={bits}", flush=True)
+    print(f"streaming store D={D} bits={bits} base={base}", flush=True)
     rng = np.random.default_rng(D + bits)
     K = rng.standard_normal((Hkv, T + n_app, D)).astype(F16)
     V = rng.standard_normal((Hkv, T + n_app, D)).astype(F16)
@@ -498,7 +498,8 @@ def test_streaming_store_matches_oracle(paper_env, D, bits):
     common = dict(num_layers=1, num_heads=Hq, num_kv_heads=Hkv, head_dim=D, page_size=16,
                   max_pages=(T + n_app) // 16 + 4, base_bits=bits, group_size=32, k_channel_group=32,
                   v_token_block=4, sketch_dim=32, read_budget_mode="absolute", read_abs_k=6, read_abs_v=6,
-                  route_policy="joint", store_budget_mode="absolute", store_abs_k=2, store_abs_v=4)
+                  route_policy="joint", store_budget_mode="absolute", store_abs_k=2, store_abs_v=4,
+                  base_quantizer=base)
     oc = OCache(OCfg(**common))
     for h in range(Hkv):
         write_pages_for_kv_head(oc, 0, h, K[h, :T], V[h, :T])
@@ -524,8 +525,11 @@ def test_streaming_store_matches_oracle(paper_env, D, bits):
             assert m is not None, (h, p)
             assert cache.k_slot[0, h, 0, p].tolist() == list(m.k_residual_slots), (h, p)
             assert cache.v_slot[0, h, 0, p].tolist() == list(m.v_residual_slots), (h, p)
-    # decode-filled pages hold slots now (the reference's fill store leaves none)
-    assert any(s >= 0 for s in oc.meta_table[0][0][P - 2].k_residual_slots)
+    # decode-filled pages hold slots now (the reference's fill store leaves
+    # none); with the KIVI base a decode row is quantised alone, per channel
+    # over one row, which is lossless for K (layer.py:1037-1075): no K slots
+    if base == "uniform":
+        assert any(s >= 0 for s in oc.meta_table[0][0][P - 2].k_residual_slots)
     out = care_kv.decode_attention(cache, 0, torch.from_numpy(Qh).cuda().unsqueeze(0))[0].cpu().numpy()
     ref = oracle_decode(oc, 0, Qh, k_mode="exact", kind="both", k_corr_scale=0.1, score_normalize=True,
                         kscore_live=True)
