@@ -315,11 +315,13 @@ void decode_apply_kernel(carekv_arena A, DecodeArgs a) {
 // out = half(O_base + correction): O_base from the split partials of the
 // streaming pass, the correction from the chunk partials of the apply pass
 // (both summed in a fixed order).
-__global__ __launch_bounds__(256) void decode_combine_kernel(int Hkv, int D, DecodeArgs a) {
+__global__ __launch_bounds__(64) void decode_combine_kernel(int Hkv, int D, DecodeArgs a) {
   const int kvh = blockIdx.x, b = blockIdx.y;
   const int GQ = a.GQ;
   const int bk = b * Hkv + kvh;
-  for (int idx = threadIdx.x; idx < GQ * D; idx += 256) {
+  // one thread per output element: a wave of 64 per block, blockIdx.z over
+  // the (query, dim) elements of the pair
+  for (int idx = blockIdx.z * 64 + threadIdx.x; idx < GQ * D; idx += 64 * gridDim.z) {
     const int qq = idx / D, d = idx % D;
     long orow = (long)b * a.Hq + kvh * GQ + qq;
     if (a.pf) {  // prefill rows: the column's (row, head); padding columns write nothing
@@ -378,7 +380,8 @@ int launch_decode_apply(const carekv_arena& A, const DecodeArgs& a, hipStream_t 
 }
 
 int launch_decode_combine(const carekv_arena& A, const DecodeArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(decode_combine_kernel, dim3(A.n_kv_heads, a.B), dim3(256), 0, s, A.n_kv_heads, A.head_dim, a);
+  hipLaunchKernelGGL(decode_combine_kernel, dim3(A.n_kv_heads, a.B, (a.GQ * A.head_dim + 63) / 64), dim3(64), 0, s,
+                     A.n_kv_heads, A.head_dim, a);
   CAREKV_CHECK_LAUNCH("decode_combine");
   return CAREKV_OK;
 }
