@@ -501,3 +501,26 @@ def test_streaming_fill_store_gives_decode_pages_slots():
         slots[streaming] = [c.meta_table[0][0][p].k_residual_slots for p in (1, 2)]
     assert all(s < 0 for row in slots[False] for s in row)
     assert all(sum(s >= 0 for s in row) == 2 for row in slots[True])
+
+
+def test_prefill_stored_read_zero_is_base(golden):
+    """READ = 0 in carekv_stored mode is the base_quant output bit for bit
+    (layer.py:810-823), and the causal base of the first rows does not see
+    the later tokens: truncating the prompt leaves those rows unchanged up
+    to fp32 summation order.  (The correction of a row
+    does depend on later pages: their candidates count in the normalisation
+    and the budgets.)"""
+    g = golden("prefill_gqa8_d64.npz")
+    c, spec, Kh, Vh = build_oracle_prefill(g, "gqa8_d64")
+    c.cfg.read_abs_k = c.cfg.read_abs_v = 0
+    Qh = g["Q"].transpose(1, 0, 2)
+    corr = prefill_stored(c, 0, Qh, Kh, Vh, k_mode="exact", kind="both", k_corr_scale=0.1, score_normalize=True,
+                          kscore_live=True)
+    base = prefill_stored(c, 0, Qh, Kh, Vh, correction=False)
+    assert np.array_equal(corr.view(np.uint16), base.view(np.uint16))
+    T = Qh.shape[1]
+    short = prefill_stored(c, 0, Qh[:, :T // 2], Kh[:, :T // 2], Vh[:, :T // 2], correction=False)
+    ref = base[:T // 2]
+    err = np.abs(short.astype(F32) - ref.astype(F32))
+    # (where the sum cancels, a few small outputs move up to 2.4e-4)
+    assert np.all(err <= np.maximum(np.spacing(np.maximum(np.abs(ref), np.abs(short))).astype(F32), 2.5e-4))
