@@ -151,59 +151,49 @@ def load_traffic(kernel, workload):
 
 def oracle_slice_from_device(cache, seq, kvh, spec):
     """Copy one (sequence, kv head) of the device cache into the CPU oracle."""
-    import numpy as np
-    from oracle.cache import OCache, OCfg, OMeta
-    cfg = cache.cfg
-    P = cache.num_pages(0, kvh, seq)
-    kivi = bool(spec.get("kivi"))
-    ocfg = OCfg(num_layers=1, num_heads=spec["Hq"] // spec["Hkv"], num_kv_heads=1, head_dim=cfg.head_dim,
-                page_size=16, max_pages=P, base_bits=cfg.base_bits, group_size=32, k_channel_group=32,
-                v_token_block=4, sketch_dim=cfg.sketch_dim, read_budget_mode="absolute", read_abs_k=spec["rk"],
-                read_abs_v=spec["rv"], route_policy="joint", store_budget_mode="ratio", store_budget_ratio=0.03,
-                base_quantizer="kivi_style" if kivi else "uniform")
-    oc = OCache(ocfg, max_slots=cache.n_slots)
-    g = lambda t: t[0, kvh, seq, :P].cpu().numpy()  # noqa: E731
-    if kivi:  # fp16 rows of the side buffer
-        oc.base_K_hat_fp16[0, 0] = g(cache.kcodes).view(np.float16)
-        oc.base_V_hat_fp16[0, 0] = g(cache.vcodes).view(np.float16)
-    else:
-        oc.base_K_codes[0, 0] = g(cache.kcodes)
-        oc.base_V_codes[0, 0] = g(cache.vcodes)
-        oc.base_K_scale[0, 0] = g(cache.kscale)
-        oc.base_V_scale[0, 0] = g(cache.vscale)
-        oc.base_K_scale_master[0, 0] = g(cache.kmaster)
-        oc.base_V_scale_master[0, 0] = g(cache.vmaster)
-    oc.valid_tokens[0, 0] = g(cache.valid)
-    oc.k_residual_buf[:] = cache.k_res[seq].cpu().numpy()
-    oc.v_residual_buf[:] = cache.v_res[seq].cpu().numpy()
-    oc.k_residual_scale[:, 0] = cache.k_res_scale[seq].cpu().numpy()
-    oc.v_residual_scale[:, 0] = cache.v_res_scale[seq].cpu().numpy()
-    hm, ks, vs, ke, ve, sk = (g(cache.has_meta), g(cache.k_slot), g(cache.v_slot), g(cache.k_err),
-                              g(cache.v_err), g(cache.k_sketch))
-    for p in range(P):
-        if hm[p]:
-            oc.meta_table[0][0][p] = OMeta(page_id=p, layer_id=0, kv_head=0, token_start=p * 16,
-                                           num_tokens=int(oc.valid_tokens[0, 0, p]),
-                                           k_residual_slots=ks[p].tolist(), v_residual_slots=vs[p].tolist(),
-                                           k_error_norm=ke[p], v_error_norm=ve[p], k_sketch=sk[p])
-    oc.next_page[0][0] = P
-    return oc
+    from oracle.check import oracle_slice_from_device as copy_slice
+    return copy_slice(cache, seq, kvh, num_heads=spec["Hq"] // spec["Hkv"], read_budget_mode="absolute",
+                      read_abs_k=spec["rk"], read_abs_v=spec["rv"], route_policy="joint",
+                      store_budget_mode="ratio", store_budget_ratio=0.03)
 
 
-def cpu_baseline(cache, spec, q_np, slices):
+def slice_ids(spec, slices):
+    """(sequence, kv head) pairs of the sampled slices, spread over both."""
+    B, Hkv = spec["B"], spec["Hkv"]
+    out, seen = [], set()
+    for i in range(slices * 4):
+        sk = ((i * 37) % B, (i * 5 + i // B) % Hkv)
+        if sk not in seen:
+            seen.add(sk)
+            out.append(sk)
+        if len(out) == slices:
+            break
+    return out
+
+
+def cpu_baseline(cache, spec, q_np, slices, out_np=None, diag_np=None):
     """Time the oracle (numpy restatement of the reference decode path:
     read_base_concat + dequantize + base attention + vectorized joint
     correction) on `slices` (sequence, kv head) slices; extrapolate to the
-    whole batch."""
+    whole batch.
+
+    With the GPU's output and diag rows, also check them against the
+    oracle on the same slices (outside the timed region): selections equal
+    up to epsilon ties of the normalised scores (1e-4 relative), and the
+    output within max-abs 2e-3 (or one fp16 ulp where larger) of the oracle
+    recomputed under the GPU's selection where a tie was crossed."""
     import numpy as np
     from oracle import quant as Q
     from oracle.attention import base_attention, vectorized_joint_correction
+    from oracle.check import compare_selection, forced_selection, oracle_candidates, output_errors
     grp = spec["Hq"] // spec["Hkv"]
     total = 0.0
-    for i in range(slices):
-        seq, kvh = i % spec["B"], (i // spec["B"]) % spec["Hkv"]
+    par = dict(slices=0, rows=0, sel_exact=0, sel_tie=0, sel_bad=0, max_abs=0.0, rel_l2=0.0, bar_ratio=0.0)
+    for seq, kvh in slice_ids(spec, slices):
         oc = oracle_slice_from_device(cache, seq, kvh, spec)
         Qg = q_np[seq, kvh * grp:(kvh + 1) * grp]
+        kw = dict(kind="both", k_corr_scale=0.1, score_normalize=True, kscore_live=True, k_mode="exact")
+        d = {}
         t0 = time.perf_counter()
         pids = oc.all_page_ids(0, 0)
         if spec.get("kivi"):  # attention.py:997-1008: the fp16 side buffer, no dequantisation
@@ -214,12 +204,36 @@ def cpu_baseline(cache, spec, q_np, slices):
             Kh = Q.dequantize(Kc, Ks, 32).astype(np.float32)
             Vh = Q.dequantize(Vc, Vs, 32).astype(np.float32)
         S, A, O = base_attention(Kh, Vh, Qg.astype(np.float32))
-        d = vectorized_joint_correction(oc, 0, 0, pids, Qg, S, A, Vh, O, kind="both", k_corr_scale=0.1,
-                                        score_normalize=True, kscore_live=True, k_mode="exact")
-        _ = (O + d).astype(np.float16)
+        dlt = vectorized_joint_correction(oc, 0, 0, pids, Qg, S, A, Vh, O, diag=d, **kw)
+        ref = (O + dlt).astype(np.float16)
         total += time.perf_counter() - t0
-    per_slice = total / slices
-    return per_slice * spec["B"] * spec["Hkv"] * 1e6, per_slice
+        par["slices"] += 1
+        if out_np is None or diag_np is None:
+            continue
+        Kcand, Vcand = oracle_candidates(oc, 0, 0, len(pids))
+        rows = diag_np[seq, kvh * grp:(kvh + 1) * grp]
+        ex, tie, bad = compare_selection(rows, d, Kcand, Vcand, eps=1e-4)
+        par["rows"] += ex + tie + bad
+        par["sel_exact"] += ex
+        par["sel_tie"] += tie
+        par["sel_bad"] += bad
+        if tie:  # the oracle's output under the GPU's selection
+            dlt = vectorized_joint_correction(oc, 0, 0, pids, Qg, S, A, Vh, O,
+                                              force_sel=forced_selection(rows, Kcand, Vcand), **kw)
+            ref = (O + dlt).astype(np.float16)
+        mx, rel, ratio = output_errors(out_np[seq, kvh * grp:(kvh + 1) * grp], ref)
+        par["max_abs"] = max(par["max_abs"], mx)
+        par["rel_l2"] = max(par["rel_l2"], rel)
+        par["bar_ratio"] = max(par["bar_ratio"], ratio)
+    per_slice = total / max(par["slices"], 1)
+    if out_np is not None:
+        par["pass"] = bool(par["slices"] > 0 and par["sel_bad"] == 0 and par["bar_ratio"] <= 1.0
+                           and par["rel_l2"] <= 1e-2)
+        par["bar"] = ("selections equal up to epsilon ties (1e-4 relative); out within max-abs 2e-3 "
+                      "(or 1 fp16 ulp) and rel-L2 1e-2 of the oracle under the GPU's selection")
+        for k in ("max_abs", "rel_l2", "bar_ratio"):
+            par[k] = float(f"{par[k]:.3g}")
+    return per_slice * spec["B"] * spec["Hkv"] * 1e6, per_slice, par
 
 
 def prefill_bench(args):
@@ -542,6 +556,7 @@ def main():
     out, diag = care_kv.decode_attention(cache, 0, q, diag_cap=512, split_pages=args.split_pages)
     torch.cuda.synchronize()
     diag_np = diag.cpu().numpy()
+    out_first = out.clone()
     stream_bytes, nbytes, k_slots, v_union = algorithmic_bytes(spec, cfg, cache, diag_np)
     corr = not args.no_correction
     for _ in range(args.warmup):
@@ -579,10 +594,19 @@ def main():
         f"K slots {k_slots}, V union {v_union}")
     log("[bench] phases (us): " + ", ".join(f"{n} {t:.1f}" for n, t in zip(names, phase)) +
         f"; streaming kernel {stream_bytes / 1e9:.3f} GB -> {stream_gbps:.0f} GB/s")
+    # the timed steps recompute the same output: it must not change
+    deterministic = bool(torch.equal(out, out_first)) if corr else None
     cpu = None
+    parity = None
     if not args.no_cpu_baseline:
         q_np = q.cpu().numpy()
-        cpu_us, per_slice = cpu_baseline(cache, spec, q_np, args.cpu_slices)
+        cpu_us, per_slice, parity = cpu_baseline(cache, spec, q_np, args.cpu_slices,
+                                                 out_np=out_first.cpu().numpy() if corr else None,
+                                                 diag_np=diag_np)
+        if corr:
+            parity["deterministic"] = deterministic
+            parity["pass"] = bool(parity["pass"] and deterministic)
+            log(f"[bench] parity vs oracle on {parity['slices']} slices: {parity}")
         try:
             import threadpoolctl
             info = threadpoolctl.threadpool_info()
@@ -621,8 +645,12 @@ def main():
                      "algorithmic_bytes_per_launch": int(stream_bytes), "launch_us": round(phase[0], 2),
                      "step_frac": round(gbps / 8000.0, 4), "step_algorithmic_bytes": int(nbytes)},
         "cpu_baseline": cpu,
+        "parity": parity,
     }
     print(json.dumps(line), flush=True)
+    if parity is not None and corr and not parity["pass"]:
+        log("[bench] PARITY FAILED: the GPU output or selections differ from the oracle beyond the bar")
+        sys.exit(3)
 
 
 if __name__ == "__main__":

@@ -277,7 +277,7 @@ def golden_decode_proxy(ck):
 
 
 def _prefill_case(ck, name, *, Hq, Hkv, D, T, seed, outlier_mult, store, read_k, read_v, k_mode="exact",
-                  policy="joint", base_bits=3):
+                  policy="joint", base_bits=3, impl="vectorized", kscore_live=1):
     """CAREKVLayer.prefill in carekv_stored mode (layer.py:643-840) with the
     vectorized correction over all kv_group x T queries of a kv head
     (layer.py:538-557): the causal base attention over the prefill's own
@@ -285,8 +285,8 @@ def _prefill_case(ck, name, *, Hq, Hkv, D, T, seed, outlier_mult, store, read_k,
     weights.  Also the base_quant output of the same prompt (fresh cache)."""
     from CARE_KV.care_kv.attention import set_chunk_recorder
     env = dict(CAREKV_STORE_POLICY="residual_kind_aware", CAREKV_PREFILL_RESIDUAL_KIND="both",
-               CAREKV_K_CORRECTION_MODE=k_mode, CAREKV_KSCORE_LIVE="1", CAREKV_SCORE_NORMALIZE="1",
-               CAREKV_DEBUG_STATS="0", CAREKV_CORRECTION_IMPL="vectorized")
+               CAREKV_K_CORRECTION_MODE=k_mode, CAREKV_KSCORE_LIVE=str(kscore_live), CAREKV_SCORE_NORMALIZE="1",
+               CAREKV_DEBUG_STATS="0", CAREKV_CORRECTION_IMPL=impl)
     _set_env(**env)
     K, V = _gen_kv(seed, Hkv, T, D, outlier_mult=outlier_mult)
     qg = torch.Generator().manual_seed(seed + 200)
@@ -299,7 +299,7 @@ def _prefill_case(ck, name, *, Hq, Hkv, D, T, seed, outlier_mult, store, read_k,
                              max_pages=T // 16 + 4, base_bits=base_bits, group_size=32, k_channel_group=32,
                              v_token_block=4, sketch_dim=32, packed_base=True, scale_quant="int8",
                              read_budget_ratio=0.0, read_budget_mode="absolute", read_abs_k=read_k,
-                             read_abs_v=read_v, route_policy=policy, correction_impl="vectorized", **store)
+                             read_abs_v=read_v, route_policy=policy, correction_impl=impl, **store)
         cache = ck.CAREKVCache(cfg, torch.device("cpu"))
         layer = _selector_layer(ck, cfg)
         rec = []
@@ -321,7 +321,7 @@ def _prefill_case(ck, name, *, Hq, Hkv, D, T, seed, outlier_mult, store, read_k,
     d.update({k: v for k, v in out.items() if k.startswith("h")})
     d.update(K=K.numpy(), V=V.numpy(), Q=Q.numpy(), O=out["carekv_stored"], O_base=out["base_quant"],
              T=np.array(T), n_append=np.array(0), read_k=np.array(read_k), read_v=np.array(read_v))
-    _set_env(CAREKV_PREFILL_MODE="fp", CAREKV_CORRECTION_IMPL="cached")
+    _set_env(CAREKV_PREFILL_MODE="fp", CAREKV_CORRECTION_IMPL="cached", CAREKV_KSCORE_LIVE="1")
     np.savez_compressed(os.path.join(HERE, f"prefill_{name}.npz"), **d)
 
 
@@ -337,6 +337,64 @@ def golden_prefill(ck):
     # MHA, linear K mode
     _prefill_case(ck, "mha_d128_linear", Hq=2, Hkv=2, D=128, T=120, seed=23, outlier_mult=6.0, store=ratio3,
                   read_k=3, read_v=3, k_mode="linear")
+
+
+def golden_prefill_cached(ck):
+    """CAREKVLayer.prefill in carekv_stored mode with correction_impl="cached"
+    (the CAREKVAdapter default): the per-(head, row) apply_slot_corrections
+    loop over ResidualRouter.route (layer.py:573-640, attention.py:208-374,
+    residual_router.py:88-452).  The router has no query-aware K score, so
+    CAREKV_KSCORE_LIVE=1 must give the same output as 0 (the second case)."""
+    ratio3 = dict(store_budget_mode="ratio", store_budget_ratio=0.03)
+    _prefill_case(ck, "cached_gqa4_d64", Hq=8, Hkv=2, D=64, T=100, seed=31, outlier_mult=8.0,
+                  store=dict(store_budget_mode="absolute", store_abs_k=2, store_abs_v=4), read_k=4, read_v=4,
+                  k_mode="exact", policy="joint", impl="cached", kscore_live=0)
+    _prefill_case(ck, "cached_mha_d128_linear", Hq=2, Hkv=2, D=128, T=90, seed=32, outlier_mult=6.0, store=ratio3,
+                  read_k=3, read_v=3, k_mode="linear", policy="separate", impl="cached", kscore_live=1)
+
+
+def _decode_step_case(ck, name, *, Hq, Hkv, D, T, n_append, seed, outlier_mult, store, read_k, read_v, k_mode,
+                      policy):
+    """The reference's decode_step with its correction gate open
+    (read_budget_ratio > 0, attention.py:1025): every step appends the token
+    (store on page fill with K_orig = K_hat) and runs CAREKVMultiHeadAttention
+    with apply_slot_corrections over ResidualRouter.route (the sketch-proxy
+    selector; the router reads no CAREKV_KSCORE_LIVE) under the absolute
+    read budgets.  Every step's output is kept."""
+    _set_env(CAREKV_STORE_POLICY="residual_kind_aware", CAREKV_PREFILL_RESIDUAL_KIND="both",
+             CAREKV_K_CORRECTION_MODE=k_mode, CAREKV_KSCORE_LIVE="1", CAREKV_SCORE_NORMALIZE="1",
+             CAREKV_K_CORRECTION_SCALE="0.1", CAREKV_DEBUG_STATS="0")
+    cfg = ck.CacheConfig(num_layers=1, num_heads=Hq, num_kv_heads=Hkv, head_dim=D, page_size=16,
+                         max_pages=T // 16 + n_append // 16 + 4, base_bits=3, group_size=32, k_channel_group=32,
+                         v_token_block=4, sketch_dim=32, packed_base=True, scale_quant="int8",
+                         read_budget_ratio=0.03, read_budget_mode="absolute", read_abs_k=read_k,
+                         read_abs_v=read_v, route_policy=policy, **store)
+    cache = ck.CAREKVCache(cfg, torch.device("cpu"))
+    layer = _selector_layer(ck, cfg)
+    K, V = _gen_kv(seed, Hkv, T + n_append, D, outlier_mult=outlier_mult)
+    Qall = torch.randn(n_append, Hq, D, generator=torch.Generator().manual_seed(seed + 300)).half()
+    for h in range(Hkv):
+        layer._write_pages_for_kv_head(cache, h, K[h, :T], V[h, :T], token_start_abs=0, sink_tokens=4)
+    outs = []
+    for i, t in enumerate(range(T, T + n_append)):
+        hidden = torch.cat([Qall[i].reshape(-1), K[:, t].reshape(-1), V[:, t].reshape(-1)])[None]
+        outs.append(layer.decode_step(cache, hidden)[0, :Hq * D].reshape(Hq, D))
+    d = _cache_arrays(cache)
+    d.update(K=K.numpy(), V=V.numpy(), Qall=Qall.numpy(), outs=torch.stack(outs).numpy(), T=np.array(T),
+             n_append=np.array(n_append), read_k=np.array(read_k), read_v=np.array(read_v))
+    np.savez_compressed(os.path.join(HERE, f"decode_step_{name}.npz"), **d)
+
+
+def golden_decode_step(ck):
+    # GQA 4, D=128: the prompt's partial page fills and a decode-opened page
+    # follows (zero master); joint read of 6 + 6 slots, exact K correction
+    _decode_step_case(ck, "gqa4_d128", Hq=8, Hkv=2, D=128, T=250, n_append=24, seed=41, outlier_mult=10.0,
+                      store=dict(store_budget_mode="absolute", store_abs_k=2, store_abs_v=4), read_k=6,
+                      read_v=6, k_mode="exact", policy="joint")
+    # GQA 8, D=64 (TinyLlama heads), separate policy, linear K correction
+    _decode_step_case(ck, "gqa8_d64_linear", Hq=16, Hkv=2, D=64, T=120, n_append=12, seed=42, outlier_mult=8.0,
+                      store=dict(store_budget_mode="ratio", store_budget_ratio=0.03), read_k=5, read_v=5,
+                      k_mode="linear", policy="separate")
 
 
 ROUTE_VARIANTS = [  # (route_policy, adaptive_score (rel, abs, min_keep) or None)
@@ -371,14 +429,10 @@ def golden_route(ck):
     sf = 1.0 / math.sqrt(D)
     for h in range(Hkv):
         pids = cache.all_page_ids(0, h)
-        if base_quantizer == "uniform":
-            Kc, Ks, Vc, Vs, _ = cache.read_base_concat(0, h, pids)
-            N = Kc.shape[0]
-            Kb = ck.dequantize(Kc, Ks, (N, D), layer.base_qcfg).float()
-            Vb = ck.dequantize(Vc, Vs, (N, D), layer.base_qcfg).float()
-        else:  # the fp16 side buffer (attention.py:997-1008)
-            Kh, Vh, _ = cache.read_base_hat_concat(0, h, pids)
-            Kb, Vb = Kh.float(), Vh.float()
+        Kc, Ks, Vc, Vs, _ = cache.read_base_concat(0, h, pids)  # the uniform base
+        N = Kc.shape[0]
+        Kb = ck.dequantize(Kc, Ks, (N, D), layer.base_qcfg).float()
+        Vb = ck.dequantize(Vc, Vs, (N, D), layer.base_qcfg).float()
         heads = list(range(h * grp, (h + 1) * grp))
         S = torch.stack([(Kb @ Qh[i].float()) * sf for i in heads])
         A = torch.softmax(S, dim=1)
@@ -501,7 +555,7 @@ def golden_activation_slices():
 
 
 PARTS = ("activations", "sketch", "store", "append", "decode", "decode_proxy", "decode_kivi", "prefill", "route",
-         "fixture")
+         "fixture", "prefill_cached", "decode_step")
 
 if __name__ == "__main__":
     # CAREKV_GOLDEN_PARTS=decode_proxy,... writes only those fixtures
@@ -515,8 +569,8 @@ if __name__ == "__main__":
         ck = _import_reference()
         fns = dict(sketch=golden_sketch, store=golden_store, append=golden_append, decode=golden_decode,
                    decode_proxy=golden_decode_proxy, decode_kivi=golden_decode_kivi, prefill=golden_prefill,
-                   route=golden_route,
-                   fixture=golden_reference_fixture)
+                   route=golden_route, fixture=golden_reference_fixture,
+                   prefill_cached=golden_prefill_cached, decode_step=golden_decode_step)
         for p in parts:
             if p in fns:
                 fns[p](ck)

@@ -9,6 +9,8 @@ import numpy as np
 from oracle import quant as Q
 from oracle.attention import decode_attention as oracle_decode
 from oracle.cache import OCache, OCfg
+from oracle.check import (compare_selection, decode_diag, oracle_candidates, oracle_selection,  # noqa: F401
+                          output_errors, ties_explain)
 from oracle.store import decode_append, write_pages_for_kv_head
 
 F16, F32 = np.float16, np.float32
@@ -96,64 +98,3 @@ def build_oracle_case(g, name):
     for t in range(T, T + n_app):
         decode_append(c, 0, g["K"][:, t], g["V"][:, t])
     return c, spec
-
-
-def oracle_candidates(oc, layer, h, n_pages):
-    """Candidate ids (kind, page, sub) in the reference's index order."""
-    cfg = oc.cfg
-    K, V = [], []
-    for p in range(n_pages):
-        m = oc.meta_table[layer][h][p]
-        nv = int(oc.valid_tokens[layer, h, p])
-        if nv == 0 or m is None:
-            continue
-        for cg, s in enumerate(m.k_residual_slots):
-            if s >= 0:
-                K.append((0, p, cg))
-        for vb, s in enumerate(m.v_residual_slots):
-            if s >= 0 and vb * cfg.v_token_block < nv:
-                V.append((1, p, vb))
-    return K, V
-
-
-def decode_diag(code_row):
-    out = []
-    for x in code_row:
-        x = int(x)
-        if x < 0:
-            break
-        out.append((x >> 30, (x >> 3) & ((1 << 27) - 1), x & 7))
-    return out
-
-
-def oracle_selection(diag_h, Kc, Vc):
-    """Per query row: set of selected candidate ids from the oracle diag."""
-    rows = []
-    sk, sv = diag_h["sel_k"], diag_h["sel_v"]
-    for j in range(sk.shape[0] if sk is not None else sv.shape[0]):
-        s = set()
-        if sk is not None:
-            s |= {Kc[i] for i in np.nonzero(sk[j])[0]}
-        if sv is not None:
-            s |= {Vc[i] for i in np.nonzero(sv[j])[0]}
-        rows.append(s)
-    return rows
-
-
-def ties_explain(mine: set, ref: set, diag_h, Kc, Vc, j, eps=1e-4):
-    """True if every disagreement is between candidates whose normalised
-    scores sit within eps (relative) of the selection boundary."""
-    if mine == ref:
-        return True
-    sK, sV = diag_h["score_K_r"], diag_h["score_V_r"]
-    vals = {}
-    if sK is not None:
-        vals.update({c: float(sK[j, i]) for i, c in enumerate(Kc)})
-    if sV is not None:
-        vals.update({c: float(sV[j, i]) for i, c in enumerate(Vc)})
-    ref_vals = sorted((vals[c] for c in ref), reverse=True)
-    kth = ref_vals[-1] if ref_vals else 0.0
-    for c in mine ^ ref:
-        if c not in vals or abs(vals[c] - kth) > eps * max(abs(kth), 1e-30):
-            return False
-    return True

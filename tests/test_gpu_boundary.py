@@ -226,3 +226,45 @@ def test_adapter_patches_a_given_model(monkeypatch):
     assert torch.isfinite(logits.float()).all()
     st = a.collect_debug_stats()
     assert st["stored_k_slots"] > 0 and st["stored_v_slots"] > 0
+
+
+@pytest.mark.parametrize("name", ["gqa4_d128", "gqa4_d128_kivi"])
+def test_layer_decode_step_matches_reference(monkeypatch, name):
+    """CAREKVLayer.decode_step against the reference's own decode_step
+    (layer.py:978-1163) on a decode golden: the prompt's pages, then 27
+    decode steps whose appends fill the prompt's partial page and open two
+    new pages (store on fill with K_orig = K_hat, zero master for the
+    decode-opened page).  Identity projections pick q / k / v out of
+    hidden = [q; k; v] and W_O returns the attention output, so the layer's
+    last output is the reference's decode_step_out (read_budget_ratio = 0:
+    the reference's decode attention is the base path, attention.py:1025)."""
+    import care_kv
+    from helpers import DECODE_CASES, PAPER_ENV, case_cfg_kwargs, load_golden
+    for k, v in PAPER_ENV.items():
+        monkeypatch.setenv(k, v)
+    monkeypatch.setenv("CAREKV_K_CORRECTION_MODE", "exact")
+    print(f"layer decode_step golden {name}", flush=True)
+    g = load_golden(f"decode_{name}.npz")
+    spec = DECODE_CASES[name]
+    cfg = care_kv.CacheConfig(packed_base=True, scale_quant="int8", read_budget_ratio=0.0,
+                              **case_cfg_kwargs(g, spec))
+    T, n_app = int(g["T"]), int(g["n_append"])
+    Hq, Hkv, D = spec["Hq"], spec["Hkv"], spec["D"]
+    nq, nk = Hq * D, Hkv * D
+    eye = torch.eye(nq + 2 * nk, dtype=torch.float16, device="cuda")
+    lay = care_kv.CAREKVLayer(cfg, 0, eye[:nq].contiguous(), eye[nq:nq + nk].contiguous(),
+                              eye[nq + nk:].contiguous(), eye[:, :nq].contiguous())
+    K, V, Qall = (torch.from_numpy(g[n]).cuda() for n in ("K", "V", "Qall"))
+    cache = care_kv.CAREKVCache(cfg, n_seq=1)
+    cache.write_prefill(0, K[:, :T], V[:, :T])
+    out = None
+    for i, t in enumerate(range(T, T + n_app)):
+        hidden = torch.cat([Qall[i].reshape(-1), K[:, t].reshape(-1), V[:, t].reshape(-1)])[None]
+        out = lay.decode_step(cache, hidden)
+    got = out[0, :nq].reshape(Hq, D).float().cpu().numpy()
+    ref = g["decode_step_out"].astype(np.float32)
+    err = np.abs(got - ref)
+    assert np.all(err <= np.maximum(2e-3, np.spacing(np.abs(g["decode_step_out"])).astype(np.float32))), err.max()
+    # the cache after the appends equals the reference's, byte for byte
+    from test_gpu_parity import compare_cache_to_golden
+    compare_cache_to_golden(cache, g)

@@ -524,3 +524,118 @@ def test_prefill_stored_read_zero_is_base(golden):
     err = np.abs(short.astype(F32) - ref.astype(F32))
     # (where the sum cancels, a few small outputs move up to 2.4e-4)
     assert np.all(err <= np.maximum(np.spacing(np.maximum(np.abs(ref), np.abs(short))).astype(F32), 2.5e-4))
+
+
+# ------------------------------------------------------------ the router path (correction_impl=cached, decode_step)
+CACHED_PREFILL_CASES = {
+    "cached_gqa4_d64": dict(Hq=8, Hkv=2, D=64, store=dict(store_budget_mode="absolute", store_abs_k=2,
+                                                           store_abs_v=4), k_mode="exact", policy="joint"),
+    "cached_mha_d128_linear": dict(Hq=2, Hkv=2, D=128, store=dict(store_budget_mode="ratio", store_budget_ratio=0.03),
+                                   k_mode="linear", policy="separate"),
+}
+
+
+def _oracle_prompt(g, spec, T):
+    oc = OCache(OCfg(num_layers=1, num_heads=spec["Hq"], num_kv_heads=spec["Hkv"], head_dim=spec["D"], page_size=16,
+                     max_pages=T // 16 + 4, base_bits=3, group_size=32, k_channel_group=32, v_token_block=4,
+                     sketch_dim=32, read_budget_mode="absolute", read_abs_k=int(g["read_k"]),
+                     read_abs_v=int(g["read_v"]), route_policy=spec["policy"], **spec["store"]))
+    hats = [write_pages_for_kv_head(oc, 0, h, g["K"][h, :T], g["V"][h, :T]) for h in range(spec["Hkv"])]
+    return oc, np.stack([a for a, _ in hats]), np.stack([b for _, b in hats])
+
+
+@pytest.mark.parametrize("name", list(CACHED_PREFILL_CASES))
+def test_prefill_cached_golden(golden, name):
+    """CAREKVLayer.prefill in carekv_stored mode with correction_impl="cached"
+    (per-(head, row) apply_slot_corrections over ResidualRouter.route,
+    layer.py:573-640): the oracle's batched correction with the router's
+    sketch-proxy K score gives the reference output within 1e-3; the
+    query-aware K score does not (the cached path reads no KSCORE_LIVE, and
+    the second golden was written with CAREKV_KSCORE_LIVE=1)."""
+    g = golden(f"prefill_{name}.npz")
+    spec = CACHED_PREFILL_CASES[name]
+    T = int(g["T"])
+    oc, Kh, Vh = _oracle_prompt(g, spec, T)
+    _compare_cache(oc, g)
+    Qh = g["Q"].transpose(1, 0, 2)
+    kw = dict(k_mode=spec["k_mode"], kind="both", k_corr_scale=0.1, score_normalize=True)
+    proxy = prefill_stored(oc, 0, Qh, Kh, Vh, kscore_live=False, **kw)
+    err = np.abs(proxy.astype(F32) - g["O"].astype(F32))
+    assert err.max() <= 1e-3, err.max()
+    live = prefill_stored(oc, 0, Qh, Kh, Vh, kscore_live=True, **kw)
+    assert np.abs(live.astype(F32) - g["O"].astype(F32)).max() > 1e-2
+
+
+@pytest.mark.parametrize("name,Hq,D,k_mode,policy",
+                         [("gqa4_d128", 8, 128, "exact", "joint"), ("gqa8_d64_linear", 16, 64, "linear", "separate")])
+def test_decode_step_corrected_golden(golden, name, Hq, D, k_mode, policy):
+    """The reference's decode_step with its correction gate open
+    (read_budget_ratio > 0, attention.py:1025): apply_slot_corrections over
+    ResidualRouter.route per query head.  The oracle's decode_append (store
+    on fill with K_orig = K_hat, zero master on the decode-opened page) and
+    decode_attention with the sketch-proxy selector give every step's output
+    within the decode bar."""
+    g = golden(f"decode_step_{name}.npz")
+    T, n = int(g["T"]), int(g["n_append"])
+    store = (dict(store_budget_mode="absolute", store_abs_k=2, store_abs_v=4) if name == "gqa4_d128"
+             else dict(store_budget_mode="ratio", store_budget_ratio=0.03))
+    spec = dict(Hq=Hq, Hkv=2, D=D, policy=policy, store=store)
+    oc = OCache(OCfg(num_layers=1, num_heads=Hq, num_kv_heads=2, head_dim=D, page_size=16, max_pages=(T + n) // 16 + 4,
+                     base_bits=3, group_size=32, k_channel_group=32, v_token_block=4, sketch_dim=32,
+                     read_budget_mode="absolute", read_abs_k=int(g["read_k"]), read_abs_v=int(g["read_v"]),
+                     route_policy=policy, **store))
+    for h in range(2):
+        write_pages_for_kv_head(oc, 0, h, g["K"][h, :T], g["V"][h, :T])
+    for i, t in enumerate(range(T, T + n)):
+        decode_append(oc, 0, g["K"][:, t], g["V"][:, t])
+        o = decode_attention(oc, 0, g["Qall"][i], k_mode=k_mode, kind="both", k_corr_scale=0.1,
+                             score_normalize=True, kscore_live=False)
+        ref = g["outs"][i]
+        err = np.abs(o.astype(F32) - ref.astype(F32))
+        assert np.all(err <= np.maximum(2e-3, np.spacing(np.abs(ref)).astype(F32))), (i, err.max())
+    _compare_cache(oc, g)
+    del spec
+
+
+def test_streaming_fill_store_residuals_are_true_minus_base():
+    """decode_append(streaming=True): the K and V residual slots of a page the
+    decode appends fill hold pack_4bit of (true rows - the page's own
+    dequantised rows), K per 32-channel group over the page's 16 rows and V
+    per 4-row block, and its error norms are those residuals' row-norm
+    means."""
+    rng = np.random.default_rng(5)
+    D, T, n = 64, 20, 30
+    K = rng.standard_normal((1, T + n, D)).astype(F16)
+    V = rng.standard_normal((1, T + n, D)).astype(F16)
+    K[:, :, 7] *= F16(6.0)
+    c = OCache(OCfg(num_layers=1, num_heads=2, num_kv_heads=1, head_dim=D, page_size=16, max_pages=8, base_bits=3,
+                    group_size=32, k_channel_group=32, v_token_block=4, sketch_dim=32, store_budget_mode="absolute",
+                    store_abs_k=2, store_abs_v=4))
+    write_pages_for_kv_head(c, 0, 0, K[0, :T], V[0, :T])
+    for t in range(T, T + n):
+        decode_append(c, 0, K[:, t], V[:, t], streaming=True)
+    for p in (1, 2):  # the prompt's partial page refilled by decode, a decode-opened page
+        m = c.meta_table[0][0][p]
+        rows = slice(p * 16, p * 16 + 16)
+        for nm, X, codes, which in (("K", K[0, rows], c.base_K_codes, "K"), ("V", V[0, rows], c.base_V_codes, "V")):
+            Xh = Q.dequantize(c.unpack_rows(codes[0, 0, p]), c.page_scales(0, 0, p, which), 32).astype(F16)
+            R = (X.astype(F16) - Xh).astype(F16).astype(F32)
+            if nm == "K":
+                for cg, slot in enumerate(m.k_residual_slots):
+                    if slot < 0:
+                        continue
+                    blk = R[:, cg * 32:(cg + 1) * 32]
+                    packed, scale = Q.pack_4bit(blk.ravel())
+                    assert np.array_equal(c.k_residual_buf[slot], packed), (p, cg)
+                    assert c.k_residual_scale[slot, 0] == scale, (p, cg)
+                    want = F16(np.mean(np.sqrt((blk.astype(F32) ** 2).sum(1))))
+                    assert abs(float(m.k_error_norm[cg]) - float(want)) <= float(np.spacing(want)), (p, cg)
+            else:
+                for vb, slot in enumerate(m.v_residual_slots):
+                    if slot < 0:
+                        continue
+                    blk = R[vb * 4:(vb + 1) * 4]
+                    packed, scale = Q.pack_4bit(blk.ravel())
+                    assert np.array_equal(c.v_residual_buf[slot], packed), (p, vb)
+                    assert c.v_residual_scale[slot, 0] == scale, (p, vb)
+        assert sum(s >= 0 for s in m.k_residual_slots) == 2 and sum(s >= 0 for s in m.v_residual_slots) == 4
