@@ -121,6 +121,22 @@ def check(rc: int, what: str):
         raise CarekvError(f"{what} failed (code {rc}): {msg.decode() if msg else ''}")
 
 
+def check_enabled() -> bool:
+    """CAREKV_CHECK=1: after each launch, read the call's status word back
+    (a device-to-host copy, which waits for the stream) and raise on an
+    overflow the kernels flagged.  Off by default: the hot path never syncs."""
+    return os.environ.get("CAREKV_CHECK", "0") == "1"
+
+
+def check_status(ws: torch.Tensor, index: int, what: str):
+    """Raise if the int32 status word at ``index`` of the workspace is set."""
+    flag = int(ws[4 * index:4 * index + 4].view(torch.int32).item())
+    if flag != 0:
+        raise CarekvError(f"{what}: the kernels flagged an overflow (status {flag}): a page holds more stored "
+                          "residual slots than the record capacity (k_cap / v_cap), or a slot id fell past the "
+                          "arena's n_slots; those slots were left out")
+
+
 def ptr(t: torch.Tensor | None) -> int | None:
     if t is None:
         return None

@@ -111,6 +111,8 @@ def prefill_correction(cache: CAREKVCache, layer: int, q: torch.Tensor, k_hat: t
         _lib.check(lib.carekv_prefill_correct(a, dp, pp, q[r0].data_ptr(), out[r0].data_ptr(), ws.data_ptr(),
                                               ws.numel(), None if diag is None else diag[r0].data_ptr(),
                                               int(diag_cap), _lib.stream_ptr(dev)), "carekv_prefill_correct")
+        if _lib.check_enabled():
+            _lib.check_status(ws, 0, "carekv_prefill_correct")
     return (out, diag) if diag_cap > 0 else out
 
 
@@ -159,16 +161,18 @@ def decode_attention(cache: CAREKVCache, layer: int, q: torch.Tensor, seqs: Opti
         dp.phase_events = ctypes.cast(ev_arr, ctypes.c_void_p)
     lib = _lib.load()
     a = cache.arena(layer)
+    if out is None:
+        out = torch.empty(B, Hq, D, dtype=torch.float16, device=dev)
+    diag = torch.empty(B, Hq, diag_cap, dtype=torch.int32, device=dev) if diag_cap > 0 else None
     nbytes = int(lib.carekv_decode_workspace_bytes(a, dp))
     if nbytes < 0:
         raise _lib.CarekvError("carekv_decode_workspace_bytes rejected the parameters")
     ws = cache.workspace("decode", nbytes)
-    if out is None:
-        out = torch.empty(B, Hq, D, dtype=torch.float16, device=dev)
-    diag = torch.empty(B, Hq, diag_cap, dtype=torch.int32, device=dev) if diag_cap > 0 else None
     _lib.check(lib.carekv_decode_attn(a, dp, q.data_ptr(), out.data_ptr(), ws.data_ptr(), ws.numel(),
                                       None if diag is None else diag.data_ptr(), int(diag_cap),
                                       _lib.stream_ptr(dev)), "carekv_decode_attn")
+    if _lib.check_enabled():
+        _lib.check_status(ws, 0, "carekv_decode_attn")
     return (out, diag) if diag_cap > 0 else out
 
 

@@ -180,6 +180,8 @@ class CAREKVCache:
         self.k_cap, self.v_cap = store_caps(cfg)
         if n_slots is None:
             n_slots = max(64, P * H * L * self.k_cap, P * H * L * self.v_cap)
+            if self.streaming_store:  # the prompt's partial last page is stored twice (prefill, then on fill)
+                n_slots += L * H * max(self.k_cap, self.v_cap)
         self.n_slots = n_slots
         self.k_slot_bytes = T * cfg.k_channel_group * cfg.residual_bits // 8
         self.v_slot_bytes = cfg.v_token_block * D * cfg.residual_bits // 8
@@ -330,6 +332,8 @@ class CAREKVCache:
         _lib.check(lib.carekv_store_pages(a, sp, Kp.data_ptr(), Vp.data_ptr(), jobs_d.data_ptr(), len(jobs),
                                           gp_d.data_ptr(), B, ws.data_ptr(), _lib.stream_ptr(self.device)),
                    "carekv_store_pages")
+        if _lib.check_enabled():
+            _lib.check_status(ws, 4 * len(jobs), "carekv_store_pages")
         if self.streaming_store:  # the last page stays open: keep its true rows
             last = T - (n_new - 1) * ps
             sl = torch.tensor(seqs, device=self.device)
@@ -417,6 +421,8 @@ class CAREKVCache:
         _lib.check(lib.carekv_store_pages(self.arena(layer), sp, Kp.data_ptr(), Vp.data_ptr(), jobs_d.data_ptr(),
                                           len(jobs), gp_d.data_ptr(), len(seqs), ws.data_ptr(),
                                           _lib.stream_ptr(self.device)), "carekv_store_pages (streaming)")
+        if _lib.check_enabled():
+            _lib.check_status(ws, 4 * len(jobs), "carekv_store_pages (streaming)")
         self.open_k[layer, si, hi] = 0
         self.open_v[layer, si, hi] = 0
 

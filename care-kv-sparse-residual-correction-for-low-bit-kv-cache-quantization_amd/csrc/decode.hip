@@ -249,3 +249,4 @@ extern "C" int carekv_prefill_correct(const carekv_arena* arena, const carekv_de
   if (rc != CAREKV_OK) return rc;
   return run_decode(arena, &dp, &pf, q, out, workspace, workspace_bytes, diag, diag_cap, stream);
 }
+

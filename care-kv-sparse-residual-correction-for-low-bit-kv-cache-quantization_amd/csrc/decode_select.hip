@@ -274,6 +274,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
   const float* vsq_row = a.pf ? a.pf_vsq + (long)kvh * a.pf_pages : nullptr;
   float sumK = 0.f, sumV = 0.f;
   int cntK = 0, cntV = 0;
+  // a page holding more stored slots than the records have room for (k_cap,
+  // v_cap) cannot be scored in full: flag the call (the stored slots past
+  // the caps are left out)
+  bool ovf = false;
   if constexpr (PX) {  // K scores of the sketch proxy, one page per thread
 #pragma unroll 1
     for (int p = tid; p < np; p += kBlock) {
@@ -284,7 +288,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
       int rk = 0;
 #pragma unroll 1
       for (int cg = 0; cg < NCG; ++cg) {
-        if (!ok || !slot_ok(A, A.k_slot[pg * NCG + cg]) || rk >= k_cap) continue;
+        if (!ok || !slot_ok(A, A.k_slot[pg * NCG + cg])) continue;
+        if (rk >= k_cap) { ovf = true; continue; }
         const uint16_t* ks = A.k_sketch + (pg * NCG + cg) * skd;
         float dot = 0.f;
         for (int j = 0; j < skd; ++j) dot = fmaf(s_qs[cg * 64 + j], h2f(ks[j]), dot);
@@ -316,9 +321,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
       const float r0 = rp[0], M2 = rp[1], M3 = rp[2], M4 = rp[3], E = rp[4];
       const bool ok = L > 0.f && nv > 0 && hm;
       const float c = ok ? __builtin_amdgcn_exp2f(r0 - M) * invL : 0.f;
-      bool kh = false;
+      int nks = 0, nvs = 0;
 #pragma unroll
-      for (int cg = 0; cg < NCG; ++cg) kh |= slot_ok(A, ksl[cg]);
+      for (int cg = 0; cg < NCG; ++cg) nks += slot_ok(A, ksl[cg]) ? 1 : 0;
+#pragma unroll
+      for (int vb = 0; vb < kVtb; ++vb) nvs += slot_ok(A, vsl[vb]) ? 1 : 0;
+      ovf |= hm && (nks > 1 || nvs > 1);
+      const bool kh = nks > 0;
       float ks = -1.f;
       if (ok && kh) {
         const float q2 = c * c * (M2 - c * (2.f * M3 - c * M4));
@@ -368,7 +377,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
       int rk = 0;
 #pragma unroll
       for (int cg = 0; cg < NCG; ++cg) {
-        if (!ok || !slot_ok(A, ksl[cg]) || rk >= k_cap) continue;
+        if (!ok || !slot_ok(A, ksl[cg])) continue;
+        if (rk >= k_cap) { ovf = true; continue; }
         float M2 = 0.f, M3 = 0.f, M4 = 0.f;
 #pragma unroll
         for (int j = 0; j < NCG; ++j)
@@ -387,7 +397,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
     int rv = 0;
 #pragma unroll
     for (int vb = 0; vb < kVtb; ++vb) {
-      if (!ok || !slot_ok(A, vsl[vb]) || rv >= v_cap) continue;
+      if (!ok || !slot_ok(A, vsl[vb])) continue;
+      if (rv >= v_cap) { ovf = true; continue; }
       float vsc = -1.f;
       if (vb * kVtb < nv) {
         float E = 0.f;
@@ -416,15 +427,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
       if (nv <= 0 || !A.has_meta[pg]) continue;
       int rk = 0, rv = 0;  // the stored slots by rank, as the scoring loops count them
       for (int cg = 0; cg < NCG; ++cg) rk += slot_ok(A, A.k_slot[pg * NCG + cg]) ? 1 : 0;
+      ovf |= rk > k_cap;
       cntK += min(rk, k_cap);
       for (int vb = 0; vb < kVtb; ++vb) {
         if (!slot_ok(A, A.v_slot[pg * kVtb + vb])) continue;
-        if (rv >= v_cap) break;
+        if (rv >= v_cap) { ovf = true; break; }
         if (vb * kVtb < nv) ++cntV;
         ++rv;
       }
     }
   }
+  if (ovf) *a.err_flag = 1;
   float tK = sumK, tV = sumV;
   int n_k = cntK, n_v = cntV;
   block_sum4(tK, tV, n_k, n_v, bs);  // also orders the score stores before their reads

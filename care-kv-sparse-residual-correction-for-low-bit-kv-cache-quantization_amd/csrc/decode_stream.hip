@@ -45,6 +45,8 @@ void decode_stream_kernel(carekv_arena A, DecodeArgs a) {
   __shared__ float s_m[4][16], s_l[4][16];
 
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  // the call's status word starts clear; the select kernel (a later launch) sets it
+  if ((split | kvh | b) == 0 && threadIdx.x == 0) *a.err_flag = 0;
   const int GQ = a.GQ;
   const int bk = b * A.n_kv_heads + kvh;
   const EntryRow er = entry_row(A, a, b);
@@ -194,7 +196,7 @@ void decode_stream_kernel(carekv_arena A, DecodeArgs a) {
       for (int cg = 0; cg < NCG; ++cg) {
         const int slot = cm.ksl[cg];
         if (slot < 0) continue;
-        if (rk >= a.k_cap) { if (lane == 0) *a.err_flag = 1; break; }
+        if (rk >= a.k_cap) break;  // flagged by the select kernel
         if (a.proxy) { ++rk; continue; }  // the sketch proxy scores K slots without the moments
         const long so = (long)seq * A.n_slots + slot;
         const float4_t racc = kslot_dot_w(krow[cg], sqr, D, cg, ln, lj);
@@ -225,10 +227,7 @@ void decode_stream_kernel(carekv_arena A, DecodeArgs a) {
         if (vb == lj) my_rank = rv;
         ++rv;
       }
-      if (my_rank >= 0 && ln < GQ) {
-        if (my_rank < a.v_cap) rec[1 + 3 * a.k_cap + my_rank] = (e[0] + e[1]) + (e[2] + e[3]);
-        else *a.err_flag = 1;
-      }
+      if (my_rank >= 0 && my_rank < a.v_cap && ln < GQ) rec[1 + 3 * a.k_cap + my_rank] = (e[0] + e[1]) + (e[2] + e[3]);
     }
     lds_sync_wave();
   }

@@ -70,6 +70,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
   __shared__ __align__(16) uint16_t s_vs[4][4 * NCG * 16];  // per wave: [page][G][token] V scales
 
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  // the call's status word starts clear; the select kernel (a later launch) sets it
+  if ((split | kvh | b) == 0 && threadIdx.x == 0) *a.err_flag = 0;
   const int GQ = a.GQ;
   const int bk = b * A.n_kv_heads + kvh;
   const int seq_raw = a.seq_slot[b], np_raw = a.n_pages[b];
@@ -347,8 +349,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
       __builtin_amdgcn_raw_buffer_store_b64(u2_t{e01, e23}, rs_ws,
                                             vo_e, so_e + (uint32_t)p0 * 32u, 0);
     const uint32_t vmask = (uint32_t)(vbal >> (16 * lj + 6)) & 0xfu;
-    uint32_t kmask = kmask0;
-    if ((int)__builtin_popcount(kmask) > a.k_cap && sbk == 0 && sc == 0) *a.err_flag = 1;
+    uint32_t kmask = kmask0;  // stored slots past k_cap are not scored (the select kernel flags them)
     for (int r = 0; mom && r < a.k_cap; ++r) {
       const bool has = kmask != 0u;
       if (!__any(has)) break;
@@ -400,7 +401,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
       if (vrank < a.v_cap)
         __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint((e[0] + e[1]) + (e[2] + e[3])), rs_ws,
                                               vo_rec + (uint32_t)vrank * 4u, so_rp + (uint32_t)(1 + 3 * a.k_cap) * 4u, 0);
-      else *a.err_flag = 1;
     }
   }
 

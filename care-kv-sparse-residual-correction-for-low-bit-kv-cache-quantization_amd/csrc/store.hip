@@ -116,6 +116,9 @@ __global__ __launch_bounds__(256) void store_pages_kernel(carekv_arena A, carekv
   constexpr int CB = 4 * BITS;     // packed bytes per 32 codes
   const int lane = threadIdx.x & 63;
   const int job_id = blockIdx.x * 4 + (threadIdx.x >> 6);
+  // the call's slot-overflow word (after the job records) starts clear in
+  // the count pass; the write pass sets it
+  if (MODE == 0 && blockIdx.x == 0 && threadIdx.x == 0) ws.v[n_jobs * 4] = 0;
   if (job_id >= n_jobs) return;
   const carekv_page_job job = jobs[job_id];
   const int t = lane / NG, g = lane % NG;
@@ -650,6 +653,9 @@ __global__ void quantize_rows_kernel(const uint16_t* __restrict__ x, int rows, i
 
 using namespace carekv;
 
+// per job 4 int32 (counts, then slot bases), then the call's status word:
+// nonzero when a slot id would fall past the arena's n_slots (those slots are
+// dropped, never written)
 extern "C" int64_t carekv_store_workspace_bytes(int32_t n_jobs) { return (int64_t)n_jobs * 16 + 16; }
 
 template <int D, int BITS>

@@ -120,6 +120,8 @@ int carekv_store_pages(const carekv_arena* arena, const carekv_store_params* sp,
                        const uint16_t* K, const uint16_t* V, const carekv_page_job* jobs_dev,
                        int32_t n_jobs, const int32_t* group_ptr_dev, int32_t n_groups,
                        void* workspace, void* stream);
+/* The int32 at workspace[4 * n_jobs] is the call's status word: 0, or
+ * nonzero when a slot id would fall past n_slots (those slots are dropped). */
 int64_t carekv_store_workspace_bytes(int32_t n_jobs);
 
 /* One decode-token append per row (layer.py:1028-1146, cache.py:656-701):
@@ -186,7 +188,11 @@ typedef struct carekv_decode_params {
   int32_t min_keep;        /* CAREKV_READ_MIN_KEEP                             */
 } carekv_decode_params;
 
-/* q, out: fp16 [batch][n_heads][head_dim].  diag (optional, NULL to skip):
+/* q, out: fp16 [batch][n_heads][head_dim].  The first int32 of the
+ * workspace is the call's status word: 0, or nonzero when a page holds more
+ * stored residual slots than k_cap / v_cap (those slots are left out of the
+ * scoring); it is written on the device, read it after the stream is done.
+ * diag (optional, NULL to skip):
  * int32 [batch][n_heads][diag_cap] selected candidates, each encoded
  * kind<<30 | page<<3 | sub (kind 0 = K with sub = channel group,
  * 1 = V with sub = token block), sorted ascending, -1 padded. */

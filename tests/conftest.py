@@ -9,6 +9,8 @@ GOLDEN = os.path.join(ROOT, "tests", "golden")
 for p in (ROOT, PKG_DIR):
     if p not in sys.path:
         sys.path.insert(0, p)
+# every GPU test reads each call's overflow status back and fails on a flag
+os.environ.setdefault("CAREKV_CHECK", "1")
 
 
 def pytest_configure(config):

@@ -604,3 +604,36 @@ def test_decode_route_policies_vs_oracle(paper_env, case, D, Hq, Hkv, T):
     assert n_sel > 0
     err = np.abs(out - o_out.astype(F32))
     assert err.max() <= 2e-3, err.max()
+
+
+# ------------------------------------------------------------------ overflow status
+def test_overflow_status_is_raised(paper_env):
+    """The kernels flag what they cannot hold instead of dropping it
+    silently: a page with more stored K slots than the decode records'
+    capacity (forced from the host by lowering k_cap), and slot ids past a
+    too-small slot arena.  With CAREKV_CHECK=1 the host reads the status word
+    back and raises; a call without overflow after them passes (the status
+    starts clear every call)."""
+    import care_kv
+    paper_env.setenv("CAREKV_CHECK", "1")
+    rng = np.random.default_rng(7)
+    D, Hq, Hkv, T = 64, 8, 2, 100
+    cfg = care_kv.CacheConfig(num_layers=1, num_heads=Hq, num_kv_heads=Hkv, head_dim=D, page_size=16, max_pages=10,
+                              base_bits=3, group_size=32, packed_base=True, scale_quant="int8",
+                              store_budget_mode="absolute", store_abs_k=2, store_abs_v=2,
+                              read_budget_mode="absolute", read_abs_k=4, read_abs_v=4, route_policy="joint",
+                              read_budget_ratio=0.0)
+    K = torch.from_numpy(rng.standard_normal((Hkv, T, D)).astype(F16)).cuda()
+    V = torch.from_numpy(rng.standard_normal((Hkv, T, D)).astype(F16)).cuda()
+    q = torch.from_numpy(rng.standard_normal((1, Hq, D)).astype(F16)).cuda()
+    cache = care_kv.CAREKVCache(cfg, device="cuda")
+    cache.write_prefill(0, K, V)
+    care_kv.decode_attention(cache, 0, q)  # no overflow
+    cache.k_cap = 1  # two stored K slots per page, room for one
+    with pytest.raises(care_kv.CarekvError, match="overflow"):
+        care_kv.decode_attention(cache, 0, q)
+    cache.k_cap = 2
+    care_kv.decode_attention(cache, 0, q)  # the next call starts clear
+    small = care_kv.CAREKVCache(cfg, device="cuda", n_slots=5)  # 7 pages x 2 kv heads x 2 slots do not fit
+    with pytest.raises(care_kv.CarekvError, match="overflow"):
+        small.write_prefill(0, K, V)
