@@ -65,7 +65,11 @@ PAGE_JOB_INTS = 6
 EXPORTS = ["carekv_store_pages", "carekv_store_workspace_bytes", "carekv_append_rows", "carekv_decode_attn",
            "carekv_decode_workspace_bytes", "carekv_read_pages", "carekv_quantize_rows", "carekv_prefill_attn",
            "carekv_dequantize_rows", "carekv_kivi_qdq", "carekv_prefill_correct",
-           "carekv_prefill_correct_workspace_bytes", "carekv_last_error"]
+           "carekv_prefill_correct_workspace_bytes", "carekv_decode_attn_static", "carekv_last_error"]
+
+# bytes of the per-GPU static workspace of carekv_decode_attn_static
+# (CAREKV_STATIC_SCRATCH_BYTES in include/carekv.h)
+STATIC_SCRATCH_BYTES = 64 << 20
 
 
 def lib_path() -> str:
@@ -95,6 +99,8 @@ def load(path: str | None = None):
         lib.carekv_decode_workspace_bytes.argtypes = [C.POINTER(Arena), C.POINTER(DecodeParams)]
         lib.carekv_decode_attn.restype = C.c_int
         lib.carekv_decode_attn.argtypes = [C.POINTER(Arena), C.POINTER(DecodeParams), vp, vp, vp, i64, vp, i32, vp]
+        lib.carekv_decode_attn_static.restype = C.c_int
+        lib.carekv_decode_attn_static.argtypes = [C.POINTER(Arena), C.POINTER(DecodeParams), vp, vp, vp, i32, vp]
         lib.carekv_read_pages.restype = C.c_int
         lib.carekv_read_pages.argtypes = [C.POINTER(Arena), i32, i32, i32, vp, vp, vp, vp, vp, vp]
         lib.carekv_quantize_rows.restype = C.c_int

@@ -118,14 +118,20 @@ def prefill_correction(cache: CAREKVCache, layer: int, q: torch.Tensor, k_hat: t
 
 def decode_attention(cache: CAREKVCache, layer: int, q: torch.Tensor, seqs: Optional[Sequence[int]] = None, *,
                      correction: bool = True, knobs: Optional[ReadKnobs] = None, split_pages: Optional[int] = None,
-                     diag_cap: int = 0, out: Optional[torch.Tensor] = None, phase_events=None):
+                     diag_cap: int = 0, out: Optional[torch.Tensor] = None, phase_events=None,
+                     no_alloc: bool = False):
     """q: (B, Hq, D) fp16 post-RoPE queries of B sequences -> (B, Hq, D) fp16.
 
     With ``diag_cap > 0`` also returns the selected candidates per query
     head as an int32 (B, Hq, diag_cap) tensor (kind<<30 | page<<3 | sub, -1
     padded), for parity checks.  ``phase_events``: optional sequence of 5
     recorded torch.cuda.Event (timing enabled), re-recorded on the launch
-    stream around the streaming, select, apply and combine kernels."""
+    stream around the streaming, select, apply and combine kernels.
+
+    ``no_alloc``: run through ``carekv_decode_attn_static``, whose workspace
+    is the library's per-GPU static array (at most
+    ``_lib.STATIC_SCRATCH_BYTES``) instead of a buffer the cache owns; the
+    library call then allocates nothing (pass ``out``)."""
     cfg: CacheConfig = cache.cfg
     if q.dim() == 2:
         q = q.unsqueeze(0)
@@ -164,6 +170,11 @@ def decode_attention(cache: CAREKVCache, layer: int, q: torch.Tensor, seqs: Opti
     if out is None:
         out = torch.empty(B, Hq, D, dtype=torch.float16, device=dev)
     diag = torch.empty(B, Hq, diag_cap, dtype=torch.int32, device=dev) if diag_cap > 0 else None
+    if no_alloc:
+        _lib.check(lib.carekv_decode_attn_static(a, dp, q.data_ptr(), out.data_ptr(),
+                                                 None if diag is None else diag.data_ptr(), int(diag_cap),
+                                                 _lib.stream_ptr(dev)), "carekv_decode_attn_static")
+        return (out, diag) if diag_cap > 0 else out
     nbytes = int(lib.carekv_decode_workspace_bytes(a, dp))
     if nbytes < 0:
         raise _lib.CarekvError("carekv_decode_workspace_bytes rejected the parameters")

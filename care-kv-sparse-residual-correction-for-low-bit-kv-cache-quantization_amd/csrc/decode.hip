@@ -1,5 +1,7 @@
 // C ABI of the decode path: workspace layout, argument checks, launches of
 // the streaming, select, apply and combine kernels on the caller's stream.
+#include <mutex>
+
 #include "block_util.h"
 #include "decode_common.h"
 #include "host_util.h"
@@ -250,3 +252,62 @@ extern "C" int carekv_prefill_correct(const carekv_arena* arena, const carekv_de
   return run_decode(arena, &dp, &pf, q, out, workspace, workspace_bytes, diag, diag_cap, stream);
 }
 
+// ------------------------------------------------------------------ no-allocation variant
+// carekv_decode_attn_static: the decode step with its workspace in a
+// file-scope device array instead of a caller buffer, for callers that
+// cannot allocate (graph capture, tight serving loops).  Each GPU holds its
+// own copy of the array for the life of the process; host code reaches it
+// only through the address hipGetSymbolAddress returns on that device (the
+// array's name is a host-side stand-in).  Calls that overlap on one GPU share
+// the array and race.
+namespace {
+static __device__ __align__(256) char scratch[CAREKV_STATIC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device (looked up once per
+// device), or null with the error message set.
+void* static_scratch(int dev) {
+  if (dev < 0 || dev >= kMaxDevices) {
+    set_error("carekv_decode_attn_static: device %d out of range", dev);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lk(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      set_error("carekv_decode_attn_static: hipGetSymbolAddress failed on device %d: %s", dev,
+                hipGetErrorString(e));
+      return nullptr;
+    }
+    g_scratch[dev] = p;
+  }
+  return g_scratch[dev];
+}
+}  // namespace
+
+extern "C" int carekv_decode_attn_static(const carekv_arena* arena, const carekv_decode_params* dp,
+                                         const uint16_t* q, uint16_t* out, int32_t* diag, int32_t diag_cap,
+                                         void* stream) {
+  CAREKV_REQUIRE(arena && dp, "null argument");
+  CAREKV_REQUIRE(dp->split_pages > 0 && arena->n_kv_heads > 0, "split_pages and n_kv_heads must be positive");
+  int dev = -1, sdev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || hipStreamGetDevice((hipStream_t)stream, &sdev) != hipSuccess) {
+    set_error("carekv_decode_attn_static: cannot resolve the current device or the stream's device");
+    return CAREKV_ELAUNCH;
+  }
+  CAREKV_REQUIRE(dev == sdev, "the stream's device must be the current device");
+  const int64_t need = ws_layout(*arena, *dp).total;
+  if (need > (int64_t)CAREKV_STATIC_SCRATCH_BYTES) {
+    set_error("carekv_decode_attn_static: this step needs %lld workspace bytes, the static scratch holds %lld "
+              "(CAREKV_STATIC_SCRATCH_BYTES): lower the batch or max_pages_used, or use carekv_decode_attn "
+              "with a caller workspace", (long long)need, (long long)CAREKV_STATIC_SCRATCH_BYTES);
+    return CAREKV_ESPACE;
+  }
+  void* ws = static_scratch(dev);
+  if (!ws) return CAREKV_ELAUNCH;
+  return run_decode(arena, dp, nullptr, q, out, ws, CAREKV_STATIC_SCRATCH_BYTES, diag, diag_cap, stream);
+}

@@ -201,6 +201,22 @@ int carekv_decode_attn(const carekv_arena* arena, const carekv_decode_params* dp
                        int32_t diag_cap, void* stream);
 int64_t carekv_decode_workspace_bytes(const carekv_arena* arena, const carekv_decode_params* dp);
 
+/* No reference counterpart: carekv_decode_attn for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Same arguments and results as carekv_decode_attn
+ * without the workspace: the step's workspace is a file-scope device array
+ * of CAREKV_STATIC_SCRATCH_BYTES per GPU, held by each GPU the library runs
+ * on until the process ends.  Steps needing more workspace than that
+ * (carekv_decode_workspace_bytes) fail with CAREKV_ESPACE and a message.
+ * The call allocates nothing; the stream's device must be current.  Every
+ * call on one GPU shares that GPU's array: calls that overlap on one GPU
+ * (two streams, two threads) race.  The overflow status word lives in the
+ * array and is not read back; check a configuration with carekv_decode_attn
+ * first. */
+#define CAREKV_STATIC_SCRATCH_BYTES (64L << 20)
+int carekv_decode_attn_static(const carekv_arena* arena, const carekv_decode_params* dp, const uint16_t* q,
+                              uint16_t* out, int32_t* diag, int32_t diag_cap, void* stream);
+
 /* read_base_concat (cache.py:720-772) for one (seq, kv_head): unpacked int8
  * codes [N][D] and fp16 scales [N][G] of the valid rows of pages 0..n_pages-1
  * (int8 scales expanded as half(code * master)).  row_start_dev: int32
