@@ -27,7 +27,8 @@ class Arena(C.Structure):
         [(n, C.c_int32) for n in (
             "n_seq", "n_kv_heads", "max_pages", "head_dim", "base_bits", "page_size", "group_size",
             "k_channel_group", "v_token_block", "sketch_dim", "scale_mode", "residual_bits", "n_slots",
-            "hat_bits_k", "hat_bits_v")]
+            "hat_bits_k", "hat_bits_v")] + \
+        [("open_kscale", C.c_void_p), ("open_vscale", C.c_void_p), ("rescale_open", C.c_int32)]
 
 
 class StoreParams(C.Structure):

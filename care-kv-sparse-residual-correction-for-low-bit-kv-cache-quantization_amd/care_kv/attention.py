@@ -23,9 +23,27 @@ import torch
 
 from . import _lib
 from .cache import CAREKVCache, get_sketch_proj
-from .config import CacheConfig, ReadKnobs, resolve_read_knobs
+from .config import CacheConfig, ReadKnobs, any_read_budget, resolve_read_knobs
 
 KIND_CODE = {"both": 0, "k": 1, "v": 2}
+
+
+def decode_read_mode(cfg: CacheConfig, layer: int):
+    """(correction on, read knobs) of a decode step through
+    ``CAREKVLayer.decode_step`` / ``CAREKVMultiHeadAttention``.
+
+    ``cfg.compat``: as the reference's decode path, which corrects only when
+    read_budget_ratio > 0 (attention.py:1025) and then selects per query
+    head through ResidualRouter.route (apply_slot_corrections,
+    attention.py:208-374; the router reads no CAREKV_KSCORE_LIVE), i.e. with
+    the sketch-proxy K score.  Otherwise the correction runs whenever a read
+    budget is set (layer.py:813-819's test) with the knobs of
+    ``resolve_read_knobs`` (the query-aware score under CAREKV_KSCORE_LIVE=1)."""
+    knobs = resolve_read_knobs(cfg, layer)
+    if cfg.compat:
+        knobs.kscore_live = False
+        return cfg.read_budget_ratio > 0, knobs
+    return any_read_budget(cfg), knobs
 
 
 def default_split_pages(max_pages: int, rows: int) -> int:
@@ -59,9 +77,15 @@ def prefill_correction(cache: CAREKVCache, layer: int, q: torch.Tensor, k_hat: t
                        lse: torch.Tensor, seq: int = 0, *, knobs: Optional[ReadKnobs] = None,
                        split_pages: Optional[int] = None, diag_cap: int = 0, rows_per_call: Optional[int] = None):
     """The prefill-time correction of ``carekv_stored`` mode (layer.py:780-838)
-    with the vectorized correction over all kv_group x T queries
-    (layer.py:538-557), for the prompt that sequence ``seq`` of the cache
-    holds (written by ``write_prefill`` from token 0).
+    over all kv_group x T queries, for the prompt that sequence ``seq`` of
+    the cache holds (written by ``write_prefill`` from token 0).  With
+    ``knobs.kscore_live`` it is the vectorized correction of
+    correction_impl=vectorized (layer.py:538-557); without, the per-(head,
+    row) apply_slot_corrections over ResidualRouter.route of
+    correction_impl=cached / python (layer.py:573-640, the router's sketch
+    proxy score, its policies and thresholds), which the reference's own test
+    holds equal to the vectorized form over the same scores
+    (tests/test_vectorized_carekv.py:83-162).
 
     q (T, Hq, D) fp16 post-RoPE queries; k_hat / v_hat (Hkv, T, D) fp16 the
     page writer's dequantised prompt (``quant_dequant`` for the uniform
@@ -72,9 +96,6 @@ def prefill_correction(cache: CAREKVCache, layer: int, q: torch.Tensor, k_hat: t
     cfg: CacheConfig = cache.cfg
     if knobs is None:
         knobs = resolve_read_knobs(cfg, layer)
-    if not knobs.kscore_live:
-        raise NotImplementedError("the prefill correction is built for the query-aware K score "
-                                  "(CAREKV_KSCORE_LIVE=1) only")
     T, Hq, D = q.shape
     Hkv = cfg.num_kv_heads
     if (Hq, D) != (cfg.num_heads, cfg.head_dim) or k_hat.shape != (Hkv, T, D) or v_hat.shape != (Hkv, T, D) \
@@ -99,6 +120,9 @@ def prefill_correction(cache: CAREKVCache, layer: int, q: torch.Tensor, k_hat: t
     diag = torch.empty(T, Hq, diag_cap, dtype=torch.int32, device=dev) if diag_cap > 0 else None
     dp = _read_params(cache, layer, knobs, batch=0, n_heads=Hq, correction=True, split_pages=split_pages,
                       max_pages=pages)
+    if not knobs.kscore_live:  # the router's sketch-proxy K score
+        dp.k_proxy = 1
+        dp.sketch_proj = get_sketch_proj(cfg.head_dim, cfg.k_channel_group, cfg.sketch_dim, dev).data_ptr()
     for r0 in range(0, T, rows_per_call):
         n = min(rows_per_call, T - r0)
         pp = _lib.PrefillCorrParams(seq=seq, n_tokens=T, row_begin=r0, n_rows=n, k_hat=k_hat.data_ptr(),
@@ -198,16 +222,16 @@ class CAREKVMultiHeadAttention:
     def forward(self, cache: CAREKVCache, Q: torch.Tensor, page_ids=None, kind: str = "both",
                 k_corr_scale: float = 1.0, score_normalize: bool = False, debug_stats=None, seq: int = 0,
                 correction: Optional[bool] = None):
-        """Q (num_heads, D) -> (num_heads, D) fp16.  The reference applies its
-        correction only when read_budget_ratio > 0 (attention.py:1025);
-        ``correction=None`` keeps that gate."""
+        """Q (num_heads, D) -> (num_heads, D) fp16.  ``correction=None``: the
+        gate and selector of ``decode_read_mode`` (under ``cfg.compat`` the
+        reference's: only when read_budget_ratio > 0, attention.py:1025)."""
         cfg = self.cfg
-        knobs = resolve_read_knobs(cfg, self.layer_id)
+        gate, knobs = decode_read_mode(cfg, self.layer_id)
         knobs.kind = kind
         knobs.k_corr_scale = k_corr_scale
         knobs.normalize = score_normalize
         if correction is None:
-            correction = cfg.read_budget_ratio > 0
+            correction = gate
         return decode_attention(cache, self.layer_id, Q.unsqueeze(0), [seq], correction=correction,
                                 knobs=knobs)[0]
 

@@ -133,12 +133,18 @@ class CAREKVCache:
     """Device-resident paged cache for ``n_seq`` sequences of one model."""
 
     def __init__(self, cfg: CacheConfig, device=None, n_seq: int = 1, n_slots: Optional[int] = None,
-                 streaming_store: bool = False):
+                 streaming_store: Optional[bool] = None):
         """``streaming_store`` (no reference counterpart): keep
         each open page's true fp16 rows and, when decode appends fill the
         page, store its residuals against the page's own base instead of
         the reference's zero-residual fill store (layer.py:1128-1146), so
-        that decode-filled pages get slots."""
+        that decode-filled pages get slots.  None: on unless ``cfg.compat``.
+
+        Unless ``cfg.compat``, decode appends into int8-scale pages re-encode
+        the open page as write_base encodes its valid rows (the fp16 group
+        scales of every open page are kept for that) instead of the
+        reference's fixed-master encoding, whose decode-opened pages read back
+        as zero (cache.py:689-695)."""
         check_kernel_config(cfg)
         if device is None:
             device = torch.device("cuda", torch.cuda.current_device())
@@ -172,7 +178,12 @@ class CAREKVCache:
         self.v_err = torch.zeros(*shp, self.nvb, dtype=F16, device=dev)
         self.k_sketch = torch.zeros(*shp, self.ncg, cfg.sketch_dim, dtype=F16, device=dev)
         self.v_sq = torch.zeros(*shp, dtype=torch.float32, device=dev)
-        self.streaming_store = bool(streaming_store)
+        self.streaming_store = (not cfg.compat) if streaming_store is None else bool(streaming_store)
+        # open pages' fp16 group scales, for the re-encoding append
+        self.rescale_open = self.scale_mode == 1 and not self.hat and not cfg.compat
+        if self.rescale_open:
+            self.open_ks = torch.zeros(L, H, n_seq, T, G, dtype=F16, device=dev)
+            self.open_vs = torch.zeros_like(self.open_ks)
         if self.streaming_store:
             # true rows of every (layer, seq, kv head)'s open page
             self.open_k = torch.zeros(L, n_seq, H, T, D, dtype=F16, device=dev)
@@ -217,7 +228,9 @@ class CAREKVCache:
                 base_bits=self._arena_bits, page_size=cfg.page_size, group_size=cfg.group_size,
                 k_channel_group=cfg.k_channel_group, v_token_block=cfg.v_token_block, sketch_dim=cfg.sketch_dim,
                 scale_mode=self.scale_mode, residual_bits=cfg.residual_bits, n_slots=self.n_slots,
-                hat_bits_k=hat_bits(cfg)[0], hat_bits_v=hat_bits(cfg)[1])
+                hat_bits_k=hat_bits(cfg)[0], hat_bits_v=hat_bits(cfg)[1],
+                open_kscale=g(self.open_ks) if self.rescale_open else None,
+                open_vscale=g(self.open_vs) if self.rescale_open else None, rescale_open=int(self.rescale_open))
             self._arenas[layer] = a
         return a
 
@@ -334,6 +347,20 @@ class CAREKVCache:
                    "carekv_store_pages")
         if _lib.check_enabled():
             _lib.check_status(ws, 4 * len(jobs), "carekv_store_pages")
+        if self.rescale_open:  # the last page stays open: keep its rows' fp16 group scales
+            last = T - (n_new - 1) * ps
+            if last < ps:
+                G = D // cfg.group_size
+                tail = torch.cat([K[:, :, (n_new - 1) * ps:], V[:, :, (n_new - 1) * ps:]], 0).to(F16).contiguous()
+                codes = torch.empty(2 * B * H * last, D, dtype=torch.int8, device=self.device)
+                sc = torch.empty(2 * B * H * last, G, dtype=F16, device=self.device)
+                _lib.check(lib.carekv_quantize_rows(tail.data_ptr(), 2 * B * H * last, D, cfg.base_bits, 32, 0,
+                                                    codes.data_ptr(), sc.data_ptr(), _lib.stream_ptr(self.device)),
+                           "carekv_quantize_rows (open page scales)")
+                sc = sc.view(2, B, H, last, G)
+                sl = torch.tensor(seqs, device=self.device)
+                self.open_ks[layer][:, sl, :last] = sc[0].transpose(0, 1)
+                self.open_vs[layer][:, sl, :last] = sc[1].transpose(0, 1)
         if self.streaming_store:  # the last page stays open: keep its true rows
             last = T - (n_new - 1) * ps
             sl = torch.tensor(seqs, device=self.device)

@@ -50,6 +50,9 @@ def apply_carekv_env_overrides(kwargs: dict) -> dict:
         ("CAREKV_BASELINE_SCORE", "baseline_score", str),
     ):
         _set(name, key, conv)
+    # no reference counterpart: CAREKV_COMPAT=1 reproduces the reference's
+    # decode-path defects (CacheConfig.compat)
+    _set("CAREKV_COMPAT", "compat", as_bool)
     ls = env.get("CAREKV_LAYER_SENSITIVITY", "")
     if ls:
         try:
@@ -106,6 +109,20 @@ class CacheConfig:
     correction_impl: str = "cached"
     pack_impl: str = "vectorized"
     budget_policy: str = "uniform"
+    # No reference counterpart.  compat=True reproduces three defects of the
+    # reference's decode path exactly (the parity mode the reference goldens
+    # run under): (i) decode_step corrects only when read_budget_ratio > 0
+    # (attention.py:1025), (ii) a page the decode opens keeps a zero int8
+    # scale master, so its rows read back as zero (cache.py:689-695), (iii) a
+    # page the decode fills is stored with K_orig = K_hat, i.e. without slots
+    # (layer.py:1088-1146); decode_step and CAREKVMultiHeadAttention then
+    # select through the router's sketch-proxy score as the reference's
+    # decode path does (apply_slot_corrections -> ResidualRouter.route).
+    # compat=False (the default) fixes them: decode_step corrects whenever a
+    # read budget is set (with the query-aware score under
+    # CAREKV_KSCORE_LIVE=1), open pages are re-encoded as write_base encodes
+    # their valid rows, and filled pages are stored from their true rows.
+    compat: bool = False
 
     def __post_init__(self):
         if self.layer_sensitivity is None:

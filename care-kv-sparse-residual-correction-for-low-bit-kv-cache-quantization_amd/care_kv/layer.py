@@ -25,9 +25,9 @@ from typing import Any, Dict, Optional, Sequence, Tuple
 import torch
 from torch import Tensor, nn
 
-from .attention import decode_attention, prefill_correction
+from .attention import decode_attention, decode_read_mode, prefill_correction
 from .cache import CAREKVCache
-from .config import CacheConfig, any_read_budget
+from .config import CacheConfig, any_read_budget, resolve_read_knobs
 from .prefill import prefill_attention, quant_dequant
 
 try:  # the reference takes RoPE from transformers as well (layer.py:65-69)
@@ -50,6 +50,19 @@ def resolve_prefill_mode() -> str:
     if raw not in PREFILL_MODES:
         raise ValueError(f"CAREKV_PREFILL_MODE={raw!r} is not one of {PREFILL_MODES}")
     return raw
+
+
+def prefill_read_knobs(cfg: CacheConfig, layer_id: int):
+    """Read knobs of the carekv_stored prefill correction by
+    cfg.correction_impl (layer.py:514-557): ``vectorized`` runs
+    vectorized_joint_correction, whose K score follows CAREKV_KSCORE_LIVE;
+    ``cached`` / ``python`` run apply_slot_corrections per (head, row) over
+    ResidualRouter.route, which has no query-aware K score (the sketch
+    proxy, whatever CAREKV_KSCORE_LIVE says)."""
+    knobs = resolve_read_knobs(cfg, layer_id)
+    if cfg.correction_impl != "vectorized":
+        knobs.kscore_live = False
+    return knobs
 
 
 def _rope(q: Tensor, k: Tensor, cos: Tensor, sin: Tensor) -> Tuple[Tensor, Tensor]:
@@ -152,22 +165,15 @@ class CAREKVLayer(nn.Module):
                 Khat = quant_dequant(Kh, cfg.base_bits, cfg.group_size)
                 Vhat = quant_dequant(Vh, cfg.base_bits, cfg.group_size)
             stored = mode == "carekv_stored" and any_read_budget(cfg)
-            if stored and os.environ.get("CAREKV_KSCORE_LIVE", "0") != "1":
-                stored = False
-                if "carekv_stored_proxy" not in _warned:
-                    _warned.add("carekv_stored_proxy")
-                    warnings.warn("CAREKV_PREFILL_MODE=carekv_stored with the sketch-proxy K score "
-                                  "(CAREKV_KSCORE_LIVE=0): the prefill correction is built for the query-aware "
-                                  "score only; the prefill output is the base attention over K_hat / V_hat",
-                                  RuntimeWarning, stacklevel=2)
             if stored and token_start_abs != 0:
                 raise NotImplementedError("carekv_stored prefill correction of a prompt continuation "
                                           "(token_start_abs > 0): the reference scores one prompt at a time")
             O, lse = prefill_attention(Qh, Khat, Vhat, return_lse=True)
             if stored:  # layer.py:808-838: the sparse correction from the stored slots
+                knobs = prefill_read_knobs(cfg, self.layer_id)
                 for b, sq in enumerate(seqs):
                     O[b] = prefill_correction(cache, self.layer_id, Qh[b].transpose(0, 1), Khat[b], Vhat[b],
-                                              lse[b], seq=sq).transpose(0, 1)
+                                              lse[b], seq=sq, knobs=knobs).transpose(0, 1)
         out = self._out(O, hidden.dtype).to(hidden.dtype)
         return out[0] if squeeze else out
 
@@ -178,8 +184,8 @@ class CAREKVLayer(nn.Module):
         """layer.py:978-1163 for a batch: hidden (1, model_dim) of one
         sequence or (B, 1, model_dim) -> same shape.  Appends the token's
         K / V (store on page fill with K_orig = K_hat, layer.py:1088-1146),
-        then runs the decode attention, with the comb+ex correction when a
-        read budget ratio is set."""
+        then runs the decode attention with the correction
+        ``decode_read_mode`` resolves."""
         squeeze = hidden.dim() == 2
         if squeeze:
             hidden = hidden.unsqueeze(0)
@@ -190,8 +196,8 @@ class CAREKVLayer(nn.Module):
             Q, K = _rope(Q, K, cos.to(Q.dtype), sin.to(Q.dtype))
         seqs = list(range(B)) if seqs is None else list(seqs)
         cache.append(self.layer_id, K[:, :, 0].to(F16), V[:, :, 0].to(F16), seqs=seqs)
-        # the reference corrects only when read_budget_ratio > 0 (attention.py:1025)
-        O = decode_attention(cache, self.layer_id, Q[:, :, 0].to(F16), seqs=seqs,
-                             correction=self.cfg.read_budget_ratio > 0)  # (B, Hq, D)
+        correction, knobs = decode_read_mode(self.cfg, self.layer_id)
+        O = decode_attention(cache, self.layer_id, Q[:, :, 0].to(F16), seqs=seqs, correction=correction,
+                             knobs=knobs)  # (B, Hq, D)
         out = self._out(O.unsqueeze(2), hidden.dtype).to(hidden.dtype)  # (B, 1, model_dim)
         return out[0] if squeeze else out

@@ -61,10 +61,11 @@ class CAREKVLlamaAttention(nn.Module):
     def _cache_for(self, batch: int, device) -> CAREKVCache:
         st = self._shared
         if st.cache is None or st.cache.n_seq < batch or st.cache.device != torch.device(device):
-            # CAREKV_STREAMING_STORE=1: the opt-in streaming fill store (no
-            # reference counterpart; CAREKVCache(streaming_store=True))
+            # the streaming fill store (no reference counterpart) is on unless
+            # cfg.compat; CAREKV_STREAMING_STORE=1 / 0 forces it on / off
+            env = os.environ.get("CAREKV_STREAMING_STORE", "")
             st.cache = CAREKVCache(self.cfg, device=device, n_seq=batch,
-                                   streaming_store=os.environ.get("CAREKV_STREAMING_STORE", "0") == "1")
+                                   streaming_store=None if env == "" else env == "1")
             st.prefilled.clear()
         return st.cache
 

@@ -32,6 +32,10 @@ bool check_arena(const carekv_arena& A) {
     set_error("scale_mode=int8 needs master buffers");
     return false;
   }
+  if (!hat && A.scale_mode == 1 && A.rescale_open && (!A.open_kscale || !A.open_vscale)) {
+    set_error("rescale_open needs the open pages' fp16 scales (open_kscale, open_vscale)");
+    return false;
+  }
   if (A.page_size != 16 || A.group_size != 32 || A.k_channel_group != 32 || A.v_token_block != 4) {
     set_error("kernels support page_size=16, group_size=32, k_channel_group=32, v_token_block=4 "
               "(got %d/%d/%d/%d)", A.page_size, A.group_size, A.k_channel_group, A.v_token_block);

@@ -10,12 +10,13 @@ using namespace carekv;
 
 namespace {
 struct WsLayout {
-  long err, pml, po, rec, ebuf, scores, mask, ml, num, den, xbuf, prox, total;
+  long err, pml, po, rec, ebuf, scores, mask, ml, num, den, xbuf, prox, xmax, total;
   int nsplit, F, ncand;
 };
 
-// gq: query columns per (entry, kv head); 0 = n_heads / n_kv_heads
-WsLayout ws_layout(const carekv_arena& A, const carekv_decode_params& dp, int gq = 0) {
+// gq: query columns per (entry, kv head); 0 = n_heads / n_kv_heads; pf:
+// prefill rows
+WsLayout ws_layout(const carekv_arena& A, const carekv_decode_params& dp, int gq = 0, bool pf = false) {
   WsLayout L{};
   const long BH = (long)dp.batch * A.n_kv_heads;
   const int GQ = gq > 0 ? gq : dp.n_heads / A.n_kv_heads;
@@ -40,6 +41,7 @@ WsLayout ws_layout(const carekv_arena& A, const carekv_decode_params& dp, int gq
   const bool need_x = dp.correction != 0 && (dp.k_proxy != 0 || dp.route_policy == 3);
   L.xbuf = off; off += need_x ? al(BH * GQ * (long)Pm * 16 * 4) : 0;
   L.prox = off; off += proxy ? al(BH * GQ * (long)Pm * 4 * 4) : 0;
+  L.xmax = off; off += (pf && proxy) ? al(BH * L.nsplit * 4 * 16 * 4) : 0;
   L.total = off;
   return L;
 }
@@ -102,7 +104,7 @@ int run_decode(const carekv_arena* arena, const carekv_decode_params* dp, const 
   const bool need_x = dp->correction != 0 && (proxy || dp->route_policy == 3);
   CAREKV_REQUIRE(!proxy || (A.k_sketch && A.k_channel_group == 32 && A.sketch_dim >= 1 && A.sketch_dim <= 64),
                  "the sketch proxy needs k_sketch, k_channel_group 32 and sketch_dim in 1..64");
-  const WsLayout L = ws_layout(A, *dp, GQ);
+  const WsLayout L = ws_layout(A, *dp, GQ, pf != nullptr);
   const long vsq_off = L.total, need = L.total + (pf ? (long)A.n_kv_heads * pf->pages * 4 : 0);
   if (workspace_bytes < need) {
     set_error("%s: workspace too small (%lld < %lld)", pf ? "carekv_prefill_correct" : "carekv_decode_attn",
@@ -130,6 +132,7 @@ int run_decode(const carekv_arena* arena, const carekv_decode_params* dp, const 
   a.adaptive_score = dp->adaptive_score != 0;
   a.rel_thr = dp->rel_threshold; a.abs_thr = dp->abs_threshold; a.min_keep = dp->min_keep;
   a.prox = proxy ? (float*)(ws + L.prox) : nullptr;
+  a.xmax = (pf && proxy) ? (float*)(ws + L.xmax) : nullptr;
   a.ws_span = (uint32_t)(L.prox - L.rec);
   a.ws_e_off = (uint32_t)(L.ebuf - L.rec);
   a.ws_x_off = (uint32_t)(L.xbuf - L.rec);
@@ -215,7 +218,6 @@ int prefill_setup(const carekv_arena* arena, const carekv_decode_params* read,
   CAREKV_REQUIRE(pp->k_hat && pp->v_hat && pp->lse, "k_hat, v_hat and lse are required");
   CAREKV_REQUIRE((long)pp->n_tokens * A.head_dim * 2 < (1L << 32), "prompt rows exceed 4 GiB per kv head");
   CAREKV_REQUIRE(read->correction != 0, "prefill rows run the correction (correction must be 1)");
-  CAREKV_REQUIRE(read->k_proxy == 0, "prefill rows support the query-aware K score only (k_proxy must be 0)");
   CAREKV_REQUIRE(read->n_heads > 0 && read->n_heads % A.n_kv_heads == 0 && read->n_heads / A.n_kv_heads <= 16,
                  "n_heads must be a multiple of n_kv_heads with at most 16 query heads per kv head");
   dp = *read;
@@ -238,7 +240,7 @@ extern "C" int64_t carekv_prefill_correct_workspace_bytes(const carekv_arena* ar
   carekv_decode_params dp{};
   PfRows pf{};
   if (prefill_setup(arena, read, pp, dp, pf) != CAREKV_OK || dp.split_pages <= 0) return -1;
-  return ws_layout(*arena, dp, pf.G0 * pf.R).total + (int64_t)arena->n_kv_heads * pf.pages * 4;
+  return ws_layout(*arena, dp, pf.G0 * pf.R, true).total + (int64_t)arena->n_kv_heads * pf.pages * 4;
 }
 
 extern "C" int carekv_prefill_correct(const carekv_arena* arena, const carekv_decode_params* read,

@@ -23,6 +23,8 @@ struct DecodeArgs {
   float* den;          // [B*Hkv][nsplit][GQ]     apply partial denominators
   float* xbuf;         // [B*Hkv][GQ][Pmax][16]   fp32 base-2 logits x (sketch proxy, adaptive policy)
   float* prox;         // [B*Hkv][GQ][Pmax][4]    mass, boundary, vdiff (sketch proxy only)
+  float* xmax;         // [B*Hkv][nsplit][4][16]  prefill rows with the sketch proxy: each wave's
+                       //                         maximum base-2 logit per query column
   const float* sketch_proj;  // [32][sketch_dim] fp32 (sketch proxy only)
   int32_t* diag;
   int32_t* err_flag;

@@ -14,6 +14,14 @@
 //
 // Lane l = 16 j + m: token m, dims [j D/4, (j+1) D/4) of the page for the
 // distance sums; afterwards the 16 lanes of row j finish query 4 k + j.
+//
+// PF (prefill rows, the per-(head, row) router of correction_impl=cached,
+// layer.py:573-640): a is the reference's fp16 attention weight of the row
+// (the streaming pass's stored weights, against the row's log-sum-exp),
+// s_top the row's largest logit (the streaming pass's per-wave maxima),
+// O_base the fp16 base output half(sum_t a_t V_hat_t) (layer.py:964-965),
+// V_hat the prompt's dense fp16 rows; logits past the row are -inf and
+// their weights 0.
 #include "decode_page.h"
 #include "host_util.h"
 
@@ -25,7 +33,7 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v;
 }
 
-template <int D, int BITS, int SM>
+template <int D, int BITS, int SM, bool PF = false>
 __global__ __launch_bounds__(256) void decode_proxy_kernel(carekv_arena A, DecodeArgs a) {
   using G = PageGeom<D, BITS>;
   using PB = typename G::PB;
@@ -33,14 +41,13 @@ __global__ __launch_bounds__(256) void decode_proxy_kernel(carekv_arena A, Decod
   constexpr float kEps = 1e-6f;               // residual_router.py:34
   constexpr float kLn2 = 0.693147180559945f;  // margins back from base-2 logits
   __shared__ float s_o[16 * D];               // O_base [query][dim]
-  __shared__ float s_M[16], s_L[16];
+  __shared__ float s_M[16], s_L[16], s_Mp[16];
 
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int GQ = a.GQ;
   const int bk = b * A.n_kv_heads + kvh;
-  const int seq_raw = a.seq_slot[b], np_raw = a.n_pages[b];
-  const bool row_ok = seq_raw >= 0 && seq_raw < A.n_seq && np_raw >= 0 && np_raw <= a.Pmax;
-  const int seq = row_ok ? seq_raw : 0, np = row_ok ? np_raw : 0;
+  const EntryRow er = entry_row(A, a, b);
+  const int seq = er.seq, np = er.np;
   const int p_begin = split * a.SP, p_end = min(p_begin + a.SP, np);
   if (p_begin >= p_end) return;  // uniform over the work-group
   const int lane = threadIdx.x & 63;
@@ -60,13 +67,17 @@ __global__ __launch_bounds__(256) void decode_proxy_kernel(carekv_arena A, Decod
         const float ms = a.pml[base * 2];
         if (ms != -INFINITY) L += a.pml[base * 2 + 1] * __builtin_amdgcn_exp2f(ms - M);
       }
-    s_M[qq] = M;
+    float xm = -INFINITY;
+    if constexpr (PF)
+      for (int i = 0; i < a.nsplit * 4; ++i) xm = fmaxf(xm, a.xmax[((long)bk * a.nsplit * 4 + i) * 16 + qq]);
+    s_M[qq] = PF ? xm : M;  // the margins' s_top
     s_L[qq] = L;
+    s_Mp[qq] = M;           // the split partials' reference maximum
   }
   __syncthreads();
   for (int i = threadIdx.x; i < GQ * D; i += 256) {
     const int qq = i / D, d = i % D;
-    const float M = s_M[qq], L = s_L[qq];
+    const float M = s_Mp[qq], L = s_L[qq];
     float O = 0.f;
     if (M != -INFINITY)
       for (int s = 0; s < a.nsplit; ++s) {
@@ -74,11 +85,19 @@ __global__ __launch_bounds__(256) void decode_proxy_kernel(carekv_arena A, Decod
         const float ms = a.pml[base * 2];
         if (ms != -INFINITY) O += a.po[base * D + d] * __builtin_amdgcn_exp2f(ms - M);
       }
-    s_o[i] = L > 0.f ? O / L : 0.f;
+    // prefill rows: the fp16 base output, the weights already normalised
+    s_o[i] = PF ? (float)(_Float16)O : (L > 0.f ? O / L : 0.f);
   }
   __syncthreads();
 
-  const RowRes rr = row_resources<D, BITS, SM>(A, pg_base);
+  RowRes rr;
+  if constexpr (PF) {
+    static_assert(BITS == 16, "prefill rows are fp16");
+    rr.vc = make_rsrc(a.pf_v + (long)kvh * a.pf_T * D, (uint32_t)a.pf_T * D * 2);  // rows past the prompt read 0
+    rr.kc = rr.ks = rr.vs = make_rsrc(nullptr, 0u);
+  } else {
+    rr = row_resources<D, BITS, SM>(A, pg_base);
+  }
   const float* ob = s_o + lj * CH;
   for (int p = p_begin + w; p < p_end; p += 4) {
     const long pg = pg_base + p;
@@ -127,7 +146,8 @@ __global__ __launch_bounds__(256) void decode_proxy_kernel(carekv_arena A, Decod
         const float M = s_M[qq], L = s_L[qq];
         const float x = a.xbuf[(((long)bk * GQ + qq) * a.Pmax + p) * 16 + ln];
         if (x != -INFINITY && M != -INFINITY && L > 0.f) {
-          at = __builtin_amdgcn_exp2f(x - M) / L;
+          if constexpr (PF) at = h2f(a.ebuf[(((long)bk * GQ + qq) * a.Pmax + p) * 16 + ln]);
+          else at = __builtin_amdgcn_exp2f(x - M) / L;
           bt = at * (1.f / fmaxf((M - x) * kLn2, kEps));
           vt = at * sqrtf(d2);
         }
@@ -143,6 +163,12 @@ __global__ __launch_bounds__(256) void decode_proxy_kernel(carekv_arena A, Decod
 
 int launch_decode_proxy(const carekv_arena& A, const DecodeArgs& a, hipStream_t s) {
   const dim3 grid(a.nsplit, A.n_kv_heads, a.B);
+  if (a.pf) {
+    if (A.head_dim == 64) hipLaunchKernelGGL((decode_proxy_kernel<64, 16, 0, true>), grid, dim3(256), 0, s, A, a);
+    else hipLaunchKernelGGL((decode_proxy_kernel<128, 16, 0, true>), grid, dim3(256), 0, s, A, a);
+    CAREKV_CHECK_LAUNCH("decode_proxy (prefill rows)");
+    return CAREKV_OK;
+  }
   return dispatch_dbs16(A.head_dim, A.base_bits, A.scale_mode, [&](auto d, auto bb, auto sm) {
     hipLaunchKernelGGL((decode_proxy_kernel<decltype(d)::value, decltype(bb)::value, decltype(sm)::value>), grid,
                        dim3(256), 0, s, A, a);

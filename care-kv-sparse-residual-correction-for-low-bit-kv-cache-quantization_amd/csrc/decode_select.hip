@@ -253,10 +253,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
   const int skd = A.sketch_dim;
   if constexpr (PX) {
     const uint16_t* qg = a.q + ((long)b * a.Hq + kvh * GQ + qq) * D;
+    if (a.pf) {  // prefill rows: the column's (row, head); a padding column sketches zero
+      const PfCol x = pf_col(a, b, kvh, qq);
+      qg = x.ok ? a.q + pf_row_off(a, x) * D : nullptr;
+    }
     for (int i = tid; i < NCG * skd; i += kBlock) {
       const int cg = i / skd, j = i % skd;
       float acc = 0.f;
-      for (int c = 0; c < 32; ++c) acc = fmaf(h2f(qg[cg * 32 + c]), a.sketch_proj[c * skd + j], acc);
+      if (qg)
+        for (int c = 0; c < 32; ++c) acc = fmaf(h2f(qg[cg * 32 + c]), a.sketch_proj[c * skd + j], acc);
       s_qs[cg * 64 + j] = acc;
     }
     __syncthreads();

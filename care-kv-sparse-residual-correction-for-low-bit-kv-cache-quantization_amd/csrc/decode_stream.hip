@@ -85,6 +85,7 @@ void decode_stream_kernel(carekv_arena A, DecodeArgs a) {
 
   uint32_t* vt = reinterpret_cast<uint32_t*>(smem) + w * VT_WORDS;
   float m_run = -INFINITY, l_run = 0.f;
+  float x_max = -INFINITY;  // prefill rows with the sketch proxy: the column's largest logit
   int ntok_l = 0;  // prefill rows: tokens the lane's query column sees
   if constexpr (PF) {  // lane column ln (padding columns hold zero queries)
     const PfCol x = pf_col(a, b, kvh, ln);
@@ -152,6 +153,7 @@ void decode_stream_kernel(carekv_arena A, DecodeArgs a) {
     if (a.xbuf && corr && ln < GQ)  // logits for the proxy's margins / the entropy
       *reinterpret_cast<float4*>(a.xbuf + (((long)bk * GQ + ln) * a.Pmax + p) * 16 + 4 * lj) =
           make_float4(x[0], x[1], x[2], x[3]);
+    if constexpr (PF) x_max = fmaxf(x_max, fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])));
     float m_new, f_old;
     if constexpr (PF) {
       m_new = m_run;
@@ -232,6 +234,13 @@ void decode_stream_kernel(carekv_arena A, DecodeArgs a) {
     lds_sync_wave();
   }
 
+  if constexpr (PF) {
+    // s_top of the router's margins (residual_router.py:126): the softmax here
+    // runs against the row's fixed log-sum-exp, so the maximum logit of each
+    // column is kept on the side, per wave
+    x_max = col_max(x_max);
+    if (a.xmax && lj == 0) a.xmax[(((long)bk * a.nsplit + split) * 4 + w) * 16 + ln] = x_max;
+  }
   // ---- merge the 4 waves' (m, l, O) and write the split partial, half
   // of the dims per round; V slot 16t + n (tile t, column n) maps back to dim
   // chunk*CH + slot_code[slot % CH].

@@ -510,16 +510,21 @@ __global__ __launch_bounds__(256) void append_hat_rows_kernel(carekv_arena A, co
   float av = 0.f;
   for (int d = lane; d < D; d += 64) av = fmaxf(av, fabsf(h2f(Vx[(long)row * D + d])));
   const float sv = kivi_scale(wave_max(av), A.hat_bits_v);
+  float vs = 0.f;  // this row's share of the page's sum of V_hat^2
   for (int d = lane; d < D; d += 64) {
     const float k = h2f(Kx[(long)row * D + d]);
     krow[d] = f2h(kivi_value(k, kivi_scale(fabsf(k), A.hat_bits_k), A.hat_bits_k));
-    vrow[d] = f2h(kivi_value(h2f(Vx[(long)row * D + d]), sv, A.hat_bits_v));
+    const uint16_t vh = f2h(kivi_value(h2f(Vx[(long)row * D + d]), sv, A.hat_bits_v));
+    vrow[d] = vh;
+    vs += h2f(vh) * h2f(vh);
   }
+  vs = wave_sum(vs);
   const bool full = off + 1 == kPage;
   if (lane == 0) {
     A.valid[pg] = off + 1;
     if (fresh) A.has_meta[pg] = full ? 1 : 0;
-    if (full) { A.has_meta[pg] = 1; A.v_sq[pg] = 0.f; }
+    if (full) A.has_meta[pg] = 1;
+    A.v_sq[pg] = full ? 0.f : (fresh ? 0.f : A.v_sq[pg]) + vs;
   }
   if (full) {
     // store on page fill with K_orig = K_hat: zero residual -> no slots,
@@ -531,6 +536,18 @@ __global__ __launch_bounds__(256) void append_hat_rows_kernel(carekv_arena A, co
 }
 
 // Decode append: one wave per (row); lane g < D/32 quantizes group g.
+// Int8 page scales (scale_mode 1) take one of two encodings:
+//   * the reference's (cache.py:689-695): the row's scale codes against the
+//     page's fixed master, clamped at 1e-8 -- a page the decode opens keeps
+//     master 0, so its rows read back as zero;
+//   * rescale_open: the page is encoded as write_base encodes a page holding
+//     its valid rows (cache.py:592-604): master = half(max scale / 127) over
+//     the rows so far and every row's code against it, from the fp16 scales
+//     of the open page kept in open_kscale / open_vscale (this row's are
+//     added there).  When the page fills, its bytes are those write_base
+//     gives the 16 rows.
+// The page's sum of V_hat^2 (v_sq, read by the query-aware K score of its
+// stored K slots) is recomputed over the valid rows as they now read back.
 template <int D, int BITS>
 __global__ __launch_bounds__(256) void append_rows_kernel(carekv_arena A, const uint16_t* __restrict__ Kx,
                                                           const uint16_t* __restrict__ Vx,
@@ -545,38 +562,93 @@ __global__ __launch_bounds__(256) void append_rows_kernel(carekv_arena A, const 
   const long pg = ((long)kvh * A.n_seq + seq) * A.max_pages + page;
   const int off = fresh ? 0 : A.valid[pg];
   if (off >= kPage) return;  // caller contract violated; never write past the page
+  const bool i8 = A.scale_mode == 1;
+  const bool rescale = i8 && A.rescale_open != 0;
+  int cv[32];
+  _Float16 sk = (_Float16)0.f, sv = (_Float16)0.f;
   if (lane < NG) {
     const int g = lane;
     float xk[32], xv[32];
-    int ck[32], cv[32];
+    int ck[32];
     for (int i = 0; i < 32; ++i) {
       xk[i] = h2f(Kx[(long)row * D + g * 32 + i]);
       xv[i] = h2f(Vx[(long)row * D + g * 32 + i]);
     }
-    const _Float16 sk = quant_group<BITS>(xk, ck), sv = quant_group<BITS>(xv, cv);
+    sk = quant_group<BITS>(xk, ck);
+    sv = quant_group<BITS>(xv, cv);
     uint32_t w[BITS];
     pack_group<BITS>(ck, w);
     store_bytes<CB>(A.kcodes + (pg * kPage + off) * RB + g * CB, w);
     pack_group<BITS>(cv, w);
     store_bytes<CB>(A.vcodes + (pg * kPage + off) * RB + g * CB, w);
-    if (A.scale_mode == 1) {
-      const float mk = fmaxf(fresh ? 0.f : h2f(A.kmaster[pg]), 1e-8f);
-      const float mv = fmaxf(fresh ? 0.f : h2f(A.vmaster[pg]), 1e-8f);
-      ((int8_t*)A.kscale)[(pg * kPage + off) * NG + g] = scale_code((float)sk, mk);
-      ((int8_t*)A.vscale)[(pg * kPage + off) * NG + g] = scale_code((float)sv, mv);
-    } else {
+    if (!i8) {
       ((uint16_t*)A.kscale)[(pg * kPage + off) * NG + g] = half2bits(sk);
       ((uint16_t*)A.vscale)[(pg * kPage + off) * NG + g] = half2bits(sv);
     }
   }
+  // lane l < 16 NG: row r = l / NG, group gg = l % NG of the page
+  const int r = lane / NG, gg = lane % NG;
+  const bool cell = lane < kPage * NG && r <= off;
+  float mk = 0.f, mv = 0.f;  // the page's masters after this row (int8 scales)
+  if (rescale) {
+    const long ob = ((long)kvh * A.n_seq + seq) * kPage * NG;
+    const float nk = __shfl((float)sk, gg, 64), nv = __shfl((float)sv, gg, 64);
+    float s_k = 0.f, s_v = 0.f;
+    if (cell) {
+      s_k = r < off ? h2f(A.open_kscale[ob + r * NG + gg]) : nk;
+      s_v = r < off ? h2f(A.open_vscale[ob + r * NG + gg]) : nv;
+    }
+    mk = (float)(_Float16)(wave_max(s_k) / 127.f);
+    mv = (float)(_Float16)(wave_max(s_v) / 127.f);
+    if (cell) {
+      ((int8_t*)A.kscale)[(pg * kPage + r) * NG + gg] = scale_code(s_k, mk);
+      ((int8_t*)A.vscale)[(pg * kPage + r) * NG + gg] = scale_code(s_v, mv);
+    }
+    if (lane < NG) {
+      A.open_kscale[ob + off * NG + lane] = half2bits(sk);
+      A.open_vscale[ob + off * NG + lane] = half2bits(sv);
+    }
+  } else if (i8) {
+    mk = fmaxf(fresh ? 0.f : h2f(A.kmaster[pg]), 1e-8f);
+    mv = fmaxf(fresh ? 0.f : h2f(A.vmaster[pg]), 1e-8f);
+    if (lane < NG) {
+      ((int8_t*)A.kscale)[(pg * kPage + off) * NG + lane] = scale_code((float)sk, mk);
+      ((int8_t*)A.vscale)[(pg * kPage + off) * NG + lane] = scale_code((float)sv, mv);
+    }
+  }
+  // sum of V_hat^2 over the valid rows: earlier rows from the page, this row
+  // from the registers of lanes g < NG
+  float vs = 0.f;
+  if (lane < NG) {
+    _Float16 s = sv;
+    if (i8) s = (_Float16)((float)scale_code((float)sv, mv) * (rescale ? mv : (fresh ? 0.f : h2f(A.vmaster[pg]))));
+#pragma unroll
+    for (int i = 0; i < 32; ++i) { const float x = (float)dq(cv[i], s); vs += x * x; }
+  }
+  if (cell && r < off) {
+    uint32_t w[BITS];
+    load_bytes<CB>(w, A.vcodes + (pg * kPage + r) * RB + gg * CB);
+    _Float16 s;
+    if (i8) {
+      const int8_t q = ((const int8_t*)A.vscale)[(pg * kPage + r) * NG + gg];
+      s = (_Float16)((float)(rescale ? scale_code(h2f(A.open_vscale[((long)kvh * A.n_seq + seq) * kPage * NG +
+                                                                    r * NG + gg]), mv) : q) *
+                     (rescale ? mv : h2f(A.vmaster[pg])));
+    } else {
+      s = bits2half(((const uint16_t*)A.vscale)[(pg * kPage + r) * NG + gg]);
+    }
+#pragma unroll
+    for (int i = 0; i < 32; ++i) { const float x = (float)dq(get_code<BITS>(w, i), s); vs += x * x; }
+  }
+  vs = wave_sum(vs);
   const bool full = off + 1 == kPage;
   if (lane == 0) {
     A.valid[pg] = off + 1;
-    if (fresh) {
-      if (A.scale_mode == 1) { A.kmaster[pg] = 0; A.vmaster[pg] = 0; }
-      A.has_meta[pg] = full ? 1 : 0;
-    }
-    if (full) { A.has_meta[pg] = 1; A.v_sq[pg] = 0.f; }
+    if (rescale) { A.kmaster[pg] = half2bits((_Float16)mk); A.vmaster[pg] = half2bits((_Float16)mv); }
+    else if (fresh && i8) { A.kmaster[pg] = 0; A.vmaster[pg] = 0; }
+    if (fresh) A.has_meta[pg] = full ? 1 : 0;
+    if (full) A.has_meta[pg] = 1;
+    A.v_sq[pg] = full ? 0.f : vs;
   }
   if (full) {
     // store on page fill with K_orig = K_hat: zero residual -> no slots,

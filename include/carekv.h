@@ -72,6 +72,17 @@ typedef struct carekv_arena {
   int32_t k_channel_group, v_token_block, sketch_dim, scale_mode, residual_bits, n_slots;
   int32_t hat_bits_k, hat_bits_v; /* base_bits = 16: the KIVI bits of a decode
                                    * append's K and V row (layer.py:197-202)  */
+  /* Decode appends into int8-scale pages (scale_mode 1).  rescale_open = 0:
+   * the reference's encoding, the row's scale codes against the page's fixed
+   * master (cache.py:689-695; a page the decode opens keeps master 0 and its
+   * rows read back as zero).  rescale_open = 1 (no reference counterpart):
+   * the open page is re-encoded as write_base encodes its valid rows, from
+   * their fp16 group scales in open_kscale / open_vscale, fp16
+   * [n_kv_heads][n_seq][page_size][D/group] (the prompt writer fills the
+   * rows of a partial last page, the append adds its row). */
+  uint16_t* open_kscale;
+  uint16_t* open_vscale;
+  int32_t rescale_open;
 } carekv_arena;
 
 /* Store-time knobs, resolved on the host from CacheConfig and the

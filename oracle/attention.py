@@ -436,7 +436,8 @@ def decode_attention(cache: OCache, layer_id, Qh, page_ids_by_kvh=None, correcti
     return out
 
 
-def prefill_stored(cache: OCache, layer_id, Qh, K_hat, V_hat, correction=True, diag=None, **corr_kw):
+def prefill_stored(cache: OCache, layer_id, Qh, K_hat, V_hat, correction=True, diag=None, force_sel=None,
+                   **corr_kw):
     """Prefill attention of ``CAREKVLayer.prefill`` in carekv_stored mode
     (layer.py:780-838) with the vectorized correction (layer.py:538-557).
 
@@ -448,7 +449,8 @@ def prefill_stored(cache: OCache, layer_id, Qh, K_hat, V_hat, correction=True, d
     kv_group x T queries (head-major) against every page of the kv head,
     out = half(O_base + delta).  ``correction=False`` or no read budget gives
     the base (the any_read_budget short-circuit, layer.py:810-823).
-    Returns (T, Hq, D) fp16."""
+    ``force_sel``: {kv head: (sel_k, sel_v)} replaces the selection of those
+    kv heads (rows head-major, as the diag).  Returns (T, Hq, D) fp16."""
     cfg = cache.cfg
     Qh = np.asarray(Qh, F16)
     Hq, T, D = Qh.shape
@@ -477,7 +479,8 @@ def prefill_stored(cache: OCache, layer_id, Qh, K_hat, V_hat, correction=True, d
         d = None if diag is None else diag.setdefault(h, {})
         delta = vectorized_joint_correction(cache, layer_id, h, pids, Qg.reshape(-1, D), S.reshape(-1, T),
                                             A.astype(F32).reshape(-1, T), Vf, O_base.astype(F32).reshape(-1, D),
-                                            diag=d, **corr_kw)
+                                            diag=d, force_sel=None if force_sel is None else force_sel.get(h),
+                                            **corr_kw)
         out[heads] = (O_base.astype(F32) + delta.reshape(grp, T, D)).astype(F16)
         if d is not None:
             d.update(S=S.reshape(-1, T), A=A.astype(F32).reshape(-1, T), V_hat=Vf, K_hat=Kf)

@@ -130,6 +130,7 @@ class OCache:
         else:
             self.base_K_hat_fp16 = self.base_V_hat_fp16 = None
         self.open_rows = {}  # (layer, kv head, page) -> true K / V rows of an open page (streaming store)
+        self.open_scales = {}  # (layer, kv head, page) -> fp16 group scales of an open page's rows (re-encoding)
         if max_slots is None:                                   # cache.py:507-509
             ratio_est = int(P * H * L * cfg.store_budget_ratio * 4)
             abs_est = int(P * H * L * (cfg.store_abs_k + cfg.store_abs_v) * 2)

@@ -199,14 +199,16 @@ def write_pages_for_kv_head(cache: OCache, layer_id: int, kv_h: int, K_kv, V_kv,
         process_page(cache, layer_id, kv_h, pid, Kp, Vp, Kc, Ks, Vc, Vs,
                      token_start=token_start_abs + t0, num_valid=nv,
                      is_recent=is_recent, is_sink=is_sink, P=P, **store_kw)
-        if nv < ps:  # the open page's true rows, for a streaming fill store
+        if nv < ps:  # the open page's true rows and fp16 group scales (streaming store, re-encoding append)
             cache.open_rows[(layer_id, kv_h, pid)] = (Kp.copy(), Vp.copy())
+            cache.open_scales[(layer_id, kv_h, pid)] = (np.asarray(Ks, F16)[:nv].copy(), np.asarray(Vs, F16)[:nv].copy())
         k_hat.append(Q.dequantize(Kc, Ks, cfg.group_size).astype(K_kv.dtype)[:nv])
         v_hat.append(Q.dequantize(Vc, Vs, cfg.group_size).astype(V_kv.dtype)[:nv])
     return np.concatenate(k_hat), np.concatenate(v_hat)
 
 
-def decode_append(cache: OCache, layer_id: int, k_rows, v_rows, streaming: bool = False, **store_kw):
+def decode_append(cache: OCache, layer_id: int, k_rows, v_rows, streaming: bool = False, rescale: bool = False,
+                  **store_kw):
     """Cache side of ``CAREKVLayer.decode_step`` (``layer.py:1001-1146``,
     uniform base quantizer): append one token per kv head into the open page
     (allocating one when full) and, when the append fills the page, run the
@@ -217,7 +219,15 @@ def decode_append(cache: OCache, layer_id: int, k_rows, v_rows, streaming: bool 
     page's true rows are kept (``cache.open_rows``, the prompt's partial last
     page included) and the fill store runs process_page on them against the
     page's own codes and read-back scales (the page's K_hat / V_hat rows for
-    the side-buffer base), so decode-filled pages get residual slots."""
+    the side-buffer base), so decode-filled pages get residual slots.
+
+    ``rescale=True`` (no reference counterpart; int8 page scales): instead of
+    encoding the row's scales against the page's fixed master
+    (``cache.py:689-695``, zero on a page the decode opened), the open page
+    is re-encoded as ``write_base`` encodes its valid rows so far
+    (``write_scale_page`` over their fp16 group scales, ``cache.py:592-604``).
+    Together with ``streaming=True`` this is the decode path of a cache
+    built with ``compat=False``."""
     cfg = cache.cfg
     k_rows = np.asarray(k_rows)
     v_rows = np.asarray(v_rows)
@@ -251,7 +261,20 @@ def decode_append(cache: OCache, layer_id: int, k_rows, v_rows, streaming: bool 
             continue
         kc, ks = Q.quantize(k_rows[h:h + 1], cfg.base_bits, cfg.group_size)
         vc, vs = Q.quantize(v_rows[h:h + 1], cfg.base_bits, cfg.group_size)
-        cache.append_to_page(layer_id, h, pid, kc[0], ks[0], vc[0], vs[0])
+        off = cache.append_to_page(layer_id, h, pid, kc[0], ks[0], vc[0], vs[0])
+        if rescale and cfg.scale_quant == "int8":
+            G = cfg.head_dim // cfg.group_size
+            oks, ovs = cache.open_scales.get((layer_id, h, pid), (np.zeros((0, G), F16), np.zeros((0, G), F16)))
+            oks = np.concatenate([oks[:off], np.asarray(ks, F16)[:1]])
+            ovs = np.concatenate([ovs[:off], np.asarray(vs, F16)[:1]])
+            cache.open_scales[(layer_id, h, pid)] = (oks, ovs)
+            for S, dst, mst in ((oks, cache.base_K_scale, cache.base_K_scale_master),
+                                (ovs, cache.base_V_scale, cache.base_V_scale_master)):
+                codes, master = Q.write_scale_page(S)
+                dst[layer_id, h, pid, :off + 1] = codes
+                mst[layer_id, h, pid] = master
+            if off + 1 == ps:
+                cache.open_scales.pop((layer_id, h, pid), None)
         if int(cache.valid_tokens[layer_id, h, pid]) == ps:
             Kc = cache.unpack_rows(cache.base_K_codes[layer_id, h, pid])
             Vc = cache.unpack_rows(cache.base_V_codes[layer_id, h, pid])

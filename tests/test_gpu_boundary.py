@@ -77,7 +77,8 @@ def test_layer_prefill_matches_oracle(monkeypatch, mode):
 
 
 def test_layer_prefill_carekv_stored_matches_reference(monkeypatch):
-    """CAREKVLayer.prefill in carekv_stored mode (layer.py:780-838) on the
+    """CAREKVLayer.prefill in carekv_stored mode with correction_impl =
+    vectorized (layer.py:538-557, 780-838; the golden's setting) on the
     reference prefill golden: identity projections pick q / k / v out of
     hidden = [q; k; v] and W_O returns the attention output (both exact in
     fp16), so the layer output is the corrected attention itself."""
@@ -91,7 +92,7 @@ def test_layer_prefill_carekv_stored_matches_reference(monkeypatch):
     g = load_golden("prefill_gqa8_d64.npz")
     spec = PREFILL_CASES["gqa8_d64"]
     cfg = care_kv.CacheConfig(packed_base=True, scale_quant="int8", read_budget_ratio=0.0,
-                              **prefill_cfg_kwargs(g, spec))
+                              correction_impl="vectorized", **prefill_cfg_kwargs(g, spec))
     T, Hq, Hkv, D = int(g["T"]), spec["Hq"], spec["Hkv"], spec["D"]
     nq, nk = Hq * D, Hkv * D
     eye = torch.eye(nq + 2 * nk, dtype=torch.float16, device="cuda")
@@ -220,7 +221,9 @@ def test_adapter_patches_a_given_model(monkeypatch):
     care_kv.layer._warned.clear()
     m = a.setup_model(_tiny_llama(2))
     ids = torch.randint(0, 1000, (1, 20), generator=torch.Generator().manual_seed(3)).cuda()
-    with pytest.warns(RuntimeWarning):
+    import warnings
+    with warnings.catch_warnings():
+        warnings.simplefilter("error", RuntimeWarning)  # the default cached path is built: no fallback warning
         with torch.no_grad():
             logits = m(ids).logits
     assert torch.isfinite(logits.float()).all()
@@ -246,7 +249,7 @@ def test_layer_decode_step_matches_reference(monkeypatch, name):
     print(f"layer decode_step golden {name}", flush=True)
     g = load_golden(f"decode_{name}.npz")
     spec = DECODE_CASES[name]
-    cfg = care_kv.CacheConfig(packed_base=True, scale_quant="int8", read_budget_ratio=0.0,
+    cfg = care_kv.CacheConfig(packed_base=True, scale_quant="int8", read_budget_ratio=0.0, compat=True,
                               **case_cfg_kwargs(g, spec))
     T, n_app = int(g["T"]), int(g["n_append"])
     Hq, Hkv, D = spec["Hq"], spec["Hkv"], spec["D"]
@@ -266,5 +269,48 @@ def test_layer_decode_step_matches_reference(monkeypatch, name):
     err = np.abs(got - ref)
     assert np.all(err <= np.maximum(2e-3, np.spacing(np.abs(g["decode_step_out"])).astype(np.float32))), err.max()
     # the cache after the appends equals the reference's, byte for byte
+    from test_gpu_parity import compare_cache_to_golden
+    compare_cache_to_golden(cache, g)
+
+
+@pytest.mark.parametrize("name,Hq,D,k_mode,policy",
+                         [("gqa4_d128", 8, 128, "exact", "joint"), ("gqa8_d64_linear", 16, 64, "linear", "separate")])
+def test_layer_decode_step_corrected_matches_reference(monkeypatch, name, Hq, D, k_mode, policy):
+    """compat=True: CAREKVLayer.decode_step with the reference's correction
+    gate open (read_budget_ratio > 0, attention.py:1025) selects through the
+    router's sketch-proxy score (apply_slot_corrections over
+    ResidualRouter.route; CAREKV_KSCORE_LIVE=1 is set and ignored, as in the
+    reference) and gives every one of the reference's decode steps within
+    the decode bar: the prompt's partial page filled by the appends, a
+    decode-opened page with its zero master, a page filled by decode."""
+    import care_kv
+    from helpers import PAPER_ENV, load_golden
+    for k, v in PAPER_ENV.items():
+        monkeypatch.setenv(k, v)
+    monkeypatch.setenv("CAREKV_K_CORRECTION_MODE", k_mode)
+    print(f"layer decode_step corrected golden {name}", flush=True)
+    g = load_golden(f"decode_step_{name}.npz")
+    T, n = int(g["T"]), int(g["n_append"])
+    store = (dict(store_budget_mode="absolute", store_abs_k=2, store_abs_v=4) if name == "gqa4_d128"
+             else dict(store_budget_mode="ratio", store_budget_ratio=0.03))
+    Hkv = 2
+    cfg = care_kv.CacheConfig(num_layers=1, num_heads=Hq, num_kv_heads=Hkv, head_dim=D, page_size=16,
+                              max_pages=T // 16 + n // 16 + 4, base_bits=3, group_size=32, k_channel_group=32,
+                              v_token_block=4, sketch_dim=32, packed_base=True, scale_quant="int8",
+                              read_budget_ratio=0.03, read_budget_mode="absolute", read_abs_k=int(g["read_k"]),
+                              read_abs_v=int(g["read_v"]), route_policy=policy, compat=True, **store)
+    nq, nk = Hq * D, Hkv * D
+    eye = torch.eye(nq + 2 * nk, dtype=torch.float16, device="cuda")
+    lay = care_kv.CAREKVLayer(cfg, 0, eye[:nq].contiguous(), eye[nq:nq + nk].contiguous(),
+                              eye[nq + nk:].contiguous(), eye[:, :nq].contiguous())
+    K, V, Qall = (torch.from_numpy(g[x]).cuda() for x in ("K", "V", "Qall"))
+    cache = care_kv.CAREKVCache(cfg, n_seq=1)
+    cache.write_prefill(0, K[:, :T], V[:, :T])
+    for i, t in enumerate(range(T, T + n)):
+        hidden = torch.cat([Qall[i].reshape(-1), K[:, t].reshape(-1), V[:, t].reshape(-1)])[None]
+        got = lay.decode_step(cache, hidden)[0, :nq].reshape(Hq, D).float().cpu().numpy()
+        ref = g["outs"][i]
+        err = np.abs(got - ref.astype(np.float32))
+        assert np.all(err <= np.maximum(2e-3, np.spacing(np.abs(ref)).astype(np.float32))), (i, err.max())
     from test_gpu_parity import compare_cache_to_golden
     compare_cache_to_golden(cache, g)

@@ -3,10 +3,11 @@
 * ``carekv_quantize_rows`` + ``carekv_dequantize_rows`` reproduce
   ``quantize`` / ``dequantize`` (quantizer.py:31-82) bit for bit.
 * ``carekv_prefill_attn`` reproduces ``_causal_attention_pure``
-  (layer.py:935-972): every output element within
-  ``2e-3 * v_scale + 1e-2 * |ref|`` of the oracle, where v_scale is
-  max(1, rms of V) (the bar is max-abs 2e-3 / rel 1e-2 on unit-scale data);
-  the log-sum-exp within 1e-3 absolute.
+  (layer.py:935-972): every output element within max-abs 2e-3 (or one fp16
+  ulp of the reference where that is larger) and the output within
+  relative L2 1e-2 of the oracle; for V with per-channel log-normal scales
+  (config 4) the absolute bar is 2e-3 times the rms of V; the log-sum-exp
+  within 1e-3 absolute.
 """
 import math
 
@@ -38,14 +39,17 @@ def _inputs(B, Hq, Hkv, T, D, seed, v_lognormal=False):
     return q, k, v.half()
 
 
-def _check(out, ref, v):
+def _check(out, ref, v, lognormal=False):
+    ulp = np.spacing(np.abs(ref.astype(F16))).astype(F32)
     out = out.astype(F32)
     ref = ref.astype(F32)
-    vs = max(1.0, float(np.sqrt(np.mean(v.astype(F32) ** 2))))
+    vs = max(1.0, float(np.sqrt(np.mean(v.astype(F32) ** 2)))) if lognormal else 1.0
     err = np.abs(out - ref)
-    bound = 2e-3 * vs + 1e-2 * np.abs(ref)
+    bound = np.maximum(2e-3 * vs, ulp)
     assert np.isfinite(out).all()
     assert (err <= bound).all(), f"max err {err.max():.3e}, worst ratio {(err / bound).max():.2f}"
+    rel = float(np.linalg.norm(out - ref) / max(np.linalg.norm(ref), 1e-30))
+    assert rel <= 1e-2, rel
 
 
 PREFILL_CASES = [
@@ -71,7 +75,7 @@ def test_prefill_attention_vs_oracle(case):
     out, lse = out.cpu().numpy(), lse.cpu().numpy()
     for b in range(B):
         ref, ref_lse = causal_attention_pure(q[b].numpy(), k[b].numpy(), v[b].numpy(), causal=causal)
-        _check(out[b], ref, v[b].numpy())
+        _check(out[b], ref, v[b].numpy(), logn)
         assert np.abs(lse[b] - ref_lse).max() < 1e-3
 
 

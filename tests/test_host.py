@@ -176,8 +176,9 @@ def test_prefill_mode_resolution(monkeypatch):
 def test_prefill_correct_rejects_bad_rows():
     """carekv_prefill_correct_workspace_bytes validates the prompt rows and
     the read knobs on the host (no device call): rows outside the prompt, a
-    prompt longer than the arena, the sketch proxy and correction off are
-    refused with -1; a valid request sizes the workspace."""
+    prompt longer than the arena and correction off are refused with -1; a
+    valid request sizes the workspace, with the sketch proxy (the router of
+    correction_impl=cached) larger by its records and per-wave maxima."""
     import ctypes as C
     _lib = _ensure_built()
     lib = _lib.load()
@@ -195,7 +196,8 @@ def test_prefill_correct_rejects_bad_rows():
     assert ws(n_tokens=16 * 8 + 1, n_rows=1) == -1  # more pages than the arena row
     assert ws(seq=2) == -1                         # no such sequence slot
     assert ws(k_hat=0) == -1                       # missing K_hat
+    live = ws()
     dp.k_proxy = 1
-    assert ws() == -1                              # the sketch proxy is not built for prompt rows
+    assert ws() > live                             # the router's proxy records and logit maxima
     dp.k_proxy, dp.correction = 0, 0
     assert ws() == -1                              # the pass is the correction

@@ -639,3 +639,52 @@ def test_streaming_fill_store_residuals_are_true_minus_base():
                     assert np.array_equal(c.v_residual_buf[slot], packed), (p, vb)
                     assert c.v_residual_scale[slot, 0] == scale, (p, vb)
         assert sum(s >= 0 for s in m.k_residual_slots) == 2 and sum(s >= 0 for s in m.v_residual_slots) == 4
+
+
+def test_reencoding_append_matches_write_base():
+    """decode_append(rescale=True) (the compat=False append; no reference
+    counterpart): after 16 appends a decode-opened page holds exactly the
+    codes, int8 scale codes and master that write_base gives those 16 rows
+    (cache.py:592-654); the prompt's partial page, refilled by the appends,
+    holds what write_base gives its 16 rows; an open page reads back within
+    INT3 quantisation error of its rows (the reference's encoding reads a
+    decode-opened page back as zeros)."""
+    rng = np.random.default_rng(11)
+    D, T, n = 64, 20, 30
+    K = (rng.standard_normal((1, T + n, D)) * np.exp(rng.standard_normal((1, 1, D)))).astype(F16)
+    V = rng.standard_normal((1, T + n, D)).astype(F16)
+    kw = dict(num_layers=1, num_heads=2, num_kv_heads=1, head_dim=D, page_size=16, max_pages=8, base_bits=3,
+              group_size=32, k_channel_group=32, v_token_block=4, sketch_dim=32, store_budget_mode="absolute",
+              store_abs_k=1, store_abs_v=1)
+    c = OCache(OCfg(**kw))
+    ref = OCache(OCfg(**kw))
+    write_pages_for_kv_head(c, 0, 0, K[0, :T], V[0, :T])
+    for t in range(T, T + n):
+        decode_append(c, 0, K[:, t], V[:, t], rescale=True)
+        if t == T + 20:  # page 2 (tokens 32..47) is open with 9 rows: check its first 5
+            p, nv = 2, 5
+            rows = slice(32, 32 + nv)
+            for X, codes, which in ((K, c.base_K_codes, "K"), (V, c.base_V_codes, "V")):
+                got = Q.dequantize(c.unpack_rows(codes[0, 0, p])[:nv], c.page_scales(0, 0, p, which)[:nv], 32)
+                want = Q.dequantize(*Q.quantize(X[0, rows], 3, 32), 32)  # INT3 with fp16 scales
+                err = np.abs(got.astype(F32) - X[0, rows].astype(F32))
+                bound = np.abs(X[0, rows].astype(F32)).reshape(nv, -1, 32).max(-1).repeat(32, -1) / 3 * 0.51 + 1e-3
+                assert np.all(err <= bound * 1.1) and np.abs(got).max() > 0, which
+                assert np.abs(got.astype(F32) - want.astype(F32)).max() <= 0.05 * np.abs(want).max(), which
+    for p in (1, 2):  # page 1: prompt rows 16..19 + appends; page 2: decode-opened
+        rows = slice(p * 16, p * 16 + 16)
+        pid = ref.alloc_page(0, 0)
+        Kc, Ks = Q.quantize(K[0, rows], 3, 32)
+        Vc, Vs = Q.quantize(V[0, rows], 3, 32)
+        ref.write_base(0, 0, pid, Kc, Ks, Vc, Vs, num_valid=16)
+        for a, b in ((c.base_K_codes, ref.base_K_codes), (c.base_V_codes, ref.base_V_codes),
+                     (c.base_K_scale, ref.base_K_scale), (c.base_V_scale, ref.base_V_scale)):
+            assert np.array_equal(a[0, 0, p], b[0, 0, pid]), p
+        assert c.base_K_scale_master[0, 0, p] == ref.base_K_scale_master[0, 0, pid]
+        assert c.base_V_scale_master[0, 0, p] == ref.base_V_scale_master[0, 0, pid]
+    # the reference's encoding: a decode-opened page reads back as zeros
+    z = OCache(OCfg(**kw))
+    write_pages_for_kv_head(z, 0, 0, K[0, :T], V[0, :T])
+    for t in range(T, T + 20):
+        decode_append(z, 0, K[:, t], V[:, t])
+    assert np.all(Q.dequantize(z.unpack_rows(z.base_K_codes[0, 0, 2])[:4], z.page_scales(0, 0, 2, "K")[:4], 32) == 0)
