@@ -35,7 +35,8 @@ class StoreParams(C.Structure):
     _fields_ = [("k_budget", C.c_int32), ("v_budget", C.c_int32), ("joint_budget", C.c_int32),
                 ("joint", C.c_int32), ("store_none", C.c_int32), ("sensitivity", C.c_double),
                 ("sink_tokens", C.c_int32), ("sketch_proj", C.c_void_p), ("k_hat", C.c_void_p),
-                ("v_hat", C.c_void_p), ("keep_base", C.c_int32)]
+                ("v_hat", C.c_void_p), ("keep_base", C.c_int32), ("k_codes_in", C.c_void_p),
+                ("k_scale_in", C.c_void_p), ("v_codes_in", C.c_void_p), ("v_scale_in", C.c_void_p)]
 
 
 class DecodeParams(C.Structure):
@@ -47,7 +48,8 @@ class DecodeParams(C.Structure):
                 ("ratio_k", C.c_double), ("ratio_v", C.c_double), ("k_cap", C.c_int32), ("v_cap", C.c_int32),
                 ("split_pages", C.c_int32), ("phase_events", C.c_void_p), ("k_proxy", C.c_int32),
                 ("sketch_proj", C.c_void_p), ("route_policy", C.c_int32), ("adaptive_score", C.c_int32),
-                ("rel_threshold", C.c_double), ("abs_threshold", C.c_double), ("min_keep", C.c_int32)]
+                ("rel_threshold", C.c_double), ("abs_threshold", C.c_double), ("min_keep", C.c_int32),
+                ("read_counts", C.c_void_p)]
 
 
 class PrefillParams(C.Structure):
@@ -66,7 +68,9 @@ PAGE_JOB_INTS = 6
 EXPORTS = ["carekv_store_pages", "carekv_store_workspace_bytes", "carekv_append_rows", "carekv_decode_attn",
            "carekv_decode_workspace_bytes", "carekv_read_pages", "carekv_quantize_rows", "carekv_prefill_attn",
            "carekv_dequantize_rows", "carekv_kivi_qdq", "carekv_prefill_correct",
-           "carekv_prefill_correct_workspace_bytes", "carekv_decode_attn_static", "carekv_last_error"]
+           "carekv_prefill_correct_workspace_bytes", "carekv_decode_attn_static", "carekv_write_base", "carekv_append_coded_rows",
+           "carekv_pack_codes", "carekv_unpack_codes", "carekv_pack_4bit", "carekv_unpack_4bit",
+           "carekv_quantize_rows_f32", "carekv_dequantize_rows_f32", "carekv_last_error"]
 
 # bytes of the per-GPU static workspace of carekv_decode_attn_static
 # (CAREKV_STATIC_SCRATCH_BYTES in include/carekv.h)
@@ -103,7 +107,9 @@ def load(path: str | None = None):
         lib.carekv_decode_attn_static.restype = C.c_int
         lib.carekv_decode_attn_static.argtypes = [C.POINTER(Arena), C.POINTER(DecodeParams), vp, vp, vp, i32, vp]
         lib.carekv_read_pages.restype = C.c_int
-        lib.carekv_read_pages.argtypes = [C.POINTER(Arena), i32, i32, i32, vp, vp, vp, vp, vp, vp]
+        lib.carekv_read_pages.argtypes = [C.POINTER(Arena), i32, i32, i32, vp, vp, vp, vp, vp, vp, vp]
+        lib.carekv_append_coded_rows.restype = C.c_int
+        lib.carekv_append_coded_rows.argtypes = [C.POINTER(Arena), vp, vp, vp, vp, vp, i32, vp]
         lib.carekv_quantize_rows.restype = C.c_int
         lib.carekv_quantize_rows.argtypes = [vp, i32, i32, i32, i32, i32, vp, vp, vp]
         lib.carekv_prefill_attn.restype = C.c_int
@@ -116,6 +122,19 @@ def load(path: str | None = None):
         lib.carekv_prefill_correct.restype = C.c_int
         lib.carekv_prefill_correct.argtypes = [C.POINTER(Arena), C.POINTER(DecodeParams),
                                                C.POINTER(PrefillCorrParams), vp, vp, vp, i64, vp, i32, vp]
+        lib.carekv_write_base.restype = C.c_int
+        lib.carekv_write_base.argtypes = [C.POINTER(Arena), i32, i32, i32, vp, vp, vp, vp, i32, vp]
+        for nm in ("carekv_pack_codes", "carekv_unpack_codes"):
+            getattr(lib, nm).restype = C.c_int
+            getattr(lib, nm).argtypes = [vp, i64, i32, i32, vp, vp]
+        lib.carekv_pack_4bit.restype = C.c_int
+        lib.carekv_pack_4bit.argtypes = [vp, i32, i64, vp, vp, vp]
+        lib.carekv_unpack_4bit.restype = C.c_int
+        lib.carekv_unpack_4bit.argtypes = [vp, vp, i64, vp, vp]
+        lib.carekv_quantize_rows_f32.restype = C.c_int
+        lib.carekv_quantize_rows_f32.argtypes = [vp, i64, i32, i32, i32, vp, vp, vp]
+        lib.carekv_dequantize_rows_f32.restype = C.c_int
+        lib.carekv_dequantize_rows_f32.argtypes = [vp, vp, i64, i32, i32, vp, vp]
         lib.carekv_kivi_qdq.restype = C.c_int
         lib.carekv_kivi_qdq.argtypes = [vp, i32, i32, i32, i32, i32, vp, vp]
         _lib = lib

@@ -82,6 +82,8 @@ class CAREKVAdapter:
     def setup_model(self, model_id: Union[str, nn.Module]):
         """carekv_adapter.py:101-172: set the environment, load (a local
         checkpoint path, fp16) or take the given model, patch it."""
+        from .attention import reset_debug_stats
+        reset_debug_stats()
         for k, v in self.env().items():
             os.environ[k] = v
         torch.manual_seed(0)
@@ -107,7 +109,11 @@ class CAREKVAdapter:
         return m
 
     def collect_debug_stats(self):
-        """carekv_adapter.py:174-181 (slot reads are not counted on device)."""
+        """carekv_adapter.py:174-181: the K / V slots the correction read
+        (device counters, CAREKV_DEBUG_STATS=1 as setup_model sets it) and the
+        slots the store holds."""
+        from .attention import get_debug_stats
+        st = get_debug_stats()
         sk = sv = 0
         if self.model is not None:
             for mod in self.model.modules():
@@ -118,7 +124,8 @@ class CAREKVAdapter:
                         sk += k
                         sv += v
                     break
-        return dict(k_reads=0, v_reads=0, stored_k_slots=int(sk), stored_v_slots=int(sv))
+        return dict(k_reads=int(st["k_slots_read"]), v_reads=int(st["v_slots_read"]), stored_k_slots=int(sk),
+                    stored_v_slots=int(sv))
 
     def estimate_memory(self, seq_len: int, num_layers: int = 22, hkv: int = 4, head_dim: int = 64):
         """carekv_adapter.py:183-223, uniform base."""

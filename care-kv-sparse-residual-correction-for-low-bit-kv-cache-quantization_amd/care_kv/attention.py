@@ -27,6 +27,49 @@ from .config import CacheConfig, ReadKnobs, any_read_budget, resolve_read_knobs
 
 KIND_CODE = {"both": 0, "k": 1, "v": 2}
 
+# ------------------------------------------------------------------ debug stats
+# Process-global read counters (layer.py:90-126): with CAREKV_DEBUG_STATS=1
+# every decode / prefill-correction launch adds, on the device, the K slots
+# and V blocks it selected and the queries it corrected (the select kernel's
+# atomics); get_debug_stats reads them back.
+_READ_COUNTS: dict = {}
+
+
+def debug_stats_enabled() -> bool:
+    """layer.py:116-117."""
+    return os.environ.get("CAREKV_DEBUG_STATS", "0") == "1"
+
+
+def _read_counts_ptr(device) -> int:
+    if not debug_stats_enabled():
+        return 0
+    key = str(device)
+    t = _READ_COUNTS.get(key)
+    if t is None:
+        t = torch.zeros(3, dtype=torch.int64, device=device)
+        _READ_COUNTS[key] = t
+    return t.data_ptr()
+
+
+def get_debug_stats() -> dict:
+    """layer.py:120-121: a snapshot of the debug counters (reads the device
+    counters back).  k_slots_read / v_slots_read / n_queries are counted on
+    the device; the delta-norm sums of the reference's per-query path are not
+    accumulated (0.0)."""
+    k = v = n = 0
+    for t in _READ_COUNTS.values():
+        a, b, c = (int(x) for x in t.tolist())
+        k, v, n = k + a, v + b, n + c
+    return {"v_slots_read": v, "k_slots_read": k, "n_queries": n, "delta_v_norm_sum": 0.0,
+            "delta_k_norm_sum": 0.0, "delta_o_norm_sum": 0.0, "o_base_norm_sum": 0.0, "imp_gini_sum": 0.0,
+            "imp_norm_entropy_sum": 0.0, "imp_top1pct_mass_sum": 0.0, "imp_count": 0}
+
+
+def reset_debug_stats() -> None:
+    """layer.py:123-126."""
+    for t in _READ_COUNTS.values():
+        t.zero_()
+
 
 def decode_read_mode(cfg: CacheConfig, layer: int):
     """(correction on, read knobs) of a decode step through
@@ -123,6 +166,7 @@ def prefill_correction(cache: CAREKVCache, layer: int, q: torch.Tensor, k_hat: t
     if not knobs.kscore_live:  # the router's sketch-proxy K score
         dp.k_proxy = 1
         dp.sketch_proj = get_sketch_proj(cfg.head_dim, cfg.k_channel_group, cfg.sketch_dim, dev).data_ptr()
+    dp.read_counts = _read_counts_ptr(dev)
     for r0 in range(0, T, rows_per_call):
         n = min(rows_per_call, T - r0)
         pp = _lib.PrefillCorrParams(seq=seq, n_tokens=T, row_begin=r0, n_rows=n, k_hat=k_hat.data_ptr(),
@@ -143,7 +187,7 @@ def prefill_correction(cache: CAREKVCache, layer: int, q: torch.Tensor, k_hat: t
 def decode_attention(cache: CAREKVCache, layer: int, q: torch.Tensor, seqs: Optional[Sequence[int]] = None, *,
                      correction: bool = True, knobs: Optional[ReadKnobs] = None, split_pages: Optional[int] = None,
                      diag_cap: int = 0, out: Optional[torch.Tensor] = None, phase_events=None,
-                     no_alloc: bool = False):
+                     no_alloc: bool = False, n_pages: Optional[Sequence[int]] = None, count_reads: bool = True):
     """q: (B, Hq, D) fp16 post-RoPE queries of B sequences -> (B, Hq, D) fp16.
 
     With ``diag_cap > 0`` also returns the selected candidates per query
@@ -155,7 +199,9 @@ def decode_attention(cache: CAREKVCache, layer: int, q: torch.Tensor, seqs: Opti
     ``no_alloc``: run through ``carekv_decode_attn_static``, whose workspace
     is the library's per-GPU static array (at most
     ``_lib.STATIC_SCRATCH_BYTES``) instead of a buffer the cache owns; the
-    library call then allocates nothing (pass ``out``)."""
+    library call then allocates nothing (pass ``out``).  ``n_pages``: per
+    sequence, attend to its first n pages only (default: all of them).
+    ``count_reads=False`` keeps the launch out of the debug read counters."""
     cfg: CacheConfig = cache.cfg
     if q.dim() == 2:
         q = q.unsqueeze(0)
@@ -166,6 +212,8 @@ def decode_attention(cache: CAREKVCache, layer: int, q: torch.Tensor, seqs: Opti
         knobs = resolve_read_knobs(cfg, layer)
     q = q.to(torch.float16).contiguous()
     npages = np.array([cache.num_pages(layer, 0, s) for s in seqs], dtype=np.int32)
+    if n_pages is not None:
+        npages = np.minimum(npages, np.asarray(list(n_pages), dtype=np.int32))
     max_np = int(npages.max()) if B else 0
     dev = cache.device
     key = (tuple(seqs), npages.tobytes())
@@ -183,6 +231,8 @@ def decode_attention(cache: CAREKVCache, layer: int, q: torch.Tensor, seqs: Opti
         P = get_sketch_proj(cfg.head_dim, cfg.k_channel_group, cfg.sketch_dim, dev)
         dp.k_proxy = 1
         dp.sketch_proj = P.data_ptr()
+    if correction and count_reads:
+        dp.read_counts = _read_counts_ptr(dev)
     ev_arr = None
     if phase_events is not None:
         if len(phase_events) != 5:
@@ -211,6 +261,56 @@ def decode_attention(cache: CAREKVCache, layer: int, q: torch.Tensor, seqs: Opti
     return (out, diag) if diag_cap > 0 else out
 
 
+def apply_slot_corrections(cache: CAREKVCache, cfg: CacheConfig, router, layer_id: int, kv_head: int, page_ids,
+                           q: torch.Tensor, s_base=None, a_base=None, V_base=None, O_base=None, kind: str = "both",
+                           k_corr_scale: float = 1.0, score_normalize: bool = False, debug_stats=None,
+                           slot_cache=None, seq: int = 0) -> torch.Tensor:
+    """attention.py:208-374: the correction dO (D,) for one query from the
+    stored slots the router selects (ResidualRouter.route's score, linear or
+    exact K correction per CAREKV_K_CORRECTION_MODE), as the decode kernels
+    compute it from the cache pages.  dO is returned as the fp32 difference
+    between the corrected fp16 output and O_base (the reference's callers
+    form half(O_base + dO), which this reproduces); without O_base, the
+    kernels' base output is used."""
+    out, sel = single_query_decode(cache, layer_id, kv_head, q, seq=seq, page_ids=page_ids, kind=kind,
+                                   k_corr_scale=k_corr_scale, score_normalize=score_normalize, router=True,
+                                   correction=True, want_diag=True)
+    if O_base is None:
+        O_base, _ = single_query_decode(cache, layer_id, kv_head, q, seq=seq, page_ids=page_ids, correction=False)
+    if debug_stats is not None:
+        nk = sum(1 for c in sel if c[0] == 0)
+        debug_stats["k_slots_read"] = debug_stats.get("k_slots_read", 0) + nk
+        debug_stats["v_slots_read"] = debug_stats.get("v_slots_read", 0) + len(sel) - nk
+        debug_stats["n_queries"] = debug_stats.get("n_queries", 0) + 1
+    return out.float() - O_base.float()
+
+
+class CAREKVAttention:
+    """Per-query-head decode (attention.py:964-1039)."""
+
+    def __init__(self, cfg: CacheConfig, layer_id: int, device=None):
+        self.cfg, self.layer_id, self.device = cfg, layer_id, device
+        from .residual import ResidualRouter
+        self.router = ResidualRouter(cfg, layer_id, device)
+        self.scale_factor = 1.0 / math.sqrt(cfg.head_dim)
+
+    def forward(self, cache: CAREKVCache, kv_head: int, q: torch.Tensor, page_ids=None, kind: str = "both",
+                k_corr_scale: float = 1.0, score_normalize: bool = False, debug_stats=None, seq: int = 0):
+        """Base attention of q over the kv head's pages, corrected through
+        the router when ``decode_read_mode`` opens the gate (under
+        cfg.compat: read_budget_ratio > 0, attention.py:1025).  (D,) in q's
+        dtype; zeros when the kv head holds no page."""
+        if cache.num_pages(self.layer_id, kv_head, seq) == 0 or (page_ids is not None and len(page_ids) == 0):
+            return torch.zeros(self.cfg.head_dim, dtype=q.dtype, device=q.device)
+        gate, knobs = decode_read_mode(self.cfg, self.layer_id)
+        out, _ = single_query_decode(cache, self.layer_id, kv_head, q, seq=seq, page_ids=page_ids, kind=kind,
+                                     k_corr_scale=k_corr_scale, score_normalize=score_normalize,
+                                     router=not knobs.kscore_live, correction=gate and kind in ("v", "k", "both"))
+        return out.to(q.dtype)
+
+    __call__ = forward
+
+
 class CAREKVMultiHeadAttention:
     """Multi-head decode for one sequence (attention.py:1042-1077)."""
 
@@ -236,3 +336,53 @@ class CAREKVMultiHeadAttention:
                                 knobs=knobs)[0]
 
     __call__ = forward
+
+
+def single_query_decode(cache: CAREKVCache, layer: int, kv_head: int, q: torch.Tensor, *, seq: int = 0,
+                        page_ids=None, kind: str = "both", k_corr_scale: float = 1.0, score_normalize: bool = False,
+                        router: bool = True, correction: bool = True, want_diag: bool = False):
+    """Decode output of one query vector q (D,) against kv head ``kv_head``
+    of sequence ``seq`` (pages ``page_ids``, a prefix 0..n-1 of the kv
+    head's pages, default all): the batched kernels over a one-row batch
+    whose other query heads are zero (selection is per query row,
+    attention.py:830-875).  ``router``: ResidualRouter.route's sketch-proxy
+    score (the per-query reference path); else the knobs of the environment.
+    Returns (out (D,) fp16, selected candidate ids [(kind, page, sub)] when
+    ``want_diag``)."""
+    cfg = cache.cfg
+    grp = cfg.num_heads // cfg.num_kv_heads
+    n_all = cache.num_pages(layer, kv_head, seq)
+    n = n_all if page_ids is None else len(page_ids)
+    if page_ids is not None and list(page_ids) != list(range(n)):
+        raise NotImplementedError("the decode kernels read a prefix of a kv head's pages (0..n-1)")
+    knobs = resolve_read_knobs(cfg, layer)
+    knobs.kind, knobs.k_corr_scale, knobs.normalize = kind, k_corr_scale, score_normalize
+    if router:
+        knobs.kscore_live = False
+    Q = torch.zeros(1, cfg.num_heads, cfg.head_dim, dtype=torch.float16, device=cache.device)
+    h = kv_head * grp
+    Q[0, h] = q.to(torch.float16)
+    count = correction and debug_stats_enabled()
+    diag_cap = (cache.k_cap + cache.v_cap) * max(n, 1) if (want_diag or count) else 0
+    # the launch's other (zero) query heads select too: count this query's reads only
+    res = decode_attention(cache, layer, Q, [seq], correction=correction, knobs=knobs, n_pages=[n],
+                           diag_cap=diag_cap, count_reads=False)
+    if not diag_cap:
+        return res[0, h], None
+    out, diag = res
+    sel = _diag_ids(diag[0, h].cpu())
+    if count:
+        _read_counts_ptr(cache.device)
+        nk = sum(1 for c in sel if c[0] == 0)
+        _READ_COUNTS[str(cache.device)] += torch.tensor([nk, len(sel) - nk, 1], dtype=torch.int64,
+                                                        device=cache.device)
+    return out[0, h], (sel if want_diag else None)
+
+
+def _diag_ids(row) -> list:
+    out = []
+    for x in row.tolist():
+        if x < 0:
+            break
+        out.append((x >> 30, (x >> 3) & ((1 << 27) - 1), x & 7))
+    return out

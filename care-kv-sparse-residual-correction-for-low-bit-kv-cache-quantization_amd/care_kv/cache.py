@@ -207,6 +207,7 @@ class CAREKVCache:
         self.valid_host = np.zeros((L, H, n_seq, P), dtype=np.int32)
         self._token_start = np.zeros((L, H, n_seq, P), dtype=np.int64)
         self._arenas: Dict[int, _lib.Arena] = {}
+        self._freed: Dict[Tuple[int, int], List[int]] = {}  # (seq, 0 K / 1 V) -> freed slot ids
         self._ws: Dict[str, torch.Tensor] = {}
         self._row_tables: Dict[tuple, torch.Tensor] = {}
         _lib.load()
@@ -276,6 +277,8 @@ class CAREKVCache:
         self.k_slot[:, :, seq].fill_(-1)
         self.v_slot[:, :, seq].fill_(-1)
         self.next_slot[seq].zero_()
+        self._freed.pop((seq, 0), None)
+        self._freed.pop((seq, 1), None)
         self.next_page[:, :, seq] = 0
         self.valid_host[:, :, seq] = 0
         self._token_start[:, :, seq] = 0
@@ -474,13 +477,15 @@ class CAREKVCache:
 
     def read_base_concat(self, layer: int, kv_head: int, page_ids: Optional[List[int]] = None, seq: int = 0):
         """(K_codes int8 (N, D), K_scale fp16 (N, G), V_codes, V_scale, valid_lens)
-        for the valid rows of pages 0..n-1 (cache.py:720-772)."""
-        n = self.num_pages(layer, kv_head, seq)
-        if page_ids is not None and list(page_ids) != list(range(len(page_ids))):
-            raise NotImplementedError("read_base_concat reads a prefix of pages (0..n-1)")
-        if page_ids is not None:
-            n = len(page_ids)
-        lens = [int(x) for x in self.valid_host[layer, kv_head, seq, :n]]
+        for the valid rows of the listed pages (all pages when None), in list
+        order (cache.py:720-772)."""
+        n_all = self.num_pages(layer, kv_head, seq)
+        pids = list(range(n_all)) if page_ids is None else [int(p) for p in page_ids]
+        if any(p < 0 or p >= self.cfg.max_pages for p in pids):
+            raise IndexError(f"page ids must lie in [0, {self.cfg.max_pages})")
+        if self.hat:
+            raise _lib.CarekvError("read_base_concat needs a packed base (use read_base_hat_concat)")
+        lens = [int(self.valid_host[layer, kv_head, seq, p]) for p in pids]
         N = sum(lens)
         D, G = self.cfg.head_dim, self.cfg.head_dim // self.cfg.group_size
         kc = torch.zeros(N, D, dtype=torch.int8, device=self.device)
@@ -489,12 +494,148 @@ class CAREKVCache:
         vs = torch.zeros_like(ks)
         if N:
             rs = torch.from_numpy(np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int32)).to(self.device)
+            pl = torch.tensor(pids, dtype=torch.int32, device=self.device)
             lib = _lib.load()
-            _lib.check(lib.carekv_read_pages(self.arena(layer), seq, kv_head, n, rs.data_ptr(), kc.data_ptr(),
-                                             ks.data_ptr(), vc.data_ptr(), vs.data_ptr(),
+            _lib.check(lib.carekv_read_pages(self.arena(layer), seq, kv_head, len(pids), pl.data_ptr(), rs.data_ptr(),
+                                             kc.data_ptr(), ks.data_ptr(), vc.data_ptr(), vs.data_ptr(),
                                              _lib.stream_ptr(self.device)), "carekv_read_pages")
             torch.cuda.current_stream(self.device).synchronize()
         return kc, ks, vc, vs, lens
+
+    def read_base(self, layer: int, kv_head: int, page_ids: List[int], seq: int = 0):
+        """cache.py:776-798: every row (padding included) of the listed pages,
+        (K_codes (P*T, D) int8, K_scale (P*T, G) fp16, V_codes, V_scale)."""
+        from .quantizer import unpack_codes_2d
+        if self.hat:
+            raise _lib.CarekvError("read_base needs a packed base")
+        cfg = self.cfg
+        pl = torch.tensor([int(p) for p in page_ids], dtype=torch.long, device=self.device)
+        out = []
+        for codes, sc, master in ((self.kcodes, self.kscale, self.kmaster), (self.vcodes, self.vscale, self.vmaster)):
+            rows = codes[layer, kv_head, seq, pl].reshape(-1, self._packed_row_bytes)
+            c = unpack_codes_2d(rows, cfg.base_bits, cfg.head_dim)
+            s_ = sc[layer, kv_head, seq, pl]
+            if self.scale_mode:  # cache.py:713-718: half(code * master)
+                s_ = (s_.float() * master[layer, kv_head, seq, pl].float()[:, None, None]).to(F16)
+            out += [c, s_.reshape(-1, s_.shape[-1])]
+        return out[0], out[1], out[2], out[3]
+
+    # ------------------------------------------------------------ reference page / slot interface
+    def alloc_k_slot(self, seq: int = 0) -> int:
+        """cache.py:548-557: the next free K slot id of the sequence (ascending,
+        then the freed ones in the order they were freed).  The store kernels
+        allocate from the same counter; they do not reuse freed ids."""
+        return self._alloc_slot(seq, 0)
+
+    def alloc_v_slot(self, seq: int = 0) -> int:
+        """cache.py:559-561."""
+        return self._alloc_slot(seq, 1)
+
+    def free_k_slot(self, slot: int, seq: int = 0):
+        """cache.py:563-564."""
+        self._freed.setdefault((seq, 0), []).append(int(slot))
+
+    def free_v_slot(self, slot: int, seq: int = 0):
+        """cache.py:566-567."""
+        self._freed.setdefault((seq, 1), []).append(int(slot))
+
+    def _alloc_slot(self, seq: int, kind: int) -> int:
+        nxt = int(self.next_slot[seq, kind].item())
+        if nxt < self.n_slots:
+            self.next_slot[seq, kind] = nxt + 1
+            return nxt
+        freed = self._freed.get((seq, kind), [])
+        assert freed, ("K" if kind == 0 else "V") + " residual buffer is full"
+        return freed.pop(0)
+
+    def write_base(self, layer: int, kv_head: int, page_id: int, K_codes: torch.Tensor, K_scale: torch.Tensor,
+                   V_codes: torch.Tensor, V_scale: torch.Tensor, num_valid: int, seq: int = 0):
+        """cache.py:617-654 through carekv_write_base: pack the page's codes
+        ((T, D) int8, zero padded to the page), encode its (T, G) fp16 scales
+        (int8 codes under a per-page master with scale_quant=int8), record
+        num_valid."""
+        cfg = self.cfg
+        assert 0 <= num_valid <= cfg.page_size, num_valid
+        if self.hat:
+            raise _lib.CarekvError("write_base needs a packed base (use write_base_kivi)")
+        pad = lambda t: torch.nn.functional.pad(t, (0, 0, 0, cfg.page_size - t.shape[0])) if t.shape[0] < cfg.page_size else t  # noqa: E731,E501
+        kc, vc = pad(K_codes.to(torch.int8)).contiguous(), pad(V_codes.to(torch.int8)).contiguous()
+        ksc, vsc = pad(K_scale.to(F16)).contiguous(), pad(V_scale.to(F16)).contiguous()
+        for t in (kc, vc, ksc, vsc):
+            _lib.ptr(t)
+        lib = _lib.load()
+        _lib.check(lib.carekv_write_base(self.arena(layer), seq, kv_head, page_id, kc.data_ptr(), ksc.data_ptr(),
+                                         vc.data_ptr(), vsc.data_ptr(), int(num_valid),
+                                         _lib.stream_ptr(self.device)), "carekv_write_base")
+        self.valid_host[layer, kv_head, seq, page_id] = num_valid
+        if self.rescale_open and num_valid < cfg.page_size:  # the open page's fp16 scales, for the re-encoding append
+            self.open_ks[layer, kv_head, seq, :num_valid] = ksc[:num_valid]
+            self.open_vs[layer, kv_head, seq, :num_valid] = vsc[:num_valid]
+
+    def append_to_page(self, layer: int, kv_head: int, page_id: int, K_codes_row: torch.Tensor,
+                       K_scale_row: torch.Tensor, V_codes_row: torch.Tensor, V_scale_row: torch.Tensor,
+                       seq: int = 0) -> int:
+        """cache.py:656-701: append one quantized row ((D,) int8 codes, (G,)
+        fp16 scales) at the page's next offset; returns the offset.  The int8
+        scale encoding is the cache's (the reference's fixed master under
+        cfg.compat, else the page re-encoded as write_base encodes it)."""
+        cfg = self.cfg
+        off = int(self.valid_host[layer, kv_head, seq, page_id])
+        assert off < cfg.page_size, "page already full"
+        dest = torch.tensor([[seq, kv_head, page_id, int(off == 0)]], dtype=torch.int32, device=self.device)
+        kc = K_codes_row.to(torch.int8).reshape(1, -1).contiguous()
+        vc = V_codes_row.to(torch.int8).reshape(1, -1).contiguous()
+        ksc = K_scale_row.to(F16).reshape(1, -1).contiguous()
+        vsc = V_scale_row.to(F16).reshape(1, -1).contiguous()
+        for t in (kc, vc, ksc, vsc):
+            _lib.ptr(t)
+        lib = _lib.load()
+        _lib.check(lib.carekv_append_coded_rows(self.arena(layer), kc.data_ptr(), ksc.data_ptr(), vc.data_ptr(),
+                                                vsc.data_ptr(), dest.data_ptr(), 1, _lib.stream_ptr(self.device)),
+                   "carekv_append_coded_rows")
+        self.valid_host[layer, kv_head, seq, page_id] = off + 1
+        return off
+
+    def write_base_kivi(self, layer: int, kv_head: int, page_id: int, K_hat: torch.Tensor, V_hat: torch.Tensor,
+                        num_valid: int, seq: int = 0):
+        """cache.py:800-818: the page's fp16 K_hat / V_hat rows (side buffer)."""
+        assert self.hat, "write_base_kivi requires a side-buffer base quantizer"
+        assert 0 <= num_valid <= self.cfg.page_size, num_valid
+        T = K_hat.shape[0]
+        self.kcodes[layer, kv_head, seq, page_id].view(F16)[:T] = K_hat.to(F16)
+        self.vcodes[layer, kv_head, seq, page_id].view(F16)[:T] = V_hat.to(F16)
+        self.valid[layer, kv_head, seq, page_id] = num_valid
+        self.valid_host[layer, kv_head, seq, page_id] = num_valid
+
+    def append_to_page_kivi(self, layer: int, kv_head: int, page_id: int, K_hat_row: torch.Tensor,
+                            V_hat_row: torch.Tensor, seq: int = 0) -> int:
+        """cache.py:820-838: one fp16 K_hat / V_hat row at the page's next offset."""
+        assert self.hat, "append_to_page_kivi requires a side-buffer base quantizer"
+        off = int(self.valid_host[layer, kv_head, seq, page_id])
+        assert off < self.cfg.page_size, "page already full"
+        self.kcodes[layer, kv_head, seq, page_id].view(F16)[off] = K_hat_row.to(F16)
+        self.vcodes[layer, kv_head, seq, page_id].view(F16)[off] = V_hat_row.to(F16)
+        self.valid[layer, kv_head, seq, page_id] = off + 1
+        self.valid_host[layer, kv_head, seq, page_id] = off + 1
+        return off
+
+    def write_k_residual(self, slot: int, packed: torch.Tensor, scale: torch.Tensor, seq: int = 0):
+        """cache.py:871-873."""
+        self.k_res[seq, slot] = packed.flatten().to(torch.int8)
+        self.k_res_scale[seq, slot] = scale.flatten()[0].to(F16)
+
+    def write_v_residual(self, slot: int, packed: torch.Tensor, scale: torch.Tensor, seq: int = 0):
+        """cache.py:875-877."""
+        self.v_res[seq, slot] = packed.flatten().to(torch.int8)
+        self.v_res_scale[seq, slot] = scale.flatten()[0].to(F16)
+
+    def read_k_residual(self, slot: int, seq: int = 0):
+        """cache.py:879-880: (packed (slot_bytes,) int8, scale (1,) fp16)."""
+        return self.k_res[seq, slot], self.k_res_scale[seq, slot:slot + 1]
+
+    def read_v_residual(self, slot: int, seq: int = 0):
+        """cache.py:882-883."""
+        return self.v_res[seq, slot], self.v_res_scale[seq, slot:slot + 1]
 
     def page_meta(self, layer: int, kv_head: int, page_id: int, seq: int = 0) -> Optional[PageMeta]:
         idx = (layer, kv_head, seq, page_id)

@@ -25,7 +25,8 @@ from typing import Any, Dict, Optional, Sequence, Tuple
 import torch
 from torch import Tensor, nn
 
-from .attention import decode_attention, decode_read_mode, prefill_correction
+from .attention import (decode_attention, decode_read_mode, get_debug_stats, prefill_correction,  # noqa: F401
+                        reset_debug_stats)
 from .cache import CAREKVCache
 from .config import CacheConfig, any_read_budget, resolve_read_knobs
 from .prefill import prefill_attention, quant_dequant

@@ -138,6 +138,7 @@ int run_decode(const carekv_arena* arena, const carekv_decode_params* dp, const 
   a.ws_x_off = (uint32_t)(L.xbuf - L.rec);
   a.sketch_proj = dp->sketch_proj;
   a.diag = diag; a.diag_cap = diag_cap;
+  a.read_counts = dp->read_counts;
   a.B = dp->batch; a.Hq = dp->n_heads; a.GQ = GQ; a.nsplit = L.nsplit; a.SP = dp->split_pages;
   a.Pmax = dp->max_pages_used > 0 ? dp->max_pages_used : 1;
   a.k_cap = dp->k_cap; a.v_cap = dp->v_cap; a.F = L.F; a.ncand = L.ncand;

@@ -28,6 +28,7 @@ struct DecodeArgs {
   const float* sketch_proj;  // [32][sketch_dim] fp32 (sketch proxy only)
   int32_t* diag;
   int32_t* err_flag;
+  unsigned long long* read_counts;  // optional [3]: K reads, V reads, corrected queries
   int diag_cap;
   int B, Hq, GQ, nsplit, SP, Pmax, k_cap, v_cap, F, ncand;
   float sm_scale, sm_log2, sens, k_corr_scale, lam_k, lam_v, inv_sqrt_d;

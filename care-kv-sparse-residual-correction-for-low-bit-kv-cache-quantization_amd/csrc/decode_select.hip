@@ -598,6 +598,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
       __syncthreads();
     }
   }
+  if (a.read_counts) {
+    // ---- debug read counters: this query's selected K slots and V blocks
+    // (each thread reads back the mask bytes it wrote)
+    int ck = 0, cvb = 0;
+    for (int p = tid; p < np; p += kBlock) {
+      ck += __popc(maskq[p] & 15u);
+      cvb += __popc((unsigned)maskq[p] >> 4);
+    }
+    ck = block_isum_fast(ck, bs);
+    cvb = block_isum_fast(cvb, bs);
+    if (tid == 0 && L > 0.f) {
+      atomicAdd(a.read_counts, (unsigned long long)ck);
+      atomicAdd(a.read_counts + 1, (unsigned long long)cvb);
+      atomicAdd(a.read_counts + 2, 1ull);
+    }
+  }
   if (!diagp) return;
   // ---- diag: selected candidates in ascending candidate order (each
   // thread reads back the mask bytes it wrote)

@@ -162,7 +162,18 @@ __global__ __launch_bounds__(256) void store_pages_kernel(carekv_arena A, carekv
         xv[i + 2 * j] = h2f((uint16_t)wb[j]); xv[i + 2 * j + 1] = h2f((uint16_t)(wb[j] >> 16));
       }
     }
-    if (sp.keep_base) {
+    if (sp.k_codes_in) {
+      // process_page on a page write_base wrote: the caller's base codes and
+      // fp16 group scales (residual_store.py:276-285); the page keeps its base
+      const long ri = (long)job_id * kPage + t;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        ck[i] = sp.k_codes_in[ri * D + g * 32 + i];
+        cv[i] = sp.v_codes_in[ri * D + g * 32 + i];
+      }
+      sk = bits2half(sp.k_scale_in[ri * NG + g]);
+      sv = bits2half(sp.v_scale_in[ri * NG + g]);
+    } else if (sp.keep_base) {
       // streaming store of a page the decode appends filled: the page keeps
       // its base, the residual is taken against it as the decode reads it,
       // half(code * half(scale code * master)) (layer.py:1104-1133)
@@ -249,12 +260,19 @@ __global__ __launch_bounds__(256) void store_pages_kernel(carekv_arena A, carekv
     vs = wave_sum(vs);
     if (lane == 0) A.v_sq[pg] = vs;
   }
-  if (MODE == 0 && BITS != 16 && sp.keep_base) {
-    // ---- the page keeps its base; only the sum of V_hat^2 is refreshed
+  if (MODE == 0 && BITS != 16 && (sp.keep_base || sp.k_codes_in)) {
+    // ---- the page keeps its base; only the sum of V_hat^2 is refreshed, over
+    // the rows as the decode reads them back
     float vs = 0.f;
     if (active && t < nvld) {
+      _Float16 svr = sv;
+      if (sp.k_codes_in) {
+        const long row = pg * kPage + t;
+        svr = A.scale_mode == 1 ? (_Float16)((float)((const int8_t*)A.vscale)[row * NG + g] * h2f(A.vmaster[pg]))
+                                : bits2half(((const uint16_t*)A.vscale)[row * NG + g]);
+      }
 #pragma unroll
-      for (int i = 0; i < 32; ++i) { const float vh = (float)dq(cv[i], sv); vs += vh * vh; }
+      for (int i = 0; i < 32; ++i) { const float vh = (float)dq(cv[i], svr); vs += vh * vh; }
     }
     vs = wave_sum(vs);
     if (lane == 0) A.v_sq[pg] = vs;
@@ -548,10 +566,21 @@ __global__ __launch_bounds__(256) void append_hat_rows_kernel(carekv_arena A, co
 //     gives the 16 rows.
 // The page's sum of V_hat^2 (v_sq, read by the query-aware K score of its
 // stored K slots) is recomputed over the valid rows as they now read back.
+// Coded rows (append_to_page, cache.py:656-701): the caller's int8 codes and
+// fp16 group scales replace the row quantizer, and a full page gets no
+// metadata (the store on fill belongs to the decode step, not the append).
+struct CodedRows {
+  const int8_t* kc;
+  const uint16_t* ks;
+  const int8_t* vc;
+  const uint16_t* vs;
+};
+
 template <int D, int BITS>
 __global__ __launch_bounds__(256) void append_rows_kernel(carekv_arena A, const uint16_t* __restrict__ Kx,
                                                           const uint16_t* __restrict__ Vx,
-                                                          const int32_t* __restrict__ dest, int n_rows) {
+                                                          const int32_t* __restrict__ dest, int n_rows,
+                                                          CodedRows cr) {
   constexpr int NG = D / 32;
   constexpr int RB = row_bytes(D, BITS);
   constexpr int CB = 4 * BITS;
@@ -570,12 +599,21 @@ __global__ __launch_bounds__(256) void append_rows_kernel(carekv_arena A, const 
     const int g = lane;
     float xk[32], xv[32];
     int ck[32];
-    for (int i = 0; i < 32; ++i) {
-      xk[i] = h2f(Kx[(long)row * D + g * 32 + i]);
-      xv[i] = h2f(Vx[(long)row * D + g * 32 + i]);
+    if (cr.kc) {
+      for (int i = 0; i < 32; ++i) {
+        ck[i] = cr.kc[(long)row * D + g * 32 + i];
+        cv[i] = cr.vc[(long)row * D + g * 32 + i];
+      }
+      sk = bits2half(cr.ks[(long)row * NG + g]);
+      sv = bits2half(cr.vs[(long)row * NG + g]);
+    } else {
+      for (int i = 0; i < 32; ++i) {
+        xk[i] = h2f(Kx[(long)row * D + g * 32 + i]);
+        xv[i] = h2f(Vx[(long)row * D + g * 32 + i]);
+      }
+      sk = quant_group<BITS>(xk, ck);
+      sv = quant_group<BITS>(xv, cv);
     }
-    sk = quant_group<BITS>(xk, ck);
-    sv = quant_group<BITS>(xv, cv);
     uint32_t w[BITS];
     pack_group<BITS>(ck, w);
     store_bytes<CB>(A.kcodes + (pg * kPage + off) * RB + g * CB, w);
@@ -641,7 +679,7 @@ __global__ __launch_bounds__(256) void append_rows_kernel(carekv_arena A, const 
     for (int i = 0; i < 32; ++i) { const float x = (float)dq(get_code<BITS>(w, i), s); vs += x * x; }
   }
   vs = wave_sum(vs);
-  const bool full = off + 1 == kPage;
+  const bool full = off + 1 == kPage && !cr.kc;  // the decode step's store on fill
   if (lane == 0) {
     A.valid[pg] = off + 1;
     if (rescale) { A.kmaster[pg] = half2bits((_Float16)mk); A.vmaster[pg] = half2bits((_Float16)mv); }
@@ -662,6 +700,7 @@ __global__ __launch_bounds__(256) void append_rows_kernel(carekv_arena A, const 
 // read_base_concat for one (seq, kv head): unpacked codes + fp16 scales.
 template <int D, int BITS>
 __global__ __launch_bounds__(256) void read_pages_kernel(carekv_arena A, int seq, int kvh, int n_pages,
+                                                         const int32_t* __restrict__ page_ids,
                                                          const int32_t* __restrict__ row_start, int8_t* kc,
                                                          uint16_t* ks, int8_t* vc, uint16_t* vs) {
   constexpr int NG = D / 32;
@@ -669,7 +708,9 @@ __global__ __launch_bounds__(256) void read_pages_kernel(carekv_arena A, int seq
   constexpr int CB = 4 * BITS;
   const int p = blockIdx.x;
   if (p >= n_pages) return;
-  const long pg = ((long)kvh * A.n_seq + seq) * A.max_pages + p;
+  const int page = page_ids ? page_ids[p] : p;
+  if (page < 0 || page >= A.max_pages) return;
+  const long pg = ((long)kvh * A.n_seq + seq) * A.max_pages + page;
   const int n = A.valid[pg];
   const int r0 = row_start[p];
   for (int idx = threadIdx.x; idx < n * NG; idx += blockDim.x) {
@@ -769,9 +810,29 @@ extern "C" int carekv_store_pages(const carekv_arena* arena, const carekv_store_
   });
 }
 
+namespace {
+int append_any(const carekv_arena* arena, const uint16_t* k_rows, const uint16_t* v_rows, const int32_t* dest_dev,
+               int32_t n_rows, const CodedRows& cr, void* stream);
+}  // namespace
+
 extern "C" int carekv_append_rows(const carekv_arena* arena, const uint16_t* k_rows, const uint16_t* v_rows,
                                   const int32_t* dest_dev, int32_t n_rows, void* stream) {
-  CAREKV_REQUIRE(arena && k_rows && v_rows && dest_dev, "null argument");
+  CAREKV_REQUIRE(k_rows && v_rows, "null argument");
+  return append_any(arena, k_rows, v_rows, dest_dev, n_rows, CodedRows{nullptr, nullptr, nullptr, nullptr}, stream);
+}
+
+extern "C" int carekv_append_coded_rows(const carekv_arena* arena, const int8_t* k_codes, const uint16_t* k_scale,
+                                        const int8_t* v_codes, const uint16_t* v_scale, const int32_t* dest_dev,
+                                        int32_t n_rows, void* stream) {
+  CAREKV_REQUIRE(k_codes && k_scale && v_codes && v_scale, "null argument");
+  CAREKV_REQUIRE(arena && arena->base_bits != 16, "coded rows need a packed base");
+  return append_any(arena, nullptr, nullptr, dest_dev, n_rows, CodedRows{k_codes, k_scale, v_codes, v_scale}, stream);
+}
+
+namespace {
+int append_any(const carekv_arena* arena, const uint16_t* k_rows, const uint16_t* v_rows, const int32_t* dest_dev,
+               int32_t n_rows, const CodedRows& cr, void* stream) {
+  CAREKV_REQUIRE(arena && dest_dev, "null argument");
   if (n_rows <= 0) return CAREKV_OK;
   const carekv_arena& A = *arena;
   CAREKV_REQUIRE(check_arena(A), last_error_buf());
@@ -788,26 +849,27 @@ extern "C" int carekv_append_rows(const carekv_arena* arena, const uint16_t* k_r
   }
   return dispatch_db(A.head_dim, A.base_bits, [&](auto d, auto b) {
     hipLaunchKernelGGL((append_rows_kernel<decltype(d)::value, decltype(b)::value>), dim3((n_rows + 3) / 4),
-                       dim3(256), 0, s, A, k_rows, v_rows, dest_dev, n_rows);
+                       dim3(256), 0, s, A, k_rows, v_rows, dest_dev, n_rows, cr);
     CAREKV_CHECK_LAUNCH("append_rows");
     return CAREKV_OK;
   });
 }
+}  // namespace
 
 extern "C" int carekv_read_pages(const carekv_arena* arena, int32_t seq, int32_t kv_head, int32_t n_pages,
-                                 const int32_t* row_start_dev, int8_t* kc, uint16_t* ks, int8_t* vc, uint16_t* vs,
-                                 void* stream) {
+                                 const int32_t* page_ids_dev, const int32_t* row_start_dev, int8_t* kc, uint16_t* ks,
+                                 int8_t* vc, uint16_t* vs, void* stream) {
   CAREKV_REQUIRE(arena && row_start_dev && kc && ks && vc && vs, "null argument");
   const carekv_arena& A = *arena;
   CAREKV_REQUIRE(check_arena(A), last_error_buf());
   CAREKV_REQUIRE(seq >= 0 && seq < A.n_seq && kv_head >= 0 && kv_head < A.n_kv_heads, "seq/kv_head out of range");
-  CAREKV_REQUIRE(n_pages >= 0 && n_pages <= A.max_pages, "n_pages out of range");
+  CAREKV_REQUIRE(n_pages >= 0 && (page_ids_dev || n_pages <= A.max_pages), "n_pages out of range");
   CAREKV_REQUIRE(A.base_bits != 16, "the fp16 base has no codes to read: read its pages directly");
   if (n_pages == 0) return CAREKV_OK;
   hipStream_t s = (hipStream_t)stream;
   return dispatch_db(A.head_dim, A.base_bits, [&](auto d, auto b) {
     hipLaunchKernelGGL((read_pages_kernel<decltype(d)::value, decltype(b)::value>), dim3(n_pages), dim3(64), 0, s,
-                       A, seq, kv_head, n_pages, row_start_dev, kc, ks, vc, vs);
+                       A, seq, kv_head, n_pages, page_ids_dev, row_start_dev, kc, ks, vc, vs);
     CAREKV_CHECK_LAUNCH("read_pages");
     return CAREKV_OK;
   });

@@ -108,6 +108,15 @@ typedef struct carekv_store_params {
                             * reference stores such pages with K_orig = K_hat
                             * (layer.py:1128-1146), which leaves them no slots.
                             * 0: store as the prefill does                    */
+  /* process_page on a page carekv_write_base wrote (packed bases;
+   * residual_store.py:239-464 with its K_codes / K_scale / V_codes / V_scale
+   * arguments): int8 [n_jobs*page_size][head_dim] unpacked codes and fp16
+   * [n_jobs*page_size][D/group] group scales the residuals are taken
+   * against; the pages keep their base.  NULL: quantize K / V here.      */
+  const int8_t* k_codes_in;
+  const uint16_t* k_scale_in;
+  const int8_t* v_codes_in;
+  const uint16_t* v_scale_in;
 } carekv_store_params;
 
 /* One page write (prefill).  X rows for page j are X[j*page_size .. +page_size),
@@ -148,6 +157,16 @@ int64_t carekv_store_workspace_bytes(int32_t n_jobs);
  * with a zero master and no metadata, like the reference's zeroed buffers. */
 int carekv_append_rows(const carekv_arena* arena, const uint16_t* k_rows, const uint16_t* v_rows,
                        const int32_t* dest_dev, int32_t n_rows, void* stream);
+
+/* CAREKVCache.append_to_page (cache.py:656-701): rows already quantized by
+ * the caller, int8 codes [n_rows][head_dim] and fp16 group scales
+ * [n_rows][D/group], packed at (seq, kv_head, page, valid[pg]) with the
+ * arena's scale encoding (as carekv_append_rows); dest_dev as there.  A page
+ * the rows fill gets no metadata (the decode step's store on fill is not part
+ * of the append).  Packed bases only. */
+int carekv_append_coded_rows(const carekv_arena* arena, const int8_t* k_codes, const uint16_t* k_scale,
+                             const int8_t* v_codes, const uint16_t* v_scale, const int32_t* dest_dev,
+                             int32_t n_rows, void* stream);
 
 /* Decode attention + comb+ex residual correction.  Replaces, per sequence
  * and kv head, CAREKVCache.read_base_concat (cache.py:720-772) + dequantize
@@ -197,6 +216,11 @@ typedef struct carekv_decode_params {
                             * thresholds after the policy (:366-410)          */
   double rel_threshold, abs_threshold; /* CAREKV_READ_RELATIVE/ABSOLUTE_THRESHOLD */
   int32_t min_keep;        /* CAREKV_READ_MIN_KEEP                             */
+  unsigned long long* read_counts; /* optional device [3], NULL to skip: the
+                            * call adds the K slots and V blocks it selected
+                            * and the queries it corrected (the debug stats
+                            * k_slots_read / v_slots_read / n_queries,
+                            * attention.py:358-372,944-946)                   */
 } carekv_decode_params;
 
 /* q, out: fp16 [batch][n_heads][head_dim].  The first int32 of the
@@ -229,12 +253,45 @@ int carekv_decode_attn_static(const carekv_arena* arena, const carekv_decode_par
                               uint16_t* out, int32_t* diag, int32_t diag_cap, void* stream);
 
 /* read_base_concat (cache.py:720-772) for one (seq, kv_head): unpacked int8
- * codes [N][D] and fp16 scales [N][G] of the valid rows of pages 0..n_pages-1
- * (int8 scales expanded as half(code * master)).  row_start_dev: int32
- * [n_pages] exclusive prefix of valid[] (host computed). */
+ * codes [N][D] and fp16 scales [N][G] of the valid rows of the listed pages
+ * (int8 scales expanded as half(code * master)).  page_ids_dev: int32
+ * [n_pages] page ids, or NULL for pages 0..n_pages-1; row_start_dev: int32
+ * [n_pages] exclusive prefix of the listed pages' valid counts (host
+ * computed). */
 int carekv_read_pages(const carekv_arena* arena, int32_t seq, int32_t kv_head, int32_t n_pages,
-                      const int32_t* row_start_dev, int8_t* kc, uint16_t* ks, int8_t* vc,
-                      uint16_t* vs, void* stream);
+                      const int32_t* page_ids_dev, const int32_t* row_start_dev, int8_t* kc, uint16_t* ks,
+                      int8_t* vc, uint16_t* vs, void* stream);
+
+/* CAREKVCache.write_base (cache.py:617-654) of one page: k_codes / v_codes
+ * int8 [page_size][head_dim] unpacked codes, k_scale / v_scale fp16
+ * [page_size][D/group]; packs the codes, encodes the scales (int8 codes
+ * under the page's fp16 master, cache.py:592-604, or fp16) and sets the
+ * page's valid count. */
+int carekv_write_base(const carekv_arena* arena, int32_t seq, int32_t kv_head, int32_t page, const int8_t* k_codes,
+                      const uint16_t* k_scale, const int8_t* v_codes, const uint16_t* v_scale, int32_t num_valid,
+                      void* stream);
+
+/* pack_codes_2d / unpack_codes_2d (quantizer.py:257-383): int8 codes
+ * [rows][D] <-> packed [rows][D*bits/8]; INT3 packs 8 codes into a 24-bit
+ * little-endian word, INT2 4 and INT4 2 codes into a byte, LSB first.  The
+ * 1-D pack_int* / unpack_int* (quantizer.py:147-249) are one row of the
+ * zero-padded codes.  D a multiple of 8 (INT3), 4 (INT2) or 2 (INT4). */
+int carekv_pack_codes(const int8_t* codes, int64_t rows, int32_t D, int32_t bits, int8_t* packed, void* stream);
+int carekv_unpack_codes(const int8_t* packed, int64_t rows, int32_t D, int32_t bits, int8_t* codes, void* stream);
+
+/* pack_4bit / unpack_4bit (residual_store.py:121-146): x float32 (x_fp16 = 0)
+ * or fp16, numel values -> packed int8 [(numel + 1) / 2], scale fp16 [1]
+ * (s = max|x| / 7 in the input's arithmetic); unpack gives float32
+ * code * float(scale). */
+int carekv_pack_4bit(const void* x, int32_t x_fp16, int64_t numel, int8_t* packed, uint16_t* scale, void* stream);
+int carekv_unpack_4bit(const int8_t* packed, const uint16_t* scale, int64_t numel, float* out, void* stream);
+
+/* quantize / dequantize (quantizer.py:31-82) on float32 rows, in fp32
+ * arithmetic: codes int8 [rows][D], scale float32 [rows][D/group]; group 32. */
+int carekv_quantize_rows_f32(const float* x, int64_t rows, int32_t D, int32_t bits, int32_t group, int8_t* codes,
+                             float* scale, void* stream);
+int carekv_dequantize_rows_f32(const int8_t* codes, const float* scale, int64_t rows, int32_t D, int32_t group,
+                               float* out, void* stream);
 
 /* Symmetric per-group quantizer on fp16 rows (quantizer.py:31-64, fp16
  * arithmetic) with optional bit packing (quantizer.py:364-372).

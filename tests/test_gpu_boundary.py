@@ -229,6 +229,8 @@ def test_adapter_patches_a_given_model(monkeypatch):
     assert torch.isfinite(logits.float()).all()
     st = a.collect_debug_stats()
     assert st["stored_k_slots"] > 0 and st["stored_v_slots"] > 0
+    # the reference's gate for a CARE-KV row: slots were read (CLAUDE.md:141-142)
+    assert st["k_reads"] > 0 and st["v_reads"] > 0
 
 
 @pytest.mark.parametrize("name", ["gqa4_d128", "gqa4_d128_kivi"])

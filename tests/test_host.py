@@ -20,7 +20,7 @@ def test_library_exports_header_symbols():
     _lib = _ensure_built()
     lib = _lib.load()
     hdr = open(os.path.join(ROOT, "include", "carekv.h")).read()
-    declared = set(re.findall(r"\b(carekv_[a-z_]+)\s*\(", hdr))
+    declared = set(re.findall(r"\b(carekv_[a-z0-9_]+)\s*\(", hdr))
     assert declared, "no declarations parsed"
     for name in sorted(declared):
         assert hasattr(lib, name), name
@@ -36,7 +36,7 @@ def _struct_fields(hdr, name):
         stmt = stmt.strip()
         if not stmt:
             continue
-        decl = re.sub(r"^(const\s+)?\w+\s*", "", stmt)          # drop the type
+        decl = re.sub(r"^(const\s+)?(unsigned\s+)?(long\s+)*\w+\s*", "", stmt)  # drop the type
         names += [re.sub(r"[\s*]", "", d) for d in decl.split(",")]
     return names
 
