@@ -111,16 +111,17 @@ class CAREKVLayer(nn.Module):
     @staticmethod
     def _check_mask(attention_mask: Optional[Tensor], T: int):
         """The kernel applies the causal mask itself (the attention_mask=None
-        branch of layer.py:951-962).  An additive mask that masks more than
-        the causal triangle (padding) is refused rather than ignored."""
-        if attention_mask is None or not torch.is_tensor(attention_mask) or attention_mask.dtype == torch.bool:
-            if torch.is_tensor(attention_mask) and attention_mask.dtype == torch.bool:
-                last = attention_mask.reshape(-1, attention_mask.shape[-1])[-1]
-                if not bool(last.all()):
-                    raise NotImplementedError("padded attention masks are not supported by the prefill kernel")
+        branch of layer.py:951-962).  A mask that masks more than the causal
+        triangle in any sequence of the batch (padding) is refused rather than
+        ignored: the last query row of every sequence must see all keys
+        (boolean masks: all True; additive masks: no negative entry)."""
+        if attention_mask is None or not torch.is_tensor(attention_mask):
             return
-        last = attention_mask.reshape(-1, attention_mask.shape[-2], attention_mask.shape[-1])[:, -1, -T:]
-        if bool((last < 0).any()):
+        m = attention_mask
+        if m.dim() >= 2:
+            m = m.reshape(-1, m.shape[-2], m.shape[-1])[:, -1, -T:] if m.dim() > 2 else m[:, -T:]
+        padded = (not bool(m.all())) if m.dtype == torch.bool else bool((m < 0).any())
+        if padded:
             raise NotImplementedError("padded attention masks are not supported by the prefill kernel")
 
     # ------------------------------------------------------------ prefill

@@ -201,3 +201,27 @@ def test_prefill_correct_rejects_bad_rows():
     assert ws() > live                             # the router's proxy records and logit maxima
     dp.k_proxy, dp.correction = 0, 0
     assert ws() == -1                              # the pass is the correction
+
+
+def test_padded_masks_refused_in_any_sequence():
+    """CAREKVLayer._check_mask: a left-padded sequence anywhere in the batch
+    is refused (boolean (B, 1, T, S) masks as HF's sdpa path builds them and
+    additive float masks), a causal-only mask passes."""
+    import torch
+    _ensure_built()
+    from care_kv.layer import CAREKVLayer
+    B, T = 3, 6
+    causal = torch.tril(torch.ones(T, T, dtype=torch.bool))[None, None].expand(B, 1, T, T).clone()
+    CAREKVLayer._check_mask(causal, T)
+    padded = causal.clone()
+    padded[0, :, :, :2] = False  # sequence 0 left-padded by two tokens
+    with pytest.raises(NotImplementedError):
+        CAREKVLayer._check_mask(padded, T)
+    add = torch.zeros(B, 1, T, T)
+    add.masked_fill_(~causal, float("-inf"))
+    CAREKVLayer._check_mask(add, T)
+    add[1, :, :, 0] = float("-inf")  # only sequence 1 padded
+    with pytest.raises(NotImplementedError):
+        CAREKVLayer._check_mask(add, T)
+    with pytest.raises(NotImplementedError):  # a (B, S) keep-mask with a zero
+        CAREKVLayer._check_mask(torch.tensor([[1, 1, 1], [0, 1, 1]], dtype=torch.bool), 3)
