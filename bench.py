@@ -614,7 +614,7 @@ def main():
         except Exception:
             cores = int(os.environ.get("OMP_NUM_THREADS", "1"))
         cpu = {"value": round(cpu_us, 1), "unit": "us/step", "cores": cores, "kind": "port",
-               "sample": f"{args.cpu_slices} of {B * Hkv} (sequence, kv-head) slices of the same cache "
+               "sample": f"{len(slice_ids(spec, args.cpu_slices))} of {B * Hkv} (sequence, kv-head) slices of the same cache "
                          f"({per_slice:.3f} s each, numpy oracle), extrapolated x{B * Hkv}"}
         log(f"[bench] cpu oracle {per_slice:.3f} s/slice -> {cpu_us / 1e3:.1f} ms/step extrapolated")
     # the library runs the 4-query-head streaming kernel when a kv head has at

@@ -90,11 +90,14 @@ def decode_read_mode(cfg: CacheConfig, layer: int):
 
 
 def default_split_pages(max_pages: int, rows: int) -> int:
-    """Pages per work-group: enough work-groups to fill 256 CUs several times
-    over, and a multiple of 16 (4 waves x 4-page windows)."""
-    target = int(os.environ.get("CAREKV_DECODE_TARGET_WGS", "4096"))
-    sp = math.ceil(max(1, max_pages) * max(1, rows) / target)
-    sp = max(16, min(256, sp))
+    """Pages per work-group of the streaming pass, a multiple of 16 (4 waves
+    x 4-page windows): long enough that each wave's start-up (q staging, the
+    first window's loads, the split merge) spreads over several windows --
+    half a row, at most 256 pages -- and short enough that the grid keeps at
+    least CAREKV_DECODE_MIN_WGS (default 1024: four per CU) work-groups."""
+    min_wgs = max(1, int(os.environ.get("CAREKV_DECODE_MIN_WGS", "1024")))
+    P, R = max(1, max_pages), max(1, rows)
+    sp = max(16, min(256, -(-P // 2), (P * R) // min_wgs))
     return (sp + 15) // 16 * 16
 
 

@@ -23,7 +23,7 @@ WsLayout ws_layout(const carekv_arena& A, const carekv_decode_params& dp, int gq
   const int D = A.head_dim;
   const int Pm = dp.max_pages_used > 0 ? dp.max_pages_used : 1;
   L.nsplit = (Pm + dp.split_pages - 1) / dp.split_pages;
-  L.F = 1 + 3 * dp.k_cap + dp.v_cap;
+  L.F = 2 + 4 * dp.k_cap + dp.v_cap;
   L.ncand = Pm * (dp.k_cap + dp.v_cap);
   auto al = [](long x) { return (x + 255) / 256 * 256; };
   long off = 0;

@@ -100,13 +100,23 @@ __device__ __forceinline__ long pf_row_off(const DecodeArgs& a, const PfCol& x) 
   return (long)(x.row - a.pf_row0) * a.Hq + x.head;
 }
 
-// Page record per (sequence, kv head, query, page), F floats:
+// Page record per (sequence, kv head, query, page), F = 2 + 4*k_cap +
+// v_cap floats:
 //   [0]                      m_ref: running max of the base-2 logits
 //                            x = s * log2(e) at the page
-//   [1 + 3r .. 3 + 3r]       M2, M3, M4 of the r-th stored K slot (cg order)
-//   [1 + 3*k_cap + r]        sum_t e_t over the r-th stored V block
-// with e_t = 2^(x_t - m_ref) and Mk = sum_t dS_t^2 e_t^k over the page's
-// valid tokens.  Written only for pages with metadata.
+//   [1 + 4r .. 3 + 4r]       M2, M3, M4 of the r-th stored K slot (cg order)
+//   [4 + 4r]                 D*: dS_t*^2 of the r-th stored K slot
+//   [1 + 4*k_cap]            e_t*
+//   [2 + 4*k_cap + r]        sum_t e_t over the r-th stored V block
+// with e_t = 2^(x_t - m_ref), t* the page's first token of largest e_t, and
+// Mk = sum_t dS_t^2 e_t^k over the page's valid tokens other than t*.  The
+// K score sum_t dS_t^2 a_t^2 (1 - a_t)^2 (a_t = c e_t) is then
+// c^2 [M2 - 2 c M3 + c^2 M4 + D* (e* (1 - c e*))^2]: the one token whose a_t
+// can exceed 1/2 (where the expansion cancels) is evaluated directly, as
+// the reference evaluates A (1 - A), and the select kernel keeps c outside
+// the square root (c^2 of a page far below the maximum underflows fp32
+// where the reference's per-token terms do not).  Written only for pages
+// with metadata.
 //
 // ebuf holds the page's e_t (0 past the valid tokens) for the apply pass.
 // With the sketch proxy the K moments are not written; xbuf holds the

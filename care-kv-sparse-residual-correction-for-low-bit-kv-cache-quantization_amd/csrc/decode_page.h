@@ -55,6 +55,16 @@ __device__ __forceinline__ float moments_reduce(float a, float b, float c) {
   return __uint_as_float(xc[0]) + __uint_as_float(xc[1]);  // lower half: x total, upper half: c total
 }
 
+// Four values reduced the same way: group j ends with the sum of the j-th.
+__device__ __forceinline__ float moments_reduce4(float a, float b, float c, float d) {
+  const auto ab = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  const float x = __uint_as_float(ab[0]) + __uint_as_float(ab[1]);  // even rows: a pair sum, odd rows: b
+  const auto cd = __builtin_amdgcn_permlane16_swap(__float_as_uint(c), __float_as_uint(d), false, false);
+  const float y = __uint_as_float(cd[0]) + __uint_as_float(cd[1]);  // even rows: c pair sum, odd rows: d
+  const auto xy = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+  return __uint_as_float(xy[0]) + __uint_as_float(xy[1]);  // rows 0..3: a, b, c, d totals
+}
+
 // Sum over the four lanes m, m+16, m+32, m+48 (the token groups of a query).
 __device__ __forceinline__ float col_sum(float v) { return pair32_sum(pair16_sum(v)); }
 __device__ __forceinline__ float col_max(float v) { return pair32_max(pair16_max(v)); }

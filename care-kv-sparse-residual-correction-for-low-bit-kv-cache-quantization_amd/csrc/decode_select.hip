@@ -27,6 +27,23 @@ namespace carekv {
 
 constexpr float kEps = 1e-6f;  // residual_router.py:34
 
+// v_sqrt_f32 and v_exp_f32 read and give fp32 denormals as zero, while the
+// reference's fp32 arithmetic keeps them: the attention mass and the K
+// score terms of a page far below the maximum fall under 2^-126 there and
+// still rank candidates.  These scale such arguments into the normal range.
+__device__ __forceinline__ float sqrt_dn(float x) {
+  return x < 0x1p-100f ? __builtin_amdgcn_sqrtf(x * 0x1p100f) * 0x1p-50f : __builtin_amdgcn_sqrtf(x);
+}
+__device__ __forceinline__ float exp2_dn(float x) {
+  return x < -126.f ? __builtin_amdgcn_exp2f(x + 64.f) * 0x1p-64f : __builtin_amdgcn_exp2f(x);
+}
+// The reference sums the per-token squares (dS_t A_t (1 - A_t))^2 in fp32;
+// when even sum_t (dS_t A_t)^2 = c^2 (M2 + D* e*^2) is at most 2^-150,
+// every one of them rounds to zero there and its K score is exactly 0.
+__device__ __forceinline__ bool kscore_underflows(float c, float M2, float Ds, float es) {
+  return c * sqrt_dn(M2 + Ds * (es * es)) <= 0x1p-75f;
+}
+
 template <int N>
 __device__ __forceinline__ void load_slots(int* out, const int32_t* p) {
   if constexpr (N == 4) {
@@ -185,13 +202,13 @@ constexpr int kLdsCand = 8192;  // candidates kept in LDS (32 KB); more go to th
 constexpr int kXcd = 8;
 
 // PX: K scores from the sketch proxy records instead of the moments.
-// K1: k_cap = v_cap = 1 (records [m_ref, M2, M3, M4, mass]), the common
+// K1: k_cap = v_cap = 1 (records [m_ref, M2, M3, M4, D*, e*, mass]), the common
 // store budget of one K and one V slot per page, scored without the
 // generic rank loops.
 template <int D, bool PX, bool K1>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) void decode_select_kernel(carekv_arena A, DecodeArgs a) {
   constexpr int NCG = D / 32;
-  constexpr int FMAX = 1 + 3 * NCG + kVtb;
+  constexpr int FMAX = 2 + 4 * NCG + kVtb;
   __shared__ BlockScratch bs;
   __shared__ int hist[2][256];  // one histogram per wave pair
   __shared__ float s_qs[NCG * 64];  // q_cg P per channel group (sketch proxy)
@@ -322,10 +339,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
       load_slots<NCG>(ksl, A.k_slot + pg * NCG);
       load_slots<kVtb>(vsl, A.v_slot + pg * kVtb);
       const uint2 e2 = *reinterpret_cast<const uint2*>(A.v_err + pg * kVtb);
-      const float* rp = recq + (long)p * 5;
-      const float r0 = rp[0], M2 = rp[1], M3 = rp[2], M4 = rp[3], E = rp[4];
+      const float* rp = recq + (long)p * 7;
+      const float r0 = rp[0], M2 = rp[1], M3 = rp[2], M4 = rp[3], Ds = rp[4], es = rp[5], E = rp[6];
       const bool ok = L > 0.f && nv > 0 && hm;
-      const float c = ok ? __builtin_amdgcn_exp2f(r0 - M) * invL : 0.f;
+      const float c = ok ? exp2_dn(r0 - M) * invL : 0.f;
       int nks = 0, nvs = 0;
 #pragma unroll
       for (int cg = 0; cg < NCG; ++cg) nks += slot_ok(A, ksl[cg]) ? 1 : 0;
@@ -335,8 +352,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
       const bool kh = nks > 0;
       float ks = -1.f;
       if (ok && kh) {
-        const float q2 = c * c * (M2 - c * (2.f * M3 - c * M4));
-        ks = __builtin_amdgcn_sqrtf(fmaxf(q2, 0.f)) * __builtin_amdgcn_sqrtf(vsq);
+        // sum_t dS^2 a^2 (1 - a)^2 = c^2 [M2 - c (2 M3 - c M4) + D* (e* (1 - a*))^2]: the page's
+        // token t* evaluated directly, and c kept outside the root (c^2 of a far page underflows)
+        const float wr = es * (1.f - c * es);
+        const float q2 = (M2 - c * (2.f * M3 - c * M4)) + Ds * (wr * wr);
+        ks = kscore_underflows(c, M2, Ds, es) ? 0.f : (c * sqrt_dn(fmaxf(q2, 0.f))) * __builtin_amdgcn_sqrtf(vsq);
         if (!isfinite(ks)) ks = 0.f;
         ks = ks * a.sens;
         sumK += ks;
@@ -376,20 +396,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
 #pragma unroll
     for (int f = 0; f < FMAX; ++f) r[f] = f < F ? rp[f] : 0.f;
     const bool ok = L > 0.f && nv > 0 && hm;
-    const float c = ok ? __builtin_amdgcn_exp2f(r[0] - M) * invL : 0.f;
+    const float c = ok ? exp2_dn(r[0] - M) * invL : 0.f;
     const float vnorm = __builtin_amdgcn_sqrtf(vsq);
     if constexpr (!PX) {
+      float es = 0.f;  // e of the page's token t*
+#pragma unroll
+      for (int f = 1; f < FMAX; ++f)
+        if (f == 1 + 4 * k_cap) es = r[f];
+      const float wr = es * (1.f - c * es);
       int rk = 0;
 #pragma unroll
       for (int cg = 0; cg < NCG; ++cg) {
         if (!ok || !slot_ok(A, ksl[cg])) continue;
         if (rk >= k_cap) { ovf = true; continue; }
-        float M2 = 0.f, M3 = 0.f, M4 = 0.f;
+        float M2 = 0.f, M3 = 0.f, M4 = 0.f, Ds = 0.f;
 #pragma unroll
         for (int j = 0; j < NCG; ++j)
-          if (j == rk) { M2 = r[1 + 3 * j]; M3 = r[2 + 3 * j]; M4 = r[3 + 3 * j]; }
-        const float q2 = c * c * (M2 - c * (2.f * M3 - c * M4));
-        float ks = __builtin_amdgcn_sqrtf(fmaxf(q2, 0.f)) * vnorm;
+          if (j == rk) { M2 = r[1 + 4 * j]; M3 = r[2 + 4 * j]; M4 = r[3 + 4 * j]; Ds = r[4 + 4 * j]; }
+        const float q2 = (M2 - c * (2.f * M3 - c * M4)) + Ds * (wr * wr);
+        float ks = kscore_underflows(c, M2, Ds, es) ? 0.f : (c * sqrt_dn(fmaxf(q2, 0.f))) * vnorm;
         if (!isfinite(ks)) ks = 0.f;
         ks = ks * a.sens;
         sc[p * k_cap + rk] = ks;
@@ -407,7 +432,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
       float vsc = -1.f;
       if (vb * kVtb < nv) {
         float E = 0.f;
-        const int fe = 1 + 3 * k_cap + rv;
+        const int fe = 2 + 4 * k_cap + rv;
 #pragma unroll
         for (int f = 1; f < FMAX; ++f)
           if (f == fe) E = r[f];
@@ -515,7 +540,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
         const int nvp = A.valid[pg_base + (i >> 4)];
         if ((i & 15) >= nvp) continue;
         ++nt;
-        float at = L > 0.f ? __builtin_amdgcn_exp2f(xq[i] - M) : 0.f;
+        float at = L > 0.f ? exp2_dn(xq[i] - M) : 0.f;
         at = a.pf ? (float)(_Float16)at : at / L;
         const float ac = fmaxf(at, kEps);
         h += ac * logf(ac);

@@ -189,7 +189,19 @@ void decode_stream_kernel(carekv_arena A, DecodeArgs a) {
     if (corr && cm.meta) {
       // ---- page record (layout in decode_common.h)
       float* rec = a.rec + ((long)bk * GQ * a.Pmax + p) * a.F + ln * rq;
-      if (lj == 0 && ln < GQ) rec[0] = m_new;
+      // t*: the page's first token of largest e for the lane's query (istar:
+      // its index among the lane's 4 tokens, out of range in the other lanes)
+      const float emax = col_max(fmaxf(fmaxf(e[0], e[1]), fmaxf(e[2], e[3])));
+      int fi = 4;
+#pragma unroll
+      for (int i = 3; i >= 0; --i)
+        if (e[i] == emax) fi = i;
+      const float tstar = -col_max(-(fi < 4 ? (float)(4 * lj + fi) : 16.f));
+      const int istar = (int)tstar - 4 * lj;
+      if (lj == 0 && ln < GQ) {
+        rec[0] = m_new;
+        rec[1 + 4 * a.k_cap] = emax;
+      }
       if (ln < GQ)
         *reinterpret_cast<uint2*>(a.ebuf + (((long)bk * GQ + ln) * a.Pmax + p) * 16 + 4 * lj) =
             make_uint2(h2bits(half2_t{ap[0], ap[1]}), h2bits(half2_t{ap[2], ap[3]}));
@@ -202,23 +214,28 @@ void decode_stream_kernel(carekv_arena A, DecodeArgs a) {
         if (a.proxy) { ++rk; continue; }  // the sketch proxy scores K slots without the moments
         const long so = (long)seq * A.n_slots + slot;
         const float4_t racc = kslot_dot_w(krow[cg], sqr, D, cg, ln, lj);
-        // moments of u = racc * e (dS = racc * f scales them by f^2):
-        // M2 = sum u^2, M3 = sum u^2 e, M4 = sum (u e)^2
-        float M2 = 0.f, M3 = 0.f, M4 = 0.f;
+        // moments of u = racc * e over the tokens other than t* (dS = racc
+        // * f scales them by f^2): M2 = sum u^2, M3 = sum u^2 e, M4 = sum
+        // (u e)^2; D* = racc_t*^2
+        float M2 = 0.f, M3 = 0.f, M4 = 0.f, Ds = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
+          if (i == istar) {
+            Ds = racc[i] * racc[i];
+            continue;
+          }
           const float u = racc[i] * e[i];
           const float ue = u * e[i];
           M2 = fmaf(u, u, M2);
           M3 = fmaf(ue, u, M3);
           M4 = fmaf(ue, ue, M4);
         }
-        // reduce over the 4 token groups j: group 0 ends with M2, 1 with
-        // M3, 2 and 3 with M4
-        const float mj = moments_reduce(M2, M3, M4);
-        if (lj < 3 && ln < GQ) {
+        // reduce over the 4 token groups j: group j ends with the j-th of
+        // M2, M3, M4, D*
+        const float mj = moments_reduce4(M2, M3, M4, Ds);
+        if (ln < GQ) {
           const float f = h2f(A.k_res_scale[so]) * a.inv_sqrt_d;
-          rec[1 + 3 * rk + lj] = mj * (f * f);
+          rec[1 + 4 * rk + lj] = mj * (f * f);
         }
         ++rk;
       }
@@ -229,7 +246,7 @@ void decode_stream_kernel(carekv_arena A, DecodeArgs a) {
         if (vb == lj) my_rank = rv;
         ++rv;
       }
-      if (my_rank >= 0 && my_rank < a.v_cap && ln < GQ) rec[1 + 3 * a.k_cap + my_rank] = (e[0] + e[1]) + (e[2] + e[3]);
+      if (my_rank >= 0 && my_rank < a.v_cap && ln < GQ) rec[2 + 4 * a.k_cap + my_rank] = (e[0] + e[1]) + (e[2] + e[3]);
     }
     lds_sync_wave();
   }

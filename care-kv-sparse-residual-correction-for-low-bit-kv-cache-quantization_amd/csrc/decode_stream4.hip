@@ -345,6 +345,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     const bool rec_lane = sc < GQ && my_meta != 0 && my_nv > 0;
     const uint32_t so_rp = so_rec + (uint32_t)(p0 * a.F) * 4u;  // the window's part of the offsets is uniform
     if (rec_lane && sbk == 0) __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(m_new), rs_ws, vo_rec, so_rp, 0);
+    // t*: the first token of largest e of page lj for query sc (istar: its
+    // index among the lane's 4 tokens, out of range in the other lanes)
+    int istar = -1;
+    if (mom) {
+      const float emax = row4_max(fmaxf(fmaxf(e[0], e[1]), fmaxf(e[2], e[3])));
+      int fi = 4;
+#pragma unroll
+      for (int i = 3; i >= 0; --i)
+        if (e[i] == emax) fi = i;
+      const float tstar = -row4_max(-(fi < 4 ? (float)(4 * sbk + fi) : 16.f));
+      istar = (int)tstar - 4 * sbk;
+      if (rec_lane && sbk == 0)
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(emax), rs_ws, vo_rec,
+                                              so_rp + (uint32_t)(1 + 4 * a.k_cap) * 4u, 0);
+    }
     if (rec_lane)
       __builtin_amdgcn_raw_buffer_store_b64(u2_t{e01, e23}, rs_ws,
                                             vo_e, so_e + (uint32_t)p0 * 32u, 0);
@@ -375,24 +390,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         const half4_t bq = *reinterpret_cast<const half4_t*>(sqr4 + ((cgr * 8 + s) * 4 + sc) * 4);
         racc = mfma4x4(ar, bq, racc);
       }
-      // moments of u = racc * e (dS = racc * f scales them by f^2)
-      float M2 = 0.f, M3 = 0.f, M4 = 0.f;
+      // moments of u = racc * e over the tokens other than t* (dS = racc *
+      // f scales them by f^2), and D* = racc_t*^2
+      float M2 = 0.f, M3 = 0.f, M4 = 0.f, Ds = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
+        if (i == istar) {
+          Ds = racc[i] * racc[i];
+          continue;
+        }
         const float u = racc[i] * e[i];
         const float ue = u * e[i];
         M2 = fmaf(u, u, M2);
         M3 = fmaf(ue, u, M3);
         M4 = fmaf(ue, ue, M4);
       }
-      M2 = row4_sum(M2); M3 = row4_sum(M3); M4 = row4_sum(M4);
+      M2 = row4_sum(M2); M3 = row4_sum(M3); M4 = row4_sum(M4); Ds = row4_sum(Ds);
       if (has && rec_lane && sbk == 0) {
         const float f = h2f((uint16_t)kscr) * a.inv_sqrt_d;
         const float f2 = f * f;
-        const uint32_t o = so_rp + (uint32_t)(1 + 3 * r) * 4u;
+        const uint32_t o = so_rp + (uint32_t)(1 + 4 * r) * 4u;
         __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(M2 * f2), rs_ws, vo_rec, o, 0);
         __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(M3 * f2), rs_ws, vo_rec, o + 4u, 0);
         __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(M4 * f2), rs_ws, vo_rec, o + 8u, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(Ds * f2), rs_ws, vo_rec, o + 12u, 0);
       }
     }
     // V block sbk of page lj: its stored-slot rank and mass
@@ -400,7 +421,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
       const int vrank = (int)__builtin_popcount(__builtin_amdgcn_ubfe(vmask, 0u, (uint32_t)sbk));  // blocks before sbk
       if (vrank < a.v_cap)
         __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint((e[0] + e[1]) + (e[2] + e[3])), rs_ws,
-                                              vo_rec + (uint32_t)vrank * 4u, so_rp + (uint32_t)(1 + 3 * a.k_cap) * 4u, 0);
+                                              vo_rec + (uint32_t)vrank * 4u, so_rp + (uint32_t)(2 + 4 * a.k_cap) * 4u, 0);
     }
   }
 

@@ -146,3 +146,42 @@ def test_workspace_spill_vs_oracle(paper_env):
     torch.cuda.synchronize()
     _check_slices(cache, q, out, diag, [(0, 0), (0, 1), (1, 0), (1, 1)], 64, 64,
                   dict(store_budget_mode="absolute", store_abs_k=2, store_abs_v=4))
+
+
+def test_peaked_attention_vs_oracle(paper_env):
+    """MHA with heavy-tailed K/V (config 2's Student-t channels) and, in
+    every head, one token whose key lines up with the query (logit 22 over
+    a typical maximum near 10): that token takes nearly all the attention
+    (1 - a around 1e-5), where sum dS^2 a^2 (1 - a)^2 expanded in moments
+    of a would cancel, and the other pages' K score terms fall to fp32
+    denormals; the K scores, selections and outputs must still follow the
+    oracle."""
+    import care_kv
+    dev = torch.device("cuda", 0)
+    B, Hq, Hkv, D, N = 2, 4, 4, 128, 4096
+    cfg = care_kv.CacheConfig(num_layers=1, num_heads=Hq, num_kv_heads=Hkv, head_dim=D, page_size=16,
+                              max_pages=N // 16 + 4, base_bits=3, group_size=32, k_channel_group=32,
+                              v_token_block=4, sketch_dim=32, packed_base=True, scale_quant="int8",
+                              store_budget_mode="ratio", store_budget_ratio=0.03, read_budget_ratio=0.0,
+                              read_budget_mode="absolute", read_abs_k=64, read_abs_v=64, route_policy="joint")
+    cache = care_kv.CAREKVCache(cfg, device=dev, n_seq=B)
+    g = torch.Generator(device=dev).manual_seed(31)
+    q = torch.randn(B, Hq, D, generator=g, device=dev)
+    for b in range(B):
+        K = torch.randn(Hkv, N, D, generator=g, device=dev)
+        V = torch.randn(Hkv, N, D, generator=g, device=dev)
+        for X in (K, V):  # 2% of the channels Student-t (nu = 3), x6
+            ch = torch.randperm(D, generator=g, device=dev)[:3]
+            z = torch.randn(Hkv, N, 3, generator=g, device=dev)
+            chi = (torch.randn(3, Hkv, N, 3, generator=g, device=dev) ** 2).sum(0)
+            X[:, :, ch] = 6.0 * z / torch.sqrt(chi / 3.0)
+        for h in range(Hkv):  # the dominant token, in a different page per head
+            t = 1000 + 517 * h + 131 * b
+            K[h, t] = q[b, h] * (22.0 * math.sqrt(D) / float(q[b, h].norm()) ** 2)
+        cache.write_prefill(0, K.half(), V.half(), seqs=[b])
+    q = q.half()
+    out, diag = care_kv.decode_attention(cache, 0, q, diag_cap=256)
+    torch.cuda.synchronize()
+    n = _check_slices(cache, q, out, diag, [(b, h) for b in range(B) for h in range(Hkv)], 64, 64,
+                      dict(store_budget_mode="ratio", store_budget_ratio=0.03))
+    assert n == B * Hq
