@@ -291,6 +291,44 @@ def prefill_bench(args):
     ms = ev0.elapsed_time(ev1) / args.steps
     flops = 4.0 * B * H * D * (T * (T + 1) / 2)  # QK^T and PV over the causal triangle
     tflops = flops / (ms * 1e-3) / 1e12
+    cpu = parity = None
+    if not args.no_cpu_baseline:
+        # the oracle (numpy restatement of _causal_attention_pure) on 512 query rows of two (sequence, head)
+        # pairs, timed, extrapolated per row to the whole batch (the oracle's cost per row is one full
+        # T-long score row, masked), and the GPU output of those rows checked against it
+        import numpy as np
+        from oracle.attention import causal_attention_pure
+        from oracle.check import output_errors
+        rows = np.linspace(0, T - 1, 512).astype(np.int64)
+        pairs = [(0, 0), (B - 1, H - 1)]
+        t_cpu, mx_all, rel_all, ratio_all = 0.0, 0.0, 0.0, 0.0
+        for (bb, hh) in pairs:
+            qn = q[bb, hh:hh + 1].cpu().numpy()
+            kn, vn = kh[bb, hh:hh + 1].cpu().numpy(), vh[bb, hh:hh + 1].cpu().numpy()
+            t0 = time.perf_counter()
+            ref, _ = causal_attention_pure(qn, kn, vn, causal=True, rows=rows)
+            t_cpu += time.perf_counter() - t0
+            got = out[bb, hh, torch.from_numpy(rows).to(dev)].cpu().numpy()
+            # the bar of tests/test_gpu_prefill.py: 2e-3 of the head's V scale (log-normal channels), or one
+            # fp16 ulp of the reference where larger
+            vs = max(1.0, float(np.sqrt(np.mean(vn.astype(np.float32) ** 2))))
+            mx, rel, ratio = output_errors(got, ref[0], atol=2e-3 * vs)
+            mx_all, rel_all, ratio_all = max(mx_all, mx), max(rel_all, rel), max(ratio_all, ratio)
+        per_row = t_cpu / (len(pairs) * len(rows))
+        cpu_ms = per_row * B * H * T * 1e3
+        try:
+            import threadpoolctl
+            cores = max([i.get("num_threads", 1) for i in threadpoolctl.threadpool_info()] + [1])
+        except Exception:
+            cores = int(os.environ.get("OMP_NUM_THREADS", "1"))
+        cpu = {"value": round(cpu_ms, 1), "unit": "ms/step", "cores": cores, "kind": "port",
+               "sample": f"{len(rows)} query rows of {len(pairs)} of {B * H} (sequence, head) pairs, numpy "
+                         f"oracle ({per_row * 1e3:.3f} ms per row), extrapolated per row to {B * H * T} rows"}
+        parity = {"rows": len(pairs) * len(rows), "max_abs": round(mx_all, 6), "rel_l2": round(rel_all, 6),
+                  "bar_ratio": round(ratio_all, 3), "pass": bool(ratio_all <= 1.0 and rel_all <= 1e-2),
+                  "bar": "out within 2e-3 x rms(V) (or 1 fp16 ulp) and rel-L2 1e-2 of the oracle"}
+        log(f"[bench] c4 cpu oracle {per_row * 1e3:.3f} ms/row -> {cpu_ms / 1e3:.1f} s/step extrapolated; "
+            f"parity {parity}")
     store_bytes = 2 * B * H * T * D * 2  # fp16 K and V read once by the store path
     log(f"[bench] c4 prefill attention {ms * 1e3:.1f} us/step, {flops / 1e12:.3f} TFLOP -> {tflops:.1f} TFLOP/s "
         f"({tflops / 2500 * 100:.1f}% of 2.5 PF fp16 dense); store path {store_ms:.1f} ms for {B} sequences")
@@ -306,9 +344,13 @@ def prefill_bench(args):
                      "algorithmic_flops_per_launch": flops, "launch_us": round(ms * 1e3, 2)},
         "store_path": {"ms": round(store_ms, 3), "fp16_bytes_in": store_bytes,
                        "gbps_in": round(store_bytes / (store_ms * 1e-3) / 1e9, 1)},
-        "cpu_baseline": None,
+        "cpu_baseline": cpu,
+        "parity": parity,
     }
     print(json.dumps(line), flush=True)
+    if parity is not None and not parity["pass"]:
+        log("[bench] PARITY FAILED: the GPU prefill attention differs from the oracle beyond the bar")
+        sys.exit(3)
 
 
 # prefill-time carekv_stored correction (layer.py:780-838) at the TinyLlama
