@@ -148,17 +148,20 @@ def test_workspace_spill_vs_oracle(paper_env):
                   dict(store_budget_mode="absolute", store_abs_k=2, store_abs_v=4))
 
 
-def test_peaked_attention_vs_oracle(paper_env):
+@pytest.mark.parametrize("Hq,Hkv", [(4, 4), (16, 2)], ids=["mha-stream4", "gqa8-generic"])
+def test_peaked_attention_vs_oracle(paper_env, Hq, Hkv):
     """MHA with heavy-tailed K/V (config 2's Student-t channels) and, in
     every head, one token whose key lines up with the query (logit 22 over
     a typical maximum near 10): that token takes nearly all the attention
     (1 - a around 1e-5), where sum dS^2 a^2 (1 - a)^2 expanded in moments
     of a would cancel, and the other pages' K score terms fall to fp32
     denormals; the K scores, selections and outputs must still follow the
-    oracle."""
+    oracle; through the 4-query-head streaming kernel (MHA) and the generic
+    one (8 query heads per kv head)."""
     import care_kv
     dev = torch.device("cuda", 0)
-    B, Hq, Hkv, D, N = 2, 4, 4, 128, 4096
+    B, D, N = 2, 128, 4096
+    grp = Hq // Hkv
     cfg = care_kv.CacheConfig(num_layers=1, num_heads=Hq, num_kv_heads=Hkv, head_dim=D, page_size=16,
                               max_pages=N // 16 + 4, base_bits=3, group_size=32, k_channel_group=32,
                               v_token_block=4, sketch_dim=32, packed_base=True, scale_quant="int8",
@@ -175,9 +178,10 @@ def test_peaked_attention_vs_oracle(paper_env):
             z = torch.randn(Hkv, N, 3, generator=g, device=dev)
             chi = (torch.randn(3, Hkv, N, 3, generator=g, device=dev) ** 2).sum(0)
             X[:, :, ch] = 6.0 * z / torch.sqrt(chi / 3.0)
-        for h in range(Hkv):  # the dominant token, in a different page per head
+        for h in range(Hkv):  # the dominant token of the group's first query head, a different page per head
             t = 1000 + 517 * h + 131 * b
-            K[h, t] = q[b, h] * (22.0 * math.sqrt(D) / float(q[b, h].norm()) ** 2)
+            qh = q[b, h * grp]
+            K[h, t] = qh * (22.0 * math.sqrt(D) / float(qh.norm()) ** 2)
         cache.write_prefill(0, K.half(), V.half(), seqs=[b])
     q = q.half()
     out, diag = care_kv.decode_attention(cache, 0, q, diag_cap=256)
