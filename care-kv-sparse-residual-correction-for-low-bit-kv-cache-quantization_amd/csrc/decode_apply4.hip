@@ -32,7 +32,10 @@
 
 namespace carekv {
 
-template <int D, int BITS, int SM>
+// K1: at most one stored K slot and one stored V block per page (k_cap =
+// v_cap = 1, the common store budget): the page's slot and block come from
+// two ballots over the metadata lanes instead of the per-rank searches.
+template <int D, int BITS, int SM, bool K1>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void decode_apply4_kernel(carekv_arena A, DecodeArgs a) {
   using G = PageGeom<D, BITS>;
   using PR = Pairs<4, 32, 4>;  // pair schedule of a K residual row
@@ -135,7 +138,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     }
     const unsigned kbits = x.mk & 15u, vbits = x.mk >> 4;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < (K1 ? 1 : 4); ++r) {
       const unsigned long long kb = __ballot((kbits >> r) & 1u), vb = __ballot((vbits >> r) & 1u);
 #pragma unroll
       for (int pi = 0; pi < 4; ++pi) {
@@ -168,6 +171,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     e.mref = a.rec[r * a.F];
     return e;
   };
+  // K1: the first stored K channel group (-1: none) and the first stored V
+  // block of the lane's page lj, from ballots over its metadata lanes
+  struct First { int cg, slot, vb; };
+  auto first_slots = [&](const WinPre& x) {
+    First f;
+    const int fld = lane & 15;
+    const bool in_arena = x.meta >= 0 && x.meta < A.n_slots;
+    const unsigned long long kb = __ballot(fld >= 2 && fld < 2 + NCG && in_arena);
+    const unsigned long long vb = __ballot(fld >= 6 && fld < 6 + kVtb && in_arena);
+    const uint32_t km = (uint32_t)(kb >> (16 * lj + 2)) & ((1u << NCG) - 1u);
+    const uint32_t vm = (uint32_t)(vb >> (16 * lj + 6)) & 0xfu;
+    f.cg = km ? (int)__builtin_ctz(km) : -1;
+    f.vb = vm ? (int)__builtin_ctz(vm) : -1;
+    f.slot = __shfl(x.meta, (lane & 48) + 2 + (km ? (int)__builtin_ctz(km) : 0), 64);
+    return f;
+  };
   // K residual row ln of the lowest selected rank of the lane's page lj
   struct KRow { uint32_t w[4]; float scale; int rank; };
   auto load_krow = [&](const WinPre& x, const Plan& p) {
@@ -175,12 +194,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     const unsigned ka = lj == 0 ? p.kany[0] : lj == 1 ? p.kany[1] : lj == 2 ? p.kany[2] : p.kany[3];
     const int r0 = ka ? __builtin_ctz(ka) : -1;
     int slot = -1, cnt = 0;
+    if constexpr (K1) {
+      const First f = first_slots(x);
+      slot = (r0 == 0 && f.cg >= 0) ? f.slot : -1;
+    } else {
 #pragma unroll
-    for (int cg = 0; cg < NCG; ++cg) {
-      const int s = __shfl(x.meta, (lane & 48) + 2 + cg, 64);
-      if (s < 0 || s >= A.n_slots) continue;
-      if (cnt == r0) slot = s;
-      ++cnt;
+      for (int cg = 0; cg < NCG; ++cg) {
+        const int s = __shfl(x.meta, (lane & 48) + 2 + cg, 64);
+        if (s < 0 || s >= A.n_slots) continue;
+        if (cnt == r0) slot = s;
+        ++cnt;
+      }
     }
     const auto v = __builtin_amdgcn_raw_buffer_load_b128(kres, slot >= 0 ? (uint32_t)slot * G::KSB + ln * 16 : kOut, 0, 0);
     k.w[0] = v[0]; k.w[1] = v[1]; k.w[2] = v[2]; k.w[3] = v[3];
@@ -254,7 +278,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
 
     // ---- dS over the selected K slots (rank r: r-th stored slot of the page)
     float wk[4] = {0.f, 0.f, 0.f, 0.f};
-    {
+    First cf{-1, -1, -1};
+    if constexpr (K1) cf = first_slots(cur);
+    if constexpr (K1) {
+      // the page's one stored K slot, its row prefetched by load_krow
+      const unsigned ka = lj == 0 ? cp.kany[0] : lj == 1 ? cp.kany[1] : lj == 2 ? cp.kany[2] : cp.kany[3];
+      if (kany_all & 1u) {
+        const bool need = cf.cg >= 0 && (ka & 1u);
+        const int cgq = cf.cg >= 0 ? cf.cg : 0;
+        float4_t racc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 8; ++s) {
+          const half2_t c0 = code_pair<4, 32, 4>(kr0.w, 2 * s);
+          const half2_t c1 = code_pair<4, 32, 4>(kr0.w, 2 * s + 1);
+          const half4_t ar = {c0[0], c0[1], c1[0], c1[1]};
+          const half4_t bq = *reinterpret_cast<const half4_t*>(sqr4 + ((cgq * 8 + s) * 4 + sc) * 4);
+          racc = mfma4x4(ar, bq, racc);
+        }
+        const float use = (need && (kbits & 1u)) ? kr0.scale : 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) wk[i] = fmaf(racc[i], use, wk[i]);
+      }
+    } else {
       int kslot[NCG];
 #pragma unroll
       for (int cg = 0; cg < NCG; ++cg) {
@@ -304,12 +349,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
 
     // ---- weights of V_hat (ck) and of the V residual rows (cv)
     int vrank = -1, rvn = 0;
+    if constexpr (K1) {
+      vrank = sbk == cf.vb ? 0 : -1;  // later stored blocks rank past v_cap
+    } else {
 #pragma unroll
-    for (int v = 0; v < kVtb; ++v) {
-      const int s = __shfl(cur.meta, (lane & 48) + 6 + v, 64);
-      if (s < 0 || s >= A.n_slots) continue;
-      if (v == sbk) vrank = rvn;
-      ++rvn;
+      for (int v = 0; v < kVtb; ++v) {
+        const int s = __shfl(cur.meta, (lane & 48) + 6 + v, 64);
+        if (s < 0 || s >= A.n_slots) continue;
+        if (v == sbk) vrank = rvn;
+        ++rvn;
+      }
     }
     const bool vsel = vrank >= 0 && vrank < a.v_cap && ((vbits >> vrank) & 1u) && 4 * sbk < my_nv;
     float ck[4], cv[4];
@@ -396,8 +445,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
 int launch_decode_apply4(const carekv_arena& A, const DecodeArgs& a, hipStream_t s) {
   const dim3 grid(a.napply, A.n_kv_heads, a.B);
   return dispatch_dbs(A.head_dim, A.base_bits, A.scale_mode, [&](auto d, auto bb, auto sm) {
-    hipLaunchKernelGGL((decode_apply4_kernel<decltype(d)::value, decltype(bb)::value, decltype(sm)::value>), grid,
-                       dim3(256), 0, s, A, a);
+    if (a.k_cap == 1 && a.v_cap == 1)
+      hipLaunchKernelGGL((decode_apply4_kernel<decltype(d)::value, decltype(bb)::value, decltype(sm)::value, true>),
+                         grid, dim3(256), 0, s, A, a);
+    else
+      hipLaunchKernelGGL((decode_apply4_kernel<decltype(d)::value, decltype(bb)::value, decltype(sm)::value, false>),
+                         grid, dim3(256), 0, s, A, a);
     CAREKV_CHECK_LAUNCH("decode_apply4");
     return CAREKV_OK;
   });
