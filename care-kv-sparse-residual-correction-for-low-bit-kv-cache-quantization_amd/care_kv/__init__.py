@@ -21,7 +21,7 @@ from .attention import (CAREKVAttention, CAREKVMultiHeadAttention, apply_slot_co
                         get_debug_stats, prefill_correction, reset_debug_stats)
 from .prefill import dequantize_rows, prefill_attention, quant_dequant, quantize_rows
 from .layer import CAREKVLayer
-from .llama_patch import CAREKVLlamaAttention, patch_llama_model, reset_all_caches
+from .llama_patch import CAREKVHFCache, CAREKVLlamaAttention, patch_llama_model, reset_all_caches
 from .adapter import CAREKVAdapter
 from ._lib import CarekvError
 
@@ -44,5 +44,5 @@ __all__ = [
     # additions of this build
     "resolve_read_knobs", "resolve_store_knobs", "get_sketch_proj", "kivi_qdq",
     "decode_attention", "prefill_correction", "prefill_attention", "quantize_rows", "dequantize_rows",
-    "quant_dequant", "CAREKVAdapter", "CarekvError",
+    "quant_dequant", "CAREKVAdapter", "CarekvError", "CAREKVHFCache",
 ]

@@ -109,20 +109,81 @@ class CAREKVLayer(nn.Module):
         return O.transpose(1, 2).reshape(B, T, Hq * D).to(self.W_O.dtype) @ self.W_O.T
 
     @staticmethod
-    def _check_mask(attention_mask: Optional[Tensor], T: int):
-        """The kernel applies the causal mask itself (the attention_mask=None
-        branch of layer.py:951-962).  A mask that masks more than the causal
-        triangle in any sequence of the batch (padding) is refused rather than
-        ignored: the last query row of every sequence must see all keys
-        (boolean masks: all True; additive masks: no negative entry)."""
+    def _key_runs(attention_mask: Optional[Tensor], B: int, T: int) -> Optional[list]:
+        """Each sequence's run of real tokens [s, e) of the T prompt rows, or
+        None when every sequence sees all of them (the kernel applies the
+        causal mask itself, as the attention_mask=None branch of
+        layer.py:951-962 does).
+
+        The mask is the one layer.py:952-957 adds to the scores: (T, T),
+        (B or 1, T, T) or (B or 1, 1, T, T), boolean (True: visible) or
+        additive (0: visible, at most half the dtype's lowest value:
+        masked); a (B, S) keep-mask (nonzero: a real token) is read as
+        HF's models take it.  A sequence's real tokens are the keys its last
+        query row sees; they must form one run (left or right padding).
+        Other additive values (a bias the kernel would not apply) and
+        visible sets with holes are refused."""
         if attention_mask is None or not torch.is_tensor(attention_mask):
-            return
+            return None
         m = attention_mask
-        if m.dim() >= 2:
-            m = m.reshape(-1, m.shape[-2], m.shape[-1])[:, -1, -T:] if m.dim() > 2 else m[:, -T:]
-        padded = (not bool(m.all())) if m.dtype == torch.bool else bool((m < 0).any())
-        if padded:
-            raise NotImplementedError("padded attention masks are not supported by the prefill kernel")
+        if m.dim() == 2 and tuple(m.shape) != (T, T) and m.shape[0] == B and m.shape[1] >= T:
+            vis = m[:, -T:] != 0                       # (B, S) keep-mask
+        else:
+            if m.dim() == 4:
+                m = m[:, 0]
+            if m.dim() == 2:
+                m = m.unsqueeze(0)
+            if m.dim() != 3 or m.shape[-1] < T or m.shape[-2] < T:
+                raise NotImplementedError(f"attention mask of shape {tuple(attention_mask.shape)}: expected "
+                                          "(T, T), (B, T, T), (B, 1, T, T) or a (B, S) keep-mask")
+            m = m[:, -T:, -T:]
+            if m.dtype == torch.bool:
+                vis = m[:, -1]
+            else:
+                lo = torch.finfo(m.dtype).min / 2 if m.dtype.is_floating_point else -1
+                if bool((~((m == 0) | (m <= lo))).any()):
+                    raise NotImplementedError("an additive attention mask with values other than 0 and the "
+                                              "masked minimum (a score bias) is not applied by the prefill kernel")
+                vis = m[:, -1] == 0
+        if bool(vis.all()):
+            return None
+        if vis.shape[0] not in (1, B):
+            raise NotImplementedError(f"attention mask batch {vis.shape[0]} for {B} sequences")
+        vis = vis.expand(B, T).cpu()
+        runs = []
+        for b in range(B):
+            idx = torch.nonzero(vis[b]).flatten()
+            s, e = (int(idx[0]), int(idx[-1]) + 1) if idx.numel() else (0, 0)
+            if e - s != idx.numel():
+                raise NotImplementedError(f"sequence {b}: the visible keys of its last row are not one run "
+                                          "(only left or right padding is supported)")
+            runs.append((s, e))
+        return runs
+
+    def _prefill_runs(self, cache: CAREKVCache, hidden: Tensor, runs, sink_tokens: int,
+                      position_embeddings, token_start_abs: int, seqs: Sequence[int]) -> Tensor:
+        """A padded batch: the sequences whose rows are all real run as one
+        batch, every other sequence alone over its real rows [s, e) (RoPE
+        rows sliced alike), so no pad row reaches a page or an attention
+        row.  Pad rows of the output are zero."""
+        B, T, _ = hidden.shape
+        out = hidden.new_zeros((B, T, self.W_O.shape[0]))
+
+        def pe(rows, sl):
+            if position_embeddings is None:
+                return None
+            return tuple((x[rows] if x.shape[0] == B else x[[0] * len(rows)])[:, sl] for x in position_embeddings)
+        full = [b for b, (s, e) in enumerate(runs) if (s, e) == (0, T)]
+        if full:
+            out[full] = self.prefill(cache, hidden[full], sink_tokens=sink_tokens,
+                                     position_embeddings=pe(full, slice(None)), token_start_abs=token_start_abs,
+                                     seqs=[seqs[b] for b in full])
+        for b, (s, e) in enumerate(runs):
+            if (s, e) != (0, T) and e > s:
+                out[b, s:e] = self.prefill(cache, hidden[b:b + 1, s:e], sink_tokens=sink_tokens,
+                                           position_embeddings=pe([b], slice(s, e)),
+                                           token_start_abs=token_start_abs, seqs=[seqs[b]])[0]
+        return out
 
     # ------------------------------------------------------------ prefill
     def prefill(self, cache: CAREKVCache, hidden: Tensor, sink_tokens: int = 4,
@@ -137,20 +198,29 @@ class CAREKVLayer(nn.Module):
         dequantised K_hat / V_hat otherwise; ``carekv_stored`` adds the
         sparse correction from the stored slots (``prefill_correction``,
         layer.py:808-838).  The in-memory correction of ``carekv_eval`` is
-        not built: that mode returns the base attention and warns once."""
+        not built: that mode returns the base attention and warns once.
+
+        A padding mask (left or right padding) keeps each sequence's pad
+        rows out of its pages and its attention: those sequences run over
+        their real rows alone and their pad rows return zero.  The reference
+        adds the mask to one sequence's scores and still stores the pad rows
+        (layer.py:952-957); its B > 1 loop cannot broadcast a batched mask."""
         squeeze = hidden.dim() == 2
         if squeeze:
             hidden = hidden.unsqueeze(0)
         cfg = self.cfg
         B, T, _ = hidden.shape
         mode = resolve_prefill_mode()
-        self._check_mask(attention_mask, T)
+        seqs = list(range(B)) if seqs is None else list(seqs)
+        runs = self._key_runs(attention_mask, B, T)
+        if runs is not None:
+            out = self._prefill_runs(cache, hidden, runs, sink_tokens, position_embeddings, token_start_abs, seqs)
+            return out[0] if squeeze else out
         Q, K, V = self._project(hidden)
         if position_embeddings is not None:
             cos, sin = position_embeddings
             Q, K = _rope(Q, K, cos.to(Q.dtype), sin.to(Q.dtype))
         Qh, Kh, Vh = Q.to(F16).contiguous(), K.to(F16).contiguous(), V.to(F16).contiguous()
-        seqs = list(range(B)) if seqs is None else list(seqs)
         hats = cache.write_prefill(self.layer_id, Kh, Vh, token_start_abs=token_start_abs,
                                    sink_tokens=sink_tokens, seqs=seqs)
         if mode == "fp":

@@ -12,7 +12,13 @@ row).  Differences from the reference, all at the boundary:
 * the forward accepts both the transformers 4.x keyword ``past_key_value``
   and the 5.x ``past_key_values``, and returns ``(attn_output, None)`` on
   5.x (``LlamaDecoderLayer`` unpacks two values) and the reference's
-  3-tuple on 4.x.
+  3-tuple on 4.x;
+* on transformers 5.x the patched model's own cache is a
+  ``CAREKVHFCache``: an HF ``Cache`` whose layers hold only the token count
+  HF reads (the rows live in the CARE-KV arena it exposes as
+  ``care_cache``), instead of the reference's DynamicCache of fp16 zeros
+  (llama_patch.py:262-285, a second KV cache's worth of memory).  A cache
+  the caller passes in is kept and fed one-wide placeholders.
 """
 from __future__ import annotations
 
@@ -31,6 +37,79 @@ try:
     _HF_MAJOR = int(transformers.__version__.split(".")[0])
 except Exception:  # pragma: no cover
     _HF_MAJOR = 5
+
+
+if _HF_MAJOR >= 5:
+    from transformers.cache_utils import Cache, CacheLayerMixin, DynamicCache
+
+    class _CareLengthLayer(CacheLayerMixin):
+        """One layer of ``CAREKVHFCache``: the number of tokens the layer's
+        CARE-KV pages hold, which is all HF reads from a cache layer
+        (sequence length, mask sizes)."""
+
+        is_sliding = False
+        is_compileable = False
+
+        def __init__(self):
+            super().__init__()
+            self.length = 0
+
+        def lazy_initialization(self, key_states, value_states):
+            self.dtype, self.device = key_states.dtype, key_states.device
+            self.is_initialized = True
+
+        def update(self, key_states, value_states, *args, **kwargs):
+            """Counts the rows; the states themselves go to the CARE-KV pages."""
+            if not self.is_initialized:
+                self.lazy_initialization(key_states, value_states)
+            self.length += key_states.shape[-2]
+            return key_states, value_states
+
+        def get_mask_sizes(self, query_length: int):
+            return self.length + query_length, 0
+
+        def get_seq_length(self) -> int:
+            return self.length
+
+        def get_max_length(self) -> int:
+            return -1
+
+        def reset(self):
+            self.length = 0
+
+        def offload(self):
+            pass
+
+        def prefetch(self):
+            pass
+
+        def _unsupported(self, *args, **kwargs):
+            raise NotImplementedError("CAREKVHFCache does not crop, reorder or repeat rows (no beam search, "
+                                      "no assisted decoding): the pages are append-only")
+
+        crop = reorder_cache = batch_repeat_interleave = batch_select_indices = _unsupported
+
+    class CAREKVHFCache(Cache):
+        """The HF ``Cache`` of a patched model: per-layer token counts over
+        the CARE-KV cache the patched attention modules share (no fp16 K/V
+        copy, llama_patch.py:262-285).  ``care_cache`` is that
+        ``CAREKVCache``."""
+
+        def __init__(self, shared: Optional["_SharedState"] = None):
+            super().__init__(layer_class_to_replicate=_CareLengthLayer)
+            self._shared = shared
+
+        @property
+        def care_cache(self):
+            return None if self._shared is None else self._shared.cache
+
+        def advance(self, layer_idx: int, n_tokens: int):
+            """Record n_tokens new rows of layer ``layer_idx``."""
+            while len(self.layers) <= layer_idx:
+                self.layers.append(_CareLengthLayer())
+            self.layers[layer_idx].length += int(n_tokens)
+else:  # pragma: no cover - transformers 4.x keeps the one-wide placeholders
+    CAREKVHFCache = None
 
 
 class _SharedState:
@@ -135,11 +214,13 @@ class CAREKVLlamaAttention(nn.Module):
 
         # keep HF's own cache length in step so that it sends one token per
         # decode call (llama_patch.py:262-285).  The reference appends fp16
-        # zeros of the full K/V shape (a second KV cache's worth of memory);
-        # here the placeholders have head_dim 1: the length HF reads
-        # (shape[-2], of a non-empty tensor) advances at 1/head_dim of the
-        # memory.
-        if use_cache and pkv is not None and hasattr(pkv, "update"):
+        # zeros of the full K/V shape (a second KV cache's worth of memory).
+        # A CAREKVHFCache just counts the rows; a cache the caller passed
+        # gets placeholders of head_dim 1: the length HF reads (shape[-2],
+        # of a non-empty tensor) advances at 1/head_dim of the memory.
+        if use_cache and CAREKVHFCache is not None and isinstance(pkv, CAREKVHFCache):
+            pkv.advance(self.layer_id, T)
+        elif use_cache and pkv is not None and hasattr(pkv, "update"):
             try:
                 z = hidden_states.new_zeros((B, self.cfg.num_kv_heads, T, 1))
                 pkv.update(z, z, self.layer_id)
@@ -171,8 +252,38 @@ def patch_llama_model(model: nn.Module, care_cfg: CacheConfig, device: Optional[
             parent = getattr(parent, part)
         layer_id = next((int(p) for p in parts if p.isdigit()), 0)
         setattr(parent, parts[-1], CAREKVLlamaAttention(module, care_cfg, layer_id, device, shared=shared))
+    if CAREKVHFCache is not None and targets:
+        _install_hf_cache(model, shared)
     print(f"[CARE-KV] Replaced {len(targets)} attention layers with CARE-KV.")
     return model
+
+
+def _install_hf_cache(model: nn.Module, shared: _SharedState):
+    """Make ``CAREKVHFCache`` the cache the patched model makes for itself:
+    ``generate``'s default DynamicCache (``_prepare_cache_for_generation``)
+    and the one the decoder stack creates when called with use_cache and no
+    cache.  Caches the caller passes in are left alone."""
+    prep = getattr(model, "_prepare_cache_for_generation", None)
+    if prep is not None:
+        def prepare(*args, **kwargs):
+            model_kwargs = kwargs["model_kwargs"] if "model_kwargs" in kwargs else args[1]
+            given = model_kwargs.get("past_key_values")
+            out = prep(*args, **kwargs)
+            made = model_kwargs.get("past_key_values")
+            if given is None and type(made) is DynamicCache:
+                model_kwargs["past_key_values"] = CAREKVHFCache(shared)
+            return out
+        model._prepare_cache_for_generation = prepare
+    decoder = getattr(model, "model", None)
+    if isinstance(decoder, nn.Module) and hasattr(decoder, "layers"):
+        cfg_use_cache = bool(getattr(getattr(decoder, "config", None), "use_cache", False))
+
+        def pre_hook(module, args, kwargs):
+            use = kwargs.get("use_cache")
+            if kwargs.get("past_key_values") is None and (use if use is not None else cfg_use_cache):
+                kwargs["past_key_values"] = CAREKVHFCache(shared)
+            return args, kwargs
+        decoder.register_forward_pre_hook(pre_hook, with_kwargs=True)
 
 
 def reset_all_caches(model: nn.Module):

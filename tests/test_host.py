@@ -203,25 +203,80 @@ def test_prefill_correct_rejects_bad_rows():
     assert ws() == -1                              # the pass is the correction
 
 
-def test_padded_masks_refused_in_any_sequence():
-    """CAREKVLayer._check_mask: a left-padded sequence anywhere in the batch
-    is refused (boolean (B, 1, T, S) masks as HF's sdpa path builds them and
-    additive float masks), a causal-only mask passes."""
+def test_padding_mask_runs():
+    """CAREKVLayer._key_runs: causal-only masks (boolean, additive, (T, T))
+    need no split; a left- or right-padded sequence anywhere in the batch
+    gets its run of real rows from the keys its last row sees (boolean
+    (B, 1, T, S) masks as HF's sdpa path builds them, additive masks with
+    -inf or the dtype's lowest value, (B, S) keep-masks); holes and score
+    biases are refused."""
     import torch
     _ensure_built()
     from care_kv.layer import CAREKVLayer
+    runs = CAREKVLayer._key_runs
     B, T = 3, 6
     causal = torch.tril(torch.ones(T, T, dtype=torch.bool))[None, None].expand(B, 1, T, T).clone()
-    CAREKVLayer._check_mask(causal, T)
+    assert runs(causal, B, T) is None
+    assert runs(torch.tril(torch.ones(T, T, dtype=torch.bool)), B, T) is None
     padded = causal.clone()
-    padded[0, :, :, :2] = False  # sequence 0 left-padded by two tokens
+    padded[0, :, :, :2] = False                    # sequence 0 left-padded by two tokens
+    padded[2, :, :, 4:] = False                    # sequence 2 right-padded by two
+    assert runs(padded, B, T) == [(2, 6), (0, 6), (0, 4)]
+    add = torch.zeros(B, 1, T, T, dtype=torch.float16)
+    add.masked_fill_(~causal, torch.finfo(torch.float16).min)
+    assert runs(add, B, T) is None
+    add[1, :, :, 0] = float("-inf")                # only sequence 1 padded
+    assert runs(add, B, T) == [(0, 6), (1, 6), (0, 6)]
+    add[1, :, :, :] = float("-inf")                # an all-pad sequence: an empty run
+    assert runs(add, B, T) == [(0, 6), (0, 0), (0, 6)]
+    keep = torch.tensor([[1, 1, 1, 1], [0, 1, 1, 1]])
+    assert runs(keep, 2, 3) is None                # the last 3 of 4 keys are real
+    assert runs(keep, 2, 4) == [(0, 4), (1, 4)]
+    holed = causal.clone()
+    holed[1, :, :, 3] = False
     with pytest.raises(NotImplementedError):
-        CAREKVLayer._check_mask(padded, T)
-    add = torch.zeros(B, 1, T, T)
-    add.masked_fill_(~causal, float("-inf"))
-    CAREKVLayer._check_mask(add, T)
-    add[1, :, :, 0] = float("-inf")  # only sequence 1 padded
+        runs(holed, B, T)
+    bias = torch.zeros(B, 1, T, T)
+    bias[0, :, :, 1] = -0.5                        # a score bias, not a mask
     with pytest.raises(NotImplementedError):
-        CAREKVLayer._check_mask(add, T)
-    with pytest.raises(NotImplementedError):  # a (B, S) keep-mask with a zero
-        CAREKVLayer._check_mask(torch.tensor([[1, 1, 1], [0, 1, 1]], dtype=torch.bool), 3)
+        runs(bias, B, T)
+    with pytest.raises(NotImplementedError):
+        runs(torch.zeros(B, 1, T - 1, T - 1, dtype=torch.bool), B, T)
+
+
+def test_patched_model_makes_a_carekv_hf_cache(monkeypatch):
+    """patch_llama_model on transformers 5.x: generate's default cache and the
+    decoder's own cache (use_cache, no cache given) are CAREKVHFCache, whose
+    layers count the rows HF reads; a cache the caller passes is kept.  Run
+    on the CPU with CAREKV_RETURN=original (HF's attention behind the patch),
+    which exercises the cache plumbing without the HIP library."""
+    import torch
+    import care_kv
+    transformers = pytest.importorskip("transformers")
+    if int(transformers.__version__.split(".")[0]) < 5:
+        pytest.skip("CAREKVHFCache is built for transformers 5.x")
+    from transformers import DynamicCache, LlamaConfig, LlamaForCausalLM
+    monkeypatch.setenv("CAREKV_RETURN", "original")
+    torch.manual_seed(0)
+    c = LlamaConfig(hidden_size=64, intermediate_size=128, num_hidden_layers=2, num_attention_heads=4,
+                    num_key_value_heads=2, vocab_size=100, max_position_embeddings=128)
+    model = LlamaForCausalLM(c).eval()
+    cfg = care_kv.CacheConfig(num_layers=2, num_heads=4, num_kv_heads=2, head_dim=16, max_pages=8)
+    care_kv.patch_llama_model(model, cfg)
+    ids = torch.randint(0, 100, (2, 9))
+    with torch.no_grad():
+        out = model.generate(ids, max_new_tokens=4, do_sample=False, return_dict_in_generate=True,
+                             pad_token_id=0)
+        pkv = out.past_key_values
+        assert isinstance(pkv, care_kv.CAREKVHFCache)
+        assert [pkv.get_seq_length(i) for i in range(2)] == [12, 12]   # 9 prompt rows + 3 fed back
+        assert pkv.get_mask_sizes(1, 0) == (13, 0)
+        mine = DynamicCache()
+        out = model.generate(ids, max_new_tokens=2, do_sample=False, return_dict_in_generate=True,
+                             pad_token_id=0, past_key_values=mine)
+        assert out.past_key_values is mine
+        r = model(ids, use_cache=True)
+        assert isinstance(r.past_key_values, care_kv.CAREKVHFCache) and r.past_key_values.get_seq_length() == 9
+        assert model(ids, use_cache=False).past_key_values is None
+    with pytest.raises(NotImplementedError):
+        pkv.crop(-1)
