@@ -43,6 +43,12 @@ CONFIGS = {
     # per-token V), kept as the reference keeps it, fp16 K_hat / V_hat pages
     "c3kivi": dict(B=64, Hq=32, Hkv=8, D=128, N=32768, rk=128, rv=128, dist="outlier10", seed=3, kivi=2,
                    workload="config3 Mistral-7B GQA decode B=64 32q/8kv D=128 N=32768, KIVI-style INT2 base"),
+    # the same KIVI-style INT2 base stored packed (CacheConfig.kivi_packed):
+    # 2-bit prompt pages, per-channel K scales, per-token V scales; the same
+    # K_hat / V_hat values as the side buffer
+    "c3kivip": dict(B=64, Hq=32, Hkv=8, D=128, N=32768, rk=128, rv=128, dist="outlier10", seed=3, kivi=2,
+                    packed=True, workload="config3 Mistral-7B GQA decode B=64 32q/8kv D=128 N=32768, "
+                                          "KIVI-style INT2 base, packed pages"),
 }
 
 
@@ -91,7 +97,9 @@ def algorithmic_bytes(spec, cfg, cache, diag_np):
     bits, G, P = cfg.base_bits, D // 32, math.ceil(N / 16)
     grp = Hq // Hkv
     k_slots = (cache.k_slot[0, :, :B, :P] >= 0).sum().item()          # stored K slots (all b, kvh)
-    if spec.get("kivi"):  # fp16 K_hat / V_hat rows, no scales
+    if spec.get("packed"):  # 2-bit K and V codes, fp16 V scales per (row, group), fp16 K channel scales
+        base = 2 * N * D * 2 / 8 + N * G * 2 + D * 2
+    elif spec.get("kivi"):  # fp16 K_hat / V_hat rows, no scales
         base = 2 * N * D * 2
     else:                 # K + V codes, int8 scales, fp16 masters
         base = 2 * N * D * bits / 8 + 2 * N * G + 2 * P * 2
@@ -579,6 +587,8 @@ def main():
     P = math.ceil(N / 16)
     kivi = spec.get("kivi")
     base_kw = dict(base_bits=kivi, base_quantizer="kivi_style") if kivi else dict(base_bits=3)
+    if spec.get("packed"):
+        base_kw.update(kivi_packed=True, kivi_tail_pages=4)
     cfg = care_kv.CacheConfig(num_layers=1, num_heads=Hq, num_kv_heads=Hkv, head_dim=D, page_size=16,
                               max_pages=P + 4, group_size=32, k_channel_group=32, v_token_block=4,
                               sketch_dim=32, packed_base=True, scale_quant="int8", store_budget_mode="ratio",
@@ -662,19 +672,22 @@ def main():
     # the library runs the 4-query-head streaming kernel when a kv head has at
     # most 4 query heads and the split is a multiple of 16 pages
     sp = args.split_pages or care_kv.attention.default_split_pages(P, B * Hkv)
-    stream_kernel = ("decode_stream4_kernel" if Hq // Hkv <= 4 and sp % 16 == 0 and not kivi
+    packed = bool(spec.get("packed"))
+    stream_kernel = ("decode_stream4_kernel" if Hq // Hkv <= 4 and sp % 16 == 0 and (packed or not kivi)
                      else "decode_stream_kernel")
-    kbits, ksm = (16, 0) if kivi else (cfg.base_bits, 1)
+    kbits, ksm = (2, 0) if packed else ((16, 0) if kivi else (cfg.base_bits, 1))
     tr = load_traffic(stream_kernel, args.config + ("_base" if args.no_correction else ""))
     traffic = None if tr is None else tr.get("hbm_bytes_per_launch")
     line = {
         "metric": "CARE-KV decode-attn us/step + HBM GB/s (% roofline), Mistral-7B shape 32K ctx",
         "value": round(us_step, 2), "unit": "us/step", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
-        "dtype": ("fp16 K_hat/V_hat side buffer (KIVI INT2 values)" if kivi else "int3-packed KV") +
+        "dtype": ("int2-packed KIVI KV (per-channel K, per-token V scales)" if packed else
+                  "fp16 K_hat/V_hat side buffer (KIVI INT2 values)" if kivi else "int3-packed KV") +
                  ", fp16 q/out, fp32 softmax", "data": "synthetic",
         "config": {"workload": spec["workload"], "global_batch": B, "seq_len": N, "parallelism": "single-gpu",
-                   "base": (f"KIVI-style INT{kivi} (per-channel K, per-token V), fp16 side buffer" if kivi
+                   "base": (f"KIVI-style INT{kivi} (per-channel K, per-token V), packed pages" if packed else
+                            f"KIVI-style INT{kivi} (per-channel K, per-token V), fp16 side buffer" if kivi
                             else "uniform INT3 g=32, int8 page scales"),
                    "store": "ratio 0.03 (1K+1V slot/page)",
                    "read": f"joint top-{spec['rk'] + spec['rv']} (K {spec['rk']} + V {spec['rv']}), "

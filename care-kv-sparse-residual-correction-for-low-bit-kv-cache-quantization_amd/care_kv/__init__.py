@@ -11,7 +11,7 @@ this build: the batched entry points ``decode_attention`` /
 """
 from .config import (CacheConfig, apply_carekv_env_overrides, layer_budget_multiplier,
                      resolve_read_knobs, resolve_store_knobs)
-from .cache import CAREKVCache, PageMeta, get_sketch_proj, kivi_qdq, packed_row_bytes
+from .cache import CAREKVCache, PageMeta, get_sketch_proj, kivi_codes, kivi_qdq, packed_row_bytes
 from .quantizer import (QuantConfig, KQuantizer, VQuantizer, quantize, dequantize, quantize_and_residual,
                         pack_int2, unpack_int2, pack_int3, unpack_int3, pack_int4, unpack_int4,
                         pack_int2_2d, unpack_int2_2d, pack_int3_2d, unpack_int3_2d, pack_int4_2d, unpack_int4_2d,
@@ -42,7 +42,7 @@ __all__ = [
     "CAREKVLayer", "get_debug_stats", "reset_debug_stats",
     "CAREKVLlamaAttention", "patch_llama_model", "reset_all_caches",
     # additions of this build
-    "resolve_read_knobs", "resolve_store_knobs", "get_sketch_proj", "kivi_qdq",
+    "resolve_read_knobs", "resolve_store_knobs", "get_sketch_proj", "kivi_qdq", "kivi_codes",
     "decode_attention", "prefill_correction", "prefill_attention", "quantize_rows", "dequantize_rows",
     "quant_dequant", "CAREKVAdapter", "CarekvError", "CAREKVHFCache",
 ]

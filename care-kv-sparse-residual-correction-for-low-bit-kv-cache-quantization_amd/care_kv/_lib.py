@@ -28,7 +28,10 @@ class Arena(C.Structure):
             "n_seq", "n_kv_heads", "max_pages", "head_dim", "base_bits", "page_size", "group_size",
             "k_channel_group", "v_token_block", "sketch_dim", "scale_mode", "residual_bits", "n_slots",
             "hat_bits_k", "hat_bits_v")] + \
-        [("open_kscale", C.c_void_p), ("open_vscale", C.c_void_p), ("rescale_open", C.c_int32)]
+        [("open_kscale", C.c_void_p), ("open_vscale", C.c_void_p), ("rescale_open", C.c_int32)] + \
+        [("kivi_packed", C.c_int32), ("kchan", C.c_void_p), ("n_packed", C.c_void_p), ("tail_k", C.c_void_p),
+         ("tail_v", C.c_void_p), ("tail_pages", C.c_int32), ("code_pages", C.c_int32),
+         ("code_page_off", C.c_void_p)]
 
 
 class StoreParams(C.Structure):
@@ -49,7 +52,7 @@ class DecodeParams(C.Structure):
                 ("split_pages", C.c_int32), ("phase_events", C.c_void_p), ("k_proxy", C.c_int32),
                 ("sketch_proj", C.c_void_p), ("route_policy", C.c_int32), ("adaptive_score", C.c_int32),
                 ("rel_threshold", C.c_double), ("abs_threshold", C.c_double), ("min_keep", C.c_int32),
-                ("read_counts", C.c_void_p)]
+                ("read_counts", C.c_void_p), ("packed_pages_used", C.c_int32), ("tail_pages_used", C.c_int32)]
 
 
 class PrefillParams(C.Structure):
@@ -70,7 +73,8 @@ EXPORTS = ["carekv_store_pages", "carekv_store_workspace_bytes", "carekv_append_
            "carekv_dequantize_rows", "carekv_kivi_qdq", "carekv_prefill_correct",
            "carekv_prefill_correct_workspace_bytes", "carekv_decode_attn_static", "carekv_write_base", "carekv_append_coded_rows",
            "carekv_pack_codes", "carekv_unpack_codes", "carekv_pack_4bit", "carekv_unpack_4bit",
-           "carekv_quantize_rows_f32", "carekv_dequantize_rows_f32", "carekv_last_error"]
+           "carekv_quantize_rows_f32", "carekv_dequantize_rows_f32", "carekv_kivi_codes", "carekv_read_hat_pages",
+           "carekv_last_error"]
 
 # bytes of the per-GPU static workspace of carekv_decode_attn_static
 # (CAREKV_STATIC_SCRATCH_BYTES in include/carekv.h)
@@ -137,6 +141,10 @@ def load(path: str | None = None):
         lib.carekv_dequantize_rows_f32.argtypes = [vp, vp, i64, i32, i32, vp, vp]
         lib.carekv_kivi_qdq.restype = C.c_int
         lib.carekv_kivi_qdq.argtypes = [vp, i32, i32, i32, i32, i32, vp, vp]
+        lib.carekv_kivi_codes.restype = C.c_int
+        lib.carekv_kivi_codes.argtypes = [vp, i32, i32, i32, i32, i32, vp, vp, vp]
+        lib.carekv_read_hat_pages.restype = C.c_int
+        lib.carekv_read_hat_pages.argtypes = [C.POINTER(Arena), i32, i32, i32, vp, vp, vp, vp, vp]
         _lib = lib
         return lib
 

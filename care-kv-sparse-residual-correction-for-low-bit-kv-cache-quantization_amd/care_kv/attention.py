@@ -230,6 +230,9 @@ def decode_attention(cache: CAREKVCache, layer: int, q: torch.Tensor, seqs: Opti
         split_pages = default_split_pages(max_np, B * cfg.num_kv_heads)
     dp = _read_params(cache, layer, knobs, batch=B, n_heads=Hq, correction=correction, split_pages=split_pages,
                       max_pages=max_np, seq_ptr=meta[0].data_ptr(), np_ptr=meta[1].data_ptr())
+    if cache.kivi_packed and B:  # the packed prefix and the fp16 tail run as separate page ranges
+        pp = np.minimum(npages, cache.n_packed[seqs])
+        dp.packed_pages_used, dp.tail_pages_used = int(pp.max()), int((npages - pp).max())
     if correction and not knobs.kscore_live:
         P = get_sketch_proj(cfg.head_dim, cfg.k_channel_group, cfg.sketch_dim, dev)
         dp.k_proxy = 1

@@ -129,6 +129,23 @@ def kivi_qdq(x: torch.Tensor, bits: int, per_channel: bool) -> torch.Tensor:
     return out
 
 
+def kivi_codes(x: torch.Tensor, bits: int, per_channel: bool) -> Tuple[torch.Tensor, torch.Tensor]:
+    """The codes and scales behind ``kivi_qdq`` (carekv_kivi_codes; no
+    reference counterpart): x fp16 (..., T, D) -> int8 codes (..., T, D) and
+    fp16 scales (..., D) per channel or (..., T) per token, NaN where the
+    max |x| is 0, so that half(code * scale) is kivi_qdq's output."""
+    _lib.ptr(x)
+    x = x.to(F16).contiguous()
+    T, D = x.shape[-2], x.shape[-1]
+    n_mat = x.numel() // max(T * D, 1)
+    codes = torch.empty(x.shape, dtype=torch.int8, device=x.device)
+    scale = torch.empty(x.shape[:-2] + ((D,) if per_channel else (T,)), dtype=F16, device=x.device)
+    lib = _lib.load()
+    _lib.check(lib.carekv_kivi_codes(x.data_ptr(), n_mat, T, D, int(bits), int(per_channel), codes.data_ptr(),
+                                     scale.data_ptr(), _lib.stream_ptr(x.device)), "carekv_kivi_codes")
+    return codes, scale
+
+
 class CAREKVCache:
     """Device-resident paged cache for ``n_seq`` sequences of one model."""
 
@@ -157,14 +174,29 @@ class CAREKVCache:
         G = D // cfg.group_size
         self.ncg = D // cfg.k_channel_group
         self.nvb = math.ceil(T / cfg.v_token_block)
-        self.hat = cfg.base_quantizer in HAT_QUANTIZERS  # fp16 K_hat / V_hat pages
-        self._arena_bits = 16 if self.hat else cfg.base_bits
-        self._packed_row_bytes = 2 * D if self.hat else packed_row_bytes(D, cfg.base_bits)
+        self.hat = cfg.base_quantizer in HAT_QUANTIZERS  # K_hat / V_hat of the KIVI-style quant-dequant
+        # the packed KIVI base (no reference counterpart): 2-bit prompt pages,
+        # fp16 K_hat / V_hat only for the later rows
+        self.kivi_packed = self.hat and bool(getattr(cfg, "kivi_packed", False))
+        if self.kivi_packed and hat_bits(cfg) != (2, 2):
+            raise NotImplementedError(f"kivi_packed is built for the 2-bit KIVI base (got K/V bits {hat_bits(cfg)})")
+        if self.kivi_packed and cfg.num_heads // cfg.num_kv_heads > 4:
+            raise NotImplementedError("kivi_packed decodes with at most 4 query heads per kv head")
+        self._arena_bits = 2 if self.kivi_packed else (16 if self.hat else cfg.base_bits)
+        self._packed_row_bytes = (2 * D if self.hat and not self.kivi_packed
+                                  else packed_row_bytes(D, self._arena_bits))
         dev = self.device
         shp = (L, H, n_seq, P)
         self.kcodes = torch.zeros(*shp, T, self._packed_row_bytes, dtype=torch.int8, device=dev)
         self.vcodes = torch.zeros_like(self.kcodes)
-        self.scale_mode = 1 if cfg.scale_quant == "int8" else 0
+        self.scale_mode = 1 if cfg.scale_quant == "int8" and not self.kivi_packed else 0
+        if self.kivi_packed:
+            self.tail_pages = int(cfg.kivi_tail_pages) if cfg.kivi_tail_pages > 0 else P
+            self.kchan = torch.zeros(L, H, n_seq, D, dtype=F16, device=dev)  # per-channel K scales of the prompt
+            self.tail_k = torch.zeros(L, H, n_seq, self.tail_pages, T, D, dtype=F16, device=dev)
+            self.tail_v = torch.zeros_like(self.tail_k)
+            self.n_packed = np.zeros(n_seq, dtype=np.int32)  # packed prompt pages per sequence
+            self.n_packed_d = torch.zeros(n_seq, dtype=torch.int32, device=dev)
         sdt = torch.int8 if self.scale_mode else F16
         self.kscale = torch.zeros(*shp, T, G, dtype=sdt, device=dev)
         self.vscale = torch.zeros_like(self.kscale)
@@ -232,6 +264,10 @@ class CAREKVCache:
                 hat_bits_k=hat_bits(cfg)[0], hat_bits_v=hat_bits(cfg)[1],
                 open_kscale=g(self.open_ks) if self.rescale_open else None,
                 open_vscale=g(self.open_vs) if self.rescale_open else None, rescale_open=int(self.rescale_open))
+            if self.kivi_packed:
+                a.kivi_packed = 1
+                a.kchan, a.n_packed = g(self.kchan), self.n_packed_d.data_ptr()
+                a.tail_k, a.tail_v, a.tail_pages = g(self.tail_k), g(self.tail_v), self.tail_pages
             self._arenas[layer] = a
         return a
 
@@ -282,6 +318,9 @@ class CAREKVCache:
         self.next_page[:, :, seq] = 0
         self.valid_host[:, :, seq] = 0
         self._token_start[:, :, seq] = 0
+        if self.kivi_packed:
+            self.n_packed[seq] = 0
+            self.n_packed_d[seq] = 0
 
     # ------------------------------------------------------------ page writes
     def write_prefill(self, layer: int, K: torch.Tensor, V: torch.Tensor, token_start_abs: int = 0,
@@ -320,6 +359,29 @@ class CAREKVCache:
         if hats is not None:
             Khp = pads(hats[0]).contiguous().view(B * H * n_new * ps, D)
             Vhp = pads(hats[1]).contiguous().view(B * H * n_new * ps, D)
+        kivi_in = None
+        if self.kivi_packed:
+            # the full pages of a prompt into empty sequences go packed, the
+            # rest (a partial last page, a continuation) to the fp16 tail
+            fresh = all(int(self.next_page[layer, h, s_]) == 0 for s_ in seqs for h in range(H))
+            n_full = T // ps if fresh else 0
+            sl = torch.tensor(seqs, device=self.device)
+            if fresh:
+                self.n_packed[seqs] = n_full
+                self.n_packed_d[sl] = n_full
+            for s_ in seqs:
+                top = int(self.next_page[layer, 0, s_]) + n_new - int(self.n_packed[s_])
+                if top > self.tail_pages:
+                    raise _lib.CarekvError(f"packed KIVI tail full: sequence {s_} needs {top} fp16 tail pages, "
+                                           f"the cache holds {self.tail_pages} (kivi_tail_pages)")
+            kc, ks = kivi_codes(K.to(F16), 2, per_channel=True)    # (B, H, T, D), (B, H, D)
+            vc, vs = kivi_codes(V.to(F16), 2, per_channel=False)   # (B, H, T, D), (B, H, T)
+            if fresh:
+                self.kchan[layer][:, sl] = ks.transpose(0, 1)
+            G = D // cfg.group_size
+            padc = lambda x: torch.nn.functional.pad(x, (0, 0, 0, pad)) if pad else x  # noqa: E731
+            kivi_in = (padc(kc).contiguous().view(-1, D), padc(vc).contiguous().view(-1, D),
+                       padc(vs.unsqueeze(-1).expand(B, H, T, G)).contiguous().view(-1, G))
         jobs = np.zeros((B * H * n_new, _lib.PAGE_JOB_INTS), dtype=np.int32)
         group_ptr = np.zeros(B + 1, dtype=np.int32)
         j = 0
@@ -342,6 +404,8 @@ class CAREKVCache:
                               sketch_proj=self.sketch_proj.data_ptr(),
                               k_hat=Khp.data_ptr() if Khp is not None else None,
                               v_hat=Vhp.data_ptr() if Vhp is not None else None)
+        if kivi_in is not None:
+            sp.k_codes_in, sp.v_codes_in, sp.v_scale_in = (t.data_ptr() for t in kivi_in)
         lib = _lib.load()
         ws = self.workspace("store", int(lib.carekv_store_workspace_bytes(len(jobs))))
         a = self.arena(layer)
@@ -393,6 +457,9 @@ class CAREKVCache:
                 pid = self.get_open_page(layer, h, s)
                 fresh = 0
                 if pid is None:
+                    if self.kivi_packed and int(self.next_page[layer, h, s]) - int(self.n_packed[s]) >= self.tail_pages:
+                        raise _lib.CarekvError(f"packed KIVI tail full: sequence {s} has no fp16 tail page left "
+                                               f"({self.tail_pages} per sequence, kivi_tail_pages)")
                     pid = self.alloc_page(layer, h, s)
                     fresh = 1
                     self._token_start[layer, h, s, pid] = self.total_valid_tokens(layer, h, s)
@@ -439,10 +506,20 @@ class CAREKVCache:
                               joint=int(knobs.joint), store_none=int(knobs.store_none),
                               sensitivity=knobs.sensitivity, sink_tokens=4,
                               sketch_proj=self.sketch_proj.data_ptr(), keep_base=0 if self.hat else 1)
+        keep = []
         if self.hat:  # the fp16 base: the pages' own K_hat / V_hat rows as the residual base
             pi = torch.tensor([f[2] for f in filled], device=self.device)
-            Khat = self.kcodes[layer, hi, si, pi].view(F16).contiguous().view(-1, cfg.head_dim)
-            Vhat = self.vcodes[layer, hi, si, pi].view(F16).contiguous().view(-1, cfg.head_dim)
+            if self.kivi_packed:  # filled pages are tail pages
+                ti = pi - torch.from_numpy(self.n_packed).to(self.device).long()[si]
+                Khat = self.tail_k[layer, hi, si, ti].contiguous().view(-1, cfg.head_dim)
+                Vhat = self.tail_v[layer, hi, si, ti].contiguous().view(-1, cfg.head_dim)
+                zc = torch.zeros(Khat.shape, dtype=torch.int8, device=self.device)
+                zs = torch.zeros(Khat.shape[0], cfg.head_dim // cfg.group_size, dtype=F16, device=self.device)
+                keep += [zc, zs]
+                sp.k_codes_in, sp.v_codes_in, sp.v_scale_in = zc.data_ptr(), zc.data_ptr(), zs.data_ptr()
+            else:
+                Khat = self.kcodes[layer, hi, si, pi].view(F16).contiguous().view(-1, cfg.head_dim)
+                Vhat = self.vcodes[layer, hi, si, pi].view(F16).contiguous().view(-1, cfg.head_dim)
             sp.k_hat, sp.v_hat = Khat.data_ptr(), Vhat.data_ptr()
         lib = _lib.load()
         ws = self.workspace("store", int(lib.carekv_store_workspace_bytes(len(jobs))))
@@ -466,6 +543,18 @@ class CAREKVCache:
         pids = list(range(n)) if page_ids is None else list(page_ids)
         lens = [int(self.valid_host[layer, kv_head, seq, p]) for p in pids]
         D = self.cfg.head_dim
+        if self.kivi_packed:  # packed prompt pages dequantised, tail pages copied (carekv_read_hat_pages)
+            N = sum(lens)
+            kh = torch.zeros(N, D, dtype=F16, device=self.device)
+            vh = torch.zeros_like(kh)
+            if N:
+                rs = torch.from_numpy(np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.int32)).to(self.device)
+                pl = torch.tensor(pids, dtype=torch.int32, device=self.device)
+                lib = _lib.load()
+                _lib.check(lib.carekv_read_hat_pages(self.arena(layer), seq, kv_head, len(pids), pl.data_ptr(),
+                                                     rs.data_ptr(), kh.data_ptr(), vh.data_ptr(),
+                                                     _lib.stream_ptr(self.device)), "carekv_read_hat_pages")
+            return kh, vh, lens
         kh = self.kcodes[layer, kv_head, seq].view(F16).view(self.cfg.max_pages, self.cfg.page_size, D)
         vh = self.vcodes[layer, kv_head, seq].view(F16).view(self.cfg.max_pages, self.cfg.page_size, D)
         ks = [kh[p, :n_] for p, n_ in zip(pids, lens) if n_]
@@ -602,8 +691,9 @@ class CAREKVCache:
         assert self.hat, "write_base_kivi requires a side-buffer base quantizer"
         assert 0 <= num_valid <= self.cfg.page_size, num_valid
         T = K_hat.shape[0]
-        self.kcodes[layer, kv_head, seq, page_id].view(F16)[:T] = K_hat.to(F16)
-        self.vcodes[layer, kv_head, seq, page_id].view(F16)[:T] = V_hat.to(F16)
+        kp, vp = self._hat_page(layer, kv_head, page_id, seq)
+        kp[:T] = K_hat.to(F16)
+        vp[:T] = V_hat.to(F16)
         self.valid[layer, kv_head, seq, page_id] = num_valid
         self.valid_host[layer, kv_head, seq, page_id] = num_valid
 
@@ -613,11 +703,23 @@ class CAREKVCache:
         assert self.hat, "append_to_page_kivi requires a side-buffer base quantizer"
         off = int(self.valid_host[layer, kv_head, seq, page_id])
         assert off < self.cfg.page_size, "page already full"
-        self.kcodes[layer, kv_head, seq, page_id].view(F16)[off] = K_hat_row.to(F16)
-        self.vcodes[layer, kv_head, seq, page_id].view(F16)[off] = V_hat_row.to(F16)
+        kp, vp = self._hat_page(layer, kv_head, page_id, seq)
+        kp[off] = K_hat_row.to(F16)
+        vp[off] = V_hat_row.to(F16)
         self.valid[layer, kv_head, seq, page_id] = off + 1
         self.valid_host[layer, kv_head, seq, page_id] = off + 1
         return off
+
+    def _hat_page(self, layer: int, kv_head: int, page_id: int, seq: int):
+        """(K_hat, V_hat) fp16 (page_size, D) views of a side-buffer page; on
+        a packed KIVI cache only the fp16 tail pages have them."""
+        if self.kivi_packed:
+            tp = page_id - int(self.n_packed[seq])
+            if not 0 <= tp < self.tail_pages:
+                raise _lib.CarekvError(f"page {page_id} of a packed KIVI cache is not an fp16 tail page "
+                                       f"(packed pages: {int(self.n_packed[seq])}, tail pages: {self.tail_pages})")
+            return self.tail_k[layer, kv_head, seq, tp], self.tail_v[layer, kv_head, seq, tp]
+        return (self.kcodes[layer, kv_head, seq, page_id].view(F16), self.vcodes[layer, kv_head, seq, page_id].view(F16))
 
     def write_k_residual(self, slot: int, packed: torch.Tensor, scale: torch.Tensor, seq: int = 0):
         """cache.py:871-873."""
@@ -662,8 +764,10 @@ class CAREKVCache:
     def _view(self, t):
         return t[:, :, 0] if self.n_seq == 1 else t
 
-    base_K_hat_fp16 = property(lambda self: self._view(self.kcodes).view(F16) if self.hat else None)
-    base_V_hat_fp16 = property(lambda self: self._view(self.vcodes).view(F16) if self.hat else None)
+    base_K_hat_fp16 = property(lambda self: self._view(self.kcodes).view(F16)
+                               if self.hat and not self.kivi_packed else None)
+    base_V_hat_fp16 = property(lambda self: self._view(self.vcodes).view(F16)
+                               if self.hat and not self.kivi_packed else None)
     base_K_codes = property(lambda self: self._view(self.kcodes))
     base_V_codes = property(lambda self: self._view(self.vcodes))
     base_K_scale = property(lambda self: self._view(self.kscale))

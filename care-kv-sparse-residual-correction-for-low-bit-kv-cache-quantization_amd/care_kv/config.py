@@ -53,6 +53,9 @@ def apply_carekv_env_overrides(kwargs: dict) -> dict:
     # no reference counterpart: CAREKV_COMPAT=1 reproduces the reference's
     # decode-path defects (CacheConfig.compat)
     _set("CAREKV_COMPAT", "compat", as_bool)
+    # no reference counterpart: the packed KIVI base (CacheConfig.kivi_packed)
+    _set("CAREKV_KIVI_PACKED", "kivi_packed", as_bool)
+    _set("CAREKV_KIVI_TAIL_PAGES", "kivi_tail_pages", int)
     ls = env.get("CAREKV_LAYER_SENSITIVITY", "")
     if ls:
         try:
@@ -123,6 +126,17 @@ class CacheConfig:
     # CAREKV_KSCORE_LIVE=1), open pages are re-encoded as write_base encodes
     # their valid rows, and filled pages are stored from their true rows.
     compat: bool = False
+    # No reference counterpart.  kivi_packed=True stores the kivi_style /
+    # kvquant_style 2-bit base packed instead of as the reference's fp16
+    # side-buffer pages (cache.py:487-499): the prompt's full pages as 2-bit
+    # codes, K against one per-channel scale vector per (layer, kv head,
+    # sequence), V against per-token scales, and only the later rows (the
+    # prompt's partial last page, the decode rows, which the reference keeps
+    # near-lossless) as fp16 K_hat / V_hat, in kivi_tail_pages pages per
+    # (layer, kv head, sequence) (0: max_pages).  K_hat / V_hat, and with
+    # them every output, are the side-buffer base's.
+    kivi_packed: bool = False
+    kivi_tail_pages: int = 0
 
     def __post_init__(self):
         if self.layer_sensitivity is None:

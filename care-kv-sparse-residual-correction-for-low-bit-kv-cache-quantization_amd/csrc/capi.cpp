@@ -57,6 +57,17 @@ bool check_arena(const carekv_arena& A) {
     set_error("scale_mode must be 0 (fp16) or 1 (int8)");
     return false;
   }
+  if (A.code_pages != 0 || A.code_page_off) {
+    set_error("code_pages / code_page_off are set by the library on its own views (callers pass 0)");
+    return false;
+  }
+  if (A.kivi_packed &&
+      (A.base_bits != 2 || A.scale_mode != 0 || A.hat_bits_k != 2 || A.hat_bits_v != 2 || !A.kchan ||
+       !A.n_packed || !A.tail_k || !A.tail_v || A.tail_pages <= 0)) {
+    set_error("a packed KIVI arena needs base_bits 2, scale_mode 0 (fp16), hat_bits_k = hat_bits_v = 2, kchan, "
+              "n_packed, tail_k, tail_v and tail_pages > 0");
+    return false;
+  }
   if (A.sketch_dim <= 0 || A.sketch_dim > 64) {
     set_error("sketch_dim must be in 1..64 (got %d)", A.sketch_dim);
     return false;

@@ -119,6 +119,35 @@ __device__ __forceinline__ void store_bytes(int8_t* p, const uint32_t* w) {
 
 __host__ __device__ constexpr int row_bytes(int D, int bits) { return D * bits / 8; }
 
+// Code-buffer page of the row whose metadata pages start at pg_base
+// (= (kv head * n_seq + seq) * max_pages): pg_base itself, or on a view with
+// a code-page map (carekv_arena::code_pages > 0) the row's code pages moved
+// back by its offset, so that page p of the row is code page
+// code_base + p.
+__device__ __forceinline__ long code_base(const carekv_arena& A, long pg_base) {
+  if (A.code_pages <= 0) return pg_base;
+  const long r = pg_base / A.max_pages;  // kv head * n_seq + seq
+  return r * A.code_pages - A.code_page_off[r % A.n_seq];
+}
+// One past the last page of the row the code-page map holds.
+__device__ __forceinline__ int code_page_limit(const carekv_arena& A, long pg_base) {
+  const long r = pg_base / A.max_pages;
+  return A.code_page_off[r % A.n_seq] + A.code_pages;
+}
+// Whether the code-page map (if any) holds metadata page pg.
+__device__ __forceinline__ bool code_pg_in(const carekv_arena& A, long pg) {
+  if (A.code_pages <= 0) return true;
+  const long r = pg / A.max_pages;
+  const long t = pg - r * A.max_pages - A.code_page_off[r % A.n_seq];
+  return t >= 0 && t < A.code_pages;
+}
+// Code-buffer page of metadata page pg.
+__device__ __forceinline__ long code_pg(const carekv_arena& A, long pg) {
+  if (A.code_pages <= 0) return pg;
+  const long r = pg / A.max_pages;
+  return code_base(A, r * A.max_pages) + (pg - r * A.max_pages);
+}
+
 // Wait for this wave's outstanding LDS operations; also a compiler barrier
 // for memory so LDS writes by other lanes are read after they landed.
 __device__ __forceinline__ void lds_sync_wave() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }

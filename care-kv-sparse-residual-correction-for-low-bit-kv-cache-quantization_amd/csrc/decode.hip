@@ -23,6 +23,12 @@ WsLayout ws_layout(const carekv_arena& A, const carekv_decode_params& dp, int gq
   const int D = A.head_dim;
   const int Pm = dp.max_pages_used > 0 ? dp.max_pages_used : 1;
   L.nsplit = (Pm + dp.split_pages - 1) / dp.split_pages;
+  if (A.kivi_packed && !pf) {  // the packed prefix and the fp16 tail split apart
+    const int pp = dp.packed_pages_used > 0 ? dp.packed_pages_used : 0;
+    const int tp = dp.tail_pages_used > 0 ? dp.tail_pages_used : 0;
+    L.nsplit = (pp + dp.split_pages - 1) / dp.split_pages + (tp + dp.split_pages - 1) / dp.split_pages;
+    if (L.nsplit == 0) L.nsplit = 1;
+  }
   L.F = 2 + 4 * dp.k_cap + dp.v_cap;
   L.ncand = Pm * (dp.k_cap + dp.v_cap);
   auto al = [](long x) { return (x + 255) / 256 * 256; };
@@ -104,6 +110,15 @@ int run_decode(const carekv_arena* arena, const carekv_decode_params* dp, const 
   const bool need_x = dp->correction != 0 && (proxy || dp->route_policy == 3);
   CAREKV_REQUIRE(!proxy || (A.k_sketch && A.k_channel_group == 32 && A.sketch_dim >= 1 && A.sketch_dim <= 64),
                  "the sketch proxy needs k_sketch, k_channel_group 32 and sketch_dim in 1..64");
+  const bool kv = A.kivi_packed != 0 && !pf;
+  if (kv) {
+    CAREKV_REQUIRE(GQ <= 4 && dp->split_pages % 16 == 0,
+                   "a packed KIVI arena decodes with at most 4 query heads per kv head and split_pages a "
+                   "multiple of 16");
+    CAREKV_REQUIRE(dp->packed_pages_used >= 0 && dp->tail_pages_used >= 0 &&
+                       dp->packed_pages_used <= A.max_pages && dp->tail_pages_used <= A.tail_pages,
+                   "packed_pages_used / tail_pages_used out of range");
+  }
   const WsLayout L = ws_layout(A, *dp, GQ, pf != nullptr);
   const long vsq_off = L.total, need = L.total + (pf ? (long)A.n_kv_heads * pf->pages * 4 : 0);
   if (workspace_bytes < need) {
@@ -154,6 +169,13 @@ int run_decode(const carekv_arena* arena, const carekv_decode_params* dp, const 
   a.correction = dp->correction; a.kind = dp->kind; a.joint = dp->joint; a.normalize = dp->normalize;
   a.k_exact = dp->k_exact; a.budget_ratio = dp->budget_ratio; a.abs_k = dp->abs_k; a.abs_v = dp->abs_v;
   a.ratio_k = dp->ratio_k; a.ratio_v = dp->ratio_v;
+  // splits and apply chunks of the packed prefix (range 1) and the fp16
+  // tail (range 2) of a packed KIVI arena; one range (0) otherwise
+  int ns_p = L.nsplit, ns_t = 0, na_p = 0, na_t = 0;
+  if (kv) {
+    ns_p = (dp->packed_pages_used + a.SP - 1) / a.SP;
+    ns_t = L.nsplit - ns_p;
+  }
   {  // apply chunks: the largest power-of-two multiple of the split (at most
      // 1024 pages) that still gives >= 1024 work-groups, which every CU holds
      // at once; fewer, longer chunks amortise the per-work-group item scan
@@ -161,8 +183,41 @@ int run_decode(const carekv_arena* arena, const carekv_decode_params* dp, const 
     int m = 1;
     while (a.SP * 2 * m <= 1024 && pairs * ((a.nsplit + 2 * m - 1) / (2 * m)) >= 1024) m *= 2;
     a.SPA = a.SP * m;
-    a.napply = (a.nsplit + m - 1) / m;
+    na_p = (ns_p + m - 1) / m;
+    na_t = (ns_t + m - 1) / m;
+    a.napply = na_p + na_t;
   }
+  // the tail view: the fp16 side-buffer rows of tail_k / tail_v under the
+  // code-page map of n_packed
+  carekv_arena At = A;
+  if (kv) {
+    At.base_bits = 16;
+    At.scale_mode = 0;
+    At.kcodes = (int8_t*)A.tail_k;
+    At.vcodes = (int8_t*)A.tail_v;
+    At.kivi_packed = 0;
+    At.code_pages = A.tail_pages;
+    At.code_page_off = A.n_packed;
+  }
+  // one call per range with pages (the prefix first: its first split clears the status word)
+  auto ranges = [&](auto&& launch, bool chunks) -> int {
+    if (!kv) {
+      a.range = 0; a.split_base = 0; a.nsplit_run = a.nsplit; a.chunk_base = 0; a.napply_run = a.napply;
+      return launch(A);
+    }
+    int rc = CAREKV_OK;
+    const int n_p = chunks ? na_p : ns_p, n_t = chunks ? na_t : ns_t;
+    if (n_p > 0) {
+      a.range = 1; a.split_base = 0; a.nsplit_run = ns_p; a.chunk_base = 0; a.napply_run = na_p;
+      rc = launch(A);
+    }
+    if (rc == CAREKV_OK && n_t > 0) {
+      a.range = 2; a.split_base = ns_p; a.nsplit_run = ns_t; a.chunk_base = na_p; a.napply_run = na_t;
+      rc = launch(At);
+    }
+    a.range = 0;
+    return rc;
+  };
   hipStream_t s = (hipStream_t)stream;
   if (pf) {
     const carekv_prefill_corr_params& P = *pf->p;
@@ -184,12 +239,14 @@ int run_decode(const carekv_arena* arena, const carekv_decode_params* dp, const 
     return CAREKV_OK;
   };
   int rc = mark(0);
-  if (rc == CAREKV_OK) rc = launch_decode_stream(A, a, s);
+  if (rc == CAREKV_OK) rc = ranges([&](const carekv_arena& V) { return launch_decode_stream(V, a, s); }, false);
   if (rc == CAREKV_OK) rc = mark(1);
-  if (rc == CAREKV_OK && proxy) rc = launch_decode_proxy(A, a, s);
+  if (rc == CAREKV_OK && proxy)
+    rc = ranges([&](const carekv_arena& V) { return launch_decode_proxy(V, a, s); }, false);
   if (rc == CAREKV_OK) rc = launch_decode_select(A, a, s);
   if (rc == CAREKV_OK) rc = mark(2);
-  if (rc == CAREKV_OK && a.correction) rc = launch_decode_apply(A, a, s);
+  if (rc == CAREKV_OK && a.correction)
+    rc = ranges([&](const carekv_arena& V) { return launch_decode_apply(V, a, s); }, true);
   if (rc == CAREKV_OK) rc = mark(3);
   if (rc == CAREKV_OK && a.correction) rc = launch_decode_combine(A, a, s);
   if (rc == CAREKV_OK) rc = mark(4);

@@ -100,7 +100,9 @@ void decode_apply_kernel(carekv_arena A, DecodeArgs a) {
   const long qrow = (long)bk * GQ + (qv ? ln : 0);  // this lane's query row of the workspace
 
   // ---- pages of the chunk with any selected slot
-  const int p_begin = chunk * a.SPA, p_end = min(p_begin + a.SPA, np);
+  int p_lo, p_hi;
+  launch_pages(A, a, seq, np, p_lo, p_hi);
+  const int p_begin = p_lo + chunk * a.SPA, p_end = min(p_begin + a.SPA, p_hi);
   int n_items = 0;
   for (int p0 = p_begin; p0 < p_end; p0 += kBlock) {
     const int p = p0 + threadIdx.x;
@@ -304,7 +306,7 @@ void decode_apply_kernel(carekv_arena A, DecodeArgs a) {
   // ---- merge the waves and write the chunk partial
   den = col_sum(den);
   if (lj == 0) s_den[w][ln] = den;
-  const long cbase = ((long)bk * a.nsplit + chunk) * GQ;
+  const long cbase = ((long)bk * a.nsplit + a.chunk_base + chunk) * GQ;
   sum_waves<D, BITS>(reinterpret_cast<float*>(smem), nacc, w, ln, lj, GQ, a.num + cbase * D);
   if ((int)threadIdx.x < GQ) {
     const int qq = threadIdx.x;
@@ -368,7 +370,7 @@ int launch_decode_apply(const carekv_arena& A, const DecodeArgs& a, hipStream_t 
   }
   if (!a.pf && A.base_bits != 16 && a.GQ <= 4)
     return launch_decode_apply4(A, a, s);  // windows of 4 pages, 4x4x4 layout
-  const dim3 grid(a.napply, A.n_kv_heads, a.B);
+  const dim3 grid(a.napply_run, A.n_kv_heads, a.B);
   // prefill rows read the prompt's fp16 K_hat / V_hat whatever the cache base
   const int bits = a.pf ? 16 : A.base_bits, smode = a.pf ? 0 : A.scale_mode;
   return dispatch_dbs16(A.head_dim, bits, smode, [&](auto d, auto bb, auto sm) {

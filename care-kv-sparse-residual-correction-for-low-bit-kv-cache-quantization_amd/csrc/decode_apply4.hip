@@ -17,6 +17,10 @@
 //   * num += cv R_V for the selected V blocks of the window, 4 blocks per
 //     tile, dequantised by all 64 lanes.
 // den accumulates the K weights; decode_combine_kernel finishes.
+// With 2-bit bases (HL) each weight runs as fp16 hi + lo halves, as in
+// decode_apply.hip: their logit shifts dS are large (up to ~5 with the KIVI
+// base) and the weighted rows partly cancel against O_base, where fp16
+// weights alone cost up to a few hundredths at |O| ~ 1.
 //
 // The loop is a software pipeline: the pages, metadata and mask bytes of a
 // window are read two windows ahead, and each load that depends on them
@@ -40,6 +44,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
   using G = PageGeom<D, BITS>;
   using PR = Pairs<4, 32, 4>;  // pair schedule of a K residual row
   constexpr int NCG = G::NCG, CH = G::CH, CHB = G::CHB, RB = G::RB, NWC = G::NWC;
+  constexpr bool HL = BITS == 2;  // weights as fp16 hi + lo
   constexpr int VT_WORDS = kPage * G::VROW;
   constexpr int MERGE_BYTES = 4 * 4 * D * 4;  // [wave][query][D] fp32
   constexpr int TILE_BYTES = 4 * VT_WORDS * 4;
@@ -51,6 +56,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
   __shared__ int s_items[kMaxSP];
   __shared__ float s_den[4][4];
   __shared__ __align__(16) uint2 s_pk[4][64], s_pv[4][64];  // per wave: [page][query][token group] ck, cv
+  __shared__ __align__(16) uint2 s_pkl[HL ? 4 : 1][64], s_pvl[HL ? 4 : 1][64];  // HL: their lo halves
   __shared__ int s_blk[4][2][16];  // per wave and window parity: selected V blocks, (4 pi + vb) | slot << 4
   __shared__ BlockScratch bs;
 
@@ -76,7 +82,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
   const long qrow = (long)bk * GQ + (qv ? sc : 0);  // this lane's query row of the workspace
 
   // ---- pages of the chunk with any selected slot
-  const int p_begin = chunk * a.SPA, p_end = min(p_begin + a.SPA, np);
+  int p_lo, p_hi;
+  launch_pages(A, a, seq, np, p_lo, p_hi);
+  const int p_begin = p_lo + chunk * a.SPA, p_end = min(p_begin + a.SPA, p_hi);
   int n_items = 0;
   for (int p0 = p_begin; p0 < p_end; p0 += kBlock) {
     const int p = p0 + threadIdx.x;
@@ -378,6 +386,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     const half2_t cv01 = {(_Float16)cv[0], (_Float16)cv[1]}, cv23 = {(_Float16)cv[2], (_Float16)cv[3]};
     pw_store_strided(s_pk[w], h2bits(ck01), h2bits(ck23), lane);
     pw_store(s_pv[w], h2bits(cv01), h2bits(cv23), lane);
+    if constexpr (HL) {
+      const half2_t kl01 = {(_Float16)(ck[0] - (float)ck01[0]), (_Float16)(ck[1] - (float)ck01[1])};
+      const half2_t kl23 = {(_Float16)(ck[2] - (float)ck23[0]), (_Float16)(ck[3] - (float)ck23[1])};
+      const half2_t vl01 = {(_Float16)(cv[0] - (float)cv01[0]), (_Float16)(cv[1] - (float)cv01[1])};
+      const half2_t vl23 = {(_Float16)(cv[2] - (float)cv23[0]), (_Float16)(cv[3] - (float)cv23[1])};
+      pw_store_strided(s_pkl[w], h2bits(kl01), h2bits(kl23), lane);
+      pw_store(s_pvl[w], h2bits(vl01), h2bits(vl23), lane);
+    }
 
     // ---- num += ck V_hat, page by page
 #pragma unroll
@@ -398,6 +414,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
       pw_load(s_pk[w], pi, sc, pg);
 #pragma unroll
       for (int g = 0; g < 4; ++g) pv4_group<D, BITS>(vt, g, pg[g].x, pg[g].y, nacc, lane);
+      if constexpr (HL) {
+        pw_load(s_pkl[w], pi, sc, pg);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) pv4_group<D, BITS>(vt, g, pg[g].x, pg[g].y, nacc, lane);
+      }
       lds_sync_wave();
     }
 
@@ -421,6 +442,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         const int bu = s_blk[w][par][r0 + u] & 15;
         const uint2 pu = s_pv[w][((bu >> 2) * 4 + sc) * 4 + (bu & 3)];
         pv4_group<D, BITS>(vt, u, pu.x, pu.y, nacc, lane);
+        if constexpr (HL) {
+          const uint2 pl = s_pvl[w][((bu >> 2) * 4 + sc) * 4 + (bu & 3)];
+          pv4_group<D, BITS>(vt, u, pl.x, pl.y, nacc, lane);
+        }
       }
       lds_sync_wave();
     }
@@ -434,7 +459,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     den = pair32_sum(pair16_sum(d));  // lanes with query sc hold its total
   }
   if (lane < 4) s_den[w][lane] = den;
-  const long cbase = ((long)bk * a.nsplit + chunk) * GQ;
+  const long cbase = ((long)bk * a.nsplit + a.chunk_base + chunk) * GQ;
   sum4_waves<D, BITS>(reinterpret_cast<float*>(smem), nacc, w, lane, GQ, a.num + cbase * D);
   if ((int)threadIdx.x < GQ) {
     const int qq = threadIdx.x;
@@ -443,7 +468,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
 }
 
 int launch_decode_apply4(const carekv_arena& A, const DecodeArgs& a, hipStream_t s) {
-  const dim3 grid(a.napply, A.n_kv_heads, a.B);
+  const dim3 grid(a.napply_run, A.n_kv_heads, a.B);
   return dispatch_dbs(A.head_dim, A.base_bits, A.scale_mode, [&](auto d, auto bb, auto sm) {
     if (a.k_cap == 1 && a.v_cap == 1)
       hipLaunchKernelGGL((decode_apply4_kernel<decltype(d)::value, decltype(bb)::value, decltype(sm)::value, true>),

@@ -34,6 +34,13 @@ struct DecodeArgs {
   float sm_scale, sm_log2, sens, k_corr_scale, lam_k, lam_v, inv_sqrt_d;
   int correction, kind, joint, normalize, k_exact, budget_ratio, abs_k, abs_v;
   int SPA, napply;  // apply pass: pages per chunk (a multiple of SP) and chunk count (<= nsplit)
+  // One launch of the streaming / proxy / apply kernels covers range 0: all
+  // pages of each row, or on a packed KIVI arena range 1: the packed prefix
+  // (pages below the row's n_packed) or range 2: the fp16 tail (the pages
+  // from n_packed on).  Its grid has nsplit_run splits (napply_run chunks),
+  // whose split partials go to slots split_base.. (chunk partials to
+  // chunk_base..) of the nsplit (napply) the select and combine kernels read.
+  int range, split_base, nsplit_run, chunk_base, napply_run;
   int proxy;        // 1: K scores from the sketch proxy (prox records), 0: from the moments
   int policy;       // 0 separate, 1 joint, 2 k_first, 3 adaptive (ResidualRouter.route)
   int adaptive_score, min_keep;  // read_budget_mode adaptive_score and its floor
@@ -80,6 +87,18 @@ __device__ __forceinline__ EntryRow entry_row(const carekv_arena& A, const Decod
     e.ntok = 0x7fffffff;
   }
   return e;
+}
+
+// Pages [lo, hi) of a row of np pages that a launch covers (DecodeArgs::range).
+__device__ __forceinline__ void launch_pages(const carekv_arena& A, const DecodeArgs& a, int seq, int np, int& lo,
+                                             int& hi) {
+  lo = 0;
+  hi = np;
+  if (a.range != 0) {
+    const int off = min(max(A.n_packed[seq], 0), np);
+    if (a.range == 1) hi = off;
+    else lo = off;
+  }
 }
 
 // Query column c of prefill entry b of kv head kvh: its prompt row, its

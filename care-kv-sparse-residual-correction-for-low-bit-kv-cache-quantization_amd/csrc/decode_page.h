@@ -291,21 +291,32 @@ struct RowRes {
 };
 
 // pg_end clamps the resources at that page of the row: a load past it
-// returns 0 without a memory access.
+// returns 0 without a memory access.  On a view with a code-page map
+// (carekv_arena::code_pages; fp16 pages only) the resources start at the
+// row's code pages shifted back by its offset, so page p still loads at
+// p * page bytes; the caller touches only pages the map holds.
 template <int D, int BITS, int SM>
 __device__ __forceinline__ RowRes row_resources(const carekv_arena& A, long pg_base, int pg_end = -1) {
   using G = PageGeom<D, BITS>;
-  const uint32_t rows = (uint32_t)(pg_end >= 0 ? pg_end : A.max_pages) * kPage;
+  long cb = pg_base;
+  int lim = A.max_pages;
+  if constexpr (BITS == 16) {  // maps hold fp16 pages only (the tail of a packed KIVI arena)
+    if (A.code_pages > 0) {
+      cb = code_base(A, pg_base);
+      lim = code_page_limit(A, pg_base);
+    }
+  }
+  const uint32_t rows = (uint32_t)(pg_end >= 0 ? min(pg_end, lim) : lim) * kPage;
   constexpr int ssz = SM == 1 ? 1 : 2;
   RowRes r;
-  r.kc = make_rsrc(A.kcodes + pg_base * kPage * G::RB, rows * G::RB);
-  r.vc = make_rsrc(A.vcodes + pg_base * kPage * G::RB, rows * G::RB);
+  r.kc = make_rsrc(A.kcodes + cb * kPage * G::RB, rows * G::RB);
+  r.vc = make_rsrc(A.vcodes + cb * kPage * G::RB, rows * G::RB);
   if constexpr (BITS == 16) {  // no scales: empty resources, loads return 0
     r.ks = make_rsrc(nullptr, 0u);
     r.vs = make_rsrc(nullptr, 0u);
   } else {
-    r.ks = make_rsrc((const char*)A.kscale + pg_base * kPage * G::NCG * ssz, rows * G::NCG * ssz);
-    r.vs = make_rsrc((const char*)A.vscale + pg_base * kPage * G::NCG * ssz, rows * G::NCG * ssz);
+    r.ks = make_rsrc((const char*)A.kscale + cb * kPage * G::NCG * ssz, rows * G::NCG * ssz);
+    r.vs = make_rsrc((const char*)A.vscale + cb * kPage * G::NCG * ssz, rows * G::NCG * ssz);
   }
   return r;
 }

@@ -48,7 +48,9 @@ __global__ __launch_bounds__(256) void decode_proxy_kernel(carekv_arena A, Decod
   const int bk = b * A.n_kv_heads + kvh;
   const EntryRow er = entry_row(A, a, b);
   const int seq = er.seq, np = er.np;
-  const int p_begin = split * a.SP, p_end = min(p_begin + a.SP, np);
+  int p_lo, p_hi;
+  launch_pages(A, a, seq, np, p_lo, p_hi);
+  const int p_begin = p_lo + split * a.SP, p_end = min(p_begin + a.SP, p_hi);
   if (p_begin >= p_end) return;  // uniform over the work-group
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -162,7 +164,7 @@ __global__ __launch_bounds__(256) void decode_proxy_kernel(carekv_arena A, Decod
 }
 
 int launch_decode_proxy(const carekv_arena& A, const DecodeArgs& a, hipStream_t s) {
-  const dim3 grid(a.nsplit, A.n_kv_heads, a.B);
+  const dim3 grid(a.nsplit_run, A.n_kv_heads, a.B);
   if (a.pf) {
     if (A.head_dim == 64) hipLaunchKernelGGL((decode_proxy_kernel<64, 16, 0, true>), grid, dim3(256), 0, s, A, a);
     else hipLaunchKernelGGL((decode_proxy_kernel<128, 16, 0, true>), grid, dim3(256), 0, s, A, a);

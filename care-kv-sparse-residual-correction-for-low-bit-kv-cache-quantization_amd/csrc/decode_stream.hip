@@ -46,7 +46,7 @@ void decode_stream_kernel(carekv_arena A, DecodeArgs a) {
 
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   // the call's status word starts clear; the select kernel (a later launch) sets it
-  if ((split | kvh | b) == 0 && threadIdx.x == 0) *a.err_flag = 0;
+  if (((a.split_base + split) | kvh | b) == 0 && threadIdx.x == 0) *a.err_flag = 0;
   const int GQ = a.GQ;
   const int bk = b * A.n_kv_heads + kvh;
   const EntryRow er = entry_row(A, a, b);
@@ -96,7 +96,9 @@ void decode_stream_kernel(carekv_arena A, DecodeArgs a) {
 #pragma unroll
   for (int t = 0; t < NT; ++t) oacc[t] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-  const int p_begin = split * a.SP, p_end = min(p_begin + a.SP, np);
+  int p_lo, p_hi;
+  launch_pages(A, a, seq, np, p_lo, p_hi);
+  const int p_begin = p_lo + split * a.SP, p_end = min(p_begin + a.SP, p_hi);
 
   PageRegs<D, BITS> nx;
   int nmv = 0;  // next page's metadata, one field per lane
@@ -262,12 +264,12 @@ void decode_stream_kernel(carekv_arena A, DecodeArgs a) {
   // of the dims per round; V slot 16t + n (tile t, column n) maps back to dim
   // chunk*CH + slot_code[slot % CH].
   merge_waves<D, BITS>(reinterpret_cast<float*>(smem), s_m, s_l, m_run, l_run, oacc, w, ln, lj, GQ,
-                       a.po + ((long)bk * a.nsplit + split) * 16 * D,
-                       a.pml + ((long)bk * a.nsplit + split) * 16 * 2);
+                       a.po + ((long)bk * a.nsplit + a.split_base + split) * 16 * D,
+                       a.pml + ((long)bk * a.nsplit + a.split_base + split) * 16 * 2);
 }
 
 int launch_decode_stream(const carekv_arena& A, const DecodeArgs& a, hipStream_t s) {
-  dim3 grid(a.nsplit, A.n_kv_heads, a.B);
+  dim3 grid(a.nsplit_run, A.n_kv_heads, a.B);
   if (a.pf) {
     auto go = [&](auto kern) {
       hipLaunchKernelGGL(kern, grid, dim3(256), 0, s, A, a);

@@ -24,6 +24,24 @@
 //   else of this pass.
 // The page records and split partials are those of decode_stream.hip, with
 // m_ref the running max at the window.
+//
+// KV (the packed KIVI prefix, carekv_arena::kivi_packed): 2-bit K codes
+// against one per-channel scale vector s_c of the (kv head, sequence).
+// K_hat = half(code * s_c) = code * s_c exactly for codes -2..1, so
+// S = sum_c (q_c s_c) code_c with every product exact: q_c s_c (22
+// significant bits, exact in fp32) is split into fp16 hi + lo, both run
+// through the MFMA against the exact integer codes, and the two
+// accumulators sum to S up to fp32 order.  A power-of-two 2^E per work-group
+// keeps the largest |q_c s_c| 2^E near 2^15 so that hi and lo stay normal;
+// S is scaled back by 2^-E.  The V pages are those of a 2-bit base with
+// fp16 group scales; the V product runs on exact signed fp16 codes (two ops
+// per pair) against the weights P' = half(e) s_V, exact in fp32 and carried
+// as fp16 hi + lo, and L sums half(e): the base output and its normaliser
+// then weigh V_hat exactly as the apply pass does (half(e) V_hat).  The
+// KIVI base's K corrections can remove most of the mass (|dO| above |O|,
+// 1 + den / L down to a few hundredths), which amplifies any error of the
+// base output: the offset-code form of the uniform bases, whose offset
+// 2^(b-1) sum(P') cancels against the code sum, loses about 1e-4 there.
 #include "decode_page.h"
 #include "host_util.h"
 
@@ -49,7 +67,7 @@ struct WinV {
   uint32_t vsc[VSW];
 };
 
-template <int D, int BITS, int SM>
+template <int D, int BITS, int SM, bool KV = false>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) void decode_stream4_kernel(carekv_arena A, DecodeArgs a) {
   using G = PageGeom<D, BITS>;
   using WK = WinK<D, BITS, SM>;
@@ -64,9 +82,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
   constexpr int LDS_BYTES = MERGE_BYTES > TILE_BYTES ? MERGE_BYTES : TILE_BYTES;
   __shared__ __align__(16) char smem[LDS_BYTES];
   __shared__ __align__(16) _Float16 sq4[NS4 * 16];       // [step][query][4]: q in the row pair order
+  __shared__ __align__(16) _Float16 sq4lo[KV ? NS4 * 16 : 4];  // KV: the lo halves of q_c s_c 2^E
+  __shared__ float s_red[4];
   __shared__ __align__(16) _Float16 sqr4[NCG * 8 * 16];  // [cg][step][query][4]: q in the residual order
   __shared__ float s_m[4][4], s_l[4][4];
   __shared__ __align__(16) uint16_t s_pw[4][4 * NCG * 64];  // per wave: [page][G][query][16] weights P'
+  __shared__ __align__(16) uint16_t s_pwl[KV ? 4 : 1][KV ? 4 * NCG * 64 : 8];  // KV: their lo halves
   __shared__ __align__(16) uint16_t s_vs[4][4 * NCG * 16];  // per wave: [page][G][token] V scales
 
   const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
@@ -82,7 +103,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
   const int ln = lane & 15, lj = lane >> 4;  // V side: token ln, chunk lj; K side: token ln of page lj
   const int sc = lane & 3, sbk = ln >> 2;    // S layout: query sc, tokens 4*sbk.. of page lj
   const long pg_base = ((long)kvh * A.n_seq + seq) * A.max_pages;
-  const int p_begin = split * a.SP, p_end = min(p_begin + a.SP, np);
+  // the packed KIVI prefix stops at the row's n_packed; its launch (range 1)
+  // and the uniform bases' (range 0) both start at split slot 0
+  int p_hi = np;
+  if constexpr (KV) p_hi = min(np, max(A.n_packed[seq], 0));
+  const int p_begin = split * a.SP, p_end = min(p_begin + a.SP, p_hi);
   // code and scale loads past page p_end read out of range of the resources
   // (0, no memory access), so every prefetch is issued unconditionally and
   // the in-order load counter never waits across a branch
@@ -107,11 +132,38 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
   const int8_t* kres_row = A.k_res + (long)seq * A.n_slots * G::KSB;  // K residual slots of the sequence
   const uint16_t* kres_sc = A.k_res_scale + (long)seq * A.n_slots;
 
+  float s_back = 1.f;  // KV: 2^-E
   {  // q in the MFMA orders
     const uint16_t* qg = a.q + ((long)b * a.Hq + kvh * GQ) * D;
-    for (int i = threadIdx.x; i < NS4 * 16; i += 256) {
-      const int s = i >> 4, c = (i >> 2) & 3, e = i & 3;
-      sq4[i] = c < GQ ? bits2half(qg[c * D + PF::T.slot_code[4 * s + e]]) : (_Float16)0.f;
+    if constexpr (KV) {
+      const uint16_t* kc = A.kchan + ((long)kvh * A.n_seq + seq) * D;
+      float mx = 0.f;
+      for (int i = threadIdx.x; i < NS4 * 16; i += 256) {
+        const int s = i >> 4, c = (i >> 2) & 3, e = i & 3, ch = PF::T.slot_code[4 * s + e];
+        if (c < GQ) mx = fmaxf(mx, fabsf(h2f(qg[c * D + ch]) * h2f(kc[ch])));
+      }
+      mx = wave_max(mx);
+      if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = mx;
+      __syncthreads();
+      mx = fmaxf(fmaxf(s_red[0], s_red[1]), fmaxf(s_red[2], s_red[3]));
+      // |q s| 2^E <= 2^15: the exponent of mx read from its bits (mx normal
+      // or 0; a non-finite mx keeps E = 0)
+      int E = 0;
+      if (mx > 0.f && mx < INFINITY) E = min(max(15 - ((int)((__float_as_uint(mx) >> 23) & 0xffu) - 127) - 1, -100), 100);
+      const float up = __builtin_ldexpf(1.f, E);
+      s_back = __builtin_ldexpf(1.f, -E);
+      for (int i = threadIdx.x; i < NS4 * 16; i += 256) {
+        const int s = i >> 4, c = (i >> 2) & 3, e = i & 3, ch = PF::T.slot_code[4 * s + e];
+        const float v = c < GQ ? h2f(qg[c * D + ch]) * h2f(kc[ch]) * up : 0.f;  // exact in fp32
+        const _Float16 hi = (_Float16)v;
+        sq4[i] = hi;
+        sq4lo[i] = (_Float16)(v - (float)hi);
+      }
+    } else {
+      for (int i = threadIdx.x; i < NS4 * 16; i += 256) {
+        const int s = i >> 4, c = (i >> 2) & 3, e = i & 3;
+        sq4[i] = c < GQ ? bits2half(qg[c * D + PF::T.slot_code[4 * s + e]]) : (_Float16)0.f;
+      }
     }
     for (int i = threadIdx.x; i < NCG * 128; i += 256) {
       const int cg = i >> 7, s = (i >> 4) & 7, c = (i >> 2) & 3, e = i & 3;
@@ -136,7 +188,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
   auto load_k = [&](int q0) {
     const uint32_t krow = (uint32_t)((q0 + lj) * kPage + ln);
     buf_load_row<RB>(kx.kw, rr.kc, krow * RB);
-    if constexpr (SM == 1) {
+    if constexpr (KV) {
+      // no K scales: the channel scales ride on q
+    } else if constexpr (SM == 1) {
       if constexpr (NCG == 4) kx.ksc[0] = __builtin_amdgcn_raw_buffer_load_b32(rr.ks, krow * NCG, 0, 0);
       else kx.ksc[0] = __builtin_amdgcn_raw_buffer_load_b16(rr.ks, krow * NCG, 0, 0);
     } else {
@@ -244,26 +298,39 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
 
     __builtin_amdgcn_sched_barrier(0);  // phases stay apart: bounds the live registers
     // ---- S = K_hat q on 4x4x4 blocks
-    _Float16 ksg[NCG];
-    {
-      const float km = SM == 1 ? h2f((uint16_t)__shfl(cmeta, (lane & 48) + 10, 64)) : 0.f;
-#pragma unroll
-      for (int g = 0; g < NCG; ++g) {
-        if constexpr (SM == 1) ksg[g] = (_Float16)((float)(int8_t)(kx.ksc[0] >> (8 * g)) * km);
-        else ksg[g] = bits2half((uint16_t)(kx.ksc[g >> 1] >> (16 * (g & 1))));
-      }
-    }
     float4_t sa0 = {0.f, 0.f, 0.f, 0.f}, sa1 = {0.f, 0.f, 0.f, 0.f};
+    if constexpr (KV) {
 #pragma unroll
-    for (int s = 0; s < NS4; ++s) {
-      const int g = PF::T.a[2 * s] / 32;
-      const half2_t ss = {ksg[g], ksg[g]};
-      const half2_t c0 = code_pair<BITS, D, BITS>(kx.kw, 2 * s) * ss;
-      const half2_t c1 = code_pair<BITS, D, BITS>(kx.kw, 2 * s + 1) * ss;
-      const half4_t ak = {c0[0], c0[1], c1[0], c1[1]};
-      const half4_t bq = *reinterpret_cast<const half4_t*>(sq4 + (s * 4 + sc) * 4);
-      if (s & 1) sa1 = mfma4x4(ak, bq, sa1);
-      else sa0 = mfma4x4(ak, bq, sa0);
+      for (int s = 0; s < NS4; ++s) {
+        const half2_t c0 = code_pair<BITS, D, BITS>(kx.kw, 2 * s);
+        const half2_t c1 = code_pair<BITS, D, BITS>(kx.kw, 2 * s + 1);
+        const half4_t ak = {c0[0], c0[1], c1[0], c1[1]};
+        const half4_t bh = *reinterpret_cast<const half4_t*>(sq4 + (s * 4 + sc) * 4);
+        const half4_t bl = *reinterpret_cast<const half4_t*>(sq4lo + (s * 4 + sc) * 4);
+        sa0 = mfma4x4(ak, bh, sa0);
+        sa1 = mfma4x4(ak, bl, sa1);
+      }
+    } else {
+      _Float16 ksg[NCG];
+      {
+        const float km = SM == 1 ? h2f((uint16_t)__shfl(cmeta, (lane & 48) + 10, 64)) : 0.f;
+#pragma unroll
+        for (int g = 0; g < NCG; ++g) {
+          if constexpr (SM == 1) ksg[g] = (_Float16)((float)(int8_t)(kx.ksc[0] >> (8 * g)) * km);
+          else ksg[g] = bits2half((uint16_t)(kx.ksc[g >> 1] >> (16 * (g & 1))));
+        }
+      }
+#pragma unroll
+      for (int s = 0; s < NS4; ++s) {
+        const int g = PF::T.a[2 * s] / 32;
+        const half2_t ss = {ksg[g], ksg[g]};
+        const half2_t c0 = code_pair<BITS, D, BITS>(kx.kw, 2 * s) * ss;
+        const half2_t c1 = code_pair<BITS, D, BITS>(kx.kw, 2 * s + 1) * ss;
+        const half4_t ak = {c0[0], c0[1], c1[0], c1[1]};
+        const half4_t bq = *reinterpret_cast<const half4_t*>(sq4 + (s * 4 + sc) * 4);
+        if (s & 1) sa1 = mfma4x4(ak, bq, sa1);
+        else sa0 = mfma4x4(ak, bq, sa0);
+      }
     }
 
     __builtin_amdgcn_sched_barrier(0);
@@ -271,7 +338,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     // ---- online softmax over the window (lane: tokens 4*sbk+i of page lj, query sc)
     float x[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) x[i] = (4 * sbk + i < my_nv) ? (sa0[i] + sa1[i]) * sm_log2 : -INFINITY;
+    for (int i = 0; i < 4; ++i) {
+      const float sv = KV ? (sa0[i] + sa1[i]) * s_back : sa0[i] + sa1[i];
+      x[i] = (4 * sbk + i < my_nv) ? sv * sm_log2 : -INFINITY;
+    }
     if (a.xbuf && corr && sc < GQ && my_nv > 0) {  // logits for the proxy's margins / the entropy
       typedef uint32_t u4_t __attribute__((ext_vector_type(4)));
       __builtin_amdgcn_raw_buffer_store_b128(
@@ -286,7 +356,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     float e[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) e[i] = __builtin_amdgcn_exp2f(x[i] - m_use);
-    l_run = l_run * f_old + pair32_sum(pair16_sum(row4_sum((e[0] + e[1]) + (e[2] + e[3]))));
+    float lsum = (e[0] + e[1]) + (e[2] + e[3]);
+    if constexpr (KV) {  // L over the fp16 weights the V product and the apply pass use
+      lsum = ((float)(_Float16)e[0] + (float)(_Float16)e[1]) + ((float)(_Float16)e[2] + (float)(_Float16)e[3]);
+    }
+    l_run = l_run * f_old + pair32_sum(pair16_sum(row4_sum(lsum)));
     if (__builtin_expect(__any(f_old != 1.f), 0)) {
 #pragma unroll
       for (int h = 0; h < D / 64; ++h) oacc[h] *= f_old;  // the lane's own query
@@ -305,10 +379,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         half2_t s01, s23;
         __builtin_memcpy(&s01, &sv.x, 4);
         __builtin_memcpy(&s23, &sv.y, 4);
-        const half2_t p01 = eh01 * s01, p23 = eh23 * s23;
-        wsum[g] = __builtin_amdgcn_fdot2(p01, one2, wsum[g], false);
-        wsum[g] = __builtin_amdgcn_fdot2(p23, one2, wsum[g], false);
-        pwg_store<NCG>(s_pw[w], g, h2bits(p01), h2bits(p23), lane);
+        if constexpr (KV) {
+          float pf[4] = {(float)eh01[0] * (float)s01[0], (float)eh01[1] * (float)s01[1],
+                         (float)eh23[0] * (float)s23[0], (float)eh23[1] * (float)s23[1]};  // exact
+          const half2_t h01 = {(_Float16)pf[0], (_Float16)pf[1]}, h23 = {(_Float16)pf[2], (_Float16)pf[3]};
+          const half2_t l01 = {(_Float16)(pf[0] - (float)h01[0]), (_Float16)(pf[1] - (float)h01[1])};
+          const half2_t l23 = {(_Float16)(pf[2] - (float)h23[0]), (_Float16)(pf[3] - (float)h23[1])};
+          wsum[g] += (pf[0] + pf[1]) + (pf[2] + pf[3]);
+          pwg_store<NCG>(s_pw[w], g, h2bits(h01), h2bits(h23), lane);
+          pwg_store<NCG>(s_pwl[w], g, h2bits(l01), h2bits(l23), lane);
+        } else {
+          const half2_t p01 = eh01 * s01, p23 = eh23 * s23;
+          wsum[g] = __builtin_amdgcn_fdot2(p01, one2, wsum[g], false);
+          wsum[g] = __builtin_amdgcn_fdot2(p23, one2, wsum[g], false);
+          pwg_store<NCG>(s_pw[w], g, h2bits(p01), h2bits(p23), lane);
+        }
       }
     }
 
@@ -320,7 +405,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
       if (live) {
         uint32_t vp[CH / 2];
 #pragma unroll
-        for (int i = 0; i < CH / 2; ++i) vp[i] = code_pair_sub<BITS, CH, BITS>(cv.vw[pi], i);
+        for (int i = 0; i < CH / 2; ++i) {
+          if constexpr (KV) {  // exact signed codes: no offset to take back
+            const half2_t c = code_pair<BITS, CH, BITS>(cv.vw[pi], i);
+            vp[i] = h2bits(c);
+          } else {
+            vp[i] = code_pair_sub<BITS, CH, BITS>(cv.vw[pi], i);
+          }
+        }
         vtile_write_raw<D, BITS>(vt, vp, ln, lj);
       }
       load_vpage(cv, p0 + 16, pi);  // the next window's page pi into the registers just consumed
@@ -332,6 +424,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
         pwg_load<NCG>(s_pw[w], pi, 2 * h + (lane >> 5), sc, pg);
 #pragma unroll
         for (int g = 0; g < 4; ++g) pv4_step<D, BITS>(vt, g, h, pg[g].x, pg[g].y, oacc[h], lane);
+        if constexpr (KV) {
+          pwg_load<NCG>(s_pwl[w], pi, 2 * h + (lane >> 5), sc, pg);
+#pragma unroll
+          for (int g = 0; g < 4; ++g) pv4_step<D, BITS>(vt, g, h, pg[g].x, pg[g].y, oacc[h], lane);
+        }
       }
       lds_sync_wave();
     }
@@ -437,13 +534,35 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
       bias[h] = (lane >> 5) ? hi : lo;
     }
   }
-  merge4_waves_raw<D, BITS>(reinterpret_cast<float*>(smem), s_m, s_l, m_run, l_run, oacc, bias, w, lane, GQ,
-                           a.po + ((long)bk * a.nsplit + split) * 16 * D,
-                           a.pml + ((long)bk * a.nsplit + split) * 16 * 2);
+  if constexpr (KV)
+    merge4_waves<D, BITS>(reinterpret_cast<float*>(smem), s_m, s_l, m_run, l_run, oacc, w, lane, GQ,
+                          a.po + ((long)bk * a.nsplit + split) * 16 * D, a.pml + ((long)bk * a.nsplit + split) * 16 * 2);
+  else
+    merge4_waves_raw<D, BITS>(reinterpret_cast<float*>(smem), s_m, s_l, m_run, l_run, oacc, bias, w, lane, GQ,
+                             a.po + ((long)bk * a.nsplit + split) * 16 * D,
+                             a.pml + ((long)bk * a.nsplit + split) * 16 * 2);
 }
 
 int launch_decode_stream4(const carekv_arena& A, const DecodeArgs& a, hipStream_t s) {
-  dim3 grid(a.nsplit, A.n_kv_heads, a.B);
+  dim3 grid(a.nsplit_run, A.n_kv_heads, a.B);
+  if (a.split_base != 0 || a.range != (A.kivi_packed ? 1 : 0)) {
+    set_error("decode_stream4: runs the whole row of a uniform base or the packed KIVI prefix from split 0");
+    return CAREKV_EINVAL;
+  }
+  if (A.kivi_packed) {
+    if (A.base_bits != 2 || A.scale_mode != 0) {
+      set_error("decode_stream4: a packed KIVI arena has base_bits 2 and scale_mode 0");
+      return CAREKV_EINVAL;
+    }
+    if (A.head_dim == 64) hipLaunchKernelGGL((decode_stream4_kernel<64, 2, 0, true>), grid, dim3(256), 0, s, A, a);
+    else if (A.head_dim == 128) hipLaunchKernelGGL((decode_stream4_kernel<128, 2, 0, true>), grid, dim3(256), 0, s, A, a);
+    else {
+      set_error("decode_stream4: head_dim %d (kernels: 64, 128)", A.head_dim);
+      return CAREKV_EINVAL;
+    }
+    CAREKV_CHECK_LAUNCH("decode_stream4 (packed KIVI)");
+    return CAREKV_OK;
+  }
   return dispatch_dbs(A.head_dim, A.base_bits, A.scale_mode, [&](auto d, auto bb, auto sm) {
     hipLaunchKernelGGL((decode_stream4_kernel<decltype(d)::value, decltype(bb)::value, decltype(sm)::value>), grid,
                        dim3(256), 0, s, A, a);

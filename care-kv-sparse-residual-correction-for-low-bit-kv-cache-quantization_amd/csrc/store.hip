@@ -125,6 +125,10 @@ __global__ __launch_bounds__(256) void store_pages_kernel(carekv_arena A, carekv
   const bool active = t < kPage;
   const int nvld = job.num_valid;
   const long pg = ((long)job.kv_head * A.n_seq + job.seq) * A.max_pages + job.page;
+  // a packed KIVI arena's call runs once over the packed prefix and once
+  // over a view of its fp16 tail: each launch takes only its own pages
+  if (A.kivi_packed && job.page >= A.n_packed[job.seq]) return;
+  if (!code_pg_in(A, pg)) return;
 
   // ---- quantize own (t, g) group of K and V, fp16 chain (or, for the fp16
   // side-buffer base, take the given K_hat / V_hat)
@@ -162,7 +166,20 @@ __global__ __launch_bounds__(256) void store_pages_kernel(carekv_arena A, carekv
         xv[i + 2 * j] = h2f((uint16_t)wb[j]); xv[i + 2 * j + 1] = h2f((uint16_t)(wb[j] >> 16));
       }
     }
-    if (sp.k_codes_in) {
+    if (A.kivi_packed) {
+      // packed KIVI prefix page: the caller's 2-bit codes and per-token V
+      // scales; the residuals are taken against K_hat / V_hat, which
+      // half(code * scale) reproduces (K's per-channel scales live in kchan)
+      const long ri = (long)job_id * kPage + t;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) {
+        ck[i] = sp.k_codes_in[ri * D + g * 32 + i];
+        cv[i] = sp.v_codes_in[ri * D + g * 32 + i];
+        hk[i] = h2f(sp.k_hat[ri * D + g * 32 + i]);
+        hv[i] = h2f(sp.v_hat[ri * D + g * 32 + i]);
+      }
+      sv = bits2half(sp.v_scale_in[ri * NG + g]);
+    } else if (sp.k_codes_in) {
       // process_page on a page write_base wrote: the caller's base codes and
       // fp16 group scales (residual_store.py:276-285); the page keeps its base
       const long ri = (long)job_id * kPage + t;
@@ -196,11 +213,14 @@ __global__ __launch_bounds__(256) void store_pages_kernel(carekv_arena A, carekv
       sk = quant_group<BITS>(xk, ck);
       sv = quant_group<BITS>(xv, cv);
     }
-    // residual against the fp16 scale (residual_store.py:276-285)
+    // residual against the fp16 scale (residual_store.py:276-285), or
+    // against the KIVI K_hat / V_hat
+    const bool kv = A.kivi_packed != 0;
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
-      rk[i] = (t < nvld) ? (float)(_Float16)(xk[i] - (float)dq(ck[i], sk)) : 0.f;
-      rv[i] = (t < nvld) ? (float)(_Float16)(xv[i] - (float)dq(cv[i], sv)) : 0.f;
+      const float bk = kv ? hk[i] : (float)dq(ck[i], sk), bv = kv ? hv[i] : (float)dq(cv[i], sv);
+      rk[i] = (t < nvld) ? (float)(_Float16)(xk[i] - bk) : 0.f;
+      rv[i] = (t < nvld) ? (float)(_Float16)(xv[i] - bv) : 0.f;
     }
   } else {
 #pragma unroll
@@ -241,16 +261,18 @@ __global__ __launch_bounds__(256) void store_pages_kernel(carekv_arena A, carekv
   select_candidates<NG>(kerr, verr, sp, struct_prior, sel_k, nk, sel_v, nv, okind, oidx, nord);
 
   if constexpr (MODE == 0 && BITS == 16) {
-    // ---- fp16 side-buffer rows (cache.py:800-818) and sum of V_hat^2
-    if (active) {
+    // ---- fp16 side-buffer rows (cache.py:800-818) and sum of V_hat^2; on a
+    // code-page map only the pages it holds (the host sends no others)
+    if (active && code_pg_in(A, pg)) {
       uint32_t wk[16], wv[16];
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         wk[i] = (uint32_t)f2h(hk[2 * i]) | ((uint32_t)f2h(hk[2 * i + 1]) << 16);
         wv[i] = (uint32_t)f2h(hv[2 * i]) | ((uint32_t)f2h(hv[2 * i + 1]) << 16);
       }
-      store_bytes<64>(A.kcodes + (pg * kPage + t) * RB + g * 64, wk);
-      store_bytes<64>(A.vcodes + (pg * kPage + t) * RB + g * 64, wv);
+      const long cpg = code_pg(A, pg);
+      store_bytes<64>(A.kcodes + (cpg * kPage + t) * RB + g * 64, wk);
+      store_bytes<64>(A.vcodes + (cpg * kPage + t) * RB + g * 64, wv);
     }
     float vs = 0.f;
     if (active && t < nvld) {
@@ -260,7 +282,7 @@ __global__ __launch_bounds__(256) void store_pages_kernel(carekv_arena A, carekv
     vs = wave_sum(vs);
     if (lane == 0) A.v_sq[pg] = vs;
   }
-  if (MODE == 0 && BITS != 16 && (sp.keep_base || sp.k_codes_in)) {
+  if (MODE == 0 && BITS != 16 && !A.kivi_packed && (sp.keep_base || sp.k_codes_in)) {
     // ---- the page keeps its base; only the sum of V_hat^2 is refreshed, over
     // the rows as the decode reads them back
     float vs = 0.f;
@@ -523,8 +545,10 @@ __global__ __launch_bounds__(256) void append_hat_rows_kernel(carekv_arena A, co
   const long pg = ((long)kvh * A.n_seq + seq) * A.max_pages + page;
   const int off = fresh ? 0 : A.valid[pg];
   if (off >= kPage) return;  // caller contract violated; never write past the page
-  uint16_t* krow = reinterpret_cast<uint16_t*>(A.kcodes) + (pg * kPage + off) * D;
-  uint16_t* vrow = reinterpret_cast<uint16_t*>(A.vcodes) + (pg * kPage + off) * D;
+  if (!code_pg_in(A, pg)) return;  // a page the code-page map does not hold: never written
+  const long cpg = code_pg(A, pg);
+  uint16_t* krow = reinterpret_cast<uint16_t*>(A.kcodes) + (cpg * kPage + off) * D;
+  uint16_t* vrow = reinterpret_cast<uint16_t*>(A.vcodes) + (cpg * kPage + off) * D;
   float av = 0.f;
   for (int d = lane; d < D; d += 64) av = fmaxf(av, fabsf(h2f(Vx[(long)row * D + d])));
   const float sv = kivi_scale(wave_max(av), A.hat_bits_v);
@@ -736,6 +760,103 @@ __global__ __launch_bounds__(256) void read_pages_kernel(carekv_arena A, int seq
   }
 }
 
+// Codes and scales of the KIVI quant-dequant (carekv_kivi_codes): one
+// work-group per (matrix, 64 columns) for K per channel over the rows, one
+// wave per row for V per token.  A scale whose max|x| is 0 is stored as NaN.
+__device__ __forceinline__ int kivi_code(float x, float scale, int bits) {
+  const float qmax = (float)((1 << (bits - 1)) - 1);
+  const float q = rintf((float)(_Float16)(x / scale));
+  return (q != q) ? 0 : (int)fminf(fmaxf(q, -qmax - 1.f), qmax);
+}
+__global__ __launch_bounds__(256) void kivi_channel_codes_kernel(const uint16_t* __restrict__ x, int rows, int D,
+                                                                 int bits, int8_t* __restrict__ codes,
+                                                                 uint16_t* __restrict__ scale) {
+  __shared__ float s_max[4][64];
+  const int m = blockIdx.x, c0 = blockIdx.y * 64;
+  const int lane = threadIdx.x & 63, rg = threadIdx.x >> 6;
+  const int d = c0 + lane;
+  const long base = (long)m * rows * D;
+  float a = 0.f;
+  if (d < D)
+    for (int r = rg; r < rows; r += 4) a = fmaxf(a, fabsf(h2f(x[base + (long)r * D + d])));
+  s_max[rg][lane] = a;
+  __syncthreads();
+  const float amax = fmaxf(fmaxf(s_max[0][lane], s_max[1][lane]), fmaxf(s_max[2][lane], s_max[3][lane]));
+  const float sc = kivi_scale(amax, bits);
+  if (d < D) {
+    for (int r = rg; r < rows; r += 4) {
+      const long i = base + (long)r * D + d;
+      codes[i] = (int8_t)kivi_code(h2f(x[i]), sc, bits);
+    }
+    if (rg == 0) scale[(long)m * D + d] = amax == 0.f ? (uint16_t)0x7e00u : f2h(sc);
+  }
+}
+__global__ __launch_bounds__(256) void kivi_token_codes_kernel(const uint16_t* __restrict__ x, long n_rows, int D,
+                                                               int bits, int8_t* __restrict__ codes,
+                                                               uint16_t* __restrict__ scale) {
+  const long row = (long)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= n_rows) return;
+  const uint16_t* xr = x + row * D;
+  float a = 0.f;
+  for (int d = lane; d < D; d += 64) a = fmaxf(a, fabsf(h2f(xr[d])));
+  const float amax = wave_max(a);
+  const float sc = kivi_scale(amax, bits);
+  for (int d = lane; d < D; d += 64) codes[row * D + d] = (int8_t)kivi_code(h2f(xr[d]), sc, bits);
+  if (lane == 0) scale[row] = amax == 0.f ? (uint16_t)0x7e00u : f2h(sc);
+}
+
+// read_base_hat_concat (carekv_read_hat_pages): one 64-thread block per page;
+// K_hat / V_hat rows of a fp16 page (the side-buffer base, or the tail of a
+// packed KIVI arena) copied, of a packed KIVI prefix page dequantised.
+template <int D>
+__global__ __launch_bounds__(64) void read_hat_pages_kernel(carekv_arena A, int seq, int kvh, int n_pages,
+                                                            const int32_t* __restrict__ page_ids,
+                                                            const int32_t* __restrict__ row_start,
+                                                            uint16_t* __restrict__ kh, uint16_t* __restrict__ vh) {
+  constexpr int NG = D / 32;
+  constexpr int RB2 = row_bytes(D, 2);
+  const int p = blockIdx.x;
+  if (p >= n_pages) return;
+  const int page = page_ids ? page_ids[p] : p;
+  if (page < 0 || page >= A.max_pages) return;
+  const long pg = ((long)kvh * A.n_seq + seq) * A.max_pages + page;
+  const int n = A.valid[pg];
+  const long r0 = row_start[p];
+  const bool packed = A.kivi_packed && page < A.n_packed[seq];
+  if (packed) {
+    const uint16_t* kc = A.kchan + ((long)kvh * A.n_seq + seq) * D;
+    for (int idx = threadIdx.x; idx < n * D; idx += 64) {
+      const int t = idx / D, d = idx % D, g = d / 32;
+      uint32_t w[2];
+      load_bytes<8>(w, A.kcodes + (pg * kPage + t) * RB2 + g * 8);
+      const int ck = get_code<2>(w, d % 32);
+      load_bytes<8>(w, A.vcodes + (pg * kPage + t) * RB2 + g * 8);
+      const int cv = get_code<2>(w, d % 32);
+      const _Float16 vs = bits2half(((const uint16_t*)A.vscale)[(pg * kPage + t) * NG + g]);
+      kh[(r0 + t) * D + d] = half2bits(dq(ck, bits2half(kc[d])));
+      vh[(r0 + t) * D + d] = half2bits(dq(cv, vs));
+    }
+    return;
+  }
+  const uint16_t* ksrc;
+  const uint16_t* vsrc;
+  if (A.kivi_packed) {
+    const int tp = page - A.n_packed[seq];
+    if (tp >= A.tail_pages) return;
+    const long tpg = ((long)kvh * A.n_seq + seq) * A.tail_pages + tp;
+    ksrc = A.tail_k + tpg * kPage * D;
+    vsrc = A.tail_v + tpg * kPage * D;
+  } else {
+    ksrc = reinterpret_cast<const uint16_t*>(A.kcodes) + pg * kPage * D;
+    vsrc = reinterpret_cast<const uint16_t*>(A.vcodes) + pg * kPage * D;
+  }
+  for (int idx = threadIdx.x; idx < n * D; idx += 64) {
+    kh[r0 * D + idx] = ksrc[idx];
+    vh[r0 * D + idx] = vsrc[idx];
+  }
+}
+
 // Row quantizer API (quantizer.py:31-64 + pack_codes_2d).
 template <int BITS>
 __global__ void quantize_rows_kernel(const uint16_t* __restrict__ x, int rows, int D, int pack, int8_t* codes,
@@ -785,6 +906,42 @@ static int launch_store(const carekv_arena& A, const carekv_store_params& sp, co
   return CAREKV_OK;
 }
 
+// The fp16 tail of a packed KIVI arena as a side-buffer arena under the
+// code-page map of n_packed.
+static carekv_arena kivi_tail_view(const carekv_arena& A) {
+  carekv_arena At = A;
+  At.base_bits = 16;
+  At.scale_mode = 0;
+  At.kcodes = (int8_t*)A.tail_k;
+  At.vcodes = (int8_t*)A.tail_v;
+  At.kivi_packed = 0;
+  At.code_pages = A.tail_pages;
+  At.code_page_off = A.n_packed;
+  return At;
+}
+
+// Both kinds of page of a packed KIVI arena in one slot allocation: the
+// count passes of the prefix and the tail, the scan over all jobs, then the
+// two write passes.
+template <int D>
+static int launch_store_kivi(const carekv_arena& A, const carekv_store_params& sp, const uint16_t* K,
+                             const uint16_t* V, const carekv_page_job* jobs, int n_jobs, const int32_t* group_ptr,
+                             int n_groups, StoreWs ws, hipStream_t s) {
+  const carekv_arena At = kivi_tail_view(A);
+  const int blocks = (n_jobs + 3) / 4;
+  hipLaunchKernelGGL((store_pages_kernel<D, 2, 0>), dim3(blocks), dim3(256), 0, s, A, sp, K, V, jobs, n_jobs, ws);
+  CAREKV_CHECK_LAUNCH("store_pages(count, packed KIVI prefix)");
+  hipLaunchKernelGGL((store_pages_kernel<D, 16, 0>), dim3(blocks), dim3(256), 0, s, At, sp, K, V, jobs, n_jobs, ws);
+  CAREKV_CHECK_LAUNCH("store_pages(count, packed KIVI tail)");
+  hipLaunchKernelGGL(store_scan_kernel, dim3(n_groups), dim3(256), 0, s, A, jobs, group_ptr, ws);
+  CAREKV_CHECK_LAUNCH("store_scan");
+  hipLaunchKernelGGL((store_pages_kernel<D, 2, 1>), dim3(blocks), dim3(256), 0, s, A, sp, K, V, jobs, n_jobs, ws);
+  CAREKV_CHECK_LAUNCH("store_pages(write, packed KIVI prefix)");
+  hipLaunchKernelGGL((store_pages_kernel<D, 16, 1>), dim3(blocks), dim3(256), 0, s, At, sp, K, V, jobs, n_jobs, ws);
+  CAREKV_CHECK_LAUNCH("store_pages(write, packed KIVI tail)");
+  return CAREKV_OK;
+}
+
 extern "C" int carekv_store_pages(const carekv_arena* arena, const carekv_store_params* sp, const uint16_t* K,
                                   const uint16_t* V, const carekv_page_job* jobs_dev, int32_t n_jobs,
                                   const int32_t* group_ptr_dev, int32_t n_groups, void* workspace,
@@ -798,6 +955,13 @@ extern "C" int carekv_store_pages(const carekv_arena* arena, const carekv_store_
   CAREKV_REQUIRE(sp->sketch_proj != nullptr, "sketch_proj is required");
   StoreWs ws{(int32_t*)workspace};
   hipStream_t s = (hipStream_t)stream;
+  if (A.kivi_packed) {
+    CAREKV_REQUIRE(sp->k_hat && sp->v_hat && sp->k_codes_in && sp->v_codes_in && sp->v_scale_in,
+                   "a packed KIVI arena stores from k_hat, v_hat, k_codes_in, v_codes_in and v_scale_in");
+    CAREKV_REQUIRE(!sp->keep_base, "keep_base is built for the uniform packed bases");
+    if (A.head_dim == 64) return launch_store_kivi<64>(A, *sp, K, V, jobs_dev, n_jobs, group_ptr_dev, n_groups, ws, s);
+    return launch_store_kivi<128>(A, *sp, K, V, jobs_dev, n_jobs, group_ptr_dev, n_groups, ws, s);
+  }
   if (A.base_bits == 16) {
     CAREKV_REQUIRE(sp->k_hat && sp->v_hat, "the fp16 base (base_bits=16) needs k_hat and v_hat");
     CAREKV_REQUIRE(!sp->keep_base, "keep_base (streaming store) is built for the packed bases");
@@ -834,8 +998,12 @@ int append_any(const carekv_arena* arena, const uint16_t* k_rows, const uint16_t
                int32_t n_rows, const CodedRows& cr, void* stream) {
   CAREKV_REQUIRE(arena && dest_dev, "null argument");
   if (n_rows <= 0) return CAREKV_OK;
-  const carekv_arena& A = *arena;
-  CAREKV_REQUIRE(check_arena(A), last_error_buf());
+  CAREKV_REQUIRE(check_arena(*arena), last_error_buf());
+  carekv_arena A = *arena;
+  if (A.kivi_packed) {  // decode rows go to the fp16 tail
+    CAREKV_REQUIRE(k_rows && v_rows, "a packed KIVI arena appends fp16 rows");
+    A = kivi_tail_view(*arena);
+  }
   hipStream_t s = (hipStream_t)stream;
   if (A.base_bits == 16) {
     if (A.head_dim == 64)
@@ -864,7 +1032,8 @@ extern "C" int carekv_read_pages(const carekv_arena* arena, int32_t seq, int32_t
   CAREKV_REQUIRE(check_arena(A), last_error_buf());
   CAREKV_REQUIRE(seq >= 0 && seq < A.n_seq && kv_head >= 0 && kv_head < A.n_kv_heads, "seq/kv_head out of range");
   CAREKV_REQUIRE(n_pages >= 0 && (page_ids_dev || n_pages <= A.max_pages), "n_pages out of range");
-  CAREKV_REQUIRE(A.base_bits != 16, "the fp16 base has no codes to read: read its pages directly");
+  CAREKV_REQUIRE(A.base_bits != 16 && !A.kivi_packed,
+                 "the fp16 and packed KIVI bases have no uniform codes to read: use carekv_read_hat_pages");
   if (n_pages == 0) return CAREKV_OK;
   hipStream_t s = (hipStream_t)stream;
   return dispatch_db(A.head_dim, A.base_bits, [&](auto d, auto b) {
@@ -890,6 +1059,48 @@ extern "C" int carekv_quantize_rows(const uint16_t* x, int32_t rows, int32_t D, 
     default: hipLaunchKernelGGL(quantize_rows_kernel<4>, dim3(blocks), dim3(256), 0, s, x, rows, D, pack, codes, scale); break;
   }
   CAREKV_CHECK_LAUNCH("quantize_rows");
+  return CAREKV_OK;
+}
+
+extern "C" int carekv_kivi_codes(const uint16_t* x, int32_t n_mat, int32_t rows, int32_t D, int32_t bits,
+                                 int32_t per_channel, int8_t* codes, uint16_t* scale, void* stream) {
+  CAREKV_REQUIRE(x && codes && scale, "null argument");
+  CAREKV_REQUIRE(bits >= 2 && bits <= 4, "bits must be 2, 3 or 4");
+  CAREKV_REQUIRE(D > 0 && D <= 1024 && n_mat >= 0 && rows >= 0, "bad shape");
+  if (n_mat == 0 || rows == 0) return CAREKV_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (per_channel) {
+    CAREKV_REQUIRE(n_mat <= 65535 * 1024, "too many matrices");
+    hipLaunchKernelGGL(kivi_channel_codes_kernel, dim3(n_mat, (D + 63) / 64), dim3(256), 0, s, x, rows, D, bits,
+                       codes, scale);
+  } else {
+    const long n_rows = (long)n_mat * rows;
+    CAREKV_REQUIRE((n_rows + 3) / 4 <= 0x7fffffffL, "too many rows");
+    hipLaunchKernelGGL(kivi_token_codes_kernel, dim3((unsigned)((n_rows + 3) / 4)), dim3(256), 0, s, x, n_rows, D,
+                       bits, codes, scale);
+  }
+  CAREKV_CHECK_LAUNCH("kivi_codes");
+  return CAREKV_OK;
+}
+
+extern "C" int carekv_read_hat_pages(const carekv_arena* arena, int32_t seq, int32_t kv_head, int32_t n_pages,
+                                     const int32_t* page_ids_dev, const int32_t* row_start_dev, uint16_t* k_hat,
+                                     uint16_t* v_hat, void* stream) {
+  CAREKV_REQUIRE(arena && row_start_dev && k_hat && v_hat, "null argument");
+  const carekv_arena& A = *arena;
+  CAREKV_REQUIRE(check_arena(A), last_error_buf());
+  CAREKV_REQUIRE(A.base_bits == 16 || A.kivi_packed, "carekv_read_hat_pages reads the fp16 and packed KIVI bases");
+  CAREKV_REQUIRE(seq >= 0 && seq < A.n_seq && kv_head >= 0 && kv_head < A.n_kv_heads, "seq/kv_head out of range");
+  CAREKV_REQUIRE(n_pages >= 0 && (page_ids_dev || n_pages <= A.max_pages), "n_pages out of range");
+  if (n_pages == 0) return CAREKV_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (A.head_dim == 64)
+    hipLaunchKernelGGL(read_hat_pages_kernel<64>, dim3(n_pages), dim3(64), 0, s, A, seq, kv_head, n_pages,
+                       page_ids_dev, row_start_dev, k_hat, v_hat);
+  else
+    hipLaunchKernelGGL(read_hat_pages_kernel<128>, dim3(n_pages), dim3(64), 0, s, A, seq, kv_head, n_pages,
+                       page_ids_dev, row_start_dev, k_hat, v_hat);
+  CAREKV_CHECK_LAUNCH("read_hat_pages");
   return CAREKV_OK;
 }
 

@@ -83,6 +83,31 @@ typedef struct carekv_arena {
   uint16_t* open_kscale;
   uint16_t* open_vscale;
   int32_t rescale_open;
+  /* Packed KIVI-style base (no reference counterpart: the reference keeps the
+   * KIVI K_hat / V_hat as fp16 side-buffer pages, cache.py:487-499, 800-865).
+   * kivi_packed = 1 (base_bits 2, scale_mode 0, hat_bits_k = hat_bits_v = 2):
+   * pages 0 .. n_packed[s]-1 of sequence s hold the prompt's full pages as
+   * 2-bit codes, K against one per-channel scale vector per (kv head,
+   * sequence) in kchan (fp16 [n_kv_heads][n_seq][head_dim], the scales of
+   * quant_dequant_kivi_k over the prompt, kivi_helpers.py:35-47), V against
+   * its row's per-token scale (quant_dequant_kivi_v, :50-59), kept in vscale
+   * as fp16 [row][D/group] with every group of a row equal (kscale unused).
+   * The later pages (the prompt's partial last page, the decode rows) are
+   * the fp16 K_hat / V_hat rows of the side-buffer base in tail_k / tail_v,
+   * [n_kv_heads][n_seq][tail_pages][page_size][head_dim]: page p of sequence
+   * s at tail page p - n_packed[s].  kivi_packed = 0: all four unused. */
+  int32_t kivi_packed;
+  const uint16_t* kchan;
+  const int32_t* n_packed;  /* device [n_seq] */
+  uint16_t* tail_k;
+  uint16_t* tail_v;
+  int32_t tail_pages;
+  /* Code-buffer page map of the views the library launches over; callers
+   * set both to 0.  code_pages > 0: kcodes / vcodes / kscale / vscale hold
+   * code_pages pages per (kv head, sequence) and page p of sequence s sits
+   * at code page p - code_page_off[s]. */
+  int32_t code_pages;
+  const int32_t* code_page_off;
 } carekv_arena;
 
 /* Store-time knobs, resolved on the host from CacheConfig and the
@@ -117,6 +142,13 @@ typedef struct carekv_store_params {
   const uint16_t* k_scale_in;
   const int8_t* v_codes_in;
   const uint16_t* v_scale_in;
+  /* Packed KIVI arenas (kivi_packed = 1) take k_hat / v_hat for every job
+   * (the residual base) and k_codes_in / v_codes_in / v_scale_in laid out as
+   * there: a page below n_packed[seq] (set before the call) is written from
+   * the 2-bit codes of carekv_kivi_codes, V with its row's per-token scale
+   * in all D/group entries of the row (k_scale_in unused); a later page goes
+   * to the fp16 tail as the side-buffer base writes it (its codes unused).
+   * Slot ids follow job order across both kinds of page. */
 } carekv_store_params;
 
 /* One page write (prefill).  X rows for page j are X[j*page_size .. +page_size),
@@ -221,6 +253,9 @@ typedef struct carekv_decode_params {
                             * and the queries it corrected (the debug stats
                             * k_slots_read / v_slots_read / n_queries,
                             * attention.py:358-372,944-946)                   */
+  int32_t packed_pages_used; /* kivi_packed arenas: host upper bounds over the */
+  int32_t tail_pages_used;   /* rows of min(n_pages, n_packed) and of
+                              * n_pages - n_packed (ignored otherwise)         */
 } carekv_decode_params;
 
 /* q, out: fp16 [batch][n_heads][head_dim].  The first int32 of the
@@ -309,6 +344,27 @@ int carekv_quantize_rows(const uint16_t* x, int32_t rows, int32_t D, int32_t bit
  * single-row K) gives NaN, as in the reference.  bits 2, 3 or 4; D <= 1024. */
 int carekv_kivi_qdq(const uint16_t* x, int32_t n_mat, int32_t rows, int32_t D, int32_t bits, int32_t per_channel,
                     uint16_t* out, void* stream);
+
+/* No reference counterpart (the reference keeps only the fp16 K_hat / V_hat
+ * of carekv_kivi_qdq): the codes and scales behind them, for the packed KIVI
+ * pages.  codes int8 [n_mat][rows][D], code = clamp(rint(half(x / scale)))
+ * and 0 where that is NaN; scale fp16 [n_mat][D] (per_channel) or
+ * [n_mat][rows], NaN where max|x| = 0 (so that half(code * scale) is
+ * carekv_kivi_qdq's NaN there).  half(code * scale) equals carekv_kivi_qdq
+ * bit for bit up to the sign of zero, except where a nonzero max|x| gives a
+ * scale of 0 in fp16 (max|x| < 2^-25 qmax): there the exact zeros of x
+ * dequantise to 0 instead of NaN. */
+int carekv_kivi_codes(const uint16_t* x, int32_t n_mat, int32_t rows, int32_t D, int32_t bits, int32_t per_channel,
+                      int8_t* codes, uint16_t* scale, void* stream);
+
+/* read_base_hat_concat of the side-buffer base (cache.py:487-499, 800-865)
+ * for base_bits = 16 and packed KIVI arenas: the fp16 K_hat / V_hat rows of
+ * pages page_ids_dev[0..n_pages) (or 0..n_pages-1 when NULL) of (seq,
+ * kv_head), page p's valid rows at k_hat / v_hat rows row_start_dev[p]..
+ * (fp16 [rows][head_dim]); a packed page dequantises half(code * scale). */
+int carekv_read_hat_pages(const carekv_arena* arena, int32_t seq, int32_t kv_head, int32_t n_pages,
+                          const int32_t* page_ids_dev, const int32_t* row_start_dev, uint16_t* k_hat,
+                          uint16_t* v_hat, void* stream);
 
 /* Prefill attention over dequantised K/V: CAREKVLayer._causal_attention_pure
  * (layer.py:935-972) for a batch of sequences, with GQA heads read in place

@@ -136,7 +136,15 @@ def oracle_slice_from_device(cache, seq, kvh, layer=0, **cfg_kw):
     kw.update(cfg_kw)
     oc = OCache(OCfg(**kw), max_slots=cache.n_slots)
     g = lambda t: t[layer, kvh, seq, :P].cpu().numpy()  # noqa: E731
-    if oc.cfg.side_buffer:  # fp16 rows of the side buffer
+    if oc.cfg.side_buffer and getattr(cache, "kivi_packed", False):
+        # the packed KIVI base, read back as the side buffer it stands for
+        kh, vh, lens = cache.read_base_hat_concat(layer, kvh, list(range(P)), seq=seq)
+        kh, vh, r = kh.cpu().numpy(), vh.cpu().numpy(), 0
+        for p, n in enumerate(lens):
+            oc.base_K_hat_fp16[0, 0, p, :n] = kh[r:r + n]
+            oc.base_V_hat_fp16[0, 0, p, :n] = vh[r:r + n]
+            r += n
+    elif oc.cfg.side_buffer:  # fp16 rows of the side buffer
         oc.base_K_hat_fp16[0, 0, :P] = g(cache.kcodes).view(F16)
         oc.base_V_hat_fp16[0, 0, :P] = g(cache.vcodes).view(F16)
     else:

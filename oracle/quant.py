@@ -88,6 +88,29 @@ def kivi_qdq(x, bits: int, per_channel: bool):
     return _rt(q * scale.astype(F32), dt)
 
 
+def kivi_codes(x, bits: int, per_channel: bool):
+    """The packed KIVI form of ``kivi_qdq`` (no reference counterpart; the
+    reference keeps only the dequantised fp16 side buffer): (codes int8 of
+    x's shape, scales of shape (..., 1, D) per channel or (..., T, 1) per
+    token) with the quotient, rint and clamp of ``kivi_qdq`` and a NaN
+    quotient coded 0; a scale whose max |x| is 0 is NaN, so that
+    half(code * scale) reproduces kivi_qdq's NaNs there.  A nonzero max |x|
+    whose scale is 0 in fp16 (below 2^-25 qmax) codes its exact zeros as 0
+    where kivi_qdq gives NaN: that case is left out of the packed form."""
+    x = np.asarray(x)
+    dt = x.dtype
+    qm = float(qmax_of(bits))
+    axis = -2 if per_channel else -1
+    m = np.abs(x).max(axis=axis, keepdims=True)
+    scale = _rt(m.astype(F32) / F32(qm), dt)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        q = _rt(x.astype(F32) / scale.astype(F32), dt)
+    q = np.rint(q.astype(F32))
+    codes = np.where(np.isnan(q), 0, np.clip(q, -qm - 1, qm)).astype(np.int8)
+    scale = np.where(m == 0, np.asarray(np.nan, dtype=dt), scale)
+    return codes, scale
+
+
 def quantize_and_residual(x, bits, group_size):
     """``quantizer.py:85-99``."""
     codes, scale = quantize(x, bits, group_size)

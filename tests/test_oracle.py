@@ -688,3 +688,31 @@ def test_reencoding_append_matches_write_base():
     for t in range(T, T + 20):
         decode_append(z, 0, K[:, t], V[:, t])
     assert np.all(Q.dequantize(z.unpack_rows(z.base_K_codes[0, 0, 2])[:4], z.page_scales(0, 0, 2, "K")[:4], 32) == 0)
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4])
+def test_kivi_codes_dequantise_to_kivi_qdq(bits):
+    """The packed KIVI form (no reference counterpart) against the side
+    buffer the reference keeps: half(code * scale) equals kivi_qdq (pinned
+    by the KIVI decode goldens' K_hat / V_hat) up to the sign of zero, NaN
+    where it is NaN (an all-zero K channel, an all-zero V row, a zero
+    component of a one-row K); the codes lie in [-2^(b-1), 2^(b-1) - 1]."""
+    rng = np.random.default_rng(bits)
+    X = (rng.standard_normal((3, 70, 128)) * np.exp(rng.standard_normal((1, 1, 128)))).astype(np.float16)
+    X[1, :, 5] = 0
+    X[2, 9, :] = 0
+    X[0, 3, 11] = 0
+    qm = 2 ** (bits - 1)
+    cases = [(X, True), (X, False), (X[0, 3:4], True)]
+    for x, per_channel in cases:
+        codes, scale = Q.kivi_codes(x, bits, per_channel)
+        assert codes.min() >= -qm and codes.max() <= qm - 1
+        got = (codes.astype(np.float32) * scale.astype(np.float32)).astype(np.float16)
+        ref = Q.kivi_qdq(x, bits, per_channel)
+        nan = np.isnan(ref)
+        assert np.array_equal(np.isnan(got), nan), per_channel
+        assert np.array_equal(got[~nan], ref[~nan]), per_channel    # +0 == -0
+    # the NaNs come from the all-zero channel / row and the one-row zero, nowhere else
+    assert np.isnan(Q.kivi_qdq(X, bits, True)[1, :, 5]).all()
+    assert np.isnan(Q.kivi_qdq(X, bits, False)[2, 9]).all()
+    assert np.isnan(Q.kivi_qdq(X[0, 3:4], bits, True)[0, 11])
