@@ -19,7 +19,7 @@ from .quantizer import (QuantConfig, KQuantizer, VQuantizer, quantize, dequantiz
 from .residual import ResidualStoreManager, ResidualRouter, pack_4bit, unpack_4bit
 from .attention import (CAREKVAttention, CAREKVMultiHeadAttention, apply_slot_corrections, decode_attention,
                         get_debug_stats, prefill_correction, reset_debug_stats)
-from .prefill import dequantize_rows, prefill_attention, quant_dequant, quantize_rows
+from .prefill import dequantize_rows, prefill_attention, prefill_eval, quant_dequant, quantize_rows
 from .layer import CAREKVLayer
 from .llama_patch import CAREKVHFCache, CAREKVLlamaAttention, patch_llama_model, reset_all_caches
 from .adapter import CAREKVAdapter
@@ -43,6 +43,6 @@ __all__ = [
     "CAREKVLlamaAttention", "patch_llama_model", "reset_all_caches",
     # additions of this build
     "resolve_read_knobs", "resolve_store_knobs", "get_sketch_proj", "kivi_qdq", "kivi_codes",
-    "decode_attention", "prefill_correction", "prefill_attention", "quantize_rows", "dequantize_rows",
+    "decode_attention", "prefill_correction", "prefill_attention", "prefill_eval", "quantize_rows", "dequantize_rows",
     "quant_dequant", "CAREKVAdapter", "CarekvError", "CAREKVHFCache",
 ]

@@ -65,6 +65,12 @@ class PrefillCorrParams(C.Structure):
         [(n, C.c_void_p) for n in ("k_hat", "v_hat", "lse")]
 
 
+class PrefillEvalParams(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("batch", "n_heads", "n_kv_heads", "seq_len", "head_dim")] + \
+        [("ratio", C.c_double)] + [(n, C.c_int32) for n in ("min_residuals", "kind", "v_score_norm", "normalize")] + \
+        [("k_corr_scale", C.c_float), ("diag_cap", C.c_int32)]
+
+
 # page job: int32 x 6 (seq, kv_head, page, num_valid, token_start, is_recent)
 PAGE_JOB_INTS = 6
 
@@ -74,7 +80,7 @@ EXPORTS = ["carekv_store_pages", "carekv_store_workspace_bytes", "carekv_append_
            "carekv_prefill_correct_workspace_bytes", "carekv_decode_attn_static", "carekv_write_base", "carekv_append_coded_rows",
            "carekv_pack_codes", "carekv_unpack_codes", "carekv_pack_4bit", "carekv_unpack_4bit",
            "carekv_quantize_rows_f32", "carekv_dequantize_rows_f32", "carekv_kivi_codes", "carekv_read_hat_pages",
-           "carekv_last_error"]
+           "carekv_prefill_eval", "carekv_last_error"]
 
 # bytes of the per-GPU static workspace of carekv_decode_attn_static
 # (CAREKV_STATIC_SCRATCH_BYTES in include/carekv.h)
@@ -145,6 +151,8 @@ def load(path: str | None = None):
         lib.carekv_kivi_codes.argtypes = [vp, i32, i32, i32, i32, i32, vp, vp, vp]
         lib.carekv_read_hat_pages.restype = C.c_int
         lib.carekv_read_hat_pages.argtypes = [C.POINTER(Arena), i32, i32, i32, vp, vp, vp, vp, vp]
+        lib.carekv_prefill_eval.restype = C.c_int
+        lib.carekv_prefill_eval.argtypes = [C.POINTER(PrefillEvalParams), vp, vp, vp, vp, vp, vp, vp, vp, vp]
         _lib = lib
         return lib
 

@@ -12,14 +12,15 @@ the HIP library:
   mode or over the fp16-scale K_hat / V_hat in the quantised modes
   (``carekv_prefill_attn``, layer.py:759-781), plus the stored-slot sparse
   correction in ``carekv_stored`` mode (``prefill_correction``,
-  ``carekv_prefill_correct``, layer.py:808-838);
+  ``carekv_prefill_correct``, layer.py:808-838) or the in-memory one in
+  ``carekv_eval`` mode (``prefill_eval``, ``carekv_prefill_eval``,
+  layer.py:363-456, 792-806);
 * decode attention with the comb+ex correction is ``decode_attention``
   (``carekv_decode_attn``, layer.py:1148-1160).
 """
 from __future__ import annotations
 
 import os
-import warnings
 from typing import Any, Dict, Optional, Sequence, Tuple
 
 import torch
@@ -29,7 +30,7 @@ from .attention import (decode_attention, decode_read_mode, get_debug_stats, pre
                         reset_debug_stats)
 from .cache import CAREKVCache
 from .config import CacheConfig, any_read_budget, resolve_read_knobs
-from .prefill import prefill_attention, quant_dequant
+from .prefill import eval_knobs, prefill_attention, prefill_eval, quant_dequant
 
 try:  # the reference takes RoPE from transformers as well (layer.py:65-69)
     from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
@@ -38,7 +39,6 @@ except Exception:  # pragma: no cover - transformers missing
 
 F16 = torch.float16
 PREFILL_MODES = ("fp", "base_quant", "carekv_eval", "carekv_stored")
-_warned = set()
 
 
 def resolve_prefill_mode() -> str:
@@ -197,8 +197,8 @@ class CAREKVLayer(nn.Module):
         output is attention over (K_post, V) in ``fp`` mode and over the
         dequantised K_hat / V_hat otherwise; ``carekv_stored`` adds the
         sparse correction from the stored slots (``prefill_correction``,
-        layer.py:808-838).  The in-memory correction of ``carekv_eval`` is
-        not built: that mode returns the base attention and warns once.
+        layer.py:808-838), ``carekv_eval`` the token-level correction from
+        the full in-memory residuals (``prefill_eval``, layer.py:363-456).
 
         A padding mask (left or right padding) keeps each sequence's pad
         rows out of its pages and its attention: those sequences run over
@@ -226,11 +226,6 @@ class CAREKVLayer(nn.Module):
         if mode == "fp":
             O = prefill_attention(Qh, Kh, Vh)
         else:
-            if mode == "carekv_eval" and mode not in _warned:
-                _warned.add(mode)
-                warnings.warn("CAREKV_PREFILL_MODE=carekv_eval: the in-memory prefill correction is not built; "
-                              "the prefill output is the base attention over K_hat / V_hat (carekv_stored and "
-                              "the decode-time correction are built)", RuntimeWarning, stacklevel=2)
             if hats is not None:  # side-buffer base: the K_hat / V_hat the pages hold (layer.py:328-332)
                 Khat, Vhat = (hats[0].unsqueeze(0), hats[1].unsqueeze(0)) if hats[0].dim() == 3 else hats
             else:
@@ -241,6 +236,8 @@ class CAREKVLayer(nn.Module):
                 raise NotImplementedError("carekv_stored prefill correction of a prompt continuation "
                                           "(token_start_abs > 0): the reference scores one prompt at a time")
             O, lse = prefill_attention(Qh, Khat, Vhat, return_lse=True)
+            if mode == "carekv_eval":  # layer.py:792-806: full in-memory residuals
+                O = prefill_eval(Qh, Kh, Vh, Khat, Vhat, O, **eval_knobs(cfg.read_budget_ratio))
             if stored:  # layer.py:808-838: the sparse correction from the stored slots
                 knobs = prefill_read_knobs(cfg, self.layer_id)
                 for b, sq in enumerate(seqs):

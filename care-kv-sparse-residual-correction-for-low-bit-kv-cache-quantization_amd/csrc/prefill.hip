@@ -19,6 +19,8 @@
 //     gfx950 transpose load ds_read_b64_tr_b16 for the same token order.
 // The K tile rows are padded to 2D + 16 bytes and the V tile rows to 2D + 32
 // bytes, which keeps both LDS read patterns free of bank conflicts.
+#include <cmath>
+
 #include "decode_page.h"
 #include "host_util.h"
 
@@ -227,9 +229,279 @@ __global__ void dequantize_rows_kernel(const int8_t* __restrict__ codes, const u
   out[i] = f2h((float)codes[i] * h2f(scale[r * (D / 32) + d / 32]));
 }
 
+// carekv_eval prefill correction (CAREKVLayer._apply_sparse_prefill_correction_eval,
+// layer.py:363-456): one work-group per (row t, query head, sequence).
+//   0. the row's softmax in fp32 over x_j = q.K_hat_j / sqrt(D), j <= t
+//      (max, then the sum of exp(x - max); layer.py:963), as the base
+//      weights a_j = half(exp(x_j - max) / sum) of the reference;
+//   1. every token j <= t of the row, 16 lanes a token (D/16 dims a lane):
+//      q.K_hat_j, q.r_k, ||r_v||^2, ||V_hat_j - o||^2 with r_k =
+//      half(K - K_hat), r_v = half(V - V_hat) (layer.py:770-775); a_j; the V
+//      and K scores to LDS;
+//   2. the final scores (kind, per-kind mean normalisation);
+//   3. the k-th largest score by a bitwise search over the (non-negative)
+//      float bits, then the selected tokens in index order (ties at the k-th
+//      value to the lower indices);
+//   4. dO_V and dO_K over the selected tokens, with the terms recomputed by
+//      the same code as in 1 (same values), summed over the waves in LDS.
+constexpr int kEvalMaxT = 8192;
+
+struct EvalArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const uint16_t* kh;
+  const uint16_t* vh;
+  const uint16_t* o;
+  uint16_t* out;
+  int32_t* diag;
+  int B, Hq, Hkv, T, diag_cap, min_res, kind, v_norm, normalize;
+  double ratio;
+  float k_corr, inv_sqrt_d, sqrt_d;
+};
+
+template <int D>
+__global__ __launch_bounds__(256) void prefill_eval_kernel(EvalArgs a) {
+  constexpr int PL = D / 16;  // dims a lane holds of its token
+  __shared__ float s_v[kEvalMaxT];  // V scores, then the final scores
+  __shared__ int s_k[kEvalMaxT];    // K scores (float bits), then the selected tokens
+  __shared__ float s_red[4][4];
+  __shared__ int s_cnt[2][256];
+  __shared__ float s_acc[4][2][D];
+  const int t = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int hk = h / (a.Hq / a.Hkv);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int c = lane & 15, slot = lane >> 4;  // dims c*PL.., token slot of the wave
+  const int n = t + 1;
+  const long rowoff = (((long)b * a.Hq + h) * a.T + t) * D;
+  const long kvbase = ((long)b * a.Hkv + hk) * a.T * D;
+  float qf[PL], of[PL];
+#pragma unroll
+  for (int i = 0; i < PL; ++i) {
+    qf[i] = h2f(a.q[rowoff + c * PL + i]);
+    of[i] = h2f(a.o[rowoff + c * PL + i]);
+  }
+
+  // the terms of token j (every lane of the 16-lane group ends with the totals)
+  auto terms = [&](int j, float& sq, float& qd, float& rvn2, float& vd2, float (&rv)[PL], float (&vh)[PL]) {
+    const long r = kvbase + (long)j * D + c * PL;
+    sq = qd = rvn2 = vd2 = 0.f;
+#pragma unroll
+    for (int i = 0; i < PL; ++i) {
+      const float kk = h2f(a.k[r + i]), kh = h2f(a.kh[r + i]);
+      const float vv = h2f(a.v[r + i]);
+      vh[i] = h2f(a.vh[r + i]);
+      sq = fmaf(qf[i], kh, sq);
+      const float rk = (float)(_Float16)(kk - kh);
+      qd = fmaf(qf[i], rk, qd);
+      rv[i] = (float)(_Float16)(vv - vh[i]);
+      rvn2 = fmaf(rv[i], rv[i], rvn2);
+      const float dv = vh[i] - of[i];
+      vd2 = fmaf(dv, dv, vd2);
+    }
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) {
+      sq += __shfl_xor(sq, o, 64);
+      qd += __shfl_xor(qd, o, 64);
+      rvn2 += __shfl_xor(rvn2, o, 64);
+      vd2 += __shfl_xor(vd2, o, 64);
+    }
+  };
+
+  // ---- 0. the row's fp32 softmax: max and sum of exp(x - max), x = q.K_hat / sqrt(D)
+  float mx = -INFINITY;
+  for (int j0 = 0; j0 < n; j0 += 16) {
+    const int j = j0 + 4 * w + slot;
+    const bool ok = j < n;
+    const long r = kvbase + (long)(ok ? j : 0) * D + c * PL;
+    float sq = 0.f;
+#pragma unroll
+    for (int i = 0; i < PL; ++i) sq = fmaf(qf[i], h2f(a.kh[r + i]), sq);
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) sq += __shfl_xor(sq, o, 64);
+    if (ok && c == 0) {
+      const float x = sq / a.sqrt_d;
+      s_v[j] = x;
+      mx = fmaxf(mx, x);
+    }
+  }
+  mx = wave_max(mx);
+  if (lane == 0) s_red[0][w] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(s_red[0][0], s_red[0][1]), fmaxf(s_red[0][2], s_red[0][3]));
+  float es = 0.f;
+  for (int j = tid; j < n; j += 256) es += expf(s_v[j] - mx);
+  es = wave_sum(es);
+  if (lane == 0) s_red[1][w] = es;
+  __syncthreads();
+  const float den = ((s_red[1][0] + s_red[1][1]) + s_red[1][2]) + s_red[1][3];
+  // the fp16 base weight (softmax in fp32, cast to fp16)
+  auto weight = [&](float sq) { return (float)(_Float16)(expf(sq / a.sqrt_d - mx) / den); };
+
+  // ---- 1. token scores
+  float vsum = 0.f, ksum = 0.f;
+  for (int j0 = 0; j0 < n; j0 += 16) {
+    const int j = j0 + 4 * w + slot;
+    const bool ok = j < n;
+    float sq, qd, rvn2, vd2, rv[PL], vh[PL];
+    terms(ok ? j : 0, sq, qd, rvn2, vd2, rv, vh);
+    if (ok && c == 0) {
+      const float aw = weight(sq);
+      const float vdiff = sqrtf(vd2), qdot = qd * a.inv_sqrt_d;
+      float vs = aw * sqrtf(rvn2);
+      if (!a.v_norm) vs = vs * vdiff;
+      const float ks = aw * fabsf(qdot) * vdiff;
+      s_v[j] = vs;
+      s_k[j] = __float_as_int(ks);
+      vsum += fabsf(vs);
+      ksum += fabsf(ks);
+    }
+  }
+  vsum = wave_sum(vsum);
+  ksum = wave_sum(ksum);
+  if (lane == 0) { s_red[2][w] = vsum; s_red[3][w] = ksum; }
+  __syncthreads();
+  // ---- 2. final scores
+  {
+    const float vm = fmaxf((((s_red[2][0] + s_red[2][1]) + s_red[2][2]) + s_red[2][3]) / (float)n, 1e-8f);
+    const float km = fmaxf((((s_red[3][0] + s_red[3][1]) + s_red[3][2]) + s_red[3][3]) / (float)n, 1e-8f);
+    for (int j = tid; j < n; j += 256) {
+      const float vs = s_v[j], ks = __int_as_float(s_k[j]);
+      s_v[j] = a.kind == 2 ? vs : a.kind == 1 ? ks : (a.normalize ? vs / vm + ks / km : vs + ks);
+    }
+  }
+  __syncthreads();
+  int K = (int)((double)n * a.ratio);
+  K = min(max(a.min_res, K), n);
+  // block sum of an int (two barriers)
+  auto block_count = [&](int x, int which) -> int {
+    x = (int)wave_sum((float)x);
+    if (lane == 0) s_cnt[which][w] = x;
+    __syncthreads();
+    const int tot = s_cnt[which][0] + s_cnt[which][1] + s_cnt[which][2] + s_cnt[which][3];
+    __syncthreads();
+    return tot;
+  };
+  // ---- 3. the k-th largest score and the selected tokens in index order
+  int nsel = 0;
+  if (K > 0) {
+    uint32_t tau = 0u;
+    for (int bit = 31; bit >= 0; --bit) {
+      const uint32_t cand = tau | (1u << bit);
+      int cnt = 0;
+      for (int j = tid; j < n; j += 256) cnt += __float_as_uint(s_v[j]) >= cand;
+      if (block_count(cnt, 0) >= K) tau = cand;
+    }
+    const int L = (n + 255) / 256, j0 = tid * L, j1 = min(j0 + L, n);
+    int gt = 0, eq = 0;
+    for (int j = j0; j < j1; ++j) {
+      const uint32_t x = __float_as_uint(s_v[j]);
+      gt += x > tau;
+      eq += x == tau;
+    }
+    const int need_eq = K - block_count(gt, 0);
+    s_cnt[0][tid] = eq;
+    __syncthreads();
+    if (tid == 0) {  // exclusive scans: equal tokens before each chunk, then selected tokens
+      int acc = 0;
+      for (int i = 0; i < 256; ++i) { const int e = s_cnt[0][i]; s_cnt[0][i] = acc; acc += e; }
+    }
+    __syncthreads();
+    const int eq_take = min(max(need_eq - s_cnt[0][tid], 0), eq);
+    s_cnt[1][tid] = gt + eq_take;
+    __syncthreads();
+    if (tid == 0) {
+      int acc = 0;
+      for (int i = 0; i < 256; ++i) { const int e = s_cnt[1][i]; s_cnt[1][i] = acc; acc += e; }
+    }
+    __syncthreads();
+    int pos = s_cnt[1][tid], taken = 0;
+    for (int j = j0; j < j1; ++j) {
+      const uint32_t x = __float_as_uint(s_v[j]);
+      if (x > tau || (x == tau && taken < eq_take)) {
+        taken += x == tau;
+        s_k[pos++] = j;  // the K scores are consumed
+      }
+    }
+    nsel = K;
+    __syncthreads();
+  }
+  // ---- 4. corrections over the selected tokens
+  float dv[PL], dk[PL];
+#pragma unroll
+  for (int i = 0; i < PL; ++i) dv[i] = dk[i] = 0.f;
+  for (int i0 = 0; i0 < nsel; i0 += 16) {
+    const int i = i0 + 4 * w + slot;
+    const bool ok = i < nsel;
+    const int j = s_k[ok ? i : 0];
+    float sq, qd, rvn2, vd2, rv[PL], vh[PL];
+    terms(j, sq, qd, rvn2, vd2, rv, vh);
+    if (ok) {
+      const float aw = weight(sq);
+      const float qc = fminf(fmaxf(qd * a.inv_sqrt_d, -2.f), 2.f);
+#pragma unroll
+      for (int p = 0; p < PL; ++p) {
+        dv[p] += aw * rv[p];
+        dk[p] += (aw * qc) * (vh[p] - of[p]);
+      }
+    }
+  }
+#pragma unroll
+  for (int p = 0; p < PL; ++p) {
+    dv[p] += __shfl_xor(dv[p], 16, 64);
+    dv[p] += __shfl_xor(dv[p], 32, 64);
+    dk[p] += __shfl_xor(dk[p], 16, 64);
+    dk[p] += __shfl_xor(dk[p], 32, 64);
+  }
+  if (slot == 0) {
+#pragma unroll
+    for (int p = 0; p < PL; ++p) {
+      s_acc[w][0][c * PL + p] = dv[p];
+      s_acc[w][1][c * PL + p] = dk[p];
+    }
+  }
+  __syncthreads();
+  for (int d = tid; d < D; d += 256) {
+    const float o = h2f(a.o[rowoff + d]);
+    const float tv = a.kind == 1 ? 0.f : ((s_acc[0][0][d] + s_acc[1][0][d]) + s_acc[2][0][d]) + s_acc[3][0][d];
+    const float tk = a.kind == 2 ? 0.f : ((s_acc[0][1][d] + s_acc[1][1][d]) + s_acc[2][1][d]) + s_acc[3][1][d];
+    a.out[rowoff + d] = f2h((o + tv) + a.k_corr * tk);
+  }
+  if (a.diag) {
+    int32_t* dg = a.diag + (((long)b * a.Hq + h) * a.T + t) * a.diag_cap;
+    for (int i = tid; i < a.diag_cap; i += 256) dg[i] = i < nsel ? s_k[i] : -1;
+  }
+}
+
 }  // namespace carekv
 
 using namespace carekv;
+
+extern "C" int carekv_prefill_eval(const carekv_prefill_eval_params* p, const uint16_t* q, const uint16_t* k,
+                                   const uint16_t* v, const uint16_t* k_hat, const uint16_t* v_hat,
+                                   const uint16_t* o_base, uint16_t* out, int32_t* diag, void* stream) {
+  CAREKV_REQUIRE(p && q && k && v && k_hat && v_hat && o_base && out, "null argument");
+  CAREKV_REQUIRE(p->head_dim == 64 || p->head_dim == 128, "head_dim must be 64 or 128");
+  CAREKV_REQUIRE(p->batch > 0 && p->n_heads > 0 && p->n_kv_heads > 0 && p->n_heads % p->n_kv_heads == 0,
+                 "batch and head counts must be positive, n_heads a multiple of n_kv_heads");
+  CAREKV_REQUIRE(p->seq_len > 0 && p->seq_len <= kEvalMaxT, "seq_len must be in 1..8192");
+  CAREKV_REQUIRE(p->ratio >= 0.0 && p->min_residuals >= 0, "ratio and min_residuals must be non-negative");
+  CAREKV_REQUIRE(p->kind >= 0 && p->kind <= 2, "kind must be 0 (both), 1 (k) or 2 (v)");
+  CAREKV_REQUIRE(!diag || p->diag_cap > 0, "diag needs diag_cap > 0");
+  EvalArgs a{};
+  a.q = q; a.k = k; a.v = v; a.kh = k_hat; a.vh = v_hat; a.o = o_base; a.out = out; a.diag = diag;
+  a.B = p->batch; a.Hq = p->n_heads; a.Hkv = p->n_kv_heads; a.T = p->seq_len; a.diag_cap = diag ? p->diag_cap : 0;
+  a.min_res = p->min_residuals; a.kind = p->kind; a.v_norm = p->v_score_norm != 0; a.normalize = p->normalize != 0;
+  a.ratio = p->ratio; a.k_corr = p->k_corr_scale;
+  a.sqrt_d = (float)std::sqrt((double)p->head_dim);
+  a.inv_sqrt_d = (float)(1.0 / std::sqrt((double)p->head_dim));
+  const dim3 grid(p->seq_len, p->n_heads, p->batch);
+  hipStream_t s = (hipStream_t)stream;
+  if (p->head_dim == 128) hipLaunchKernelGGL(prefill_eval_kernel<128>, grid, dim3(256), 0, s, a);
+  else hipLaunchKernelGGL(prefill_eval_kernel<64>, grid, dim3(256), 0, s, a);
+  CAREKV_CHECK_LAUNCH("prefill_eval");
+  return CAREKV_OK;
+}
 
 extern "C" int carekv_prefill_attn(const carekv_prefill_params* pp, const uint16_t* q, const uint16_t* k,
                                    const uint16_t* v, uint16_t* out, float* lse, void* stream) {

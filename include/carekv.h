@@ -384,6 +384,40 @@ typedef struct carekv_prefill_params {
 int carekv_prefill_attn(const carekv_prefill_params* params, const uint16_t* q, const uint16_t* k,
                         const uint16_t* v, uint16_t* out, float* lse, void* stream);
 
+/* Prefill in carekv_eval mode: CAREKVLayer._apply_sparse_prefill_correction_eval
+ * (layer.py:363-456) over the causal base attention, as prefill calls it
+ * (layer.py:792-806).  For every query head h and row t, over the row's
+ * tokens j <= t with a_j the fp16 base weight (the row's softmax of
+ * q.K_hat_j / sqrt(D) in fp32, cast to fp16; layer.py:963), r_k =
+ * half(K - K_hat), r_v = half(V - V_hat):
+ *   v_score = a ||r_v|| ||V_hat_j - o|| (v_score_norm: a ||r_v||),
+ *   k_score = a |q.r_k / sqrt(D)| ||V_hat_j - o||,
+ *   score by kind (both: v + k, or v / mean|v| + k / mean|k| when normalize),
+ *   the top min(max(min_residuals, int((t + 1) ratio)), t + 1) tokens (ties
+ *   to the lower index), and
+ *   out = half(o + sum a r_v + k_corr_scale sum a clamp(q.r_k / sqrt(D),
+ *   -2, 2) (V_hat_j - o)).
+ * q, o_base, out fp16 [batch][n_heads][seq_len][head_dim] (o_base the base
+ * output of carekv_prefill_attn over K_hat / V_hat); k, v (true post-RoPE
+ * rows), k_hat, v_hat fp16
+ * [batch][n_kv_heads][seq_len][head_dim].  diag (optional, diag_cap > 0):
+ * int32 [batch][n_heads][seq_len][diag_cap] the selected token indices,
+ * ascending, -1 padded.  seq_len <= 8192, head_dim 64 or 128. */
+typedef struct carekv_prefill_eval_params {
+  int32_t batch, n_heads, n_kv_heads, seq_len, head_dim;
+  double ratio;           /* CAREKV_PREFILL_RESIDUAL_RATIO (default cfg.read_budget_ratio) */
+  int32_t min_residuals;  /* CAREKV_PREFILL_MIN_RESIDUALS                     */
+  int32_t kind;           /* CAREKV_PREFILL_RESIDUAL_KIND: 0 both, 1 k, 2 v   */
+  int32_t v_score_norm;   /* CAREKV_V_SCORE: 1 norm, 0 output_aware           */
+  int32_t normalize;      /* CAREKV_SCORE_NORMALIZE                           */
+  float k_corr_scale;     /* CAREKV_K_CORRECTION_SCALE                        */
+  int32_t diag_cap;
+} carekv_prefill_eval_params;
+
+int carekv_prefill_eval(const carekv_prefill_eval_params* params, const uint16_t* q, const uint16_t* k,
+                        const uint16_t* v, const uint16_t* k_hat, const uint16_t* v_hat, const uint16_t* o_base,
+                        uint16_t* out, int32_t* diag, void* stream);
+
 /* Prefill-time sparse correction of CAREKVLayer.prefill in carekv_stored
  * mode (layer.py:780-838) with the vectorized correction over all
  * kv_group x T queries of each kv head (layer.py:538-557): for every prompt

@@ -21,6 +21,9 @@ Follows ``attention.py`` of the reference:
   * ``causal_attention_pure``      -- layer.py:935-972 (the prefill
     attention over dequantised K/V, attention_mask=None branch), with the
     GQA heads of layer.py:774-775 read in place.
+  * ``prefill_eval``               -- layer.py:363-456, 792-806 (the
+    carekv_eval prefill: token-level top-k over the full in-memory
+    residuals).
 """
 from __future__ import annotations
 
@@ -519,3 +522,87 @@ def causal_attention_pure(Qh, K, V, causal=True, rows=None):
         out[h] = (A.astype(F32) @ Vf).astype(F16)
         lse[h] = (m[:, 0] + np.log(z[:, 0])).astype(F32)
     return out, lse
+
+
+def prefill_eval(Qh, K, V, K_hat, V_hat, *, ratio, min_residuals=1, kind="both", v_score="output_aware",
+                 normalize=False, k_corr_scale=0.1, diag=None, force_sel=None, o_base=None):
+    """``CAREKVLayer`` prefill in ``carekv_eval`` mode (layer.py:792-806): the
+    causal base attention over K_hat / V_hat (``causal_attention_pure``,
+    fp16 weights A and fp16 O_base), then
+    ``_apply_sparse_prefill_correction_eval`` (layer.py:363-456) per (query
+    head, row t) with the full in-memory residuals r_k = half(K - K_hat),
+    r_v = half(V - V_hat) (layer.py:770-775):
+      n = t + 1, k = min(max(min_residuals, int(n * ratio)), n)
+      v_diff_t = ||V_hat_t - o||, qdot_t = (r_k,t . q) / sqrt(D)
+      v_score = a ||r_v|| v_diff (output_aware) or a ||r_v|| (norm)
+      k_score = a |qdot| v_diff
+      score = v, k, v + k or v / mean|v| + k / mean|k| (clamped 1e-8)
+      top-k tokens (ties to the lower index);
+      dO_V = sum a r_v, dO_K = sum a clamp(qdot, -2, 2) (V_hat - o)
+      out = half(o + dO_V + k_corr_scale dO_K)  (terms of the kind only).
+    Qh (Hq, T, D) fp16 post-RoPE; K, V, K_hat, V_hat (Hkv, T, D) fp16.
+    ``diag`` receives {(h, t): (selected token indices, scores)};
+    ``force_sel`` maps (h, t) to the token indices to use instead of the
+    top-k; ``o_base`` (Hq, T, D) fp16 replaces the base output O (the
+    weights A stay the fp32 softmax cast to fp16), to hold the correction
+    alone to a device whose base attention rounds differently.
+    Returns (T, Hq, D) fp16."""
+    Qh = np.asarray(Qh, F16)
+    Hq, T, D = Qh.shape
+    Hkv = np.asarray(K).shape[0]
+    grp = Hq // Hkv
+    O = causal_attention_pure(Qh, K_hat, V_hat)[0] if o_base is None else np.asarray(o_base, F16)
+    rk = (np.asarray(K, F16).astype(F32) - np.asarray(K_hat, F16).astype(F32)).astype(F16).astype(F32)
+    rv = (np.asarray(V, F16).astype(F32) - np.asarray(V_hat, F16).astype(F32)).astype(F16).astype(F32)
+    Vh = np.asarray(V_hat, F16).astype(F32)
+    Kh = np.asarray(K_hat, F16).astype(F32)
+    scale = F32(1.0 / math.sqrt(D))
+    out = O.astype(F32).copy()
+    mn = np.finfo(F32).min
+    for h in range(Hq):
+        hk = h // grp
+        q = Qh[h].astype(F32)
+        S = (q @ Kh[hk].T) / F32(math.sqrt(D))
+        S = S + np.where(np.arange(T)[None, :] > np.arange(T)[:, None], mn, F32(0)).astype(F32)
+        m = S.max(axis=-1, keepdims=True)
+        e = np.exp(S - m, dtype=F32)
+        A = (e / e.sum(axis=-1, keepdims=True, dtype=F32)).astype(F16).astype(F32)
+        qdot_all = (q @ rk[hk].T) * scale                        # (T rows, T tokens)
+        rvn = np.sqrt((rv[hk] * rv[hk]).sum(-1, dtype=F32))      # (T,)
+        for t in range(T):
+            n = t + 1
+            k = min(max(int(min_residuals), int(n * ratio)), n)
+            if k <= 0:
+                continue
+            a = A[t, :n]
+            o = O[h, t].astype(F32)
+            vdiff = np.sqrt(((Vh[hk, :n] - o[None, :]) ** 2).sum(-1, dtype=F32))
+            vs = a * rvn[:n] if v_score == "norm" else a * rvn[:n] * vdiff
+            qd = qdot_all[t, :n]
+            ks = a * np.abs(qd) * vdiff
+            if kind == "v":
+                sc = vs
+            elif kind == "k":
+                sc = ks
+            elif normalize:
+                vm = max(float(np.abs(vs).mean(dtype=F32)), 1e-8)
+                km = max(float(np.abs(ks).mean(dtype=F32)), 1e-8)
+                sc = vs / F32(vm) + ks / F32(km)
+            else:
+                sc = vs + ks
+            if force_sel is not None and (h, t) in force_sel:
+                idx = force_sel[(h, t)]
+            else:
+                idx = np.argsort(-sc, kind="stable")[:k]  # ties to the lower index
+            idx = np.sort(np.asarray(idx, dtype=np.int64))
+            if diag is not None:
+                diag[(h, t)] = (idx, sc)
+            a_s = a[idx]
+            dv = (a_s[:, None] * rv[hk, idx]).sum(0, dtype=F32) if kind in ("v", "both") else np.zeros(D, F32)
+            if kind in ("k", "both"):
+                qc = np.clip(qd[idx], -2.0, 2.0)
+                dk = ((a_s * qc)[:, None] * (Vh[hk, idx] - o[None, :])).sum(0, dtype=F32)
+            else:
+                dk = np.zeros(D, F32)
+            out[h, t] = o + dv + F32(k_corr_scale) * dk
+    return out.astype(F16).transpose(1, 0, 2)

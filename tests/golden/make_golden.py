@@ -353,6 +353,39 @@ def golden_prefill_cached(ck):
                   read_k=3, read_v=3, k_mode="linear", policy="separate", impl="cached", kscore_live=1)
 
 
+def golden_prefill_eval(ck):
+    """CAREKVLayer.prefill in carekv_eval mode (layer.py:792-806, 363-456):
+    the causal base attention over the prefill's K_hat / V_hat, then the
+    per-(head, row) top-k correction from the full in-memory residuals.
+    Two knob sets: both kinds normalised with the output-aware V score, and
+    the K kind alone with a larger residual ratio."""
+    cases = (("eval_gqa4_d64", dict(Hq=8, Hkv=2, D=64, T=90, seed=41, outlier_mult=8.0),
+              dict(CAREKV_PREFILL_RESIDUAL_RATIO="0.05", CAREKV_PREFILL_MIN_RESIDUALS="1",
+                   CAREKV_PREFILL_RESIDUAL_KIND="both", CAREKV_V_SCORE="output_aware", CAREKV_SCORE_NORMALIZE="1",
+                   CAREKV_K_CORRECTION_SCALE="0.1")),
+             ("eval_mha_d128_k", dict(Hq=2, Hkv=2, D=128, T=70, seed=42, outlier_mult=10.0),
+              dict(CAREKV_PREFILL_RESIDUAL_RATIO="0.1", CAREKV_PREFILL_MIN_RESIDUALS="2",
+                   CAREKV_PREFILL_RESIDUAL_KIND="k", CAREKV_V_SCORE="norm", CAREKV_SCORE_NORMALIZE="0",
+                   CAREKV_K_CORRECTION_SCALE="0.3")))
+    for name, shape, env in cases:
+        Hq, Hkv, D, T = shape["Hq"], shape["Hkv"], shape["D"], shape["T"]
+        _set_env(CAREKV_PREFILL_MODE="carekv_eval", CAREKV_DEBUG_STATS="0", **env)
+        K, V = _gen_kv(shape["seed"], Hkv, T, D, outlier_mult=shape["outlier_mult"])
+        Q = torch.randn(T, Hq, D, generator=torch.Generator().manual_seed(shape["seed"] + 200)).half()
+        hidden = torch.cat([Q.reshape(T, -1), K.permute(1, 0, 2).reshape(T, -1), V.permute(1, 0, 2).reshape(T, -1)], 1)
+        cfg = ck.CacheConfig(num_layers=1, num_heads=Hq, num_kv_heads=Hkv, head_dim=D, page_size=16,
+                             max_pages=T // 16 + 4, base_bits=3, group_size=32, k_channel_group=32, v_token_block=4,
+                             sketch_dim=32, packed_base=True, scale_quant="int8", read_budget_ratio=0.0,
+                             store_budget_mode="ratio", store_budget_ratio=0.03)
+        cache = ck.CAREKVCache(cfg, torch.device("cpu"))
+        o = _selector_layer(ck, cfg).prefill(cache, hidden)
+        d = dict(K=K.numpy(), V=V.numpy(), Q=Q.numpy(), O=o[:, :Hq * D].reshape(T, Hq, D).numpy(), T=np.array(T),
+                 **{k.lower(): np.array(v) for k, v in env.items()})
+        np.savez_compressed(os.path.join(HERE, f"prefill_{name}.npz"), **d)
+    _set_env(CAREKV_PREFILL_MODE="fp", CAREKV_PREFILL_RESIDUAL_KIND="both", CAREKV_SCORE_NORMALIZE="1",
+             CAREKV_K_CORRECTION_SCALE="0.1")
+
+
 def _decode_step_case(ck, name, *, Hq, Hkv, D, T, n_append, seed, outlier_mult, store, read_k, read_v, k_mode,
                       policy):
     """The reference's decode_step with its correction gate open
@@ -555,7 +588,7 @@ def golden_activation_slices():
 
 
 PARTS = ("activations", "sketch", "store", "append", "decode", "decode_proxy", "decode_kivi", "prefill", "route",
-         "fixture", "prefill_cached", "decode_step")
+         "fixture", "prefill_cached", "decode_step", "prefill_eval")
 
 if __name__ == "__main__":
     # CAREKV_GOLDEN_PARTS=decode_proxy,... writes only those fixtures
@@ -570,7 +603,8 @@ if __name__ == "__main__":
         fns = dict(sketch=golden_sketch, store=golden_store, append=golden_append, decode=golden_decode,
                    decode_proxy=golden_decode_proxy, decode_kivi=golden_decode_kivi, prefill=golden_prefill,
                    route=golden_route, fixture=golden_reference_fixture,
-                   prefill_cached=golden_prefill_cached, decode_step=golden_decode_step)
+                   prefill_cached=golden_prefill_cached, decode_step=golden_decode_step,
+                   prefill_eval=golden_prefill_eval)
         for p in parts:
             if p in fns:
                 fns[p](ck)

@@ -98,3 +98,33 @@ def build_oracle_case(g, name):
     for t in range(T, T + n_app):
         decode_append(c, 0, g["K"][:, t], g["V"][:, t])
     return c, spec
+
+
+# prefill carekv_eval golden cases (tests/golden/make_golden.py:golden_prefill_eval)
+EVAL_CASES = {
+    "eval_gqa4_d64": dict(Hq=8, Hkv=2, D=64),
+    "eval_mha_d128_k": dict(Hq=2, Hkv=2, D=128),
+}
+
+
+def eval_knobs(g):
+    """prefill_eval knobs of a carekv_eval golden (the env it was written under)."""
+    return dict(ratio=float(g["carekv_prefill_residual_ratio"]),
+                min_residuals=int(g["carekv_prefill_min_residuals"]),
+                kind=str(g["carekv_prefill_residual_kind"]), v_score=str(g["carekv_v_score"]),
+                normalize=str(g["carekv_score_normalize"]) == "1",
+                k_corr_scale=float(g["carekv_k_correction_scale"]))
+
+
+def eval_hats(g, spec):
+    """The page writer's K_hat / V_hat of a carekv_eval golden's prompt."""
+    T = int(g["T"])
+    c = OCache(OCfg(num_layers=1, num_heads=spec["Hq"], num_kv_heads=spec["Hkv"], head_dim=spec["D"], page_size=16,
+                    max_pages=T // 16 + 4, base_bits=3, group_size=32, k_channel_group=32, v_token_block=4,
+                    sketch_dim=32, store_budget_mode="ratio", store_budget_ratio=0.03))
+    kh, vh = [], []
+    for h in range(spec["Hkv"]):
+        a, b = write_pages_for_kv_head(c, 0, h, g["K"][h, :T], g["V"][h, :T], token_start_abs=0, sink_tokens=4)
+        kh.append(a)
+        vh.append(b)
+    return np.stack(kh), np.stack(vh)

@@ -46,7 +46,8 @@ def test_c_structs_match_header_layout():
     _lib = _ensure_built()
     hdr = open(os.path.join(ROOT, "include", "carekv.h")).read()
     for cname, py in (("carekv_arena", _lib.Arena), ("carekv_store_params", _lib.StoreParams),
-                      ("carekv_decode_params", _lib.DecodeParams), ("carekv_prefill_params", _lib.PrefillParams)):
+                      ("carekv_decode_params", _lib.DecodeParams), ("carekv_prefill_params", _lib.PrefillParams),
+                      ("carekv_prefill_eval_params", _lib.PrefillEvalParams)):
         assert [f[0] for f in py._fields_] == _struct_fields(hdr, cname), cname
 
 
@@ -280,3 +281,37 @@ def test_patched_model_makes_a_carekv_hf_cache(monkeypatch):
         assert model(ids, use_cache=False).past_key_values is None
     with pytest.raises(NotImplementedError):
         pkv.crop(-1)
+
+
+def test_prefill_eval_knobs_match_reference(monkeypatch):
+    """carekv_eval knobs (layer.py:375-393): defaults, the read budget ratio
+    as the ratio's default, errors on unknown kinds; the entry point refuses
+    rows past its LDS score buffer before any launch."""
+    import ctypes as C
+    from care_kv import prefill
+    _lib = _ensure_built()
+    for k in ("CAREKV_PREFILL_RESIDUAL_RATIO", "CAREKV_PREFILL_MIN_RESIDUALS", "CAREKV_PREFILL_RESIDUAL_KIND",
+              "CAREKV_V_SCORE", "CAREKV_SCORE_NORMALIZE", "CAREKV_K_CORRECTION_SCALE"):
+        monkeypatch.delenv(k, raising=False)
+    assert prefill.eval_knobs(0.07) == dict(ratio=0.07, min_residuals=1, kind="both", v_score="output_aware",
+                                            normalize=False, k_corr_scale=0.1)
+    monkeypatch.setenv("CAREKV_PREFILL_RESIDUAL_KIND", "V")
+    monkeypatch.setenv("CAREKV_SCORE_NORMALIZE", "1")
+    monkeypatch.setenv("CAREKV_PREFILL_RESIDUAL_RATIO", "0.2")
+    kn = prefill.eval_knobs(0.07)
+    assert (kn["kind"], kn["normalize"], kn["ratio"]) == ("v", True, 0.2)
+    monkeypatch.setenv("CAREKV_PREFILL_RESIDUAL_KIND", "kv")
+    with pytest.raises(ValueError):
+        prefill.eval_knobs(0.0)
+    monkeypatch.setenv("CAREKV_PREFILL_RESIDUAL_KIND", "both")
+    monkeypatch.setenv("CAREKV_V_SCORE", "l2")
+    with pytest.raises(ValueError):
+        prefill.eval_knobs(0.0)
+    lib = _lib.load()
+    pp = _lib.PrefillEvalParams(batch=1, n_heads=2, n_kv_heads=2, seq_len=8193, head_dim=64, ratio=0.1,
+                                min_residuals=1, kind=0, v_score_norm=0, normalize=0, k_corr_scale=0.1)
+    fake = [C.c_void_p(4096)] * 7  # never dereferenced: the checks fail first
+    assert lib.carekv_prefill_eval(pp, *fake, None, None) != 0
+    assert b"seq_len" in lib.carekv_last_error()
+    pp.seq_len, pp.n_kv_heads = 100, 3
+    assert lib.carekv_prefill_eval(pp, *fake, None, None) != 0

@@ -716,3 +716,28 @@ def test_kivi_codes_dequantise_to_kivi_qdq(bits):
     assert np.isnan(Q.kivi_qdq(X, bits, True)[1, :, 5]).all()
     assert np.isnan(Q.kivi_qdq(X, bits, False)[2, 9]).all()
     assert np.isnan(Q.kivi_qdq(X[0, 3:4], bits, True)[0, 11])
+
+
+@pytest.mark.parametrize("name", ["eval_gqa4_d64", "eval_mha_d128_k"])
+def test_prefill_eval_golden(golden, name):
+    """CAREKVLayer.prefill in carekv_eval mode (layer.py:792-806, 363-456)
+    against the reference's output: the token-level top-k correction from
+    the in-memory residuals over the causal fp16 base.  The base differs
+    from torch's fp16 einsum by fp32 summation order (one fp16 rounding on
+    a fraction of the outputs), which can also move a score by that much."""
+    from helpers import EVAL_CASES, eval_hats, eval_knobs
+    from oracle.attention import prefill_eval
+    g = golden(f"prefill_{name}.npz")
+    spec = EVAL_CASES[name]
+    Kh, Vh = eval_hats(g, spec)
+    T = int(g["T"])
+    out = prefill_eval(g["Q"].transpose(1, 0, 2), g["K"][:, :T], g["V"][:, :T], Kh, Vh, **eval_knobs(g))
+    ref = g["O"]
+    err = np.abs(out.astype(F32) - ref.astype(F32))
+    ulp = np.spacing(np.maximum(np.abs(ref), np.abs(out)).astype(F16)).astype(F32)
+    assert np.all(err <= np.maximum(2 * ulp, 5e-4)), (err.max(), np.unravel_index(err.argmax(), err.shape))
+    assert np.mean(err > 0) < 2e-2, np.mean(err > 0)
+    # the correction changed the output (it is not the base)
+    from oracle.attention import causal_attention_pure
+    base, _ = causal_attention_pure(g["Q"].transpose(1, 0, 2), Kh, Vh)
+    assert np.abs(base.transpose(1, 0, 2).astype(F32) - ref.astype(F32)).max() > 1e-2
