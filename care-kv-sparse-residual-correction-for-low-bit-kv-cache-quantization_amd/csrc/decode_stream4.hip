@@ -48,9 +48,11 @@
 namespace carekv {
 
 // One window's share of a lane: the K side (K rows and scales; reloaded for
-// the next window once the window's PV is done, so the records and the next
-// window's top cover the latency) and the V side (fetched a whole window
-// ahead).  The register cap of 4 waves per SIMD holds with both in flight.
+// the next window as soon as the S step has consumed them, so the softmax,
+// the records and the PV step cover the latency) and the V side (fetched a
+// whole window ahead).  The register cap of 4 waves per SIMD holds with both
+// in flight because the records run before the PV step, so that their
+// registers (the weights, the residual rows) are free during it.
 template <int D, int BITS, int SM>
 struct WinK {
   static constexpr int RB = row_bytes(D, BITS), NWR = RB / 4, NCG = D / 32;
@@ -235,12 +237,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
 
   // Load schedule of a window (one register set per buffer): this
   // window's first K residual rows at the top; the next window's K rows and
-  // metadata once the S step has consumed the K registers; the next
+  // metadata right after the S step has consumed the K registers; the next
   // window's V codes page by page as the PV step consumes them, its V
   // scales once they are in LDS.  The loads complete in issue order, so
-  // the records wait for nothing issued after the top, the next window's S
-  // step for nothing issued during the PV step, and every load has most of
-  // a window to land.
+  // the records wait for nothing issued after the top, and the next
+  // window's S step has the softmax, the records and the PV step of this
+  // one to wait through.
   int p0 = p_begin + 4 * w;
   int meta_nx = 0;
   WV cv;
@@ -333,6 +335,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
       }
     }
 
+    load_k(p0 + 16);  // the next window's K rows and metadata, while this window runs
+    meta_nx = load_meta(p0 + 16);
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- online softmax over the window (lane: tokens 4*sbk+i of page lj, query sc)
@@ -398,44 +402,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     }
 
     __builtin_amdgcn_sched_barrier(0);
-    // ---- O += P V_hat, page by page
-#pragma unroll
-    for (int pi = 0; pi < 4; ++pi) {
-      const bool live = nvp[pi] > 0;
-      if (live) {
-        uint32_t vp[CH / 2];
-#pragma unroll
-        for (int i = 0; i < CH / 2; ++i) {
-          if constexpr (KV) {  // exact signed codes: no offset to take back
-            const half2_t c = code_pair<BITS, CH, BITS>(cv.vw[pi], i);
-            vp[i] = h2bits(c);
-          } else {
-            vp[i] = code_pair_sub<BITS, CH, BITS>(cv.vw[pi], i);
-          }
-        }
-        vtile_write_raw<D, BITS>(vt, vp, ln, lj);
-      }
-      load_vpage(cv, p0 + 16, pi);  // the next window's page pi into the registers just consumed
-      if (!live) continue;
-      lds_sync_wave();
-#pragma unroll
-      for (int h = 0; h < D / 64; ++h) {
-        uint2 pg[4];  // P'[query sc][tokens g, g+4, g+8, g+12] of page pi, the lane's group
-        pwg_load<NCG>(s_pw[w], pi, 2 * h + (lane >> 5), sc, pg);
-#pragma unroll
-        for (int g = 0; g < 4; ++g) pv4_step<D, BITS>(vt, g, h, pg[g].x, pg[g].y, oacc[h], lane);
-        if constexpr (KV) {
-          pwg_load<NCG>(s_pwl[w], pi, 2 * h + (lane >> 5), sc, pg);
-#pragma unroll
-          for (int g = 0; g < 4; ++g) pv4_step<D, BITS>(vt, g, h, pg[g].x, pg[g].y, oacc[h], lane);
-        }
-      }
-      lds_sync_wave();
-    }
-    load_k(p0 + 16);  // the next window's K rows and metadata
-    meta_nx = load_meta(p0 + 16);
-    __builtin_amdgcn_sched_barrier(0);
-    if (!corr) continue;
+    if (corr) {
     // ---- page records: m_ref, K-slot moments, V-block masses (this lane:
     // page lj, query sc; the lanes with sbk == 0 write)
     const int my_page = p0 + lj;
@@ -471,6 +438,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
       if (r == 0) {
         rw[0] = rw0[0]; rw[1] = rw0[1]; rw[2] = rw0[2]; rw[3] = rw0[3];
         kscr = ksc0;
+        // the scale is read here, not at the top of the window where its load
+        // was just issued (a conversion there would wait for it)
+        asm volatile("" : "+v"(kscr));
       } else {
         const int slotr = __shfl(cmeta, (lane & 48) + 2 + cgr, 64);
         const uint32_t soff = has ? (uint32_t)slotr : 0u;  // lanes without a slot read slot 0 and drop it
@@ -519,6 +489,42 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
       if (vrank < a.v_cap)
         __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint((e[0] + e[1]) + (e[2] + e[3])), rs_ws,
                                               vo_rec + (uint32_t)vrank * 4u, so_rp + (uint32_t)(2 + 4 * a.k_cap) * 4u, 0);
+    }
+    }  // records
+    __builtin_amdgcn_sched_barrier(0);
+    // ---- O += P V_hat, page by page
+#pragma unroll
+    for (int pi = 0; pi < 4; ++pi) {
+      const bool live = nvp[pi] > 0;
+      if (live) {
+        uint32_t vp[CH / 2];
+#pragma unroll
+        for (int i = 0; i < CH / 2; ++i) {
+          if constexpr (KV) {  // exact signed codes: no offset to take back
+            const half2_t c = code_pair<BITS, CH, BITS>(cv.vw[pi], i);
+            vp[i] = h2bits(c);
+          } else {
+            vp[i] = code_pair_sub<BITS, CH, BITS>(cv.vw[pi], i);
+          }
+        }
+        vtile_write_raw<D, BITS>(vt, vp, ln, lj);
+      }
+      load_vpage(cv, p0 + 16, pi);  // the next window's page pi into the registers just consumed
+      if (!live) continue;
+      lds_sync_wave();
+#pragma unroll
+      for (int h = 0; h < D / 64; ++h) {
+        uint2 pg[4];  // P'[query sc][tokens g, g+4, g+8, g+12] of page pi, the lane's group
+        pwg_load<NCG>(s_pw[w], pi, 2 * h + (lane >> 5), sc, pg);
+#pragma unroll
+        for (int g = 0; g < 4; ++g) pv4_step<D, BITS>(vt, g, h, pg[g].x, pg[g].y, oacc[h], lane);
+        if constexpr (KV) {
+          pwg_load<NCG>(s_pwl[w], pi, 2 * h + (lane >> 5), sc, pg);
+#pragma unroll
+          for (int g = 0; g < 4; ++g) pv4_step<D, BITS>(vt, g, h, pg[g].x, pg[g].y, oacc[h], lane);
+        }
+      }
+      lds_sync_wave();
     }
   }
 

@@ -218,7 +218,6 @@ def test_adapter_patches_a_given_model(monkeypatch):
     a = care_kv.CAREKVAdapter(sk=1, sv=1, rk=2, rv=2)
     for k, v in a.env().items():  # restored after the test
         monkeypatch.setenv(k, v)
-    care_kv.layer._warned.clear()
     m = a.setup_model(_tiny_llama(2))
     ids = torch.randint(0, 1000, (1, 20), generator=torch.Generator().manual_seed(3)).cuda()
     import warnings
