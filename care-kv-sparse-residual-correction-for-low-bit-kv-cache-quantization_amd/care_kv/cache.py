@@ -382,19 +382,29 @@ class CAREKVCache:
             padc = lambda x: torch.nn.functional.pad(x, (0, 0, 0, pad)) if pad else x  # noqa: E731
             kivi_in = (padc(kc).contiguous().view(-1, D), padc(vc).contiguous().view(-1, D),
                        padc(vs.unsqueeze(-1).expand(B, H, T, G)).contiguous().view(-1, G))
-        jobs = np.zeros((B * H * n_new, _lib.PAGE_JOB_INTS), dtype=np.int32)
-        group_ptr = np.zeros(B + 1, dtype=np.int32)
-        j = 0
-        for bi, s in enumerate(seqs):
-            for h in range(H):
-                for p in range(n_new):
-                    pid = self.alloc_page(layer, h, s)
-                    nv = min(ps, T - p * ps)
-                    jobs[j] = (s, h, pid, nv, token_start_abs + p * ps, int(p >= n_new - 4))
-                    self.valid_host[layer, h, s, pid] = nv
-                    self._token_start[layer, h, s, pid] = token_start_abs + p * ps
-                    j += 1
-            group_ptr[bi + 1] = j
+        # page jobs, sequence-major then kv head then page (the reference's
+        # per-head page loop order); each (sequence, kv head) takes the next
+        # n_new page ids of its row at once
+        sarr = np.asarray(seqs, dtype=np.int64)
+        start = self.next_page[layer][:, sarr].T.astype(np.int64)          # (B, H)
+        assert (start + n_new <= cfg.max_pages).all(), "KV cache is full"
+        pr = np.arange(n_new, dtype=np.int64)
+        pids = start[:, :, None] + pr                                        # (B, H, n_new)
+        nv = np.minimum(ps, T - pr * ps)
+        tstart = token_start_abs + pr * ps
+        jobs = np.empty((B, H, n_new, _lib.PAGE_JOB_INTS), dtype=np.int32)
+        jobs[..., 0] = sarr[:, None, None]
+        jobs[..., 1] = np.arange(H)[None, :, None]
+        jobs[..., 2] = pids
+        jobs[..., 3] = nv
+        jobs[..., 4] = tstart
+        jobs[..., 5] = pr >= n_new - 4
+        jobs = jobs.reshape(B * H * n_new, _lib.PAGE_JOB_INTS)
+        hh, ss = np.arange(H)[None, :, None], sarr[:, None, None]
+        self.valid_host[layer, hh, ss, pids] = nv
+        self._token_start[layer, hh, ss, pids] = tstart
+        self.next_page[layer][:, sarr] += n_new
+        group_ptr = (np.arange(B + 1) * (H * n_new)).astype(np.int32)
         jobs_d = torch.from_numpy(jobs).to(self.device, non_blocking=False)
         gp_d = torch.from_numpy(group_ptr).to(self.device)
         knobs = resolve_store_knobs(cfg, layer)
