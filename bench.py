@@ -271,13 +271,12 @@ def prefill_bench(args):
                               store_budget_mode="ratio", store_budget_ratio=0.03, read_budget_ratio=0.0)
     cache = care_kv.CAREKVCache(cfg, device=dev, n_seq=B)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    cache.write_prefill(0, kx[0], vx[0], seqs=[0])  # warm-up (allocations, library load)
+    cache.write_prefill(0, kx, vx, seqs=list(range(B)))  # warm-up (allocations, library load)
     torch.cuda.synchronize()
     cache = care_kv.CAREKVCache(cfg, device=dev, n_seq=B)
     torch.cuda.synchronize()
     e0.record()
-    for b in range(B):
-        cache.write_prefill(0, kx[b], vx[b], seqs=[b])
+    cache.write_prefill(0, kx, vx, seqs=list(range(B)))  # the whole batch in one call, as CAREKVLayer.prefill
     e1.record()
     e1.synchronize()
     store_ms = e0.elapsed_time(e1)

@@ -445,32 +445,54 @@ __global__ __launch_bounds__(256) void store_pages_kernel(carekv_arena A, carekv
 // calls); bases start at next_slot[seq], which is advanced.
 __global__ __launch_bounds__(256) void store_scan_kernel(carekv_arena A, const carekv_page_job* __restrict__ jobs,
                                                          const int32_t* __restrict__ group_ptr, StoreWs ws) {
-  __shared__ int sk[256], sv[256];
+  // chunks of 1024 jobs: 4 consecutive jobs a thread, a wave scan of the
+  // thread totals (shuffles), the 4 wave totals through LDS
+  __shared__ int s_wk[4], s_wv[4];
   __shared__ int carry_k, carry_v;
   const int g = blockIdx.x;
   const int j0 = group_ptr[g], j1 = group_ptr[g + 1];
   if (j1 <= j0) return;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int seq = jobs[j0].seq;
   if (threadIdx.x == 0) { carry_k = A.next_slot[2 * seq]; carry_v = A.next_slot[2 * seq + 1]; }
   __syncthreads();
-  for (int base = j0; base < j1; base += 256) {
-    const int j = base + threadIdx.x;
-    const int ck = j < j1 ? ws.v[j * 4] : 0, cv = j < j1 ? ws.v[j * 4 + 1] : 0;
-    sk[threadIdx.x] = ck; sv[threadIdx.x] = cv;
-    __syncthreads();
-    for (int o = 1; o < 256; o <<= 1) {   // Hillis-Steele inclusive scan
-      const int ak = threadIdx.x >= o ? sk[threadIdx.x - o] : 0;
-      const int av = threadIdx.x >= o ? sv[threadIdx.x - o] : 0;
-      __syncthreads();
-      sk[threadIdx.x] += ak; sv[threadIdx.x] += av;
-      __syncthreads();
+  for (int base = j0; base < j1; base += 1024) {
+    const int jb = base + 4 * threadIdx.x;
+    int ck[4], cv[4], tk = 0, tv = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool ok = jb + i < j1;
+      ck[i] = ok ? ws.v[(jb + i) * 4] : 0;
+      cv[i] = ok ? ws.v[(jb + i) * 4 + 1] : 0;
+      tk += ck[i];
+      tv += cv[i];
     }
-    if (j < j1) {
-      ws.v[j * 4 + 2] = carry_k + sk[threadIdx.x] - ck;
-      ws.v[j * 4 + 3] = carry_v + sv[threadIdx.x] - cv;
+    int ik = tk, iv = tv;  // inclusive scan of the thread totals over the wave
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const int yk = __shfl_up(ik, o, 64), yv = __shfl_up(iv, o, 64);
+      if (lane >= o) { ik += yk; iv += yv; }
     }
+    if (lane == 63) { s_wk[w] = ik; s_wv[w] = iv; }
     __syncthreads();
-    if (threadIdx.x == 255) { carry_k += sk[255]; carry_v += sv[255]; }
+    int off_k = carry_k, off_v = carry_v;  // slots before this thread's first job
+    for (int ww = 0; ww < w; ++ww) { off_k += s_wk[ww]; off_v += s_wv[ww]; }
+    off_k += ik - tk;
+    off_v += iv - tv;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (jb + i < j1) {
+        ws.v[(jb + i) * 4 + 2] = off_k;
+        ws.v[(jb + i) * 4 + 3] = off_v;
+      }
+      off_k += ck[i];
+      off_v += cv[i];
+    }
+    __syncthreads();  // every thread has read the carries and wave totals
+    if (threadIdx.x == 0) {
+      carry_k += ((s_wk[0] + s_wk[1]) + s_wk[2]) + s_wk[3];
+      carry_v += ((s_wv[0] + s_wv[1]) + s_wv[2]) + s_wv[3];
+    }
     __syncthreads();
   }
   if (threadIdx.x == 0) { A.next_slot[2 * seq] = carry_k; A.next_slot[2 * seq + 1] = carry_v; }
