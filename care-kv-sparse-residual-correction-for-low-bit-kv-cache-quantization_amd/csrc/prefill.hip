@@ -131,26 +131,30 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
           s[tt][1] = mfma16x32(ak, qf[1][ks], s[tt][1]);
         }
       }
-      // ---- scale, mask (the wave's diagonal and the end of the sequence)
+      // ---- mask (the wave's diagonal and the end of the sequence), then
+      // the base-2 logits x = s * log2(e)/sqrt(D) folded into the exponent:
+      // max x = c * max s for c > 0 (rounding is monotone), and
+      // exp2(x - m) is taken as exp2(fma(s, c, -m))
       const bool edge = (a.causal && t0 + KT - 1 > qw0) || t0 + KT > T;
+      const float c = a.sm_log2;
       float p[4][2][4];
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
         const int qi = qw0 + 16 * qb + c16;
+        if (edge) {
+#pragma unroll
+          for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int tok = t0 + 16 * tt + 4 * g + i;
+              if (tok >= T || (a.causal && tok > qi)) s[tt][qb][i] = -INFINITY;
+            }
+        }
         float mx = -INFINITY;
 #pragma unroll
         for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            float x = s[tt][qb][i] * a.sm_log2;
-            if (edge) {
-              const int tok = t0 + 16 * tt + 4 * g + i;
-              if (tok >= T || (a.causal && tok > qi)) x = -INFINITY;
-            }
-            p[tt][qb][i] = x;
-            mx = fmaxf(mx, x);
-          }
-        mx = pair32_max(pair16_max(mx));
+          mx = fmaxf(mx, fmaxf(fmaxf(s[tt][qb][0], s[tt][qb][1]), fmaxf(s[tt][qb][2], s[tt][qb][3])));
+        mx = pair32_max(pair16_max(mx)) * c;
         const float m_new = fmaxf(m_run[qb], mx);  // finite: token 0 is visible to every query
         const float f = __builtin_amdgcn_exp2f(m_run[qb] - m_new);
         m_run[qb] = m_new;
@@ -159,7 +163,7 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
         for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float e = __builtin_amdgcn_exp2f(p[tt][qb][i] - m_new);
+            const float e = __builtin_amdgcn_exp2f(fmaf(s[tt][qb][i], c, -m_new));
             p[tt][qb][i] = e;
             ls += e;
           }
