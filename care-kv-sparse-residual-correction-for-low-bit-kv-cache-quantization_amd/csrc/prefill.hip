@@ -86,7 +86,10 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
       const int c = threadIdx.x + 256 * k;
       const int rc = c % (KT * CHR), row = rc / CHR, col = rc % CHR;
       const uint32_t off = ((uint32_t)(j * KT + row) * D + col * 8) * 2;
-      const auto v = __builtin_amdgcn_raw_buffer_load_b128(c < KT * CHR ? rk : rv, off, 0, 0);
+      // chunks 0 .. KT*CHR-1 are K, the rest V: with 256 threads that is
+      // k < NCH / 2, known at compile time (a per-lane choice of resource
+      // would make every load a waterfall loop)
+      const auto v = __builtin_amdgcn_raw_buffer_load_b128(k < NCH / 2 ? rk : rv, off, 0, 0);
       stg[k][0] = v[0]; stg[k][1] = v[1]; stg[k][2] = v[2]; stg[k][3] = v[3];
     }
   };
@@ -95,7 +98,7 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
     for (int k = 0; k < NCH; ++k) {
       const int c = threadIdx.x + 256 * k;
       const int rc = c % (KT * CHR), row = rc / CHR, col = rc % CHR;
-      char* dst = lds + buf * BUF + (c < KT * CHR ? row * KRS : KBUF + row * VRS) + col * 16;
+      char* dst = lds + buf * BUF + (k < NCH / 2 ? row * KRS : KBUF + row * VRS) + col * 16;
       *reinterpret_cast<uint4*>(dst) = make_uint4(stg[k][0], stg[k][1], stg[k][2], stg[k][3]);
     }
   };
@@ -142,12 +145,17 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
       for (int qb = 0; qb < 2; ++qb) {
         const int qi = qw0 + 16 * qb + c16;
         if (edge) {
+          // token 16 tt + i of the lane's rows is t0 + 4g + 16 tt + i; the
+          // limits pass through an empty asm so that the compares stay on
+          // this branch (most tiles are not edge tiles)
+          int lim_t = T - t0 - 4 * g, lim_q = a.causal ? qi - t0 - 4 * g : 0x3fffffff;
+          asm volatile("" : "+v"(lim_t), "+v"(lim_q));
 #pragma unroll
           for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-              const int tok = t0 + 16 * tt + 4 * g + i;
-              if (tok >= T || (a.causal && tok > qi)) s[tt][qb][i] = -INFINITY;
+              const int o = 16 * tt + i;
+              if (o >= lim_t || o > lim_q) s[tt][qb][i] = -INFINITY;
             }
         }
         float mx = -INFINITY;
