@@ -459,18 +459,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
       }
       // moments of u = racc * e over the tokens other than t* (dS = racc *
       // f scales them by f^2), and D* = racc_t*^2
+      // t*'s terms enter as exact zeros (the sums are non-negative, so
+      // adding +0 changes no bit), which keeps the loop free of branches
       float M2 = 0.f, M3 = 0.f, M4 = 0.f, Ds = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        if (i == istar) {
-          Ds = racc[i] * racc[i];
-          continue;
-        }
-        const float u = racc[i] * e[i];
-        const float ue = u * e[i];
+        const bool st = i == istar;
+        const float r2 = racc[i] * racc[i];
+        const float u = st ? 0.f : racc[i] * e[i];
+        const float ue = st ? 0.f : u * e[i];
         M2 = fmaf(u, u, M2);
         M3 = fmaf(ue, u, M3);
         M4 = fmaf(ue, ue, M4);
+        Ds = st ? r2 : Ds;
       }
       M2 = row4_sum(M2); M3 = row4_sum(M3); M4 = row4_sum(M4); Ds = row4_sum(Ds);
       if (has && rec_lane && sbk == 0) {
