@@ -214,7 +214,7 @@ def decode_attention(cache: CAREKVCache, layer: int, q: torch.Tensor, seqs: Opti
     if knobs is None:
         knobs = resolve_read_knobs(cfg, layer)
     q = q.to(torch.float16).contiguous()
-    npages = np.array([cache.num_pages(layer, 0, s) for s in seqs], dtype=np.int32)
+    npages = cache.next_page[layer, 0, np.asarray(seqs, dtype=np.int64)].astype(np.int32)
     if n_pages is not None:
         npages = np.minimum(npages, np.asarray(list(n_pages), dtype=np.int32))
     max_np = int(npages.max()) if B else 0

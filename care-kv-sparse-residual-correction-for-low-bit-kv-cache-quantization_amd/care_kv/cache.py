@@ -458,27 +458,37 @@ class CAREKVCache:
             k, v = k.unsqueeze(0), v.unsqueeze(0)
         B, H, D = k.shape
         seqs = list(range(B)) if seqs is None else list(seqs)
-        dest = np.zeros((B * H, 4), dtype=np.int32)
-        offs = np.zeros(B * H, dtype=np.int64)
-        filled = []  # (seq, kv head, page) the appends fill
-        r = 0
-        for s in seqs:
-            for h in range(H):
-                pid = self.get_open_page(layer, h, s)
-                fresh = 0
-                if pid is None:
-                    if self.kivi_packed and int(self.next_page[layer, h, s]) - int(self.n_packed[s]) >= self.tail_pages:
-                        raise _lib.CarekvError(f"packed KIVI tail full: sequence {s} has no fp16 tail page left "
-                                               f"({self.tail_pages} per sequence, kivi_tail_pages)")
-                    pid = self.alloc_page(layer, h, s)
-                    fresh = 1
-                    self._token_start[layer, h, s, pid] = self.total_valid_tokens(layer, h, s)
-                dest[r] = (s, h, pid, fresh)
-                offs[r] = self.valid_host[layer, h, s, pid]
-                self.valid_host[layer, h, s, pid] += 1
-                if self.valid_host[layer, h, s, pid] == cfg.page_size:
-                    filled.append((s, h, pid))
-                r += 1
+        # the row bookkeeping of every (sequence, kv head) at once: the open
+        # page (the last page while it is not full) or a fresh one
+        ps = cfg.page_size
+        sarr = np.asarray(seqs, dtype=np.int64)
+        hh, ss = np.arange(H)[None, :], sarr[:, None]
+        nxt = self.next_page[layer][:, sarr].T                              # (B, H)
+        vlast = self.valid_host[layer][hh, ss, np.maximum(nxt - 1, 0)]
+        fresh = ~((nxt > 0) & (vlast < ps))
+        if fresh.any():
+            if self.kivi_packed:
+                over = fresh & (nxt - self.n_packed[sarr][:, None] >= self.tail_pages)
+                if over.any():
+                    s_ = int(sarr[np.nonzero(over)[0][0]])
+                    raise _lib.CarekvError(f"packed KIVI tail full: sequence {s_} has no fp16 tail page left "
+                                           f"({self.tail_pages} per sequence, kivi_tail_pages)")
+            assert (nxt[fresh] < cfg.max_pages).all(), "KV cache is full"
+        pid = np.where(fresh, nxt, nxt - 1)
+        if fresh.any():
+            # a fresh page starts at the row's token count (pages past the row's
+            # next page hold no valid rows)
+            tot = self.valid_host[layer][:, sarr, :].sum(-1).T               # (B, H)
+            fb, fh = np.nonzero(fresh)
+            self._token_start[layer, fh, sarr[fb], pid[fb, fh]] = tot[fb, fh]
+            self.next_page[layer][:, sarr] += fresh.T
+        offs = self.valid_host[layer][hh, ss, pid]
+        self.valid_host[layer][hh, ss, pid] = offs + 1
+        dest = np.stack([np.broadcast_to(ss, (B, H)), np.broadcast_to(hh, (B, H)), pid, fresh],
+                        -1).reshape(B * H, 4).astype(np.int32)
+        fb, fh = np.nonzero(offs + 1 == ps)
+        filled = [(int(sarr[b_]), int(h_), int(pid[b_, h_])) for b_, h_ in zip(fb, fh)]  # the pages the appends fill
+        offs = offs.reshape(B * H).astype(np.int64)
         dest_d = torch.from_numpy(dest).to(self.device)
         kk = k.to(F16).contiguous().view(B * H, D)
         vv = v.to(F16).contiguous().view(B * H, D)

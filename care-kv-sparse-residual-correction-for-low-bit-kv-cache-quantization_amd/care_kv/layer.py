@@ -235,7 +235,10 @@ class CAREKVLayer(nn.Module):
             if stored and token_start_abs != 0:
                 raise NotImplementedError("carekv_stored prefill correction of a prompt continuation "
                                           "(token_start_abs > 0): the reference scores one prompt at a time")
-            O, lse = prefill_attention(Qh, Khat, Vhat, return_lse=True)
+            # the stored-slot correction weighs the prompt rows with the base's
+            # log-sum-exp; the other modes need only O
+            O, lse = prefill_attention(Qh, Khat, Vhat, return_lse=True) if stored else \
+                (prefill_attention(Qh, Khat, Vhat), None)
             if mode == "carekv_eval":  # layer.py:792-806: full in-memory residuals
                 O = prefill_eval(Qh, Kh, Vh, Khat, Vhat, O, **eval_knobs(cfg.read_budget_ratio))
             if stored:  # layer.py:808-838: the sparse correction from the stored slots
