@@ -4,9 +4,11 @@
 // optionally, the per-row log-sum-exp from which any weight can be rebuilt.
 //
 // One work-group per (block of 128 queries, query head, sequence), 4 waves of
-// 32 queries.  K and V tiles of 64 tokens are staged in LDS (double
-// buffered, one barrier per tile; the next tile's global loads are in flight
-// while the current one is used):
+// 32 queries, on a one-dimensional grid whose order starts the longest
+// (latest) query blocks of every (sequence, head) first.  K and V tiles of 32
+// tokens are staged in LDS (double buffered, one barrier per tile; the next
+// tile's global loads are in flight while the current one is used); at 160
+// VGPRs and 35 KB of LDS three work-groups share a CU:
 //   * S^T = K_hat Q^T: A = K tile rows (one 16-byte LDS read per lane and
 //     32-dim step), B = Q^T held in registers; lane l receives the scores of
 //     tokens 16tt + 4(l/16) + i for query l % 16 of a 16-query sub-block;
@@ -37,8 +39,9 @@ struct PrefillArgs {
 };
 
 template <int D>
-__global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
-  constexpr int KT = 64;              // tokens per K/V tile
+__global__ __launch_bounds__(256, 3) void prefill_attn_kernel(PrefillArgs a) {
+  constexpr int KT = 32;              // tokens per K/V tile
+  constexpr int TT = KT / 16, NU = KT / 32;
   constexpr int QB = 128;             // queries per work-group
   constexpr int KRS = 2 * D + 16;     // K tile row stride, bytes
   constexpr int VRS = 2 * D + 32;     // V tile row stride, bytes
@@ -51,8 +54,10 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
   typedef short short4_t __attribute__((ext_vector_type(4)));
   typedef __attribute__((address_space(3))) short4_t lds_short4;
 
-  const int qblk = gridDim.x - 1 - blockIdx.x;  // the longest (latest) blocks start first
-  const int h = blockIdx.y, b = blockIdx.z;
+  // the longest (latest) query blocks of every (sequence, head) start first
+  const int nhb = a.Hq * a.B, nqb = gridDim.x / nhb;
+  const int qblk = nqb - 1 - (int)blockIdx.x / nhb, hb = (int)blockIdx.x % nhb;
+  const int h = hb % a.Hq, b = hb / a.Hq;
   const int hk = h / (a.Hq / a.Hkv);
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -121,9 +126,9 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
     const int t0 = j * KT;
     if (!a.causal || t0 <= qw0 + 31) {  // some query of the wave sees this tile
       // ---- S^T = K_hat Q^T
-      float4_t s[4][2];
+      float4_t s[TT][2];
 #pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
+      for (int tt = 0; tt < TT; ++tt) {
         s[tt][0] = float4_t{0.f, 0.f, 0.f, 0.f};
         s[tt][1] = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -140,7 +145,7 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
       // exp2(x - m) is taken as exp2(fma(s, c, -m))
       const bool edge = (a.causal && t0 + KT - 1 > qw0) || t0 + KT > T;
       const float c = a.sm_log2;
-      float p[4][2][4];
+      float p[TT][2][4];
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
         const int qi = qw0 + 16 * qb + c16;
@@ -151,24 +156,27 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
           int lim_t = T - t0 - 4 * g, lim_q = a.causal ? qi - t0 - 4 * g : 0x3fffffff;
           asm volatile("" : "+v"(lim_t), "+v"(lim_q));
 #pragma unroll
-          for (int tt = 0; tt < 4; ++tt)
+          for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               const int o = 16 * tt + i;
               if (o >= lim_t || o > lim_q) s[tt][qb][i] = -INFINITY;
             }
         }
-        float mx = -INFINITY;
+        // a chain of three-operand maxima over the lane's 16 scores
+        float mx = s[0][qb][0];
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt)
-          mx = fmaxf(mx, fmaxf(fmaxf(s[tt][qb][0], s[tt][qb][1]), fmaxf(s[tt][qb][2], s[tt][qb][3])));
+        for (int k = 1; k < 4 * TT; k += 2) {
+          const int k2 = k + 1 < 4 * TT ? k + 1 : k;
+          mx = fmaxf(fmaxf(mx, s[k / 4][qb][k % 4]), s[k2 / 4][qb][k2 % 4]);
+        }
         mx = pair32_max(pair16_max(mx)) * c;
         const float m_new = fmaxf(m_run[qb], mx);  // finite: token 0 is visible to every query
         const float f = __builtin_amdgcn_exp2f(m_run[qb] - m_new);
         m_run[qb] = m_new;
         float ls = 0.f;
 #pragma unroll
-        for (int tt = 0; tt < 4; ++tt)
+        for (int tt = 0; tt < TT; ++tt)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const float e = __builtin_amdgcn_exp2f(fmaf(s[tt][qb][i], c, -m_new));
@@ -183,7 +191,7 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_kernel(PrefillArgs a) {
       }
       // ---- O^T += V_hat^T P^T, 32 tokens per step
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
+      for (int u = 0; u < NU; ++u) {
         half8_t bp[2];
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb)
@@ -528,7 +536,9 @@ extern "C" int carekv_prefill_attn(const carekv_prefill_params* pp, const uint16
   a.q = q; a.k = k; a.v = v; a.out = out; a.lse = lse;
   a.B = pp->batch; a.Hq = pp->n_heads; a.Hkv = pp->n_kv_heads; a.T = pp->seq_len; a.causal = pp->causal != 0;
   a.sm_log2 = pp->sm_scale * 1.4426950408889634f;
-  const dim3 grid((pp->seq_len + 127) / 128, pp->n_heads, pp->batch);
+  const long nblk = (long)((pp->seq_len + 127) / 128) * pp->n_heads * pp->batch;
+  CAREKV_REQUIRE(nblk < (1L << 31), "too many query blocks");
+  const dim3 grid((unsigned)nblk);
   hipStream_t s = (hipStream_t)stream;
   if (pp->head_dim == 128) hipLaunchKernelGGL(prefill_attn_kernel<128>, grid, dim3(256), 0, s, a);
   else hipLaunchKernelGGL(prefill_attn_kernel<64>, grid, dim3(256), 0, s, a);

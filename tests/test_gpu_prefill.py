@@ -80,14 +80,14 @@ def test_prefill_attention_vs_oracle(case):
 
 
 def test_prefill_attention_long_sequence_rows():
-    """T = 4096 (32 query blocks, 64 key tiles): sampled rows at block and
+    """T = 4096 (32 query blocks, 128 key tiles): sampled rows at block and
     tile boundaries against the oracle restricted to those rows."""
     import care_kv
     B, Hq, Hkv, T, D = 1, 2, 1, 4096, 128
     print("prefill long rows T=4096", flush=True)
     q, k, v = _inputs(B, Hq, Hkv, T, D, 99)
     out = care_kv.prefill_attention(q.cuda(), k.cuda(), v.cuda()).cpu().numpy()
-    rows = [0, 1, 63, 64, 127, 128, 2047, 2048, 4032, 4095]
+    rows = [0, 1, 31, 32, 63, 64, 95, 127, 128, 2047, 2048, 4032, 4095]
     ref, _ = causal_attention_pure(q[0].numpy(), k[0].numpy(), v[0].numpy(), rows=rows)
     _check(out[0][:, rows], ref, v[0].numpy())
 
