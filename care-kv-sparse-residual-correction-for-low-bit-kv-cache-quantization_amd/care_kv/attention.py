@@ -22,7 +22,7 @@ import numpy as np
 import torch
 
 from . import _lib
-from .cache import CAREKVCache, get_sketch_proj
+from .cache import CAREKVCache, get_sketch_proj, to_device
 from .config import CacheConfig, ReadKnobs, any_read_budget, resolve_read_knobs
 
 KIND_CODE = {"both": 0, "k": 1, "v": 2}
@@ -222,7 +222,7 @@ def decode_attention(cache: CAREKVCache, layer: int, q: torch.Tensor, seqs: Opti
     key = (tuple(seqs), npages.tobytes())
     meta = cache._row_tables.get(key)
     if meta is None:  # device row table, reused while the batch is unchanged
-        meta = torch.from_numpy(np.stack([np.array(seqs, dtype=np.int32), npages])).to(dev)
+        meta = to_device(np.stack([np.array(seqs, dtype=np.int32), npages]), dev)
         if len(cache._row_tables) > 64:
             cache._row_tables.clear()
         cache._row_tables[key] = meta

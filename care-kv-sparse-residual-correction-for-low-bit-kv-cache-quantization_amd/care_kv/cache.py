@@ -48,6 +48,18 @@ class PageMeta:
     prior_score: float = 0.0
 
 
+def to_device(arr: np.ndarray, device) -> torch.Tensor:
+    """A host array on the device without waiting for the stream: the bytes
+    go through a fresh pinned buffer, which torch's caching host allocator
+    keeps until the asynchronous copy has run.  A pageable copy would wait
+    for every kernel queued before it, so that the host could not run ahead
+    of the GPU in a decode loop."""
+    t = torch.from_numpy(np.ascontiguousarray(arr))
+    if torch.device(device).type != "cuda":
+        return t.to(device)
+    return t.pin_memory().to(device, non_blocking=True)
+
+
 def packed_row_bytes(D: int, bits: int) -> int:
     if bits == 2 and D % 4 == 0:
         return D // 4
@@ -405,8 +417,8 @@ class CAREKVCache:
         self._token_start[layer, hh, ss, pids] = tstart
         self.next_page[layer][:, sarr] += n_new
         group_ptr = (np.arange(B + 1) * (H * n_new)).astype(np.int32)
-        jobs_d = torch.from_numpy(jobs).to(self.device, non_blocking=False)
-        gp_d = torch.from_numpy(group_ptr).to(self.device)
+        jobs_d = to_device(jobs, self.device)
+        gp_d = to_device(group_ptr, self.device)
         knobs = resolve_store_knobs(cfg, layer)
         sp = _lib.StoreParams(k_budget=knobs.k_budget, v_budget=knobs.v_budget, joint_budget=knobs.joint_budget,
                               joint=int(knobs.joint), store_none=int(knobs.store_none),
@@ -489,18 +501,25 @@ class CAREKVCache:
         fb, fh = np.nonzero(offs + 1 == ps)
         filled = [(int(sarr[b_]), int(h_), int(pid[b_, h_])) for b_, h_ in zip(fb, fh)]  # the pages the appends fill
         offs = offs.reshape(B * H).astype(np.int64)
-        dest_d = torch.from_numpy(dest).to(self.device)
+        # one upload: the page destinations (int32 [B*H][4]) and, with the
+        # streaming store, the rows of the open-page buffers (seq, head, offset)
+        # flattened (int64 [B*H])
+        n = B * H
+        buf = np.empty(2 * n + (n if self.streaming_store else 0), dtype=np.int64)
+        buf[:2 * n].view(np.int32)[:] = dest.reshape(-1)
+        if self.streaming_store:
+            buf[2 * n:] = (dest[:, 0].astype(np.int64) * H + dest[:, 1]) * ps + offs
+        buf_d = to_device(buf, self.device)
+        dest_d = buf_d[:2 * n].view(torch.int32)
         kk = k.to(F16).contiguous().view(B * H, D)
         vv = v.to(F16).contiguous().view(B * H, D)
         lib = _lib.load()
         _lib.check(lib.carekv_append_rows(self.arena(layer), kk.data_ptr(), vv.data_ptr(), dest_d.data_ptr(), B * H,
                                           _lib.stream_ptr(self.device)), "carekv_append_rows")
         if self.streaming_store:
-            si = torch.from_numpy(dest[:, 0].astype(np.int64)).to(self.device)
-            hi = torch.from_numpy(dest[:, 1].astype(np.int64)).to(self.device)
-            oi = torch.from_numpy(offs).to(self.device)
-            self.open_k[layer, si, hi, oi] = kk
-            self.open_v[layer, si, hi, oi] = vv
+            rows = buf_d[2 * n:]
+            self.open_k[layer].view(-1, D).index_copy_(0, rows, kk)
+            self.open_v[layer].view(-1, D).index_copy_(0, rows, vv)
             if filled:
                 self._streaming_fill_store(layer, filled)
 
@@ -517,8 +536,8 @@ class CAREKVCache:
         for j, (s, h, pid) in enumerate(filled):
             jobs[j] = (s, h, pid, ps, int(self._token_start[layer, h, s, pid]), 1)
             group_ptr[seqs.index(s) + 1] = j + 1
-        si = torch.tensor([f[0] for f in filled], device=self.device)
-        hi = torch.tensor([f[1] for f in filled], device=self.device)
+        idx = to_device(np.array(filled, dtype=np.int64).T.copy(), self.device)  # (seq, head, page) rows
+        si, hi = idx[0], idx[1]
         Kp = self.open_k[layer, si, hi].contiguous().view(-1, cfg.head_dim)
         Vp = self.open_v[layer, si, hi].contiguous().view(-1, cfg.head_dim)
         knobs = resolve_store_knobs(cfg, layer)
@@ -528,9 +547,9 @@ class CAREKVCache:
                               sketch_proj=self.sketch_proj.data_ptr(), keep_base=0 if self.hat else 1)
         keep = []
         if self.hat:  # the fp16 base: the pages' own K_hat / V_hat rows as the residual base
-            pi = torch.tensor([f[2] for f in filled], device=self.device)
+            pi = idx[2]
             if self.kivi_packed:  # filled pages are tail pages
-                ti = pi - torch.from_numpy(self.n_packed).to(self.device).long()[si]
+                ti = pi - to_device(self.n_packed.astype(np.int64), self.device)[si]
                 Khat = self.tail_k[layer, hi, si, ti].contiguous().view(-1, cfg.head_dim)
                 Vhat = self.tail_v[layer, hi, si, ti].contiguous().view(-1, cfg.head_dim)
                 zc = torch.zeros(Khat.shape, dtype=torch.int8, device=self.device)
@@ -543,8 +562,8 @@ class CAREKVCache:
             sp.k_hat, sp.v_hat = Khat.data_ptr(), Vhat.data_ptr()
         lib = _lib.load()
         ws = self.workspace("store", int(lib.carekv_store_workspace_bytes(len(jobs))))
-        jobs_d = torch.from_numpy(jobs).to(self.device)
-        gp_d = torch.from_numpy(group_ptr).to(self.device)
+        jobs_d = to_device(jobs, self.device)
+        gp_d = to_device(group_ptr, self.device)
         _lib.check(lib.carekv_store_pages(self.arena(layer), sp, Kp.data_ptr(), Vp.data_ptr(), jobs_d.data_ptr(),
                                           len(jobs), gp_d.data_ptr(), len(seqs), ws.data_ptr(),
                                           _lib.stream_ptr(self.device)), "carekv_store_pages (streaming)")
