@@ -329,7 +329,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
     // and the first stored V block (attention.py:540-573, 386-441 with one
     // slot per kind), scored as in the generic loop below
     const bool sens1 = a.sens_d == 1.0;
-#pragma unroll 2
+    // not unrolled: at the 64-VGPR bound of eight waves per SIMD a second
+    // page in flight spills to scratch
+#pragma unroll 1
     for (int p = tid; p < np; p += kBlock) {
       const long pg = pg_base + p;
       const int nv = A.valid[pg];
