@@ -125,7 +125,9 @@ __global__ __launch_bounds__(256, 3) void prefill_attn_kernel(PrefillArgs a) {
     const char* vb = kb + KBUF;
     const int t0 = j * KT;
     if (!a.causal || t0 <= qw0 + 31) {  // some query of the wave sees this tile
-      // ---- S^T = K_hat Q^T
+      // ---- S^T = K_hat Q^T (raised wave priority over the MFMA blocks: a wave
+      // with products to issue goes before the CU's other waves' softmax)
+      __builtin_amdgcn_s_setprio(1);
       float4_t s[TT][2];
 #pragma unroll
       for (int tt = 0; tt < TT; ++tt) {
@@ -139,6 +141,7 @@ __global__ __launch_bounds__(256, 3) void prefill_attn_kernel(PrefillArgs a) {
           s[tt][1] = mfma16x32(ak, qf[1][ks], s[tt][1]);
         }
       }
+      __builtin_amdgcn_s_setprio(0);
       // ---- mask (the wave's diagonal and the end of the sequence), then
       // the base-2 logits x = s * log2(e)/sqrt(D) folded into the exponent:
       // max x = c * max s for c > 0 (rounding is monotone), and
@@ -189,6 +192,7 @@ __global__ __launch_bounds__(256, 3) void prefill_attn_kernel(PrefillArgs a) {
           for (int dt = 0; dt < DT; ++dt) o[qb][dt] *= f;
         }
       }
+      __builtin_amdgcn_s_setprio(1);
       // ---- O^T += V_hat^T P^T, 32 tokens per step
 #pragma unroll
       for (int u = 0; u < NU; ++u) {
@@ -213,6 +217,7 @@ __global__ __launch_bounds__(256, 3) void prefill_attn_kernel(PrefillArgs a) {
         }
       }
     }
+    __builtin_amdgcn_s_setprio(0);
     if (j + 1 < nt) store_tile((j + 1) & 1);
     if (j + 2 < nt) load_tile(j + 2);
     __syncthreads();
