@@ -74,7 +74,8 @@ void decode_apply_kernel(carekv_arena A, DecodeArgs a) {
   __shared__ float s_den[4][16];
   __shared__ BlockScratch bs;
 
-  const int chunk = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  // prefill rows: the latest (longest) rows first
+  const int chunk = blockIdx.x, kvh = blockIdx.y, b = a.pf ? (int)(gridDim.z - 1 - blockIdx.z) : (int)blockIdx.z;
   const int GQ = a.GQ;
   const int bk = b * A.n_kv_heads + kvh;
   const EntryRow er = entry_row(A, a, b);

@@ -60,7 +60,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
   __shared__ int s_blk[4][2][16];  // per wave and window parity: selected V blocks, (4 pi + vb) | slot << 4
   __shared__ BlockScratch bs;
 
-  const int chunk = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  // prefill rows: the latest (longest) rows first
+  const int chunk = blockIdx.x, kvh = blockIdx.y, b = a.pf ? (int)(gridDim.z - 1 - blockIdx.z) : (int)blockIdx.z;
   const int GQ = a.GQ;
   const int bk = b * A.n_kv_heads + kvh;
   const int seq_raw = a.seq_slot[b], np_raw = a.n_pages[b];

@@ -43,7 +43,8 @@ __global__ __launch_bounds__(256) void decode_proxy_kernel(carekv_arena A, Decod
   __shared__ float s_o[16 * D];               // O_base [query][dim]
   __shared__ float s_M[16], s_L[16], s_Mp[16];
 
-  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  // prefill rows: the latest (longest) rows first
+  const int split = blockIdx.x, kvh = blockIdx.y, b = a.pf ? (int)(gridDim.z - 1 - blockIdx.z) : (int)blockIdx.z;
   const int GQ = a.GQ;
   const int bk = b * A.n_kv_heads + kvh;
   const EntryRow er = entry_row(A, a, b);

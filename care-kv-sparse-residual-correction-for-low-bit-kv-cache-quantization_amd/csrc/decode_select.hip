@@ -214,7 +214,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
   __shared__ float s_qs[NCG * 64];  // q_cg P per channel group (sketch proxy)
   extern __shared__ float s_cand[];  // ncand floats when they fit (size set at launch)
   const int GQ = a.GQ;
-  const int win = blockIdx.x / (kXcd * GQ), rem = blockIdx.x % (kXcd * GQ);
+  // prefill rows: the latest (longest) rows first (a window keeps its XCD)
+  const int win_d = blockIdx.x / (kXcd * GQ), rem = blockIdx.x % (kXcd * GQ);
+  const int win = a.pf ? (int)(gridDim.x / (kXcd * GQ)) - 1 - win_d : win_d;
   const int pair = win * kXcd + rem % kXcd, qq = rem / kXcd;
   if (pair >= a.B * A.n_kv_heads) return;
   const int kvh = pair % A.n_kv_heads, b = pair / A.n_kv_heads;

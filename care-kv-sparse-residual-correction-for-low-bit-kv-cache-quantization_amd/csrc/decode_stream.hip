@@ -44,7 +44,8 @@ void decode_stream_kernel(carekv_arena A, DecodeArgs a) {
   __shared__ __align__(16) _Float16 sqr[16 * D];
   __shared__ float s_m[4][16], s_l[4][16];
 
-  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  // prefill rows: the latest (longest) rows first
+  const int split = blockIdx.x, kvh = blockIdx.y, b = a.pf ? (int)(gridDim.z - 1 - blockIdx.z) : (int)blockIdx.z;
   // the call's status word starts clear; the select kernel (a later launch) sets it
   if (((a.split_base + split) | kvh | b) == 0 && threadIdx.x == 0) *a.err_flag = 0;
   const int GQ = a.GQ;

@@ -92,7 +92,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
   __shared__ __align__(16) uint16_t s_pwl[KV ? 4 : 1][KV ? 4 * NCG * 64 : 8];  // KV: their lo halves
   __shared__ __align__(16) uint16_t s_vs[4][4 * NCG * 16];  // per wave: [page][G][token] V scales
 
-  const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  // prefill rows: the latest (longest) rows first
+  const int split = blockIdx.x, kvh = blockIdx.y, b = a.pf ? (int)(gridDim.z - 1 - blockIdx.z) : (int)blockIdx.z;
   // the call's status word starts clear; the select kernel (a later launch) sets it
   if ((split | kvh | b) == 0 && threadIdx.x == 0) *a.err_flag = 0;
   const int GQ = a.GQ;
