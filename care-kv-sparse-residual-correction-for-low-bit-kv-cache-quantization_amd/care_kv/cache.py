@@ -56,7 +56,7 @@ def to_device(arr: np.ndarray, device) -> torch.Tensor:
     of the GPU in a decode loop."""
     t = torch.from_numpy(np.ascontiguousarray(arr))
     if torch.device(device).type != "cuda":
-        return t.to(device)
+        return t.to(device, copy=True)
     return t.pin_memory().to(device, non_blocking=True)
 
 

@@ -315,3 +315,21 @@ def test_prefill_eval_knobs_match_reference(monkeypatch):
     assert b"seq_len" in lib.carekv_last_error()
     pp.seq_len, pp.n_kv_heads = 100, 3
     assert lib.carekv_prefill_eval(pp, *fake, None, None) != 0
+
+
+def test_to_device_host_fallback_copies():
+    """cache.to_device: on a host device a plain copy (the pinned,
+    non-blocking path needs a GPU); dtype and values survive, and the result
+    does not alias the source array (the append reuses its host arrays)."""
+    import numpy as np
+    import torch
+    from care_kv.cache import to_device
+    for dt, view in ((np.int32, True), (np.int64, True), (np.int32, False), (np.int64, False)):
+        a = np.arange(12, dtype=dt).reshape(3, 4)
+        if view:
+            a = a[:, ::2]  # a non-contiguous view
+        t = to_device(a, torch.device("cpu"))
+        assert t.dtype == torch.from_numpy(a.copy()).dtype and t.is_contiguous()
+        assert np.array_equal(t.numpy(), a)
+        a[...] = -1
+        assert not np.array_equal(t.numpy(), a)
