@@ -7,8 +7,8 @@
 // 32 queries, on a one-dimensional grid whose order starts the longest
 // (latest) query blocks of every (sequence, head) first.  K and V tiles of 32
 // tokens are staged in LDS (double buffered, one barrier per tile; the next
-// tile's global loads are in flight while the current one is used); at 160
-// VGPRs and 35 KB of LDS three work-groups share a CU:
+// tile's global loads are in flight while the current one is used); at
+// D = 128, 160 VGPRs and 35 KB of LDS, three work-groups share a CU:
 //   * S^T = K_hat Q^T: A = K tile rows (one 16-byte LDS read per lane and
 //     32-dim step), B = Q^T held in registers; lane l receives the scores of
 //     tokens 16tt + 4(l/16) + i for query l % 16 of a 16-query sub-block;
@@ -20,7 +20,9 @@
 //     the A operand V_hat^T comes from the token-major V tile through the
 //     gfx950 transpose load ds_read_b64_tr_b16 for the same token order.
 // The K tile rows are padded to 2D + 16 bytes and the V tile rows to 2D + 32
-// bytes, which keeps both LDS read patterns free of bank conflicts.
+// bytes, so that each group of consecutive lanes of either LDS read pattern
+// touches every bank once.  (The LDS counters still show conflict cycles, the
+// same for other K paddings, i.e. not from the K reads.)
 #include <cmath>
 
 #include "decode_page.h"
