@@ -21,8 +21,7 @@
 //     gfx950 transpose load ds_read_b64_tr_b16 for the same token order.
 // The K tile rows are padded to 2D + 16 bytes and the V tile rows to 2D + 32
 // bytes, so that each group of consecutive lanes of either LDS read pattern
-// touches every bank once.  (The LDS counters still show conflict cycles, the
-// same for other K paddings, i.e. not from the K reads.)
+// touches every bank once.
 #include <cmath>
 
 #include "decode_page.h"
