@@ -289,12 +289,18 @@ struct EvalArgs {
 template <int D>
 __global__ __launch_bounds__(256) void prefill_eval_kernel(EvalArgs a) {
   constexpr int PL = D / 16;  // dims a lane holds of its token
-  __shared__ float s_v[kEvalMaxT];  // V scores, then the final scores
-  __shared__ int s_k[kEvalMaxT];    // K scores (float bits), then the selected tokens
+  // sized at launch to the prompt (2 T words), so that short prompts fit
+  // more work-groups per CU: [T] V scores, then the final scores; [T] K
+  // scores (float bits), then the selected tokens
+  extern __shared__ float s_dyn[];
+  float* const s_v = s_dyn;
+  int* const s_k = reinterpret_cast<int*>(s_dyn + a.T);
   __shared__ float s_red[4][4];
   __shared__ int s_cnt[2][256];
   __shared__ float s_acc[4][2][D];
-  const int t = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  // a one-dimensional grid, the latest (longest) rows of every (sequence, head) first
+  const int nhb = a.Hq * a.B, hb = (int)blockIdx.x % nhb;
+  const int t = a.T - 1 - (int)blockIdx.x / nhb, h = hb % a.Hq, b = hb / a.Hq;
   const int hk = h / (a.Hq / a.Hkv);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int c = lane & 15, slot = lane >> 4;  // dims c*PL.., token slot of the wave
@@ -521,10 +527,13 @@ extern "C" int carekv_prefill_eval(const carekv_prefill_eval_params* p, const ui
   a.ratio = p->ratio; a.k_corr = p->k_corr_scale;
   a.sqrt_d = (float)std::sqrt((double)p->head_dim);
   a.inv_sqrt_d = (float)(1.0 / std::sqrt((double)p->head_dim));
-  const dim3 grid(p->seq_len, p->n_heads, p->batch);
+  const long nblk = (long)p->seq_len * p->n_heads * p->batch;
+  CAREKV_REQUIRE(nblk < (1L << 31), "too many (row, head, sequence) work-groups");
+  const dim3 grid((unsigned)nblk);
+  const size_t shmem = (size_t)p->seq_len * 2 * sizeof(float);
   hipStream_t s = (hipStream_t)stream;
-  if (p->head_dim == 128) hipLaunchKernelGGL(prefill_eval_kernel<128>, grid, dim3(256), 0, s, a);
-  else hipLaunchKernelGGL(prefill_eval_kernel<64>, grid, dim3(256), 0, s, a);
+  if (p->head_dim == 128) hipLaunchKernelGGL(prefill_eval_kernel<128>, grid, dim3(256), shmem, s, a);
+  else hipLaunchKernelGGL(prefill_eval_kernel<64>, grid, dim3(256), shmem, s, a);
   CAREKV_CHECK_LAUNCH("prefill_eval");
   return CAREKV_OK;
 }
