@@ -219,3 +219,35 @@ def test_prefill_eval_batch_and_layer(monkeypatch):
     O1 = care_kv.prefill_attention(Qh.cuda(), Khat, Vhat)
     ref = care_kv.prefill_eval(Qh.cuda(), K.cuda(), V.cuda(), Khat, Vhat, O1, **knobs)
     assert torch.equal(out, ref)
+
+
+def test_prefill_eval_max_length():
+    """T = 8192, the longest prompt (the score arrays take 64 KiB of dynamic
+    LDS): rows before 512 see only the first 512 tokens, so they equal, bit
+    for bit, a T = 512 run over that prefix, which is itself checked against
+    the oracle; the last rows are finite and select k = max(1, int((t + 1)
+    ratio)) ascending tokens at or before the row."""
+    import care_kv
+    T, n = 8192, 512
+    print(f"carekv_eval max length T={T}", flush=True)
+    Qh, K, V, Kh, Vh = _rand_case(2, 1, 64, T, seed=23)
+    knobs = dict(ratio=0.02, min_residuals=1, kind="both", v_score="output_aware", normalize=False,
+                 k_corr_scale=0.1)
+    d = [torch.from_numpy(np.ascontiguousarray(x)).cuda() for x in (Qh, K, V, Kh, Vh)]
+    O = care_kv.prefill_attention(d[0], d[3], d[4])
+    out, dg = care_kv.prefill_eval(*d, O, diag_cap=200, **knobs)
+    dp = [x[:, :n].contiguous() for x in d]
+    Op = care_kv.prefill_attention(dp[0], dp[3], dp[4])
+    outp, dgp = care_kv.prefill_eval(*dp, Op, diag_cap=200, **knobs)
+    torch.cuda.synchronize()
+    assert torch.equal(O[:, :n], Op)
+    assert torch.equal(out[:, :n], outp) and torch.equal(dg[:, :n], dgp)
+    assert bool(torch.isfinite(out.float()).all())
+    dg = dg.cpu().numpy()
+    for t in (n, 4095, 4096, T - 2, T - 1):
+        k = min(max(1, int((t + 1) * knobs["ratio"])), t + 1)
+        for h in range(2):
+            got = dg[h, t]
+            assert np.all(got[:k] >= 0) and np.all(np.diff(got[:k]) > 0) and got[k - 1] <= t, (h, t)
+            assert np.all(got[k:] == -1), (h, t)
+    _check_against_oracle(Qh[:, :n], K[:, :n], V[:, :n], Kh[:, :n], Vh[:, :n], knobs)
