@@ -5,9 +5,11 @@ the tensors handed to it are not on a HIP device.  There is no fallback.
 """
 from __future__ import annotations
 
+import collections
 import ctypes as C
 import os
 import threading
+import warnings
 
 import torch
 
@@ -31,14 +33,14 @@ class Arena(C.Structure):
         [("open_kscale", C.c_void_p), ("open_vscale", C.c_void_p), ("rescale_open", C.c_int32)] + \
         [("kivi_packed", C.c_int32), ("kchan", C.c_void_p), ("n_packed", C.c_void_p), ("tail_k", C.c_void_p),
          ("tail_v", C.c_void_p), ("tail_pages", C.c_int32), ("code_pages", C.c_int32),
-         ("code_page_off", C.c_void_p)]
+         ("code_page_off", C.c_void_p), ("streaming_store", C.c_int32)]
 
 
 class StoreParams(C.Structure):
     _fields_ = [("k_budget", C.c_int32), ("v_budget", C.c_int32), ("joint_budget", C.c_int32),
                 ("joint", C.c_int32), ("store_none", C.c_int32), ("sensitivity", C.c_double),
                 ("sink_tokens", C.c_int32), ("sketch_proj", C.c_void_p), ("k_hat", C.c_void_p),
-                ("v_hat", C.c_void_p), ("keep_base", C.c_int32), ("k_codes_in", C.c_void_p),
+                ("v_hat", C.c_void_p), ("keep_base", C.c_int32), ("reuse_slots", C.c_int32), ("k_codes_in", C.c_void_p),
                 ("k_scale_in", C.c_void_p), ("v_codes_in", C.c_void_p), ("v_scale_in", C.c_void_p)]
 
 
@@ -177,6 +179,49 @@ def check_status(ws: torch.Tensor, index: int, what: str):
         raise CarekvError(f"{what}: the kernels flagged an overflow (status {flag}): a page holds more stored "
                           "residual slots than the record capacity (k_cap / v_cap), or a slot id fell past the "
                           "arena's n_slots; those slots were left out")
+
+
+class StatusWatch:
+    """Reports the store calls' status words without waiting for the
+    stream: each word is copied to pinned host memory behind an event, and a
+    later call (or ``poll``) warns, once per call site, about a word that was
+    set (slot ids past the arena's n_slots, whose residuals were dropped)."""
+
+    def __init__(self, n: int = 64):
+        self.host = None
+        self.n = n
+        self.pending = collections.deque()  # (host index, event, what)
+        self.next = 0
+        self.warned = set()
+        self.flagged = 0
+
+    def watch(self, ws: torch.Tensor, index: int, what: str):
+        self.poll()
+        if self.host is None:
+            self.host = torch.zeros(self.n, dtype=torch.int32, pin_memory=True)
+        if len(self.pending) == self.n:
+            self.pending[0][1].synchronize()
+            self.poll()
+        i = self.next
+        self.next = (self.next + 1) % self.n
+        self.host[i:i + 1].copy_(ws[4 * index:4 * index + 4].view(torch.int32), non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record()
+        self.pending.append((i, ev, what))
+
+    def poll(self, wait: bool = False) -> int:
+        """Check the landed words (all of them with ``wait``); returns how
+        many set words were seen so far."""
+        while self.pending and (wait or self.pending[0][1].query()):
+            i, ev, what = self.pending.popleft()
+            ev.synchronize()
+            if int(self.host[i]) != 0:
+                self.flagged += 1
+                if what not in self.warned:
+                    self.warned.add(what)
+                    warnings.warn(f"{what}: residual slot ids fell past the arena's n_slots and those slots were "
+                                  "dropped; size the cache with a larger n_slots", RuntimeWarning, stacklevel=3)
+        return self.flagged
 
 
 def ptr(t: torch.Tensor | None) -> int | None:

@@ -254,6 +254,7 @@ class CAREKVCache:
         self._freed: Dict[Tuple[int, int], List[int]] = {}  # (seq, 0 K / 1 V) -> freed slot ids
         self._ws: Dict[str, torch.Tensor] = {}
         self._row_tables: Dict[tuple, torch.Tensor] = {}
+        self.status = _lib.StatusWatch()  # store calls' slot-overflow words, read without a sync
         _lib.load()
 
     # ------------------------------------------------------------ C structs
@@ -275,7 +276,8 @@ class CAREKVCache:
                 scale_mode=self.scale_mode, residual_bits=cfg.residual_bits, n_slots=self.n_slots,
                 hat_bits_k=hat_bits(cfg)[0], hat_bits_v=hat_bits(cfg)[1],
                 open_kscale=g(self.open_ks) if self.rescale_open else None,
-                open_vscale=g(self.open_vs) if self.rescale_open else None, rescale_open=int(self.rescale_open))
+                open_vscale=g(self.open_vs) if self.rescale_open else None, rescale_open=int(self.rescale_open),
+                streaming_store=int(self.streaming_store))
             if self.kivi_packed:
                 a.kivi_packed = 1
                 a.kchan, a.n_packed = g(self.kchan), self.n_packed_d.data_ptr()
@@ -436,6 +438,8 @@ class CAREKVCache:
                    "carekv_store_pages")
         if _lib.check_enabled():
             _lib.check_status(ws, 4 * len(jobs), "carekv_store_pages")
+        else:
+            self.status.watch(ws, 4 * len(jobs), "carekv_store_pages")
         if self.rescale_open:  # the last page stays open: keep its rows' fp16 group scales
             last = T - (n_new - 1) * ps
             if last < ps:
@@ -544,7 +548,8 @@ class CAREKVCache:
         sp = _lib.StoreParams(k_budget=knobs.k_budget, v_budget=knobs.v_budget, joint_budget=knobs.joint_budget,
                               joint=int(knobs.joint), store_none=int(knobs.store_none),
                               sensitivity=knobs.sensitivity, sink_tokens=4,
-                              sketch_proj=self.sketch_proj.data_ptr(), keep_base=0 if self.hat else 1)
+                              sketch_proj=self.sketch_proj.data_ptr(), keep_base=0 if self.hat else 1,
+                              reuse_slots=1)
         keep = []
         if self.hat:  # the fp16 base: the pages' own K_hat / V_hat rows as the residual base
             pi = idx[2]
@@ -569,6 +574,8 @@ class CAREKVCache:
                                           _lib.stream_ptr(self.device)), "carekv_store_pages (streaming)")
         if _lib.check_enabled():
             _lib.check_status(ws, 4 * len(jobs), "carekv_store_pages (streaming)")
+        else:
+            self.status.watch(ws, 4 * len(jobs), "carekv_store_pages (streaming)")
         self.open_k[layer, si, hi] = 0
         self.open_v[layer, si, hi] = 0
 

@@ -113,6 +113,8 @@ class ResidualStoreManager:
                                           _lib.stream_ptr(cache.device)), "carekv_store_pages (process_page)")
         if _lib.check_enabled():
             _lib.check_status(ws, 4, "carekv_store_pages (process_page)")
+        else:
+            cache.status.watch(ws, 4, "carekv_store_pages (process_page)")
         cache.valid_host[self.layer_id, kv_head, seq, page_id] = num_valid
         cache._token_start[self.layer_id, kv_head, seq, page_id] = token_start
         return cache.page_meta(self.layer_id, kv_head, page_id, seq)

@@ -403,7 +403,9 @@ __global__ __launch_bounds__(256) void prefill_eval_kernel(EvalArgs a) {
     }
   }
   __syncthreads();
-  int K = (int)((double)n * a.ratio);
+  // int(n * ratio) (layer.py:397); a ratio of 1 or more keeps all n, so the
+  // conversion only ever sees values below n
+  int K = a.ratio >= 1.0 ? n : (int)((double)n * a.ratio);
   K = min(max(a.min_res, K), n);
   // block sum of an int (two barriers)
   auto block_count = [&](int x, int which) -> int {
@@ -517,6 +519,8 @@ extern "C" int carekv_prefill_eval(const carekv_prefill_eval_params* p, const ui
   CAREKV_REQUIRE(p->batch > 0 && p->n_heads > 0 && p->n_kv_heads > 0 && p->n_heads % p->n_kv_heads == 0,
                  "batch and head counts must be positive, n_heads a multiple of n_kv_heads");
   CAREKV_REQUIRE(p->seq_len > 0 && p->seq_len <= kEvalMaxT, "seq_len must be in 1..8192");
+  // Python's int(n * ratio) raises on an infinite or NaN product (layer.py:397)
+  CAREKV_REQUIRE(std::isfinite(p->ratio), "ratio must be finite");
   CAREKV_REQUIRE(p->ratio >= 0.0 && p->min_residuals >= 0, "ratio and min_residuals must be non-negative");
   CAREKV_REQUIRE(p->kind >= 0 && p->kind <= 2, "kind must be 0 (both), 1 (k) or 2 (v)");
   CAREKV_REQUIRE(!diag || p->diag_cap > 0, "diag needs diag_cap > 0");

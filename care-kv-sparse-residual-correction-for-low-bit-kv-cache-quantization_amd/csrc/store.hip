@@ -366,11 +366,27 @@ __global__ __launch_bounds__(256) void store_pages_kernel(carekv_arena A, carekv
     }
     if (lane < NG) A.k_err[pg * NG + lane] = f2h(kerr[lane]);
     if (lane < kVtb) A.v_err[pg * kVtb + lane] = f2h(verr[lane]);
+    // streaming store: the slot ids the page holds from an earlier store (a
+    // prompt's partial last page) are reused first, so only the rest are
+    // counted for new ids; a page without metadata holds none (its slot
+    // tables are cleared here, before the write pass reads them)
+    int reuse_k = 0, reuse_v = 0;
+    if (sp.reuse_slots) {
+      if (A.has_meta[pg]) {
+#pragma unroll
+        for (int c = 0; c < NG; ++c) reuse_k += A.k_slot[pg * NG + c] >= 0;
+#pragma unroll
+        for (int b = 0; b < kVtb; ++b) reuse_v += A.v_slot[pg * kVtb + b] >= 0;
+      } else {
+        if (lane < NG) A.k_slot[pg * NG + lane] = -1;
+        if (lane < kVtb) A.v_slot[pg * kVtb + lane] = -1;
+      }
+    }
     if (lane == 0) {
       A.valid[pg] = nvld;
       A.has_meta[pg] = 1;
-      ws.v[job_id * 4 + 0] = nk;
-      ws.v[job_id * 4 + 1] = nv;
+      ws.v[job_id * 4 + 0] = nk - min(reuse_k, nk);
+      ws.v[job_id * 4 + 1] = nv - min(reuse_v, nv);
     }
   } else {
     // ---- residual slots at the scanned bases (residual_store.py:424-438)
@@ -383,13 +399,35 @@ __global__ __launch_bounds__(256) void store_pages_kernel(carekv_arena A, carekv
     for (int c = 0; c < NG; ++c) kslot_of[c] = -1;
 #pragma unroll
     for (int b = 0; b < kVtb; ++b) vslot_of[b] = -1;
-    // slot ids past the arena are dropped (never written) and flagged
+    // streaming store: the page's earlier slot ids, ascending, go to the
+    // first selected candidates of their kind (the count pass left them out
+    // of the new ids; a page without metadata had its tables cleared there)
+    int old_k[NG], old_v[kVtb], n_ok = 0, n_ov = 0;
+    if (sp.reuse_slots) {
+#pragma unroll
+      for (int c = 0; c < NG; ++c) {
+        const int id = A.k_slot[pg * NG + c];
+        if (id >= 0) old_k[n_ok++] = id;
+      }
+#pragma unroll
+      for (int b = 0; b < kVtb; ++b) {
+        const int id = A.v_slot[pg * kVtb + b];
+        if (id >= 0) old_v[n_ov++] = id;
+      }
+      for (int i = 1; i < n_ok; ++i)
+        for (int j = i; j > 0 && old_k[j] < old_k[j - 1]; --j) { const int u = old_k[j]; old_k[j] = old_k[j - 1]; old_k[j - 1] = u; }
+      for (int i = 1; i < n_ov; ++i)
+        for (int j = i; j > 0 && old_v[j] < old_v[j - 1]; --j) { const int u = old_v[j]; old_v[j] = old_v[j - 1]; old_v[j - 1] = u; }
+    }
+    // new slot ids past the arena are dropped (never written) and flagged
     for (int i = 0; i < nk; ++i) {
-      if (base_k + i < A.n_slots) kslot_of[sel_k[i]] = base_k + i;
+      if (i < n_ok) kslot_of[sel_k[i]] = old_k[i];
+      else if (base_k + (i - n_ok) < A.n_slots) kslot_of[sel_k[i]] = base_k + (i - n_ok);
       else if (lane == 0) ws.v[n_jobs * 4] = 1;
     }
     for (int i = 0; i < nv; ++i) {
-      if (base_v + i < A.n_slots) vslot_of[sel_v[i]] = base_v + i;
+      if (i < n_ov) vslot_of[sel_v[i]] = old_v[i];
+      else if (base_v + (i - n_ov) < A.n_slots) vslot_of[sel_v[i]] = base_v + (i - n_ov);
       else if (lane == 0) ws.v[n_jobs * 4] = 1;
     }
     // K payload of channel group g: pack_4bit(R_K[:, cg]) over all 16 rows
@@ -583,7 +621,9 @@ __global__ __launch_bounds__(256) void append_hat_rows_kernel(carekv_arena A, co
     vs += h2f(vh) * h2f(vh);
   }
   vs = wave_sum(vs);
-  const bool full = off + 1 == kPage;
+  // the store on fill, unless the caller's streaming store writes the page's
+  // metadata (it reads the slots the page holds)
+  const bool full = off + 1 == kPage && !A.streaming_store;
   if (lane == 0) {
     A.valid[pg] = off + 1;
     if (fresh) A.has_meta[pg] = full ? 1 : 0;
@@ -609,7 +649,10 @@ __global__ __launch_bounds__(256) void append_hat_rows_kernel(carekv_arena A, co
 //     the rows so far and every row's code against it, from the fp16 scales
 //     of the open page kept in open_kscale / open_vscale (this row's are
 //     added there).  When the page fills, its bytes are those write_base
-//     gives the 16 rows.
+//     gives the 16 rows.  A page that holds stored residual slots (a
+//     prompt's partial last page) is not re-encoded: its slots are residuals
+//     against its rows as the prompt wrote them, so it keeps the reference's
+//     fixed-master encoding (the first form) until it fills.
 // The page's sum of V_hat^2 (v_sq, read by the query-aware K score of its
 // stored K slots) is recomputed over the valid rows as they now read back.
 // Coded rows (append_to_page, cache.py:656-701): the caller's int8 codes and
@@ -638,7 +681,14 @@ __global__ __launch_bounds__(256) void append_rows_kernel(carekv_arena A, const 
   const int off = fresh ? 0 : A.valid[pg];
   if (off >= kPage) return;  // caller contract violated; never write past the page
   const bool i8 = A.scale_mode == 1;
-  const bool rescale = i8 && A.rescale_open != 0;
+  // stored slots on the page (only a page with metadata can hold any)
+  bool slots = false;
+  if (!fresh && A.has_meta[pg]) {
+    const int id = lane < NG ? A.k_slot[pg * NG + lane]
+                             : (lane < NG + kVtb ? A.v_slot[pg * kVtb + lane - NG] : -1);
+    slots = __ballot(id >= 0) != 0ull;
+  }
+  const bool rescale = i8 && A.rescale_open != 0 && !slots;
   int cv[32];
   _Float16 sk = (_Float16)0.f, sv = (_Float16)0.f;
   if (lane < NG) {
@@ -725,7 +775,9 @@ __global__ __launch_bounds__(256) void append_rows_kernel(carekv_arena A, const 
     for (int i = 0; i < 32; ++i) { const float x = (float)dq(get_code<BITS>(w, i), s); vs += x * x; }
   }
   vs = wave_sum(vs);
-  const bool full = off + 1 == kPage && !cr.kc;  // the decode step's store on fill
+  // the decode step's store on fill, unless the caller's streaming store
+  // writes the page's metadata (it reads the slots the page holds)
+  const bool full = off + 1 == kPage && !cr.kc && !A.streaming_store;
   if (lane == 0) {
     A.valid[pg] = off + 1;
     if (rescale) { A.kmaster[pg] = half2bits((_Float16)mk); A.vmaster[pg] = half2bits((_Float16)mv); }

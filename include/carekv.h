@@ -108,6 +108,13 @@ typedef struct carekv_arena {
    * at code page p - code_page_off[s]. */
   int32_t code_pages;
   const int32_t* code_page_off;
+  /* streaming_store = 1 (no reference counterpart): the caller runs the
+   * streaming fill store (carekv_store_pages with reuse_slots, and keep_base
+   * on the packed bases) on every page a decode append fills, so
+   * carekv_append_rows leaves such a page's metadata and slots to that store
+   * instead of writing the reference's K_orig = K_hat metadata (no slots;
+   * layer.py:1128-1146).  0: the reference's fill store in the append. */
+  int32_t streaming_store;
 } carekv_arena;
 
 /* Store-time knobs, resolved on the host from CacheConfig and the
@@ -133,6 +140,14 @@ typedef struct carekv_store_params {
                             * reference stores such pages with K_orig = K_hat
                             * (layer.py:1128-1146), which leaves them no slots.
                             * 0: store as the prefill does                    */
+  int32_t reuse_slots;     /* 1: the streaming fill store (no reference
+                            * counterpart): a page's slot ids from an earlier
+                            * store (a prompt's partial last page, metadata
+                            * present) go, ascending, to its first selected
+                            * candidates of their kind before new ids are
+                            * taken; ids it no longer needs stay unused.
+                            * A page without metadata holds none.  0: every
+                            * selected candidate takes a new id             */
   /* process_page on a page carekv_write_base wrote (packed bases;
    * residual_store.py:239-464 with its K_codes / K_scale / V_codes / V_scale
    * arguments): int8 [n_jobs*page_size][head_dim] unpacked codes and fp16

@@ -525,7 +525,7 @@ def causal_attention_pure(Qh, K, V, causal=True, rows=None):
 
 
 def prefill_eval(Qh, K, V, K_hat, V_hat, *, ratio, min_residuals=1, kind="both", v_score="output_aware",
-                 normalize=False, k_corr_scale=0.1, diag=None, force_sel=None, o_base=None):
+                 normalize=False, k_corr_scale=0.1, diag=None, force_sel=None, o_base=None, rows=None):
     """``CAREKVLayer`` prefill in ``carekv_eval`` mode (layer.py:792-806): the
     causal base attention over K_hat / V_hat (``causal_attention_pure``,
     fp16 weights A and fp16 O_base), then
@@ -546,11 +546,15 @@ def prefill_eval(Qh, K, V, K_hat, V_hat, *, ratio, min_residuals=1, kind="both",
     top-k; ``o_base`` (Hq, T, D) fp16 replaces the base output O (the
     weights A stay the fp32 softmax cast to fp16), to hold the correction
     alone to a device whose base attention rounds differently.
+    ``rows`` (needs ``o_base``): only those rows t are corrected (each row's
+    scores and weights computed from that row alone; the other rows keep
+    O), for long prompts.
     Returns (T, Hq, D) fp16."""
     Qh = np.asarray(Qh, F16)
     Hq, T, D = Qh.shape
     Hkv = np.asarray(K).shape[0]
     grp = Hq // Hkv
+    assert rows is None or o_base is not None, "rows needs o_base"
     O = causal_attention_pure(Qh, K_hat, V_hat)[0] if o_base is None else np.asarray(o_base, F16)
     rk = (np.asarray(K, F16).astype(F32) - np.asarray(K_hat, F16).astype(F32)).astype(F16).astype(F32)
     rv = (np.asarray(V, F16).astype(F32) - np.asarray(V_hat, F16).astype(F32)).astype(F16).astype(F32)
@@ -559,26 +563,37 @@ def prefill_eval(Qh, K, V, K_hat, V_hat, *, ratio, min_residuals=1, kind="both",
     scale = F32(1.0 / math.sqrt(D))
     out = O.astype(F32).copy()
     mn = np.finfo(F32).min
+    row_list = list(range(T)) if rows is None else sorted(int(t) for t in rows)
+
+    def weights(q, hk, ts):
+        # layer.py:955-964 on rows ts: fp32 scores / sqrt(D), causal mask,
+        # softmax, cast to fp16
+        S = (q[ts] @ Kh[hk].T) / F32(math.sqrt(D))
+        S = S + np.where(np.arange(T)[None, :] > np.asarray(ts)[:, None], mn, F32(0)).astype(F32)
+        m = S.max(axis=-1, keepdims=True)
+        e = np.exp(S - m, dtype=F32)
+        return (e / e.sum(axis=-1, keepdims=True, dtype=F32)).astype(F16).astype(F32)
+
     for h in range(Hq):
         hk = h // grp
         q = Qh[h].astype(F32)
-        S = (q @ Kh[hk].T) / F32(math.sqrt(D))
-        S = S + np.where(np.arange(T)[None, :] > np.arange(T)[:, None], mn, F32(0)).astype(F32)
-        m = S.max(axis=-1, keepdims=True)
-        e = np.exp(S - m, dtype=F32)
-        A = (e / e.sum(axis=-1, keepdims=True, dtype=F32)).astype(F16).astype(F32)
-        qdot_all = (q @ rk[hk].T) * scale                        # (T rows, T tokens)
         rvn = np.sqrt((rv[hk] * rv[hk]).sum(-1, dtype=F32))      # (T,)
-        for t in range(T):
+        if rows is None:
+            A = weights(q, hk, np.arange(T))
+            qdot_all = (q @ rk[hk].T) * scale                    # (T rows, T tokens)
+        for t in row_list:
             n = t + 1
             k = min(max(int(min_residuals), int(n * ratio)), n)
             if k <= 0:
                 continue
-            a = A[t, :n]
+            if rows is None:
+                a, qd = A[t, :n], qdot_all[t, :n]
+            else:
+                a = weights(q, hk, [t])[0, :n]
+                qd = ((q[t:t + 1] @ rk[hk].T) * scale)[0, :n]
             o = O[h, t].astype(F32)
             vdiff = np.sqrt(((Vh[hk, :n] - o[None, :]) ** 2).sum(-1, dtype=F32))
             vs = a * rvn[:n] if v_score == "norm" else a * rvn[:n] * vdiff
-            qd = qdot_all[t, :n]
             ks = a * np.abs(qd) * vdiff
             if kind == "v":
                 sc = vs

@@ -37,9 +37,15 @@ def process_page(cache: OCache, layer_id: int, kv_head: int, page_id: int,
                  token_start: int, num_valid: int, is_recent=True, is_sink=False,
                  store_policy: str = "residual_kind_aware", residual_kind: str = "both",
                  min_per_kind: int = 1, k_frac: float = 1.0, v_frac: float = 1.0,
-                 K_hat_override=None, V_hat_override=None, P=None) -> OMeta:
+                 K_hat_override=None, V_hat_override=None, P=None, reuse_slots: bool = False) -> OMeta:
     """``ResidualStoreManager.process_page`` (``residual_store.py:239-464``)
-    with the default (no-op) selector-variant / position-policy knobs."""
+    with the default (no-op) selector-variant / position-policy knobs.
+
+    ``reuse_slots=True`` (no reference counterpart; the streaming fill
+    store): the slot ids of the page's earlier metadata (a prompt's partial
+    last page), ascending, go to the first selected candidates of their kind
+    before new ids are allocated; ids no longer needed stay unused.  The reference overwrites the metadata
+    and orphans them (``residual_store.py:463``)."""
     cfg = cache.cfg
     K_orig = np.asarray(K_orig)
     V_orig = np.asarray(V_orig)
@@ -128,13 +134,16 @@ def process_page(cache: OCache, layer_id: int, kv_head: int, page_id: int,
 
     k_slots = [-1] * num_cg
     v_slots = [-1] * num_vb
+    old = cache.meta_table[layer_id][kv_head][page_id] if reuse_slots else None
+    reuse_k = sorted(x for x in old.k_residual_slots if x >= 0) if old is not None else []
+    reuse_v = sorted(x for x in old.v_residual_slots if x >= 0) if old is not None else []
     for c in selected:
         if c["kind"] == "K":
-            s = cache.alloc_k_slot()
+            s = reuse_k.pop(0) if reuse_k else cache.alloc_k_slot()
             cache.write_k_residual(s, c["payload"], c["scale"])
             k_slots[c["idx"]] = s
         else:
-            s = cache.alloc_v_slot()
+            s = reuse_v.pop(0) if reuse_v else cache.alloc_v_slot()
             cache.write_v_residual(s, c["payload"], c["scale"])
             v_slots[c["idx"]] = s
     meta = OMeta(page_id=page_id, layer_id=layer_id, kv_head=kv_head, token_start=token_start,
@@ -225,9 +234,12 @@ def decode_append(cache: OCache, layer_id: int, k_rows, v_rows, streaming: bool 
     encoding the row's scales against the page's fixed master
     (``cache.py:689-695``, zero on a page the decode opened), the open page
     is re-encoded as ``write_base`` encodes its valid rows so far
-    (``write_scale_page`` over their fp16 group scales, ``cache.py:592-604``).
+    (``write_scale_page`` over their fp16 group scales, ``cache.py:592-604``),
+    unless it holds stored residual slots (a prompt's partial last page: its
+    slots are residuals against its rows as the prompt wrote them, so it
+    keeps the fixed-master encoding until it fills).
     Together with ``streaming=True`` this is the decode path of a cache
-    built with ``compat=False``."""
+    built with ``compat=False``; its fill store reuses the page's slot ids."""
     cfg = cache.cfg
     k_rows = np.asarray(k_rows)
     v_rows = np.asarray(v_rows)
@@ -257,12 +269,15 @@ def decode_append(cache: OCache, layer_id: int, k_rows, v_rows, streaming: bool 
                 Ko, Vo = cache.open_rows.pop((layer_id, h, pid)) if streaming else (Kh, Vh)
                 process_page(cache, layer_id, h, pid, Ko, Vo, None, None, None, None, token_start=ts,
                              num_valid=ps, is_recent=True, is_sink=ts < 4, K_hat_override=Kh,
-                             V_hat_override=Vh, **store_kw)
+                             V_hat_override=Vh, reuse_slots=streaming, **store_kw)
             continue
         kc, ks = Q.quantize(k_rows[h:h + 1], cfg.base_bits, cfg.group_size)
         vc, vs = Q.quantize(v_rows[h:h + 1], cfg.base_bits, cfg.group_size)
+        meta = cache.meta_table[layer_id][h][pid]
+        has_slots = meta is not None and (any(x >= 0 for x in meta.k_residual_slots)
+                                          or any(x >= 0 for x in meta.v_residual_slots))
         off = cache.append_to_page(layer_id, h, pid, kc[0], ks[0], vc[0], vs[0])
-        if rescale and cfg.scale_quant == "int8":
+        if rescale and cfg.scale_quant == "int8" and not has_slots:
             G = cfg.head_dim // cfg.group_size
             oks, ovs = cache.open_scales.get((layer_id, h, pid), (np.zeros((0, G), F16), np.zeros((0, G), F16)))
             oks = np.concatenate([oks[:off], np.asarray(ks, F16)[:1]])
@@ -286,4 +301,4 @@ def decode_append(cache: OCache, layer_id: int, k_rows, v_rows, streaming: bool 
             if streaming:  # the true rows instead of K_hat
                 Kh, Vh = cache.open_rows.pop((layer_id, h, pid))
             process_page(cache, layer_id, h, pid, Kh, Vh, Kc, Ks, Vc, Vs, token_start=ts,
-                         num_valid=ps, is_recent=True, is_sink=ts < 4, **store_kw)
+                         num_valid=ps, is_recent=True, is_sink=ts < 4, reuse_slots=streaming, **store_kw)

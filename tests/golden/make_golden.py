@@ -357,8 +357,9 @@ def golden_prefill_eval(ck):
     """CAREKVLayer.prefill in carekv_eval mode (layer.py:792-806, 363-456):
     the causal base attention over the prefill's K_hat / V_hat, then the
     per-(head, row) top-k correction from the full in-memory residuals.
-    Two knob sets: both kinds normalised with the output-aware V score, and
-    the K kind alone with a larger residual ratio."""
+    Three knob sets: both kinds normalised with the output-aware V score,
+    the K kind alone with a larger residual ratio, and the V kind alone
+    (output-aware score, min_residuals 2)."""
     cases = (("eval_gqa4_d64", dict(Hq=8, Hkv=2, D=64, T=90, seed=41, outlier_mult=8.0),
               dict(CAREKV_PREFILL_RESIDUAL_RATIO="0.05", CAREKV_PREFILL_MIN_RESIDUALS="1",
                    CAREKV_PREFILL_RESIDUAL_KIND="both", CAREKV_V_SCORE="output_aware", CAREKV_SCORE_NORMALIZE="1",
@@ -366,7 +367,14 @@ def golden_prefill_eval(ck):
              ("eval_mha_d128_k", dict(Hq=2, Hkv=2, D=128, T=70, seed=42, outlier_mult=10.0),
               dict(CAREKV_PREFILL_RESIDUAL_RATIO="0.1", CAREKV_PREFILL_MIN_RESIDUALS="2",
                    CAREKV_PREFILL_RESIDUAL_KIND="k", CAREKV_V_SCORE="norm", CAREKV_SCORE_NORMALIZE="0",
-                   CAREKV_K_CORRECTION_SCALE="0.3")))
+                   CAREKV_K_CORRECTION_SCALE="0.3")),
+             ("eval_gqa2_d128_v", dict(Hq=4, Hkv=2, D=128, T=80, seed=43, outlier_mult=8.0),
+              dict(CAREKV_PREFILL_RESIDUAL_RATIO="0.04", CAREKV_PREFILL_MIN_RESIDUALS="2",
+                   CAREKV_PREFILL_RESIDUAL_KIND="v", CAREKV_V_SCORE="output_aware", CAREKV_SCORE_NORMALIZE="0",
+                   CAREKV_K_CORRECTION_SCALE="0.1")))
+    only = os.environ.get("CAREKV_GOLDEN_EVAL_CASES")
+    if only:
+        cases = tuple(c for c in cases if c[0] in only.split(","))
     for name, shape, env in cases:
         Hq, Hkv, D, T = shape["Hq"], shape["Hkv"], shape["D"], shape["T"]
         _set_env(CAREKV_PREFILL_MODE="carekv_eval", CAREKV_DEBUG_STATS="0", **env)

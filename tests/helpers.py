@@ -104,6 +104,7 @@ def build_oracle_case(g, name):
 EVAL_CASES = {
     "eval_gqa4_d64": dict(Hq=8, Hkv=2, D=64),
     "eval_mha_d128_k": dict(Hq=2, Hkv=2, D=128),
+    "eval_gqa2_d128_v": dict(Hq=4, Hkv=2, D=128),
 }
 
 
@@ -128,3 +129,35 @@ def eval_hats(g, spec):
         kh.append(a)
         vh.append(b)
     return np.stack(kh), np.stack(vh)
+
+
+def oracle_cache_arrays(c, layer=0):
+    """An oracle cache's layer as the arrays of a store golden (the keys
+    tests/golden/make_golden.py writes from the reference's cache): codes,
+    scales, masters, valid counts, slot payloads and scales, and per page the
+    slot ids (-2 where the page has no metadata), errors and sketches."""
+    cfg = c.cfg
+    d = dict(K_codes=c.base_K_codes[layer], V_codes=c.base_V_codes[layer], K_scale=c.base_K_scale[layer],
+             V_scale=c.base_V_scale[layer], valid=c.valid_tokens[layer])
+    if c.base_K_scale_master is not None:
+        d["K_master"] = c.base_K_scale_master[layer]
+        d["V_master"] = c.base_V_scale_master[layer]
+    nk, nv = c.next_k_slot, c.next_v_slot
+    d.update(k_res=c.k_residual_buf[:nk], k_res_scale=c.k_residual_scale[:nk], v_res=c.v_residual_buf[:nv],
+             v_res_scale=c.v_residual_scale[:nv])
+    H, P = c.valid_tokens.shape[1], c.valid_tokens.shape[2]
+    ncg, nvb = cfg.head_dim // cfg.k_channel_group, math.ceil(cfg.page_size / cfg.v_token_block)
+    ks = np.full((H, P, ncg), -2, np.int32)
+    vs = np.full((H, P, nvb), -2, np.int32)
+    ke = np.zeros((H, P, ncg), F16)
+    ve = np.zeros((H, P, nvb), F16)
+    sk = np.zeros((H, P, ncg, cfg.sketch_dim), F16)
+    for h in range(H):
+        for p in range(P):
+            m = c.meta_table[layer][h][p]
+            if m is None:
+                continue
+            ks[h, p], vs[h, p] = m.k_residual_slots, m.v_residual_slots
+            ke[h, p], ve[h, p], sk[h, p] = m.k_error_norm, m.v_error_norm, m.k_sketch
+    d.update(k_slots=ks, v_slots=vs, k_err=ke, v_err=ve, k_sketch=sk)
+    return d

@@ -14,8 +14,8 @@ import pytest
 import torch
 
 from helpers import (DECODE_CASES, PAPER_ENV, PREFILL_CASES, build_oracle_case, build_oracle_prefill,
-                     case_cfg_kwargs, decode_diag, load_golden, oracle_candidates, oracle_selection,
-                     prefill_cfg_kwargs, ties_explain)
+                     case_cfg_kwargs, decode_diag, load_golden, oracle_cache_arrays, oracle_candidates,
+                     oracle_selection, prefill_cfg_kwargs, ties_explain)
 from oracle import quant as Q
 from oracle.attention import decode_attention as oracle_decode
 from oracle.attention import prefill_stored
@@ -495,6 +495,159 @@ def test_decode_random_vs_oracle(paper_env, case, live):
     assert n_tie * 16 <= max(Hq, 16), n_tie  # at most 1 query row in 16 crosses a tie
 
 
+# ------------------------------------------------------------------ INT4 base (config 4's quantizer)
+INT4_STORES = {"ratio3": dict(store_budget_mode="ratio", store_budget_ratio=0.03),
+               "abs2k4v": dict(store_budget_mode="absolute", store_abs_k=2, store_abs_v=4)}
+
+
+def _rounding_allowance(Kh, Vh, Qh, grp):
+    """Per (query head, dim): 2^-10 * sum_t a_t |V_hat_t| over the fp32
+    softmax weights a of the base attention.  Both the reference and the
+    kernel round each weight to fp16 at different points (the reference a,
+    the kernel a and then a times the V scale), so an output may differ from
+    the reference's by about that much, which matters only where |V| is
+    large (per-channel log-normal scales)."""
+    out = []
+    for h in range(Qh.shape[0]):
+        k, v = Kh[h // grp].astype(np.float64), Vh[h // grp].astype(np.float64)
+        s = (Qh[h].astype(np.float64) @ k.T) / math.sqrt(k.shape[1])
+        a = np.exp(s - s.max())
+        out.append(2.0 ** -10 * (a / a.sum()) @ np.abs(v))
+    return np.stack(out)
+
+
+@pytest.mark.parametrize("Hq,Hkv", [(16, 4), (4, 4), (16, 2)], ids=["gq4", "gq1", "gq8"])
+@pytest.mark.parametrize("store", sorted(INT4_STORES))
+def test_int4_store_and_decode_vs_oracle(paper_env, store, Hq, Hkv):
+    """Config 4 names INT4 next to INT3: write_prefill at base_bits 4 and
+    D = 128 gives the oracle's page bytes (codes, int8 scale codes,
+    masters), metadata, slot ids and 4-bit slot payloads (write_pages_for_kv_head
+    on the same rows, pinned by the store goldens at INT3), before and after
+    decode appends, for two inputs:
+      * decode data (K and V ~N(0, 1), 4 K channels x10, as config 3): the
+        corrected decode (exact renormalisation; the 4-query-head streaming
+        and apply kernels at GQ 4 and 1, the generic ones at GQ 8) meets the
+        decode bar against oracle.decode_attention, selections equal up to
+        epsilon ties;
+      * config 4's data (per-channel log-normal K and V scales): the base
+        decode meets max(2e-3, 1 ulp) plus the weight-rounding allowance.
+    """
+    import care_kv
+    D, bits, T, n_app = 128, 4, 600, 9
+    paper_env.setenv("CAREKV_K_CORRECTION_MODE", "exact")
+    for data in ("decode", "lognormal"):
+        print(f"int4 store+decode store={store} Hq={Hq} Hkv={Hkv} data={data}", flush=True)
+        rng = np.random.default_rng(400 + Hq + Hkv + len(store))
+        if data == "decode":
+            K = rng.standard_normal((Hkv, T + n_app, D))
+            K[:, :, rng.permutation(D)[:4]] *= 10.0
+            V = rng.standard_normal((Hkv, T + n_app, D))
+        else:
+            K = rng.standard_normal((Hkv, T + n_app, D)) * np.exp(rng.standard_normal((Hkv, 1, D)))
+            V = rng.standard_normal((Hkv, T + n_app, D)) * np.exp(rng.standard_normal((Hkv, 1, D)))
+        K, V = K.astype(F16), V.astype(F16)
+        Qh = rng.standard_normal((Hq, D)).astype(F16)
+        common = dict(num_layers=1, num_heads=Hq, num_kv_heads=Hkv, head_dim=D, page_size=16,
+                      max_pages=(T + n_app) // 16 + 4, base_bits=bits, group_size=32, k_channel_group=32,
+                      v_token_block=4, sketch_dim=32, read_budget_mode="absolute", read_abs_k=8, read_abs_v=8,
+                      route_policy="joint", **INT4_STORES[store])
+        oc = OCache(OCfg(**common), max_slots=common["max_pages"] * Hkv * 4)
+        for h in range(Hkv):
+            write_pages_for_kv_head(oc, 0, h, K[h, :T], V[h, :T])
+        cfg = care_kv.CacheConfig(packed_base=True, scale_quant="int8", read_budget_ratio=0.0, compat=True,
+                                  **common)
+        cache = care_kv.CAREKVCache(cfg, device="cuda")
+        Kd, Vd = torch.from_numpy(K).cuda(), torch.from_numpy(V).cuda()
+        cache.write_prefill(0, Kd[:, :T], Vd[:, :T])
+        torch.cuda.synchronize()
+        compare_cache_to_golden(cache, oracle_cache_arrays(oc))
+        for t in range(T, T + n_app):
+            decode_append(oc, 0, K[:, t], V[:, t])
+            cache.append(0, Kd[:, t], Vd[:, t])
+        torch.cuda.synchronize()
+        compare_cache_to_golden(cache, oracle_cache_arrays(oc))
+        q = torch.from_numpy(Qh).cuda().unsqueeze(0)
+        if data == "lognormal":
+            out = care_kv.decode_attention(cache, 0, q, correction=False)[0].cpu().numpy().astype(F32)
+            ref = oracle_decode(oc, 0, Qh, correction=False).astype(F32)
+            kh, vh = [], []
+            for h in range(Hkv):
+                kc, ks, vc, vs, _ = oc.read_base_concat(0, h, oc.all_page_ids(0, h))
+                kh.append(Q.dequantize(kc, ks, 32))
+                vh.append(Q.dequantize(vc, vs, 32))
+            allow = _rounding_allowance(kh, vh, Qh, Hq // Hkv)
+            ulp = np.spacing(np.abs(ref).astype(F16)).astype(F32)
+            err = np.abs(out - ref)
+            assert np.all(err <= np.maximum(2e-3, ulp + allow)), float((err / np.maximum(2e-3, ulp + allow)).max())
+            assert np.linalg.norm(out - ref) <= 1e-2 * np.linalg.norm(ref)
+            continue
+        odiag = {}
+        o_out = oracle_decode(oc, 0, Qh, k_mode="exact", kind="both", k_corr_scale=0.1, score_normalize=True,
+                              kscore_live=True, diag=odiag)
+        out, diag = care_kv.decode_attention(cache, 0, q, diag_cap=64)
+        out = out[0].cpu().numpy().astype(F32)
+        ref = o_out.astype(F32)
+        grp, diag, n_tie = Hq // Hkv, diag[0].cpu().numpy(), 0
+        for h in range(Hkv):
+            Kc, Vc = oracle_candidates(oc, 0, h, oc.next_page[0][h])
+            ref_rows = oracle_selection(odiag[h], Kc, Vc)
+            for j in range(grp):
+                mine = set(decode_diag(diag[h * grp + j]))
+                n_tie += mine != ref_rows[j]
+                assert ties_explain(mine, ref_rows[j], odiag[h], Kc, Vc, j, eps=1e-4), (h, j)
+        assert n_tie * 16 <= max(Hq, 16), n_tie
+        err = np.abs(out - ref)
+        ulp = np.spacing(np.abs(ref).astype(F16)).astype(F32)
+        assert np.all(err <= np.maximum(2e-3, ulp)), err.max()
+        assert np.linalg.norm(out - ref) <= 1e-2 * np.linalg.norm(ref)
+
+
+@pytest.mark.parametrize("bits", [4, 3])
+def test_config4_store_full_shape(bits):
+    """Config 4's store at its full shape (4 sequences, 40 kv heads, 8192
+    tokens, D = 128, K and V with per-channel log-normal scales, store ratio
+    3%), one batched write_prefill: sampled (sequence, kv head) slices hold
+    the oracle's page bytes, metadata and slot payloads (the oracle writes
+    each slice alone, so its slot ids are compared relative to the slice's
+    first id), and the slot counters equal 4 * 40 * 512 pages' worth."""
+    import care_kv
+    B, H, T, D = 4, 40, 8192, 128
+    print(f"config 4 store bits={bits}", flush=True)
+    g = torch.Generator().manual_seed(4)
+    K = torch.randn(B, H, T, D, generator=g) * torch.exp(torch.randn(1, H, 1, D, generator=g))
+    V = torch.randn(B, H, T, D, generator=g) * torch.exp(torch.randn(1, H, 1, D, generator=g))
+    K, V = K.half(), V.half()
+    common = dict(num_layers=1, num_heads=H, num_kv_heads=H, head_dim=D, page_size=16, max_pages=T // 16,
+                  base_bits=bits, group_size=32, k_channel_group=32, v_token_block=4, sketch_dim=32,
+                  store_budget_mode="ratio", store_budget_ratio=0.03)
+    cfg = care_kv.CacheConfig(packed_base=True, scale_quant="int8", read_budget_ratio=0.0, compat=True, **common)
+    cache = care_kv.CAREKVCache(cfg, device="cuda", n_seq=B)
+    cache.write_prefill(0, K.cuda(), V.cuda(), seqs=list(range(B)))
+    torch.cuda.synchronize()
+    P = T // 16
+    assert cache.next_slot.tolist() == [[H * P, H * P]] * B  # one K and one V slot a page (max(1, int(n * 0.03)))
+    for s, h in ((0, 0), (3, H - 1), (2, 17)):
+        oc = OCache(OCfg(**{**common, "num_heads": 1, "num_kv_heads": 1}), max_slots=P)
+        write_pages_for_kv_head(oc, 0, 0, K[s, h].numpy(), V[s, h].numpy())
+        ref = oracle_cache_arrays(oc)
+        valid = cache.valid[0, h, s].cpu().numpy()
+        assert np.array_equal(valid, ref["valid"][0])
+        for nm, t in (("K_codes", cache.kcodes), ("V_codes", cache.vcodes), ("K_scale", cache.kscale),
+                      ("V_scale", cache.vscale), ("K_master", cache.kmaster), ("V_master", cache.vmaster)):
+            assert np.array_equal(t[0, h, s].cpu().numpy(), ref[nm][0]), (nm, s, h)
+        ks, vs = cache.k_slot[0, h, s].cpu().numpy(), cache.v_slot[0, h, s].cpu().numpy()
+        k0, v0 = int(ks[ks >= 0].min()), int(vs[vs >= 0].min())
+        assert (k0, v0) == (h * P, h * P), (s, h, k0, v0)  # kv-head-major slot order within the sequence
+        assert np.array_equal(np.where(ks >= 0, ks - k0, -1), ref["k_slots"][0]), (s, h)
+        assert np.array_equal(np.where(vs >= 0, vs - v0, -1), ref["v_slots"][0]), (s, h)
+        assert np.array_equal(cache.k_res[s, k0:k0 + P].cpu().numpy(), ref["k_res"])
+        assert np.array_equal(cache.v_res[s, v0:v0 + P].cpu().numpy(), ref["v_res"])
+        assert np.array_equal(cache.k_res_scale[s, k0:k0 + P].cpu().numpy(), ref["k_res_scale"][:, 0])
+        assert np.array_equal(cache.v_res_scale[s, v0:v0 + P].cpu().numpy(), ref["v_res_scale"][:, 0])
+        for nm, t in (("k_err", cache.k_err), ("v_err", cache.v_err), ("k_sketch", cache.k_sketch)):
+            assert _ulp_diff(t[0, h, s].cpu().numpy(), ref[nm][0]) <= 1, (nm, s, h)
+
+
 def test_batched_sequences_match_single(paper_env):
     """B sequences in one launch == each sequence decoded alone."""
     import care_kv
@@ -524,22 +677,29 @@ def test_batched_sequences_match_single(paper_env):
     assert torch.count_nonzero(both[4]) == 0  # nothing to attend to: zeros, as an empty softmax sum gives
 
 
-@pytest.mark.parametrize("D,bits,base", [(64, 3, "uniform"), (128, 2, "uniform"), (64, 2, "kivi_style")])
-def test_streaming_store_matches_oracle(paper_env, D, bits, base):
+@pytest.mark.parametrize("D,bits,base,jump", [(64, 3, "uniform", 1.0), (128, 2, "uniform", 1.0),
+                                              (64, 2, "kivi_style", 1.0), (64, 3, "uniform", 2.0)])
+def test_streaming_store_matches_oracle(paper_env, D, bits, base, jump):
     """The default decode appends (compat=False, no reference counterpart):
     they fill the prompt's partial page and three decode-opened pages, each
-    open page re-encoded as write_base encodes its rows and each fill stored
-    from the true rows against the page's own base -- page bytes, slot ids,
-    residual bytes and scales equal the oracle's (process_page on the same
-    inputs), and the decode over the cache matches the oracle's."""
+    open page without stored slots re-encoded as write_base encodes its rows
+    and each fill stored from the true rows against the page's own base,
+    reusing the slot ids the page held -- page bytes, slot ids, residual
+    bytes and scales equal the oracle's (process_page on the same inputs),
+    and the decode over the cache matches the oracle's.  jump: the appended
+    rows are that much larger than the prompt's; the prompt's partial page,
+    which holds slots, keeps its prefill encoding (master and scale codes)
+    until it fills."""
     import care_kv
     paper_env.setenv("CAREKV_K_CORRECTION_MODE", "exact")
     Hq, Hkv, T, n_app = 8, 2, 100, 60
-    print(f"streaming store D={D} bits={bits} base={base}", flush=True)
+    print(f"streaming store D={D} bits={bits} base={base} jump={jump}", flush=True)
     rng = np.random.default_rng(D + bits)
     K = rng.standard_normal((Hkv, T + n_app, D)).astype(F16)
     V = rng.standard_normal((Hkv, T + n_app, D)).astype(F16)
     K[:, :, rng.permutation(D)[:3]] *= F16(6.0)
+    K[:, T:] *= F16(jump)
+    V[:, T:] *= F16(jump)
     Qh = rng.standard_normal((Hq, D)).astype(F16)
     common = dict(num_layers=1, num_heads=Hq, num_kv_heads=Hkv, head_dim=D, page_size=16,
                   max_pages=(T + n_app) // 16 + 4, base_bits=bits, group_size=32, k_channel_group=32,
@@ -555,9 +715,22 @@ def test_streaming_store_matches_oracle(paper_env, D, bits, base):
     cache = care_kv.CAREKVCache(cfg, device="cuda")  # the default (compat=False): streaming store, re-encoding
     Kd, Vd = torch.from_numpy(K).cuda(), torch.from_numpy(V).cuda()
     cache.write_prefill(0, Kd[:, :T], Vd[:, :T])
+    pre_k = cache.k_slot[0, :, 0, T // 16].clone()  # the prompt's partial page
+    pre_v = cache.v_slot[0, :, 0, T // 16].clone()
+    pre_km = cache.kmaster[0, :, 0, T // 16].clone()
+    pre_ks = cache.kscale[0, :, 0, T // 16, :T % 16].clone()
     for t in range(T, T + n_app):
         cache.append(0, Kd[:, t], Vd[:, t])
+        if t == T + 2 and jump > 1:  # the prompt page still holds its slots and its prefill encoding
+            assert torch.equal(cache.k_slot[0, :, 0, T // 16], pre_k)
+            assert torch.equal(cache.kmaster[0, :, 0, T // 16], pre_km)
+            assert torch.equal(cache.kscale[0, :, 0, T // 16, :T % 16], pre_ks)
     torch.cuda.synchronize()
+    for h in range(Hkv):  # its refill reuses the slot ids it held
+        for pre, now in ((pre_k[h], cache.k_slot[0, h, 0, T // 16]), (pre_v[h], cache.v_slot[0, h, 0, T // 16])):
+            old_ids = sorted(x for x in pre.tolist() if x >= 0)
+            new_ids = sorted(x for x in now.tolist() if x >= 0)
+            assert set(old_ids) <= set(new_ids) or set(new_ids) <= set(old_ids), (h, old_ids, new_ids)
     nk, nv = oc.next_k_slot, oc.next_v_slot
     valid = cache.valid[0, :, 0].cpu().numpy()
     assert np.array_equal(valid, oc.valid_tokens[0])
@@ -601,9 +774,11 @@ def test_streaming_store_matches_oracle(paper_env, D, bits, base):
         assert any(s >= 0 for s in oc.meta_table[0][0][P - 2].k_residual_slots)
     out = care_kv.decode_attention(cache, 0, torch.from_numpy(Qh).cuda().unsqueeze(0))[0].cpu().numpy()
     ref = oracle_decode(oc, 0, Qh, k_mode="exact", kind="both", k_corr_scale=0.1, score_normalize=True,
-                        kscore_live=True)
-    err = np.abs(out.astype(F32) - ref.astype(F32))
-    assert err.max() <= 2e-3, err.max()
+                        kscore_live=True).astype(F32)
+    err = np.abs(out.astype(F32) - ref)
+    ulp = np.spacing(np.abs(ref).astype(F16)).astype(F32)
+    assert np.all(err <= np.maximum(2e-3, ulp)), err.max()
+    assert np.linalg.norm(out.astype(F32) - ref) <= 1e-2 * np.linalg.norm(ref)
 
 
 # ------------------------------------------------------------------ router policies vs oracle

@@ -3,11 +3,15 @@
 * ``carekv_quantize_rows`` + ``carekv_dequantize_rows`` reproduce
   ``quantize`` / ``dequantize`` (quantizer.py:31-82) bit for bit.
 * ``carekv_prefill_attn`` reproduces ``_causal_attention_pure``
-  (layer.py:935-972): every output element within max-abs 2e-3 (or one fp16
-  ulp of the reference where that is larger) and the output within
-  relative L2 1e-2 of the oracle; for V with per-channel log-normal scales
-  (config 4) the absolute bar is 2e-3 times the rms of V; the log-sum-exp
-  within 1e-3 absolute.
+  (layer.py:935-972): every output element within max-abs 2e-3, or, where
+  that is larger, one fp16 ulp of the reference plus the weight-rounding
+  allowance 2^-11 sum_t a_t |v_t| (the reference rounds each normalised
+  weight a_t to fp16, the kernel each unnormalised exp2(x - m) before it
+  divides by the row sum: two independent roundings of up to 2^-12 of
+  a_t each, which only shows where |V| is large, as with config 4's
+  per-channel log-normal scales), and the output within relative L2 1e-2
+  of the oracle; for normal V and for log-normal V, at config 4's full
+  shape on sampled rows.  The log-sum-exp within 1e-3 absolute.
 """
 import math
 
@@ -39,13 +43,29 @@ def _inputs(B, Hq, Hkv, T, D, seed, v_lognormal=False):
     return q, k, v.half()
 
 
-def _check(out, ref, v, lognormal=False):
+def _allowance(q, k, v, rows=None, causal=True):
+    """2^-11 sum_t a_t |v_t| per (head, row, dim) from the fp64 softmax
+    weights: q (H, T, D), k / v (Hkv, T, D)."""
+    H, T, D = q.shape
+    grp = H // k.shape[0]
+    rows = np.arange(T) if rows is None else np.asarray(rows)
+    out = np.zeros((H, len(rows), D))
+    for h in range(H):
+        kk, vv = k[h // grp].astype(np.float64), np.abs(v[h // grp].astype(np.float64))
+        s = (q[h, rows].astype(np.float64) @ kk.T) / math.sqrt(D)
+        if causal:
+            s = np.where(np.arange(T)[None, :] > rows[:, None], -np.inf, s)
+        a = np.exp(s - s.max(-1, keepdims=True))
+        out[h] = 2.0 ** -11 * (a / a.sum(-1, keepdims=True)) @ vv
+    return out
+
+
+def _check(out, ref, allow=0.0):
     ulp = np.spacing(np.abs(ref.astype(F16))).astype(F32)
     out = out.astype(F32)
     ref = ref.astype(F32)
-    vs = max(1.0, float(np.sqrt(np.mean(v.astype(F32) ** 2)))) if lognormal else 1.0
     err = np.abs(out - ref)
-    bound = np.maximum(2e-3 * vs, ulp)
+    bound = np.maximum(2e-3, ulp + allow)
     assert np.isfinite(out).all()
     assert (err <= bound).all(), f"max err {err.max():.3e}, worst ratio {(err / bound).max():.2f}"
     rel = float(np.linalg.norm(out - ref) / max(np.linalg.norm(ref), 1e-30))
@@ -75,7 +95,7 @@ def test_prefill_attention_vs_oracle(case):
     out, lse = out.cpu().numpy(), lse.cpu().numpy()
     for b in range(B):
         ref, ref_lse = causal_attention_pure(q[b].numpy(), k[b].numpy(), v[b].numpy(), causal=causal)
-        _check(out[b], ref, v[b].numpy(), logn)
+        _check(out[b], ref, _allowance(q[b].numpy(), k[b].numpy(), v[b].numpy(), causal=causal))
         assert np.abs(lse[b] - ref_lse).max() < 1e-3
 
 
@@ -89,7 +109,32 @@ def test_prefill_attention_long_sequence_rows():
     out = care_kv.prefill_attention(q.cuda(), k.cuda(), v.cuda()).cpu().numpy()
     rows = [0, 1, 31, 32, 63, 64, 95, 127, 128, 2047, 2048, 4032, 4095]
     ref, _ = causal_attention_pure(q[0].numpy(), k[0].numpy(), v[0].numpy(), rows=rows)
-    _check(out[0][:, rows], ref, v[0].numpy())
+    _check(out[0][:, rows], ref)
+
+
+def test_prefill_attention_config4_rows():
+    """Config 4 at its full shape: B = 4, 40 heads, T = 8192, D = 128, K and
+    V with per-channel log-normal scales (sigma 1), over the INT4-dequantised
+    K_hat / V_hat the prefill attends to; sampled rows (block and tile
+    boundaries, the last row) of sampled (sequence, head)s against the oracle
+    restricted to those rows."""
+    import care_kv
+    B, H, T, D = 4, 40, 8192, 128
+    print("prefill config 4 rows", flush=True)
+    g = torch.Generator().manual_seed(4)
+    q = torch.randn(B, H, T, D, generator=g).half()
+    K = (torch.randn(B, H, T, D, generator=g) * torch.exp(torch.randn(1, H, 1, D, generator=g))).half()
+    V = (torch.randn(B, H, T, D, generator=g) * torch.exp(torch.randn(1, H, 1, D, generator=g))).half()
+    Kh = care_kv.quant_dequant(K.cuda(), 4, 32)
+    Vh = care_kv.quant_dequant(V.cuda(), 4, 32)
+    out = care_kv.prefill_attention(q.cuda(), Kh, Vh)
+    torch.cuda.synchronize()
+    rows = [0, 1, 127, 128, 4095, 4096, 8000, T - 1]
+    for s, h in ((0, 0), (3, 39), (1, 22)):
+        o = out[s, h, rows].cpu().numpy()[None]
+        kh, vh = Kh[s, h:h + 1].cpu().numpy(), Vh[s, h:h + 1].cpu().numpy()
+        ref, _ = causal_attention_pure(q[s, h:h + 1].numpy(), kh, vh, rows=rows)
+        _check(o, ref, _allowance(q[s, h:h + 1].numpy(), kh, vh, rows=rows))
 
 
 def test_prefill_attention_is_causal():

@@ -106,8 +106,9 @@ def _check_against_oracle(Qh, K, V, Kh, Vh, knobs, *, max_flips=None):
 @pytest.mark.parametrize("name", sorted(EVAL_CASES))
 def test_prefill_eval_reference_golden(name):
     """The reference's carekv_eval goldens (GQA 4 at D = 64 with both kinds
-    normalised; MHA at D = 128 with the K kind alone, min_residuals 2)
-    against the oracle and against the golden output."""
+    normalised; MHA at D = 128 with the K kind alone, min_residuals 2; GQA 2
+    at D = 128 with the V kind alone, min_residuals 2) against the oracle and
+    against the golden output."""
     print(f"carekv_eval golden {name}", flush=True)
     g = load_golden(f"prefill_{name}.npz")
     spec = EVAL_CASES[name]
@@ -251,3 +252,60 @@ def test_prefill_eval_max_length():
             assert np.all(got[:k] >= 0) and np.all(np.diff(got[:k]) > 0) and got[k - 1] <= t, (h, t)
             assert np.all(got[k:] == -1), (h, t)
     _check_against_oracle(Qh[:, :n], K[:, :n], V[:, :n], Kh[:, :n], Vh[:, :n], knobs)
+
+
+def test_prefill_eval_max_length_d128():
+    """T = 8192 at head_dim 128 (64 KiB of dynamic score arrays plus the
+    kernel's static LDS): sampled long rows of both query heads against the
+    oracle restricted to those rows, over the same base output (selections
+    up to near-ties, outputs under the bar)."""
+    import care_kv
+    T, Hq, Hkv, D = 8192, 2, 1, 128
+    rows = [511, 4095, 6000, T - 1]
+    print(f"carekv_eval max length D={D} T={T} rows={rows}", flush=True)
+    Qh, K, V, Kh, Vh = _rand_case(Hq, Hkv, D, T, seed=29)
+    knobs = dict(ratio=0.01, min_residuals=1, kind="both", v_score="output_aware", normalize=True,
+                 k_corr_scale=0.1)
+    d = [torch.from_numpy(np.ascontiguousarray(x)).cuda() for x in (Qh, K, V, Kh, Vh)]
+    O = care_kv.prefill_attention(d[0], d[3], d[4])
+    out, dg = care_kv.prefill_eval(*d, O, diag_cap=128, **knobs)
+    torch.cuda.synchronize()
+    out = out.cpu().numpy().transpose(1, 0, 2)
+    dg, O = dg.cpu().numpy(), O.cpu().numpy()
+    assert np.isfinite(out.astype(F32)).all()
+    diag = {}
+    oracle_eval(Qh, K, V, Kh, Vh, diag=diag, o_base=O, rows=rows, **knobs)
+    force, sel = {}, {}
+    for (h, t), (idx, sc) in diag.items():
+        got = dg[h, t]
+        got = got[got >= 0]
+        assert len(got) == len(idx) == max(1, int((t + 1) * knobs["ratio"])), (h, t, len(got), len(idx))
+        sel[(h, t)] = got
+        if not np.array_equal(got, idx):
+            tol = 1e-5 * float(np.abs(sc).max()) + 1e-30
+            assert abs(float(sc[got].min()) - float(sc[idx].min())) <= tol, (h, t)
+            force[(h, t)] = got
+    assert len(force) <= 2, len(force)
+    ref = oracle_eval(Qh, K, V, Kh, Vh, force_sel=force, o_base=O, rows=rows, **knobs)
+    _bar(out, ref, sel, V, Vh, knobs["k_corr_scale"], Hq // Hkv, rows=sorted(sel), max_frac=0.25)
+
+
+def test_prefill_eval_rejects_non_finite_ratio():
+    """An infinite or NaN ratio raises before any kernel runs (Python's
+    int(n * ratio) raises there, layer.py:397); a huge finite ratio keeps
+    every token, as int(n * ratio) >= n does."""
+    import care_kv
+    print("carekv_eval ratio edges", flush=True)
+    Qh, K, V, Kh, Vh = _rand_case(2, 1, 64, 40, seed=31)
+    d = [torch.from_numpy(np.ascontiguousarray(x)).cuda() for x in (Qh, K, V, Kh, Vh)]
+    O = care_kv.prefill_attention(d[0], d[3], d[4])
+    base = dict(min_residuals=1, kind="both", v_score="output_aware", normalize=False, k_corr_scale=0.1)
+    for bad in (float("inf"), float("nan")):
+        with pytest.raises(care_kv.CarekvError, match="finite"):
+            care_kv.prefill_eval(*d, O, ratio=bad, **base)
+    _, dg = care_kv.prefill_eval(*d, O, ratio=1e300, diag_cap=40, **base)
+    _, dg1 = care_kv.prefill_eval(*d, O, ratio=1.0, diag_cap=40, **base)
+    assert torch.equal(dg, dg1)
+    dg = dg.cpu().numpy()
+    for t in range(40):
+        assert np.array_equal(dg[:, t, :t + 1], np.broadcast_to(np.arange(t + 1), (2, t + 1))), t

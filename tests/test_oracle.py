@@ -645,10 +645,11 @@ def test_reencoding_append_matches_write_base():
     """decode_append(rescale=True) (the compat=False append; no reference
     counterpart): after 16 appends a decode-opened page holds exactly the
     codes, int8 scale codes and master that write_base gives those 16 rows
-    (cache.py:592-654); the prompt's partial page, refilled by the appends,
-    holds what write_base gives its 16 rows; an open page reads back within
-    INT3 quantisation error of its rows (the reference's encoding reads a
-    decode-opened page back as zeros)."""
+    (cache.py:592-654); the prompt's partial page, which holds stored slots,
+    keeps the reference's fixed-master encoding (its prefill scale codes and
+    master); an open page reads back within INT3 quantisation error of its
+    rows (the reference's encoding reads a decode-opened page back as
+    zeros)."""
     rng = np.random.default_rng(11)
     D, T, n = 64, 20, 30
     K = (rng.standard_normal((1, T + n, D)) * np.exp(rng.standard_normal((1, 1, D)))).astype(F16)
@@ -671,7 +672,14 @@ def test_reencoding_append_matches_write_base():
                 bound = np.abs(X[0, rows].astype(F32)).reshape(nv, -1, 32).max(-1).repeat(32, -1) / 3 * 0.51 + 1e-3
                 assert np.all(err <= bound * 1.1) and np.abs(got).max() > 0, which
                 assert np.abs(got.astype(F32) - want.astype(F32)).max() <= 0.05 * np.abs(want).max(), which
-    for p in (1, 2):  # page 1: prompt rows 16..19 + appends; page 2: decode-opened
+    # page 1 (prompt rows 16..19, then appends) holds slots: not re-encoded
+    pre = OCache(OCfg(**kw))
+    write_pages_for_kv_head(pre, 0, 0, K[0, :T], V[0, :T])
+    assert any(x >= 0 for x in pre.meta_table[0][0][1].k_residual_slots)
+    assert np.array_equal(c.base_K_scale[0, 0, 1, :4], pre.base_K_scale[0, 0, 1, :4])
+    assert c.base_K_scale_master[0, 0, 1] == pre.base_K_scale_master[0, 0, 1]
+    assert c.base_V_scale_master[0, 0, 1] == pre.base_V_scale_master[0, 0, 1]
+    for p in (2,):  # page 2: decode-opened
         rows = slice(p * 16, p * 16 + 16)
         pid = ref.alloc_page(0, 0)
         Kc, Ks = Q.quantize(K[0, rows], 3, 32)
@@ -688,6 +696,64 @@ def test_reencoding_append_matches_write_base():
     for t in range(T, T + 20):
         decode_append(z, 0, K[:, t], V[:, t])
     assert np.all(Q.dequantize(z.unpack_rows(z.base_K_codes[0, 0, 2])[:4], z.page_scales(0, 0, 2, "K")[:4], 32) == 0)
+
+
+def test_reencoding_keeps_slot_pages_and_fill_reuses_their_slots():
+    """The compat=False decode append (streaming + rescale, no reference
+    counterpart) on a prompt whose partial last page holds stored slots, when
+    the appended rows are 16x larger than the prompt's: the page keeps its
+    prefill encoding (the reference's fixed master), so each of its prompt
+    rows still reads back as K_hat with K_hat + its K slot residual within
+    the 4-bit residual error of the true row (re-encoding against the raised
+    master would move K_hat away from the residual's base: 0.49 of the
+    residual range here against 0.09); when the page fills, its new slots
+    reuse the prefill's slot ids, so the page takes no new K id."""
+    rng = np.random.default_rng(21)
+    D, T, n = 64, 20, 12
+    K = rng.standard_normal((1, T + n, D)).astype(F16)
+    V = rng.standard_normal((1, T + n, D)).astype(F16)
+    K[:, T:] *= F16(16.0)
+    V[:, T:] *= F16(16.0)
+    kw = dict(num_layers=1, num_heads=2, num_kv_heads=1, head_dim=D, page_size=16, max_pages=8, base_bits=3,
+              group_size=32, k_channel_group=32, v_token_block=4, sketch_dim=32, store_budget_mode="absolute",
+              store_abs_k=2, store_abs_v=1)
+    c = OCache(OCfg(**kw))
+    write_pages_for_kv_head(c, 0, 0, K[0, :T], V[0, :T])
+    m0 = c.meta_table[0][0][1]
+    k_ids, v_ids = list(m0.k_residual_slots), list(m0.v_residual_slots)
+    nk0, nv0 = c.next_k_slot, c.next_v_slot
+    assert sorted(k_ids) == [nk0 - 2, nk0 - 1] and sum(x >= 0 for x in v_ids) == 1
+    km0, sc0 = c.base_K_scale_master[0, 0, 1], c.base_K_scale[0, 0, 1, :4].copy()
+
+    def corrected_err(cache):
+        Kh = Q.dequantize(cache.unpack_rows(cache.base_K_codes[0, 0, 1])[:4], cache.page_scales(0, 0, 1, "K")[:4], 32)
+        worst = 0.0
+        for cg, slot in enumerate(m0.k_residual_slots):
+            R = Q.unpack_4bit(cache.k_residual_buf[slot], cache.k_residual_scale[slot, 0], 16 * 32).reshape(16, 32)
+            cols = slice(cg * 32, cg * 32 + 32)
+            rel = np.abs(Kh[:, cols].astype(F32) + R[:4] - K[0, 16:20, cols].astype(F32))
+            worst = max(worst, float(rel.max()) / float(np.abs(R).max() + 1e-6))
+        return worst
+
+    for t in range(T, T + 5):  # the page still open
+        decode_append(c, 0, K[:, t], V[:, t], streaming=True, rescale=True)
+    assert c.base_K_scale_master[0, 0, 1] == km0 and np.array_equal(c.base_K_scale[0, 0, 1, :4], sc0)
+    # 4-bit residual rounding (1/14 of the range) plus the int8 scale-code rounding of the prompt
+    assert corrected_err(c) <= 0.2, corrected_err(c)
+    for t in range(T + 5, T + n):  # fills the page
+        decode_append(c, 0, K[:, t], V[:, t], streaming=True, rescale=True)
+    m1 = c.meta_table[0][0][1]
+    assert sorted(x for x in m1.k_residual_slots if x >= 0) == sorted(k_ids)
+    used_v = sorted(x for x in m1.v_residual_slots if x >= 0)
+    assert used_v[:1] == sorted(x for x in v_ids if x >= 0)  # the prefill's V id first, then new ones
+    assert c.next_k_slot == nk0 and c.next_v_slot == nv0 + len(used_v) - 1
+    # a page without slots is re-encoded by the same appends
+    z = OCache(OCfg(**{**kw, "store_abs_k": 0, "store_abs_v": 0}))
+    write_pages_for_kv_head(z, 0, 0, K[0, :T], V[0, :T])
+    before = z.page_scales(0, 0, 1, "K")[:4].copy()
+    for t in range(T, T + 5):
+        decode_append(z, 0, K[:, t], V[:, t], streaming=True, rescale=True)
+    assert not np.array_equal(z.page_scales(0, 0, 1, "K")[:4], before)
 
 
 @pytest.mark.parametrize("bits", [2, 3, 4])
@@ -718,7 +784,7 @@ def test_kivi_codes_dequantise_to_kivi_qdq(bits):
     assert np.isnan(Q.kivi_qdq(X[0, 3:4], bits, True)[0, 11])
 
 
-@pytest.mark.parametrize("name", ["eval_gqa4_d64", "eval_mha_d128_k"])
+@pytest.mark.parametrize("name", ["eval_gqa4_d64", "eval_mha_d128_k", "eval_gqa2_d128_v"])
 def test_prefill_eval_golden(golden, name):
     """CAREKVLayer.prefill in carekv_eval mode (layer.py:792-806, 363-456)
     against the reference's output: the token-level top-k correction from
@@ -741,3 +807,96 @@ def test_prefill_eval_golden(golden, name):
     from oracle.attention import causal_attention_pure
     base, _ = causal_attention_pure(g["Q"].transpose(1, 0, 2), Kh, Vh)
     assert np.abs(base.transpose(1, 0, 2).astype(F32) - ref.astype(F32)).max() > 1e-2
+
+
+@pytest.mark.parametrize("knobs", [dict(ratio=0.05, kind="both", normalize=True), dict(ratio=0.1, kind="k"),
+                                   dict(ratio=0.03, kind="v", min_residuals=2)], ids=["both", "k", "v"])
+def test_prefill_eval_rows_equal_full(knobs):
+    """prefill_eval(rows=...) (the long-prompt form, each row's weights
+    from that row alone) gives the full evaluation's selections on those
+    rows, its scores up to the fp32 order of a one-row product (1e-5 of
+    the row's largest score), outputs
+    within one fp16 ulp (equal here), and leaves the other rows at the base."""
+    from oracle.attention import causal_attention_pure, prefill_eval
+    rng = np.random.default_rng(3)
+    Hq, Hkv, D, T = 4, 2, 64, 150
+    K = rng.standard_normal((Hkv, T, D)).astype(F16)
+    V = rng.standard_normal((Hkv, T, D)).astype(F16)
+    Qh = (rng.standard_normal((Hq, T, D)) * 0.7).astype(F16)
+    Kh = Q.dequantize(*Q.quantize(K, 2, 32), 32)
+    Vh = Q.dequantize(*Q.quantize(V, 2, 32), 32)
+    O = causal_attention_pure(Qh, Kh, Vh)[0]
+    d1, d2 = {}, {}
+    full = prefill_eval(Qh, K, V, Kh, Vh, o_base=O, diag=d1, **knobs)
+    rows = [0, 17, 63, 149]
+    part = prefill_eval(Qh, K, V, Kh, Vh, o_base=O, diag=d2, rows=rows, **knobs)
+    assert sorted(d2) == sorted((h, t) for h in range(Hq) for t in rows)
+    for key, (idx, sc) in d2.items():
+        assert np.array_equal(idx, d1[key][0]), key
+        assert np.abs(sc - d1[key][1]).max() <= 1e-5 * np.abs(d1[key][1]).max(), key
+    ulp = np.spacing(np.abs(full[rows]).astype(F16)).astype(F32)
+    assert np.all(np.abs(part[rows].astype(F32) - full[rows].astype(F32)) <= ulp)
+    others = [t for t in range(T) if t not in rows]
+    assert np.array_equal(part[others], O.transpose(1, 0, 2)[others])
+
+
+def test_pack_8bit_closed_form():
+    """pack_8bit / unpack_8bit and the 8-bit branches of pack_residual /
+    unpack_residual (residual_store.py:149-176): s = max|x| / 127 in fp32,
+    codes = clamp(round-half-even(x / s), -128, 127) as int8, stored scale
+    half(s), unpack = code * float(half(s)).  Checked on values whose codes
+    the closed form fixes (s = 1 exactly; ties to even), on the all-zero
+    block (1e-8 floor: every code 0, the fp16 scale underflows to 0), and on
+    random blocks through the round-trip bound |x - x'| <= s / 2 + the fp16
+    scale's rounding."""
+    x = np.array([127, -127, 63.5, 62.5, 0.4, -0.6, -1.5, 0], F32)
+    codes, scale = Q.pack_8bit(x)
+    assert codes.dtype == np.int8 and scale.dtype == F16 and float(scale) == 1.0
+    assert codes.tolist() == [127, -127, 64, 62, 0, -1, -2, 0]
+    assert np.array_equal(Q.unpack_8bit(codes, scale, 8), codes.astype(F32))
+    for bits, pk, uk in ((8, Q.pack_8bit, Q.unpack_8bit), (4, Q.pack_4bit, Q.unpack_4bit)):
+        a, sa = Q.pack_residual(x, bits)
+        b, sb = pk(x)
+        assert np.array_equal(a, b) and sa == sb, bits
+        assert np.array_equal(Q.unpack_residual(a, sa, 8, bits), uk(b, sb, 8)), bits
+    z, sz = Q.pack_8bit(np.zeros((4, 64), F32))
+    assert z.shape == (256,) and not z.any() and float(sz) == 0.0
+    rng = np.random.default_rng(8)
+    for _ in range(20):
+        blk = (rng.standard_normal((4, 64)) * np.exp(rng.standard_normal())).astype(F32)
+        c, s = Q.pack_8bit(blk)
+        s32 = F32(F32(np.abs(blk).max()) / F32(127.0))
+        assert np.array_equal(c, np.clip(np.rint(blk / s32), -128, 127).astype(np.int8).ravel())
+        back = Q.unpack_8bit(c, s, blk.size).reshape(blk.shape)
+        assert np.all(np.abs(back - blk) <= s32 / 2 + 127 * abs(float(s) - float(s32)) + 1e-6)
+
+
+def test_layer_budget_multiplier_closed_form():
+    """layer_budget_multiplier (cache.py:166-202) in the oracle and in the
+    product (care_kv.config): uniform and one layer give 1; u_shaped gives
+    w_l = 0.5 + 1.5 |2 l / (L - 1) - 1| over its mean (L = 3: 4/3, 1/3, 4/3;
+    L = 5: w = 2, 1.25, 0.5, 1.25, 2 over 1.4), whose mean is 1;
+    sensitivity gives s_l / mean(s), or 1 when the mean is not positive;
+    layer_head_impact is uniform-equivalent."""
+    from oracle.cache import layer_budget_multiplier as olbm
+    from care_kv.config import CacheConfig, layer_budget_multiplier as plbm
+
+    def both(L, policy, sens=None):
+        oc = OCfg(num_layers=L, num_heads=4, num_kv_heads=2, head_dim=64, budget_policy=policy,
+                  layer_sensitivity=sens)
+        pc = CacheConfig(num_layers=L, num_heads=4, num_kv_heads=2, head_dim=64, budget_policy=policy,
+                         layer_sensitivity=sens)
+        o = [olbm(oc, l) for l in range(L)]
+        p = [plbm(pc, l) for l in range(L)]
+        assert np.allclose(o, p, rtol=0, atol=1e-15), (L, policy, o, p)
+        return o
+
+    assert both(4, "uniform") == [1.0] * 4
+    assert both(1, "u_shaped") == [1.0] and both(1, "sensitivity", [3.0]) == [1.0]
+    assert np.allclose(both(3, "u_shaped"), [4 / 3, 1 / 3, 4 / 3], rtol=1e-14)
+    assert np.allclose(both(5, "u_shaped"), np.array([2, 1.25, 0.5, 1.25, 2]) / 1.4, rtol=1e-14)
+    assert abs(np.mean(both(22, "u_shaped")) - 1.0) < 1e-12
+    assert np.allclose(both(3, "sensitivity", [1.0, 2.0, 3.0]), [0.5, 1.0, 1.5], rtol=1e-14)
+    assert both(3, "sensitivity", [0.0, 0.0, 0.0]) == [1.0] * 3
+    assert both(3, "sensitivity", [1.0, -2.0, 0.5]) == [1.0] * 3
+    assert both(3, "layer_head_impact") == [1.0] * 3
