@@ -107,7 +107,7 @@ def load(path: str | None = None):
         vp, i32, i64 = C.c_void_p, C.c_int32, C.c_int64
         lib.carekv_last_error.restype = C.c_char_p
         lib.carekv_store_workspace_bytes.restype = i64
-        lib.carekv_store_workspace_bytes.argtypes = [i32]
+        lib.carekv_store_workspace_bytes.argtypes = [C.POINTER(Arena), C.POINTER(StoreParams), i32]
         lib.carekv_store_pages.restype = C.c_int
         lib.carekv_store_pages.argtypes = [C.POINTER(Arena), C.POINTER(StoreParams), vp, vp, vp, i32, vp, i32, vp, vp]
         lib.carekv_append_rows.restype = C.c_int
@@ -163,6 +163,15 @@ def check(rc: int, what: str):
     if rc != 0:
         msg = load().carekv_last_error()
         raise CarekvError(f"{what} failed (code {rc}): {msg.decode() if msg else ''}")
+
+
+def store_workspace_bytes(lib, arena, sp, n_jobs: int) -> int:
+    """carekv_store_workspace_bytes for a call with this arena, these store
+    params and n_jobs page jobs (raises on an invalid argument)."""
+    n = int(lib.carekv_store_workspace_bytes(arena, sp, int(n_jobs)))
+    if n < 0:
+        check(-1, "carekv_store_workspace_bytes")
+    return n
 
 
 def check_enabled() -> bool:

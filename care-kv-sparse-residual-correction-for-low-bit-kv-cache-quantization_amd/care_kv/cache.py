@@ -431,8 +431,8 @@ class CAREKVCache:
         if kivi_in is not None:
             sp.k_codes_in, sp.v_codes_in, sp.v_scale_in = (t.data_ptr() for t in kivi_in)
         lib = _lib.load()
-        ws = self.workspace("store", int(lib.carekv_store_workspace_bytes(len(jobs))))
         a = self.arena(layer)
+        ws = self.workspace("store", _lib.store_workspace_bytes(lib, a, sp, len(jobs)))
         _lib.check(lib.carekv_store_pages(a, sp, Kp.data_ptr(), Vp.data_ptr(), jobs_d.data_ptr(), len(jobs),
                                           gp_d.data_ptr(), B, ws.data_ptr(), _lib.stream_ptr(self.device)),
                    "carekv_store_pages")
@@ -566,7 +566,7 @@ class CAREKVCache:
                 Vhat = self.vcodes[layer, hi, si, pi].view(F16).contiguous().view(-1, cfg.head_dim)
             sp.k_hat, sp.v_hat = Khat.data_ptr(), Vhat.data_ptr()
         lib = _lib.load()
-        ws = self.workspace("store", int(lib.carekv_store_workspace_bytes(len(jobs))))
+        ws = self.workspace("store", _lib.store_workspace_bytes(lib, self.arena(layer), sp, len(jobs)))
         jobs_d = to_device(jobs, self.device)
         gp_d = to_device(group_ptr, self.device)
         _lib.check(lib.carekv_store_pages(self.arena(layer), sp, Kp.data_ptr(), Vp.data_ptr(), jobs_d.data_ptr(),

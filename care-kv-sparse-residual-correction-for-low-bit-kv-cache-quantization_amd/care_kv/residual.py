@@ -107,7 +107,7 @@ class ResidualStoreManager:
         jobs_d = torch.from_numpy(jobs).to(cache.device)
         gp = torch.tensor([0, 1], dtype=torch.int32, device=cache.device)
         lib = _lib.load()
-        ws = cache.workspace("store", int(lib.carekv_store_workspace_bytes(1)))
+        ws = cache.workspace("store", _lib.store_workspace_bytes(lib, cache.arena(self.layer_id), sp, 1))
         _lib.check(lib.carekv_store_pages(cache.arena(self.layer_id), sp, Ko.data_ptr(), Vo.data_ptr(),
                                           jobs_d.data_ptr(), 1, gp.data_ptr(), 1, ws.data_ptr(),
                                           _lib.stream_ptr(cache.device)), "carekv_store_pages (process_page)")

@@ -57,483 +57,898 @@ __device__ __forceinline__ int8_t scale_code(float s, float m) {
   return (int8_t)fminf(fmaxf(rintf(q), -128.f), 127.f);
 }
 
-// Store decision for one page: candidate order by prior (double, stable,
-// descending), prior > 0 only, per-kind budgets or joint budget
-// (residual_store.py:372-422).  sel_k/sel_v receive candidate indices in
-// slot-allocation order; returns counts.
-template <int NCG>
-__device__ __forceinline__ void select_candidates(const float* kerr, const float* verr,
-                                                  const carekv_store_params& sp, double struct_prior,
-                                                  int* sel_k, int& nk, int* sel_v, int& nv, int* order_kind,
-                                                  int* order_idx, int& n_order) {
-  double pk[NCG], pv[kVtb];
-  int ik[NCG], iv[kVtb];
-#pragma unroll
-  for (int i = 0; i < NCG; ++i) { pk[i] = (double)kerr[i] * sp.sensitivity * struct_prior; ik[i] = i; }
-#pragma unroll
-  for (int i = 0; i < kVtb; ++i) { pv[i] = (double)verr[i] * sp.sensitivity * struct_prior; iv[i] = i; }
-  // stable insertion sort, descending
-  for (int i = 1; i < NCG; ++i)
-    for (int j = i; j > 0 && pk[j] > pk[j - 1]; --j) {
-      double t = pk[j]; pk[j] = pk[j - 1]; pk[j - 1] = t;
-      int u = ik[j]; ik[j] = ik[j - 1]; ik[j - 1] = u;
-    }
-  for (int i = 1; i < kVtb; ++i)
-    for (int j = i; j > 0 && pv[j] > pv[j - 1]; --j) {
-      double t = pv[j]; pv[j] = pv[j - 1]; pv[j - 1] = t;
-      int u = iv[j]; iv[j] = iv[j - 1]; iv[j - 1] = u;
-    }
-  int pos_k = 0, pos_v = 0;
-  for (int i = 0; i < NCG; ++i) pos_k += pk[i] > 0.0;
-  for (int i = 0; i < kVtb; ++i) pos_v += pv[i] > 0.0;
-  nk = nv = n_order = 0;
-  if (sp.store_none) return;
-  if (sp.joint) {
-    // merge the two sorted positive lists, K before V on equal priors
-    int a = 0, b = 0;
-    while (n_order < sp.joint_budget && (a < pos_k || b < pos_v)) {
-      const bool take_k = (b >= pos_v) || (a < pos_k && pk[a] >= pv[b]);
-      if (take_k) { order_kind[n_order] = 0; order_idx[n_order++] = ik[a]; sel_k[nk++] = ik[a++]; }
-      else        { order_kind[n_order] = 1; order_idx[n_order++] = iv[b]; sel_v[nv++] = iv[b++]; }
-    }
+// ---------------------------------------------------------------- page store
+// One wave stores one page job in a single pass over the page's K and V
+// rows (residual_store.py:239-464 after the page write of cache.py:592-654):
+// codes, scales and masters, the residuals, the candidate errors and K
+// sketches, the store decision, and the 4-bit payloads of the selected
+// candidates, which go to a per-job staging area of the workspace.  A scan
+// then gives each job its slot ids in call order and a scatter moves the
+// staged payloads to their slots.
+//
+// Lane layout: lane l holds, for chunk i = 0..3, token t = 4 i + l / 16 and
+// the EPL = D / 16 channels EPL * (l % 16) .. + EPL - 1 of that token.  A
+// chunk is thus one V candidate block (4 tokens), and a quant group (32
+// channels of one row) is LPG = 32 / EPL consecutive lanes; a K candidate
+// (one 32-channel group over 16 tokens) is the LPG-lane group of every row
+// in every chunk.
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kNvb = kPage / kVtb;  // V candidate blocks per page
+
+enum StorePath : int {
+  kPathFresh = 0,    // quantize K / V and write the packed page
+  kPathKeep = 1,     // streaming fill store: the page keeps its codes and scales
+  kPathCodesIn = 2,  // process_page on the caller's codes and fp16 scales
+  kPathKivi = 3,     // packed KIVI prefix page: given 2-bit codes, V scales, K_hat / V_hat
+  kPathHat = 4,      // fp16 side-buffer base: given K_hat / V_hat rows
+};
+
+template <int D>
+struct PageLay {
+  static constexpr int EPL = D / 16;              // fp16 values per lane and chunk
+  static constexpr int NP = EPL / 2;              // fp16 pairs per lane and chunk
+  static constexpr int LPG = kGroup / EPL;        // lanes per quant group
+  static constexpr int NG = D / kGroup;           // quant groups (= K candidates) per row
+  static constexpr int P = kPage * NG;            // (token, group) pairs per page
+  static constexpr int KSB = kPage * kGroup / 2;  // 4-bit K slot bytes
+  static constexpr int VSB = kVtb * D / 2;        // 4-bit V slot bytes
+};
+
+// LDS of one wave of the store pass.
+template <int D>
+struct StoreLds {
+  uint16_t rk[kPage * D];          // K residual rows (fp16 bits), token-major
+  float mean[D];                   // K residual column means
+  uint16_t sf[kPage * D / kGroup]; // group scales by (token, group)
+  uint16_t svr[kPage * D / kGroup];// V group scales as the decode reads them back
+};
+
+// Staged decisions and payloads of one call, in the workspace after the job
+// records: per job a header word (bits 0-2 K count, 3-5 V count, 6-8 and
+// 9-11 the counts of reused K / V ids, 12-19 and 20-27 the candidate index
+// of each K / V selection in slot order, 2 bits each), up to mk K and mv V
+// payloads and their fp16 scales (K first).
+struct StoreStage {
+  uint32_t* head;
+  int8_t* kpay;
+  int8_t* vpay;
+  uint16_t* scale;
+  int mk, mv;
+};
+
+// Most selections of one kind a page can make under the call's budgets.
+__host__ __device__ inline void store_caps(const carekv_store_params& sp, int ng, int* mk, int* mv) {
+  if (sp.store_none) {
+    *mk = *mv = 0;
+    return;
+  }
+  const int kb = sp.joint ? sp.joint_budget : sp.k_budget;
+  const int vb = sp.joint ? sp.joint_budget : sp.v_budget;
+  *mk = kb < 0 ? 0 : (kb > ng ? ng : kb);
+  *mv = vb < 0 ? 0 : (vb > kNvb ? kNvb : vb);
+}
+
+// ---- cross-lane helpers (all 64 lanes active)
+constexpr int kDppXor1 = 0xB1;         // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;         // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;  // lane i <- 7 - i within 8
+constexpr int kDppMirror = 0x140;      // lane i <- 15 - i within 16
+constexpr int kDppShl1 = 0x101;        // lane i <- lane i + 1 of its row
+constexpr int kDppShl2 = 0x102;        // lane i <- lane i + 2 of its row
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __uint_as_float(dpp_u<CTRL>(__float_as_uint(v)));
+}
+// Sum / max over aligned N-lane groups of a 16-lane row (N = 1, 2, 4, 8, 16);
+// every lane of a group ends with the same bits (the ops commute).
+template <int N>
+__device__ __forceinline__ float grp_sum(float v) {
+  if constexpr (N >= 2) v += dpp_f<kDppXor1>(v);
+  if constexpr (N >= 4) v += dpp_f<kDppXor2>(v);
+  if constexpr (N >= 8) v += dpp_f<kDppHalfMirror>(v);
+  if constexpr (N >= 16) v += dpp_f<kDppMirror>(v);
+  return v;
+}
+template <int N>
+__device__ __forceinline__ uint32_t grp_max_u(uint32_t v) {
+  if constexpr (N >= 2) v = max(v, dpp_u<kDppXor1>(v));
+  if constexpr (N >= 4) v = max(v, dpp_u<kDppXor2>(v));
+  if constexpr (N >= 8) v = max(v, dpp_u<kDppHalfMirror>(v));
+  if constexpr (N >= 16) v = max(v, dpp_u<kDppMirror>(v));
+  return v;
+}
+// Sum / max over the four rows (lanes c, c+16, c+32, c+48) with the gfx950
+// lane swaps: the two halves of each swap hold a pair in some order.
+__device__ __forceinline__ float rows_sum(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+__device__ __forceinline__ uint32_t rows_max_u(uint32_t v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = max((uint32_t)a[0], (uint32_t)a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  return max((uint32_t)b[0], (uint32_t)b[1]);
+}
+
+// half(x / s) for the fp16 group scale s > 0 (rc = rcp(s)), the quotient
+// of quantizer.py:58.  q1 is one Newton step from x * rc, within 0.5 ulp
+// (fp32) plus a 2^-45 relative term of x / s.  x and s are fp16 values, so
+// x / s lies no closer than 2^-23 relative (one fp32 ulp) to a midpoint of
+// two fp16 values: with odd parts X, S of x, s and an fp16 midpoint m with
+// 12-bit odd part M, x = m s would need X = M S >= 2^11, and otherwise
+// |x - m s| is at least one unit of m s's last place.  q1 is therefore on
+// the same side of every fp16 rounding boundary as x / s, and half(q1) =
+// half(x / s), the rounding of the reference's float32 quotient (float32
+// carries more than 2 * 11 + 2 bits, so its quotient rounds to fp16 as the
+// exact one does).
+__device__ __forceinline__ _Float16 quant_q(float x, float s, float rc) {
+  // x * rc as an fma with a +0 addend (which takes x as fp16; it differs
+  // from the product only in the sign of a zero, which the code drops)
+  const float q0 = __builtin_fmaf(x, rc, 0.0f);
+  const float e = __builtin_fmaf(-q0, s, x);
+  return (_Float16)__builtin_fmaf(e, rc, q0);
+}
+// The group scale half(m / qmax) (quantizer.py:55) for the fp16 max m: the
+// same Newton quotient (m and qmax are fp16 values).
+template <int BITS>
+__device__ __forceinline__ _Float16 group_scale(float m) {
+  constexpr int qmax = (1 << (BITS - 1)) - 1;
+  if constexpr (qmax == 1) {
+    return (_Float16)m;
   } else {
-    const int kb = min(sp.k_budget, pos_k), vb = min(sp.v_budget, pos_v);
-    for (int i = 0; i < kb; ++i) { order_kind[n_order] = 0; order_idx[n_order++] = ik[i]; sel_k[nk++] = ik[i]; }
-    for (int i = 0; i < vb; ++i) { order_kind[n_order] = 1; order_idx[n_order++] = iv[i]; sel_v[nv++] = iv[i]; }
+    constexpr float rq = 1.0f / (float)qmax;
+    return quant_q(m, (float)qmax, rq);
+  }
+}
+// Codes enter the page biased by 1536: for an fp16 q with |q| < 512, the
+// fp16 sum q + 1536 lies in [1024, 2048), where fp16 steps by 1, so it is
+// 1536 + rint(q) (round half to even: 1536 is even); its bits are
+// 0x6600 + code, whose low BITS bits are the code's two's complement.
+// With a normal scale s = half(m / qmax) and |x| <= m, |x / s| <= qmax
+// (1 + 2^-11) rounds to at most qmax: the clamp binds only for subnormal
+// scales (CLAMP).
+constexpr float kCodeBias = 1536.f;
+template <int BITS, bool CLAMP>
+__device__ __forceinline__ h2_t biased_codes(h2_t q) {
+  constexpr int qmax = (1 << (BITS - 1)) - 1;
+  const h2_t y = q + h2_t{(_Float16)kCodeBias, (_Float16)kCodeBias};
+  if constexpr (!CLAMP) return y;
+  return __builtin_elementwise_min(__builtin_elementwise_max(y, h2_t{(_Float16)(kCodeBias - qmax - 1), (_Float16)(kCodeBias - qmax - 1)}),
+                                   h2_t{(_Float16)(kCodeBias + qmax), (_Float16)(kCodeBias + qmax)});
+}
+// The biased code of x for a zero scale (a group whose max |x| rounds to 0
+// in fp16): x / 0 is +-inf (clamped) or NaN for x = 0 (coded 0).
+template <int BITS>
+__device__ __forceinline__ _Float16 biased_code_zero(float x) {
+  constexpr int qmax = (1 << (BITS - 1)) - 1;
+  return (_Float16)(kCodeBias + (x > 0.f ? (float)qmax : (x < 0.f ? (float)(-qmax - 1) : 0.f)));
+}
+
+// 4-bit residual code of x against the fp32 slot scale s (residual_store.py
+// :121-136): clamp(rint(x / s), -8, 7) with x / s rounded to fp32.  The
+// Newton quotient q1 is within 1.5 fp32 ulps of the rounded quotient, so the
+// two round to the same integer unless q1 lies within 2^-18 of a half
+// integer; such lanes take the exact quotient (amb).
+__device__ __forceinline__ int res_code(float x, float s, float rc, bool& amb) {
+  const float q0 = __builtin_fmaf(x, rc, -0.0f);
+  const float e = __builtin_fmaf(-q0, s, x);
+  const float q1 = __builtin_fmaf(e, rc, q0);
+  const float c = rintf(q1);
+  amb = amb || fabsf(q1 - c) > 0.5f - 0x1p-18f;
+  return (int)fminf(fmaxf(c, -8.f), 7.f);
+}
+__device__ __forceinline__ int res_code_exact(float x, float s) {
+  return (int)fminf(fmaxf(rintf(x / s), -8.f), 7.f);
+}
+
+// Pack 2m fp16 residuals of this lane as 4-bit codes against slot scale s:
+// code k at bits 4k (pack_4bit's low nibble first).
+template <int NPAIR>
+__device__ __forceinline__ uint32_t pack_res(const h2_t* v, float s) {
+  const float rc = __builtin_amdgcn_rcpf(s);
+  bool amb = false;
+  uint32_t w = 0;
+#pragma unroll
+  for (int p = 0; p < NPAIR; ++p) {
+    const int c0 = res_code((float)v[p][0], s, rc, amb), c1 = res_code((float)v[p][1], s, rc, amb);
+    w |= (((uint32_t)c0 & 15u) | (((uint32_t)c1 & 15u) << 4)) << (8 * p);
+  }
+  if (amb) {
+    w = 0;
+#pragma unroll
+    for (int p = 0; p < NPAIR; ++p) {
+      const int c0 = res_code_exact((float)v[p][0], s), c1 = res_code_exact((float)v[p][1], s);
+      w |= (((uint32_t)c0 & 15u) | (((uint32_t)c1 & 15u) << 4)) << (8 * p);
+    }
+  }
+  return w;
+}
+
+// Max |v| over this lane's NPAIR fp16 pairs as fp16 magnitude bits.
+template <int NPAIR>
+__device__ __forceinline__ uint32_t absmax_bits(const h2_t* v) {
+  u16x2_t m = {0, 0};
+#pragma unroll
+  for (int p = 0; p < NPAIR; ++p)
+    m = __builtin_elementwise_max(m, __builtin_bit_cast(u16x2_t, __builtin_bit_cast(uint32_t, v[p]) & 0x7fff7fffu));
+  return max((uint32_t)m[0], (uint32_t)m[1]);
+}
+
+// Store this lane's W = EPL * BITS code bits F of chunk i.  The page's
+// packed rows are one little-endian bit string in which lane l of chunk i
+// holds bits [(64 i + l) W, +W); each dword is written whole by one lane.
+template <int D, int BITS>
+__device__ __forceinline__ void store_code_bits(int8_t* page_rows, int i, int lane, uint32_t F) {
+  constexpr int W = (D / 16) * BITS;
+  uint32_t* base = reinterpret_cast<uint32_t*>(page_rows) + i * 2 * W;  // chunk i: 64 W bits
+  if constexpr (W == 32) {
+    base[lane] = F;
+  } else if constexpr (W == 16) {
+    const uint32_t n = dpp_u<kDppShl1>(F);
+    if (!(lane & 1)) base[lane >> 1] = F | (n << 16);
+  } else if constexpr (W == 8) {
+    const uint32_t a = F | (dpp_u<kDppShl1>(F) << 8);
+    const uint32_t b = a | (dpp_u<kDppShl2>(a) << 16);
+    if (!(lane & 3)) base[lane >> 2] = b;
+  } else if constexpr (W == 24) {  // a quad holds 96 bits = 3 dwords
+    const uint32_t n = dpp_u<kDppShl1>(F);
+    const int p = lane & 3;
+    if (p < 3) base[3 * (lane >> 2) + p] = (F >> (8 * p)) | (n << (24 - 8 * p));
+  } else {
+    static_assert(W == 12, "code field width");
+    const uint32_t G = F | (dpp_u<kDppShl1>(F) << 12);  // lane pairs: 24 bits
+    const uint32_t n = dpp_u<kDppShl2>(G);
+    const int p = (lane & 7) >> 1;
+    if (!(lane & 1) && p < 3) base[3 * (lane >> 3) + p] = (G >> (8 * p)) | (n << (24 - 8 * p));
+  }
+}
+// Read back this lane's W code bits of chunk i (the layout above).
+template <int D, int BITS>
+__device__ __forceinline__ uint32_t load_code_bits(const int8_t* page_rows, int i, int lane) {
+  constexpr int W = (D / 16) * BITS;
+  const uint32_t* w = reinterpret_cast<const uint32_t*>(page_rows);
+  const int bit = (64 * i + lane) * W;
+  const int wi = bit >> 5, sh = bit & 31;
+  uint64_t v = w[wi];
+  if (sh + W > 32) v |= (uint64_t)w[wi + 1] << 32;
+  return (uint32_t)(v >> sh) & (uint32_t)((1ull << W) - 1ull);
+}
+
+template <int NP>
+__device__ __forceinline__ void load_chunk(uint32_t* w, const uint16_t* p) {
+  if constexpr (NP == 4) {
+    const uint4 v = *reinterpret_cast<const uint4*>(p);
+    w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+  } else {
+    const uint2 v = *reinterpret_cast<const uint2*>(p);
+    w[0] = v.x; w[1] = v.y;
+  }
+}
+template <int NP>
+__device__ __forceinline__ void store_chunk(uint16_t* p, const uint32_t* w) {
+  if constexpr (NP == 4) *reinterpret_cast<uint4*>(p) = make_uint4(w[0], w[1], w[2], w[3]);
+  else *reinterpret_cast<uint2*>(p) = make_uint2(w[0], w[1]);
+}
+// EPL int8 codes at p as fp16 pairs.
+template <int NP>
+__device__ __forceinline__ void load_codes_i8(h2_t* c, const int8_t* p) {
+  uint32_t w[(NP + 1) / 2];
+  if constexpr (NP == 4) {
+    const uint2 v = *reinterpret_cast<const uint2*>(p);
+    w[0] = v.x; w[1] = v.y;
+  } else {
+    w[0] = *reinterpret_cast<const uint32_t*>(p);
+  }
+#pragma unroll
+  for (int q = 0; q < NP; ++q) {
+    const int32_t a = (int32_t)(w[q >> 1] << (24 - 16 * (q & 1))) >> 24;
+    const int32_t b = (int32_t)(w[q >> 1] << (16 - 16 * (q & 1))) >> 24;
+    c[q] = h2_t{(_Float16)a, (_Float16)b};
+  }
+}
+// Biased fp16 code pairs (1536 + code) -> the W-bit field with code k at
+// bits BITS k: the low BITS bits of each half, weighted by dot2.
+template <int BITS, int NP>
+__device__ __forceinline__ uint32_t code_field(const h2_t* y) {
+  constexpr uint32_t M = (1u << BITS) - 1u;
+  constexpr int P0 = (15 / BITS - 1) / 2 + 1;  // pairs whose weights fit 16 bits
+  uint32_t lo = 0, hi = 0;
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const u16x2_t z = __builtin_bit_cast(u16x2_t, __builtin_bit_cast(uint32_t, y[p]) & (M | (M << 16)));
+    const int q = p < P0 ? p : p - P0;
+    const u16x2_t wgt = {(unsigned short)(1u << (2 * q * BITS)), (unsigned short)(1u << ((2 * q + 1) * BITS))};
+    if (p < P0) lo = __builtin_amdgcn_udot2(z, wgt, lo, false);
+    else hi = __builtin_amdgcn_udot2(z, wgt, hi, false);
+  }
+  if constexpr (NP > P0) return lo | (hi << (2 * P0 * BITS));
+  else return lo;
+}
+// The W-bit field -> fp16 code pairs (sign-extended BITS-bit fields).
+template <int BITS, int NP>
+__device__ __forceinline__ void field_codes(uint32_t F, h2_t* c) {
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    const int a = (int)(F << (32 - BITS * (2 * p + 1))) >> (32 - BITS);
+    const int b = (int)(F << (32 - BITS * (2 * p + 2))) >> (32 - BITS);
+    c[p] = h2_t{(_Float16)a, (_Float16)b};
   }
 }
 
-// One wave per page job.  Lane l handles token t = l / NG, quant group g = l % NG.
-// MODE 0: write base + metadata + counts.  MODE 1: write residual slots.
-template <int D, int BITS, int MODE>
-__global__ __launch_bounds__(256) void store_pages_kernel(carekv_arena A, carekv_store_params sp,
-                                                          const uint16_t* __restrict__ Kx,
-                                                          const uint16_t* __restrict__ Vx,
-                                                          const carekv_page_job* __restrict__ jobs,
-                                                          int n_jobs, StoreWs ws) {
-  constexpr int NG = D / 32;       // quant groups == K channel groups
-  constexpr int RB = row_bytes(D, BITS);
-  constexpr int CB = 4 * BITS;     // packed bytes per 32 codes
-  const int lane = threadIdx.x & 63;
-  const int job_id = blockIdx.x * 4 + (threadIdx.x >> 6);
-  // the call's slot-overflow word (after the job records) starts clear in
-  // the count pass; the write pass sets it
-  if (MODE == 0 && blockIdx.x == 0 && threadIdx.x == 0) ws.v[n_jobs * 4] = 0;
-  if (job_id >= n_jobs) return;
-  const carekv_page_job job = jobs[job_id];
-  const int t = lane / NG, g = lane % NG;
-  const bool active = t < kPage;
+// One kind (K or V) of one page: the residual base, the page write
+// (codes, scales, master) where the path writes the page, and the
+// residual chunks, zero past num_valid.  sq[i]: this lane's partial sum of
+// squared residuals of chunk i; vsq: its partial sum of V_hat^2 over the
+// valid rows as the decode reads them (V only).
+template <int D, int BITS, int PATH, bool IS_V>
+__device__ __forceinline__ void store_kind(const carekv_arena& A, const carekv_store_params& sp,
+                                           const uint32_t (&x)[4][PageLay<D>::NP], h2_t (&res)[4][PageLay<D>::NP],
+                                           float (&sq)[4], float& vsq, StoreLds<D>& S, int lane, long pg,
+                                           int job_id, int nvld) {
+  using L = PageLay<D>;
+  constexpr int EPL = L::EPL, NP = L::NP, LPG = L::LPG, NG = L::NG, P = L::P;
+  const int r = lane >> 4, c16 = lane & 15, gl = c16 / LPG, j = c16 % LPG;
+  const long tile = (long)job_id * kPage * D;
+  const long rows = (long)job_id * kPage;  // first input row of the job
+  _Float16 s[4] = {0, 0, 0, 0};            // the rows' group scales (code paths)
+  h2_t base[4][NP], code[4][NP];
+  uint32_t field[4];                       // packed code bits (page-writing paths)
+  _Float16 svr[4] = {0, 0, 0, 0};          // V: scale of V_hat as read back
+
+  if constexpr (PATH == kPathHat || PATH == kPathKivi) {
+    const uint16_t* hat = IS_V ? sp.v_hat : sp.k_hat;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t w[NP];
+      load_chunk<NP>(w, hat + tile + (long)(4 * i + r) * D + EPL * c16);
+#pragma unroll
+      for (int p = 0; p < NP; ++p) base[i][p] = __builtin_bit_cast(h2_t, w[p]);
+    }
+  }
+  if constexpr (PATH == kPathFresh) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      // max |x| over the group (exact), scale = half(max / qmax)
+      const uint32_t m = grp_max_u<LPG>(absmax_bits<NP>(reinterpret_cast<const h2_t*>(x[i])));
+      s[i] = group_scale<BITS>(h2f((uint16_t)m));
+      const float sf = (float)s[i];
+      const float rc = __builtin_amdgcn_rcpf(sf);
+      h2_t y[NP];  // 1536 + clamp(rint(half(x / s))) (quantizer.py:58-60)
+      if (sf >= 0x1p-14f) {
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+          const h2_t xh = __builtin_bit_cast(h2_t, x[i][p]);
+          y[p] = biased_codes<BITS, false>(h2_t{quant_q((float)xh[0], sf, rc), quant_q((float)xh[1], sf, rc)});
+        }
+      } else if (sf != 0.f) {
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+          const h2_t xh = __builtin_bit_cast(h2_t, x[i][p]);
+          y[p] = biased_codes<BITS, true>(h2_t{quant_q((float)xh[0], sf, rc), quant_q((float)xh[1], sf, rc)});
+        }
+      } else {
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+          const h2_t xh = __builtin_bit_cast(h2_t, x[i][p]);
+          y[p] = h2_t{biased_code_zero<BITS>((float)xh[0]), biased_code_zero<BITS>((float)xh[1])};
+        }
+      }
+      field[i] = code_field<BITS, NP>(y);
+#pragma unroll
+      for (int p = 0; p < NP; ++p) code[i][p] = y[p] - h2_t{(_Float16)kCodeBias, (_Float16)kCodeBias};
+    }
+  } else if constexpr (PATH == kPathKeep) {
+    // the page's own base as the decode reads it: half(code * half(scale code * master))
+    const int8_t* prow = (IS_V ? A.vcodes : A.kcodes) + pg * kPage * row_bytes(D, BITS);
+    const float mst = A.scale_mode == 1 ? h2f((IS_V ? A.vmaster : A.kmaster)[pg]) : 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      field_codes<BITS, NP>(load_code_bits<D, BITS>(prow, i, lane), code[i]);
+      const long si = (pg * kPage + 4 * i + r) * NG + gl;
+      const void* sc = IS_V ? A.vscale : A.kscale;
+      s[i] = A.scale_mode == 1 ? (_Float16)((float)((const int8_t*)sc)[si] * mst)
+                               : bits2half(((const uint16_t*)sc)[si]);
+      svr[i] = s[i];
+    }
+  } else if constexpr (PATH == kPathCodesIn || PATH == kPathKivi) {
+    const int8_t* cin = IS_V ? sp.v_codes_in : sp.k_codes_in;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      load_codes_i8<NP>(code[i], cin + tile + (long)(4 * i + r) * D + EPL * c16);
+      const long ri = (rows + 4 * i + r) * NG + gl;
+      if constexpr (PATH == kPathCodesIn) {
+        s[i] = bits2half((IS_V ? sp.v_scale_in : sp.k_scale_in)[ri]);
+        if (IS_V) {  // V_hat as the page holds it (write_base's scales)
+          const long si = (pg * kPage + 4 * i + r) * NG + gl;
+          svr[i] = A.scale_mode == 1 ? (_Float16)((float)((const int8_t*)A.vscale)[si] * h2f(A.vmaster[pg]))
+                                     : bits2half(((const uint16_t*)A.vscale)[si]);
+        }
+      } else {
+        s[i] = IS_V ? bits2half(sp.v_scale_in[ri]) : (_Float16)0;  // KIVI K: per-channel scales elsewhere
+      }
+    }
+  }
+
+  if constexpr (PATH == kPathFresh || PATH == kPathKivi) {
+    // ---- the page: packed codes, scales by (token, group), master
+    int8_t* prow = (IS_V ? A.vcodes : A.kcodes) + pg * kPage * row_bytes(D, BITS);
+    if constexpr (PATH == kPathKivi) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        h2_t y[NP];
+#pragma unroll
+        for (int p = 0; p < NP; ++p) y[p] = code[i][p] + h2_t{(_Float16)kCodeBias, (_Float16)kCodeBias};
+        field[i] = code_field<BITS, NP>(y);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) store_code_bits<D, BITS>(prow, i, lane, field[i]);
+    if (j == 0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) S.sf[(4 * i + r) * NG + gl] = half2bits(s[i]);
+    }
+    lds_sync_wave();
+    const int pl = lane % P;
+    const _Float16 sp_ = bits2half(S.sf[pl]);
+    void* sc = IS_V ? A.vscale : A.kscale;
+    if (A.scale_mode == 1) {
+      // int8 codes against half(max scale / 127) (cache.py:592-606)
+      const float m = h2f((uint16_t)rows_max_u(grp_max_u<16>(half2bits(sp_))));
+      const _Float16 mh = (_Float16)(m / 127.f);
+      const int8_t q = scale_code((float)sp_, (float)mh);
+      if (lane < P) ((int8_t*)sc)[pg * kPage * NG + pl] = q;
+      if (lane == 0) (IS_V ? A.vmaster : A.kmaster)[pg] = half2bits(mh);
+      if constexpr (IS_V) {
+        if (lane < P) S.svr[pl] = half2bits((_Float16)((float)q * (float)mh));
+        lds_sync_wave();
+#pragma unroll
+        for (int i = 0; i < 4; ++i) svr[i] = bits2half(S.svr[(4 * i + r) * NG + gl]);
+      }
+    } else {
+      if (lane < P) ((uint16_t*)sc)[pg * kPage * NG + pl] = half2bits(sp_);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) svr[i] = s[i];
+    }
+  }
+
+  // ---- residuals (R = half(X - X_hat), residual_store.py:276-285), zero past num_valid
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const h2_t s2 = h2_t{s[i], s[i]};
+    float a = 0.f, vs = 0.f;
+    const uint32_t keep = 4 * i + r < nvld ? ~0u : 0u;  // rows past num_valid: zero
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const h2_t xh = __builtin_bit_cast(h2_t, x[i][p]);
+      h2_t b;
+      if constexpr (PATH == kPathHat || PATH == kPathKivi) b = base[i][p];
+      else b = code[i][p] * s2;
+      const h2_t rr = __builtin_bit_cast(h2_t, __builtin_bit_cast(uint32_t, xh - b) & keep);
+      res[i][p] = rr;
+      a = __builtin_amdgcn_fdot2(rr, rr, a, false);
+      if constexpr (IS_V) {
+        h2_t vh;
+        if constexpr (PATH == kPathHat) vh = base[i][p];
+        else if constexpr (PATH == kPathKeep) vh = b;
+        else vh = code[i][p] * h2_t{svr[i], svr[i]};
+        vh = __builtin_bit_cast(h2_t, __builtin_bit_cast(uint32_t, vh) & keep);
+        vs = __builtin_amdgcn_fdot2(vh, vh, vs, false);
+      }
+    }
+    sq[i] = a;
+    if constexpr (IS_V) vsq += vs;
+  }
+
+  if constexpr (PATH == kPathHat) {
+    // ---- the fp16 side-buffer rows (cache.py:800-818) on the page's code page
+    uint16_t* dst = reinterpret_cast<uint16_t*>(IS_V ? A.vcodes : A.kcodes) + code_pg(A, pg) * kPage * D;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t w[NP];
+#pragma unroll
+      for (int p = 0; p < NP; ++p) w[p] = __builtin_bit_cast(uint32_t, base[i][p]);
+      store_chunk<NP>(dst + (4 * i + r) * D + EPL * c16, w);
+    }
+  }
+}
+
+template <int D, int BITS, int PATH>
+__device__ __forceinline__ void store_page(const carekv_arena& A, const carekv_store_params& sp,
+                                           const uint16_t* __restrict__ Kx, const uint16_t* __restrict__ Vx,
+                                           const carekv_page_job& job, int job_id, StoreWs ws,
+                                           const StoreStage& st, StoreLds<D>& S, const float* sP, int SD,
+                                           int lane) {
+  using L = PageLay<D>;
+  constexpr int EPL = L::EPL, NP = L::NP, LPG = L::LPG, NG = L::NG, KSB = L::KSB, VSB = L::VSB;
   const int nvld = job.num_valid;
   const long pg = ((long)job.kv_head * A.n_seq + job.seq) * A.max_pages + job.page;
   // a packed KIVI arena's call runs once over the packed prefix and once
   // over a view of its fp16 tail: each launch takes only its own pages
-  if (A.kivi_packed && job.page >= A.n_packed[job.seq]) return;
+  if (PATH == kPathKivi && job.page >= A.n_packed[job.seq]) return;
   if (!code_pg_in(A, pg)) return;
+  const int r = lane >> 4, c16 = lane & 15, gl = c16 / LPG;
+  const long tile = (long)job_id * kPage * D;
 
-  // ---- quantize own (t, g) group of K and V, fp16 chain (or, for the fp16
-  // side-buffer base, take the given K_hat / V_hat)
-  float xk[32], xv[32], rk[32], rv[32];
-  int ck[32], cv[32];
-  _Float16 sk = 0, sv = 0;
-  float hk[32], hv[32];  // K_hat / V_hat of the fp16 base
-  if constexpr (BITS == 16) {
-    if (active) {
-      const long o = ((long)job_id * kPage + t) * D + g * 32;
+  uint32_t xk[4][NP], xv[4][NP];
 #pragma unroll
-      for (int i = 0; i < 32; ++i) {
-        xk[i] = h2f(Kx[o + i]); xv[i] = h2f(Vx[o + i]);
-        hk[i] = h2f(sp.k_hat[o + i]); hv[i] = h2f(sp.v_hat[o + i]);
-        // residual against the given K_hat (residual_store.py:272-285)
-        rk[i] = (t < nvld) ? (float)(_Float16)(xk[i] - hk[i]) : 0.f;
-        rv[i] = (t < nvld) ? (float)(_Float16)(xv[i] - hv[i]) : 0.f;
-        ck[i] = cv[i] = 0;
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 32; ++i) { rk[i] = rv[i] = hk[i] = hv[i] = 0.f; ck[i] = cv[i] = 0; }
-    }
-  } else if (active) {
-    const uint16_t* kp = Kx + ((long)job_id * kPage + t) * D + g * 32;
-    const uint16_t* vp = Vx + ((long)job_id * kPage + t) * D + g * 32;
-#pragma unroll
-    for (int i = 0; i < 32; i += 8) {
-      uint4 a = *reinterpret_cast<const uint4*>(kp + i);
-      uint4 b = *reinterpret_cast<const uint4*>(vp + i);
-      const uint32_t wa[4] = {a.x, a.y, a.z, a.w}, wb[4] = {b.x, b.y, b.z, b.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        xk[i + 2 * j] = h2f((uint16_t)wa[j]); xk[i + 2 * j + 1] = h2f((uint16_t)(wa[j] >> 16));
-        xv[i + 2 * j] = h2f((uint16_t)wb[j]); xv[i + 2 * j + 1] = h2f((uint16_t)(wb[j] >> 16));
-      }
-    }
-    if (A.kivi_packed) {
-      // packed KIVI prefix page: the caller's 2-bit codes and per-token V
-      // scales; the residuals are taken against K_hat / V_hat, which
-      // half(code * scale) reproduces (K's per-channel scales live in kchan)
-      const long ri = (long)job_id * kPage + t;
-#pragma unroll
-      for (int i = 0; i < 32; ++i) {
-        ck[i] = sp.k_codes_in[ri * D + g * 32 + i];
-        cv[i] = sp.v_codes_in[ri * D + g * 32 + i];
-        hk[i] = h2f(sp.k_hat[ri * D + g * 32 + i]);
-        hv[i] = h2f(sp.v_hat[ri * D + g * 32 + i]);
-      }
-      sv = bits2half(sp.v_scale_in[ri * NG + g]);
-    } else if (sp.k_codes_in) {
-      // process_page on a page write_base wrote: the caller's base codes and
-      // fp16 group scales (residual_store.py:276-285); the page keeps its base
-      const long ri = (long)job_id * kPage + t;
-#pragma unroll
-      for (int i = 0; i < 32; ++i) {
-        ck[i] = sp.k_codes_in[ri * D + g * 32 + i];
-        cv[i] = sp.v_codes_in[ri * D + g * 32 + i];
-      }
-      sk = bits2half(sp.k_scale_in[ri * NG + g]);
-      sv = bits2half(sp.v_scale_in[ri * NG + g]);
-    } else if (sp.keep_base) {
-      // streaming store of a page the decode appends filled: the page keeps
-      // its base, the residual is taken against it as the decode reads it,
-      // half(code * half(scale code * master)) (layer.py:1104-1133)
-      const long row = pg * kPage + t;
-      uint32_t w[BITS];
-      load_bytes<CB>(w, A.kcodes + row * RB + g * CB);
-#pragma unroll
-      for (int i = 0; i < 32; ++i) ck[i] = get_code<BITS>(w, i);
-      load_bytes<CB>(w, A.vcodes + row * RB + g * CB);
-#pragma unroll
-      for (int i = 0; i < 32; ++i) cv[i] = get_code<BITS>(w, i);
-      if (A.scale_mode == 1) {
-        sk = (_Float16)((float)((const int8_t*)A.kscale)[row * NG + g] * h2f(A.kmaster[pg]));
-        sv = (_Float16)((float)((const int8_t*)A.vscale)[row * NG + g] * h2f(A.vmaster[pg]));
-      } else {
-        sk = bits2half(((const uint16_t*)A.kscale)[row * NG + g]);
-        sv = bits2half(((const uint16_t*)A.vscale)[row * NG + g]);
-      }
-    } else {
-      sk = quant_group<BITS>(xk, ck);
-      sv = quant_group<BITS>(xv, cv);
-    }
-    // residual against the fp16 scale (residual_store.py:276-285), or
-    // against the KIVI K_hat / V_hat
-    const bool kv = A.kivi_packed != 0;
-#pragma unroll
-    for (int i = 0; i < 32; ++i) {
-      const float bk = kv ? hk[i] : (float)dq(ck[i], sk), bv = kv ? hv[i] : (float)dq(cv[i], sv);
-      rk[i] = (t < nvld) ? (float)(_Float16)(xk[i] - bk) : 0.f;
-      rv[i] = (t < nvld) ? (float)(_Float16)(xv[i] - bv) : 0.f;
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 32; ++i) { rk[i] = rv[i] = 0.f; ck[i] = cv[i] = 0; }
+  for (int i = 0; i < 4; ++i) {
+    load_chunk<NP>(xk[i], Kx + tile + (long)(4 * i + r) * D + EPL * c16);
+    load_chunk<NP>(xv[i], Vx + tile + (long)(4 * i + r) * D + EPL * c16);
   }
 
-  // ---- candidate errors (fp32): K per channel group, V per 4-token block
-  float sq_k = 0.f, sq_v = 0.f;
+  // ---- K: page write, residuals, candidate errors, sketch
+  h2_t rk[4][NP];
+  float sq[4], vsq = 0.f;
+  store_kind<D, BITS, PATH, false>(A, sp, xk, rk, sq, vsq, S, lane, pg, job_id, nvld);
+  float kn = 0.f;  // sum over this lane's tokens of ||R_K[t, group]||
 #pragma unroll
-  for (int i = 0; i < 32; ++i) { sq_k += rk[i] * rk[i]; sq_v += rv[i] * rv[i]; }
-  float nrm_k = active ? sqrtf(sq_k) : 0.f;      // ||R_K[t, cg]||
-  float kerr[NG], verr[kVtb];
+  for (int i = 0; i < 4; ++i) {
+    const float g2 = grp_sum<LPG>(sq[i]);
+    kn += 4 * i + r < nvld ? __builtin_amdgcn_sqrtf(g2) : 0.f;
+  }
+  kn = rows_sum(kn);
+  const float kerr_l = nvld > 0 ? kn / (float)nvld : 0.f;  // k_error_norm of group gl
+  // residual rows to LDS (the K payloads read them back)
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t w[NP];
+#pragma unroll
+    for (int p = 0; p < NP; ++p) w[p] = __builtin_bit_cast(uint32_t, rk[i][p]);
+    store_chunk<NP>(&S.rk[(4 * i + r) * D + EPL * c16], w);
+  }
+  // column means of R_K over the valid rows -> sketch half(mean @ P) (residual_store.py:305,311-312)
   {
-    float s = nrm_k;  // sum over tokens (lanes with equal g)
+    float cs[EPL];
 #pragma unroll
-    for (int o = NG; o < NG * kPage; o <<= 1) s += __shfl_xor(s, o, 64);
+    for (int e = 0; e < EPL; ++e) {
+      float a = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a = __builtin_fmaf((float)rk[i][e >> 1][e & 1], 1.0f, a);
+      cs[e] = rows_sum(a);
+    }
+    const float inv = nvld > 0 ? 1.f / (float)nvld : 0.f;
+    if (r == 0) {
+#pragma unroll
+      for (int e = 0; e < EPL; ++e) S.mean[EPL * c16 + e] = cs[e] * inv;
+    }
+  }
+  lds_sync_wave();
+  {
+    // sketch[g][k] = sum_c mean[32 g + c] P[c][k] on the fp32 MFMA 16x16x4:
+    // A[row = l % 16][kk = l / 16] = mean of channel 4 st + kk of group row (rows
+    // past NG zero), B[kk][col] = P[4 st + kk][16 t + col]; lanes 0..15 end with
+    // C[row g = 0..3][col = lane] in their four accumulator registers.
+    const int T = (SD + 15) >> 4, SDp = 16 * T;
+    const int m = lane & 15, kk = lane >> 4;
+    float4_t acc[4] = {};
+#pragma unroll
+    for (int st = 0; st < kGroup / 4; ++st) {
+      const float a = m < NG ? S.mean[kGroup * m + 4 * st + kk] : 0.f;
+#pragma unroll
+      for (int t = 0; t < 4; ++t)
+        if (t < T) acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, sP[(4 * st + kk) * SDp + 16 * t + m], acc[t], 0, 0, 0);
+    }
+    if (lane < 16) {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        if (t >= T || 16 * t + lane >= SD) continue;
+#pragma unroll
+        for (int g = 0; g < NG; ++g) A.k_sketch[(pg * NG + g) * SD + 16 * t + lane] = f2h(acc[t][g]);
+      }
+    }
+  }
+
+  // ---- V: page write, residuals, candidate errors, sum of V_hat^2
+  h2_t rv[4][NP];
+  store_kind<D, BITS, PATH, true>(A, sp, xv, rv, sq, vsq, S, lane, pg, job_id, nvld);
+  float verr[kNvb];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float row = grp_sum<16>(sq[i]);
+    const float tn = rows_sum(4 * i + r < nvld ? __builtin_amdgcn_sqrtf(row) : 0.f);
+    const int cnt = min(max(nvld - 4 * i, 0), kVtb);
+    verr[i] = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(cnt > 0 ? tn / (float)cnt : 0.f)));
+  }
+  vsq = rows_sum(grp_sum<16>(vsq));
+
+  // ---- uniform candidate errors and the store decision (residual_store.py:372-422).  Every
+  // candidate's prior is err * sensitivity * struct_prior with the same positive factor, so
+  // priors order as the errors do and are positive where the errors are (sensitivity > 0).
+  float kerr[NG];
+#pragma unroll
+  for (int g = 0; g < NG; ++g) kerr[g] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(kerr_l), g * LPG));
+  int nk = 0, nv = 0;
+  uint32_t kord = 0, vord = 0;
+  if (!sp.store_none && sp.sensitivity > 0.0) {
+    bool kp[NG], vp[kNvb];
+#pragma unroll
+    for (int c = 0; c < NG; ++c) kp[c] = kerr[c] > 0.f;
+#pragma unroll
+    for (int b = 0; b < kNvb; ++b) vp[b] = verr[b] > 0.f;
 #pragma unroll
     for (int c = 0; c < NG; ++c) {
-      const float sc = __shfl(s, c, 64);
-      kerr[c] = nvld > 0 ? sc / (float)nvld : 0.f;
+      if (!kp[c]) continue;
+      int rank = 0, vbefore = 0;  // stable descending order; V before K only on a larger error
+#pragma unroll
+      for (int c2 = 0; c2 < NG; ++c2) rank += kp[c2] && (kerr[c2] > kerr[c] || (kerr[c2] == kerr[c] && c2 < c));
+#pragma unroll
+      for (int b = 0; b < kNvb; ++b) vbefore += vp[b] && verr[b] > kerr[c];
+      const bool sel = sp.joint ? rank + vbefore < sp.joint_budget : rank < sp.k_budget;
+      if (sel) { kord |= (uint32_t)c << (2 * rank); ++nk; }
     }
-    float tv = sq_v;  // ||R_V[t]||^2 over the row: sum over the NG lanes of token t
 #pragma unroll
-    for (int o = 1; o < NG; o <<= 1) tv += __shfl_xor(tv, o, 64);
-    const float tn = (active && t < nvld) ? sqrtf(tv) : 0.f;
+    for (int b = 0; b < kNvb; ++b) {
+      if (!vp[b]) continue;
+      int rank = 0, kbefore = 0;
 #pragma unroll
-    for (int b = 0; b < kVtb; ++b) {
-      float acc = 0.f;
-      for (int i = 0; i < kVtb; ++i) acc += __shfl(tn, (b * kVtb + i) * NG, 64);
-      const int t0 = b * kVtb, t1 = min(t0 + kVtb, nvld);
-      verr[b] = t1 > t0 ? acc / (float)(t1 - t0) : 0.f;
+      for (int b2 = 0; b2 < kNvb; ++b2) rank += vp[b2] && (verr[b2] > verr[b] || (verr[b2] == verr[b] && b2 < b));
+#pragma unroll
+      for (int c = 0; c < NG; ++c) kbefore += kp[c] && kerr[c] >= verr[b];
+      const bool sel = sp.joint ? rank + kbefore < sp.joint_budget : rank < sp.v_budget;
+      if (sel) { vord |= (uint32_t)b << (2 * rank); ++nv; }
     }
   }
-  double struct_prior = 1.0;
-  if (job.is_recent) struct_prior *= 1.5;
-  if (job.token_start < sp.sink_tokens) struct_prior *= 2.0;
-  int sel_k[NG], sel_v[kVtb], okind[NG + kVtb], oidx[NG + kVtb], nk, nv, nord;
-  select_candidates<NG>(kerr, verr, sp, struct_prior, sel_k, nk, sel_v, nv, okind, oidx, nord);
 
-  if constexpr (MODE == 0 && BITS == 16) {
-    // ---- fp16 side-buffer rows (cache.py:800-818) and sum of V_hat^2; on a
-    // code-page map only the pages it holds (the host sends no others)
-    if (active && code_pg_in(A, pg)) {
-      uint32_t wk[16], wv[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        wk[i] = (uint32_t)f2h(hk[2 * i]) | ((uint32_t)f2h(hk[2 * i + 1]) << 16);
-        wv[i] = (uint32_t)f2h(hv[2 * i]) | ((uint32_t)f2h(hv[2 * i + 1]) << 16);
-      }
-      const long cpg = code_pg(A, pg);
-      store_bytes<64>(A.kcodes + (cpg * kPage + t) * RB + g * 64, wk);
-      store_bytes<64>(A.vcodes + (cpg * kPage + t) * RB + g * 64, wv);
-    }
-    float vs = 0.f;
-    if (active && t < nvld) {
-#pragma unroll
-      for (int i = 0; i < 32; ++i) vs += hv[i] * hv[i];
-    }
-    vs = wave_sum(vs);
-    if (lane == 0) A.v_sq[pg] = vs;
+  // ---- payloads of the selections, in slot order, to the staging area
+  const int ms = st.mk + st.mv;
+  for (int i = 0; i < nk; ++i) {
+    const int c = (kord >> (2 * i)) & 3;
+    // pack_4bit(R_K[:, cg]): lane l takes token l / 4, channels 8 (l % 4) .. + 7 of the group
+    const uint4 raw = *reinterpret_cast<const uint4*>(&S.rk[(lane >> 2) * D + kGroup * c + 8 * (lane & 3)]);
+    const h2_t v[4] = {__builtin_bit_cast(h2_t, raw.x), __builtin_bit_cast(h2_t, raw.y),
+                       __builtin_bit_cast(h2_t, raw.z), __builtin_bit_cast(h2_t, raw.w)};
+    const float m = h2f((uint16_t)rows_max_u(grp_max_u<16>(absmax_bits<4>(v))));
+    const float s = fmaxf(m, 1e-8f) / 7.0f;
+    const uint32_t w = pack_res<4>(v, s);
+    *reinterpret_cast<uint32_t*>(st.kpay + ((long)job_id * st.mk + i) * KSB + 4 * lane) = w;
+    if (lane == 0) st.scale[(long)job_id * ms + i] = f2h(s);
   }
-  if (MODE == 0 && BITS != 16 && !A.kivi_packed && (sp.keep_base || sp.k_codes_in)) {
-    // ---- the page keeps its base; only the sum of V_hat^2 is refreshed, over
-    // the rows as the decode reads them back
-    float vs = 0.f;
-    if (active && t < nvld) {
-      _Float16 svr = sv;
-      if (sp.k_codes_in) {
-        const long row = pg * kPage + t;
-        svr = A.scale_mode == 1 ? (_Float16)((float)((const int8_t*)A.vscale)[row * NG + g] * h2f(A.vmaster[pg]))
-                                : bits2half(((const uint16_t*)A.vscale)[row * NG + g]);
-      }
+  for (int i = 0; i < nv; ++i) {
+    const int b = (vord >> (2 * i)) & 3;
+    // pack_4bit(R_V[4b .. 4b+3, :]): chunk b of every lane, in row-major order
+    h2_t v[NP];
 #pragma unroll
-      for (int i = 0; i < 32; ++i) { const float vh = (float)dq(cv[i], svr); vs += vh * vh; }
-    }
-    vs = wave_sum(vs);
-    if (lane == 0) A.v_sq[pg] = vs;
-  } else if constexpr (MODE == 0 && BITS != 16) {
-    // ---- packed base codes
-    if (active) {
-      uint32_t w[BITS];
-      pack_group<BITS>(ck, w);
-      store_bytes<CB>(A.kcodes + (pg * kPage + t) * RB + g * CB, w);
-      pack_group<BITS>(cv, w);
-      store_bytes<CB>(A.vcodes + (pg * kPage + t) * RB + g * CB, w);
-    }
-    // ---- scales
-    if (A.scale_mode == 1) {
-      const float mk = wave_max(active ? (float)sk : 0.f);
-      const float mv = wave_max(active ? (float)sv : 0.f);
-      const _Float16 mkh = (_Float16)(mk / 127.f), mvh = (_Float16)(mv / 127.f);
-      const int8_t qk = scale_code((float)sk, (float)mkh), qv = scale_code((float)sv, (float)mvh);
-      if (active) {
-        ((int8_t*)A.kscale)[(pg * kPage + t) * NG + g] = qk;
-        ((int8_t*)A.vscale)[(pg * kPage + t) * NG + g] = qv;
-      }
-      // V_hat as read back from the cache: half(code * half(scode * master))
-      const _Float16 svr = (_Float16)((float)qv * (float)mvh);
-      float vs = 0.f;
-      if (active && t < nvld) {
-#pragma unroll
-        for (int i = 0; i < 32; ++i) { const float vh = (float)dq(cv[i], svr); vs += vh * vh; }
-      }
-      vs = wave_sum(vs);
-      if (lane == 0) {
-        A.kmaster[pg] = half2bits(mkh);
-        A.vmaster[pg] = half2bits(mvh);
-        A.v_sq[pg] = vs;
-      }
-    } else {
-      if (active) {
-        ((uint16_t*)A.kscale)[(pg * kPage + t) * NG + g] = half2bits(sk);
-        ((uint16_t*)A.vscale)[(pg * kPage + t) * NG + g] = half2bits(sv);
-      }
-      float vs = 0.f;
-      if (active && t < nvld) {
-#pragma unroll
-        for (int i = 0; i < 32; ++i) { const float vh = (float)dq(cv[i], sv); vs += vh * vh; }
-      }
-      vs = wave_sum(vs);
-      if (lane == 0) A.v_sq[pg] = vs;
-    }
+    for (int p = 0; p < NP; ++p) v[p] = b == 0 ? rv[0][p] : (b == 1 ? rv[1][p] : (b == 2 ? rv[2][p] : rv[3][p]));
+    const float m = h2f((uint16_t)rows_max_u(grp_max_u<16>(absmax_bits<NP>(v))));
+    const float s = fmaxf(m, 1e-8f) / 7.0f;
+    const uint32_t w = pack_res<NP>(v, s);
+    int8_t* dst = st.vpay + ((long)job_id * st.mv + i) * VSB + (EPL / 2) * lane;
+    if constexpr (NP == 4) *reinterpret_cast<uint32_t*>(dst) = w;
+    else *reinterpret_cast<uint16_t*>(dst) = (uint16_t)w;
+    if (lane == 0) st.scale[(long)job_id * ms + st.mk + i] = f2h(s);
   }
-  if (MODE == 0) {
-    // ---- K sketch: half(mean_t R_K[t, cg] @ P)  (residual_store.py:305,311-312)
-    {
-      float mean[32];
+
+  // ---- metadata, counts (the streaming fill store reuses the page's earlier ids first)
+  if (lane < NG * LPG && (lane & (LPG - 1)) == 0) A.k_err[pg * NG + gl] = f2h(kerr_l);
+  if (lane < kNvb) A.v_err[pg * kNvb + lane] = f2h(lane == 0 ? verr[0] : (lane == 1 ? verr[1] : (lane == 2 ? verr[2] : verr[3])));
+  if (lane == 0) {
+    int n_ok = 0, n_ov = 0;
+    if (sp.reuse_slots && A.has_meta[pg]) {
 #pragma unroll
-      for (int i = 0; i < 32; ++i) {
-        float s = rk[i];
+      for (int c = 0; c < NG; ++c) n_ok += A.k_slot[pg * NG + c] >= 0;
 #pragma unroll
-        for (int o = NG; o < NG * kPage; o <<= 1) s += __shfl_xor(s, o, 64);
-        mean[i] = nvld > 0 ? s / (float)nvld : 0.f;
-      }
-      const int SD = A.sketch_dim;
-      for (int k = t; k < SD; k += kPage) {
-        if (!active) break;
-        float acc = 0.f;
-#pragma unroll
-        for (int c = 0; c < 32; ++c) acc += mean[c] * sp.sketch_proj[c * SD + k];
-        A.k_sketch[(pg * NG + g) * SD + k] = f2h(acc);
-      }
+      for (int b = 0; b < kNvb; ++b) n_ov += A.v_slot[pg * kNvb + b] >= 0;
     }
-    if (lane < NG) A.k_err[pg * NG + lane] = f2h(kerr[lane]);
-    if (lane < kVtb) A.v_err[pg * kVtb + lane] = f2h(verr[lane]);
-    // streaming store: the slot ids the page holds from an earlier store (a
-    // prompt's partial last page) are reused first, so only the rest are
-    // counted for new ids; a page without metadata holds none (its slot
-    // tables are cleared here, before the write pass reads them)
-    int reuse_k = 0, reuse_v = 0;
-    if (sp.reuse_slots) {
-      if (A.has_meta[pg]) {
-#pragma unroll
-        for (int c = 0; c < NG; ++c) reuse_k += A.k_slot[pg * NG + c] >= 0;
-#pragma unroll
-        for (int b = 0; b < kVtb; ++b) reuse_v += A.v_slot[pg * kVtb + b] >= 0;
-      } else {
-        if (lane < NG) A.k_slot[pg * NG + lane] = -1;
-        if (lane < kVtb) A.v_slot[pg * kVtb + lane] = -1;
-      }
-    }
-    if (lane == 0) {
-      A.valid[pg] = nvld;
-      A.has_meta[pg] = 1;
-      ws.v[job_id * 4 + 0] = nk - min(reuse_k, nk);
-      ws.v[job_id * 4 + 1] = nv - min(reuse_v, nv);
-    }
-  } else {
-    // ---- residual slots at the scanned bases (residual_store.py:424-438)
-    const int base_k = ws.v[job_id * 4 + 2], base_v = ws.v[job_id * 4 + 3];
-    const long seq_off = (long)job.seq * A.n_slots;
-    constexpr int KSB = kPage * 32 / 2;     // 16 tokens x 32 channels, 4-bit
-    const int VSB = kVtb * D / 2;
-    int kslot_of[NG], vslot_of[kVtb];
-#pragma unroll
-    for (int c = 0; c < NG; ++c) kslot_of[c] = -1;
-#pragma unroll
-    for (int b = 0; b < kVtb; ++b) vslot_of[b] = -1;
-    // streaming store: the page's earlier slot ids, ascending, go to the
-    // first selected candidates of their kind (the count pass left them out
-    // of the new ids; a page without metadata had its tables cleared there)
-    int old_k[NG], old_v[kVtb], n_ok = 0, n_ov = 0;
-    if (sp.reuse_slots) {
-#pragma unroll
-      for (int c = 0; c < NG; ++c) {
-        const int id = A.k_slot[pg * NG + c];
-        if (id >= 0) old_k[n_ok++] = id;
-      }
-#pragma unroll
-      for (int b = 0; b < kVtb; ++b) {
-        const int id = A.v_slot[pg * kVtb + b];
-        if (id >= 0) old_v[n_ov++] = id;
-      }
-      for (int i = 1; i < n_ok; ++i)
-        for (int j = i; j > 0 && old_k[j] < old_k[j - 1]; --j) { const int u = old_k[j]; old_k[j] = old_k[j - 1]; old_k[j - 1] = u; }
-      for (int i = 1; i < n_ov; ++i)
-        for (int j = i; j > 0 && old_v[j] < old_v[j - 1]; --j) { const int u = old_v[j]; old_v[j] = old_v[j - 1]; old_v[j - 1] = u; }
-    }
-    // new slot ids past the arena are dropped (never written) and flagged
-    for (int i = 0; i < nk; ++i) {
-      if (i < n_ok) kslot_of[sel_k[i]] = old_k[i];
-      else if (base_k + (i - n_ok) < A.n_slots) kslot_of[sel_k[i]] = base_k + (i - n_ok);
-      else if (lane == 0) ws.v[n_jobs * 4] = 1;
-    }
-    for (int i = 0; i < nv; ++i) {
-      if (i < n_ov) vslot_of[sel_v[i]] = old_v[i];
-      else if (base_v + (i - n_ov) < A.n_slots) vslot_of[sel_v[i]] = base_v + (i - n_ov);
-      else if (lane == 0) ws.v[n_jobs * 4] = 1;
-    }
-    // K payload of channel group g: pack_4bit(R_K[:, cg]) over all 16 rows
-    {
-      float m = 0.f;
-#pragma unroll
-      for (int i = 0; i < 32; ++i) m = fmaxf(m, fabsf(rk[i]));
-#pragma unroll
-      for (int o = NG; o < NG * kPage; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-      const float s = fmaxf(m, 1e-8f) / 7.0f;
-      const int slot = kslot_of[g];
-      if (active && slot >= 0) {
-        uint32_t w[4] = {0, 0, 0, 0};
-#pragma unroll
-        for (int i = 0; i < 32; ++i) {
-          const int c = (int)fminf(fmaxf(rintf(rk[i] / s), -8.f), 7.f);
-          w[i >> 3] |= ((uint32_t)c & 15u) << (4 * (i & 7));
-        }
-        int8_t* dst = A.k_res + (seq_off + slot) * KSB + t * 16;
-        *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
-        if (t == 0) A.k_res_scale[seq_off + slot] = f2h(s);
-      }
-    }
-    // V payload of block t/4: pack_4bit(R_V[4b..4b+3, :])
-    {
-      float m = 0.f;
-#pragma unroll
-      for (int i = 0; i < 32; ++i) m = fmaxf(m, fabsf(rv[i]));
-#pragma unroll
-      for (int o = 1; o < NG * kVtb; o <<= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-      const float s = fmaxf(m, 1e-8f) / 7.0f;
-      const int b = t / kVtb;
-      const int slot = active ? vslot_of[b] : -1;
-      if (slot >= 0) {
-        uint32_t w[4] = {0, 0, 0, 0};
-#pragma unroll
-        for (int i = 0; i < 32; ++i) {
-          const int c = (int)fminf(fmaxf(rintf(rv[i] / s), -8.f), 7.f);
-          w[i >> 3] |= ((uint32_t)c & 15u) << (4 * (i & 7));
-        }
-        int8_t* dst = A.v_res + (seq_off + slot) * VSB + (t - b * kVtb) * (D / 2) + g * 16;
-        *reinterpret_cast<uint4*>(dst) = make_uint4(w[0], w[1], w[2], w[3]);
-        if (t == b * kVtb && g == 0) A.v_res_scale[seq_off + slot] = f2h(s);
-      }
-    }
-    if (lane < NG) A.k_slot[pg * NG + lane] = kslot_of[lane];
-    if (lane < kVtb) A.v_slot[pg * kVtb + lane] = vslot_of[lane];
+    A.v_sq[pg] = vsq;
+    st.head[job_id] = (uint32_t)nk | ((uint32_t)nv << 3) | ((uint32_t)n_ok << 6) | ((uint32_t)n_ov << 9) |
+                      (kord << 12) | (vord << 20);
+    ws.v[job_id * 4 + 0] = nk - min(n_ok, nk);
+    ws.v[job_id * 4 + 1] = nv - min(n_ov, nv);
   }
 }
 
-// Exclusive scan of per-job slot counts inside each sequence group (jobs of
-// one group are contiguous and ordered like the reference's process_page
-// calls); bases start at next_slot[seq], which is advanced.
-__global__ __launch_bounds__(256) void store_scan_kernel(carekv_arena A, const carekv_page_job* __restrict__ jobs,
-                                                         const int32_t* __restrict__ group_ptr, StoreWs ws) {
-  // chunks of 1024 jobs: 4 consecutive jobs a thread, a wave scan of the
-  // thread totals (shuffles), the 4 wave totals through LDS
-  __shared__ int s_wk[4], s_wv[4];
-  __shared__ int carry_k, carry_v;
+// Bytes of the sketch projection at the start of the store pass's LDS: the
+// 32 x sketch_dim fp32 matrix with its rows padded to a multiple of 16.
+__host__ __device__ constexpr int store_lds_p_bytes(int sd) { return kGroup * ((sd + 15) / 16 * 16) * 4; }
+
+// The store pass: each wave takes jobs blockIdx.x * 4 + wave, then every
+// gridDim.x * 4-th; the sketch projection sits in LDS for the whole block.
+template <int D, int BITS, int PATH>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 && PATH != kPathKivi ? 4 : 1))) void store_pages_kernel(carekv_arena A, carekv_store_params sp,
+                                                          const uint16_t* __restrict__ Kx,
+                                                          const uint16_t* __restrict__ Vx,
+                                                          const carekv_page_job* __restrict__ jobs,
+                                                          int n_jobs, StoreWs ws, StoreStage st) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  const int SD = A.sketch_dim, SDp = (SD + 15) / 16 * 16;
+  float* sP = reinterpret_cast<float*>(smem);
+  for (int k = threadIdx.x; k < kGroup * SDp; k += 256) {
+    const int c = k / SDp, n = k - c * SDp;
+    sP[k] = n < SD ? sp.sketch_proj[c * SD + n] : 0.f;
+  }
+  __syncthreads();
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  StoreLds<D>& S = reinterpret_cast<StoreLds<D>*>(smem + store_lds_p_bytes(SD))[wave];
+  // the call's slot-overflow word (after the job records) starts clear; the scatter sets it
+  if (blockIdx.x == 0 && threadIdx.x == 0) ws.v[n_jobs * 4] = 0;
+  for (int job_id = blockIdx.x * 4 + wave; job_id < n_jobs; job_id += gridDim.x * 4)
+    store_page<D, BITS, PATH>(A, sp, Kx, Vx, jobs[job_id], job_id, ws, st, S, sP, SD, lane);
+}
+
+// Exclusive scan of the per-job new-slot counts inside each sequence group
+// (jobs of one group are contiguous and ordered like the reference's
+// process_page calls); bases start at next_slot[seq], which is advanced.
+// One block of 1024 threads per group.  A round takes up to kScanRows rows
+// of 1024 jobs; thread t holds job 1024 k + t of every row k, so loads and
+// stores are lane-consecutive and all of a round's loads are in flight at
+// once.  A job's base is the carry, plus the totals of the rows before
+// its own, plus the totals of the waves before its own in its row, plus
+// the wave-level exclusive scan.  Counts are at most 4 per job, so a wave
+// scans K and V counts packed as K | V << 16.
+constexpr int kScanRows = 24;
+__global__ __launch_bounds__(1024) void store_scan_kernel(carekv_arena A, const carekv_page_job* __restrict__ jobs,
+                                                          const int32_t* __restrict__ group_ptr, StoreWs ws) {
+  __shared__ uint32_t s_wave[kScanRows][16];  // per row and wave: total (packed), then exclusive prefix
+  __shared__ int2 s_row[kScanRows];           // per row: exclusive prefix over the rows (K, V)
+  __shared__ int2 s_tot;
   const int g = blockIdx.x;
   const int j0 = group_ptr[g], j1 = group_ptr[g + 1];
   if (j1 <= j0) return;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int n = j1 - j0;
   const int seq = jobs[j0].seq;
-  if (threadIdx.x == 0) { carry_k = A.next_slot[2 * seq]; carry_v = A.next_slot[2 * seq + 1]; }
-  __syncthreads();
-  for (int base = j0; base < j1; base += 1024) {
-    const int jb = base + 4 * threadIdx.x;
-    int ck[4], cv[4], tk = 0, tv = 0;
+  int carry_k = A.next_slot[2 * seq], carry_v = A.next_slot[2 * seq + 1];
+  for (int base = 0; base < n; base += 1024 * kScanRows) {
+    const int rows = min(kScanRows, (n - base + 1023) / 1024);
+    uint32_t c[kScanRows], inc[kScanRows];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const bool ok = jb + i < j1;
-      ck[i] = ok ? ws.v[(jb + i) * 4] : 0;
-      cv[i] = ok ? ws.v[(jb + i) * 4 + 1] : 0;
-      tk += ck[i];
-      tv += cv[i];
-    }
-    int ik = tk, iv = tv;  // inclusive scan of the thread totals over the wave
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const int yk = __shfl_up(ik, o, 64), yv = __shfl_up(iv, o, 64);
-      if (lane >= o) { ik += yk; iv += yv; }
-    }
-    if (lane == 63) { s_wk[w] = ik; s_wv[w] = iv; }
-    __syncthreads();
-    int off_k = carry_k, off_v = carry_v;  // slots before this thread's first job
-    for (int ww = 0; ww < w; ++ww) { off_k += s_wk[ww]; off_v += s_wv[ww]; }
-    off_k += ik - tk;
-    off_v += iv - tv;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      if (jb + i < j1) {
-        ws.v[(jb + i) * 4 + 2] = off_k;
-        ws.v[(jb + i) * 4 + 3] = off_v;
+    for (int k = 0; k < kScanRows; ++k) {
+      const int j = base + 1024 * k + t;
+      c[k] = 0;
+      if (k < rows && j < n) {
+        const int2 v = *reinterpret_cast<const int2*>(ws.v + (long)(j0 + j) * 4);
+        c[k] = (uint32_t)v.x | ((uint32_t)v.y << 16);
       }
-      off_k += ck[i];
-      off_v += cv[i];
     }
-    __syncthreads();  // every thread has read the carries and wave totals
-    if (threadIdx.x == 0) {
-      carry_k += ((s_wk[0] + s_wk[1]) + s_wk[2]) + s_wk[3];
-      carry_v += ((s_wv[0] + s_wv[1]) + s_wv[2]) + s_wv[3];
+#pragma unroll
+    for (int k = 0; k < kScanRows; ++k) {
+      if (k >= rows) break;
+      uint32_t x = c[k];  // inclusive scan over the wave
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t y = __shfl_up(x, o, 64);
+        if (lane >= o) x += y;
+      }
+      inc[k] = x;
+      if (lane == 63) s_wave[k][w] = x;
     }
     __syncthreads();
+    if (t < rows * 16) {  // one thread per (row, wave): exclusive prefix over the row's waves
+      // (the 16 threads of a row are one quarter of one wave: all its reads precede its writes)
+      const int k = t >> 4, ww = t & 15;
+      uint32_t pre = 0, tot = 0;
+      for (int i = 0; i < 16; ++i) {
+        const uint32_t v = s_wave[k][i];
+        pre += i < ww ? v : 0u;
+        tot += v;
+      }
+      s_wave[k][ww] = pre;
+      if (ww == 0) s_row[k] = make_int2((int)(tot & 0xffffu), (int)(tot >> 16));
+    }
+    __syncthreads();
+    if (t == 0) {  // exclusive prefix over the rows
+      int pk = 0, pv = 0;
+      for (int k = 0; k < rows; ++k) {
+        const int2 v = s_row[k];
+        s_row[k] = make_int2(pk, pv);
+        pk += v.x;
+        pv += v.y;
+      }
+      s_tot = make_int2(pk, pv);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kScanRows; ++k) {
+      if (k >= rows) break;
+      const int j = base + 1024 * k + t;
+      const uint32_t ex = s_wave[k][w] + inc[k] - c[k];  // packed, per field < 2^16
+      const int2 r = s_row[k];
+      if (j < n)
+        *reinterpret_cast<int2*>(ws.v + (long)(j0 + j) * 4 + 2) =
+            make_int2(carry_k + r.x + (int)(ex & 0xffffu), carry_v + r.y + (int)(ex >> 16));
+    }
+    carry_k += s_tot.x;
+    carry_v += s_tot.y;
+    __syncthreads();  // LDS is rewritten by the next round
   }
-  if (threadIdx.x == 0) { A.next_slot[2 * seq] = carry_k; A.next_slot[2 * seq + 1] = carry_v; }
+  if (t == 0) { A.next_slot[2 * seq] = carry_k; A.next_slot[2 * seq + 1] = carry_v; }
+}
+
+// Slot id of the i-th selection of a kind: the page's earlier ids first
+// (ascending), then new ids from the scanned base; -1 past the arena.
+__device__ __forceinline__ int slot_of(int i, int n_old, const int* old, int n_cand, int base, int n_slots) {
+  if (i < n_old) {
+    // the i-th smallest of the page's earlier ids (>= 0), n_cand entries
+    int id = -1;
+#pragma unroll
+    for (int c = 0; c < n_cand; ++c) {
+      if (old[c] < 0) continue;
+      int rank = 0;
+#pragma unroll
+      for (int c2 = 0; c2 < n_cand; ++c2) rank += old[c2] >= 0 && old[c2] < old[c];
+      if (rank == i) id = old[c];
+    }
+    return id;
+  }
+  const int id = base + (i - n_old);
+  return id < n_slots ? id : -1;
+}
+
+// The scatter: slot tables, slot payloads and scales, valid / has_meta of
+// every job (residual_store.py:424-438).  16 lanes per job, 16 jobs a block.
+template <int D>
+__global__ __launch_bounds__(256) void store_slots_kernel(carekv_arena A, const carekv_page_job* __restrict__ jobs,
+                                                          int n_jobs, StoreWs ws, StoreStage st) {
+  using L = PageLay<D>;
+  constexpr int NG = L::NG, KSB = L::KSB, VSB = L::VSB, VP = VSB / 16;
+  const int sub = threadIdx.x & 15;
+  const int job_id = blockIdx.x * 16 + (threadIdx.x >> 4);
+  if (job_id >= n_jobs) return;
+  const carekv_page_job job = jobs[job_id];
+  const uint32_t h = st.head[job_id];
+  const int2 base = *reinterpret_cast<const int2*>(ws.v + (long)job_id * 4 + 2);
+  const long pg = ((long)job.kv_head * A.n_seq + job.seq) * A.max_pages + job.page;
+  const int nk = min((int)(h & 7), st.mk), nv = min((int)((h >> 3) & 7), st.mv);
+  const int n_ok = (h >> 6) & 7, n_ov = (h >> 9) & 7;
+  int old_k[NG], old_v[kNvb];
+#pragma unroll
+  for (int c = 0; c < NG; ++c) old_k[c] = n_ok ? A.k_slot[pg * NG + c] : -1;
+#pragma unroll
+  for (int b = 0; b < kNvb; ++b) old_v[b] = n_ov ? A.v_slot[pg * kNvb + b] : -1;
+  const long seq_off = (long)job.seq * A.n_slots;
+  const int ms = st.mk + st.mv;
+  // payloads: lane sub copies 16-byte piece sub of each
+#pragma unroll
+  for (int i = 0; i < NG; ++i) {
+    if (i >= nk) break;
+    const int id = slot_of(i, n_ok, old_k, NG, base.x, A.n_slots);
+    const uint4 v = *reinterpret_cast<const uint4*>(st.kpay + ((long)job_id * st.mk + i) * KSB + 16 * sub);
+    if (id >= 0) *reinterpret_cast<uint4*>(A.k_res + (seq_off + id) * KSB + 16 * sub) = v;
+  }
+#pragma unroll
+  for (int i = 0; i < kNvb; ++i) {
+    if (i >= nv) break;
+    if (sub < VP) {
+      const int id = slot_of(i, n_ov, old_v, kNvb, base.y, A.n_slots);
+      const uint4 v = *reinterpret_cast<const uint4*>(st.vpay + ((long)job_id * st.mv + i) * VSB + 16 * sub);
+      if (id >= 0) *reinterpret_cast<uint4*>(A.v_res + (seq_off + id) * VSB + 16 * sub) = v;
+    }
+  }
+  if (sub < NG) {  // slot tables: candidate c holds the id of its selection, -1 if none
+    int id = -1;
+    for (int i = 0; i < nk; ++i)
+      if ((int)((h >> (12 + 2 * i)) & 3) == sub) id = slot_of(i, n_ok, old_k, NG, base.x, A.n_slots);
+    A.k_slot[pg * NG + sub] = id;
+  } else if (sub >= 4 && sub < 4 + nk) {
+    const int id = slot_of(sub - 4, n_ok, old_k, NG, base.x, A.n_slots);
+    if (id >= 0) A.k_res_scale[seq_off + id] = st.scale[(long)job_id * ms + sub - 4];
+  } else if (sub >= 8 && sub < 8 + kNvb) {
+    const int b = sub - 8;
+    int id = -1;
+    for (int i = 0; i < nv; ++i)
+      if ((int)((h >> (20 + 2 * i)) & 3) == b) id = slot_of(i, n_ov, old_v, kNvb, base.y, A.n_slots);
+    A.v_slot[pg * kNvb + b] = id;
+  } else if (sub >= 12 && sub < 12 + nv) {
+    const int id = slot_of(sub - 12, n_ov, old_v, kNvb, base.y, A.n_slots);
+    if (id >= 0) A.v_res_scale[seq_off + id] = st.scale[(long)job_id * ms + st.mk + sub - 12];
+  }
+  if (sub == 15) {
+    A.valid[pg] = job.num_valid;
+    A.has_meta[pg] = 1;
+    // new ids past the arena are dropped (never written) and flagged
+    if ((nk > n_ok && base.x + (nk - n_ok) > A.n_slots) || (nv > n_ov && base.y + (nv - n_ov) > A.n_slots))
+      ws.v[n_jobs * 4] = 1;
+  }
 }
 
 // KIVI-style value (kivi_helpers.py:35-59): half(clamp(rint(half(x / s))) * s)
@@ -957,26 +1372,74 @@ __global__ void quantize_rows_kernel(const uint16_t* __restrict__ x, int rows, i
 }  // namespace carekv
 
 // ------------------------------------------------------------------ host side
+#include <algorithm>
+
 #include "host_util.h"
 
 using namespace carekv;
 
-// per job 4 int32 (counts, then slot bases), then the call's status word:
-// nonzero when a slot id would fall past the arena's n_slots (those slots are
-// dropped, never written)
-extern "C" int64_t carekv_store_workspace_bytes(int32_t n_jobs) { return (int64_t)n_jobs * 16 + 16; }
+// Workspace of carekv_store_pages: per job 4 int32 (counts, then slot
+// bases), the call's status word (nonzero when a slot id would fall past the
+// arena's n_slots: those slots are dropped, never written), then the store
+// pass's staging area (headers, payloads, scales), each part 256-byte aligned.
+struct StageLayout {
+  int64_t head, kpay, vpay, scale, total;
+  int mk, mv;
+};
+static StageLayout stage_layout(int64_t n_jobs, int D, const carekv_store_params& sp) {
+  auto al = [](int64_t x) { return (x + 255) & ~(int64_t)255; };
+  StageLayout L;
+  store_caps(sp, D / kGroup, &L.mk, &L.mv);
+  int64_t o = al(n_jobs * 16 + 16);
+  L.head = o;
+  o = al(o + n_jobs * 4);
+  L.kpay = o;
+  o = al(o + n_jobs * L.mk * (kPage * kGroup / 2));
+  L.vpay = o;
+  o = al(o + n_jobs * L.mv * (kVtb * D / 2));
+  L.scale = o;
+  o = al(o + n_jobs * (L.mk + L.mv) * 2);
+  L.total = o;
+  return L;
+}
+static StoreStage make_stage(void* ws, const StageLayout& L) {
+  char* b = static_cast<char*>(ws);
+  return StoreStage{reinterpret_cast<uint32_t*>(b + L.head), reinterpret_cast<int8_t*>(b + L.kpay),
+                    reinterpret_cast<int8_t*>(b + L.vpay), reinterpret_cast<uint16_t*>(b + L.scale), L.mk, L.mv};
+}
 
-template <int D, int BITS>
-static int launch_store(const carekv_arena& A, const carekv_store_params& sp, const uint16_t* K, const uint16_t* V,
-                        const carekv_page_job* jobs, int n_jobs, const int32_t* group_ptr, int n_groups,
-                        StoreWs ws, hipStream_t s) {
-  const int blocks = (n_jobs + 3) / 4;
-  hipLaunchKernelGGL((store_pages_kernel<D, BITS, 0>), dim3(blocks), dim3(256), 0, s, A, sp, K, V, jobs, n_jobs, ws);
-  CAREKV_CHECK_LAUNCH("store_pages(count)");
-  hipLaunchKernelGGL(store_scan_kernel, dim3(n_groups), dim3(256), 0, s, A, jobs, group_ptr, ws);
+extern "C" int64_t carekv_store_workspace_bytes(const carekv_arena* arena, const carekv_store_params* sp,
+                                                int32_t n_jobs) {
+  if (!arena || !sp || n_jobs < 0) {
+    set_error("carekv_store_workspace_bytes: null arena / params or negative n_jobs");
+    return -1;
+  }
+  return stage_layout(n_jobs, arena->head_dim, *sp).total;
+}
+
+// Blocks of the store pass: enough to fill the chip several times over;
+// each wave then loops over its share of the jobs.
+constexpr int kStorePassBlocks = 2048;
+
+template <int D, int BITS, int PATH>
+static int launch_pass(const carekv_arena& A, const carekv_store_params& sp, const uint16_t* K, const uint16_t* V,
+                       const carekv_page_job* jobs, int n_jobs, StoreWs ws, const StoreStage& st, hipStream_t s,
+                       const char* what) {
+  const int blocks = std::min((n_jobs + 3) / 4, kStorePassBlocks);
+  const int lds = store_lds_p_bytes(A.sketch_dim) + 4 * (int)sizeof(StoreLds<D>);
+  hipLaunchKernelGGL((store_pages_kernel<D, BITS, PATH>), dim3(blocks), dim3(256), lds, s, A, sp, K, V, jobs,
+                     n_jobs, ws, st);
+  CAREKV_CHECK_LAUNCH(what);
+  return CAREKV_OK;
+}
+
+template <int D>
+static int launch_slots(const carekv_arena& A, const carekv_page_job* jobs, int n_jobs, const int32_t* group_ptr,
+                        int n_groups, StoreWs ws, const StoreStage& st, hipStream_t s) {
+  hipLaunchKernelGGL(store_scan_kernel, dim3(n_groups), dim3(1024), 0, s, A, jobs, group_ptr, ws);
   CAREKV_CHECK_LAUNCH("store_scan");
-  hipLaunchKernelGGL((store_pages_kernel<D, BITS, 1>), dim3(blocks), dim3(256), 0, s, A, sp, K, V, jobs, n_jobs, ws);
-  CAREKV_CHECK_LAUNCH("store_pages(write)");
+  hipLaunchKernelGGL((store_slots_kernel<D>), dim3((n_jobs + 15) / 16), dim3(256), 0, s, A, jobs, n_jobs, ws, st);
+  CAREKV_CHECK_LAUNCH("store_slots");
   return CAREKV_OK;
 }
 
@@ -994,26 +1457,30 @@ static carekv_arena kivi_tail_view(const carekv_arena& A) {
   return At;
 }
 
-// Both kinds of page of a packed KIVI arena in one slot allocation: the
-// count passes of the prefix and the tail, the scan over all jobs, then the
-// two write passes.
-template <int D>
-static int launch_store_kivi(const carekv_arena& A, const carekv_store_params& sp, const uint16_t* K,
-                             const uint16_t* V, const carekv_page_job* jobs, int n_jobs, const int32_t* group_ptr,
-                             int n_groups, StoreWs ws, hipStream_t s) {
-  const carekv_arena At = kivi_tail_view(A);
-  const int blocks = (n_jobs + 3) / 4;
-  hipLaunchKernelGGL((store_pages_kernel<D, 2, 0>), dim3(blocks), dim3(256), 0, s, A, sp, K, V, jobs, n_jobs, ws);
-  CAREKV_CHECK_LAUNCH("store_pages(count, packed KIVI prefix)");
-  hipLaunchKernelGGL((store_pages_kernel<D, 16, 0>), dim3(blocks), dim3(256), 0, s, At, sp, K, V, jobs, n_jobs, ws);
-  CAREKV_CHECK_LAUNCH("store_pages(count, packed KIVI tail)");
-  hipLaunchKernelGGL(store_scan_kernel, dim3(n_groups), dim3(256), 0, s, A, jobs, group_ptr, ws);
-  CAREKV_CHECK_LAUNCH("store_scan");
-  hipLaunchKernelGGL((store_pages_kernel<D, 2, 1>), dim3(blocks), dim3(256), 0, s, A, sp, K, V, jobs, n_jobs, ws);
-  CAREKV_CHECK_LAUNCH("store_pages(write, packed KIVI prefix)");
-  hipLaunchKernelGGL((store_pages_kernel<D, 16, 1>), dim3(blocks), dim3(256), 0, s, At, sp, K, V, jobs, n_jobs, ws);
-  CAREKV_CHECK_LAUNCH("store_pages(write, packed KIVI tail)");
-  return CAREKV_OK;
+// One call: the store pass (both kinds of page of a packed KIVI arena: the
+// packed prefix, then a view of the fp16 tail), the slot scan over all jobs,
+// the scatter.
+template <int D, int BITS>
+static int launch_store(const carekv_arena& A, const carekv_store_params& sp, const uint16_t* K, const uint16_t* V,
+                        const carekv_page_job* jobs, int n_jobs, const int32_t* group_ptr, int n_groups,
+                        StoreWs ws, const StoreStage& st, hipStream_t s) {
+  int rc;
+  if (A.kivi_packed) {
+    rc = launch_pass<D, 2, kPathKivi>(A, sp, K, V, jobs, n_jobs, ws, st, s, "store_pages (packed KIVI prefix)");
+    if (rc == CAREKV_OK)
+      rc = launch_pass<D, 16, kPathHat>(kivi_tail_view(A), sp, K, V, jobs, n_jobs, ws, st, s,
+                                        "store_pages (packed KIVI tail)");
+  } else if constexpr (BITS == 16) {
+    rc = launch_pass<D, 16, kPathHat>(A, sp, K, V, jobs, n_jobs, ws, st, s, "store_pages (fp16 base)");
+  } else if (sp.k_codes_in) {
+    rc = launch_pass<D, BITS, kPathCodesIn>(A, sp, K, V, jobs, n_jobs, ws, st, s, "store_pages (given base)");
+  } else if (sp.keep_base) {
+    rc = launch_pass<D, BITS, kPathKeep>(A, sp, K, V, jobs, n_jobs, ws, st, s, "store_pages (kept base)");
+  } else {
+    rc = launch_pass<D, BITS, kPathFresh>(A, sp, K, V, jobs, n_jobs, ws, st, s, "store_pages");
+  }
+  if (rc != CAREKV_OK) return rc;
+  return launch_slots<D>(A, jobs, n_jobs, group_ptr, n_groups, ws, st, s);
 }
 
 extern "C" int carekv_store_pages(const carekv_arena* arena, const carekv_store_params* sp, const uint16_t* K,
@@ -1028,23 +1495,26 @@ extern "C" int carekv_store_pages(const carekv_arena* arena, const carekv_store_
   CAREKV_REQUIRE(A.residual_bits == 4, "kernels support residual_bits=4");
   CAREKV_REQUIRE(sp->sketch_proj != nullptr, "sketch_proj is required");
   StoreWs ws{(int32_t*)workspace};
+  const StoreStage st = make_stage(workspace, stage_layout(n_jobs, A.head_dim, *sp));
   hipStream_t s = (hipStream_t)stream;
   if (A.kivi_packed) {
     CAREKV_REQUIRE(sp->k_hat && sp->v_hat && sp->k_codes_in && sp->v_codes_in && sp->v_scale_in,
                    "a packed KIVI arena stores from k_hat, v_hat, k_codes_in, v_codes_in and v_scale_in");
     CAREKV_REQUIRE(!sp->keep_base, "keep_base is built for the uniform packed bases");
-    if (A.head_dim == 64) return launch_store_kivi<64>(A, *sp, K, V, jobs_dev, n_jobs, group_ptr_dev, n_groups, ws, s);
-    return launch_store_kivi<128>(A, *sp, K, V, jobs_dev, n_jobs, group_ptr_dev, n_groups, ws, s);
+    if (A.head_dim == 64) return launch_store<64, 2>(A, *sp, K, V, jobs_dev, n_jobs, group_ptr_dev, n_groups, ws, st, s);
+    return launch_store<128, 2>(A, *sp, K, V, jobs_dev, n_jobs, group_ptr_dev, n_groups, ws, st, s);
   }
   if (A.base_bits == 16) {
     CAREKV_REQUIRE(sp->k_hat && sp->v_hat, "the fp16 base (base_bits=16) needs k_hat and v_hat");
     CAREKV_REQUIRE(!sp->keep_base, "keep_base (streaming store) is built for the packed bases");
-    if (A.head_dim == 64) return launch_store<64, 16>(A, *sp, K, V, jobs_dev, n_jobs, group_ptr_dev, n_groups, ws, s);
-    return launch_store<128, 16>(A, *sp, K, V, jobs_dev, n_jobs, group_ptr_dev, n_groups, ws, s);
+    if (A.head_dim == 64) return launch_store<64, 16>(A, *sp, K, V, jobs_dev, n_jobs, group_ptr_dev, n_groups, ws, st, s);
+    return launch_store<128, 16>(A, *sp, K, V, jobs_dev, n_jobs, group_ptr_dev, n_groups, ws, st, s);
   }
+  CAREKV_REQUIRE(!sp->k_codes_in || (sp->k_scale_in && sp->v_codes_in && sp->v_scale_in),
+                 "k_codes_in needs k_scale_in, v_codes_in and v_scale_in");
   return dispatch_db(A.head_dim, A.base_bits, [&](auto d, auto b) {
     return launch_store<decltype(d)::value, decltype(b)::value>(A, *sp, K, V, jobs_dev, n_jobs, group_ptr_dev,
-                                                                n_groups, ws, s);
+                                                                n_groups, ws, st, s);
   });
 }
 

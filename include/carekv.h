@@ -182,14 +182,21 @@ typedef struct carekv_page_job {
  * K, V: fp16 [n_jobs*page_size][head_dim].  Jobs are grouped by sequence:
  * group g is jobs [group_ptr[g], group_ptr[g+1]) (device int32 array), all of
  * one sequence and in the reference's call order (kv head major, page
- * minor).  workspace must hold carekv_store_workspace_bytes(n_jobs) bytes. */
+ * minor).  workspace must hold carekv_store_workspace_bytes(arena, sp,
+ * n_jobs) bytes.  Three launches: one pass over every page (codes, scales,
+ * residual candidates, the store decision, the selected 4-bit payloads
+ * staged in the workspace), the slot-id scan per group, the scatter of the
+ * staged payloads to their slots. */
 int carekv_store_pages(const carekv_arena* arena, const carekv_store_params* sp,
                        const uint16_t* K, const uint16_t* V, const carekv_page_job* jobs_dev,
                        int32_t n_jobs, const int32_t* group_ptr_dev, int32_t n_groups,
                        void* workspace, void* stream);
-/* The int32 at workspace[4 * n_jobs] is the call's status word: 0, or
- * nonzero when a slot id would fall past n_slots (those slots are dropped). */
-int64_t carekv_store_workspace_bytes(int32_t n_jobs);
+/* Workspace bytes of a carekv_store_pages call with these arena, params and
+ * job count (the staging area is sized by head_dim and the per-page
+ * budgets); -1 on a null argument.  The int32 at workspace[4 * n_jobs] is
+ * the call's status word: 0, or nonzero when a slot id would fall past
+ * n_slots (those slots are dropped). */
+int64_t carekv_store_workspace_bytes(const carekv_arena* arena, const carekv_store_params* sp, int32_t n_jobs);
 
 /* One decode-token append per row (layer.py:1028-1146, cache.py:656-701):
  * quantize the row, pack it at (seq, kv_head, page, valid[pg]), encode its
