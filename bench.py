@@ -244,12 +244,34 @@ def cpu_baseline(cache, spec, q_np, slices, out_np=None, diag_np=None):
     return per_slice * spec["B"] * spec["Hkv"] * 1e6, per_slice, par
 
 
+def store_algorithmic_bytes(cache, cfg, B, H, T):
+    """Bytes the prompt store must move, once each: the fp16 K and V rows
+    read, the packed codes, int8 scale codes and fp16 masters, the page
+    metadata (valid, has_meta, slot tables, fp16 error norms and sketches,
+    fp32 sum of V_hat^2) and the 4-bit slots the call stored (with their
+    fp16 scales) written.  The staging round trip of the slot payloads is
+    not counted."""
+    D, P = cfg.head_dim, -(-T // 16)
+    ng, nvb, sd = D // 32, 4, cfg.sketch_dim
+    pages = B * H * P
+    rb = D * cfg.base_bits // 8
+    slots = cache.next_slot.sum(0).tolist()  # stored K and V slots over the call's sequences
+    terms = {"kv_fp16_in": 2 * B * H * T * D * 2,
+             "codes": pages * 2 * 16 * rb,
+             "scale_codes": pages * 2 * 16 * ng,
+             "masters": pages * 2 * 2,
+             "metadata": pages * (4 + 1 + 4 * (ng + nvb) + 2 * (ng + nvb) + 2 * ng * sd + 4),
+             "slots": int(slots[0]) * (16 * 32 // 2 + 2) + int(slots[1]) * (4 * D // 2 + 2)}
+    return int(sum(terms.values())), terms
+
+
 def prefill_bench(args):
     """Config 4: causal prefill attention over dequantised K/V (layer.py:935-972)
     at B=4, 40 heads, D=128, T=8192, plus the quantize + pack + residual store
     of the same K/V into pages (timed separately).  One step = one layer's
     prefill attention for the batch."""
     os.environ.update(PAPER_ENV)
+    import numpy as np
     import torch
     import care_kv
     c = PREFILL_CONFIG
@@ -273,13 +295,23 @@ def prefill_bench(args):
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     cache.write_prefill(0, kx, vx, seqs=list(range(B)))  # warm-up (allocations, library load)
     torch.cuda.synchronize()
-    cache = care_kv.CAREKVCache(cfg, device=dev, n_seq=B)
-    torch.cuda.synchronize()
-    e0.record()
-    cache.write_prefill(0, kx, vx, seqs=list(range(B)))  # the whole batch in one call, as CAREKVLayer.prefill
-    e1.record()
-    e1.synchronize()
-    store_ms = e0.elapsed_time(e1)
+    # the store kernels (pass, slot scan, scatter), timed with HIP events on their stream around
+    # their launches inside write_prefill, over fresh caches; and write_prefill's wall time
+    store_us, store_ms_all = [], []
+    for _ in range(5):
+        cache = care_kv.CAREKVCache(cfg, device=dev, n_seq=B)
+        k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        cache.store_events = (k0, k1)
+        torch.cuda.synchronize()
+        e0.record()
+        cache.write_prefill(0, kx, vx, seqs=list(range(B)))  # the whole batch in one call, as CAREKVLayer.prefill
+        e1.record()
+        e1.synchronize()
+        store_us.append(k0.elapsed_time(k1) * 1e3)
+        store_ms_all.append(e0.elapsed_time(e1))
+    store_kernels_us = float(np.median(store_us))
+    store_ms = float(np.median(store_ms_all))
+    store_bytes_alg, store_terms = store_algorithmic_bytes(cache, cfg, B, H, T)
     # K_hat, V_hat of the prefill path (fp16 group scales)
     kh = care_kv.quant_dequant(kx, c["bits"])
     vh = care_kv.quant_dequant(vx, c["bits"])
@@ -305,7 +337,6 @@ def prefill_bench(args):
         # T-long score row, masked), and the GPU output of those rows checked against it
         import numpy as np
         from oracle.attention import causal_attention_pure
-        from oracle.check import output_errors
         rows = np.linspace(0, T - 1, 512).astype(np.int64)
         pairs = [(0, 0), (B - 1, H - 1)]
         t_cpu, mx_all, rel_all, ratio_all = 0.0, 0.0, 0.0, 0.0
@@ -315,11 +346,19 @@ def prefill_bench(args):
             t0 = time.perf_counter()
             ref, _ = causal_attention_pure(qn, kn, vn, causal=True, rows=rows)
             t_cpu += time.perf_counter() - t0
-            got = out[bb, hh, torch.from_numpy(rows).to(dev)].cpu().numpy()
-            # the bar of tests/test_gpu_prefill.py: 2e-3 of the head's V scale (log-normal channels), or one
-            # fp16 ulp of the reference where larger
-            vs = max(1.0, float(np.sqrt(np.mean(vn.astype(np.float32) ** 2))))
-            mx, rel, ratio = output_errors(got, ref[0], atol=2e-3 * vs)
+            got = out[bb, hh, torch.from_numpy(rows).to(dev)].cpu().numpy().astype(np.float32)
+            # the bar of tests/test_gpu_prefill.py: max(2e-3, one fp16 ulp of the reference plus the
+            # weight-rounding allowance 2^-11 sum_t a_t |v_t| from the fp64 softmax weights)
+            s = (qn[0].astype(np.float64)[rows] @ kn[0].astype(np.float64).T) / math.sqrt(D)
+            s = np.where(np.arange(T)[None, :] > rows[:, None], -np.inf, s)
+            a = np.exp(s - s.max(-1, keepdims=True))
+            allow = 2.0 ** -11 * (a / a.sum(-1, keepdims=True)) @ np.abs(vn[0].astype(np.float64))
+            r32 = ref[0].astype(np.float32)
+            bound = np.maximum(2e-3, np.spacing(np.abs(ref[0].astype(np.float16))).astype(np.float64) + allow)
+            err = np.abs(got.astype(np.float64) - r32)
+            mx = float(err.max())
+            ratio = float((err / bound).max())
+            rel = float(np.linalg.norm(got - r32) / max(np.linalg.norm(r32), 1e-30))
             mx_all, rel_all, ratio_all = max(mx_all, mx), max(rel_all, rel), max(ratio_all, ratio)
         per_row = t_cpu / (len(pairs) * len(rows))
         cpu_ms = per_row * B * H * T * 1e3
@@ -333,12 +372,16 @@ def prefill_bench(args):
                          f"oracle ({per_row * 1e3:.3f} ms per row), extrapolated per row to {B * H * T} rows"}
         parity = {"rows": len(pairs) * len(rows), "max_abs": round(mx_all, 6), "rel_l2": round(rel_all, 6),
                   "bar_ratio": round(ratio_all, 3), "pass": bool(ratio_all <= 1.0 and rel_all <= 1e-2),
-                  "bar": "out within 2e-3 x rms(V) (or 1 fp16 ulp) and rel-L2 1e-2 of the oracle"}
+                  "bar": "out within max(2e-3, 1 fp16 ulp + 2^-11 sum_t a_t |v_t|) and rel-L2 1e-2 of the oracle"}
         log(f"[bench] c4 cpu oracle {per_row * 1e3:.3f} ms/row -> {cpu_ms / 1e3:.1f} s/step extrapolated; "
             f"parity {parity}")
-    store_bytes = 2 * B * H * T * D * 2  # fp16 K and V read once by the store path
+    store_gbs = store_bytes_alg / (store_kernels_us * 1e-6) / 1e9
+    tr = load_traffic("store", "c4")  # the three store kernels' counter traffic per call
+    store_traffic = None if tr is None else tr.get("hbm_bytes_per_launch")
     log(f"[bench] c4 prefill attention {ms * 1e3:.1f} us/step, {flops / 1e12:.3f} TFLOP -> {tflops:.1f} TFLOP/s "
-        f"({tflops / 2500 * 100:.1f}% of 2.5 PF fp16 dense); store path {store_ms:.1f} ms for {B} sequences")
+        f"({tflops / 2500 * 100:.1f}% of 2.5 PF fp16 dense); store kernels {store_kernels_us:.1f} us "
+        f"({store_bytes_alg / 1e6:.1f} MB -> {store_gbs:.0f} GB/s, {store_gbs / 8000 * 100:.1f}% of 8 TB/s), "
+        f"write_prefill {store_ms:.2f} ms wall for {B} sequences")
     line = {
         "metric": "CARE-KV prefill attention over dequantised K/V, TFLOP/s (Llama-2-13B shape, 8K prompt)",
         "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -349,8 +392,12 @@ def prefill_bench(args):
         "roofline": {"bound": "mfma", "kernel": f"prefill_attn_kernel<{D}>", "achieved": round(tflops, 2),
                      "peak": 2500.0, "unit": "TFLOP/s", "frac": round(tflops / 2500.0, 4), "traffic": None,
                      "algorithmic_flops_per_launch": flops, "launch_us": round(ms * 1e3, 2)},
-        "store_path": {"ms": round(store_ms, 3), "fp16_bytes_in": store_bytes,
-                       "gbps_in": round(store_bytes / (store_ms * 1e-3) / 1e9, 1)},
+        "store": {"kernels": "store_pages_kernel + store_scan_kernel + store_slots_kernel",
+                  "roofline": {"bound": "hbm", "achieved": round(store_gbs, 1), "peak": 8000.0, "unit": "GB/s",
+                               "frac": round(store_gbs / 8000.0, 4), "traffic": store_traffic,
+                               "algorithmic_bytes_per_call": store_bytes_alg, "terms": store_terms,
+                               "launch_us": round(store_kernels_us, 2)},
+                  "write_prefill_ms_wall": round(store_ms, 3)},
         "cpu_baseline": cpu,
         "parity": parity,
     }

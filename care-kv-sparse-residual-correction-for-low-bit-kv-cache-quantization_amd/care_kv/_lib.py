@@ -44,6 +44,10 @@ class StoreParams(C.Structure):
                 ("k_scale_in", C.c_void_p), ("v_codes_in", C.c_void_p), ("v_scale_in", C.c_void_p)]
 
 
+class PrefillGrid(C.Structure):
+    _fields_ = [("n_rows", C.c_int32), ("n_tokens", C.c_int32), ("token_start", C.c_int32), ("rows", C.c_void_p)]
+
+
 class DecodeParams(C.Structure):
     _fields_ = [("batch", C.c_int32), ("n_heads", C.c_int32), ("seq_slot", C.c_void_p), ("n_pages", C.c_void_p),
                 ("max_pages_used", C.c_int32), ("sm_scale", C.c_float), ("sensitivity", C.c_float),
@@ -76,7 +80,7 @@ class PrefillEvalParams(C.Structure):
 # page job: int32 x 6 (seq, kv_head, page, num_valid, token_start, is_recent)
 PAGE_JOB_INTS = 6
 
-EXPORTS = ["carekv_store_pages", "carekv_store_workspace_bytes", "carekv_append_rows", "carekv_decode_attn",
+EXPORTS = ["carekv_store_pages", "carekv_store_prefill", "carekv_store_workspace_bytes", "carekv_append_rows", "carekv_decode_attn",
            "carekv_decode_workspace_bytes", "carekv_read_pages", "carekv_quantize_rows", "carekv_prefill_attn",
            "carekv_dequantize_rows", "carekv_kivi_qdq", "carekv_prefill_correct",
            "carekv_prefill_correct_workspace_bytes", "carekv_decode_attn_static", "carekv_write_base", "carekv_append_coded_rows",
@@ -110,6 +114,9 @@ def load(path: str | None = None):
         lib.carekv_store_workspace_bytes.argtypes = [C.POINTER(Arena), C.POINTER(StoreParams), i32]
         lib.carekv_store_pages.restype = C.c_int
         lib.carekv_store_pages.argtypes = [C.POINTER(Arena), C.POINTER(StoreParams), vp, vp, vp, i32, vp, i32, vp, vp]
+        lib.carekv_store_prefill.restype = C.c_int
+        lib.carekv_store_prefill.argtypes = [C.POINTER(Arena), C.POINTER(StoreParams), vp, vp, C.POINTER(PrefillGrid),
+                                             vp, vp]
         lib.carekv_append_rows.restype = C.c_int
         lib.carekv_append_rows.argtypes = [C.POINTER(Arena), vp, vp, vp, i32, vp]
         lib.carekv_decode_workspace_bytes.restype = i64

@@ -255,6 +255,9 @@ class CAREKVCache:
         self._ws: Dict[str, torch.Tensor] = {}
         self._row_tables: Dict[tuple, torch.Tensor] = {}
         self.status = _lib.StatusWatch()  # store calls' slot-overflow words, read without a sync
+        # optional (start, end) torch.cuda.Event pair that write_prefill records
+        # on the stream right before and after its store launches
+        self.store_events = None
         _lib.load()
 
     # ------------------------------------------------------------ C structs
@@ -396,31 +399,24 @@ class CAREKVCache:
             padc = lambda x: torch.nn.functional.pad(x, (0, 0, 0, pad)) if pad else x  # noqa: E731
             kivi_in = (padc(kc).contiguous().view(-1, D), padc(vc).contiguous().view(-1, D),
                        padc(vs.unsqueeze(-1).expand(B, H, T, G)).contiguous().view(-1, G))
-        # page jobs, sequence-major then kv head then page (the reference's
-        # per-head page loop order); each (sequence, kv head) takes the next
-        # n_new page ids of its row at once
+        # the page jobs, sequence-major then kv head then page (the reference's
+        # per-head page loop order), are generated on the device from each
+        # (sequence, kv head)'s first page id: it takes the next n_new page
+        # ids of its row at once
         sarr = np.asarray(seqs, dtype=np.int64)
         start = self.next_page[layer][:, sarr].T.astype(np.int64)          # (B, H)
         assert (start + n_new <= cfg.max_pages).all(), "KV cache is full"
         pr = np.arange(n_new, dtype=np.int64)
-        pids = start[:, :, None] + pr                                        # (B, H, n_new)
-        nv = np.minimum(ps, T - pr * ps)
-        tstart = token_start_abs + pr * ps
-        jobs = np.empty((B, H, n_new, _lib.PAGE_JOB_INTS), dtype=np.int32)
-        jobs[..., 0] = sarr[:, None, None]
-        jobs[..., 1] = np.arange(H)[None, :, None]
-        jobs[..., 2] = pids
-        jobs[..., 3] = nv
-        jobs[..., 4] = tstart
-        jobs[..., 5] = pr >= n_new - 4
-        jobs = jobs.reshape(B * H * n_new, _lib.PAGE_JOB_INTS)
-        hh, ss = np.arange(H)[None, :, None], sarr[:, None, None]
-        self.valid_host[layer, hh, ss, pids] = nv
-        self._token_start[layer, hh, ss, pids] = tstart
+        nv = np.minimum(ps, T - pr * ps).astype(np.int32)
+        tstart = (token_start_abs + pr * ps).astype(np.int32)
+        for s0 in np.unique(start):  # host copies of valid / token_start, one slice per first page id
+            hs, bs = np.nonzero(start.T == s0)
+            self.valid_host[layer, hs, sarr[bs], s0:s0 + n_new] = nv
+            self._token_start[layer, hs, sarr[bs], s0:s0 + n_new] = tstart
         self.next_page[layer][:, sarr] += n_new
-        group_ptr = (np.arange(B + 1) * (H * n_new)).astype(np.int32)
-        jobs_d = to_device(jobs, self.device)
-        gp_d = to_device(group_ptr, self.device)
+        rows_d = to_device(np.concatenate([sarr, start.reshape(-1)]).astype(np.int32), self.device)
+        grid = _lib.PrefillGrid(n_rows=B, n_tokens=T, token_start=int(token_start_abs), rows=rows_d.data_ptr())
+        n_jobs = B * H * n_new
         knobs = resolve_store_knobs(cfg, layer)
         sp = _lib.StoreParams(k_budget=knobs.k_budget, v_budget=knobs.v_budget, joint_budget=knobs.joint_budget,
                               joint=int(knobs.joint), store_none=int(knobs.store_none),
@@ -432,14 +428,18 @@ class CAREKVCache:
             sp.k_codes_in, sp.v_codes_in, sp.v_scale_in = (t.data_ptr() for t in kivi_in)
         lib = _lib.load()
         a = self.arena(layer)
-        ws = self.workspace("store", _lib.store_workspace_bytes(lib, a, sp, len(jobs)))
-        _lib.check(lib.carekv_store_pages(a, sp, Kp.data_ptr(), Vp.data_ptr(), jobs_d.data_ptr(), len(jobs),
-                                          gp_d.data_ptr(), B, ws.data_ptr(), _lib.stream_ptr(self.device)),
-                   "carekv_store_pages")
+        ws = self.workspace("store", _lib.store_workspace_bytes(lib, a, sp, n_jobs))
+        ev = self.store_events  # (start, end) events around the store launches, for timing
+        if ev is not None:
+            ev[0].record()
+        _lib.check(lib.carekv_store_prefill(a, sp, Kp.data_ptr(), Vp.data_ptr(), grid, ws.data_ptr(),
+                                            _lib.stream_ptr(self.device)), "carekv_store_prefill")
+        if ev is not None:
+            ev[1].record()
         if _lib.check_enabled():
-            _lib.check_status(ws, 4 * len(jobs), "carekv_store_pages")
+            _lib.check_status(ws, 4 * n_jobs, "carekv_store_prefill")
         else:
-            self.status.watch(ws, 4 * len(jobs), "carekv_store_pages")
+            self.status.watch(ws, 4 * n_jobs, "carekv_store_prefill")
         if self.rescale_open:  # the last page stays open: keep its rows' fp16 group scales
             last = T - (n_new - 1) * ps
             if last < ps:

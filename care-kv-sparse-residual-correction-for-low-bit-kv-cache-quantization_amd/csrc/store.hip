@@ -664,25 +664,29 @@ __device__ __forceinline__ void store_page(const carekv_arena& A, const carekv_s
   // ---- uniform candidate errors and the store decision (residual_store.py:372-422).  Every
   // candidate's prior is err * sensitivity * struct_prior with the same positive factor, so
   // priors order as the errors do and are positive where the errors are (sensitivity > 0).
-  float kerr[NG];
+  // The errors are non-negative floats, which order as their bit patterns: the ranks are
+  // integer compares of uniform values (a NaN error is not positive, as a NaN prior).
+  uint32_t ke[NG], ve[kNvb];
 #pragma unroll
-  for (int g = 0; g < NG; ++g) kerr[g] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(kerr_l), g * LPG));
+  for (int g = 0; g < NG; ++g) ke[g] = (uint32_t)__builtin_amdgcn_readlane(__float_as_int(kerr_l), g * LPG);
+#pragma unroll
+  for (int b = 0; b < kNvb; ++b) ve[b] = __float_as_uint(verr[b]);
   int nk = 0, nv = 0;
   uint32_t kord = 0, vord = 0;
   if (!sp.store_none && sp.sensitivity > 0.0) {
     bool kp[NG], vp[kNvb];
 #pragma unroll
-    for (int c = 0; c < NG; ++c) kp[c] = kerr[c] > 0.f;
+    for (int c = 0; c < NG; ++c) kp[c] = ke[c] - 1u < 0x7f800000u;  // 0 < err <= inf
 #pragma unroll
-    for (int b = 0; b < kNvb; ++b) vp[b] = verr[b] > 0.f;
+    for (int b = 0; b < kNvb; ++b) vp[b] = ve[b] - 1u < 0x7f800000u;
 #pragma unroll
     for (int c = 0; c < NG; ++c) {
       if (!kp[c]) continue;
       int rank = 0, vbefore = 0;  // stable descending order; V before K only on a larger error
 #pragma unroll
-      for (int c2 = 0; c2 < NG; ++c2) rank += kp[c2] && (kerr[c2] > kerr[c] || (kerr[c2] == kerr[c] && c2 < c));
+      for (int c2 = 0; c2 < NG; ++c2) rank += kp[c2] && (ke[c2] > ke[c] || (ke[c2] == ke[c] && c2 < c));
 #pragma unroll
-      for (int b = 0; b < kNvb; ++b) vbefore += vp[b] && verr[b] > kerr[c];
+      for (int b = 0; b < kNvb; ++b) vbefore += vp[b] && ve[b] > ke[c];
       const bool sel = sp.joint ? rank + vbefore < sp.joint_budget : rank < sp.k_budget;
       if (sel) { kord |= (uint32_t)c << (2 * rank); ++nk; }
     }
@@ -691,9 +695,9 @@ __device__ __forceinline__ void store_page(const carekv_arena& A, const carekv_s
       if (!vp[b]) continue;
       int rank = 0, kbefore = 0;
 #pragma unroll
-      for (int b2 = 0; b2 < kNvb; ++b2) rank += vp[b2] && (verr[b2] > verr[b] || (verr[b2] == verr[b] && b2 < b));
+      for (int b2 = 0; b2 < kNvb; ++b2) rank += vp[b2] && (ve[b2] > ve[b] || (ve[b2] == ve[b] && b2 < b));
 #pragma unroll
-      for (int c = 0; c < NG; ++c) kbefore += kp[c] && kerr[c] >= verr[b];
+      for (int c = 0; c < NG; ++c) kbefore += kp[c] && ke[c] >= ve[b];
       const bool sel = sp.joint ? rank + kbefore < sp.joint_budget : rank < sp.v_budget;
       if (sel) { vord |= (uint32_t)b << (2 * rank); ++nv; }
     }
@@ -717,8 +721,12 @@ __device__ __forceinline__ void store_page(const carekv_arena& A, const carekv_s
     const int b = (vord >> (2 * i)) & 3;
     // pack_4bit(R_V[4b .. 4b+3, :]): chunk b of every lane, in row-major order
     h2_t v[NP];
-#pragma unroll
-    for (int p = 0; p < NP; ++p) v[p] = b == 0 ? rv[0][p] : (b == 1 ? rv[1][p] : (b == 2 ? rv[2][p] : rv[3][p]));
+    switch (b) {  // b is uniform
+      case 0: for (int p = 0; p < NP; ++p) v[p] = rv[0][p]; break;
+      case 1: for (int p = 0; p < NP; ++p) v[p] = rv[1][p]; break;
+      case 2: for (int p = 0; p < NP; ++p) v[p] = rv[2][p]; break;
+      default: for (int p = 0; p < NP; ++p) v[p] = rv[3][p]; break;
+    }
     const float m = h2f((uint16_t)rows_max_u(grp_max_u<16>(absmax_bits<NP>(v))));
     const float s = fmaxf(m, 1e-8f) / 7.0f;
     const uint32_t w = pack_res<NP>(v, s);
@@ -747,6 +755,37 @@ __device__ __forceinline__ void store_page(const carekv_arena& A, const carekv_s
   }
 }
 
+// Page jobs of a store call: an explicit job array with its sequence
+// groups, or a prompt chunk's grid (carekv_prefill_grid) that generates
+// job j = (row b, kv head h, page p) in row-major order, group b = row b.
+struct JobSrc {
+  const carekv_page_job* jobs;  // nullptr: the grid
+  const int32_t* group_ptr;
+  const int32_t* rows;          // grid: row slots, then first page ids
+  int32_t n_rows, n_kvh, n_pages, n_tokens, token_start;
+  __device__ __forceinline__ carekv_page_job get(int j) const {
+    if (jobs) return jobs[j];
+    const int p = j % n_pages, bh = j / n_pages, b = bh / n_kvh, h = bh - b * n_kvh;
+    carekv_page_job o;
+    o.seq = rows[b];
+    o.kv_head = h;
+    o.page = rows[n_rows + bh] + p;
+    o.num_valid = min(kPage, n_tokens - kPage * p);
+    o.token_start = token_start + kPage * p;
+    o.is_recent = p >= n_pages - 4;
+    return o;
+  }
+  __device__ __forceinline__ void group(int g, int& j0, int& j1) const {
+    if (jobs) {
+      j0 = group_ptr[g];
+      j1 = group_ptr[g + 1];
+    } else {
+      j0 = g * n_kvh * n_pages;
+      j1 = j0 + n_kvh * n_pages;
+    }
+  }
+};
+
 // Bytes of the sketch projection at the start of the store pass's LDS: the
 // 32 x sketch_dim fp32 matrix with its rows padded to a multiple of 16.
 __host__ __device__ constexpr int store_lds_p_bytes(int sd) { return kGroup * ((sd + 15) / 16 * 16) * 4; }
@@ -756,8 +795,7 @@ __host__ __device__ constexpr int store_lds_p_bytes(int sd) { return kGroup * ((
 template <int D, int BITS, int PATH>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 && PATH != kPathKivi ? 4 : 1))) void store_pages_kernel(carekv_arena A, carekv_store_params sp,
                                                           const uint16_t* __restrict__ Kx,
-                                                          const uint16_t* __restrict__ Vx,
-                                                          const carekv_page_job* __restrict__ jobs,
+                                                          const uint16_t* __restrict__ Vx, JobSrc src,
                                                           int n_jobs, StoreWs ws, StoreStage st) {
   extern __shared__ __align__(16) unsigned char smem[];
   const int SD = A.sketch_dim, SDp = (SD + 15) / 16 * 16;
@@ -772,7 +810,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 &&
   // the call's slot-overflow word (after the job records) starts clear; the scatter sets it
   if (blockIdx.x == 0 && threadIdx.x == 0) ws.v[n_jobs * 4] = 0;
   for (int job_id = blockIdx.x * 4 + wave; job_id < n_jobs; job_id += gridDim.x * 4)
-    store_page<D, BITS, PATH>(A, sp, Kx, Vx, jobs[job_id], job_id, ws, st, S, sP, SD, lane);
+    store_page<D, BITS, PATH>(A, sp, Kx, Vx, src.get(job_id), job_id, ws, st, S, sP, SD, lane);
 }
 
 // Exclusive scan of the per-job new-slot counts inside each sequence group
@@ -786,17 +824,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D == 128 &&
 // the wave-level exclusive scan.  Counts are at most 4 per job, so a wave
 // scans K and V counts packed as K | V << 16.
 constexpr int kScanRows = 24;
-__global__ __launch_bounds__(1024) void store_scan_kernel(carekv_arena A, const carekv_page_job* __restrict__ jobs,
-                                                          const int32_t* __restrict__ group_ptr, StoreWs ws) {
+__global__ __launch_bounds__(1024) void store_scan_kernel(carekv_arena A, JobSrc src, StoreWs ws) {
   __shared__ uint32_t s_wave[kScanRows][16];  // per row and wave: total (packed), then exclusive prefix
   __shared__ int2 s_row[kScanRows];           // per row: exclusive prefix over the rows (K, V)
   __shared__ int2 s_tot;
   const int g = blockIdx.x;
-  const int j0 = group_ptr[g], j1 = group_ptr[g + 1];
+  int j0, j1;
+  src.group(g, j0, j1);
   if (j1 <= j0) return;
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int n = j1 - j0;
-  const int seq = jobs[j0].seq;
+  const int seq = src.get(j0).seq;
   int carry_k = A.next_slot[2 * seq], carry_v = A.next_slot[2 * seq + 1];
   for (int base = 0; base < n; base += 1024 * kScanRows) {
     const int rows = min(kScanRows, (n - base + 1023) / 1024);
@@ -887,14 +925,14 @@ __device__ __forceinline__ int slot_of(int i, int n_old, const int* old, int n_c
 // The scatter: slot tables, slot payloads and scales, valid / has_meta of
 // every job (residual_store.py:424-438).  16 lanes per job, 16 jobs a block.
 template <int D>
-__global__ __launch_bounds__(256) void store_slots_kernel(carekv_arena A, const carekv_page_job* __restrict__ jobs,
-                                                          int n_jobs, StoreWs ws, StoreStage st) {
+__global__ __launch_bounds__(256) void store_slots_kernel(carekv_arena A, JobSrc src, int n_jobs, StoreWs ws,
+                                                          StoreStage st) {
   using L = PageLay<D>;
   constexpr int NG = L::NG, KSB = L::KSB, VSB = L::VSB, VP = VSB / 16;
   const int sub = threadIdx.x & 15;
   const int job_id = blockIdx.x * 16 + (threadIdx.x >> 4);
   if (job_id >= n_jobs) return;
-  const carekv_page_job job = jobs[job_id];
+  const carekv_page_job job = src.get(job_id);
   const uint32_t h = st.head[job_id];
   const int2 base = *reinterpret_cast<const int2*>(ws.v + (long)job_id * 4 + 2);
   const long pg = ((long)job.kv_head * A.n_seq + job.seq) * A.max_pages + job.page;
@@ -1423,22 +1461,22 @@ constexpr int kStorePassBlocks = 2048;
 
 template <int D, int BITS, int PATH>
 static int launch_pass(const carekv_arena& A, const carekv_store_params& sp, const uint16_t* K, const uint16_t* V,
-                       const carekv_page_job* jobs, int n_jobs, StoreWs ws, const StoreStage& st, hipStream_t s,
+                       const JobSrc& src, int n_jobs, StoreWs ws, const StoreStage& st, hipStream_t s,
                        const char* what) {
   const int blocks = std::min((n_jobs + 3) / 4, kStorePassBlocks);
   const int lds = store_lds_p_bytes(A.sketch_dim) + 4 * (int)sizeof(StoreLds<D>);
-  hipLaunchKernelGGL((store_pages_kernel<D, BITS, PATH>), dim3(blocks), dim3(256), lds, s, A, sp, K, V, jobs,
+  hipLaunchKernelGGL((store_pages_kernel<D, BITS, PATH>), dim3(blocks), dim3(256), lds, s, A, sp, K, V, src,
                      n_jobs, ws, st);
   CAREKV_CHECK_LAUNCH(what);
   return CAREKV_OK;
 }
 
 template <int D>
-static int launch_slots(const carekv_arena& A, const carekv_page_job* jobs, int n_jobs, const int32_t* group_ptr,
-                        int n_groups, StoreWs ws, const StoreStage& st, hipStream_t s) {
-  hipLaunchKernelGGL(store_scan_kernel, dim3(n_groups), dim3(1024), 0, s, A, jobs, group_ptr, ws);
+static int launch_slots(const carekv_arena& A, const JobSrc& src, int n_jobs, int n_groups, StoreWs ws,
+                        const StoreStage& st, hipStream_t s) {
+  hipLaunchKernelGGL(store_scan_kernel, dim3(n_groups), dim3(1024), 0, s, A, src, ws);
   CAREKV_CHECK_LAUNCH("store_scan");
-  hipLaunchKernelGGL((store_slots_kernel<D>), dim3((n_jobs + 15) / 16), dim3(256), 0, s, A, jobs, n_jobs, ws, st);
+  hipLaunchKernelGGL((store_slots_kernel<D>), dim3((n_jobs + 15) / 16), dim3(256), 0, s, A, src, n_jobs, ws, st);
   CAREKV_CHECK_LAUNCH("store_slots");
   return CAREKV_OK;
 }
@@ -1462,34 +1500,30 @@ static carekv_arena kivi_tail_view(const carekv_arena& A) {
 // the scatter.
 template <int D, int BITS>
 static int launch_store(const carekv_arena& A, const carekv_store_params& sp, const uint16_t* K, const uint16_t* V,
-                        const carekv_page_job* jobs, int n_jobs, const int32_t* group_ptr, int n_groups,
-                        StoreWs ws, const StoreStage& st, hipStream_t s) {
+                        const JobSrc& src, int n_jobs, int n_groups, StoreWs ws, const StoreStage& st,
+                        hipStream_t s) {
   int rc;
   if (A.kivi_packed) {
-    rc = launch_pass<D, 2, kPathKivi>(A, sp, K, V, jobs, n_jobs, ws, st, s, "store_pages (packed KIVI prefix)");
+    rc = launch_pass<D, 2, kPathKivi>(A, sp, K, V, src, n_jobs, ws, st, s, "store_pages (packed KIVI prefix)");
     if (rc == CAREKV_OK)
-      rc = launch_pass<D, 16, kPathHat>(kivi_tail_view(A), sp, K, V, jobs, n_jobs, ws, st, s,
+      rc = launch_pass<D, 16, kPathHat>(kivi_tail_view(A), sp, K, V, src, n_jobs, ws, st, s,
                                         "store_pages (packed KIVI tail)");
   } else if constexpr (BITS == 16) {
-    rc = launch_pass<D, 16, kPathHat>(A, sp, K, V, jobs, n_jobs, ws, st, s, "store_pages (fp16 base)");
+    rc = launch_pass<D, 16, kPathHat>(A, sp, K, V, src, n_jobs, ws, st, s, "store_pages (fp16 base)");
   } else if (sp.k_codes_in) {
-    rc = launch_pass<D, BITS, kPathCodesIn>(A, sp, K, V, jobs, n_jobs, ws, st, s, "store_pages (given base)");
+    rc = launch_pass<D, BITS, kPathCodesIn>(A, sp, K, V, src, n_jobs, ws, st, s, "store_pages (given base)");
   } else if (sp.keep_base) {
-    rc = launch_pass<D, BITS, kPathKeep>(A, sp, K, V, jobs, n_jobs, ws, st, s, "store_pages (kept base)");
+    rc = launch_pass<D, BITS, kPathKeep>(A, sp, K, V, src, n_jobs, ws, st, s, "store_pages (kept base)");
   } else {
-    rc = launch_pass<D, BITS, kPathFresh>(A, sp, K, V, jobs, n_jobs, ws, st, s, "store_pages");
+    rc = launch_pass<D, BITS, kPathFresh>(A, sp, K, V, src, n_jobs, ws, st, s, "store_pages");
   }
   if (rc != CAREKV_OK) return rc;
-  return launch_slots<D>(A, jobs, n_jobs, group_ptr, n_groups, ws, st, s);
+  return launch_slots<D>(A, src, n_jobs, n_groups, ws, st, s);
 }
 
-extern "C" int carekv_store_pages(const carekv_arena* arena, const carekv_store_params* sp, const uint16_t* K,
-                                  const uint16_t* V, const carekv_page_job* jobs_dev, int32_t n_jobs,
-                                  const int32_t* group_ptr_dev, int32_t n_groups, void* workspace,
-                                  void* stream) {
-  CAREKV_REQUIRE(arena && sp && K && V && jobs_dev && group_ptr_dev && workspace, "null argument");
-  CAREKV_REQUIRE(n_jobs >= 0 && n_groups >= 0, "negative sizes");
-  if (n_jobs == 0) return CAREKV_OK;
+// Checks and dispatch shared by carekv_store_pages and carekv_store_prefill.
+static int store_any(const carekv_arena* arena, const carekv_store_params* sp, const uint16_t* K, const uint16_t* V,
+                     const JobSrc& src, int n_jobs, int n_groups, void* workspace, void* stream) {
   const carekv_arena& A = *arena;
   CAREKV_REQUIRE(check_arena(A), last_error_buf());
   CAREKV_REQUIRE(A.residual_bits == 4, "kernels support residual_bits=4");
@@ -1501,21 +1535,52 @@ extern "C" int carekv_store_pages(const carekv_arena* arena, const carekv_store_
     CAREKV_REQUIRE(sp->k_hat && sp->v_hat && sp->k_codes_in && sp->v_codes_in && sp->v_scale_in,
                    "a packed KIVI arena stores from k_hat, v_hat, k_codes_in, v_codes_in and v_scale_in");
     CAREKV_REQUIRE(!sp->keep_base, "keep_base is built for the uniform packed bases");
-    if (A.head_dim == 64) return launch_store<64, 2>(A, *sp, K, V, jobs_dev, n_jobs, group_ptr_dev, n_groups, ws, st, s);
-    return launch_store<128, 2>(A, *sp, K, V, jobs_dev, n_jobs, group_ptr_dev, n_groups, ws, st, s);
+    if (A.head_dim == 64) return launch_store<64, 2>(A, *sp, K, V, src, n_jobs, n_groups, ws, st, s);
+    return launch_store<128, 2>(A, *sp, K, V, src, n_jobs, n_groups, ws, st, s);
   }
   if (A.base_bits == 16) {
     CAREKV_REQUIRE(sp->k_hat && sp->v_hat, "the fp16 base (base_bits=16) needs k_hat and v_hat");
     CAREKV_REQUIRE(!sp->keep_base, "keep_base (streaming store) is built for the packed bases");
-    if (A.head_dim == 64) return launch_store<64, 16>(A, *sp, K, V, jobs_dev, n_jobs, group_ptr_dev, n_groups, ws, st, s);
-    return launch_store<128, 16>(A, *sp, K, V, jobs_dev, n_jobs, group_ptr_dev, n_groups, ws, st, s);
+    if (A.head_dim == 64) return launch_store<64, 16>(A, *sp, K, V, src, n_jobs, n_groups, ws, st, s);
+    return launch_store<128, 16>(A, *sp, K, V, src, n_jobs, n_groups, ws, st, s);
   }
   CAREKV_REQUIRE(!sp->k_codes_in || (sp->k_scale_in && sp->v_codes_in && sp->v_scale_in),
                  "k_codes_in needs k_scale_in, v_codes_in and v_scale_in");
   return dispatch_db(A.head_dim, A.base_bits, [&](auto d, auto b) {
-    return launch_store<decltype(d)::value, decltype(b)::value>(A, *sp, K, V, jobs_dev, n_jobs, group_ptr_dev,
-                                                                n_groups, ws, st, s);
+    return launch_store<decltype(d)::value, decltype(b)::value>(A, *sp, K, V, src, n_jobs, n_groups, ws, st, s);
   });
+}
+
+extern "C" int carekv_store_pages(const carekv_arena* arena, const carekv_store_params* sp, const uint16_t* K,
+                                  const uint16_t* V, const carekv_page_job* jobs_dev, int32_t n_jobs,
+                                  const int32_t* group_ptr_dev, int32_t n_groups, void* workspace,
+                                  void* stream) {
+  CAREKV_REQUIRE(arena && sp && K && V && jobs_dev && group_ptr_dev && workspace, "null argument");
+  CAREKV_REQUIRE(n_jobs >= 0 && n_groups >= 0, "negative sizes");
+  if (n_jobs == 0) return CAREKV_OK;
+  JobSrc src{};
+  src.jobs = jobs_dev;
+  src.group_ptr = group_ptr_dev;
+  return store_any(arena, sp, K, V, src, n_jobs, n_groups, workspace, stream);
+}
+
+extern "C" int carekv_store_prefill(const carekv_arena* arena, const carekv_store_params* sp, const uint16_t* K,
+                                    const uint16_t* V, const carekv_prefill_grid* grid, void* workspace,
+                                    void* stream) {
+  CAREKV_REQUIRE(arena && sp && K && V && grid && grid->rows && workspace, "null argument");
+  CAREKV_REQUIRE(grid->n_rows > 0 && grid->n_tokens > 0 && grid->token_start >= 0, "empty or negative grid");
+  const int ps = arena->page_size > 0 ? arena->page_size : kPage;
+  const int64_t n_pages = (grid->n_tokens + ps - 1) / ps;
+  const int64_t n_jobs = (int64_t)grid->n_rows * arena->n_kv_heads * n_pages;
+  CAREKV_REQUIRE(n_jobs < (1ll << 31), "grid too large");
+  JobSrc src{};
+  src.rows = grid->rows;
+  src.n_rows = grid->n_rows;
+  src.n_kvh = arena->n_kv_heads;
+  src.n_pages = (int32_t)n_pages;
+  src.n_tokens = grid->n_tokens;
+  src.token_start = grid->token_start;
+  return store_any(arena, sp, K, V, src, (int)n_jobs, grid->n_rows, workspace, stream);
 }
 
 namespace {

@@ -191,6 +191,30 @@ int carekv_store_pages(const carekv_arena* arena, const carekv_store_params* sp,
                        const uint16_t* K, const uint16_t* V, const carekv_page_job* jobs_dev,
                        int32_t n_jobs, const int32_t* group_ptr_dev, int32_t n_groups,
                        void* workspace, void* stream);
+/* A prompt chunk of n_rows sequences, every kv head, as page jobs the
+ * device generates (carekv_store_prefill): job j is (row b, kv head h,
+ * page p) in row-major order over (n_rows, n_kv_heads, n_pages), n_pages =
+ * ceil(n_tokens / page_size), with seq = rows[b], page = rows[n_rows +
+ * b * n_kv_heads + h] + p, num_valid = min(page_size, n_tokens - p *
+ * page_size), token_start = token_start + p * page_size, is_recent =
+ * p >= n_pages - 4 (layer.py:254-275); one sequence group per row. */
+typedef struct carekv_prefill_grid {
+  int32_t n_rows;        /* B > 0                                            */
+  int32_t n_tokens;      /* T > 0 tokens per row                             */
+  int32_t token_start;   /* absolute position of the chunk's first token     */
+  const int32_t* rows;   /* device int32 [n_rows + n_rows * n_kv_heads]      */
+} carekv_prefill_grid;
+
+/* carekv_store_pages over the jobs of a prompt chunk's grid, generated on
+ * the device: what CAREKVLayer.prefill runs for every kv head
+ * (_write_pages_for_kv_head, layer.py:204-334) in one call, without a host
+ * job list.  K, V: fp16 [n_rows][n_kv_heads][n_pages * page_size]
+ * [head_dim], zero padded past n_tokens; workspace as carekv_store_pages
+ * with n_jobs = n_rows * n_kv_heads * n_pages. */
+int carekv_store_prefill(const carekv_arena* arena, const carekv_store_params* sp,
+                         const uint16_t* K, const uint16_t* V, const carekv_prefill_grid* grid,
+                         void* workspace, void* stream);
+
 /* Workspace bytes of a carekv_store_pages call with these arena, params and
  * job count (the staging area is sized by head_dim and the per-page
  * budgets); -1 on a null argument.  The int32 at workspace[4 * n_jobs] is

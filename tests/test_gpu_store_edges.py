@@ -157,3 +157,38 @@ def test_store_tiny_values(bits):
     cache.write_prefill(0, torch.from_numpy(K).cuda(), torch.from_numpy(V).cuda())
     torch.cuda.synchronize()
     _check_slices(cache, common, K, V, H, P)
+
+
+def test_prefill_grid_ragged_starts_match_single():
+    """carekv_store_prefill's device-generated jobs: a second prompt chunk
+    for three sequences whose first chunks had different lengths (so each
+    (sequence, kv head) starts at its own page), in one call, leaves the
+    arena byte-identical to the same chunk written one sequence at a time."""
+    import care_kv
+    H, D = 2, 128
+    cfg = care_kv.CacheConfig(num_layers=1, num_heads=4, num_kv_heads=H, head_dim=D, page_size=16, max_pages=24,
+                              base_bits=3, group_size=32, k_channel_group=32, v_token_block=4, sketch_dim=32,
+                              packed_base=True, scale_quant="int8", store_budget_mode="absolute", store_abs_k=2,
+                              store_abs_v=1, read_budget_ratio=0.0, compat=True)
+    g = torch.Generator().manual_seed(5)
+    first = [48, 16, 80]
+    chunk = [torch.randn(3, H, 37, D, generator=g).half() for _ in range(2)]
+    pre = [[torch.randn(H, n, D, generator=g).half() for _ in range(2)] for n in first]
+    caches = []
+    for batched in (True, False):
+        c = care_kv.CAREKVCache(cfg, device="cuda", n_seq=3)
+        for s, (k, v) in enumerate(pre):
+            c.write_prefill(0, k.cuda(), v.cuda(), seqs=[s])
+        if batched:
+            c.write_prefill(0, chunk[0].cuda(), chunk[1].cuda(), token_start_abs=0, seqs=[0, 1, 2])
+        else:
+            for s in range(3):
+                c.write_prefill(0, chunk[0][s:s + 1].cuda(), chunk[1][s:s + 1].cuda(), token_start_abs=0, seqs=[s])
+        torch.cuda.synchronize()
+        caches.append(c)
+    a, b = caches
+    for nm in ("kcodes", "vcodes", "kscale", "vscale", "kmaster", "vmaster", "valid", "has_meta", "k_slot", "v_slot",
+               "k_err", "v_err", "k_sketch", "v_sq", "k_res", "v_res", "k_res_scale", "v_res_scale", "next_slot"):
+        assert torch.equal(getattr(a, nm), getattr(b, nm)), nm
+    assert np.array_equal(a.valid_host, b.valid_host) and np.array_equal(a._token_start, b._token_start)
+    assert np.array_equal(a.next_page, b.next_page)

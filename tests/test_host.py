@@ -47,7 +47,8 @@ def test_c_structs_match_header_layout():
     hdr = open(os.path.join(ROOT, "include", "carekv.h")).read()
     for cname, py in (("carekv_arena", _lib.Arena), ("carekv_store_params", _lib.StoreParams),
                       ("carekv_decode_params", _lib.DecodeParams), ("carekv_prefill_params", _lib.PrefillParams),
-                      ("carekv_prefill_eval_params", _lib.PrefillEvalParams)):
+                      ("carekv_prefill_eval_params", _lib.PrefillEvalParams),
+                      ("carekv_prefill_grid", _lib.PrefillGrid)):
         assert [f[0] for f in py._fields_] == _struct_fields(hdr, cname), cname
 
 
