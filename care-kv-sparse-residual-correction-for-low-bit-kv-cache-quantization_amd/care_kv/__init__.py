@@ -3,7 +3,7 @@
 The public surface follows the reference package's ``__init__`` (same names,
 arguments and results): the cache and its configuration, the quantizer and
 bit packers, the store-time and read-time residual classes, the attention
-and layer classes, the LLaMA patch and the debug counters; the compute runs
+and layer classes, the LLaMA patch the debug counters and the analysis utilities; the compute runs
 in ``libcarekv_hip.so`` through a C ABI (include/carekv.h).  Additions of
 this build: the batched entry points ``decode_attention`` /
 ``prefill_correction`` / ``prefill_attention``, ``CAREKVAdapter`` and
@@ -21,6 +21,9 @@ from .attention import (CAREKVAttention, CAREKVMultiHeadAttention, apply_slot_co
                         get_debug_stats, prefill_correction, reset_debug_stats)
 from .prefill import dequantize_rows, prefill_attention, prefill_eval, quant_dequant, quantize_rows
 from .layer import CAREKVLayer
+from .attention import get_imp_per_layer
+from .utils import (ABLATION_VARIANTS, budget_sweep, calibrate_layer_sensitivity, compute_boundary_risk_stats,
+                    compute_perplexity, estimate_memory_bytes, print_memory_table)
 from .llama_patch import CAREKVHFCache, CAREKVLlamaAttention, patch_llama_model, reset_all_caches
 from .adapter import CAREKVAdapter
 from ._lib import CarekvError
@@ -39,8 +42,12 @@ __all__ = [
     "ResidualStoreManager", "pack_4bit", "unpack_4bit",
     "ResidualRouter",
     "CAREKVAttention", "CAREKVMultiHeadAttention", "apply_slot_corrections",
-    "CAREKVLayer", "get_debug_stats", "reset_debug_stats",
+    "CAREKVLayer", "get_debug_stats", "reset_debug_stats", "get_imp_per_layer",
     "CAREKVLlamaAttention", "patch_llama_model", "reset_all_caches",
+    "estimate_memory_bytes", "print_memory_table",
+    "calibrate_layer_sensitivity", "compute_perplexity",
+    "budget_sweep", "compute_boundary_risk_stats",
+    "ABLATION_VARIANTS",
     # additions of this build
     "resolve_read_knobs", "resolve_store_knobs", "get_sketch_proj", "kivi_qdq", "kivi_codes",
     "decode_attention", "prefill_correction", "prefill_attention", "prefill_eval", "quantize_rows", "dequantize_rows",

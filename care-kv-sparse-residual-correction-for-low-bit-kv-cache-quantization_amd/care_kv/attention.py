@@ -51,24 +51,76 @@ def _read_counts_ptr(device) -> int:
     return t.data_ptr()
 
 
+# Host-side sums of the reference's debug dict: the delta norms of the
+# per-query correction (apply_slot_corrections / CAREKVAttention with a
+# debug dict, attention.py:358-372) and the token-importance dispersion of
+# the carekv_stored prefill (CAREKV_DUMP_IMPORTANCE=1, layer.py:477-502).
+# The batched decode and prefill kernels, like the reference's vectorized
+# path (attention.py:945-947), count slot reads only.
+_HOST_STATS = {"delta_v_norm_sum": 0.0, "delta_k_norm_sum": 0.0, "delta_o_norm_sum": 0.0, "o_base_norm_sum": 0.0,
+               "imp_gini_sum": 0.0, "imp_norm_entropy_sum": 0.0, "imp_top1pct_mass_sum": 0.0, "imp_count": 0}
+# layer id -> [gini sum, normalised entropy sum, top-1% mass sum, count]
+_IMP_PER_LAYER: dict = {}
+
+
 def get_debug_stats() -> dict:
-    """layer.py:120-121: a snapshot of the debug counters (reads the device
-    counters back).  k_slots_read / v_slots_read / n_queries are counted on
-    the device; the delta-norm sums of the reference's per-query path are not
-    accumulated (0.0)."""
+    """layer.py:120-121: a snapshot of the debug counters.  k_slots_read /
+    v_slots_read / n_queries are counted on the device by every corrected
+    launch (read back here); the delta-norm sums accumulate on the per-query
+    path and the importance sums in the carekv_stored prefill."""
     k = v = n = 0
     for t in _READ_COUNTS.values():
         a, b, c = (int(x) for x in t.tolist())
         k, v, n = k + a, v + b, n + c
-    return {"v_slots_read": v, "k_slots_read": k, "n_queries": n, "delta_v_norm_sum": 0.0,
-            "delta_k_norm_sum": 0.0, "delta_o_norm_sum": 0.0, "o_base_norm_sum": 0.0, "imp_gini_sum": 0.0,
-            "imp_norm_entropy_sum": 0.0, "imp_top1pct_mass_sum": 0.0, "imp_count": 0}
+    return {"v_slots_read": v, "k_slots_read": k, "n_queries": n, **_HOST_STATS}
 
 
 def reset_debug_stats() -> None:
     """layer.py:123-126."""
     for t in _READ_COUNTS.values():
         t.zero_()
+    for key in _HOST_STATS:
+        _HOST_STATS[key] = 0 if key == "imp_count" else 0.0
+    _IMP_PER_LAYER.clear()
+
+
+def get_imp_per_layer() -> dict:
+    """layer.py:107-114: per-layer means of the token-importance dispersion
+    (empty unless CAREKV_DUMP_IMPORTANCE=1 and CAREKV_DEBUG_STATS=1 were set
+    during a carekv_stored prefill)."""
+    return {lid: dict(gini=g / c, norm_entropy=e / c, top1pct_mass=t / c, count=c)
+            for lid, (g, e, t, c) in _IMP_PER_LAYER.items() if c}
+
+
+def importance_probe(layer_id: int, q: torch.Tensor, k_hat: torch.Tensor) -> None:
+    """layer.py:477-502 for one prompt: the attention mass each key gets
+    from every query head and causal prompt row of the base attention over
+    K_hat (fp32 softmax), its Gini coefficient, entropy normalised by
+    log(N) and the mass share of the top 1% of keys, added to the debug
+    sums and the layer's.  q (Hq, T, D), k_hat (Hkv, T, D)."""
+    Hq, T, D = q.shape
+    grp = Hq // k_hat.shape[0]
+    mass = torch.zeros(T, dtype=torch.float32, device=q.device)
+    causal = torch.ones(T, T, dtype=torch.bool, device=q.device).tril_()
+    for h in range(Hq):
+        s = (q[h].float() @ k_hat[h // grp].float().transpose(0, 1)) / math.sqrt(D)
+        mass += torch.softmax(s.masked_fill(~causal, float("-inf")), dim=-1).sum(0)
+    tot = mass.sum().clamp_min(1e-9)
+    p = mass / tot
+    ent = float(-(p * (p + 1e-12).log()).sum() / math.log(max(T, 2)))
+    srt = torch.sort(mass).values
+    i = torch.arange(1, T + 1, device=q.device, dtype=srt.dtype)
+    gini = float(((2 * i - T - 1) * srt).sum() / (T * srt.sum().clamp_min(1e-9)))
+    top1 = float(torch.topk(mass, max(1, T // 100)).values.sum() / tot)
+    _HOST_STATS["imp_gini_sum"] += gini
+    _HOST_STATS["imp_norm_entropy_sum"] += ent
+    _HOST_STATS["imp_top1pct_mass_sum"] += top1
+    _HOST_STATS["imp_count"] += 1
+    acc = _IMP_PER_LAYER.setdefault(layer_id, [0.0, 0.0, 0.0, 0])
+    acc[0] += gini
+    acc[1] += ent
+    acc[2] += top1
+    acc[3] += 1
 
 
 def decode_read_mode(cfg: CacheConfig, layer: int):
@@ -284,11 +336,63 @@ def apply_slot_corrections(cache: CAREKVCache, cfg: CacheConfig, router, layer_i
     if O_base is None:
         O_base, _ = single_query_decode(cache, layer_id, kv_head, q, seq=seq, page_ids=page_ids, correction=False)
     if debug_stats is not None:
-        nk = sum(1 for c in sel if c[0] == 0)
-        debug_stats["k_slots_read"] = debug_stats.get("k_slots_read", 0) + nk
-        debug_stats["v_slots_read"] = debug_stats.get("v_slots_read", 0) + len(sel) - nk
-        debug_stats["n_queries"] = debug_stats.get("n_queries", 0) + 1
+        _debug_accumulate(debug_stats, cache, layer_id, kv_head, seq, page_ids, q, sel, out, O_base, k_corr_scale)
     return out.float() - O_base.float()
+
+
+def _base_rows(cache: CAREKVCache, layer: int, kv_head: int, page_ids, seq: int):
+    """(K_hat, V_hat) fp16 (N, D) of the listed pages' valid rows as the
+    decode reads them, and their valid counts."""
+    if cache.hat:
+        return cache.read_base_hat_concat(layer, kv_head, page_ids, seq=seq)
+    from .prefill import dequantize_rows
+    kc, ks, vc, vs, lens = cache.read_base_concat(layer, kv_head, page_ids, seq=seq)
+    g = cache.cfg.group_size
+    return dequantize_rows(kc, ks, g), dequantize_rows(vc, vs, g), lens
+
+
+def _debug_accumulate(stats: dict, cache: CAREKVCache, layer: int, kv_head: int, seq: int, page_ids, q, sel, out,
+                      O_base, k_corr_scale: float) -> None:
+    """The debug sums of one corrected query (attention.py:358-372): slots
+    read, |dV| of the linear V term sum_t a_t R_V,t over the selected V
+    blocks, |k_corr_scale dK| of the linear K term sum_t a_t (q . R_K,t)
+    (V_t - O_base) over the selected K groups (attention.py:273-340), |dO|
+    of the applied correction and |O_base|; a_t is the fp32 softmax of the
+    listed pages' K_hat rows."""
+    cfg = cache.cfg
+    pids = cache.all_page_ids(layer, kv_head, seq) if page_ids is None else [int(p) for p in page_ids]
+    nk = sum(1 for c in sel if c[0] == 0)
+    stats["k_slots_read"] = stats.get("k_slots_read", 0) + nk
+    stats["v_slots_read"] = stats.get("v_slots_read", 0) + len(sel) - nk
+    stats["n_queries"] = stats.get("n_queries", 0) + 1
+    D, ps, cg, vb = cfg.head_dim, cfg.page_size, cfg.k_channel_group, cfg.v_token_block
+    Kh, Vh, lens = _base_rows(cache, layer, kv_head, pids, seq)
+    qf = q.float().reshape(-1)
+    a = torch.softmax((Kh.float() @ qf) / math.sqrt(D), dim=0)
+    off = np.concatenate([[0], np.cumsum(lens)]).astype(np.int64)
+    where = {p: i for i, p in enumerate(pids)}
+    Ob = O_base.float().reshape(-1)
+    dV = torch.zeros(D, dtype=torch.float32, device=q.device)
+    dK = torch.zeros_like(dV)
+    from .residual import unpack_4bit
+    for kind_, page, sub in sel:
+        i = where[page]
+        p0, n = int(off[i]), int(lens[i])
+        if kind_ == 1:
+            slot = int(cache.v_slot[layer, kv_head, seq, page, sub])
+            R = unpack_4bit(cache.v_res[seq, slot], cache.v_res_scale[seq, slot:slot + 1], vb * D).view(vb, D)
+            t0, t1 = sub * vb, min(sub * vb + vb, n)
+            if t1 > t0:
+                dV += (a[p0 + t0:p0 + t1, None] * R[:t1 - t0]).sum(0)
+        else:
+            slot = int(cache.k_slot[layer, kv_head, seq, page, sub])
+            R = unpack_4bit(cache.k_res[seq, slot], cache.k_res_scale[seq, slot:slot + 1], ps * cg).view(ps, cg)[:n]
+            qd = R @ qf[sub * cg:(sub + 1) * cg]
+            dK += ((a[p0:p0 + n] * qd)[:, None] * (Vh[p0:p0 + n].float() - Ob)).sum(0)
+    stats["delta_v_norm_sum"] = stats.get("delta_v_norm_sum", 0.0) + float(dV.norm())
+    stats["delta_k_norm_sum"] = stats.get("delta_k_norm_sum", 0.0) + float((k_corr_scale * dK).norm())
+    stats["delta_o_norm_sum"] = stats.get("delta_o_norm_sum", 0.0) + float((out.float().reshape(-1) - Ob).norm())
+    stats["o_base_norm_sum"] = stats.get("o_base_norm_sum", 0.0) + float(Ob.norm())
 
 
 class CAREKVAttention:
@@ -309,9 +413,16 @@ class CAREKVAttention:
         if cache.num_pages(self.layer_id, kv_head, seq) == 0 or (page_ids is not None and len(page_ids) == 0):
             return torch.zeros(self.cfg.head_dim, dtype=q.dtype, device=q.device)
         gate, knobs = decode_read_mode(self.cfg, self.layer_id)
-        out, _ = single_query_decode(cache, self.layer_id, kv_head, q, seq=seq, page_ids=page_ids, kind=kind,
-                                     k_corr_scale=k_corr_scale, score_normalize=score_normalize,
-                                     router=not knobs.kscore_live, correction=gate and kind in ("v", "k", "both"))
+        corr = gate and kind in ("v", "k", "both")
+        out, sel = single_query_decode(cache, self.layer_id, kv_head, q, seq=seq, page_ids=page_ids, kind=kind,
+                                       k_corr_scale=k_corr_scale, score_normalize=score_normalize,
+                                       router=not knobs.kscore_live, correction=corr,
+                                       want_diag=corr and debug_stats is not None)
+        if corr and debug_stats is not None:
+            O_base, _ = single_query_decode(cache, self.layer_id, kv_head, q, seq=seq, page_ids=page_ids,
+                                            correction=False)
+            _debug_accumulate(debug_stats, cache, self.layer_id, kv_head, seq, page_ids, q, sel, out, O_base,
+                              k_corr_scale)
         return out.to(q.dtype)
 
     __call__ = forward
@@ -348,8 +459,9 @@ def single_query_decode(cache: CAREKVCache, layer: int, kv_head: int, q: torch.T
                         page_ids=None, kind: str = "both", k_corr_scale: float = 1.0, score_normalize: bool = False,
                         router: bool = True, correction: bool = True, want_diag: bool = False):
     """Decode output of one query vector q (D,) against kv head ``kv_head``
-    of sequence ``seq`` (pages ``page_ids``, a prefix 0..n-1 of the kv
-    head's pages, default all): the batched kernels over a one-row batch
+    of sequence ``seq`` (pages ``page_ids`` in list order, default all;
+    a list other than 0..n-1 is gathered into a page view first): the
+    batched kernels over a one-row batch
     whose other query heads are zero (selection is per query row,
     attention.py:830-875).  ``router``: ResidualRouter.route's sketch-proxy
     score (the per-query reference path); else the knobs of the environment.
@@ -359,8 +471,15 @@ def single_query_decode(cache: CAREKVCache, layer: int, kv_head: int, q: torch.T
     grp = cfg.num_heads // cfg.num_kv_heads
     n_all = cache.num_pages(layer, kv_head, seq)
     n = n_all if page_ids is None else len(page_ids)
-    if page_ids is not None and list(page_ids) != list(range(n)):
-        raise NotImplementedError("the decode kernels read a prefix of a kv head's pages (0..n-1)")
+    if page_ids is not None and [int(p) for p in page_ids] != list(range(n)):
+        # any other page list: the pages gathered, in list order, into a
+        # one-sequence view whose prefix the kernels read
+        pids = [int(p) for p in page_ids]
+        view = cache.page_view(layer, kv_head, pids, seq=seq)
+        out, sel = single_query_decode(view, layer, kv_head, q, seq=0, kind=kind, k_corr_scale=k_corr_scale,
+                                       score_normalize=score_normalize, router=router, correction=correction,
+                                       want_diag=want_diag)
+        return out, (None if sel is None else [(c, pids[p], sub) for c, p, sub in sel])
     knobs = resolve_read_knobs(cfg, layer)
     knobs.kind, knobs.k_corr_scale, knobs.normalize = kind, k_corr_scale, score_normalize
     if router:

@@ -323,6 +323,35 @@ class CAREKVCache:
         n = self.num_pages(layer, kv_head, seq)
         return int(self.valid_host[layer, kv_head, seq, :n].sum())
 
+    # per-page device arrays, indexed [layer, kv head, sequence, page, ...]
+    _PAGE_ARRAYS = ("kcodes", "vcodes", "kscale", "vscale", "kmaster", "vmaster", "valid", "has_meta", "k_slot",
+                    "v_slot", "k_err", "v_err", "k_sketch", "v_sq")
+
+    def page_view(self, layer: int, kv_head: int, page_ids: Sequence[int], seq: int = 0) -> "CAREKVCache":
+        """A one-sequence cache of the same configuration whose (layer,
+        kv_head) holds pages ``page_ids`` of sequence ``seq``, in list order,
+        as its pages 0..n-1, with the sequence's residual slots (slot ids
+        unchanged): the page list of CAREKVAttention.forward(page_ids=...)
+        (attention.py:979-990) as a prefix the decode kernels read."""
+        if self.kivi_packed:
+            raise NotImplementedError("page_view of a packed KIVI arena (packed prompt pages and fp16 tail)")
+        pids = [int(p) for p in page_ids]
+        n = len(pids)
+        if n == 0 or min(pids) < 0 or max(pids) >= self.cfg.max_pages:
+            raise IndexError(f"page ids must be a non-empty list in [0, {self.cfg.max_pages})")
+        cfg = CacheConfig(**{**self.cfg.__dict__, "max_pages": max(n, 1)})
+        v = CAREKVCache(cfg, device=self.device, n_seq=1, n_slots=self.n_slots,
+                        streaming_store=self.streaming_store)
+        idx = torch.tensor(pids, device=self.device)
+        for nm in self._PAGE_ARRAYS:
+            getattr(v, nm)[layer, kv_head, 0, :n] = getattr(self, nm)[layer, kv_head, seq].index_select(0, idx)
+        for nm in ("k_res", "v_res", "k_res_scale", "v_res_scale", "next_slot"):
+            getattr(v, nm)[0] = getattr(self, nm)[seq]
+        v.next_page[layer, :, 0] = n  # the other kv heads' pages stay empty (no valid rows)
+        v.valid_host[layer, kv_head, 0, :n] = self.valid_host[layer, kv_head, seq, pids]
+        v._token_start[layer, kv_head, 0, :n] = self._token_start[layer, kv_head, seq, pids]
+        return v
+
     def reset_sequence(self, seq: int):
         """Forget a sequence slot (pages, metadata, residual slots)."""
         self.valid[:, :, seq].zero_()

@@ -26,8 +26,8 @@ from typing import Any, Dict, Optional, Sequence, Tuple
 import torch
 from torch import Tensor, nn
 
-from .attention import (decode_attention, decode_read_mode, get_debug_stats, prefill_correction,  # noqa: F401
-                        reset_debug_stats)
+from .attention import (debug_stats_enabled, decode_attention, decode_read_mode, get_debug_stats,  # noqa: F401
+                        get_imp_per_layer, importance_probe, prefill_correction, reset_debug_stats)
 from .cache import CAREKVCache
 from .config import CacheConfig, any_read_budget, resolve_read_knobs
 from .prefill import eval_knobs, prefill_attention, prefill_eval, quant_dequant
@@ -243,6 +243,9 @@ class CAREKVLayer(nn.Module):
                 O = prefill_eval(Qh, Kh, Vh, Khat, Vhat, O, **eval_knobs(cfg.read_budget_ratio))
             if stored:  # layer.py:808-838: the sparse correction from the stored slots
                 knobs = prefill_read_knobs(cfg, self.layer_id)
+                if os.environ.get("CAREKV_DUMP_IMPORTANCE", "0") == "1" and debug_stats_enabled():
+                    for b in range(len(seqs)):  # layer.py:477-502
+                        importance_probe(self.layer_id, Qh[b], Khat[b])
                 for b, sq in enumerate(seqs):
                     O[b] = prefill_correction(cache, self.layer_id, Qh[b].transpose(0, 1), Khat[b], Vhat[b],
                                               lse[b], seq=sq, knobs=knobs).transpose(0, 1)

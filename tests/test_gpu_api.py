@@ -226,3 +226,77 @@ def test_router_attention_and_read_counters_match_oracle(paper_env):
     assert np.abs(out.float().cpu().numpy() - ref.astype(F32)).max() <= 2e-3
     care_kv.reset_debug_stats()
     assert care_kv.get_debug_stats()["k_slots_read"] == 0
+
+
+def test_page_lists_and_debug_norms(paper_env):
+    """CAREKVAttention.forward over page lists other than 0..n-1 (a subset
+    in shuffled order, attention.py:979-990) against the oracle's decode over
+    the same list, and apply_slot_corrections' debug dict: slot reads, and
+    the norms of the linear V term, the linear K term, the applied
+    correction and O_base (attention.py:358-372) against an fp64
+    recomputation from the oracle cache's rows and slots for the GPU's
+    selection."""
+    import care_kv
+    rng = np.random.default_rng(31)
+    D, Hq, Hkv, T = 64, 8, 2, 200
+    K = rng.standard_normal((Hkv, T, D)).astype(F16)
+    V = rng.standard_normal((Hkv, T, D)).astype(F16)
+    K[:, :, rng.permutation(D)[:3]] *= F16(6.0)
+    Qh = rng.standard_normal((Hq, D)).astype(F16)
+    common = dict(num_layers=1, num_heads=Hq, num_kv_heads=Hkv, head_dim=D, page_size=16, max_pages=T // 16 + 4,
+                  base_bits=3, group_size=32, k_channel_group=32, v_token_block=4, sketch_dim=32,
+                  read_budget_mode="absolute", read_abs_k=4, read_abs_v=4, route_policy="joint",
+                  store_budget_mode="absolute", store_abs_k=2, store_abs_v=2)
+    oc = OCache(OCfg(**common))
+    for h in range(Hkv):
+        write_pages_for_kv_head(oc, 0, h, K[h], V[h])
+    cfg = care_kv.CacheConfig(packed_base=True, scale_quant="int8", read_budget_ratio=0.03, compat=True, **common)
+    cache = care_kv.CAREKVCache(cfg, device="cuda")
+    cache.write_prefill(0, torch.from_numpy(K).cuda(), torch.from_numpy(V).cuda())
+    lists = {0: [7, 2, 11, 0, 5], 1: [12, 3, 4, 9]}  # page 12 is the partial last page
+    ref = oracle_decode(oc, 0, Qh, page_ids_by_kvh=lists, k_mode="exact", kind="both", k_corr_scale=1.0,
+                        score_normalize=True, kscore_live=False)
+    attn = care_kv.CAREKVAttention(cfg, 0, "cuda")
+    router = care_kv.ResidualRouter(cfg, 0, "cuda")
+    grp = Hq // Hkv
+    for h, pids in lists.items():
+        for j in range(grp):
+            q = torch.from_numpy(Qh[h * grp + j]).cuda()
+            o = attn.forward(cache, h, q, page_ids=pids, kind="both", k_corr_scale=1.0, score_normalize=True)
+            assert np.abs(o.float().cpu().numpy() - ref[h * grp + j].astype(F32)).max() <= 2e-3, (h, j)
+            # the debug norms of one corrected query, recomputed in fp64
+            stats = {}
+            ob, _ = care_kv.attention.single_query_decode(cache, 0, h, q, page_ids=pids, correction=False)
+            d = care_kv.apply_slot_corrections(cache, cfg, router, 0, h, pids, q, O_base=ob.float(), kind="both",
+                                               k_corr_scale=0.5, score_normalize=True, debug_stats=stats)
+            _, sel = care_kv.attention.single_query_decode(cache, 0, h, q, page_ids=pids, kind="both",
+                                                           k_corr_scale=0.5, score_normalize=True, want_diag=True)
+            Kc, Ks, Vc, Vs, lens = oc.read_base_concat(0, h, pids)
+            Kf = Q.dequantize(Kc, Ks, 32).astype(np.float64)
+            Vf = Q.dequantize(Vc, Vs, 32).astype(np.float64)
+            qf = Qh[h * grp + j].astype(np.float64)
+            s = Kf @ qf / math.sqrt(D)
+            a = np.exp(s - s.max())
+            a /= a.sum()
+            off = np.concatenate([[0], np.cumsum(lens)])
+            obf = ob.float().cpu().numpy().astype(np.float64)
+            dV, dK = np.zeros(D), np.zeros(D)
+            for kind_, p, sub in sel:
+                i = pids.index(p)
+                p0, n = off[i], lens[i]
+                meta = oc.meta_table[0][h][p]
+                if kind_ == 1:
+                    slot = meta.v_residual_slots[sub]
+                    R = Q.unpack_4bit(oc.v_residual_buf[slot], oc.v_residual_scale[slot, 0], 4 * D).reshape(4, D)
+                    t0, t1 = 4 * sub, min(4 * sub + 4, n)
+                    dV += (a[p0 + t0:p0 + t1, None] * R[:t1 - t0]).sum(0)
+                else:
+                    slot = meta.k_residual_slots[sub]
+                    R = Q.unpack_4bit(oc.k_residual_buf[slot], oc.k_residual_scale[slot, 0], 16 * 32).reshape(16, 32)[:n]
+                    qd = R.astype(np.float64) @ qf[32 * sub:32 * sub + 32]
+                    dK += ((a[p0:p0 + n] * qd)[:, None] * (Vf[p0:p0 + n] - obf)).sum(0)
+            nk = sum(1 for c in sel if c[0] == 0)
+            assert stats["k_slots_read"] == nk and stats["v_slots_read"] == len(sel) - nk and stats["n_queries"] == 1
+            for key, want in (("delta_v_norm_sum", np.linalg.norm(dV)), ("delta_k_norm_sum", 0.5 * np.linalg.norm(dK)),
+                              ("delta_o_norm_sum", float(d.norm())), ("o_base_norm_sum", np.linalg.norm(obf))):
+                assert abs(stats[key] - want) <= 1e-3 * max(want, 1e-3), (key, stats[key], want)
