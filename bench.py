@@ -689,6 +689,8 @@ def main():
     ap.add_argument("--config", default="c3", choices=sorted(CONFIGS) + ["c4", "c5", "pfc", "pev"])
     ap.add_argument("--cpu-slices", type=int, default=16)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--eager", action="store_true",
+                    help="time eager launches of the decode step instead of replays of its HIP graph")
     ap.add_argument("--split-pages", type=int, default=None)
     ap.add_argument("--no-correction", action="store_true",
                     help="time the base attention path only (streaming pass + split combine)")
@@ -760,16 +762,47 @@ def main():
         for e in row:
             e.record(stream)
     torch.cuda.synchronize()
-    # timed region: K steps with nothing else on the stream
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    ev0.record(stream)
-    for k in range(args.steps):
-        care_kv.decode_attention(cache, 0, q, out=out, split_pages=args.split_pages, correction=corr)
-    ev1.record(stream)
-    ev1.synchronize()
-    ms_total = ev0.elapsed_time(ev1)
-    ms_step = ms_total / args.steps
+    # one decode step captured as a HIP graph (its four kernels; the caller's
+    # q, output and workspace buffers), checked against eager launches on
+    # replays with eager steps in between
+    graph = None
+    if not args.eager:
+        side = torch.cuda.Stream(device=dev)
+        side.wait_stream(stream)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.stream(side):
+            care_kv.decode_attention(cache, 0, q, out=out, split_pages=args.split_pages, correction=corr)
+            torch.cuda.synchronize()
+            with torch.cuda.graph(graph, stream=side):
+                care_kv.decode_attention(cache, 0, q, out=out, split_pages=args.split_pages, correction=corr)
+        torch.cuda.synchronize()
+        ref = torch.empty_like(out)
+        for _ in range(3):
+            care_kv.decode_attention(cache, 0, q, out=ref, split_pages=args.split_pages, correction=corr)
+            out.zero_()
+            graph.replay()
+            torch.cuda.synchronize()
+            if not torch.equal(out, ref):
+                log("[bench] graph replay differs from the eager step")
+                sys.exit(3)
+
+    def timed(replay):
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        ev0.record(stream)
+        for k in range(args.steps):
+            if replay:
+                graph.replay()
+            else:
+                care_kv.decode_attention(cache, 0, q, out=out, split_pages=args.split_pages, correction=corr)
+        ev1.record(stream)
+        ev1.synchronize()
+        return ev0.elapsed_time(ev1) / args.steps
+
+    # timed region: K steps with nothing else on the stream (graph replays
+    # unless --eager), and the same K steps launched eagerly for reference
+    ms_eager = timed(False)
+    ms_step = ms_eager if graph is None else timed(True)
     us_step = ms_step * 1e3
     # a second pass of K steps with per-kernel events for the phase split
     for k in range(args.steps):
@@ -780,7 +813,8 @@ def main():
     names = ["stream", "select", "apply", "combine"]
     gbps = nbytes / (ms_step * 1e-3) / 1e9
     stream_gbps = stream_bytes / (phase[0] * 1e-6) / 1e9
-    log(f"[bench] {us_step:.1f} us/step, {nbytes / 1e9:.3f} GB algorithmic/step, {gbps:.0f} GB/s, "
+    log(f"[bench] {us_step:.1f} us/step ({'eager' if graph is None else 'graph replay'}; eager launches "
+        f"{ms_eager * 1e3:.1f}), {nbytes / 1e9:.3f} GB algorithmic/step, {gbps:.0f} GB/s, "
         f"K slots {k_slots}, V union {v_union}")
     log("[bench] phases (us): " + ", ".join(f"{n} {t:.1f}" for n, t in zip(names, phase)) +
         f"; streaming kernel {stream_bytes / 1e9:.3f} GB -> {stream_gbps:.0f} GB/s")
@@ -831,6 +865,8 @@ def main():
                    "read": f"joint top-{spec['rk'] + spec['rv']} (K {spec['rk']} + V {spec['rv']}), "
                            "KSCORE_LIVE, normalize, exact"},
         "hbm_gbps": round(gbps, 1),
+        "launch": "eager" if graph is None else "hip graph of one step, replayed",
+        "us_per_step_eager": round(ms_eager * 1e3, 2),
         "phases_us": {n: round(t, 2) for n, t in zip(names, phase)},
         "roofline": {"bound": "hbm", "kernel": f"{stream_kernel}<{D},{kbits},{ksm}>",
                      "achieved": round(stream_gbps, 1), "peak": 8000.0, "unit": "GB/s",

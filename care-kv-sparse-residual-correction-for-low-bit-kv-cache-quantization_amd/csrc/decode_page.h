@@ -640,6 +640,36 @@ __device__ __forceinline__ float row4_max(float v) {
   return fmaxf(v, row_ror<8>(v));
 }
 
+// Max / min reductions on integers: one DPP or lane-swap op per step, where
+// the float max needs its inputs canonicalised first.
+template <int N>
+__device__ __forceinline__ int row_ror_i(int v) {
+  return __builtin_amdgcn_update_dpp(0, v, 0x120 + N, 0xf, 0xf, false);
+}
+__device__ __forceinline__ int row4_max_i(int v) {
+  v = max(v, row_ror_i<4>(v));
+  return max(v, row_ror_i<8>(v));
+}
+__device__ __forceinline__ int row4_min_i(int v) {
+  v = min(v, row_ror_i<4>(v));
+  return min(v, row_ror_i<8>(v));
+}
+__device__ __forceinline__ int pair16_max_i(int v) {
+  const auto r = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+  return max((int)r[0], (int)r[1]);
+}
+__device__ __forceinline__ int pair32_max_i(int v) {
+  const auto r = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+  return max((int)r[0], (int)r[1]);
+}
+// Order key of a float: the signed-integer order of the keys is the float
+// order for every value but NaN (-0 sorts just below +0); its own inverse.
+__device__ __forceinline__ int fkey(float f) {
+  const int b = __float_as_int(f);
+  return b ^ ((b >> 31) & 0x7fffffff);
+}
+__device__ __forceinline__ float fkey_inv(int k) { return __int_as_float(k ^ ((k >> 31) & 0x7fffffff)); }
+
 __device__ __forceinline__ uint32_t pack_h2(float x, float y) {
   const half2_t h = {(_Float16)x, (_Float16)y};
   return h2bits(h);

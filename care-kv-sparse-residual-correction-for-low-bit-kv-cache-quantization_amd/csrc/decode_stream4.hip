@@ -353,7 +353,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
           u4_t{__float_as_uint(x[0]), __float_as_uint(x[1]), __float_as_uint(x[2]), __float_as_uint(x[3])}, rs_ws,
           vo_x, so_x + (uint32_t)p0 * 64u, 0);
     }
-    const float mx = pair32_max(pair16_max(row4_max(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])))));
+    const float mx = fkey_inv(pair32_max_i(pair16_max_i(row4_max_i(fkey(fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3])))))));
     const float m_new = fmaxf(m_run, mx);
     const float m_use = m_new == -INFINITY ? 0.f : m_new;  // a window with no valid token so far
     const float f_old = __builtin_amdgcn_exp2f(m_run - m_use);
@@ -414,13 +414,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     // index among the lane's 4 tokens, out of range in the other lanes)
     int istar = -1;
     if (mom) {
-      const float emax = row4_max(fmaxf(fmaxf(e[0], e[1]), fmaxf(e[2], e[3])));
+      // e >= 0: the integer order of the bits is the float order
+      const float emax = __int_as_float(row4_max_i(max(max(__float_as_int(e[0]), __float_as_int(e[1])),
+                                                       max(__float_as_int(e[2]), __float_as_int(e[3])))));
       int fi = 4;
 #pragma unroll
       for (int i = 3; i >= 0; --i)
         if (e[i] == emax) fi = i;
-      const float tstar = -row4_max(-(fi < 4 ? (float)(4 * sbk + fi) : 16.f));
-      istar = (int)tstar - 4 * sbk;
+      istar = row4_min_i(fi < 4 ? 4 * sbk + fi : 16) - 4 * sbk;
       if (rec_lane && sbk == 0)
         __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(emax), rs_ws, vo_rec,
                                               so_rp + (uint32_t)(1 + 4 * a.k_cap) * 4u, 0);
