@@ -673,12 +673,305 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
   for (int i = sel_run + tid; i < a.diag_cap; i += kBlock) diagp[i] = -1;
 }
 
+// Wave-per-query form of decode_select_kernel<D, false, true> for rows of
+// at most 256 pages (prompt rows of the prefill correction, short decode
+// rows): one wave per query column, four columns per work-group and no
+// barrier, where the work-group form spends most of a short row on its
+// block reductions and four radix passes.  Lane l holds pages l + 64j.
+// Every float sum is taken in the work-group form's order (a butterfly per
+// 64 pages, then the four totals in page order), the k-th largest key comes
+// from a binary search over its 31 bits, and ties at it are taken in
+// candidate order, so the (M, L), masks and diag lists are the same bits.
+// One K and one V candidate per page (k_cap = v_cap = 1), the joint or
+// separate policy, no adaptive_score, correction on, the moments' K score.
+template <int D>
+__global__ __launch_bounds__(256) void decode_select_wave_kernel(carekv_arena A, DecodeArgs a) {
+  constexpr int NCG = D / 32;
+  constexpr int NJ = 4;  // pages per lane
+  const int GQ = a.GQ, ngq = (GQ + 3) / 4;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  // the ngq work-groups of one (sequence, kv head) on one XCD, as in the
+  // work-group form; prefill rows: the latest (longest) rows first
+  const int win_d = blockIdx.x / (kXcd * ngq), rem = blockIdx.x % (kXcd * ngq);
+  const int win = a.pf ? (int)(gridDim.x / (kXcd * ngq)) - 1 - win_d : win_d;
+  const int pair = win * kXcd + rem % kXcd, qq = (rem / kXcd) * 4 + w;
+  if (pair >= a.B * A.n_kv_heads || qq >= GQ) return;  // whole waves; no barrier follows
+  const int kvh = pair % A.n_kv_heads, b = pair / A.n_kv_heads;
+  const int bk = b * A.n_kv_heads + kvh;
+  const EntryRow er = entry_row(A, a, b);
+  const int np = er.np, seq = er.seq;
+  const long pg_base = ((long)kvh * A.n_seq + seq) * A.max_pages;
+  const long bq = (long)bk * GQ + qq;
+  int32_t* diagp = nullptr;
+  if (a.diag) {
+    if (a.pf) {
+      const PfCol x = pf_col(a, b, kvh, qq);
+      diagp = x.ok ? a.diag + pf_row_off(a, x) * a.diag_cap : nullptr;
+    } else {
+      diagp = a.diag + ((long)b * a.Hq + kvh * GQ + qq) * a.diag_cap;
+    }
+  }
+  // sum of one value per (lane, j) in the work-group form's order
+  auto ordered_sum = [&](const float (&v)[NJ]) {
+    float t = 0.f;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) t = j == 0 ? wave_sum_f(v[0]) : t + wave_sum_f(v[j]);
+    return t;
+  };
+
+  // ---- softmax statistics from the split partials (nsplit <= 256)
+  float mloc = -INFINITY;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int s = lane + 64 * j;
+    if (s < a.nsplit) mloc = fmaxf(mloc, a.pml[(((long)bk * a.nsplit + s) * 16 + qq) * 2]);
+  }
+  const float M = wave_max_f(mloc);
+  float lj[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    lj[j] = 0.f;
+    const int s = lane + 64 * j;
+    if (M != -INFINITY && s < a.nsplit) {
+      const long base = ((long)bk * a.nsplit + s) * 16 + qq;
+      const float ms = a.pml[base * 2];
+      if (ms != -INFINITY) lj[j] = a.pml[base * 2 + 1] * __builtin_amdgcn_exp2f(ms - M);
+    }
+  }
+  const float L = ordered_sum(lj);
+  if (lane == 0) { a.ml[bq * 2] = M; a.ml[bq * 2 + 1] = L; }
+
+  // ---- one K and one V score per page (decode_select_kernel's K1 scoring)
+  const float* recq = a.rec + bq * a.Pmax * a.F;
+  const float invL = L > 0.f ? (a.pf ? 1.f : 1.f / L) : 0.f;
+  const float* vsq_row = a.pf ? a.pf_vsq + (long)kvh * a.pf_pages : nullptr;
+  const bool sens1 = a.sens_d == 1.0;
+  float sK[NJ], sV[NJ];
+  int cgK[NJ], vbV[NJ];
+  int cntK = 0, cntV = 0;
+  bool ovf = false;
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int p = lane + 64 * j;
+    sK[j] = sV[j] = -1.f;
+    cgK[j] = vbV[j] = -1;
+    if (p >= np) continue;
+    const long pg = pg_base + p;
+    const int nv = A.valid[pg];
+    const int hm = A.has_meta[pg];
+    const float vsq = vsq_row ? vsq_row[p] : A.v_sq[pg];
+    int ksl[NCG], vsl[kVtb];
+    load_slots<NCG>(ksl, A.k_slot + pg * NCG);
+    load_slots<kVtb>(vsl, A.v_slot + pg * kVtb);
+    const uint2 e2 = *reinterpret_cast<const uint2*>(A.v_err + pg * kVtb);
+    const float* rp = recq + (long)p * 7;
+    const float r0 = rp[0], M2 = rp[1], M3 = rp[2], M4 = rp[3], Ds = rp[4], es = rp[5], E = rp[6];
+    const bool ok = L > 0.f && nv > 0 && hm;
+    const float c = ok ? exp2_dn(r0 - M) * invL : 0.f;
+    int nks = 0, nvs = 0, cg1 = -1, vb1 = -1;
+#pragma unroll
+    for (int cg = NCG - 1; cg >= 0; --cg)
+      if (slot_ok(A, ksl[cg])) { ++nks; cg1 = cg; }
+#pragma unroll
+    for (int vb = kVtb - 1; vb >= 0; --vb)
+      if (slot_ok(A, vsl[vb])) { ++nvs; vb1 = vb; }
+    ovf |= hm && (nks > 1 || nvs > 1);
+    cgK[j] = cg1;
+    vbV[j] = vb1;
+    if (ok && nks > 0) {
+      const float wr = es * (1.f - c * es);
+      const float q2 = (M2 - c * (2.f * M3 - c * M4)) + Ds * (wr * wr);
+      float ks = kscore_underflows(c, M2, Ds, es) ? 0.f : (c * sqrt_dn(fmaxf(q2, 0.f))) * __builtin_amdgcn_sqrtf(vsq);
+      if (!isfinite(ks)) ks = 0.f;
+      sK[j] = ks * a.sens;
+      ++cntK;
+    }
+    if (ok && vb1 >= 0 && vb1 * kVtb < nv) {
+      const uint32_t ew = vb1 < 2 ? e2.x : e2.y;
+      const float ve = h2f((uint16_t)(ew >> (16 * (vb1 & 1))));
+      const float verr_s = sens1 ? ve : (float)((double)ve * a.sens_d);
+      sV[j] = ((c * E) * verr_s) * a.sens;
+      ++cntV;
+    }
+  }
+  if (a.pf) {  // the prompt's later pages: candidates that count, scored 0 (layer.py:514-517)
+    for (int p = np + lane; p < a.pf_pages; p += 64) {
+      const long pg = pg_base + p;
+      const int nv = A.valid[pg];
+      if (nv <= 0 || !A.has_meta[pg]) continue;
+      int rk = 0, rv = 0;
+      for (int cg = 0; cg < NCG; ++cg) rk += slot_ok(A, A.k_slot[pg * NCG + cg]) ? 1 : 0;
+      ovf |= rk > 1;
+      cntK += min(rk, 1);
+      for (int vb = 0; vb < kVtb; ++vb) {
+        if (!slot_ok(A, A.v_slot[pg * kVtb + vb])) continue;
+        if (rv >= 1) { ovf = true; break; }
+        if (vb * kVtb < nv) ++cntV;
+        ++rv;
+      }
+    }
+  }
+  if (__any(ovf) && lane == 0) *a.err_flag = 1;
+  float pk[NJ], pvv[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) { pk[j] = sK[j] >= 0.f ? sK[j] : 0.f; pvv[j] = sV[j] >= 0.f ? sV[j] : 0.f; }
+  const float tK = ordered_sum(pk), tV = ordered_sum(pvv);
+  const int n_k = wave_sum_i(cntK), n_v = wave_sum_i(cntV);
+
+  // ---- read budgets, normalisation, keys (as decode_select_kernel)
+  const bool want_k = (a.kind == 0 || a.kind == 1) && n_k > 0;
+  const bool want_v = (a.kind == 0 || a.kind == 2) && n_v > 0;
+  const int totk = want_k ? n_k : 0, totv = want_v ? n_v : 0;
+  int bud_k, bud_v;
+  if (!a.budget_ratio) {
+    bud_k = a.abs_k; bud_v = a.abs_v;
+  } else {
+    bud_k = (a.ratio_k > 0.0 && totk > 0) ? max(1, (int)((double)totk * a.ratio_k)) : 0;
+    bud_v = (a.ratio_v > 0.0 && totv > 0) ? max(1, (int)((double)totv * a.ratio_v)) : 0;
+  }
+  if (a.kind == 2) bud_k = 0;
+  if (a.kind == 1) bud_v = 0;
+  bud_k = min(bud_k, totk);
+  bud_v = min(bud_v, totv);
+  const bool haveK = want_k && bud_k > 0, haveV = want_v && bud_v > 0;
+  const bool do_norm = a.normalize && a.kind == 0 && haveK && haveV;
+  const bool joint = a.policy == 1 && a.kind == 0 && haveK && haveV;
+  const float divK = n_k > 0 ? fmaxf(tK / (float)n_k, kEps) : kEps;
+  const float divV = n_v > 0 ? fmaxf(tV / (float)n_v, kEps) : kEps;
+  int kK[NJ], kV[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    float x = sK[j];
+    kK[j] = -1;
+    if (x >= 0.f) {
+      if (do_norm) x = (x / divK) * a.lam_k;
+      kK[j] = (int)(__float_as_uint(x) & 0x7fffffffu);
+    }
+    x = sV[j];
+    kV[j] = -1;
+    if (x >= 0.f) {
+      if (do_norm) x = (x / divV) * a.lam_v;
+      kV[j] = (int)(__float_as_uint(x) & 0x7fffffffu);
+    }
+  }
+
+  // ---- thresholds: the k-th largest key of the K keys, the V keys or both
+  // (keys -1: no candidate); every key taken when k reaches their count
+  auto count_ge = [&](int t, bool useK, bool useV) {  // ballots: no cross-lane data movement
+    int n = 0;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      if (useK) n += __builtin_popcountll(__ballot(kK[j] >= t));
+      if (useV) n += __builtin_popcountll(__ballot(kV[j] >= t));
+    }
+    return n;
+  };
+  auto select = [&](int k, bool useK, bool useV) {
+    Sel r{0u, INT_MAX, 0, true};
+    if (count_ge(0, useK, useV) <= k) return r;
+    uint32_t tau = 0u;
+    for (int bit = 30; bit >= 0; --bit) {
+      const uint32_t t = tau | (1u << bit);
+      if (count_ge((int)t, useK, useV) >= k) tau = t;
+    }
+    r.tau = tau;
+    r.take = k - count_ge((int)tau + 1, useK, useV);
+    r.eq = count_ge((int)tau, useK, useV) - count_ge((int)tau + 1, useK, useV);
+    return r;
+  };
+  const int takeK = haveK ? min(bud_k, n_k) : 0, takeV = haveV ? min(bud_v, n_v) : 0;
+  Sel sk{0u, 0, 0, false}, sv{0u, 0, 0, false};
+  if (joint) {
+    sk = select(min(bud_k + bud_v, n_k + n_v), true, true);
+    sv = sk;
+  } else {
+    if (takeK > 0) sk = select(takeK, true, false);
+    if (takeV > 0) sv = select(takeV, false, true);
+  }
+
+  // ---- masks: keys above tau, ties at tau in candidate order (page order;
+  // a joint selection's V ties after every K tie)
+  const uint64_t below = (1ull << lane) - 1ull;
+  int eq_runK = 0, eq_runV = 0;
+  if (joint && sk.on && sk.take < sk.eq) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) eq_runV += __builtin_popcountll(__ballot(kK[j] >= 0 && (uint32_t)kK[j] == sk.tau));
+  }
+  uint8_t* maskq = a.mask + bq * a.Pmax;
+  unsigned selK[NJ], selV[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int p = lane + 64 * j;
+    const bool eqk = sk.on && kK[j] >= 0 && (uint32_t)kK[j] == sk.tau;
+    const bool eqv = sv.on && kV[j] >= 0 && (uint32_t)kV[j] == sv.tau;
+    const uint64_t bk_eq = __ballot(eqk), bv_eq = __ballot(eqv);
+    const int rk = eq_runK + __builtin_popcountll(bk_eq & below);
+    const int rv = eq_runV + __builtin_popcountll(bv_eq & below);
+    eq_runK += __builtin_popcountll(bk_eq);
+    eq_runV += __builtin_popcountll(bv_eq);
+    bool tk = false, tv = false;
+    if (sk.on && kK[j] >= 0) tk = (uint32_t)kK[j] > sk.tau || (eqk && rk < sk.take);
+    if (sv.on && kV[j] >= 0) tv = (uint32_t)kV[j] > sv.tau || (eqv && rv < sv.take);
+    selK[j] = tk ? 1u : 0u;
+    selV[j] = tv ? 1u : 0u;
+    if (p < np) maskq[p] = (uint8_t)(selK[j] | (selV[j] << 4));
+  }
+  if (a.read_counts) {
+    int ck = 0, cvb = 0;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) { ck += (int)selK[j]; cvb += (int)selV[j]; }
+    ck = wave_sum_i(ck);
+    cvb = wave_sum_i(cvb);
+    if (lane == 0 && L > 0.f) {
+      atomicAdd(a.read_counts, (unsigned long long)ck);
+      atomicAdd(a.read_counts + 1, (unsigned long long)cvb);
+      atomicAdd(a.read_counts + 2, 1ull);
+    }
+  }
+  if (!diagp) return;
+  // ---- diag: selected candidates in ascending candidate order (K then V)
+  int run = 0;
+  for (int kind = 0; kind < 2; ++kind) {
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int p = lane + 64 * j;
+      const bool on = kind == 0 ? selK[j] != 0u : selV[j] != 0u;
+      const uint64_t bal = __ballot(on);
+      const int pos = run + __builtin_popcountll(bal & below);
+      run += __builtin_popcountll(bal);
+      if (on && pos < a.diag_cap) diagp[pos] = (kind << 30) | (p << 3) | (kind == 0 ? cgK[j] : vbV[j]);
+    }
+  }
+  for (int i = run + lane; i < a.diag_cap; i += 64) diagp[i] = -1;
+}
+
 int launch_decode_select(const carekv_arena& A, const DecodeArgs& a, hipStream_t s) {
   const int pairs = a.B * A.n_kv_heads;
   const dim3 grid(((pairs + kXcd - 1) / kXcd) * kXcd * a.GQ);
   const size_t lds = (a.correction && a.ncand <= kLdsCand) ? (size_t)a.ncand * sizeof(float) : 0;
   const bool px = a.correction && a.proxy;
   const bool k1 = a.k_cap == 1 && a.v_cap == 1;
+  // rows of at most 256 pages with one K and one V slot, and enough query
+  // columns to fill the GPU with waves (or short rows, where the work-group
+  // form's fixed cost dominates): a wave per query.  CAREKV_SELECT_WAVE=0
+  // keeps the work-group form, =2 takes the wave form for every row it covers.
+  const char* env = getenv("CAREKV_SELECT_WAVE");
+  const int wmode = env ? env[0] - '0' : 1;
+  const long cols = (long)pairs * a.GQ;
+  if (wmode != 0 && a.correction && !px && k1 && (a.policy == 0 || a.policy == 1) && !a.adaptive_score &&
+      a.Pmax <= 256 && a.nsplit <= 256 && a.F == 7 && (wmode == 2 || cols >= 2048 || a.Pmax <= 64)) {
+    const int ngq = (a.GQ + 3) / 4;
+    const dim3 gw(((pairs + kXcd - 1) / kXcd) * kXcd * ngq);
+    if (A.head_dim == 64) hipLaunchKernelGGL((decode_select_wave_kernel<64>), gw, dim3(kBlock), 0, s, A, a);
+    else if (A.head_dim == 128) hipLaunchKernelGGL((decode_select_wave_kernel<128>), gw, dim3(kBlock), 0, s, A, a);
+    else {
+      set_error("unsupported head_dim %d", A.head_dim);
+      return CAREKV_EINVAL;
+    }
+    CAREKV_CHECK_LAUNCH("decode_select (wave per query)");
+    return CAREKV_OK;
+  }
   if (A.head_dim == 64) {
     if (px) hipLaunchKernelGGL((decode_select_kernel<64, true, false>), grid, dim3(kBlock), lds, s, A, a);
     else if (k1) hipLaunchKernelGGL((decode_select_kernel<64, false, true>), grid, dim3(kBlock), lds, s, A, a);
