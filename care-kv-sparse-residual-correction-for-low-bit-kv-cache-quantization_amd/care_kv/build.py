@@ -21,7 +21,7 @@ REPO = os.path.dirname(ROOT)
 INCLUDE = os.path.join(REPO, "include")
 LIB_NAME = "libcarekv_hip.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
-SOURCES = ["capi.cpp", "store.hip", "decode.hip", "decode_stream.hip", "decode_stream4.hip", "decode_proxy.hip", "decode_select.hip", "decode_apply.hip", "decode_apply4.hip", "prefill.hip", "ops.hip"]
+SOURCES = ["capi.cpp", "store.hip", "decode.hip", "decode_stream.hip", "decode_stream4.hip", "decode_proxy.hip", "decode_select.hip", "decode_apply.hip", "decode_apply4.hip", "prefill.hip", "prefill_rows.hip", "ops.hip"]
 ARCH = os.environ.get("CAREKV_OFFLOAD_ARCH", "gfx950")
 
 

@@ -286,6 +286,13 @@ int prefill_setup(const carekv_arena* arena, const carekv_decode_params* read,
   pf.R = 16 / pf.G0;
   dp.batch = (pp->n_rows + pf.R - 1) / pf.R;
   dp.max_pages_used = pages;
+  // with the moments' K score the streaming pass runs on blocks of 8
+  // entries over every visible page at once (pf_rows_stream_kernel), one
+  // split per entry (CAREKV_PF_ROWS=0: entry by entry over the caller's splits)
+  const char* env = getenv("CAREKV_PF_ROWS");
+  if (!(env && env[0] == '0') && read->k_proxy == 0 && read->route_policy != 3 && pages <= 1024 &&
+      (A.head_dim == 64 || A.head_dim == 128))
+    dp.split_pages = (pages + 3) / 4 * 4;
   dp.seq_slot = nullptr;
   dp.n_pages = nullptr;
   return CAREKV_OK;

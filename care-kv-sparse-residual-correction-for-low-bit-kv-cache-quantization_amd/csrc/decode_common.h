@@ -147,6 +147,7 @@ __device__ __forceinline__ long pf_row_off(const DecodeArgs& a, const PfCol& x) 
 
 int launch_decode_stream(const carekv_arena& A, const DecodeArgs& a, hipStream_t s);
 int launch_decode_stream4(const carekv_arena& A, const DecodeArgs& a, hipStream_t s);  // GQ <= 4, SP % 16 == 0
+int launch_pf_rows_stream(const carekv_arena& A, const DecodeArgs& a, hipStream_t s);  // prefill rows, one split
 int launch_decode_proxy(const carekv_arena& A, const DecodeArgs& a, hipStream_t s);
 int launch_decode_select(const carekv_arena& A, const DecodeArgs& a, hipStream_t s);
 int launch_decode_apply(const carekv_arena& A, const DecodeArgs& a, hipStream_t s);
