@@ -317,50 +317,93 @@ void decode_apply_kernel(carekv_arena A, DecodeArgs a) {
 
 // out = half(O_base + correction): O_base from the split partials of the
 // streaming pass, the correction from the chunk partials of the apply pass
-// (both summed in a fixed order).
-__global__ __launch_bounds__(64) void decode_combine_kernel(int Hkv, int D, DecodeArgs a) {
-  const int kvh = blockIdx.x, b = blockIdx.y;
-  const int GQ = a.GQ;
-  const int bk = b * Hkv + kvh;
-  // one thread per output element: a wave of 64 per block, blockIdx.z over
-  // the (query, dim) elements of the pair
-  for (int idx = blockIdx.z * 64 + threadIdx.x; idx < GQ * D; idx += 64 * gridDim.z) {
-    const int qq = idx / D, d = idx % D;
-    long orow = (long)b * a.Hq + kvh * GQ + qq;
-    if (a.pf) {  // prefill rows: the column's (row, head); padding columns write nothing
-      const PfCol x = pf_col(a, b, kvh, qq);
-      if (!x.ok) continue;
-      orow = pf_row_off(a, x);
+// (both summed in a fixed order, O_base with fma(po, 2^(m_s - M), O)).
+// A thread takes 4 consecutive dims of one query; every load of its splits
+// and chunks is issued before the sums that use it (batches of 8 splits and
+// 4 chunks, indices clamped to the last one, read whatever L is), so a wave
+// waits about one memory latency per batch instead of one per split.
+__global__ __launch_bounds__(256) void decode_combine_kernel(int Hkv, int D, int out_al8, DecodeArgs a) {
+  const int D4 = D >> 2, GQ = a.GQ;
+  const long gid = (long)blockIdx.x * 256 + threadIdx.x;
+  if (gid >= (long)a.B * Hkv * GQ * D4) return;
+  const int d = (int)(gid % D4) * 4;
+  const long r = gid / D4;
+  const int qq = (int)(r % GQ), bk = (int)(r / GQ);
+  const int b = bk / Hkv, kvh = bk % Hkv;
+  long orow = (long)b * a.Hq + kvh * GQ + qq;
+  if (a.pf) {  // prefill rows: the column's (row, head); padding columns write nothing
+    const PfCol x = pf_col(a, b, kvh, qq);
+    if (!x.ok) return;
+    orow = pf_row_off(a, x);
+  }
+  const long bq = (long)bk * GQ + qq;
+  const float M = a.ml[bq * 2], L = a.ml[bq * 2 + 1];
+  const int ns = a.nsplit, na = a.napply;
+  const long sb = (long)bk * ns * 16 + qq;   // split s: row sb + 16 s of po / pml
+  const long cb0 = (long)bk * ns * GQ + qq;  // chunk c: row cb0 + c GQ of num / den
+  float4 O = make_float4(0.f, 0.f, 0.f, 0.f), nm = make_float4(0.f, 0.f, 0.f, 0.f);
+  float dn = 0.f;
+  const int nb = max((ns + 7) / 8, (na + 3) / 4);
+  for (int k = 0; k < nb; ++k) {  // batch k: splits 8k .. 8k+7 and chunks 4k .. 4k+3
+    float ms[8], dv[4];
+    float4 pv[8], nv[4];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const long base = sb + 16L * min(8 * k + j, ns - 1);
+      ms[j] = a.pml[base * 2];
+      pv[j] = *reinterpret_cast<const float4*>(a.po + base * D + d);
     }
-    const long bq = (long)bk * GQ + qq;
-    const float M = a.ml[bq * 2], L = a.ml[bq * 2 + 1];
-    float O = 0.f, nm = 0.f, dn = 0.f;
-    if (L > 0.f) {
-      for (int s = 0; s < a.nsplit; ++s) {
-        const long base = ((long)bk * a.nsplit + s) * 16 + qq;
-        const float ms = a.pml[base * 2];
-        if (ms != -INFINITY) O += a.po[base * D + d] * __builtin_amdgcn_exp2f(ms - M);
-      }
-      for (int c = 0; c < a.napply; ++c) {
-        const long cb = ((long)bk * a.nsplit + c) * GQ + qq;
-        nm += a.num[cb * D + d];
-        dn += a.den[cb];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const long cb = cb0 + (long)max(min(4 * k + j, na - 1), 0) * GQ;
+      nv[j] = *reinterpret_cast<const float4*>(a.num + cb * D + d);
+      dv[j] = a.den[cb];
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float e = __builtin_amdgcn_exp2f(ms[j] - M);
+      if (8 * k + j < ns && ms[j] != -INFINITY) {
+        O.x = fmaf(pv[j].x, e, O.x);
+        O.y = fmaf(pv[j].y, e, O.y);
+        O.z = fmaf(pv[j].z, e, O.z);
+        O.w = fmaf(pv[j].w, e, O.w);
       }
     }
-    const float ob = L > 0.f ? O / L : 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {  // chunks past the last add +0, which leaves a sum begun at +0 unchanged
+      const bool in = 4 * k + j < na;
+      nm.x += in ? nv[j].x : 0.f;
+      nm.y += in ? nv[j].y : 0.f;
+      nm.z += in ? nv[j].z : 0.f;
+      nm.w += in ? nv[j].w : 0.f;
+      dn += in ? dv[j] : 0.f;
+    }
+  }
+  auto fin = [&](float Oc, float nmc) -> uint32_t {
+    const float ob = L > 0.f ? Oc / L : 0.f;
     float o = ob;
     if (L > 0.f) {
       if (a.k_exact) {
-        o = (ob + nm / L) / (1.f + dn / L);
+        o = (ob + nmc / L) / (1.f + dn / L);
       } else if (a.pf) {
         // prefill rows: the reference adds the linear terms to its
         // unnormalised fp16-weight O_base (layer.py:553-557)
-        o = O + (nm - dn * O);
+        o = Oc + (nmc - dn * Oc);
       } else {
-        o = ob + (nm - dn * ob) / L;
+        o = ob + (nmc - dn * ob) / L;
       }
     }
-    a.out[orow * D + d] = f2h(o);
+    return f2h(o);
+  };
+  const uint32_t h0 = fin(O.x, nm.x), h1 = fin(O.y, nm.y), h2 = fin(O.z, nm.z), h3 = fin(O.w, nm.w);
+  uint16_t* op = a.out + orow * D + d;
+  if (out_al8) {
+    *reinterpret_cast<uint2*>(op) = make_uint2(h0 | (h1 << 16), h2 | (h3 << 16));
+  } else {
+    op[0] = (uint16_t)h0;
+    op[1] = (uint16_t)h1;
+    op[2] = (uint16_t)h2;
+    op[3] = (uint16_t)h3;
   }
 }
 
@@ -383,8 +426,15 @@ int launch_decode_apply(const carekv_arena& A, const DecodeArgs& a, hipStream_t 
 }
 
 int launch_decode_combine(const carekv_arena& A, const DecodeArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL(decode_combine_kernel, dim3(A.n_kv_heads, a.B, (a.GQ * A.head_dim + 63) / 64), dim3(64), 0, s,
-                     A.n_kv_heads, A.head_dim, a);
+  if (A.head_dim % 4 != 0) {
+    set_error("decode_combine: head_dim %d is not a multiple of 4", A.head_dim);
+    return CAREKV_EINVAL;
+  }
+  const long n = (long)a.B * A.n_kv_heads * a.GQ * (A.head_dim / 4);
+  if (n == 0) return CAREKV_OK;
+  const int out_al8 = (reinterpret_cast<uintptr_t>(a.out) & 7) == 0;
+  hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, A.n_kv_heads,
+                     A.head_dim, out_al8, a);
   CAREKV_CHECK_LAUNCH("decode_combine");
   return CAREKV_OK;
 }
