@@ -19,6 +19,8 @@
 // -> np*k_cap + p*v_cap + r (the reference's [score_K | score_V] order).
 #include <limits.h>
 
+#include <type_traits>
+
 #include "block_util.h"
 #include "decode_common.h"
 #include "host_util.h"
@@ -69,7 +71,7 @@ struct Sel {
 // k-th largest key of the candidates [lo, hi) (key -1: empty position),
 // by 8-bit radix passes from the top; two histograms (one per wave pair)
 // spread the LDS atomics.
-__device__ Sel radix_select(const int* key, int lo, int hi, int k, int (*hist)[256], BlockScratch& bs) {
+__device__ __forceinline__ Sel radix_select(const int* key, int lo, int hi, int k, int (*hist)[256], BlockScratch& bs) {
   Sel r{0u, INT_MAX, 0, true};
   int cnt = 0;
   for (int i = lo + threadIdx.x; i < hi; i += kBlock) cnt += key[i] >= 0;
@@ -140,7 +142,7 @@ __device__ Sel radix_select(const int* key, int lo, int hi, int k, int (*hist)[2
 // every K tie).  which: bit 0 rewrites the K bits of the mask bytes, bit 1
 // the V bits; the other kind's bits are kept.  Each thread owns pages
 // tid, tid + kBlock, ...
-__device__ void write_masks(const int* key, uint8_t* maskq, int np, int k_cap, int v_cap, int nK, const Sel& sk,
+__device__ __forceinline__ void write_masks(const int* key, uint8_t* maskq, int np, int k_cap, int v_cap, int nK, const Sel& sk,
                             const Sel& sv, bool joint, int which, BlockScratch& bs) {
   const int tid = threadIdx.x;
   const bool rankK = sk.on && sk.take < sk.eq, rankV = sv.on && sv.take < sv.eq;
@@ -205,7 +207,11 @@ constexpr int kXcd = 8;
 // K1: k_cap = v_cap = 1 (records [m_ref, M2, M3, M4, D*, e*, mass]), the common
 // store budget of one K and one V slot per page, scored without the
 // generic rank loops.
-template <int D, bool PX, bool K1>
+// LC: the candidates' scores and keys live in LDS (ncand <= kLdsCand), else
+// in the workspace; a compile-time choice, so that every access has a known
+// address space (a generic pointer makes each one a flat access, and the
+// waits around flat accesses cover every outstanding load)
+template <int D, bool PX, bool K1, bool LC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) void decode_select_kernel(carekv_arena A, DecodeArgs a) {
   constexpr int NCG = D / 32;
   constexpr int FMAX = 2 + 4 * NCG + kVtb;
@@ -290,7 +296,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
   const int k_cap = a.k_cap, v_cap = a.v_cap, F = a.F;
   const int nK = np * k_cap, nV = np * v_cap;
   const float* recq = a.rec + bq * a.Pmax * F;
-  float* sc = a.ncand <= kLdsCand ? s_cand : a.scores + bq * a.ncand;
+  float* sc = LC ? s_cand : a.scores + bq * a.ncand;
   int* key = reinterpret_cast<int*>(sc);
   uint8_t* maskq = a.mask + bq * a.Pmax;
   // prefill rows: e_t are already the reference's attention weights
@@ -345,8 +351,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
       const uint2 e2 = *reinterpret_cast<const uint2*>(A.v_err + pg * kVtb);
       const float* rp = recq + (long)p * 7;
       const float r0 = rp[0], M2 = rp[1], M3 = rp[2], M4 = rp[3], Ds = rp[4], es = rp[5], E = rp[6];
+      // v_sq is used only under the K-score branch; held here, so that its
+      // load stays with the page's other loads instead of sinking into the
+      // branch behind a wait of its own
+      float vsq_h = vsq;
+      asm volatile("" : "+v"(vsq_h));
       const bool ok = L > 0.f && nv > 0 && hm;
-      const float c = ok ? exp2_dn(r0 - M) * invL : 0.f;
+      // a select on the exponent (exp2_dn(-inf) = 0), so that the record's
+      // load is issued with the page's other loads rather than behind ok
+      const float c = exp2_dn(ok ? r0 - M : -INFINITY) * invL;
       int nks = 0, nvs = 0;
 #pragma unroll
       for (int cg = 0; cg < NCG; ++cg) nks += slot_ok(A, ksl[cg]) ? 1 : 0;
@@ -360,7 +373,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
         // token t* evaluated directly, and c kept outside the root (c^2 of a far page underflows)
         const float wr = es * (1.f - c * es);
         const float q2 = (M2 - c * (2.f * M3 - c * M4)) + Ds * (wr * wr);
-        ks = kscore_underflows(c, M2, Ds, es) ? 0.f : (c * sqrt_dn(fmaxf(q2, 0.f))) * __builtin_amdgcn_sqrtf(vsq);
+        ks = kscore_underflows(c, M2, Ds, es) ? 0.f : (c * sqrt_dn(fmaxf(q2, 0.f))) * __builtin_amdgcn_sqrtf(vsq_h);
         if (!isfinite(ks)) ks = 0.f;
         ks = ks * a.sens;
         sumK += ks;
@@ -400,7 +413,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
 #pragma unroll
     for (int f = 0; f < FMAX; ++f) r[f] = f < F ? rp[f] : 0.f;
     const bool ok = L > 0.f && nv > 0 && hm;
-    const float c = ok ? exp2_dn(r[0] - M) * invL : 0.f;
+    const float c = exp2_dn(ok ? r[0] - M : -INFINITY) * invL;
     const float vnorm = __builtin_amdgcn_sqrtf(vsq);
     if constexpr (!PX) {
       float es = 0.f;  // e of the page's token t*
@@ -972,15 +985,26 @@ int launch_decode_select(const carekv_arena& A, const DecodeArgs& a, hipStream_t
     CAREKV_CHECK_LAUNCH("decode_select (wave per query)");
     return CAREKV_OK;
   }
-  if (A.head_dim == 64) {
-    if (px) hipLaunchKernelGGL((decode_select_kernel<64, true, false>), grid, dim3(kBlock), lds, s, A, a);
-    else if (k1) hipLaunchKernelGGL((decode_select_kernel<64, false, true>), grid, dim3(kBlock), lds, s, A, a);
-    else hipLaunchKernelGGL((decode_select_kernel<64, false, false>), grid, dim3(kBlock), lds, s, A, a);
-  } else if (A.head_dim == 128) {
-    if (px) hipLaunchKernelGGL((decode_select_kernel<128, true, false>), grid, dim3(kBlock), lds, s, A, a);
-    else if (k1) hipLaunchKernelGGL((decode_select_kernel<128, false, true>), grid, dim3(kBlock), lds, s, A, a);
-    else hipLaunchKernelGGL((decode_select_kernel<128, false, false>), grid, dim3(kBlock), lds, s, A, a);
-  } else {
+  const bool lc = lds > 0;
+  auto go = [&](auto d, auto p, auto k, auto l) {
+    hipLaunchKernelGGL((decode_select_kernel<decltype(d)::value, decltype(p)::value, decltype(k)::value,
+                                             decltype(l)::value>),
+                       grid, dim3(kBlock), lds, s, A, a);
+  };
+  using T = std::true_type;
+  using F = std::false_type;
+  auto by_lc = [&](auto d, auto p, auto k) {
+    if (lc) go(d, p, k, T{});
+    else go(d, p, k, F{});
+  };
+  auto by_kind = [&](auto d) {
+    if (px) by_lc(d, T{}, F{});
+    else if (k1) by_lc(d, F{}, T{});
+    else by_lc(d, F{}, F{});
+  };
+  if (A.head_dim == 64) by_kind(std::integral_constant<int, 64>{});
+  else if (A.head_dim == 128) by_kind(std::integral_constant<int, 128>{});
+  else {
     set_error("unsupported head_dim %d", A.head_dim);
     return CAREKV_EINVAL;
   }
