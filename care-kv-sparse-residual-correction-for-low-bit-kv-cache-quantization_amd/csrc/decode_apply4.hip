@@ -122,18 +122,25 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
   };
 
   // ---- pipeline stages
-  // page (S side: page lj), its metadata field ln, the lane's mask byte
+  // page (S side: page lj), its metadata field ln, the lane's mask byte.
+  // load_pre issues the raw loads (the field's aligned word, the mask byte)
+  // and finish_pre, one window later, turns them into the field and the
+  // mask, so that no wait for them falls in the window that issued them.
   struct WinPre { int page, meta; unsigned mk; };
   auto load_pre = [&](int base) {
     WinPre x;
     const int it = base + lj;
     x.page = it < n_items ? s_items[min(it, kMaxSP - 1)] : -1;
-    const bool ok = x.page >= 0;
-    const int pc = ok ? x.page : 0;
-    x.meta = meta_field_any<NCG, SM>(A, pg_base, pc, ok, ln);
-    const unsigned m = maskb[(long)(qv ? sc : 0) * a.Pmax + pc];
-    x.mk = (ok && qv) ? m : 0u;
+    const int pc = x.page >= 0 ? x.page : 0;
+    x.meta = (int)meta_word_load<NCG, SM>(A, pg_base + pc, ln);
+    x.mk = maskb[(long)(qv ? sc : 0) * a.Pmax + pc];
     return x;
+  };
+  auto finish_pre = [&](WinPre& x) {
+    const bool ok = x.page >= 0;
+    const long pg = pg_base + (ok ? x.page : 0);
+    x.meta = ok ? meta_word_field<NCG, SM>(A, (uint32_t)x.meta, pg, ln) : 0;
+    x.mk = (ok && qv) ? x.mk : 0u;
   };
   // uniform digest of a window: pages, which slot ranks any query selected
   struct Plan { int pg[4]; unsigned kany[4], vany[4]; int nblk; };
@@ -255,6 +262,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
   // ---- prologue: window 0 resolved, window 1's page records in flight
   int base = 4 * w, par = 0;
   WinPre pre0 = load_pre(base), pre1 = load_pre(base + 16);
+  finish_pre(pre0);
   Plan plan0 = make_plan(pre0, 0);
   WinE e0 = load_e(pre0);
   KRow kr0 = load_krow(pre0, plan0);
@@ -267,6 +275,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4, 8))) voi
     const WinE ce = e0;
     pre0 = pre1;
     pre1 = load_pre(base + 32);
+    finish_pre(pre0);
     plan0 = make_plan(pre0, par ^ 1);
     e0 = load_e(pre0);
 

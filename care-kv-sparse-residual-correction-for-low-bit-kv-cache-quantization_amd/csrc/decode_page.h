@@ -748,6 +748,38 @@ __device__ __forceinline__ int meta_field_row(const carekv_arena& A, long pg_bas
   return ok ? v : 0;
 }
 
+// meta_field_any in two steps: meta_word_load issues one 32-bit load of the
+// aligned word that holds field f of page pg (the 16-bit masters and the
+// 8-bit has_meta are read through the aligned word holding them; such a word
+// lies in the same mapped page as the field), and meta_word_field extracts
+// the field where it is used.  A prefetch that selects among several loads
+// at once waits for all of them right behind the loads; one raw word waits
+// only where its field is first needed.
+template <int NCG, int SM>
+__device__ __forceinline__ uint32_t meta_word_load(const carekv_arena& A, long pg, int f) {
+  const bool in_ks = f >= 2 && f < 2 + NCG, in_vs = f >= 6 && f < 6 + kVtb;
+  const char* p;
+  if (in_ks) p = reinterpret_cast<const char*>(A.k_slot + pg * NCG + (f - 2));
+  else if (in_vs) p = reinterpret_cast<const char*>(A.v_slot + pg * kVtb + (f - 6));
+  else if (f == 1) p = reinterpret_cast<const char*>(A.has_meta + pg);
+  else if (SM == 1 && f == 10) p = reinterpret_cast<const char*>(A.kmaster + pg);
+  else if (SM == 1 && f == 11) p = reinterpret_cast<const char*>(A.vmaster + pg);
+  else p = reinterpret_cast<const char*>(A.valid + pg);  // field 0; other fields drop the word
+  // aligned by pointer arithmetic on p, which keeps its (global) address space
+  return *reinterpret_cast<const uint32_t*>(p - (reinterpret_cast<uintptr_t>(p) & 3u));
+}
+template <int NCG, int SM>
+__device__ __forceinline__ int meta_word_field(const carekv_arena& A, uint32_t w, long pg, int f) {
+  const bool in_ks = f >= 2 && f < 2 + NCG, in_vs = f >= 6 && f < 6 + kVtb;
+  if (f == 0 || in_ks || in_vs) return (int)w;
+  if (f == 1) return (int)(int8_t)(w >> (8u * (uint32_t)(reinterpret_cast<uintptr_t>(A.has_meta + pg) & 3u)));
+  if (SM == 1 && (f == 10 || f == 11)) {
+    const uint16_t* m = f == 10 ? A.kmaster + pg : A.vmaster + pg;
+    return (int)((w >> (8u * (uint32_t)(reinterpret_cast<uintptr_t>(m) & 2u))) & 0xffffu);
+  }
+  return 0;
+}
+
 template <int NCG, int SM>
 __device__ __forceinline__ int meta_field_any(const carekv_arena& A, long pg_base, int p, bool ok, int f) {
   const long pg = pg_base + (ok ? p : 0);
