@@ -47,9 +47,10 @@ struct ApplyItem {
   uint32_t vw[NWC];    // V codes of token ln, chunk lj (when a K slot is selected)
   uint32_t vsc;        // its scale code
   uint32_t kr[NCG];    // K residual word of each stored slot (cg order) that is selected
-  float krs[NCG];      // and its scale
+  uint32_t krs[NCG];   // and its scale (fp16 bits: converted where the item is used, since a
+                       // conversion at the load would wait for it and for every load before it)
   uint32_t rv[CH / 8]; // V residual chunk of tile row ln (when its block is selected)
-  float rvs;           // and its scale
+  uint32_t rvs;        // and its scale (fp16 bits)
   bool rsel;           // tile row ln holds a selected V block
 };
 
@@ -178,13 +179,13 @@ void decode_apply_kernel(carekv_arena A, DecodeArgs a) {
       int rk = 0;
 #pragma unroll
       for (int cg = 0; cg < NCG; ++cg) {
-        d.kr[cg] = 0u; d.krs[cg] = 0.f;
+        d.kr[cg] = 0u; d.krs[cg] = 0u;
         if (pm.ksl[cg] < 0) continue;
         if (rk < a.k_cap && ((d.kany >> rk) & 1u)) {
           const long so = (long)seq * A.n_slots + pm.ksl[cg];
           const __amdgpu_buffer_rsrc_t r = make_rsrc(A.k_res + so * G::KSB, G::KSB);
           d.kr[cg] = __builtin_amdgcn_raw_buffer_load_b32(r, ln * 16 + lj * 4, 0, 0);
-          d.krs[cg] = h2f(A.k_res_scale[so]);
+          d.krs[cg] = A.k_res_scale[so];
         }
         ++rk;
       }
@@ -205,7 +206,7 @@ void decode_apply_kernel(carekv_arena A, DecodeArgs a) {
         const long so = (long)seq * A.n_slots + rslot;
         const __amdgpu_buffer_rsrc_t r = make_rsrc(A.v_res + so * G::VSB, G::VSB);
         buf_load<CH / 2>(d.rv, r, (ln & 3) * (D / 2) + lj * (CH / 2));
-        d.rvs = h2f(A.v_res_scale[so]);
+        d.rvs = A.v_res_scale[so];
       }
     }
   };
@@ -245,7 +246,7 @@ void decode_apply_kernel(carekv_arena A, DecodeArgs a) {
         if (rk >= a.k_cap) break;
         if ((cur.kany >> rk) & 1u) {
           const float4_t racc = kslot_dot_w(cur.kr[cg], sqr, D, cg, ln, lj);
-          const float rs = ((kbits >> rk) & 1u) ? cur.krs[cg] : 0.f;
+          const float rs = ((kbits >> rk) & 1u) ? h2f((uint16_t)cur.krs[cg]) : 0.f;
 #pragma unroll
           for (int i = 0; i < 4; ++i) wk[i] = fmaf(racc[i], rs, wk[i]);
         }
@@ -293,7 +294,7 @@ void decode_apply_kernel(carekv_arena A, DecodeArgs a) {
     if (cur.vany) {
       if (cur.rsel) {
         half2_t rp[CH / 2];
-        dequant_pairs<4, CH, BITS>(cur.rv, (_Float16)cur.rvs, rp);
+        dequant_pairs<4, CH, BITS>(cur.rv, bits2half((uint16_t)cur.rvs), rp);
         vtile_write<D, BITS>(vt, rp, ln, lj);
       }
       half4_t ah, al;
