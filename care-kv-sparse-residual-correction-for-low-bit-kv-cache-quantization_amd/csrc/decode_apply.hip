@@ -318,7 +318,9 @@ void decode_apply_kernel(carekv_arena A, DecodeArgs a) {
 
 // out = half(O_base + correction): O_base from the split partials of the
 // streaming pass, the correction from the chunk partials of the apply pass
-// (both summed in a fixed order, O_base with fma(po, 2^(m_s - M), O)).
+// (both summed in a fixed order; O_base as O + po 2^(m_s - M), the product
+// and the sum rounded apart, as the select kernel forms it without a
+// correction).
 // A thread takes 4 consecutive dims of one query; every load of its splits
 // and chunks is issued before the sums that use it (batches of 8 splits and
 // 4 chunks, indices clamped to the last one, read whatever L is), so a wave
@@ -363,11 +365,11 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(int Hkv, int D, int
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const float e = __builtin_amdgcn_exp2f(ms[j] - M);
-      if (8 * k + j < ns && ms[j] != -INFINITY) {
-        O.x = fmaf(pv[j].x, e, O.x);
-        O.y = fmaf(pv[j].y, e, O.y);
-        O.z = fmaf(pv[j].z, e, O.z);
-        O.w = fmaf(pv[j].w, e, O.w);
+      if (8 * k + j < ns && ms[j] != -INFINITY) {  // product and sum rounded apart (no contraction)
+        O.x += pv[j].x * e;
+        O.y += pv[j].y * e;
+        O.z += pv[j].z * e;
+        O.w += pv[j].w * e;
       }
     }
 #pragma unroll
