@@ -252,6 +252,43 @@ def test_read_zero_is_base_bit_exact(paper_env):
     assert torch.equal(base, corr0)
 
 
+@pytest.mark.parametrize("Hq,Hkv,D,k_mode", [(16, 4, 128, "exact"), (16, 4, 128, "linear"), (16, 2, 64, "exact")])
+def test_zero_residuals_correction_is_base_bit_exact(paper_env, Hq, Hkv, D, k_mode):
+    """K and V exactly representable in INT3 (integer codes in [-3, 3], every
+    32-dim group reaching |3|, so the group scale and the int8 page scale
+    decode to 1 and K_hat = K): every stored residual is 0, so whatever the
+    router selects adds exactly nothing (dS = 0, e^0 - 1 = 0, R_V = 0) and
+    the corrected step (streaming with records, select, apply, combine) must
+    give the base-only step's output bit for bit.  This holds the combine's
+    O_base to the select kernel's base path (same sums, same rounding)."""
+    import care_kv
+    paper_env.setenv("CAREKV_K_CORRECTION_MODE", k_mode)
+    print(f"zero residuals Hq={Hq} Hkv={Hkv} D={D} {k_mode}", flush=True)
+    dev = torch.device("cuda", 0)
+    lens = [700, 333, 1024]
+    cfg = care_kv.CacheConfig(num_layers=1, num_heads=Hq, num_kv_heads=Hkv, head_dim=D, page_size=16,
+                              max_pages=max(lens) // 16 + 4, base_bits=3, group_size=32, k_channel_group=32,
+                              v_token_block=4, sketch_dim=32, packed_base=True, scale_quant="int8",
+                              store_budget_mode="ratio", store_budget_ratio=0.03, read_budget_ratio=0.0,
+                              read_budget_mode="absolute", read_abs_k=16, read_abs_v=16, route_policy="joint")
+    cache = care_kv.CAREKVCache(cfg, device=dev, n_seq=len(lens))
+    g = torch.Generator(device=dev).manual_seed(D + Hq)
+
+    def exact_int3(n):
+        x = torch.randint(-3, 4, (Hkv, n, D), generator=g, device=dev).float()
+        x.view(Hkv, n, D // 32, 32)[..., 0] = 3.0  # every group's max |x| is 3: scale 1
+        return x.half()
+
+    for b, n in enumerate(lens):
+        cache.write_prefill(0, exact_int3(n), exact_int3(n), seqs=[b])
+    q = torch.randn(len(lens), Hq, D, generator=g, device=dev).half()
+    base = care_kv.decode_attention(cache, 0, q, correction=False)
+    corr = care_kv.decode_attention(cache, 0, q, correction=True)
+    torch.cuda.synchronize()
+    assert torch.isfinite(base.float()).all()
+    assert torch.equal(base.view(torch.int16), corr.view(torch.int16))
+
+
 # ------------------------------------------------------------------ prefill carekv_stored
 @pytest.mark.parametrize("name", list(PREFILL_CASES))
 def test_prefill_correction_matches_reference(paper_env, name):
