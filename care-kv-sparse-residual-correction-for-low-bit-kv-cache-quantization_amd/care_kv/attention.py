@@ -208,8 +208,8 @@ def prefill_correction(cache: CAREKVCache, layer: int, q: torch.Tensor, k_hat: t
     if cache.num_pages(layer, 0, seq) != pages:
         raise ValueError(f"sequence {seq} holds {cache.num_pages(layer, 0, seq)} pages, the prompt needs {pages}: "
                          "the cache must hold exactly the prompt")
-    if rows_per_call is None:  # bound the workspace: rows x pages x query heads
-        rows_per_call = max(1, min(T, (1 << 22) // max(1, pages * Hq)))
+    if rows_per_call is None:  # bound the workspace: rows x pages x query heads <= 2^23 (about 0.6 GB)
+        rows_per_call = max(1, min(T, (1 << 23) // max(1, pages * Hq)))
     if split_pages is None:
         split_pages = default_split_pages(pages, rows_per_call * Hkv)
     lib = _lib.load()
