@@ -83,6 +83,69 @@ __global__ __launch_bounds__(256) void prompt_vsq_kernel(const uint16_t* __restr
   if (lane == 0) vsq[(long)kvh * pages + p] = acc;
 }
 
+// The candidates of the prompt's later pages, per kv head, as suffix counts
+// over the pages (DecodeArgs::pf_suf): the select kernels read them at a
+// row's page count instead of walking the pages past the row.  Page p
+// counts when it holds valid rows and metadata: min(stored K slots, k_cap),
+// its stored V blocks of rank < v_cap that start inside the valid rows, and
+// an overflow when it holds more K slots than k_cap or more V blocks than
+// v_cap.  One work-group per kv head, chunks of 256 pages from the end.
+__global__ __launch_bounds__(256) void prompt_suffix_kernel(carekv_arena A, int seq, int pages, int k_cap, int v_cap,
+                                                            int* __restrict__ suf) {
+  __shared__ BlockScratch bs;
+  const int kvh = blockIdx.x, tid = threadIdx.x;
+  const int ncg = A.head_dim / 32;
+  const long pg_base = ((long)kvh * A.n_seq + seq) * A.max_pages;
+  int* sk = suf + (long)kvh * 3 * (pages + 1);
+  int* sv = sk + (pages + 1);
+  int* so = sv + (pages + 1);
+  if (tid == 0) { sk[pages] = 0; sv[pages] = 0; so[pages] = 0; }
+  int ck = 0, cv = 0, co = 0;  // totals of the pages from hi on
+  for (int hi = pages; hi > 0; hi -= kBlock) {
+    const int p = hi - 1 - tid;  // descending with the thread index
+    int nk = 0, nvb = 0, ov = 0;
+    if (p >= 0) {
+      const long pg = pg_base + p;
+      const int nv = A.valid[pg];
+      if (nv > 0 && A.has_meta[pg]) {
+        int rk = 0;
+        for (int cg = 0; cg < ncg; ++cg) {
+          const int sl = A.k_slot[pg * ncg + cg];
+          rk += (sl >= 0 && sl < A.n_slots) ? 1 : 0;
+        }
+        ov = rk > k_cap ? 1 : 0;
+        nk = min(rk, k_cap);
+        int rv = 0;
+        for (int vb = 0; vb < kVtb; ++vb) {
+          const int sl = A.v_slot[pg * kVtb + vb];
+          if (!(sl >= 0 && sl < A.n_slots)) continue;
+          if (rv >= v_cap) { ov = 1; break; }
+          if (vb * kVtb < nv) ++nvb;
+          ++rv;
+        }
+      }
+    }
+    // exclusive scans over the thread index = the chunk's pages above p
+    int tk, tv, to;
+    const int ek = block_excl_scan(nk, bs, &tk);
+    const int ev = block_excl_scan(nvb, bs, &tv);
+    const int eo = block_excl_scan(ov, bs, &to);
+    if (p >= 0) {
+      sk[p] = ck + ek + nk;
+      sv[p] = cv + ev + nvb;
+      so[p] = (co + eo + ov) > 0 ? 1 : 0;
+    }
+    ck += tk; cv += tv; co += to;
+  }
+}
+
+// Workspace bytes a prefill-rows call needs beyond the decode layout: v_sq
+// per (kv head, page), then the suffix counts.
+long pf_extra_bytes(const carekv_arena& A, int pages) {
+  const long vsq = ((long)A.n_kv_heads * pages * 4 + 255) / 256 * 256;
+  return vsq + (long)A.n_kv_heads * 3 * (pages + 1) * 4;
+}
+
 int run_decode(const carekv_arena* arena, const carekv_decode_params* dp, const PfRows* pf, const uint16_t* q,
                uint16_t* out, void* workspace, int64_t workspace_bytes, int32_t* diag, int32_t diag_cap,
                void* stream) {
@@ -120,7 +183,7 @@ int run_decode(const carekv_arena* arena, const carekv_decode_params* dp, const 
                    "packed_pages_used / tail_pages_used out of range");
   }
   const WsLayout L = ws_layout(A, *dp, GQ, pf != nullptr);
-  const long vsq_off = L.total, need = L.total + (pf ? (long)A.n_kv_heads * pf->pages * 4 : 0);
+  const long vsq_off = L.total, need = L.total + (pf ? pf_extra_bytes(A, pf->pages) : 0);
   if (workspace_bytes < need) {
     set_error("%s: workspace too small (%lld < %lld)", pf ? "carekv_prefill_correct" : "carekv_decode_attn",
               (long long)workspace_bytes, (long long)need);
@@ -229,6 +292,11 @@ int run_decode(const carekv_arena* arena, const carekv_decode_params* dp, const 
     hipLaunchKernelGGL(prompt_vsq_kernel, dim3((unsigned)((pf->pages + 3) / 4), A.n_kv_heads), dim3(256), 0, s,
                        P.v_hat, P.n_tokens, A.head_dim, pf->pages, a.pf_vsq);
     CAREKV_CHECK_LAUNCH("prompt_vsq");
+    int* suf = (int*)(ws + vsq_off + ((long)A.n_kv_heads * pf->pages * 4 + 255) / 256 * 256);
+    a.pf_suf = suf;
+    hipLaunchKernelGGL(prompt_suffix_kernel, dim3(A.n_kv_heads), dim3(kBlock), 0, s, A, P.seq, pf->pages, a.k_cap,
+                       a.v_cap, suf);
+    CAREKV_CHECK_LAUNCH("prompt_suffix");
   }
   hipEvent_t* ev = (hipEvent_t*)dp->phase_events;
   auto mark = [&](int i) -> int {
@@ -286,7 +354,7 @@ int prefill_setup(const carekv_arena* arena, const carekv_decode_params* read,
   pf.R = 16 / pf.G0;
   dp.batch = (pp->n_rows + pf.R - 1) / pf.R;
   dp.max_pages_used = pages;
-  // with the moments' K score the streaming pass runs on blocks of 8
+  // with the moments' K score the streaming pass runs on blocks of 4
   // entries over every visible page at once (pf_rows_stream_kernel), one
   // split per entry (CAREKV_PF_ROWS=0: entry by entry over the caller's splits)
   const char* env = getenv("CAREKV_PF_ROWS");
@@ -305,7 +373,7 @@ extern "C" int64_t carekv_prefill_correct_workspace_bytes(const carekv_arena* ar
   carekv_decode_params dp{};
   PfRows pf{};
   if (prefill_setup(arena, read, pp, dp, pf) != CAREKV_OK || dp.split_pages <= 0) return -1;
-  return ws_layout(*arena, dp, pf.G0 * pf.R, true).total + (int64_t)arena->n_kv_heads * pf.pages * 4;
+  return ws_layout(*arena, dp, pf.G0 * pf.R, true).total + pf_extra_bytes(*arena, pf.pages);
 }
 
 extern "C" int carekv_prefill_correct(const carekv_arena* arena, const carekv_decode_params* read,

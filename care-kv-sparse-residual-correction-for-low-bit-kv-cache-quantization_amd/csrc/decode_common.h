@@ -65,6 +65,11 @@ struct DecodeArgs {
   const uint16_t* pf_v;
   const float* pf_lse;
   float* pf_vsq;  // [Hkv][pf_pages] sum of V_hat^2 over each page's prompt rows
+  // [Hkv][3][pf_pages + 1]: over pages p .. pf_pages-1, the K slots and V
+  // blocks a row seeing pages 0 .. p-1 counts without scoring (each page
+  // capped at k_cap / v_cap as the select kernels count it), and 1 when one
+  // of those pages holds more than the caps
+  const int* pf_suf;
 };
 
 // The cache row and visible extent of batch entry b (for prefill rows, of

@@ -464,25 +464,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
     }
     for (; rv < v_cap; ++rv) sc[nK + p * v_cap + rv] = -1.f;
   }
-  if (a.pf) {
+  if (a.pf && tid == 0) {
     // prefill rows: the candidates of the prompt's later pages score 0
     // (A = 0 past the row) but count, as in the reference's candidate set
-    // over all pages of the kv head (layer.py:514-517)
-    for (int p = np + tid; p < a.pf_pages; p += kBlock) {
-      const long pg = pg_base + p;
-      const int nv = A.valid[pg];
-      if (nv <= 0 || !A.has_meta[pg]) continue;
-      int rk = 0, rv = 0;  // the stored slots by rank, as the scoring loops count them
-      for (int cg = 0; cg < NCG; ++cg) rk += slot_ok(A, A.k_slot[pg * NCG + cg]) ? 1 : 0;
-      ovf |= rk > k_cap;
-      cntK += min(rk, k_cap);
-      for (int vb = 0; vb < kVtb; ++vb) {
-        if (!slot_ok(A, A.v_slot[pg * kVtb + vb])) continue;
-        if (rv >= v_cap) { ovf = true; break; }
-        if (vb * kVtb < nv) ++cntV;
-        ++rv;
-      }
-    }
+    // over all pages of the kv head (layer.py:514-517): their suffix counts
+    const int* suf = a.pf_suf + (long)kvh * 3 * (a.pf_pages + 1);
+    cntK += suf[np];
+    cntV += suf[(a.pf_pages + 1) + np];
+    ovf |= suf[2 * (a.pf_pages + 1) + np] != 0;
   }
   if (ovf) *a.err_flag = 1;
   float tK = sumK, tV = sumV;
@@ -808,22 +797,11 @@ __global__ __launch_bounds__(256) void decode_select_wave_kernel(carekv_arena A,
       ++cntV;
     }
   }
-  if (a.pf) {  // the prompt's later pages: candidates that count, scored 0 (layer.py:514-517)
-    for (int p = np + lane; p < a.pf_pages; p += 64) {
-      const long pg = pg_base + p;
-      const int nv = A.valid[pg];
-      if (nv <= 0 || !A.has_meta[pg]) continue;
-      int rk = 0, rv = 0;
-      for (int cg = 0; cg < NCG; ++cg) rk += slot_ok(A, A.k_slot[pg * NCG + cg]) ? 1 : 0;
-      ovf |= rk > 1;
-      cntK += min(rk, 1);
-      for (int vb = 0; vb < kVtb; ++vb) {
-        if (!slot_ok(A, A.v_slot[pg * kVtb + vb])) continue;
-        if (rv >= 1) { ovf = true; break; }
-        if (vb * kVtb < nv) ++cntV;
-        ++rv;
-      }
-    }
+  if (a.pf && lane == 0) {  // the prompt's later pages: candidates that count, scored 0 (layer.py:514-517)
+    const int* suf = a.pf_suf + (long)kvh * 3 * (a.pf_pages + 1);
+    cntK += suf[np];
+    cntV += suf[(a.pf_pages + 1) + np];
+    ovf |= suf[2 * (a.pf_pages + 1) + np] != 0;
   }
   if (__any(ovf) && lane == 0) *a.err_flag = 1;
   float pk[NJ], pvv[NJ];
