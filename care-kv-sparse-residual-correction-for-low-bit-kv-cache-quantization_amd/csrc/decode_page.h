@@ -694,35 +694,19 @@ __device__ __forceinline__ void buf_load_row(uint32_t* w, __amdgpu_buffer_rsrc_t
   }
 }
 
-// Field f of page pg's metadata (the lane layout of meta_lanes_load); 0
-// when page_ok is false.
-template <int NCG>
-__device__ __forceinline__ int meta_field_load(const carekv_arena& A, long pg, bool page_ok, int f) {
-  int v = 0;
-  if (!page_ok) return 0;
-  if (f == 0) v = A.valid[pg];
-  else if (f == 1) v = A.has_meta[pg];
-  else if (f < 2 + NCG) v = A.k_slot[pg * NCG + f - 2];
-  else if (f >= 6 && f < 10) v = A.v_slot[pg * kVtb + f - 6];
-  else if (f == 10 && A.scale_mode == 1) v = A.kmaster[pg];
-  else if (f == 11 && A.scale_mode == 1) v = A.vmaster[pg];
-  return v;
-}
-
-// Field f of page p of a row (layout of meta_field_load) with no branch:
-// three loads (the int32, fp16 and int8 arrays) that every lane issues.  A
-// lane whose field is in another array, or whose page is not ok, reads page
-// 0 of the row (always mapped) and drops the value; a page that is not ok
-// gives 0.
 // *(T*)(base + off) with a 32-bit byte offset (base uniform).
 template <typename T>
 __device__ __forceinline__ T ld_off(const void* base, uint32_t off) {
   return *reinterpret_cast<const T*>(reinterpret_cast<const char*>(base) + off);
 }
 
-// meta_field_any with every load on a row base (uniform) plus a 32-bit lane
-// index: five loads per lane (valid, k_slot, v_slot, master, has_meta) and
-// a select of values, so no per-lane 64-bit address stays live.
+// Field f of page p of a row (the lane layout of meta_lanes_load: 0 valid,
+// 1 has_meta, 2.. the K slots, 6..9 the V slots, 10 / 11 the K / V scale
+// masters), 0 when the page is not ok.  Every load is on a row base
+// (uniform) plus a 32-bit lane index: five loads per lane (valid, k_slot,
+// v_slot, master, has_meta) and a select of values, so no per-lane 64-bit
+// address stays live; a lane whose field is in another array, or whose page
+// is not ok, reads page 0 of the row (always mapped) and drops the value.
 template <int NCG, int SM>
 __device__ __forceinline__ int meta_field_row(const carekv_arena& A, long pg_base, int p, bool ok, int f) {
   const uint32_t pp = ok ? (uint32_t)p : 0u;
@@ -748,7 +732,8 @@ __device__ __forceinline__ int meta_field_row(const carekv_arena& A, long pg_bas
   return ok ? v : 0;
 }
 
-// meta_field_any in two steps: meta_word_load issues one 32-bit load of the
+// Field f of page pg (the layout of meta_field_row) in two steps:
+// meta_word_load issues one 32-bit load of the
 // aligned word that holds field f of page pg (the 16-bit masters and the
 // 8-bit has_meta are read through the aligned word holding them; such a word
 // lies in the same mapped page as the field), and meta_word_field extracts
@@ -778,22 +763,6 @@ __device__ __forceinline__ int meta_word_field(const carekv_arena& A, uint32_t w
     return (int)((w >> (8u * (uint32_t)(reinterpret_cast<uintptr_t>(m) & 2u))) & 0xffffu);
   }
   return 0;
-}
-
-template <int NCG, int SM>
-__device__ __forceinline__ int meta_field_any(const carekv_arena& A, long pg_base, int p, bool ok, int f) {
-  const long pg = pg_base + (ok ? p : 0);
-  const bool in_ks = f >= 2 && f < 2 + NCG, in_vs = f >= 6 && f < 6 + kVtb;
-  const int32_t* p32 = in_ks ? A.k_slot + pg * NCG + (f - 2) : in_vs ? A.v_slot + pg * kVtb + (f - 6) : A.valid + pg;
-  const int v32 = *p32;
-  int v16 = 0;
-  if constexpr (SM == 1) v16 = (int)(f == 11 ? A.vmaster : A.kmaster)[pg];
-  const int v8 = (int)A.has_meta[pg];
-  int v = 0;
-  if (f == 0 || in_ks || in_vs) v = v32;
-  if (f == 1) v = v8;
-  if (f == 10 || f == 11) v = v16;
-  return ok ? v : 0;
 }
 
 // ---------------------------------------------------------------- 4x4x4 PV
