@@ -366,6 +366,9 @@ PREFILL_RANDOM = [
     (64, 8, 2, 5, "joint", "exact", (1, 1), (2, 2)),          # one partial page
     (128, 8, 2, 16, "separate", "exact", (2, 4), (3, 3)),     # exactly one page
     (128, 8, 2, 150, "joint", "exact", (2, 4), (6, 6), "kivi_style"),  # the KIVI-style fp16 side buffer
+    # 263 pages: the work-group select form (rows past 256 pages) and the
+    # later pages' candidate counts over two 256-page chunks of the suffix scan
+    (64, 2, 1, 4200, "joint", "exact", (1, 1), (8, 8)),
 ]
 
 
