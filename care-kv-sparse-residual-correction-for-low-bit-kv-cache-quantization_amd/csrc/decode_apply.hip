@@ -322,9 +322,12 @@ void decode_apply_kernel(carekv_arena A, DecodeArgs a) {
 // and the sum rounded apart, as the select kernel forms it without a
 // correction).
 // A thread takes 4 consecutive dims of one query; every load of its splits
-// and chunks is issued before the sums that use it (batches of 8 splits and
-// 4 chunks, indices clamped to the last one, read whatever L is), so a wave
-// waits about one memory latency per batch instead of one per split.
+// and chunks is issued before the sums that use it (batches of SB splits and
+// CB chunks, indices clamped to the last one, read whatever L is), so a wave
+// waits about one memory latency per batch instead of one per split.  The
+// host sizes the batches to the counts (8 / 2 / 1 splits, 4 / 2 / 1 chunks),
+// so that a call with one split does not issue seven clamped repeats.
+template <int SB, int CB>
 __global__ __launch_bounds__(256) void decode_combine_kernel(int Hkv, int D, int out_al8, DecodeArgs a) {
   const int D4 = D >> 2, GQ = a.GQ;
   const long gid = (long)blockIdx.x * 256 + threadIdx.x;
@@ -346,26 +349,26 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(int Hkv, int D, int
   const long cb0 = (long)bk * ns * GQ + qq;  // chunk c: row cb0 + c GQ of num / den
   float4 O = make_float4(0.f, 0.f, 0.f, 0.f), nm = make_float4(0.f, 0.f, 0.f, 0.f);
   float dn = 0.f;
-  const int nb = max((ns + 7) / 8, (na + 3) / 4);
-  for (int k = 0; k < nb; ++k) {  // batch k: splits 8k .. 8k+7 and chunks 4k .. 4k+3
-    float ms[8], dv[4];
-    float4 pv[8], nv[4];
+  const int nb = max((ns + SB - 1) / SB, (na + CB - 1) / CB);
+  for (int k = 0; k < nb; ++k) {  // batch k: splits SB k .. SB k + SB-1 and chunks CB k .. CB k + CB-1
+    float ms[SB], dv[CB];
+    float4 pv[SB], nv[CB];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const long base = sb + 16L * min(8 * k + j, ns - 1);
+    for (int j = 0; j < SB; ++j) {
+      const long base = sb + 16L * min(SB * k + j, ns - 1);
       ms[j] = a.pml[base * 2];
       pv[j] = *reinterpret_cast<const float4*>(a.po + base * D + d);
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const long cb = cb0 + (long)max(min(4 * k + j, na - 1), 0) * GQ;
+    for (int j = 0; j < CB; ++j) {
+      const long cb = cb0 + (long)max(min(CB * k + j, na - 1), 0) * GQ;
       nv[j] = *reinterpret_cast<const float4*>(a.num + cb * D + d);
       dv[j] = a.den[cb];
     }
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
+    for (int j = 0; j < SB; ++j) {
       const float e = __builtin_amdgcn_exp2f(ms[j] - M);
-      if (8 * k + j < ns && ms[j] != -INFINITY) {  // product and sum rounded apart (no contraction)
+      if (SB * k + j < ns && ms[j] != -INFINITY) {  // product and sum rounded apart (no contraction)
         O.x += pv[j].x * e;
         O.y += pv[j].y * e;
         O.z += pv[j].z * e;
@@ -373,8 +376,8 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(int Hkv, int D, int
       }
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {  // chunks past the last add +0, which leaves a sum begun at +0 unchanged
-      const bool in = 4 * k + j < na;
+    for (int j = 0; j < CB; ++j) {  // chunks past the last add +0, which leaves a sum begun at +0 unchanged
+      const bool in = CB * k + j < na;
       nm.x += in ? nv[j].x : 0.f;
       nm.y += in ? nv[j].y : 0.f;
       nm.z += in ? nv[j].z : 0.f;
@@ -436,8 +439,22 @@ int launch_decode_combine(const carekv_arena& A, const DecodeArgs& a, hipStream_
   const long n = (long)a.B * A.n_kv_heads * a.GQ * (A.head_dim / 4);
   if (n == 0) return CAREKV_OK;
   const int out_al8 = (reinterpret_cast<uintptr_t>(a.out) & 7) == 0;
-  hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, A.n_kv_heads,
-                     A.head_dim, out_al8, a);
+  const dim3 grid((unsigned)((n + 255) / 256));
+  const int sb = a.nsplit >= 8 ? 8 : a.nsplit >= 2 ? 2 : 1, cb = a.napply >= 4 ? 4 : a.napply >= 2 ? 2 : 1;
+  auto go = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(256), 0, s, A.n_kv_heads, A.head_dim, out_al8, a); };
+  if (sb == 8) {
+    if (cb == 4) go(decode_combine_kernel<8, 4>);
+    else if (cb == 2) go(decode_combine_kernel<8, 2>);
+    else go(decode_combine_kernel<8, 1>);
+  } else if (sb == 2) {
+    if (cb == 4) go(decode_combine_kernel<2, 4>);
+    else if (cb == 2) go(decode_combine_kernel<2, 2>);
+    else go(decode_combine_kernel<2, 1>);
+  } else {
+    if (cb == 4) go(decode_combine_kernel<1, 4>);
+    else if (cb == 2) go(decode_combine_kernel<1, 2>);
+    else go(decode_combine_kernel<1, 1>);
+  }
   CAREKV_CHECK_LAUNCH("decode_combine");
   return CAREKV_OK;
 }
