@@ -64,6 +64,7 @@ struct PfRows {
   const carekv_prefill_corr_params* p;
   int pages;
   int R, G0;  // rows per entry, query heads per kv head
+  bool rows;  // the streaming pass over blocks of entries (pf_rows_stream_kernel)
 };
 
 __global__ __launch_bounds__(256) void prompt_vsq_kernel(const uint16_t* __restrict__ v, int T, int D, int pages,
@@ -285,6 +286,7 @@ int run_decode(const carekv_arena* arena, const carekv_decode_params* dp, const 
   if (pf) {
     const carekv_prefill_corr_params& P = *pf->p;
     a.pf = 1;
+    a.pf_rows = pf->rows ? 1 : 0;
     a.pf_seq = P.seq; a.pf_row0 = P.row_begin; a.pf_row_end = P.row_begin + P.n_rows;
     a.pf_R = pf->R; a.pf_G0 = pf->G0; a.pf_pages = pf->pages; a.pf_T = P.n_tokens;
     a.pf_k = P.k_hat; a.pf_v = P.v_hat; a.pf_lse = P.lse;
@@ -355,12 +357,20 @@ int prefill_setup(const carekv_arena* arena, const carekv_decode_params* read,
   dp.batch = (pp->n_rows + pf.R - 1) / pf.R;
   dp.max_pages_used = pages;
   // with the moments' K score the streaming pass runs on blocks of 4
-  // entries over every visible page at once (pf_rows_stream_kernel), one
-  // split per entry (CAREKV_PF_ROWS=0: entry by entry over the caller's splits)
+  // entries (pf_rows_stream_kernel) in splits of kPfSplit pages, so that the
+  // longest rows' serial chains stay short (at most 16 splits; the split's
+  // pages are a multiple of 4).  CAREKV_PF_ROWS=0: entry by entry over the
+  // caller's splits; CAREKV_PF_SPLIT overrides the pages per split.
   const char* env = getenv("CAREKV_PF_ROWS");
-  if (!(env && env[0] == '0') && read->k_proxy == 0 && read->route_policy != 3 && pages <= 1024 &&
-      (A.head_dim == 64 || A.head_dim == 128))
-    dp.split_pages = (pages + 3) / 4 * 4;
+  pf.rows = !(env && env[0] == '0') && read->k_proxy == 0 && read->route_policy != 3 && pages <= 1024 &&
+            (A.head_dim == 64 || A.head_dim == 128);
+  if (pf.rows) {
+    const char* es = getenv("CAREKV_PF_SPLIT");
+    int sp = es ? atoi(es) : kPfSplit;
+    sp = max(sp, (pages + 15) / 16);
+    sp = min(max((sp + 3) / 4 * 4, 4), (pages + 3) / 4 * 4);
+    dp.split_pages = sp;
+  }
   dp.seq_slot = nullptr;
   dp.n_pages = nullptr;
   return CAREKV_OK;

@@ -344,18 +344,18 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(int Hkv, int D, int
   }
   const long bq = (long)bk * GQ + qq;
   const float M = a.ml[bq * 2], L = a.ml[bq * 2 + 1];
-  const int ns = a.nsplit, na = a.napply;
+  const int ns = a.nsplit, nsr = splits_read(a, b), na = a.napply;
   const long sb = (long)bk * ns * 16 + qq;   // split s: row sb + 16 s of po / pml
   const long cb0 = (long)bk * ns * GQ + qq;  // chunk c: row cb0 + c GQ of num / den
   float4 O = make_float4(0.f, 0.f, 0.f, 0.f), nm = make_float4(0.f, 0.f, 0.f, 0.f);
   float dn = 0.f;
-  const int nb = max((ns + SB - 1) / SB, (na + CB - 1) / CB);
+  const int nb = max((nsr + SB - 1) / SB, (na + CB - 1) / CB);
   for (int k = 0; k < nb; ++k) {  // batch k: splits SB k .. SB k + SB-1 and chunks CB k .. CB k + CB-1
     float ms[SB], dv[CB];
     float4 pv[SB], nv[CB];
 #pragma unroll
     for (int j = 0; j < SB; ++j) {
-      const long base = sb + 16L * min(SB * k + j, ns - 1);
+      const long base = sb + 16L * min(SB * k + j, nsr - 1);
       ms[j] = a.pml[base * 2];
       pv[j] = *reinterpret_cast<const float4*>(a.po + base * D + d);
     }
@@ -368,7 +368,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(int Hkv, int D, int
 #pragma unroll
     for (int j = 0; j < SB; ++j) {
       const float e = __builtin_amdgcn_exp2f(ms[j] - M);
-      if (SB * k + j < ns && ms[j] != -INFINITY) {  // product and sum rounded apart (no contraction)
+      if (SB * k + j < nsr && ms[j] != -INFINITY) {  // product and sum rounded apart (no contraction)
         O.x += pv[j].x * e;
         O.y += pv[j].y * e;
         O.z += pv[j].z * e;

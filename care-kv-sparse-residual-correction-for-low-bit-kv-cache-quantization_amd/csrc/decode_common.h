@@ -7,6 +7,11 @@
 
 namespace carekv {
 
+// Pages per split of the prefill correction's streaming pass over blocks of
+// rows (pf_rows_stream_kernel): every work-group's serial chain of tiles
+// stays this short, however long the prompt.
+constexpr int kPfSplit = 32;
+
 struct DecodeArgs {
   const uint16_t* q;
   uint16_t* out;
@@ -60,6 +65,9 @@ struct DecodeArgs {
   // columns are (row pf_row0 + b * pf_R + c / pf_G0, head c % pf_G0 of the
   // kv head's group); rows from pf_row_end on are padding.
   int pf;
+  // prefill rows through pf_rows_stream_kernel (blocks of 4 entries, splits
+  // of SP pages) rather than the entry-by-entry streaming kernel
+  int pf_rows;
   int pf_seq, pf_row0, pf_row_end, pf_R, pf_G0, pf_pages, pf_T;
   const uint16_t* pf_k;
   const uint16_t* pf_v;
@@ -118,6 +126,14 @@ __device__ __forceinline__ PfCol pf_col(const DecodeArgs& a, int b, int kvh, int
   x.head = kvh * a.pf_G0 + c % a.pf_G0;
   x.ok = c < a.GQ && x.row < a.pf_row_end;
   return x;
+}
+// Split partials of entry b that hold data: all of them, except in the
+// prefill rows pass, which writes no partial for a split past the entry's
+// last page (its rows see pages 0 .. row / kPage).
+__device__ __forceinline__ int splits_read(const DecodeArgs& a, int b) {
+  if (!a.pf_rows) return a.nsplit;
+  const int row = min(a.pf_row0 + (b + 1) * a.pf_R, a.pf_row_end) - 1;
+  return min(a.nsplit, (row / kPage + a.SP) / a.SP);
 }
 // Element offset of a column's row in q / out / diag rows ([n_rows][Hq][.]).
 __device__ __forceinline__ long pf_row_off(const DecodeArgs& a, const PfCol& x) {

@@ -243,12 +243,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
   }
 
   // ---- softmax statistics from the split partials
+  const int nsr = splits_read(a, b);
   float mloc = -INFINITY;
-  for (int s = tid; s < a.nsplit; s += kBlock) mloc = fmaxf(mloc, a.pml[(((long)bk * a.nsplit + s) * 16 + qq) * 2]);
+  for (int s = tid; s < nsr; s += kBlock) mloc = fmaxf(mloc, a.pml[(((long)bk * a.nsplit + s) * 16 + qq) * 2]);
   const float M = block_max_fast(mloc, bs);
   float lloc = 0.f;
   if (M != -INFINITY)
-    for (int s = tid; s < a.nsplit; s += kBlock) {
+    for (int s = tid; s < nsr; s += kBlock) {
       const long base = ((long)bk * a.nsplit + s) * 16 + qq;
       const float ms = a.pml[base * 2];
       if (ms != -INFINITY) lloc += a.pml[base * 2 + 1] * __builtin_amdgcn_exp2f(ms - M);
@@ -262,7 +263,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(8, 8))) voi
       float O = 0.f;
       if (M != -INFINITY)
 #pragma unroll 8
-        for (int s = 0; s < a.nsplit; ++s) {
+        for (int s = 0; s < nsr; ++s) {
           const long base = ((long)bk * a.nsplit + s) * 16 + qq;
           const float ms = a.pml[base * 2];
           if (ms != -INFINITY) O += a.po[base * D + d] * __builtin_amdgcn_exp2f(ms - M);
@@ -723,11 +724,12 @@ __global__ __launch_bounds__(256) void decode_select_wave_kernel(carekv_arena A,
   };
 
   // ---- softmax statistics from the split partials (nsplit <= 256)
+  const int nsr = splits_read(a, b);
   float mloc = -INFINITY;
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     const int s = lane + 64 * j;
-    if (s < a.nsplit) mloc = fmaxf(mloc, a.pml[(((long)bk * a.nsplit + s) * 16 + qq) * 2]);
+    if (s < nsr) mloc = fmaxf(mloc, a.pml[(((long)bk * a.nsplit + s) * 16 + qq) * 2]);
   }
   const float M = wave_max_f(mloc);
   float lj[NJ];
@@ -735,7 +737,7 @@ __global__ __launch_bounds__(256) void decode_select_wave_kernel(carekv_arena A,
   for (int j = 0; j < NJ; ++j) {
     lj[j] = 0.f;
     const int s = lane + 64 * j;
-    if (M != -INFINITY && s < a.nsplit) {
+    if (M != -INFINITY && s < nsr) {
       const long base = ((long)bk * a.nsplit + s) * 16 + qq;
       const float ms = a.pml[base * 2];
       if (ms != -INFINITY) lj[j] = a.pml[base * 2 + 1] * __builtin_amdgcn_exp2f(ms - M);

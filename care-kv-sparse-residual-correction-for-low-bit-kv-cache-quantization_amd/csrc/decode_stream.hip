@@ -273,7 +273,7 @@ int launch_decode_stream(const carekv_arena& A, const DecodeArgs& a, hipStream_t
   dim3 grid(a.nsplit_run, A.n_kv_heads, a.B);
   if (a.pf) {
     // one split (the host's choice when the rows take the work-group-per-8-entries pass)
-    if (a.nsplit == 1 && !a.proxy && !a.xbuf) return launch_pf_rows_stream(A, a, s);
+    if (a.pf_rows) return launch_pf_rows_stream(A, a, s);
     auto go = [&](auto kern) {
       hipLaunchKernelGGL(kern, grid, dim3(256), 0, s, A, a);
       CAREKV_CHECK_LAUNCH("decode_stream (prefill rows)");

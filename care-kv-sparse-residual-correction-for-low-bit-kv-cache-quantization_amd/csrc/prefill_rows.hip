@@ -18,8 +18,15 @@
 //   * per (column, page) the generic kernel's record: m_ref, t* and e*, the
 //     K slots' moments (dS on the same MFMA from the residual rows), the V
 //     blocks' masses, and the fp16 weights (ebuf);
-//   * O += e V_hat on the same tile (transpose load), and L = sum e, as one
-//     split partial per entry (the host runs this pass with one split).
+//   * O += e V_hat on the same tile (transpose load), and L = sum e, as the
+//     entry's partial of the work-group's split.
+// The grid's third dimension splits the pages (SP a split): a row's work
+// grows with its index, and with all of a prompt's entries resident at once
+// the longest rows' chains of tiles would otherwise run alone at the end.
+// Every split's partial carries the same fixed maximum lse2, so the merges
+// add the partials with weight exp2(0) = 1: the splits change only the fp32
+// order of the O and L sums.  A split past an entry's last page writes no
+// partial, and the select and combine kernels read none (splits_read).
 #include "decode_page.h"
 #include "host_util.h"
 
@@ -88,6 +95,13 @@ __global__ __launch_bounds__(256, 2) void pf_rows_stream_kernel(carekv_arena A, 
       }
     }
   }
+  // pages of the work-group: those of its last entry; its split: tiles
+  // jt0 .. jt1-1 (SP / 2 tiles a split)
+  const int np_wg = entry_row(A, a, min(e0 + EPW, a.B) - 1).np;
+  const int nt = (np_wg + 1) / 2;
+  const int split = blockIdx.z, tps = a.SP / 2;
+  const int jt0 = split * tps, jt1 = min(jt0 + tps, nt);
+  if (jt0 >= jt1) return;  // past every entry's pages: no partial (splits_read)
   for (int i = threadIdx.x; i < EPW * 16 * D; i += 256) {
     const int el = i / (16 * D), n = (i / D) % 16, d = i % D;
     const int b = e0 + el;
@@ -96,9 +110,6 @@ __global__ __launch_bounds__(256, 2) void pf_rows_stream_kernel(carekv_arena A, 
     sqr[i] = ok ? bits2half(a.q[pf_row_off(a, x) * D + (d & ~7) + PK::T.slot_code[d & 7]]) : (_Float16)0.f;
   }
 
-  // pages of the work-group: those of its last entry
-  const int np_wg = entry_row(A, a, min(e0 + EPW, a.B) - 1).np;
-  const int nt = (np_wg + 1) / 2;
   const uint32_t span = (uint32_t)T * D * 2;  // rows past the prompt read as 0
   const __amdgpu_buffer_rsrc_t rk = make_rsrc(a.pf_k + (long)kvh * T * D, span);
   const __amdgpu_buffer_rsrc_t rv = make_rsrc(a.pf_v + (long)kvh * T * D, span);
@@ -129,6 +140,24 @@ __global__ __launch_bounds__(256, 2) void pf_rows_stream_kernel(carekv_arena A, 
       mv[tt] = p < np_wg ? meta_lanes_load<NCG>(A, pg_base + p, lane) : 0;
     }
   };
+  // K residual words (lane: token ln, bytes 4lj..) and raw fp16 scales of
+  // the two pages' stored slots; a page without a slot (or without
+  // metadata) reads past the end of the resources, i.e. 0 with no memory
+  // access, so that the loads are issued by every lane without a branch
+  constexpr int KSB = PageGeom<D, 16>::KSB;
+  const __amdgpu_buffer_rsrc_t rkr = make_rsrc(A.k_res + (long)seq * A.n_slots * KSB, (uint32_t)A.n_slots * KSB);
+  const __amdgpu_buffer_rsrc_t rks = make_rsrc(A.k_res_scale + (long)seq * A.n_slots, (uint32_t)A.n_slots * 2u);
+  auto load_kres = [&](const PageMeta<NCG>* m, uint32_t (*kw)[NCG], uint32_t (*ks)[NCG]) {
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+      for (int cg = 0; cg < NCG; ++cg) {
+        const bool has = corr && m[tt].meta && m[tt].ksl[cg] >= 0;
+        const uint32_t slot = has ? (uint32_t)m[tt].ksl[cg] : (uint32_t)A.n_slots;
+        kw[tt][cg] = __builtin_amdgcn_raw_buffer_load_b32(rkr, slot * KSB + ln * 16 + lj * 4, 0, 0);
+        ks[tt][cg] = __builtin_amdgcn_raw_buffer_load_b16(rks, slot * 2u, 0, 0);
+      }
+  };
 
   float4_t o[QB][DT];
   float lpart[QB];
@@ -139,35 +168,27 @@ __global__ __launch_bounds__(256, 2) void pf_rows_stream_kernel(carekv_arena A, 
     for (int dt = 0; dt < DT; ++dt) o[qb][dt] = float4_t{0.f, 0.f, 0.f, 0.f};
   }
 
-  int mv_nx[2] = {0, 0};
-  if (nt > 0) {
-    load_tile(0);
-    store_tile(0);
-    load_meta2(0, mv_nx);
-  }
+  // Load schedule: the metadata of tile jt + 1 is in flight during tile jt;
+  // the K residual words and scales of a tile are issued at its top, ahead
+  // of its S products.  (Issuing them a tile ahead measured the same at 25
+  // VGPRs more: the pass is bound by its longest chain of tiles, which the
+  // splits keep short, not by these loads.)
+  int mv_nx[2];
+  load_tile(jt0);
+  store_tile(0);
+  load_meta2(jt0, mv_nx);
   __syncthreads();
-  if (nt > 1) load_tile(1);
+  if (jt0 + 1 < jt1) load_tile(jt0 + 1);
 
-  for (int jt = 0; jt < nt; ++jt) {
-    const char* kb = lds + (jt & 1) * BUF;
+  for (int jt = jt0; jt < jt1; ++jt) {
+    const char* kb = lds + ((jt - jt0) & 1) * BUF;
     const char* vb = kb + KBUF;
     PageMeta<NCG> cm[2];
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) cm[tt] = meta_from_lanes<NCG>(mv_nx[tt], A);
-    if (jt + 1 < nt) load_meta2(jt + 1, mv_nx);
-    // K residual words of the two pages' stored slots (lane: token ln, bytes 4lj..)
-    uint32_t krow[2][NCG];
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-      for (int cg = 0; cg < NCG; ++cg) {
-        krow[tt][cg] = 0u;
-        if (corr && cm[tt].meta && cm[tt].ksl[cg] >= 0) {
-          const long so = (long)seq * A.n_slots + cm[tt].ksl[cg];
-          const __amdgpu_buffer_rsrc_t r = make_rsrc(A.k_res + so * PageGeom<D, 16>::KSB, PageGeom<D, 16>::KSB);
-          krow[tt][cg] = __builtin_amdgcn_raw_buffer_load_b32(r, ln * 16 + lj * 4, 0, 0);
-        }
-      }
+    if (jt + 1 < jt1) load_meta2(jt + 1, mv_nx);
+    uint32_t krow[2][NCG], ksc[2][NCG];
+    load_kres(cm, krow, ksc);
 
     // ---- S = K_hat q per page and entry, and the page's weights and record
     float ep[2][QB][4];  // [page][entry][token i]
@@ -241,8 +262,7 @@ __global__ __launch_bounds__(256, 2) void pf_rows_stream_kernel(carekv_arena A, 
           }
           const float mj = moments_reduce4(M2, M3, M4, Ds);
           if (ln < GQ) {
-            const long so = (long)seq * A.n_slots + slot;
-            const float f = h2f(A.k_res_scale[so]) * a.inv_sqrt_d;
+            const float f = h2f((uint16_t)ksc[tt][cg]) * a.inv_sqrt_d;
             rec[1 + 4 * rkk + lj] = mj * (f * f);
           }
           ++rkk;
@@ -279,23 +299,24 @@ __global__ __launch_bounds__(256, 2) void pf_rows_stream_kernel(carekv_arena A, 
         for (int qb = 0; qb < QB; ++qb) o[qb][dt] = mfma16x32(av, bp[qb], o[qb][dt]);
       }
     }
-    if (jt + 1 < nt) store_tile((jt + 1) & 1);
-    if (jt + 2 < nt) load_tile(jt + 2);
+    if (jt + 1 < jt1) store_tile((jt + 1 - jt0) & 1);
+    if (jt + 2 < jt1) load_tile(jt + 2);
     __syncthreads();
   }
 
-  // ---- the entries' split partials (one split): O unnormalised, (lse2, L)
+  // ---- the entries' split partials: O unnormalised, (lse2, L); none for
+  // an entry whose pages end before the split (splits_read)
 #pragma unroll
   for (int qb = 0; qb < QB; ++qb) {
     const float lt = col_sum(lpart[qb]);
-    if (!eok[qb] || ln >= GQ) continue;
+    if (!eok[qb] || ln >= GQ || split * a.SP >= enp[qb]) continue;
     const long bk = (long)eb[qb] * A.n_kv_heads + kvh;
-    float* po = a.po + (bk * a.nsplit * 16 + ln) * D + 4 * lj;
+    float* po = a.po + ((bk * a.nsplit + split) * 16 + ln) * D + 4 * lj;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
       *reinterpret_cast<float4*>(po + 16 * dt) = make_float4(o[qb][dt][0], o[qb][dt][1], o[qb][dt][2], o[qb][dt][3]);
     if (lj == 0) {
-      float* pml = a.pml + (bk * a.nsplit * 16 + ln) * 2;
+      float* pml = a.pml + ((bk * a.nsplit + split) * 16 + ln) * 2;
       pml[0] = lse2[qb];
       pml[1] = lt;
     }
@@ -303,13 +324,14 @@ __global__ __launch_bounds__(256, 2) void pf_rows_stream_kernel(carekv_arena A, 
 }
 
 int launch_pf_rows_stream(const carekv_arena& A, const DecodeArgs& a, hipStream_t s) {
-  if (!a.pf || a.nsplit != 1 || a.proxy || a.xbuf) {
-    set_error("pf_rows_stream: prefill rows with one split, the moments' K score and no logit buffer");
+  if (!a.pf || a.proxy || a.xbuf || a.SP % 2 != 0 || a.nsplit * a.SP < a.pf_pages) {
+    set_error("pf_rows_stream: prefill rows with the moments' K score, no logit buffer and splits of whole tiles "
+              "covering every page");
     return CAREKV_EINVAL;
   }
-  // one entry per wave: two waves per SIMD at a call's entry count (two
-  // entries per wave, one wave per SIMD, measured 30% slower)
-  const dim3 grid((a.B + 3) / 4, A.n_kv_heads);
+  // one entry per wave (two entries per wave, one wave per SIMD, measured
+  // 30% slower), one split per grid layer
+  const dim3 grid((a.B + 3) / 4, A.n_kv_heads, a.nsplit);
   if (A.head_dim == 64) hipLaunchKernelGGL((pf_rows_stream_kernel<64, 1>), grid, dim3(256), 0, s, A, a);
   else if (A.head_dim == 128) hipLaunchKernelGGL((pf_rows_stream_kernel<128, 1>), grid, dim3(256), 0, s, A, a);
   else {

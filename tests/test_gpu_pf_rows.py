@@ -4,14 +4,16 @@ the entry-by-entry pass (needs a GPU).
 pf_rows_stream_kernel forms the same page records and stored fp16 weights
 as decode_stream_kernel in prefill-rows mode (S in the same MFMA reduction
 order, the same record arithmetic), so the selections must be equal; the
-base output O and its normaliser L are summed over the whole row at once
-instead of per split and wave, so the corrected outputs may differ in the
-last fp32 bits, i.e. by at most one fp16 ulp (checked at two).  Cases:
-head_dim 64 and 128, 1 / 4 / 8 query heads per kv head (16, 4, 2 rows per
-entry), one and several stored slots per page, exact and linear K
-corrections, ragged calls (rows_per_call not a multiple of the rows per
-entry).  CAREKV_PF_ROWS=0 selects the entry-by-entry pass; both are held
-to the reference goldens in test_gpu_parity.py.
+base output O and its normaliser L are summed per split of this pass's
+own size (32 pages, or CAREKV_PF_SPLIT) instead of per split and wave of
+the entry pass, so the corrected outputs may differ in the last fp32
+bits, i.e. by at most one fp16 ulp (checked at two).  Cases: head_dim 64
+and 128, 1 / 4 / 8 query heads per kv head (16, 4, 2 rows per entry), one
+and several stored slots per page, exact and linear K corrections, ragged
+calls (rows_per_call not a multiple of the rows per entry), and splits of
+8 pages (9 splits, the later ones past the short entries' pages).
+CAREKV_PF_ROWS=0 selects the entry-by-entry pass; both are held to the
+reference goldens in test_gpu_parity.py.
 """
 import numpy as np
 import pytest
@@ -36,20 +38,23 @@ def paper_env(monkeypatch):
 
 
 CASES = [
-    # T, Hq, Hkv, D, (store K, store V), k_mode, rows_per_call
-    (1100, 32, 4, 64, None, "exact", 300),
-    (777, 16, 4, 128, (2, 4), "exact", 257),
-    (600, 8, 8, 128, None, "linear", 600),
-    (530, 16, 2, 64, (1, 2), "exact", 101),
+    # T, Hq, Hkv, D, (store K, store V), k_mode, rows_per_call, pages per split (None: the default)
+    (1100, 32, 4, 64, None, "exact", 300, None),
+    (777, 16, 4, 128, (2, 4), "exact", 257, None),
+    (600, 8, 8, 128, None, "linear", 600, None),
+    (530, 16, 2, 64, (1, 2), "exact", 101, None),
+    (1100, 32, 4, 64, None, "exact", 1100, 8),
 ]
 
 
-@pytest.mark.parametrize("case", CASES, ids=[f"T{c[0]}-g{c[1] // c[2]}-D{c[3]}-{c[5]}" for c in CASES])
+@pytest.mark.parametrize("case", CASES, ids=[f"T{c[0]}-g{c[1] // c[2]}-D{c[3]}-{c[5]}-sp{c[7]}" for c in CASES])
 def test_pf_rows_pass_matches_entry_pass(paper_env, case):
     import care_kv
-    T, Hq, Hkv, D, store, k_mode, rpc = case
-    print(f"pf rows case T={T} Hq={Hq} Hkv={Hkv} D={D} store={store} {k_mode}", flush=True)
+    T, Hq, Hkv, D, store, k_mode, rpc, split = case
+    print(f"pf rows case T={T} Hq={Hq} Hkv={Hkv} D={D} store={store} {k_mode} split={split}", flush=True)
     paper_env.setenv("CAREKV_K_CORRECTION_MODE", k_mode)
+    if split is not None:
+        paper_env.setenv("CAREKV_PF_SPLIT", str(split))
     dev = torch.device("cuda", 0)
     sb = dict(store_budget_mode="ratio", store_budget_ratio=0.03) if store is None else \
         dict(store_budget_mode="absolute", store_abs_k=store[0], store_abs_v=store[1])
