@@ -715,11 +715,17 @@ __global__ __launch_bounds__(256) void decode_select_wave_kernel(carekv_arena A,
       diagp = a.diag + ((long)b * a.Hq + kvh * GQ + qq) * a.diag_cap;
     }
   }
-  // sum of one value per (lane, j) in the work-group form's order
-  auto ordered_sum = [&](const float (&v)[NJ]) {
+  // Lane l holds items l + 64j for j < nj (wave-uniform): a row's pages, or
+  // the split partials; the slices j >= nj hold no item and are skipped (a
+  // scalar branch), which changes no value: their keys are -1, their ballots
+  // empty and their sums +0.
+  const int njp = (np + 63) / 64;
+  // sum of one value per (lane, j < nj) in the work-group form's order
+  auto ordered_sum = [&](const float (&v)[NJ], int nj) {
     float t = 0.f;
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) t = j == 0 ? wave_sum_f(v[0]) : t + wave_sum_f(v[j]);
+    for (int j = 0; j < NJ; ++j)
+      if (j < nj) t = j == 0 ? wave_sum_f(v[0]) : t + wave_sum_f(v[j]);
     return t;
   };
 
@@ -743,7 +749,7 @@ __global__ __launch_bounds__(256) void decode_select_wave_kernel(carekv_arena A,
       if (ms != -INFINITY) lj[j] = a.pml[base * 2 + 1] * __builtin_amdgcn_exp2f(ms - M);
     }
   }
-  const float L = ordered_sum(lj);
+  const float L = ordered_sum(lj, (nsr + 63) / 64);
   if (lane == 0) { a.ml[bq * 2] = M; a.ml[bq * 2 + 1] = L; }
 
   // ---- one K and one V score per page (decode_select_kernel's K1 scoring)
@@ -809,7 +815,7 @@ __global__ __launch_bounds__(256) void decode_select_wave_kernel(carekv_arena A,
   float pk[NJ], pvv[NJ];
 #pragma unroll
   for (int j = 0; j < NJ; ++j) { pk[j] = sK[j] >= 0.f ? sK[j] : 0.f; pvv[j] = sV[j] >= 0.f ? sV[j] : 0.f; }
-  const float tK = ordered_sum(pk), tV = ordered_sum(pvv);
+  const float tK = ordered_sum(pk, njp), tV = ordered_sum(pvv, njp);
   const int n_k = wave_sum_i(cntK), n_v = wave_sum_i(cntV);
 
   // ---- read budgets, normalisation, keys (as decode_select_kernel)
@@ -855,6 +861,7 @@ __global__ __launch_bounds__(256) void decode_select_wave_kernel(carekv_arena A,
     int n = 0;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
+      if (j >= njp) break;
       if (useK) n += __builtin_popcountll(__ballot(kK[j] >= t));
       if (useV) n += __builtin_popcountll(__ballot(kV[j] >= t));
     }
@@ -889,12 +896,15 @@ __global__ __launch_bounds__(256) void decode_select_wave_kernel(carekv_arena A,
   int eq_runK = 0, eq_runV = 0;
   if (joint && sk.on && sk.take < sk.eq) {
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) eq_runV += __builtin_popcountll(__ballot(kK[j] >= 0 && (uint32_t)kK[j] == sk.tau));
+    for (int j = 0; j < NJ; ++j)
+      if (j < njp) eq_runV += __builtin_popcountll(__ballot(kK[j] >= 0 && (uint32_t)kK[j] == sk.tau));
   }
   uint8_t* maskq = a.mask + bq * a.Pmax;
   unsigned selK[NJ], selV[NJ];
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
+    selK[j] = selV[j] = 0u;
+    if (j >= njp) continue;
     const int p = lane + 64 * j;
     const bool eqk = sk.on && kK[j] >= 0 && (uint32_t)kK[j] == sk.tau;
     const bool eqv = sv.on && kV[j] >= 0 && (uint32_t)kV[j] == sv.tau;
@@ -928,6 +938,7 @@ __global__ __launch_bounds__(256) void decode_select_wave_kernel(carekv_arena A,
   for (int kind = 0; kind < 2; ++kind) {
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
+      if (j >= njp) break;
       const int p = lane + 64 * j;
       const bool on = kind == 0 ? selK[j] != 0u : selV[j] != 0u;
       const uint64_t bal = __ballot(on);
