@@ -102,12 +102,30 @@ __global__ __launch_bounds__(256, 2) void pf_rows_stream_kernel(carekv_arena A, 
   const int split = blockIdx.z, tps = a.SP / 2;
   const int jt0 = split * tps, jt1 = min(jt0 + tps, nt);
   if (jt0 >= jt1) return;  // past every entry's pages: no partial (splits_read)
-  for (int i = threadIdx.x; i < EPW * 16 * D; i += 256) {
-    const int el = i / (16 * D), n = (i / D) % 16, d = i % D;
+  {  // every entry's q in the residual pair order: thread t fills dims
+     // [(t % 4) D/4, ..) of column (t / 4) % 16 of entry t / 64, one column
+     // lookup per thread; within each 8-dim block the order is
+     // {0, 4, 1, 5, 2, 6, 3, 7}, two byte permutes per pair of output words
+    static_assert(EPW * 16 * 4 == 256, "one thread per quarter column");
+    static_assert(PK::T.slot_code[0] == 0 && PK::T.slot_code[1] == 4 && PK::T.slot_code[2] == 1 &&
+                      PK::T.slot_code[3] == 5 && PK::T.slot_code[4] == 2 && PK::T.slot_code[5] == 6 &&
+                      PK::T.slot_code[6] == 3 && PK::T.slot_code[7] == 7,
+                  "residual pair order inside an 8-dim block");
+    constexpr int DPT = D / 4;
+    const int el = threadIdx.x >> 6, n = (threadIdx.x >> 2) & 15, d0 = (threadIdx.x & 3) * DPT;
     const int b = e0 + el;
     const PfCol x = pf_col(a, b, kvh, n);
     const bool ok = b < a.B && x.ok;
-    sqr[i] = ok ? bits2half(a.q[pf_row_off(a, x) * D + (d & ~7) + PK::T.slot_code[d & 7]]) : (_Float16)0.f;
+    const uint16_t* qr = a.q + (ok ? pf_row_off(a, x) * D : 0) + d0;
+    _Float16* dst = sqr + (el * 16 + n) * D + d0;
+#pragma unroll
+    for (int c = 0; c < DPT; c += 8) {
+      const uint4 v = ok ? *reinterpret_cast<const uint4*>(qr + c) : make_uint4(0u, 0u, 0u, 0u);
+      // v.x = (h1, h0), v.y = (h3, h2), v.z = (h5, h4), v.w = (h7, h6)
+      *reinterpret_cast<uint4*>(dst + c) =
+          make_uint4(__builtin_amdgcn_perm(v.z, v.x, 0x05040100u), __builtin_amdgcn_perm(v.z, v.x, 0x07060302u),
+                     __builtin_amdgcn_perm(v.w, v.y, 0x05040100u), __builtin_amdgcn_perm(v.w, v.y, 0x07060302u));
+    }
   }
 
   const uint32_t span = (uint32_t)T * D * 2;  // rows past the prompt read as 0
