@@ -64,7 +64,6 @@ __global__ __launch_bounds__(256, 2) void pf_rows_stream_kernel(carekv_arena A, 
   const long pg_base = ((long)kvh * A.n_seq + seq) * A.max_pages;
   const bool corr = a.correction != 0;
   const float sm_log2 = a.sm_log2;
-  const long rq = (long)a.Pmax * a.F;
 
   // ---- q: the generic kernel's S operands for the wave's two entries, and
   // every entry's q in the residual order for the K slots' dS
@@ -151,13 +150,49 @@ __global__ __launch_bounds__(256, 2) void pf_rows_stream_kernel(carekv_arena A, 
       *reinterpret_cast<uint4*>(dst) = make_uint4(stg[k][0], stg[k][1], stg[k][2], stg[k][3]);
     }
   };
-  auto load_meta2 = [&](int j, int* mv) {
+  // Page metadata without a branch on the lane or the page: one dword per
+  // lane (lane 0 valid, 2.. k_slot, 6..9 v_slot; the other lanes read valid
+  // again, unused) from a per-lane address, and the page's has_meta byte;
+  // a page past the work-group's last one reads that last page and is
+  // dropped where the metadata is used.  A load under a branch would leave
+  // the compiler unable to count the loads in flight, and its wait for the
+  // metadata would then also wait for the next tile's K_hat / V_hat loads
+  // and for every record store.
+  struct MetaRaw { int w, hm; };
+  auto load_meta2 = [&](int j, MetaRaw* mv) {
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
-      const int p = 2 * j + tt;
-      mv[tt] = p < np_wg ? meta_lanes_load<NCG>(A, pg_base + p, lane) : 0;
+      const long pg = pg_base + min(2 * j + tt, np_wg - 1);
+      const int* src = A.valid + pg;
+      if (lane >= 2 && lane < 2 + NCG) src = A.k_slot + pg * NCG + (lane - 2);
+      if (lane >= 6 && lane < 6 + kVtb) src = A.v_slot + pg * kVtb + (lane - 6);
+      mv[tt].w = *src;
+      mv[tt].hm = A.has_meta[pg];
     }
   };
+  auto meta_of = [&](const MetaRaw& r, int p) {
+    PageMeta<NCG> m{};
+    if (p >= np_wg) return m;  // wave-uniform
+    m.nv = __builtin_amdgcn_readlane(r.w, 0);
+    m.meta = __builtin_amdgcn_readfirstlane(r.hm);
+#pragma unroll
+    for (int c = 0; c < NCG; ++c) {
+      const int sl = __builtin_amdgcn_readlane(r.w, 2 + c);
+      m.ksl[c] = sl < A.n_slots ? sl : -1;
+    }
+#pragma unroll
+    for (int v = 0; v < kVtb; ++v) {
+      const int sl = __builtin_amdgcn_readlane(r.w, 6 + v);
+      m.vsl[v] = sl < A.n_slots ? sl : -1;
+    }
+    return m;
+  };
+  // records and stored weights through one buffer resource over the
+  // workspace (rec .. xbuf, below 4 GiB): a lane with nothing to write
+  // stores past its end, which the hardware drops, so no store sits behind
+  // a lane branch either
+  const __amdgpu_buffer_rsrc_t rs_ws = make_rsrc(a.rec, a.ws_span);
+  constexpr uint32_t kDrop = 0xfffffff0u;
   // K residual words (lane: token ln, bytes 4lj..) and raw fp16 scales of
   // the two pages' stored slots; a page without a slot (or without
   // metadata) reads past the end of the resources, i.e. 0 with no memory
@@ -191,7 +226,7 @@ __global__ __launch_bounds__(256, 2) void pf_rows_stream_kernel(carekv_arena A, 
   // of its S products.  (Issuing them a tile ahead measured the same at 25
   // VGPRs more: the pass is bound by its longest chain of tiles, which the
   // splits keep short, not by these loads.)
-  int mv_nx[2];
+  MetaRaw mv_nx[2];
   load_tile(jt0);
   store_tile(0);
   load_meta2(jt0, mv_nx);
@@ -203,7 +238,7 @@ __global__ __launch_bounds__(256, 2) void pf_rows_stream_kernel(carekv_arena A, 
     const char* vb = kb + KBUF;
     PageMeta<NCG> cm[2];
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) cm[tt] = meta_from_lanes<NCG>(mv_nx[tt], A);
+    for (int tt = 0; tt < 2; ++tt) cm[tt] = meta_of(mv_nx[tt], 2 * jt + tt);
     if (jt + 1 < jt1) load_meta2(jt + 1, mv_nx);
     uint32_t krow[2][NCG], ksc[2][NCG];
     load_kres(cm, krow, ksc);
@@ -242,7 +277,10 @@ __global__ __launch_bounds__(256, 2) void pf_rows_stream_kernel(carekv_arena A, 
         // ---- page record (layout in decode_common.h)
         const int b = eb[qb];
         const long bk = (long)b * A.n_kv_heads + kvh;
-        float* rec = a.rec + (bk * GQ * a.Pmax + p) * a.F + ln * rq;
+        // byte offsets of this lane's record and stored weights (query ln)
+        const uint32_t ro = (uint32_t)(((bk * GQ + ln) * a.Pmax + p) * a.F) * 4u;
+        const uint32_t eo = a.ws_e_off + (uint32_t)(((bk * GQ + ln) * a.Pmax + p) * 16 + 4 * lj) * 2u;
+        const bool qok = ln < GQ;
         const float emax = col_max(fmaxf(fmaxf(e[0], e[1]), fmaxf(e[2], e[3])));
         int fi = 4;
 #pragma unroll
@@ -250,13 +288,13 @@ __global__ __launch_bounds__(256, 2) void pf_rows_stream_kernel(carekv_arena A, 
           if (e[i] == emax) fi = i;
         const float tstar = -col_max(-(fi < 4 ? (float)(4 * lj + fi) : 16.f));
         const int istar = (int)tstar - 4 * lj;
-        if (lj == 0 && ln < GQ) {
-          rec[0] = lse2[qb];
-          rec[1 + 4 * a.k_cap] = emax;
-        }
-        if (ln < GQ)
-          *reinterpret_cast<uint2*>(a.ebuf + ((bk * GQ + ln) * a.Pmax + p) * 16 + 4 * lj) =
-              make_uint2(pack_h2(e[0], e[1]), pack_h2(e[2], e[3]));
+        typedef uint32_t u2_t __attribute__((ext_vector_type(2)));
+        const uint32_t ro0 = (lj == 0 && qok) ? ro : kDrop;
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(lse2[qb]), rs_ws, ro0, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(emax), rs_ws,
+                                              ro0 == kDrop ? kDrop : ro0 + (uint32_t)(1 + 4 * a.k_cap) * 4u, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b64(u2_t{pack_h2(e[0], e[1]), pack_h2(e[2], e[3])}, rs_ws,
+                                              qok ? eo : kDrop, 0, 0);
         const _Float16* sqe = sqr + (QB * w + qb) * 16 * D;
         int rkk = 0;
 #pragma unroll
@@ -279,9 +317,10 @@ __global__ __launch_bounds__(256, 2) void pf_rows_stream_kernel(carekv_arena A, 
             M4 = fmaf(ue, ue, M4);
           }
           const float mj = moments_reduce4(M2, M3, M4, Ds);
-          if (ln < GQ) {
+          {
             const float f = h2f((uint16_t)ksc[tt][cg]) * a.inv_sqrt_d;
-            rec[1 + 4 * rkk + lj] = mj * (f * f);
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(mj * (f * f)), rs_ws,
+                                                  qok ? ro + (uint32_t)(1 + 4 * rkk + lj) * 4u : kDrop, 0, 0);
           }
           ++rkk;
         }
@@ -292,7 +331,9 @@ __global__ __launch_bounds__(256, 2) void pf_rows_stream_kernel(carekv_arena A, 
           if (vb2 == lj) my_rank = rvv;
           ++rvv;
         }
-        if (my_rank >= 0 && my_rank < a.v_cap && ln < GQ) rec[2 + 4 * a.k_cap + my_rank] = (e[0] + e[1]) + (e[2] + e[3]);
+        __builtin_amdgcn_raw_buffer_store_b32(
+            __float_as_uint((e[0] + e[1]) + (e[2] + e[3])), rs_ws,
+            (my_rank >= 0 && my_rank < a.v_cap && qok) ? ro + (uint32_t)(2 + 4 * a.k_cap + my_rank) * 4u : kDrop, 0, 0);
       }
     }
 
