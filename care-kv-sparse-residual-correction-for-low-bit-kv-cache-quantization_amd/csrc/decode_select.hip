@@ -761,48 +761,77 @@ __global__ __launch_bounds__(256) void decode_select_wave_kernel(carekv_arena A,
   int cgK[NJ], vbV[NJ];
   int cntK = 0, cntV = 0;
   bool ovf = false;
+  // Two page slices at a time: the loads of both are issued (every lane,
+  // its page clamped to the row's last) before either is scored, so that a
+  // lane waits one memory round trip per pair of slices, not per slice; the
+  // scoring is the same arithmetic on the same values.
+  struct PageIn {
+    int nv, hm, ksl[NCG], vsl[kVtb];
+    float vsq, r[7];
+    uint2 e2;
+  };
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
-    const int p = lane + 64 * j;
     sK[j] = sV[j] = -1.f;
     cgK[j] = vbV[j] = -1;
-    if (p >= np) continue;
-    const long pg = pg_base + p;
-    const int nv = A.valid[pg];
-    const int hm = A.has_meta[pg];
-    const float vsq = vsq_row ? vsq_row[p] : A.v_sq[pg];
-    int ksl[NCG], vsl[kVtb];
-    load_slots<NCG>(ksl, A.k_slot + pg * NCG);
-    load_slots<kVtb>(vsl, A.v_slot + pg * kVtb);
-    const uint2 e2 = *reinterpret_cast<const uint2*>(A.v_err + pg * kVtb);
-    const float* rp = recq + (long)p * 7;
-    const float r0 = rp[0], M2 = rp[1], M3 = rp[2], M4 = rp[3], Ds = rp[4], es = rp[5], E = rp[6];
-    const bool ok = L > 0.f && nv > 0 && hm;
-    const float c = ok ? exp2_dn(r0 - M) * invL : 0.f;
-    int nks = 0, nvs = 0, cg1 = -1, vb1 = -1;
+  }
 #pragma unroll
-    for (int cg = NCG - 1; cg >= 0; --cg)
-      if (slot_ok(A, ksl[cg])) { ++nks; cg1 = cg; }
+  for (int j0 = 0; j0 < NJ; j0 += 2) {
+    if (j0 >= njp) break;
+    PageIn in[2];
 #pragma unroll
-    for (int vb = kVtb - 1; vb >= 0; --vb)
-      if (slot_ok(A, vsl[vb])) { ++nvs; vb1 = vb; }
-    ovf |= hm && (nks > 1 || nvs > 1);
-    cgK[j] = cg1;
-    vbV[j] = vb1;
-    if (ok && nks > 0) {
-      const float wr = es * (1.f - c * es);
-      const float q2 = (M2 - c * (2.f * M3 - c * M4)) + Ds * (wr * wr);
-      float ks = kscore_underflows(c, M2, Ds, es) ? 0.f : (c * sqrt_dn(fmaxf(q2, 0.f))) * __builtin_amdgcn_sqrtf(vsq);
-      if (!isfinite(ks)) ks = 0.f;
-      sK[j] = ks * a.sens;
-      ++cntK;
+    for (int h = 0; h < 2; ++h) {
+      const int pc = min(lane + 64 * (j0 + h), np - 1);
+      const long pg = pg_base + pc;
+      in[h].nv = A.valid[pg];
+      in[h].hm = A.has_meta[pg];
+      in[h].vsq = vsq_row ? vsq_row[pc] : A.v_sq[pg];
+      load_slots<NCG>(in[h].ksl, A.k_slot + pg * NCG);
+      load_slots<kVtb>(in[h].vsl, A.v_slot + pg * kVtb);
+      in[h].e2 = *reinterpret_cast<const uint2*>(A.v_err + pg * kVtb);
+      const float* rp = recq + (long)pc * 7;
+#pragma unroll
+      for (int k = 0; k < 7; ++k) in[h].r[k] = rp[k];
     }
-    if (ok && vb1 >= 0 && vb1 * kVtb < nv) {
-      const uint32_t ew = vb1 < 2 ? e2.x : e2.y;
-      const float ve = h2f((uint16_t)(ew >> (16 * (vb1 & 1))));
-      const float verr_s = sens1 ? ve : (float)((double)ve * a.sens_d);
-      sV[j] = ((c * E) * verr_s) * a.sens;
-      ++cntV;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int j = j0 + h;
+      const int p = lane + 64 * j;
+      if (p >= np) continue;
+      const int nv = in[h].nv, hm = in[h].hm;
+      const float vsq = in[h].vsq;
+      const int* ksl = in[h].ksl;
+      const int* vsl = in[h].vsl;
+      const uint2 e2 = in[h].e2;
+      const float r0 = in[h].r[0], M2 = in[h].r[1], M3 = in[h].r[2], M4 = in[h].r[3], Ds = in[h].r[4],
+                  es = in[h].r[5], E = in[h].r[6];
+      const bool ok = L > 0.f && nv > 0 && hm;
+      const float c = ok ? exp2_dn(r0 - M) * invL : 0.f;
+      int nks = 0, nvs = 0, cg1 = -1, vb1 = -1;
+#pragma unroll
+      for (int cg = NCG - 1; cg >= 0; --cg)
+        if (slot_ok(A, ksl[cg])) { ++nks; cg1 = cg; }
+#pragma unroll
+      for (int vb = kVtb - 1; vb >= 0; --vb)
+        if (slot_ok(A, vsl[vb])) { ++nvs; vb1 = vb; }
+      ovf |= hm && (nks > 1 || nvs > 1);
+      cgK[j] = cg1;
+      vbV[j] = vb1;
+      if (ok && nks > 0) {
+        const float wr = es * (1.f - c * es);
+        const float q2 = (M2 - c * (2.f * M3 - c * M4)) + Ds * (wr * wr);
+        float ks = kscore_underflows(c, M2, Ds, es) ? 0.f : (c * sqrt_dn(fmaxf(q2, 0.f))) * __builtin_amdgcn_sqrtf(vsq);
+        if (!isfinite(ks)) ks = 0.f;
+        sK[j] = ks * a.sens;
+        ++cntK;
+      }
+      if (ok && vb1 >= 0 && vb1 * kVtb < nv) {
+        const uint32_t ew = vb1 < 2 ? e2.x : e2.y;
+        const float ve = h2f((uint16_t)(ew >> (16 * (vb1 & 1))));
+        const float verr_s = sens1 ? ve : (float)((double)ve * a.sens_d);
+        sV[j] = ((c * E) * verr_s) * a.sens;
+        ++cntV;
+      }
     }
   }
   if (a.pf && lane == 0) {  // the prompt's later pages: candidates that count, scored 0 (layer.py:514-517)
